@@ -1,0 +1,152 @@
+/*
+ * vmi.h -- C ABI of the MI355X speculative-decode MoE library (libvmi.so).
+ *
+ * Plain pointers, sizes and a hipStream_t passed as void*.  No exceptions cross
+ * this boundary: every entry point returns VMI_OK (0) or a negative status and
+ * records a message retrievable with vmi_last_error() (thread-local).
+ * All device pointers must be contiguous row-major buffers on the current HIP
+ * device.  Calls are stream-ordered and asynchronous: they never synchronise the
+ * host.  Errors the device detects while running (a routed slot outside the
+ * pool, for instance) are OR-ed into the workspace status word; read them with
+ * vmi_workspace_status().
+ *
+ * Packed weight format (MLX affine, LSB-first): a projection stack with n
+ * matrices of shape [out, in] is three arrays
+ *   w  uint32 [n, out, in*bits/32]   value of column c sits at bits (c*bits)%32
+ *                                    of word (c*bits)/32 of its row
+ *   s  uint16 [n, out, in/group]     bf16 bit patterns of the scales
+ *   b  uint16 [n, out, in/group]     bf16 bit patterns of the biases
+ * and dequantises to w = q * s + b (fused_moe.cpp:131-145).
+ */
+#ifndef VMI_H_
+#define VMI_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum vmi_status {
+    VMI_OK = 0,
+    VMI_ERR_INVALID = -1,     /* bad pointer, shape or argument */
+    VMI_ERR_UNSUPPORTED = -2, /* valid but not built (bits, group, shape) */
+    VMI_ERR_HIP = -3,         /* a HIP runtime call failed */
+    VMI_ERR_WORKSPACE = -4    /* workspace missing or too small */
+};
+
+enum vmi_dtype { VMI_F32 = 0, VMI_BF16 = 1 };
+
+/* Device-side status bits (vmi_workspace_status). */
+#define VMI_STATUS_BAD_SLOT 0x1u   /* a routed slot was outside [0, cap) */
+#define VMI_STATUS_BAD_ROUTE 0x2u  /* router produced a non-finite logit */
+
+/* Last error message of the calling thread ("" when none). */
+const char* vmi_last_error(void);
+/* ABI version; bumped on any incompatible change. */
+int vmi_version(void);
+
+/* One affine-quantised projection stack (see header comment). */
+typedef struct vmi_qmat {
+    const uint32_t* w;
+    const uint16_t* s;
+    const uint16_t* b;
+} vmi_qmat;
+
+/* ------------------------------------------------------------------------
+ * vmi_fused_moe_slots -- replaces fused_moe_slots
+ *   native/ext/compute/fused_moe.h:18-23 (declaration),
+ *   native/ext/compute/fused_moe.cpp:514-556, 635-664 (primitive + factory),
+ *   native/ext/bindings.cpp:300-320 (Python binding).
+ * Same argument meaning: x [T, hidden] (x_dtype VMI_F32 as the reference's
+ * caller passes, native_moe.py:481, or VMI_BF16), local_slots int32 [T*k]
+ * token-major (token = pair / k, fused_moe.cpp:235), scores f32 [T*k],
+ * gate/up stacks [cap, inter, hidden], down stack [cap, hidden, inter],
+ * out [T, hidden] in out_dtype = sum_j scores[t*k+j] * expert_{slot}(x_t)
+ * (SwiGLU expert: g*sigmoid(g)*u then down; fixed j order as reduce_pairs).
+ * Supported: bits == 4, group == 64, T*k <= 160, T <= 16,
+ * hidden in {256, 512, 1024, 2048}, inter in {128, 256, 512}.
+ * The reference raises on shape mismatch (fused_moe.cpp:522-524); this
+ * returns VMI_ERR_INVALID.  A slot outside [0, cap) contributes zero and sets
+ * VMI_STATUS_BAD_SLOT.
+ * workspace: device memory of vmi_fused_moe_slots_workspace_bytes(T, k,
+ * hidden, inter) bytes whose first 4 bytes (the status word) are zero before
+ * its first use; it may be reused by later calls on the same stream but never
+ * by two calls in flight at once.
+ * ------------------------------------------------------------------------ */
+size_t vmi_fused_moe_slots_workspace_bytes(int T, int k, int hidden, int inter);
+int vmi_fused_moe_slots(const void* x, int x_dtype, const int32_t* local_slots, const float* scores,
+                        vmi_qmat gate, vmi_qmat up, vmi_qmat down, int T, int k, int hidden, int inter, int group,
+                        int bits, int cap, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* ------------------------------------------------------------------------
+ * vmi_moe_layer -- one full routed-MoE layer on a verify batch; replaces the
+ * production branch of FileStreamingMoeBlock.__call__
+ *   mlx_streaming/core/moe/block.py:245-1013 (router :251-253, softmax/top-k/
+ *   renorm :321-329, pool acquire -> local slots :680-684, SwitchGLU expert
+ *   compute compute.py:145-170, combine :1008, shared expert :102-109,
+ *   :1009-1012), and the MTP layer's StreamingMTPMoE.__call__
+ *   mlx_streaming/mtp/qwen3_next_mtp.py:122-137.
+ * Steps: xn = x, or with norm_weight the pre-MoE RMSNorm
+ * xn = bf16(x * (1/sqrt(mean(x^2) + norm_eps)) * norm_weight) (the decoder
+ * layer's post_attention_layernorm ahead of its MoE block); raw = router(xn)
+ * (+ logit_bias); ids = top-k of raw (logit
+ * descending, ties to the lower expert id); scores = softmax over the k
+ * (norm_topk_prob) or over all experts; slot = slot_table[id] (identity when
+ * NULL); out = sum_j scores_j * expert_slot(xn) + sigmoid(shared_gate(xn)) *
+ * shared(xn) (+ residual).  x, residual and out are bf16 [T, hidden]; out must
+ * not alias x.  ids_out / scores_out (may be NULL) receive [T, k].
+ * Supported: expert bits 4, router/shared-gate bits 4 or 8, group 64,
+ * T <= 16, num_experts <= 1024, top_k <= 16, hidden/inter as above.
+ * ------------------------------------------------------------------------ */
+typedef struct vmi_moe_layer_desc {
+    int hidden, inter, num_experts, top_k, group, bits;
+    int norm_topk_prob;
+    int router_bits;              /* 4 or 8 */
+    int cap;                      /* pool slots in gate/up/down */
+    vmi_qmat router;              /* [1, num_experts, hidden] */
+    const float* router_logit_bias; /* [num_experts] added to raw logits, or NULL */
+    const int32_t* slot_table;    /* [num_experts] expert -> pool slot, or NULL */
+    vmi_qmat gate, up, down;      /* pool stacks [cap, ...] */
+    vmi_qmat shared_gate, shared_up, shared_down; /* [1, ...]; shared_gate.w == NULL: no shared expert */
+    vmi_qmat shared_expert_gate;  /* [1, 1, hidden]; .w == NULL: gate fixed to 1 */
+    int shared_expert_gate_bits;  /* 4 or 8 */
+    const uint16_t* norm_weight;  /* [hidden] bf16 RMSNorm weight, or NULL: no norm */
+    float norm_eps;
+} vmi_moe_layer_desc;
+
+size_t vmi_moe_layer_workspace_bytes(int T, int top_k, int hidden, int inter, int num_experts);
+int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, const uint16_t* residual,
+                  uint16_t* out, int32_t* ids_out, float* scores_out, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* Reads and clears the device status word of a workspace (synchronises the
+ * stream).  *flags receives VMI_STATUS_* bits. */
+int vmi_workspace_status(void* workspace, void* stream, uint32_t* flags);
+
+/* ------------------------------------------------------------------------
+ * vmi_dequant_affine -- materialise w = q*s + b as f32 [rows, cols]
+ * (qvalue, fused_moe.cpp:131-145).  Used to check dequantisation bit-exactly.
+ * bits in {4, 8}; cols*bits % 32 == 0; cols % group == 0.
+ * ------------------------------------------------------------------------ */
+int vmi_dequant_affine(vmi_qmat m, int rows, int cols, int group, int bits, float* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Synthetic data (no reference counterpart: the reference loads real
+ * checkpoints).  Bit-identical to the CPU generator used by the tests:
+ * element i = (sum of four 16-bit words of Philox4x32-10 block i/2 -
+ * 131070) * scale, quantised per group of 64 by min/max with bf16
+ * scale/bias.  vmi_synth_quantized fills a [rows, cols] projection;
+ * vmi_synth_bf16 fills n bf16 values.
+ * ------------------------------------------------------------------------ */
+int vmi_synth_quantized(uint64_t seed, uint32_t stream_id, int64_t rows, int cols, int group, int bits, float scale,
+                        uint32_t* w, uint16_t* s, uint16_t* b, void* stream);
+int vmi_synth_bf16(uint64_t seed, uint32_t stream_id, int64_t n, float scale, uint16_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VMI_H_ */

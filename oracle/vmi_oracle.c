@@ -1,0 +1,643 @@
+/*
+ * vmi_oracle.c -- CPU oracle for the speculative-decode MoE hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * or as the reported CPU baseline.  The product path (vates_amd) never calls it.
+ *
+ * Every function restates the reference algorithm it cites (paths are relative
+ * to the AMOS144/Vates checkout).  Floating-point "truth" paths accumulate in
+ * double; the router path reproduces the GPU kernel's fp32 operation order
+ * exactly so that routed expert ids are bit-identical.  Build with
+ * -ffp-contract=off: every fused multiply-add below is written as fmaf().
+ *
+ * Pinning (see tests/test_oracle_*.py):
+ *   philox          Random123 known-answer vectors
+ *   dequant         closed-form nibble order / affine values; reference fixture
+ *                   (test_native_moe_ext.py:20-47 weight=arange, scale=bf16(0.001))
+ *   quantize        round-trip bound |w - deq| <= s/2 (+ bf16 edge), brute force
+ *   qgemv / experts numpy float64 matmul of the dequantised matrices
+ *   route/top-k     numpy argsort brute force, tie rule, scipy softmax
+ *   route reduce    literal known answer test_expert_major_prefill.py:89-103
+ *   expert-major    literal known answer test_expert_major_prefill.py:33-60
+ *   accept greedy   literal known answers test_mtp_generate.py:211-223,
+ *                   spec == non-spec greedy invariant on toy models
+ *   accept stoch.   exact output-distribution enumeration on tiny vocabularies
+ */
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <math.h>
+
+#define ORC_OK 0
+#define ORC_EINVAL -1
+#define ORC_ESLOT -2
+#define ORC_ENOMEM -3
+
+/* ------------------------------------------------------------------ bf16 */
+static inline float bf16_to_f32(uint16_t v) {
+    uint32_t u = (uint32_t)v << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* Round-to-nearest-even fp32 -> bf16 (NaN kept quiet). */
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t v) { return bf16_to_f32(v); }
+
+/* ---------------------------------------------------------------- Philox */
+/* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel Random Numbers: As
+ * Easy as 1, 2, 3", SC'11).  Integer-only, so the GPU generator produces the
+ * same words. */
+void orc_philox4x32_10(const uint32_t ctr_in[4], const uint32_t key_in[2], uint32_t out[4]) {
+    uint32_t c0 = ctr_in[0], c1 = ctr_in[1], c2 = ctr_in[2], c3 = ctr_in[3];
+    uint32_t k0 = key_in[0], k1 = key_in[1];
+    for (int r = 0; r < 10; ++r) {
+        uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+        uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+        uint32_t n0 = hi1 ^ c1 ^ k0;
+        uint32_t n2 = hi0 ^ c3 ^ k1;
+        c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* Irwin-Hall(4) approximate normal: element i of stream `stream` under `seed`
+ * is ((u0+u1+u2+u3) - 131070) * scale with u* the four 16-bit halves of one
+ * Philox half-block.  `scale` = std / 37837.2265 (the Irwin-Hall std of four
+ * uniform 16-bit words).  The integer sum and one fp32 multiply are exact
+ * across CPU and GPU, so synthetic tensors are bit-identical. */
+static inline float synth_one(uint64_t seed, uint32_t stream, uint64_t i, float scale) {
+    uint32_t ctr[4] = {(uint32_t)(i >> 1), (uint32_t)(i >> 33), stream, 0x5eed0001u};
+    uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t o[4];
+    orc_philox4x32_10(ctr, key, o);
+    uint32_t a = (i & 1) ? o[2] : o[0];
+    uint32_t b = (i & 1) ? o[3] : o[1];
+    int32_t s = (int32_t)((a & 0xffffu) + (a >> 16) + (b & 0xffffu) + (b >> 16)) - 131070;
+    return (float)s * scale;
+}
+
+void orc_synth_normal(uint64_t seed, uint32_t stream, uint64_t n, float scale, float* out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = synth_one(seed, stream, i, scale);
+}
+
+void orc_synth_normal_bf16(uint64_t seed, uint32_t stream, uint64_t n, float scale, uint16_t* out) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = orc_f32_to_bf16(synth_one(seed, stream, i, scale));
+}
+
+/* ------------------------------------------------------------ quantise */
+/* Affine quantiser used to make fixture and synthetic weights.  It follows the
+ * reference's own CPU restatement native/bench/compute/qlinear_bench.cpp:37-80
+ * (per-group min/max, scale=(max-min)/qmax, bias=min, round, clamp, LSB-first
+ * packing), with one documented change: scale and bias are rounded to bf16
+ * first and q is computed against the rounded values, as the packed format
+ * stores bf16 scales/biases (native_moe.py:57-72).
+ * Packing: value at column c occupies bits (c*bits)%32 of word (c*bits)/32
+ * of its row (fused_moe.cpp:131-145).  bits in {4, 8}. */
+static void quant_row(const float* w, int cols, int group, int bits, uint32_t* wq, uint16_t* s, uint16_t* b) {
+    int groups = cols / group;
+    int words = cols * bits / 32;
+    int qmax = (1 << bits) - 1;
+    memset(wq, 0, sizeof(uint32_t) * (size_t)words);
+    for (int g = 0; g < groups; ++g) {
+        const float* v = w + (size_t)g * group;
+        float mn = v[0], mx = v[0];
+        for (int i = 1; i < group; ++i) {
+            if (v[i] < mn) mn = v[i];
+            if (v[i] > mx) mx = v[i];
+        }
+        float scale = (mx - mn) / (float)qmax;
+        if (scale == 0.0f) scale = 1.0f;
+        uint16_t sb = orc_f32_to_bf16(scale);
+        uint16_t bb = orc_f32_to_bf16(mn);
+        float sf = bf16_to_f32(sb), bf = bf16_to_f32(bb);
+        if (sf == 0.0f) { sb = 0x3f80; sf = 1.0f; }
+        s[g] = sb;
+        b[g] = bb;
+        for (int i = 0; i < group; ++i) {
+            int c = g * group + i;
+            float qf = roundf((v[i] - bf) / sf);
+            int q = (int)qf;
+            if (!(qf >= 0.0f)) q = 0;
+            if (q > qmax) q = qmax;
+            int bit = c * bits;
+            wq[bit / 32] |= ((uint32_t)q) << (bit % 32);
+        }
+    }
+}
+
+int orc_quantize_affine(const float* w, int rows, int cols, int group, int bits,
+                        uint32_t* wq, uint16_t* s, uint16_t* b) {
+    if (rows <= 0 || cols <= 0 || group <= 0 || cols % group || (bits != 4 && bits != 8) || (cols * bits) % 32)
+        return ORC_EINVAL;
+    int words = cols * bits / 32, groups = cols / group;
+    for (int r = 0; r < rows; ++r)
+        quant_row(w + (size_t)r * cols, cols, group, bits, wq + (size_t)r * words, s + (size_t)r * groups,
+                  b + (size_t)r * groups);
+    return ORC_OK;
+}
+
+/* Synthetic N(0, std)-like matrix [rows, cols] drawn with orc_synth_normal
+ * (element index r*cols+c) and quantised with orc_quantize_affine. */
+int orc_synth_quantized(uint64_t seed, uint32_t stream, int rows, int cols, int group, int bits, float scale,
+                        uint32_t* wq, uint16_t* s, uint16_t* b) {
+    if (rows <= 0 || cols <= 0 || group <= 0 || cols % group || (bits != 4 && bits != 8) || (cols * bits) % 32)
+        return ORC_EINVAL;
+    float* row = (float*)malloc(sizeof(float) * (size_t)cols);
+    if (!row) return ORC_ENOMEM;
+    int words = cols * bits / 32, groups = cols / group;
+    for (int r = 0; r < rows; ++r) {
+        for (int c = 0; c < cols; ++c) row[c] = synth_one(seed, stream, (uint64_t)r * cols + c, scale);
+        quant_row(row, cols, group, bits, wq + (size_t)r * words, s + (size_t)r * groups, b + (size_t)r * groups);
+    }
+    free(row);
+    return ORC_OK;
+}
+
+/* ------------------------------------------------------------- dequant */
+/* qvalue (fused_moe.cpp:131-145; custom_kernel.py:170-184):
+ *   q = (w[row, (c*bits)/32] >> ((c*bits)%32)) & (2^bits-1)
+ *   w = q * scale[row, c/group] + bias[row, c/group]
+ * q*scale is exact in fp32 (<= 8-bit q times an 8-bit bf16 significand), so the
+ * single rounding of the add makes this value FMA-invariant. */
+static inline float deq(const uint32_t* wrow, const uint16_t* srow, const uint16_t* brow, int c, int group, int bits) {
+    int bit = c * bits;
+    uint32_t q = wrow[bit / 32] >> (bit % 32);
+    if ((bit % 32) + bits > 32) q |= wrow[bit / 32 + 1] << (32 - bit % 32);
+    q &= (1u << bits) - 1u;
+    int g = c / group;
+    return fmaf((float)q, bf16_to_f32(srow[g]), bf16_to_f32(brow[g]));
+}
+
+int orc_dequant_affine(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int rows, int cols, int group,
+                       int bits, float* out) {
+    if (rows <= 0 || cols <= 0 || group <= 0 || cols % group || bits < 1 || bits > 8 || (cols * bits) % 32)
+        return ORC_EINVAL;
+    int words = cols * bits / 32, groups = cols / group;
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c)
+            out[(size_t)r * cols + c] = deq(wq + (size_t)r * words, s + (size_t)r * groups, b + (size_t)r * groups, c,
+                                            group, bits);
+    return ORC_OK;
+}
+
+/* y[t, r] = sum_c deq(W)[r, c] * x[t, c], double accumulation. */
+static void qgemv_f64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int rows, int cols, int group,
+                      int bits, const double* x, int T, double* y) {
+    int words = cols * bits / 32, groups = cols / group;
+    for (int r = 0; r < rows; ++r) {
+        const uint32_t* wr = wq + (size_t)r * words;
+        const uint16_t* sr = s + (size_t)r * groups;
+        const uint16_t* br = b + (size_t)r * groups;
+        for (int t = 0; t < T; ++t) {
+            double acc = 0.0;
+            const double* xt = x + (size_t)t * cols;
+            for (int c = 0; c < cols; ++c) acc += (double)deq(wr, sr, br, c, group, bits) * xt[c];
+            y[(size_t)t * rows + r] = acc;
+        }
+    }
+}
+
+int orc_qgemv_f64(const uint32_t* wq, const uint16_t* s, const uint16_t* b, int rows, int cols, int group, int bits,
+                  const float* x, int T, double* y) {
+    if (rows <= 0 || cols <= 0 || T <= 0 || cols % group || (cols * bits) % 32) return ORC_EINVAL;
+    double* xd = (double*)malloc(sizeof(double) * (size_t)T * cols);
+    if (!xd) return ORC_ENOMEM;
+    for (size_t i = 0; i < (size_t)T * cols; ++i) xd[i] = x[i];
+    qgemv_f64(wq, s, b, rows, cols, group, bits, xd, T, y);
+    free(xd);
+    return ORC_OK;
+}
+
+/* Sum of 64 lane partials in the GPU's canonical wave-reduction tree
+ * (vmi_wave_sum_canon): inside each 16-lane row a[l] + a[l^1], then + [l^2],
+ * then + the lane mirrored inside its 8-lane half row, then + the lane
+ * mirrored inside its 16-lane row; the four row sums as (R0 + R1) + (R2 + R3). */
+static float canon_sum64(const float* a) {
+    float b[64], c[64], d[64], e[64];
+    for (int l = 0; l < 64; ++l) b[l] = a[l] + a[l ^ 1];
+    for (int l = 0; l < 64; ++l) c[l] = b[l] + b[l ^ 2];
+    for (int l = 0; l < 64; ++l) d[l] = c[l] + c[(l & ~7) | (7 - (l & 7))];
+    for (int l = 0; l < 64; ++l) e[l] = d[l] + d[(l & ~15) | (15 - (l & 15))];
+    return (e[0] + e[16]) + (e[32] + e[48]);
+}
+
+/* -------------------------------------------------------------- router */
+/* Router logits in the GPU kernel's exact fp32 order (k_router in
+ * vates_amd/csrc/vmi_moe.hip): lane l of a 64-lane wave owns columns
+ * [l*cpl, (l+1)*cpl) with cpl = cols/64 and accumulates acc = fmaf(deq, x,
+ * acc) in column order; the 64 partials meet in canon_sum64.  The logit bias,
+ * if any, is added last.
+ * Semantics: raw_gates = self.gate(x) (block.py:251-253). */
+static float router_row_f32(const uint32_t* wr, const uint16_t* sr, const uint16_t* br, int cols, int group, int bits,
+                            const float* xt) {
+    float a[64];
+    int cpl = cols / 64;
+    for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int j = 0; j < cpl; ++j) {
+            int c = l * cpl + j;
+            acc = fmaf(deq(wr, sr, br, c, group, bits), xt[c], acc);
+        }
+        a[l] = acc;
+    }
+    return canon_sum64(a);
+}
+
+int orc_router_logits_f32(const uint32_t* wq, const uint16_t* s, const uint16_t* b, const float* logit_bias, int E,
+                          int H, int group, int bits, const uint16_t* x_bf16, int T, float* logits) {
+    if (E <= 0 || T <= 0 || H % 64 || H % group || (H / 64) % 8) return ORC_EINVAL;
+    int words = H * bits / 32, groups = H / group;
+    float* xt = (float*)malloc(sizeof(float) * (size_t)H);
+    if (!xt) return ORC_ENOMEM;
+    for (int t = 0; t < T; ++t) {
+        for (int c = 0; c < H; ++c) xt[c] = bf16_to_f32(x_bf16[(size_t)t * H + c]);
+        for (int e = 0; e < E; ++e) {
+            float v = router_row_f32(wq + (size_t)e * words, s + (size_t)e * groups, b + (size_t)e * groups, H, group,
+                                     bits, xt);
+            if (logit_bias) v = v + logit_bias[e];
+            logits[(size_t)t * E + e] = v;
+        }
+    }
+    free(xt);
+    return ORC_OK;
+}
+
+/* Top-k routing (block.py:321-329; qwen3_next_mtp.py:124-128):
+ *   gates = softmax(raw, precise) ; inds = top-k(gates) ; s = gates[inds]
+ *   if norm_topk_prob: s /= sum(s)
+ * Selection is made on the logits (softmax is monotone), ordered by logit
+ * descending, ties to the lower expert index (argpartition leaves ties
+ * unspecified, block.py:323); NaN logits rank below every number.
+ * Scores in double. */
+static int better(float a, int ia, float b, int ib) {
+    int na = isnan(a), nb = isnan(b);
+    if (na != nb) return nb;
+    if (!na && a != b) return a > b;
+    return ia < ib;
+}
+
+int orc_topk_softmax(const float* logits, int T, int E, int k, int norm, int32_t* ids, float* scores) {
+    if (T <= 0 || E <= 0 || k <= 0 || k > E || k > 64) return ORC_EINVAL;
+    for (int t = 0; t < T; ++t) {
+        const float* l = logits + (size_t)t * E;
+        int sel[64];
+        for (int j = 0; j < k; ++j) {
+            int best = -1;
+            for (int e = 0; e < E; ++e) {
+                int used = 0;
+                for (int q = 0; q < j; ++q) used |= (sel[q] == e);
+                if (used) continue;
+                if (best < 0 || better(l[e], e, l[best], best)) best = e;
+            }
+            sel[j] = best;
+        }
+        double m = -INFINITY;
+        for (int e = 0; e < E; ++e)
+            if (!isnan(l[e]) && l[e] > m) m = l[e];
+        double denom = 0.0;
+        if (norm) {
+            for (int j = 0; j < k; ++j) denom += exp((double)l[sel[j]] - m);
+        } else {
+            for (int e = 0; e < E; ++e) denom += exp((double)l[e] - m);
+        }
+        for (int j = 0; j < k; ++j) {
+            ids[(size_t)t * k + j] = sel[j];
+            scores[(size_t)t * k + j] = (float)(exp((double)l[sel[j]] - m) / denom);
+        }
+    }
+    return ORC_OK;
+}
+
+/* ------------------------------------------------------------- experts */
+typedef struct {
+    const uint32_t *gw, *uw, *dw;
+    const uint16_t *gs, *gb, *us, *ub, *ds, *db;
+} orc_pool;
+
+/* One SwiGLU expert on one token (fused_moe.cpp:221-283; custom_kernel.py:263-339):
+ *   g = Wg x ; u = Wu x ; a = g * sigmoid(g) * u ; y = Wd a      (double) */
+static void expert_f64(const orc_pool* p, int slot, const double* x, int H, int I, int group, int bits, double* a,
+                       double* y) {
+    size_t gu_words = (size_t)H * bits / 32, gu_groups = (size_t)H / group;
+    size_t d_words = (size_t)I * bits / 32, d_groups = (size_t)I / group;
+    for (int r = 0; r < I; ++r) {
+        size_t row = (size_t)slot * I + r;
+        double g = 0.0, u = 0.0;
+        for (int c = 0; c < H; ++c) {
+            g += (double)deq(p->gw + row * gu_words, p->gs + row * gu_groups, p->gb + row * gu_groups, c, group, bits) * x[c];
+            u += (double)deq(p->uw + row * gu_words, p->us + row * gu_groups, p->ub + row * gu_groups, c, group, bits) * x[c];
+        }
+        a[r] = g * (1.0 / (1.0 + exp(-g))) * u;
+    }
+    for (int h = 0; h < H; ++h) {
+        size_t row = (size_t)slot * H + h;
+        double acc = 0.0;
+        for (int r = 0; r < I; ++r)
+            acc += (double)deq(p->dw + row * d_words, p->ds + row * d_groups, p->db + row * d_groups, r, group, bits) * a[r];
+        y[h] = acc;
+    }
+}
+
+/* fused_moe_slots (bindings.cpp:300-320; fused_moe.cpp:514-556, 635-664):
+ * x f32 [T, H]; local_slots [T*k] token-major (token = pair / k,
+ * fused_moe.cpp:235); scores f32 [T*k]; pool arrays [cap, out, in*bits/32] /
+ * [cap, out, in/group]; out f32 [T, H] = sum_j scores[t*k+j] * y[t*k+j] in
+ * fixed j order (reduce_pairs, fused_moe.cpp:284-298).  A slot outside
+ * [0, cap) is an error. */
+/* All pair outputs y[p] = expert(slots[p], x[p / k]) in parallel (double). */
+static int pairs_f64(const orc_pool* pool, const int32_t* slots, int npairs, int k, const double* xd, int H, int I,
+                     int group, int bits, double* y_all) {
+    int err = 0;
+#pragma omp parallel
+    {
+        double* a = (double*)malloc(sizeof(double) * I);
+        if (!a) {
+#pragma omp atomic write
+            err = 1;
+        } else {
+#pragma omp for schedule(dynamic, 1)
+            for (int p = 0; p < npairs; ++p)
+                expert_f64(pool, slots[p], xd + (size_t)(p / k) * H, H, I, group, bits, a, y_all + (size_t)p * H);
+            free(a);
+        }
+    }
+    return err ? ORC_ENOMEM : ORC_OK;
+}
+
+int orc_fused_moe_slots(const float* x, const int32_t* slots, const float* scores, const uint32_t* gw,
+                        const uint16_t* gs, const uint16_t* gb, const uint32_t* uw, const uint16_t* us,
+                        const uint16_t* ub, const uint32_t* dw, const uint16_t* ds, const uint16_t* db, int T, int k,
+                        int H, int I, int group, int bits, int cap, float* out) {
+    if (T <= 0 || k <= 0 || H % group || I % group || (H * bits) % 32 || (I * bits) % 32) return ORC_EINVAL;
+    for (int p = 0; p < T * k; ++p)
+        if (slots[p] < 0 || slots[p] >= cap) return ORC_ESLOT;
+    orc_pool pool = {gw, uw, dw, gs, gb, us, ub, ds, db};
+    double* xd = (double*)malloc(sizeof(double) * (size_t)T * H);
+    double* y = (double*)malloc(sizeof(double) * (size_t)T * k * H);
+    if (!xd || !y) { free(xd); free(y); return ORC_ENOMEM; }
+    for (size_t i = 0; i < (size_t)T * H; ++i) xd[i] = x[i];
+    int rc = pairs_f64(&pool, slots, T * k, k, xd, H, I, group, bits, y);
+    if (rc == ORC_OK) {
+        for (int t = 0; t < T; ++t)
+            for (int h = 0; h < H; ++h) {
+                double acc = 0.0;
+                for (int j = 0; j < k; ++j) acc += y[((size_t)t * k + j) * H + h] * (double)scores[t * k + j];
+                out[(size_t)t * H + h] = (float)acc;
+            }
+    }
+    free(xd); free(y);
+    return rc;
+}
+
+/* Pre-MoE RMSNorm (the decoder layer's post_attention_layernorm ahead of its
+ * MoE block; mlx rms_norm: x * rsqrt(mean(x^2) + eps) * w, output in bf16) in
+ * the GPU kernel's canonical order: lane l of 64 sums x^2 over columns
+ * [l*cpl, (l+1)*cpl) with fmaf in column order, then canon_sum64; the
+ * inverse rms is 1/sqrt(ss/H + eps) with correctly rounded sqrt and division;
+ * xn = bf16((x * inv) * w). */
+int orc_rmsnorm_bf16(const uint16_t* x_bf16, const uint16_t* w_bf16, float eps, int T, int H, uint16_t* out,
+                     float* inv_out) {
+    if (T <= 0 || H % 64 || (H / 64) % 8) return ORC_EINVAL;
+    int cpl = H / 64;
+    for (int t = 0; t < T; ++t) {
+        const uint16_t* xr = x_bf16 + (size_t)t * H;
+        float a[64];
+        for (int l = 0; l < 64; ++l) {
+            float ss = 0.0f;
+            for (int j = 0; j < cpl; ++j) {
+                float v = bf16_to_f32(xr[l * cpl + j]);
+                ss = fmaf(v, v, ss);
+            }
+            a[l] = ss;
+        }
+        float inv = 1.0f / sqrtf(canon_sum64(a) * (1.0f / (float)H) + eps);
+        if (inv_out) inv_out[t] = inv;
+        for (int c = 0; c < H; ++c)
+            out[(size_t)t * H + c] = orc_f32_to_bf16((bf16_to_f32(xr[c]) * inv) * bf16_to_f32(w_bf16[c]));
+    }
+    return ORC_OK;
+}
+
+/* Full MoE layer (FileStreamingMoeBlock.__call__, block.py:245-1013, production
+ * branch; shared expert block.py:102-109, :1009-1012):
+ *   xn = rmsnorm(x) when norm_w, else x       -> bf16, GPU order (bit-exact)
+ *   raw = router(xn) (+ logit_bias)           -> fp32, GPU order (bit-exact)
+ *   ids, scores = topk_softmax(raw)           -> block.py:321-329
+ *   local = slot_table[ids]                   -> resident_pool.py:549-580
+ *   y = sum_j scores_j * expert(local_j, xn)  -> block.py:1008
+ *   y += sigmoid(shared_gate(xn)) * shared(xn) -> block.py:102-109
+ *   out = bf16(y (+ x if residual))
+ * x is bf16 [T, H].  Outputs: out_f32 (pre-rounding), out_bf16, ids, scores,
+ * slots.  Returns ORC_ESLOT when the table maps a routed expert outside
+ * [0, cap). */
+int orc_moe_layer(const uint16_t* x_bf16, int T, int H, int I, int E, int k, int group, int norm_topk,
+                  const uint32_t* rw, const uint16_t* rs, const uint16_t* rb, int router_bits, const float* logit_bias,
+                  const int32_t* slot_table, int cap, const uint32_t* gw, const uint16_t* gs, const uint16_t* gb,
+                  const uint32_t* uw, const uint16_t* us, const uint16_t* ub, const uint32_t* dw, const uint16_t* ds,
+                  const uint16_t* db, int bits, const uint32_t* sh_gw, const uint16_t* sh_gs, const uint16_t* sh_gb,
+                  const uint32_t* sh_uw, const uint16_t* sh_us, const uint16_t* sh_ub, const uint32_t* sh_dw,
+                  const uint16_t* sh_ds, const uint16_t* sh_db, const uint32_t* sg_w, const uint16_t* sg_s,
+                  const uint16_t* sg_b, int sg_bits, const uint16_t* norm_w, float norm_eps, int residual,
+                  float* out_f32, uint16_t* out_bf16, int32_t* ids, float* scores, int32_t* slots) {
+    if (T <= 0 || k <= 0 || k > E || H % group || I % group) return ORC_EINVAL;
+    const uint16_t* x_raw = x_bf16;
+    uint16_t* xn = NULL;
+    if (norm_w) {
+        xn = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)T * H);
+        if (!xn) return ORC_ENOMEM;
+        int nrc = orc_rmsnorm_bf16(x_raw, norm_w, norm_eps, T, H, xn, NULL);
+        if (nrc) { free(xn); return nrc; }
+        x_bf16 = xn;
+    }
+    float* logits = (float*)malloc(sizeof(float) * (size_t)T * E);
+    if (!logits) { free(xn); return ORC_ENOMEM; }
+    int rc = orc_router_logits_f32(rw, rs, rb, logit_bias, E, H, group, router_bits, x_bf16, T, logits);
+    if (rc) { free(logits); free(xn); return rc; }
+    rc = orc_topk_softmax(logits, T, E, k, norm_topk, ids, scores);
+    free(logits);
+    if (rc) { free(xn); return rc; }
+    int bad = 0;
+    for (int p = 0; p < T * k; ++p) {
+        int e = ids[p];
+        int sl = slot_table ? slot_table[e] : e;
+        slots[p] = sl;
+        if (sl < 0 || sl >= cap) bad = 1;
+    }
+    if (bad) { free(xn); return ORC_ESLOT; }
+    orc_pool pool = {gw, uw, dw, gs, gb, us, ub, ds, db};
+    orc_pool shp = {sh_gw, sh_uw, sh_dw, sh_gs, sh_gb, sh_us, sh_ub, sh_ds, sh_db};
+    double* xd = (double*)malloc(sizeof(double) * (size_t)T * H);
+    double* y = (double*)malloc(sizeof(double) * (size_t)T * k * H);
+    double* ysh = (double*)malloc(sizeof(double) * (size_t)T * H);
+    if (!xd || !y || !ysh) { free(xd); free(y); free(ysh); free(xn); return ORC_ENOMEM; }
+    for (size_t i = 0; i < (size_t)T * H; ++i) xd[i] = bf16_to_f32(x_bf16[i]);
+    rc = pairs_f64(&pool, slots, T * k, k, xd, H, I, group, bits, y);
+    if (rc == ORC_OK && sh_gw) {
+        int32_t* zero = (int32_t*)calloc((size_t)T, sizeof(int32_t));
+        rc = zero ? pairs_f64(&shp, zero, T, 1, xd, H, I, group, bits, ysh) : ORC_ENOMEM;
+        free(zero);
+    }
+    if (rc == ORC_OK) {
+        for (int t = 0; t < T; ++t) {
+            const double* xt = xd + (size_t)t * H;
+            double gate = 1.0;
+            if (sh_gw && sg_w) {
+                double gl = 0.0;
+                for (int c = 0; c < H; ++c) gl += (double)deq(sg_w, sg_s, sg_b, c, group, sg_bits) * xt[c];
+                gate = 1.0 / (1.0 + exp(-gl));
+            }
+            for (int h = 0; h < H; ++h) {
+                double acc = 0.0;
+                for (int j = 0; j < k; ++j) acc += y[((size_t)t * k + j) * H + h] * (double)scores[t * k + j];
+                if (sh_gw) acc += gate * ysh[(size_t)t * H + h];
+                double v = acc + (residual ? (double)bf16_to_f32(x_raw[(size_t)t * H + h]) : 0.0);
+                if (out_f32) out_f32[(size_t)t * H + h] = (float)v;
+                if (out_bf16) out_bf16[(size_t)t * H + h] = orc_f32_to_bf16((float)v);
+            }
+        }
+    }
+    free(xd); free(y); free(ysh); free(xn);
+    return rc;
+}
+
+/* ------------------------------------------------- expert-major prefill */
+/* Group formation (block.py:141-172): per-expert counts of the flattened
+ * routes; walk experts in ascending id, skip empty ones, close a group when it
+ * already holds max_group_experts experts or adding the next expert would
+ * exceed max_assignments.  Writes group_start[g] (index into the expert list)
+ * and returns the number of groups; experts_out lists the non-empty experts in
+ * ascending order. */
+int orc_expert_major_groups(const int32_t* route_ids, int n_routes, int num_experts, int max_group_experts,
+                            int max_assignments, int32_t* counts, int32_t* experts_out, int32_t* n_experts_out,
+                            int32_t* group_start, int32_t* group_assign) {
+    if (n_routes < 0 || num_experts <= 0 || max_group_experts <= 0) return ORC_EINVAL;
+    for (int e = 0; e < num_experts; ++e) counts[e] = 0;
+    for (int i = 0; i < n_routes; ++i) {
+        if (route_ids[i] < 0 || route_ids[i] >= num_experts) return ORC_EINVAL;
+        counts[route_ids[i]]++;
+    }
+    int ng = 0, ne = 0, in_group = 0, assign = 0;
+    for (int e = 0; e < num_experts; ++e) {
+        if (counts[e] == 0) continue;
+        if (in_group && (in_group >= max_group_experts || assign + counts[e] > max_assignments)) {
+            group_assign[ng - 1] = assign;
+            in_group = 0;
+            assign = 0;
+        }
+        if (in_group == 0) group_start[ng++] = ne;
+        experts_out[ne++] = e;
+        in_group++;
+        assign += counts[e];
+    }
+    if (ng) group_assign[ng - 1] = assign;
+    *n_experts_out = ne;
+    return ng;
+}
+
+/* deterministic_route_reduce (custom_kernel.py:20-118): `assignment_pos` holds
+ * unique positions in the flattened [tokens, k] route table; rows of
+ * `weighted` belong to those positions.  Each touched token's new value is
+ * previous[token] followed by the values of its routes added one at a time in
+ * ascending route-rank order, rounding after every add (to bf16 when
+ * `bf16_acc`); untouched tokens keep `previous`.  In place on `out` (which
+ * holds previous on entry). */
+int orc_route_reduce(float* out, const float* weighted, const int32_t* assignment_pos, int n, int tokens, int hidden,
+                     int k, int bf16_acc) {
+    if (n < 0 || tokens <= 0 || hidden <= 0 || k <= 0) return ORC_EINVAL;
+    int32_t* order = (int32_t*)malloc(sizeof(int32_t) * (n > 0 ? n : 1));
+    if (!order) return ORC_ENOMEM;
+    for (int i = 0; i < n; ++i) order[i] = i;
+    /* insertion sort by position (positions are unique) */
+    for (int i = 1; i < n; ++i) {
+        int v = order[i], j = i - 1;
+        while (j >= 0 && assignment_pos[order[j]] > assignment_pos[v]) { order[j + 1] = order[j]; --j; }
+        order[j + 1] = v;
+    }
+    for (int i = 0; i < n; ++i) {
+        int pos = assignment_pos[order[i]];
+        if (pos < 0 || pos >= tokens * k) { free(order); return ORC_EINVAL; }
+    }
+    for (int i = 0; i < n; ++i) {
+        int row = order[i];
+        int tok = assignment_pos[row] / k;
+        for (int h = 0; h < hidden; ++h) {
+            float v = out[(size_t)tok * hidden + h] + weighted[(size_t)row * hidden + h];
+            if (bf16_acc) v = bf16_to_f32(orc_f32_to_bf16(v));
+            out[(size_t)tok * hidden + h] = v;
+        }
+    }
+    free(order);
+    return ORC_OK;
+}
+
+/* ----------------------------------------------------------- acceptance */
+/* accept_prefix (generate.py:338-351): longest prefix with preds[j]==drafts[j].
+ * Emission (generate.py:819, :850-856):
+ *   mode 0 (verify T=K: [x, d1..d_{K-1}]):  m<K -> drafts[:m]+[preds[m]];
+ *          m==K -> drafts[:K]; accepted_len = min(m+1, K)
+ *   mode 1 (verify T=K+1: [x, d1..dK]): drafts[:m]+[preds[m]] for m<=K;
+ *          accepted_len = m+1
+ * preds must hold K (mode 0) or K+1 (mode 1) entries. */
+int orc_accept_greedy(const int32_t* drafts, const int32_t* preds, int K, int mode, int32_t* emitted,
+                      int32_t* n_emitted, int32_t* matched, int32_t* accepted_len) {
+    if (K <= 0 || (mode != 0 && mode != 1)) return ORC_EINVAL;
+    int m = 0;
+    while (m < K && preds[m] == drafts[m]) ++m;
+    int n = 0;
+    for (int j = 0; j < m; ++j) emitted[n++] = drafts[j];
+    if (mode == 0) {
+        if (m < K) emitted[n++] = preds[m];
+        *accepted_len = (m + 1 < K) ? m + 1 : K;
+    } else {
+        emitted[n++] = preds[m];
+        *accepted_len = m + 1;
+    }
+    *n_emitted = n;
+    *matched = m;
+    return ORC_OK;
+}
+
+/* Greedy argmax over a row (ties -> lowest index; NaN ranks lowest). */
+int orc_argmax_rows(const float* logits, int rows, int V, int32_t* out) {
+    if (rows <= 0 || V <= 0) return ORC_EINVAL;
+    for (int r = 0; r < rows; ++r) {
+        const float* l = logits + (size_t)r * V;
+        int best = 0;
+        for (int v = 1; v < V; ++v)
+            if (better(l[v], v, l[best], best)) best = v;
+        out[r] = best;
+    }
+    return ORC_OK;
+}
+
+/* Tree verify selection (generate.py:355-420): P paths each of K drafts;
+ * preds [P, K]; winner = max matched, ties -> lowest path index
+ * (generate.py:383); emission as mode 0 on the winner. */
+int orc_accept_tree(const int32_t* paths, const int32_t* preds, int P, int K, int32_t* best_path, int32_t* emitted,
+                    int32_t* n_emitted, int32_t* matched, int32_t* accepted_len) {
+    if (P <= 0 || K <= 0) return ORC_EINVAL;
+    int best = 0, bm = -1;
+    for (int p = 0; p < P; ++p) {
+        int m = 0;
+        while (m < K && preds[p * K + m] == paths[p * K + m]) ++m;
+        if (m > bm) { bm = m; best = p; }
+    }
+    *best_path = best;
+    return orc_accept_greedy(paths + best * K, preds + best * K, K, 0, emitted, n_emitted, matched, accepted_len);
+}
+
+int orc_version(void) { return 1; }

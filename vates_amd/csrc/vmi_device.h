@@ -1,0 +1,171 @@
+// Device-side helpers shared by the libvmi kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 vmi_half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 vmi_bf8 __attribute__((ext_vector_type(8)));
+typedef float vmi_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vmi_u4 __attribute__((ext_vector_type(4)));
+
+#define VMI_WAVE 64
+
+__device__ __forceinline__ float vmi_bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 bit pattern (quiet NaN kept).
+__device__ __forceinline__ uint16_t vmi_f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t vmi_h2_bits(_Float16 lo, _Float16 hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+// 16x16x32 f16 MFMA: D[i][j] += sum_k A[i][k] B[k][j].  Lane l supplies
+// A[l%16][8*(l/16)+s] and B[8*(l/16)+s][l%16] (s = 0..7) and holds
+// D[4*(l/16)+r][l%16] (r = 0..3).
+__device__ __forceinline__ vmi_f4 vmi_mfma_f16(const vmi_u4& a, const vmi_u4& b, const vmi_f4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vmi_half8, a), __builtin_bit_cast(vmi_half8, b),
+                                                   c, 0, 0, 0);
+}
+__device__ __forceinline__ vmi_f4 vmi_mfma_bf16(const vmi_u4& a, const vmi_u4& b, const vmi_f4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(vmi_bf8, a), __builtin_bit_cast(vmi_bf8, b), c,
+                                                    0, 0, 0);
+}
+
+// Eight 4-bit values of one packed word as MFMA f16 operands, exactly:
+// halves are fp16 subnormals n * 2^-24 (n in bits 0-3) or n * 2^-20 (bits 4-7).
+//   r0 = (n0, n4) * 2^-24      r1 = (n1, n5) * 2^-20
+//   r2 = (n2, n6) * 2^-24      r3 = (n3, n7) * 2^-20
+// so operand slot s holds column perm[s] = {0,4,1,5,2,6,3,7}[s], scaled by 16
+// for s in {2,3,6,7}; the matching activation operand divides those slots by 16.
+__device__ __forceinline__ vmi_u4 vmi_unpack_u4_f16(uint32_t w) {
+    vmi_u4 r;
+    r[0] = w & 0x000F000Fu;
+    r[1] = w & 0x00F000F0u;
+    uint32_t t = w >> 8;
+    r[2] = t & 0x000F000Fu;
+    r[3] = t & 0x00F000F0u;
+    return r;
+}
+
+// ---------------------------------------------------------------- DPP
+// Row permutes of gfx9 DPP: xor 1 and xor 2 inside quads, mirror inside
+// 8-lane half rows and 16-lane rows.  A reduction through the four leaves
+// every lane of a 16-lane row holding the row result; the four rows then
+// meet through readlane (uniform, no LDS traffic).
+#define VMI_DPP_XOR1 0xB1
+#define VMI_DPP_XOR2 0x4E
+#define VMI_DPP_HALF_MIRROR 0x141
+#define VMI_DPP_MIRROR 0x140
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t vmi_dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float vmi_dpp_f32(float v) {
+    return __uint_as_float(vmi_dpp_u32<CTRL>(__float_as_uint(v)));
+}
+__device__ __forceinline__ float vmi_readlane_f32(float v, int lane) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
+}
+
+// Wave sum in the canonical tree shared with the CPU oracle: per 16-lane row
+// v += v[l^1]; v += v[l^2]; v += v[half-mirror]; v += v[mirror]; then
+// (R0 + R1) + (R2 + R3) over the rows.  Uniform result.
+__device__ __forceinline__ float vmi_wave_sum_canon(float v) {
+    v = v + vmi_dpp_f32<VMI_DPP_XOR1>(v);
+    v = v + vmi_dpp_f32<VMI_DPP_XOR2>(v);
+    v = v + vmi_dpp_f32<VMI_DPP_HALF_MIRROR>(v);
+    v = v + vmi_dpp_f32<VMI_DPP_MIRROR>(v);
+    const float r0 = vmi_readlane_f32(v, 0), r1 = vmi_readlane_f32(v, 16);
+    const float r2 = vmi_readlane_f32(v, 32), r3 = vmi_readlane_f32(v, 48);
+    return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ float vmi_wave_max(float v) {
+    v = fmaxf(v, vmi_dpp_f32<VMI_DPP_XOR1>(v));
+    v = fmaxf(v, vmi_dpp_f32<VMI_DPP_XOR2>(v));
+    v = fmaxf(v, vmi_dpp_f32<VMI_DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, vmi_dpp_f32<VMI_DPP_MIRROR>(v));
+    const float r0 = vmi_readlane_f32(v, 0), r1 = vmi_readlane_f32(v, 16);
+    const float r2 = vmi_readlane_f32(v, 32), r3 = vmi_readlane_f32(v, 48);
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ uint64_t vmi_u64_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t vmi_dpp_u64(uint64_t v) {
+    const uint32_t lo = vmi_dpp_u32<CTRL>((uint32_t)v), hi = vmi_dpp_u32<CTRL>((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t vmi_readlane_u64(uint64_t v, int lane) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Wave-wide maximum of a 64-bit key (uniform result).
+__device__ __forceinline__ uint64_t vmi_wave_max_u64(uint64_t v) {
+    v = vmi_u64_max(v, vmi_dpp_u64<VMI_DPP_XOR1>(v));
+    v = vmi_u64_max(v, vmi_dpp_u64<VMI_DPP_XOR2>(v));
+    v = vmi_u64_max(v, vmi_dpp_u64<VMI_DPP_HALF_MIRROR>(v));
+    v = vmi_u64_max(v, vmi_dpp_u64<VMI_DPP_MIRROR>(v));
+    return vmi_u64_max(vmi_u64_max(vmi_readlane_u64(v, 0), vmi_readlane_u64(v, 16)),
+                       vmi_u64_max(vmi_readlane_u64(v, 32), vmi_readlane_u64(v, 48)));
+}
+
+// Order key of a float for "larger value first, NaN last": -0 is folded
+// into +0, NaN maps to 0 (below -inf).
+__device__ __forceinline__ uint32_t vmi_order_key(float f) {
+    if (f != f) return 0u;
+    uint32_t u = __float_as_uint(f);
+    if (u == 0x80000000u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float vmi_order_key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+// 64-bit rank key: value order, then lower index first.
+__device__ __forceinline__ uint64_t vmi_rank_key(float f, int idx) {
+    return ((uint64_t)vmi_order_key(f) << 32) | (uint32_t)(0xffffffffu - (uint32_t)idx);
+}
+
+// Power-of-two factor f with max|x| * f in (2^13, 2^14]; 1 for zero / non-finite.
+__device__ __forceinline__ float vmi_fp16_range_scale(float amax) {
+    if (!(amax > 0.0f) || !(amax < 3.0e38f)) return 1.0f;
+    int e;
+    frexpf(amax, &e);  // amax = m * 2^e, m in [0.5, 1)
+    return ldexpf(1.0f, 14 - e);
+}
+
+// Strict total order used for top-k and argmax: larger value first, then lower
+// index; NaN ranks below every number.
+__device__ __forceinline__ bool vmi_better(float a, int ia, float b, int ib) {
+    bool na = a != a, nb = b != b;
+    if (na != nb) return nb;
+    if (!na && a != b) return a > b;
+    return ia < ib;
+}
+
+// ---------------------------------------------------------- buffer loads
+// Raw buffer resource over [base, base + bytes): loads past `bytes` return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t vmi_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint2 vmi_bload_b64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t vmi_bload_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+__device__ __forceinline__ uint32_t vmi_bload_b16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}

@@ -1,0 +1,105 @@
+"""Synthetic Qwen3-Next-shaped MoE layers resident in HBM.
+
+A layer holds an 8-bit router [E, H], a pool of ``cap`` 4-bit SwiGLU experts
+(gate/up [cap, I, H], down [cap, H, I]), a 4-bit shared expert, an 8-bit
+shared-expert gate [1, H], an expert->slot table (a seeded permutation when
+cap == E, as the resident pool's table in resident_pool.py:549-580) and an
+optional per-expert router logit bias ``alpha * log z(e)`` where z is a
+Zipf(s) pmf over a seeded expert ranking, which skews routing the way real
+expert popularity does.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+import torch
+
+from .moe import MoELayer, QuantizedProj
+from .synth import synth_proj
+
+# stream ids of one layer's tensors: layer * 16 + index
+_ROUTER, _GATE, _UP, _DOWN, _SH_GATE, _SH_UP, _SH_DOWN, _SGATE = range(8)
+
+
+@dataclass
+class LayerWeights:
+    router: QuantizedProj
+    gate: QuantizedProj
+    up: QuantizedProj
+    down: QuantizedProj
+    sh_gate: QuantizedProj
+    sh_up: QuantizedProj
+    sh_down: QuantizedProj
+    sgate: QuantizedProj
+    table: Optional[torch.Tensor]
+    bias: Optional[torch.Tensor]
+    norm: Optional[torch.Tensor]
+    hidden: int
+    inter: int
+    num_experts: int
+    router_bits: int
+    sgate_bits: int
+
+
+def zipf_bias(seed: int, layer: int, num_experts: int, s: float, alpha: float) -> np.ndarray:
+    """alpha * log z(e), z = Zipf(s) pmf over a seeded ranking of the experts."""
+    rng = np.random.default_rng([seed, layer, 0x21BF])
+    rank = rng.permutation(num_experts)
+    z = 1.0 / np.arange(1, num_experts + 1, dtype=np.float64) ** s
+    z /= z.sum()
+    bias = np.empty(num_experts, dtype=np.float32)
+    bias[rank] = (alpha * np.log(z)).astype(np.float32)
+    return bias
+
+
+def norm_weight(seed: int, layer: int, hidden: int) -> np.ndarray:
+    """RMSNorm weight as bf16 bit patterns: 1 + N(0, 0.1^2), rounded to nearest even."""
+    rng = np.random.default_rng([seed, layer, 0x4E0A])
+    w = (1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    u = w.view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def slot_permutation(seed: int, layer: int, num_experts: int) -> np.ndarray:
+    rng = np.random.default_rng([seed, layer, 0x5107])
+    return rng.permutation(num_experts).astype(np.int32)
+
+
+def synth_layer(seed: int, layer: int, *, hidden: int = 2048, inter: int = 512, num_experts: int = 512,
+                cap: Optional[int] = None, router_bits: int = 8, sgate_bits: int = 8, std: float = 0.02,
+                zipf_s: float = 1.1, zipf_alpha: float = 0.0, permute_slots: bool = True, with_norm: bool = True,
+                device=None) -> LayerWeights:
+    cap = num_experts if cap is None else cap
+    device = torch.device(device or "cuda")
+    base = layer * 16
+    mk = lambda idx, n, o, i, bits=4: synth_proj(seed, base + idx, n, o, i, bits=bits, std=std, device=device)
+    router = mk(_ROUTER, 1, num_experts, hidden, router_bits)
+    gate = mk(_GATE, cap, inter, hidden)
+    up = mk(_UP, cap, inter, hidden)
+    down = mk(_DOWN, cap, hidden, inter)
+    sh_gate = mk(_SH_GATE, 1, inter, hidden)
+    sh_up = mk(_SH_UP, 1, inter, hidden)
+    sh_down = mk(_SH_DOWN, 1, hidden, inter)
+    sgate = mk(_SGATE, 1, 1, hidden, sgate_bits)
+    table = None
+    if permute_slots and cap == num_experts:
+        table = torch.from_numpy(slot_permutation(seed, layer, num_experts)).to(device)
+    elif cap != num_experts:
+        table = torch.from_numpy((np.arange(num_experts) % cap).astype(np.int32)).to(device)
+    bias = None
+    if zipf_alpha:
+        bias = torch.from_numpy(zipf_bias(seed, layer, num_experts, zipf_s, zipf_alpha)).to(device)
+    norm = None
+    if with_norm:
+        norm = torch.from_numpy(norm_weight(seed, layer, hidden).view(np.int16)).to(device).view(torch.bfloat16)
+    return LayerWeights(router, gate, up, down, sh_gate, sh_up, sh_down, sgate, table, bias, norm, hidden, inter,
+                        num_experts, router_bits, sgate_bits)
+
+
+def make_layer(w: LayerWeights, top_k: int = 10, norm_topk_prob: bool = True) -> MoELayer:
+    return MoELayer(w.router, w.gate, w.up, w.down, top_k=top_k, norm_topk_prob=norm_topk_prob,
+                    router_bits=w.router_bits, shared_gate=w.sh_gate, shared_up=w.sh_up, shared_down=w.sh_down,
+                    shared_expert_gate=w.sgate, shared_expert_gate_bits=w.sgate_bits, slot_table=w.table,
+                    router_logit_bias=w.bias, norm_weight=w.norm)
