@@ -98,6 +98,19 @@ __device__ __forceinline__ float vmi_wave_max(float v) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Wave-wide maximum of an unsigned 32-bit value (uniform result).
+__device__ __forceinline__ uint32_t vmi_wave_max_u32(uint32_t v) {
+    v = max(v, vmi_dpp_u32<VMI_DPP_XOR1>(v));
+    v = max(v, vmi_dpp_u32<VMI_DPP_XOR2>(v));
+    v = max(v, vmi_dpp_u32<VMI_DPP_HALF_MIRROR>(v));
+    v = max(v, vmi_dpp_u32<VMI_DPP_MIRROR>(v));
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
 __device__ __forceinline__ uint64_t vmi_u64_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 template <int CTRL>
@@ -158,6 +171,18 @@ __device__ __forceinline__ bool vmi_better(float a, int ia, float b, int ib) {
 // Raw buffer resource over [base, base + bytes): loads past `bytes` return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t vmi_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// Raw-buffer range checks use the per-lane offset: a lane whose offset is
+// VMI_OOB reads zeros without touching memory.
+#define VMI_OOB 0x80000000u
+__device__ __forceinline__ vmi_u4 vmi_bload_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    vmi_u4 o;
+    o[0] = v[0];
+    o[1] = v[1];
+    o[2] = v[2];
+    o[3] = v[3];
+    return o;
 }
 __device__ __forceinline__ uint2 vmi_bload_b64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);

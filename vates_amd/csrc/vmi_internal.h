@@ -19,29 +19,28 @@ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 constexpr int kRouteMaxPairs = 160;
 constexpr int kRouteMaxT = 16;
 
-// Distinct-slot table of one verify batch, written by one workgroup.
+// Routing of one verify batch as the down/combine kernel reads it, written by
+// one workgroup of the gate/up kernel.
 struct RouteInfo {
-    int32_t U;                                  // distinct valid slots
-    int32_t uslot[kRouteMaxPairs];              // slot of distinct index u
-    uint32_t umask[kRouteMaxPairs];             // tokens routed to u
-    int16_t upair[kRouteMaxPairs][kRouteMaxT];  // first pair (t*k+j) of (u, t), -1 if none
-    int32_t psrc[kRouteMaxPairs];               // pair whose partial output serves pair p, -1 if invalid
+    int32_t U;                               // distinct valid slots
+    int32_t uslot[kRouteMaxPairs];           // slot of distinct index u (first-appearance order)
+    float wt[kRouteMaxPairs][kRouteMaxT];    // combine weight of (u, token): sum of its pairs' scores
 };
 
-// Workspace carve-up shared by vmi_fused_moe_slots and vmi_moe_layer.
+// Workspace carve-up shared by vmi_fused_moe_slots and vmi_moe_layer.  Expert
+// activations are indexed by distinct slot u < T*k; index T*k is the shared
+// expert.
 struct MoeWorkspace {
     uint32_t* status;     // device status word (VMI_STATUS_*)
     RouteInfo* route;
     float* logits;        // [T, E]
     float* sg_logit;      // [T]
-    float* sg;            // [T]
-    int32_t* ids;         // [T*k]
-    float* scores;        // [T*k]
-    int32_t* slots;       // [T*k]
-    uint32_t __attribute__((ext_vector_type(4)))* xop;  // [T, H/64, 4, 2] MFMA operands
-    float* xsum;          // [T, H/64]
-    float* fscale;        // [T]
-    float* part;          // [T*k + T, inter/64, hidden] per-slice partial outputs
+    uint32_t __attribute__((ext_vector_type(4)))* xop;    // [T, H/8] MFMA operands of the MoE input
+    float* xsum;          // [T, H/64] per-group sums of those operands
+    float* fscale;        // [T] power-of-two range factor of the operands
+    uint32_t __attribute__((ext_vector_type(4)))* actop;  // [T*k+1, T, I/8] down-projection operands
+    float* axs;           // [T*k+1, T, I/64] per-group activation sums
+    float* aifa;          // [T*k+1, I/64, 16] inverse range factor per group and token
     size_t bytes;
 };
 
