@@ -53,6 +53,19 @@ __device__ __forceinline__ vmi_u4 vmi_unpack_u4_f16(uint32_t w) {
     return r;
 }
 
+// Eight 4-bit values of one packed word as bf16 MFMA operands (128 + n),
+// exact, in the same slot order as vmi_unpack_u4_f16 (columns
+// {0,4,1,5,2,6,3,7}); the 128 * sum(activation) excess is removed by the
+// caller.  bf16 0x4300 is 128.0 with a mantissa step of 1.
+__device__ __forceinline__ vmi_u4 vmi_unpack_u4_bf16_128(uint32_t w) {
+    vmi_u4 r;
+    r[0] = (w & 0x000F000Fu) | 0x43004300u;
+    r[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+    r[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+    r[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+    return r;
+}
+
 // ---------------------------------------------------------------- DPP
 // Row permutes of gfx9 DPP: xor 1 and xor 2 inside quads, mirror inside
 // 8-lane half rows and 16-lane rows.  A reduction through the four leaves
@@ -166,6 +179,19 @@ __device__ __forceinline__ bool vmi_better(float a, int ia, float b, int ib) {
     if (!na && a != b) return a > b;
     return ia < ib;
 }
+
+// ------------------------------------------------------- direct-to-LDS loads
+// global_load_lds: lane l's `size` bytes from its own global address land at
+// lds + size*l (lds is wave-uniform); vmcnt counts the copy until the bytes are
+// in LDS.  The 16-byte form exists on gfx950 only, so the host pass (which
+// never runs kernel code) sees an empty statement.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define VMI_LDS_DMA16(g, lds) __builtin_amdgcn_global_load_lds((const void*)(g), (lds), 16, 0, 0)
+#define VMI_LDS_DMA4(g, lds) __builtin_amdgcn_global_load_lds((const void*)(g), (lds), 4, 0, 0)
+#else
+#define VMI_LDS_DMA16(g, lds) ((void)0)
+#define VMI_LDS_DMA4(g, lds) ((void)0)
+#endif
 
 // ---------------------------------------------------------- buffer loads
 // Raw buffer resource over [base, base + bytes): loads past `bytes` return 0.

@@ -38,9 +38,8 @@ struct MoeWorkspace {
     uint32_t __attribute__((ext_vector_type(4)))* xop;    // [T, H/8] MFMA operands of the MoE input
     float* xsum;          // [T, H/64] per-group sums of those operands
     float* fscale;        // [T] power-of-two range factor of the operands
-    uint32_t __attribute__((ext_vector_type(4)))* actop;  // [T*k+1, T, I/8] down-projection operands
+    uint32_t __attribute__((ext_vector_type(4)))* actop;  // [T*k+1, T, I/8] bf16 down-projection operands
     float* axs;           // [T*k+1, T, I/64] per-group activation sums
-    float* aifa;          // [T*k+1, I/64, 16] inverse range factor per group and token
     size_t bytes;
 };
 

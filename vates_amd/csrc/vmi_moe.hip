@@ -2,10 +2,10 @@
 //
 // Three stream-ordered kernels per layer; kernel boundaries carry every
 // cross-workgroup dependency (no fences, no counters, no spin waits):
-//   k_router    router logits, one wave per two router rows: the optional
-//               pre-MoE RMSNorm is computed once per workgroup into LDS, the
-//               logit accumulates in a fixed fp32 order (bit-identical to the
-//               CPU oracle).  T extra workgroups write the MoE input once in
+//   k_router    router logits, one wave per router row: the optional pre-MoE
+//               RMSNorm is computed once per workgroup into LDS, the logit
+//               accumulates in a fixed fp32 order (bit-identical to the CPU
+//               oracle).  The first T workgroups also write the MoE input in
 //               MFMA operand order.
 //   k_gateup    one workgroup per (distinct slot, 64-row slice of the
 //               intermediate dimension), shared-expert slices first.  Every
@@ -37,8 +37,6 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kDownWaves = 8;
-constexpr int kDownThreads = kDownWaves * VMI_WAVE;
 constexpr int kMaxT = 16;
 constexpr int kMaxPairs = 160;
 constexpr int kMaxK = 16;
@@ -46,12 +44,16 @@ constexpr int kMaxE = 1024;
 constexpr int kSlice = 64;        // intermediate rows per k_gateup workgroup (= one down group)
 constexpr int kMaxInter = 512;
 constexpr int kFirstTable = 1024; // LDS first-occurrence table covers cap <= 1024
-constexpr int kTPad = 16;         // token stride of the per-group inverse range factors
 constexpr float kTwo24 = 16777216.0f;
 
 static_assert(kMaxPairs == vmi::kRouteMaxPairs && kMaxT == vmi::kRouteMaxT, "route table sizes");
 
 using vmi::RouteInfo;
+
+// Wave index within the workgroup as a scalar (uniform) value, so values and
+// buffer descriptors derived from it stay in SGPRs.
+__device__ __forceinline__ int vmi_wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+__device__ __forceinline__ int vmi_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 __device__ __forceinline__ float vmi_bf16r(float v) { return vmi_bf16_to_f32(vmi_f32_to_bf16(v)); }
 
@@ -163,7 +165,7 @@ __device__ void write_operands(const XT* __restrict__ xrow, const uint16_t* __re
                                int t, const OperandOut& o) {
     __shared__ float s_red[kThreads / VMI_WAVE];
     __shared__ float s_inv;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     constexpr int kChunksPerThread = (64 * CPL) / (8 * kThreads) > 0 ? (64 * CPL) / (8 * kThreads) : 1;
     const bool active = 8 * tid < H;
     float v[kChunksPerThread][8];
@@ -243,66 +245,131 @@ struct RouterArgs {
     const float* bias;
     vmi_qmat sgate;
     int sgbits, has_sgate;
-    int row_wgs;      // workgroups carrying router rows
+    int row_wgs;      // workgroups (four router rows each)
     float* logits;    // [T, E]
     float* sg_logit;  // [T]
     OperandOut ops;
 };
 
-constexpr int kRouterRowsPerWave = 2;
+// MFMA operands of token t from its (normalised) input held in LDS as packed
+// bf16 chunks xn[j] = columns 8j..8j+7 (all 256 threads of the workgroup):
+// the same values, range factor and group sums as write_operands.
+__device__ void operands_from_lds(const uint4* __restrict__ xn, int H, int t, const OperandOut& o) {
+    __shared__ float s_am[kThreads / VMI_WAVE];
+    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
+    const bool active = 8 * tid < H;  // H <= 2048: at most one chunk per thread
+    float v[8];
+    if (active) {
+        unpack_bf16x8(xn[tid], v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = vmi_wave_max(amax);
+    if (lane == 0) s_am[w] = amax;
+    __syncthreads();
+    float am = s_am[0];
+#pragma unroll
+    for (int i = 1; i < kThreads / VMI_WAVE; ++i) am = fmaxf(am, s_am[i]);
+    const float f = vmi_fp16_range_scale(am);
+    float xs = 0.0f;
+    const vmi_u4 op = make_act_operand(v, f, xs);
+    xs += __shfl_xor(xs, 1, VMI_WAVE);
+    xs += __shfl_xor(xs, 2, VMI_WAVE);
+    xs += __shfl_xor(xs, 4, VMI_WAVE);
+    if (active) {
+        o.xop[(size_t)t * (H / 8) + tid] = op;
+        if ((tid & 7) == 0) o.xsum[(size_t)t * (H / 64) + tid / 8] = xs;
+    }
+    if (tid == 0) o.fscale[t] = f;
+}
 
-// Router rows: wave w of workgroup b takes rows 2(4b + w) and 2(4b + w) + 1
-// (row E is the shared-expert gate).  Lane l owns columns [l*CPL, (l+1)*CPL),
-// accumulating fmaf(w, x, acc) in column order; the 64 partials meet in the
-// canonical wave-sum tree.  The (normalised) input is built once per
-// workgroup in LDS: wave w normalises tokens w, w+4, ...  The CPU oracle
-// reproduces this order bit for bit (orc_router_logits_f32).  Workgroups past
-// row_wgs each write one token's MFMA operands.
+// Router rows: wave w of workgroup b takes row 4b + w (row E is the
+// shared-expert gate).  Lane l owns columns [l*CPL, (l+1)*CPL), accumulating
+// fmaf(w, x, acc) in column order; the 64 partials meet in the canonical
+// wave-sum tree.  The (normalised) input is built once per workgroup in LDS:
+// wave w normalises tokens w, w+4, ...  The CPU oracle reproduces this order
+// bit for bit (orc_router_logits_f32).  Workgroup b < T also writes token b's
+// MFMA operands from that LDS copy.
 template <int CPL>
 __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     constexpr int NCH = CPL / 8;  // packed 8-column chunks per lane
-    constexpr int RPW = kRouterRowsPerWave;
     __shared__ uint4 s_xn[kMaxT][64 * NCH];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     const int T = a.T, H = a.H;
-    if ((int)blockIdx.x >= a.row_wgs) {
-        const int t = blockIdx.x - a.row_wgs;
-        write_operands<uint16_t, CPL>(a.x + (size_t)t * H, a.norm_w, a.eps, H, t, a.ops);
-        return;
-    }
     const int G = H / 64;
     const int c0 = lane * CPL;
-    const int row0 = (blockIdx.x * (kThreads / VMI_WAVE) + w) * RPW;
+    const int row = blockIdx.x * (kThreads / VMI_WAVE) + w;
     const int nrows = a.E + a.has_sgate;
-    const bool is_sg = row0 >= a.E;  // E is even: a wave holds router rows only or the gate row only
+    const bool row_ok = row < nrows;
+    const bool is_sg = row >= a.E;  // wave-uniform
     const vmi_qmat m = is_sg ? a.sgate : a.router;
     const int bits = is_sg ? a.sgbits : a.rbits;
-    // weights: 8-bit -> CPL/4 words, 4-bit -> CPL/8 words of this lane's columns
-    uint32_t wword[RPW][CPL / 4];
-    uint16_t sv[RPW], bv[RPW];
+    const int r = is_sg ? 0 : row;
+    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+    // first the input of this wave's first token and the norm weights (the
+    // normalisation needs them), then the router row; the compiler barrier
+    // keeps that issue order (loads retire in order)
+    const __amdgpu_buffer_rsrc_t rx = vmi_rsrc(a.x, (uint32_t)T * H * 2u);
+    const __amdgpu_buffer_rsrc_t rn = vmi_rsrc(a.norm_w ? a.norm_w : a.x, a.norm_w ? (uint32_t)H * 2u : 0u);
+    uint4 xr0[NCH], nwv[NCH];
 #pragma unroll
-    for (int k = 0; k < RPW; ++k) {
-        const int row = row0 + k;
-        const bool ok = row < nrows;
-        const int r = ok ? (is_sg ? 0 : row) : 0;
-        const uint32_t* wrow = m.w + (size_t)r * (size_t)(H * bits / 32) + (size_t)c0 * bits / 32;
-#pragma unroll
-        for (int i = 0; i < CPL / 4; ++i) wword[k][i] = (ok && (bits == 8 || i < CPL / 8)) ? wrow[i] : 0u;
-        sv[k] = ok ? m.s[(size_t)r * G + c0 / 64] : (uint16_t)0;
-        bv[k] = ok ? m.b[(size_t)r * G + c0 / 64] : (uint16_t)0;
+    for (int ch = 0; ch < NCH; ++ch) {
+        const vmi_u4 xv = vmi_bload_b128(rx, (w < T) ? (uint32_t)(w * H + c0 + 8 * ch) * 2u : VMI_OOB, 0);
+        const vmi_u4 nv = vmi_bload_b128(rn, (uint32_t)(c0 + 8 * ch) * 2u, 0);
+        xr0[ch] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+        nwv[ch] = make_uint4(nv[0], nv[1], nv[2], nv[3]);
     }
+    asm volatile("" ::: "memory");
+    // weights: 8-bit -> CPL/4 words, 4-bit -> CPL/8 words of this lane's columns
+    const uint32_t row_words = (uint32_t)(H * bits / 32);
+    const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(m.w + (size_t)r * row_words, row_ok ? row_words * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rs = vmi_rsrc(m.s + (size_t)r * G, row_ok ? (uint32_t)G * 2u : 0u);
+    const __amdgpu_buffer_rsrc_t rb = vmi_rsrc(m.b + (size_t)r * G, row_ok ? (uint32_t)G * 2u : 0u);
+    const uint32_t wbase = (uint32_t)(c0 * bits / 32) * 4u;
+    const int nwords = CPL * bits / 32;  // words of this lane's columns: 1, 2, 4 or 8 (wave-uniform)
+    uint32_t wword[CPL / 4];
+#pragma unroll
+    for (int i = 0; i < CPL / 4; ++i) wword[i] = 0u;
+    if (nwords >= 4) {
+#pragma unroll
+        for (int i = 0; i < (CPL / 16 > 0 ? CPL / 16 : 1); ++i) {
+            const vmi_u4 q = vmi_bload_b128(rw, (4 * i < nwords) ? wbase + 16u * i : VMI_OOB, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (4 * i + j < CPL / 4) wword[4 * i + j] = q[j];
+        }
+    } else if (nwords == 2) {
+        const uint2 q = vmi_bload_b64(rw, wbase, 0);
+        wword[0] = q.x;
+        wword[1] = q.y;
+    } else {
+        wword[0] = vmi_bload_b32(rw, wbase, 0);
+    }
+    const uint32_t sv = vmi_bload_b16(rs, (uint32_t)(c0 / 64) * 2u, 0);
+    const uint32_t bv = vmi_bload_b16(rb, (uint32_t)(c0 / 64) * 2u, 0);
     // the MoE input, normalised, for every token into LDS
     for (int t = w; t < T; t += kThreads / VMI_WAVE) {
         uint4 xr[NCH];
 #pragma unroll
-        for (int ch = 0; ch < NCH; ++ch) xr[ch] = *reinterpret_cast<const uint4*>(a.x + (size_t)t * H + c0 + 8 * ch);
+        for (int ch = 0; ch < NCH; ++ch) {
+            if (t == w) {
+                xr[ch] = xr0[ch];
+            } else {
+                const vmi_u4 xv = vmi_bload_b128(rx, (uint32_t)(t * H + c0 + 8 * ch) * 2u, 0);
+                xr[ch] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+            }
+        }
         if (a.norm_w) {
             const float inv = canonical_inv_rms<NCH>(xr, H, a.eps);
 #pragma unroll
             for (int ch = 0; ch < NCH; ++ch) {
                 float xf[8], nw[8];
                 unpack_bf16x8(xr[ch], xf);
-                unpack_bf16x8(*reinterpret_cast<const uint4*>(a.norm_w + c0 + 8 * ch), nw);
+                unpack_bf16x8(nwv[ch], nw);
                 uint32_t pk[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
@@ -315,47 +382,37 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
         for (int ch = 0; ch < NCH; ++ch) s_xn[t][lane * NCH + ch] = xr[ch];
     }
     __syncthreads();
-    if (row0 >= nrows) return;
-    // dequantised weights (w = q*s + b is exact in fp32)
-    float wv[RPW][CPL];
-#pragma unroll
-    for (int k = 0; k < RPW; ++k) {
-        const float sc = vmi_bf16_to_f32(sv[k]), bi = vmi_bf16_to_f32(bv[k]);
+    if (row_ok) {
+        // dequantised weights (w = q*s + b is exact in fp32)
+        float wv[CPL];
+        const float sc = vmi_bf16_to_f32(sv), bi = vmi_bf16_to_f32(bv);
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
-            const uint32_t qv = (bits == 4) ? (wword[k][c / 8] >> (4 * (c % 8))) & 15u
-                                            : (wword[k][c / 4] >> (8 * (c % 4))) & 255u;
-            wv[k][c] = fmaf((float)qv, sc, bi);
+            const uint32_t qv = (bits == 4) ? (wword[c / 8] >> (4 * (c % 8))) & 15u
+                                            : (wword[c / 4] >> (8 * (c % 4))) & 255u;
+            wv[c] = fmaf((float)qv, sc, bi);
         }
-    }
-    for (int t = 0; t < T; ++t) {
-        // chunk reads rotated by lane/4 (4 chunks) or lane/8 (2 chunks) to spread LDS banks
-        uint4 xr[NCH];
+        for (int t = 0; t < T; ++t) {
+            // chunk reads rotated by lane/4 (4 chunks) or lane/8 (2 chunks) to spread LDS banks
+            uint4 xr[NCH];
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const int ch = (NCH == 1) ? 0 : ((i + (NCH == 4 ? (lane >> 2) : (lane >> 3))) & (NCH - 1));
-            const uint4 v = s_xn[t][lane * NCH + ch];
+            for (int i = 0; i < NCH; ++i) {
+                const int ch = (NCH == 1) ? 0 : ((i + (NCH == 4 ? (lane >> 2) : (lane >> 3))) & (NCH - 1));
+                const uint4 v = s_xn[t][lane * NCH + ch];
 #pragma unroll
-            for (int cc = 0; cc < NCH; ++cc)
-                if (cc == ch) xr[cc] = v;
-        }
-        float acc[RPW];
+                for (int cc = 0; cc < NCH; ++cc)
+                    if (cc == ch) xr[cc] = v;
+            }
+            float acc = 0.0f;
 #pragma unroll
-        for (int k = 0; k < RPW; ++k) acc[k] = 0.0f;
+            for (int ch = 0; ch < NCH; ++ch) {
+                float xf[8];
+                unpack_bf16x8(xr[ch], xf);
 #pragma unroll
-        for (int ch = 0; ch < NCH; ++ch) {
-            float xf[8];
-            unpack_bf16x8(xr[ch], xf);
-#pragma unroll
-            for (int k = 0; k < RPW; ++k)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc[k] = fmaf(wv[k][8 * ch + i], xf[i], acc[k]);
-        }
-#pragma unroll
-        for (int k = 0; k < RPW; ++k) {
-            float v = vmi_wave_sum_canon(acc[k]);
-            const int row = row0 + k;
-            if (lane == 0 && row < nrows) {
+                for (int i = 0; i < 8; ++i) acc = fmaf(wv[8 * ch + i], xf[i], acc);
+            }
+            float v = vmi_wave_sum_canon(acc);
+            if (lane == 0) {
                 if (is_sg) {
                     a.sg_logit[t] = v;
                 } else {
@@ -365,6 +422,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
             }
         }
     }
+    if ((int)blockIdx.x < T) operands_from_lds(s_xn[blockIdx.x], H, blockIdx.x, a.ops);
 }
 
 // ----------------------------------------------------------- routing
@@ -381,78 +439,102 @@ struct RouteLds {
     uint32_t bad;
 };
 
-// Top-k key: larger value first; NaN maps to 1 (below every number), 0 marks
-// a taken element.
-__device__ __forceinline__ uint32_t topk_key(float f) { return (f != f) ? 1u : vmi_order_key(f); }
+// Top-k rank key of logit l at expert index e: order key of the value in the
+// high word (larger value first; -0 folded into +0; NaN maps to 1, below
+// every number) and ~e in the low word (lower index first on ties).  Keys are
+// unique, so a wave-wide maximum names one winner; 0 marks a taken slot.
+__device__ __forceinline__ uint64_t topk_rank_key(float f, int e) {
+    uint32_t u = __float_as_uint(f);
+    u = (u == 0x80000000u) ? 0u : u;
+    const uint32_t ok = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const uint32_t hi = (f != f) ? 1u : ok;
+    return ((uint64_t)hi << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+}
 
-// Softmax + top-k + renorm of token t's logits by one wave (block.py:321-329):
-// k rounds of a wave-wide maximum over 32-bit value keys; the winner is the
-// lowest expert index holding the maximum (ballots in index order).  Writes
-// the token's k pairs to LDS.
+// Compare-exchange of 64-bit keys: a keeps the larger when desc.
+__device__ __forceinline__ void cx64(uint64_t& a, uint64_t& b, bool desc) {
+    const bool sw = desc ? (a < b) : (a > b);
+    const uint64_t lo = sw ? b : a, hi = sw ? a : b;
+    a = lo;
+    b = hi;
+}
+
+// Softmax + top-k + renorm of token t's logits by one wave (block.py:321-329).
+// Lane l holds experts l + 64i (i < NI) as rank keys, sorted descending once
+// (bitonic network); each of the k rounds (a rolled loop: this code runs once
+// per workgroup, so it is kept small for the instruction cache) takes the
+// wave-wide maximum of the lanes' heads and the single winning lane pops its
+// head.  Lane j keeps the j-th selection; exp, the renormalising sum (in j
+// order) and the scores are lane-parallel.
+template <int NI>
 __device__ void topk_token(const float* __restrict__ lt, int E, int k, int norm, int t, RouteLds& R) {
     const int lane = threadIdx.x & 63;
-    const int NI = E / 64;
-    float v[kMaxE / 64];
-    uint32_t key[kMaxE / 64];
+    const __amdgpu_buffer_rsrc_t rl = vmi_rsrc(lt, (uint32_t)E * 4u);
+    const int nreal = E >> 6;  // E is a multiple of 64: slot i is real for i < E/64 (uniform)
+    float v[NI];
+    uint64_t key[NI];
 #pragma unroll
-    for (int i = 0; i < kMaxE / 64; ++i) {
-        v[i] = (i < NI) ? lt[lane + 64 * i] : 0.0f;
-        key[i] = (i < NI) ? topk_key(v[i]) : 0u;
+    for (int i = 0; i < NI; ++i) v[i] = __uint_as_float(vmi_bload_b32(rl, (uint32_t)(lane + 64 * i) * 4u, 0));
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const uint64_t kk = topk_rank_key(v[i], lane + 64 * i);
+        key[i] = (i < nreal) ? kk : 0ull;
     }
-    float sel_val[kMaxK];
-    int sel_idx[kMaxK];
 #pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
-        sel_val[j] = 0.0f;
-        sel_idx[j] = 0;
-        if (j < k) {
-            uint32_t mx = key[0];
+    for (int size = 2; size <= NI; size *= 2)
 #pragma unroll
-            for (int i = 1; i < kMaxE / 64; ++i) mx = max(mx, key[i]);
-            const uint32_t M = vmi_wave_max_u32(mx);
-            int idx = -1;
+        for (int stride = size / 2; stride > 0; stride /= 2)
 #pragma unroll
-            for (int i = 0; i < kMaxE / 64; ++i) {
-                if (i < NI && idx < 0) {
-                    const uint64_t b = __ballot(key[i] == M);
-                    if (b) idx = 64 * i + __builtin_ctzll(b);
-                }
+            for (int i = 0; i < NI; ++i) {
+                const int j = i ^ stride;
+                if (j > i) cx64(key[i], key[j], (i & size) == 0);
             }
+    uint64_t my_key = 0ull;
+#pragma unroll 1
+    for (int j = 0; j < k; ++j) {
+        const uint64_t M = vmi_wave_max_u64(key[0]);
+        if (key[0] == M) {
 #pragma unroll
-            for (int i = 0; i < kMaxE / 64; ++i)
-                if (64 * i + lane == idx) key[i] = 0u;
-            sel_idx[j] = idx;
-            sel_val[j] = vmi_order_key_value(M);
+            for (int i = 0; i + 1 < NI; ++i) key[i] = key[i + 1];
+            key[NI - 1] = 0ull;
         }
+        if (lane == j) my_key = M;
     }
-    const float mx = sel_val[0];
-    bool bad = false;
-    float e[kMaxK];
+    const int my_idx = (int)(0xffffffffu - (uint32_t)my_key);
+    const float my_val = vmi_order_key_value((uint32_t)(my_key >> 32));
+    const float mx = vmi_readlane_f32(my_val, 0);
+    const bool sel = lane < k;
+    const bool bad = __ballot(sel && !(fabsf(my_val) < 3.0e38f)) != 0;
+    const float e = sel ? expf(my_val - mx) : 0.0f;
     float den = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
-        e[j] = 0.0f;
-        if (j < k) {
-            bad |= !(fabsf(sel_val[j]) < 3.0e38f);
-            e[j] = expf(sel_val[j] - mx);
-            if (norm) den = den + e[j];
-        }
-    }
-    if (!norm) {
+    if (norm) {
+#pragma unroll 1
+        for (int j = 0; j < k; ++j) den = den + vmi_readlane_f32(e, j);
+    } else {
         float part = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kMaxE / 64; ++i)
-            if (i < NI) part = part + expf(v[i] - mx);
+        for (int i = 0; i < NI; ++i)
+            if (i < nreal) part = part + expf(v[i] - mx);
         den = vmi_wave_sum_canon(part);
     }
-#pragma unroll
-    for (int j = 0; j < kMaxK; ++j) {
-        if (j < k && lane == j) {
-            R.ids[t * k + j] = sel_idx[j];
-            R.scores[t * k + j] = e[j] / den;
-        }
+    if (sel) {
+        R.ids[t * k + lane] = my_idx;
+        R.scores[t * k + lane] = e / den;
     }
     if (bad && lane == 0) atomicOr(&R.bad, VMI_STATUS_BAD_ROUTE);
+}
+
+__device__ void topk_dispatch(const float* __restrict__ lt, int E, int k, int norm, int t, RouteLds& R) {
+    if (E <= 64)
+        topk_token<1>(lt, E, k, norm, t, R);
+    else if (E <= 128)
+        topk_token<2>(lt, E, k, norm, t, R);
+    else if (E <= 256)
+        topk_token<4>(lt, E, k, norm, t, R);
+    else if (E <= 512)
+        topk_token<8>(lt, E, k, norm, t, R);
+    else
+        topk_token<16>(lt, E, k, norm, t, R);
 }
 
 // Distinct valid slots in first-appearance order over the token-major pair
@@ -460,7 +542,7 @@ __device__ void topk_token(const float* __restrict__ lt, int E, int k, int norm,
 // first-occurrence table (only the entries of slots in use are touched).
 // Fills rank/uslot/umask/U.  Called by all threads of a 256-thread workgroup.
 __device__ void dedup_lds(int npairs, int k, int cap, RouteLds& R, int32_t* s_first) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     const bool table = cap <= kFirstTable;
     if (tid < kMaxPairs) R.umask[tid] = 0u;
     const int s = (tid < npairs) ? R.slot[tid] : -1;
@@ -520,24 +602,28 @@ struct GateUpArgs {
     uint32_t* status;
     int32_t* ids_out;             // [T*k] or nullptr
     float* scores_out;            // [T*k] or nullptr
-    vmi_u4* actop;                // [npairs+1, T, I/8]
-    float* axs;                   // [npairs+1, T, I/64]
-    float* aifa;                  // [npairs+1, I/64, kTPad]
+    vmi_u4* actop;                // [npairs+1, T, I/8] bf16 down-projection operands
+    float* axs;                   // [npairs+1, T, I/64] their per-group sums
 };
 
 // Routing of the batch inside one k_gateup workgroup (all threads).  The
 // workgroup `publish` additionally writes the route table for k_downcomb, the
 // caller's ids/scores and the status bits.
 __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, int32_t* s_first, bool publish) {
-    const int tid = threadIdx.x, w = tid >> 6;
+    const int tid = threadIdx.x, w = vmi_wave_id();
     const int T = a.T, k = a.k, npairs = a.npairs;
     if (tid == 0) R.bad = 0u;
     if (!a.from_slots) {
-        if (a.table)
-            for (int e = tid; e < a.E; e += kThreads) s_table[e] = a.table[e];
-        __syncthreads();
+        if (a.table) {
+            const __amdgpu_buffer_rsrc_t rt = vmi_rsrc(a.table, (uint32_t)a.E * 4u);
+            int32_t tv[kMaxE / kThreads];
+#pragma unroll
+            for (int i = 0; i < kMaxE / kThreads; ++i) tv[i] = (int32_t)vmi_bload_b32(rt, (uint32_t)(tid + kThreads * i) * 4u, 0);
+#pragma unroll
+            for (int i = 0; i < kMaxE / kThreads; ++i) s_table[tid + kThreads * i] = tv[i];
+        }
         for (int t = w; t < T; t += kThreads / VMI_WAVE)
-            topk_token(a.logits + (size_t)t * a.E, a.E, k, a.norm, t, R);
+            topk_dispatch(a.logits + (size_t)t * a.E, a.E, k, a.norm, t, R);
         __syncthreads();
         if (tid < npairs) {
             const int id = R.ids[tid];
@@ -563,7 +649,7 @@ __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, 
     if (!publish) return;
     const int U = R.U;
     if (tid == 0) a.route->U = U;
-    if (tid < U) a.route->uslot[tid] = R.uslot[tid];
+    if (tid < npairs) a.route->uslot[tid] = tid < U ? R.uslot[tid] : -1;
     // combine weight of (u, t): its pairs' scores in j order
     for (int i = tid; i < U * T; i += kThreads) {
         const int u = i / T, t = i - u * T;
@@ -599,7 +685,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     __shared__ RouteLds R;
     __shared__ int32_t s_table[kMaxE];
     __shared__ int32_t s_first[kFirstTable];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     const int q = lane >> 4, r = lane & 15;
     const int T = a.T, I = a.I, NC = I / kSlice;
     const int nsh = a.has_shared ? NC : 0;
@@ -607,37 +693,31 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     const bool is_shared = item < nsh;
     const vmi_u4 zero4 = {0u, 0u, 0u, 0u};
 
-    // the MoE input operands go to registers first (they arrive during routing)
-    vmi_u4 xr[XPT];
-#pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-        const int idx = tid + kThreads * i;
-        xr[i] = (idx < T * H8) ? a.xop[idx] : zero4;
-    }
-    // (every global load the arithmetic needs is issued before the weight loads:
-    // loads retire in issue order)
-    constexpr int XSPT = (kT * NG + kThreads - 1) / kThreads;
-    float xsr[XSPT];
-#pragma unroll
-    for (int i = 0; i < XSPT; ++i) {
-        const int idx = tid + kThreads * i;
-        xsr[i] = (idx < T * NG) ? a.xsum[idx] : 0.0f;
-    }
-    const float invr = (tid < T) ? 1.0f / a.fscale[tid] : 0.0f;
-
     int slot = 0, c = item, aidx = a.npairs;
     uint32_t tmask = (1u << T) - 1u;
     if (!is_shared) {
         route_batch(a, R, s_table, s_first, item == nsh);
         const int ii = item - nsh, u = ii / NC;
-        if (u >= R.U) return;
+        if (u >= vmi_uniform(R.U)) return;
         c = ii - u * NC;
-        slot = R.uslot[u];
-        tmask = R.umask[u];
+        slot = vmi_uniform(R.uslot[u]);
+        tmask = (uint32_t)vmi_uniform((int)R.umask[u]);
         aidx = u;
     }
 
-    // every weight load of the item: scales, biases, then gate/up words by m
+    // the MoE input operands, then every weight load of the item (scales,
+    // biases, gate/up words by m): loads retire in issue order, so everything
+    // the arithmetic needs first is issued first
+    const __amdgpu_buffer_rsrc_t rxo = vmi_rsrc(a.xop, (uint32_t)T * H8 * 16u);
+    vmi_u4 xr[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) xr[i] = vmi_bload_b128(rxo, (uint32_t)(tid + kThreads * i) * 16u, 0);
+    constexpr int XSPT = (kT * NG + kThreads - 1) / kThreads;
+    const __amdgpu_buffer_rsrc_t rxs = vmi_rsrc(a.xsum, (uint32_t)T * NG * 4u);
+    uint32_t xsr[XSPT];
+#pragma unroll
+    for (int i = 0; i < XSPT; ++i) xsr[i] = vmi_bload_b32(rxs, (uint32_t)(tid + kThreads * i) * 4u, 0);
+    const uint32_t fsr = vmi_bload_b32(vmi_rsrc(a.fscale, (uint32_t)T * 4u), (uint32_t)tid * 4u, 0);
     const vmi_qmat mg = is_shared ? a.sh_gate : a.gate;
     const vmi_qmat mu = is_shared ? a.sh_up : a.up;
     const uint32_t wbytes = (uint32_t)I * (H / 2), sbytes = (uint32_t)I * NG * 2u;
@@ -691,9 +771,9 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
 #pragma unroll
     for (int i = 0; i < XSPT; ++i) {
         const int idx = tid + kThreads * i;
-        if (idx < T * NG) s_xs[idx / NG][idx % NG] = xsr[i];
+        if (idx < T * NG) s_xs[idx / NG][idx % NG] = __uint_as_float(xsr[i]);
     }
-    if (tid < T) s_inv[tid] = invr;
+    if (tid < T) s_inv[tid] = 1.0f / __uint_as_float(fsr);
     __syncthreads();
 
     // main MFMAs: m-th load pair covers groups 2m (K blocks 0-1) and 2m+1 (2-3)
@@ -773,32 +853,31 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
         }
     }
     __syncthreads();
-    // down-projection operands of this slice: thread (t, kk) packs columns 8kk..8kk+7
+    // down-projection operands of this slice: bf16 activations, thread (t, kk)
+    // packs columns 8kk..8kk+7 in slot order {0,4,1,5,2,6,3,7}
+    // (vmi_unpack_u4_bf16_128); the slice's fp32 sum of those bf16 values
+    // feeds the affine-bias term
     const int NGd = NC;
     if (w < (T + 7) / 8) {
         const int t = 8 * w + (lane >> 3), kk = lane & 7;
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = (t < T) ? s_act[t][8 * kk + i] : 0.0f;
-        float am = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
-        am = fmaxf(am, __shfl_xor(am, 1, VMI_WAVE));
-        am = fmaxf(am, __shfl_xor(am, 2, VMI_WAVE));
-        am = fmaxf(am, __shfl_xor(am, 4, VMI_WAVE));
-        const float fa = vmi_fp16_range_scale(am);
+        uint32_t hb[8];
         float xs = 0.0f;
-        const vmi_u4 op = make_act_operand(v, fa, xs);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            hb[i] = (t < T) ? vmi_f32_to_bf16(s_act[t][8 * kk + i]) : 0u;
+            xs += vmi_bf16_to_f32(hb[i]);
+        }
+        vmi_u4 op;
+        op[0] = hb[0] | (hb[4] << 16);
+        op[1] = hb[1] | (hb[5] << 16);
+        op[2] = hb[2] | (hb[6] << 16);
+        op[3] = hb[3] | (hb[7] << 16);
         xs += __shfl_xor(xs, 1, VMI_WAVE);
         xs += __shfl_xor(xs, 2, VMI_WAVE);
         xs += __shfl_xor(xs, 4, VMI_WAVE);
         if (t < T) {
-            const float ifa = 1.0f / fa;
             a.actop[((size_t)aidx * T + t) * (I / 8) + 8 * c + kk] = op;
-            if (kk == 0) {
-                a.axs[((size_t)aidx * T + t) * NGd + c] = xs * ifa;
-                a.aifa[((size_t)aidx * NGd + c) * kTPad + t] = ifa;
-            }
+            if (kk == 0) a.axs[((size_t)aidx * T + t) * NGd + c] = xs;
         }
     }
 }
@@ -808,144 +887,188 @@ struct DownArgs {
     int T, H, I, npairs, has_shared, has_sgate;
     const RouteInfo* route;
     vmi_qmat down, sh_down;
-    const vmi_u4* actop;
-    const float* axs;
-    const float* aifa;
+    const vmi_u4* actop;       // [npairs+1, T, I/8] bf16 operands
+    const float* axs;          // [npairs+1, T, I/64]
     const float* sg_logit;     // [T] (has_sgate)
     const uint16_t* residual;  // [T, H] or nullptr
     void* out;
     int out_dtype;
 };
 
-// One workgroup (8 waves) per 16 output rows h0..h0+15.  Wave w takes experts
-// e = w, w+8, ... of the list [shared (when present), distinct slots 0..U-1]:
-// the 16 down rows x inter of expert e (16-byte loads, two groups per load),
-// the expert's activation operands, then weight * (down . act) summed per
-// token into registers; the 8 waves' sums meet in LDS in wave order, plus the
-// residual.
-template <int NMD, bool PACK>
-__global__ __launch_bounds__(kDownThreads, 1) void k_downcomb(DownArgs a) {
-    __shared__ float s_red[kDownWaves][4][VMI_WAVE];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+// One quantisation row of a scale or bias matrix (NG = I/64 <= 8 bf16 values)
+// as words: word m holds groups 2m (low half) and 2m+1 (high half).  Exact-size
+// loads, chosen at compile time (NMD = ceil(NG/2); EVEN: NG = 2*NMD).
+template <int NMD, bool EVEN>
+__device__ __forceinline__ void load_group_row(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t (&wv)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wv[i] = 0u;
+    if constexpr (NMD == 4 && EVEN) {
+        const vmi_u4 v = vmi_bload_b128(rs, off, 0);
+        wv[0] = v[0]; wv[1] = v[1]; wv[2] = v[2]; wv[3] = v[3];
+    } else {
+        constexpr int FULL = EVEN ? NMD : NMD - 1;
+        if constexpr (FULL >= 2) {
+            const uint2 v = vmi_bload_b64(rs, off, 0);
+            wv[0] = v.x; wv[1] = v.y;
+        } else if constexpr (FULL == 1) {
+            wv[0] = vmi_bload_b32(rs, off, 0);
+        }
+        if constexpr (FULL == 3) wv[2] = vmi_bload_b32(rs, off + 8u, 0);
+        if constexpr (!EVEN) wv[NMD - 1] = vmi_bload_b16(rs, off + 4u * (NMD - 1), 0);
+    }
+}
+
+// One workgroup (NW waves) per 16 output rows h0..h0+15.  Wave w takes experts
+// e = w, w+NW, ... of the list [shared (when present), distinct slots in
+// first-appearance order], P at a time: for a chunk every load is issued first
+// - the experts' 16 down rows (16-byte loads, two groups each), scales and
+// biases into registers, their bf16 activation operands, activation sums and
+// combine weights straight into LDS (global_load_lds) - then one wait, then the
+// chunk's MFMAs.  Down weights enter the bf16 MFMA as exact (128 + q); the
+// 128 * sum(act) excess is removed with the affine-bias term.  Per token the
+// wave accumulates weight * (down . act); the waves' sums meet in LDS in wave
+// order, plus the residual.  LDS holds NW * P * TB <= 128 token rows of 64
+// activation words; lanes that carry no token read a zero block.
+template <int NMD, bool EVEN, bool PACK, int NW, int P, int TB>
+__global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
+    __shared__ uint4 s_act[NW][P][TB * 64];
+    __shared__ uint4 s_zero[64];
+    __shared__ float s_axs[NW][P][TB * 8];
+    __shared__ float s_wt[NW][P][16];
+    __shared__ float s_red[NW][4][VMI_WAVE];
+    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     const int q = lane >> 4, r = lane & 15;
     const int T = a.T, H = a.H, I = a.I, I8 = I / 8, NGd = I / 64;
     const int h = blockIdx.x * 16 + r;
     const int tq = lane >> 4;
     const int par = PACK ? (tq >> 1) : 0;
     const int tt0 = PACK ? 4 * (tq & 1) : 4 * tq;  // first token of this lane's D rows
-    const vmi_u4 zero4 = {0u, 0u, 0u, 0u};
     const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
     const int tk = PACK ? (r & 7) : r;
     const bool areal = PACK ? (((q < 2) == (r < 8)) && tk < T) : (r < T);
-    const int ne = a.has_shared + a.route->U;
+    if (tid < 64) s_zero[tid] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    const int hs = a.has_shared;
+    const int nmax = hs + a.npairs;  // experts the list can hold; distinct slots past U read -1
+    const int nact = T * I8;         // activation words of one expert
+    const int nax = T * NGd;         // activation sums of one expert
+    const uint32_t rowoff = (uint32_t)h * NGd * 2u;
     float wsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int e = w; e < ne; e += kDownWaves) {
-        const bool sh = a.has_shared && e == 0;
-        const int u = e - a.has_shared;
-        const int aidx = sh ? a.npairs : u;
-        const int slot = sh ? 0 : a.route->uslot[u];
-        const vmi_qmat md = sh ? a.sh_down : a.down;
-        // activation-side operands (L2 resident) before the weights
-        const __amdgpu_buffer_rsrc_t ra = vmi_rsrc(a.actop + (size_t)aidx * T * I8, (uint32_t)T * I8 * 16u);
-        vmi_u4 A[NMD][4];
+    for (int e0 = w; e0 < nmax; e0 += NW * P) {
+        // ---- slots of the chunk (lane j < P), one vector load
+        const int ej = e0 + NW * lane;
+        const int uj = ej - hs;
+        int sl = -1;
+        if (lane < P && ej < nmax) sl = (hs && ej == 0) ? 0 : a.route->uslot[uj];
+        int slot[P];
+        bool ok[P];
 #pragma unroll
-        for (int m = 0; m < NMD; ++m)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int wi = 16 * m + 4 * q + j;
-                A[m][j] = vmi_bload_b128(ra, (areal && wi < I8) ? (uint32_t)(tk * I8 + wi) * 16u : VMI_OOB, 0);
-            }
-        const float* ifa_base = a.aifa + (size_t)aidx * NGd * kTPad;
-        float4 ifa0[NMD], ifa1[NMD];
-#pragma unroll
-        for (int m = 0; m < NMD; ++m) {
-            const int g0 = 2 * m + par;
-            ifa0[m] = g0 < NGd ? *reinterpret_cast<const float4*>(ifa_base + g0 * kTPad + tt0)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-            if constexpr (!PACK) {
-                const int g1 = 2 * m + 1;
-                ifa1[m] = g1 < NGd ? *reinterpret_cast<const float4*>(ifa_base + g1 * kTPad + tt0)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+        for (int j = 0; j < P; ++j) {
+            slot[j] = __builtin_amdgcn_readlane(sl, j);
+            ok[j] = slot[j] >= 0;
         }
-        float x0 = 0.0f, x1 = 0.0f;
-        if (r < T) {
-            const float* xb = a.axs + ((size_t)aidx * T + r) * NGd;
-            if (2 * q < NGd) x0 = xb[2 * q];
-            if (2 * q + 1 < NGd) x1 = xb[2 * q + 1];
-        }
-        float wv[4];
+        if (!ok[0]) break;  // first-appearance order: nothing valid past an invalid slot
+        // ---- issue: LDS side first, then registers
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = tt0 + i;
-            float v = 0.0f;
-            if (t < T) {
-                if (sh)
-                    v = a.has_sgate ? 1.0f / (1.0f + expf(-a.sg_logit[t])) : 1.0f;
-                else
-                    v = a.route->wt[u][t];
-            }
-            wv[i] = v;
-        }
-        // weights, scales, biases of rows h
-        const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(md.w + (size_t)slot * H * I8, (uint32_t)H * (I / 2));
-        const __amdgpu_buffer_rsrc_t rs = vmi_rsrc(md.s + (size_t)slot * H * NGd, (uint32_t)H * NGd * 2u);
-        const __amdgpu_buffer_rsrc_t rb = vmi_rsrc(md.b + (size_t)slot * H * NGd, (uint32_t)H * NGd * 2u);
-        vmi_u4 W[NMD];
+        for (int j = 0; j < P; ++j) {
+            if (ok[j]) {
+                const int e = e0 + NW * j;
+                const bool sh = hs && e == 0;
+                const int aidx = sh ? a.npairs : e - hs;
+                const vmi_u4* asrc = a.actop + (size_t)aidx * nact;
 #pragma unroll
-        for (int m = 0; m < NMD; ++m) {
-            const uint32_t off = 64u * m + 16u * q;
-            W[m] = vmi_bload_b128(rw, off < (uint32_t)(I / 2) ? (uint32_t)h * (I / 2) + off : VMI_OOB, 0);
-        }
-        uint32_t s0[NMD], s1[NMD];
+                for (int n = 0; n < TB; ++n)
+                    if (n * 64 < nact && n * 64 + lane < nact) VMI_LDS_DMA16(asrc + n * 64 + lane, &s_act[w][j][n * 64]);
+                const float* xsrc = a.axs + (size_t)aidx * nax;
 #pragma unroll
-        for (int m = 0; m < NMD; ++m) {
-            const int g0 = 2 * m + par;
-            s0[m] = vmi_bload_b16(rs, g0 < NGd ? (uint32_t)(h * NGd + g0) * 2u : VMI_OOB, 0);
-            if constexpr (!PACK) {
-                const int g1 = 2 * m + 1;
-                s1[m] = vmi_bload_b16(rs, g1 < NGd ? (uint32_t)(h * NGd + g1) * 2u : VMI_OOB, 0);
+                for (int n = 0; n < (TB * 8 + 63) / 64; ++n)
+                    if (n * 64 < nax && n * 64 + lane < nax) VMI_LDS_DMA4(xsrc + n * 64 + lane, &s_axs[w][j][n * 64]);
+                const float* wsrc = sh ? a.sg_logit : &a.route->wt[sh ? 0 : e - hs][0];
+                if (lane < T && (!sh || a.has_sgate)) VMI_LDS_DMA4(wsrc + lane, &s_wt[w][j][0]);
             }
         }
-        const uint32_t b0 = vmi_bload_b16(rb, 2 * q < NGd ? (uint32_t)(h * NGd + 2 * q) * 2u : VMI_OOB, 0);
-        const uint32_t b1 = vmi_bload_b16(rb, 2 * q + 1 < NGd ? (uint32_t)(h * NGd + 2 * q + 1) * 2u : VMI_OOB, 0);
-
-        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        vmi_u4 W[P][NMD];
+        uint32_t sw[P][4], bw[P][4];
 #pragma unroll
-        for (int m = 0; m < NMD; ++m) {
-            if constexpr (PACK) {
-                vmi_f4 d = zf;
+        for (int j = 0; j < P; ++j) {
+            const int e = e0 + NW * j;
+            const bool sh = hs && e == 0;
+            const vmi_qmat md = sh ? a.sh_down : a.down;
+            const int sj = ok[j] ? slot[j] : 0;
+            const uint32_t mbytes = ok[j] ? (uint32_t)H * (I / 2) : 0u, gbytes = ok[j] ? (uint32_t)H * NGd * 2u : 0u;
+            const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(md.w + (size_t)sj * H * I8, mbytes);
+            const __amdgpu_buffer_rsrc_t rs = vmi_rsrc(md.s + (size_t)sj * H * NGd, gbytes);
+            const __amdgpu_buffer_rsrc_t rb = vmi_rsrc(md.b + (size_t)sj * H * NGd, gbytes);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) d = vmi_mfma_f16(A[m][j], vmi_unpack_u4_f16(W[m][j]), d);
-                const float sc = vmi_bf16_to_f32(s0[m]) * kTwo24;
-                const float fi[4] = {ifa0[m].x, ifa0[m].y, ifa0[m].z, ifa0[m].w};
+            for (int m = 0; m < NMD; ++m) {
+                const uint32_t off = 64u * m + 16u * q;
+                W[j][m] = vmi_bload_b128(rw, off < (uint32_t)(I / 2) ? (uint32_t)h * (I / 2) + off : VMI_OOB, 0);
+            }
+            load_group_row<NMD, EVEN>(rs, rowoff, sw[j]);
+            load_group_row<NMD, EVEN>(rb, rowoff, bw[j]);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // ---- compute the chunk
 #pragma unroll
-                for (int i = 0; i < 4; ++i) y[i] = fmaf((tt0 + i < T) ? sc * fi[i] : 0.0f, d[i], y[i]);
-            } else {
-                vmi_f4 d0 = zf, d1 = zf;
+        for (int j = 0; j < P; ++j) {
+            if (!ok[j]) break;
+            const int e = e0 + NW * j;
+            const bool sh = hs && e == 0;
+            // lane's activation words: 16m + 4q + j4 of token tk, or the zero block
+            const uint4* abase = areal ? &s_act[w][j][tk * I8 + 4 * q] : &s_zero[0];
+            float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const vmi_u4 bw = vmi_unpack_u4_f16(W[m][j]);
-                    d0 = vmi_mfma_f16(q < 2 ? A[m][j] : zero4, bw, d0);
-                    d1 = vmi_mfma_f16(q < 2 ? zero4 : A[m][j], bw, d1);
+            for (int m = 0; m < NMD; ++m) {
+                // the odd group of the last load does not exist when NGd is odd
+                const bool mreal = EVEN || m + 1 < NMD || q < 2;
+                const uint4* ab = mreal ? abase : &s_zero[0];
+                vmi_u4 A[4];
+#pragma unroll
+                for (int j4 = 0; j4 < 4; ++j4) {
+                    const uint4 v4 = ab[16 * m + j4];
+                    A[j4] = vmi_u4{v4.x, v4.y, v4.z, v4.w};
                 }
-                const float sc0 = vmi_bf16_to_f32(s0[m]) * kTwo24, sc1 = vmi_bf16_to_f32(s1[m]) * kTwo24;
-                const float f0[4] = {ifa0[m].x, ifa0[m].y, ifa0[m].z, ifa0[m].w};
-                const float f1[4] = {ifa1[m].x, ifa1[m].y, ifa1[m].z, ifa1[m].w};
+                const uint32_t swm = sw[j][m];
+                if constexpr (PACK) {
+                    vmi_f4 d = zf;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool ok = tt0 + i < T;
-                    y[i] = fmaf(ok ? sc0 * f0[i] : 0.0f, d0[i], y[i]);
-                    y[i] = fmaf(ok ? sc1 * f1[i] : 0.0f, d1[i], y[i]);
+                    for (int j4 = 0; j4 < 4; ++j4) d = vmi_mfma_bf16(A[j4], vmi_unpack_u4_bf16_128(W[j][m][j4]), d);
+                    const float sc = __uint_as_float(par ? (swm & 0xffff0000u) : (swm << 16));
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) y[i] = fmaf(sc, d[i], y[i]);
+                } else {
+                    const vmi_u4 z = {0u, 0u, 0u, 0u};
+                    vmi_f4 d0 = zf, d1 = zf;
+#pragma unroll
+                    for (int j4 = 0; j4 < 4; ++j4) {
+                        const vmi_u4 bq = vmi_unpack_u4_bf16_128(W[j][m][j4]);
+                        d0 = vmi_mfma_bf16(q < 2 ? A[j4] : z, bq, d0);
+                        d1 = vmi_mfma_bf16(q < 2 ? z : A[j4], bq, d1);
+                    }
+                    const float sc0 = __uint_as_float(swm << 16), sc1 = __uint_as_float(swm & 0xffff0000u);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) y[i] = fmaf(sc1, d1[i], fmaf(sc0, d0[i], y[i]));
                 }
             }
-        }
-        const vmi_f4 db = vmi_mfma_bf16(bias_a_operand(x0, x1), bias_b_operand(b0 | (b1 << 16)), zf);
+            // affine bias and the 128-offset correction: lane block q carries groups 2q, 2q+1
+            const int xr = r < T ? r : 0;
+            const float x0 = (r < T && 2 * q < NGd) ? s_axs[w][j][xr * NGd + 2 * q] : 0.0f;
+            const float x1 = (r < T && 2 * q + 1 < NGd) ? s_axs[w][j][xr * NGd + 2 * q + 1] : 0.0f;
+            const vmi_u4 ab2 = bias_a_operand(x0, x1);
+            const uint32_t bq = q == 0 ? bw[j][0] : q == 1 ? bw[j][1] : q == 2 ? bw[j][2] : bw[j][3];
+            const uint32_t sq = q == 0 ? sw[j][0] : q == 1 ? sw[j][1] : q == 2 ? sw[j][2] : sw[j][3];
+            const vmi_f4 db = vmi_mfma_bf16(ab2, bias_b_operand(bq), zf);
+            const vmi_f4 ds = vmi_mfma_bf16(ab2, bias_b_operand(sq), zf);
+            const float4 wr4 = *reinterpret_cast<const float4*>(&s_wt[w][j][tt0]);
+            const float wr[4] = {wr4.x, wr4.y, wr4.z, wr4.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float v = y[i];
-            if constexpr (PACK) v += __shfl_xor(v, 32, VMI_WAVE);
-            wsum[i] = fmaf(wv[i], v + db[i], wsum[i]);
+            for (int i = 0; i < 4; ++i) {
+                float v = y[i];
+                if constexpr (PACK) v += __shfl_xor(v, 32, VMI_WAVE);
+                const float g = sh ? (a.has_sgate ? 1.0f / (1.0f + expf(-wr[i])) : 1.0f) : wr[i];
+                const float wt = (tt0 + i < T) ? g : 0.0f;
+                wsum[i] = fmaf(wt, fmaf(-128.0f, ds[i], v + db[i]), wsum[i]);
+            }
         }
     }
 #pragma unroll
@@ -956,7 +1079,7 @@ __global__ __launch_bounds__(kDownThreads, 1) void k_downcomb(DownArgs a) {
         const int l = 16 * (t >> 2) + rr, i = t & 3;
         float acc = 0.0f;
 #pragma unroll
-        for (int ww = 0; ww < kDownWaves; ++ww) acc += s_red[ww][i][l];
+        for (int ww = 0; ww < NW; ++ww) acc += s_red[ww][i][l];
         const size_t o = (size_t)t * H + blockIdx.x * 16 + rr;
         if (a.residual) acc += vmi_bf16_to_f32(a.residual[o]);
         if (a.out_dtype == VMI_BF16)
@@ -1014,20 +1137,36 @@ hipError_t launch_gateup(const GateUpArgs& ga, int H, hipStream_t s) {
     return ga.T <= 8 ? launch_gateup_t<true>(ga, H, s) : launch_gateup_t<false>(ga, H, s);
 }
 
-template <bool PACK>
+template <bool PACK, int NW, int P, int TB>
 hipError_t launch_downcomb_t(const DownArgs& da, hipStream_t s) {
-    const dim3 grid(da.H / 16);
+    const dim3 grid(da.H / 16), block(NW * VMI_WAVE);
+    const bool even = (da.I / 64) % 2 == 0;
     switch ((da.I + 127) / 128) {
-        case 1: hipLaunchKernelGGL((k_downcomb<1, PACK>), grid, dim3(kDownThreads), 0, s, da); break;
-        case 2: hipLaunchKernelGGL((k_downcomb<2, PACK>), grid, dim3(kDownThreads), 0, s, da); break;
-        case 3: hipLaunchKernelGGL((k_downcomb<3, PACK>), grid, dim3(kDownThreads), 0, s, da); break;
-        default: hipLaunchKernelGGL((k_downcomb<4, PACK>), grid, dim3(kDownThreads), 0, s, da); break;
+        case 1:
+            if (even) hipLaunchKernelGGL((k_downcomb<1, true, PACK, NW, P, TB>), grid, block, 0, s, da);
+            else hipLaunchKernelGGL((k_downcomb<1, false, PACK, NW, P, TB>), grid, block, 0, s, da);
+            break;
+        case 2:
+            if (even) hipLaunchKernelGGL((k_downcomb<2, true, PACK, NW, P, TB>), grid, block, 0, s, da);
+            else hipLaunchKernelGGL((k_downcomb<2, false, PACK, NW, P, TB>), grid, block, 0, s, da);
+            break;
+        case 3:
+            if (even) hipLaunchKernelGGL((k_downcomb<3, true, PACK, NW, P, TB>), grid, block, 0, s, da);
+            else hipLaunchKernelGGL((k_downcomb<3, false, PACK, NW, P, TB>), grid, block, 0, s, da);
+            break;
+        default:
+            if (even) hipLaunchKernelGGL((k_downcomb<4, true, PACK, NW, P, TB>), grid, block, 0, s, da);
+            else hipLaunchKernelGGL((k_downcomb<4, false, PACK, NW, P, TB>), grid, block, 0, s, da);
+            break;
     }
     return hipGetLastError();
 }
 
+// LDS holds NW * P * TB = 128 token rows of activation operands.
 hipError_t launch_downcomb(const DownArgs& da, hipStream_t s) {
-    return da.T <= 8 ? launch_downcomb_t<true>(da, s) : launch_downcomb_t<false>(da, s);
+    if (da.T <= 4) return launch_downcomb_t<true, 16, 2, 4>(da, s);
+    if (da.T <= 8) return launch_downcomb_t<true, 16, 1, 8>(da, s);
+    return launch_downcomb_t<false, 8, 1, 16>(da, s);
 }
 
 template <typename XT>
@@ -1063,7 +1202,6 @@ MoeWorkspace carve_workspace(void* base, int T, int k, int hidden, int inter, in
     w.fscale = reinterpret_cast<float*>(take(sizeof(float) * (size_t)T));
     w.actop = reinterpret_cast<vmi_u4*>(take(sizeof(uint16_t) * nact * T * inter));
     w.axs = reinterpret_cast<float*>(take(sizeof(float) * nact * T * (inter / 64)));
-    w.aifa = reinterpret_cast<float*>(take(sizeof(float) * nact * (inter / 64) * kTPad));
     w.bytes = off;
     return w;
 }
@@ -1115,14 +1253,14 @@ extern "C" int vmi_fused_moe_slots(const void* x, int x_dtype, const int32_t* lo
     ga.gate = gate; ga.up = up; ga.sh_gate = gate; ga.sh_up = up;
     ga.xop = ws.xop; ga.xsum = ws.xsum; ga.fscale = ws.fscale;
     ga.route = ws.route; ga.status = ws.status;
-    ga.actop = ws.actop; ga.axs = ws.axs; ga.aifa = ws.aifa;
+    ga.actop = ws.actop; ga.axs = ws.axs;
     e = launch_gateup(ga, hidden, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "k_gateup launch");
 
     DownArgs da{};
     da.T = T; da.H = hidden; da.I = inter; da.npairs = T * k; da.has_shared = 0; da.has_sgate = 0;
     da.route = ws.route; da.down = down; da.sh_down = down;
-    da.actop = ws.actop; da.axs = ws.axs; da.aifa = ws.aifa;
+    da.actop = ws.actop; da.axs = ws.axs;
     da.residual = nullptr; da.out = out; da.out_dtype = out_dtype;
     e = launch_downcomb(da, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "k_downcomb launch");
@@ -1168,10 +1306,11 @@ extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, 
     ra.sgate = has_sgate ? D.shared_expert_gate : D.router;
     ra.sgbits = has_sgate ? D.shared_expert_gate_bits : D.router_bits;
     ra.has_sgate = has_sgate;
-    constexpr int rows_per_wg = kRouterRowsPerWave * (kThreads / VMI_WAVE);
+    constexpr int rows_per_wg = kThreads / VMI_WAVE;
     ra.row_wgs = (D.num_experts + has_sgate + rows_per_wg - 1) / rows_per_wg;
+    if (ra.row_wgs < T) ra.row_wgs = T;  // workgroup t < T writes token t's operands
     ra.logits = ws.logits; ra.sg_logit = ws.sg_logit; ra.ops = ops;
-    const dim3 rgrid(ra.row_wgs + T);
+    const dim3 rgrid(ra.row_wgs);
     switch (D.hidden) {
         case 512: hipLaunchKernelGGL(k_router<8>, rgrid, dim3(kThreads), 0, s, ra); break;
         case 1024: hipLaunchKernelGGL(k_router<16>, rgrid, dim3(kThreads), 0, s, ra); break;
@@ -1189,7 +1328,7 @@ extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, 
     ga.sh_up = has_shared ? D.shared_up : D.up;
     ga.xop = ws.xop; ga.xsum = ws.xsum; ga.fscale = ws.fscale;
     ga.route = ws.route; ga.status = ws.status; ga.ids_out = ids_out; ga.scores_out = scores_out;
-    ga.actop = ws.actop; ga.axs = ws.axs; ga.aifa = ws.aifa;
+    ga.actop = ws.actop; ga.axs = ws.axs;
     e = launch_gateup(ga, D.hidden, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "k_gateup launch");
 
@@ -1197,7 +1336,7 @@ extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, 
     da.T = T; da.H = D.hidden; da.I = D.inter; da.npairs = T * D.top_k;
     da.has_shared = has_shared; da.has_sgate = has_sgate;
     da.route = ws.route; da.down = D.down; da.sh_down = has_shared ? D.shared_down : D.down;
-    da.actop = ws.actop; da.axs = ws.axs; da.aifa = ws.aifa; da.sg_logit = ws.sg_logit;
+    da.actop = ws.actop; da.axs = ws.axs; da.sg_logit = ws.sg_logit;
     da.residual = residual; da.out = out; da.out_dtype = VMI_BF16;
     e = launch_downcomb(da, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "k_downcomb launch");
