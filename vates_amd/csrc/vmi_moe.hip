@@ -392,32 +392,53 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
                                             : (wword[c / 4] >> (8 * (c % 4))) & 255u;
             wv[c] = fmaf((float)qv, sc, bi);
         }
-        for (int t = 0; t < T; ++t) {
-            // chunk reads rotated by lane/4 (4 chunks) or lane/8 (2 chunks) to spread LDS banks
-            uint4 xr[NCH];
+        // four tokens at a time: four independent fmaf chains, each in column order
+        constexpr int TB = 4;
+        for (int t0 = 0; t0 < T; t0 += TB) {
+            float acc[TB];
 #pragma unroll
-            for (int i = 0; i < NCH; ++i) {
-                const int ch = (NCH == 1) ? 0 : ((i + (NCH == 4 ? (lane >> 2) : (lane >> 3))) & (NCH - 1));
-                const uint4 v = s_xn[t][lane * NCH + ch];
+            for (int q = 0; q < TB; ++q) acc[q] = 0.0f;
+            // chunk reads rotated by lane/4 (4 chunks) or lane/8 (2 chunks) to spread LDS banks;
+            // the accumulation itself runs over the chunks in column order below
+            uint4 xr[TB][NCH];
 #pragma unroll
-                for (int cc = 0; cc < NCH; ++cc)
-                    if (cc == ch) xr[cc] = v;
+            for (int q = 0; q < TB; ++q) {
+                const int t = (t0 + q < T) ? t0 + q : t0;
+#pragma unroll
+                for (int i = 0; i < NCH; ++i) {
+                    const int ch = (NCH == 1) ? 0 : ((i + (NCH == 4 ? (lane >> 2) : (lane >> 3))) & (NCH - 1));
+                    const uint4 v = s_xn[t][lane * NCH + ch];
+#pragma unroll
+                    for (int cc = 0; cc < NCH; ++cc)
+                        if (cc == ch) xr[q][cc] = v;
+                }
             }
-            float acc = 0.0f;
 #pragma unroll
             for (int ch = 0; ch < NCH; ++ch) {
-                float xf[8];
-                unpack_bf16x8(xr[ch], xf);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) acc = fmaf(wv[8 * ch + i], xf[i], acc);
+                for (int q = 0; q < TB; ++q) {
+                    float xf[8];
+                    unpack_bf16x8(xr[q][ch], xf);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[q] = fmaf(wv[8 * ch + i], xf[i], acc[q]);
+                }
             }
-            float v = vmi_wave_sum_canon(acc);
+            float v[TB];
+#pragma unroll
+            for (int q = 0; q < TB; ++q) v[q] = vmi_wave_sum_canon(acc[q]);
             if (lane == 0) {
-                if (is_sg) {
-                    a.sg_logit[t] = v;
-                } else {
-                    if (a.bias) v = v + a.bias[row];
-                    a.logits[(size_t)t * a.E + row] = v;
+#pragma unroll
+                for (int q = 0; q < TB; ++q) {
+                    const int t = t0 + q;
+                    if (t < T) {
+                        if (is_sg) {
+                            a.sg_logit[t] = v[q];
+                        } else {
+                            float lv = v[q];
+                            if (a.bias) lv = lv + a.bias[row];
+                            a.logits[(size_t)t * a.E + row] = lv;
+                        }
+                    }
                 }
             }
         }
