@@ -76,6 +76,71 @@ def cpu_baseline(layers_w, x_bank, args, budget_s: float):
                       f"{el:.1f} s, float64 oracle with OpenMP"}
 
 
+def bench_lm_head(args) -> int:
+    """lm_head GEMV + fused argmax over the full vocabulary: bf16 [V, 2048] head
+    (622 MB at V=151936), T tokens RMS-normalised in the kernel, f32 logits out.
+    Algorithmic bytes per launch = V*H*2 (head) + T*H*2 (x) + H*2 (norm weight)
+    + T*V*4 (logits)."""
+    import torch
+    from vates_amd.head import lm_head
+    from vates_amd.synth import synth_bf16
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    T, H, V = args.T, args.hidden, args.vocab
+    W = synth_bf16(SEED, 0x4EAD, (V, H), std=0.02, device=dev)
+    nw = synth_bf16(SEED, 0x4EAE, (H,), std=0.1, device=dev) + 1.0
+    xs = synth_bf16(SEED, 0x4EAF, (args.steps + args.warmup, T, H), device=dev)
+    logits = torch.empty((T, V), dtype=torch.float32, device=dev)
+    am = torch.empty(T, dtype=torch.int32, device=dev)
+    mx = torch.empty(T, dtype=torch.float32, device=dev)
+    for s in range(args.warmup):
+        lm_head(xs[args.steps + s], W, nw, logits=logits, argmax=am, max_logit=mx)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for s in range(args.steps):
+        lm_head(xs[s], W, nw, logits=logits, argmax=am, max_logit=mx)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    us = ms * 1e3 / args.steps
+    nbytes = V * H * 2 + T * H * 2 + H * 2 + T * V * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    eprint(f"[bench] lm_head T={T} V={V}: {us:.2f} us per launch, {gbs:.1f} GB/s")
+
+    cpu = None
+    if args.cpu_baseline_s > 0:
+        from oracle import oracle as orc
+        from oracle.torch_bridge import u16
+        rows = 8192
+        Wn, xn, nwn = u16(W[:rows]), u16(xs[0]), u16(nw)
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_baseline_s:
+            orc.lm_head(xn, nwn, 1e-6, Wn)
+            done += 1
+        el = time.perf_counter() - t0
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+        threads = min(threads, len(os.sched_getaffinity(0)))
+        cpu = {"value": round(done * (rows * H * 2 + T * rows * 4) / el / 1e9, 4), "unit": "GB/s", "cores": threads,
+               "kind": "port", "sample": f"{done} oracle calls over the first {rows} head rows, T={T}, {el:.1f} s, "
+                                         f"float64 accumulation with OpenMP"}
+    line = {
+        "metric": "lm_head GEMV + argmax HBM GB/s", "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 x bf16 MFMA, f32 accumulate", "data": "synthetic",
+        "config": {"workload": f"lm_head over vocab {V}, hidden {H}, T={T}, RMSNorm fused, f32 logits + argmax",
+                   "T": T, "vocab": V, "hidden": H},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "unit_of_work": "one vmi_lm_head call",
+                     "bytes_per_launch": nbytes, "us_per_launch": round(us, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -89,11 +154,17 @@ def main() -> int:
     ap.add_argument("--experts", type=int, default=512)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-baseline-s", type=float, default=15.0)
+    ap.add_argument("--path", choices=["moe", "lm_head"], default="moe",
+                    help="moe: the 48-layer verify stack (default); lm_head: the vocabulary GEMV + argmax")
+    ap.add_argument("--vocab", type=int, default=151936)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this path is single-device (all weights resident in one "
               "MI355X's HBM); run with --gpus 1", file=sys.stderr)
         return 2
+
+    if args.path == "lm_head":
+        return bench_lm_head(args)
 
     import torch
     from vates_amd.synth import synth_bf16

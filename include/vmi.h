@@ -134,6 +134,29 @@ int vmi_workspace_status(void* workspace, void* stream, uint32_t* flags);
 int vmi_dequant_affine(vmi_qmat m, int rows, int cols, int group, int bits, float* out, void* stream);
 
 /* ------------------------------------------------------------------------
+ * vmi_lm_head -- logits = weight . rmsnorm(x) over the whole vocabulary with
+ * the per-token argmax fused in; replaces the verify forward's tail
+ *   mlx_streaming/mtp/generate.py:208-217 (H_for_logits = inner.norm(h);
+ *   logits = model.lm_head(H_for_logits)) and :756 (preds = mx.argmax of the
+ *   verify logits), and the draft step's argmax
+ *   mlx_streaming/mtp/drafter.py:20-40 (d = int(mx.argmax(lg))).
+ * x bf16 [T, hidden]; norm_weight bf16 [hidden], or NULL for no norm (then x
+ * is used as given); the norm is bf16(x * 1/sqrt(mean(x^2) + norm_eps) * w).
+ * weight bf16 [vocab, hidden] (a tied embedding or the head).  Outputs, each
+ * optional: logits f32 [T, vocab]; argmax int32 [T] and max_logit f32 [T],
+ * the first maximum of each row (ties to the lower vocabulary row, NaN
+ * never wins - mx.argmax's rule).  Accumulation is fp32 (bf16 MFMA).
+ * Supported: T <= 16, hidden a multiple of 512 up to 2048, pointers 16-byte
+ * aligned.  workspace (required when argmax or max_logit is requested):
+ * vmi_lm_head_workspace_bytes(T, vocab) bytes, all zero before the first
+ * call and left zero by every call; one call in flight per workspace.
+ * ------------------------------------------------------------------------ */
+size_t vmi_lm_head_workspace_bytes(int T, int vocab);
+int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weight, float norm_eps,
+                const uint16_t* weight, int vocab, float* logits, int32_t* argmax, float* max_logit,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Synthetic data (no reference counterpart: the reference loads real
  * checkpoints).  Bit-identical to the CPU generator used by the tests:
  * element i = (sum of four 16-bit words of Philox4x32-10 block i/2 -

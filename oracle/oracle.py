@@ -255,3 +255,20 @@ def rmsnorm_bf16(x_bf16, w_bf16, eps):
     _chk(lib().orc_rmsnorm_bf16(_p(x_bf16), _p(np.ascontiguousarray(w_bf16, np.uint16)), c_float(eps), T, H,
                                 _p(out), _p(inv)), "rmsnorm")
     return out, inv
+
+
+def lm_head(x: np.ndarray, norm_w, eps: float, W: np.ndarray):
+    """logits (float64 [T, V]) and |x||w| sums of rmsnorm(x) . W^T; x, norm_w, W
+    are bf16 bit patterns (uint16)."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    W = np.ascontiguousarray(W, dtype=np.uint16)
+    T, H = x.shape
+    V = W.shape[0]
+    nw = None if norm_w is None else np.ascontiguousarray(norm_w, dtype=np.uint16)
+    logits = np.empty((T, V), dtype=np.float64)
+    absdot = np.empty((T, V), dtype=np.float64)
+    fn = lib().orc_lm_head_f64
+    fn.argtypes = [c_void_p, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p, c_void_p]
+    _chk(fn(_p(x), T, H, _p(nw), c_float(eps), _p(W), V, _p(logits), _p(absdot)), "lm_head")
+    return logits, absdot
+

@@ -584,6 +584,45 @@ int orc_route_reduce(float* out, const float* weighted, const int32_t* assignmen
     return ORC_OK;
 }
 
+/* ---------------------------------------------------------------- lm_head */
+/* logits = W . rmsnorm(x) (generate.py:208-217; drafter.py:20-40): xn is the
+ * bf16 RMSNorm output (orc_rmsnorm_bf16, the GPU's exact operand) or x itself
+ * when norm_w is NULL; W bf16 [V, H]; logits[t][v] = sum_h xn[t][h] W[v][h] in
+ * double.  absdot (optional) receives sum_h |xn W|, the scale of the fp32
+ * rounding error of any accumulation order. */
+int orc_lm_head_f64(const uint16_t* x, int T, int H, const uint16_t* norm_w, float eps, const uint16_t* W, int V,
+                    double* logits, double* absdot) {
+    if (T <= 0 || H <= 0 || V <= 0) return ORC_EINVAL;
+    uint16_t* xn = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)T * H);
+    double* xd = (double*)malloc(sizeof(double) * (size_t)T * H);
+    if (!xn || !xd) { free(xn); free(xd); return ORC_ENOMEM; }
+    if (norm_w) {
+        int rc = orc_rmsnorm_bf16(x, norm_w, eps, T, H, xn, NULL);
+        if (rc) { free(xn); free(xd); return rc; }
+    } else {
+        memcpy(xn, x, sizeof(uint16_t) * (size_t)T * H);
+    }
+    for (size_t i = 0; i < (size_t)T * H; ++i) xd[i] = (double)bf16_to_f32(xn[i]);
+#pragma omp parallel for schedule(static)
+    for (int v = 0; v < V; ++v) {
+        const uint16_t* wr = W + (size_t)v * H;
+        for (int t = 0; t < T; ++t) {
+            const double* xr = xd + (size_t)t * H;
+            double acc = 0.0, aa = 0.0;
+            for (int h = 0; h < H; ++h) {
+                const double p = xr[h] * (double)bf16_to_f32(wr[h]);
+                acc += p;
+                aa += fabs(p);
+            }
+            logits[(size_t)t * V + v] = acc;
+            if (absdot) absdot[(size_t)t * V + v] = aa;
+        }
+    }
+    free(xn);
+    free(xd);
+    return ORC_OK;
+}
+
 /* ----------------------------------------------------------- acceptance */
 /* accept_prefix (generate.py:338-351): longest prefix with preds[j]==drafts[j].
  * Emission (generate.py:819, :850-856):

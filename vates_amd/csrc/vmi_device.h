@@ -193,6 +193,29 @@ __device__ __forceinline__ bool vmi_better(float a, int ia, float b, int ib) {
 #define VMI_LDS_DMA4(g, lds) ((void)0)
 #endif
 
+// The same 16-byte copy as opaque inline assembly, for software pipelines:
+// the compiler's wait-count pass does not see it, so it never adds a
+// conservative wait for it ahead of unrelated LDS reads.  The caller orders
+// it with s_waitcnt vmcnt(N) before reading the bytes (vector-memory loads
+// retire in issue order) and retires its own LDS reads of a buffer before
+// refilling it.  lds must be wave-uniform.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is clobbered on purpose
+__device__ __forceinline__ void vmi_lds_dma16_opaque(const void* g, const void* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(g), "s"(m0)
+                 : "memory", "m0");
+#else
+    (void)g;
+    (void)lds;
+#endif
+}
+#pragma clang diagnostic pop
+
 // ---------------------------------------------------------- buffer loads
 // Raw buffer resource over [base, base + bytes): loads past `bytes` return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t vmi_rsrc(const void* base, uint32_t bytes) {

@@ -1,0 +1,309 @@
+// lm_head of the verify batch and of the draft step: logits = W_lm . rmsnorm(h)
+// over the full vocabulary, with the per-token argmax fused in.
+//
+// W is bf16 [V, H] row-major (the tied embedding of the drafter, or the
+// model's head).  One workgroup per CU; each owns a contiguous range of
+// 16-row vocabulary tiles and its waves take the tiles of that range in turn.
+// A wave streams its tile through a ring of NBUF 4 KB LDS buffers filled by
+// global_load_lds: every DMA instruction moves 4 rows x 256 contiguous bytes,
+// so the weight stream is read in long contiguous runs rather than the
+// 16-rows-by-64-bytes pattern an MFMA operand load would need.  Buffers are
+// XOR-swizzled (16-byte unit u of row r is stored at unit u ^ r) so the
+// operand reads out of LDS are free of bank conflicts.  The normalised tokens
+// are staged once per workgroup in LDS as the A operand of
+// v_mfma_f32_16x16x32_bf16 (A = tokens, B = W^T tile), fp32 accumulation.
+//
+// Argmax: every lane keeps the best (logit, row) key of its outputs; keys are
+// reduced per wave, per workgroup, and the last workgroup to finish (an
+// acquire/release arrival counter in the workspace, reset by that workgroup)
+// reduces the per-workgroup keys.  Ties resolve to the lower vocabulary row,
+// NaN ranks below every number - mx.argmax's first-maximum rule
+// (mlx_streaming/mtp/generate.py:756, drafter.py:31).
+//
+// Semantics: generate.py:208-217 (logits = lm_head(norm(h))),
+// drafter.py:20-40 (draft token = argmax of the MTP head's logits).
+
+#include "vmi_device.h"
+#include "vmi_internal.h"
+
+namespace {
+
+constexpr int kHeadMaxH = 2048;      // LDS holds up to this many hidden values per token
+constexpr int kHeadMaxGrid = 1024;   // per-workgroup argmax keys kept in the workspace
+constexpr int kHeadMaxT = 16;
+constexpr int kChunk = 4096;         // bytes of one staged chunk: 16 rows x 256 B (128 hidden values)
+
+__device__ __forceinline__ int head_wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+struct HeadArgs {
+    const uint16_t* x;        // [T, H] bf16
+    const uint16_t* norm_w;   // [H] bf16 or null
+    float eps;
+    const uint16_t* W;        // [V, H] bf16
+    int T, H, V, ntiles;
+    float* logits;            // [T, V] or null
+    uint64_t* partial;        // [gridDim.x, kHeadMaxT] workgroup keys
+    uint32_t* counter;        // arrival counter, 0 between calls
+    int32_t* argmax;          // [T] or null
+    float* maxval;            // [T] or null
+    int want_keys;
+};
+
+__device__ __forceinline__ uint64_t row_max_u64(uint64_t v) {
+    v = vmi_u64_max(v, vmi_dpp_u64<VMI_DPP_XOR1>(v));
+    v = vmi_u64_max(v, vmi_dpp_u64<VMI_DPP_XOR2>(v));
+    v = vmi_u64_max(v, vmi_dpp_u64<VMI_DPP_HALF_MIRROR>(v));
+    v = vmi_u64_max(v, vmi_dpp_u64<VMI_DPP_MIRROR>(v));
+    return v;  // every lane of a 16-lane row holds its row's maximum
+}
+
+// Token t of the batch into LDS as bf16: x itself, or the RMSNorm
+// bf16(x * inv_rms * w) with inv_rms from the canonical fixed-order sum (lane
+// l owns the H/64 contiguous values l*H/64.., summed in order, then the
+// canonical wave tree) - the order the CPU oracle restates.
+__device__ void stage_token(const HeadArgs& a, int t, uint8_t* s_row) {
+    const int lane = threadIdx.x & 63;
+    const int cpl = a.H >> 6;        // values per lane, a multiple of 8
+    const int nv = cpl >> 3;         // 16-byte vectors per lane (<= 4)
+    const uint16_t* xr = a.x + (size_t)t * a.H + lane * cpl;
+    uint4 xv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+        if (v < nv) xv[v] = *reinterpret_cast<const uint4*>(xr + 8 * v);
+    if (a.norm_w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            if (v < nv) {
+                const uint32_t q[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float lo = __uint_as_float(q[i] << 16), hi = __uint_as_float(q[i] & 0xffff0000u);
+                    ss = fmaf(lo, lo, ss);
+                    ss = fmaf(hi, hi, ss);
+                }
+            }
+        }
+        ss = vmi_wave_sum_canon(ss);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)a.H) + a.eps));
+        const uint16_t* nw = a.norm_w + lane * cpl;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            if (v < nv) {
+                const uint4 wv = *reinterpret_cast<const uint4*>(nw + 8 * v);
+                const uint32_t q[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
+                const uint32_t g[4] = {wv.x, wv.y, wv.z, wv.w};
+                uint32_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float lo = (__uint_as_float(q[i] << 16) * inv) * __uint_as_float(g[i] << 16);
+                    const float hi = (__uint_as_float(q[i] & 0xffff0000u) * inv) * __uint_as_float(g[i] & 0xffff0000u);
+                    o[i] = (uint32_t)vmi_f32_to_bf16(lo) | ((uint32_t)vmi_f32_to_bf16(hi) << 16);
+                }
+                xv[v] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+        if (v < nv) *reinterpret_cast<uint4*>(s_row + 2 * (lane * cpl + 8 * v)) = xv[v];
+}
+
+template <int MAXT, int NW, int NBUF>
+__global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
+    constexpr int kRow = 2 * kHeadMaxH + 16;  // LDS bytes per token row (16-byte pad: conflict-free A reads)
+    __shared__ __attribute__((aligned(16))) uint8_t s_x[MAXT * kRow];
+    // One array per ring slot: the compiler tells LDS-DMA targets apart by
+    // variable, so a read of one slot never waits for DMAs into the others.
+    __shared__ __attribute__((aligned(16))) uint8_t s_w0[NW][kChunk];
+    __shared__ __attribute__((aligned(16))) uint8_t s_w1[NW][kChunk];
+    __shared__ __attribute__((aligned(16))) uint8_t s_w2[NBUF > 2 ? NW : 1][NBUF > 2 ? kChunk : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t s_w3[NBUF > 3 ? NW : 1][NBUF > 3 ? kChunk : 16];
+    __shared__ uint64_t s_best[NW][MAXT];
+    __shared__ int s_last;
+
+    const int lane = threadIdx.x & 63, w = head_wave_id();
+    const int T = a.T, H = a.H, V = a.V;
+    for (int t = w; t < T; t += NW) stage_token(a, t, s_x + t * kRow);
+    __syncthreads();
+
+    const int G = gridDim.x, b = blockIdx.x;
+    const int tb = (int)((int64_t)a.ntiles * b / G), te = (int)((int64_t)a.ntiles * (b + 1) / G);
+    const int nmine = (te - tb - w + NW - 1) / NW > 0 ? (te - tb - w + NW - 1) / NW : 0;
+    const int nch = H >> 7;                  // 128 hidden values per chunk
+    const int total = nmine * nch;
+    const size_t row_bytes = (size_t)H * 2;
+
+    const int n = lane & 15, g = lane >> 4;  // MFMA column (vocab row in tile) / K group
+    const uint8_t* wbase = reinterpret_cast<const uint8_t*>(a.W);
+
+    // DMA of chunk q (tile j = q / nch of this wave, hidden block c = q % nch):
+    // instruction i brings rows 4i..4i+3, lane l row 4i + l/16, and fetches the
+    // row's 16-byte unit (l%16) ^ row so that LDS unit u of row r holds unit u ^ r.
+    auto slot = [&](int u) -> uint8_t* {  // u is a constant after unrolling
+        return u == 0 ? &s_w0[w][0] : u == 1 ? &s_w1[w][0] : u == 2 ? &s_w2[w][0] : &s_w3[w][0];
+    };
+    auto issue = [&](int q, uint8_t* buf) {
+        const int j = q / nch, c = q - j * nch;
+        const int tile = tb + w + j * NW;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * i + g;
+            const int row = min(tile * 16 + r, V - 1);
+            const uint8_t* src = wbase + (size_t)row * row_bytes + 256 * c + 16 * ((lane & 15) ^ r);
+            vmi_lds_dma16_opaque(src, buf + 1024 * i);
+        }
+    };
+
+    uint64_t best[4] = {0ull, 0ull, 0ull, 0ull};
+    vmi_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const bool a_live = n < T;  // A row n is token n; rows past T stay zero
+
+    // nch is a multiple of 4 (H % 512 == 0), so every group of NBUF chunks
+    // lies inside one tile and the unrolled body below needs no guards.
+    auto consume = [&](int c, const uint8_t* buf) {
+        const uint8_t* xrow = s_x + n * kRow + 256 * c;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const vmi_u4 bv = *reinterpret_cast<const vmi_u4*>(buf + 256 * n + 16 * ((4 * m + g) ^ n));
+            vmi_u4 av = {0u, 0u, 0u, 0u};
+            if (a_live) av = *reinterpret_cast<const vmi_u4*>(xrow + 64 * m + 16 * g);
+            acc = vmi_mfma_bf16(av, bv, acc);
+        }
+    };
+
+    // A wave without tiles (small vocabularies) issues nothing: every DMA
+    // below addresses a chunk in [0, total).
+    if (total > 0) {
+#pragma unroll
+    for (int u = 0; u < NBUF - 1; ++u) issue(min(u, total - 1), slot(u));
+#pragma unroll 1
+    for (int j = 0; j < nmine; ++j) {
+#pragma unroll 1
+        for (int c0 = 0; c0 < nch; c0 += NBUF) {
+#pragma unroll
+            for (int u = 0; u < NBUF; ++u) {
+                const int q = j * nch + c0 + u;
+                // Refill the slot the previous step read (its LDS reads retire
+                // first).  Past the end the last chunk is fetched again into
+                // slots that are never read.
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                issue(min(q + NBUF - 1, total - 1), slot((u + NBUF - 1) % NBUF));
+                wait_vmcnt<4 * (NBUF - 1)>();
+                consume(c0 + u, slot(u));
+            }
+        }
+        // D[token 4g + r][vocab row n] sits in acc[r].
+        const int row = (tb + w + j * NW) * 16 + n;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 4 * g + r;
+            if (t < T && row < V) {
+                if (a.logits) a.logits[(size_t)t * V + row] = acc[r];
+                best[r] = vmi_u64_max(best[r], vmi_rank_key(acc[r], row));
+            }
+        }
+        acc = vmi_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    }
+    wait_vmcnt<0>();
+    if (!a.want_keys) return;
+
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint64_t k = row_max_u64(best[r]);
+        const int t = 4 * g + r;
+        if (n == 0 && t < MAXT) s_best[w][t] = k;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int t = 0; t < T; ++t) {
+            uint64_t k = 0ull;
+            for (int v = 0; v < NW; ++v) k = vmi_u64_max(k, s_best[v][t]);
+            __hip_atomic_store(&a.partial[(size_t)b * kHeadMaxT + t], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const uint32_t prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (prev == (uint32_t)(G - 1));
+    }
+    __syncthreads();
+    if (!s_last) return;
+    for (int t = w; t < T; t += NW) {
+        uint64_t k = 0ull;
+        for (int i = lane; i < G; i += 64)
+            k = vmi_u64_max(k, __hip_atomic_load(&a.partial[(size_t)i * kHeadMaxT + t], __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT));
+        k = vmi_wave_max_u64(k);
+        if (lane == 0) {
+            if (a.argmax) a.argmax[t] = (int32_t)(0xffffffffu - (uint32_t)k);
+            if (a.maxval) a.maxval[t] = vmi_order_key_value((uint32_t)(k >> 32));
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+int device_cus() {
+    static int cached = 0;
+    if (cached > 0) return cached;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                hipSuccess || cus <= 0)
+        cus = 256;
+    cached = cus;
+    return cached;
+}
+
+}  // namespace
+
+extern "C" size_t vmi_lm_head_workspace_bytes(int T, int vocab) {
+    if (T <= 0 || vocab <= 0) return 0;
+    return vmi::align256((size_t)kHeadMaxGrid * kHeadMaxT * sizeof(uint64_t)) + 256;
+}
+
+extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weight, float norm_eps,
+                           const uint16_t* weight, int vocab, float* logits, int32_t* argmax, float* max_logit,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    vmi::clear_error();
+    if (T <= 0 || T > kHeadMaxT) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, %d]", T, kHeadMaxT);
+    if (hidden <= 0 || hidden % 512 || hidden > kHeadMaxH)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "hidden=%d must be a multiple of 512 up to %d", hidden, kHeadMaxH);
+    if (vocab <= 0) return vmi::fail(VMI_ERR_INVALID, "vocab=%d", vocab);
+    if ((size_t)vocab * (size_t)hidden * 2 > ((size_t)1 << 40)) return vmi::fail(VMI_ERR_UNSUPPORTED, "head too large");
+    if (!x || !weight) return vmi::fail(VMI_ERR_INVALID, "null x/weight");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+         reinterpret_cast<uintptr_t>(norm_weight)) & 15)
+        return vmi::fail(VMI_ERR_INVALID, "x, weight and norm_weight must be 16-byte aligned");
+    const bool want_keys = argmax || max_logit;
+    if (!logits && !want_keys) return vmi::fail(VMI_ERR_INVALID, "nothing to compute (logits, argmax and max all null)");
+    const size_t need = vmi_lm_head_workspace_bytes(T, vocab);
+    if (want_keys && (!workspace || workspace_bytes < need))
+        return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+
+    HeadArgs a{};
+    a.x = x; a.norm_w = norm_weight; a.eps = norm_eps; a.W = weight;
+    a.T = T; a.H = hidden; a.V = vocab; a.ntiles = (vocab + 15) / 16;
+    a.logits = logits; a.argmax = argmax; a.maxval = max_logit; a.want_keys = want_keys ? 1 : 0;
+    if (want_keys) {
+        uint8_t* ws = static_cast<uint8_t*>(workspace);
+        a.partial = reinterpret_cast<uint64_t*>(ws);
+        a.counter = reinterpret_cast<uint32_t*>(ws + vmi::align256((size_t)kHeadMaxGrid * kHeadMaxT * sizeof(uint64_t)));
+    }
+    int G = device_cus();
+    if (G > kHeadMaxGrid) G = kHeadMaxGrid;
+    if (G > a.ntiles) G = a.ntiles;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (T <= 4)
+        hipLaunchKernelGGL((k_head<4, 8, 4>), dim3(G), dim3(8 * 64), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_head<16, 8, 2>), dim3(G), dim3(8 * 64), 0, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return vmi::hip_fail(e, "k_head launch");
+    return VMI_OK;
+}

@@ -1,0 +1,57 @@
+"""lm_head over the vocabulary with the argmax fused in (libvmi ``vmi_lm_head``).
+
+The analogue of the verify forward's tail ``logits = model.lm_head(inner.norm(h))``
+followed by ``preds = mx.argmax(logits, -1)`` (mlx_streaming/mtp/generate.py:208-217,
+:756) and of the draft step's ``int(mx.argmax(lg))`` (mlx_streaming/mtp/drafter.py:20-40).
+Errors raise ``VmiError``; there is no fallback path.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from ._lib import VmiError, check, load
+from .moe import _require, _stream_handle, workspace
+
+
+def lm_head(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor] = None, *,
+            eps: float = 1e-6, want_logits: bool = True, logits: Optional[torch.Tensor] = None,
+            argmax: Optional[torch.Tensor] = None, max_logit: Optional[torch.Tensor] = None, stream=None):
+    """Returns (logits f32 [T, V] or None, argmax int32 [T], max logit f32 [T]).
+
+    x bf16 [T, H] (T <= 16), weight bf16 [V, H], norm_weight bf16 [H] or None.
+    """
+    dev = x.device
+    if x.dim() != 2:
+        raise VmiError(f"x must be [T, hidden], got {tuple(x.shape)}")
+    T, H = x.shape
+    if weight.dim() != 2 or weight.shape[1] != H:
+        raise VmiError(f"weight must be [vocab, {H}], got {tuple(weight.shape)}")
+    V = weight.shape[0]
+    _require(x, "x", 2, dev)
+    _require(weight, "weight", 2, dev)
+    if norm_weight is not None:
+        _require(norm_weight, "norm_weight", 2, dev)
+        if norm_weight.numel() != H:
+            raise VmiError(f"norm_weight must have {H} elements")
+    if want_logits and logits is None:
+        logits = torch.empty((T, V), dtype=torch.float32, device=dev)
+    if argmax is None:
+        argmax = torch.empty(T, dtype=torch.int32, device=dev)
+    if max_logit is None:
+        max_logit = torch.empty(T, dtype=torch.float32, device=dev)
+    for t, name, n in ((logits, "logits", T * V), (argmax, "argmax", T), (max_logit, "max_logit", T)):
+        if t is not None:
+            _require(t, name, 4, dev)
+            if t.numel() != n:
+                raise VmiError(f"{name} must have {n} elements")
+    sh = _stream_handle(stream)
+    lib = load()
+    nbytes = lib.vmi_lm_head_workspace_bytes(T, V)
+    ws = workspace(nbytes, dev, sh, tag="lm_head")
+    rc = lib.vmi_lm_head(x.data_ptr(), T, H, None if norm_weight is None else norm_weight.data_ptr(), float(eps),
+                         weight.data_ptr(), V, None if logits is None else logits.data_ptr(), argmax.data_ptr(),
+                         max_logit.data_ptr(), ws.data_ptr(), ws.numel(), sh)
+    check(rc, "vmi_lm_head")
+    return logits, argmax, max_logit

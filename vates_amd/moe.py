@@ -48,11 +48,12 @@ def _require(t: torch.Tensor, name: str, elem: int, device: torch.device) -> Non
         raise VmiError(f"{name} must have {elem}-byte elements (got {t.dtype})")
 
 
-def workspace(nbytes: int, device: torch.device, stream_handle: int) -> torch.Tensor:
-    """Workspace cached per (device, stream).  It starts zero-filled so the
-    device status word reads 0; calls on one stream are serialised, so reuse
-    across them is safe."""
-    key = (device.index, stream_handle)
+def workspace(nbytes: int, device: torch.device, stream_handle: int, tag: str = "moe") -> torch.Tensor:
+    """Workspace cached per (device, stream, tag).  It starts zero-filled so
+    the device status word and arrival counters read 0; calls on one stream are
+    serialised, so reuse across them is safe.  Entry points whose workspaces
+    keep state between calls (status word, counters) use distinct tags."""
+    key = (device.index, stream_handle, tag)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
