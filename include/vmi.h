@@ -157,6 +157,64 @@ int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weigh
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Acceptance.  Every entry point writes an int32 result record of 4 + K + 1
+ * entries: [0] n_emitted, [1] matched (drafts accepted), [2] accepted_len
+ * (verify positions whose state is kept), [3] winning path (-1: no finite
+ * logit in some row, nothing emitted), [4 ..] the emitted tokens.
+ *
+ * vmi_accept_greedy -- replaces accept_prefix and the emission rules
+ *   mlx_streaming/mtp/generate.py:338-351 (longest prefix with preds == drafts),
+ *   :819 (accepted_len = min(matched + 1, K)), :850-856 (drafts[:m] + [preds[m]],
+ *   or drafts[:K] when all match), and tree_verify_step's winner selection
+ *   :379-386 (most matches, ties to the lower path index).
+ * drafts int32 [P, K]; preds int32 [P, K + mode] (argmax of the verify
+ * logits, e.g. from vmi_lm_head).  mode 0: the verify batch is [x, d1..d_{K-1}]
+ * (the reference's T = K layout, K predictions); mode 1: [x, d1..dK] (T = K+1,
+ * emits drafts[:m] + [preds[m]] for every m <= K, accepted_len = m + 1; P = 1).
+ * K <= 15, P <= 65535.
+ * ------------------------------------------------------------------------ */
+int vmi_accept_greedy(const int32_t* drafts, const int32_t* preds, int P, int K, int mode, int32_t* result,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * vmi_accept_stochastic -- speculative sampling (Leviathan et al. 2023,
+ * Algorithm 1; Chen et al. 2023) in one kernel.  No reference counterpart:
+ * the reference accepts greedily only (generate.py:338-351); this is the
+ * published method on its verify layout.
+ * target_logits f32 [K+1, vocab] (verify rows of [x, d1..dK]); draft_logits
+ * f32 [K, vocab] (the drafter's rows that d1..dK were sampled from) or NULL
+ * for greedy drafts (q one-hot at each draft); drafts int32 [K].
+ * p, q = temperature / top-p transforms on integer masses:
+ *   W_j = floor(2^31 * 2^((l_j - max l) * s)), s = fp32((1/temperature)*log2 e),
+ *   nucleus = {W_j >= theta}, theta the largest value whose at-or-above mass
+ *   reaches ceil(top_p * sum W) (ties join together), p(j) = W_j / nucleus mass.
+ * Draft i is kept when U_i 2^-32 * q(d_i) <= p(d_i) and p(d_i) > 0; at the first
+ * rejection the token is drawn from floor(2^31 max(0, p - q)) masses (from p
+ * when those are all zero); with every draft kept a bonus token is drawn from
+ * p_K.  Draws: t = floor(V_i * total / 2^32), token = first index whose
+ * running mass exceeds t.  (U_i, V_i) = words 0, 1 of Philox4x32-10 with key
+ * seed and counter (offset lo, offset hi, i, 0x5A3D1E57).  Bit-identical to
+ * the CPU oracle.  temperature > 0 (use vmi_accept_greedy for 0), 0 < top_p <= 1.
+ * workspace: vmi_accept_stochastic_workspace_bytes(K, vocab, draft_logits != NULL)
+ * bytes, zero before the first call and left so by every call.
+ * ------------------------------------------------------------------------ */
+size_t vmi_accept_stochastic_workspace_bytes(int K, int vocab, int has_draft_logits);
+int vmi_accept_stochastic(const float* target_logits, const float* draft_logits, const int32_t* drafts, int K,
+                          int vocab, float temperature, float top_p, uint64_t seed, uint64_t offset, int32_t* result,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * vmi_sample_top_p -- one token per row of logits f32 [rows, vocab] from the
+ * same temperature / top-p distribution (row r uses V_r of counter
+ * (offset, r)); the drafter's sampler when drafting stochastically.  The
+ * reference drafts by argmax only (drafter.py:20-40).  out int32 [rows]
+ * (-1 for a row without a finite logit).
+ * ------------------------------------------------------------------------ */
+size_t vmi_sample_top_p_workspace_bytes(int rows, int vocab);
+int vmi_sample_top_p(const float* logits, int rows, int vocab, float temperature, float top_p, uint64_t seed,
+                     uint64_t offset, int32_t* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Synthetic data (no reference counterpart: the reference loads real
  * checkpoints).  Bit-identical to the CPU generator used by the tests:
  * element i = (sum of four 16-bit words of Philox4x32-10 block i/2 -

@@ -272,3 +272,44 @@ def lm_head(x: np.ndarray, norm_w, eps: float, W: np.ndarray):
     _chk(fn(_p(x), T, H, _p(nw), c_float(eps), _p(W), V, _p(logits), _p(absdot)), "lm_head")
     return logits, absdot
 
+
+
+def sd_masses(logits_row, temperature: float, top_p: float):
+    """Integer masses W (uint32 [V]), nucleus threshold, Z_S and Z of one row."""
+    l = np.ascontiguousarray(logits_row, dtype=np.float32)
+    V = l.size
+    W = np.empty(V, dtype=np.uint32)
+    th = (c_uint32 * 1)()
+    zs = (c_uint64 * 1)()
+    z = (c_uint64 * 1)()
+    fn = lib().orc_sd_masses
+    fn.argtypes = [c_void_p, c_int, c_float, c_float, c_void_p, c_void_p, c_void_p, c_void_p]
+    _chk(fn(_p(l), V, c_float(temperature), c_float(top_p), _p(W), th, zs, z), "sd_masses")
+    return W, int(th[0]), int(zs[0]), int(z[0])
+
+
+def sample_top_p(logits, temperature: float, top_p: float, seed: int, offset: int) -> np.ndarray:
+    l = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, V = l.shape
+    out = np.empty(rows, dtype=np.int32)
+    fn = lib().orc_sample_top_p
+    fn.argtypes = [c_void_p, c_int, c_int, c_float, c_float, c_uint64, c_uint64, c_void_p]
+    _chk(fn(_p(l), rows, V, c_float(temperature), c_float(top_p), c_uint64(seed), c_uint64(offset), _p(out)),
+         "sample_top_p")
+    return out
+
+
+def accept_stochastic(target, draft, drafts, temperature: float, top_p: float, seed: int, offset: int):
+    """(emitted tokens, matched, accepted_len) of speculative sampling."""
+    t = np.ascontiguousarray(target, dtype=np.float32)
+    K = t.shape[0] - 1
+    V = t.shape[1]
+    d = None if draft is None else np.ascontiguousarray(draft, dtype=np.float32)
+    dr = np.ascontiguousarray(drafts, dtype=np.int32)
+    res = np.zeros(4 + K + 1, dtype=np.int32)
+    fn = lib().orc_accept_stochastic
+    fn.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_float, c_uint64, c_uint64, c_void_p]
+    _chk(fn(_p(t), _p(d), _p(dr), K, V, c_float(temperature), c_float(top_p), c_uint64(seed), c_uint64(offset),
+            _p(res)), "accept_stochastic")
+    n = int(res[0])
+    return [int(v) for v in res[4:4 + n]], int(res[1]), int(res[2]), res

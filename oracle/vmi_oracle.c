@@ -679,4 +679,196 @@ int orc_accept_tree(const int32_t* paths, const int32_t* preds, int P, int K, in
     return orc_accept_greedy(paths + best * K, preds + best * K, K, 0, emitted, n_emitted, matched, accepted_len);
 }
 
+/* ----------------------------------------------- stochastic acceptance
+ * Speculative sampling (Leviathan et al. 2023, Algorithm 1; Chen et al. 2023):
+ * draft d_i is kept when u_i * q(d_i) <= p(d_i); at the first rejection the
+ * token is drawn from norm(max(0, p - q)); when all K drafts are kept a bonus
+ * token is drawn from p_K.  The reference has no stochastic path (its drafts
+ * and acceptance are greedy, generate.py:338-351); this is the published
+ * method on the reference's verify layout (K drafts, K+1 target rows).
+ *
+ * p and q are temperature / top-p (nucleus, Holtzman et al. 2020) transforms
+ * of logits, defined on integer masses so that every order of summation gives
+ * the same bits:
+ *   s = (float)((1/temperature) * log2(e))          (double, then rounded)
+ *   W_j = floor(2^31 * 2^z), z = (l_j - max_l) * s    (fp32 ops; 2^z below)
+ *   Z = sum W_j (uint64); C = ceil(top_p * Z) (double)
+ *   theta = the largest value with sum_{W_j >= theta} W_j >= C
+ *   nucleus S = {j : W_j >= theta, W_j > 0}, Z_S = sum_S W_j
+ *   p(j) = W_j / Z_S on S, 0 elsewhere (double division)
+ * 2^z: n = rint(z), f = z - n in [-1/2, 1/2], degree-6 Taylor polynomial of
+ * 2^f (coefficients (ln 2)^k / k! rounded to fp32, Horner with fmaf), scaled
+ * by 2^(n + 31) exactly; W = 0 for z < -32 or NaN.  Relative error of the
+ * polynomial against 2^f: < 2.5e-7.
+ * Uniforms: Philox4x32-10, key (seed lo, seed hi), counter (offset lo,
+ * offset hi, position i, 0x5A3D1E57): word 0 = U_i (acceptance, u = U_i 2^-32),
+ * word 1 = V_i (resampling).
+ * Sampling from integer masses R_j with total R: t = floor(V_i * R / 2^32)
+ * (128-bit product), token = smallest j with R_0 + .. + R_j > t.
+ * Residual masses: R_j = floor(2^31 * max(0, p(j) - q(j))) (double); when they
+ * sum to 0 the token is drawn from p.  Without draft logits q is one-hot at
+ * the draft (greedy drafting). */
+static const float kExp2C[7] = {0x1p+0f, 0x1.62e43p-1f, 0x1.ebfbep-3f, 0x1.c6b08ep-5f,
+                                0x1.3b2ab6p-7f, 0x1.5d87fep-10f, 0x1.430912p-13f};
+
+static inline uint32_t sd_weight(float l, float M, float s2) {
+    const float z = (l - M) * s2;
+    if (!(z >= -32.0f)) return 0u;
+    const float n = rintf(z);
+    const float f = z - n;
+    float p = kExp2C[6];
+    for (int k = 5; k >= 0; --k) p = fmaf(p, f, kExp2C[k]);
+    return (uint32_t)ldexpf(p, (int)n + 31);
+}
+
+float orc_sd_scale(float temperature) { return (float)((1.0 / (double)temperature) * 1.4426950408889634); }
+
+static int cmp_u32_desc(const void* a, const void* b) {
+    const uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
+    return (x < y) - (x > y);
+}
+
+/* Integer masses and nucleus of one logit row (definitions above).  Returns
+ * 0, or ORC_EINVAL when no logit is finite (Z = 0). */
+int orc_sd_masses(const float* l, int V, float temperature, float top_p, uint32_t* W, uint32_t* theta,
+                  uint64_t* zs, uint64_t* z_all) {
+    if (V <= 0 || !(temperature > 0.0f)) return ORC_EINVAL;
+    const float s2 = orc_sd_scale(temperature);
+    float M = -INFINITY;
+    for (int j = 0; j < V; ++j) M = fmaxf(M, l[j]);
+    uint64_t Z = 0;
+    for (int j = 0; j < V; ++j) {
+        W[j] = sd_weight(l[j], M, s2);
+        Z += W[j];
+    }
+    *z_all = Z;
+    if (Z == 0) return ORC_EINVAL;
+    uint64_t C = (top_p >= 1.0f) ? Z : (uint64_t)ceil((double)top_p * (double)Z);
+    if (C == 0) C = 1;
+    uint32_t* srt = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)V);
+    if (!srt) return ORC_ENOMEM;
+    memcpy(srt, W, sizeof(uint32_t) * (size_t)V);
+    qsort(srt, (size_t)V, sizeof(uint32_t), cmp_u32_desc);
+    uint64_t acc = 0;
+    uint32_t th = 1;
+    for (int i = 0; i < V && srt[i] > 0;) {
+        const uint32_t v = srt[i];
+        while (i < V && srt[i] == v) acc += srt[i++];  /* every tie of v joins at once */
+        if (acc >= C) { th = v; break; }
+    }
+    free(srt);
+    uint64_t Zs = 0;
+    for (int j = 0; j < V; ++j)
+        if (W[j] >= th && W[j] > 0) Zs += W[j];
+    *theta = th;
+    *zs = Zs;
+    return ORC_OK;
+}
+
+static void sd_uniforms(uint64_t seed, uint64_t offset, int i, uint32_t* U, uint32_t* Vr) {
+    const uint32_t ctr[4] = {(uint32_t)offset, (uint32_t)(offset >> 32), (uint32_t)i, 0x5A3D1E57u};
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t o[4];
+    orc_philox4x32_10(ctr, key, o);
+    *U = o[0];
+    *Vr = o[1];
+}
+
+static int sd_pick(const uint32_t* R, int V, uint64_t total, uint32_t vr) {
+    const uint64_t t = (uint64_t)(((unsigned __int128)total * ((uint64_t)vr << 32)) >> 64);
+    uint64_t acc = 0;
+    for (int j = 0; j < V; ++j) {
+        acc += R[j];
+        if (acc > t) return j;
+    }
+    return V - 1; /* unreachable when total = sum R */
+}
+
+/* Samples one token per row of logits [rows, V] from the temperature / top-p
+ * distribution with uniform V_r of position r (the drafter's sampler). */
+int orc_sample_top_p(const float* logits, int rows, int V, float temperature, float top_p, uint64_t seed,
+                     uint64_t offset, int32_t* out) {
+    uint32_t* W = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)V);
+    if (!W) return ORC_ENOMEM;
+    for (int r = 0; r < rows; ++r) {
+        uint32_t th;
+        uint64_t zs, z;
+        int rc = orc_sd_masses(logits + (size_t)r * V, V, temperature, top_p, W, &th, &zs, &z);
+        if (rc) { free(W); return rc; }
+        for (int j = 0; j < V; ++j)
+            if (W[j] < th) W[j] = 0;
+        uint32_t U, Vr;
+        sd_uniforms(seed, offset, r, &U, &Vr);
+        out[r] = sd_pick(W, V, zs, Vr);
+    }
+    free(W);
+    return ORC_OK;
+}
+
+/* result int32 [4 + K + 1]: n_emitted, matched, accepted_len, best_path (0),
+ * emitted tokens.  target [K+1, V]; draft [K, V] or NULL (one-hot drafts). */
+int orc_accept_stochastic(const float* target, const float* draft, const int32_t* drafts, int K, int V,
+                          float temperature, float top_p, uint64_t seed, uint64_t offset, int32_t* result) {
+    if (K <= 0 || V <= 0) return ORC_EINVAL;
+    const int nd = (K + 1) + (draft ? K : 0);
+    uint32_t* W = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)V * nd);
+    uint32_t* R = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)V);
+    uint32_t th[64];
+    uint64_t zs[64];
+    if (!W || !R || nd > 64) { free(W); free(R); return ORC_ENOMEM; }
+    for (int d = 0; d < nd; ++d) {
+        const float* row = d <= K ? target + (size_t)d * V : draft + (size_t)(d - K - 1) * V;
+        uint64_t z;
+        int rc = orc_sd_masses(row, V, temperature, top_p, W + (size_t)d * V, &th[d], &zs[d], &z);
+        if (rc) { free(W); free(R); return rc; }
+    }
+#define PMASS(d, j) (W[(size_t)(d) * V + (j)] >= th[d] ? W[(size_t)(d) * V + (j)] : 0u)
+    int m = 0;
+    for (; m < K; ++m) {
+        const int dj = drafts[m];
+        uint32_t U, Vr;
+        sd_uniforms(seed, offset, m, &U, &Vr);
+        double pp = 0.0, qq = 1.0;
+        if (dj >= 0 && dj < V) {
+            pp = (double)PMASS(m, dj) / (double)zs[m];
+            if (draft) qq = (double)PMASS(K + 1 + m, dj) / (double)zs[K + 1 + m];
+        }
+        const double u = (double)U * 0x1p-32;
+        if (!(pp > 0.0 && u * qq <= pp)) break;
+    }
+    uint32_t U, Vr;
+    sd_uniforms(seed, offset, m, &U, &Vr);
+    int tok;
+    if (m < K) {
+        uint64_t tot = 0;
+        for (int j = 0; j < V; ++j) {
+            const double pj = (double)PMASS(m, j) / (double)zs[m];
+            double qj;
+            if (draft) qj = (double)PMASS(K + 1 + m, j) / (double)zs[K + 1 + m];
+            else qj = (j == drafts[m]) ? 1.0 : 0.0;
+            const double r = pj - qj;
+            R[j] = r > 0.0 ? (uint32_t)(r * 0x1p31) : 0u;
+            tot += R[j];
+        }
+        if (tot == 0) {
+            for (int j = 0; j < V; ++j) R[j] = PMASS(m, j);
+            tot = zs[m];
+        }
+        tok = sd_pick(R, V, tot, Vr);
+    } else {
+        for (int j = 0; j < V; ++j) R[j] = PMASS(K, j);
+        tok = sd_pick(R, V, zs[K], Vr);
+    }
+#undef PMASS
+    result[0] = m + 1;
+    result[1] = m;
+    result[2] = m + 1;
+    result[3] = 0;
+    for (int j = 0; j < m; ++j) result[4 + j] = drafts[j];
+    result[4 + m] = tok;
+    free(W);
+    free(R);
+    return ORC_OK;
+}
+
 int orc_version(void) { return 1; }

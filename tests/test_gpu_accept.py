@@ -1,0 +1,155 @@
+"""GPU acceptance kernels against the CPU oracle: every result record is
+bit-exact (integer work and IEEE-double decisions on integer masses).
+
+Greedy: the reference's literal accept_prefix answers
+(tests/test_mtp_generate.py:211-223, kept in tests/golden), random chains in
+both verify layouts and P-path trees.  Stochastic: random small vocabularies
+with and without draft logits, the full 151,936 vocabulary with target logits
+N(0, 3) and a planted argmax agreement of 0.7 at temperature 0.7 / top-p 0.9,
+and the edge cases (identical draft, a row without finite logits).
+"""
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_known_answers.json"
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _t(a, dev, dtype=None):
+    import torch
+    return torch.as_tensor(np.ascontiguousarray(a), device=dev, dtype=dtype)
+
+
+def test_greedy_reference_known_answers(gpu, orc):
+    log("case: greedy accept, reference known answers")
+    import torch
+    from vates_amd.accept import accept_greedy, decode_result
+    for case in json.loads(GOLDEN.read_text())["accept_prefix"]:
+        d = _t(np.array(case["drafts"], np.int32), gpu)
+        p = _t(np.array(case["preds"], np.int32), gpu)
+        r = decode_result(accept_greedy(d, p, mode=0).cpu())
+        assert r["matched"] == case["matched"]
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_greedy_random_chains(gpu, orc, mode):
+    log(f"case: greedy accept random chains mode={mode}")
+    import torch
+    from vates_amd.accept import accept_greedy, decode_result
+    rng = np.random.default_rng(40 + mode)
+    for _ in range(200):
+        K = int(rng.integers(1, 16))
+        drafts = rng.integers(0, 4, K).astype(np.int32)
+        preds = np.where(rng.random(K + mode) < 0.7, np.append(drafts, 0)[:K + mode],
+                         rng.integers(0, 4, K + mode)).astype(np.int32)
+        em, m, acc = orc.accept_greedy(drafts, preds, mode)
+        r = decode_result(accept_greedy(_t(drafts, gpu), _t(preds, gpu), mode=mode).cpu())
+        assert (r["emitted"], r["matched"], r["accepted_len"], r["path"]) == (em, m, acc, 0)
+
+
+def test_greedy_tree_paths(gpu, orc):
+    log("case: greedy tree verify winners")
+    import torch
+    from vates_amd.accept import accept_greedy, decode_result
+    rng = np.random.default_rng(42)
+    for _ in range(200):
+        P, K = int(rng.integers(1, 70)), int(rng.integers(1, 6))
+        paths = rng.integers(0, 3, (P, K)).astype(np.int32)
+        preds = rng.integers(0, 3, (P, K)).astype(np.int32)
+        best, em, m, acc = orc.accept_tree(paths, preds)
+        r = decode_result(accept_greedy(_t(paths, gpu), _t(preds, gpu), mode=0).cpu())
+        assert (r["path"], r["emitted"], r["matched"], r["accepted_len"]) == (best, em, m, acc)
+
+
+def _record(orc, target, draft, drafts, temp, top_p, seed, offset):
+    return orc.accept_stochastic(target, draft, drafts, temp, top_p, seed, offset)[3]
+
+
+@pytest.mark.parametrize("with_draft", [True, False])
+def test_stochastic_small_vocab_bit_exact(gpu, orc, with_draft):
+    log(f"case: stochastic accept small vocab with_draft={with_draft}")
+    import torch
+    from vates_amd.accept import accept_stochastic
+    rng = np.random.default_rng(50 + with_draft)
+    for case in range(120):
+        K = int(rng.integers(1, 6))
+        V = int(rng.choice([2, 7, 64, 1000, 4099]))
+        temp = float(rng.choice([0.7, 1.0, 1.7]))
+        top_p = float(rng.choice([0.9, 1.0, 0.5]))
+        target = rng.normal(0, 3, (K + 1, V)).astype(np.float32)
+        draft = rng.normal(0, 3, (K, V)).astype(np.float32) if with_draft else None
+        if case % 3 == 0 and with_draft:
+            draft = target[:K] + rng.normal(0, 0.3, (K, V)).astype(np.float32)
+        drafts = (orc.sample_top_p(draft, temp, top_p, 7, case) if with_draft
+                  else np.argmax(target[:K] + rng.normal(0, 2, (K, V)), axis=1).astype(np.int32))
+        seed, offset = int(rng.integers(0, 2**63)), case
+        want = _record(orc, target, draft, drafts, temp, top_p, seed, offset)
+        got = accept_stochastic(_t(target, gpu), None if draft is None else _t(draft, gpu), _t(drafts, gpu),
+                                temperature=temp, top_p=top_p, seed=seed, offset=offset).cpu().numpy()
+        assert np.array_equal(got[:4 + want[0]], want[:4 + want[0]]), (case, K, V, got, want)
+
+
+def test_stochastic_full_vocab_planted(gpu, orc):
+    log("case: stochastic accept V=151936 K=3, N(0,3) logits, planted agreement 0.7")
+    import torch
+    from vates_amd.accept import accept_stochastic
+    rng = np.random.default_rng(60)
+    K, V = 3, 151936
+    hist = np.zeros(K + 1, int)
+    for case in range(6):
+        target = rng.normal(0, 3, (K + 1, V)).astype(np.float32)
+        draft = rng.normal(0, 3, (K, V)).astype(np.float32)
+        drafts = np.argmax(draft, axis=1).astype(np.int32)
+        for i in range(K):
+            if rng.random() < 0.7:
+                target[i, drafts[i]] = target[i].max() + 1.0
+        for dl in (draft, None):
+            want = _record(orc, target, dl, drafts, 0.7, 0.9, 99, case)
+            got = accept_stochastic(_t(target, gpu), None if dl is None else _t(dl, gpu), _t(drafts, gpu),
+                                    temperature=0.7, top_p=0.9, seed=99, offset=case).cpu().numpy()
+            assert np.array_equal(got[:4 + want[0]], want[:4 + want[0]]), (case, got, want)
+            hist[want[1]] += 1
+    log(f"matched histogram {hist.tolist()}")
+
+
+def test_stochastic_edges(gpu, orc):
+    log("case: stochastic accept edges (identical draft, NaN row)")
+    import torch
+    from vates_amd.accept import accept_stochastic, decode_result, sample_top_p
+    rng = np.random.default_rng(61)
+    K, V = 4, 5000
+    target = rng.normal(0, 3, (K + 1, V)).astype(np.float32)
+    tt = _t(target, gpu)
+    for s in range(10):
+        drafts = sample_top_p(tt[:K].contiguous(), temperature=0.7, top_p=0.9, seed=3, offset=s)
+        r = decode_result(accept_stochastic(tt, tt[:K].contiguous(), drafts, temperature=0.7, top_p=0.9, seed=4,
+                                            offset=s).cpu())
+        assert r["matched"] == K and r["emitted"][:K] == drafts.cpu().tolist()
+    bad = target.copy()
+    bad[2] = np.nan
+    r = decode_result(accept_stochastic(_t(bad, gpu), None, _t(np.zeros(K, np.int32), gpu), temperature=0.7,
+                                        top_p=0.9, seed=1, offset=0).cpu())
+    assert r["path"] == -1 and r["emitted"] == []
+
+
+@pytest.mark.parametrize("V", [3, 1000, 151936])
+def test_sample_top_p_bit_exact(gpu, orc, V):
+    log(f"case: sample_top_p V={V}")
+    import torch
+    from vates_amd.accept import sample_top_p
+    rng = np.random.default_rng(70)
+    rows = 5
+    logits = rng.normal(0, 3, (rows, V)).astype(np.float32)
+    for temp, top_p in ((0.7, 0.9), (1.0, 1.0), (0.3, 0.5)):
+        want = orc.sample_top_p(logits, temp, top_p, 1234, 77)
+        got = sample_top_p(_t(logits, gpu), temperature=temp, top_p=top_p, seed=1234, offset=77).cpu().numpy()
+        assert np.array_equal(got, want)

@@ -62,6 +62,13 @@ _SIGNATURES = {
     "vmi_synth_quantized": (c_int, [c_uint64, c_uint32, c_int64, c_int, c_int, c_int, c_float, c_void_p, c_void_p,
                                     c_void_p, c_void_p]),
     "vmi_synth_bf16": (c_int, [c_uint64, c_uint32, c_int64, c_float, c_void_p, c_void_p]),
+    "vmi_accept_greedy": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "vmi_accept_stochastic_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "vmi_accept_stochastic": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_float, c_uint64,
+                                      c_uint64, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "vmi_sample_top_p_workspace_bytes": (c_size_t, [c_int, c_int]),
+    "vmi_sample_top_p": (c_int, [c_void_p, c_int, c_int, c_float, c_float, c_uint64, c_uint64, c_void_p, c_void_p,
+                                 c_size_t, c_void_p]),
     "vmi_lm_head_workspace_bytes": (c_size_t, [c_int, c_int]),
     "vmi_lm_head": (c_int, [c_void_p, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p, c_void_p,
                             c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -1,0 +1,99 @@
+"""Acceptance of a speculative verify step on the device (libvmi).
+
+* ``accept_greedy`` mirrors ``accept_prefix`` plus the emission rules of the
+  reference's decode loop (mlx_streaming/mtp/generate.py:338-351, :819,
+  :850-856) and the tree winner rule (:379-386).
+* ``accept_stochastic`` is speculative sampling (Leviathan et al. 2023) on the
+  same verify layout; the reference has no stochastic path.
+* ``sample_top_p`` draws one token per logit row from the temperature / top-p
+  distribution that ``accept_stochastic`` uses.
+
+Results stay on the device: an int32 record [n_emitted, matched, accepted_len,
+path, tokens...]; ``decode_result`` turns a host copy into Python values.
+Errors raise ``VmiError``; there is no fallback path.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from ._lib import VmiError, check, load
+from .moe import _require, _stream_handle, workspace
+
+
+def decode_result(rec) -> dict:
+    r = [int(v) for v in (rec.tolist() if hasattr(rec, "tolist") else rec)]
+    n = r[0]
+    return {"emitted": r[4:4 + n], "matched": r[1], "accepted_len": r[2], "path": r[3]}
+
+
+def _result(K: int, dev, out: Optional[torch.Tensor]) -> torch.Tensor:
+    if out is None:
+        out = torch.zeros(4 + K + 1, dtype=torch.int32, device=dev)
+    _require(out, "result", 4, dev)
+    if out.numel() < 4 + K + 1:
+        raise VmiError(f"result needs {4 + K + 1} entries")
+    return out
+
+
+def accept_greedy(drafts: torch.Tensor, preds: torch.Tensor, *, mode: int = 1, out: Optional[torch.Tensor] = None,
+                  stream=None) -> torch.Tensor:
+    """drafts int32 [K] or [P, K]; preds int32 [K + mode] or [P, K + mode]."""
+    dev = drafts.device
+    d2 = drafts.reshape(-1, drafts.shape[-1])
+    P, K = d2.shape
+    if preds.numel() != P * (K + mode):
+        raise VmiError(f"preds must hold {P} x {K + mode} entries")
+    _require(d2, "drafts", 4, dev)
+    _require(preds, "preds", 4, dev)
+    out = _result(K, dev, out)
+    rc = load().vmi_accept_greedy(d2.data_ptr(), preds.data_ptr(), P, K, mode, out.data_ptr(),
+                                  _stream_handle(stream))
+    check(rc, "vmi_accept_greedy")
+    return out
+
+
+def accept_stochastic(target_logits: torch.Tensor, draft_logits: Optional[torch.Tensor], drafts: torch.Tensor, *,
+                      temperature: float, top_p: float, seed: int, offset: int, out: Optional[torch.Tensor] = None,
+                      stream=None) -> torch.Tensor:
+    """target_logits f32 [K+1, V]; draft_logits f32 [K, V] or None; drafts int32 [K]."""
+    dev = target_logits.device
+    K1, V = target_logits.shape
+    K = K1 - 1
+    _require(target_logits, "target_logits", 4, dev)
+    _require(drafts, "drafts", 4, dev)
+    if drafts.numel() != K:
+        raise VmiError(f"drafts must hold {K} entries")
+    if draft_logits is not None:
+        _require(draft_logits, "draft_logits", 4, dev)
+        if tuple(draft_logits.shape) != (K, V):
+            raise VmiError(f"draft_logits must be [{K}, {V}]")
+    out = _result(K, dev, out)
+    sh = _stream_handle(stream)
+    lib = load()
+    nbytes = lib.vmi_accept_stochastic_workspace_bytes(K, V, int(draft_logits is not None))
+    ws = workspace(nbytes, dev, sh, tag="accept")
+    rc = lib.vmi_accept_stochastic(target_logits.data_ptr(), None if draft_logits is None else draft_logits.data_ptr(),
+                                   drafts.data_ptr(), K, V, float(temperature), float(top_p), int(seed) & (2**64 - 1),
+                                   int(offset) & (2**64 - 1), out.data_ptr(), ws.data_ptr(), ws.numel(), sh)
+    check(rc, "vmi_accept_stochastic")
+    return out
+
+
+def sample_top_p(logits: torch.Tensor, *, temperature: float, top_p: float, seed: int, offset: int,
+                 out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """logits f32 [rows, V] -> int32 [rows]."""
+    dev = logits.device
+    rows, V = logits.shape
+    _require(logits, "logits", 4, dev)
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int32, device=dev)
+    _require(out, "out", 4, dev)
+    sh = _stream_handle(stream)
+    lib = load()
+    ws = workspace(lib.vmi_sample_top_p_workspace_bytes(rows, V), dev, sh, tag="sample")
+    rc = lib.vmi_sample_top_p(logits.data_ptr(), rows, V, float(temperature), float(top_p), int(seed) & (2**64 - 1),
+                              int(offset) & (2**64 - 1), out.data_ptr(), ws.data_ptr(), ws.numel(), sh)
+    check(rc, "vmi_sample_top_p")
+    return out

@@ -1,0 +1,797 @@
+// Acceptance of a speculative verify step, on the device.
+//
+// k_accept_greedy   longest-prefix acceptance (generate.py:338-351) of one
+//                   draft chain, or of P draft paths with the winner chosen as
+//                   the longest match, ties to the lower path (generate.py:383),
+//                   and the emission rules of generate.py:819, :850-856.
+// Speculative sampling (Leviathan et al. 2023, Algorithm 1): keep draft d_i
+// when u_i q(d_i) <= p(d_i), else draw from norm(max(0, p - q)); a bonus token
+// from p_K when every draft is kept.  p and q are temperature / top-p
+// transforms of the target and draft logits.  The same machinery samples one
+// token per row (the drafter's sampler).  Each distribution's vocabulary is
+// split over NB workgroups so that the whole chip streams it:
+//   k_sd_max     row maxima per slice; clears the row's histograms
+//   k_sd_mass    integer masses W (kept in the workspace), level-1 histogram
+//   k_sd_level2  crossing bin of level 1, level-2 histogram inside it
+//   k_sd_level3  level-3 histogram; the last slice of a row to finish fixes
+//                the nucleus threshold and mass
+//   k_sd_draw    acceptance decisions (recomputed identically by every
+//                slice), masses of the distribution to draw from per slice;
+//                the last slice of a draw finds the token.
+// "Last to finish" is a release/acquire arrival counter per row in the
+// workspace, reset by that workgroup.  Histograms are integer sums (global
+// atomics), so their value does not depend on arrival order.
+//
+// Every probability is an integer mass (W_j = floor(2^31 2^z), z =
+// (l_j - max l) / temperature * log2 e, 2^z from a fixed fp32 polynomial), so
+// sums are exact in any order and the results are bit-identical to the CPU
+// oracle; decisions use IEEE double operations only.  Uniforms come from
+// Philox4x32-10 (key = seed, counter = (offset, position, 0x5A3D1E57)).
+
+#include "vmi_device.h"
+#include "vmi_internal.h"
+
+namespace {
+
+#pragma clang fp contract(off)
+
+constexpr int kMaxK = 15;
+constexpr int kBins = 2048;          // radix levels 1 and 2 (11 bits), level 3 uses 1024 (10 bits)
+constexpr uint32_t kCtrTag = 0x5A3D1E57u;
+
+__device__ __forceinline__ int acc_wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// Degree-6 Taylor polynomial of 2^f, f in [-1/2, 1/2]: (ln 2)^k / k! in fp32.
+__device__ __forceinline__ uint32_t sd_weight(float l, float M, float s2) {
+    const float z = (l - M) * s2;
+    if (!(z >= -32.0f)) return 0u;
+    const float n = rintf(z);
+    const float f = z - n;
+    float p = 0x1.430912p-13f;
+    p = __builtin_fmaf(p, f, 0x1.5d87fep-10f);
+    p = __builtin_fmaf(p, f, 0x1.3b2ab6p-7f);
+    p = __builtin_fmaf(p, f, 0x1.c6b08ep-5f);
+    p = __builtin_fmaf(p, f, 0x1.ebfbep-3f);
+    p = __builtin_fmaf(p, f, 0x1.62e43p-1f);
+    p = __builtin_fmaf(p, f, 0x1p+0f);
+    return (uint32_t)ldexpf(p, (int)n + 31);
+}
+
+__device__ __forceinline__ void philox(uint32_t c[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint32_t hi0 = __umulhi(0xD2511F53u, c[0]), lo0 = 0xD2511F53u * c[0];
+        const uint32_t hi1 = __umulhi(0xCD9E8D57u, c[2]), lo1 = 0xCD9E8D57u * c[2];
+        const uint32_t n0 = hi1 ^ c[1] ^ k0;
+        const uint32_t n2 = hi0 ^ c[3] ^ k1;
+        c[0] = n0; c[1] = lo1; c[2] = n2; c[3] = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+}
+
+__device__ __forceinline__ void sd_uniforms(uint64_t seed, uint64_t offset, int i, uint32_t& U, uint32_t& Vr) {
+    uint32_t c[4] = {(uint32_t)offset, (uint32_t)(offset >> 32), (uint32_t)i, kCtrTag};
+    philox(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    U = c[0];
+    Vr = c[1];
+}
+
+constexpr int kSdThreads = 256;
+constexpr int kSdWaves = kSdThreads / 64;
+constexpr int kMaxRows = 64;         // distributions per call / rows per draw
+constexpr int kHistAll = 2 * kBins + 1024;
+
+struct SdStats {
+    uint32_t theta;          // nucleus: W >= theta (theta >= 1)
+    uint32_t valid;          // 0 when the row has no finite logit
+    unsigned long long zs;   // nucleus mass
+    unsigned long long z;    // total mass
+    unsigned long long C;    // ceil(top_p * z)
+    uint32_t b1, b2;
+    unsigned long long above1, above2;
+};
+
+struct SdArgs {
+    const float* base0;      // rows [0, n0)
+    int n0;
+    const float* base1;      // rows [n0, nd)
+    int nd, V, NB, chunk;
+    float s2, top_p;
+    uint64_t seed, offset;
+    int accept, K, has_q;    // accept mode: K drafts, draft rows present
+    const int32_t* drafts;
+    uint32_t* ctr_d;         // [kMaxRows] arrival counters of k_sd_level3
+    uint32_t* ctr_r;         // [kMaxRows] arrival counters of k_sd_draw
+    SdStats* stats;          // [nd]
+    float* pmax;             // [nd, NB]
+    unsigned long long* hist;  // [nd, kHistAll]: level 1 | level 2 | level 3
+    unsigned long long* partR; // [rows, NB]
+    unsigned long long* partP; // [rows, NB]
+    uint32_t* W;             // [nd, V]
+    int32_t* out;            // accept: result record; sample: [rows]
+};
+
+__device__ __forceinline__ const float* sd_row(const SdArgs& a, int d) {
+    return d < a.n0 ? a.base0 + (size_t)d * a.V : a.base1 + (size_t)(d - a.n0) * a.V;
+}
+
+// Adds v to bin b of an LDS histogram, merging runs of one bin per thread
+// (most masses are tiny and share a bin: this keeps atomics off a hot spot).
+struct BinRun {
+    int bin = -1;
+    unsigned long long sum = 0;
+    __device__ void add(unsigned long long* h, int b, uint32_t v) {
+        if (b != bin) {
+            if (bin >= 0 && sum) atomicAdd(&h[bin], sum);
+            bin = b;
+            sum = 0;
+        }
+        sum += v;
+    }
+    __device__ void flush(unsigned long long* h) {
+        if (bin >= 0 && sum) atomicAdd(&h[bin], sum);
+        bin = -1;
+        sum = 0;
+    }
+};
+
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// One wave: the largest bin b of h[0..nbins) with above + sum_{i >= b} h[i] >= C,
+// and above + sum_{i > b} h[i].  Uniform results.
+__device__ void find_crossing(const unsigned long long* h, int nbins, uint64_t C, uint64_t above, uint32_t& b_out,
+                              uint64_t& above_out) {
+    const int lane = threadIdx.x & 63;
+    const int per = nbins / 64;
+    uint64_t own = 0;
+    for (int i = 0; i < per; ++i) own += h[lane * per + i];
+    uint64_t acc = above;
+    int L = 0;
+    for (int l = 63; l >= 0; --l) {
+        const uint64_t v = readlane64(own, l);
+        if (acc + v >= C) { L = l; break; }
+        acc += v;
+    }
+    int b = L * per;
+    for (int i = per - 1; i >= 0; --i) {
+        const uint64_t v = h[L * per + i];
+        if (acc + v >= C) { b = L * per + i; break; }
+        acc += v;
+    }
+    b_out = (uint32_t)b;
+    above_out = acc;
+}
+
+__device__ uint64_t block_sum_u64(unsigned long long* red, uint64_t v) {
+    const int lane = threadIdx.x & 63, w = acc_wave_id();
+    for (int o = 32; o >= 1; o >>= 1) v += shfl_xor64(v, o);
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    uint64_t t = 0;
+    for (int i = 0; i < kSdWaves; ++i) t += red[i];
+    __syncthreads();
+    return t;
+}
+
+// Adds the non-zero bins of an LDS histogram into a global one.
+__device__ void flush_hist(const unsigned long long* lds, unsigned long long* g, int nbins) {
+    for (int i = threadIdx.x; i < nbins; i += kSdThreads)
+        if (lds[i]) atomicAdd(&g[i], lds[i]);
+}
+
+__device__ __forceinline__ void slice_of(const SdArgs& a, int b, int& j0, int& j1) {
+    j0 = b * a.chunk;
+    j1 = min(a.V, j0 + a.chunk);
+}
+
+// f(j, src[j]) for every j of [j0, j1) owned by this thread (stride
+// kSdThreads), with kBatch loads in flight before any is used.
+constexpr int kBatch = 8;
+template <typename T, typename F>
+__device__ __forceinline__ void for_slice(int j0, int j1, const T* __restrict__ src, F f) {
+    for (int base = j0 + (int)threadIdx.x; base < j1; base += kBatch * kSdThreads) {
+        T v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int j = base + u * kSdThreads;
+            v[u] = j < j1 ? src[j] : T(0);
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int j = base + u * kSdThreads;
+            if (j < j1) f(j, v[u]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kSdThreads) void k_sd_max(SdArgs a) {
+    __shared__ float s_red[kSdWaves];
+    const int d = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
+    int j0, j1;
+    slice_of(a, b, j0, j1);
+    const float* __restrict__ row = sd_row(a, d);
+    float m0 = -INFINITY;
+    for_slice(j0, j1, row, [&](int, float l) { m0 = fmaxf(m0, l); });
+    float m = vmi_wave_max(m0);
+    if ((tid & 63) == 0) s_red[acc_wave_id()] = m;
+    unsigned long long* h = a.hist + (size_t)d * kHistAll;
+    for (int i = b * kSdThreads + tid; i < kHistAll; i += a.NB * kSdThreads) h[i] = 0ull;
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < kSdWaves; ++i) m = fmaxf(m, s_red[i]);
+        a.pmax[d * a.NB + b] = m;
+    }
+}
+
+__global__ __launch_bounds__(kSdThreads) void k_sd_mass(SdArgs a) {
+    __shared__ unsigned long long s_h[kBins];
+    __shared__ float s_red[kSdWaves];
+    const int d = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
+    float m = -INFINITY;
+    for (int i = tid; i < a.NB; i += kSdThreads) m = fmaxf(m, a.pmax[d * a.NB + i]);
+    m = vmi_wave_max(m);
+    if ((tid & 63) == 0) s_red[acc_wave_id()] = m;
+    for (int i = tid; i < kBins; i += kSdThreads) s_h[i] = 0ull;
+    __syncthreads();
+    float M = s_red[0];
+    for (int i = 1; i < kSdWaves; ++i) M = fmaxf(M, s_red[i]);
+    int j0, j1;
+    slice_of(a, b, j0, j1);
+    const float* __restrict__ row = sd_row(a, d);
+    uint32_t* __restrict__ W = a.W + (size_t)d * a.V;
+    BinRun run;
+    const float s2 = a.s2;
+    for_slice(j0, j1, row, [&](int j, float l) {
+        const uint32_t x = sd_weight(l, M, s2);
+        W[j] = x;
+        run.add(s_h, (int)(x >> 21), x);
+    });
+    run.flush(s_h);
+    __syncthreads();
+    flush_hist(s_h, a.hist + (size_t)d * kHistAll, kBins);
+}
+
+__global__ __launch_bounds__(kSdThreads) void k_sd_level2(SdArgs a) {
+    __shared__ unsigned long long s_h[kBins];
+    __shared__ unsigned long long s_red[kSdWaves];
+    __shared__ uint32_t s_b1;
+    __shared__ unsigned long long s_above1;
+    const int d = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
+    const unsigned long long* g1 = a.hist + (size_t)d * kHistAll;
+    uint64_t part = 0;
+    for (int i = tid; i < kBins; i += kSdThreads) {
+        s_h[i] = g1[i];
+        part += s_h[i];
+    }
+    const uint64_t Z = block_sum_u64(s_red, part);
+    SdStats* st = &a.stats[d];
+    if (Z == 0) {
+        if (b == 0 && tid == 0) st->valid = 0;
+        return;
+    }
+    uint64_t C = (a.top_p >= 1.0f) ? Z : (uint64_t)ceil((double)a.top_p * (double)Z);
+    if (C == 0) C = 1;
+    if (acc_wave_id() == 0) {
+        uint32_t b1;
+        uint64_t above1;
+        find_crossing(s_h, kBins, C, 0, b1, above1);
+        if (tid == 0) {
+            s_b1 = b1;
+            s_above1 = above1;
+            if (b == 0) {
+                st->valid = 1;
+                st->z = Z;
+                st->C = C;
+                st->b1 = b1;
+                st->above1 = above1;
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t b1 = s_b1;
+    for (int i = tid; i < kBins; i += kSdThreads) s_h[i] = 0ull;
+    __syncthreads();
+    int j0, j1;
+    slice_of(a, b, j0, j1);
+    const uint32_t* __restrict__ W = a.W + (size_t)d * a.V;
+    BinRun run;
+    for_slice(j0, j1, W, [&](int, uint32_t x) {
+        if ((x >> 21) == b1) run.add(s_h, (int)((x >> 10) & 0x7ffu), x);
+    });
+    run.flush(s_h);
+    __syncthreads();
+    flush_hist(s_h, a.hist + (size_t)d * kHistAll + kBins, kBins);
+}
+
+__global__ __launch_bounds__(kSdThreads) void k_sd_level3(SdArgs a) {
+    __shared__ unsigned long long s_h[kBins];
+    __shared__ uint32_t s_pre;
+    __shared__ unsigned long long s_above2;
+    __shared__ int s_last;
+    const int d = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
+    SdStats* st = &a.stats[d];
+    if (!st->valid) return;  // uniform: written by the previous kernel
+    const uint64_t C = st->C;
+    const unsigned long long* g2 = a.hist + (size_t)d * kHistAll + kBins;
+    for (int i = tid; i < kBins; i += kSdThreads) s_h[i] = g2[i];
+    __syncthreads();
+    if (acc_wave_id() == 0) {
+        uint32_t b2;
+        uint64_t above2;
+        find_crossing(s_h, kBins, C, st->above1, b2, above2);
+        if (tid == 0) {
+            s_pre = (st->b1 << 11) | b2;
+            s_above2 = above2;
+            if (b == 0) {
+                st->b2 = b2;
+                st->above2 = above2;
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t pre = s_pre;
+    for (int i = tid; i < 1024; i += kSdThreads) s_h[i] = 0ull;
+    __syncthreads();
+    int j0, j1;
+    slice_of(a, b, j0, j1);
+    const uint32_t* __restrict__ W = a.W + (size_t)d * a.V;
+    BinRun run;
+    for_slice(j0, j1, W, [&](int, uint32_t x) {
+        if ((x >> 10) == pre) run.add(s_h, (int)(x & 0x3ffu), x);
+    });
+    run.flush(s_h);
+    __syncthreads();
+    unsigned long long* g3 = a.hist + (size_t)d * kHistAll + 2 * kBins;
+    flush_hist(s_h, g3, 1024);
+    // the last slice of row d to finish fixes the nucleus
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&a.ctr_d[d], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == (uint32_t)(a.NB - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    for (int i = tid; i < 1024; i += kSdThreads)
+        s_h[i] = __hip_atomic_load(&g3[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (acc_wave_id() == 0) {
+        uint32_t b3;
+        uint64_t above3;
+        find_crossing(s_h, 1024, C, s_above2, b3, above3);
+        if (tid == 0) {
+            st->theta = (pre << 10) | b3;
+            st->zs = above3 + s_h[b3];
+            __hip_atomic_store(&a.ctr_d[d], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t nucleus_mass(const uint32_t* __restrict__ W, uint32_t theta, int j) {
+    const uint32_t x = W[j];
+    return x >= theta ? x : 0u;
+}
+
+// What one draw samples from, recomputed identically by every workgroup.
+struct DrawPlan {
+    int bad;        // some distribution has no finite logit
+    int m;          // accept mode: drafts kept
+    int dp, dq;     // distribution rows of p (and q when residual with draft rows)
+    int resid;      // residual max(0, p - q) instead of p
+    int dm;         // draft token at the rejected position (one-hot q)
+    uint32_t Vr;    // resampling uniform
+    uint32_t th_p, th_q;
+    double zp, zq;
+};
+
+__device__ DrawPlan plan_draw(const SdArgs& a, int r) {
+    DrawPlan P{};
+    if (!a.accept) {
+        const SdStats& s = a.stats[r];
+        P.bad = !s.valid;
+        P.dp = r;
+        P.th_p = s.theta;
+        P.zp = (double)s.zs;
+        uint32_t U;
+        sd_uniforms(a.seed, a.offset, r, U, P.Vr);
+        return P;
+    }
+    for (int d = 0; d < a.nd; ++d) P.bad |= !a.stats[d].valid;
+    if (P.bad) return P;
+    const int K = a.K, V = a.V;
+    int m = 0;
+    for (; m < K; ++m) {
+        const int dj = a.drafts[m];
+        uint32_t U, Vr;
+        sd_uniforms(a.seed, a.offset, m, U, Vr);
+        double pp = 0.0, qq = 1.0;
+        if (dj >= 0 && dj < V) {
+            const SdStats& sp = a.stats[m];
+            pp = (double)nucleus_mass(a.W + (size_t)m * V, sp.theta, dj) / (double)sp.zs;
+            if (a.has_q) {
+                const SdStats& sq = a.stats[K + 1 + m];
+                qq = (double)nucleus_mass(a.W + (size_t)(K + 1 + m) * V, sq.theta, dj) / (double)sq.zs;
+            }
+        }
+        const double u = (double)U * 0x1p-32;
+        if (!(pp > 0.0 && u * qq <= pp)) break;
+    }
+    P.m = m;
+    uint32_t U;
+    sd_uniforms(a.seed, a.offset, m, U, P.Vr);
+    P.dp = m;
+    P.th_p = a.stats[m].theta;
+    P.zp = (double)a.stats[m].zs;
+    P.resid = m < K;
+    if (P.resid) {
+        P.dm = a.drafts[m];
+        if (a.has_q) {
+            P.dq = K + 1 + m;
+            P.th_q = a.stats[P.dq].theta;
+            P.zq = (double)a.stats[P.dq].zs;
+        }
+    }
+    return P;
+}
+
+// floor(2^31 max(0, p(j) - q(j))) from the nucleus mass pm of p at j and the
+// raw draft mass wq at j.
+__device__ __forceinline__ uint32_t resid_value(const SdArgs& a, const DrawPlan& P, int j, uint32_t pm, uint32_t wq) {
+    const double pj = (double)pm / P.zp;
+    const double qj = a.has_q ? (double)(wq >= P.th_q ? wq : 0u) / P.zq : (j == P.dm ? 1.0 : 0.0);
+    const double rr = pj - qj;
+    return rr > 0.0 ? (uint32_t)(rr * 0x1p31) : 0u;
+}
+
+__device__ __forceinline__ uint32_t resid_mass(const SdArgs& a, const DrawPlan& P, int j) {
+    const uint32_t pm = nucleus_mass(a.W + (size_t)P.dp * a.V, P.th_p, j);
+    const uint32_t wq = a.has_q ? a.W[(size_t)P.dq * a.V + j] : 0u;
+    return resid_value(a, P, j, pm, wq);
+}
+
+__global__ __launch_bounds__(kSdThreads) void k_sd_draw(SdArgs a) {
+    __shared__ unsigned long long s_red[kSdWaves];
+    __shared__ unsigned long long s_scan[kSdThreads];
+    __shared__ int s_last, s_bstar, s_tok;
+    __shared__ unsigned long long s_base, s_t;
+    __shared__ int s_use_p;
+    const int r = blockIdx.y, b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const DrawPlan P = plan_draw(a, r);
+    int j0, j1;
+    slice_of(a, b, j0, j1);
+    uint64_t sr = 0, sp = 0;
+    if (!P.bad) {
+        const uint32_t* __restrict__ Wp = a.W + (size_t)P.dp * a.V;
+        const uint32_t* __restrict__ Wq = a.has_q && P.resid ? a.W + (size_t)P.dq * a.V : Wp;
+        for (int base = j0 + tid; base < j1; base += kBatch * kSdThreads) {
+            uint32_t vp[kBatch], vq[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int j = base + u * kSdThreads;
+                vp[u] = j < j1 ? Wp[j] : 0u;
+                vq[u] = j < j1 ? Wq[j] : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int j = base + u * kSdThreads;
+                if (j < j1) {
+                    const uint32_t p = vp[u] >= P.th_p ? vp[u] : 0u;
+                    sp += p;
+                    if (P.resid) sr += resid_value(a, P, j, p, vq[u]);
+                }
+            }
+        }
+    }
+    sr = block_sum_u64(s_red, sr);
+    sp = block_sum_u64(s_red, sp);
+    if (tid == 0) {
+        a.partR[r * a.NB + b] = sr;
+        a.partP[r * a.NB + b] = sp;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&a.ctr_r[r], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == (uint32_t)(a.NB - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (P.bad) {
+        if (tid == 0) {
+            if (a.accept) {
+                a.out[0] = 0; a.out[1] = 0; a.out[2] = 0; a.out[3] = -1;
+            } else {
+                a.out[r] = -1;
+            }
+            __hip_atomic_store(&a.ctr_r[r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+    // totals, the slice holding the draw point, and the mass before it (wave 0;
+    // lane i holds slices i and i + 64, NB <= 128)
+    if (acc_wave_id() == 0) {
+        const unsigned long long* pr = a.partR + r * a.NB;
+        const unsigned long long* pp = a.partP + r * a.NB;
+        uint64_t r0 = 0, r1 = 0, p0 = 0, p1 = 0;
+        if (lane < a.NB) {
+            r0 = __hip_atomic_load(&pr[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            p0 = __hip_atomic_load(&pp[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (lane + 64 < a.NB) {
+            r1 = __hip_atomic_load(&pr[lane + 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            p1 = __hip_atomic_load(&pp[lane + 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        uint64_t totR = r0 + r1, totP = p0 + p1;
+        for (int o = 32; o >= 1; o >>= 1) {
+            totR += shfl_xor64(totR, o);
+            totP += shfl_xor64(totP, o);
+        }
+        const int use_p = !(P.resid && totR > 0);
+        const uint64_t tot = use_p ? totP : totR;
+        const uint64_t v0 = use_p ? p0 : r0, v1 = use_p ? p1 : r1;
+        const uint64_t t = __umul64hi(tot, (uint64_t)P.Vr << 32);
+        uint64_t acc = 0;
+        int bstar = a.NB - 1;
+        bool found = false;
+        for (int i = 0; i < 64 && i < a.NB && !found; ++i) {
+            const uint64_t v = readlane64(v0, i);
+            if (acc + v > t) { bstar = i; found = true; } else { acc += v; }
+        }
+        for (int i = 0; i < 64 && i + 64 < a.NB && !found; ++i) {
+            const uint64_t v = readlane64(v1, i);
+            if (acc + v > t) { bstar = i + 64; found = true; } else { acc += v; }
+        }
+        if (lane == 0) {
+            s_bstar = bstar;
+            s_base = acc;
+            s_t = t;
+            s_use_p = use_p;
+            s_tok = -1;
+        }
+    }
+    __syncthreads();
+    // inside slice b*: thread i owns the contiguous group of kBatch indices
+    // k0 + kBatch i ..; an exclusive scan of the group sums finds the group
+    // holding the draw point, whose owner walks it.
+    const int bs = s_bstar, use_p = s_use_p;
+    const uint64_t t = s_t;
+    int k0, k1;
+    slice_of(a, bs, k0, k1);
+    for (int g0 = k0; g0 < k1; g0 += kBatch * kSdThreads) {
+        const int gj = g0 + kBatch * tid;
+        uint32_t v[kBatch];
+        uint64_t gs = 0;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int j = gj + u;
+            v[u] = j < k1 ? (use_p ? nucleus_mass(a.W + (size_t)P.dp * a.V, P.th_p, j) : resid_mass(a, P, j)) : 0u;
+            gs += v[u];
+        }
+        s_scan[tid] = gs;
+        __syncthreads();
+        for (int o = 1; o < kSdThreads; o <<= 1) {
+            const uint64_t add = tid >= o ? s_scan[tid - o] : 0ull;
+            __syncthreads();
+            s_scan[tid] += add;
+            __syncthreads();
+        }
+        const uint64_t base = s_base;
+        const uint64_t incl = base + s_scan[tid];
+        uint64_t run = incl - gs;
+        if (gs > 0 && run <= t && incl > t) {
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                run += v[u];
+                if (run > t) { s_tok = gj + u; break; }
+            }
+        }
+        __syncthreads();
+        if (tid == 0) s_base = base + s_scan[kSdThreads - 1];
+        __syncthreads();
+        if (s_tok >= 0) break;
+    }
+    if (tid == 0) {
+        int tok = s_tok;
+        if (tok < 0) tok = k1 - 1;  // unreachable: t < total
+        if (a.accept) {
+            const int m = P.m;
+            a.out[0] = m + 1;
+            a.out[1] = m;
+            a.out[2] = m + 1;
+            a.out[3] = 0;
+            for (int j = 0; j < m; ++j) a.out[4 + j] = a.drafts[j];
+            a.out[4 + m] = tok;
+        } else {
+            a.out[r] = tok;
+        }
+        __hip_atomic_store(&a.ctr_r[r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// ------------------------------------------------------------------ greedy
+struct GreedyArgs {
+    const int32_t* drafts;  // [P, K]
+    const int32_t* preds;   // [P, K + mode]
+    int P, K, mode;
+    int32_t* result;        // [4 + K + 1]
+};
+
+__global__ __launch_bounds__(64) void k_accept_greedy(GreedyArgs a) {
+    const int lane = threadIdx.x;
+    const int K = a.K, Kp = a.K + a.mode;
+    // lane p: matched length of path p; key = matched desc, then lower path
+    int best = -1, bestp = 0;
+    for (int p0 = 0; p0 < a.P; p0 += 64) {
+        const int p = p0 + lane;
+        int m = -1;
+        if (p < a.P) {
+            m = 0;
+            while (m < K && a.preds[(size_t)p * Kp + m] == a.drafts[(size_t)p * K + m]) ++m;
+        }
+        const uint32_t key = m < 0 ? 0u : ((uint32_t)(m + 1) << 16) | (uint32_t)(0xffff - p);
+        const uint32_t top = vmi_wave_max_u32(key);
+        const int tm = (int)(top >> 16) - 1, tp = 0xffff - (int)(top & 0xffff);
+        if (tm > best) { best = tm; bestp = tp; }
+    }
+    if (lane == 0) {
+        const int32_t* dr = a.drafts + (size_t)bestp * K;
+        const int32_t* pr = a.preds + (size_t)bestp * Kp;
+        const int m = best;
+        int n = 0;
+        for (int j = 0; j < m; ++j) a.result[4 + n++] = dr[j];
+        int acc_len;
+        if (a.mode == 0) {
+            if (m < K) a.result[4 + n++] = pr[m];
+            acc_len = m + 1 < K ? m + 1 : K;
+        } else {
+            a.result[4 + n++] = pr[m];
+            acc_len = m + 1;
+        }
+        a.result[0] = n;
+        a.result[1] = m;
+        a.result[2] = acc_len;
+        a.result[3] = bestp;
+    }
+}
+
+// Workspace: counters first (fixed offsets whatever the shape, zero between
+// calls), then per-row state.
+struct SdLayout {
+    size_t ctr_d, ctr_r, stats, pmax, hist, partR, partP, W, bytes;
+};
+
+SdLayout sd_layout(int nd, int rows, int V, int NB) {
+    SdLayout L{};
+    size_t off = 0;
+    L.ctr_d = off; off += kMaxRows * sizeof(uint32_t);
+    L.ctr_r = off; off += kMaxRows * sizeof(uint32_t);
+    off = vmi::align256(off);
+    L.stats = off; off += vmi::align256((size_t)nd * sizeof(SdStats));
+    L.pmax = off; off += vmi::align256((size_t)nd * NB * sizeof(float));
+    L.hist = off; off += vmi::align256((size_t)nd * kHistAll * sizeof(unsigned long long));
+    L.partR = off; off += vmi::align256((size_t)rows * NB * sizeof(unsigned long long));
+    L.partP = off; off += vmi::align256((size_t)rows * NB * sizeof(unsigned long long));
+    L.W = off; off += vmi::align256((size_t)nd * V * sizeof(uint32_t));
+    L.bytes = off;
+    return L;
+}
+
+// Slices per row: at most kBatch * kSdThreads = 2048 logits each (one batch
+// of loads per thread), at most 128 slices.
+int sd_slices(int V) {
+    int nb = (V + kBatch * kSdThreads - 1) / (kBatch * kSdThreads);
+    return nb < 1 ? 1 : (nb > 128 ? 128 : nb);
+}
+
+float sd_scale(float temperature) { return (float)((1.0 / (double)temperature) * 1.4426950408889634); }
+
+hipError_t sd_launch(SdArgs& a, int rows, hipStream_t s) {
+    const dim3 blk(kSdThreads), gd(a.NB, a.nd);
+    hipLaunchKernelGGL(k_sd_max, gd, blk, 0, s, a);
+    hipLaunchKernelGGL(k_sd_mass, gd, blk, 0, s, a);
+    hipLaunchKernelGGL(k_sd_level2, gd, blk, 0, s, a);
+    hipLaunchKernelGGL(k_sd_level3, gd, blk, 0, s, a);
+    hipLaunchKernelGGL(k_sd_draw, dim3(a.NB, rows), blk, 0, s, a);
+    return hipGetLastError();
+}
+
+void sd_bind(SdArgs& a, uint8_t* ws, const SdLayout& L) {
+    a.ctr_d = reinterpret_cast<uint32_t*>(ws + L.ctr_d);
+    a.ctr_r = reinterpret_cast<uint32_t*>(ws + L.ctr_r);
+    a.stats = reinterpret_cast<SdStats*>(ws + L.stats);
+    a.pmax = reinterpret_cast<float*>(ws + L.pmax);
+    a.hist = reinterpret_cast<unsigned long long*>(ws + L.hist);
+    a.partR = reinterpret_cast<unsigned long long*>(ws + L.partR);
+    a.partP = reinterpret_cast<unsigned long long*>(ws + L.partP);
+    a.W = reinterpret_cast<uint32_t*>(ws + L.W);
+}
+
+}  // namespace
+
+extern "C" int vmi_accept_greedy(const int32_t* drafts, const int32_t* preds, int P, int K, int mode, int32_t* result,
+                                 void* stream) {
+    vmi::clear_error();
+    if (P <= 0 || P > 0xffff || K <= 0 || K > kMaxK) return vmi::fail(VMI_ERR_INVALID, "P=%d K=%d", P, K);
+    if (mode != 0 && mode != 1) return vmi::fail(VMI_ERR_INVALID, "mode=%d", mode);
+    if (mode == 1 && P != 1) return vmi::fail(VMI_ERR_INVALID, "mode 1 (K+1 verify rows) takes one chain");
+    if (!drafts || !preds || !result) return vmi::fail(VMI_ERR_INVALID, "null drafts/preds/result");
+    GreedyArgs g{drafts, preds, P, K, mode, result};
+    hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), g);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "k_accept_greedy launch");
+}
+
+extern "C" size_t vmi_accept_stochastic_workspace_bytes(int K, int vocab, int has_draft_logits) {
+    if (K <= 0 || K > kMaxK || vocab <= 0) return 0;
+    const int nd = (K + 1) + (has_draft_logits ? K : 0);
+    return sd_layout(nd, 1, vocab, sd_slices(vocab)).bytes;
+}
+
+extern "C" int vmi_accept_stochastic(const float* target_logits, const float* draft_logits, const int32_t* drafts,
+                                     int K, int vocab, float temperature, float top_p, uint64_t seed, uint64_t offset,
+                                     int32_t* result, void* workspace, size_t workspace_bytes, void* stream) {
+    vmi::clear_error();
+    if (K <= 0 || K > kMaxK) return vmi::fail(VMI_ERR_UNSUPPORTED, "K=%d must be in [1, %d]", K, kMaxK);
+    if (vocab <= 0 || vocab > (1 << 24)) return vmi::fail(VMI_ERR_INVALID, "vocab=%d", vocab);
+    if (!(temperature > 0.0f) || !(temperature < 1e30f))
+        return vmi::fail(VMI_ERR_INVALID, "temperature must be positive (use vmi_accept_greedy for 0)");
+    if (!(top_p > 0.0f) || top_p > 1.0f) return vmi::fail(VMI_ERR_INVALID, "top_p must be in (0, 1]");
+    if (!target_logits || !drafts || !result) return vmi::fail(VMI_ERR_INVALID, "null target/drafts/result");
+    const int nd = (K + 1) + (draft_logits ? K : 0);
+    const int NB = sd_slices(vocab);
+    const SdLayout L = sd_layout(nd, 1, vocab, NB);
+    if (!workspace || workspace_bytes < L.bytes)
+        return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
+    SdArgs a{};
+    a.base0 = target_logits; a.n0 = K + 1; a.base1 = draft_logits;
+    a.nd = nd; a.V = vocab; a.NB = NB; a.chunk = (vocab + NB - 1) / NB;
+    a.s2 = sd_scale(temperature); a.top_p = top_p; a.seed = seed; a.offset = offset;
+    a.accept = 1; a.K = K; a.has_q = draft_logits != nullptr; a.drafts = drafts;
+    a.out = result;
+    sd_bind(a, static_cast<uint8_t*>(workspace), L);
+    const hipError_t e = sd_launch(a, 1, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "stochastic acceptance launch");
+}
+
+extern "C" size_t vmi_sample_top_p_workspace_bytes(int rows, int vocab) {
+    if (rows <= 0 || rows > kMaxRows || vocab <= 0) return 0;
+    return sd_layout(rows, rows, vocab, sd_slices(vocab)).bytes;
+}
+
+extern "C" int vmi_sample_top_p(const float* logits, int rows, int vocab, float temperature, float top_p,
+                                uint64_t seed, uint64_t offset, int32_t* out, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+    vmi::clear_error();
+    if (rows <= 0 || rows > kMaxRows) return vmi::fail(VMI_ERR_UNSUPPORTED, "rows=%d must be in [1, %d]", rows, kMaxRows);
+    if (vocab <= 0 || vocab > (1 << 24)) return vmi::fail(VMI_ERR_INVALID, "vocab=%d", vocab);
+    if (!(temperature > 0.0f) || !(temperature < 1e30f)) return vmi::fail(VMI_ERR_INVALID, "temperature must be positive");
+    if (!(top_p > 0.0f) || top_p > 1.0f) return vmi::fail(VMI_ERR_INVALID, "top_p must be in (0, 1]");
+    if (!logits || !out) return vmi::fail(VMI_ERR_INVALID, "null logits/out");
+    const int NB = sd_slices(vocab);
+    const SdLayout L = sd_layout(rows, rows, vocab, NB);
+    if (!workspace || workspace_bytes < L.bytes)
+        return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
+    SdArgs a{};
+    a.base0 = logits; a.n0 = rows; a.base1 = nullptr;
+    a.nd = rows; a.V = vocab; a.NB = NB; a.chunk = (vocab + NB - 1) / NB;
+    a.s2 = sd_scale(temperature); a.top_p = top_p; a.seed = seed; a.offset = offset;
+    a.accept = 0; a.K = 0; a.has_q = 0; a.drafts = nullptr;
+    a.out = out;
+    sd_bind(a, static_cast<uint8_t*>(workspace), L);
+    const hipError_t e = sd_launch(a, rows, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "top-p sampling launch");
+}
