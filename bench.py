@@ -141,6 +141,90 @@ def bench_lm_head(args) -> int:
     return 0
 
 
+PEAK_MFMA_TFLOPS = 2500.0  # dense fp16/bf16
+
+
+def bench_prefill(args) -> int:
+    """Expert-major prefill of one MoE layer (hidden 2048, 512 experts top-10,
+    inter 512, 8-bit router, shared expert, Zipf(1.1) routing) on a T-token
+    prompt, bf16 activations N(0,1).  FLOPs per launch = (T*k + T) * 6*H*I
+    (routed assignments and the shared expert: gate, up, down) + 2*T*E*H
+    (router); algorithmic HBM bytes = distinct experts * 1,769,472 + shared
+    1,769,472 + router 1,114,112 + x in, residual in, out (3*T*H*2)."""
+    import torch
+    from vates_amd.synth import synth_bf16
+    from vates_amd.workload import make_layer, synth_layer
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    T, H, k, E, I = args.T, args.hidden, args.top_k, args.experts, args.inter
+    w = synth_layer(SEED, 0, hidden=H, inter=I, num_experts=E, zipf_s=ZIPF_S, zipf_alpha=1.0, device=dev)
+    moe = make_layer(w, top_k=k)
+    xs = synth_bf16(SEED, 0x9F11, (2, T, H), device=dev)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    ids = torch.empty((T, k), dtype=torch.int32, device=dev)
+    for s in range(args.warmup):
+        moe.prefill(xs[s % 2], residual=xs[s % 2], out=out, ids_out=ids)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for s in range(args.steps):
+        moe.prefill(xs[s % 2], residual=xs[s % 2], out=out, ids_out=ids)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    us = ms * 1e3 / args.steps
+    U = int(np.unique(ids.cpu().numpy()).size)
+    flops = (T * k + T) * 6.0 * H * I + 2.0 * T * E * H
+    nbytes = U * EXPERT_BYTES + EXPERT_BYTES + ROUTER8_BYTES + 3 * T * H * 2
+    tfs = flops / (us * 1e-6) / 1e12
+    gbs = nbytes / (us * 1e-6) / 1e9
+    hbm_bound = flops / nbytes < PEAK_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    eprint(f"[bench] prefill T={T}: {us:.1f} us per layer, {tfs:.1f} TFLOP/s, {gbs:.1f} GB/s, {U} experts touched")
+    from vates_amd.moe import workspace, workspace_status
+    ws = workspace(moe.prefill_workspace_bytes(T), dev, torch.cuda.current_stream().cuda_stream, tag="prefill")
+    if workspace_status(ws):
+        eprint("[bench] device status flags set")
+        return 3
+    cpu = None
+    if args.cpu_baseline_s > 0:
+        from oracle import oracle as orc
+        from oracle.torch_bridge import layer_np, u16
+        L = layer_np(w, k, True)
+        xn = u16(xs[0])
+        rows = 32
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_baseline_s:
+            orc.moe_layer(xn[done % (T // rows) * rows:(done % (T // rows) + 1) * rows], L, residual=True)
+            done += 1
+        el = time.perf_counter() - t0
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+        threads = min(threads, len(os.sched_getaffinity(0)))
+        cpu = {"value": round(done * rows * (k + 1) * 6.0 * H * I / el / 1e12, 6), "unit": "TFLOP/s",
+               "cores": threads, "kind": "port",
+               "sample": f"{done} oracle layer calls of {rows} tokens each, {el:.1f} s, float64 with OpenMP"}
+    line = {
+        "metric": "expert-major MoE prefill " + ("HBM GB/s" if hbm_bound else "MFMA TFLOP/s"),
+        "value": round(gbs if hbm_bound else tfs, 2), "unit": "GB/s" if hbm_bound else "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u4 weights x f16/bf16 MFMA, f32 accumulate (bf16 in/out)", "data": "synthetic",
+        "config": {"workload": f"expert-major prefill of one MoE layer, T={T}, {E} experts top-{k}, hidden {H}, "
+                               f"inter {I}, Zipf(1.1) routing, shared expert",
+                   "T": T, "experts_touched": U, "tflops_per_s": round(tfs, 2), "hbm_gbs": round(gbs, 2)},
+        "roofline": {"bound": "hbm" if hbm_bound else "mfma",
+                     "achieved": round(gbs if hbm_bound else tfs, 2),
+                     "peak": PEAK_HBM_GBS if hbm_bound else PEAK_MFMA_TFLOPS,
+                     "unit": "GB/s" if hbm_bound else "TFLOP/s",
+                     "frac": round((gbs / PEAK_HBM_GBS) if hbm_bound else (tfs / PEAK_MFMA_TFLOPS), 4),
+                     "traffic": None, "unit_of_work": "one vmi_moe_prefill call",
+                     "flops_per_launch": flops, "bytes_per_launch": nbytes, "us_per_launch": round(us, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,8 +238,9 @@ def main() -> int:
     ap.add_argument("--experts", type=int, default=512)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-baseline-s", type=float, default=15.0)
-    ap.add_argument("--path", choices=["moe", "lm_head"], default="moe",
-                    help="moe: the 48-layer verify stack (default); lm_head: the vocabulary GEMV + argmax")
+    ap.add_argument("--path", choices=["moe", "lm_head", "prefill"], default="moe",
+                    help="moe: the 48-layer verify stack (default); lm_head: the vocabulary GEMV + argmax; "
+                         "prefill: one expert-major MoE layer on a T-token prompt")
     ap.add_argument("--vocab", type=int, default=151936)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -165,6 +250,8 @@ def main() -> int:
 
     if args.path == "lm_head":
         return bench_lm_head(args)
+    if args.path == "prefill":
+        return bench_prefill(args)
 
     import torch
     from vates_amd.synth import synth_bf16

@@ -122,6 +122,32 @@ int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, cons
                   uint16_t* out, int32_t* ids_out, float* scores_out, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* ------------------------------------------------------------------------
+ * vmi_moe_prefill -- the same layer on a long prompt, expert-major; replaces
+ * FileStreamingMoeBlock._expert_major_forward
+ *   mlx_streaming/core/moe/block.py:111-243 (histogram + argsort of routed
+ *   experts, per-expert gathers, SwitchGLU per group, weighted scatter) and
+ *   its deterministic reduce core/moe/custom_kernel.py:20-118.
+ * With every expert resident there is no group bound: one pass sorts the T*k
+ * routes by pool slot and runs grouped MFMA GEMMs over 64-route tiles of each
+ * slot (gate/up + SwiGLU, then down); the shared expert is a dense GEMM over
+ * all tokens.  Every (token, rank) result has its own row and the combine adds
+ * ranks 0..k-1, then the gated shared expert, in fp32 in that order: the output
+ * is deterministic.  Router logits come from an MFMA GEMM (fp32 accumulation in
+ * the matrix cores' order), so routed ids can differ from vmi_moe_layer's at
+ * near-ties of the k-th logit.
+ * desc as vmi_moe_layer (hidden 512, 1024 or 2048; inter a multiple of 64;
+ * num_experts a multiple of 64 up to 1024; top_k <= 16; cap <= 1024);
+ * T <= 65536; x, residual, out bf16 [T, hidden].  workspace:
+ * vmi_moe_prefill_workspace_bytes(...) bytes (first 4 bytes: the status word,
+ * zero before first use).
+ * ------------------------------------------------------------------------ */
+size_t vmi_moe_prefill_workspace_bytes(int T, int top_k, int hidden, int inter, int num_experts, int cap,
+                                       int router_bits);
+int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, const uint16_t* residual,
+                    uint16_t* out, int32_t* ids_out, float* scores_out, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* Reads and clears the device status word of a workspace (synchronises the
  * stream).  *flags receives VMI_STATUS_* bits. */
 int vmi_workspace_status(void* workspace, void* stream, uint32_t* flags);

@@ -313,3 +313,26 @@ def accept_stochastic(target, draft, drafts, temperature: float, top_p: float, s
             _p(res)), "accept_stochastic")
     n = int(res[0])
     return [int(v) for v in res[4:4 + n]], int(res[1]), int(res[2]), res
+
+
+def moe_layer_routed(x_bf16, L: dict, ids, scores, residual=False):
+    """orc_moe_layer with the routing given: (out_f32, out_bf16)."""
+    x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    H, k = L["H"], L["k"]
+    T = x_bf16.size // H
+    ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(T, k)
+    scores = np.ascontiguousarray(scores, dtype=np.float32).reshape(T, k)
+    out_f32 = np.empty((T, H), dtype=np.float32)
+    out_bf16 = np.empty((T, H), dtype=np.uint16)
+    g = L.get
+    rc = lib().orc_moe_layer_routed(
+        _p(x_bf16), T, H, L["I"], L["E"], k, L["group"], _p(g("table")), L["cap"],
+        _p(L["gate_w"]), _p(L["gate_s"]), _p(L["gate_b"]), _p(L["up_w"]), _p(L["up_s"]), _p(L["up_b"]),
+        _p(L["down_w"]), _p(L["down_s"]), _p(L["down_b"]), L["bits"],
+        _p(g("sh_gate_w")), _p(g("sh_gate_s")), _p(g("sh_gate_b")), _p(g("sh_up_w")), _p(g("sh_up_s")),
+        _p(g("sh_up_b")), _p(g("sh_down_w")), _p(g("sh_down_s")), _p(g("sh_down_b")),
+        _p(g("sg_w")), _p(g("sg_s")), _p(g("sg_b")), g("sg_bits", 8), _p(g("norm_w")), c_float(g("norm_eps", 1e-6)),
+        int(residual), _p(ids), _p(scores), _p(out_f32), _p(out_bf16))
+    _chk(rc, "moe_layer_routed")
+    return out_f32, out_bf16
+

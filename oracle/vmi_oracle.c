@@ -444,7 +444,7 @@ int orc_rmsnorm_bf16(const uint16_t* x_bf16, const uint16_t* w_bf16, float eps, 
  * x is bf16 [T, H].  Outputs: out_f32 (pre-rounding), out_bf16, ids, scores,
  * slots.  Returns ORC_ESLOT when the table maps a routed expert outside
  * [0, cap). */
-int orc_moe_layer(const uint16_t* x_bf16, int T, int H, int I, int E, int k, int group, int norm_topk,
+static int moe_layer_impl(const uint16_t* x_bf16, int T, int H, int I, int E, int k, int group, int norm_topk,
                   const uint32_t* rw, const uint16_t* rs, const uint16_t* rb, int router_bits, const float* logit_bias,
                   const int32_t* slot_table, int cap, const uint32_t* gw, const uint16_t* gs, const uint16_t* gb,
                   const uint32_t* uw, const uint16_t* us, const uint16_t* ub, const uint32_t* dw, const uint16_t* ds,
@@ -452,7 +452,8 @@ int orc_moe_layer(const uint16_t* x_bf16, int T, int H, int I, int E, int k, int
                   const uint32_t* sh_uw, const uint16_t* sh_us, const uint16_t* sh_ub, const uint32_t* sh_dw,
                   const uint16_t* sh_ds, const uint16_t* sh_db, const uint32_t* sg_w, const uint16_t* sg_s,
                   const uint16_t* sg_b, int sg_bits, const uint16_t* norm_w, float norm_eps, int residual,
-                  float* out_f32, uint16_t* out_bf16, int32_t* ids, float* scores, int32_t* slots) {
+                  float* out_f32, uint16_t* out_bf16, int32_t* ids, float* scores, int32_t* slots,
+                  const int32_t* ids_in, const float* scores_in) {
     if (T <= 0 || k <= 0 || k > E || H % group || I % group) return ORC_EINVAL;
     const uint16_t* x_raw = x_bf16;
     uint16_t* xn = NULL;
@@ -463,13 +464,19 @@ int orc_moe_layer(const uint16_t* x_bf16, int T, int H, int I, int E, int k, int
         if (nrc) { free(xn); return nrc; }
         x_bf16 = xn;
     }
-    float* logits = (float*)malloc(sizeof(float) * (size_t)T * E);
-    if (!logits) { free(xn); return ORC_ENOMEM; }
-    int rc = orc_router_logits_f32(rw, rs, rb, logit_bias, E, H, group, router_bits, x_bf16, T, logits);
-    if (rc) { free(logits); free(xn); return rc; }
-    rc = orc_topk_softmax(logits, T, E, k, norm_topk, ids, scores);
-    free(logits);
-    if (rc) { free(xn); return rc; }
+    int rc = ORC_OK;
+    if (ids_in) {
+        memcpy(ids, ids_in, sizeof(int32_t) * (size_t)T * k);
+        memcpy(scores, scores_in, sizeof(float) * (size_t)T * k);
+    } else {
+        float* logits = (float*)malloc(sizeof(float) * (size_t)T * E);
+        if (!logits) { free(xn); return ORC_ENOMEM; }
+        rc = orc_router_logits_f32(rw, rs, rb, logit_bias, E, H, group, router_bits, x_bf16, T, logits);
+        if (rc) { free(logits); free(xn); return rc; }
+        rc = orc_topk_softmax(logits, T, E, k, norm_topk, ids, scores);
+        free(logits);
+        if (rc) { free(xn); return rc; }
+    }
     int bad = 0;
     for (int p = 0; p < T * k; ++p) {
         int e = ids[p];
@@ -511,6 +518,46 @@ int orc_moe_layer(const uint16_t* x_bf16, int T, int H, int I, int E, int k, int
         }
     }
     free(xd); free(y); free(ysh); free(xn);
+    return rc;
+}
+
+int orc_moe_layer(const uint16_t* x_bf16, int T, int H, int I, int E, int k, int group, int norm_topk,
+                  const uint32_t* rw, const uint16_t* rs, const uint16_t* rb, int router_bits, const float* logit_bias,
+                  const int32_t* slot_table, int cap, const uint32_t* gw, const uint16_t* gs, const uint16_t* gb,
+                  const uint32_t* uw, const uint16_t* us, const uint16_t* ub, const uint32_t* dw, const uint16_t* ds,
+                  const uint16_t* db, int bits, const uint32_t* sh_gw, const uint16_t* sh_gs, const uint16_t* sh_gb,
+                  const uint32_t* sh_uw, const uint16_t* sh_us, const uint16_t* sh_ub, const uint32_t* sh_dw,
+                  const uint16_t* sh_ds, const uint16_t* sh_db, const uint32_t* sg_w, const uint16_t* sg_s,
+                  const uint16_t* sg_b, int sg_bits, const uint16_t* norm_w, float norm_eps, int residual,
+                  float* out_f32, uint16_t* out_bf16, int32_t* ids, float* scores, int32_t* slots) {
+    return moe_layer_impl(x_bf16, T, H, I, E, k, group, norm_topk, rw, rs, rb, router_bits, logit_bias, slot_table,
+                          cap, gw, gs, gb, uw, us, ub, dw, ds, db, bits, sh_gw, sh_gs, sh_gb, sh_uw, sh_us, sh_ub,
+                          sh_dw, sh_ds, sh_db, sg_w, sg_s, sg_b, sg_bits, norm_w, norm_eps, residual, out_f32,
+                          out_bf16, ids, scores, slots, NULL, NULL);
+}
+
+/* The same layer with the routing given (ids [T, k] and their combine scores):
+ * checks expert math independently of near-tie routing decisions. */
+int orc_moe_layer_routed(const uint16_t* x_bf16, int T, int H, int I, int E, int k, int group,
+                         const int32_t* slot_table, int cap, const uint32_t* gw, const uint16_t* gs,
+                         const uint16_t* gb, const uint32_t* uw, const uint16_t* us, const uint16_t* ub,
+                         const uint32_t* dw, const uint16_t* ds, const uint16_t* db, int bits, const uint32_t* sh_gw,
+                         const uint16_t* sh_gs, const uint16_t* sh_gb, const uint32_t* sh_uw, const uint16_t* sh_us,
+                         const uint16_t* sh_ub, const uint32_t* sh_dw, const uint16_t* sh_ds, const uint16_t* sh_db,
+                         const uint32_t* sg_w, const uint16_t* sg_s, const uint16_t* sg_b, int sg_bits,
+                         const uint16_t* norm_w, float norm_eps, int residual, const int32_t* ids_in,
+                         const float* scores_in, float* out_f32, uint16_t* out_bf16) {
+    int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)T * k);
+    float* sc = (float*)malloc(sizeof(float) * (size_t)T * k);
+    int32_t* sl = (int32_t*)malloc(sizeof(int32_t) * (size_t)T * k);
+    int rc = (!ids || !sc || !sl) ? ORC_ENOMEM
+             : moe_layer_impl(x_bf16, T, H, I, E, k, group, 1, NULL, NULL, NULL, 8, NULL, slot_table, cap, gw, gs,
+                              gb, uw, us, ub, dw, ds, db, bits, sh_gw, sh_gs, sh_gb, sh_uw, sh_us, sh_ub, sh_dw,
+                              sh_ds, sh_db, sg_w, sg_s, sg_b, sg_bits, norm_w, norm_eps, residual, out_f32, out_bf16,
+                              ids, sc, sl, ids_in, scores_in);
+    free(ids);
+    free(sc);
+    free(sl);
     return rc;
 }
 

@@ -1,0 +1,115 @@
+"""GPU parity of the expert-major prefill (vmi_moe_prefill) against the CPU oracle.
+
+Bars (written here):
+  routed ids: equal to the oracle's for every token whose top-(k+1) router
+  logits are separated by more than 1e-4 (1 + |logit|) (the prefill router is
+  an MFMA GEMM; near-ties of fp32 rounding may order differently);
+  MoE outputs: with the GPU's own routing given to the oracle, relative L2
+  <= 1e-2, cosine >= 0.9999, max |err| <= 1e-2 max |ref| per token;
+  the layer is bit-deterministic run to run, and at T=2048 agrees with the
+  verify-batch kernels (vmi_moe_layer) on the same tokens.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+REL, COS = 1e-2, 0.9999
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+from oracle.torch_bridge import layer_np, u16  # noqa: E402
+
+
+def assert_close(got, ref, what):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    for t in range(ref.shape[0]):
+        g, r = got[t], ref[t]
+        rel = np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30)
+        cos = float(g @ r / max(np.linalg.norm(g) * np.linalg.norm(r), 1e-30))
+        mx = np.abs(g - r).max() / max(np.abs(r).max(), 1e-30)
+        assert rel <= REL and cos >= COS and mx <= REL, f"{what} token {t}: rel={rel:.3g} cos={cos:.7f} max={mx:.3g}"
+
+
+def clear_tokens(orc, L, x_np, k):
+    """Tokens whose oracle router logits have no near-tie among the top k+1."""
+    xn = orc.rmsnorm_bf16(x_np, L["norm_w"], L["norm_eps"])[0] if L["norm_w"] is not None else x_np
+    lg = orc.router_logits(L["router_w"], L["router_s"], L["router_b"], xn, L["E"], L["H"], bits=L["router_bits"],
+                           bias=L["bias"])
+    srt = -np.sort(-lg, axis=1)[:, :k + 1]
+    gaps = np.abs(np.diff(srt, axis=1)).min(axis=1)
+    return gaps > 1e-4 * (1.0 + np.abs(srt).max(axis=1))
+
+
+def _case(gpu, orc, T, *, H, I, E, k, router_bits=8, zipf_alpha=1.0, with_norm=True, residual=True, seed=51):
+    import torch
+    from vates_amd.synth import synth_bf16
+    from vates_amd.workload import make_layer, synth_layer
+    w = synth_layer(seed, 0, hidden=H, inter=I, num_experts=E, router_bits=router_bits, zipf_alpha=zipf_alpha,
+                    with_norm=with_norm, device=gpu)
+    moe = make_layer(w, top_k=k)
+    x = synth_bf16(seed, 2000 + T, (T, H), device=gpu)
+    ids = torch.empty((T, k), dtype=torch.int32, device=gpu)
+    sc = torch.empty((T, k), dtype=torch.float32, device=gpu)
+    out = moe.prefill(x, residual=x if residual else None, ids_out=ids, scores_out=sc)
+    torch.cuda.synchronize()
+    return w, moe, x, out, ids, sc
+
+
+def _check_against_oracle(orc, w, x, out, ids, sc, k, residual, what):
+    T = x.shape[0]
+    L = layer_np(w, k, True)
+    x_np = u16(x)
+    _, _, rid, _, _ = orc.moe_layer(x_np, L, residual=residual)
+    clear = clear_tokens(orc, L, x_np, k)
+    gid = ids.cpu().numpy()
+    assert np.array_equal(gid[clear], rid[clear]), f"{what}: routed ids differ on clearly separated tokens"
+    assert clear.mean() > 0.8
+    ref32, _ = orc.moe_layer_routed(x_np, L, gid, sc.cpu().numpy(), residual=residual)
+    got = orc.bf16_to_f32(u16(out).reshape(T, -1))
+    assert_close(got, ref32, what)
+
+
+@pytest.mark.parametrize("T", [1, 70, 200])
+@pytest.mark.parametrize("router_bits", [8, 4])
+def test_prefill_parity_small(gpu, orc, T, router_bits):
+    for residual in (True, False):
+        log(f"case: prefill H=512 I=128 E=64 k=4 T={T} router_bits={router_bits} residual={residual}")
+        w, moe, x, out, ids, sc = _case(gpu, orc, T, H=512, I=128, E=64, k=4, router_bits=router_bits,
+                                        residual=residual, with_norm=(T != 70))
+        _check_against_oracle(orc, w, x, out, ids, sc, 4, residual, f"small T={T}")
+
+
+def test_prefill_parity_full_shape(gpu, orc):
+    log("case: prefill H=2048 I=512 E=512 k=10 T=192")
+    w, moe, x, out, ids, sc = _case(gpu, orc, 192, H=2048, I=512, E=512, k=10)
+    _check_against_oracle(orc, w, x, out, ids, sc, 10, True, "full T=192")
+
+
+def test_prefill_deterministic_and_matches_verify_path(gpu, orc):
+    log("case: prefill T=2048 full shape vs verify kernels on 4 x 16 tokens")
+    import torch
+    T, k = 2048, 10
+    w, moe, x, out, ids, sc = _case(gpu, orc, T, H=2048, I=512, E=512, k=k)
+    out2 = moe.prefill(x, residual=x)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), "prefill not bit-deterministic"
+    assert torch.isfinite(out.float()).all()
+    L = layer_np(w, k, True)
+    for t0 in (0, 512, 1500, T - 16):
+        xs = x[t0:t0 + 16].contiguous()
+        did = torch.empty((16, k), dtype=torch.int32, device=gpu)
+        dec = moe(xs, residual=xs, ids_out=did)
+        torch.cuda.synchronize()
+        clear = clear_tokens(orc, L, u16(xs), k)
+        assert np.array_equal(ids[t0:t0 + 16].cpu().numpy()[clear], did.cpu().numpy()[clear])
+        a = orc.bf16_to_f32(u16(out[t0:t0 + 16]).reshape(16, -1))
+        b = orc.bf16_to_f32(u16(dec).reshape(16, -1))
+        same = np.array([np.array_equal(ids[t0 + i].cpu().numpy(), did[i].cpu().numpy()) for i in range(16)])
+        assert_close(a[same], b[same], f"prefill vs verify at {t0}")

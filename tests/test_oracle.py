@@ -233,6 +233,16 @@ def test_moe_layer_is_router_topk_experts_shared(orc):
         ref += gate * _expert_np(orc, shp, 0, xf[t], H, I)
         np.testing.assert_allclose(out_f32[t], ref, rtol=1e-5, atol=1e-6)
     assert np.array_equal(out_bf16, orc.f32_to_bf16(out_f32))
+    # the same layer with its own routing given reproduces every bit
+    r32, r16 = orc.moe_layer_routed(x, L, ids, sc, residual=True)
+    assert np.array_equal(r32.view(np.uint32), out_f32.view(np.uint32)) and np.array_equal(r16, out_bf16)
+    # and a different routing changes it
+    ids2 = ids.copy()
+    ids2[0, 0] = (ids2[0, 0] + 1) % E
+    while ids2[0, 0] in ids[0]:
+        ids2[0, 0] = (ids2[0, 0] + 1) % E
+    d32, _ = orc.moe_layer_routed(x, L, ids2, sc, residual=True)
+    assert not np.array_equal(d32[0], out_f32[0]) and np.array_equal(d32[1], out_f32[1])
 
 
 def test_oracle_small_fixture_unchanged(orc):

@@ -57,6 +57,9 @@ _SIGNATURES = {
     "vmi_moe_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "vmi_moe_layer": (c_int, [POINTER(MoeLayerDesc), c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_size_t, c_void_p]),
+    "vmi_moe_prefill_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
+    "vmi_moe_prefill": (c_int, [POINTER(MoeLayerDesc), c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_size_t, c_void_p]),
     "vmi_workspace_status": (c_int, [c_void_p, c_void_p, POINTER(c_uint32)]),
     "vmi_dequant_affine": (c_int, [QMat, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
     "vmi_synth_quantized": (c_int, [c_uint64, c_uint32, c_int64, c_int, c_int, c_int, c_float, c_void_p, c_void_p,

@@ -1,0 +1,772 @@
+// Expert-major prefill of one MoE layer (long prompts, T up to 65536 tokens).
+//
+// The reference computes a long prefill by expert groups
+// (mlx_streaming/core/moe/block.py:111-243): histogram of routed experts,
+// argsort, per-expert gathers of the routed token rows, SwitchGLU on each
+// group, and a deterministic scatter of the weighted results in route-rank
+// order (core/moe/custom_kernel.py:20-118).  With every expert resident in HBM
+// there is no group-size bound to respect, so one pass covers the layer:
+//
+//   k_pf_prep     per token: optional RMSNorm, MFMA operands of x (fp16, range
+//                 factor per token), per-group operand sums; clears counters
+//   k_pf_router   router logits [T, E] as a grouped MFMA GEMM on the 4/8-bit
+//                 router (weights enter the MFMA as exact fp16 subnormals)
+//   k_pf_sgate    shared-expert gate logit per token (one wave per token)
+//   k_pf_topk     one wave per token: top-k, softmax, renorm, slot table,
+//                 per-slot counts
+//   k_pf_scan     exclusive scan of the counts, the list of 64-row M tiles
+//   k_pf_place    every routed (token, rank) into its slot's list
+//   k_pf_gateup   per (M tile, 64 intermediate rows): gate and up MFMA GEMMs
+//                 over the tile's gathered tokens, SwiGLU, bf16 operands of
+//                 the activations and their per-group sums
+//   k_pf_down     per (M tile, 64 hidden rows): down MFMA GEMM, times the
+//                 route's combine weight, one bf16 row per (token, rank)
+//   k_pf_combine  out[t] = sum over ranks 0..k (rank k: the gated shared
+//                 expert) in rank order, fp32, + residual
+//
+// Route (token t, rank j) owns row t*(k+1) + j of the activation and result
+// buffers, so no result depends on the order in which assignments are placed:
+// the layer is bit-deterministic run to run.
+//
+// 4-bit weights are exact fp16 subnormals in gate/up (nibble masks, slot order
+// {0,4,1,5,2,6,3,7}, /16 on odd nibbles folded into the activation operand)
+// and exact bf16 (128 + q) in down; per-group scale and bias are applied to
+// each group's MFMA result (FMA), with the bias through per-group operand sums.
+
+#include "vmi_device.h"
+#include "vmi_internal.h"
+
+namespace {
+
+constexpr int kPfThreads = 256;
+constexpr int kTileM = 64;
+constexpr int kPfMaxE = 1024;
+constexpr int kPfMaxK = 16;
+
+__device__ __forceinline__ int pf_wave() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+struct PfArgs {
+    int T, H, I, E, k, cap, norm_topk, router_bits, sg_bits, has_shared, has_sgate;
+    const uint16_t* x;          // [T, H] bf16
+    const uint16_t* norm_w;     // [H] or null
+    float eps;
+    const uint16_t* residual;   // [T, H] or null
+    vmi_qmat router;            // [E, H]
+    const float* logit_bias;    // [E] or null
+    const int32_t* table;       // [E] or null
+    vmi_qmat gate, up, down;    // [cap, ...]
+    vmi_qmat sh_gate, sh_up, sh_down, sgate;
+    // workspace
+    vmi_u4* xop4;               // [T, H/8] fp16 operands, 4-bit slot order
+    float* xsum4;               // [T, H/64]
+    vmi_u4* xop8;               // [T, H/8] fp16 operands, 8-bit slot order (8-bit router)
+    float* xsum8;               // [T, H/64]
+    float* fscale;              // [T]
+    float* logits;              // [T, E]
+    float* sglogit;             // [T]
+    int32_t* ids;               // [T, k]
+    float* scores;              // [T, k]
+    int32_t* slots;             // [T, k] (-1: invalid)
+    int32_t* counts;            // [cap]
+    int32_t* offsets;           // [cap]
+    int32_t* fill;              // [cap]
+    int4* tiles;                // [max_tiles]: slot (-1 shared), list start (or token start), rows, 0
+    int32_t* ntiles;            // [1]
+    int32_t* list;              // [T*k] route rows t*(k+1)+j grouped by slot
+    vmi_u4* actop;              // [T*(k+1), I/8] bf16 operands
+    float* axs;                 // [T*(k+1), I/64]
+    uint16_t* ybuf;             // [T*(k+1), H] bf16 weighted expert outputs
+    uint16_t* out;              // [T, H]
+    uint32_t* status;
+    int32_t* ids_out;
+    float* scores_out;
+    int max_tiles;
+};
+
+// ------------------------------------------------------------------ prep
+// fp16 operand of 8 columns for 4-bit words: slots {0,4,1,5,2,6,3,7}, odd
+// nibble slots divided by 16; s accumulates what the MFMA multiplies.
+__device__ __forceinline__ vmi_u4 op4(const float (&v)[8], float f, float& s) {
+    const _Float16 h0 = (_Float16)(v[0] * f), h1 = (_Float16)(v[4] * f);
+    const _Float16 h2 = (_Float16)(v[1] * f * 0.0625f), h3 = (_Float16)(v[5] * f * 0.0625f);
+    const _Float16 h4 = (_Float16)(v[2] * f), h5 = (_Float16)(v[6] * f);
+    const _Float16 h6 = (_Float16)(v[3] * f * 0.0625f), h7 = (_Float16)(v[7] * f * 0.0625f);
+    s += (float)h0 + (float)h1 + (float)h4 + (float)h5 + 16.0f * ((float)h2 + (float)h3 + (float)h6 + (float)h7);
+    vmi_u4 r;
+    r[0] = vmi_h2_bits(h0, h1);
+    r[1] = vmi_h2_bits(h2, h3);
+    r[2] = vmi_h2_bits(h4, h5);
+    r[3] = vmi_h2_bits(h6, h7);
+    return r;
+}
+
+// fp16 operand of 8 columns for 8-bit words (two words of 4 columns):
+// slots {0,2,1,3,4,6,5,7}.
+__device__ __forceinline__ vmi_u4 op8(const float (&v)[8], float f, float& s) {
+    _Float16 h[8];
+    const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        h[i] = (_Float16)(v[perm[i]] * f);
+        s += (float)h[i];
+    }
+    vmi_u4 r;
+    r[0] = vmi_h2_bits(h[0], h[1]);
+    r[1] = vmi_h2_bits(h[2], h[3]);
+    r[2] = vmi_h2_bits(h[4], h[5]);
+    r[3] = vmi_h2_bits(h[6], h[7]);
+    return r;
+}
+
+// Eight 8-bit values of two packed words as exact fp16 subnormals n * 2^-24,
+// slot order {0,2,1,3,4,6,5,7}.
+__device__ __forceinline__ vmi_u4 unpack_u8_f16(uint32_t w0, uint32_t w1) {
+    vmi_u4 r;
+    r[0] = w0 & 0x00FF00FFu;
+    r[1] = (w0 >> 8) & 0x00FF00FFu;
+    r[2] = w1 & 0x00FF00FFu;
+    r[3] = (w1 >> 8) & 0x00FF00FFu;
+    return r;
+}
+
+__device__ __forceinline__ void bf16x8(const uint4& q, float (&v)[8]) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+
+// One wave per token; lane l owns columns [l*H/64, (l+1)*H/64) (H/512 chunks
+// of 8).  RMSNorm (canonical order) when norm_w, range factor, operands.
+template <int NCH>
+__global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * (kPfThreads / 64) + pf_wave();
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < a.cap; i += kPfThreads) a.counts[i] = 0;
+    if (t >= a.T) return;
+    constexpr int cpl = 8 * NCH;
+    const uint16_t* xr = a.x + (size_t)t * a.H + lane * cpl;
+    float v[NCH][8];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) bf16x8(*reinterpret_cast<const uint4*>(xr + 8 * c), v[c]);
+    if (a.norm_w) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss = fmaf(v[c][i], v[c][i], ss);
+        ss = vmi_wave_sum_canon(ss);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)a.H) + a.eps));
+        const uint16_t* nw = a.norm_w + lane * cpl;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            float g[8];
+            bf16x8(*reinterpret_cast<const uint4*>(nw + 8 * c), g);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[c][i] = vmi_bf16_to_f32(vmi_f32_to_bf16((v[c][i] * inv) * g[i]));
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
+    amax = vmi_wave_max(amax);
+    const float f = vmi_fp16_range_scale(amax);
+    // group of 64 columns = 8 chunks: lanes (8 / NCH) per group
+    constexpr int LPG = 8 / NCH;
+    float s4 = 0.0f, s8 = 0.0f;
+    const size_t orow = (size_t)t * (a.H / 8) + lane * NCH;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        a.xop4[orow + c] = op4(v[c], f, s4);
+        if (a.xop8) a.xop8[orow + c] = op8(v[c], f, s8);
+    }
+    // lanes of one group sum their partials in lane order
+#pragma unroll
+    for (int o = 1; o < LPG; o <<= 1) {
+        s4 += __shfl_xor(s4, o);
+        s8 += __shfl_xor(s8, o);
+    }
+    if ((lane % LPG) == 0) {
+        const size_t g = (size_t)t * (a.H / 64) + lane / LPG;
+        a.xsum4[g] = s4;
+        if (a.xsum8) a.xsum8[g] = s8;
+    }
+    if (lane == 0) a.fscale[t] = f;
+}
+
+// ------------------------------------------------------- grouped GEMM core
+// One wave accumulates a 16 (rows) x 16 (output features) tile over the
+// quantisation groups of K: per group two MFMAs with the group's weights as
+// exact subnormals, then acc += D * scale * 2^24 + bias * operand_sum.
+// Lane l: A row m = l%16 (rows of the tile), K block q = l/16; B column
+// n = l%16; D rows 4q + r, column n.
+
+// ----------------------------------------------------------------- router
+// Grid (ceil(T/64), E/64), 4 waves: wave w owns rows 16w..16w+15 of the 64
+// tokens and all 64 experts of the N tile (4 subtiles).
+template <int BITS>
+__global__ __launch_bounds__(kPfThreads) void k_pf_router(PfArgs a) {
+    const int lane = threadIdx.x & 63, w = pf_wave();
+    const int m = lane & 15, q = lane >> 4;
+    const int t0 = blockIdx.x * kTileM + 16 * w;
+    const int e0 = blockIdx.y * 64;
+    const int tm = t0 + m;
+    const bool row_ok = tm < a.T;
+    const int HW = a.H / 8, G = a.H / 64;
+    const vmi_u4* xop = BITS == 4 ? a.xop4 : a.xop8;
+    const float* xs = BITS == 4 ? a.xsum4 : a.xsum8;
+    const vmi_u4* arow = xop + (size_t)(row_ok ? tm : 0) * HW;
+    const int wpr = a.H * BITS / 32;  // packed words per router row
+    vmi_f4 acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[s] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < G; ++g) {
+        vmi_u4 a0 = arow[8 * g + 2 * q], a1 = arow[8 * g + 2 * q + 1];
+        if (!row_ok) a0 = a1 = vmi_u4{0u, 0u, 0u, 0u};
+        float xsr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tr = t0 + 4 * q + r;
+            xsr[r] = tr < a.T ? xs[(size_t)tr * G + g] : 0.0f;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int e = e0 + 16 * s + m;  // B column of this lane
+            const uint32_t* wr = a.router.w + (size_t)e * wpr;
+            vmi_u4 b0, b1;
+            if (BITS == 4) {
+                const uint2 ww = *reinterpret_cast<const uint2*>(wr + 8 * g + 2 * q);
+                b0 = vmi_unpack_u4_f16(ww.x);
+                b1 = vmi_unpack_u4_f16(ww.y);
+            } else {
+                // group g = 16 words; MFMA 0 takes words 8g'.. for K block q: columns 16q..16q+7
+                const uint4 ww = *reinterpret_cast<const uint4*>(wr + 16 * g + 4 * q);
+                b0 = unpack_u8_f16(ww.x, ww.y);
+                b1 = unpack_u8_f16(ww.z, ww.w);
+            }
+            vmi_f4 d = vmi_mfma_f16(a0, b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
+            d = vmi_mfma_f16(a1, b1, d);
+            const float sc = vmi_bf16_to_f32(a.router.s[(size_t)e * G + g]) * 16777216.0f;
+            const float bi = vmi_bf16_to_f32(a.router.b[(size_t)e * G + g]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[s][r] = fmaf(d[r], sc, fmaf(bi, xsr[r], acc[s][r]));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int tr = t0 + 4 * q + r;
+        if (tr >= a.T) continue;
+        const float inv = 1.0f / a.fscale[tr];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int e = e0 + 16 * s + m;
+            float v = acc[s][r] * inv;
+            if (a.logit_bias) v += a.logit_bias[e];
+            a.logits[(size_t)tr * a.E + e] = v;
+        }
+    }
+}
+
+// Shared-expert gate logit: one wave per token, lane-contiguous columns in a
+// fixed order, on the effective fp16 operands (x * f) and the dequantised
+// gate row, canonical wave sum, divided by f.
+template <int NCH>
+__global__ __launch_bounds__(kPfThreads) void k_pf_sgate(PfArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * (kPfThreads / 64) + pf_wave();
+    if (t >= a.T) return;
+    const int bits = a.sg_bits;
+    const vmi_u4* xo = a.xop4 + (size_t)t * (a.H / 8) + lane * NCH;
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const vmi_u4 u = xo[c];
+        // op4 slot s holds column {0,4,1,5,2,6,3,7}[s]; odd columns carry /16
+        float xv[8];
+        const _Float16 h[8] = {
+            __builtin_bit_cast(_Float16, (uint16_t)(u[0] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[0] >> 16)),
+            __builtin_bit_cast(_Float16, (uint16_t)(u[1] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[1] >> 16)),
+            __builtin_bit_cast(_Float16, (uint16_t)(u[2] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[2] >> 16)),
+            __builtin_bit_cast(_Float16, (uint16_t)(u[3] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[3] >> 16))};
+        xv[0] = (float)h[0];
+        xv[4] = (float)h[1];
+        xv[1] = 16.0f * (float)h[2];
+        xv[5] = 16.0f * (float)h[3];
+        xv[2] = (float)h[4];
+        xv[6] = (float)h[5];
+        xv[3] = 16.0f * (float)h[6];
+        xv[7] = 16.0f * (float)h[7];
+        const int c0 = 8 * (lane * NCH + c);  // first column of this word
+        const int gi = c0 >> 6;
+        const float sc = vmi_bf16_to_f32(a.sgate.s[gi]), bi = vmi_bf16_to_f32(a.sgate.b[gi]);
+        uint32_t qv[8];
+        if (bits == 4) {
+            const uint32_t wd = a.sgate.w[c0 >> 3];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qv[i] = (wd >> (4 * i)) & 0xFu;
+        } else {
+            const uint32_t w0 = a.sgate.w[c0 >> 2], w1 = a.sgate.w[(c0 >> 2) + 1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                qv[i] = (w0 >> (8 * i)) & 0xFFu;
+                qv[4 + i] = (w1 >> (8 * i)) & 0xFFu;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = fmaf(xv[i], fmaf((float)qv[i], sc, bi), acc);
+    }
+    acc = vmi_wave_sum_canon(acc);
+    if (lane == 0) a.sglogit[t] = acc / a.fscale[t];
+}
+
+// ------------------------------------------------------------------ top-k
+__device__ __forceinline__ uint64_t pf_rank_key(float f, int e) {
+    uint32_t u = __float_as_uint(f);
+    u = (u == 0x80000000u) ? 0u : u;
+    const uint32_t ok = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const uint32_t hi = (f != f) ? 1u : ok;
+    return ((uint64_t)hi << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+}
+
+// One wave per token (block.py:321-329): lane l holds experts l + 64 i
+// (i < E/64 <= 16) in registers; k rounds of a wave-wide maximum over each
+// lane's best remaining rank key.
+__global__ __launch_bounds__(kPfThreads) void k_pf_topk(PfArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * (kPfThreads / 64) + pf_wave();
+    if (t >= a.T) return;
+    const float* lt = a.logits + (size_t)t * a.E;
+    const int NI = a.E / 64;  // E is a multiple of 64, at most 1024
+    uint64_t key[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) key[i] = i < NI ? pf_rank_key(lt[lane + 64 * i], lane + 64 * i) : 0ull;
+    uint64_t my_key = 0ull;
+    float mx = 0.0f;
+    for (int j = 0; j < a.k; ++j) {
+        uint64_t best = 0ull;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) best = key[i] > best ? key[i] : best;
+        const uint64_t M = vmi_wave_max_u64(best);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (key[i] == M) key[i] = 0ull;  // the one lane holding the winner drops it
+        if (lane == j) my_key = M;
+    }
+    const bool sel = lane < a.k;
+    const int my_idx = (int)(0xffffffffu - (uint32_t)my_key);
+    const float my_val = sel ? lt[my_idx] : 0.0f;
+    mx = vmi_readlane_f32(my_val, 0);
+    const bool bad = __ballot(sel && !(fabsf(my_val) < 3.0e38f)) != 0;
+    const float e = sel ? expf(my_val - mx) : 0.0f;
+    float den = 0.0f;
+    if (a.norm_topk) {
+        for (int j = 0; j < a.k; ++j) den = den + vmi_readlane_f32(e, j);
+    } else {
+        float part = 0.0f;
+        for (int i = 0; i < NI; ++i) part = part + expf(lt[lane + 64 * i] - mx);
+        den = vmi_wave_sum_canon(part);
+    }
+    if (sel) {
+        const float sc = e / den;
+        const int slot = a.table ? a.table[my_idx] : my_idx;
+        const bool ok = slot >= 0 && slot < a.cap;
+        a.ids[t * a.k + lane] = my_idx;
+        a.scores[t * a.k + lane] = sc;
+        a.slots[t * a.k + lane] = ok ? slot : -1;
+        if (a.ids_out) a.ids_out[t * a.k + lane] = my_idx;
+        if (a.scores_out) a.scores_out[t * a.k + lane] = sc;
+        if (ok) atomicAdd(&a.counts[slot], 1);
+        else atomicOr(a.status, VMI_STATUS_BAD_SLOT);
+    }
+    if (bad && lane == 0) atomicOr(a.status, VMI_STATUS_BAD_ROUTE);
+}
+
+// ------------------------------------------------------------ scan, place
+// One workgroup of 1024 threads, cap <= 1024: offsets, tiles, fill reset.
+__global__ __launch_bounds__(1024) void k_pf_scan(PfArgs a) {
+    __shared__ int s_cnt[1024];
+    __shared__ int s_tl[1024];
+    const int tid = threadIdx.x;
+    const int c = tid < a.cap ? a.counts[tid] : 0;
+    s_cnt[tid] = c;
+    s_tl[tid] = (c + kTileM - 1) / kTileM;
+    __syncthreads();
+    // inclusive Hillis-Steele scans of counts and tile counts
+    for (int o = 1; o < 1024; o <<= 1) {
+        const int ac = tid >= o ? s_cnt[tid - o] : 0;
+        const int at = tid >= o ? s_tl[tid - o] : 0;
+        __syncthreads();
+        s_cnt[tid] += ac;
+        s_tl[tid] += at;
+        __syncthreads();
+    }
+    const int off = s_cnt[tid] - c;
+    const int ntl = (c + kTileM - 1) / kTileM;
+    const int toff = s_tl[tid] - ntl;
+    if (tid < a.cap) {
+        a.offsets[tid] = off;
+        a.fill[tid] = 0;
+        for (int i = 0; i < ntl; ++i)
+            a.tiles[toff + i] = make_int4(tid, off + i * kTileM, min(kTileM, c - i * kTileM), 0);
+    }
+    const int routed_tiles = s_tl[1023];
+    const int sh_tiles = a.has_shared ? (a.T + kTileM - 1) / kTileM : 0;
+    for (int i = tid; i < sh_tiles; i += 1024)
+        a.tiles[routed_tiles + i] = make_int4(-1, i * kTileM, min(kTileM, a.T - i * kTileM), 0);
+    if (tid == 0) a.ntiles[0] = routed_tiles + sh_tiles;
+}
+
+__global__ __launch_bounds__(kPfThreads) void k_pf_place(PfArgs a) {
+    const int p = blockIdx.x * kPfThreads + threadIdx.x;
+    if (p >= a.T * a.k) return;
+    const int slot = a.slots[p];
+    if (slot < 0) return;
+    const int t = p / a.k, j = p - t * a.k;
+    const int pos = a.offsets[slot] + atomicAdd(&a.fill[slot], 1);
+    a.list[pos] = t * (a.k + 1) + j;
+}
+
+// Route row of tile row i (or -1 past the tile).
+__device__ __forceinline__ int tile_route(const PfArgs& a, const int4& tl, int i) {
+    if (i >= tl.z) return -1;
+    return tl.x >= 0 ? a.list[tl.y + i] : (tl.y + i) * (a.k + 1) + a.k;
+}
+
+// ---------------------------------------------------------------- gate/up
+// Grid (max_tiles, I/64), 4 waves; wave w: tile rows 16w..16w+15, the 64
+// intermediate rows of the N tile (4 subtiles) in gate and in up.
+__global__ __launch_bounds__(kPfThreads) void k_pf_gateup(PfArgs a) {
+    __shared__ float s_act[kTileM][64 + 1];
+    __shared__ int s_route[kTileM];
+    const int ti = blockIdx.x;
+    if (ti >= a.ntiles[0]) return;
+    const int4 tl = a.tiles[ti];
+    const int lane = threadIdx.x & 63, w = pf_wave(), tid = threadIdx.x;
+    const int m = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.y * 64;
+    if (tid < kTileM) s_route[tid] = tile_route(a, tl, tid);
+    __syncthreads();
+    const vmi_qmat G = tl.x >= 0 ? a.gate : a.sh_gate;
+    const vmi_qmat U = tl.x >= 0 ? a.up : a.sh_up;
+    const size_t mat = tl.x >= 0 ? (size_t)tl.x : 0;
+    const int H = a.H, HW = H / 8, NG = H / 64;
+    const int my_route = s_route[16 * w + m];
+    const int my_tok = my_route >= 0 ? my_route / (a.k + 1) : 0;
+    const vmi_u4* arow = a.xop4 + (size_t)my_tok * HW;
+    int rtok[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int rr = s_route[16 * w + 4 * q + r];
+        rtok[r] = rr >= 0 ? rr / (a.k + 1) : -1;
+    }
+    vmi_f4 ag[4], au[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) ag[s] = au[s] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+    const size_t wrow0 = mat * (size_t)a.I + n0;  // first weight row of the N tile
+    for (int g = 0; g < NG; ++g) {
+        vmi_u4 a0 = arow[8 * g + 2 * q], a1 = arow[8 * g + 2 * q + 1];
+        if (my_route < 0) a0 = a1 = vmi_u4{0u, 0u, 0u, 0u};
+        float xsr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xsr[r] = rtok[r] >= 0 ? a.xsum4[(size_t)rtok[r] * NG + g] : 0.0f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const size_t row = wrow0 + 16 * s + m;
+            const uint2 wg = *reinterpret_cast<const uint2*>(G.w + row * HW + 8 * g + 2 * q);
+            const uint2 wu = *reinterpret_cast<const uint2*>(U.w + row * HW + 8 * g + 2 * q);
+            vmi_f4 dg = vmi_mfma_f16(a0, vmi_unpack_u4_f16(wg.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
+            dg = vmi_mfma_f16(a1, vmi_unpack_u4_f16(wg.y), dg);
+            vmi_f4 du = vmi_mfma_f16(a0, vmi_unpack_u4_f16(wu.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
+            du = vmi_mfma_f16(a1, vmi_unpack_u4_f16(wu.y), du);
+            const float sg = vmi_bf16_to_f32(G.s[row * NG + g]) * 16777216.0f;
+            const float bg = vmi_bf16_to_f32(G.b[row * NG + g]);
+            const float su = vmi_bf16_to_f32(U.s[row * NG + g]) * 16777216.0f;
+            const float bu = vmi_bf16_to_f32(U.b[row * NG + g]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                ag[s][r] = fmaf(dg[r], sg, fmaf(bg, xsr[r], ag[s][r]));
+                au[s][r] = fmaf(du[r], su, fmaf(bu, xsr[r], au[s][r]));
+            }
+        }
+    }
+    // SwiGLU into LDS: act[row][col], rows 16w + 4q + r, cols 16 s + m
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float inv = rtok[r] >= 0 ? 1.0f / a.fscale[rtok[r]] : 0.0f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float gv = ag[s][r] * inv, uv = au[s][r] * inv;
+            const float act = gv / (1.0f + expf(-gv)) * uv;
+            s_act[16 * w + 4 * q + r][16 * s + m] = act;
+        }
+    }
+    __syncthreads();
+    // bf16 operands: thread -> (row, word of 8 columns): 64 rows x 8 words
+    const int IW = a.I / 8, IG = a.I / 64;
+    for (int i = tid; i < kTileM * 8; i += kPfThreads) {
+        const int row = i >> 3, wd = i & 7;
+        const int route = s_route[row];
+        if (route < 0) continue;
+        float v[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = vmi_bf16_to_f32(vmi_f32_to_bf16(s_act[row][8 * wd + c]));
+        // slot order of vmi_unpack_u4_bf16_128: {0,4,1,5,2,6,3,7}
+        vmi_u4 o;
+        o[0] = (uint32_t)vmi_f32_to_bf16(v[0]) | ((uint32_t)vmi_f32_to_bf16(v[4]) << 16);
+        o[1] = (uint32_t)vmi_f32_to_bf16(v[1]) | ((uint32_t)vmi_f32_to_bf16(v[5]) << 16);
+        o[2] = (uint32_t)vmi_f32_to_bf16(v[2]) | ((uint32_t)vmi_f32_to_bf16(v[6]) << 16);
+        o[3] = (uint32_t)vmi_f32_to_bf16(v[3]) | ((uint32_t)vmi_f32_to_bf16(v[7]) << 16);
+        a.actop[(size_t)route * IW + (n0 >> 3) + wd] = o;
+    }
+    // per-group sums of the bf16 activations: one group = this N tile
+    if (tid < kTileM) {
+        const int route = s_route[tid];
+        if (route >= 0) {
+            float sum = 0.0f;
+            for (int c = 0; c < 64; ++c) sum += vmi_bf16_to_f32(vmi_f32_to_bf16(s_act[tid][c]));
+            a.axs[(size_t)route * IG + (n0 >> 6)] = sum;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ down
+// Grid (max_tiles, H/64), 4 waves: wave w tile rows 16w..16w+15, 64 hidden
+// rows (4 subtiles).  bf16 MFMA with weights 128 + q (exact) and the
+// correction y = sum_g s (D_g - 128 A_g) + b A_g, A_g the group's act sum.
+__global__ __launch_bounds__(kPfThreads) void k_pf_down(PfArgs a) {
+    __shared__ int s_route[kTileM];
+    const int ti = blockIdx.x;
+    if (ti >= a.ntiles[0]) return;
+    const int4 tl = a.tiles[ti];
+    const int lane = threadIdx.x & 63, w = pf_wave(), tid = threadIdx.x;
+    const int m = lane & 15, q = lane >> 4;
+    const int h0 = blockIdx.y * 64;
+    if (tid < kTileM) s_route[tid] = tile_route(a, tl, tid);
+    __syncthreads();
+    const vmi_qmat D = tl.x >= 0 ? a.down : a.sh_down;
+    const size_t mat = tl.x >= 0 ? (size_t)tl.x : 0;
+    const int IW = a.I / 8, IG = a.I / 64;
+    const int my_route = s_route[16 * w + m];
+    const vmi_u4* arow = a.actop + (size_t)(my_route >= 0 ? my_route : 0) * IW;
+    int rr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rr[r] = s_route[16 * w + 4 * q + r];
+    vmi_f4 acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[s] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+    const size_t drow0 = mat * (size_t)a.H + h0;
+    for (int g = 0; g < IG; ++g) {
+        vmi_u4 a0 = arow[8 * g + 2 * q], a1 = arow[8 * g + 2 * q + 1];
+        if (my_route < 0) a0 = a1 = vmi_u4{0u, 0u, 0u, 0u};
+        float asr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) asr[r] = rr[r] >= 0 ? a.axs[(size_t)rr[r] * IG + g] : 0.0f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const size_t row = drow0 + 16 * s + m;
+            const uint2 wd = *reinterpret_cast<const uint2*>(D.w + row * IW + 8 * g + 2 * q);
+            vmi_f4 d = vmi_mfma_bf16(a0, vmi_unpack_u4_bf16_128(wd.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
+            d = vmi_mfma_bf16(a1, vmi_unpack_u4_bf16_128(wd.y), d);
+            const float sc = vmi_bf16_to_f32(D.s[row * IG + g]);
+            const float bi = vmi_bf16_to_f32(D.b[row * IG + g]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[s][r] = fmaf(sc, fmaf(-128.0f, asr[r], d[r]), fmaf(bi, asr[r], acc[s][r]));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int route = rr[r];
+        if (route < 0) continue;
+        const int t = route / (a.k + 1), j = route - t * (a.k + 1);
+        float wgt;
+        if (j < a.k) {
+            wgt = a.scores[t * a.k + j];
+        } else {
+            wgt = a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a.ybuf[(size_t)route * a.H + h0 + 16 * s + m] = vmi_f32_to_bf16(acc[s][r] * wgt);
+    }
+}
+
+// --------------------------------------------------------------- combine
+// out[t][h] = bf16(sum_{j <= k} y[t(k+1)+j][h] (valid routes, rank order) + residual)
+__global__ __launch_bounds__(kPfThreads) void k_pf_combine(PfArgs a) {
+    const int t = blockIdx.x;
+    const int K1 = a.k + 1;
+    for (int h = threadIdx.x * 4; h < a.H; h += kPfThreads * 4) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < K1; ++j) {
+            const bool ok = j < a.k ? a.slots[t * a.k + j] >= 0 : a.has_shared;
+            if (!ok) continue;
+            const uint2 y = *reinterpret_cast<const uint2*>(a.ybuf + ((size_t)t * K1 + j) * a.H + h);
+            acc[0] += __uint_as_float(y.x << 16);
+            acc[1] += __uint_as_float(y.x & 0xffff0000u);
+            acc[2] += __uint_as_float(y.y << 16);
+            acc[3] += __uint_as_float(y.y & 0xffff0000u);
+        }
+        if (a.residual) {
+            const uint2 rv = *reinterpret_cast<const uint2*>(a.residual + (size_t)t * a.H + h);
+            acc[0] += __uint_as_float(rv.x << 16);
+            acc[1] += __uint_as_float(rv.x & 0xffff0000u);
+            acc[2] += __uint_as_float(rv.y << 16);
+            acc[3] += __uint_as_float(rv.y & 0xffff0000u);
+        }
+        uint2 o;
+        o.x = (uint32_t)vmi_f32_to_bf16(acc[0]) | ((uint32_t)vmi_f32_to_bf16(acc[1]) << 16);
+        o.y = (uint32_t)vmi_f32_to_bf16(acc[2]) | ((uint32_t)vmi_f32_to_bf16(acc[3]) << 16);
+        *reinterpret_cast<uint2*>(a.out + (size_t)t * a.H + h) = o;
+    }
+}
+
+// -------------------------------------------------------------- workspace
+struct PfLayout {
+    size_t status, xop4, xsum4, xop8, xsum8, fscale, logits, sglogit, ids, scores, slots, counts, offsets, fill,
+        tiles, ntiles, list, actop, axs, ybuf, bytes;
+    int max_tiles;
+};
+
+PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) {
+    PfLayout L{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += vmi::align256(bytes);
+        return o;
+    };
+    const size_t R = (size_t)T * (k + 1);
+    L.max_tiles = (T * k + kTileM - 1) / kTileM + cap + (T + kTileM - 1) / kTileM;
+    L.status = take(256);
+    L.xop4 = take((size_t)T * (H / 8) * 16);
+    L.xsum4 = take((size_t)T * (H / 64) * 4);
+    L.xop8 = router_bits == 8 ? take((size_t)T * (H / 8) * 16) : 0;
+    L.xsum8 = router_bits == 8 ? take((size_t)T * (H / 64) * 4) : 0;
+    L.fscale = take((size_t)T * 4);
+    L.logits = take((size_t)T * E * 4);
+    L.sglogit = take((size_t)T * 4);
+    L.ids = take((size_t)T * k * 4);
+    L.scores = take((size_t)T * k * 4);
+    L.slots = take((size_t)T * k * 4);
+    L.counts = take((size_t)cap * 4);
+    L.offsets = take((size_t)cap * 4);
+    L.fill = take((size_t)cap * 4);
+    L.tiles = take((size_t)L.max_tiles * 16);
+    L.ntiles = take(4);
+    L.list = take((size_t)T * k * 4);
+    L.actop = take(R * (I / 8) * 16);
+    L.axs = take(R * (I / 64) * 4);
+    L.ybuf = take(R * H * 2);
+    L.bytes = off;
+    return L;
+}
+
+}  // namespace
+
+extern "C" size_t vmi_moe_prefill_workspace_bytes(int T, int top_k, int hidden, int inter, int num_experts, int cap,
+                                                  int router_bits) {
+    if (T <= 0 || top_k <= 0 || hidden <= 0 || inter <= 0 || num_experts <= 0 || cap <= 0) return 0;
+    return pf_layout(T, top_k, hidden, inter, num_experts, cap, router_bits).bytes;
+}
+
+extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, const uint16_t* residual,
+                               uint16_t* out, int32_t* ids_out, float* scores_out, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    vmi::clear_error();
+    if (!desc) return vmi::fail(VMI_ERR_INVALID, "null desc");
+    const vmi_moe_layer_desc& D = *desc;
+    if (T <= 0 || T > 65536) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, 65536]", T);
+    if (D.bits != 4 || D.group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", D.bits, D.group);
+    if (D.hidden != 512 && D.hidden != 1024 && D.hidden != 2048)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "hidden=%d must be 512, 1024 or 2048", D.hidden);
+    if (D.inter % 64 || D.inter <= 0 || D.inter > 4096)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "inter=%d must be a multiple of 64", D.inter);
+    if (D.num_experts % 64 || D.num_experts <= 0 || D.num_experts > kPfMaxE)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "num_experts=%d must be a multiple of 64 up to %d", D.num_experts,
+                         kPfMaxE);
+    if (D.top_k <= 0 || D.top_k > kPfMaxK || D.top_k > D.num_experts)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "top_k=%d", D.top_k);
+    if (D.cap <= 0 || D.cap > 1024) return vmi::fail(VMI_ERR_UNSUPPORTED, "cap=%d must be in [1, 1024]", D.cap);
+    if (D.router_bits != 4 && D.router_bits != 8) return vmi::fail(VMI_ERR_UNSUPPORTED, "router_bits=%d", D.router_bits);
+    const bool has_shared = D.shared_gate.w != nullptr;
+    const bool has_sgate = has_shared && D.shared_expert_gate.w != nullptr;
+    if (has_sgate && D.shared_expert_gate_bits != 4 && D.shared_expert_gate_bits != 8)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "shared_expert_gate_bits=%d", D.shared_expert_gate_bits);
+    if (!x || !out || !D.router.w || !D.gate.w || !D.up.w || !D.down.w)
+        return vmi::fail(VMI_ERR_INVALID, "null x/out/weights");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual) |
+         reinterpret_cast<uintptr_t>(D.router.w) | reinterpret_cast<uintptr_t>(D.gate.w) |
+         reinterpret_cast<uintptr_t>(D.up.w) | reinterpret_cast<uintptr_t>(D.down.w) |
+         reinterpret_cast<uintptr_t>(D.norm_weight)) & 15)
+        return vmi::fail(VMI_ERR_INVALID, "x, out, residual, norm weight and packed weights must be 16-byte aligned");
+    const PfLayout L = pf_layout(T, D.top_k, D.hidden, D.inter, D.num_experts, D.cap, D.router_bits);
+    if (!workspace || workspace_bytes < L.bytes)
+        return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    PfArgs a{};
+    a.T = T; a.H = D.hidden; a.I = D.inter; a.E = D.num_experts; a.k = D.top_k; a.cap = D.cap;
+    a.norm_topk = D.norm_topk_prob; a.router_bits = D.router_bits; a.sg_bits = D.shared_expert_gate_bits;
+    a.has_shared = has_shared; a.has_sgate = has_sgate;
+    a.x = x; a.norm_w = D.norm_weight; a.eps = D.norm_eps; a.residual = residual;
+    a.router = D.router; a.logit_bias = D.router_logit_bias; a.table = D.slot_table;
+    a.gate = D.gate; a.up = D.up; a.down = D.down;
+    a.sh_gate = has_shared ? D.shared_gate : D.gate;
+    a.sh_up = has_shared ? D.shared_up : D.up;
+    a.sh_down = has_shared ? D.shared_down : D.down;
+    a.sgate = D.shared_expert_gate;
+    a.status = reinterpret_cast<uint32_t*>(ws + L.status);
+    a.xop4 = reinterpret_cast<vmi_u4*>(ws + L.xop4);
+    a.xsum4 = reinterpret_cast<float*>(ws + L.xsum4);
+    a.xop8 = D.router_bits == 8 ? reinterpret_cast<vmi_u4*>(ws + L.xop8) : nullptr;
+    a.xsum8 = D.router_bits == 8 ? reinterpret_cast<float*>(ws + L.xsum8) : nullptr;
+    a.fscale = reinterpret_cast<float*>(ws + L.fscale);
+    a.logits = reinterpret_cast<float*>(ws + L.logits);
+    a.sglogit = reinterpret_cast<float*>(ws + L.sglogit);
+    a.ids = reinterpret_cast<int32_t*>(ws + L.ids);
+    a.scores = reinterpret_cast<float*>(ws + L.scores);
+    a.slots = reinterpret_cast<int32_t*>(ws + L.slots);
+    a.counts = reinterpret_cast<int32_t*>(ws + L.counts);
+    a.offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
+    a.fill = reinterpret_cast<int32_t*>(ws + L.fill);
+    a.tiles = reinterpret_cast<int4*>(ws + L.tiles);
+    a.ntiles = reinterpret_cast<int32_t*>(ws + L.ntiles);
+    a.list = reinterpret_cast<int32_t*>(ws + L.list);
+    a.actop = reinterpret_cast<vmi_u4*>(ws + L.actop);
+    a.axs = reinterpret_cast<float*>(ws + L.axs);
+    a.ybuf = reinterpret_cast<uint16_t*>(ws + L.ybuf);
+    a.out = out; a.ids_out = ids_out; a.scores_out = scores_out;
+    a.max_tiles = L.max_tiles;
+
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int tok_blocks = (T + 3) / 4;
+    switch (D.hidden / 512) {
+        case 1: hipLaunchKernelGGL(k_pf_prep<1>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(k_pf_prep<2>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
+        case 4: hipLaunchKernelGGL(k_pf_prep<4>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
+        default: return vmi::fail(VMI_ERR_UNSUPPORTED, "hidden=%d must be 512, 1024 or 2048", D.hidden);
+    }
+    const dim3 rgrid((T + kTileM - 1) / kTileM, D.num_experts / 64);
+    if (D.router_bits == 4)
+        hipLaunchKernelGGL(k_pf_router<4>, rgrid, dim3(kPfThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL(k_pf_router<8>, rgrid, dim3(kPfThreads), 0, s, a);
+    if (has_sgate) {
+        switch (D.hidden / 512) {
+            case 1: hipLaunchKernelGGL(k_pf_sgate<1>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
+            case 2: hipLaunchKernelGGL(k_pf_sgate<2>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
+            default: hipLaunchKernelGGL(k_pf_sgate<4>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
+        }
+    }
+    hipLaunchKernelGGL(k_pf_topk, dim3(tok_blocks), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
+    hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_gateup, dim3(L.max_tiles, D.inter / 64), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_down, dim3(L.max_tiles, D.hidden / 64), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(kPfThreads), 0, s, a);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill launch");
+}

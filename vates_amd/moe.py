@@ -205,6 +205,43 @@ class MoELayer:
     def workspace_bytes(self, T: int) -> int:
         return load().vmi_moe_layer_workspace_bytes(T, self.top_k, self.hidden, self.inter, self.num_experts)
 
+    def prefill_workspace_bytes(self, T: int) -> int:
+        return load().vmi_moe_prefill_workspace_bytes(T, self.top_k, self.hidden, self.inter, self.num_experts,
+                                                      self.cap, self.desc.router_bits)
+
+    def prefill(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None, *,
+                out: Optional[torch.Tensor] = None, ids_out: Optional[torch.Tensor] = None,
+                scores_out: Optional[torch.Tensor] = None, stream=None,
+                ws: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The layer on a long prompt, expert-major (block.py:111-243): x bf16 [T, hidden]."""
+        lib = load()
+        if x.dtype != torch.bfloat16 or x.shape[-1] != self.hidden:
+            raise VmiError("x must be bf16 [..., hidden]")
+        _require(x, "x", 2, self.device)
+        T = x.numel() // self.hidden
+        if residual is not None:
+            if residual.shape != x.shape or residual.dtype != torch.bfloat16:
+                raise VmiError("residual must match x (bf16)")
+            _require(residual, "residual", 2, self.device)
+        if out is None:
+            out = torch.empty_like(x)
+        else:
+            _require(out, "out", 2, self.device)
+            if out.shape != x.shape or out.dtype != torch.bfloat16:
+                raise VmiError("out must match x (bf16)")
+        for name, t, dt in (("ids_out", ids_out, torch.int32), ("scores_out", scores_out, torch.float32)):
+            if t is not None:
+                if t.dtype != dt or t.numel() != T * self.top_k:
+                    raise VmiError(f"{name} must be {dt} [T, top_k]")
+                _require(t, name, 4, self.device)
+        sh = _stream_handle(stream)
+        if ws is None:
+            ws = workspace(self.prefill_workspace_bytes(T), self.device, sh, tag="prefill")
+        rc = lib.vmi_moe_prefill(ctypes.byref(self.desc), x.data_ptr(), T, _ptr(residual), out.data_ptr(),
+                                 _ptr(ids_out), _ptr(scores_out), ws.data_ptr(), ws.numel(), sh)
+        check(rc, "vmi_moe_prefill")
+        return out
+
     def __call__(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None, *, out: Optional[torch.Tensor] = None,
                  ids_out: Optional[torch.Tensor] = None, scores_out: Optional[torch.Tensor] = None,
                  stream=None, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
