@@ -12,8 +12,8 @@
 //   k_pf_router   router logits [T, E] as a grouped MFMA GEMM on the 4/8-bit
 //                 router (weights enter the MFMA as exact fp16 subnormals)
 //   k_pf_sgate    shared-expert gate logit per token (one wave per token)
-//   k_pf_topk     one wave per token: top-k, softmax, renorm, slot table,
-//                 per-slot counts
+//   k_pf_topk     one wave per token: top-k, softmax, renorm, slot table
+//   k_pf_count    routes per slot and each route's rank in its slot
 //   k_pf_scan     exclusive scan of the counts, the list of 64-row M tiles
 //   k_pf_place    every routed (token, rank) into its slot's list
 //   k_pf_gateup   per (M tile, 64 intermediate rows): gate and up MFMA GEMMs
@@ -69,7 +69,7 @@ struct PfArgs {
     int32_t* slots;             // [T, k] (-1: invalid)
     int32_t* counts;            // [cap]
     int32_t* offsets;           // [cap]
-    int32_t* fill;              // [cap]
+    int32_t* fill;              // [T*k] rank of each route inside its slot
     int4* tiles;                // [max_tiles]: slot (-1 shared), list start (or token start), rows, 0
     int32_t* ntiles;            // [1]
     int32_t* list;              // [T*k] route rows t*(k+1)+j grouped by slot
@@ -380,14 +380,13 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_topk(PfArgs a) {
         a.slots[t * a.k + lane] = ok ? slot : -1;
         if (a.ids_out) a.ids_out[t * a.k + lane] = my_idx;
         if (a.scores_out) a.scores_out[t * a.k + lane] = sc;
-        if (ok) atomicAdd(&a.counts[slot], 1);
-        else atomicOr(a.status, VMI_STATUS_BAD_SLOT);
+        if (!ok) atomicOr(a.status, VMI_STATUS_BAD_SLOT);
     }
     if (bad && lane == 0) atomicOr(a.status, VMI_STATUS_BAD_ROUTE);
 }
 
 // ------------------------------------------------------------ scan, place
-// One workgroup of 1024 threads, cap <= 1024: offsets, tiles, fill reset.
+// One workgroup of 1024 threads, cap <= 1024: slot offsets and the tile list.
 __global__ __launch_bounds__(1024) void k_pf_scan(PfArgs a) {
     __shared__ int s_cnt[1024];
     __shared__ int s_tl[1024];
@@ -410,7 +409,6 @@ __global__ __launch_bounds__(1024) void k_pf_scan(PfArgs a) {
     const int toff = s_tl[tid] - ntl;
     if (tid < a.cap) {
         a.offsets[tid] = off;
-        a.fill[tid] = 0;
         for (int i = 0; i < ntl; ++i)
             a.tiles[toff + i] = make_int4(tid, off + i * kTileM, min(kTileM, c - i * kTileM), 0);
     }
@@ -421,14 +419,48 @@ __global__ __launch_bounds__(1024) void k_pf_scan(PfArgs a) {
     if (tid == 0) a.ntiles[0] = routed_tiles + sh_tiles;
 }
 
+// Routes per slot and each route's rank inside its slot: a block counts its
+// kCountRoutes routes in LDS, then adds one total per slot it touched to the
+// global count, whose old value is the block's base.  (Popular slots see one
+// global atomic per block instead of one per route.)  The rank order inside a
+// slot is arrival order; no result depends on it.
+constexpr int kCountRoutes = 2048;
+__global__ __launch_bounds__(kPfThreads) void k_pf_count(PfArgs a) {
+    __shared__ int s_cnt[1024];
+    __shared__ int s_base[1024];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < a.cap; i += kPfThreads) s_cnt[i] = 0;
+    __syncthreads();
+    const int p0 = blockIdx.x * kCountRoutes, n = min(kCountRoutes, a.T * a.k - p0);
+    int local[kCountRoutes / kPfThreads];
+#pragma unroll
+    for (int i = 0; i < kCountRoutes / kPfThreads; ++i) {
+        const int p = tid + i * kPfThreads;
+        local[i] = -1;
+        if (p < n) {
+            const int slot = a.slots[p0 + p];
+            if (slot >= 0) local[i] = atomicAdd(&s_cnt[slot], 1);
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < a.cap; i += kPfThreads)
+        s_base[i] = s_cnt[i] ? atomicAdd(&a.counts[i], s_cnt[i]) : 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kCountRoutes / kPfThreads; ++i) {
+        const int p = tid + i * kPfThreads;
+        if (p < n && local[i] >= 0) a.fill[p0 + p] = s_base[a.slots[p0 + p]] + local[i];
+    }
+}
+
+// Every valid route into its slot's list at offsets[slot] + rank.
 __global__ __launch_bounds__(kPfThreads) void k_pf_place(PfArgs a) {
     const int p = blockIdx.x * kPfThreads + threadIdx.x;
     if (p >= a.T * a.k) return;
     const int slot = a.slots[p];
     if (slot < 0) return;
     const int t = p / a.k, j = p - t * a.k;
-    const int pos = a.offsets[slot] + atomicAdd(&a.fill[slot], 1);
-    a.list[pos] = t * (a.k + 1) + j;
+    a.list[a.offsets[slot] + a.fill[p]] = t * (a.k + 1) + j;
 }
 
 // Route row of tile row i (or -1 past the tile).
@@ -594,6 +626,251 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_down(PfArgs a) {
     }
 }
 
+// ------------------------------------------- pipelined grouped GEMMs
+// Both GEMMs stream their weights one quantisation group (64 K values, 32 B
+// per row) at a time through a ring of 4 LDS slots of 4 KB: every thread moves
+// one 16-byte piece per group with global_load_lds (opaque to the compiler's
+// wait-count pass; ordered by explicit vmcnt waits), prefetch distance 3
+// groups.  Row r's 16-byte halves are swapped when bit 3 of r is set, so the
+// 8-byte operand reads of 16 consecutive rows hit distinct banks.  Per-group
+// scales (times 2^24 for the subnormal operands) and biases, and the operand
+// sums of the tile's rows, are loaded into LDS once per tile.
+
+constexpr int kRing = 4;
+constexpr int kMaxG = 32;  // quantisation groups along K (K <= 2048)
+
+template <int N>
+__device__ __forceinline__ void pf_wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__device__ __forceinline__ uint32_t ring_off(int row, int unit8) {
+    // byte offset of 8-byte unit `unit8` (0..3) of row `row` inside a slot
+    return 32u * row + 16u * (((unsigned)unit8 >> 1) ^ (((unsigned)row >> 3) & 1u)) + 8u * (unit8 & 1);
+}
+
+struct Ring {
+    uint8_t* s0;
+    uint8_t* s1;
+    uint8_t* s2;
+    uint8_t* s3;
+    __device__ __forceinline__ uint8_t* at(int u) const { return u == 0 ? s0 : u == 1 ? s1 : u == 2 ? s2 : s3; }
+};
+
+// Gate/up: tile M 64 routes x N 64 intermediate rows, gate and up.
+__global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup2(PfArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t r0[4096], r1[4096], r2[4096], r3[4096];
+    __shared__ __attribute__((aligned(16))) float2 s_sb[kMaxG][2][64];
+    __shared__ __attribute__((aligned(16))) float s_xs[kMaxG][kTileM];
+    __shared__ float s_act[kTileM][64 + 1];
+    __shared__ int s_route[kTileM];
+    __shared__ int s_tok[kTileM];
+    const int ti = blockIdx.x;
+    if (ti >= a.ntiles[0]) return;
+    const int4 tl = a.tiles[ti];
+    const int lane = threadIdx.x & 63, w = pf_wave(), tid = threadIdx.x;
+    const int n = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.y * 64;
+    const int H = a.H, HW = H / 8, G = H / 64;
+    const vmi_qmat Gm = tl.x >= 0 ? a.gate : a.sh_gate;
+    const vmi_qmat Um = tl.x >= 0 ? a.up : a.sh_up;
+    const size_t row0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)a.I + n0;
+    if (tid < kTileM) {
+        const int rt = tile_route(a, tl, tid);
+        s_route[tid] = rt;
+        s_tok[tid] = rt >= 0 ? rt / (a.k + 1) : 0;
+    }
+    // scales / biases: 2 matrices x {s, b} x 64 rows x G groups, 16-byte loads of 8 groups
+    for (int i = tid; i < 2 * 2 * 64 * (G / 8); i += kPfThreads) {
+        const int chunk = i % (G / 8), row = (i / (G / 8)) % 64, sb = (i / (G / 8 * 64)) % 2, mt = i / (G / 8 * 128);
+        const vmi_qmat& M = mt == 0 ? Gm : Um;
+        const uint16_t* src = (sb == 0 ? M.s : M.b) + (row0 + row) * G + 8 * chunk;
+        const uint4 v = *reinterpret_cast<const uint4*>(src);
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float f = vmi_bf16_to_f32((wv[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+            float* dst = reinterpret_cast<float*>(&s_sb[8 * chunk + j][mt][row]);
+            dst[sb] = sb == 0 ? f * 16777216.0f : f;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < kTileM * G; i += kPfThreads) {
+        const int row = i / G, g = i - row * G;
+        s_xs[g][row] = a.xsum4[(size_t)s_tok[row] * G + g];
+    }
+    const Ring R{r0, r1, r2, r3};
+    // this thread's DMA piece: matrix mt, row r, half h (16i bytes into a slot)
+    const int dmt = tid >> 7, dr = (tid >> 1) & 63, dh = tid & 1;
+    const uint32_t* dsrc = (dmt == 0 ? Gm.w : Um.w) + (row0 + dr) * HW + 4 * (dh ^ ((dr >> 3) & 1));
+    const vmi_u4* arow = a.xop4 + (size_t)s_tok[16 * w + n] * HW;
+    auto issue = [&](int g, int u, vmi_u4& x0, vmi_u4& x1) {
+        vmi_lds_dma16_opaque(dsrc + 8 * g, R.at(u) + 1024 * w);
+        x0 = arow[8 * g + 2 * q];
+        x1 = arow[8 * g + 2 * q + 1];
+    };
+    vmi_u4 ap[kRing][2];
+    vmi_f4 acc[2][4];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) acc[m][s4] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kRing - 1; ++u) issue(u < G ? u : G - 1, u, ap[u][0], ap[u][1]);
+#pragma unroll 1
+    for (int g0 = 0; g0 < G; g0 += kRing) {
+#pragma unroll
+        for (int u = 0; u < kRing; ++u) {
+            const int g = g0 + u;
+            pf_wait_vmcnt<3 * (kRing - 2)>();  // group g's DMA and operand loads have landed
+            __syncthreads();                    // every wave's piece of group g; slot of g-1 free
+            const int gn = g + kRing - 1;
+            issue(gn < G ? gn : G - 1, (u + kRing - 1) % kRing, ap[(u + kRing - 1) % kRing][0],
+                  ap[(u + kRing - 1) % kRing][1]);
+            const uint8_t* slot = R.at(u);
+            const float4 xs = *reinterpret_cast<const float4*>(&s_xs[g][16 * w + 4 * q]);
+            const float xsr[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+                for (int s4 = 0; s4 < 4; ++s4) {
+                    const int row = 16 * s4 + n;
+                    const uint2 wq = *reinterpret_cast<const uint2*>(slot + 2048 * mt + ring_off(row, q));
+                    vmi_f4 d = vmi_mfma_f16(ap[u][0], vmi_unpack_u4_f16(wq.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
+                    d = vmi_mfma_f16(ap[u][1], vmi_unpack_u4_f16(wq.y), d);
+                    const float2 sb = s_sb[g][mt][row];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[mt][s4][r] = fmaf(d[r], sb.x, fmaf(sb.y, xsr[r], acc[mt][s4][r]));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep groups apart: bounded live registers
+        }
+    }
+    pf_wait_vmcnt<0>();
+    // SwiGLU into LDS: rows 16w + 4q + r, columns 16 s4 + n
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 16 * w + 4 * q + r;
+        const float inv = s_route[row] >= 0 ? 1.0f / a.fscale[s_tok[row]] : 0.0f;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const float gv = acc[0][s4][r] * inv, uv = acc[1][s4][r] * inv;
+            s_act[row][16 * s4 + n] = gv / (1.0f + expf(-gv)) * uv;
+        }
+    }
+    __syncthreads();
+    const int IW = a.I / 8, IG = a.I / 64;
+    for (int i = tid; i < kTileM * 8; i += kPfThreads) {
+        const int row = i >> 3, wd = i & 7;
+        const int route = s_route[row];
+        if (route < 0) continue;
+        uint16_t b[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) b[c] = vmi_f32_to_bf16(s_act[row][8 * wd + c]);
+        vmi_u4 o;  // slot order of vmi_unpack_u4_bf16_128: {0,4,1,5,2,6,3,7}
+        o[0] = (uint32_t)b[0] | ((uint32_t)b[4] << 16);
+        o[1] = (uint32_t)b[1] | ((uint32_t)b[5] << 16);
+        o[2] = (uint32_t)b[2] | ((uint32_t)b[6] << 16);
+        o[3] = (uint32_t)b[3] | ((uint32_t)b[7] << 16);
+        a.actop[(size_t)route * IW + (n0 >> 3) + wd] = o;
+    }
+    if (tid < kTileM) {
+        const int route = s_route[tid];
+        if (route >= 0) {
+            float sum = 0.0f;
+            for (int c = 0; c < 64; ++c) sum += vmi_bf16_to_f32(vmi_f32_to_bf16(s_act[tid][c]));
+            a.axs[(size_t)route * IG + (n0 >> 6)] = sum;
+        }
+    }
+}
+
+// Down: tile M 64 routes x N 128 hidden rows; K = inter.
+__global__ __launch_bounds__(kPfThreads, 2) void k_pf_down2(PfArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t r0[4096], r1[4096], r2[4096], r3[4096];
+    __shared__ __attribute__((aligned(16))) float2 s_sb[kMaxG][128];
+    __shared__ __attribute__((aligned(16))) float s_as[kMaxG][kTileM];
+    __shared__ int s_route[kTileM];
+    const int ti = blockIdx.x;
+    if (ti >= a.ntiles[0]) return;
+    const int4 tl = a.tiles[ti];
+    const int lane = threadIdx.x & 63, w = pf_wave(), tid = threadIdx.x;
+    const int n = lane & 15, q = lane >> 4;
+    const int h0 = blockIdx.y * 128;
+    const int IW = a.I / 8, G = a.I / 64;
+    const vmi_qmat Dm = tl.x >= 0 ? a.down : a.sh_down;
+    const size_t row0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)a.H + h0;
+    if (tid < kTileM) s_route[tid] = tile_route(a, tl, tid);
+    // scales / biases: {s, b} x 128 rows x G groups (G a multiple of 1; 8-group chunks when possible)
+    for (int i = tid; i < 2 * 128 * G; i += kPfThreads) {
+        const int g = i % G, row = (i / G) % 128, sb = i / (G * 128);
+        const float f = vmi_bf16_to_f32((sb == 0 ? Dm.s : Dm.b)[(row0 + row) * G + g]);
+        reinterpret_cast<float*>(&s_sb[g][row])[sb] = f;
+    }
+    __syncthreads();
+    for (int i = tid; i < kTileM * G; i += kPfThreads) {
+        const int row = i / G, g = i - row * G;
+        const int rt = s_route[row];
+        s_as[g][row] = rt >= 0 ? a.axs[(size_t)rt * G + g] : 0.0f;
+    }
+    const Ring R{r0, r1, r2, r3};
+    const int dr = tid >> 1, dh = tid & 1;
+    const uint32_t* dsrc = Dm.w + (row0 + dr) * IW + 4 * (dh ^ ((dr >> 3) & 1));
+    const int my_route = s_route[16 * w + n];
+    const vmi_u4* arow = a.actop + (size_t)(my_route >= 0 ? my_route : 0) * IW;
+    auto issue = [&](int g, int u, vmi_u4& x0, vmi_u4& x1) {
+        vmi_lds_dma16_opaque(dsrc + 8 * g, R.at(u) + 1024 * w);
+        x0 = arow[8 * g + 2 * q];
+        x1 = arow[8 * g + 2 * q + 1];
+    };
+    vmi_u4 ap[kRing][2];
+    vmi_f4 acc[8];
+#pragma unroll
+    for (int s8 = 0; s8 < 8; ++s8) acc[s8] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kRing - 1; ++u) issue(u < G ? u : G - 1, u, ap[u][0], ap[u][1]);
+#pragma unroll 1
+    for (int g0 = 0; g0 < G; g0 += kRing) {
+#pragma unroll
+        for (int u = 0; u < kRing; ++u) {
+            const int g = g0 + u;
+            if (g < G) {  // uniform
+                pf_wait_vmcnt<3 * (kRing - 2)>();
+                __syncthreads();
+                const int gn = g + kRing - 1;
+                issue(gn < G ? gn : G - 1, (u + kRing - 1) % kRing, ap[(u + kRing - 1) % kRing][0],
+                      ap[(u + kRing - 1) % kRing][1]);
+                const uint8_t* slot = R.at(u);
+                const float4 as = *reinterpret_cast<const float4*>(&s_as[g][16 * w + 4 * q]);
+                const float asr[4] = {as.x, as.y, as.z, as.w};
+#pragma unroll
+                for (int s8 = 0; s8 < 8; ++s8) {
+                    const int row = 16 * s8 + n;
+                    const uint2 wq = *reinterpret_cast<const uint2*>(slot + ring_off(row, q));
+                    vmi_f4 d = vmi_mfma_bf16(ap[u][0], vmi_unpack_u4_bf16_128(wq.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
+                    d = vmi_mfma_bf16(ap[u][1], vmi_unpack_u4_bf16_128(wq.y), d);
+                    const float2 sb = s_sb[g][row];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[s8][r] = fmaf(sb.x, fmaf(-128.0f, asr[r], d[r]), fmaf(sb.y, asr[r], acc[s8][r]));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    pf_wait_vmcnt<0>();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int route = s_route[16 * w + 4 * q + r];
+        if (route < 0) continue;
+        const int t = route / (a.k + 1), j = route - t * (a.k + 1);
+        const float wgt = j < a.k ? a.scores[t * a.k + j]
+                                  : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8)
+            a.ybuf[(size_t)route * a.H + h0 + 16 * s8 + n] = vmi_f32_to_bf16(acc[s8][r] * wgt);
+    }
+}
+
 // --------------------------------------------------------------- combine
 // out[t][h] = bf16(sum_{j <= k} y[t(k+1)+j][h] (valid routes, rank order) + residual)
 __global__ __launch_bounds__(kPfThreads) void k_pf_combine(PfArgs a) {
@@ -654,7 +931,7 @@ PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) 
     L.slots = take((size_t)T * k * 4);
     L.counts = take((size_t)cap * 4);
     L.offsets = take((size_t)cap * 4);
-    L.fill = take((size_t)cap * 4);
+    L.fill = take((size_t)T * k * 4);
     L.tiles = take((size_t)L.max_tiles * 16);
     L.ntiles = take(4);
     L.list = take((size_t)T * k * 4);
@@ -683,8 +960,8 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     if (D.bits != 4 || D.group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", D.bits, D.group);
     if (D.hidden != 512 && D.hidden != 1024 && D.hidden != 2048)
         return vmi::fail(VMI_ERR_UNSUPPORTED, "hidden=%d must be 512, 1024 or 2048", D.hidden);
-    if (D.inter % 64 || D.inter <= 0 || D.inter > 4096)
-        return vmi::fail(VMI_ERR_UNSUPPORTED, "inter=%d must be a multiple of 64", D.inter);
+    if (D.inter % 64 || D.inter <= 0 || D.inter > 2048)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "inter=%d must be a multiple of 64 up to 2048", D.inter);
     if (D.num_experts % 64 || D.num_experts <= 0 || D.num_experts > kPfMaxE)
         return vmi::fail(VMI_ERR_UNSUPPORTED, "num_experts=%d must be a multiple of 64 up to %d", D.num_experts,
                          kPfMaxE);
@@ -762,10 +1039,11 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
         }
     }
     hipLaunchKernelGGL(k_pf_topk, dim3(tok_blocks), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_count, dim3((T * D.top_k + kCountRoutes - 1) / kCountRoutes), dim3(kPfThreads), 0, s, a);
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
-    hipLaunchKernelGGL(k_pf_gateup, dim3(L.max_tiles, D.inter / 64), dim3(kPfThreads), 0, s, a);
-    hipLaunchKernelGGL(k_pf_down, dim3(L.max_tiles, D.hidden / 64), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_gateup2, dim3(L.max_tiles, D.inter / 64), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_down2, dim3(L.max_tiles, D.hidden / 128), dim3(kPfThreads), 0, s, a);
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(kPfThreads), 0, s, a);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill launch");
