@@ -183,6 +183,49 @@ int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weigh
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * vmi_qgemv -- y = W x for a small batch of tokens with an affine-quantised W
+ * (the reference's quantized Linear layers: QuantizedLinear of mlx, as used
+ * by the MTP fc and attention projections, qwen3_next_mtp.py:28-30, 40-53).
+ * x bf16 [T, K]; W [N, K] packed (bits 4 or 8, group 64); out f32 [T, N]
+ * and/or out_bf16 = bf16(y + residual) [T, N] (residual bf16 or NULL).
+ * T <= 8, T*K <= 32768, K a multiple of 64.
+ * ------------------------------------------------------------------------ */
+int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int group, float* out,
+              const uint16_t* residual, uint16_t* out_bf16, void* stream);
+
+/* ------------------------------------------------------------------------
+ * vmi_attention_layer -- the full-attention block of a Qwen3-Next decoder
+ * layer on a verify batch or a draft step: out = x + attn(rmsnorm(x)).
+ * Replaces the attention half of mlx-lm's Qwen3NextDecoderLayer as the MTP
+ * layer runs it (mlx_streaming/mtp/qwen3_next_mtp.py:53, mtp_step :60-63) and
+ * the main model's full-attention layers (generate.py:101-220).
+ * q_proj emits [q | gate] per head (n_heads x 2 x head_dim rows); q and k get
+ * a per-head RMSNorm (q_norm, k_norm weights over head_dim), then the rotary
+ * embedding on their first rope_dim dims (pairs (i, i + rope_dim/2),
+ * angle pos * rope_theta^(-2i/rope_dim)); k and v are appended as bf16 to the
+ * caches at positions pos0 .. pos0+T-1; token t attends to cache positions
+ * <= pos0 + t with softmax(q k / sqrt(head_dim)); the result times
+ * sigmoid(gate) goes through o_proj and is added to x.
+ * k_cache, v_cache: bf16 [n_kv_heads, max_len, head_dim].  head_dim 256;
+ * T * n_heads / n_kv_heads <= 64; norm weights are the multipliers applied
+ * (a checkpoint's zero-centred weights plus one).
+ * ------------------------------------------------------------------------ */
+typedef struct vmi_attn_layer_desc {
+    int hidden, n_heads, n_kv_heads, head_dim, rope_dim;
+    float rope_theta, norm_eps;
+    int bits, group;
+    const uint16_t* input_norm;   /* [hidden] */
+    vmi_qmat q_proj, k_proj, v_proj, o_proj;
+    const uint16_t* q_norm;       /* [head_dim] */
+    const uint16_t* k_norm;       /* [head_dim] */
+} vmi_attn_layer_desc;
+
+size_t vmi_attention_layer_workspace_bytes(int T, int hidden, int n_heads, int n_kv_heads);
+int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int T, int pos0, uint16_t* k_cache,
+                        uint16_t* v_cache, int max_len, uint16_t* out, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/* ------------------------------------------------------------------------
  * Acceptance.  Every entry point writes an int32 result record of 4 + K + 1
  * entries: [0] n_emitted, [1] matched (drafts accepted), [2] accepted_len
  * (verify positions whose state is kept), [3] winning path (-1: no finite

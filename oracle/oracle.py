@@ -336,3 +336,29 @@ def moe_layer_routed(x_bf16, L: dict, ids, scores, residual=False):
     _chk(rc, "moe_layer_routed")
     return out_f32, out_bf16
 
+
+def attention_layer(x, A: dict, pos0: int, k_cache, v_cache):
+    """Full-attention block in float64: (out [T, H], k_new [T, n_kv, 256], v_new).
+    A: H, n_heads, n_kv, rope_dim, theta, eps, bits, in_norm, q/k/v/o _w/_s/_b,
+    q_norm, k_norm (bf16 bits / packed arrays); caches bf16 bits [n_kv, max_len, 256]."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    H = A["H"]
+    T = x.size // H
+    n_kv = A["n_kv"]
+    kc = np.ascontiguousarray(k_cache, dtype=np.uint16)
+    vc = np.ascontiguousarray(v_cache, dtype=np.uint16)
+    max_len = kc.shape[1]
+    out = np.empty((T, H), dtype=np.float64)
+    kn = np.empty((T, n_kv, 256), dtype=np.float64)
+    vn = np.empty((T, n_kv, 256), dtype=np.float64)
+    fn = lib().orc_attention_layer_f64
+    fn.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_void_p] + [c_void_p] * 12 + \
+        [c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p]
+    a = {k: (np.ascontiguousarray(v) if isinstance(v, np.ndarray) else v) for k, v in A.items()}
+    _chk(fn(_p(x), T, H, A["n_heads"], n_kv, A["rope_dim"], c_float(A["theta"]), c_float(A["eps"]), _p(a["in_norm"]),
+            _p(a["q_w"]), _p(a["q_s"]), _p(a["q_b"]), _p(a["k_w"]), _p(a["k_s"]), _p(a["k_b"]),
+            _p(a["v_w"]), _p(a["v_s"]), _p(a["v_b"]), _p(a["o_w"]), _p(a["o_s"]), _p(a["o_b"]), A["bits"],
+            _p(a["q_norm"]), _p(a["k_norm"]), pos0, _p(kc), _p(vc), max_len, _p(out), _p(kn), _p(vn)),
+         "attention_layer")
+    return out, kn, vn
+

@@ -631,6 +631,110 @@ int orc_route_reduce(float* out, const float* weighted, const int32_t* assignmen
     return ORC_OK;
 }
 
+/* ------------------------------------------------------------- attention */
+/* Full-attention block of a Qwen3-Next decoder layer on T tokens at cache
+ * positions pos0.. (the MTP layer, qwen3_next_mtp.py:53; the architecture of
+ * mlx-lm's / transformers' Qwen3NextAttention), in double:
+ *   xn = rmsnorm(x) (bf16, orc_rmsnorm_bf16); q|gate, k, v = W xn;
+ *   per head q, k: q * inv_rms(q) * q_norm (eps), rotary on dims < rope_dim
+ *   (pairs (i, i + rope_dim/2), angle pos * theta^(-2i/rope_dim));
+ *   token t attends to positions <= pos0 + t: cache entries < pos0 come from
+ *   k_cache/v_cache (bf16 [n_kv, max_len, 256]), the batch's own from the
+ *   values just computed; o = softmax(q k / sqrt(256)) v * sigmoid(gate);
+ *   out = x + o_proj o.
+ * k_new / v_new (optional, double [T, n_kv, 256]) receive the batch's k (after
+ * norm and rotary) and v.  GQA: query head h reads kv head h / (n_heads/n_kv). */
+int orc_attention_layer_f64(const uint16_t* x, int T, int H, int n_heads, int n_kv, int rope_dim, float theta,
+                            float eps, const uint16_t* in_norm, const uint32_t* qw, const uint16_t* qs,
+                            const uint16_t* qb, const uint32_t* kw, const uint16_t* ks, const uint16_t* kb,
+                            const uint32_t* vw, const uint16_t* vs, const uint16_t* vb, const uint32_t* ow,
+                            const uint16_t* os, const uint16_t* ob, int bits, const uint16_t* q_norm,
+                            const uint16_t* k_norm, int pos0, const uint16_t* k_cache, const uint16_t* v_cache,
+                            int max_len, double* out, double* k_new, double* v_new) {
+    const int D = 256, G = n_heads / n_kv, group = 64;
+    if (T <= 0 || n_kv <= 0 || n_heads % n_kv || rope_dim > D || pos0 < 0 || pos0 + T > max_len) return ORC_EINVAL;
+    uint16_t* xn = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)T * H);
+    double* xd = (double*)malloc(sizeof(double) * (size_t)T * H);
+    double* qg = (double*)malloc(sizeof(double) * (size_t)T * n_heads * 2 * D);
+    double* kk = (double*)malloc(sizeof(double) * (size_t)T * n_kv * D);
+    double* vv = (double*)malloc(sizeof(double) * (size_t)T * n_kv * D);
+    double* att = (double*)malloc(sizeof(double) * (size_t)T * n_heads * D);
+    double* sc = (double*)malloc(sizeof(double) * (size_t)(pos0 + T));
+    int rc = (!xn || !xd || !qg || !kk || !vv || !att || !sc) ? ORC_ENOMEM : ORC_OK;
+    if (rc == ORC_OK) rc = orc_rmsnorm_bf16(x, in_norm, eps, T, H, xn, NULL);
+    if (rc == ORC_OK) {
+        for (size_t i = 0; i < (size_t)T * H; ++i) xd[i] = bf16_to_f32(xn[i]);
+        qgemv_f64(qw, qs, qb, n_heads * 2 * D, H, group, bits, xd, T, qg);
+        qgemv_f64(kw, ks, kb, n_kv * D, H, group, bits, xd, T, kk);
+        qgemv_f64(vw, vs, vb, n_kv * D, H, group, bits, xd, T, vv);
+        const int half = rope_dim / 2;
+        for (int t = 0; t < T; ++t) {
+            const int pos = pos0 + t;
+            for (int h = 0; h < n_heads + n_kv; ++h) {
+                double* v = h < n_heads ? qg + ((size_t)t * n_heads + h) * 2 * D : kk + ((size_t)t * n_kv + (h - n_heads)) * D;
+                const uint16_t* nw = h < n_heads ? q_norm : k_norm;
+                double ss = 0.0;
+                for (int d = 0; d < D; ++d) ss += v[d] * v[d];
+                const double inv = 1.0 / sqrt(ss / D + (double)eps);
+                double tmp[256];
+                for (int d = 0; d < D; ++d) tmp[d] = v[d] * inv * (double)bf16_to_f32(nw[d]);
+                for (int d = 0; d < D; ++d) {
+                    double r = tmp[d];
+                    if (d < rope_dim) {
+                        const int i = d < half ? d : d - half;
+                        const double ang = (double)pos * pow((double)theta, -(double)(2 * i) / (double)rope_dim);
+                        const double partner = d < half ? -tmp[d + half] : tmp[d - half];
+                        r = tmp[d] * cos(ang) + partner * sin(ang);
+                    }
+                    v[d] = r;
+                }
+            }
+        }
+        if (k_new) memcpy(k_new, kk, sizeof(double) * (size_t)T * n_kv * D);
+        if (v_new) memcpy(v_new, vv, sizeof(double) * (size_t)T * n_kv * D);
+        for (int t = 0; t < T; ++t) {
+            for (int h = 0; h < n_heads; ++h) {
+                const int g = h / G;
+                const double* q = qg + ((size_t)t * n_heads + h) * 2 * D;
+                const double* gate = q + D;
+                const int L = pos0 + t + 1;
+                double mx = -INFINITY;
+                for (int j = 0; j < L; ++j) {
+                    double dot = 0.0;
+                    if (j < pos0) {
+                        const uint16_t* kr = k_cache + ((size_t)g * max_len + j) * D;
+                        for (int d = 0; d < D; ++d) dot += q[d] * (double)bf16_to_f32(kr[d]);
+                    } else {
+                        const double* kr = kk + ((size_t)(j - pos0) * n_kv + g) * D;
+                        for (int d = 0; d < D; ++d) dot += q[d] * kr[d];
+                    }
+                    sc[j] = dot / 16.0;
+                    if (sc[j] > mx) mx = sc[j];
+                }
+                double den = 0.0;
+                for (int j = 0; j < L; ++j) { sc[j] = exp(sc[j] - mx); den += sc[j]; }
+                double* o = att + ((size_t)t * n_heads + h) * D;
+                for (int d = 0; d < D; ++d) o[d] = 0.0;
+                for (int j = 0; j < L; ++j) {
+                    const double p = sc[j] / den;
+                    if (j < pos0) {
+                        const uint16_t* vr = v_cache + ((size_t)g * max_len + j) * D;
+                        for (int d = 0; d < D; ++d) o[d] += p * (double)bf16_to_f32(vr[d]);
+                    } else {
+                        const double* vr = vv + ((size_t)(j - pos0) * n_kv + g) * D;
+                        for (int d = 0; d < D; ++d) o[d] += p * vr[d];
+                    }
+                }
+                for (int d = 0; d < D; ++d) o[d] *= 1.0 / (1.0 + exp(-gate[d]));
+            }
+        }
+        qgemv_f64(ow, os, ob, H, n_heads * D, group, bits, att, T, out);
+        for (size_t i = 0; i < (size_t)T * H; ++i) out[i] += bf16_to_f32(x[i]);
+    }
+    free(xn); free(xd); free(qg); free(kk); free(vv); free(att); free(sc);
+    return rc;
+}
+
 /* ---------------------------------------------------------------- lm_head */
 /* logits = W . rmsnorm(x) (generate.py:208-217; drafter.py:20-40): xn is the
  * bf16 RMSNorm output (orc_rmsnorm_bf16, the GPU's exact operand) or x itself

@@ -72,6 +72,11 @@ _SIGNATURES = {
     "vmi_sample_top_p_workspace_bytes": (c_size_t, [c_int, c_int]),
     "vmi_sample_top_p": (c_int, [c_void_p, c_int, c_int, c_float, c_float, c_uint64, c_uint64, c_void_p, c_void_p,
                                  c_size_t, c_void_p]),
+    "vmi_qgemv": (c_int, [c_void_p, c_int, c_int, QMat, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
+                          c_void_p]),
+    "vmi_attention_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "vmi_attention_layer": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                                    c_size_t, c_void_p]),
     "vmi_lm_head_workspace_bytes": (c_size_t, [c_int, c_int]),
     "vmi_lm_head": (c_int, [c_void_p, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p, c_void_p,
                             c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -1,0 +1,105 @@
+"""Full-attention decoder block and quantised GEMV on libvmi.
+
+``AttentionLayer`` is the attention half of a Qwen3-Next decoder layer as the
+MTP layer runs it (mlx_streaming/mtp/qwen3_next_mtp.py:34-57, ``self.layer``)
+and as the main model's full-attention layers run it in the verify forward
+(mlx_streaming/mtp/generate.py:101-220): out = x + attn(rmsnorm(x)) with the KV
+cache updated in place.  ``KVCache`` holds one layer's bf16 keys and values
+[n_kv_heads, max_len, 256] and the number of committed positions, the analogue
+of mlx-lm's KVCache with its trim (mlx_streaming/mtp/kv_cache.py:222-251).
+Errors raise ``VmiError``; there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from ._lib import QMat, VmiError, check, load
+from .moe import QuantizedProj, _require, _stream_handle, workspace
+
+
+class AttnDesc(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("n_heads", ctypes.c_int), ("n_kv_heads", ctypes.c_int),
+                ("head_dim", ctypes.c_int), ("rope_dim", ctypes.c_int), ("rope_theta", ctypes.c_float),
+                ("norm_eps", ctypes.c_float), ("bits", ctypes.c_int), ("group", ctypes.c_int),
+                ("input_norm", ctypes.c_void_p), ("q_proj", QMat), ("k_proj", QMat), ("v_proj", QMat),
+                ("o_proj", QMat), ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p)]
+
+
+def qgemv(x: torch.Tensor, w: QuantizedProj, *, bits: int = 4, out: Optional[torch.Tensor] = None,
+          residual: Optional[torch.Tensor] = None, out_bf16: Optional[torch.Tensor] = None, stream=None):
+    """y = W x for x bf16 [T, K] (T <= 8): f32 [T, N] and/or bf16(y + residual)."""
+    T, K = x.shape
+    N = w.weight.shape[-2]
+    dev = x.device
+    _require(x, "x", 2, dev)
+    if out is None and out_bf16 is None:
+        out = torch.empty((T, N), dtype=torch.float32, device=dev)
+    rc = load().vmi_qgemv(x.data_ptr(), T, K, w.qmat(), N, bits, 64, None if out is None else out.data_ptr(),
+                          None if residual is None else residual.data_ptr(),
+                          None if out_bf16 is None else out_bf16.data_ptr(), _stream_handle(stream))
+    check(rc, "vmi_qgemv")
+    return out if out is not None else out_bf16
+
+
+class KVCache:
+    """bf16 keys and values of one attention layer, [n_kv_heads, max_len, 256]."""
+
+    def __init__(self, n_kv_heads: int, max_len: int, device, head_dim: int = 256):
+        self.k = torch.zeros((n_kv_heads, max_len, head_dim), dtype=torch.bfloat16, device=device)
+        self.v = torch.zeros_like(self.k)
+        self.max_len = max_len
+        self.length = 0  # committed positions
+
+    def trim(self, n: int) -> None:
+        """Drops the last n positions (kv_cache.py:222-251: rejected drafts)."""
+        if n < 0 or n > self.length:
+            raise VmiError(f"cannot trim {n} of {self.length} positions")
+        self.length -= n
+
+
+class AttentionLayer:
+    def __init__(self, q_proj: QuantizedProj, k_proj: QuantizedProj, v_proj: QuantizedProj, o_proj: QuantizedProj,
+                 input_norm: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor, *, n_heads: int = 16,
+                 n_kv_heads: int = 2, rope_dim: int = 64, rope_theta: float = 1e7, eps: float = 1e-6,
+                 bits: int = 4):
+        dev = input_norm.device
+        self.device = dev
+        self.hidden = input_norm.numel()
+        self.n_heads, self.n_kv = n_heads, n_kv_heads
+        for name, p in (("q_proj", q_proj), ("k_proj", k_proj), ("v_proj", v_proj), ("o_proj", o_proj)):
+            p.check(name, dev)
+        for name, t in (("input_norm", input_norm), ("q_norm", q_norm), ("k_norm", k_norm)):
+            _require(t, name, 2, dev)
+        self._keep = (q_proj, k_proj, v_proj, o_proj, input_norm, q_norm, k_norm)
+        d = AttnDesc()
+        d.hidden, d.n_heads, d.n_kv_heads, d.head_dim, d.rope_dim = self.hidden, n_heads, n_kv_heads, 256, rope_dim
+        d.rope_theta, d.norm_eps, d.bits, d.group = rope_theta, eps, bits, 64
+        d.input_norm = input_norm.data_ptr()
+        d.q_proj, d.k_proj, d.v_proj, d.o_proj = q_proj.qmat(), k_proj.qmat(), v_proj.qmat(), o_proj.qmat()
+        d.q_norm, d.k_norm = q_norm.data_ptr(), k_norm.data_ptr()
+        self.desc = d
+
+    def new_cache(self, max_len: int) -> KVCache:
+        return KVCache(self.n_kv, max_len, self.device)
+
+    def __call__(self, x: torch.Tensor, cache: KVCache, *, pos0: Optional[int] = None,
+                 out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """x bf16 [T, hidden] at cache positions pos0.. (default: cache.length);
+        appends k, v there and sets cache.length = pos0 + T."""
+        T = x.shape[0]
+        pos0 = cache.length if pos0 is None else pos0
+        _require(x, "x", 2, self.device)
+        if out is None:
+            out = torch.empty_like(x)
+        sh = _stream_handle(stream)
+        lib = load()
+        ws = workspace(lib.vmi_attention_layer_workspace_bytes(T, self.hidden, self.n_heads, self.n_kv), self.device,
+                       sh, tag="attention")
+        rc = lib.vmi_attention_layer(ctypes.byref(self.desc), x.data_ptr(), T, pos0, cache.k.data_ptr(),
+                                     cache.v.data_ptr(), cache.max_len, out.data_ptr(), ws.data_ptr(), ws.numel(), sh)
+        check(rc, "vmi_attention_layer")
+        cache.length = pos0 + T
+        return out

@@ -1,0 +1,575 @@
+// Full-attention decoder block of the verify batch and of the MTP draft step
+// (Qwen3-Next gated attention: GQA, per-head q/k RMSNorm, partial rotary
+// embedding, sigmoid output gate), and the quantised GEMV it is built on.
+//
+// The reference runs this block through mlx-lm's Qwen3NextAttention inside the
+// MTP layer (mlx_streaming/mtp/qwen3_next_mtp.py:34-57, layer(x) at :53) and in
+// the main model's full-attention layers (generate.py:101-220).  The same
+// architecture is published in Hugging Face transformers' modeling_qwen3_next
+// (Qwen3NextAttention: q_proj emits [q | gate] per head, q_norm/k_norm over
+// head_dim, rotary on the first rotary_dim dims with rotate_half pairs
+// (i, i + rotary_dim/2), softmax(q k^T / sqrt(head_dim)) v, times
+// sigmoid(gate), o_proj).
+//
+// Kernels:
+//   k_rms_rows     bf16(x * inv_rms * w) per token (canonical fixed order)
+//   k_qgemv        y[t][n] = sum_k x[t][k] W[n][k], 4/8-bit affine W, T <= 8:
+//                  one wave per output row, 16 bytes of packed weights per
+//                  lane per step, tokens staged in LDS, fp32 accumulation
+//   k_qk_rope      per (token, head): q/k RMSNorm, rotary, q as bf16, k and v
+//                  appended to the bf16 KV cache at the token's position
+//   k_attn_chunk   per (kv head, key chunk): scores and P.V for the 8T query
+//                  rows of the head group with bf16 MFMAs, online softmax
+//                  over 64-key steps; writes the chunk's (max, sum, O)
+//   k_attn_merge   per (token, head): merges the chunks, times sigmoid(gate),
+//                  bf16 input of o_proj
+
+#include "vmi_device.h"
+#include "vmi_internal.h"
+
+namespace {
+
+constexpr int kAThreads = 256;
+constexpr int kQgMaxT = 8;
+constexpr int kHeadDim = 256;
+constexpr int kKeyStep = 64;       // keys per MFMA step inside a chunk
+
+__device__ __forceinline__ int at_wave() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+__device__ __forceinline__ void bf16x8f(const uint4& q, float (&v)[8]) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+
+// ---------------------------------------------------------------- RMSNorm
+struct RmsArgs {
+    const uint16_t* x;   // [T, H]
+    const uint16_t* w;   // [H]
+    float eps;
+    int T, H;
+    uint16_t* out;       // [T, H]
+};
+
+// One wave per token; lane l owns H/64 contiguous values (H % 512 == 0).
+__global__ __launch_bounds__(kAThreads) void k_rms_rows(RmsArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * (kAThreads / 64) + at_wave();
+    if (t >= a.T) return;
+    const int cpl = a.H / 64, nv = cpl / 8;
+    const uint16_t* xr = a.x + (size_t)t * a.H + lane * cpl;
+    float ss = 0.0f;
+    for (int v = 0; v < nv; ++v) {
+        float f[8];
+        bf16x8f(*reinterpret_cast<const uint4*>(xr + 8 * v), f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+    }
+    ss = vmi_wave_sum_canon(ss);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)a.H) + a.eps));
+    for (int v = 0; v < nv; ++v) {
+        float f[8], g[8];
+        bf16x8f(*reinterpret_cast<const uint4*>(xr + 8 * v), f);
+        bf16x8f(*reinterpret_cast<const uint4*>(a.w + lane * cpl + 8 * v), g);
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            o[i] = (uint32_t)vmi_f32_to_bf16((f[2 * i] * inv) * g[2 * i]) |
+                   ((uint32_t)vmi_f32_to_bf16((f[2 * i + 1] * inv) * g[2 * i + 1]) << 16);
+        *reinterpret_cast<uint4*>(a.out + (size_t)t * a.H + lane * cpl + 8 * v) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// ------------------------------------------------------------------ GEMV
+// Up to three weight matrices stacked along the output rows (q, k, v).
+struct QgArgs {
+    const uint16_t* x;      // [T, K] bf16
+    int T, K, bits;
+    vmi_qmat m[3];
+    int rows[3];            // rows of each matrix
+    int nrows;              // total
+    float* out;             // [T, out_stride] f32: row n of the stack at column n
+    int out_stride;
+    const uint16_t* residual;  // optional [T, out_stride] bf16: out_bf16 = bf16(y + residual)
+    uint16_t* out_bf16;        // optional
+};
+
+// One wave per output row, 4 rows per workgroup.  Lane l takes 32-column
+// blocks l, l + 64, ...; per block sum_c x_c q_c and sum_c x_c meet the
+// block's group scale and bias once.
+__global__ __launch_bounds__(kAThreads) void k_qgemv(QgArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t s_x[];  // [T][K]
+    const int lane = threadIdx.x & 63, w = at_wave();
+    const int T = a.T, K = a.K;
+    for (int i = threadIdx.x * 8; i < T * K; i += kAThreads * 8)
+        *reinterpret_cast<uint4*>(&s_x[i]) = *reinterpret_cast<const uint4*>(&a.x[i]);
+    __syncthreads();
+    const int n = blockIdx.x * (kAThreads / 64) + w;
+    if (n >= a.nrows) return;
+    int mi = 0, r = n;
+    while (mi < 2 && r >= a.rows[mi]) r -= a.rows[mi++];
+    const vmi_qmat M = a.m[mi];
+    const int G = K / 64;
+    const int wpr = K * a.bits / 32;
+    float acc[kQgMaxT];
+#pragma unroll
+    for (int t = 0; t < kQgMaxT; ++t) acc[t] = 0.0f;
+    for (int blk = lane; blk < K / 32; blk += 64) {
+        const int c0 = 32 * blk;
+        float wq[32];
+        if (a.bits == 4) {
+            const uint4 p = *reinterpret_cast<const uint4*>(M.w + (size_t)r * wpr + c0 / 8);
+            const uint32_t ww[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+            for (int i = 0; i < 32; ++i) wq[i] = (float)((ww[i >> 3] >> (4 * (i & 7))) & 0xFu);
+        } else {
+            const uint4 p0 = *reinterpret_cast<const uint4*>(M.w + (size_t)r * wpr + c0 / 4);
+            const uint4 p1 = *reinterpret_cast<const uint4*>(M.w + (size_t)r * wpr + c0 / 4 + 4);
+            const uint32_t ww[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+            for (int i = 0; i < 32; ++i) wq[i] = (float)((ww[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+        }
+        const float sc = vmi_bf16_to_f32(M.s[(size_t)r * G + c0 / 64]);
+        const float bi = vmi_bf16_to_f32(M.b[(size_t)r * G + c0 / 64]);
+#pragma unroll
+        for (int t = 0; t < kQgMaxT; ++t) {
+            if (t < T) {
+                float xq = 0.0f, xs = 0.0f;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float xf[8];
+                    bf16x8f(*reinterpret_cast<const uint4*>(&s_x[t * K + c0 + 8 * v]), xf);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        xq = fmaf(xf[i], wq[8 * v + i], xq);
+                        xs += xf[i];
+                    }
+                }
+                acc[t] = fmaf(xq, sc, fmaf(xs, bi, acc[t]));
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < kQgMaxT; ++t) {
+        if (t < T) {
+            const float y = vmi_wave_sum_canon(acc[t]);
+            if (lane == 0) {
+                if (a.out) a.out[(size_t)t * a.out_stride + n] = y;
+                if (a.out_bf16) {
+                    const float rr = a.residual ? vmi_bf16_to_f32(a.residual[(size_t)t * a.out_stride + n]) : 0.0f;
+                    a.out_bf16[(size_t)t * a.out_stride + n] = vmi_f32_to_bf16(y + rr);
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------- q/k norm, rotary
+struct RopeArgs {
+    const float* qkv;        // [T, stride]: q|gate per head (n_heads * 2 * 256), then k (n_kv * 256), then v
+    int stride;
+    int T, n_heads, n_kv, rope_dim, pos0, max_len;
+    float theta, eps;
+    const uint16_t* q_norm;  // [256]
+    const uint16_t* k_norm;  // [256]
+    uint16_t* q_out;         // [T, n_heads, 256] bf16
+    uint16_t* k_cache;       // [n_kv, max_len, 256]
+    uint16_t* v_cache;
+};
+
+// One wave per (token, head): 4 values per lane.  Heads [0, n_heads) are
+// queries, [n_heads, n_heads + n_kv) keys (values copied alongside).
+__global__ __launch_bounds__(kAThreads) void k_qk_rope(RopeArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int item = blockIdx.x * (kAThreads / 64) + at_wave();
+    const int per_tok = a.n_heads + a.n_kv;
+    if (item >= a.T * per_tok) return;
+    const int t = item / per_tok, h = item - t * per_tok;
+    const bool is_q = h < a.n_heads;
+    const float* src = is_q ? a.qkv + (size_t)t * a.stride + (size_t)h * 2 * kHeadDim
+                            : a.qkv + (size_t)t * a.stride + (size_t)a.n_heads * 2 * kHeadDim +
+                                  (size_t)(h - a.n_heads) * kHeadDim;
+    const uint16_t* nw = is_q ? a.q_norm : a.k_norm;
+    // lane holds dims d = lane + 64 j (j < 4): rotary partners (i, i + rd/2) live in one lane
+    // only when rd/2 is a multiple of 64, so the partner comes through LDS.
+    __shared__ float s_v[kAThreads / 64][kHeadDim];
+    const int w = at_wave();
+    float v[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = src[lane + 64 * j];
+        ss = fmaf(v[j], v[j], ss);
+    }
+    ss = vmi_wave_sum_canon(ss);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)kHeadDim) + a.eps));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        // normalised value as the model dtype (bf16), then rotary in fp32
+        v[j] = vmi_bf16_to_f32(vmi_f32_to_bf16((v[j] * inv) * vmi_bf16_to_f32(nw[lane + 64 * j])));
+        s_v[w][lane + 64 * j] = v[j];
+    }
+    __builtin_amdgcn_wave_barrier();  // s_v[w] is this wave's own row: LDS order within a wave suffices
+    const int pos = a.pos0 + t;
+    const int half = a.rope_dim / 2;
+    uint16_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        float r = v[j];
+        if (d < a.rope_dim) {
+            // angle pos * theta^(-2i/rd) in double: fp32 rounding of angles up to ~3e4 rad
+            // would move the rotation by ~1e-3
+            const int i = d < half ? d : d - half;
+            const double ang = (double)pos * pow((double)a.theta, -(double)(2 * i) / (double)a.rope_dim);
+            const float cs = (float)cos(ang), sn = (float)sin(ang);
+            const float partner = d < half ? -s_v[w][d + half] : s_v[w][d - half];
+            r = v[j] * cs + partner * sn;
+        }
+        o[j] = vmi_f32_to_bf16(r);
+    }
+    if (is_q) {
+        uint16_t* qo = a.q_out + ((size_t)t * a.n_heads + h) * kHeadDim;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) qo[lane + 64 * j] = o[j];
+    } else {
+        const int g = h - a.n_heads;
+        uint16_t* kc = a.k_cache + ((size_t)g * a.max_len + pos) * kHeadDim;
+        uint16_t* vc = a.v_cache + ((size_t)g * a.max_len + pos) * kHeadDim;
+        const float* vsrc = a.qkv + (size_t)t * a.stride + (size_t)a.n_heads * 2 * kHeadDim +
+                            (size_t)a.n_kv * kHeadDim + (size_t)g * kHeadDim;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            kc[lane + 64 * j] = o[j];
+            vc[lane + 64 * j] = vmi_f32_to_bf16(vsrc[lane + 64 * j]);
+        }
+    }
+}
+
+// -------------------------------------------------------------- attention
+struct AttnArgs {
+    const uint16_t* q;        // [T, n_heads, 256] bf16
+    const uint16_t* k_cache;  // [n_kv, max_len, 256]
+    const uint16_t* v_cache;
+    int T, n_heads, n_kv, pos0, max_len;
+    int chunk;                // keys per workgroup (multiple of 64)
+    int nchunks;
+    float* part_o;            // [n_kv, nchunks, RP, 256]
+    float* part_ml;           // [n_kv, nchunks, RP, 2]
+    const float* qkv;         // for the gate in the merge
+    int stride;
+    uint16_t* o;              // [T, n_heads * 256] bf16 gated attention output
+};
+
+// Rows of a head group: r = t * G + hl (G = n_heads / n_kv query heads per kv
+// head), RP = R rounded up to 16.  One workgroup: 4 waves, 64 keys per step.
+// Scores: wave w takes keys 16w..16w+15 of the step for every row subtile;
+// P.V: wave w takes dims 64w..64w+63.  Online softmax across steps.
+template <int MS>  // row subtiles of 16 (RP = 16 MS)
+__global__ __launch_bounds__(kAThreads) void k_attn_chunk(AttnArgs a) {
+    constexpr int RP = 16 * MS;
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[RP][kHeadDim + 8];
+    __shared__ __attribute__((aligned(16))) uint16_t s_vt[kHeadDim][kKeyStep + 8];
+    __shared__ __attribute__((aligned(16))) uint16_t s_p[RP][kKeyStep + 8];
+    __shared__ float s_s[RP][kKeyStep + 1];
+    __shared__ float s_m[RP], s_l[RP], s_scale[RP];
+    const int g = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, w = at_wave();
+    const int nl = lane & 15, q4 = lane >> 4;
+    const int G = a.n_heads / a.n_kv;
+    const int R = a.T * G;
+    const int L = a.pos0 + a.T;  // keys present
+    const int k0 = c * a.chunk, k1 = min(L, k0 + a.chunk);
+    // queries of this head group
+    for (int i = tid; i < RP * (kHeadDim / 8); i += kAThreads) {
+        const int row = i / (kHeadDim / 8), d8 = i % (kHeadDim / 8);
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (row < R) {
+            const int t = row / G, hl = row % G;
+            v = *reinterpret_cast<const uint4*>(a.q + ((size_t)t * a.n_heads + g * G + hl) * kHeadDim + 8 * d8);
+        }
+        *reinterpret_cast<uint4*>(&s_q[row][8 * d8]) = v;
+    }
+    if (tid < RP) {
+        s_m[tid] = -INFINITY;
+        s_l[tid] = 0.0f;
+    }
+    vmi_f4 oacc[MS][4];
+#pragma unroll
+    for (int m = 0; m < MS; ++m)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) oacc[m][s] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+    const uint16_t* kc = a.k_cache + (size_t)g * a.max_len * kHeadDim;
+    const uint16_t* vc = a.v_cache + (size_t)g * a.max_len * kHeadDim;
+    __syncthreads();
+    for (int j0 = k0; j0 < k1; j0 += kKeyStep) {
+        // V of this step into LDS, transposed: s_vt[dim][key]
+        for (int i = tid; i < kKeyStep * (kHeadDim / 8); i += kAThreads) {
+            const int key = i / (kHeadDim / 8), d8 = i % (kHeadDim / 8);
+            const int kk = j0 + key;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (kk < k1) v = *reinterpret_cast<const uint4*>(vc + (size_t)kk * kHeadDim + 8 * d8);
+            const uint32_t ww[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s_vt[8 * d8 + e][key] = (uint16_t)(ww[e >> 1] >> (16 * (e & 1)));
+        }
+        // scores: B = K^T, lane's key j0 + 16w + nl, dims 32kk + 8q4
+        const int key = j0 + 16 * w + nl;
+        const bool kok = key < k1;
+        vmi_u4 kb[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            kb[kk] = vmi_u4{0u, 0u, 0u, 0u};
+            if (kok) {
+                const uint4 v = *reinterpret_cast<const uint4*>(kc + (size_t)key * kHeadDim + 32 * kk + 8 * q4);
+                kb[kk] = vmi_u4{v.x, v.y, v.z, v.w};
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MS; ++m) {
+            vmi_f4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const uint4 av = *reinterpret_cast<const uint4*>(&s_q[16 * m + nl][32 * kk + 8 * q4]);
+                sacc = vmi_mfma_bf16(vmi_u4{av.x, av.y, av.z, av.w}, kb[kk], sacc);
+            }
+            // D rows 16m + 4q4 + r (query rows), column nl (key 16w + nl)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * m + 4 * q4 + r;
+                float sv = sacc[r] * 0.0625f;  // 1 / sqrt(256)
+                const int t = row / G;
+                const bool ok = kok && row < R && key <= a.pos0 + t;
+                s_s[row][16 * w + nl] = ok ? sv : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // online softmax per row: thread per row
+        if (tid < RP) {
+            const int row = tid;
+            float mx = s_m[row];
+            for (int j = 0; j < kKeyStep; ++j) mx = fmaxf(mx, s_s[row][j]);
+            const float scale = mx == -INFINITY ? 1.0f : expf(s_m[row] - mx);
+            float l = s_l[row] * scale;
+            for (int j = 0; j < kKeyStep; ++j) {
+                const float p = mx == -INFINITY ? 0.0f : expf(s_s[row][j] - mx);
+                const uint16_t pb = vmi_f32_to_bf16(p);
+                s_p[row][j] = pb;
+                l += vmi_bf16_to_f32(pb);
+            }
+            s_m[row] = mx;
+            s_l[row] = l;
+            s_scale[row] = scale;
+        }
+        __syncthreads();
+        // O = O * scale + P V: wave w dims 64w + 16s + nl; A = P rows, K = 64 keys
+#pragma unroll
+        for (int m = 0; m < MS; ++m) {
+            float sc[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[r] = s_scale[16 * m + 4 * q4 + r];
+            vmi_u4 pa[2];
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const uint4 av = *reinterpret_cast<const uint4*>(&s_p[16 * m + nl][32 * kk + 8 * q4]);
+                pa[kk] = vmi_u4{av.x, av.y, av.z, av.w};
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int d = 64 * w + 16 * s + nl;
+                vmi_f4 acc = oacc[m][s];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r] *= sc[r];
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const uint4 bv = *reinterpret_cast<const uint4*>(&s_vt[d][32 * kk + 8 * q4]);
+                    acc = vmi_mfma_bf16(pa[kk], vmi_u4{bv.x, bv.y, bv.z, bv.w}, acc);
+                }
+                oacc[m][s] = acc;
+            }
+        }
+        __syncthreads();
+    }
+    // partials: D rows 16m + 4q4 + r, dims 64w + 16s + nl
+    float* po = a.part_o + ((size_t)g * a.nchunks + c) * RP * kHeadDim;
+#pragma unroll
+    for (int m = 0; m < MS; ++m)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) po[(size_t)(16 * m + 4 * q4 + r) * kHeadDim + 64 * w + 16 * s + nl] = oacc[m][s][r];
+    if (tid < RP) {
+        float* pml = a.part_ml + (((size_t)g * a.nchunks + c) * RP + tid) * 2;
+        pml[0] = s_m[tid];
+        pml[1] = s_l[tid];
+    }
+}
+
+// One workgroup per (token, head): 256 threads = the head's dims.
+__global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
+    const int t = blockIdx.x / a.n_heads, h = blockIdx.x % a.n_heads, d = threadIdx.x;
+    const int G = a.n_heads / a.n_kv, g = h / G, row = t * G + (h % G);
+    float M = -INFINITY;
+    for (int c = 0; c < a.nchunks; ++c) M = fmaxf(M, a.part_ml[(((size_t)g * a.nchunks + c) * RP + row) * 2]);
+    float num = 0.0f, den = 0.0f;
+    for (int c = 0; c < a.nchunks; ++c) {
+        const float* ml = a.part_ml + (((size_t)g * a.nchunks + c) * RP + row) * 2;
+        if (ml[0] == -INFINITY) continue;
+        const float f = expf(ml[0] - M);
+        den = fmaf(ml[1], f, den);
+        num = fmaf(a.part_o[(((size_t)g * a.nchunks + c) * RP + row) * kHeadDim + d], f, num);
+    }
+    const float gate = a.qkv[(size_t)t * a.stride + (size_t)h * 2 * kHeadDim + kHeadDim + d];
+    const float y = (den > 0.0f ? num / den : 0.0f) / (1.0f + expf(-gate));
+    a.o[((size_t)t * a.n_heads + h) * kHeadDim + d] = vmi_f32_to_bf16(y);
+}
+
+// ------------------------------------------------------------------ host
+int attn_chunks(int L) {
+    int nc = (L + 255) / 256;
+    return nc < 1 ? 1 : (nc > 128 ? 128 : nc);
+}
+
+struct AttnLayout {
+    size_t xn, qkv, q, part_o, part_ml, o, bytes;
+};
+
+AttnLayout attn_layout(int T, int H, int n_heads, int n_kv) {
+    AttnLayout L{};
+    size_t off = 0;
+    auto take = [&](size_t b) {
+        const size_t o = off;
+        off += vmi::align256(b);
+        return o;
+    };
+    const int RP = 16 * ((T * (n_heads / n_kv) + 15) / 16);
+    const int stride = n_heads * 2 * kHeadDim + 2 * n_kv * kHeadDim;
+    L.xn = take((size_t)T * H * 2);
+    L.qkv = take((size_t)T * stride * 4);
+    L.q = take((size_t)T * n_heads * kHeadDim * 2);
+    L.part_o = take((size_t)n_kv * 128 * RP * kHeadDim * 4);
+    L.part_ml = take((size_t)n_kv * 128 * RP * 2 * 4);
+    L.o = take((size_t)T * n_heads * kHeadDim * 2);
+    L.bytes = off;
+    return L;
+}
+
+hipError_t launch_qgemv(QgArgs& q, hipStream_t s) {
+    const size_t lds = (size_t)q.T * q.K * 2;
+    hipLaunchKernelGGL(k_qgemv, dim3((q.nrows + 3) / 4), dim3(kAThreads), lds, s, q);
+    return hipGetLastError();
+}
+
+bool qm_ok(const vmi_qmat& m) {
+    return m.w && m.s && m.b && !(reinterpret_cast<uintptr_t>(m.w) & 15);
+}
+
+}  // namespace
+
+extern "C" int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int group, float* out,
+                         const uint16_t* residual, uint16_t* out_bf16, void* stream) {
+    vmi::clear_error();
+    if (T <= 0 || T > kQgMaxT) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, %d]", T, kQgMaxT);
+    if (K <= 0 || K % 64 || N <= 0) return vmi::fail(VMI_ERR_INVALID, "K=%d (multiple of 64) N=%d", K, N);
+    if ((size_t)T * K * 2 > 65536) return vmi::fail(VMI_ERR_UNSUPPORTED, "T*K=%d exceeds 32768", T * K);
+    if ((bits != 4 && bits != 8) || group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", bits, group);
+    if (!x || !qm_ok(w) || (!out && !out_bf16)) return vmi::fail(VMI_ERR_INVALID, "null x/weights/out");
+    if ((reinterpret_cast<uintptr_t>(x) & 15)) return vmi::fail(VMI_ERR_INVALID, "x must be 16-byte aligned");
+    QgArgs q{};
+    q.x = x; q.T = T; q.K = K; q.bits = bits;
+    q.m[0] = w; q.m[1] = w; q.m[2] = w;
+    q.rows[0] = N; q.rows[1] = 0; q.rows[2] = 0; q.nrows = N;
+    q.out = out; q.out_stride = N; q.residual = residual; q.out_bf16 = out_bf16;
+    const hipError_t e = launch_qgemv(q, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "k_qgemv launch");
+}
+
+extern "C" size_t vmi_attention_layer_workspace_bytes(int T, int hidden, int n_heads, int n_kv_heads) {
+    if (T <= 0 || hidden <= 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) return 0;
+    return attn_layout(T, hidden, n_heads, n_kv_heads).bytes;
+}
+
+extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int T, int pos0,
+                                   uint16_t* k_cache, uint16_t* v_cache, int max_len, uint16_t* out,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    vmi::clear_error();
+    if (!desc) return vmi::fail(VMI_ERR_INVALID, "null desc");
+    const vmi_attn_layer_desc& D = *desc;
+    if (T <= 0 || T > kQgMaxT) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, %d]", T, kQgMaxT);
+    if (D.head_dim != kHeadDim) return vmi::fail(VMI_ERR_UNSUPPORTED, "head_dim=%d (256 only)", D.head_dim);
+    if (D.n_heads <= 0 || D.n_kv_heads <= 0 || D.n_heads % D.n_kv_heads)
+        return vmi::fail(VMI_ERR_INVALID, "n_heads=%d n_kv_heads=%d", D.n_heads, D.n_kv_heads);
+    const int G = D.n_heads / D.n_kv_heads;
+    if (T * G > 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "T * heads per kv head = %d exceeds 64", T * G);
+    if (D.hidden % 512 || D.hidden > 4096) return vmi::fail(VMI_ERR_UNSUPPORTED, "hidden=%d", D.hidden);
+    if (D.n_heads * kHeadDim * T * 2 > 65536 || D.hidden * T * 2 > 65536)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "T too large for the projection GEMV");
+    if (D.rope_dim < 0 || D.rope_dim > kHeadDim || D.rope_dim % 2) return vmi::fail(VMI_ERR_INVALID, "rope_dim=%d", D.rope_dim);
+    if ((D.bits != 4 && D.bits != 8) || D.group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", D.bits, D.group);
+    if (pos0 < 0 || pos0 + T > max_len) return vmi::fail(VMI_ERR_INVALID, "pos0=%d T=%d max_len=%d", pos0, T, max_len);
+    if (!x || !out || !k_cache || !v_cache || !D.input_norm || !D.q_norm || !D.k_norm)
+        return vmi::fail(VMI_ERR_INVALID, "null x/out/cache/norm weights");
+    if (!qm_ok(D.q_proj) || !qm_ok(D.k_proj) || !qm_ok(D.v_proj) || !qm_ok(D.o_proj))
+        return vmi::fail(VMI_ERR_INVALID, "projection weights must be non-null and 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(k_cache) |
+         reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(D.input_norm)) & 15)
+        return vmi::fail(VMI_ERR_INVALID, "x, out, caches and norm weight must be 16-byte aligned");
+    const AttnLayout L = attn_layout(T, D.hidden, D.n_heads, D.n_kv_heads);
+    if (!workspace || workspace_bytes < L.bytes)
+        return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    uint16_t* xn = reinterpret_cast<uint16_t*>(ws + L.xn);
+    float* qkv = reinterpret_cast<float*>(ws + L.qkv);
+    uint16_t* qb = reinterpret_cast<uint16_t*>(ws + L.q);
+    uint16_t* ob = reinterpret_cast<uint16_t*>(ws + L.o);
+    const int stride = D.n_heads * 2 * kHeadDim + 2 * D.n_kv_heads * kHeadDim;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    RmsArgs ra{x, D.input_norm, D.norm_eps, T, D.hidden, xn};
+    hipLaunchKernelGGL(k_rms_rows, dim3((T + 3) / 4), dim3(kAThreads), 0, s, ra);
+
+    QgArgs q{};
+    q.x = xn; q.T = T; q.K = D.hidden; q.bits = D.bits;
+    q.m[0] = D.q_proj; q.m[1] = D.k_proj; q.m[2] = D.v_proj;
+    q.rows[0] = D.n_heads * 2 * kHeadDim; q.rows[1] = D.n_kv_heads * kHeadDim; q.rows[2] = D.n_kv_heads * kHeadDim;
+    q.nrows = stride; q.out = qkv; q.out_stride = stride;
+    hipError_t e = launch_qgemv(q, s);
+    if (e != hipSuccess) return vmi::hip_fail(e, "qkv projection launch");
+
+    RopeArgs rp{};
+    rp.qkv = qkv; rp.stride = stride; rp.T = T; rp.n_heads = D.n_heads; rp.n_kv = D.n_kv_heads;
+    rp.rope_dim = D.rope_dim; rp.pos0 = pos0; rp.max_len = max_len; rp.theta = D.rope_theta; rp.eps = D.norm_eps;
+    rp.q_norm = D.q_norm; rp.k_norm = D.k_norm; rp.q_out = qb; rp.k_cache = k_cache; rp.v_cache = v_cache;
+    hipLaunchKernelGGL(k_qk_rope, dim3((T * (D.n_heads + D.n_kv_heads) + 3) / 4), dim3(kAThreads), 0, s, rp);
+
+    AttnArgs at{};
+    at.q = qb; at.k_cache = k_cache; at.v_cache = v_cache;
+    at.T = T; at.n_heads = D.n_heads; at.n_kv = D.n_kv_heads; at.pos0 = pos0; at.max_len = max_len;
+    const int Lk = pos0 + T;
+    at.nchunks = attn_chunks(Lk);
+    at.chunk = ((Lk + at.nchunks - 1) / at.nchunks + kKeyStep - 1) / kKeyStep * kKeyStep;
+    at.part_o = reinterpret_cast<float*>(ws + L.part_o);
+    at.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
+    at.qkv = qkv; at.stride = stride; at.o = ob;
+    const int MS = (T * G + 15) / 16;
+    const dim3 ag(at.nchunks, D.n_kv_heads);
+    switch (MS) {
+        case 1: hipLaunchKernelGGL(k_attn_chunk<1>, ag, dim3(kAThreads), 0, s, at); break;
+        case 2: hipLaunchKernelGGL(k_attn_chunk<2>, ag, dim3(kAThreads), 0, s, at); break;
+        case 3: hipLaunchKernelGGL(k_attn_chunk<3>, ag, dim3(kAThreads), 0, s, at); break;
+        default: hipLaunchKernelGGL(k_attn_chunk<4>, ag, dim3(kAThreads), 0, s, at); break;
+    }
+    hipLaunchKernelGGL(k_attn_merge, dim3(T * D.n_heads), dim3(kAThreads), 0, s, at, 16 * MS);
+
+    QgArgs o{};
+    o.x = ob; o.T = T; o.K = D.n_heads * kHeadDim; o.bits = D.bits;
+    o.m[0] = D.o_proj; o.m[1] = D.o_proj; o.m[2] = D.o_proj;
+    o.rows[0] = D.hidden; o.rows[1] = 0; o.rows[2] = 0; o.nrows = D.hidden;
+    o.out = nullptr; o.out_stride = D.hidden; o.residual = x; o.out_bf16 = out;
+    e = launch_qgemv(o, s);
+    if (e != hipSuccess) return vmi::hip_fail(e, "o_proj launch");
+    return VMI_OK;
+}
