@@ -208,7 +208,10 @@ int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int 
  * sigmoid(gate) goes through o_proj and is added to x.
  * k_cache, v_cache: bf16 [n_kv_heads, max_len, head_dim].  head_dim 256;
  * T * n_heads / n_kv_heads <= 64; norm weights are the multipliers applied
- * (a checkpoint's zero-centred weights plus one).
+ * (a checkpoint's zero-centred weights plus one).  Keys are processed in
+ * chunks of 256 at fixed positions, so a token's result does not depend on
+ * the batch it is verified in.  workspace: vmi_attention_layer_workspace_bytes
+ * (T, hidden, n_heads, n_kv_heads, max_len) bytes.
  * ------------------------------------------------------------------------ */
 typedef struct vmi_attn_layer_desc {
     int hidden, n_heads, n_kv_heads, head_dim, rope_dim;
@@ -220,10 +223,34 @@ typedef struct vmi_attn_layer_desc {
     const uint16_t* k_norm;       /* [head_dim] */
 } vmi_attn_layer_desc;
 
-size_t vmi_attention_layer_workspace_bytes(int T, int hidden, int n_heads, int n_kv_heads);
+size_t vmi_attention_layer_workspace_bytes(int T, int hidden, int n_heads, int n_kv_heads, int max_len);
 int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int T, int pos0, uint16_t* k_cache,
                         uint16_t* v_cache, int max_len, uint16_t* out, void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/* ------------------------------------------------------------------------
+ * vmi_rmsnorm -- out = bf16(x * 1/sqrt(mean(x^2) + eps) * weight) per token
+ * (mlx RMSNorm as the MTP module applies it: pre_fc_norm_embedding,
+ * pre_fc_norm_hidden and norm, qwen3_next_mtp.py:27-31, 46-49, 54).  With ids
+ * (int32 [T]) the rows are gathered from the table x [rows, hidden] first -
+ * the embedding lookup embed_tokens(next_ids) of qwen3_next_mtp.py:46; an id
+ * outside [0, rows) reads row 0 and sets VMI_STATUS_BAD_SLOT in *status
+ * (may be NULL).  weight NULL: the rows are copied unnormalised (the main
+ * model's embedding lookup).  Output row t starts at out + t * out_stride
+ * (out_stride >= hidden: writes one half of a concatenation in place).
+ * hidden a multiple of 512; x, weight, out 16-byte aligned.
+ * ------------------------------------------------------------------------ */
+int vmi_rmsnorm(const uint16_t* x, const int32_t* ids, int rows, int T, int hidden, const uint16_t* weight, float eps,
+                uint16_t* out, int out_stride, uint32_t* status, void* stream);
+
+/* ------------------------------------------------------------------------
+ * vmi_topk_rows -- the k largest entries of each row of f32 logits
+ * [rows, vocab] in descending order (ties to the lower index, NaN last): the
+ * drafter's top-P first tokens of draft_paths (mlx_streaming/mtp/drafter.py:
+ * 150-160, mx.argsort(lg)[-P:][::-1]).  ids int32 [rows, k]; vals f32
+ * [rows, k] or NULL.  k <= 16.
+ * ------------------------------------------------------------------------ */
+int vmi_topk_rows(const float* logits, int rows, int vocab, int k, int32_t* ids, float* vals, void* stream);
 
 /* ------------------------------------------------------------------------
  * Acceptance.  Every entry point writes an int32 result record of 4 + K + 1

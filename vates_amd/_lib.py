@@ -74,9 +74,12 @@ _SIGNATURES = {
                                  c_size_t, c_void_p]),
     "vmi_qgemv": (c_int, [c_void_p, c_int, c_int, QMat, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
                           c_void_p]),
-    "vmi_attention_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "vmi_attention_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "vmi_attention_layer": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
                                     c_size_t, c_void_p]),
+    "vmi_rmsnorm": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p,
+                            c_void_p]),
+    "vmi_topk_rows": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "vmi_lm_head_workspace_bytes": (c_size_t, [c_int, c_int]),
     "vmi_lm_head": (c_int, [c_void_p, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p, c_void_p,
                             c_void_p, c_void_p, c_size_t, c_void_p]),

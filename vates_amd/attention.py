@@ -96,8 +96,8 @@ class AttentionLayer:
             out = torch.empty_like(x)
         sh = _stream_handle(stream)
         lib = load()
-        ws = workspace(lib.vmi_attention_layer_workspace_bytes(T, self.hidden, self.n_heads, self.n_kv), self.device,
-                       sh, tag="attention")
+        ws = workspace(lib.vmi_attention_layer_workspace_bytes(T, self.hidden, self.n_heads, self.n_kv, cache.max_len),
+                       self.device, sh, tag="attention")
         rc = lib.vmi_attention_layer(ctypes.byref(self.desc), x.data_ptr(), T, pos0, cache.k.data_ptr(),
                                      cache.v.data_ptr(), cache.max_len, out.data_ptr(), ws.data_ptr(), ws.numel(), sh)
         check(rc, "vmi_attention_layer")

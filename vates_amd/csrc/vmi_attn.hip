@@ -47,11 +47,15 @@ __device__ __forceinline__ void bf16x8f(const uint4& q, float (&v)[8]) {
 
 // ---------------------------------------------------------------- RMSNorm
 struct RmsArgs {
-    const uint16_t* x;   // [T, H]
+    const uint16_t* x;   // [T, H], or a table [rows, H] gathered through ids
     const uint16_t* w;   // [H]
     float eps;
     int T, H;
     uint16_t* out;       // [T, H]
+    const int32_t* ids;  // [T] row of x per token, or null
+    int rows;            // table rows (ids range)
+    uint32_t* status;    // optional: VMI_STATUS_BAD_SLOT for an id out of range
+    int out_stride;      // elements between output rows
 };
 
 // One wave per token; lane l owns H/64 contiguous values (H % 512 == 0).
@@ -60,13 +64,27 @@ __global__ __launch_bounds__(kAThreads) void k_rms_rows(RmsArgs a) {
     const int t = blockIdx.x * (kAThreads / 64) + at_wave();
     if (t >= a.T) return;
     const int cpl = a.H / 64, nv = cpl / 8;
-    const uint16_t* xr = a.x + (size_t)t * a.H + lane * cpl;
+    int row = t;
+    if (a.ids) {
+        row = a.ids[t];
+        if (row < 0 || row >= a.rows) {
+            if (lane == 0 && a.status) atomicOr(a.status, VMI_STATUS_BAD_SLOT);
+            row = 0;
+        }
+    }
+    const uint16_t* xr = a.x + (size_t)row * a.H + lane * cpl;
     float ss = 0.0f;
     for (int v = 0; v < nv; ++v) {
         float f[8];
         bf16x8f(*reinterpret_cast<const uint4*>(xr + 8 * v), f);
 #pragma unroll
         for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+    }
+    uint16_t* orow = a.out + (size_t)t * a.out_stride + lane * cpl;
+    if (!a.w) {  // plain gather
+        for (int v = 0; v < nv; ++v)
+            *reinterpret_cast<uint4*>(orow + 8 * v) = *reinterpret_cast<const uint4*>(xr + 8 * v);
+        return;
     }
     ss = vmi_wave_sum_canon(ss);
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)a.H) + a.eps));
@@ -79,7 +97,7 @@ __global__ __launch_bounds__(kAThreads) void k_rms_rows(RmsArgs a) {
         for (int i = 0; i < 4; ++i)
             o[i] = (uint32_t)vmi_f32_to_bf16((f[2 * i] * inv) * g[2 * i]) |
                    ((uint32_t)vmi_f32_to_bf16((f[2 * i + 1] * inv) * g[2 * i + 1]) << 16);
-        *reinterpret_cast<uint4*>(a.out + (size_t)t * a.H + lane * cpl + 8 * v) = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4*>(orow + 8 * v) = make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
 
@@ -428,16 +446,16 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
 }
 
 // ------------------------------------------------------------------ host
-int attn_chunks(int L) {
-    int nc = (L + 255) / 256;
-    return nc < 1 ? 1 : (nc > 128 ? 128 : nc);
-}
+// Keys are split into chunks of kChunkKeys at fixed absolute positions, so a
+// query's result does not depend on how many tokens share its batch.
+constexpr int kChunkKeys = 256;
+int attn_chunks(int L) { return (L + kChunkKeys - 1) / kChunkKeys; }
 
 struct AttnLayout {
     size_t xn, qkv, q, part_o, part_ml, o, bytes;
 };
 
-AttnLayout attn_layout(int T, int H, int n_heads, int n_kv) {
+AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len) {
     AttnLayout L{};
     size_t off = 0;
     auto take = [&](size_t b) {
@@ -450,8 +468,9 @@ AttnLayout attn_layout(int T, int H, int n_heads, int n_kv) {
     L.xn = take((size_t)T * H * 2);
     L.qkv = take((size_t)T * stride * 4);
     L.q = take((size_t)T * n_heads * kHeadDim * 2);
-    L.part_o = take((size_t)n_kv * 128 * RP * kHeadDim * 4);
-    L.part_ml = take((size_t)n_kv * 128 * RP * 2 * 4);
+    const int nc = attn_chunks(max_len);
+    L.part_o = take((size_t)n_kv * nc * RP * kHeadDim * 4);
+    L.part_ml = take((size_t)n_kv * nc * RP * 2 * 4);
     L.o = take((size_t)T * n_heads * kHeadDim * 2);
     L.bytes = off;
     return L;
@@ -487,9 +506,9 @@ extern "C" int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "k_qgemv launch");
 }
 
-extern "C" size_t vmi_attention_layer_workspace_bytes(int T, int hidden, int n_heads, int n_kv_heads) {
-    if (T <= 0 || hidden <= 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) return 0;
-    return attn_layout(T, hidden, n_heads, n_kv_heads).bytes;
+extern "C" size_t vmi_attention_layer_workspace_bytes(int T, int hidden, int n_heads, int n_kv_heads, int max_len) {
+    if (T <= 0 || hidden <= 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads || max_len <= 0) return 0;
+    return attn_layout(T, hidden, n_heads, n_kv_heads, max_len).bytes;
 }
 
 extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int T, int pos0,
@@ -517,7 +536,7 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(k_cache) |
          reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(D.input_norm)) & 15)
         return vmi::fail(VMI_ERR_INVALID, "x, out, caches and norm weight must be 16-byte aligned");
-    const AttnLayout L = attn_layout(T, D.hidden, D.n_heads, D.n_kv_heads);
+    const AttnLayout L = attn_layout(T, D.hidden, D.n_heads, D.n_kv_heads, max_len);
     if (!workspace || workspace_bytes < L.bytes)
         return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -528,7 +547,7 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     const int stride = D.n_heads * 2 * kHeadDim + 2 * D.n_kv_heads * kHeadDim;
     hipStream_t s = static_cast<hipStream_t>(stream);
 
-    RmsArgs ra{x, D.input_norm, D.norm_eps, T, D.hidden, xn};
+    RmsArgs ra{x, D.input_norm, D.norm_eps, T, D.hidden, xn, nullptr, 0, nullptr, D.hidden};
     hipLaunchKernelGGL(k_rms_rows, dim3((T + 3) / 4), dim3(kAThreads), 0, s, ra);
 
     QgArgs q{};
@@ -550,7 +569,7 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     at.T = T; at.n_heads = D.n_heads; at.n_kv = D.n_kv_heads; at.pos0 = pos0; at.max_len = max_len;
     const int Lk = pos0 + T;
     at.nchunks = attn_chunks(Lk);
-    at.chunk = ((Lk + at.nchunks - 1) / at.nchunks + kKeyStep - 1) / kKeyStep * kKeyStep;
+    at.chunk = kChunkKeys;
     at.part_o = reinterpret_cast<float*>(ws + L.part_o);
     at.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
     at.qkv = qkv; at.stride = stride; at.o = ob;
@@ -573,3 +592,19 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     if (e != hipSuccess) return vmi::hip_fail(e, "o_proj launch");
     return VMI_OK;
 }
+
+extern "C" int vmi_rmsnorm(const uint16_t* x, const int32_t* ids, int rows, int T, int hidden, const uint16_t* weight,
+                           float eps, uint16_t* out, int out_stride, uint32_t* status, void* stream) {
+    vmi::clear_error();
+    if (T <= 0 || hidden <= 0 || hidden % 512) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d hidden=%d", T, hidden);
+    if (!x || !out) return vmi::fail(VMI_ERR_INVALID, "null x/out");
+    if (ids && rows <= 0) return vmi::fail(VMI_ERR_INVALID, "rows=%d", rows);
+    if (out_stride < hidden || out_stride % 8) return vmi::fail(VMI_ERR_INVALID, "out_stride=%d", out_stride);
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(out)) & 15)
+        return vmi::fail(VMI_ERR_INVALID, "x, weight and out must be 16-byte aligned");
+    RmsArgs ra{x, weight, eps, T, hidden, out, ids, rows, status, out_stride};
+    hipLaunchKernelGGL(k_rms_rows, dim3((T + 3) / 4), dim3(kAThreads), 0, static_cast<hipStream_t>(stream), ra);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "k_rms_rows launch");
+}
+

@@ -249,6 +249,56 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
     if (threadIdx.x == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Top-k (k <= 16) of each row of f32 logits [rows, V]: one workgroup per row.
+// Every lane keeps its k best rank keys (value desc, lower index first, NaN
+// last) over a strided pass; k rounds of a workgroup-wide maximum (wave max,
+// then the 4 waves through LDS) pop the winners in order.
+struct TopkArgs {
+    const float* logits;
+    int V, k;
+    int32_t* ids;    // [rows, k]
+    float* vals;     // [rows, k] or null
+};
+
+__global__ __launch_bounds__(256) void k_topk_rows(TopkArgs a) {
+    __shared__ uint64_t s_w[4];
+    const int lane = threadIdx.x & 63, w = head_wave_id(), r = blockIdx.x;
+    const float* row = a.logits + (size_t)r * a.V;
+    uint64_t best[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) best[i] = 0ull;
+    for (int j = threadIdx.x; j < a.V; j += 256) {
+        uint64_t key = vmi_rank_key(row[j], j);
+        if (row[j] != row[j]) key = (uint64_t)(0xffffffffu - (uint32_t)j);  // NaN: below every number
+        // insert into the sorted (descending) list of length k
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (i < a.k && key > best[i]) {
+                const uint64_t t = best[i];
+                best[i] = key;
+                key = t;
+            }
+        }
+    }
+    for (int j = 0; j < a.k; ++j) {
+        const uint64_t m = vmi_wave_max_u64(best[0]);
+        if (lane == 0) s_w[w] = m;
+        __syncthreads();
+        const uint64_t M = vmi_u64_max(vmi_u64_max(s_w[0], s_w[1]), vmi_u64_max(s_w[2], s_w[3]));
+        __syncthreads();
+        if (best[0] == M) {
+#pragma unroll
+            for (int i = 0; i < 15; ++i) best[i] = best[i + 1];
+            best[15] = 0ull;
+        }
+        if (threadIdx.x == 0) {
+            const int idx = (int)(0xffffffffu - (uint32_t)M);
+            a.ids[r * a.k + j] = idx;
+            if (a.vals) a.vals[r * a.k + j] = row[idx];
+        }
+    }
+}
+
 int device_cus() {
     static int cached = 0;
     if (cached > 0) return cached;
@@ -307,3 +357,15 @@ extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t*
     if (e != hipSuccess) return vmi::hip_fail(e, "k_head launch");
     return VMI_OK;
 }
+
+extern "C" int vmi_topk_rows(const float* logits, int rows, int vocab, int k, int32_t* ids, float* vals, void* stream) {
+    vmi::clear_error();
+    if (rows <= 0 || vocab <= 0 || k <= 0 || k > 16 || k > vocab)
+        return vmi::fail(VMI_ERR_INVALID, "rows=%d vocab=%d k=%d (k <= 16)", rows, vocab, k);
+    if (!logits || !ids) return vmi::fail(VMI_ERR_INVALID, "null logits/ids");
+    TopkArgs a{logits, vocab, k, ids, vals};
+    hipLaunchKernelGGL(k_topk_rows, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "k_topk_rows launch");
+}
+

@@ -1,0 +1,124 @@
+"""MTP drafter on libvmi: the analogue of Qwen3NextMTP / mtp_step / MTPDrafter.
+
+* ``MTPLayer.step`` is ``mtp_step`` (mlx_streaming/mtp/qwen3_next_mtp.py:60-63)
+  over ``Qwen3NextMTP.__call__`` (:34-57): emb = norm_e(embed(token)),
+  hid = norm_h(hidden), x = fc([emb | hid]), x = layer(x) (full attention then
+  the routed MoE with its shared expert), H = norm(x), logits = lm_head(H).
+* ``MTPLayer.advance`` is ``mtp_advance`` (:66-73): the same without lm_head,
+  used to commit accepted positions to the MTP cache.
+* ``MTPDrafter`` mirrors ``MTPDrafter.draft`` / ``draft_paths`` / ``sync``
+  (mlx_streaming/mtp/drafter.py:20-40, 150-188).  Draft tokens stay on the
+  device: each step's argmax feeds the next step's embedding gather directly,
+  so drafting needs no host synchronisation (the reference synchronises once
+  per draft token, drafter.py:21-23).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+
+from ._lib import VmiError, check, load
+from .attention import AttentionLayer, KVCache, qgemv
+from .head import lm_head
+from .moe import MoELayer, QuantizedProj, _require, _stream_handle
+
+
+def rmsnorm(x: torch.Tensor, weight: Optional[torch.Tensor], *, eps: float = 1e-6, ids: Optional[torch.Tensor] = None,
+            out: Optional[torch.Tensor] = None, out_stride: Optional[int] = None, stream=None) -> torch.Tensor:
+    """bf16 RMSNorm per row (weight None: plain copy); with ids, rows are
+    gathered from the table x first (embedding lookup)."""
+    H = x.shape[-1]
+    T = ids.numel() if ids is not None else x.numel() // H
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
+    rc = load().vmi_rmsnorm(x.data_ptr(), None if ids is None else ids.data_ptr(),
+                            x.shape[0] if ids is not None else 0, T, H,
+                            None if weight is None else weight.data_ptr(), float(eps), out.data_ptr(),
+                            out_stride or H, None, _stream_handle(stream))
+    check(rc, "vmi_rmsnorm")
+    return out
+
+
+@dataclass
+class MTPWeights:
+    embed: torch.Tensor           # [V, H] bf16 (shared with the main model)
+    norm_emb: torch.Tensor        # [H] pre_fc_norm_embedding
+    norm_hid: torch.Tensor        # [H] pre_fc_norm_hidden
+    fc: QuantizedProj             # [1, H, 2H]
+    attn: AttentionLayer
+    moe: MoELayer                 # norm_weight = the layer's post-attention norm
+    norm: torch.Tensor            # [H] final MTP norm
+    lm_head: torch.Tensor         # [V, H] bf16 (the main model's head)
+    eps: float = 1e-6
+
+
+class MTPLayer:
+    def __init__(self, w: MTPWeights):
+        self.w = w
+        self.hidden = w.embed.shape[1]
+        self.vocab = w.embed.shape[0]
+
+    def _trunk(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None) -> torch.Tensor:
+        T, H = hidden.shape
+        cat = torch.empty((T, 2 * H), dtype=torch.bfloat16, device=hidden.device)
+        rmsnorm(self.w.embed, self.w.norm_emb, eps=self.w.eps, ids=tokens, out=cat, out_stride=2 * H, stream=stream)
+        rmsnorm(hidden, self.w.norm_hid, eps=self.w.eps, out=cat[:, H:], out_stride=2 * H, stream=stream)
+        x = torch.empty((T, H), dtype=torch.bfloat16, device=hidden.device)
+        qgemv(cat, self.w.fc, out_bf16=x, stream=stream)
+        x = self.w.attn(x, cache, stream=stream)
+        x = self.w.moe(x, residual=x, stream=stream)
+        return rmsnorm(x, self.w.norm, eps=self.w.eps, stream=stream)
+
+    def step(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, *, want_logits: bool = False,
+             stream=None):
+        """(argmax int32 [T], MTP hidden H bf16 [T, H], logits f32 [T, V] or None)."""
+        Hn = self._trunk(hidden, tokens, cache, stream)
+        logits, am, _ = lm_head(Hn, self.w.lm_head, None, want_logits=want_logits, stream=stream)
+        return am, Hn, logits
+
+    def advance(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None) -> torch.Tensor:
+        return self._trunk(hidden, tokens, cache, stream)
+
+
+class MTPDrafter:
+    def __init__(self, mtp: MTPLayer, max_len: int):
+        self.mtp = mtp
+        self.cache = mtp.w.attn.new_cache(max_len)
+
+    def draft(self, H_last: torch.Tensor, x_tok: torch.Tensor, K: int) -> torch.Tensor:
+        """K greedy drafts (int32 [K] on the device) from the main model's last
+        hidden [1, H] and the last emitted token [1]."""
+        drafts = torch.empty(K, dtype=torch.int32, device=H_last.device)
+        h, tok = H_last, x_tok
+        for i in range(K):
+            am, h, _ = self.mtp.step(h, tok, self.cache)
+            drafts[i:i + 1].copy_(am)
+            tok = drafts[i:i + 1]
+        return drafts
+
+    def draft_paths(self, H_last: torch.Tensor, x_tok: torch.Tensor, K: int, P: int) -> torch.Tensor:
+        """P paths [P, K]: the top-P first tokens (drafter.py:150-160), each
+        continued greedily from the shared position-1 state."""
+        paths = torch.empty((P, K), dtype=torch.int32, device=H_last.device)
+        am, h1, logits = self.mtp.step(H_last, x_tok, self.cache, want_logits=True)
+        firsts = torch.empty((1, P), dtype=torch.int32, device=H_last.device)
+        check(load().vmi_topk_rows(logits.data_ptr(), 1, logits.shape[1], P, firsts.data_ptr(), None,
+                                   _stream_handle(None)), "vmi_topk_rows")
+        base = self.cache.length
+        for p in range(P):
+            self.cache.length = base  # every path forks from the position-1 state
+            paths[p, 0:1].copy_(firsts[0, p:p + 1])
+            h, tok = h1, paths[p, 0:1]
+            for i in range(1, K):
+                am, h, _ = self.mtp.step(h, tok, self.cache)
+                paths[p, i:i + 1].copy_(am)
+                tok = paths[p, i:i + 1]
+        return paths
+
+    def sync(self, start: int, h_seq: torch.Tensor, tokens: torch.Tensor) -> None:
+        """Replaces the draft-time cache entries from `start` by the accepted
+        positions' (main hidden, token) pairs (drafter.py:178-188)."""
+        self.cache.length = start
+        self.mtp.advance(h_seq, tokens, self.cache)

@@ -103,3 +103,53 @@ def make_layer(w: LayerWeights, top_k: int = 10, norm_topk_prob: bool = True) ->
                     router_bits=w.router_bits, shared_gate=w.sh_gate, shared_up=w.sh_up, shared_down=w.sh_down,
                     shared_expert_gate=w.sgate, shared_expert_gate_bits=w.sgate_bits, slot_table=w.table,
                     router_logit_bias=w.bias, norm_weight=w.norm)
+
+
+def bf16_norm(seed: int, layer: int, n: int, device) -> torch.Tensor:
+    return torch.from_numpy(norm_weight(seed, layer, n).view(np.int16)).to(device).view(torch.bfloat16)
+
+
+def synth_attention(seed: int, layer: int, *, hidden: int = 2048, n_heads: int = 16, n_kv_heads: int = 2,
+                    std: float = 0.02, device=None):
+    """Qwen3-Next full-attention block: 4-bit q|gate, k, v, o projections, bf16 norms."""
+    from .attention import AttentionLayer
+    device = torch.device(device or "cuda")
+    base = layer * 16 + 8
+    q = synth_proj(seed, base, 1, n_heads * 512, hidden, std=std, device=device)
+    k = synth_proj(seed, base + 1, 1, n_kv_heads * 256, hidden, std=std, device=device)
+    v = synth_proj(seed, base + 2, 1, n_kv_heads * 256, hidden, std=std, device=device)
+    o = synth_proj(seed, base + 3, 1, hidden, n_heads * 256, std=std, device=device)
+    return AttentionLayer(q, k, v, o, bf16_norm(seed, 1000 + layer, hidden, device),
+                          bf16_norm(seed, 2000 + layer, 256, device), bf16_norm(seed, 3000 + layer, 256, device),
+                          n_heads=n_heads, n_kv_heads=n_kv_heads)
+
+
+def synth_spec_model(seed: int, *, n_layers: int = 4, attn_every: int = 4, hidden: int = 2048, inter: int = 512,
+                     num_experts: int = 512, top_k: int = 10, vocab: int = 151936, n_heads: int = 16,
+                     n_kv_heads: int = 2, zipf_alpha: float = 0.5, device=None):
+    """A random-init Qwen3-Next-shaped model for speculative decoding: bf16
+    embedding and head [vocab, hidden], n_layers decoder layers (a full-attention
+    block on every attn_every-th layer, as layer_types' interval pattern, then the
+    routed MoE with the shared expert), the final norm, and the MTP layer
+    (layer id 100: fc [hidden, 2 hidden], attention, MoE, norms)."""
+    from .decode import DecoderLayer, SpecModel
+    from .mtp import MTPLayer, MTPWeights
+    from .synth import synth_bf16
+    device = torch.device(device or "cuda")
+    embed = synth_bf16(seed, 0xE0000, (vocab, hidden), std=1.0, device=device)
+    head = synth_bf16(seed, 0xE0001, (vocab, hidden), std=0.02, device=device)
+    layers = []
+    for l in range(n_layers):
+        w = synth_layer(seed, l, hidden=hidden, inter=inter, num_experts=num_experts, zipf_alpha=zipf_alpha,
+                        device=device)
+        attn = synth_attention(seed, l, hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv_heads, device=device) \
+            if (l + 1) % attn_every == 0 else None
+        layers.append(DecoderLayer(make_layer(w, top_k=top_k), attn))
+    mw = synth_layer(seed, 100, hidden=hidden, inter=inter, num_experts=num_experts, zipf_alpha=zipf_alpha,
+                     device=device)
+    mtp = MTPLayer(MTPWeights(
+        embed=embed, norm_emb=bf16_norm(seed, 4000, hidden, device), norm_hid=bf16_norm(seed, 4001, hidden, device),
+        fc=synth_proj(seed, 100 * 16 + 15, 1, hidden, 2 * hidden, device=device),
+        attn=synth_attention(seed, 100, hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv_heads, device=device),
+        moe=make_layer(mw, top_k=top_k), norm=bf16_norm(seed, 4002, hidden, device), lm_head=head))
+    return SpecModel(embed, layers, bf16_norm(seed, 4003, hidden, device), head, mtp)
