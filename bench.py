@@ -141,6 +141,81 @@ def bench_lm_head(args) -> int:
     return 0
 
 
+def bench_decode(args) -> int:
+    """K-draft MTP speculative decoding of a random-init Qwen3-Next-shaped model:
+    `layers` decoder layers (full attention on every attn_every-th, the 512-expert
+    top-10 4-bit MoE with the shared expert on all), the MTP layer, bf16
+    embedding and head over 151,936 tokens.  The attention and MTP caches hold a
+    `context`-token synthetic prompt (random bf16 keys and values: decode speed
+    does not depend on their content).  Timed: `new_tokens` decoded tokens, wall
+    clock, including drafting, verification, acceptance, commit and the MTP
+    cache update.  Then the same start state is decoded greedily without
+    speculation and the two token streams are compared."""
+    import torch
+    from vates_amd.decode import greedy_decode, speculative_decode
+    from vates_amd.mtp import MTPDrafter
+    from vates_amd.synth import synth_bf16
+    from vates_amd.workload import synth_spec_model
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    model = synth_spec_model(SEED, n_layers=args.layers, attn_every=args.attn_every, hidden=args.hidden,
+                             inter=args.inter, num_experts=args.experts, top_k=args.top_k, vocab=args.vocab,
+                             device=dev)
+    ctx, N, K = args.context, args.new_tokens, args.K
+    max_len = ctx + N + 2 * K + 8
+    caches = model.new_caches(max_len)
+    drafter = MTPDrafter(model.mtp, max_len)
+    for i, c in enumerate(caches + [drafter.cache]):
+        if c is None:
+            continue
+        c.k[:, :ctx].copy_(synth_bf16(SEED, 0xCA000 + 2 * i, (c.k.shape[0], ctx, 256), device=dev))
+        c.v[:, :ctx].copy_(synth_bf16(SEED, 0xCA001 + 2 * i, (c.v.shape[0], ctx, 256), device=dev))
+    x0 = torch.tensor([4242], dtype=torch.int32, device=dev)
+    h0 = synth_bf16(SEED, 0xCA0FF, (1, args.hidden), device=dev)
+    torch.cuda.synchronize()
+    eprint(f"[bench] decode model resident: {torch.cuda.memory_allocated() / 2**30:.1f} GiB in {time.time() - t0:.1f} s")
+
+    def reset():
+        for c in caches:
+            if c is not None:
+                c.length = ctx
+        drafter.cache.length = ctx - 1
+
+    reset()
+    speculative_decode(model, drafter, caches, x0, h0, ctx, max(args.warmup, 1) * (K + 1), K=K)  # warm-up
+    reset()
+    torch.cuda.synchronize()
+    st = speculative_decode(model, drafter, caches, x0, h0, ctx, N, K=K)
+    torch.cuda.synchronize()
+    tps = N / st.seconds
+    eprint(f"[bench] decode: {N} tokens in {st.seconds:.3f} s = {tps:.1f} tokens/s, {st.steps} steps, "
+           f"avg accept len {st.avg_accept_len:.2f}")
+    reset()
+    gr = greedy_decode(model, caches, x0, ctx, N)
+    same = gr.tokens == st.tokens
+    first_diff = next((i for i, (a, b) in enumerate(zip(gr.tokens, st.tokens)) if a != b), None)
+    eprint(f"[bench] greedy (non-speculative): {N / gr.seconds:.1f} tokens/s; speculative == greedy: {same}")
+    hist = [st.accept_hist.count(m) for m in range(K + 1)]
+    line = {
+        "metric": "K=3 MTP decode tokens/s", "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": st.steps, "warmup": args.warmup, "ms_per_step": round(st.seconds * 1e3 / st.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u4 experts/projections, bf16 head and KV, f32 accumulate", "data": "synthetic",
+        "config": {"workload": f"{args.layers}-layer random-init Qwen3-Next-shaped model ({args.layers // args.attn_every}"
+                               f" full-attention layers, every layer MoE 512x top-{args.top_k} + shared expert, "
+                               f"linear-attention layers omitted), MTP K={K}, {N} new tokens after a {ctx}-token "
+                               f"synthetic context, vocab {args.vocab}",
+                   "accept_hist": hist, "avg_accept_len": round(st.avg_accept_len, 3),
+                   "speculative_equals_greedy": same, "first_divergence": first_diff,
+                   "greedy_tokens_per_s": round(N / gr.seconds, 2)},
+        "roofline": None, "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 PEAK_MFMA_TFLOPS = 2500.0  # dense fp16/bf16
 
 
@@ -238,9 +313,14 @@ def main() -> int:
     ap.add_argument("--experts", type=int, default=512)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-baseline-s", type=float, default=15.0)
-    ap.add_argument("--path", choices=["moe", "lm_head", "prefill"], default="moe",
+    ap.add_argument("--path", choices=["moe", "lm_head", "prefill", "decode"], default="moe",
                     help="moe: the 48-layer verify stack (default); lm_head: the vocabulary GEMV + argmax; "
-                         "prefill: one expert-major MoE layer on a T-token prompt")
+                         "prefill: one expert-major MoE layer on a T-token prompt; decode: K=3 MTP speculative "
+                         "decoding end to end")
+    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--new-tokens", type=int, default=512)
+    ap.add_argument("--K", type=int, default=3)
+    ap.add_argument("--attn-every", type=int, default=4)
     ap.add_argument("--vocab", type=int, default=151936)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -252,6 +332,8 @@ def main() -> int:
         return bench_lm_head(args)
     if args.path == "prefill":
         return bench_prefill(args)
+    if args.path == "decode":
+        return bench_decode(args)
 
     import torch
     from vates_amd.synth import synth_bf16
