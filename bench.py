@@ -170,8 +170,8 @@ def bench_decode(args) -> int:
     for i, c in enumerate(caches + [drafter.cache]):
         if c is None:
             continue
-        c.k[:, :ctx].copy_(synth_bf16(SEED, 0xCA000 + 2 * i, (c.k.shape[0], ctx, 256), device=dev))
-        c.v[:, :ctx].copy_(synth_bf16(SEED, 0xCA001 + 2 * i, (c.v.shape[0], ctx, 256), device=dev))
+        c.write(0, synth_bf16(SEED, 0xCA000 + 2 * i, (c.k.shape[0], ctx, 256), device=dev),
+                synth_bf16(SEED, 0xCA001 + 2 * i, (c.v.shape[0], ctx, 256), device=dev))
     x0 = torch.tensor([4242], dtype=torch.int32, device=dev)
     h0 = synth_bf16(SEED, 0xCA0FF, (1, args.hidden), device=dev)
     torch.cuda.synchronize()

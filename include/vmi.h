@@ -206,12 +206,20 @@ int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int 
  * caches at positions pos0 .. pos0+T-1; token t attends to cache positions
  * <= pos0 + t with softmax(q k / sqrt(head_dim)); the result times
  * sigmoid(gate) goes through o_proj and is added to x.
- * k_cache, v_cache: bf16 [n_kv_heads, max_len, head_dim].  head_dim 256;
+ * k_cache, v_cache: bf16, per kv head max_len / 32 blocks of 32 positions x
+ * head_dim (8192 elements), max_len a multiple of 32.  Inside a block,
+ * position kt and dim d are stored at
+ *   keys:   ((a*8 + (d>>5))*64 + ((d>>3)&3)*16 + nl)*8 + (d&7),
+ *           nl = 4*(kt>>3) + (kt&3), a = (kt>>2)&1
+ *   values: (((d>>4)*64 + (kt>>3)*16 + (d&15))*8 + (kt&7))
+ * (the operand order of the kernel's matrix instructions: every load is a
+ * contiguous 1 KB).  Positions >= pos0 + T are never used.  head_dim 256;
  * T * n_heads / n_kv_heads <= 64; norm weights are the multipliers applied
  * (a checkpoint's zero-centred weights plus one).  Keys are processed in
- * chunks of 256 at fixed positions, so a token's result does not depend on
- * the batch it is verified in.  workspace: vmi_attention_layer_workspace_bytes
- * (T, hidden, n_heads, n_kv_heads, max_len) bytes.
+ * chunks of 256 at fixed positions and merged in a fixed order, so a token's
+ * result does not depend on the batch it is verified in (bit for bit).
+ * workspace: vmi_attention_layer_workspace_bytes(T, hidden, n_heads,
+ * n_kv_heads, max_len) bytes.
  * ------------------------------------------------------------------------ */
 typedef struct vmi_attn_layer_desc {
     int hidden, n_heads, n_kv_heads, head_dim, rope_dim;

@@ -5,8 +5,10 @@ MTP layer runs it (mlx_streaming/mtp/qwen3_next_mtp.py:34-57, ``self.layer``)
 and as the main model's full-attention layers run it in the verify forward
 (mlx_streaming/mtp/generate.py:101-220): out = x + attn(rmsnorm(x)) with the KV
 cache updated in place.  ``KVCache`` holds one layer's bf16 keys and values
-[n_kv_heads, max_len, 256] and the number of committed positions, the analogue
-of mlx-lm's KVCache with its trim (mlx_streaming/mtp/kv_cache.py:222-251).
+and the number of committed positions, the analogue of mlx-lm's KVCache with
+its trim (mlx_streaming/mtp/kv_cache.py:222-251); its storage is blocks of 32
+positions in the attention kernel's operand order (``keys``/``values`` and
+``write`` convert from and to [n_kv_heads, positions, 256]).
 Errors raise ``VmiError``; there is no fallback path.
 """
 from __future__ import annotations
@@ -44,13 +46,39 @@ def qgemv(x: torch.Tensor, w: QuantizedProj, *, bits: int = 4, out: Optional[tor
     return out if out is not None else out_bf16
 
 
+KV_BLOCK = 32          # positions per cache block
+_PERM = {}
+
+
+def _block_perm(kind: str, device) -> torch.Tensor:
+    """Storage offset inside a block (8192 bf16) of (position kt, dim d), flattened
+    as kt * 256 + d: keys ((a*8 + kk)*64 + q4*16 + nl)*8 + e with
+    kt = 8*(nl>>2) + 4*a + (nl&3), d = 32*kk + 8*q4 + e; values
+    ((dt*64 + q4*16 + nl)*8 + e) with kt = 8*q4 + e, d = 16*dt + nl."""
+    key = (kind, str(device))
+    if key not in _PERM:
+        kt = torch.arange(KV_BLOCK).view(-1, 1)
+        d = torch.arange(256).view(1, -1)
+        if kind == "k":
+            nl, a = 4 * (kt >> 3) + (kt & 3), (kt >> 2) & 1
+            off = (((a * 8 + (d >> 5)) * 64 + ((d >> 3) & 3) * 16 + nl) << 3) + (d & 7)
+        else:
+            off = ((((d >> 4) * 64 + (kt >> 3) * 16 + (d & 15)) << 3) + (kt & 7))
+        _PERM[key] = off.reshape(-1).to(device)
+    return _PERM[key]
+
+
 class KVCache:
-    """bf16 keys and values of one attention layer, [n_kv_heads, max_len, 256]."""
+    """bf16 keys and values of one attention layer: k, v [n_kv_heads, blocks, 8192]
+    (32 positions per block, kernel operand order); capacity rounds up to 32."""
 
     def __init__(self, n_kv_heads: int, max_len: int, device, head_dim: int = 256):
-        self.k = torch.zeros((n_kv_heads, max_len, head_dim), dtype=torch.bfloat16, device=device)
+        if head_dim != 256:
+            raise VmiError(f"head_dim={head_dim} (256 only)")
+        self.max_len = -(-max_len // KV_BLOCK) * KV_BLOCK
+        nb = self.max_len // KV_BLOCK
+        self.k = torch.zeros((n_kv_heads, nb, KV_BLOCK * head_dim), dtype=torch.bfloat16, device=device)
         self.v = torch.zeros_like(self.k)
-        self.max_len = max_len
         self.length = 0  # committed positions
 
     def trim(self, n: int) -> None:
@@ -58,6 +86,32 @@ class KVCache:
         if n < 0 or n > self.length:
             raise VmiError(f"cannot trim {n} of {self.length} positions")
         self.length -= n
+
+    def _read(self, raw: torch.Tensor, kind: str, start: int, stop: int) -> torch.Tensor:
+        b0, b1 = start // KV_BLOCK, -(-stop // KV_BLOCK)
+        blk = raw[:, b0:b1]
+        logical = blk[:, :, _block_perm(kind, raw.device)].reshape(raw.shape[0], (b1 - b0) * KV_BLOCK, 256)
+        return logical[:, start - b0 * KV_BLOCK:stop - b0 * KV_BLOCK]
+
+    def keys(self, start: int = 0, stop: Optional[int] = None) -> torch.Tensor:
+        """Keys of positions start..stop-1 as [n_kv_heads, positions, 256] (a copy)."""
+        return self._read(self.k, "k", start, self.length if stop is None else stop)
+
+    def values(self, start: int = 0, stop: Optional[int] = None) -> torch.Tensor:
+        return self._read(self.v, "v", start, self.length if stop is None else stop)
+
+    def write(self, start: int, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Stores [n_kv_heads, n, 256] keys and values at positions start..start+n-1."""
+        n = keys.shape[1]
+        if start < 0 or start + n > self.max_len:
+            raise VmiError(f"positions {start}..{start + n} outside the capacity {self.max_len}")
+        b0, b1 = start // KV_BLOCK, -(-(start + n) // KV_BLOCK)
+        for raw, kind, data in ((self.k, "k", keys), (self.v, "v", values)):
+            logical = self._read(raw, kind, b0 * KV_BLOCK, b1 * KV_BLOCK).clone()
+            logical[:, start - b0 * KV_BLOCK:start - b0 * KV_BLOCK + n] = data
+            blk = torch.empty_like(raw[:, b0:b1])
+            blk[:, :, _block_perm(kind, raw.device)] = logical.reshape(raw.shape[0], b1 - b0, -1)
+            raw[:, b0:b1] = blk
 
 
 class AttentionLayer:

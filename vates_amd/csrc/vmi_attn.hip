@@ -18,11 +18,24 @@
 //                  lane per step, tokens staged in LDS, fp32 accumulation
 //   k_qk_rope      per (token, head): q/k RMSNorm, rotary, q as bf16, k and v
 //                  appended to the bf16 KV cache at the token's position
-//   k_attn_chunk   per (kv head, key chunk): scores and P.V for the 8T query
-//                  rows of the head group with bf16 MFMAs, online softmax
-//                  over 64-key steps; writes the chunk's (max, sum, O)
-//   k_attn_merge   per (token, head): merges the chunks, times sigmoid(gate),
-//                  bf16 input of o_proj
+//   k_attn_chunk   per (kv head, chunk of 256 keys), 8 waves: wave w scores
+//                  the chunk's 32-key block w against the head group's query
+//                  rows (S^T = K Q^T), the chunk max and the bf16
+//                  probabilities go through LDS, then wave w forms P V for
+//                  dims 32w..32w+31 over all 256 keys; writes (max, sum, O)
+//   k_attn_merge   per (token, head, quarter of the dims): merges the chunks
+//                  in a fixed order, times sigmoid(gate), bf16 input of o_proj
+//
+// KV cache layout: per kv head, blocks of 32 positions x 256 dims (8192 bf16,
+// 16 KB), each stored in the operand order of the MFMA that reads it, so every
+// load of the attention kernel is a contiguous 1 KB per wave:
+//   keys   element ((a*8 + kk)*64 + q4*16 + nl)*8 + e holds position
+//          kt = 8*(nl>>2) + 4*a + (nl&3) of the block, dim 32*kk + 8*q4 + e
+//          (the A operand of S^T = K Q^T: result row 4*q4 + r of tile a is
+//          then key 8*q4 + 4*a + r, so a lane's 8 scores are 8 consecutive
+//          keys, already the A operand of P V);
+//   values element ((dt*64 + q4*16 + nl)*8 + e) holds position 8*q4 + e,
+//          dim 16*dt + nl (the B operand of P V).
 
 #include "vmi_device.h"
 #include "vmi_internal.h"
@@ -32,7 +45,6 @@ namespace {
 constexpr int kAThreads = 256;
 constexpr int kQgMaxT = 8;
 constexpr int kHeadDim = 256;
-constexpr int kKeyStep = 64;       // keys per MFMA step inside a chunk
 
 __device__ __forceinline__ int at_wave() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
@@ -186,6 +198,21 @@ __global__ __launch_bounds__(kAThreads) void k_qgemv(QgArgs a) {
 }
 
 // ------------------------------------------------------- q/k norm, rotary
+// ------------------------------------------------------------ KV cache
+constexpr int kKvBlock = 32;                      // positions per cache block
+constexpr int kKvBlockElems = kKvBlock * kHeadDim;
+
+__device__ __forceinline__ size_t kv_block(int g, int max_len, int pos) {
+    return ((size_t)g * (max_len / kKvBlock) + pos / kKvBlock) * kKvBlockElems;
+}
+__device__ __forceinline__ int k_elem(int kt, int d) {
+    const int nl = 4 * (kt >> 3) + (kt & 3), a = (kt >> 2) & 1;
+    return (((a * 8 + (d >> 5)) * 64 + ((d >> 3) & 3) * 16 + nl) << 3) + (d & 7);
+}
+__device__ __forceinline__ int v_elem(int kt, int d) {
+    return ((((d >> 4) * 64 + (kt >> 3) * 16 + (d & 15)) << 3) + (kt & 7));
+}
+
 struct RopeArgs {
     const float* qkv;        // [T, stride]: q|gate per head (n_heads * 2 * 256), then k (n_kv * 256), then v
     int stride;
@@ -255,14 +282,15 @@ __global__ __launch_bounds__(kAThreads) void k_qk_rope(RopeArgs a) {
         for (int j = 0; j < 4; ++j) qo[lane + 64 * j] = o[j];
     } else {
         const int g = h - a.n_heads;
-        uint16_t* kc = a.k_cache + ((size_t)g * a.max_len + pos) * kHeadDim;
-        uint16_t* vc = a.v_cache + ((size_t)g * a.max_len + pos) * kHeadDim;
+        const size_t blk = kv_block(g, a.max_len, pos);
+        const int kt = pos % kKvBlock;
         const float* vsrc = a.qkv + (size_t)t * a.stride + (size_t)a.n_heads * 2 * kHeadDim +
                             (size_t)a.n_kv * kHeadDim + (size_t)g * kHeadDim;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            kc[lane + 64 * j] = o[j];
-            vc[lane + 64 * j] = vmi_f32_to_bf16(vsrc[lane + 64 * j]);
+            const int d = lane + 64 * j;
+            a.k_cache[blk + k_elem(kt, d)] = o[j];
+            a.v_cache[blk + v_elem(kt, d)] = vmi_f32_to_bf16(vsrc[d]);
         }
     }
 }
@@ -270,11 +298,10 @@ __global__ __launch_bounds__(kAThreads) void k_qk_rope(RopeArgs a) {
 // -------------------------------------------------------------- attention
 struct AttnArgs {
     const uint16_t* q;        // [T, n_heads, 256] bf16
-    const uint16_t* k_cache;  // [n_kv, max_len, 256]
+    const uint16_t* k_cache;  // blocks of 32 positions, see the layout above
     const uint16_t* v_cache;
     int T, n_heads, n_kv, pos0, max_len;
-    int chunk;                // keys per workgroup (multiple of 64)
-    int nchunks;
+    int nchunks;              // chunks of kChunkKeys positions
     float* part_o;            // [n_kv, nchunks, RP, 256]
     float* part_ml;           // [n_kv, nchunks, RP, 2]
     const float* qkv;         // for the gate in the merge
@@ -282,27 +309,64 @@ struct AttnArgs {
     uint16_t* o;              // [T, n_heads * 256] bf16 gated attention output
 };
 
-// Rows of a head group: r = t * G + hl (G = n_heads / n_kv query heads per kv
-// head), RP = R rounded up to 16.  One workgroup: 4 waves, 64 keys per step.
-// Scores: wave w takes keys 16w..16w+15 of the step for every row subtile;
-// P.V: wave w takes dims 64w..64w+63.  Online softmax across steps.
-template <int MS>  // row subtiles of 16 (RP = 16 MS)
-__global__ __launch_bounds__(kAThreads) void k_attn_chunk(AttnArgs a) {
+constexpr int kChunkWaves = 8;                         // one cache block per wave
+constexpr int kChunkThreads = 64 * kChunkWaves;
+constexpr int kChunkKeys = kChunkWaves * kKvBlock;     // 256
+
+__device__ __forceinline__ vmi_u4 keep_first(vmi_u4 v, int n) {  // zero bf16 elements e >= n
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        v[i] &= (2 * i < n ? 0x0000ffffu : 0u) | (2 * i + 1 < n ? 0xffff0000u : 0u);
+    return v;
+}
+
+// Rows of a head group: row = t * G + hl (G = n_heads / n_kv query heads per
+// kv head), RP = 16 MS >= T * G.  Every load is issued before the first
+// MFMA: keys of the wave's block (16 x 1 KB) and values of all 8 blocks for
+// the wave's 32 dims (16 x 1 KB).  Positions >= pos0 + T are not read past
+// their block; inside the last block they are masked (scores -inf, values
+// zeroed), so stale cache contents never reach the result.
+template <int MS>
+__global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     constexpr int RP = 16 * MS;
     __shared__ __attribute__((aligned(16))) uint16_t s_q[RP][kHeadDim + 8];
-    __shared__ __attribute__((aligned(16))) uint16_t s_vt[kHeadDim][kKeyStep + 8];
-    __shared__ __attribute__((aligned(16))) uint16_t s_p[RP][kKeyStep + 8];
-    __shared__ float s_s[RP][kKeyStep + 1];
-    __shared__ float s_m[RP], s_l[RP], s_scale[RP];
-    const int g = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
-    const int lane = tid & 63, w = at_wave();
-    const int nl = lane & 15, q4 = lane >> 4;
-    const int G = a.n_heads / a.n_kv;
-    const int R = a.T * G;
-    const int L = a.pos0 + a.T;  // keys present
-    const int k0 = c * a.chunk, k1 = min(L, k0 + a.chunk);
-    // queries of this head group
-    for (int i = tid; i < RP * (kHeadDim / 8); i += kAThreads) {
+    __shared__ vmi_u4 s_pa[MS][kChunkWaves][64];
+    __shared__ float s_wm[kChunkWaves][RP], s_wl[kChunkWaves][RP];
+    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, w = at_wave(), nl = lane & 15, q4 = lane >> 4;
+    const int G = a.n_heads / a.n_kv, R = a.T * G;
+    const int L = a.pos0 + a.T;                        // positions present
+    const int b0 = c * kChunkWaves;
+    const uint16_t* kb = a.k_cache + kv_block(g, a.max_len, 0);
+    const uint16_t* vb = a.v_cache + kv_block(g, a.max_len, 0);
+
+    vmi_u4 kr[2][8], vr[2][kChunkWaves];
+    const int bw = b0 + w;
+    if (kKvBlock * bw < L) {
+        const vmi_u4* src = reinterpret_cast<const vmi_u4*>(kb + (size_t)bw * kKvBlockElems) + lane;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) kr[h][kk] = src[(h * 8 + kk) * 64];
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) kr[h][kk] = vmi_u4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int sb = 0; sb < kChunkWaves; ++sb) {
+        const int bs = b0 + sb;
+        if (kKvBlock * bs < L) {
+            const vmi_u4* src = reinterpret_cast<const vmi_u4*>(vb + (size_t)bs * kKvBlockElems) + lane;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt) vr[dt][sb] = src[(2 * w + dt) * 64];
+        } else {
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt) vr[dt][sb] = vmi_u4{0u, 0u, 0u, 0u};
+        }
+    }
+    for (int i = tid; i < RP * (kHeadDim / 8); i += kChunkThreads) {
         const int row = i / (kHeadDim / 8), d8 = i % (kHeadDim / 8);
         uint4 v = make_uint4(0, 0, 0, 0);
         if (row < R) {
@@ -311,144 +375,176 @@ __global__ __launch_bounds__(kAThreads) void k_attn_chunk(AttnArgs a) {
         }
         *reinterpret_cast<uint4*>(&s_q[row][8 * d8]) = v;
     }
-    if (tid < RP) {
-        s_m[tid] = -INFINITY;
-        s_l[tid] = 0.0f;
-    }
-    vmi_f4 oacc[MS][4];
+    // the last block: values of positions >= L are zeroed (0 * stale could be NaN)
 #pragma unroll
-    for (int m = 0; m < MS; ++m)
+    for (int sb = 0; sb < kChunkWaves; ++sb) {
+        const int p0 = kKvBlock * (b0 + sb);
+        if (p0 < L && p0 + kKvBlock > L) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) oacc[m][s] = vmi_f4{0.f, 0.f, 0.f, 0.f};
-    const uint16_t* kc = a.k_cache + (size_t)g * a.max_len * kHeadDim;
-    const uint16_t* vc = a.v_cache + (size_t)g * a.max_len * kHeadDim;
-    __syncthreads();
-    for (int j0 = k0; j0 < k1; j0 += kKeyStep) {
-        // V of this step into LDS, transposed: s_vt[dim][key]
-        for (int i = tid; i < kKeyStep * (kHeadDim / 8); i += kAThreads) {
-            const int key = i / (kHeadDim / 8), d8 = i % (kHeadDim / 8);
-            const int kk = j0 + key;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (kk < k1) v = *reinterpret_cast<const uint4*>(vc + (size_t)kk * kHeadDim + 8 * d8);
-            const uint32_t ww[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) s_vt[8 * d8 + e][key] = (uint16_t)(ww[e >> 1] >> (16 * (e & 1)));
+            for (int dt = 0; dt < 2; ++dt) vr[dt][sb] = keep_first(vr[dt][sb], L - p0 - 8 * q4);
         }
-        // scores: B = K^T, lane's key j0 + 16w + nl, dims 32kk + 8q4
-        const int key = j0 + 16 * w + nl;
-        const bool kok = key < k1;
-        vmi_u4 kb[8];
+    }
+    __syncthreads();
+
+    // scores: lane (nl, q4) of tile h holds keys 8 q4 + 4 h + r of block bw for query row 16 m + nl
+    float sc[MS][8];
+#pragma unroll
+    for (int m = 0; m < MS; ++m) {
+        vmi_f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
-            kb[kk] = vmi_u4{0u, 0u, 0u, 0u};
-            if (kok) {
-                const uint4 v = *reinterpret_cast<const uint4*>(kc + (size_t)key * kHeadDim + 32 * kk + 8 * q4);
-                kb[kk] = vmi_u4{v.x, v.y, v.z, v.w};
-            }
+            const uint4 qv = *reinterpret_cast<const uint4*>(&s_q[16 * m + nl][32 * kk + 8 * q4]);
+            const vmi_u4 qb = {qv.x, qv.y, qv.z, qv.w};
+            acc0 = vmi_mfma_bf16(kr[0][kk], qb, acc0);
+            acc1 = vmi_mfma_bf16(kr[1][kk], qb, acc1);
         }
+        const int row = 16 * m + nl;
+        const int last = row < R ? min(L - 1, a.pos0 + row / G) : -1;  // last visible position
+        const int p = kKvBlock * bw + 8 * q4;
 #pragma unroll
-        for (int m = 0; m < MS; ++m) {
-            vmi_f4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const uint4 av = *reinterpret_cast<const uint4*>(&s_q[16 * m + nl][32 * kk + 8 * q4]);
-                sacc = vmi_mfma_bf16(vmi_u4{av.x, av.y, av.z, av.w}, kb[kk], sacc);
-            }
-            // D rows 16m + 4q4 + r (query rows), column nl (key 16w + nl)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 16 * m + 4 * q4 + r;
-                float sv = sacc[r] * 0.0625f;  // 1 / sqrt(256)
-                const int t = row / G;
-                const bool ok = kok && row < R && key <= a.pos0 + t;
-                s_s[row][16 * w + nl] = ok ? sv : -INFINITY;
-            }
+        for (int r = 0; r < 4; ++r) {
+            sc[m][r] = p + r <= last ? acc0[r] * 0.0625f : -INFINITY;  // 1 / sqrt(256)
+            sc[m][4 + r] = p + 4 + r <= last ? acc1[r] * 0.0625f : -INFINITY;
         }
-        __syncthreads();
-        // online softmax per row: thread per row
-        if (tid < RP) {
-            const int row = tid;
-            float mx = s_m[row];
-            for (int j = 0; j < kKeyStep; ++j) mx = fmaxf(mx, s_s[row][j]);
-            const float scale = mx == -INFINITY ? 1.0f : expf(s_m[row] - mx);
-            float l = s_l[row] * scale;
-            for (int j = 0; j < kKeyStep; ++j) {
-                const float p = mx == -INFINITY ? 0.0f : expf(s_s[row][j] - mx);
-                const uint16_t pb = vmi_f32_to_bf16(p);
-                s_p[row][j] = pb;
-                l += vmi_bf16_to_f32(pb);
-            }
-            s_m[row] = mx;
-            s_l[row] = l;
-            s_scale[row] = scale;
-        }
-        __syncthreads();
-        // O = O * scale + P V: wave w dims 64w + 16s + nl; A = P rows, K = 64 keys
+        float mx = sc[m][0];
 #pragma unroll
-        for (int m = 0; m < MS; ++m) {
-            float sc[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sc[r] = s_scale[16 * m + 4 * q4 + r];
-            vmi_u4 pa[2];
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const uint4 av = *reinterpret_cast<const uint4*>(&s_p[16 * m + nl][32 * kk + 8 * q4]);
-                pa[kk] = vmi_u4{av.x, av.y, av.z, av.w};
-            }
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int d = 64 * w + 16 * s + nl;
-                vmi_f4 acc = oacc[m][s];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[r] *= sc[r];
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const uint4 bv = *reinterpret_cast<const uint4*>(&s_vt[d][32 * kk + 8 * q4]);
-                    acc = vmi_mfma_bf16(pa[kk], vmi_u4{bv.x, bv.y, bv.z, bv.w}, acc);
-                }
-                oacc[m][s] = acc;
-            }
-        }
-        __syncthreads();
+        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[m][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if (q4 == 0) s_wm[w][row] = mx;
     }
-    // partials: D rows 16m + 4q4 + r, dims 64w + 16s + nl
-    float* po = a.part_o + ((size_t)g * a.nchunks + c) * RP * kHeadDim;
+    __syncthreads();
+    // probabilities against the chunk max, rounded to bf16 (the P.V operand);
+    // the row sum adds the rounded values
 #pragma unroll
-    for (int m = 0; m < MS; ++m)
+    for (int m = 0; m < MS; ++m) {
+        const int row = 16 * m + nl;
+        float M = s_wm[0][row];
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int v = 1; v < kChunkWaves; ++v) M = fmaxf(M, s_wm[v][row]);
+        float ls = 0.0f;
+        vmi_u4 pk;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) po[(size_t)(16 * m + 4 * q4 + r) * kHeadDim + 64 * w + 16 * s + nl] = oacc[m][s][r];
+        for (int i = 0; i < 4; ++i) {
+            const float x0 = sc[m][2 * i], x1 = sc[m][2 * i + 1];
+            const uint32_t u0 = x0 == -INFINITY ? 0u : vmi_f32_to_bf16(expf(x0 - M));
+            const uint32_t u1 = x1 == -INFINITY ? 0u : vmi_f32_to_bf16(expf(x1 - M));
+            ls += vmi_bf16_to_f32(u0);
+            ls += vmi_bf16_to_f32(u1);
+            pk[i] = u0 | (u1 << 16);
+        }
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        if (q4 == 0) s_wl[w][row] = ls;
+        s_pa[m][w][lane] = pk;
+    }
+    __syncthreads();
+    // O = P V for dims 32 w + 16 dt + nl; A = P of block sb (written by wave sb)
+    const size_t pbase = ((size_t)g * a.nchunks + c) * RP;
+#pragma unroll
+    for (int m = 0; m < MS; ++m) {
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+            vmi_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sb = 0; sb < kChunkWaves; ++sb) acc = vmi_mfma_bf16(s_pa[m][sb][lane], vr[dt][sb], acc);
+            float* po = a.part_o + (pbase + 16 * m + 4 * q4) * kHeadDim + 32 * w + 16 * dt + nl;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) po[r * kHeadDim] = acc[r];
+        }
+    }
     if (tid < RP) {
-        float* pml = a.part_ml + (((size_t)g * a.nchunks + c) * RP + tid) * 2;
-        pml[0] = s_m[tid];
-        pml[1] = s_l[tid];
+        float M = s_wm[0][tid], l = s_wl[0][tid];
+#pragma unroll
+        for (int v = 1; v < kChunkWaves; ++v) {
+            M = fmaxf(M, s_wm[v][tid]);
+            l += s_wl[v][tid];
+        }
+        *reinterpret_cast<float2*>(a.part_ml + (pbase + tid) * 2) = make_float2(M, l);
     }
 }
 
-// One workgroup per (token, head): 256 threads = the head's dims.
+// grid (T * n_heads, 4): one quarter of a head's dims per workgroup.  Chunk c
+// is added by slot c % 16 in increasing c and the 16 slots are combined in a
+// fixed tree, so the result does not depend on how many chunks a launch has:
+// chunks past a query's last position carry weight exactly zero.
+constexpr int kMergeMaxChunks = 2048;
 __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
-    const int t = blockIdx.x / a.n_heads, h = blockIdx.x % a.n_heads, d = threadIdx.x;
+    __shared__ float s_f[kMergeMaxChunks];
+    __shared__ float s_red[kAThreads / 64];
+    __shared__ float4 s_num[kAThreads / 64][16];
+    const int t = blockIdx.x / a.n_heads, h = blockIdx.x % a.n_heads, tid = threadIdx.x;
+    const int lane = tid & 63, w = at_wave();
     const int G = a.n_heads / a.n_kv, g = h / G, row = t * G + (h % G);
+    const int NC = a.nchunks;
+    const size_t cstride = (size_t)RP;                               // rows between chunks
+    const float* ml = a.part_ml + ((size_t)g * NC * RP + row) * 2;   // chunk c at + c * RP * 2
     float M = -INFINITY;
-    for (int c = 0; c < a.nchunks; ++c) M = fmaxf(M, a.part_ml[(((size_t)g * a.nchunks + c) * RP + row) * 2]);
-    float num = 0.0f, den = 0.0f;
-    for (int c = 0; c < a.nchunks; ++c) {
-        const float* ml = a.part_ml + (((size_t)g * a.nchunks + c) * RP + row) * 2;
-        if (ml[0] == -INFINITY) continue;
-        const float f = expf(ml[0] - M);
-        den = fmaf(ml[1], f, den);
-        num = fmaf(a.part_o[(((size_t)g * a.nchunks + c) * RP + row) * kHeadDim + d], f, num);
+    for (int c = tid; c < NC; c += kAThreads) M = fmaxf(M, ml[c * cstride * 2]);
+    M = vmi_wave_max(M);
+    if (lane == 0) s_red[w] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float den = 0.0f;
+    for (int c = tid; c < NC; c += kAThreads) {
+        const float m = ml[c * cstride * 2];
+        const float f = m == -INFINITY ? 0.0f : expf(m - M);
+        s_f[c] = f;
+        den = fmaf(ml[c * cstride * 2 + 1], f, den);
     }
-    const float gate = a.qkv[(size_t)t * a.stride + (size_t)h * 2 * kHeadDim + kHeadDim + d];
-    const float y = (den > 0.0f ? num / den : 0.0f) / (1.0f + expf(-gate));
-    a.o[((size_t)t * a.n_heads + h) * kHeadDim + d] = vmi_f32_to_bf16(y);
+    den = vmi_wave_sum_canon(den);
+    __syncthreads();
+    if (lane == 0) s_red[w] = den;
+    __syncthreads();
+    den = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+
+    const int slot = 4 * w + (lane >> 4), d0 = 64 * blockIdx.y + 4 * (lane & 15);
+    const float* po = a.part_o + ((size_t)g * NC * RP + row) * kHeadDim + d0;  // chunk c at + c * RP * 256
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c0 = slot; c0 < NC; c0 += 16 * 8) {
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = c0 + 16 * i;
+            v[i] = c < NC ? *reinterpret_cast<const float4*>(po + c * cstride * kHeadDim) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = c0 + 16 * i;
+            if (c < NC) {
+                const float f = s_f[c];
+                acc.x = fmaf(v[i].x, f, acc.x);
+                acc.y = fmaf(v[i].y, f, acc.y);
+                acc.z = fmaf(v[i].z, f, acc.z);
+                acc.w = fmaf(v[i].w, f, acc.w);
+            }
+        }
+    }
+    acc.x += __shfl_xor(acc.x, 16); acc.y += __shfl_xor(acc.y, 16);
+    acc.z += __shfl_xor(acc.z, 16); acc.w += __shfl_xor(acc.w, 16);
+    acc.x += __shfl_xor(acc.x, 32); acc.y += __shfl_xor(acc.y, 32);
+    acc.z += __shfl_xor(acc.z, 32); acc.w += __shfl_xor(acc.w, 32);
+    if (lane < 16) s_num[w][lane] = acc;
+    __syncthreads();
+    if (tid < 16) {
+        const float4 n0 = s_num[0][tid], n1 = s_num[1][tid], n2 = s_num[2][tid], n3 = s_num[3][tid];
+        const float n[4] = {(n0.x + n1.x) + (n2.x + n3.x), (n0.y + n1.y) + (n2.y + n3.y),
+                            (n0.z + n1.z) + (n2.z + n3.z), (n0.w + n1.w) + (n2.w + n3.w)};
+        const float* gp = a.qkv + (size_t)t * a.stride + (size_t)h * 2 * kHeadDim + kHeadDim + d0;
+        uint32_t out[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float y0 = (den > 0.0f ? n[2 * i] / den : 0.0f) / (1.0f + expf(-gp[2 * i]));
+            const float y1 = (den > 0.0f ? n[2 * i + 1] / den : 0.0f) / (1.0f + expf(-gp[2 * i + 1]));
+            out[i] = (uint32_t)vmi_f32_to_bf16(y0) | ((uint32_t)vmi_f32_to_bf16(y1) << 16);
+        }
+        *reinterpret_cast<uint2*>(a.o + ((size_t)t * a.n_heads + h) * kHeadDim + d0) = make_uint2(out[0], out[1]);
+    }
 }
 
 // ------------------------------------------------------------------ host
 // Keys are split into chunks of kChunkKeys at fixed absolute positions, so a
 // query's result does not depend on how many tokens share its batch.
-constexpr int kChunkKeys = 256;
 int attn_chunks(int L) { return (L + kChunkKeys - 1) / kChunkKeys; }
 
 struct AttnLayout {
@@ -529,6 +625,9 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     if (D.rope_dim < 0 || D.rope_dim > kHeadDim || D.rope_dim % 2) return vmi::fail(VMI_ERR_INVALID, "rope_dim=%d", D.rope_dim);
     if ((D.bits != 4 && D.bits != 8) || D.group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", D.bits, D.group);
     if (pos0 < 0 || pos0 + T > max_len) return vmi::fail(VMI_ERR_INVALID, "pos0=%d T=%d max_len=%d", pos0, T, max_len);
+    if (max_len % kKvBlock) return vmi::fail(VMI_ERR_INVALID, "max_len=%d must be a multiple of %d", max_len, kKvBlock);
+    if (attn_chunks(max_len) > kMergeMaxChunks)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "max_len=%d exceeds %d", max_len, kMergeMaxChunks * kChunkKeys);
     if (!x || !out || !k_cache || !v_cache || !D.input_norm || !D.q_norm || !D.k_norm)
         return vmi::fail(VMI_ERR_INVALID, "null x/out/cache/norm weights");
     if (!qm_ok(D.q_proj) || !qm_ok(D.k_proj) || !qm_ok(D.v_proj) || !qm_ok(D.o_proj))
@@ -569,19 +668,18 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     at.T = T; at.n_heads = D.n_heads; at.n_kv = D.n_kv_heads; at.pos0 = pos0; at.max_len = max_len;
     const int Lk = pos0 + T;
     at.nchunks = attn_chunks(Lk);
-    at.chunk = kChunkKeys;
     at.part_o = reinterpret_cast<float*>(ws + L.part_o);
     at.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
     at.qkv = qkv; at.stride = stride; at.o = ob;
     const int MS = (T * G + 15) / 16;
     const dim3 ag(at.nchunks, D.n_kv_heads);
     switch (MS) {
-        case 1: hipLaunchKernelGGL(k_attn_chunk<1>, ag, dim3(kAThreads), 0, s, at); break;
-        case 2: hipLaunchKernelGGL(k_attn_chunk<2>, ag, dim3(kAThreads), 0, s, at); break;
-        case 3: hipLaunchKernelGGL(k_attn_chunk<3>, ag, dim3(kAThreads), 0, s, at); break;
-        default: hipLaunchKernelGGL(k_attn_chunk<4>, ag, dim3(kAThreads), 0, s, at); break;
+        case 1: hipLaunchKernelGGL(k_attn_chunk<1>, ag, dim3(kChunkThreads), 0, s, at); break;
+        case 2: hipLaunchKernelGGL(k_attn_chunk<2>, ag, dim3(kChunkThreads), 0, s, at); break;
+        case 3: hipLaunchKernelGGL(k_attn_chunk<3>, ag, dim3(kChunkThreads), 0, s, at); break;
+        default: hipLaunchKernelGGL(k_attn_chunk<4>, ag, dim3(kChunkThreads), 0, s, at); break;
     }
-    hipLaunchKernelGGL(k_attn_merge, dim3(T * D.n_heads), dim3(kAThreads), 0, s, at, 16 * MS);
+    hipLaunchKernelGGL(k_attn_merge, dim3(T * D.n_heads, 4), dim3(kAThreads), 0, s, at, 16 * MS);
 
     QgArgs o{};
     o.x = ob; o.T = T; o.K = D.n_heads * kHeadDim; o.bits = D.bits;
