@@ -346,3 +346,30 @@ def test_accept_tree_prefers_longest_then_lowest_path(orc):
 def test_argmax_rows_ties_and_nan(orc):
     lg = np.array([[0.0, 2.0, 2.0, np.nan], [np.nan, np.nan, -1.0, -1.0]], np.float32)
     assert orc.argmax_rows(lg).tolist() == [1, 2]
+
+
+def test_rmsnorm_and_head_match_torch_float64(orc):
+    """The head's norm and product against torch's rms_norm and a float64 matmul
+    (mlx RMSNorm semantics: x / sqrt(mean(x^2) + eps) * w, rounded to bf16 once).
+    Error bars: the bf16 rounding of the normalised value (half an ulp, 2^-9
+    relative) and nothing for the product, which the oracle sums in double."""
+    import torch
+    rng = np.random.default_rng(17)
+    T, H, V = 3, 512, 700
+    x = orc.f32_to_bf16(rng.standard_normal((T, H)).astype(np.float32) * 3)
+    w = orc.f32_to_bf16(1.0 + 0.1 * rng.standard_normal(H).astype(np.float32))
+    W = orc.f32_to_bf16(0.05 * rng.standard_normal((V, H)).astype(np.float32))
+    xn, inv = orc.rmsnorm_bf16(x, w, 1e-6)
+    ref = torch.nn.functional.rms_norm(torch.tensor(orc.bf16_to_f32(x), dtype=torch.float64), (H,),
+                                       torch.tensor(orc.bf16_to_f32(w), dtype=torch.float64), eps=1e-6).numpy()
+    got = orc.bf16_to_f32(xn).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-30)
+    # the sign and the position of every element survive (no transposed or dropped term)
+    assert np.array_equal(np.sign(got), np.sign(ref))
+    logits, absdot = orc.lm_head(x, w, 1e-6, W)
+    np.testing.assert_allclose(logits, got @ orc.bf16_to_f32(W).astype(np.float64).T, rtol=0, atol=1e-9)
+    assert np.all(absdot >= np.abs(logits))
+    # no norm: plain product
+    lg2, _ = orc.lm_head(x, None, 1e-6, W)
+    np.testing.assert_allclose(lg2, orc.bf16_to_f32(x).astype(np.float64) @ orc.bf16_to_f32(W).astype(np.float64).T,
+                               rtol=0, atol=1e-9)
