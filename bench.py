@@ -143,8 +143,9 @@ def bench_lm_head(args) -> int:
 
 def bench_decode(args) -> int:
     """K-draft MTP speculative decoding of a random-init Qwen3-Next-shaped model:
-    `layers` decoder layers (full attention on every attn_every-th, the 512-expert
-    top-10 4-bit MoE with the shared expert on all), the MTP layer, bf16
+    `layers` decoder layers (full attention on every attn_every-th, Gated
+    DeltaNet linear attention on the others, the 512-expert top-10 4-bit MoE
+    with the shared expert on all), the MTP layer, bf16
     embedding and head over 151,936 tokens.  The attention and MTP caches hold a
     `context`-token synthetic prompt (random bf16 keys and values: decode speed
     does not depend on their content).  Timed: `new_tokens` decoded tokens, wall
@@ -152,6 +153,7 @@ def bench_decode(args) -> int:
     cache update.  Then the same start state is decoded greedily without
     speculation and the two token streams are compared."""
     import torch
+    from vates_amd.attention import KVCache
     from vates_amd.decode import greedy_decode, speculative_decode
     from vates_amd.mtp import MTPDrafter
     from vates_amd.synth import synth_bf16
@@ -168,8 +170,8 @@ def bench_decode(args) -> int:
     caches = model.new_caches(max_len)
     drafter = MTPDrafter(model.mtp, max_len)
     for i, c in enumerate(caches + [drafter.cache]):
-        if c is None:
-            continue
+        if not isinstance(c, KVCache):
+            continue  # linear-attention states start from zero: their cost does not depend on content
         c.write(0, synth_bf16(SEED, 0xCA000 + 2 * i, (c.k.shape[0], ctx, 256), device=dev),
                 synth_bf16(SEED, 0xCA001 + 2 * i, (c.v.shape[0], ctx, 256), device=dev))
     x0 = torch.tensor([4242], dtype=torch.int32, device=dev)
@@ -179,7 +181,11 @@ def bench_decode(args) -> int:
 
     def reset():
         for c in caches:
-            if c is not None:
+            if isinstance(c, KVCache):
+                c.length = ctx
+            elif c is not None:  # linear-attention rings hold only recent positions: restart from zero state
+                c.conv.zero_()
+                c.state.zero_()
                 c.length = ctx
         drafter.cache.length = ctx - 1
 
@@ -204,8 +210,9 @@ def bench_decode(args) -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "u4 experts/projections, bf16 head and KV, f32 accumulate", "data": "synthetic",
         "config": {"workload": f"{args.layers}-layer random-init Qwen3-Next-shaped model ({args.layers // args.attn_every}"
-                               f" full-attention layers, every layer MoE 512x top-{args.top_k} + shared expert, "
-                               f"linear-attention layers omitted), MTP K={K}, {N} new tokens after a {ctx}-token "
+                               f" full-attention and {args.layers - args.layers // args.attn_every} Gated DeltaNet "
+                               f"layers, every layer MoE 512x top-{args.top_k} + shared expert), MTP K={K}, "
+                               f"{N} new tokens after a {ctx}-token "
                                f"synthetic context, vocab {args.vocab}",
                    "accept_hist": hist, "avg_accept_len": round(st.avg_accept_len, 3),
                    "speculative_equals_greedy": same, "first_divergence": first_diff,

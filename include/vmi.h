@@ -237,6 +237,52 @@ int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int 
                         void* stream);
 
 /* ------------------------------------------------------------------------
+ * vmi_gdn_layer -- the Gated DeltaNet (linear attention) block of a
+ * Qwen3-Next decoder layer on a verify batch or decode step, capturing the
+ * state after every token: out = x + gdn(rmsnorm(x)).  Replaces mlx-lm's
+ * Qwen3NextGatedDeltaNet as the reference patches it for verification
+ * (mlx_streaming/mtp/kv_cache.py:34-102: per-token [conv, ssm] checkpoints
+ * from the multistate kernel, core/linear_attn/gated_delta_multistate.py:
+ * 27-143) and its commit (commit_verified_prefix, kv_cache.py:222-251).
+ * in_proj_qkvz rows per k-head group: [q dk | k dk | v r*dv | z r*dv]
+ * (r = n_v / n_k); in_proj_ba per group: [b r | a r]; conv input row =
+ * [q of all k-heads | k of all k-heads | v of all v-heads] (conv_dim =
+ * 2 n_k dk + n_v dv), causal depthwise conv of width 4 (conv_weight bf16
+ * [conv_dim][4], tap 3 = the current position) and SiLU; q and k of each
+ * head are divided by sqrt(mean(.^2) + 1e-6) and scaled by 1/dk and
+ * 1/sqrt(dk); beta = sigmoid(b), g = exp(-exp(A_log) softplus(a + dt_bias));
+ * per v-head (reading k-head h / r) with state S [dv][dk] in fp32:
+ *   S <- g S;  delta = beta (v - S k);  S <- S + delta k^T;  y = S q;
+ * o = y / sqrt(mean(y^2) + norm_eps) * norm_weight * silu(z) per v-head;
+ * out = x + out_proj o.
+ * conv_ring: bf16 [32][conv_dim]; row p % 32 holds the conv input of
+ * position p.  state_ring: f32 [n_slots][n_v][dv][dk]; slot p % n_slots holds
+ * the state before position p.  A call at positions pos0..pos0+T-1 reads
+ * conv rows pos0-3..pos0-1 and state slot pos0 % n_slots (zeros at pos0 = 0)
+ * and writes conv rows and the state after each token (slots pos0+1 ..
+ * pos0+T); n_slots >= T + 1.  Committing m accepted positions is continuing
+ * at pos0 + m: nothing is copied.  head dims 128, T <= 8.  workspace:
+ * vmi_gdn_layer_workspace_bytes(T, hidden, n_k_heads, n_v_heads) bytes.
+ * A T-token call equals T one-token calls bit for bit.
+ * ------------------------------------------------------------------------ */
+typedef struct vmi_gdn_layer_desc {
+    int hidden, n_k_heads, n_v_heads, head_k_dim, head_v_dim;
+    float norm_eps;
+    int bits, group;
+    const uint16_t* input_norm;   /* [hidden] */
+    vmi_qmat in_proj_qkvz, in_proj_ba, out_proj;
+    const uint16_t* conv_weight;  /* [conv_dim][4] bf16 */
+    const float* A_log;           /* [n_v_heads] */
+    const float* dt_bias;         /* [n_v_heads] */
+    const uint16_t* norm_weight;  /* [head_v_dim] */
+} vmi_gdn_layer_desc;
+
+size_t vmi_gdn_layer_workspace_bytes(int T, int hidden, int n_k_heads, int n_v_heads);
+int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, int T, int pos0, uint16_t* conv_ring,
+                  float* state_ring, int n_slots, uint16_t* out, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* ------------------------------------------------------------------------
  * vmi_rmsnorm -- out = bf16(x * 1/sqrt(mean(x^2) + eps) * weight) per token
  * (mlx RMSNorm as the MTP module applies it: pre_fc_norm_embedding,
  * pre_fc_norm_hidden and norm, qwen3_next_mtp.py:27-31, 46-49, 54).  With ids

@@ -274,6 +274,33 @@ def lm_head(x: np.ndarray, norm_w, eps: float, W: np.ndarray):
 
 
 
+def gdn_layer(x, G: dict, conv_in=None, state_in=None):
+    """Gated DeltaNet block in float64: (out [T, H], conv rows [T, conv_dim],
+    states [T, n_v, dv, dk]).  G: H, n_k, n_v, dk, dv, eps, bits, in_norm,
+    qkvz_w/_s/_b, ba_w/_s/_b, out_w/_s/_b, conv_w (bf16 bits [conv_dim, 4]),
+    A_log, dt_bias (float32 [n_v]), norm_w (bf16 bits [dv]); conv_in float64
+    [3, conv_dim] (oldest first) or None; state_in float64 [n_v, dv, dk] or None."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    H, nk, nv, dk, dv = G["H"], G["n_k"], G["n_v"], G["dk"], G["dv"]
+    T = x.size // H
+    cd = 2 * nk * dk + nv * dv
+    out = np.empty((T, H), dtype=np.float64)
+    rows = np.empty((T, cd), dtype=np.float64)
+    states = np.empty((T, nv, dv, dk), dtype=np.float64)
+    ci = None if conv_in is None else np.ascontiguousarray(conv_in, dtype=np.float64)
+    si = None if state_in is None else np.ascontiguousarray(state_in, dtype=np.float64)
+    a = {k: (np.ascontiguousarray(v) if isinstance(v, np.ndarray) else v) for k, v in G.items()}
+    fn = lib().orc_gdn_layer_f64
+    fn.argtypes = [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_float] + [c_void_p] * 10 + \
+        [c_int] + [c_void_p] * 9
+    _chk(fn(_p(x), T, H, nk, nv, dk, dv, c_float(G["eps"]), _p(a["in_norm"]),
+            _p(a["qkvz_w"]), _p(a["qkvz_s"]), _p(a["qkvz_b"]), _p(a["ba_w"]), _p(a["ba_s"]), _p(a["ba_b"]),
+            _p(a["out_w"]), _p(a["out_s"]), _p(a["out_b"]), G["bits"], _p(a["conv_w"]),
+            _p(np.ascontiguousarray(G["A_log"], np.float32)), _p(np.ascontiguousarray(G["dt_bias"], np.float32)),
+            _p(a["norm_w"]), _p(ci), _p(si), _p(out), _p(rows), _p(states)), "gdn_layer")
+    return out, rows, states
+
+
 def sd_masses(logits_row, temperature: float, top_p: float):
     """Integer masses W (uint32 [V]), nucleus threshold, Z_S and Z of one row."""
     l = np.ascontiguousarray(logits_row, dtype=np.float32)

@@ -735,6 +735,119 @@ int orc_attention_layer_f64(const uint16_t* x, int T, int H, int n_heads, int n_
     return rc;
 }
 
+/* ------------------------------------------------------- Gated DeltaNet */
+/* The linear-attention block of a Qwen3-Next decoder layer with per-token
+ * state capture, as the reference runs it at verify time
+ * (mlx_streaming/mtp/kv_cache.py:34-102 over
+ * core/linear_attn/gated_delta_multistate.py:27-143), in double:
+ *   xn = rmsnorm_bf16(x, in_norm); P = qkvz . xn ([n_k groups][q dk | k dk |
+ *   v r*dv | z r*dv], r = n_v / n_k); ba = ba_w . xn ([n_k][b r | a r]);
+ *   conv input row m_t = [q all heads | k all heads | v all heads]
+ *   (conv_dim = 2 n_k dk + n_v dv); c_t = silu(sum_j conv_w[c][j] m_{t-3+j}[c])
+ *   with m of positions before the batch from conv_in (3 rows, oldest first);
+ *   q = c_q / sqrt(mean(c_q^2) + 1e-6) / dk, k = c_k / sqrt(mean(c_k^2) + 1e-6)
+ *   / sqrt(dk) (kv_cache.py:61-63), per head;
+ *   v-head h reads k-head h / r; beta = sigmoid(b), g = exp(-exp(A_log)
+ *   softplus(a + dt_bias)); S <- S g; kv = S k; delta = (v - kv) beta;
+ *   S <- S + delta k^T; y = S q  (S [dv][dk], gated_delta_multistate.py:74-104);
+ *   o = y / sqrt(mean(y^2) + eps) * norm_w * silu(z) per v-head;
+ *   out = x + out_proj o.
+ * conv_rows (optional, [T][conv_dim]) receives m_t; states (optional,
+ * [T][n_v][dv][dk]) the state after each token; state_in NULL = zeros. */
+int orc_gdn_layer_f64(const uint16_t* x, int T, int H, int n_k, int n_v, int dk, int dv, float eps,
+                      const uint16_t* in_norm, const uint32_t* pw, const uint16_t* ps, const uint16_t* pb,
+                      const uint32_t* bw, const uint16_t* bs, const uint16_t* bb, const uint32_t* ow,
+                      const uint16_t* os, const uint16_t* ob, int bits, const uint16_t* conv_w, const float* A_log,
+                      const float* dt_bias, const uint16_t* norm_w, const double* conv_in, const double* state_in,
+                      double* out, double* conv_rows, double* states) {
+    const int group = 64;
+    if (T <= 0 || n_k <= 0 || n_v % n_k || dk <= 0 || dv <= 0) return ORC_EINVAL;
+    const int r = n_v / n_k, per_g = 2 * dk + 2 * r * dv;
+    const int nq = n_k * dk, cd = 2 * nq + n_v * dv;
+    const size_t ss = (size_t)n_v * dv * dk;
+    uint16_t* xn = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)T * H);
+    double* xd = (double*)malloc(sizeof(double) * (size_t)T * H);
+    double* P = (double*)malloc(sizeof(double) * (size_t)T * n_k * per_g);
+    double* BA = (double*)malloc(sizeof(double) * (size_t)T * 2 * n_v);
+    double* M = (double*)malloc(sizeof(double) * (size_t)(T + 3) * cd);
+    double* C = (double*)malloc(sizeof(double) * (size_t)cd);
+    double* S = (double*)malloc(sizeof(double) * ss);
+    double* o = (double*)malloc(sizeof(double) * (size_t)T * n_v * dv);
+    int rc = (!xn || !xd || !P || !BA || !M || !C || !S || !o) ? ORC_ENOMEM : ORC_OK;
+    if (rc == ORC_OK) rc = orc_rmsnorm_bf16(x, in_norm, eps, T, H, xn, NULL);
+    if (rc == ORC_OK) {
+        for (size_t i = 0; i < (size_t)T * H; ++i) xd[i] = bf16_to_f32(xn[i]);
+        qgemv_f64(pw, ps, pb, n_k * per_g, H, group, bits, xd, T, P);
+        qgemv_f64(bw, bs, bb, 2 * n_v, H, group, bits, xd, T, BA);
+        for (int j = 0; j < 3; ++j)
+            for (int c = 0; c < cd; ++c) M[(size_t)j * cd + c] = conv_in ? conv_in[(size_t)j * cd + c] : 0.0;
+        for (int t = 0; t < T; ++t) {
+            double* m = M + (size_t)(t + 3) * cd;
+            const double* pr = P + (size_t)t * n_k * per_g;
+            for (int g = 0; g < n_k; ++g)
+                for (int d = 0; d < dk; ++d) {
+                    m[g * dk + d] = pr[(size_t)g * per_g + d];
+                    m[nq + g * dk + d] = pr[(size_t)g * per_g + dk + d];
+                }
+            for (int h = 0; h < n_v; ++h)
+                for (int d = 0; d < dv; ++d)
+                    m[2 * nq + h * dv + d] = pr[(size_t)(h / r) * per_g + 2 * dk + (h % r) * dv + d];
+            if (conv_rows) memcpy(conv_rows + (size_t)t * cd, m, sizeof(double) * cd);
+        }
+        if (state_in) memcpy(S, state_in, sizeof(double) * ss);
+        else memset(S, 0, sizeof(double) * ss);
+        for (int t = 0; t < T; ++t) {
+            for (int c = 0; c < cd; ++c) {
+                double acc = 0.0;
+                for (int j = 0; j < 4; ++j) acc += (double)bf16_to_f32(conv_w[(size_t)c * 4 + j]) * M[(size_t)(t + j) * cd + c];
+                C[c] = acc / (1.0 + exp(-acc));
+            }
+            for (int h = 0; h < 2 * n_k; ++h) {  /* q heads then k heads */
+                double* v = C + (size_t)h * dk;
+                double sq = 0.0;
+                for (int d = 0; d < dk; ++d) sq += v[d] * v[d];
+                const double f = 1.0 / sqrt(sq / dk + 1e-6) / (h < n_k ? (double)dk : sqrt((double)dk));
+                for (int d = 0; d < dk; ++d) v[d] *= f;
+            }
+            const double* pr = P + (size_t)t * n_k * per_g;
+            for (int h = 0; h < n_v; ++h) {
+                const int gk = h / r, j = h % r;
+                const double b = BA[(size_t)t * 2 * n_v + gk * 2 * r + j];
+                const double a = BA[(size_t)t * 2 * n_v + gk * 2 * r + r + j];
+                const double beta = 1.0 / (1.0 + exp(-b));
+                const double sp = a + dt_bias[h] > 30.0 ? a + dt_bias[h] : log1p(exp(a + dt_bias[h]));
+                const double gd = exp(-exp((double)A_log[h]) * sp);
+                const double* q = C + (size_t)gk * dk;
+                const double* k = C + nq + (size_t)gk * dk;
+                const double* vv = C + 2 * nq + (size_t)h * dv;
+                double* Sh = S + (size_t)h * dv * dk;
+                double* y = o + ((size_t)t * n_v + h) * dv;
+                for (int e = 0; e < dv; ++e) {
+                    double* row = Sh + (size_t)e * dk;
+                    double kv = 0.0;
+                    for (int d = 0; d < dk; ++d) { row[d] *= gd; kv += row[d] * k[d]; }
+                    const double delta = (vv[e] - kv) * beta;
+                    double yo = 0.0;
+                    for (int d = 0; d < dk; ++d) { row[d] += k[d] * delta; yo += row[d] * q[d]; }
+                    y[e] = yo;
+                }
+                /* gated RMSNorm */
+                const double* z = pr + (size_t)gk * per_g + 2 * dk + r * dv + j * dv;
+                double sq = 0.0;
+                for (int e = 0; e < dv; ++e) sq += y[e] * y[e];
+                const double inv = 1.0 / sqrt(sq / dv + (double)eps);
+                for (int e = 0; e < dv; ++e)
+                    y[e] = y[e] * inv * (double)bf16_to_f32(norm_w[e]) * (z[e] / (1.0 + exp(-z[e])));
+            }
+            if (states) memcpy(states + (size_t)t * ss, S, sizeof(double) * ss);
+        }
+        qgemv_f64(ow, os, ob, H, n_v * dv, group, bits, o, T, out);
+        for (size_t i = 0; i < (size_t)T * H; ++i) out[i] += bf16_to_f32(x[i]);
+    }
+    free(xn); free(xd); free(P); free(BA); free(M); free(C); free(S); free(o);
+    return rc;
+}
+
 /* ---------------------------------------------------------------- lm_head */
 /* logits = W . rmsnorm(x) (generate.py:208-217; drafter.py:20-40): xn is the
  * bf16 RMSNorm output (orc_rmsnorm_bf16, the GPU's exact operand) or x itself

@@ -27,7 +27,7 @@ def log(msg):
 from oracle.torch_bridge import layer_np, u16, u32  # noqa: E402
 
 SMALL = dict(n_layers=4, attn_every=2, hidden=512, inter=128, num_experts=64, top_k=4, vocab=4096, n_heads=4,
-             n_kv_heads=2)
+             n_kv_heads=2, n_k_heads=2, n_v_heads=4)
 
 
 @pytest.fixture(scope="module")

@@ -10,7 +10,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libvmi.so"
-SOURCES = ["vmi_moe.hip", "vmi_util.hip", "vmi_head.hip", "vmi_accept.hip", "vmi_prefill.hip", "vmi_attn.hip"]
+SOURCES = ["vmi_moe.hip", "vmi_util.hip", "vmi_head.hip", "vmi_accept.hip", "vmi_prefill.hip", "vmi_attn.hip", "vmi_gdn.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",

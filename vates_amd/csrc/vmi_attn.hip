@@ -115,17 +115,7 @@ __global__ __launch_bounds__(kAThreads) void k_rms_rows(RmsArgs a) {
 
 // ------------------------------------------------------------------ GEMV
 // Up to three weight matrices stacked along the output rows (q, k, v).
-struct QgArgs {
-    const uint16_t* x;      // [T, K] bf16
-    int T, K, bits;
-    vmi_qmat m[3];
-    int rows[3];            // rows of each matrix
-    int nrows;              // total
-    float* out;             // [T, out_stride] f32: row n of the stack at column n
-    int out_stride;
-    const uint16_t* residual;  // optional [T, out_stride] bf16: out_bf16 = bf16(y + residual)
-    uint16_t* out_bf16;        // optional
-};
+using QgArgs = vmi::QgemvCall;
 
 // One wave per output row, 4 rows per workgroup.  Lane l takes 32-column
 // blocks l, l + 64, ...; per block sum_c x_c q_c and sum_c x_c meet the
@@ -572,17 +562,26 @@ AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len) {
     return L;
 }
 
-hipError_t launch_qgemv(QgArgs& q, hipStream_t s) {
+bool qm_ok(const vmi_qmat& m) { return vmi::qmat_ok(m); }
+
+}  // namespace
+
+hipError_t vmi::launch_qgemv(const QgemvCall& q, hipStream_t s) {
     const size_t lds = (size_t)q.T * q.K * 2;
     hipLaunchKernelGGL(k_qgemv, dim3((q.nrows + 3) / 4), dim3(kAThreads), lds, s, q);
     return hipGetLastError();
 }
 
-bool qm_ok(const vmi_qmat& m) {
-    return m.w && m.s && m.b && !(reinterpret_cast<uintptr_t>(m.w) & 15);
+hipError_t vmi::launch_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out,
+                               hipStream_t s) {
+    RmsArgs ra{x, w, eps, T, H, out, nullptr, 0, nullptr, H};
+    hipLaunchKernelGGL(k_rms_rows, dim3((T + 3) / 4), dim3(kAThreads), 0, s, ra);
+    return hipGetLastError();
 }
 
-}  // namespace
+bool vmi::qmat_ok(const vmi_qmat& m) {
+    return m.w && m.s && m.b && !(reinterpret_cast<uintptr_t>(m.w) & 15);
+}
 
 extern "C" int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int group, float* out,
                          const uint16_t* residual, uint16_t* out_bf16, void* stream) {
@@ -598,7 +597,7 @@ extern "C" int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int
     q.m[0] = w; q.m[1] = w; q.m[2] = w;
     q.rows[0] = N; q.rows[1] = 0; q.rows[2] = 0; q.nrows = N;
     q.out = out; q.out_stride = N; q.residual = residual; q.out_bf16 = out_bf16;
-    const hipError_t e = launch_qgemv(q, static_cast<hipStream_t>(stream));
+    const hipError_t e = vmi::launch_qgemv(q, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "k_qgemv launch");
 }
 
@@ -654,7 +653,7 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     q.m[0] = D.q_proj; q.m[1] = D.k_proj; q.m[2] = D.v_proj;
     q.rows[0] = D.n_heads * 2 * kHeadDim; q.rows[1] = D.n_kv_heads * kHeadDim; q.rows[2] = D.n_kv_heads * kHeadDim;
     q.nrows = stride; q.out = qkv; q.out_stride = stride;
-    hipError_t e = launch_qgemv(q, s);
+    hipError_t e = vmi::launch_qgemv(q, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "qkv projection launch");
 
     RopeArgs rp{};
@@ -686,7 +685,7 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     o.m[0] = D.o_proj; o.m[1] = D.o_proj; o.m[2] = D.o_proj;
     o.rows[0] = D.hidden; o.rows[1] = 0; o.rows[2] = 0; o.nrows = D.hidden;
     o.out = nullptr; o.out_stride = D.hidden; o.residual = x; o.out_bf16 = out;
-    e = launch_qgemv(o, s);
+    e = vmi::launch_qgemv(o, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "o_proj launch");
     return VMI_OK;
 }

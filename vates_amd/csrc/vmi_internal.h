@@ -45,4 +45,23 @@ struct MoeWorkspace {
 
 MoeWorkspace carve_workspace(void* base, int T, int k, int hidden, int inter, int num_experts);
 
+// Quantised GEMV over up to three stacked matrices (k_qgemv, vmi_attn.hip):
+// out[t][n] = sum_k x[t][k] W[n][k] for T <= 8 tokens, T * K <= 32768.
+struct QgemvCall {
+    const uint16_t* x;      // [T, K] bf16
+    int T, K, bits;
+    vmi_qmat m[3];
+    int rows[3];            // rows of each matrix
+    int nrows;              // total
+    float* out;             // [T, out_stride] f32: row n of the stack at column n
+    int out_stride;
+    const uint16_t* residual;  // optional [T, out_stride] bf16: out_bf16 = bf16(y + residual)
+    uint16_t* out_bf16;        // optional
+};
+hipError_t launch_qgemv(const QgemvCall& q, hipStream_t s);
+// bf16 RMSNorm of T rows of width H (H % 512 == 0) into out (stride H).
+hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out, hipStream_t s);
+// Non-null, 16-byte aligned packed weights.
+bool qmat_ok(const vmi_qmat& m);
+
 }  // namespace vmi

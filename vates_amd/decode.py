@@ -1,8 +1,8 @@
 """K-draft MTP speculative decoding on libvmi: the analogue of ``mtp_generate``.
 
 * ``SpecModel.forward`` is ``forward_with_hidden`` (mlx_streaming/mtp/
-  generate.py:101-220): embedding, decoder layers (full attention where the
-  layer has one, then the routed MoE with its shared expert), the final norm
+  generate.py:101-220): embedding, decoder layers (full attention or the
+  Gated DeltaNet block, then the routed MoE with its shared expert), the final norm
   and the head; returns the argmax of every position and the pre-norm hidden
   states the MTP drafter consumes (generate.py:209-216).
 * ``speculative_decode`` is the decode loop of ``mtp_generate`` in the verify
@@ -14,8 +14,8 @@
 * ``greedy_decode`` is the non-speculative reference the speculative loop must
   reproduce token for token (test_mtp_generate.py:421-489).
 
-Layers without an attention block run the MoE alone; the reference's
-Gated-DeltaNet linear-attention layers are not built here.
+Each decoder layer runs full attention or the Gated DeltaNet block (or
+neither), then the MoE block.
 Errors raise ``VmiError``; there is no fallback path.
 """
 from __future__ import annotations
@@ -29,6 +29,7 @@ import torch
 from ._lib import VmiError
 from .accept import accept_greedy
 from .attention import AttentionLayer, KVCache
+from .gdn import GatedDeltaNetLayer, GdnCache
 from .head import lm_head
 from .moe import MoELayer
 from .mtp import MTPDrafter, MTPLayer, rmsnorm
@@ -38,6 +39,7 @@ from .mtp import MTPDrafter, MTPLayer, rmsnorm
 class DecoderLayer:
     moe: MoELayer                        # norm_weight = the post-attention norm
     attn: Optional[AttentionLayer] = None
+    gdn: Optional[GatedDeltaNetLayer] = None
 
 
 @dataclass
@@ -58,22 +60,29 @@ class SpecModel:
         self.embed, self.layers, self.final_norm, self.head, self.mtp, self.eps = embed, layers, final_norm, head, mtp, eps
         self.hidden = embed.shape[1]
 
-    def new_caches(self, max_len: int) -> List[Optional[KVCache]]:
-        return [l.attn.new_cache(max_len) if l.attn is not None else None for l in self.layers]
+    def new_caches(self, max_len: int, max_batch: int = 8) -> list:
+        """Per layer: a KVCache (full attention), a GdnCache (linear attention,
+        verify batches up to max_batch tokens) or None."""
+        return [l.attn.new_cache(max_len) if l.attn is not None else
+                l.gdn.new_cache(max_batch) if l.gdn is not None else None for l in self.layers]
 
-    def forward(self, ids: torch.Tensor, caches: List[Optional[KVCache]], pos0: int, *, want_logits: bool = False):
+    def forward(self, ids: torch.Tensor, caches: list, pos0: int, *, want_logits: bool = False):
         """ids int32 [T] on the device at positions pos0..; returns (argmax int32 [T],
         pre-norm hidden bf16 [T, H], logits f32 [T, V] or None)."""
         x = rmsnorm(self.embed, None, ids=ids)
         for layer, cache in zip(self.layers, caches):
             if layer.attn is not None:
                 x = layer.attn(x, cache, pos0=pos0)
+            elif layer.gdn is not None:
+                x = layer.gdn(x, cache, pos0=pos0)
             x = layer.moe(x, residual=x)
         logits, am, _ = lm_head(x, self.head, self.final_norm, eps=self.eps, want_logits=want_logits)
         return am, x, logits
 
-    def commit(self, caches: List[Optional[KVCache]], length: int) -> None:
-        """Keeps positions < length in every attention cache (kv_cache.py:222-251)."""
+    def commit(self, caches: list, length: int) -> None:
+        """Keeps positions < length in every cache (commit_verified_prefix,
+        kv_cache.py:222-251): attention caches drop the rejected keys, linear
+        attention continues from the state captured after position length - 1."""
         for c in caches:
             if c is not None:
                 c.length = length

@@ -124,13 +124,37 @@ def synth_attention(seed: int, layer: int, *, hidden: int = 2048, n_heads: int =
                           n_heads=n_heads, n_kv_heads=n_kv_heads)
 
 
+def synth_gdn(seed: int, layer: int, *, hidden: int = 2048, n_k_heads: int = 16, n_v_heads: int = 32,
+              std: float = 0.02, device=None):
+    """Qwen3-Next Gated DeltaNet block: 4-bit qkvz, ba and out projections,
+    bf16 conv weights [conv_dim, 4] (std 0.3), A_log = log U(1, 16),
+    dt_bias ~ N(0, 1), bf16 norms."""
+    from .gdn import GatedDeltaNetLayer
+    from .synth import synth_bf16
+    device = torch.device(device or "cuda")
+    base = layer * 16 + 12
+    r = n_v_heads // n_k_heads
+    qkvz = synth_proj(seed, base, 1, n_k_heads * (256 + 256 * r), hidden, std=std, device=device)
+    ba = synth_proj(seed, base + 1, 1, 2 * n_v_heads, hidden, std=std, device=device)
+    out = synth_proj(seed, base + 2, 1, hidden, n_v_heads * 128, std=std, device=device)
+    conv_dim = 2 * n_k_heads * 128 + n_v_heads * 128
+    conv = synth_bf16(seed, 0xC0000 + layer, (conv_dim, 4), std=0.3, device=device)
+    rng = np.random.default_rng([seed, layer, 0x6D17])
+    A_log = torch.from_numpy(np.log(rng.uniform(1.0, 16.0, n_v_heads)).astype(np.float32)).to(device)
+    dt_bias = torch.from_numpy(rng.standard_normal(n_v_heads).astype(np.float32)).to(device)
+    return GatedDeltaNetLayer(qkvz, ba, out, bf16_norm(seed, 5000 + layer, hidden, device), conv, A_log, dt_bias,
+                              bf16_norm(seed, 6000 + layer, 128, device), n_k_heads=n_k_heads, n_v_heads=n_v_heads)
+
+
 def synth_spec_model(seed: int, *, n_layers: int = 4, attn_every: int = 4, hidden: int = 2048, inter: int = 512,
                      num_experts: int = 512, top_k: int = 10, vocab: int = 151936, n_heads: int = 16,
-                     n_kv_heads: int = 2, zipf_alpha: float = 0.5, device=None):
+                     n_kv_heads: int = 2, zipf_alpha: float = 0.5, linear_attention: bool = True,
+                     n_k_heads: int = 16, n_v_heads: int = 32, device=None):
     """A random-init Qwen3-Next-shaped model for speculative decoding: bf16
     embedding and head [vocab, hidden], n_layers decoder layers (a full-attention
-    block on every attn_every-th layer, as layer_types' interval pattern, then the
-    routed MoE with the shared expert), the final norm, and the MTP layer
+    block on every attn_every-th layer, as layer_types' interval pattern, a
+    Gated DeltaNet block on the others unless linear_attention is False, then
+    the routed MoE with the shared expert), the final norm, and the MTP layer
     (layer id 100: fc [hidden, 2 hidden], attention, MoE, norms)."""
     from .decode import DecoderLayer, SpecModel
     from .mtp import MTPLayer, MTPWeights
@@ -142,9 +166,12 @@ def synth_spec_model(seed: int, *, n_layers: int = 4, attn_every: int = 4, hidde
     for l in range(n_layers):
         w = synth_layer(seed, l, hidden=hidden, inter=inter, num_experts=num_experts, zipf_alpha=zipf_alpha,
                         device=device)
+        full = (l + 1) % attn_every == 0
         attn = synth_attention(seed, l, hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv_heads, device=device) \
-            if (l + 1) % attn_every == 0 else None
-        layers.append(DecoderLayer(make_layer(w, top_k=top_k), attn))
+            if full else None
+        gdn = synth_gdn(seed, l, hidden=hidden, n_k_heads=n_k_heads, n_v_heads=n_v_heads, device=device) \
+            if linear_attention and not full else None
+        layers.append(DecoderLayer(make_layer(w, top_k=top_k), attn, gdn))
     mw = synth_layer(seed, 100, hidden=hidden, inter=inter, num_experts=num_experts, zipf_alpha=zipf_alpha,
                      device=device)
     mtp = MTPLayer(MTPWeights(
