@@ -41,7 +41,8 @@ def test_qgemv_parity(gpu, orc, bits):
     import torch
     from vates_amd.attention import qgemv
     from vates_amd.synth import synth_bf16, synth_proj
-    for T, K, N in ((1, 2048, 1000), (4, 2048, 9216), (8, 4096, 256), (3, 512, 64)):
+    # K in {512, 1024, 2048, 4096} at 4 bits takes the MFMA kernel, K = 1536 the per-row one
+    for T, K, N in ((1, 2048, 1000), (4, 2048, 9216), (8, 4096, 256), (3, 512, 64), (2, 1536, 100), (5, 1024, 48)):
         log(f"case: qgemv bits={bits} T={T} K={K} N={N}")
         w = synth_proj(71, 1, 1, N, K, bits=bits, device=gpu)
         x = synth_bf16(71, 2, (T, K), device=gpu)
@@ -57,6 +58,22 @@ def test_qgemv_parity(gpu, orc, bits):
             assert np.linalg.norm(got[t] - ref[t]) <= 1e-5 * np.linalg.norm(ref[t])
         want_b = orc.bf16_to_f32(u16(res).reshape(T, N)).astype(np.float64) + got
         assert np.abs(orc.bf16_to_f32(u16(yb).reshape(T, N)) - want_b).max() <= 2 ** -7 * np.abs(want_b).max()
+
+
+def test_qgemv_batch_invariant(gpu):
+    """A token's result does not depend on the other tokens of its batch (bit for bit)."""
+    import torch
+    from vates_amd.attention import qgemv
+    from vates_amd.synth import synth_bf16, synth_proj
+    for K, N in ((2048, 12352), (4096, 2048)):
+        log(f"case: qgemv batch invariance K={K} N={N}")
+        w = synth_proj(72, 1, 1, N, K, device=gpu)
+        x = synth_bf16(72, 2, (4, K), device=gpu)
+        x[2] *= 1000.0   # a token with a different range factor must not move the others
+        y = qgemv(x, w)
+        ys = torch.cat([qgemv(x[t:t + 1].contiguous(), w) for t in range(4)])
+        torch.cuda.synchronize()
+        assert torch.equal(y, ys)
 
 
 def make_attention(gpu, seed, H=2048, n_heads=16, n_kv=2):

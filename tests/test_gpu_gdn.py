@@ -3,7 +3,8 @@
 Bars (written here): block outputs relative L2 <= 1e-2, cosine >= 0.9999 and
 max |err| <= 1e-2 max |ref| per token against the float64 oracle (bf16 conv
 inputs, fp32 recurrence); captured states relative L2 <= 1e-2 per v-head;
-conv rows within one bf16 ulp of the oracle's exact values; a T-token call equals T
+conv rows within one bf16 ulp of the oracle's exact values plus the GEMV's
+fp32 error (1e-5 of the row maximum); a T-token call equals T
 one-token calls bit for bit (outputs, conv rows, every captured state: the
 reference's multistate invariant, tests/test_gated_delta_multistate.py:29-57);
 continuing after a commit of m < T positions equals a run that only ever saw
@@ -80,8 +81,10 @@ def test_gdn_layer_parity(gpu, orc, T, prefix):
         assert_close(got, states[t], f"state after token {t}")
     got_rows = orc.bf16_to_f32(u16(cache.conv_rows(prefix + T))).astype(np.float64)
     want = rows[-3:] if T >= 3 else np.concatenate([conv_in[T:], rows])
-    # the GPU rounds its fp32 GEMV result to bf16: at most one bf16 ulp (2^-7 relative) from the exact value
-    assert np.all(np.abs(got_rows - want) <= 2.0 ** -7 * np.abs(want) + 1e-30)
+    # the GPU rounds its fp32 GEMV result to bf16: one bf16 ulp (2^-7 relative) from the exact value,
+    # plus the GEMV's fp32 accumulation error, bounded per row (1e-5 of the row's largest value)
+    bound = 2.0 ** -7 * np.abs(want) + 1e-5 * np.abs(want).max(axis=1, keepdims=True)
+    assert np.all(np.abs(got_rows - want) <= bound)
 
 
 def test_gdn_batch_equals_steps(gpu):

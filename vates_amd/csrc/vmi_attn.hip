@@ -532,6 +532,121 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
     }
 }
 
+// ------------------------------------------------------ 4-bit GEMV, MFMA
+// out[t][n] = sum_k x[t][k] W[n][k] for 4-bit W with K in {512, 1024, 2048,
+// 4096}: 8 waves per workgroup, wave = (16 weight rows, 512 columns), waves
+// splitting K meet in LDS in a fixed order.  bf16 MFMAs on exact operands: x
+// as it is (each lane reads its 16 bytes of x and puts them in slot order),
+// weights as bf16 128 + q (vmi_unpack_u4_bf16_128).  Tokens 0..7 sit in A rows
+// 0..7 against the even quantisation group of each 128-column load and in rows
+// 8..15 against the odd one, so one MFMA covers both groups and each D lane
+// applies its own group's scale:  y = sum_g s_g D_g + (b_g - 128 s_g) X_g with
+// X_g the group sum of x.  A token's result does not depend on the batch.
+constexpr int kQ4Waves = 8;
+constexpr int kQ4Threads = 64 * kQ4Waves;
+constexpr int kQ4Kw = 512;  // columns per wave
+
+__global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
+    __shared__ float s_X[kQ4Waves][kQgMaxT][8];       // group sums of x per wave: [token][group of the wave]
+    __shared__ float s_part[kQ4Waves][16][kQgMaxT];
+    const int T = a.T, K = a.K, G = K / 64;
+    const int tid = threadIdx.x, lane = tid & 63, w = at_wave();
+    const int nl = lane & 15, q4 = lane >> 4;
+    const int ks = K / kQ4Kw, tiles = kQ4Waves / ks;
+    const int tile = w / ks, kw = w % ks;
+    const int n = (blockIdx.x * tiles + tile) * 16 + nl;
+    const int nn = n < a.nrows ? n : a.nrows - 1;
+    int mi = 0, r = nn;
+    while (mi < 2 && r >= a.rows[mi]) r -= a.rows[mi++];
+    const vmi_qmat M = a.m[mi];
+    const uint4* wrow = reinterpret_cast<const uint4*>(M.w + (size_t)r * (K / 8));
+    uint4 wv[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) wv[m] = wrow[kw * 16 + 4 * m + q4];
+    const uint4 sv = *reinterpret_cast<const uint4*>(M.s + (size_t)r * G + kw * 8);
+    const uint4 bv = *reinterpret_cast<const uint4*>(M.b + (size_t)r * G + kw * 8);
+    // A operands: token tk, columns kw*512 + 128 m + 32 q4 + 8 j .. + 7
+    const int tk = nl & 7;
+    const bool xreal = ((q4 < 2) == (nl < 8)) && tk < T;
+    vmi_u4 ax[4][4];
+    float xs[4] = {0.f, 0.f, 0.f, 0.f};
+    if (xreal) {
+        const uint4* xr = reinterpret_cast<const uint4*>(a.x + (size_t)tk * K + kw * kQ4Kw) + 4 * q4;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint4 u = xr[16 * m + j];
+                ax[m][j][0] = (u.x & 0xffffu) | (u.z << 16);
+                ax[m][j][1] = (u.x >> 16) | (u.z & 0xffff0000u);
+                ax[m][j][2] = (u.y & 0xffffu) | (u.w << 16);
+                ax[m][j][3] = (u.y >> 16) | (u.w & 0xffff0000u);
+                const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xs[m] += __uint_as_float(uu[i] << 16) + __uint_as_float(uu[i] & 0xffff0000u);
+            }
+    } else {
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ax[m][j] = vmi_u4{0u, 0u, 0u, 0u};
+    }
+    // group 2m + (q4 >> 1) of the wave = 64 columns = lanes q4 and q4 ^ 1
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const float g = xs[m] + __shfl_xor(xs[m], 16);
+        if (xreal && (q4 & 1) == 0) s_X[w][tk][2 * m + (q4 >> 1)] = g;
+    }
+    const int par = q4 >> 1;
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
+    const vmi_f4 zf = {0.f, 0.f, 0.f, 0.f};
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const uint32_t ww[4] = {wv[m].x, wv[m].y, wv[m].z, wv[m].w};
+        vmi_f4 d = zf;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d = vmi_mfma_bf16(ax[m][j], vmi_unpack_u4_bf16_128(ww[j]), d);
+        const float sc = __uint_as_float(par ? (sw[m] & 0xffff0000u) : (sw[m] << 16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = fmaf(sc, d[e], acc[e]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // (b_g - 128 s_g) X_g for tokens 4 (q4 & 1) + e over the groups of this lane's parity
+    const int tb = 4 * (q4 & 1);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const float sc = __uint_as_float(par ? (sw[m] & 0xffff0000u) : (sw[m] << 16));
+        const float bi = __uint_as_float(par ? (bw[m] & 0xffff0000u) : (bw[m] << 16));
+        const float c = fmaf(-128.0f, sc, bi);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (tb + e < T) acc[e] = fmaf(c, s_X[w][tb + e][2 * m + par], acc[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], 32);
+    if (q4 < 2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s_part[w][nl][4 * q4 + e] = acc[e];
+    }
+    __syncthreads();
+    for (int i = tid; i < tiles * 16 * T; i += kQ4Threads) {
+        const int tl = i / (16 * T), rr = (i / T) % 16, t = i % T;
+        float y = s_part[tl * ks][rr][t];
+        for (int k2 = 1; k2 < ks; ++k2) y += s_part[tl * ks + k2][rr][t];
+        const int row = (blockIdx.x * tiles + tl) * 16 + rr;
+        if (row < a.nrows) {
+            if (a.out) a.out[(size_t)t * a.out_stride + row] = y;
+            if (a.out_bf16) {
+                const float res = a.residual ? vmi_bf16_to_f32(a.residual[(size_t)t * a.out_stride + row]) : 0.0f;
+                a.out_bf16[(size_t)t * a.out_stride + row] = vmi_f32_to_bf16(y + res);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ host
 // Keys are split into chunks of kChunkKeys at fixed absolute positions, so a
 // query's result does not depend on how many tokens share its batch.
@@ -567,8 +682,18 @@ bool qm_ok(const vmi_qmat& m) { return vmi::qmat_ok(m); }
 }  // namespace
 
 hipError_t vmi::launch_qgemv(const QgemvCall& q, hipStream_t s) {
-    const size_t lds = (size_t)q.T * q.K * 2;
-    hipLaunchKernelGGL(k_qgemv, dim3((q.nrows + 3) / 4), dim3(kAThreads), lds, s, q);
+    const int ks = q.K / kQ4Kw;
+    uintptr_t sb_align = 0;  // the MFMA kernel reads 8 scales / biases as one 16-byte load
+    for (int i = 0; i < 3; ++i)
+        if (q.rows[i] > 0 || i == 0)
+            sb_align |= reinterpret_cast<uintptr_t>(q.m[i].s) | reinterpret_cast<uintptr_t>(q.m[i].b);
+    if (q.bits == 4 && q.K % kQ4Kw == 0 && ks <= kQ4Waves && kQ4Waves % ks == 0 && !(sb_align & 15)) {
+        const int rows_per_wg = 16 * (kQ4Waves / ks);
+        hipLaunchKernelGGL(k_qgemv4, dim3((q.nrows + rows_per_wg - 1) / rows_per_wg), dim3(kQ4Threads), 0, s, q);
+    } else {
+        const size_t lds = (size_t)q.T * q.K * 2;
+        hipLaunchKernelGGL(k_qgemv, dim3((q.nrows + 3) / 4), dim3(kAThreads), lds, s, q);
+    }
     return hipGetLastError();
 }
 
