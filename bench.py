@@ -154,7 +154,7 @@ def bench_decode(args) -> int:
     speculation and the two token streams are compared."""
     import torch
     from vates_amd.attention import KVCache
-    from vates_amd.decode import greedy_decode, speculative_decode
+    from vates_amd.decode import GraphSpecDecoder, greedy_decode, speculative_decode
     from vates_amd.mtp import MTPDrafter
     from vates_amd.synth import synth_bf16
     from vates_amd.workload import synth_spec_model
@@ -189,20 +189,50 @@ def bench_decode(args) -> int:
                 c.length = ctx
         drafter.cache.length = ctx - 1
 
-    reset()
-    speculative_decode(model, drafter, caches, x0, h0, ctx, max(args.warmup, 1) * (K + 1), K=K)  # warm-up
-    reset()
-    torch.cuda.synchronize()
-    st = speculative_decode(model, drafter, caches, x0, h0, ctx, N, K=K)
+    def graph_run(planted=None):
+        reset()
+        dec = GraphSpecDecoder(model, drafter, caches, K=K, planted=planted is not None)
+        dec.start(x0, h0, ctx)
+        dec.capture()
+        if args.warmup:
+            dec.run(args.warmup * (K + 1), plant=planted)  # warm-up replays
+            reset()
+            dec.start(x0, h0, ctx)
+        torch.cuda.synchronize()
+        return dec.run(N, plant=planted)
+
+    if args.eager:
+        reset()
+        speculative_decode(model, drafter, caches, x0, h0, ctx, max(args.warmup, 1) * (K + 1), K=K)  # warm-up
+        reset()
+        torch.cuda.synchronize()
+        st = speculative_decode(model, drafter, caches, x0, h0, ctx, N, K=K)
+    else:
+        st = graph_run()
     torch.cuda.synchronize()
     tps = N / st.seconds
-    eprint(f"[bench] decode: {N} tokens in {st.seconds:.3f} s = {tps:.1f} tokens/s, {st.steps} steps, "
-           f"avg accept len {st.avg_accept_len:.2f}")
+    eprint(f"[bench] decode ({'eager' if args.eager else 'graph'}): {N} tokens in {st.seconds:.3f} s = "
+           f"{tps:.1f} tokens/s, {st.steps} steps, avg accept len {st.avg_accept_len:.2f}")
     reset()
-    gr = greedy_decode(model, caches, x0, ctx, N)
-    same = gr.tokens == st.tokens
-    first_diff = next((i for i, (a, b) in enumerate(zip(gr.tokens, st.tokens)) if a != b), None)
-    eprint(f"[bench] greedy (non-speculative): {N / gr.seconds:.1f} tokens/s; speculative == greedy: {same}")
+    gr = greedy_decode(model, caches, x0, ctx, N + 2 * (K + 1))
+    truth = gr.tokens
+    gr_tps = len(truth) / gr.seconds
+    same = truth[:N] == st.tokens
+    first_diff = next((i for i, (a, b) in enumerate(zip(truth, st.tokens)) if a != b), None)
+    eprint(f"[bench] greedy (non-speculative, eager): {gr_tps:.1f} tokens/s; speculative == greedy: {same}")
+    # drafts that agree with the greedy stream with probability plant_rate per position
+    rng = np.random.default_rng(SEED)
+
+    def plant(step, pos):
+        base = pos - ctx
+        return [truth[base + i] if rng.random() < args.plant_rate else (truth[base + i] + 1) % args.vocab
+                for i in range(K)]
+
+    sp = graph_run(plant)
+    sp_tps = N / sp.seconds
+    sp_same = sp.tokens == truth[:N]
+    eprint(f"[bench] decode (graph, drafts planted at agreement {args.plant_rate}): {sp_tps:.1f} tokens/s, "
+           f"avg accept len {sp.avg_accept_len:.2f}, equals greedy: {sp_same}")
     hist = [st.accept_hist.count(m) for m in range(K + 1)]
     line = {
         "metric": "K=3 MTP decode tokens/s", "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,
@@ -214,9 +244,12 @@ def bench_decode(args) -> int:
                                f"layers, every layer MoE 512x top-{args.top_k} + shared expert), MTP K={K}, "
                                f"{N} new tokens after a {ctx}-token "
                                f"synthetic context, vocab {args.vocab}",
+                   "step": "eager launches" if args.eager else "one HIP graph replay per step",
                    "accept_hist": hist, "avg_accept_len": round(st.avg_accept_len, 3),
                    "speculative_equals_greedy": same, "first_divergence": first_diff,
-                   "greedy_tokens_per_s": round(N / gr.seconds, 2)},
+                   "greedy_tokens_per_s": round(gr_tps, 2),
+                   "planted_agreement": args.plant_rate, "planted_tokens_per_s": round(sp_tps, 2),
+                   "planted_avg_accept_len": round(sp.avg_accept_len, 3), "planted_equals_greedy": sp_same},
         "roofline": None, "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
@@ -313,6 +346,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--eager", action="store_true", help="decode: launch every kernel from Python instead of graph replays")
+    ap.add_argument("--plant-rate", type=float, default=0.7, help="decode: per-position draft agreement of the planted run")
     ap.add_argument("--T", type=int, default=4)
     ap.add_argument("--top-k", type=int, default=10)
     ap.add_argument("--hidden", type=int, default=2048)

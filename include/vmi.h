@@ -218,6 +218,10 @@ int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int 
  * (a checkpoint's zero-centred weights plus one).  Keys are processed in
  * chunks of 256 at fixed positions and merged in a fixed order, so a token's
  * result does not depend on the batch it is verified in (bit for bit).
+ * pos_device (int32 on the device, or NULL): when set, the batch position is
+ * read from it when the kernels run instead of pos0 (a captured graph replays
+ * with positions that advance on the device); it is clamped to
+ * [0, max_len - T], and the chunk grid covers the whole capacity.
  * workspace: vmi_attention_layer_workspace_bytes(T, hidden, n_heads,
  * n_kv_heads, max_len) bytes.
  * ------------------------------------------------------------------------ */
@@ -232,9 +236,9 @@ typedef struct vmi_attn_layer_desc {
 } vmi_attn_layer_desc;
 
 size_t vmi_attention_layer_workspace_bytes(int T, int hidden, int n_heads, int n_kv_heads, int max_len);
-int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int T, int pos0, uint16_t* k_cache,
-                        uint16_t* v_cache, int max_len, uint16_t* out, void* workspace, size_t workspace_bytes,
-                        void* stream);
+int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int T, int pos0,
+                        const int32_t* pos_device, uint16_t* k_cache, uint16_t* v_cache, int max_len, uint16_t* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * vmi_gdn_layer -- the Gated DeltaNet (linear attention) block of a
@@ -263,7 +267,8 @@ int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int 
  * pos0+T); n_slots >= T + 1.  Committing m accepted positions is continuing
  * at pos0 + m: nothing is copied.  head dims 128, T <= 8.  workspace:
  * vmi_gdn_layer_workspace_bytes(T, hidden, n_k_heads, n_v_heads) bytes.
- * A T-token call equals T one-token calls bit for bit.
+ * A T-token call equals T one-token calls bit for bit.  pos_device (int32 on
+ * the device, or NULL): when set, pos0 is read from it when the kernels run.
  * ------------------------------------------------------------------------ */
 typedef struct vmi_gdn_layer_desc {
     int hidden, n_k_heads, n_v_heads, head_k_dim, head_v_dim;
@@ -278,9 +283,9 @@ typedef struct vmi_gdn_layer_desc {
 } vmi_gdn_layer_desc;
 
 size_t vmi_gdn_layer_workspace_bytes(int T, int hidden, int n_k_heads, int n_v_heads);
-int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, int T, int pos0, uint16_t* conv_ring,
-                  float* state_ring, int n_slots, uint16_t* out, void* workspace, size_t workspace_bytes,
-                  void* stream);
+int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, int T, int pos0, const int32_t* pos_device,
+                  uint16_t* conv_ring, float* state_ring, int n_slots, uint16_t* out, void* workspace,
+                  size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * vmi_rmsnorm -- out = bf16(x * 1/sqrt(mean(x^2) + eps) * weight) per token

@@ -148,3 +148,22 @@ def test_attention_batch_equals_steps(gpu, orc):
     assert torch.equal(c1.v.view(torch.int16), c2.v.view(torch.int16))
     # keys in chunks at fixed positions and per-row MFMA results: bit-identical
     assert torch.equal(batch.view(torch.int16), steps.view(torch.int16)), "batch result differs from single steps"
+
+
+def test_attention_position_on_device(gpu):
+    """pos_device gives the result and cache of the host position, bit for bit."""
+    import torch
+    from vates_amd.synth import synth_bf16
+    layer, _ = make_attention(gpu, 83)
+    pos0 = 700
+    c1, c2 = layer.new_cache(1024), layer.new_cache(1024)
+    pk, pv = synth_bf16(83, 20, (2, pos0, 256), device=gpu), synth_bf16(83, 21, (2, pos0, 256), device=gpu)
+    c1.write(0, pk, pv)
+    c2.write(0, pk, pv)
+    x = synth_bf16(83, 30, (4, 2048), device=gpu)
+    a = layer(x, c1, pos0=pos0)
+    b = layer(x, c2, pos0=0, pos_device=torch.tensor([pos0], dtype=torch.int32, device=gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(c1.k.view(torch.int16), c2.k.view(torch.int16))
+    assert torch.equal(c1.v.view(torch.int16), c2.v.view(torch.int16))

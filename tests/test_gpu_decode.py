@@ -162,3 +162,38 @@ def test_draft_paths_top_p(gpu, model):
     lg = logits[0].cpu().numpy()
     order = np.lexsort((np.arange(lg.size), -lg))[:3]
     assert paths[:, 0].cpu().tolist() == order.tolist()
+
+
+def test_graph_decode_equals_greedy(gpu, model):
+    """The captured-graph step (positions on the device) emits the greedy stream,
+    with the MTP layer's drafts and with planted drafts that make every
+    acceptance length 0..K occur."""
+    import torch
+    from vates_amd.decode import GraphSpecDecoder, greedy_decode, prefill
+    from vates_amd.mtp import MTPDrafter
+    n_tok, K = 40, 3
+    prompt = _prompt(gpu, seed=8)
+    caches = model.new_caches(256)
+    x, h = prefill(model, prompt, caches)
+    ref = greedy_decode(model, caches, x, prompt.numel(), n_tok + 2 * (K + 1))
+    P = prompt.numel()
+    for planted in (False, True):
+        log(f"case: graph speculative K=3 planted={planted}")
+        caches = model.new_caches(256)
+        drafter = MTPDrafter(model.mtp, 256)
+        x, h = prefill(model, prompt, caches, drafter)
+        dec = GraphSpecDecoder(model, drafter, caches, K=K, planted=planted)
+        dec.start(x, h, P)
+
+        def plant(step, pos):
+            m = step % (K + 1)
+            base = pos - P  # greedy stream index of the token at position pos + 1
+            return [ref.tokens[base + i] if i < m else (ref.tokens[base + i] + 1) % SMALL["vocab"] for i in range(K)]
+
+        st = dec.run(n_tok, plant=plant if planted else None)
+        assert st.tokens == ref.tokens[:n_tok], (st.tokens, ref.tokens[:n_tok])
+        if planted:
+            assert set(st.accept_hist) == set(range(K + 1)), st.accept_hist
+        log(f"accept_hist {st.accept_hist} steps {st.steps}")
+        # the host view of the caches follows the device positions
+        assert all(c.length == P + sum(m + 1 for m in st.accept_hist) for c in caches if c is not None)

@@ -136,3 +136,21 @@ def test_gdn_rejects_bad_arguments(gpu):
         layer(synth_bf16(94, 1, (4, 2048), device=gpu), cache)
     with pytest.raises(VmiError, match="T="):
         layer(synth_bf16(94, 1, (9, 2048), device=gpu), layer.new_cache(16))
+
+
+def test_gdn_position_on_device(gpu):
+    """pos_device gives the result and rings of the host position, bit for bit."""
+    import torch
+    from vates_amd.synth import synth_bf16
+    layer, _ = make_gdn(gpu, 95)
+    c1, c2 = layer.new_cache(8), layer.new_cache(8)
+    pre = synth_bf16(95, 1, (7, 2048), device=gpu)
+    layer(pre, c1)
+    layer(pre, c2)
+    x = synth_bf16(95, 2, (4, 2048), device=gpu)
+    a = layer(x, c1)
+    b = layer(x, c2, pos_device=torch.tensor([7], dtype=torch.int32, device=gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(c1.state, c2.state)
+    assert torch.equal(c1.conv.view(torch.int16), c2.conv.view(torch.int16))

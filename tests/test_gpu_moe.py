@@ -189,3 +189,17 @@ def test_moe_layer_repeatable_bitwise(gpu, orc, torch_mod):
     torch.cuda.synchronize()
     for o in outs:
         assert torch.equal(o.view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.parametrize("T", [4, 9, 16])
+def test_moe_layer_batch_invariant(gpu, orc, torch_mod, T):
+    """Every token's output equals its output in a batch of one, bit for bit:
+    each token adds its experts in its own rank order (speculative decoding
+    emits tokens from verify rows 1..K and must reproduce one-token decoding)."""
+    log(f"case: moe_layer batch invariance T={T}")
+    torch = torch_mod
+    for kw in (dict(), dict(zipf_alpha=2.0, H=1024, I=256, E=128, k=8)):
+        moe, x, out, ids, sc, ref, rid, rsc = _layer_case(gpu, orc, torch, T, **kw)
+        singles = torch.cat([moe(x[t:t + 1].contiguous(), residual=x[t:t + 1].contiguous()) for t in range(T)])
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), singles.view(torch.int16)), kw

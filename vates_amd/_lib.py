@@ -75,11 +75,11 @@ _SIGNATURES = {
     "vmi_qgemv": (c_int, [c_void_p, c_int, c_int, QMat, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
                           c_void_p]),
     "vmi_attention_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
-    "vmi_attention_layer": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
-                                    c_size_t, c_void_p]),
+    "vmi_attention_layer": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
+                                    c_void_p, c_size_t, c_void_p]),
     "vmi_gdn_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
-    "vmi_gdn_layer": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
-                              c_size_t, c_void_p]),
+    "vmi_gdn_layer": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
+                              c_void_p, c_size_t, c_void_p]),
     "vmi_rmsnorm": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p,
                             c_void_p]),
     "vmi_topk_rows": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),

@@ -140,9 +140,12 @@ class AttentionLayer:
         return KVCache(self.n_kv, max_len, self.device)
 
     def __call__(self, x: torch.Tensor, cache: KVCache, *, pos0: Optional[int] = None,
-                 out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+                 out: Optional[torch.Tensor] = None, stream=None,
+                 pos_device: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x bf16 [T, hidden] at cache positions pos0.. (default: cache.length);
-        appends k, v there and sets cache.length = pos0 + T."""
+        appends k, v there and sets cache.length = pos0 + T.  With pos_device
+        (int32 [1] on the device) the position is read there when the kernels
+        run and cache.length is left to the caller."""
         T = x.shape[0]
         pos0 = cache.length if pos0 is None else pos0
         _require(x, "x", 2, self.device)
@@ -152,8 +155,10 @@ class AttentionLayer:
         lib = load()
         ws = workspace(lib.vmi_attention_layer_workspace_bytes(T, self.hidden, self.n_heads, self.n_kv, cache.max_len),
                        self.device, sh, tag="attention")
-        rc = lib.vmi_attention_layer(ctypes.byref(self.desc), x.data_ptr(), T, pos0, cache.k.data_ptr(),
+        rc = lib.vmi_attention_layer(ctypes.byref(self.desc), x.data_ptr(), T, pos0,
+                                     None if pos_device is None else pos_device.data_ptr(), cache.k.data_ptr(),
                                      cache.v.data_ptr(), cache.max_len, out.data_ptr(), ws.data_ptr(), ws.numel(), sh)
         check(rc, "vmi_attention_layer")
-        cache.length = pos0 + T
+        if pos_device is None:
+            cache.length = pos0 + T
         return out

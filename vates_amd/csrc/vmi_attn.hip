@@ -46,6 +46,13 @@ constexpr int kAThreads = 256;
 constexpr int kQgMaxT = 8;
 constexpr int kHeadDim = 256;
 
+// The batch's first position: the argument, or read on the device (graph
+// replays), clamped so that pos0 + T <= max_len.
+__device__ __forceinline__ int batch_pos0(int pos0, const int32_t* pos_dev, int T, int max_len) {
+    const int p = pos_dev ? *pos_dev : pos0;
+    return min(max(p, 0), max_len - T);
+}
+
 __device__ __forceinline__ int at_wave() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 __device__ __forceinline__ void bf16x8f(const uint4& q, float (&v)[8]) {
@@ -207,6 +214,7 @@ struct RopeArgs {
     const float* qkv;        // [T, stride]: q|gate per head (n_heads * 2 * 256), then k (n_kv * 256), then v
     int stride;
     int T, n_heads, n_kv, rope_dim, pos0, max_len;
+    const int32_t* pos_dev;  // if set: pos0 is read here
     float theta, eps;
     const uint16_t* q_norm;  // [256]
     const uint16_t* k_norm;  // [256]
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(kAThreads) void k_qk_rope(RopeArgs a) {
         s_v[w][lane + 64 * j] = v[j];
     }
     __builtin_amdgcn_wave_barrier();  // s_v[w] is this wave's own row: LDS order within a wave suffices
-    const int pos = a.pos0 + t;
+    const int pos = batch_pos0(a.pos0, a.pos_dev, a.T, a.max_len) + t;
     const int half = a.rope_dim / 2;
     uint16_t o[4];
 #pragma unroll
@@ -291,9 +299,10 @@ struct AttnArgs {
     const uint16_t* k_cache;  // blocks of 32 positions, see the layout above
     const uint16_t* v_cache;
     int T, n_heads, n_kv, pos0, max_len;
-    int nchunks;              // chunks of kChunkKeys positions
-    float* part_o;            // [n_kv, nchunks, RP, 256]
-    float* part_ml;           // [n_kv, nchunks, RP, 2]
+    const int32_t* pos_dev;   // if set: pos0 is read here
+    int nstride;              // chunk capacity of the partial buffers
+    float* part_o;            // [n_kv, nstride, RP, 256]
+    float* part_ml;           // [n_kv, nstride, RP, 2]
     const float* qkv;         // for the gate in the merge
     int stride;
     uint16_t* o;              // [T, n_heads * 256] bf16 gated attention output
@@ -325,7 +334,9 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, w = at_wave(), nl = lane & 15, q4 = lane >> 4;
     const int G = a.n_heads / a.n_kv, R = a.T * G;
-    const int L = a.pos0 + a.T;                        // positions present
+    const int pos0 = batch_pos0(a.pos0, a.pos_dev, a.T, a.max_len);
+    const int L = pos0 + a.T;                          // positions present
+    if (c * kChunkKeys >= L) return;                   // chunk beyond the cache (whole workgroup)
     const int b0 = c * kChunkWaves;
     const uint16_t* kb = a.k_cache + kv_block(g, a.max_len, 0);
     const uint16_t* vb = a.v_cache + kv_block(g, a.max_len, 0);
@@ -389,7 +400,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
             acc1 = vmi_mfma_bf16(kr[1][kk], qb, acc1);
         }
         const int row = 16 * m + nl;
-        const int last = row < R ? min(L - 1, a.pos0 + row / G) : -1;  // last visible position
+        const int last = row < R ? min(L - 1, pos0 + row / G) : -1;  // last visible position
         const int p = kKvBlock * bw + 8 * q4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -430,7 +441,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     }
     __syncthreads();
     // O = P V for dims 32 w + 16 dt + nl; A = P of block sb (written by wave sb)
-    const size_t pbase = ((size_t)g * a.nchunks + c) * RP;
+    const size_t pbase = ((size_t)g * a.nstride + c) * RP;
 #pragma unroll
     for (int m = 0; m < MS; ++m) {
 #pragma unroll
@@ -466,9 +477,9 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
     const int t = blockIdx.x / a.n_heads, h = blockIdx.x % a.n_heads, tid = threadIdx.x;
     const int lane = tid & 63, w = at_wave();
     const int G = a.n_heads / a.n_kv, g = h / G, row = t * G + (h % G);
-    const int NC = a.nchunks;
-    const size_t cstride = (size_t)RP;                               // rows between chunks
-    const float* ml = a.part_ml + ((size_t)g * NC * RP + row) * 2;   // chunk c at + c * RP * 2
+    const int NC = (batch_pos0(a.pos0, a.pos_dev, a.T, a.max_len) + a.T + kChunkKeys - 1) / kChunkKeys;
+    const size_t cstride = (size_t)RP;                                      // rows between chunks
+    const float* ml = a.part_ml + ((size_t)g * a.nstride * RP + row) * 2;   // chunk c at + c * RP * 2
     float M = -INFINITY;
     for (int c = tid; c < NC; c += kAThreads) M = fmaxf(M, ml[c * cstride * 2]);
     M = vmi_wave_max(M);
@@ -489,7 +500,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
     den = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
 
     const int slot = 4 * w + (lane >> 4), d0 = 64 * blockIdx.y + 4 * (lane & 15);
-    const float* po = a.part_o + ((size_t)g * NC * RP + row) * kHeadDim + d0;  // chunk c at + c * RP * 256
+    const float* po = a.part_o + ((size_t)g * a.nstride * RP + row) * kHeadDim + d0;  // chunk c at + c * RP * 256
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int c0 = slot; c0 < NC; c0 += 16 * 8) {
         float4 v[8];
@@ -732,7 +743,7 @@ extern "C" size_t vmi_attention_layer_workspace_bytes(int T, int hidden, int n_h
 }
 
 extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int T, int pos0,
-                                   uint16_t* k_cache, uint16_t* v_cache, int max_len, uint16_t* out,
+                                   const int32_t* pos_device, uint16_t* k_cache, uint16_t* v_cache, int max_len, uint16_t* out,
                                    void* workspace, size_t workspace_bytes, void* stream) {
     vmi::clear_error();
     if (!desc) return vmi::fail(VMI_ERR_INVALID, "null desc");
@@ -748,7 +759,8 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
         return vmi::fail(VMI_ERR_UNSUPPORTED, "T too large for the projection GEMV");
     if (D.rope_dim < 0 || D.rope_dim > kHeadDim || D.rope_dim % 2) return vmi::fail(VMI_ERR_INVALID, "rope_dim=%d", D.rope_dim);
     if ((D.bits != 4 && D.bits != 8) || D.group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", D.bits, D.group);
-    if (pos0 < 0 || pos0 + T > max_len) return vmi::fail(VMI_ERR_INVALID, "pos0=%d T=%d max_len=%d", pos0, T, max_len);
+    if (T > max_len || (!pos_device && (pos0 < 0 || pos0 + T > max_len)))
+        return vmi::fail(VMI_ERR_INVALID, "pos0=%d T=%d max_len=%d", pos0, T, max_len);
     if (max_len % kKvBlock) return vmi::fail(VMI_ERR_INVALID, "max_len=%d must be a multiple of %d", max_len, kKvBlock);
     if (attn_chunks(max_len) > kMergeMaxChunks)
         return vmi::fail(VMI_ERR_UNSUPPORTED, "max_len=%d exceeds %d", max_len, kMergeMaxChunks * kChunkKeys);
@@ -783,20 +795,22 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
 
     RopeArgs rp{};
     rp.qkv = qkv; rp.stride = stride; rp.T = T; rp.n_heads = D.n_heads; rp.n_kv = D.n_kv_heads;
-    rp.rope_dim = D.rope_dim; rp.pos0 = pos0; rp.max_len = max_len; rp.theta = D.rope_theta; rp.eps = D.norm_eps;
+    rp.rope_dim = D.rope_dim; rp.pos0 = pos0; rp.pos_dev = pos_device; rp.max_len = max_len; rp.theta = D.rope_theta; rp.eps = D.norm_eps;
     rp.q_norm = D.q_norm; rp.k_norm = D.k_norm; rp.q_out = qb; rp.k_cache = k_cache; rp.v_cache = v_cache;
     hipLaunchKernelGGL(k_qk_rope, dim3((T * (D.n_heads + D.n_kv_heads) + 3) / 4), dim3(kAThreads), 0, s, rp);
 
     AttnArgs at{};
     at.q = qb; at.k_cache = k_cache; at.v_cache = v_cache;
-    at.T = T; at.n_heads = D.n_heads; at.n_kv = D.n_kv_heads; at.pos0 = pos0; at.max_len = max_len;
-    const int Lk = pos0 + T;
-    at.nchunks = attn_chunks(Lk);
+    at.T = T; at.n_heads = D.n_heads; at.n_kv = D.n_kv_heads; at.pos0 = pos0; at.pos_dev = pos_device;
+    at.max_len = max_len;
+    at.nstride = attn_chunks(max_len);
+    // with the position on the device every chunk of the capacity is launched; those past the cache exit
+    const int grid_chunks = pos_device ? at.nstride : attn_chunks(pos0 + T);
     at.part_o = reinterpret_cast<float*>(ws + L.part_o);
     at.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
     at.qkv = qkv; at.stride = stride; at.o = ob;
     const int MS = (T * G + 15) / 16;
-    const dim3 ag(at.nchunks, D.n_kv_heads);
+    const dim3 ag(grid_chunks, D.n_kv_heads);
     switch (MS) {
         case 1: hipLaunchKernelGGL(k_attn_chunk<1>, ag, dim3(kChunkThreads), 0, s, at); break;
         case 2: hipLaunchKernelGGL(k_attn_chunk<2>, ag, dim3(kChunkThreads), 0, s, at); break;

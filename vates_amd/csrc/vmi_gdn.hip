@@ -43,6 +43,7 @@ __device__ __forceinline__ int g_wave() { return __builtin_amdgcn_readfirstlane(
 
 struct GdnArgs {
     int T, pos0, n_k, n_v, r;      // r = n_v / n_k
+    const int32_t* pos_dev;        // if set: pos0 is read here (graph replays)
     int per_g, conv_dim, stride;   // proj row: [n_k groups of per_g | ba (2 n_v)]
     const float* proj;             // [T, stride] f32
     const uint16_t* conv_w;        // [conv_dim][4] bf16
@@ -69,6 +70,8 @@ __device__ __forceinline__ int conv_src(const GdnArgs& a, int c) {
     return (h / a.r) * a.per_g + 2 * kGHead + (h % a.r) * kGHead + (c % kGHead);
 }
 
+__device__ __forceinline__ int gdn_pos0(const GdnArgs& a) { return a.pos_dev ? max(*a.pos_dev, 0) : a.pos0; }
+
 __device__ __forceinline__ float bf16_round(float f) { return vmi_bf16_to_f32(vmi_f32_to_bf16(f)); }
 
 // One wave per (token, item): items 0..2 n_k - 1 are the q then k heads,
@@ -80,7 +83,8 @@ __global__ __launch_bounds__(kGThreads) void k_gdn_conv(GdnArgs a) {
     const int gid = blockIdx.x * (kGThreads / 64) + g_wave();
     if (gid >= a.T * items) return;
     const int t = gid / items, it = gid - t * items;
-    const int pos = a.pos0 + t;
+    const int pos0 = gdn_pos0(a);
+    const int pos = pos0 + t;
     const float* pr = a.proj + (size_t)t * a.stride;
     if (it == items - 1) {
         for (int h = lane; h < a.n_v; h += 64) {
@@ -107,7 +111,7 @@ __global__ __launch_bounds__(kGThreads) void k_gdn_conv(GdnArgs a) {
             const int p = pos - (kConvTaps - 1) + tap;
             float m;
             if (p == pos) m = cur;
-            else if (p >= a.pos0) m = bf16_round(a.proj[(size_t)(p - a.pos0) * a.stride + src]);
+            else if (p >= pos0) m = bf16_round(a.proj[(size_t)(p - pos0) * a.stride + src]);
             else if (p >= 0) m = vmi_bf16_to_f32(a.conv_ring[(size_t)(p % kConvRing) * a.conv_dim + c]);
             else m = 0.0f;
             acc = fmaf(vmi_bf16_to_f32(a.conv_w[(size_t)c * kConvTaps + tap]), m, acc);
@@ -149,9 +153,10 @@ __global__ __launch_bounds__(kGThreads) void k_gdn_delta(GdnArgs a) {
     const int hk = h / a.r;
     const size_t slot_elems = (size_t)a.n_v * kGHead * kGHead;
     const size_t roff = ((size_t)h * kGHead + row) * kGHead + d0;
+    const int pos0 = gdn_pos0(a);
     float S[8];
-    if (a.pos0 > 0) {
-        const float* src = a.state_ring + (size_t)(a.pos0 % a.n_slots) * slot_elems + roff;
+    if (pos0 > 0) {
+        const float* src = a.state_ring + (size_t)(pos0 % a.n_slots) * slot_elems + roff;
         const float4 u0 = *reinterpret_cast<const float4*>(src);
         const float4 u1 = *reinterpret_cast<const float4*>(src + 4);
         S[0] = u0.x; S[1] = u0.y; S[2] = u0.z; S[3] = u0.w;
@@ -184,7 +189,7 @@ __global__ __launch_bounds__(kGThreads) void k_gdn_delta(GdnArgs a) {
             yo = fmaf(S[i], qq[i], yo);
         }
         yo = sum16(yo);
-        float* dst = a.state_ring + (size_t)((a.pos0 + t + 1) % a.n_slots) * slot_elems + roff;
+        float* dst = a.state_ring + (size_t)((pos0 + t + 1) % a.n_slots) * slot_elems + roff;
         *reinterpret_cast<float4*>(dst) = make_float4(S[0], S[1], S[2], S[3]);
         *reinterpret_cast<float4*>(dst + 4) = make_float4(S[4], S[5], S[6], S[7]);
         if ((lane & 15) == 0) a.y[((size_t)t * a.n_v + h) * kGHead + row] = yo;
@@ -242,7 +247,8 @@ extern "C" size_t vmi_gdn_layer_workspace_bytes(int T, int hidden, int n_k_heads
     return gdn_layout(T, hidden, n_k_heads, n_v_heads).bytes;
 }
 
-extern "C" int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, int T, int pos0, uint16_t* conv_ring,
+extern "C" int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, int T, int pos0,
+                             const int32_t* pos_device, uint16_t* conv_ring,
                              float* state_ring, int n_slots, uint16_t* out, void* workspace, size_t workspace_bytes,
                              void* stream) {
     vmi::clear_error();
@@ -257,7 +263,7 @@ extern "C" int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, 
     if (D.n_v_heads * kGHead * T > 32768 || D.hidden * T > 32768)
         return vmi::fail(VMI_ERR_UNSUPPORTED, "T too large for the projection GEMV");
     if ((D.bits != 4 && D.bits != 8) || D.group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", D.bits, D.group);
-    if (pos0 < 0) return vmi::fail(VMI_ERR_INVALID, "pos0=%d", pos0);
+    if (!pos_device && pos0 < 0) return vmi::fail(VMI_ERR_INVALID, "pos0=%d", pos0);
     if (n_slots < T + 1) return vmi::fail(VMI_ERR_INVALID, "n_slots=%d must be at least T + 1 = %d", n_slots, T + 1);
     if (!x || !out || !conv_ring || !state_ring || !D.input_norm || !D.conv_weight || !D.A_log || !D.dt_bias ||
         !D.norm_weight)
@@ -275,7 +281,7 @@ extern "C" int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, 
     const int r = D.n_v_heads / D.n_k_heads;
 
     GdnArgs a{};
-    a.T = T; a.pos0 = pos0; a.n_k = D.n_k_heads; a.n_v = D.n_v_heads; a.r = r;
+    a.T = T; a.pos0 = pos0; a.pos_dev = pos_device; a.n_k = D.n_k_heads; a.n_v = D.n_v_heads; a.r = r;
     a.per_g = 2 * kGHead + 2 * r * kGHead;
     a.conv_dim = 2 * D.n_k_heads * kGHead + D.n_v_heads * kGHead;
     a.stride = D.n_k_heads * a.per_g + 2 * D.n_v_heads;

@@ -25,6 +25,8 @@ struct RouteInfo {
     int32_t U;                               // distinct valid slots
     int32_t uslot[kRouteMaxPairs];           // slot of distinct index u (first-appearance order)
     float wt[kRouteMaxPairs][kRouteMaxT];    // combine weight of (u, token): sum of its pairs' scores
+    int32_t jr[kRouteMaxPairs][kRouteMaxT];  // rank j of the token's first pair on u, -1 if none: the
+                                             // token's experts are added in rank order
 };
 
 // Workspace carve-up shared by vmi_fused_moe_slots and vmi_moe_layer.  Expert

@@ -671,14 +671,19 @@ __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, 
     const int U = R.U;
     if (tid == 0) a.route->U = U;
     if (tid < npairs) a.route->uslot[tid] = tid < U ? R.uslot[tid] : -1;
-    // combine weight of (u, t): its pairs' scores in j order
+    // combine weight of (u, t): its pairs' scores in j order; rank of its first pair
     for (int i = tid; i < U * T; i += kThreads) {
         const int u = i / T, t = i - u * T;
         const int s = R.uslot[u];
         float wsum = 0.0f;
+        int jr = -1;
         for (int j = 0; j < k; ++j)
-            if (R.slot[t * k + j] == s) wsum += R.scores[t * k + j];
+            if (R.slot[t * k + j] == s) {
+                wsum += R.scores[t * k + j];
+                if (jr < 0) jr = j;
+            }
         a.route->wt[u][t] = wsum;
+        a.route->jr[u][t] = jr;
     }
     if (tid < npairs && !a.from_slots) {
         if (a.ids_out) a.ids_out[tid] = R.ids[tid];
@@ -800,6 +805,9 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     // main MFMAs: m-th load pair covers groups 2m (K blocks 0-1) and 2m+1 (2-3)
     const int par = lane >> 5;  // PACK: D rows 8..15 (lanes 32..63) hold the odd group
     float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // without PACK the odd groups accumulate apart and meet the even ones at the
+    // end, as the two lane halves do with PACK: the same rounding for every T
+    float accg1[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
     const int tk = PACK ? (r & 7) : r;
     const bool xreal = PACK ? (((q < 2) == (r < 8)) && tk < T) : (r < T);
@@ -842,8 +850,10 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
             const float su0 = __uint_as_float(swu << 16), su1 = __uint_as_float(swu & 0xffff0000u);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                accg[e] = fmaf(sg1, dg1[e], fmaf(sg0, dg0[e], accg[e]));
-                accu[e] = fmaf(su1, du1[e], fmaf(su0, du0[e], accu[e]));
+                accg[e] = fmaf(sg0, dg0[e], accg[e]);
+                accu[e] = fmaf(su0, du0[e], accu[e]);
+                accg1[e] = fmaf(sg1, dg1[e], accg1[e]);
+                accu1[e] = fmaf(su1, du1[e], accu1[e]);
             }
         }
     }
@@ -864,6 +874,9 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
         if constexpr (PACK) {
             tg += __shfl_xor(tg, 32, VMI_WAVE);
             tu += __shfl_xor(tu, 32, VMI_WAVE);
+        } else {
+            tg += accg1[e];
+            tu += accu1[e];
         }
         const int t = 4 * tq + e;
         if ((!PACK || tq < 2) && t < T) {
@@ -956,7 +969,9 @@ __global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
     __shared__ uint4 s_zero[64];
     __shared__ float s_axs[NW][P][TB * 8];
     __shared__ float s_wt[NW][P][16];
-    __shared__ float s_red[NW][4][VMI_WAVE];
+    __shared__ int32_t s_jr[NW][P][16];
+    // weighted expert outputs of the 16 rows by (token, rank): routed ranks 0..k-1, shared at k
+    __shared__ float s_pair[vmi::kRouteMaxPairs + vmi::kRouteMaxT][16];
     const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     const int q = lane >> 4, r = lane & 15;
     const int T = a.T, H = a.H, I = a.I, I8 = I / 8, NGd = I / 64;
@@ -968,13 +983,14 @@ __global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
     const int tk = PACK ? (r & 7) : r;
     const bool areal = PACK ? (((q < 2) == (r < 8)) && tk < T) : (r < T);
     if (tid < 64) s_zero[tid] = make_uint4(0u, 0u, 0u, 0u);
+    const int kk1 = a.npairs / a.T + 1;  // ranks per token, the shared expert last
+    for (int i = tid; i < a.T * kk1 * 16; i += NW * VMI_WAVE) (&s_pair[0][0])[i] = 0.0f;
     __syncthreads();
     const int hs = a.has_shared;
     const int nmax = hs + a.npairs;  // experts the list can hold; distinct slots past U read -1
     const int nact = T * I8;         // activation words of one expert
     const int nax = T * NGd;         // activation sums of one expert
     const uint32_t rowoff = (uint32_t)h * NGd * 2u;
-    float wsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int e0 = w; e0 < nmax; e0 += NW * P) {
         // ---- slots of the chunk (lane j < P), one vector load
         const int ej = e0 + NW * lane;
@@ -1006,6 +1022,7 @@ __global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
                     if (n * 64 < nax && n * 64 + lane < nax) VMI_LDS_DMA4(xsrc + n * 64 + lane, &s_axs[w][j][n * 64]);
                 const float* wsrc = sh ? a.sg_logit : &a.route->wt[sh ? 0 : e - hs][0];
                 if (lane < T && (!sh || a.has_sgate)) VMI_LDS_DMA4(wsrc + lane, &s_wt[w][j][0]);
+                if (lane < T && !sh) VMI_LDS_DMA4(&a.route->jr[e - hs][0] + lane, &s_jr[w][j][0]);
             }
         }
         vmi_u4 W[P][NMD];
@@ -1038,6 +1055,7 @@ __global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
             // lane's activation words: 16m + 4q + j4 of token tk, or the zero block
             const uint4* abase = areal ? &s_act[w][j][tk * I8 + 4 * q] : &s_zero[0];
             float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            float y1[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // odd groups without PACK (see k_gateup)
 #pragma unroll
             for (int m = 0; m < NMD; ++m) {
                 // the odd group of the last load does not exist when NGd is odd
@@ -1068,7 +1086,10 @@ __global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
                     }
                     const float sc0 = __uint_as_float(swm << 16), sc1 = __uint_as_float(swm & 0xffff0000u);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) y[i] = fmaf(sc1, d1[i], fmaf(sc0, d0[i], y[i]));
+                    for (int i = 0; i < 4; ++i) {
+                        y[i] = fmaf(sc0, d0[i], y[i]);
+                        y1[i] = fmaf(sc1, d1[i], y1[i]);
+                    }
                 }
             }
             // affine bias and the 128-offset correction: lane block q carries groups 2q, 2q+1
@@ -1082,25 +1103,28 @@ __global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
             const vmi_f4 ds = vmi_mfma_bf16(ab2, bias_b_operand(sq), zf);
             const float4 wr4 = *reinterpret_cast<const float4*>(&s_wt[w][j][tt0]);
             const float wr[4] = {wr4.x, wr4.y, wr4.z, wr4.w};
+            const int4 jr4 = *reinterpret_cast<const int4*>(&s_jr[w][j][tt0]);
+            const int jrv[4] = {jr4.x, jr4.y, jr4.z, jr4.w};
+            const bool writer = !PACK || q < 2;  // PACK: lanes q and q ^ 2 hold the same sum
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float v = y[i];
                 if constexpr (PACK) v += __shfl_xor(v, 32, VMI_WAVE);
+                else v += y1[i];
                 const float g = sh ? (a.has_sgate ? 1.0f / (1.0f + expf(-wr[i])) : 1.0f) : wr[i];
-                const float wt = (tt0 + i < T) ? g : 0.0f;
-                wsum[i] = fmaf(wt, fmaf(-128.0f, ds[i], v + db[i]), wsum[i]);
+                const int t = tt0 + i;
+                const int rank = sh ? kk1 - 1 : jrv[i];
+                if (writer && t < T && rank >= 0) s_pair[t * kk1 + rank][r] = g * fmaf(-128.0f, ds[i], v + db[i]);
             }
         }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s_red[w][i][lane] = wsum[i];
     __syncthreads();
+    // each token's experts in rank order, then the shared expert: the sum does
+    // not depend on the other tokens of the batch
     if (tid < 16 * T) {
         const int t = tid >> 4, rr = tid & 15;
-        const int l = 16 * (t >> 2) + rr, i = t & 3;
         float acc = 0.0f;
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) acc += s_red[ww][i][l];
+        for (int jj = 0; jj < kk1; ++jj) acc += s_pair[t * kk1 + jj][rr];
         const size_t o = (size_t)t * H + blockIdx.x * 16 + rr;
         if (a.residual) acc += vmi_bf16_to_f32(a.residual[o]);
         if (a.out_dtype == VMI_BF16)

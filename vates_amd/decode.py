@@ -66,15 +66,17 @@ class SpecModel:
         return [l.attn.new_cache(max_len) if l.attn is not None else
                 l.gdn.new_cache(max_batch) if l.gdn is not None else None for l in self.layers]
 
-    def forward(self, ids: torch.Tensor, caches: list, pos0: int, *, want_logits: bool = False):
-        """ids int32 [T] on the device at positions pos0..; returns (argmax int32 [T],
+    def forward(self, ids: torch.Tensor, caches: list, pos0: int, *, want_logits: bool = False,
+                pos_device: Optional[torch.Tensor] = None):
+        """ids int32 [T] on the device at positions pos0.. (or at the position
+        held by pos_device, int32 [1] on the device); returns (argmax int32 [T],
         pre-norm hidden bf16 [T, H], logits f32 [T, V] or None)."""
         x = rmsnorm(self.embed, None, ids=ids)
         for layer, cache in zip(self.layers, caches):
             if layer.attn is not None:
-                x = layer.attn(x, cache, pos0=pos0)
+                x = layer.attn(x, cache, pos0=pos0, pos_device=pos_device)
             elif layer.gdn is not None:
-                x = layer.gdn(x, cache, pos0=pos0)
+                x = layer.gdn(x, cache, pos0=pos0, pos_device=pos_device)
             x = layer.moe(x, residual=x)
         logits, am, _ = lm_head(x, self.head, self.final_norm, eps=self.eps, want_logits=want_logits)
         return am, x, logits
@@ -159,3 +161,127 @@ def speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: torch.T
     st.seconds = time.perf_counter() - t0
     st.tokens = st.tokens[:n_tokens]
     return st
+
+
+class GraphSpecDecoder:
+    """The speculative decode step of ``speculative_decode`` captured once as a
+    HIP graph and replayed per step, with every position on the device.
+
+    One replay runs: the K draft steps of the MTP layer at MTP positions
+    mtp_len + i; the verify forward of [x, d1..dK] at pos; greedy acceptance
+    (``vmi_accept_greedy``, mode 1); the MTP cache update over all K + 1 rows
+    (main hidden at pos-1..pos+K-1, tokens x, d1..dK) at mtp_len, whose rows
+    past the accepted ones lie beyond the committed length and are written
+    over by the next step; and the commit: pos += accepted, mtp_len += m + 1,
+    x = the last emitted token, H_last = hidden of position pos + m.  The host
+    reads the acceptance record once per step.  Results equal
+    ``speculative_decode`` token for token (the kernels' results do not depend
+    on batch composition).
+    """
+
+    def __init__(self, model: SpecModel, drafter: MTPDrafter, caches: list, K: int = 3, planted: bool = False):
+        """planted: the verify batch takes its drafts from ``self.planted``
+        (int32 [K], written by the host before each replay) instead of the MTP
+        layer's, which still runs and keeps its cache; for drafts from another
+        source and for tests that force acceptance lengths."""
+        if model.mtp is None:
+            raise VmiError("the model has no MTP layer")
+        self.model, self.drafter, self.caches, self.K = model, drafter, caches, K
+        dev = model.embed.device
+        self.dev = dev
+        self.state = torch.zeros(2, dtype=torch.int32, device=dev)     # [pos, mtp_len]
+        self.pos, self.mtp_len = self.state[0:1], self.state[1:2]
+        self.mtp_pos = torch.zeros(K, dtype=torch.int32, device=dev)
+        self.steps_ar = torch.arange(K, dtype=torch.int32, device=dev)
+        self.x = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.H = torch.zeros((1, model.hidden), dtype=torch.bfloat16, device=dev)
+        self.drafts = torch.zeros(K, dtype=torch.int32, device=dev)
+        self.verify = torch.zeros(K + 1, dtype=torch.int32, device=dev)
+        self.hseq = torch.zeros((K + 1, model.hidden), dtype=torch.bfloat16, device=dev)
+        self.rec_buf = torch.zeros(4 + K + 1, dtype=torch.int32, device=dev)
+        self.use_planted = planted
+        self.planted = torch.zeros(K, dtype=torch.int32, device=dev)
+        self.stream = torch.cuda.Stream(device=dev)
+        self.graph = None
+        self.rec = None
+
+    def _step(self) -> torch.Tensor:
+        K, mtp = self.K, self.model.mtp
+        torch.add(self.steps_ar, self.mtp_len, out=self.mtp_pos)
+        h, tok = self.H, self.x
+        for i in range(K):
+            am, h, _ = mtp.step(h, tok, self.drafter.cache, pos_device=self.mtp_pos[i:i + 1])
+            self.drafts[i:i + 1].copy_(am)
+            tok = self.drafts[i:i + 1]
+        if self.use_planted:
+            self.drafts.copy_(self.planted)
+        self.verify[0:1].copy_(self.x)
+        self.verify[1:].copy_(self.drafts)
+        preds, hid, _ = self.model.forward(self.verify, self.caches, 0, pos_device=self.pos)
+        rec = accept_greedy(self.drafts, preds, mode=1, out=self.rec_buf)
+        self.hseq[0:1].copy_(self.H)
+        self.hseq[1:].copy_(hid[:K])
+        mtp.advance(self.hseq, self.verify, self.drafter.cache, pos_device=self.mtp_len)
+        # commit on the device
+        self.H.copy_(hid.index_select(0, rec[1:2]))
+        self.x.copy_(torch.gather(rec, 0, (rec[0:1] + 3).long()))
+        self.pos.add_(rec[2:3])
+        self.mtp_len.add_(rec[1:2] + 1)
+        return rec
+
+    def start(self, x: torch.Tensor, H_last: torch.Tensor, pos: int) -> None:
+        """Sets the state: x (int32 [1]) at position pos, H_last [1, H] the
+        hidden of pos - 1; the MTP cache length is the drafter's."""
+        self.x.copy_(x)
+        self.H.copy_(H_last)
+        self.state.copy_(torch.tensor([pos, self.drafter.cache.length], dtype=torch.int32))
+        self.pos_host = pos
+
+    def capture(self) -> None:
+        """Warms the workspaces up on the capture stream, restores the state,
+        and captures one step."""
+        saved = [t.clone() for t in (self.state, self.x, self.H)]
+        self.stream.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(self.stream):
+            self._step()
+        self.stream.synchronize()
+        for t, v in zip((self.state, self.x, self.H), saved):
+            t.copy_(v)
+        torch.cuda.synchronize(self.dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            self.rec = self._step()
+        torch.cuda.synchronize(self.dev)
+
+    def run(self, n_tokens: int, plant=None) -> DecodeStats:
+        """Decodes n_tokens tokens by graph replays.  plant(step, pos) -> K
+        draft tokens for a decoder made with planted=True."""
+        if self.graph is None:
+            self.capture()
+        K = self.K
+        need = self.pos_host + n_tokens + 2 * K + 2  # the last step overshoots by < K + 1 and writes K + 1 rows
+        for c in list(self.caches) + [self.drafter.cache]:
+            if isinstance(c, KVCache) and need > c.max_len:
+                raise VmiError(f"cache capacity {c.max_len} < {need} positions needed")
+        st = DecodeStats()
+        t0 = time.perf_counter()
+        pos = self.pos_host
+        while len(st.tokens) < n_tokens:
+            if plant is not None:
+                self.planted.copy_(torch.tensor(plant(st.steps, pos), dtype=torch.int32), non_blocking=False)
+            self.graph.replay()
+            r = self.rec.cpu().tolist()  # the step's one host synchronisation
+            n, m = r[0], r[1]
+            pos += r[2]
+            st.tokens.extend(r[4:4 + n])
+            st.accept_hist.append(m)
+            st.steps += 1
+        st.seconds = time.perf_counter() - t0
+        st.tokens = st.tokens[:n_tokens]
+        pos, mtp_len = self.state.cpu().tolist()
+        self.pos_host = pos
+        for c in self.caches:
+            if c is not None:
+                c.length = pos
+        self.drafter.cache.length = mtp_len
+        return st

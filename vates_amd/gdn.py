@@ -100,10 +100,13 @@ class GatedDeltaNetLayer:
         return GdnCache(self.n_k, self.n_v, max_batch + 1, self.device)
 
     def __call__(self, x: torch.Tensor, cache: GdnCache, *, pos0: Optional[int] = None,
-                 out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+                 out: Optional[torch.Tensor] = None, stream=None,
+                 pos_device: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x bf16 [T, hidden] at positions pos0.. (default: cache.length);
         records the conv inputs and the state after every token, sets
-        cache.length = pos0 + T."""
+        cache.length = pos0 + T.  With pos_device (int32 [1] on the device) the
+        position is read there when the kernels run and cache.length is left
+        to the caller."""
         T = x.shape[0]
         pos0 = cache.length if pos0 is None else pos0
         _require(x, "x", 2, self.device)
@@ -113,8 +116,10 @@ class GatedDeltaNetLayer:
         lib = load()
         ws = workspace(lib.vmi_gdn_layer_workspace_bytes(T, self.hidden, self.n_k, self.n_v), self.device, sh,
                        tag="gdn")
-        rc = lib.vmi_gdn_layer(ctypes.byref(self.desc), x.data_ptr(), T, pos0, cache.conv.data_ptr(),
+        rc = lib.vmi_gdn_layer(ctypes.byref(self.desc), x.data_ptr(), T, pos0,
+                               None if pos_device is None else pos_device.data_ptr(), cache.conv.data_ptr(),
                                cache.state.data_ptr(), cache.n_slots, out.data_ptr(), ws.data_ptr(), ws.numel(), sh)
         check(rc, "vmi_gdn_layer")
-        cache.length = pos0 + T
+        if pos_device is None:
+            cache.length = pos0 + T
         return out

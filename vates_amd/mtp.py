@@ -60,26 +60,29 @@ class MTPLayer:
         self.hidden = w.embed.shape[1]
         self.vocab = w.embed.shape[0]
 
-    def _trunk(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None) -> torch.Tensor:
+    def _trunk(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None,
+               pos_device: Optional[torch.Tensor] = None) -> torch.Tensor:
         T, H = hidden.shape
         cat = torch.empty((T, 2 * H), dtype=torch.bfloat16, device=hidden.device)
         rmsnorm(self.w.embed, self.w.norm_emb, eps=self.w.eps, ids=tokens, out=cat, out_stride=2 * H, stream=stream)
         rmsnorm(hidden, self.w.norm_hid, eps=self.w.eps, out=cat[:, H:], out_stride=2 * H, stream=stream)
         x = torch.empty((T, H), dtype=torch.bfloat16, device=hidden.device)
         qgemv(cat, self.w.fc, out_bf16=x, stream=stream)
-        x = self.w.attn(x, cache, stream=stream)
+        x = self.w.attn(x, cache, stream=stream, pos_device=pos_device)
         x = self.w.moe(x, residual=x, stream=stream)
         return rmsnorm(x, self.w.norm, eps=self.w.eps, stream=stream)
 
     def step(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, *, want_logits: bool = False,
-             stream=None):
-        """(argmax int32 [T], MTP hidden H bf16 [T, H], logits f32 [T, V] or None)."""
-        Hn = self._trunk(hidden, tokens, cache, stream)
+             stream=None, pos_device: Optional[torch.Tensor] = None):
+        """(argmax int32 [T], MTP hidden H bf16 [T, H], logits f32 [T, V] or None).
+        With pos_device the cache position is read on the device."""
+        Hn = self._trunk(hidden, tokens, cache, stream, pos_device)
         logits, am, _ = lm_head(Hn, self.w.lm_head, None, want_logits=want_logits, stream=stream)
         return am, Hn, logits
 
-    def advance(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None) -> torch.Tensor:
-        return self._trunk(hidden, tokens, cache, stream)
+    def advance(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None,
+                pos_device: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return self._trunk(hidden, tokens, cache, stream, pos_device)
 
 
 class MTPDrafter:
