@@ -203,3 +203,29 @@ def test_moe_layer_batch_invariant(gpu, orc, torch_mod, T):
         singles = torch.cat([moe(x[t:t + 1].contiguous(), residual=x[t:t + 1].contiguous()) for t in range(T)])
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), singles.view(torch.int16)), kw
+
+
+def test_moe_layer_router_ties(gpu, orc, torch_mod):
+    """All router logits equal: the top-k is experts 0..k-1, lower index first
+    on ties (the oracle's rule, generate.py:383's convention), in every token."""
+    log("case: moe_layer with tied router logits")
+    torch = torch_mod
+    from vates_amd.synth import synth_bf16
+    from vates_amd.workload import make_layer, synth_layer
+    k, T = 10, 4
+    w = synth_layer(44, 0, device=gpu)
+    w.router.weight.zero_()
+    w.router.scales.zero_()
+    w.router.biases.zero_()
+    moe = make_layer(w, top_k=k)
+    x = synth_bf16(44, 1, (T, 2048), device=gpu)
+    ids = torch.empty((T, k), dtype=torch.int32, device=gpu)
+    sc = torch.empty((T, k), dtype=torch.float32, device=gpu)
+    out = moe(x, residual=x, ids_out=ids, scores_out=sc)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), np.tile(np.arange(k), (T, 1)))
+    np.testing.assert_allclose(sc.cpu().numpy(), 1.0 / k, rtol=1e-6)
+    L = layer_np(w, k, True)
+    ref, _, rid, _, _ = orc.moe_layer(u16(x), L, residual=True)
+    assert np.array_equal(rid, ids.cpu().numpy())
+    assert_moe_close(orc.bf16_to_f32(u16(out).reshape(T, -1)), ref, "tied router")

@@ -484,18 +484,14 @@ __device__ __forceinline__ void cx64(uint64_t& a, uint64_t& b, bool desc) {
 // Lane l holds experts l + 64i (i < NI) as rank keys, sorted descending once
 // (bitonic network); each of the k rounds (a rolled loop: this code runs once
 // per workgroup, so it is kept small for the instruction cache) takes the
-// wave-wide maximum of the lanes' heads and the single winning lane pops its
-// head.  Lane j keeps the j-th selection; exp, the renormalising sum (in j
-// order) and the scores are lane-parallel.
+// wave-wide maximum of the lanes' heads and the winning lane records and pops
+// its head.  Lane j then reads the j-th selection; exp, the renormalising sum
+// (in j order) and the scores are lane-parallel.
 template <int NI>
-__device__ void topk_token(const float* __restrict__ lt, int E, int k, int norm, int t, RouteLds& R) {
+__device__ void topk_token(const float (&v)[NI], int E, int k, int norm, int t, RouteLds& R) {
     const int lane = threadIdx.x & 63;
-    const __amdgpu_buffer_rsrc_t rl = vmi_rsrc(lt, (uint32_t)E * 4u);
     const int nreal = E >> 6;  // E is a multiple of 64: slot i is real for i < E/64 (uniform)
-    float v[NI];
     uint64_t key[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) v[i] = __uint_as_float(vmi_bload_b32(rl, (uint32_t)(lane + 64 * i) * 4u, 0));
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const uint64_t kk = topk_rank_key(v[i], lane + 64 * i);
@@ -510,19 +506,35 @@ __device__ void topk_token(const float* __restrict__ lt, int E, int k, int norm,
                 const int j = i ^ stride;
                 if (j > i) cx64(key[i], key[j], (i & size) == 0);
             }
-    uint64_t my_key = 0ull;
+    // each round: the wave maximum of the 32-bit value keys of the lane heads;
+    // the lane holding it (a ballot names it; equal values fall back to the
+    // full (value, index) key) writes its expert and value into the round's
+    // entry itself, so no key is broadcast
 #pragma unroll 1
     for (int j = 0; j < k; ++j) {
-        const uint64_t M = vmi_wave_max_u64(key[0]);
-        if (key[0] == M) {
+        const uint32_t hv = (uint32_t)(key[0] >> 32);
+        const uint32_t Mv = vmi_wave_max_u32(hv);
+        const uint64_t cand = __ballot(hv == Mv);
+        bool win;
+        if (__popcll(cand) == 1) {
+            win = hv == Mv;
+        } else {
+            const uint64_t M = vmi_wave_max_u64(hv == Mv ? key[0] : 0ull);
+            win = key[0] == M;
+        }
+        if (win) {
+            R.ids[t * k + j] = (int)(0xffffffffu - (uint32_t)key[0]);
+            R.scores[t * k + j] = vmi_order_key_value(hv);
 #pragma unroll
             for (int i = 0; i + 1 < NI; ++i) key[i] = key[i + 1];
             key[NI - 1] = 0ull;
         }
-        if (lane == j) my_key = M;
     }
-    const int my_idx = (int)(0xffffffffu - (uint32_t)my_key);
-    const float my_val = vmi_order_key_value((uint32_t)(my_key >> 32));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int my_idx = lane < k ? R.ids[t * k + lane] : 0;
+    const float my_val = lane < k ? R.scores[t * k + lane] : 0.0f;
     const float mx = vmi_readlane_f32(my_val, 0);
     const bool sel = lane < k;
     const bool bad = __ballot(sel && !(fabsf(my_val) < 3.0e38f)) != 0;
@@ -545,17 +557,49 @@ __device__ void topk_token(const float* __restrict__ lt, int E, int k, int norm,
     if (bad && lane == 0) atomicOr(&R.bad, VMI_STATUS_BAD_ROUTE);
 }
 
-__device__ void topk_dispatch(const float* __restrict__ lt, int E, int k, int norm, int t, RouteLds& R) {
+template <int NI>
+__device__ __forceinline__ void topk_load(const float* __restrict__ lt, int E, float (&v)[NI]) {
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t rl = vmi_rsrc(lt, (uint32_t)E * 4u);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) v[i] = __uint_as_float(vmi_bload_b32(rl, (uint32_t)(lane + 64 * i) * 4u, 0));
+}
+
+// Top-k of every token of the batch (wave w: tokens w, w + 4, ...), with the
+// slot table staged alongside: the first token's logits and the table are
+// loaded together, so their latencies overlap.
+template <int NI>
+__device__ void route_topk(const float* __restrict__ logits, int T, int E, int k, int norm, const int32_t* table,
+                           int32_t* s_table, RouteLds& R) {
+    const int tid = threadIdx.x, w = vmi_wave_id();
+    float v[NI];
+    if (w < T) topk_load<NI>(logits + (size_t)w * E, E, v);
+    if (table) {
+        const __amdgpu_buffer_rsrc_t rt = vmi_rsrc(table, (uint32_t)E * 4u);
+        int32_t tv[kMaxE / kThreads];
+#pragma unroll
+        for (int i = 0; i < kMaxE / kThreads; ++i) tv[i] = (int32_t)vmi_bload_b32(rt, (uint32_t)(tid + kThreads * i) * 4u, 0);
+#pragma unroll
+        for (int i = 0; i < kMaxE / kThreads; ++i) s_table[tid + kThreads * i] = tv[i];
+    }
+    for (int t = w; t < T; t += kThreads / VMI_WAVE) {
+        if (t != w) topk_load<NI>(logits + (size_t)t * E, E, v);
+        topk_token<NI>(v, E, k, norm, t, R);
+    }
+}
+
+__device__ void route_topk_dispatch(const float* __restrict__ logits, int T, int E, int k, int norm,
+                                    const int32_t* table, int32_t* s_table, RouteLds& R) {
     if (E <= 64)
-        topk_token<1>(lt, E, k, norm, t, R);
+        route_topk<1>(logits, T, E, k, norm, table, s_table, R);
     else if (E <= 128)
-        topk_token<2>(lt, E, k, norm, t, R);
+        route_topk<2>(logits, T, E, k, norm, table, s_table, R);
     else if (E <= 256)
-        topk_token<4>(lt, E, k, norm, t, R);
+        route_topk<4>(logits, T, E, k, norm, table, s_table, R);
     else if (E <= 512)
-        topk_token<8>(lt, E, k, norm, t, R);
+        route_topk<8>(logits, T, E, k, norm, table, s_table, R);
     else
-        topk_token<16>(lt, E, k, norm, t, R);
+        route_topk<16>(logits, T, E, k, norm, table, s_table, R);
 }
 
 // Distinct valid slots in first-appearance order over the token-major pair
@@ -635,16 +679,7 @@ __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, 
     const int T = a.T, k = a.k, npairs = a.npairs;
     if (tid == 0) R.bad = 0u;
     if (!a.from_slots) {
-        if (a.table) {
-            const __amdgpu_buffer_rsrc_t rt = vmi_rsrc(a.table, (uint32_t)a.E * 4u);
-            int32_t tv[kMaxE / kThreads];
-#pragma unroll
-            for (int i = 0; i < kMaxE / kThreads; ++i) tv[i] = (int32_t)vmi_bload_b32(rt, (uint32_t)(tid + kThreads * i) * 4u, 0);
-#pragma unroll
-            for (int i = 0; i < kMaxE / kThreads; ++i) s_table[tid + kThreads * i] = tv[i];
-        }
-        for (int t = w; t < T; t += kThreads / VMI_WAVE)
-            topk_dispatch(a.logits + (size_t)t * a.E, a.E, k, a.norm, t, R);
+        route_topk_dispatch(a.logits, T, a.E, k, a.norm, a.table, s_table, R);
         __syncthreads();
         if (tid < npairs) {
             const int id = R.ids[tid];
@@ -719,6 +754,19 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     const bool is_shared = item < nsh;
     const vmi_u4 zero4 = {0u, 0u, 0u, 0u};
 
+    // the MoE input operands do not depend on the routing: issued before it,
+    // so their latency overlaps the router logits'
+    const __amdgpu_buffer_rsrc_t rxo = vmi_rsrc(a.xop, (uint32_t)T * H8 * 16u);
+    vmi_u4 xr[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) xr[i] = vmi_bload_b128(rxo, (uint32_t)(tid + kThreads * i) * 16u, 0);
+    constexpr int XSPT = (kT * NG + kThreads - 1) / kThreads;
+    const __amdgpu_buffer_rsrc_t rxs = vmi_rsrc(a.xsum, (uint32_t)T * NG * 4u);
+    uint32_t xsr[XSPT];
+#pragma unroll
+    for (int i = 0; i < XSPT; ++i) xsr[i] = vmi_bload_b32(rxs, (uint32_t)(tid + kThreads * i) * 4u, 0);
+    const uint32_t fsr = vmi_bload_b32(vmi_rsrc(a.fscale, (uint32_t)T * 4u), (uint32_t)tid * 4u, 0);
+
     int slot = 0, c = item, aidx = a.npairs;
     uint32_t tmask = (1u << T) - 1u;
     if (!is_shared) {
@@ -731,19 +779,9 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
         aidx = u;
     }
 
-    // the MoE input operands, then every weight load of the item (scales,
-    // biases, gate/up words by m): loads retire in issue order, so everything
-    // the arithmetic needs first is issued first
-    const __amdgpu_buffer_rsrc_t rxo = vmi_rsrc(a.xop, (uint32_t)T * H8 * 16u);
-    vmi_u4 xr[XPT];
-#pragma unroll
-    for (int i = 0; i < XPT; ++i) xr[i] = vmi_bload_b128(rxo, (uint32_t)(tid + kThreads * i) * 16u, 0);
-    constexpr int XSPT = (kT * NG + kThreads - 1) / kThreads;
-    const __amdgpu_buffer_rsrc_t rxs = vmi_rsrc(a.xsum, (uint32_t)T * NG * 4u);
-    uint32_t xsr[XSPT];
-#pragma unroll
-    for (int i = 0; i < XSPT; ++i) xsr[i] = vmi_bload_b32(rxs, (uint32_t)(tid + kThreads * i) * 4u, 0);
-    const uint32_t fsr = vmi_bload_b32(vmi_rsrc(a.fscale, (uint32_t)T * 4u), (uint32_t)tid * 4u, 0);
+    // every weight load of the item (scales, biases, gate/up words by m):
+    // loads retire in issue order, so everything the arithmetic needs first is
+    // issued first
     const vmi_qmat mg = is_shared ? a.sh_gate : a.gate;
     const vmi_qmat mu = is_shared ? a.sh_up : a.up;
     const uint32_t wbytes = (uint32_t)I * (H / 2), sbytes = (uint32_t)I * NG * 2u;
@@ -919,6 +957,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
 // --------------------------------------------------------- down + combine
 struct DownArgs {
     int T, H, I, npairs, has_shared, has_sgate;
+    int rpw;                   // output rows per workgroup: 16, or 8 (lanes 8..15 of each tile idle)
     const RouteInfo* route;
     vmi_qmat down, sh_down;
     const vmi_u4* actop;       // [npairs+1, T, I/8] bf16 operands
@@ -975,7 +1014,9 @@ __global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     const int q = lane >> 4, r = lane & 15;
     const int T = a.T, H = a.H, I = a.I, I8 = I / 8, NGd = I / 64;
-    const int h = blockIdx.x * 16 + r;
+    const int RPW = a.rpw;
+    const bool hrow = r < RPW;  // this lane's weight row exists
+    const int h = blockIdx.x * RPW + (hrow ? r : 0);
     const int tq = lane >> 4;
     const int par = PACK ? (tq >> 1) : 0;
     const int tt0 = PACK ? 4 * (tq & 1) : 4 * tq;  // first token of this lane's D rows
@@ -1040,7 +1081,7 @@ __global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
 #pragma unroll
             for (int m = 0; m < NMD; ++m) {
                 const uint32_t off = 64u * m + 16u * q;
-                W[j][m] = vmi_bload_b128(rw, off < (uint32_t)(I / 2) ? (uint32_t)h * (I / 2) + off : VMI_OOB, 0);
+                W[j][m] = vmi_bload_b128(rw, (hrow && off < (uint32_t)(I / 2)) ? (uint32_t)h * (I / 2) + off : VMI_OOB, 0);
             }
             load_group_row<NMD, EVEN>(rs, rowoff, sw[j]);
             load_group_row<NMD, EVEN>(rb, rowoff, bw[j]);
@@ -1114,18 +1155,18 @@ __global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
                 const float g = sh ? (a.has_sgate ? 1.0f / (1.0f + expf(-wr[i])) : 1.0f) : wr[i];
                 const int t = tt0 + i;
                 const int rank = sh ? kk1 - 1 : jrv[i];
-                if (writer && t < T && rank >= 0) s_pair[t * kk1 + rank][r] = g * fmaf(-128.0f, ds[i], v + db[i]);
+                if (writer && hrow && t < T && rank >= 0) s_pair[t * kk1 + rank][r] = g * fmaf(-128.0f, ds[i], v + db[i]);
             }
         }
     }
     __syncthreads();
     // each token's experts in rank order, then the shared expert: the sum does
     // not depend on the other tokens of the batch
-    if (tid < 16 * T) {
-        const int t = tid >> 4, rr = tid & 15;
+    if (tid < RPW * T) {
+        const int t = tid / RPW, rr = tid - t * RPW;
         float acc = 0.0f;
         for (int jj = 0; jj < kk1; ++jj) acc += s_pair[t * kk1 + jj][rr];
-        const size_t o = (size_t)t * H + blockIdx.x * 16 + rr;
+        const size_t o = (size_t)t * H + blockIdx.x * RPW + rr;
         if (a.residual) acc += vmi_bf16_to_f32(a.residual[o]);
         if (a.out_dtype == VMI_BF16)
             reinterpret_cast<uint16_t*>(a.out)[o] = vmi_f32_to_bf16(acc);
@@ -1184,7 +1225,7 @@ hipError_t launch_gateup(const GateUpArgs& ga, int H, hipStream_t s) {
 
 template <bool PACK, int NW, int P, int TB>
 hipError_t launch_downcomb_t(const DownArgs& da, hipStream_t s) {
-    const dim3 grid(da.H / 16), block(NW * VMI_WAVE);
+    const dim3 grid(da.H / da.rpw), block(NW * VMI_WAVE);
     const bool even = (da.I / 64) % 2 == 0;
     switch ((da.I + 127) / 128) {
         case 1:
@@ -1208,7 +1249,11 @@ hipError_t launch_downcomb_t(const DownArgs& da, hipStream_t s) {
 }
 
 // LDS holds NW * P * TB = 128 token rows of activation operands.
-hipError_t launch_downcomb(const DownArgs& da, hipStream_t s) {
+hipError_t launch_downcomb(const DownArgs& dai, hipStream_t s) {
+    // 8 rows per workgroup while that still leaves one workgroup per CU or
+    // fewer (hidden 2048: 256 workgroups), so that every CU streams weights
+    DownArgs da = dai;
+    da.rpw = 16;
     if (da.T <= 4) return launch_downcomb_t<true, 16, 2, 4>(da, s);
     if (da.T <= 8) return launch_downcomb_t<true, 16, 1, 8>(da, s);
     return launch_downcomb_t<false, 8, 1, 16>(da, s);
