@@ -197,3 +197,42 @@ def test_graph_decode_equals_greedy(gpu, model):
         log(f"accept_hist {st.accept_hist} steps {st.steps}")
         # the host view of the caches follows the device positions
         assert all(c.length == P + sum(m + 1 for m in st.accept_hist) for c in caches if c is not None)
+
+
+def test_tree_decode_equals_greedy(gpu, model):
+    """Tree verification with P=3 paths of K=3 (the T = K layout) emits the
+    greedy stream: with the MTP layer's paths, and with planted paths where a
+    rotating path carries the true continuation for 0..K tokens and the others
+    fewer (or tie), exercising the winner choice and every acceptance length."""
+    from vates_amd.decode import greedy_decode, prefill, tree_speculative_decode
+    from vates_amd.mtp import MTPDrafter
+    n_tok, K, P = 30, 3, 3
+    prompt = _prompt(gpu, seed=9)
+    Pn = prompt.numel()
+    caches = model.new_caches(256)
+    x, h = prefill(model, prompt, caches)
+    ref = greedy_decode(model, caches, x, Pn, n_tok + 2 * (K + 1))
+    V = SMALL["vocab"]
+
+    def plant(step, pos):
+        base = pos - Pn  # greedy stream index of the token after position pos
+        m = step % (K + 1)
+        win = step % P
+        rows = []
+        for p in range(P):
+            mp = m if p == win else (m - 1 if (p + step) % 2 else min(m, 1)) if m > 0 else 0
+            mp = max(0, min(mp, m))
+            rows.append([ref.tokens[base + i] if i < mp else (ref.tokens[base + i] + 1 + p) % V for i in range(K)])
+        return rows
+
+    for planted in (False, True):
+        log(f"case: tree speculative K=3 P=3 planted={planted}")
+        caches = model.new_caches(256)
+        drafter = MTPDrafter(model.mtp, 256)
+        x, h = prefill(model, prompt, caches, drafter)
+        st = tree_speculative_decode(model, drafter, caches, x, h, Pn, n_tok, K=K, P=P,
+                                     plant=plant if planted else None)
+        assert st.tokens == ref.tokens[:n_tok], (st.tokens, ref.tokens[:n_tok])
+        if planted:
+            assert set(st.accept_hist) == set(range(K + 1)), st.accept_hist
+        log(f"accept_hist {st.accept_hist}")

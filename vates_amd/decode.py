@@ -163,6 +163,59 @@ def speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: torch.T
     return st
 
 
+def tree_speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: torch.Tensor, H_last: torch.Tensor,
+                            pos: int, n_tokens: int, K: int = 3, P: int = 3, plant=None) -> DecodeStats:
+    """Tree verification (tree_verify_step, generate.py:355-420): the MTP
+    drafter's P paths (draft_paths: top-P first tokens, greedy continuations,
+    drafter.py:150-177), each verified as [x, d1..d_{K-1}] (the T = K layout);
+    the winner is the longest matched prefix, ties to the lower path
+    (vmi_accept_greedy, generate.py:383); emission and accepted length as
+    accept_prefix's T = K rules (generate.py:338-351, 819).
+
+    The paths are verified one after another over the same caches (each
+    writes the same positions; the linear-attention rings keep the state of
+    pos untouched), then the winner's accepted prefix is run once more so the
+    caches hold exactly its entries; the kernels' results do not depend on
+    batch size, so this equals the reference's batched forward and commit of
+    the winner's row (commit_tree_row, kv_cache.py:283-316).  plant(step, pos)
+    -> P x K draft tokens replaces the drafts (tests)."""
+    if model.mtp is None:
+        raise VmiError("the model has no MTP layer")
+    st = DecodeStats()
+    dev = x.device
+    t0 = time.perf_counter()
+    while len(st.tokens) < n_tokens:
+        mtp_start = drafter.cache.length
+        paths = drafter.draft_paths(H_last, x, K, P)           # [P, K]
+        if plant is not None:
+            paths.copy_(torch.tensor(plant(st.steps, pos), dtype=torch.int32))
+        verify = torch.cat([x.view(1, 1).expand(P, 1), paths[:, :K - 1]], dim=1).contiguous()  # [P, K]
+        preds = torch.empty((P, K), dtype=torch.int32, device=dev)
+        hids = []
+        for p in range(P):
+            am, hid, _ = model.forward(verify[p], caches, pos)
+            preds[p].copy_(am)
+            hids.append(hid)
+        rec = accept_greedy(paths, preds, mode=0)
+        r = rec.cpu().tolist()  # the step's one host synchronisation
+        n, m, acc, best = r[0], r[1], r[2], r[3]
+        emitted = r[4:4 + n]
+        # the caches now hold the last path's entries: write the winner's accepted prefix again
+        _, hid_w, _ = model.forward(verify[best, :acc].contiguous(), caches, pos)
+        model.commit(caches, pos + acc)
+        h_seq = torch.cat([H_last, hid_w[:acc - 1]]) if acc > 1 else H_last
+        drafter.sync(mtp_start, h_seq.contiguous(), verify[best, :acc].contiguous())
+        st.tokens.extend(emitted)
+        st.accept_hist.append(m)
+        st.steps += 1
+        pos += acc
+        x = torch.tensor([emitted[-1]], dtype=torch.int32, device=dev)
+        H_last = hid_w[acc - 1:acc].clone()
+    st.seconds = time.perf_counter() - t0
+    st.tokens = st.tokens[:n_tokens]
+    return st
+
+
 class GraphSpecDecoder:
     """The speculative decode step of ``speculative_decode`` captured once as a
     HIP graph and replayed per step, with every position on the device.
