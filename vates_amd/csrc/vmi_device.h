@@ -214,7 +214,53 @@ __device__ __forceinline__ void vmi_lds_dma16_opaque(const void* g, const void* 
     (void)lds;
 #endif
 }
+// The 4-byte form (lane l's dword lands at lds + 4*l), same contract.
+__device__ __forceinline__ void vmi_lds_dma4_opaque(const void* g, const void* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :
+                 : "v"(g), "s"(m0)
+                 : "memory", "m0");
+#else
+    (void)g;
+    (void)lds;
+#endif
+}
 #pragma clang diagnostic pop
+
+// Waits until at most N vector-memory operations of this wave are
+// outstanding.  Loads complete in issue order, so everything issued more than
+// N operations ago has landed.  The builtin form is seen by the compiler's
+// wait-count pass, which then treats the loads it issued itself before the
+// last N as complete; it does not count copies made by inline assembly, so
+// that view is never ahead of the hardware.  gfx9 encoding: vmcnt in bits 3:0
+// and 15:14, expcnt 7 and lgkmcnt 15 (no wait on them).
+#define VMI_VMCNT_IMM(n) ((((n) & 15) | (((n) >> 4) << 14)) | 0x0F70)
+template <int N>
+__device__ __forceinline__ void vmi_vm_wait_c() {
+    constexpr int n = N < 0 ? 0 : (N > 63 ? 63 : N);
+    __builtin_amdgcn_s_waitcnt(VMI_VMCNT_IMM(n));
+}
+// Run-time count (wave-uniform); counts above 15 wait for 15, which only
+// waits longer.
+#define VMI_VMW1(n) case n: __builtin_amdgcn_s_waitcnt(VMI_VMCNT_IMM(n)); break;
+__device__ __forceinline__ void vmi_vm_wait(int n) {
+    n = __builtin_amdgcn_readfirstlane(n < 0 ? 0 : (n > 15 ? 15 : n));
+    switch (n) {
+        VMI_VMW1(0) VMI_VMW1(1) VMI_VMW1(2) VMI_VMW1(3) VMI_VMW1(4) VMI_VMW1(5) VMI_VMW1(6) VMI_VMW1(7)
+        VMI_VMW1(8) VMI_VMW1(9) VMI_VMW1(10) VMI_VMW1(11) VMI_VMW1(12) VMI_VMW1(13) VMI_VMW1(14)
+        default: __builtin_amdgcn_s_waitcnt(VMI_VMCNT_IMM(15)); break;
+    }
+}
+#undef VMI_VMW1
+
+// A wave-uniform int through the scalar cache (s_load).  For data written by
+// an earlier kernel: the scalar cache starts empty in every kernel.
+__device__ __forceinline__ int32_t vmi_sload_i32(const int32_t* p) {
+    return *(const __attribute__((address_space(4))) int32_t*)(uintptr_t)p;
+}
 
 // ---------------------------------------------------------- buffer loads
 // Raw buffer resource over [base, base + bytes): loads past `bytes` return 0.

@@ -957,7 +957,6 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
 // --------------------------------------------------------- down + combine
 struct DownArgs {
     int T, H, I, npairs, has_shared, has_sgate;
-    int rpw;                   // output rows per workgroup: 16, or 8 (lanes 8..15 of each tile idle)
     const RouteInfo* route;
     vmi_qmat down, sh_down;
     const vmi_u4* actop;       // [npairs+1, T, I/8] bf16 operands
@@ -968,206 +967,280 @@ struct DownArgs {
     int out_dtype;
 };
 
-// One quantisation row of a scale or bias matrix (NG = I/64 <= 8 bf16 values)
-// as words: word m holds groups 2m (low half) and 2m+1 (high half).  Exact-size
-// loads, chosen at compile time (NMD = ceil(NG/2); EVEN: NG = 2*NMD).
-template <int NMD, bool EVEN>
-__device__ __forceinline__ void load_group_row(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t (&wv)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) wv[i] = 0u;
-    if constexpr (NMD == 4 && EVEN) {
-        const vmi_u4 v = vmi_bload_b128(rs, off, 0);
-        wv[0] = v[0]; wv[1] = v[1]; wv[2] = v[2]; wv[3] = v[3];
-    } else {
-        constexpr int FULL = EVEN ? NMD : NMD - 1;
-        if constexpr (FULL >= 2) {
-            const uint2 v = vmi_bload_b64(rs, off, 0);
-            wv[0] = v.x; wv[1] = v.y;
-        } else if constexpr (FULL == 1) {
-            wv[0] = vmi_bload_b32(rs, off, 0);
-        }
-        if constexpr (FULL == 3) wv[2] = vmi_bload_b32(rs, off + 8u, 0);
-        if constexpr (!EVEN) wv[NMD - 1] = vmi_bload_b16(rs, off + 4u * (NMD - 1), 0);
-    }
+constexpr int kDnRows = 8;  // output rows per workgroup
+constexpr int kDnWaves = 8;
+constexpr int kDnThreads = kDnWaves * VMI_WAVE;
+constexpr int kDnRanks = kMaxK + 1;  // a token's routed ranks, then the shared expert
+
+// bf16 in the low (hi == false) or high half of a word as fp32, by one v_perm:
+// selector bytes 4..7 pick the word's bytes, 0x0C gives zero.
+__device__ __forceinline__ float bf16_half(uint32_t w, uint32_t sel) {
+    return __uint_as_float(__builtin_amdgcn_perm(w, 0u, sel));
 }
 
-// One workgroup (NW waves) per 16 output rows h0..h0+15.  Wave w takes experts
-// e = w, w+NW, ... of the list [shared (when present), distinct slots in
-// first-appearance order], P at a time: for a chunk every load is issued first
-// - the experts' 16 down rows (16-byte loads, two groups each), scales and
-// biases into registers, their bf16 activation operands, activation sums and
-// combine weights straight into LDS (global_load_lds) - then one wait, then the
-// chunk's MFMAs.  Down weights enter the bf16 MFMA as exact (128 + q); the
-// 128 * sum(act) excess is removed with the affine-bias term.  Per token the
-// wave accumulates weight * (down . act); the waves' sums meet in LDS in wave
-// order, plus the residual.  LDS holds NW * P * TB <= 128 token rows of 64
-// activation words; lanes that carry no token read a zero block.
-template <int NMD, bool EVEN, bool PACK, int NW, int P, int TB>
-__global__ __launch_bounds__(NW * VMI_WAVE, 1) void k_downcomb(DownArgs a) {
-    __shared__ uint4 s_act[NW][P][TB * 64];
-    __shared__ uint4 s_zero[64];
-    __shared__ float s_axs[NW][P][TB * 8];
-    __shared__ float s_wt[NW][P][16];
-    __shared__ int32_t s_jr[NW][P][16];
-    // weighted expert outputs of the 16 rows by (token, rank): routed ranks 0..k-1, shared at k
-    __shared__ float s_pair[vmi::kRouteMaxPairs + vmi::kRouteMaxT][16];
+// One workgroup (8 waves) per 8 output rows h0..h0+7 of the down projection,
+// over every expert of the batch: [shared (when present), distinct slots in
+// first-appearance order].  Wave w takes experts w, w+8, ... of a chunk of
+// 8 PW experts.  Loads, all into registers and in this order:
+//   1. the bf16 activation operands of its experts' tokens (one 16-byte load
+//      per lane and token row); the first chunk's are issued before the route
+//      is read, since an expert's activation block is found from its position
+//      in the list alone;
+//   2. once the slots are known, expert by expert: the 8 weight rows (8 rows x
+//      64 bytes per load), one dword per lane of the rows' scales and biases
+//      and of the activation group sums, combine weights and ranks.
+// The activations then go to the wave's NSLOT LDS slots (an expert past NSLOT
+// keeps its registers until a slot frees), which reorders them into MFMA
+// operand order; the weights stream meanwhile.  Loads complete in issue order, so the
+// compiler's counted waits then release the experts one after another while
+// the rest of the weights stream.
+//
+// MFMA mapping (v_mfma_f32_16x16x32_bf16, lane l = 16q + r, h = r >> 3):
+//   A (weights, exact bf16 128 + n): row r = weight row r & 7 in quantisation
+//     group 2m + h, lane block q holding words 2q + j of that group;
+//   B (activations): column r = token tb + (r & 7) at the same group and words.
+// Rows and columns 0..7 meet on the even group of pair step m and 8..15 on
+// the odd one; D[4q + e][r] is useful when (q >> 1) == h: weight row
+// 4(q & 1) + e, token tb + (r & 7), group 2m + h.  Per group
+//   y += s * (D - 128 X) + b * X,   X = sum of the token's activations in it,
+// accumulated over the even and the odd groups separately (lanes h = 0, 1),
+// each weighted by the combine weight into LDS by (token, rank, half); a
+// token's output adds its ranks in order, the shared expert last, so it does
+// not depend on the other tokens of the batch.
+//
+// TS: token rows per pass (4: T <= 4; 8: T <= 16 in passes of eight tokens).
+template <int NG, int TS, int PW, int NSLOT>
+__global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
+    constexpr int CAP = PW * kDnWaves;    // experts per chunk
+    constexpr int NM2 = (NG + 1) / 2;     // group pairs
+    constexpr int RB = NG * 32;           // bytes of one weight row (I / 2)
+    constexpr int RBA = NG * 128 + 16;    // LDS bytes of one token's activation operands (+ pad)
+    constexpr int TMAX = TS == 4 ? 4 : 16;
+    constexpr int SMW = TMAX * NG + 2 * TMAX;  // dwords of X [T][NG], weights [T], ranks [T]
+    constexpr int NSM = (SMW + 63) / 64;
+    constexpr int NA = (NG * 8 + 63) / 64;     // 16-byte loads per lane of one token row
+    static_assert(8 * NG <= 64, "scales + biases of 8 rows fit one dword per lane");
+    static_assert(PW >= NSLOT && PW <= 2 * NSLOT, "experts past the slots reuse the first slots once");
+    __shared__ __align__(16) uint8_t s_act[kDnWaves][NSLOT][TS * RBA];
+    __shared__ __align__(16) uint8_t s_zero[1024];
+    __shared__ __align__(16) uint32_t s_sb[kDnWaves][64];      // scales [8][NG] then biases [8][NG] (bf16)
+    __shared__ __align__(16) uint32_t s_sm[kDnWaves][NSM * 64];
+    __shared__ __align__(16) float s_pair[TMAX][kDnRanks][2][kDnRows];
+
     const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
-    const int q = lane >> 4, r = lane & 15;
-    const int T = a.T, H = a.H, I = a.I, I8 = I / 8, NGd = I / 64;
-    const int RPW = a.rpw;
-    const bool hrow = r < RPW;  // this lane's weight row exists
-    const int h = blockIdx.x * RPW + (hrow ? r : 0);
-    const int tq = lane >> 4;
-    const int par = PACK ? (tq >> 1) : 0;
-    const int tt0 = PACK ? 4 * (tq & 1) : 4 * tq;  // first token of this lane's D rows
-    const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int tk = PACK ? (r & 7) : r;
-    const bool areal = PACK ? (((q < 2) == (r < 8)) && tk < T) : (r < T);
-    if (tid < 64) s_zero[tid] = make_uint4(0u, 0u, 0u, 0u);
-    const int kk1 = a.npairs / a.T + 1;  // ranks per token, the shared expert last
-    for (int i = tid; i < a.T * kk1 * 16; i += NW * VMI_WAVE) (&s_pair[0][0])[i] = 0.0f;
-    __syncthreads();
+    const int q = lane >> 4, r = lane & 15, h = r >> 3, rho = r & 7;
+    const int p = q >> 1;  // group parity of this lane's D rows
+    const bool useful = p == h;
+    const uint32_t sel = p ? 0x07060C0Cu : 0x05040C0Cu;
+    const int T = a.T, H = a.H, I8 = NG * 8;
+    const int h0 = blockIdx.x * kDnRows;
     const int hs = a.has_shared;
-    const int nmax = hs + a.npairs;  // experts the list can hold; distinct slots past U read -1
-    const int nact = T * I8;         // activation words of one expert
-    const int nax = T * NGd;         // activation sums of one expert
-    const uint32_t rowoff = (uint32_t)h * NGd * 2u;
-    for (int e0 = w; e0 < nmax; e0 += NW * P) {
-        // ---- slots of the chunk (lane j < P), one vector load
-        const int ej = e0 + NW * lane;
-        const int uj = ej - hs;
-        int sl = -1;
-        if (lane < P && ej < nmax) sl = (hs && ej == 0) ? 0 : a.route->uslot[uj];
-        int slot[P];
-        bool ok[P];
+    const int k = a.npairs / T;
+    const int smw = T * NG + 2 * T;
+    const int npass = (T + 7) / 8;
+    const int NEmax = hs + a.npairs;
+    const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    // activation operands of the wave's expert i (list position e), tokens
+    // tb..tb+tpass-1: lane l holds word l (+64c) of each token row
+    vmi_u4 av[PW][TS][NA];
+    auto load_act = [&](int i, int e, int tb, int tpass) {
+        const bool real = e < NEmax;
+        const int aidx = e < hs ? a.npairs : e - hs;
+        const __amdgpu_buffer_rsrc_t ra = vmi_rsrc(a.actop + (real ? ((size_t)aidx * T + tb) * I8 : 0),
+                                                   real ? (uint32_t)tpass * I8 * 16u : 0u);
 #pragma unroll
-        for (int j = 0; j < P; ++j) {
-            slot[j] = __builtin_amdgcn_readlane(sl, j);
-            ok[j] = slot[j] >= 0;
+        for (int t = 0; t < TS; ++t)
+#pragma unroll
+            for (int c = 0; c < NA; ++c)
+                av[i][t][c] = vmi_bload_b128(ra, (64 * c + lane < I8) ? (uint32_t)(t * I8 + 64 * c + lane) * 16u : VMI_OOB, 0);
+    };
+    auto store_act = [&](int i, int slot) {
+        uint8_t* al = &s_act[w][slot][0];
+#pragma unroll
+        for (int t = 0; t < TS; ++t)
+#pragma unroll
+            for (int c = 0; c < NA; ++c)
+                if (64 * c + lane < I8) *reinterpret_cast<vmi_u4*>(al + t * RBA + (64 * c + lane) * 16) = av[i][t][c];
+    };
+    // loads are kept in program order (compiler barriers between experts):
+    // they complete in issue order, which the expert loop relies on
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+        load_act(i, w + kDnWaves * i, 0, min(T, TS));
+        asm volatile("" ::: "memory");
+    }
+    // residual bits (converted at the end)
+    const bool fin = tid < T * kDnRows;
+    const uint32_t resid_bits =
+        vmi_bload_b16(vmi_rsrc(a.residual, a.residual ? (uint32_t)T * H * 2u : 0u),
+                      fin ? (uint32_t)((tid >> 3) * H + h0 + (tid & 7)) * 2u : VMI_OOB, 0);
+    // the route through the scalar cache (written by the previous kernel; the
+    // scalar cache starts empty in every kernel)
+    const int U = vmi_sload_i32(&a.route->U);
+    int slots0[PW];
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+        const int e = w + kDnWaves * i;
+        slots0[i] = (e >= hs && e < NEmax) ? vmi_sload_i32(&a.route->uslot[e - hs]) : 0;
+    }
+    for (int i = tid; i < TMAX * kDnRanks * 2 * kDnRows; i += kDnThreads) (&s_pair[0][0][0][0])[i] = 0.0f;
+    for (int i = tid; i < 1024 / 4; i += kDnThreads) reinterpret_cast<uint32_t*>(s_zero)[i] = 0u;
+    const int NE = hs + U;
+    __syncthreads();
+
+    for (int c0 = 0; c0 < NE; c0 += CAP) {
+        const int nc = min(CAP, NE - c0);
+        const int n = nc > w ? (nc - w + kDnWaves - 1) / kDnWaves : 0;  // this wave's experts (uniform)
+        int slots[PW];
+#pragma unroll
+        for (int i = 0; i < PW; ++i) {
+            const int e = c0 + w + kDnWaves * i;
+            slots[i] = c0 == 0 ? slots0[i] : ((e >= hs && e < NE) ? vmi_sload_i32(&a.route->uslot[e - hs]) : 0);
         }
-        if (!ok[0]) break;  // first-appearance order: nothing valid past an invalid slot
-        // ---- issue: LDS side first, then registers
+        auto expert = [&](int i) { return c0 + w + kDnWaves * i; };
+
+        for (int pass = 0; pass < npass; ++pass) {
+            const int tb = 8 * pass;
+            const int tpass = min(T - tb, TS);  // token rows of this pass
+            if (c0 > 0 || pass > 0) {
 #pragma unroll
-        for (int j = 0; j < P; ++j) {
-            if (ok[j]) {
-                const int e = e0 + NW * j;
-                const bool sh = hs && e == 0;
+                for (int i = 0; i < PW; ++i) {
+                    load_act(i, expert(i), tb, tpass);
+                    asm volatile("" ::: "memory");
+                }
+            }
+            // weights, scales/biases and small operands of every expert of the
+            // chunk, issued before the activations are waited for (loads
+            // complete in issue order, so that wait does not cover them); past
+            // the wave's experts the buffer ranges are empty and the dword loads
+            // read a valid dummy address, so every path issues the same loads and
+            // the compiler's counted waits stay exact
+            uint2 wts[PW][NM2];
+            uint32_t sbv[PW], smv[PW][NSM];
+#pragma unroll
+            for (int i = 0; i < PW; ++i) {
+                const bool real = i < n;
+                const int e = expert(i);
+                const bool sh = e < hs;
                 const int aidx = sh ? a.npairs : e - hs;
-                const vmi_u4* asrc = a.actop + (size_t)aidx * nact;
+                const vmi_qmat md = sh ? a.sh_down : a.down;
+                const int sj = slots[i];
+                const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(
+                    reinterpret_cast<const uint8_t*>(md.w) + (real ? ((size_t)sj * H + h0) * RB : 0), real ? 8u * RB : 0u);
 #pragma unroll
-                for (int n = 0; n < TB; ++n)
-                    if (n * 64 < nact && n * 64 + lane < nact) VMI_LDS_DMA16(asrc + n * 64 + lane, &s_act[w][j][n * 64]);
-                const float* xsrc = a.axs + (size_t)aidx * nax;
-#pragma unroll
-                for (int n = 0; n < (TB * 8 + 63) / 64; ++n)
-                    if (n * 64 < nax && n * 64 + lane < nax) VMI_LDS_DMA4(xsrc + n * 64 + lane, &s_axs[w][j][n * 64]);
-                const float* wsrc = sh ? a.sg_logit : &a.route->wt[sh ? 0 : e - hs][0];
-                if (lane < T && (!sh || a.has_sgate)) VMI_LDS_DMA4(wsrc + lane, &s_wt[w][j][0]);
-                if (lane < T && !sh) VMI_LDS_DMA4(&a.route->jr[e - hs][0] + lane, &s_jr[w][j][0]);
-            }
-        }
-        vmi_u4 W[P][NMD];
-        uint32_t sw[P][4], bw[P][4];
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            const int e = e0 + NW * j;
-            const bool sh = hs && e == 0;
-            const vmi_qmat md = sh ? a.sh_down : a.down;
-            const int sj = ok[j] ? slot[j] : 0;
-            const uint32_t mbytes = ok[j] ? (uint32_t)H * (I / 2) : 0u, gbytes = ok[j] ? (uint32_t)H * NGd * 2u : 0u;
-            const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(md.w + (size_t)sj * H * I8, mbytes);
-            const __amdgpu_buffer_rsrc_t rs = vmi_rsrc(md.s + (size_t)sj * H * NGd, gbytes);
-            const __amdgpu_buffer_rsrc_t rb = vmi_rsrc(md.b + (size_t)sj * H * NGd, gbytes);
-#pragma unroll
-            for (int m = 0; m < NMD; ++m) {
-                const uint32_t off = 64u * m + 16u * q;
-                W[j][m] = vmi_bload_b128(rw, (hrow && off < (uint32_t)(I / 2)) ? (uint32_t)h * (I / 2) + off : VMI_OOB, 0);
-            }
-            load_group_row<NMD, EVEN>(rs, rowoff, sw[j]);
-            load_group_row<NMD, EVEN>(rb, rowoff, bw[j]);
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        // ---- compute the chunk
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            if (!ok[j]) break;
-            const int e = e0 + NW * j;
-            const bool sh = hs && e == 0;
-            // lane's activation words: 16m + 4q + j4 of token tk, or the zero block
-            const uint4* abase = areal ? &s_act[w][j][tk * I8 + 4 * q] : &s_zero[0];
-            float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            float y1[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // odd groups without PACK (see k_gateup)
-#pragma unroll
-            for (int m = 0; m < NMD; ++m) {
-                // the odd group of the last load does not exist when NGd is odd
-                const bool mreal = EVEN || m + 1 < NMD || q < 2;
-                const uint4* ab = mreal ? abase : &s_zero[0];
-                vmi_u4 A[4];
-#pragma unroll
-                for (int j4 = 0; j4 < 4; ++j4) {
-                    const uint4 v4 = ab[16 * m + j4];
-                    A[j4] = vmi_u4{v4.x, v4.y, v4.z, v4.w};
+                for (int m = 0; m < NM2; ++m) {
+                    const int g = 2 * m + h;
+                    wts[i][m] = vmi_bload_b64(rw, g < NG ? (uint32_t)(rho * RB + g * 32 + 8 * q) : VMI_OOB, 0);
                 }
-                const uint32_t swm = sw[j][m];
-                if constexpr (PACK) {
-                    vmi_f4 d = zf;
+                // one dword per lane: lane l < 4NG the scales' dword l, 4NG <= l <
+                // 8NG the biases' dword l - 4NG
+                const uint32_t* sbp = reinterpret_cast<const uint32_t*>(a.axs);
+                if (real && lane < 8 * NG)
+                    sbp = lane < 4 * NG ? reinterpret_cast<const uint32_t*>(md.s + ((size_t)sj * H + h0) * NG) + lane
+                                        : reinterpret_cast<const uint32_t*>(md.b + ((size_t)sj * H + h0) * NG) + (lane - 4 * NG);
+                sbv[i] = *sbp;
+                // X [T][NG], then the combine weights [T] and ranks [T] (the shared
+                // expert: gate logits, no ranks)
 #pragma unroll
-                    for (int j4 = 0; j4 < 4; ++j4) d = vmi_mfma_bf16(A[j4], vmi_unpack_u4_bf16_128(W[j][m][j4]), d);
-                    const float sc = __uint_as_float(par ? (swm & 0xffff0000u) : (swm << 16));
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) y[i] = fmaf(sc, d[i], y[i]);
-                } else {
-                    const vmi_u4 z = {0u, 0u, 0u, 0u};
-                    vmi_f4 d0 = zf, d1 = zf;
-#pragma unroll
-                    for (int j4 = 0; j4 < 4; ++j4) {
-                        const vmi_u4 bq = vmi_unpack_u4_bf16_128(W[j][m][j4]);
-                        d0 = vmi_mfma_bf16(q < 2 ? A[j4] : z, bq, d0);
-                        d1 = vmi_mfma_bf16(q < 2 ? z : A[j4], bq, d1);
+                for (int d = 0; d < NSM; ++d) {
+                    const int idx = 64 * d + lane;
+                    const uint32_t* sp = reinterpret_cast<const uint32_t*>(a.axs);
+                    if (real && idx < smw) {
+                        if (idx < T * NG) {
+                            sp = reinterpret_cast<const uint32_t*>(a.axs + (size_t)aidx * T * NG + idx);
+                        } else if (idx < T * NG + T) {
+                            if (!sh) sp = reinterpret_cast<const uint32_t*>(&a.route->wt[e - hs][idx - T * NG]);
+                            else if (a.has_sgate) sp = reinterpret_cast<const uint32_t*>(a.sg_logit + (idx - T * NG));
+                        } else if (!sh) {
+                            sp = reinterpret_cast<const uint32_t*>(&a.route->jr[e - hs][idx - T * NG - T]);
+                        }
                     }
-                    const float sc0 = __uint_as_float(swm << 16), sc1 = __uint_as_float(swm & 0xffff0000u);
+                    smv[i][d] = *sp;
+                }
+                asm volatile("" ::: "memory");
+            }
+            // the activations landed first: into the LDS slots
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        y[i] = fmaf(sc0, d0[i], y[i]);
-                        y1[i] = fmaf(sc1, d1[i], y1[i]);
+            for (int i = 0; i < NSLOT; ++i) store_act(i, i);
+#pragma unroll
+            for (int i = 0; i < PW; ++i) {
+                if (i >= n) break;
+                const int slot = i % NSLOT;
+                if (i >= NSLOT) store_act(i, slot);  // expert i - NSLOT is done with this slot
+                const int e = expert(i);
+                const bool sh = e < hs;
+                // small operands through the wave's staging area, read back through
+                // the arrays' own type (uint32_t) so that no read can be moved
+                // ahead of these writes
+                s_sb[w][lane] = sbv[i];
+#pragma unroll
+                for (int d = 0; d < NSM; ++d) s_sm[w][64 * d + lane] = smv[i][d];
+                const uint32_t* sbl = &s_sb[w][0];
+                const uint32_t* sml = &s_sm[w][0];
+                const int tok = tb + rho;
+                const int tk = tok < T ? tok : 0;
+                const uint8_t* arow = (rho < tpass) ? &s_act[w][slot][rho * RBA] : s_zero;
+                float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int m = 0; m < NM2; ++m) {
+                    const int g = 2 * m + h;
+                    const uint8_t* ap = (g < NG) ? arow + (8 * g + 2 * q) * 16 : s_zero;
+                    const vmi_u4 a0 = *reinterpret_cast<const vmi_u4*>(ap);
+                    const vmi_u4 a1 = *reinterpret_cast<const vmi_u4*>(ap + 16);
+                    vmi_f4 D = vmi_mfma_bf16(vmi_unpack_u4_bf16_128(wts[i][m].x), a0, zf);
+                    D = vmi_mfma_bf16(vmi_unpack_u4_bf16_128(wts[i][m].y), a1, D);
+                    const int gp = 2 * m + p;
+                    if (gp < NG) {
+                        const float X = __uint_as_float(sml[tk * NG + gp]);
+#pragma unroll
+                        for (int ee = 0; ee < 4; ++ee) {
+                            const int row = 4 * (q & 1) + ee;
+                            float sv, bv;
+                            if constexpr (NG % 2 == 0) {
+                                sv = bf16_half(sbl[row * (NG / 2) + m], sel);
+                                bv = bf16_half(sbl[4 * NG + row * (NG / 2) + m], sel);
+                            } else {
+                                // bf16 element j of the scales (j < 8NG) or biases: word j / 2, half j & 1
+                                const int js = row * NG + gp, jb = 8 * NG + row * NG + gp;
+                                sv = bf16_half(sbl[js >> 1], (js & 1) ? 0x07060C0Cu : 0x05040C0Cu);
+                                bv = bf16_half(sbl[jb >> 1], (jb & 1) ? 0x07060C0Cu : 0x05040C0Cu);
+                            }
+                            y[ee] = fmaf(sv, fmaf(-128.0f, X, D[ee]), fmaf(bv, X, y[ee]));
+                        }
                     }
                 }
-            }
-            // affine bias and the 128-offset correction: lane block q carries groups 2q, 2q+1
-            const int xr = r < T ? r : 0;
-            const float x0 = (r < T && 2 * q < NGd) ? s_axs[w][j][xr * NGd + 2 * q] : 0.0f;
-            const float x1 = (r < T && 2 * q + 1 < NGd) ? s_axs[w][j][xr * NGd + 2 * q + 1] : 0.0f;
-            const vmi_u4 ab2 = bias_a_operand(x0, x1);
-            const uint32_t bq = q == 0 ? bw[j][0] : q == 1 ? bw[j][1] : q == 2 ? bw[j][2] : bw[j][3];
-            const uint32_t sq = q == 0 ? sw[j][0] : q == 1 ? sw[j][1] : q == 2 ? sw[j][2] : sw[j][3];
-            const vmi_f4 db = vmi_mfma_bf16(ab2, bias_b_operand(bq), zf);
-            const vmi_f4 ds = vmi_mfma_bf16(ab2, bias_b_operand(sq), zf);
-            const float4 wr4 = *reinterpret_cast<const float4*>(&s_wt[w][j][tt0]);
-            const float wr[4] = {wr4.x, wr4.y, wr4.z, wr4.w};
-            const int4 jr4 = *reinterpret_cast<const int4*>(&s_jr[w][j][tt0]);
-            const int jrv[4] = {jr4.x, jr4.y, jr4.z, jr4.w};
-            const bool writer = !PACK || q < 2;  // PACK: lanes q and q ^ 2 hold the same sum
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float v = y[i];
-                if constexpr (PACK) v += __shfl_xor(v, 32, VMI_WAVE);
-                else v += y1[i];
-                const float g = sh ? (a.has_sgate ? 1.0f / (1.0f + expf(-wr[i])) : 1.0f) : wr[i];
-                const int t = tt0 + i;
-                const int rank = sh ? kk1 - 1 : jrv[i];
-                if (writer && hrow && t < T && rank >= 0) s_pair[t * kk1 + rank][r] = g * fmaf(-128.0f, ds[i], v + db[i]);
+                if (useful && tok < T) {
+                    float wt;
+                    int rank;
+                    if (sh) {
+                        wt = a.has_sgate ? 1.0f / (1.0f + expf(-__uint_as_float(sml[T * NG + tok]))) : 1.0f;
+                        rank = k;
+                    } else {
+                        wt = __uint_as_float(sml[T * NG + tok]);
+                        rank = (int)sml[T * NG + T + tok];
+                    }
+                    if (rank >= 0) {
+                        float4 v;
+                        v.x = wt * y[0];
+                        v.y = wt * y[1];
+                        v.z = wt * y[2];
+                        v.w = wt * y[3];
+                        *reinterpret_cast<float4*>(&s_pair[tok][rank][h][4 * (q & 1)]) = v;
+                    }
+                }
             }
         }
     }
     __syncthreads();
-    // each token's experts in rank order, then the shared expert: the sum does
-    // not depend on the other tokens of the batch
-    if (tid < RPW * T) {
-        const int t = tid / RPW, rr = tid - t * RPW;
+    // each token's ranks in order (even + odd groups), the shared expert last,
+    // then the residual
+    if (fin) {
+        const int t = tid >> 3, rr = tid & 7;
         float acc = 0.0f;
-        for (int jj = 0; jj < kk1; ++jj) acc += s_pair[t * kk1 + jj][rr];
-        const size_t o = (size_t)t * H + blockIdx.x * RPW + rr;
-        if (a.residual) acc += vmi_bf16_to_f32(a.residual[o]);
+        for (int j = 0; j <= k; ++j) acc += s_pair[t][j][0][rr] + s_pair[t][j][1][rr];
+        acc += vmi_bf16_to_f32(resid_bits);
+        const size_t o = (size_t)t * H + h0 + rr;
         if (a.out_dtype == VMI_BF16)
             reinterpret_cast<uint16_t*>(a.out)[o] = vmi_f32_to_bf16(acc);
         else
@@ -1223,40 +1296,27 @@ hipError_t launch_gateup(const GateUpArgs& ga, int H, hipStream_t s) {
     return ga.T <= 8 ? launch_gateup_t<true>(ga, H, s) : launch_gateup_t<false>(ga, H, s);
 }
 
-template <bool PACK, int NW, int P, int TB>
-hipError_t launch_downcomb_t(const DownArgs& da, hipStream_t s) {
-    const dim3 grid(da.H / da.rpw), block(NW * VMI_WAVE);
-    const bool even = (da.I / 64) % 2 == 0;
-    switch ((da.I + 127) / 128) {
-        case 1:
-            if (even) hipLaunchKernelGGL((k_downcomb<1, true, PACK, NW, P, TB>), grid, block, 0, s, da);
-            else hipLaunchKernelGGL((k_downcomb<1, false, PACK, NW, P, TB>), grid, block, 0, s, da);
-            break;
-        case 2:
-            if (even) hipLaunchKernelGGL((k_downcomb<2, true, PACK, NW, P, TB>), grid, block, 0, s, da);
-            else hipLaunchKernelGGL((k_downcomb<2, false, PACK, NW, P, TB>), grid, block, 0, s, da);
-            break;
-        case 3:
-            if (even) hipLaunchKernelGGL((k_downcomb<3, true, PACK, NW, P, TB>), grid, block, 0, s, da);
-            else hipLaunchKernelGGL((k_downcomb<3, false, PACK, NW, P, TB>), grid, block, 0, s, da);
-            break;
-        default:
-            if (even) hipLaunchKernelGGL((k_downcomb<4, true, PACK, NW, P, TB>), grid, block, 0, s, da);
-            else hipLaunchKernelGGL((k_downcomb<4, false, PACK, NW, P, TB>), grid, block, 0, s, da);
-            break;
+template <int TS, int PW, int NSLOT>
+hipError_t launch_down_t(const DownArgs& da, hipStream_t s) {
+    const dim3 grid(da.H / kDnRows), block(kDnThreads);
+    switch (da.I / 64) {
+        case 1: hipLaunchKernelGGL((k_down_rows<1, TS, PW, NSLOT>), grid, block, 0, s, da); break;
+        case 2: hipLaunchKernelGGL((k_down_rows<2, TS, PW, NSLOT>), grid, block, 0, s, da); break;
+        case 3: hipLaunchKernelGGL((k_down_rows<3, TS, PW, NSLOT>), grid, block, 0, s, da); break;
+        case 4: hipLaunchKernelGGL((k_down_rows<4, TS, PW, NSLOT>), grid, block, 0, s, da); break;
+        case 5: hipLaunchKernelGGL((k_down_rows<5, TS, PW, NSLOT>), grid, block, 0, s, da); break;
+        case 6: hipLaunchKernelGGL((k_down_rows<6, TS, PW, NSLOT>), grid, block, 0, s, da); break;
+        case 7: hipLaunchKernelGGL((k_down_rows<7, TS, PW, NSLOT>), grid, block, 0, s, da); break;
+        default: hipLaunchKernelGGL((k_down_rows<8, TS, PW, NSLOT>), grid, block, 0, s, da); break;
     }
     return hipGetLastError();
 }
 
-// LDS holds NW * P * TB = 128 token rows of activation operands.
-hipError_t launch_downcomb(const DownArgs& dai, hipStream_t s) {
-    // 8 rows per workgroup while that still leaves one workgroup per CU or
-    // fewer (hidden 2048: 256 workgroups), so that every CU streams weights
-    DownArgs da = dai;
-    da.rpw = 16;
-    if (da.T <= 4) return launch_downcomb_t<true, 16, 2, 4>(da, s);
-    if (da.T <= 8) return launch_downcomb_t<true, 16, 1, 8>(da, s);
-    return launch_downcomb_t<false, 8, 1, 16>(da, s);
+// T <= 4: token rows of four, 5 experts a wave (40 per chunk) over 4 LDS
+// slots; larger batches: passes of eight tokens, 2 experts a wave.
+hipError_t launch_downcomb(const DownArgs& da, hipStream_t s) {
+    if (da.T <= 4) return launch_down_t<4, 5, 4>(da, s);
+    return launch_down_t<8, 2, 2>(da, s);
 }
 
 template <typename XT>
