@@ -88,6 +88,25 @@ __device__ __forceinline__ float vmi_readlane_f32(float v, int lane) {
     return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
 }
 
+// Row rotate by 8 inside each 16-lane row (lane r reads lane r ^ 8), written
+// only to lanes 8..15 (banks 2, 3) or 0..7 (banks 0, 1) of each row; the other
+// lanes keep `keep`.
+#define VMI_DPP_ROW_ROR8 0x128
+__device__ __forceinline__ vmi_u4 vmi_row_swap8_hi(const vmi_u4& keep, const vmi_u4& from) {
+    vmi_u4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        o[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)keep[i], (int)from[i], VMI_DPP_ROW_ROR8, 0xF, 0xC, false);
+    return o;
+}
+__device__ __forceinline__ vmi_u4 vmi_row_swap8_lo(const vmi_u4& keep, const vmi_u4& from) {
+    vmi_u4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        o[i] = (uint32_t)__builtin_amdgcn_update_dpp((int)keep[i], (int)from[i], VMI_DPP_ROW_ROR8, 0xF, 0x3, false);
+    return o;
+}
+
 // Wave sum in the canonical tree shared with the CPU oracle: per 16-lane row
 // v += v[l^1]; v += v[l^2]; v += v[half-mirror]; v += v[mirror]; then
 // (R0 + R1) + (R2 + R3) over the rows.  Uniform result.
@@ -272,6 +291,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t vmi_rsrc(const void* base, uin
 #define VMI_OOB 0x80000000u
 __device__ __forceinline__ vmi_u4 vmi_bload_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+    vmi_u4 o;
+    o[0] = v[0];
+    o[1] = v[1];
+    o[2] = v[2];
+    o[3] = v[3];
+    return o;
+}
+// Nontemporal form (streamed data that is read once).
+__device__ __forceinline__ vmi_u4 vmi_bload_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2);
     vmi_u4 o;
     o[0] = v[0];
     o[1] = v[1];

@@ -297,7 +297,9 @@ __device__ void operands_from_lds(const uint4* __restrict__ xn, int H, int t, co
 template <int CPL>
 __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     constexpr int NCH = CPL / 8;  // packed 8-column chunks per lane
-    __shared__ uint4 s_xn[kMaxT][64 * NCH];
+    // token t's normalised input at s_xn + t * 64 * NCH (T * 64 * NCH chunks,
+    // sized at launch so small batches leave the LDS to other workgroups)
+    extern __shared__ uint4 s_xn[];
     const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     const int T = a.T, H = a.H;
     const int G = H / 64;
@@ -351,6 +353,10 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     }
     const uint32_t sv = vmi_bload_b16(rs, (uint32_t)(c0 / 64) * 2u, 0);
     const uint32_t bv = vmi_bload_b16(rb, (uint32_t)(c0 / 64) * 2u, 0);
+    // the logit bias of this row, needed last, issued last
+    const bool has_bias = a.bias != nullptr && row_ok && !is_sg;
+    const float rbias = __uint_as_float(
+        vmi_bload_b32(vmi_rsrc(has_bias ? a.bias : a.logits, has_bias ? 4u * (uint32_t)a.E : 0u), 4u * (uint32_t)r, 0));
     // the MoE input, normalised, for every token into LDS
     for (int t = w; t < T; t += kThreads / VMI_WAVE) {
         uint4 xr[NCH];
@@ -379,7 +385,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
             }
         }
 #pragma unroll
-        for (int ch = 0; ch < NCH; ++ch) s_xn[t][lane * NCH + ch] = xr[ch];
+        for (int ch = 0; ch < NCH; ++ch) s_xn[t * 64 * NCH + lane * NCH + ch] = xr[ch];
     }
     __syncthreads();
     if (row_ok) {
@@ -407,7 +413,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
 #pragma unroll
                 for (int i = 0; i < NCH; ++i) {
                     const int ch = (NCH == 1) ? 0 : ((i + (NCH == 4 ? (lane >> 2) : (lane >> 3))) & (NCH - 1));
-                    const uint4 v = s_xn[t][lane * NCH + ch];
+                    const uint4 v = s_xn[t * 64 * NCH + lane * NCH + ch];
 #pragma unroll
                     for (int cc = 0; cc < NCH; ++cc)
                         if (cc == ch) xr[q][cc] = v;
@@ -435,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
                             a.sg_logit[t] = v[q];
                         } else {
                             float lv = v[q];
-                            if (a.bias) lv = lv + a.bias[row];
+                            if (has_bias) lv = lv + rbias;
                             a.logits[(size_t)t * a.E + row] = lv;
                         }
                     }
@@ -443,7 +449,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
             }
         }
     }
-    if ((int)blockIdx.x < T) operands_from_lds(s_xn[blockIdx.x], H, blockIdx.x, a.ops);
+    if ((int)blockIdx.x < T) operands_from_lds(s_xn + blockIdx.x * 64 * NCH, H, blockIdx.x, a.ops);
 }
 
 // ----------------------------------------------------------- routing
@@ -818,12 +824,40 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
             buw[0] = vmi_bload_b32(rub, boff, 0);
         }
     }
-    const uint32_t woff = row * (uint32_t)(H / 2) + 16u * q;
+    // Weights in whole 128-byte lines, nontemporal: load pair p covers rows
+    // 16w..16w+7 (then +8) x bytes 128p..128p+127, lanes r < 8 taking the even
+    // 64-byte chunk of row r and lanes r >= 8 the odd chunk of row r - 8.  A
+    // row rotate by 8 inside each 16-lane row then gives lane r row r's even
+    // chunk (m = 2p) and odd chunk (m = 2p + 1), the MFMA operand layout.
+    // (The 16-token form keeps 64-byte row pieces: it has no registers to
+    // spare for the second set of load targets.)
+    const uint32_t rowa = (uint32_t)(c * kSlice + 16 * w + (r & 7));
+    const uint32_t woffa = rowa * (uint32_t)(H / 2) + 64u * (uint32_t)(r >> 3) + 16u * q;
+    const uint32_t woffb = woffa + 8u * (uint32_t)(H / 2);
     vmi_u4 wg[NM], wu[NM];
+    if constexpr (!PACK) {
+        const uint32_t woff = row * (uint32_t)(H / 2) + 16u * q;
 #pragma unroll
-    for (int m = 0; m < NM; ++m) {
-        wg[m] = vmi_bload_b128(rgw, woff, 64u * m);
-        wu[m] = vmi_bload_b128(ruw, woff, 64u * m);
+        for (int m = 0; m < NM; ++m) {
+            wg[m] = vmi_bload_b128_nt(rgw, woff, 64u * m);
+            wu[m] = vmi_bload_b128_nt(ruw, woff, 64u * m);
+        }
+    } else {
+        vmi_u4 ga[NM / 2], gb[NM / 2], ua[NM / 2], ub[NM / 2];
+#pragma unroll
+        for (int pp = 0; pp < NM / 2; ++pp) {
+            ga[pp] = vmi_bload_b128_nt(rgw, woffa, 128u * pp);
+            gb[pp] = vmi_bload_b128_nt(rgw, woffb, 128u * pp);
+            ua[pp] = vmi_bload_b128_nt(ruw, woffa, 128u * pp);
+            ub[pp] = vmi_bload_b128_nt(ruw, woffb, 128u * pp);
+        }
+#pragma unroll
+        for (int pp = 0; pp < NM / 2; ++pp) {
+            wg[2 * pp] = vmi_row_swap8_hi(ga[pp], gb[pp]);
+            wg[2 * pp + 1] = vmi_row_swap8_lo(gb[pp], ga[pp]);
+            wu[2 * pp] = vmi_row_swap8_hi(ua[pp], ub[pp]);
+            wu[2 * pp + 1] = vmi_row_swap8_lo(ub[pp], ua[pp]);
+        }
     }
 
     // operands into LDS
@@ -1461,10 +1495,11 @@ extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, 
     if (ra.row_wgs < T) ra.row_wgs = T;  // workgroup t < T writes token t's operands
     ra.logits = ws.logits; ra.sg_logit = ws.sg_logit; ra.ops = ops;
     const dim3 rgrid(ra.row_wgs);
+    const size_t rlds = (size_t)T * (D.hidden / 8) * sizeof(uint4);  // T tokens x H/8 packed chunks
     switch (D.hidden) {
-        case 512: hipLaunchKernelGGL(k_router<8>, rgrid, dim3(kThreads), 0, s, ra); break;
-        case 1024: hipLaunchKernelGGL(k_router<16>, rgrid, dim3(kThreads), 0, s, ra); break;
-        default: hipLaunchKernelGGL(k_router<32>, rgrid, dim3(kThreads), 0, s, ra); break;
+        case 512: hipLaunchKernelGGL(k_router<8>, rgrid, dim3(kThreads), rlds, s, ra); break;
+        case 1024: hipLaunchKernelGGL(k_router<16>, rgrid, dim3(kThreads), rlds, s, ra); break;
+        default: hipLaunchKernelGGL(k_router<32>, rgrid, dim3(kThreads), rlds, s, ra); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return vmi::hip_fail(e, "k_router launch");
