@@ -57,12 +57,17 @@ __device__ __forceinline__ vmi_u4 vmi_unpack_u4_f16(uint32_t w) {
 // exact, in the same slot order as vmi_unpack_u4_f16 (columns
 // {0,4,1,5,2,6,3,7}); the 128 * sum(activation) excess is removed by the
 // caller.  bf16 0x4300 is 128.0 with a mantissa step of 1.
+// The constant sits in a VGPR (materialised once: the asm has no side
+// effects, so repeated copies fold), which lets each word become one
+// v_and_or_b32 (a VOP3 form takes no second literal or SGPR).
 __device__ __forceinline__ vmi_u4 vmi_unpack_u4_bf16_128(uint32_t w) {
+    uint32_t kc;
+    asm("v_mov_b32 %0, 0x43004300" : "=v"(kc));
     vmi_u4 r;
-    r[0] = (w & 0x000F000Fu) | 0x43004300u;
-    r[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-    r[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-    r[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+    r[0] = (w & 0x000F000Fu) | kc;
+    r[1] = ((w >> 4) & 0x000F000Fu) | kc;
+    r[2] = ((w >> 8) & 0x000F000Fu) | kc;
+    r[3] = ((w >> 12) & 0x000F000Fu) | kc;
     return r;
 }
 

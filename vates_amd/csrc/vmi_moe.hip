@@ -2,11 +2,11 @@
 //
 // Three stream-ordered kernels per layer; kernel boundaries carry every
 // cross-workgroup dependency (no fences, no counters, no spin waits):
-//   k_router    router logits, one wave per router row: the optional pre-MoE
-//               RMSNorm is computed once per workgroup into LDS, the logit
-//               accumulates in a fixed fp32 order (bit-identical to the CPU
-//               oracle).  The first T workgroups also write the MoE input in
-//               MFMA operand order.
+//   k_router    router logits, one wave per (router row, token): each wave
+//               normalises its token's input itself (the optional pre-MoE
+//               RMSNorm) and accumulates the logit in a fixed fp32 order
+//               (bit-identical to the CPU oracle).  One spare wave per token
+//               writes the MoE input in MFMA operand order.
 //   k_gateup    one workgroup per (distinct slot, 64-row slice of the
 //               intermediate dimension), shared-expert slices first.  Every
 //               workgroup first routes the batch itself from the logits
@@ -17,7 +17,7 @@
 //               hidden dimension; SwiGLU happens in registers and the slice's
 //               64 activations are written as down-projection MFMA operands
 //               (one quantisation group of down).
-//   k_downcomb  one workgroup per 16 output rows: every distinct slot's down
+//   k_down_rows one workgroup per 8 output rows: every distinct slot's down
 //               projection for those rows, the combine weights, the gated
 //               shared expert and the residual, summed in a fixed order.
 // vmi_fused_moe_slots runs k_prep (operands only) in place of k_router and
@@ -245,84 +245,99 @@ struct RouterArgs {
     const float* bias;
     vmi_qmat sgate;
     int sgbits, has_sgate;
-    int row_wgs;      // workgroups (four router rows each)
+    int row_wgs;      // row groups (four rows each) per token
     float* logits;    // [T, E]
     float* sg_logit;  // [T]
     OperandOut ops;
 };
 
-// MFMA operands of token t from its (normalised) input held in LDS as packed
-// bf16 chunks xn[j] = columns 8j..8j+7 (all 256 threads of the workgroup):
-// the same values, range factor and group sums as write_operands.
-__device__ void operands_from_lds(const uint4* __restrict__ xn, int H, int t, const OperandOut& o) {
-    __shared__ float s_am[kThreads / VMI_WAVE];
-    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
-    const bool active = 8 * tid < H;  // H <= 2048: at most one chunk per thread
-    float v[8];
-    if (active) {
-        unpack_bf16x8(xn[tid], v);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-    }
+// MFMA operands of token t written by one wave from its (normalised) input in
+// registers: lane l holds packed chunks xr[ch] = columns 8(l*NCH + ch) ..
+// +7.  The same values, range factor and group sums as write_operands: each
+// 64-column group's sum runs the butterfly over its 8 chunk sums (strides 1,
+// 2, 4 chunks; within the lane where the stride is below NCH, across lanes
+// above), the same additions up to operand order.
+template <int NCH>
+__device__ __forceinline__ void operands_from_wave(const uint4 (&xr)[NCH], int H, int t, const OperandOut& o) {
+    const int lane = threadIdx.x & 63;
+    float v[NCH][8];
     float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = vmi_wave_max(amax);
-    if (lane == 0) s_am[w] = amax;
-    __syncthreads();
-    float am = s_am[0];
+    for (int ch = 0; ch < NCH; ++ch) {
+        unpack_bf16x8(xr[ch], v[ch]);
 #pragma unroll
-    for (int i = 1; i < kThreads / VMI_WAVE; ++i) am = fmaxf(am, s_am[i]);
-    const float f = vmi_fp16_range_scale(am);
-    float xs = 0.0f;
-    const vmi_u4 op = make_act_operand(v, f, xs);
-    xs += __shfl_xor(xs, 1, VMI_WAVE);
-    xs += __shfl_xor(xs, 2, VMI_WAVE);
-    xs += __shfl_xor(xs, 4, VMI_WAVE);
-    if (active) {
-        o.xop[(size_t)t * (H / 8) + tid] = op;
-        if ((tid & 7) == 0) o.xsum[(size_t)t * (H / 64) + tid / 8] = xs;
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[ch][i]));
     }
-    if (tid == 0) o.fscale[t] = f;
+    amax = vmi_wave_max(amax);
+    const float f = vmi_fp16_range_scale(amax);
+    float xs[NCH];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        xs[ch] = 0.0f;
+        o.xop[(size_t)t * (H / 8) + lane * NCH + ch] = make_act_operand(v[ch], f, xs[ch]);
+    }
+#pragma unroll
+    for (int st = 1; st < 8; st *= 2) {
+        if (st < NCH) {
+            float nx[NCH];
+#pragma unroll
+            for (int ch = 0; ch < NCH; ++ch) nx[ch] = xs[ch] + xs[ch ^ st];
+#pragma unroll
+            for (int ch = 0; ch < NCH; ++ch) xs[ch] = nx[ch];
+        } else {
+#pragma unroll
+            for (int ch = 0; ch < NCH; ++ch) xs[ch] += __shfl_xor(xs[ch], st / NCH, VMI_WAVE);
+        }
+    }
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+        const int k = lane * NCH + ch;
+        if ((k & 7) == 0) o.xsum[(size_t)t * (H / 64) + k / 8] = xs[ch];
+    }
+    if (lane == 0) o.fscale[t] = f;
 }
 
-// Router rows: wave w of workgroup b takes row 4b + w (row E is the
-// shared-expert gate).  Lane l owns columns [l*CPL, (l+1)*CPL), accumulating
-// fmaf(w, x, acc) in column order; the 64 partials meet in the canonical
-// wave-sum tree.  The (normalised) input is built once per workgroup in LDS:
-// wave w normalises tokens w, w+4, ...  The CPU oracle reproduces this order
-// bit for bit (orc_router_logits_f32).  Workgroup b < T also writes token b's
-// MFMA operands from that LDS copy.
+// Router rows for one token per workgroup: workgroup i covers row group b
+// (wave w takes row 4b + w) for token t, where the T workgroups of a row group
+// sit on one XCD (workgroups are dealt to the 8 XCDs round-robin by index), so
+// the rows' weights reach that XCD's L2 once.  Row E is the shared-expert
+// gate; row E + has_sgate (the row groups always cover it) writes token t's
+// MFMA operands instead of a logit.
+// Each wave loads token t's input with lane l owning columns
+// [l*CPL, (l+1)*CPL): the canonical inverse rms, the bf16-rounded normalised
+// input, then fmaf(w, x, acc) in column order; the 64 partials meet in the
+// canonical wave-sum tree.  No LDS and no barrier: a wave depends on nothing
+// but its own loads.  The CPU oracle reproduces this order bit for bit
+// (orc_router_logits_f32).
 template <int CPL>
 __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     constexpr int NCH = CPL / 8;  // packed 8-column chunks per lane
-    // token t's normalised input at s_xn + t * 64 * NCH (T * 64 * NCH chunks,
-    // sized at launch so small batches leave the LDS to other workgroups)
-    extern __shared__ uint4 s_xn[];
-    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
+    const int lane = threadIdx.x & 63, w = vmi_wave_id();
     const int T = a.T, H = a.H;
     const int G = H / 64;
+    const int xcd = (int)blockIdx.x & 7, jb = (int)blockIdx.x >> 3;
+    const int t = jb % T, b = (jb / T) * 8 + xcd;
+    if (b >= a.row_wgs) return;
     const int c0 = lane * CPL;
-    const int row = blockIdx.x * (kThreads / VMI_WAVE) + w;
+    const int row = b * (kThreads / VMI_WAVE) + w;
     const int nrows = a.E + a.has_sgate;
     const bool row_ok = row < nrows;
-    const bool is_sg = row >= a.E;  // wave-uniform
+    const bool is_ops = row == nrows;
+    const bool is_sg = row_ok && row >= a.E;  // wave-uniform
+    if (!row_ok && !is_ops) return;
     const vmi_qmat m = is_sg ? a.sgate : a.router;
     const int bits = is_sg ? a.sgbits : a.rbits;
-    const int r = is_sg ? 0 : row;
-    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
-    // first the input of this wave's first token and the norm weights (the
-    // normalisation needs them), then the router row; the compiler barrier
-    // keeps that issue order (loads retire in order)
-    const __amdgpu_buffer_rsrc_t rx = vmi_rsrc(a.x, (uint32_t)T * H * 2u);
+    const int r = is_sg ? 0 : (row_ok ? row : 0);
+    // the input and the norm weights first (the normalisation needs them),
+    // then the router row; loads retire in issue order
+    const __amdgpu_buffer_rsrc_t rx = vmi_rsrc(a.x + (size_t)t * H, (uint32_t)H * 2u);
     const __amdgpu_buffer_rsrc_t rn = vmi_rsrc(a.norm_w ? a.norm_w : a.x, a.norm_w ? (uint32_t)H * 2u : 0u);
-    uint4 xr0[NCH], nwv[NCH];
+    uint4 xr[NCH], nwv[NCH];
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
-        const vmi_u4 xv = vmi_bload_b128(rx, (w < T) ? (uint32_t)(w * H + c0 + 8 * ch) * 2u : VMI_OOB, 0);
+        const vmi_u4 xv = vmi_bload_b128(rx, (uint32_t)(c0 + 8 * ch) * 2u, 0);
         const vmi_u4 nv = vmi_bload_b128(rn, (uint32_t)(c0 + 8 * ch) * 2u, 0);
-        xr0[ch] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
+        xr[ch] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
         nwv[ch] = make_uint4(nv[0], nv[1], nv[2], nv[3]);
     }
     asm volatile("" ::: "memory");
@@ -357,99 +372,50 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     const bool has_bias = a.bias != nullptr && row_ok && !is_sg;
     const float rbias = __uint_as_float(
         vmi_bload_b32(vmi_rsrc(has_bias ? a.bias : a.logits, has_bias ? 4u * (uint32_t)a.E : 0u), 4u * (uint32_t)r, 0));
-    // the MoE input, normalised, for every token into LDS
-    for (int t = w; t < T; t += kThreads / VMI_WAVE) {
-        uint4 xr[NCH];
+    if (a.norm_w) {
+        const float inv = canonical_inv_rms<NCH>(xr, H, a.eps);
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) {
-            if (t == w) {
-                xr[ch] = xr0[ch];
-            } else {
-                const vmi_u4 xv = vmi_bload_b128(rx, (uint32_t)(t * H + c0 + 8 * ch) * 2u, 0);
-                xr[ch] = make_uint4(xv[0], xv[1], xv[2], xv[3]);
-            }
+            float xf[8], nw[8];
+            unpack_bf16x8(xr[ch], xf);
+            unpack_bf16x8(nwv[ch], nw);
+            uint32_t pk[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                pk[i] = (uint32_t)vmi_f32_to_bf16((xf[2 * i] * inv) * nw[2 * i]) |
+                        ((uint32_t)vmi_f32_to_bf16((xf[2 * i + 1] * inv) * nw[2 * i + 1]) << 16);
+            xr[ch] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         }
-        if (a.norm_w) {
-            const float inv = canonical_inv_rms<NCH>(xr, H, a.eps);
-#pragma unroll
-            for (int ch = 0; ch < NCH; ++ch) {
-                float xf[8], nw[8];
-                unpack_bf16x8(xr[ch], xf);
-                unpack_bf16x8(nwv[ch], nw);
-                uint32_t pk[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    pk[i] = (uint32_t)vmi_f32_to_bf16((xf[2 * i] * inv) * nw[2 * i]) |
-                            ((uint32_t)vmi_f32_to_bf16((xf[2 * i + 1] * inv) * nw[2 * i + 1]) << 16);
-                xr[ch] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-            }
-        }
-#pragma unroll
-        for (int ch = 0; ch < NCH; ++ch) s_xn[t * 64 * NCH + lane * NCH + ch] = xr[ch];
     }
-    __syncthreads();
-    if (row_ok) {
-        // dequantised weights (w = q*s + b is exact in fp32)
-        float wv[CPL];
-        const float sc = vmi_bf16_to_f32(sv), bi = vmi_bf16_to_f32(bv);
+    if (is_ops) {
+        operands_from_wave<NCH>(xr, H, t, a.ops);
+        return;
+    }
+    // dequantised weights (w = q*s + b is exact in fp32), one fmaf chain in column order
+    const float sc = vmi_bf16_to_f32(sv), bi = vmi_bf16_to_f32(bv);
+    float acc = 0.0f;
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) {
+    for (int ch = 0; ch < NCH; ++ch) {
+        float xf[8];
+        unpack_bf16x8(xr[ch], xf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int c = 8 * ch + i;
             const uint32_t qv = (bits == 4) ? (wword[c / 8] >> (4 * (c % 8))) & 15u
                                             : (wword[c / 4] >> (8 * (c % 4))) & 255u;
-            wv[c] = fmaf((float)qv, sc, bi);
-        }
-        // four tokens at a time: four independent fmaf chains, each in column order
-        constexpr int TB = 4;
-        for (int t0 = 0; t0 < T; t0 += TB) {
-            float acc[TB];
-#pragma unroll
-            for (int q = 0; q < TB; ++q) acc[q] = 0.0f;
-            // chunk reads rotated by lane/4 (4 chunks) or lane/8 (2 chunks) to spread LDS banks;
-            // the accumulation itself runs over the chunks in column order below
-            uint4 xr[TB][NCH];
-#pragma unroll
-            for (int q = 0; q < TB; ++q) {
-                const int t = (t0 + q < T) ? t0 + q : t0;
-#pragma unroll
-                for (int i = 0; i < NCH; ++i) {
-                    const int ch = (NCH == 1) ? 0 : ((i + (NCH == 4 ? (lane >> 2) : (lane >> 3))) & (NCH - 1));
-                    const uint4 v = s_xn[t * 64 * NCH + lane * NCH + ch];
-#pragma unroll
-                    for (int cc = 0; cc < NCH; ++cc)
-                        if (cc == ch) xr[q][cc] = v;
-                }
-            }
-#pragma unroll
-            for (int ch = 0; ch < NCH; ++ch) {
-#pragma unroll
-                for (int q = 0; q < TB; ++q) {
-                    float xf[8];
-                    unpack_bf16x8(xr[q][ch], xf);
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) acc[q] = fmaf(wv[8 * ch + i], xf[i], acc[q]);
-                }
-            }
-            float v[TB];
-#pragma unroll
-            for (int q = 0; q < TB; ++q) v[q] = vmi_wave_sum_canon(acc[q]);
-            if (lane == 0) {
-#pragma unroll
-                for (int q = 0; q < TB; ++q) {
-                    const int t = t0 + q;
-                    if (t < T) {
-                        if (is_sg) {
-                            a.sg_logit[t] = v[q];
-                        } else {
-                            float lv = v[q];
-                            if (has_bias) lv = lv + rbias;
-                            a.logits[(size_t)t * a.E + row] = lv;
-                        }
-                    }
-                }
-            }
+            acc = fmaf(fmaf((float)qv, sc, bi), xf[i], acc);
         }
     }
-    if ((int)blockIdx.x < T) operands_from_lds(s_xn + blockIdx.x * 64 * NCH, H, blockIdx.x, a.ops);
+    const float v = vmi_wave_sum_canon(acc);
+    if (lane == 0) {
+        if (is_sg) {
+            a.sg_logit[t] = v;
+        } else {
+            float lv = v;
+            if (has_bias) lv = lv + rbias;
+            a.logits[(size_t)t * a.E + row] = lv;
+        }
+    }
 }
 
 // ----------------------------------------------------------- routing
@@ -678,7 +644,7 @@ struct GateUpArgs {
 };
 
 // Routing of the batch inside one k_gateup workgroup (all threads).  The
-// workgroup `publish` additionally writes the route table for k_downcomb, the
+// workgroup `publish` additionally writes the route table for k_down_rows, the
 // caller's ids/scores and the status bits.
 __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, int32_t* s_first, bool publish) {
     const int tid = threadIdx.x, w = vmi_wave_id();
@@ -1447,7 +1413,7 @@ extern "C" int vmi_fused_moe_slots(const void* x, int x_dtype, const int32_t* lo
     da.actop = ws.actop; da.axs = ws.axs;
     da.residual = nullptr; da.out = out; da.out_dtype = out_dtype;
     e = launch_downcomb(da, s);
-    if (e != hipSuccess) return vmi::hip_fail(e, "k_downcomb launch");
+    if (e != hipSuccess) return vmi::hip_fail(e, "k_down_rows launch");
     return VMI_OK;
 }
 
@@ -1490,16 +1456,17 @@ extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, 
     ra.sgate = has_sgate ? D.shared_expert_gate : D.router;
     ra.sgbits = has_sgate ? D.shared_expert_gate_bits : D.router_bits;
     ra.has_sgate = has_sgate;
+    // row groups of four rows covering the router rows, the shared-expert gate
+    // and one spare row (the wave that writes the MFMA operands), times T
+    // tokens, in whole blocks of 8 groups (one per XCD)
     constexpr int rows_per_wg = kThreads / VMI_WAVE;
-    ra.row_wgs = (D.num_experts + has_sgate + rows_per_wg - 1) / rows_per_wg;
-    if (ra.row_wgs < T) ra.row_wgs = T;  // workgroup t < T writes token t's operands
+    ra.row_wgs = (D.num_experts + has_sgate + 1 + rows_per_wg - 1) / rows_per_wg;
     ra.logits = ws.logits; ra.sg_logit = ws.sg_logit; ra.ops = ops;
-    const dim3 rgrid(ra.row_wgs);
-    const size_t rlds = (size_t)T * (D.hidden / 8) * sizeof(uint4);  // T tokens x H/8 packed chunks
+    const dim3 rgrid((unsigned)(((ra.row_wgs + 7) / 8) * 8 * T));
     switch (D.hidden) {
-        case 512: hipLaunchKernelGGL(k_router<8>, rgrid, dim3(kThreads), rlds, s, ra); break;
-        case 1024: hipLaunchKernelGGL(k_router<16>, rgrid, dim3(kThreads), rlds, s, ra); break;
-        default: hipLaunchKernelGGL(k_router<32>, rgrid, dim3(kThreads), rlds, s, ra); break;
+        case 512: hipLaunchKernelGGL(k_router<8>, rgrid, dim3(kThreads), 0, s, ra); break;
+        case 1024: hipLaunchKernelGGL(k_router<16>, rgrid, dim3(kThreads), 0, s, ra); break;
+        default: hipLaunchKernelGGL(k_router<32>, rgrid, dim3(kThreads), 0, s, ra); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return vmi::hip_fail(e, "k_router launch");
@@ -1524,7 +1491,7 @@ extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, 
     da.actop = ws.actop; da.axs = ws.axs; da.sg_logit = ws.sg_logit;
     da.residual = residual; da.out = out; da.out_dtype = VMI_BF16;
     e = launch_downcomb(da, s);
-    if (e != hipSuccess) return vmi::hip_fail(e, "k_downcomb launch");
+    if (e != hipSuccess) return vmi::hip_fail(e, "k_down_rows launch");
     return VMI_OK;
 }
 
