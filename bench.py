@@ -37,6 +37,16 @@ ROUTER8_BYTES = 512 * 2048 + 2 * 512 * 32 * 2  # 1,114,112
 SGATE8_BYTES = 2048 + 2 * 32 * 2  # 2,176
 SEED = 1234
 ZIPF_S, ZIPF_ALPHA = 1.1, 0.5
+# HBM bytes a layer call of the MoE stack moves, per algorithmic byte, from
+# rocprofv3 counter passes over `--layers 8 --steps 3 --warmup 1 --no-graph`
+# (32 layer calls, 31.42 distinct experts on average, 58,525,824 algorithmic
+# bytes a call): FETCH_SIZE summed over k_router, k_gateup and k_down_rows
+# 29,697.0 KiB a call x 2.000 (a plain copy of 512 MiB reads 262,157 KiB on
+# that counter) plus WRITE_SIZE 227.8 KiB x 1.000 (the copy's 524,288 KiB) =
+# 61,049,661 bytes, i.e. 1.0431 of the algorithmic bytes.
+MOE_TRAFFIC_PER_ALGO_BYTE = 1.0431
+MOE_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over 32 layer calls, scaled by a 512 MiB copy "
+                      "(x2.000 / x1.000): 61,049,661 B against 58,525,824 algorithmic B")
 
 
 def eprint(*a):
@@ -74,6 +84,32 @@ def cpu_baseline(layers_w, x_bank, args, budget_s: float):
     return {"value": round(done_bytes / el / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{done} layer calls ({n_layers} layers x {s} steps, T={args.T}) of the same stack, "
                       f"{el:.1f} s, float64 oracle with OpenMP"}
+
+
+def bench_copy(args) -> int:
+    """Calibration workload for the HBM byte counters: one elementwise pass
+    that reads and writes args.copy_mib MiB (fp32 y = x * 1), repeated
+    args.steps times.  A counter pass over it gives the counter's reading per
+    known byte."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    n = args.copy_mib * (1 << 20) // 4
+    x = torch.ones(n, dtype=torch.float32, device=dev)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        torch.mul(x, 1.0, out=y)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    nbytes = 2 * 4 * n
+    print(json.dumps({"path": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": args.steps,
+                      "us_per_launch": round(ms * 1e3 / args.steps, 3),
+                      "GBps": round(nbytes * args.steps / (ms / 1e3) / 1e9, 1)}), flush=True)
+    return 0
 
 
 def bench_lm_head(args) -> int:
@@ -355,10 +391,12 @@ def main() -> int:
     ap.add_argument("--experts", type=int, default=512)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-baseline-s", type=float, default=15.0)
-    ap.add_argument("--path", choices=["moe", "lm_head", "prefill", "decode"], default="moe",
+    ap.add_argument("--path", choices=["moe", "lm_head", "prefill", "decode", "copy"], default="moe",
                     help="moe: the 48-layer verify stack (default); lm_head: the vocabulary GEMV + argmax; "
                          "prefill: one expert-major MoE layer on a T-token prompt; decode: K=3 MTP speculative "
-                         "decoding end to end")
+                         "decoding end to end; copy: a plain elementwise copy of known size (calibrates the "
+                         "HBM byte counters)")
+    ap.add_argument("--copy-mib", type=int, default=512)
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--new-tokens", type=int, default=512)
     ap.add_argument("--K", type=int, default=3)
@@ -376,6 +414,8 @@ def main() -> int:
         return bench_prefill(args)
     if args.path == "decode":
         return bench_decode(args)
+    if args.path == "copy":
+        return bench_copy(args)
 
     import torch
     from vates_amd.synth import synth_bf16
@@ -491,7 +531,8 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(per_layer_bytes / (per_layer_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": round(MOE_TRAFFIC_PER_ALGO_BYTE * per_layer_bytes) if args.hidden == 2048 and T == 4 else None,
+            "traffic_source": MOE_TRAFFIC_SOURCE if args.hidden == 2048 and T == 4 else None,
             "unit_of_work": "one MoE layer call (router+topk, gate/up, down+combine kernels)",
             "bytes_per_launch": round(per_layer_bytes),
             "us_per_launch": round(per_layer_us, 3),

@@ -1314,7 +1314,7 @@ hipError_t launch_down_t(const DownArgs& da, hipStream_t s) {
 
 // T <= 4: token rows of four, 5 experts a wave (40 per chunk) over 4 LDS
 // slots; larger batches: passes of eight tokens, 2 experts a wave.
-hipError_t launch_downcomb(const DownArgs& da, hipStream_t s) {
+hipError_t launch_down(const DownArgs& da, hipStream_t s) {
     if (da.T <= 4) return launch_down_t<4, 5, 4>(da, s);
     return launch_down_t<8, 2, 2>(da, s);
 }
@@ -1412,7 +1412,7 @@ extern "C" int vmi_fused_moe_slots(const void* x, int x_dtype, const int32_t* lo
     da.route = ws.route; da.down = down; da.sh_down = down;
     da.actop = ws.actop; da.axs = ws.axs;
     da.residual = nullptr; da.out = out; da.out_dtype = out_dtype;
-    e = launch_downcomb(da, s);
+    e = launch_down(da, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "k_down_rows launch");
     return VMI_OK;
 }
@@ -1490,7 +1490,7 @@ extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, 
     da.route = ws.route; da.down = D.down; da.sh_down = has_shared ? D.shared_down : D.down;
     da.actop = ws.actop; da.axs = ws.axs; da.sg_logit = ws.sg_logit;
     da.residual = residual; da.out = out; da.out_dtype = VMI_BF16;
-    e = launch_downcomb(da, s);
+    e = launch_down(da, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "k_down_rows launch");
     return VMI_OK;
 }
