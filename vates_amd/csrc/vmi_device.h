@@ -135,17 +135,23 @@ __device__ __forceinline__ float vmi_wave_max(float v) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
-// Wave-wide maximum of an unsigned 32-bit value (uniform result).
+// Wave-wide maximum of an unsigned 32-bit value (uniform result): the gfx9
+// row-shift / row-broadcast scan, each step one v_max_u32_dpp (0 fills the
+// lanes a shift leaves empty, the identity of an unsigned max), lane 63
+// holding the result.
+template <int CTRL, int RM, int BM>
+__device__ __forceinline__ uint32_t vmi_dpp_u32_z(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, BM, true);
+}
 __device__ __forceinline__ uint32_t vmi_wave_max_u32(uint32_t v) {
-    v = max(v, vmi_dpp_u32<VMI_DPP_XOR1>(v));
-    v = max(v, vmi_dpp_u32<VMI_DPP_XOR2>(v));
-    v = max(v, vmi_dpp_u32<VMI_DPP_HALF_MIRROR>(v));
-    v = max(v, vmi_dpp_u32<VMI_DPP_MIRROR>(v));
-    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
-    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
-    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-    return max(max(r0, r1), max(r2, r3));
+    v = max(v, vmi_dpp_u32_z<0x111, 0xF, 0xF>(v));  // row_shr:1
+    v = max(v, vmi_dpp_u32_z<0x112, 0xF, 0xF>(v));  // row_shr:2
+    v = max(v, vmi_dpp_u32_z<0x113, 0xF, 0xF>(v));  // row_shr:3
+    v = max(v, vmi_dpp_u32_z<0x114, 0xF, 0xE>(v));  // row_shr:4, banks 1..3
+    v = max(v, vmi_dpp_u32_z<0x118, 0xF, 0xC>(v));  // row_shr:8, banks 2..3
+    v = max(v, vmi_dpp_u32_z<0x142, 0xA, 0xF>(v));  // row_bcast:15, rows 1 and 3
+    v = max(v, vmi_dpp_u32_z<0x143, 0xC, 0xF>(v));  // row_bcast:31, rows 2 and 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 __device__ __forceinline__ uint64_t vmi_u64_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
