@@ -299,17 +299,6 @@ __global__ __launch_bounds__(256) void k_topk_rows(TopkArgs a) {
     }
 }
 
-int device_cus() {
-    static int cached = 0;
-    if (cached > 0) return cached;
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                                hipSuccess || cus <= 0)
-        cus = 256;
-    cached = cus;
-    return cached;
-}
-
 }  // namespace
 
 extern "C" size_t vmi_lm_head_workspace_bytes(int T, int vocab) {
@@ -345,7 +334,7 @@ extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t*
         a.partial = reinterpret_cast<uint64_t*>(ws);
         a.counter = reinterpret_cast<uint32_t*>(ws + vmi::align256((size_t)kHeadMaxGrid * kHeadMaxT * sizeof(uint64_t)));
     }
-    int G = device_cus();
+    int G = vmi::device_cus();
     if (G > kHeadMaxGrid) G = kHeadMaxGrid;
     if (G > a.ntiles) G = a.ntiles;
     hipStream_t s = static_cast<hipStream_t>(stream);

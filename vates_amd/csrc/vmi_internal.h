@@ -15,6 +15,7 @@ int hip_fail(hipError_t e, const char* what);
 void clear_error();
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+int device_cus();  // compute units of the current device
 
 constexpr int kRouteMaxPairs = 160;
 constexpr int kRouteMaxT = 16;

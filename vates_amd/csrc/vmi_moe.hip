@@ -643,10 +643,8 @@ struct GateUpArgs {
     float* axs;                   // [npairs+1, T, I/64] their per-group sums
 };
 
-// Routing of the batch inside one k_gateup workgroup (all threads).  The
-// workgroup `publish` additionally writes the route table for k_down_rows, the
-// caller's ids/scores and the status bits.
-__device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, int32_t* s_first, bool publish) {
+// Routing of the batch inside one k_gateup workgroup (all threads).
+__device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, int32_t* s_first) {
     const int tid = threadIdx.x, w = vmi_wave_id();
     const int T = a.T, k = a.k, npairs = a.npairs;
     if (tid == 0) R.bad = 0u;
@@ -674,7 +672,14 @@ __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, 
     }
     __syncthreads();
     dedup_lds(npairs, k, a.cap, R, s_first);
-    if (!publish) return;
+}
+
+// The route table for k_down_rows, the caller's ids/scores and the status
+// bits, written by one routed workgroup once its own work is issued (nothing
+// in this kernel reads them).
+__device__ void publish_route(const GateUpArgs& a, const RouteLds& R) {
+    const int tid = threadIdx.x;
+    const int T = a.T, k = a.k, npairs = a.npairs;
     const int U = R.U;
     if (tid == 0) a.route->U = U;
     if (tid < npairs) a.route->uslot[tid] = tid < U ? R.uslot[tid] : -1;
@@ -742,9 +747,12 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     int slot = 0, c = item, aidx = a.npairs;
     uint32_t tmask = (1u << T) - 1u;
     if (!is_shared) {
-        route_batch(a, R, s_table, s_first, item == nsh);
+        route_batch(a, R, s_table, s_first);
         const int ii = item - nsh, u = ii / NC;
-        if (u >= vmi_uniform(R.U)) return;
+        if (u >= vmi_uniform(R.U)) {
+            if (item == nsh) publish_route(a, R);  // no routed item at all
+            return;
+        }
         c = ii - u * NC;
         slot = vmi_uniform(R.uslot[u]);
         tmask = (uint32_t)vmi_uniform((int)R.umask[u]);
@@ -794,37 +802,39 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     // 16w..16w+7 (then +8) x bytes 128p..128p+127, lanes r < 8 taking the even
     // 64-byte chunk of row r and lanes r >= 8 the odd chunk of row r - 8.  A
     // row rotate by 8 inside each 16-lane row then gives lane r row r's even
-    // chunk (m = 2p) and odd chunk (m = 2p + 1), the MFMA operand layout.
-    // (The 16-token form keeps 64-byte row pieces: it has no registers to
-    // spare for the second set of load targets.)
+    // chunk (m = 2p) and odd chunk (m = 2p + 1), the MFMA operand layout; the
+    // rotates happen at the MFMA that uses them, so the waits for the stream
+    // stay spread over the MFMA loop.  wl[x][2p], wl[x][2p + 1] hold pair p's
+    // two loads of matrix x (0 gate, 1 up).
+    // (The 16-token form keeps 64-byte row pieces, wl[x][m] in operand layout:
+    // it has no registers to spare for the rotates.)
     const uint32_t rowa = (uint32_t)(c * kSlice + 16 * w + (r & 7));
     const uint32_t woffa = rowa * (uint32_t)(H / 2) + 64u * (uint32_t)(r >> 3) + 16u * q;
     const uint32_t woffb = woffa + 8u * (uint32_t)(H / 2);
-    vmi_u4 wg[NM], wu[NM];
+    vmi_u4 wl[2][NM];
     if constexpr (!PACK) {
         const uint32_t woff = row * (uint32_t)(H / 2) + 16u * q;
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-            wg[m] = vmi_bload_b128_nt(rgw, woff, 64u * m);
-            wu[m] = vmi_bload_b128_nt(ruw, woff, 64u * m);
+            wl[0][m] = vmi_bload_b128_nt(rgw, woff, 64u * m);
+            wl[1][m] = vmi_bload_b128_nt(ruw, woff, 64u * m);
         }
     } else {
-        vmi_u4 ga[NM / 2], gb[NM / 2], ua[NM / 2], ub[NM / 2];
 #pragma unroll
         for (int pp = 0; pp < NM / 2; ++pp) {
-            ga[pp] = vmi_bload_b128_nt(rgw, woffa, 128u * pp);
-            gb[pp] = vmi_bload_b128_nt(rgw, woffb, 128u * pp);
-            ua[pp] = vmi_bload_b128_nt(ruw, woffa, 128u * pp);
-            ub[pp] = vmi_bload_b128_nt(ruw, woffb, 128u * pp);
-        }
-#pragma unroll
-        for (int pp = 0; pp < NM / 2; ++pp) {
-            wg[2 * pp] = vmi_row_swap8_hi(ga[pp], gb[pp]);
-            wg[2 * pp + 1] = vmi_row_swap8_lo(gb[pp], ga[pp]);
-            wu[2 * pp] = vmi_row_swap8_hi(ua[pp], ub[pp]);
-            wu[2 * pp + 1] = vmi_row_swap8_lo(ub[pp], ua[pp]);
+            wl[0][2 * pp] = vmi_bload_b128_nt(rgw, woffa, 128u * pp);
+            wl[0][2 * pp + 1] = vmi_bload_b128_nt(rgw, woffb, 128u * pp);
+            wl[1][2 * pp] = vmi_bload_b128_nt(ruw, woffa, 128u * pp);
+            wl[1][2 * pp + 1] = vmi_bload_b128_nt(ruw, woffb, 128u * pp);
         }
     }
+    auto woperand = [&](int x, int m) -> vmi_u4 {
+        if constexpr (!PACK) return wl[x][m];
+        return (m & 1) ? vmi_row_swap8_lo(wl[x][m], wl[x][m - 1]) : vmi_row_swap8_hi(wl[x][m], wl[x][m + 1]);
+    };
+
+    // the first routed workgroup publishes the route while its weights stream
+    if (item == nsh && !is_shared) publish_route(a, R);
 
     // operands into LDS
 #pragma unroll
@@ -852,6 +862,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     const int tkc = tk < T ? tk : 0;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
+        const vmi_u4 wgm = woperand(0, m), wum = woperand(1, m);
         vmi_u4 ax[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -863,8 +874,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
             vmi_f4 dg = zf, du = zf;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                dg = vmi_mfma_f16(ax[j], vmi_unpack_u4_f16(wg[m][j]), dg);
-                du = vmi_mfma_f16(ax[j], vmi_unpack_u4_f16(wu[m][j]), du);
+                dg = vmi_mfma_f16(ax[j], vmi_unpack_u4_f16(wgm[j]), dg);
+                du = vmi_mfma_f16(ax[j], vmi_unpack_u4_f16(wum[j]), du);
             }
             const float sgf = __uint_as_float(par ? (swg & 0xffff0000u) : (swg << 16));
             const float suf = __uint_as_float(par ? (swu & 0xffff0000u) : (swu << 16));
@@ -878,7 +889,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const vmi_u4 a0 = q < 2 ? ax[j] : zero4, a1 = q < 2 ? zero4 : ax[j];
-                const vmi_u4 bg = vmi_unpack_u4_f16(wg[m][j]), bu = vmi_unpack_u4_f16(wu[m][j]);
+                const vmi_u4 bg = vmi_unpack_u4_f16(wgm[j]), bu = vmi_unpack_u4_f16(wum[j]);
                 dg0 = vmi_mfma_f16(a0, bg, dg0);
                 dg1 = vmi_mfma_f16(a1, bg, dg1);
                 du0 = vmi_mfma_f16(a0, bu, du0);

@@ -26,6 +26,18 @@ int hip_fail(hipError_t e, const char* what) {
 
 void clear_error() { g_err[0] = 0; }
 
+// Compute units of the current device (queried once per device).
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] > 0) return cached[dev];
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+    return cus;
+}
+
 }  // namespace vmi
 
 extern "C" const char* vmi_last_error(void) { return g_err; }
