@@ -557,6 +557,16 @@ constexpr int kQ4Waves = 8;
 constexpr int kQ4Threads = 64 * kQ4Waves;
 constexpr int kQ4Kw = 512;  // columns per wave
 
+// NORM: x is first RMS-normalised (a.norm_w): the workgroup stages the T
+// input rows and the norm weights in LDS, wave t computes token t's inverse
+// rms in the canonical order (lane L of 64 owns columns [L*cpl, (L+1)*cpl),
+// x^2 summed with fmaf in column order, the canonical wave-sum tree, then
+// 1/sqrt(ss/K + eps) correctly rounded) and rewrites the row as
+// bf16((x * inv) * w) in place - what k_rms_rows writes - and every wave reads
+// its operands from there.
+constexpr int kQ4MaxK = 2048;  // widest K the NORM form stages
+
+template <bool NORM>
 __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     __shared__ float s_X[kQ4Waves][kQgMaxT][8];       // group sums of x per wave: [token][group of the wave]
     __shared__ float s_part[kQ4Waves][16][kQgMaxT];
@@ -570,24 +580,93 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     int mi = 0, r = nn;
     while (mi < 2 && r >= a.rows[mi]) r -= a.rows[mi++];
     const vmi_qmat M = a.m[mi];
+    // A operands: token tk, columns kw*512 + 128 m + 32 q4 + 8 j .. + 7
+    const int tk = nl & 7;
+    const bool xreal = ((q4 < 2) == (nl < 8)) && tk < T;
+    uint4 xu[4][4];
+    constexpr int NXW = NORM ? kQgMaxT * kQ4MaxK / 8 / kQ4Threads : 1;
+    vmi_u4 xw[NXW], nw;
+    if constexpr (NORM) {
+        // the T input rows and the norm weights as 16-byte words, first: the
+        // norm waits for them, and loads complete in issue order
+        const __amdgpu_buffer_rsrc_t rx = vmi_rsrc(a.x, (uint32_t)(T * K / 8) * 16u);
+        const __amdgpu_buffer_rsrc_t rn = vmi_rsrc(a.norm_w, (uint32_t)(K / 8) * 16u);
+#pragma unroll
+        for (int d = 0; d < NXW; ++d) xw[d] = vmi_bload_b128(rx, (uint32_t)(tid + kQ4Threads * d) * 16u, 0);
+        nw = vmi_bload_b128(rn, (uint32_t)tid * 16u, 0);
+        asm volatile("" ::: "memory");
+    }
     const uint4* wrow = reinterpret_cast<const uint4*>(M.w + (size_t)r * (K / 8));
     uint4 wv[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) wv[m] = wrow[kw * 16 + 4 * m + q4];
     const uint4 sv = *reinterpret_cast<const uint4*>(M.s + (size_t)r * G + kw * 8);
     const uint4 bv = *reinterpret_cast<const uint4*>(M.b + (size_t)r * G + kw * 8);
-    // A operands: token tk, columns kw*512 + 128 m + 32 q4 + 8 j .. + 7
-    const int tk = nl & 7;
-    const bool xreal = ((q4 < 2) == (nl < 8)) && tk < T;
+    // the residual of this thread's output (first pass of the final loop),
+    // issued now so that its latency overlaps the weights'
+    const int nout = tiles * 16 * T;
+    float res0 = 0.0f;
+    if (a.out_bf16 && a.residual && tid < nout) {
+        const int row0 = (blockIdx.x * tiles + tid / (16 * T)) * 16 + (tid / T) % 16;
+        if (row0 < a.nrows) res0 = vmi_bf16_to_f32(a.residual[(size_t)(tid % T) * a.out_stride + row0]);
+    }
+    if constexpr (NORM) {
+        // the rows into LDS, wave t normalises token t there, every wave then
+        // reads its operands (the weights keep streaming meanwhile)
+        __shared__ uint4 s_xn[kQgMaxT * kQ4MaxK / 8];
+        __shared__ uint4 s_nw[kQ4MaxK / 8];
+        const int nxw = T * K / 8, nnw = K / 8;
+#pragma unroll
+        for (int d = 0; d < NXW; ++d) {
+            const int i = tid + kQ4Threads * d;
+            if (i < nxw) s_xn[i] = make_uint4(xw[d][0], xw[d][1], xw[d][2], xw[d][3]);
+        }
+        if (tid < nnw) s_nw[tid] = make_uint4(nw[0], nw[1], nw[2], nw[3]);
+        __syncthreads();
+        if (w < T) {
+            const int cpl = K / 64, nv = cpl / 8;
+            uint4* row = s_xn + (size_t)w * (K / 8) + lane * nv;
+            float ss = 0.0f;
+            for (int v = 0; v < nv; ++v) {
+                float f[8];
+                bf16x8f(row[v], f);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+            }
+            ss = vmi_wave_sum_canon(ss);
+            const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)K) + a.eps));
+            for (int v = 0; v < nv; ++v) {
+                float f[8], g[8];
+                bf16x8f(row[v], f);
+                bf16x8f(s_nw[lane * nv + v], g);
+                uint32_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    o[i] = (uint32_t)vmi_f32_to_bf16((f[2 * i] * inv) * g[2 * i]) |
+                           ((uint32_t)vmi_f32_to_bf16((f[2 * i + 1] * inv) * g[2 * i + 1]) << 16);
+                row[v] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
+        __syncthreads();
+        const uint4* xr = s_xn + (size_t)(xreal ? tk : 0) * (K / 8) + kw * (kQ4Kw / 8) + 4 * q4;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xu[m][j] = xr[16 * m + j];
+    }
     vmi_u4 ax[4][4];
     float xs[4] = {0.f, 0.f, 0.f, 0.f};
     if (xreal) {
-        const uint4* xr = reinterpret_cast<const uint4*>(a.x + (size_t)tk * K + kw * kQ4Kw) + 4 * q4;
+        const uint4* xg = reinterpret_cast<const uint4*>(a.x + (size_t)tk * K + kw * kQ4Kw) + 4 * q4;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint4 u = xr[16 * m + j];
+                uint4 u;
+                if constexpr (NORM)
+                    u = xu[m][j];
+                else
+                    u = xg[16 * m + j];
                 ax[m][j][0] = (u.x & 0xffffu) | (u.z << 16);
                 ax[m][j][1] = (u.x >> 16) | (u.z & 0xffff0000u);
                 ax[m][j][2] = (u.y & 0xffffu) | (u.w << 16);
@@ -651,7 +730,9 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
         if (row < a.nrows) {
             if (a.out) a.out[(size_t)t * a.out_stride + row] = y;
             if (a.out_bf16) {
-                const float res = a.residual ? vmi_bf16_to_f32(a.residual[(size_t)t * a.out_stride + row]) : 0.0f;
+                const float res = !a.residual ? 0.0f
+                                  : i == tid ? res0
+                                             : vmi_bf16_to_f32(a.residual[(size_t)t * a.out_stride + row]);
                 a.out_bf16[(size_t)t * a.out_stride + row] = vmi_f32_to_bf16(y + res);
             }
         }
@@ -698,9 +779,14 @@ hipError_t vmi::launch_qgemv(const QgemvCall& q, hipStream_t s) {
     for (int i = 0; i < 3; ++i)
         if (q.rows[i] > 0 || i == 0)
             sb_align |= reinterpret_cast<uintptr_t>(q.m[i].s) | reinterpret_cast<uintptr_t>(q.m[i].b);
+    if (q.norm_w && !qgemv_fuses_norm(q)) return hipErrorInvalidValue;
     if (q.bits == 4 && q.K % kQ4Kw == 0 && ks <= kQ4Waves && kQ4Waves % ks == 0 && !(sb_align & 15)) {
         const int rows_per_wg = 16 * (kQ4Waves / ks);
-        hipLaunchKernelGGL(k_qgemv4, dim3((q.nrows + rows_per_wg - 1) / rows_per_wg), dim3(kQ4Threads), 0, s, q);
+        const dim3 grid((q.nrows + rows_per_wg - 1) / rows_per_wg);
+        if (q.norm_w)
+            hipLaunchKernelGGL(k_qgemv4<true>, grid, dim3(kQ4Threads), 0, s, q);
+        else
+            hipLaunchKernelGGL(k_qgemv4<false>, grid, dim3(kQ4Threads), 0, s, q);
     } else {
         const size_t lds = (size_t)q.T * q.K * 2;
         hipLaunchKernelGGL(k_qgemv, dim3((q.nrows + 3) / 4), dim3(kAThreads), lds, s, q);
@@ -713,6 +799,15 @@ hipError_t vmi::launch_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, 
     RmsArgs ra{x, w, eps, T, H, out, nullptr, 0, nullptr, H};
     hipLaunchKernelGGL(k_rms_rows, dim3((T + 3) / 4), dim3(kAThreads), 0, s, ra);
     return hipGetLastError();
+}
+
+bool vmi::qgemv_fuses_norm(const QgemvCall& q) {
+    uintptr_t sb_align = 0;
+    for (int i = 0; i < 3; ++i)
+        if (q.rows[i] > 0 || i == 0)
+            sb_align |= reinterpret_cast<uintptr_t>(q.m[i].s) | reinterpret_cast<uintptr_t>(q.m[i].b);
+    return q.bits == 4 && (q.K == 512 || q.K == 1024 || q.K == kQ4MaxK) && q.T <= kQgMaxT && !(sb_align & 15) &&
+           !(reinterpret_cast<uintptr_t>(q.norm_w) & 15);
 }
 
 bool vmi::qmat_ok(const vmi_qmat& m) {
@@ -782,14 +877,19 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     const int stride = D.n_heads * 2 * kHeadDim + 2 * D.n_kv_heads * kHeadDim;
     hipStream_t s = static_cast<hipStream_t>(stream);
 
-    RmsArgs ra{x, D.input_norm, D.norm_eps, T, D.hidden, xn, nullptr, 0, nullptr, D.hidden};
-    hipLaunchKernelGGL(k_rms_rows, dim3((T + 3) / 4), dim3(kAThreads), 0, s, ra);
-
+    // input RMSNorm inside the projection when the GEMV can take it, else its own kernel
     QgArgs q{};
-    q.x = xn; q.T = T; q.K = D.hidden; q.bits = D.bits;
+    q.x = x; q.T = T; q.K = D.hidden; q.bits = D.bits;
     q.m[0] = D.q_proj; q.m[1] = D.k_proj; q.m[2] = D.v_proj;
     q.rows[0] = D.n_heads * 2 * kHeadDim; q.rows[1] = D.n_kv_heads * kHeadDim; q.rows[2] = D.n_kv_heads * kHeadDim;
     q.nrows = stride; q.out = qkv; q.out_stride = stride;
+    q.norm_w = D.input_norm; q.eps = D.norm_eps;
+    if (!vmi::qgemv_fuses_norm(q)) {
+        RmsArgs ra{x, D.input_norm, D.norm_eps, T, D.hidden, xn, nullptr, 0, nullptr, D.hidden};
+        hipLaunchKernelGGL(k_rms_rows, dim3((T + 3) / 4), dim3(kAThreads), 0, s, ra);
+        q.x = xn;
+        q.norm_w = nullptr;
+    }
     hipError_t e = vmi::launch_qgemv(q, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "qkv projection launch");
 

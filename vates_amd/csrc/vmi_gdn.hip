@@ -296,14 +296,20 @@ extern "C" int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, 
     a.o = reinterpret_cast<uint16_t*>(ws + L.o);
     uint16_t* xn = reinterpret_cast<uint16_t*>(ws + L.xn);
 
-    hipError_t e = vmi::launch_rmsnorm(x, D.input_norm, D.norm_eps, T, D.hidden, xn, s);
-    if (e != hipSuccess) return vmi::hip_fail(e, "input norm launch");
-
+    // input RMSNorm inside the projection when the GEMV can take it, else its own kernel
     vmi::QgemvCall q{};
-    q.x = xn; q.T = T; q.K = D.hidden; q.bits = D.bits;
+    q.x = x; q.T = T; q.K = D.hidden; q.bits = D.bits;
     q.m[0] = D.in_proj_qkvz; q.m[1] = D.in_proj_ba; q.m[2] = D.in_proj_ba;
     q.rows[0] = D.n_k_heads * a.per_g; q.rows[1] = 2 * D.n_v_heads; q.rows[2] = 0;
     q.nrows = a.stride; q.out = const_cast<float*>(a.proj); q.out_stride = a.stride;
+    q.norm_w = D.input_norm; q.eps = D.norm_eps;
+    hipError_t e = hipSuccess;
+    if (!vmi::qgemv_fuses_norm(q)) {
+        e = vmi::launch_rmsnorm(x, D.input_norm, D.norm_eps, T, D.hidden, xn, s);
+        if (e != hipSuccess) return vmi::hip_fail(e, "input norm launch");
+        q.x = xn;
+        q.norm_w = nullptr;
+    }
     e = vmi::launch_qgemv(q, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "qkvz/ba projection launch");
 

@@ -60,8 +60,13 @@ struct QgemvCall {
     int out_stride;
     const uint16_t* residual;  // optional [T, out_stride] bf16: out_bf16 = bf16(y + residual)
     uint16_t* out_bf16;        // optional
+    const uint16_t* norm_w;    // optional [K] bf16: x is first RMS-normalised (canonical order)
+    float eps;
 };
 hipError_t launch_qgemv(const QgemvCall& q, hipStream_t s);
+// Whether launch_qgemv can normalise x itself (QgemvCall::norm_w): the MFMA
+// kernel with K in {512, 1024, 2048}.
+bool qgemv_fuses_norm(const QgemvCall& q);
 // bf16 RMSNorm of T rows of width H (H % 512 == 0) into out (stride H).
 hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int T, int H, uint16_t* out, hipStream_t s);
 // Non-null, 16-byte aligned packed weights.
