@@ -577,9 +577,21 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     const int tile = w / ks, kw = w % ks;
     const int n = (blockIdx.x * tiles + tile) * 16 + nl;
     const int nn = n < a.nrows ? n : a.nrows - 1;
+    // matrix of row nn, selected from the kernel arguments by value (an
+    // indexed argument would be a dependent vector load before the weights)
     int mi = 0, r = nn;
-    while (mi < 2 && r >= a.rows[mi]) r -= a.rows[mi++];
-    const vmi_qmat M = a.m[mi];
+    if (r >= a.rows[0]) {
+        r -= a.rows[0];
+        mi = 1;
+        if (r >= a.rows[1]) {
+            r -= a.rows[1];
+            mi = 2;
+        }
+    }
+    vmi_qmat M;
+    M.w = mi == 0 ? a.m[0].w : mi == 1 ? a.m[1].w : a.m[2].w;
+    M.s = mi == 0 ? a.m[0].s : mi == 1 ? a.m[1].s : a.m[2].s;
+    M.b = mi == 0 ? a.m[0].b : mi == 1 ? a.m[1].b : a.m[2].b;
     // A operands: token tk, columns kw*512 + 128 m + 32 q4 + 8 j .. + 7
     const int tk = nl & 7;
     const bool xreal = ((q4 < 2) == (nl < 8)) && tk < T;
@@ -602,14 +614,18 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     for (int m = 0; m < 4; ++m) wv[m] = wrow[kw * 16 + 4 * m + q4];
     const uint4 sv = *reinterpret_cast<const uint4*>(M.s + (size_t)r * G + kw * 8);
     const uint4 bv = *reinterpret_cast<const uint4*>(M.b + (size_t)r * G + kw * 8);
-    // the residual of this thread's output (first pass of the final loop),
-    // issued now so that its latency overlaps the weights'
+    // the residual of this thread's output (first pass of the final loop) as
+    // raw bf16 bits, issued now so that its latency overlaps the weights'; a
+    // branch-free buffer load whose value is first used at the end, so no
+    // wait on it (and on everything issued before it) lands here
     const int nout = tiles * 16 * T;
-    float res0 = 0.0f;
-    if (a.out_bf16 && a.residual && tid < nout) {
-        const int row0 = (blockIdx.x * tiles + tid / (16 * T)) * 16 + (tid / T) % 16;
-        if (row0 < a.nrows) res0 = vmi_bf16_to_f32(a.residual[(size_t)(tid % T) * a.out_stride + row0]);
-    }
+    // (unconditional: without a residual the range is empty and every lane
+    // reads zero without touching memory)
+    const __amdgpu_buffer_rsrc_t rres =
+        vmi_rsrc(a.residual, a.out_bf16 && a.residual ? (uint32_t)((size_t)T * a.out_stride * 2) : 0u);
+    const int row0 = (blockIdx.x * tiles + tid / (16 * T)) * 16 + (tid / T) % 16;
+    const uint32_t res0 = vmi_bload_b16(
+        rres, tid < nout && row0 < a.nrows ? (uint32_t)(((size_t)(tid % T) * a.out_stride + row0) * 2) : VMI_OOB, 0);
     if constexpr (NORM) {
         // the rows into LDS, wave t normalises token t there, every wave then
         // reads its operands (the weights keep streaming meanwhile)
@@ -622,10 +638,11 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
             if (i < nxw) s_xn[i] = make_uint4(xw[d][0], xw[d][1], xw[d][2], xw[d][3]);
         }
         if (tid < nnw) s_nw[tid] = make_uint4(nw[0], nw[1], nw[2], nw[3]);
+        __shared__ float s_inv[kQgMaxT];
         __syncthreads();
         if (w < T) {
             const int cpl = K / 64, nv = cpl / 8;
-            uint4* row = s_xn + (size_t)w * (K / 8) + lane * nv;
+            const uint4* row = s_xn + (size_t)w * (K / 8) + lane * nv;
             float ss = 0.0f;
             for (int v = 0; v < nv; ++v) {
                 float f[8];
@@ -634,17 +651,24 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
                 for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
             }
             ss = vmi_wave_sum_canon(ss);
-            const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)K) + a.eps));
-            for (int v = 0; v < nv; ++v) {
+            if (lane == 0) s_inv[w] = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)K) + a.eps));
+        }
+        __syncthreads();
+        // every thread rewrites its words of the rows in place
+#pragma unroll
+        for (int d = 0; d < NXW; ++d) {
+            const int i = tid + kQ4Threads * d;
+            if (i < nxw) {
+                const float inv = s_inv[i / (K / 8)];
                 float f[8], g[8];
-                bf16x8f(row[v], f);
-                bf16x8f(s_nw[lane * nv + v], g);
+                bf16x8f(s_xn[i], f);
+                bf16x8f(s_nw[i % (K / 8)], g);
                 uint32_t o[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    o[i] = (uint32_t)vmi_f32_to_bf16((f[2 * i] * inv) * g[2 * i]) |
-                           ((uint32_t)vmi_f32_to_bf16((f[2 * i + 1] * inv) * g[2 * i + 1]) << 16);
-                row[v] = make_uint4(o[0], o[1], o[2], o[3]);
+                for (int e = 0; e < 4; ++e)
+                    o[e] = (uint32_t)vmi_f32_to_bf16((f[2 * e] * inv) * g[2 * e]) |
+                           ((uint32_t)vmi_f32_to_bf16((f[2 * e + 1] * inv) * g[2 * e + 1]) << 16);
+                s_xn[i] = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }
         __syncthreads();
@@ -731,7 +755,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
             if (a.out) a.out[(size_t)t * a.out_stride + row] = y;
             if (a.out_bf16) {
                 const float res = !a.residual ? 0.0f
-                                  : i == tid ? res0
+                                  : i == tid ? __uint_as_float(res0 << 16)
                                              : vmi_bf16_to_f32(a.residual[(size_t)t * a.out_stride + row]);
                 a.out_bf16[(size_t)t * a.out_stride + row] = vmi_f32_to_bf16(y + res);
             }
