@@ -112,6 +112,17 @@ __device__ __forceinline__ vmi_u4 vmi_row_swap8_lo(const vmi_u4& keep, const vmi
     return o;
 }
 
+// Sum over each 16-lane row (the first four steps of the canonical tree
+// below); every lane of a row ends with the same value, since each step adds
+// the same two partial sums on both lanes of a pair.
+__device__ __forceinline__ float vmi_row_sum16(float v) {
+    v = v + vmi_dpp_f32<VMI_DPP_XOR1>(v);
+    v = v + vmi_dpp_f32<VMI_DPP_XOR2>(v);
+    v = v + vmi_dpp_f32<VMI_DPP_HALF_MIRROR>(v);
+    v = v + vmi_dpp_f32<VMI_DPP_MIRROR>(v);
+    return v;
+}
+
 // Wave sum in the canonical tree shared with the CPU oracle: per 16-lane row
 // v += v[l^1]; v += v[l^2]; v += v[half-mirror]; v += v[mirror]; then
 // (R0 + R1) + (R2 + R3) over the rows.  Uniform result.

@@ -18,22 +18,18 @@
 // n_slots >= T + 1 no slot it reads is overwritten.
 //
 // Kernels:
-//   k_rms_rows / k_qgemv (vmi_attn.hip)  input norm; qkvz and ba projections
-//   k_gdn_conv    per (token, head item): conv input rows rounded to bf16 and
-//                 appended to the ring, causal conv of width 4 + SiLU, q/k
-//                 normalisation (rms_norm(., 1e-6) / dk and / sqrt(dk)),
-//                 beta = sigmoid(b), g = exp(-exp(A_log) softplus(a + dt_bias))
-//   k_gdn_delta   per (v-head, 16 state rows): the delta rule over the T tokens
-//                 in fp32, 16 lanes per row; state after each token to the ring
-//   k_gdn_norm    gated RMSNorm per (token, v-head): y / rms * w * silu(z)
-//   k_qgemv       out_proj with the residual add
+//   k_qgemv4 (vmi_attn.hip)  input RMSNorm and the qkvz and ba projections
+//   k_gdn_block   per v-head: causal conv of width 4 + SiLU (conv input rows
+//                 rounded to bf16 and appended to the ring), q/k normalisation,
+//                 gate scalars, the delta rule over the T tokens in fp32 (state
+//                 after each token to the ring), gated RMSNorm
+//   k_qgemv4      out_proj with the residual add
 
 #include "vmi_device.h"
 #include "vmi_internal.h"
 
 namespace {
 
-constexpr int kGThreads = 256;
 constexpr int kGHead = 128;        // head_k_dim = head_v_dim
 constexpr int kConvRing = 32;      // conv ring rows
 constexpr int kConvTaps = 4;
@@ -52,10 +48,6 @@ struct GdnArgs {
     uint16_t* conv_ring;           // [32][conv_dim]
     float* state_ring;             // [n_slots][n_v][128][128]
     int n_slots;
-    float* qk;                     // [T][2 n_k][128]: q heads then k heads, normalised and scaled
-    float* v;                      // [T][n_v][128]
-    float* gb;                     // [T][n_v][2]: (g, beta)
-    float* y;                      // [T][n_v][128]
     const uint16_t* norm_w;        // [128]
     float eps;
     uint16_t* o;                   // [T][n_v * 128] bf16
@@ -74,149 +66,195 @@ __device__ __forceinline__ int gdn_pos0(const GdnArgs& a) { return a.pos_dev ? m
 
 __device__ __forceinline__ float bf16_round(float f) { return vmi_bf16_to_f32(vmi_f32_to_bf16(f)); }
 
-// One wave per (token, item): items 0..2 n_k - 1 are the q then k heads,
-// 2 n_k .. 2 n_k + n_v - 1 the v heads, 2 n_k + n_v the gate scalars.
-// Lane l owns channels l and l + 64 of the head.
-__global__ __launch_bounds__(kGThreads) void k_gdn_conv(GdnArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int items = 2 * a.n_k + a.n_v + 1;
-    const int gid = blockIdx.x * (kGThreads / 64) + g_wave();
-    if (gid >= a.T * items) return;
-    const int t = gid / items, it = gid - t * items;
+// One workgroup of 1024 threads per v-head h (key head hk = h / r), the
+// whole block between the projections in one launch:
+//  1. the conv operands are requested first, then the state rows of the head
+//     (thread: rows tid/16 and tid/16 + 64, dk 4 (tid % 16) .. + 3 and 64 +
+//     the same, so that 16 lanes store 256 contiguous bytes of a row): loads
+//     complete in issue order, so the conv waits for its own operands only
+//     and the state arrives during 2-3;
+//  2. conv: thread c < 384 owns channel c of [q(hk) | k(hk) | v(h)]: its window
+//     of positions pos0-3 .. pos0+T-1 (ring rows before pos0, zeros before
+//     position 0, the batch's projection rounded to bf16), the causal conv of
+//     width 4 and SiLU per token into LDS; the batch rows go to the conv ring
+//     (q/k channels by the first v-head of the group only); threads 384.. the
+//     gate scalars beta = sigmoid(b), g = exp(-exp(A_log) softplus(a + dt_bias));
+//  3. wave 2t + j normalises q (j = 0) or k (j = 1) of token t:
+//     rms_norm(., 1e-6) / dk for q, / sqrt(dk) for k (lane l owns channels l
+//     and l + 64, the canonical wave sum);
+//  4. the delta rule over the T tokens in fp32, 16 lanes per state row (sums
+//     over dk by the DPP row reduction, the same for every batch size, so a
+//     T-token call equals T one-token calls bit for bit); the state after
+//     each token to the ring, the head output y to LDS;
+//  5. wave t: the gated RMSNorm of token t, y / rms * w * silu(z), to bf16.
+constexpr int kGFThreads = 1024;
+constexpr int kGCh = 3 * kGHead;   // conv channels of a workgroup
+
+__device__ __forceinline__ void u4_to_f8(const vmi_u4& lo, const vmi_u4& hi, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[i] = __uint_as_float(lo[i]);
+        f[4 + i] = __uint_as_float(hi[i]);
+    }
+}
+
+__global__ __launch_bounds__(kGFThreads) void k_gdn_block(GdnArgs a) {
+    __shared__ float s_c[kGdnMaxT][kGCh];   // conv outputs per token: q | k | v
+    __shared__ float s_gb[kGdnMaxT][2];     // (g, beta) per token
+    __shared__ float s_y[kGdnMaxT][kGHead];
+    const int tid = threadIdx.x, lane = tid & 63, w = g_wave();
+    const int h = blockIdx.x, hk = h / a.r, T = a.T;
     const int pos0 = gdn_pos0(a);
-    const int pos = pos0 + t;
-    const float* pr = a.proj + (size_t)t * a.stride;
-    if (it == items - 1) {
-        for (int h = lane; h < a.n_v; h += 64) {
-            const float* ba = pr + a.n_k * a.per_g + (h / a.r) * 2 * a.r;
-            const float b = ba[h % a.r], av = ba[a.r + h % a.r];
-            const float x = av + a.dt_bias[h];
+
+    // 1. conv operands, gate inputs and the final norm's z and weights as raw
+    // values (converted after the state loads are issued; lanes without an
+    // operand read zeros from an out-of-range offset), then the state rows (an
+    // empty range reads zeros: nothing before position 0).  Nothing here is
+    // loaded after a store: a load waits for every earlier memory operation.
+    constexpr int NW = kConvTaps - 1 + kGdnMaxT;   // window: positions pos0 - 3 + i
+    const bool conv_wave = w <= kGCh / 64;          // waves 0..5 conv channels, wave 6 the gates
+    const int part = tid / kGHead, ch = tid % kGHead, nq = a.n_k * kGHead;
+    const int c = part == 0 ? hk * kGHead + ch : part == 1 ? nq + hk * kGHead + ch : 2 * nq + h * kGHead + ch;
+    const bool is_ch = tid < kGCh;
+    const int src = conv_src(a, is_ch ? c : 0);
+    const int gt = tid - kGCh;                      // gate token of wave 6's lanes
+    const __amdgpu_buffer_rsrc_t rp = vmi_rsrc(a.proj, (uint32_t)(T * a.stride) * 4u);
+    const __amdgpu_buffer_rsrc_t rr = vmi_rsrc(a.conv_ring, (uint32_t)(kConvRing * a.conv_dim) * 2u);
+    const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(a.conv_w, (uint32_t)(a.conv_dim * kConvTaps) * 2u);
+    const __amdgpu_buffer_rsrc_t rn = vmi_rsrc(a.norm_w, kGHead * 2u);
+    uint32_t rraw[kConvTaps - 1];
+    float praw[kGdnMaxT];
+#pragma unroll
+    for (int i = 0; i < kConvTaps - 1; ++i) {
+        const int p = pos0 - (kConvTaps - 1) + i;
+        rraw[i] = vmi_bload_b16(rr, is_ch && p >= 0 ? (uint32_t)((p % kConvRing) * a.conv_dim + c) * 2u : VMI_OOB, 0);
+    }
+#pragma unroll
+    for (int t = 0; t < kGdnMaxT; ++t)
+        praw[t] = __uint_as_float(vmi_bload_b32(rp, is_ch && t < T ? (uint32_t)(t * a.stride + src) * 4u : VMI_OOB, 0));
+    const uint2 cwraw = vmi_bload_b64(rw, is_ch ? (uint32_t)c * (kConvTaps * 2u) : VMI_OOB, 0);
+    const bool is_gate = gt >= 0 && gt < T;
+    const uint32_t gbase = (uint32_t)(gt * a.stride + a.n_k * a.per_g + hk * 2 * a.r + h % a.r);
+    const float gb_b = __uint_as_float(vmi_bload_b32(rp, is_gate ? gbase * 4u : VMI_OOB, 0));
+    const float gb_a = __uint_as_float(vmi_bload_b32(rp, is_gate ? (gbase + a.r) * 4u : VMI_OOB, 0));
+    const float dtb = a.dt_bias[h], alog = a.A_log[h];
+    // z of token w (wave w < T) and the norm weights of lanes l, l + 64
+    const uint32_t zbase = (uint32_t)(w * a.stride + hk * a.per_g + 2 * kGHead + a.r * kGHead + (h % a.r) * kGHead + lane);
+    const float z0 = __uint_as_float(vmi_bload_b32(rp, w < T ? zbase * 4u : VMI_OOB, 0));
+    const float z1 = __uint_as_float(vmi_bload_b32(rp, w < T ? (zbase + 64u) * 4u : VMI_OOB, 0));
+    const uint32_t nw0 = vmi_bload_b16(rn, (uint32_t)lane * 2u, 0), nw1 = vmi_bload_b16(rn, (uint32_t)(lane + 64) * 2u, 0);
+    asm volatile("" ::: "memory");
+    const int rowA = tid >> 4, d0 = (tid & 15) * 4;
+    const size_t slot_elems = (size_t)a.n_v * kGHead * kGHead;
+    const uint32_t offA = (uint32_t)(((size_t)h * kGHead + rowA) * kGHead + d0) * 4u;
+    const uint32_t offB = offA + 64u * kGHead * 4u;
+    const __amdgpu_buffer_rsrc_t rs =
+        vmi_rsrc(a.state_ring + (size_t)(pos0 % a.n_slots) * slot_elems, pos0 > 0 ? (uint32_t)(slot_elems * 4) : 0u);
+    const vmi_u4 sa0 = vmi_bload_b128(rs, offA, 0), sa1 = vmi_bload_b128(rs, offA + 256u, 0);
+    const vmi_u4 sb0 = vmi_bload_b128(rs, offB, 0), sb1 = vmi_bload_b128(rs, offB + 256u, 0);
+
+    // 2. conv and gate scalars
+    if (conv_wave) {
+        if (is_ch) {
+            float win[NW];
+#pragma unroll
+            for (int i = 0; i < kConvTaps - 1; ++i) win[i] = __uint_as_float(rraw[i] << 16);
+#pragma unroll
+            for (int t = 0; t < kGdnMaxT; ++t) win[kConvTaps - 1 + t] = bf16_round(praw[t]);
+            const float cw[kConvTaps] = {__uint_as_float(cwraw.x << 16), __uint_as_float(cwraw.x & 0xffff0000u),
+                                         __uint_as_float(cwraw.y << 16), __uint_as_float(cwraw.y & 0xffff0000u)};
+            const bool writer = part == 2 || h % a.r == 0;
+#pragma unroll
+            for (int t = 0; t < kGdnMaxT; ++t) {
+                if (t < T) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int tap = 0; tap < kConvTaps; ++tap) acc = fmaf(cw[tap], win[t + tap], acc);
+                    s_c[t][tid] = acc / (1.0f + expf(-acc));
+                    if (writer)
+                        a.conv_ring[(size_t)((pos0 + t) % kConvRing) * a.conv_dim + c] =
+                            vmi_f32_to_bf16(win[kConvTaps - 1 + t]);
+                }
+            }
+        } else if (gt < T) {
+            const float x = gb_a + dtb;
             const float sp = x > 30.0f ? x : log1pf(expf(x));
-            a.gb[((size_t)t * a.n_v + h) * 2] = expf(-expf(a.A_log[h]) * sp);
-            a.gb[((size_t)t * a.n_v + h) * 2 + 1] = 1.0f / (1.0f + expf(-b));
+            s_gb[gt][0] = expf(-expf(alog) * sp);
+            s_gb[gt][1] = 1.0f / (1.0f + expf(-gb_b));
         }
-        return;
     }
-    const int c0 = it * kGHead;  // first channel of the head
-    float out[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int c = c0 + lane + 64 * j;
-        const int src = conv_src(a, c);
-        const float cur = bf16_round(pr[src]);
-        a.conv_ring[(size_t)(pos % kConvRing) * a.conv_dim + c] = vmi_f32_to_bf16(cur);
-        float acc = 0.0f;
-#pragma unroll
-        for (int tap = 0; tap < kConvTaps; ++tap) {
-            const int p = pos - (kConvTaps - 1) + tap;
-            float m;
-            if (p == pos) m = cur;
-            else if (p >= pos0) m = bf16_round(a.proj[(size_t)(p - pos0) * a.stride + src]);
-            else if (p >= 0) m = vmi_bf16_to_f32(a.conv_ring[(size_t)(p % kConvRing) * a.conv_dim + c]);
-            else m = 0.0f;
-            acc = fmaf(vmi_bf16_to_f32(a.conv_w[(size_t)c * kConvTaps + tap]), m, acc);
-        }
-        out[j] = acc / (1.0f + expf(-acc));
-    }
-    if (it < 2 * a.n_k) {
-        float ss = fmaf(out[0], out[0], out[1] * out[1]);
+    __syncthreads();
+
+    // 3. q and k normalisation
+    if (w < 2 * T) {
+        const int t = w >> 1, part = w & 1;
+        float* v = &s_c[t][part * kGHead];
+        const float o0 = v[lane], o1 = v[lane + 64];
+        float ss = fmaf(o0, o0, o1 * o1);
         ss = vmi_wave_sum_canon(ss);
         const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / kGHead) + 1e-6f));
-        const float scale = it < a.n_k ? 1.0f / kGHead : 0.08838834764831845f;  // 1/128, 1/sqrt(128)
-        float* dst = a.qk + ((size_t)t * 2 * a.n_k + it) * kGHead;
-        dst[lane] = out[0] * inv * scale;
-        dst[lane + 64] = out[1] * inv * scale;
-    } else {
-        float* dst = a.v + ((size_t)t * a.n_v + (it - 2 * a.n_k)) * kGHead;
-        dst[lane] = out[0];
-        dst[lane + 64] = out[1];
+        const float scale = part == 0 ? 1.0f / kGHead : 0.08838834764831845f;  // 1/128, 1/sqrt(128)
+        v[lane] = o0 * inv * scale;
+        v[lane + 64] = o1 * inv * scale;
     }
-}
+    __syncthreads();
 
-// 16 lanes per state row (8 dk values each), 4 rows per wave, 16 rows per
-// workgroup; grid (128 / 16, n_v).  The sums over dk reduce the 16 lanes in
-// a fixed butterfly, the same for every batch size, so a T-token call equals
-// T one-token calls bit for bit.
-__device__ __forceinline__ float sum16(float v) {
-    v += __shfl_xor(v, 8);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 1);
-    return v;
-}
-
-__global__ __launch_bounds__(kGThreads) void k_gdn_delta(GdnArgs a) {
-    const int lane = threadIdx.x & 63, w = g_wave();
-    const int h = blockIdx.y;
-    const int row = blockIdx.x * 16 + w * 4 + (lane >> 4);  // dv index
-    const int d0 = (lane & 15) * 8;                          // dk slice
-    const int hk = h / a.r;
-    const size_t slot_elems = (size_t)a.n_v * kGHead * kGHead;
-    const size_t roff = ((size_t)h * kGHead + row) * kGHead + d0;
-    const int pos0 = gdn_pos0(a);
-    float S[8];
-    if (pos0 > 0) {
-        const float* src = a.state_ring + (size_t)(pos0 % a.n_slots) * slot_elems + roff;
-        const float4 u0 = *reinterpret_cast<const float4*>(src);
-        const float4 u1 = *reinterpret_cast<const float4*>(src + 4);
-        S[0] = u0.x; S[1] = u0.y; S[2] = u0.z; S[3] = u0.w;
-        S[4] = u1.x; S[5] = u1.y; S[6] = u1.z; S[7] = u1.w;
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) S[i] = 0.0f;
-    }
-    for (int t = 0; t < a.T; ++t) {
-        const float* kp = a.qk + ((size_t)t * 2 * a.n_k + a.n_k + hk) * kGHead + d0;
-        const float* qp = a.qk + ((size_t)t * 2 * a.n_k + hk) * kGHead + d0;
-        const float4 k0 = *reinterpret_cast<const float4*>(kp), k1 = *reinterpret_cast<const float4*>(kp + 4);
-        const float4 q0 = *reinterpret_cast<const float4*>(qp), q1 = *reinterpret_cast<const float4*>(qp + 4);
-        const float kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-        const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        const float g = a.gb[((size_t)t * a.n_v + h) * 2], beta = a.gb[((size_t)t * a.n_v + h) * 2 + 1];
-        const float vv = a.v[((size_t)t * a.n_v + h) * kGHead + row];
-        float kv = 0.0f;
+    // 4. delta rule
+    float S[2][8];
+    u4_to_f8(sa0, sa1, S[0]);
+    u4_to_f8(sb0, sb1, S[1]);
+    for (int t = 0; t < T; ++t) {
+        float kk[8], qq[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            S[i] *= g;
-            kv = fmaf(S[i], kk[i], kv);
+            const int d = d0 + (i & 3) + (i >> 2) * 64;
+            qq[i] = s_c[t][d];
+            kk[i] = s_c[t][kGHead + d];
         }
-        kv = sum16(kv);
-        const float delta = (vv - kv) * beta;
-        float yo = 0.0f;
+        const float g = s_gb[t][0], beta = s_gb[t][1];
+        float* slot = a.state_ring + (size_t)((pos0 + t + 1) % a.n_slots) * slot_elems;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            S[i] = fmaf(kk[i], delta, S[i]);
-            yo = fmaf(S[i], qq[i], yo);
+        for (int j = 0; j < 2; ++j) {
+            const int row = rowA + 64 * j;
+            const float vv = s_c[t][2 * kGHead + row];
+            float kv = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                S[j][i] *= g;
+                kv = fmaf(S[j][i], kk[i], kv);
+            }
+            kv = vmi_row_sum16(kv);
+            const float delta = (vv - kv) * beta;
+            float yo = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                S[j][i] = fmaf(kk[i], delta, S[j][i]);
+                yo = fmaf(S[j][i], qq[i], yo);
+            }
+            yo = vmi_row_sum16(yo);
+            float* dst = slot + ((size_t)h * kGHead + row) * kGHead + d0;
+            *reinterpret_cast<float4*>(dst) = make_float4(S[j][0], S[j][1], S[j][2], S[j][3]);
+            *reinterpret_cast<float4*>(dst + 64) = make_float4(S[j][4], S[j][5], S[j][6], S[j][7]);
+            if ((lane & 15) == 0) s_y[t][row] = yo;
         }
-        yo = sum16(yo);
-        float* dst = a.state_ring + (size_t)((pos0 + t + 1) % a.n_slots) * slot_elems + roff;
-        *reinterpret_cast<float4*>(dst) = make_float4(S[0], S[1], S[2], S[3]);
-        *reinterpret_cast<float4*>(dst + 4) = make_float4(S[4], S[5], S[6], S[7]);
-        if ((lane & 15) == 0) a.y[((size_t)t * a.n_v + h) * kGHead + row] = yo;
     }
-}
+    __syncthreads();
 
-// One wave per (token, v-head): o = y / sqrt(mean(y^2) + eps) * w * silu(z).
-__global__ __launch_bounds__(kGThreads) void k_gdn_norm(GdnArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int gid = blockIdx.x * (kGThreads / 64) + g_wave();
-    if (gid >= a.T * a.n_v) return;
-    const int t = gid / a.n_v, h = gid - t * a.n_v;
-    const float* y = a.y + (size_t)gid * kGHead;
-    const float y0 = y[lane], y1 = y[lane + 64];
-    float ss = fmaf(y0, y0, y1 * y1);
-    ss = vmi_wave_sum_canon(ss);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / kGHead) + a.eps));
-    const float* z = a.proj + (size_t)t * a.stride + (h / a.r) * a.per_g + 2 * kGHead + a.r * kGHead +
-                     (h % a.r) * kGHead;
-    const float z0 = z[lane], z1 = z[lane + 64];
-    uint16_t* o = a.o + (size_t)gid * kGHead;
-    o[lane] = vmi_f32_to_bf16(y0 * inv * vmi_bf16_to_f32(a.norm_w[lane]) * (z0 / (1.0f + expf(-z0))));
-    o[lane + 64] = vmi_f32_to_bf16(y1 * inv * vmi_bf16_to_f32(a.norm_w[lane + 64]) * (z1 / (1.0f + expf(-z1))));
+    // 5. gated RMSNorm
+    if (w < T) {
+        const int t = w;
+        const float y0 = s_y[t][lane], y1 = s_y[t][lane + 64];
+        float ss = fmaf(y0, y0, y1 * y1);
+        ss = vmi_wave_sum_canon(ss);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / kGHead) + a.eps));
+        uint16_t* o = a.o + ((size_t)t * a.n_v + h) * kGHead;
+        o[lane] = vmi_f32_to_bf16(y0 * inv * __uint_as_float(nw0 << 16) * (z0 / (1.0f + expf(-z0))));
+        o[lane + 64] = vmi_f32_to_bf16(y1 * inv * __uint_as_float(nw1 << 16) * (z1 / (1.0f + expf(-z1))));
+    }
 }
 
 struct GdnLayout {
-    size_t xn, proj, qk, v, gb, y, o, bytes;
+    size_t xn, proj, o, bytes;
 };
 
 GdnLayout gdn_layout(int T, int H, int n_k, int n_v) {
@@ -231,10 +269,6 @@ GdnLayout gdn_layout(int T, int H, int n_k, int n_v) {
     const int stride = n_k * (2 * kGHead + 2 * r * kGHead) + 2 * n_v;
     L.xn = take((size_t)T * H * 2);
     L.proj = take((size_t)T * stride * 4);
-    L.qk = take((size_t)T * 2 * n_k * kGHead * 4);
-    L.v = take((size_t)T * n_v * kGHead * 4);
-    L.gb = take((size_t)T * n_v * 2 * 4);
-    L.y = take((size_t)T * n_v * kGHead * 4);
     L.o = take((size_t)T * n_v * kGHead * 2);
     L.bytes = off;
     return L;
@@ -288,10 +322,6 @@ extern "C" int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, 
     a.proj = reinterpret_cast<float*>(ws + L.proj);
     a.conv_w = D.conv_weight; a.A_log = D.A_log; a.dt_bias = D.dt_bias;
     a.conv_ring = conv_ring; a.state_ring = state_ring; a.n_slots = n_slots;
-    a.qk = reinterpret_cast<float*>(ws + L.qk);
-    a.v = reinterpret_cast<float*>(ws + L.v);
-    a.gb = reinterpret_cast<float*>(ws + L.gb);
-    a.y = reinterpret_cast<float*>(ws + L.y);
     a.norm_w = D.norm_weight; a.eps = D.norm_eps;
     a.o = reinterpret_cast<uint16_t*>(ws + L.o);
     uint16_t* xn = reinterpret_cast<uint16_t*>(ws + L.xn);
@@ -313,10 +343,7 @@ extern "C" int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, 
     e = vmi::launch_qgemv(q, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "qkvz/ba projection launch");
 
-    const int items = 2 * D.n_k_heads + D.n_v_heads + 1;
-    hipLaunchKernelGGL(k_gdn_conv, dim3((T * items + 3) / 4), dim3(kGThreads), 0, s, a);
-    hipLaunchKernelGGL(k_gdn_delta, dim3(kGHead / 16, D.n_v_heads), dim3(kGThreads), 0, s, a);
-    hipLaunchKernelGGL(k_gdn_norm, dim3((T * D.n_v_heads + 3) / 4), dim3(kGThreads), 0, s, a);
+    hipLaunchKernelGGL(k_gdn_block, dim3(D.n_v_heads), dim3(kGFThreads), 0, s, a);
 
     vmi::QgemvCall o{};
     o.x = a.o; o.T = T; o.K = D.n_v_heads * kGHead; o.bits = D.bits;
