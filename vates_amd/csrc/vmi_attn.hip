@@ -16,13 +16,15 @@
 //   k_qgemv        y[t][n] = sum_k x[t][k] W[n][k], 4/8-bit affine W, T <= 8:
 //                  one wave per output row, 16 bytes of packed weights per
 //                  lane per step, tokens staged in LDS, fp32 accumulation
-//   k_qk_rope      per (token, head): q/k RMSNorm, rotary, q as bf16, k and v
-//                  appended to the bf16 KV cache at the token's position
-//   k_attn_chunk   per (kv head, chunk of 256 keys), 8 waves: wave w scores
-//                  the chunk's 32-key block w against the head group's query
-//                  rows (S^T = K Q^T), the chunk max and the bf16
-//                  probabilities go through LDS, then wave w forms P V for
-//                  dims 32w..32w+31 over all 256 keys; writes (max, sum, O)
+//   k_attn_chunk   per (kv head, chunk of 256 keys), 8 waves: while the
+//                  chunk's keys and values stream in, the workgroup forms the
+//                  head group's queries (q RMSNorm, rotary, bf16) and, in the
+//                  chunk holding a batch position, that position's key and
+//                  value (k RMSNorm, rotary), appended to the cache and put
+//                  into the loaded operands; wave w scores the 32-key block w
+//                  against the query rows (S^T = K Q^T), the chunk max and the
+//                  bf16 probabilities go through LDS, then wave w forms P V
+//                  for dims 32w..32w+31 over all 256 keys; writes (max, sum, O)
 //   k_attn_merge   per (token, head, quarter of the dims): merges the chunks
 //                  in a fixed order, times sigmoid(gate), bf16 input of o_proj
 //
@@ -210,101 +212,21 @@ __device__ __forceinline__ int v_elem(int kt, int d) {
     return ((((d >> 4) * 64 + (kt >> 3) * 16 + (d & 15)) << 3) + (kt & 7));
 }
 
-struct RopeArgs {
-    const float* qkv;        // [T, stride]: q|gate per head (n_heads * 2 * 256), then k (n_kv * 256), then v
-    int stride;
-    int T, n_heads, n_kv, rope_dim, pos0, max_len;
-    const int32_t* pos_dev;  // if set: pos0 is read here
-    float theta, eps;
-    const uint16_t* q_norm;  // [256]
-    const uint16_t* k_norm;  // [256]
-    uint16_t* q_out;         // [T, n_heads, 256] bf16
-    uint16_t* k_cache;       // [n_kv, max_len, 256]
-    uint16_t* v_cache;
-};
-
-// One wave per (token, head): 4 values per lane.  Heads [0, n_heads) are
-// queries, [n_heads, n_heads + n_kv) keys (values copied alongside).
-__global__ __launch_bounds__(kAThreads) void k_qk_rope(RopeArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int item = blockIdx.x * (kAThreads / 64) + at_wave();
-    const int per_tok = a.n_heads + a.n_kv;
-    if (item >= a.T * per_tok) return;
-    const int t = item / per_tok, h = item - t * per_tok;
-    const bool is_q = h < a.n_heads;
-    const float* src = is_q ? a.qkv + (size_t)t * a.stride + (size_t)h * 2 * kHeadDim
-                            : a.qkv + (size_t)t * a.stride + (size_t)a.n_heads * 2 * kHeadDim +
-                                  (size_t)(h - a.n_heads) * kHeadDim;
-    const uint16_t* nw = is_q ? a.q_norm : a.k_norm;
-    // lane holds dims d = lane + 64 j (j < 4): rotary partners (i, i + rd/2) live in one lane
-    // only when rd/2 is a multiple of 64, so the partner comes through LDS.
-    __shared__ float s_v[kAThreads / 64][kHeadDim];
-    const int w = at_wave();
-    float v[4];
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        v[j] = src[lane + 64 * j];
-        ss = fmaf(v[j], v[j], ss);
-    }
-    ss = vmi_wave_sum_canon(ss);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)kHeadDim) + a.eps));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        // normalised value as the model dtype (bf16), then rotary in fp32
-        v[j] = vmi_bf16_to_f32(vmi_f32_to_bf16((v[j] * inv) * vmi_bf16_to_f32(nw[lane + 64 * j])));
-        s_v[w][lane + 64 * j] = v[j];
-    }
-    __builtin_amdgcn_wave_barrier();  // s_v[w] is this wave's own row: LDS order within a wave suffices
-    const int pos = batch_pos0(a.pos0, a.pos_dev, a.T, a.max_len) + t;
-    const int half = a.rope_dim / 2;
-    uint16_t o[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int d = lane + 64 * j;
-        float r = v[j];
-        if (d < a.rope_dim) {
-            // angle pos * theta^(-2i/rd) in double: fp32 rounding of angles up to ~3e4 rad
-            // would move the rotation by ~1e-3
-            const int i = d < half ? d : d - half;
-            const double ang = (double)pos * pow((double)a.theta, -(double)(2 * i) / (double)a.rope_dim);
-            const float cs = (float)cos(ang), sn = (float)sin(ang);
-            const float partner = d < half ? -s_v[w][d + half] : s_v[w][d - half];
-            r = v[j] * cs + partner * sn;
-        }
-        o[j] = vmi_f32_to_bf16(r);
-    }
-    if (is_q) {
-        uint16_t* qo = a.q_out + ((size_t)t * a.n_heads + h) * kHeadDim;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) qo[lane + 64 * j] = o[j];
-    } else {
-        const int g = h - a.n_heads;
-        const size_t blk = kv_block(g, a.max_len, pos);
-        const int kt = pos % kKvBlock;
-        const float* vsrc = a.qkv + (size_t)t * a.stride + (size_t)a.n_heads * 2 * kHeadDim +
-                            (size_t)a.n_kv * kHeadDim + (size_t)g * kHeadDim;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int d = lane + 64 * j;
-            a.k_cache[blk + k_elem(kt, d)] = o[j];
-            a.v_cache[blk + v_elem(kt, d)] = vmi_f32_to_bf16(vsrc[d]);
-        }
-    }
-}
-
 // -------------------------------------------------------------- attention
 struct AttnArgs {
-    const uint16_t* q;        // [T, n_heads, 256] bf16
-    const uint16_t* k_cache;  // blocks of 32 positions, see the layout above
-    const uint16_t* v_cache;
+    const float* qkv;         // [T, stride]: q|gate per head (n_heads * 2 * 256), then k (n_kv * 256), then v
+    int stride;
+    const uint16_t* q_norm;   // [256]
+    const uint16_t* k_norm;   // [256]
+    int rope_dim;
+    float theta, eps;
+    uint16_t* k_cache;        // blocks of 32 positions, see the layout above
+    uint16_t* v_cache;
     int T, n_heads, n_kv, pos0, max_len;
     const int32_t* pos_dev;   // if set: pos0 is read here
     int nstride;              // chunk capacity of the partial buffers
     float* part_o;            // [n_kv, nstride, RP, 256]
     float* part_ml;           // [n_kv, nstride, RP, 2]
-    const float* qkv;         // for the gate in the merge
-    int stride;
     uint16_t* o;              // [T, n_heads * 256] bf16 gated attention output
 };
 
@@ -319,62 +241,173 @@ __device__ __forceinline__ vmi_u4 keep_first(vmi_u4 v, int n) {  // zero bf16 el
     return v;
 }
 
+// One head row (dims lane + 64 j in v) in place: RMSNorm in the canonical
+// order, times the norm weight, rounded to bf16 (the model dtype), then the
+// rotary pairs (i, i + rd/2) in fp32 with (cos, sin) of pos * theta^(-2i/rd)
+// from cs, rounded to bf16.  srow is the wave's own LDS row (the rotary
+// partner of a dim lives in another lane).
+__device__ __forceinline__ void norm_rope_row(float (&v)[4], const float (&nw)[4], float eps, const float2* cs, int rd,
+                                              float* srow, uint16_t (&o)[4]) {
+    const int lane = threadIdx.x & 63;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ss = fmaf(v[j], v[j], ss);
+    ss = vmi_wave_sum_canon(ss);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)kHeadDim) + eps));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        v[j] = vmi_bf16_to_f32(vmi_f32_to_bf16((v[j] * inv) * nw[j]));
+        srow[lane + 64 * j] = v[j];
+    }
+    __builtin_amdgcn_wave_barrier();  // srow is this wave's own row: LDS order within a wave suffices
+    const int half = rd / 2;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        float r = v[j];
+        if (d < rd) {
+            const float2 c = cs[d < half ? d : d - half];
+            const float partner = d < half ? -srow[d + half] : srow[d - half];
+            r = v[j] * c.x + partner * c.y;
+        }
+        o[j] = vmi_f32_to_bf16(r);
+    }
+    __builtin_amdgcn_wave_barrier();  // every lane has read its partner before srow is rewritten
+}
+
 // Rows of a head group: row = t * G + hl (G = n_heads / n_kv query heads per
-// kv head), RP = 16 MS >= T * G.  Every load is issued before the first
-// MFMA: keys of the wave's block (16 x 1 KB) and values of all 8 blocks for
-// the wave's 32 dims (16 x 1 KB).  Positions >= pos0 + T are not read past
-// their block; inside the last block they are masked (scores -inf, values
-// zeroed), so stale cache contents never reach the result.
+// kv head), RP = 16 MS >= T * G.  Loads in issue order: the projections of
+// the wave's query rows (rows w, w + 8, ...), in the chunk holding batch
+// positions the key and value projections of one of them per wave, then the
+// keys of the wave's block (16 x 1 KB) and values of all 8 blocks for the
+// wave's 32 dims (16 x 1 KB); the queries and new keys are formed while the
+// cache streams.  Positions >= pos0 + T are not read past their block; inside
+// the last block they are masked (scores -inf, values zeroed), so stale cache
+// contents never reach the result.  The batch's own positions are read from
+// the cache too, before this workgroup writes them: their operands are then
+// replaced by the new keys and values.
 template <int MS>
 __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     constexpr int RP = 16 * MS;
     __shared__ __attribute__((aligned(16))) uint16_t s_q[RP][kHeadDim + 8];
     __shared__ vmi_u4 s_pa[MS][kChunkWaves][64];
     __shared__ float s_wm[kChunkWaves][RP], s_wl[kChunkWaves][RP];
-    const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    // chunks in reverse launch order: the last (partly filled) chunk and those
+    // past the cache take the first CUs and free them early, so the full
+    // chunks beyond one per CU start while the first ones still stream
+    __shared__ float s_row[kChunkWaves][kHeadDim];                  // a wave's normalised row
+    __shared__ float2 s_cs[kQgMaxT][kHeadDim / 2];                  // (cos, sin) per (token, frequency)
+    __shared__ __attribute__((aligned(16))) uint16_t s_new[2][kQgMaxT][kHeadDim];  // new keys, values (bf16)
+    const int c = gridDim.x - 1 - blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, w = at_wave(), nl = lane & 15, q4 = lane >> 4;
-    const int G = a.n_heads / a.n_kv, R = a.T * G;
-    const int pos0 = batch_pos0(a.pos0, a.pos_dev, a.T, a.max_len);
-    const int L = pos0 + a.T;                          // positions present
+    const int T = a.T, G = a.n_heads / a.n_kv, R = T * G;
+    const int pos0 = batch_pos0(a.pos0, a.pos_dev, T, a.max_len);
+    const int L = pos0 + T;                            // positions present
     if (c * kChunkKeys >= L) return;                   // chunk beyond the cache (whole workgroup)
     const int b0 = c * kChunkWaves;
-    const uint16_t* kb = a.k_cache + kv_block(g, a.max_len, 0);
-    const uint16_t* vb = a.v_cache + kv_block(g, a.max_len, 0);
+    // batch tokens whose positions lie in this chunk: t_lo .. t_hi - 1
+    const int t_lo = max(0, c * kChunkKeys - pos0), t_hi = min(T, (c + 1) * kChunkKeys - pos0);
+    const int tn = t_lo + w;                           // this wave's new position (if tn < t_hi)
+    const bool has_new = w < t_hi - t_lo;
 
+    // projections (lanes and rows past the batch read zeros), then the cache
+    constexpr int QR = 2 * MS;                         // query rows per wave
+    const __amdgpu_buffer_rsrc_t rq = vmi_rsrc(a.qkv, (uint32_t)(T * a.stride) * 4u);
+    float qv[QR][4], kv[4], vv[4];
+    uint32_t qnr[4], knr[4];
+#pragma unroll
+    for (int i = 0; i < QR; ++i) {
+        const int row = w + kChunkWaves * i, t = row / G, h = g * G + row % G;
+        const uint32_t base = (uint32_t)(t * a.stride + h * 2 * kHeadDim + lane);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            qv[i][j] = __uint_as_float(vmi_bload_b32(rq, row < R ? (base + 64 * j) * 4u : VMI_OOB, 0));
+    }
+    {
+        const uint32_t kb_ = (uint32_t)(tn * a.stride + a.n_heads * 2 * kHeadDim + g * kHeadDim + lane);
+        const uint32_t vb_ = kb_ + (uint32_t)(a.n_kv * kHeadDim);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            kv[j] = __uint_as_float(vmi_bload_b32(rq, has_new ? (kb_ + 64 * j) * 4u : VMI_OOB, 0));
+            vv[j] = __uint_as_float(vmi_bload_b32(rq, has_new ? (vb_ + 64 * j) * 4u : VMI_OOB, 0));
+        }
+    }
+    {
+        const __amdgpu_buffer_rsrc_t rqn = vmi_rsrc(a.q_norm, kHeadDim * 2u), rkn = vmi_rsrc(a.k_norm, kHeadDim * 2u);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            qnr[j] = vmi_bload_b16(rqn, (uint32_t)(lane + 64 * j) * 2u, 0);
+            knr[j] = vmi_bload_b16(rkn, (uint32_t)(lane + 64 * j) * 2u, 0);
+        }
+    }
+    asm volatile("" ::: "memory");
+    // rotary table while the projections arrive (before the cache loads: its
+    // double-precision temporaries and the cache operands are never live
+    // together); angle pos * theta^(-2i/rd) in double (fp32 rounding of
+    // angles up to ~3e4 rad would move the rotation by ~1e-3)
+    for (int i = tid; i < T * (a.rope_dim / 2); i += kChunkThreads) {
+        const int t = i / (a.rope_dim / 2), fi = i - t * (a.rope_dim / 2);
+        const double ang = (double)(pos0 + t) * pow((double)a.theta, -(double)(2 * fi) / (double)a.rope_dim);
+        s_cs[t][fi] = make_float2((float)cos(ang), (float)sin(ang));
+    }
+    // the cache blocks: branch-free buffer loads, blocks past the cache
+    // reading zeros (a load under a branch would leave every later wait
+    // counting as if none of them had been issued)
+    const uint32_t head_bytes = (uint32_t)(a.max_len / kKvBlock) * kKvBlockElems * 2u;
+    const __amdgpu_buffer_rsrc_t rk = vmi_rsrc(a.k_cache + kv_block(g, a.max_len, 0), head_bytes);
+    const __amdgpu_buffer_rsrc_t rv = vmi_rsrc(a.v_cache + kv_block(g, a.max_len, 0), head_bytes);
     vmi_u4 kr[2][8], vr[2][kChunkWaves];
     const int bw = b0 + w;
-    if (kKvBlock * bw < L) {
-        const vmi_u4* src = reinterpret_cast<const vmi_u4*>(kb + (size_t)bw * kKvBlockElems) + lane;
+    {
+        const uint32_t kbase = kKvBlock * bw < L ? (uint32_t)bw * kKvBlockElems * 2u + lane * 16u : VMI_OOB;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) kr[h][kk] = src[(h * 8 + kk) * 64];
-    } else {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) kr[h][kk] = vmi_u4{0u, 0u, 0u, 0u};
+            for (int kk = 0; kk < 8; ++kk) kr[h][kk] = vmi_bload_b128(rk, kbase + (uint32_t)(h * 8 + kk) * 1024u, 0);
     }
 #pragma unroll
     for (int sb = 0; sb < kChunkWaves; ++sb) {
         const int bs = b0 + sb;
-        if (kKvBlock * bs < L) {
-            const vmi_u4* src = reinterpret_cast<const vmi_u4*>(vb + (size_t)bs * kKvBlockElems) + lane;
+        const uint32_t vbase =
+            kKvBlock * bs < L ? (uint32_t)bs * kKvBlockElems * 2u + (uint32_t)(2 * w) * 1024u + lane * 16u : VMI_OOB;
 #pragma unroll
-            for (int dt = 0; dt < 2; ++dt) vr[dt][sb] = src[(2 * w + dt) * 64];
-        } else {
+        for (int dt = 0; dt < 2; ++dt) vr[dt][sb] = vmi_bload_b128(rv, vbase + (uint32_t)dt * 1024u, 0);
+    }
+
+    __syncthreads();
+    float qn[4], kn[4];
 #pragma unroll
-            for (int dt = 0; dt < 2; ++dt) vr[dt][sb] = vmi_u4{0u, 0u, 0u, 0u};
+    for (int j = 0; j < 4; ++j) {
+        qn[j] = __uint_as_float(qnr[j] << 16);
+        kn[j] = __uint_as_float(knr[j] << 16);
+    }
+    // the wave's query rows into s_q (rows past the batch: zeros)
+#pragma unroll
+    for (int i = 0; i < QR; ++i) {
+        const int row = w + kChunkWaves * i;
+        if (row < RP) {
+            uint16_t o[4] = {0, 0, 0, 0};
+            if (row < R) norm_rope_row(qv[i], qn, a.eps, s_cs[row / G], a.rope_dim, s_row[w], o);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s_q[row][lane + 64 * j] = o[j];
         }
     }
-    for (int i = tid; i < RP * (kHeadDim / 8); i += kChunkThreads) {
-        const int row = i / (kHeadDim / 8), d8 = i % (kHeadDim / 8);
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (row < R) {
-            const int t = row / G, hl = row % G;
-            v = *reinterpret_cast<const uint4*>(a.q + ((size_t)t * a.n_heads + g * G + hl) * kHeadDim + 8 * d8);
+    // the new key and value of position pos0 + tn: to the cache and to LDS
+    if (has_new) {
+        const int pos = pos0 + tn;
+        uint16_t o[4];
+        norm_rope_row(kv, kn, a.eps, s_cs[tn], a.rope_dim, s_row[w], o);
+        const size_t blk = kv_block(g, a.max_len, pos);
+        const int kt = pos % kKvBlock;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = lane + 64 * j;
+            const uint16_t vb16 = vmi_f32_to_bf16(vv[j]);
+            a.k_cache[blk + k_elem(kt, d)] = o[j];
+            a.v_cache[blk + v_elem(kt, d)] = vb16;
+            s_new[0][tn][d] = o[j];
+            s_new[1][tn][d] = vb16;
         }
-        *reinterpret_cast<uint4*>(&s_q[row][8 * d8]) = v;
     }
     // the last block: values of positions >= L are zeroed (0 * stale could be NaN)
 #pragma unroll
@@ -386,6 +419,23 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         }
     }
     __syncthreads();
+    // new keys into the wave's key operands: position kt of the block sits in
+    // lanes nl = 4 (kt >> 3) + (kt & 3), tile (kt >> 2) & 1, dims 32 kk + 8 q4 ..
+    for (int t = t_lo; t < t_hi; ++t) {
+        const int p = pos0 + t;
+        if ((p >> 5) != bw) continue;
+        const int kt = p & (kKvBlock - 1);
+        if (nl == 4 * (kt >> 3) + (kt & 3)) {
+            const uint16_t* src = &s_new[0][t][8 * q4];
+            if ((kt >> 2) & 1) {
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) kr[1][kk] = *reinterpret_cast<const vmi_u4*>(src + 32 * kk);
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) kr[0][kk] = *reinterpret_cast<const vmi_u4*>(src + 32 * kk);
+            }
+        }
+    }
 
     // scores: lane (nl, q4) of tile h holds keys 8 q4 + 4 h + r of block bw for query row 16 m + nl
     float sc[MS][8];
@@ -440,6 +490,26 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         s_pa[m][w][lane] = pk;
     }
     __syncthreads();
+    // new values into the value operands: position 8 q4 + e of block sb is
+    // element e of lanes with that q4, dim 32 w + 16 dt + nl
+    for (int t = t_lo; t < t_hi; ++t) {
+        const int p = pos0 + t, kt = p & (kKvBlock - 1);
+        if (q4 != (kt >> 3)) continue;
+        const int e = kt & 7;
+#pragma unroll
+        for (int sb = 0; sb < kChunkWaves; ++sb) {
+            if ((p >> 5) != b0 + sb) continue;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt) {
+                const uint32_t nv = s_new[1][t][32 * w + 16 * dt + nl];
+#pragma unroll
+                for (int ee = 0; ee < 8; ++ee)
+                    if (ee == e)
+                        vr[dt][sb][ee >> 1] = (ee & 1) ? (vr[dt][sb][ee >> 1] & 0x0000ffffu) | (nv << 16)
+                                                       : (vr[dt][sb][ee >> 1] & 0xffff0000u) | nv;
+            }
+        }
+    }
     // O = P V for dims 32 w + 16 dt + nl; A = P of block sb (written by wave sb)
     const size_t pbase = ((size_t)g * a.nstride + c) * RP;
 #pragma unroll
@@ -769,7 +839,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
 int attn_chunks(int L) { return (L + kChunkKeys - 1) / kChunkKeys; }
 
 struct AttnLayout {
-    size_t xn, qkv, q, part_o, part_ml, o, bytes;
+    size_t xn, qkv, part_o, part_ml, o, bytes;
 };
 
 AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len) {
@@ -784,7 +854,6 @@ AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len) {
     const int stride = n_heads * 2 * kHeadDim + 2 * n_kv * kHeadDim;
     L.xn = take((size_t)T * H * 2);
     L.qkv = take((size_t)T * stride * 4);
-    L.q = take((size_t)T * n_heads * kHeadDim * 2);
     const int nc = attn_chunks(max_len);
     L.part_o = take((size_t)n_kv * nc * RP * kHeadDim * 4);
     L.part_ml = take((size_t)n_kv * nc * RP * 2 * 4);
@@ -896,7 +965,6 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     uint16_t* xn = reinterpret_cast<uint16_t*>(ws + L.xn);
     float* qkv = reinterpret_cast<float*>(ws + L.qkv);
-    uint16_t* qb = reinterpret_cast<uint16_t*>(ws + L.q);
     uint16_t* ob = reinterpret_cast<uint16_t*>(ws + L.o);
     const int stride = D.n_heads * 2 * kHeadDim + 2 * D.n_kv_heads * kHeadDim;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -917,14 +985,10 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     hipError_t e = vmi::launch_qgemv(q, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "qkv projection launch");
 
-    RopeArgs rp{};
-    rp.qkv = qkv; rp.stride = stride; rp.T = T; rp.n_heads = D.n_heads; rp.n_kv = D.n_kv_heads;
-    rp.rope_dim = D.rope_dim; rp.pos0 = pos0; rp.pos_dev = pos_device; rp.max_len = max_len; rp.theta = D.rope_theta; rp.eps = D.norm_eps;
-    rp.q_norm = D.q_norm; rp.k_norm = D.k_norm; rp.q_out = qb; rp.k_cache = k_cache; rp.v_cache = v_cache;
-    hipLaunchKernelGGL(k_qk_rope, dim3((T * (D.n_heads + D.n_kv_heads) + 3) / 4), dim3(kAThreads), 0, s, rp);
-
     AttnArgs at{};
-    at.q = qb; at.k_cache = k_cache; at.v_cache = v_cache;
+    at.qkv = qkv; at.stride = stride; at.q_norm = D.q_norm; at.k_norm = D.k_norm;
+    at.rope_dim = D.rope_dim; at.theta = D.rope_theta; at.eps = D.norm_eps;
+    at.k_cache = k_cache; at.v_cache = v_cache;
     at.T = T; at.n_heads = D.n_heads; at.n_kv = D.n_kv_heads; at.pos0 = pos0; at.pos_dev = pos_device;
     at.max_len = max_len;
     at.nstride = attn_chunks(max_len);
@@ -932,7 +996,7 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     const int grid_chunks = pos_device ? at.nstride : attn_chunks(pos0 + T);
     at.part_o = reinterpret_cast<float*>(ws + L.part_o);
     at.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
-    at.qkv = qkv; at.stride = stride; at.o = ob;
+    at.o = ob;
     const int MS = (T * G + 15) / 16;
     const dim3 ag(grid_chunks, D.n_kv_heads);
     switch (MS) {
