@@ -127,6 +127,10 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_w1[NW][kChunk];
     __shared__ __attribute__((aligned(16))) uint8_t s_w2[NBUF > 2 ? NW : 1][NBUF > 2 ? kChunk : 16];
     __shared__ __attribute__((aligned(16))) uint8_t s_w3[NBUF > 3 ? NW : 1][NBUF > 3 ? kChunk : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t s_w4[NBUF > 4 ? NW : 1][NBUF > 4 ? kChunk : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t s_w5[NBUF > 5 ? NW : 1][NBUF > 5 ? kChunk : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t s_w6[NBUF > 6 ? NW : 1][NBUF > 6 ? kChunk : 16];
+    __shared__ __attribute__((aligned(16))) uint8_t s_w7[NBUF > 7 ? NW : 1][NBUF > 7 ? kChunk : 16];
     __shared__ uint64_t s_best[NW][MAXT];
     __shared__ int s_last;
 
@@ -149,7 +153,8 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
     // instruction i brings rows 4i..4i+3, lane l row 4i + l/16, and fetches the
     // row's 16-byte unit (l%16) ^ row so that LDS unit u of row r holds unit u ^ r.
     auto slot = [&](int u) -> uint8_t* {  // u is a constant after unrolling
-        return u == 0 ? &s_w0[w][0] : u == 1 ? &s_w1[w][0] : u == 2 ? &s_w2[w][0] : &s_w3[w][0];
+        return u == 0 ? &s_w0[w][0] : u == 1 ? &s_w1[w][0] : u == 2 ? &s_w2[w][0] : u == 3 ? &s_w3[w][0]
+             : u == 4 ? &s_w4[w][0] : u == 5 ? &s_w5[w][0] : u == 6 ? &s_w6[w][0] : &s_w7[w][0];
     };
     auto issue = [&](int q, uint8_t* buf) {
         const int j = q / nch, c = q - j * nch;
@@ -167,8 +172,9 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
     vmi_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     const bool a_live = n < T;  // A row n is token n; rows past T stay zero
 
-    // nch is a multiple of 4 (H % 512 == 0), so every group of NBUF chunks
-    // lies inside one tile and the unrolled body below needs no guards.
+    // nch is a multiple of NBUF (H % 512 == 0 with 4 slots, H % 1024 == 0 with
+    // 8), so every group of NBUF chunks lies inside one tile and the unrolled
+    // body below needs no guards.
     auto consume = [&](int c, const uint8_t* buf) {
         const uint8_t* xrow = s_x + n * kRow + 256 * c;
 #pragma unroll
@@ -338,7 +344,9 @@ extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t*
     if (G > kHeadMaxGrid) G = kHeadMaxGrid;
     if (G > a.ntiles) G = a.ntiles;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (T <= 4)
+    if (T <= 4 && hidden % 1024 == 0)
+        hipLaunchKernelGGL((k_head<4, 4, 8>), dim3(G), dim3(4 * 64), 0, s, a);
+    else if (T <= 4)
         hipLaunchKernelGGL((k_head<4, 8, 4>), dim3(G), dim3(8 * 64), 0, s, a);
     else
         hipLaunchKernelGGL((k_head<16, 8, 2>), dim3(G), dim3(8 * 64), 0, s, a);
