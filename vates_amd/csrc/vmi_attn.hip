@@ -548,20 +548,45 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
     const int lane = tid & 63, w = at_wave();
     const int G = a.n_heads / a.n_kv, g = h / G, row = t * G + (h % G);
     const int NC = (batch_pos0(a.pos0, a.pos_dev, a.T, a.max_len) + a.T + kChunkKeys - 1) / kChunkKeys;
-    const size_t cstride = (size_t)RP;                                      // rows between chunks
-    const float* ml = a.part_ml + ((size_t)g * a.nstride * RP + row) * 2;   // chunk c at + c * RP * 2
+    // loads in issue order: every chunk's (max, sum) of this row (branch-free,
+    // chunks past the cache read nothing), then this lane's first 8 partial
+    // outputs, which arrive while the maximum and the denominator form
+    constexpr int kMlPer = kMergeMaxChunks / kAThreads;
+    const size_t rbase = (size_t)g * a.nstride * RP + row;
+    const __amdgpu_buffer_rsrc_t rml = vmi_rsrc(a.part_ml + rbase * 2, (uint32_t)(a.nstride * RP * 2) * 4u);
+    const __amdgpu_buffer_rsrc_t rpo =
+        vmi_rsrc(a.part_o + rbase * kHeadDim, (uint32_t)(a.nstride * RP) * kHeadDim * 4u);
+    uint2 mlr[kMlPer];
+#pragma unroll
+    for (int i = 0; i < kMlPer; ++i) {
+        const int c = tid + kAThreads * i;
+        mlr[i] = vmi_bload_b64(rml, c < NC ? (uint32_t)(c * RP * 2) * 4u : VMI_OOB, 0);
+    }
+    const int slot = 4 * w + (lane >> 4), d0 = 64 * blockIdx.y + 4 * (lane & 15);
+    vmi_u4 pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int c = slot + 16 * i;
+        pv[i] = vmi_bload_b128(rpo, c < NC ? ((uint32_t)(c * RP) * kHeadDim + d0) * 4u : VMI_OOB, 0);
+    }
     float M = -INFINITY;
-    for (int c = tid; c < NC; c += kAThreads) M = fmaxf(M, ml[c * cstride * 2]);
+#pragma unroll
+    for (int i = 0; i < kMlPer; ++i)
+        if (tid + kAThreads * i < NC) M = fmaxf(M, __uint_as_float(mlr[i].x));
     M = vmi_wave_max(M);
     if (lane == 0) s_red[w] = M;
     __syncthreads();
     M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
     float den = 0.0f;
-    for (int c = tid; c < NC; c += kAThreads) {
-        const float m = ml[c * cstride * 2];
-        const float f = m == -INFINITY ? 0.0f : expf(m - M);
-        s_f[c] = f;
-        den = fmaf(ml[c * cstride * 2 + 1], f, den);
+#pragma unroll
+    for (int i = 0; i < kMlPer; ++i) {
+        const int c = tid + kAThreads * i;
+        if (c < NC) {
+            const float m = __uint_as_float(mlr[i].x);
+            const float f = m == -INFINITY ? 0.0f : expf(m - M);
+            s_f[c] = f;
+            den = fmaf(__uint_as_float(mlr[i].y), f, den);
+        }
     }
     den = vmi_wave_sum_canon(den);
     __syncthreads();
@@ -569,26 +594,32 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
     __syncthreads();
     den = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
 
-    const int slot = 4 * w + (lane >> 4), d0 = 64 * blockIdx.y + 4 * (lane & 15);
-    const float* po = a.part_o + ((size_t)g * a.nstride * RP + row) * kHeadDim + d0;  // chunk c at + c * RP * 256
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c0 = slot; c0 < NC; c0 += 16 * 8) {
+    auto add = [&](int c, float vx, float vy, float vz, float vw) {
+        const float f = s_f[c];
+        acc.x = fmaf(vx, f, acc.x);
+        acc.y = fmaf(vy, f, acc.y);
+        acc.z = fmaf(vz, f, acc.z);
+        acc.w = fmaf(vw, f, acc.w);
+    };
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int c = slot + 16 * i;
+        if (c < NC) add(c, __uint_as_float(pv[i][0]), __uint_as_float(pv[i][1]), __uint_as_float(pv[i][2]),
+                        __uint_as_float(pv[i][3]));
+    }
+    const float* po = a.part_o + rbase * kHeadDim + d0;  // chunk c at + c * RP * 256
+    for (int c0 = slot + 16 * 8; c0 < NC; c0 += 16 * 8) {
         float4 v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int c = c0 + 16 * i;
-            v[i] = c < NC ? *reinterpret_cast<const float4*>(po + c * cstride * kHeadDim) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[i] = c < NC ? *reinterpret_cast<const float4*>(po + (size_t)c * RP * kHeadDim) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int c = c0 + 16 * i;
-            if (c < NC) {
-                const float f = s_f[c];
-                acc.x = fmaf(v[i].x, f, acc.x);
-                acc.y = fmaf(v[i].y, f, acc.y);
-                acc.z = fmaf(v[i].z, f, acc.z);
-                acc.w = fmaf(v[i].w, f, acc.w);
-            }
+            if (c < NC) add(c, v[i].x, v[i].y, v[i].z, v[i].w);
         }
     }
     acc.x += __shfl_xor(acc.x, 16); acc.y += __shfl_xor(acc.y, 16);
