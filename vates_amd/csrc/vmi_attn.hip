@@ -712,9 +712,13 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     const uint4* wrow = reinterpret_cast<const uint4*>(M.w + (size_t)r * (K / 8));
     uint4 wv[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) wv[m] = wrow[kw * 16 + 4 * m + q4];
-    const uint4 sv = *reinterpret_cast<const uint4*>(M.s + (size_t)r * G + kw * 8);
-    const uint4 bv = *reinterpret_cast<const uint4*>(M.b + (size_t)r * G + kw * 8);
+    for (int m = 0; m < 4; ++m) {  // weights are read once per step: nontemporal
+        const vmi_u4 u = __builtin_nontemporal_load(reinterpret_cast<const vmi_u4*>(wrow) + kw * 16 + 4 * m + q4);
+        wv[m] = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+    const vmi_u4 su = __builtin_nontemporal_load(reinterpret_cast<const vmi_u4*>(M.s + (size_t)r * G + kw * 8));
+    const vmi_u4 bu = __builtin_nontemporal_load(reinterpret_cast<const vmi_u4*>(M.b + (size_t)r * G + kw * 8));
+    const uint4 sv = make_uint4(su[0], su[1], su[2], su[3]), bv = make_uint4(bu[0], bu[1], bu[2], bu[3]);
     // the residual of this thread's output (first pass of the final loop) as
     // raw bf16 bits, issued now so that its latency overlaps the weights'; a
     // branch-free buffer load whose value is first used at the end, so no

@@ -233,8 +233,10 @@ __global__ __launch_bounds__(kGFThreads) void k_gdn_block(GdnArgs a) {
             }
             yo = vmi_row_sum16(yo);
             float* dst = slot + ((size_t)h * kGHead + row) * kGHead + d0;
-            *reinterpret_cast<float4*>(dst) = make_float4(S[j][0], S[j][1], S[j][2], S[j][3]);
-            *reinterpret_cast<float4*>(dst + 64) = make_float4(S[j][4], S[j][5], S[j][6], S[j][7]);
+            // the ring is read back at the next call at the earliest: nontemporal stores
+            const vmi_f4 lo = {S[j][0], S[j][1], S[j][2], S[j][3]}, hi = {S[j][4], S[j][5], S[j][6], S[j][7]};
+            __builtin_nontemporal_store(lo, reinterpret_cast<vmi_f4*>(dst));
+            __builtin_nontemporal_store(hi, reinterpret_cast<vmi_f4*>(dst + 64));
             if ((lane & 15) == 0) s_y[t][row] = yo;
         }
     }
