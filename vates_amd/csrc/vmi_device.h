@@ -255,6 +255,20 @@ __device__ __forceinline__ void vmi_lds_dma16_opaque(const void* g, const void* 
     (void)lds;
 #endif
 }
+// Nontemporal form, same contract: for a stream read once (no reuse through L2).
+__device__ __forceinline__ void vmi_lds_dma16_opaque_nt(const void* g, const void* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t m0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :
+                 : "v"(g), "s"(m0)
+                 : "memory", "m0");
+#else
+    (void)g;
+    (void)lds;
+#endif
+}
 // The 4-byte form (lane l's dword lands at lds + 4*l), same contract.
 __device__ __forceinline__ void vmi_lds_dma4_opaque(const void* g, const void* lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -329,6 +343,13 @@ __device__ __forceinline__ vmi_u4 vmi_bload_b128_nt(__amdgpu_buffer_rsrc_t r, ui
     o[2] = v[2];
     o[3] = v[3];
     return o;
+}
+__device__ __forceinline__ uint2 vmi_bload_b64_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 2);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t vmi_bload_b32_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 2);
 }
 __device__ __forceinline__ uint2 vmi_bload_b64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);

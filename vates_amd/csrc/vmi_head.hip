@@ -164,7 +164,7 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
             const int r = 4 * i + g;
             const int row = min(tile * 16 + r, V - 1);
             const uint8_t* src = wbase + (size_t)row * row_bytes + 256 * c + 16 * ((lane & 15) ^ r);
-            vmi_lds_dma16_opaque(src, buf + 1024 * i);
+            vmi_lds_dma16_opaque_nt(src, buf + 1024 * i);
         }
     };
 

@@ -354,17 +354,17 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     if (nwords >= 4) {
 #pragma unroll
         for (int i = 0; i < (CPL / 16 > 0 ? CPL / 16 : 1); ++i) {
-            const vmi_u4 q = vmi_bload_b128(rw, (4 * i < nwords) ? wbase + 16u * i : VMI_OOB, 0);
+            const vmi_u4 q = vmi_bload_b128_nt(rw, (4 * i < nwords) ? wbase + 16u * i : VMI_OOB, 0);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 if (4 * i + j < CPL / 4) wword[4 * i + j] = q[j];
         }
     } else if (nwords == 2) {
-        const uint2 q = vmi_bload_b64(rw, wbase, 0);
+        const uint2 q = vmi_bload_b64_nt(rw, wbase, 0);
         wword[0] = q.x;
         wword[1] = q.y;
     } else {
-        wword[0] = vmi_bload_b32(rw, wbase, 0);
+        wword[0] = vmi_bload_b32_nt(rw, wbase, 0);
     }
     const uint32_t sv = vmi_bload_b16(rs, (uint32_t)(c0 / 64) * 2u, 0);
     const uint32_t bv = vmi_bload_b16(rb, (uint32_t)(c0 / 64) * 2u, 0);
@@ -776,26 +776,26 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     vmi_u4 sg4[NSV], su4[NSV];
 #pragma unroll
     for (int i = 0; i < NSV; ++i) {
-        sg4[i] = vmi_bload_b128(rgs, sboff, 16u * i);
-        su4[i] = vmi_bload_b128(rus, sboff, 16u * i);
+        sg4[i] = vmi_bload_b128_nt(rgs, sboff, 16u * i);
+        su4[i] = vmi_bload_b128_nt(rus, sboff, 16u * i);
     }
     uint32_t bgw[NB], buw[NB];
     {
         const uint32_t boff = sboff + 4u * NB * q;
         if constexpr (NB == 4) {
-            const vmi_u4 g = vmi_bload_b128(rgb, boff, 0), u = vmi_bload_b128(rub, boff, 0);
+            const vmi_u4 g = vmi_bload_b128_nt(rgb, boff, 0), u = vmi_bload_b128_nt(rub, boff, 0);
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
                 bgw[b] = g[b];
                 buw[b] = u[b];
             }
         } else if constexpr (NB == 2) {
-            const uint2 g = vmi_bload_b64(rgb, boff, 0), u = vmi_bload_b64(rub, boff, 0);
+            const uint2 g = vmi_bload_b64_nt(rgb, boff, 0), u = vmi_bload_b64_nt(rub, boff, 0);
             bgw[0] = g.x; bgw[1] = g.y;
             buw[0] = u.x; buw[1] = u.y;
         } else {
-            bgw[0] = vmi_bload_b32(rgb, boff, 0);
-            buw[0] = vmi_bload_b32(rub, boff, 0);
+            bgw[0] = vmi_bload_b32_nt(rgb, boff, 0);
+            buw[0] = vmi_bload_b32_nt(rub, boff, 0);
         }
     }
     // Weights in whole 128-byte lines, nontemporal: load pair p covers rows
@@ -1142,7 +1142,7 @@ __global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
 #pragma unroll
                 for (int m = 0; m < NM2; ++m) {
                     const int g = 2 * m + h;
-                    wts[i][m] = vmi_bload_b64(rw, g < NG ? (uint32_t)(rho * RB + g * 32 + 8 * q) : VMI_OOB, 0);
+                    wts[i][m] = vmi_bload_b64_nt(rw, g < NG ? (uint32_t)(rho * RB + g * 32 + 8 * q) : VMI_OOB, 0);
                 }
                 // one dword per lane: lane l < 4NG the scales' dword l, 4NG <= l <
                 // 8NG the biases' dword l - 4NG
@@ -1150,7 +1150,7 @@ __global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
                 if (real && lane < 8 * NG)
                     sbp = lane < 4 * NG ? reinterpret_cast<const uint32_t*>(md.s + ((size_t)sj * H + h0) * NG) + lane
                                         : reinterpret_cast<const uint32_t*>(md.b + ((size_t)sj * H + h0) * NG) + (lane - 4 * NG);
-                sbv[i] = *sbp;
+                sbv[i] = __builtin_nontemporal_load(sbp);
                 // X [T][NG], then the combine weights [T] and ranks [T] (the shared
                 // expert: gate logits, no ranks)
 #pragma unroll
