@@ -363,7 +363,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) kr[h][kk] = vmi_bload_b128(rk, kbase + (uint32_t)(h * 8 + kk) * 1024u, 0);
+            for (int kk = 0; kk < 8; ++kk) kr[h][kk] = vmi_bload_b128_nt(rk, kbase + (uint32_t)(h * 8 + kk) * 1024u, 0);
     }
 #pragma unroll
     for (int sb = 0; sb < kChunkWaves; ++sb) {
@@ -371,7 +371,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         const uint32_t vbase =
             kKvBlock * bs < L ? (uint32_t)bs * kKvBlockElems * 2u + (uint32_t)(2 * w) * 1024u + lane * 16u : VMI_OOB;
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) vr[dt][sb] = vmi_bload_b128(rv, vbase + (uint32_t)dt * 1024u, 0);
+        for (int dt = 0; dt < 2; ++dt) vr[dt][sb] = vmi_bload_b128_nt(rv, vbase + (uint32_t)dt * 1024u, 0);
     }
 
     __syncthreads();

@@ -150,8 +150,8 @@ __global__ __launch_bounds__(kGFThreads) void k_gdn_block(GdnArgs a) {
     const uint32_t offB = offA + 64u * kGHead * 4u;
     const __amdgpu_buffer_rsrc_t rs =
         vmi_rsrc(a.state_ring + (size_t)(pos0 % a.n_slots) * slot_elems, pos0 > 0 ? (uint32_t)(slot_elems * 4) : 0u);
-    const vmi_u4 sa0 = vmi_bload_b128(rs, offA, 0), sa1 = vmi_bload_b128(rs, offA + 256u, 0);
-    const vmi_u4 sb0 = vmi_bload_b128(rs, offB, 0), sb1 = vmi_bload_b128(rs, offB + 256u, 0);
+    const vmi_u4 sa0 = vmi_bload_b128_nt(rs, offA, 0), sa1 = vmi_bload_b128_nt(rs, offA + 256u, 0);
+    const vmi_u4 sb0 = vmi_bload_b128_nt(rs, offB, 0), sb1 = vmi_bload_b128_nt(rs, offB + 256u, 0);
 
     // 2. conv and gate scalars
     if (conv_wave) {
