@@ -41,12 +41,12 @@ ZIPF_S, ZIPF_ALPHA = 1.1, 0.5
 # rocprofv3 counter passes over `--layers 8 --steps 3 --warmup 1 --no-graph`
 # (32 layer calls, 31.42 distinct experts on average, 58,525,824 algorithmic
 # bytes a call): FETCH_SIZE summed over k_router, k_gateup and k_down_rows
-# 29,697.0 KiB a call x 2.000 (a plain copy of 512 MiB reads 262,157 KiB on
+# 29,703.7 KiB a call x 2.000 (a plain copy of 512 MiB reads 262,157 KiB on
 # that counter) plus WRITE_SIZE 227.8 KiB x 1.000 (the copy's 524,288 KiB) =
-# 61,049,661 bytes, i.e. 1.0431 of the algorithmic bytes.
-MOE_TRAFFIC_PER_ALGO_BYTE = 1.0431
+# 61,066,445 bytes, i.e. 1.0434 of the algorithmic bytes.
+MOE_TRAFFIC_PER_ALGO_BYTE = 1.0434
 MOE_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over 32 layer calls, scaled by a 512 MiB copy "
-                      "(x2.000 / x1.000): 61,049,661 B against 58,525,824 algorithmic B")
+                      "(x2.000 / x1.000): 61,066,445 B against 58,525,824 algorithmic B")
 
 
 def eprint(*a):
