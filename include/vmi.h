@@ -332,6 +332,21 @@ int vmi_accept_greedy(const int32_t* drafts, const int32_t* preds, int P, int K,
                       void* stream);
 
 /* ------------------------------------------------------------------------
+ * vmi_spec_commit -- the commit of one speculative step on the device, after
+ * vmi_accept_greedy (mode 1), so that a captured step needs no host round
+ * trip: H = hid[matched] (bf16 [hidden]; hid holds the pre-norm hidden of
+ * the K + 1 verify rows), x = the last emitted token, pos += accepted_len,
+ * mtp_len += matched + 1, and mtp_pos[i] = mtp_len + i for i < K (the next
+ * step's draft positions).  Replaces the state update of the reference's
+ * decode loop: mlx_streaming/mtp/generate.py:850-856 (the next input token
+ * is the last emitted one), :819 (accepted_len), and kv_cache.py:222-251
+ * (committing the accepted prefix by setting lengths).  result is
+ * vmi_accept_greedy's record; H must not overlap hid.  K <= 15.
+ * ------------------------------------------------------------------------ */
+int vmi_spec_commit(const int32_t* result, const uint16_t* hid, int hidden, int K, uint16_t* H, int32_t* x,
+                    int32_t* pos, int32_t* mtp_len, int32_t* mtp_pos, void* stream);
+
+/* ------------------------------------------------------------------------
  * vmi_accept_stochastic -- speculative sampling (Leviathan et al. 2023,
  * Algorithm 1; Chen et al. 2023) in one kernel.  No reference counterpart:
  * the reference accepts greedily only (generate.py:338-351); this is the

@@ -66,6 +66,8 @@ _SIGNATURES = {
                                     c_void_p, c_void_p]),
     "vmi_synth_bf16": (c_int, [c_uint64, c_uint32, c_int64, c_float, c_void_p, c_void_p]),
     "vmi_accept_greedy": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "vmi_spec_commit": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                c_void_p]),
     "vmi_accept_stochastic_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "vmi_accept_stochastic": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_float, c_uint64,
                                       c_uint64, c_void_p, c_void_p, c_size_t, c_void_p]),

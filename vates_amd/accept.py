@@ -54,6 +54,26 @@ def accept_greedy(drafts: torch.Tensor, preds: torch.Tensor, *, mode: int = 1, o
     return out
 
 
+def spec_commit(rec: torch.Tensor, hid: torch.Tensor, H: torch.Tensor, x: torch.Tensor, pos: torch.Tensor,
+                mtp_len: torch.Tensor, mtp_pos: torch.Tensor, *, stream=None) -> None:
+    """Commits one speculative step on the device from accept_greedy's record
+    (mode 1): H = hid[matched], x = the last emitted token, pos +=
+    accepted_len, mtp_len += matched + 1, mtp_pos = mtp_len + arange(K)."""
+    dev = rec.device
+    K = mtp_pos.numel()
+    if hid.dim() != 2 or hid.shape[0] < K + 1:
+        raise VmiError(f"hid must hold at least {K + 1} rows")
+    hidden = hid.shape[1]
+    if H.numel() != hidden:
+        raise VmiError(f"H must hold {hidden} values")
+    for t, name, elem in ((rec, "result", 4), (hid, "hid", 2), (H, "H", 2), (x, "x", 4), (pos, "pos", 4),
+                          (mtp_len, "mtp_len", 4), (mtp_pos, "mtp_pos", 4)):
+        _require(t, name, elem, dev)
+    rc = load().vmi_spec_commit(rec.data_ptr(), hid.data_ptr(), hidden, K, H.data_ptr(), x.data_ptr(),
+                                pos.data_ptr(), mtp_len.data_ptr(), mtp_pos.data_ptr(), _stream_handle(stream))
+    check(rc, "vmi_spec_commit")
+
+
 def accept_stochastic(target_logits: torch.Tensor, draft_logits: Optional[torch.Tensor], drafts: torch.Tensor, *,
                       temperature: float, top_p: float, seed: int, offset: int, out: Optional[torch.Tensor] = None,
                       stream=None) -> torch.Tensor:

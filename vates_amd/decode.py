@@ -27,7 +27,7 @@ from typing import List, Optional
 import torch
 
 from ._lib import VmiError
-from .accept import accept_greedy
+from .accept import accept_greedy, spec_commit
 from .attention import AttentionLayer, KVCache
 from .gdn import GatedDeltaNetLayer, GdnCache
 from .head import lm_head
@@ -246,11 +246,12 @@ class GraphSpecDecoder:
         self.pos, self.mtp_len = self.state[0:1], self.state[1:2]
         self.mtp_pos = torch.zeros(K, dtype=torch.int32, device=dev)
         self.steps_ar = torch.arange(K, dtype=torch.int32, device=dev)
-        self.x = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.H = torch.zeros((1, model.hidden), dtype=torch.bfloat16, device=dev)
-        self.drafts = torch.zeros(K, dtype=torch.int32, device=dev)
+        # the verify batch [x, d1..dK] holds the step's input token and the
+        # drafts the MTP layer writes; row 0 of the MTP update holds H_last
         self.verify = torch.zeros(K + 1, dtype=torch.int32, device=dev)
+        self.x, self.drafts = self.verify[0:1], self.verify[1:]
         self.hseq = torch.zeros((K + 1, model.hidden), dtype=torch.bfloat16, device=dev)
+        self.H = self.hseq[0:1]
         self.rec_buf = torch.zeros(4 + K + 1, dtype=torch.int32, device=dev)
         self.use_planted = planted
         self.planted = torch.zeros(K, dtype=torch.int32, device=dev)
@@ -260,26 +261,19 @@ class GraphSpecDecoder:
 
     def _step(self) -> torch.Tensor:
         K, mtp = self.K, self.model.mtp
-        torch.add(self.steps_ar, self.mtp_len, out=self.mtp_pos)
         h, tok = self.H, self.x
         for i in range(K):
-            am, h, _ = mtp.step(h, tok, self.drafter.cache, pos_device=self.mtp_pos[i:i + 1])
-            self.drafts[i:i + 1].copy_(am)
-            tok = self.drafts[i:i + 1]
+            d = self.drafts[i:i + 1]
+            _, h, _ = mtp.step(h, tok, self.drafter.cache, pos_device=self.mtp_pos[i:i + 1], argmax_out=d)
+            tok = d
         if self.use_planted:
             self.drafts.copy_(self.planted)
-        self.verify[0:1].copy_(self.x)
-        self.verify[1:].copy_(self.drafts)
         preds, hid, _ = self.model.forward(self.verify, self.caches, 0, pos_device=self.pos)
         rec = accept_greedy(self.drafts, preds, mode=1, out=self.rec_buf)
-        self.hseq[0:1].copy_(self.H)
         self.hseq[1:].copy_(hid[:K])
         mtp.advance(self.hseq, self.verify, self.drafter.cache, pos_device=self.mtp_len)
-        # commit on the device
-        self.H.copy_(hid.index_select(0, rec[1:2]))
-        self.x.copy_(torch.gather(rec, 0, (rec[0:1] + 3).long()))
-        self.pos.add_(rec[2:3])
-        self.mtp_len.add_(rec[1:2] + 1)
+        # commit on the device (also the next step's draft positions)
+        spec_commit(rec, hid, self.H, self.x, self.pos, self.mtp_len, self.mtp_pos)
         return rec
 
     def start(self, x: torch.Tensor, H_last: torch.Tensor, pos: int) -> None:
@@ -288,17 +282,18 @@ class GraphSpecDecoder:
         self.x.copy_(x)
         self.H.copy_(H_last)
         self.state.copy_(torch.tensor([pos, self.drafter.cache.length], dtype=torch.int32))
+        torch.add(self.steps_ar, self.mtp_len, out=self.mtp_pos)
         self.pos_host = pos
 
     def capture(self) -> None:
         """Warms the workspaces up on the capture stream, restores the state,
         and captures one step."""
-        saved = [t.clone() for t in (self.state, self.x, self.H)]
+        saved = [t.clone() for t in (self.state, self.x, self.H, self.mtp_pos)]
         self.stream.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(self.stream):
             self._step()
         self.stream.synchronize()
-        for t, v in zip((self.state, self.x, self.H), saved):
+        for t, v in zip((self.state, self.x, self.H, self.mtp_pos), saved):
             t.copy_(v)
         torch.cuda.synchronize(self.dev)
         self.graph = torch.cuda.CUDAGraph()

@@ -73,11 +73,12 @@ class MTPLayer:
         return rmsnorm(x, self.w.norm, eps=self.w.eps, stream=stream)
 
     def step(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, *, want_logits: bool = False,
-             stream=None, pos_device: Optional[torch.Tensor] = None):
+             stream=None, pos_device: Optional[torch.Tensor] = None, argmax_out: Optional[torch.Tensor] = None):
         """(argmax int32 [T], MTP hidden H bf16 [T, H], logits f32 [T, V] or None).
-        With pos_device the cache position is read on the device."""
+        With pos_device the cache position is read on the device; with
+        argmax_out (int32 [T]) the argmax is written there."""
         Hn = self._trunk(hidden, tokens, cache, stream, pos_device)
-        logits, am, _ = lm_head(Hn, self.w.lm_head, None, want_logits=want_logits, stream=stream)
+        logits, am, _ = lm_head(Hn, self.w.lm_head, None, want_logits=want_logits, argmax=argmax_out, stream=stream)
         return am, Hn, logits
 
     def advance(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None,
