@@ -153,3 +153,36 @@ def test_sample_top_p_bit_exact(gpu, orc, V):
         want = orc.sample_top_p(logits, temp, top_p, 1234, 77)
         got = sample_top_p(_t(logits, gpu), temperature=temp, top_p=top_p, seed=1234, offset=77).cpu().numpy()
         assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("m", [0, 1, 3])
+def test_spec_commit_state_update(gpu, orc, m):
+    """vmi_spec_commit after a mode-1 acceptance record: H = hid[m], x = the last
+    emitted token, pos += accepted_len, mtp_len += m + 1, mtp_pos = mtp_len + i;
+    expectations from the record's definition, on random state."""
+    log(f"case: spec_commit K=3 matched={m}")
+    import torch
+    from vates_amd.accept import accept_greedy, spec_commit
+    K, hidden = 3, 2048
+    g = torch.Generator().manual_seed(11 + m)
+    drafts = torch.randint(0, 151936, (K,), generator=g, dtype=torch.int32)
+    preds = torch.randint(0, 151936, (K + 1,), generator=g, dtype=torch.int32)
+    preds[:m] = drafts[:m]
+    if m < K:
+        preds[m] = (drafts[m] + 1) % 151936
+    rec = accept_greedy(drafts.to(gpu), preds.to(gpu), mode=1)
+    hid = torch.randn((K + 1, hidden), generator=g).to(torch.bfloat16).to(gpu)
+    H = torch.zeros((1, hidden), dtype=torch.bfloat16, device=gpu)
+    x = torch.zeros(1, dtype=torch.int32, device=gpu)
+    state = torch.tensor([1000, 400], dtype=torch.int32, device=gpu)
+    mtp_pos = torch.zeros(K, dtype=torch.int32, device=gpu)
+    spec_commit(rec, hid, H, x, state[0:1], state[1:2], mtp_pos)
+    torch.cuda.synchronize()
+    r = rec.cpu().tolist()
+    assert r[1] == m and r[2] == m + 1
+    emitted = drafts[:m].tolist() + [int(preds[m])]
+    assert r[4:4 + r[0]] == emitted
+    assert torch.equal(H[0].view(torch.int16), hid[m].view(torch.int16))
+    assert int(x) == emitted[-1]
+    assert state.cpu().tolist() == [1000 + m + 1, 400 + m + 1]
+    assert mtp_pos.cpu().tolist() == [400 + m + 1 + i for i in range(K)]
