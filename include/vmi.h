@@ -123,6 +123,23 @@ int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, cons
                   void* stream);
 
 /* ------------------------------------------------------------------------
+ * vmi_moe_layer_noalloc -- vmi_moe_layer without a workspace argument and
+ * without any allocation: no counterpart in the reference.  It is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The same kernels run on a
+ * static device array of 3 MiB per GPU (held until the process ends, looked
+ * up once per device); shapes whose workspace
+ * (vmi_moe_layer_workspace_bytes) exceeds it are rejected with
+ * VMI_ERR_UNSUPPORTED.  Every call on one GPU shares that array and leaves
+ * its contents behind: calls that overlap on one GPU (two streams, two
+ * threads) race and must be serialised by the caller.  status: a device word
+ * that receives the VMI_STATUS_* bits OR-ed in (the caller clears it), or
+ * NULL to drop them.  Other arguments as vmi_moe_layer.
+ * ------------------------------------------------------------------------ */
+int vmi_moe_layer_noalloc(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, const uint16_t* residual,
+                          uint16_t* out, int32_t* ids_out, float* scores_out, uint32_t* status, void* stream);
+
+/* ------------------------------------------------------------------------
  * vmi_moe_prefill -- the same layer on a long prompt, expert-major; replaces
  * FileStreamingMoeBlock._expert_major_forward
  *   mlx_streaming/core/moe/block.py:111-243 (histogram + argsort of routed

@@ -31,6 +31,8 @@
 // Semantics follow native/ext/compute/fused_moe.cpp:221-298 (slot pair kernel
 // and reduce_pairs) and mlx_streaming/core/moe/block.py:102-109, 321-329, 1008.
 
+#include <mutex>
+
 #include "vmi_device.h"
 #include "vmi_internal.h"
 
@@ -1428,10 +1430,11 @@ extern "C" int vmi_fused_moe_slots(const void* x, int x_dtype, const int32_t* lo
     return VMI_OK;
 }
 
-extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, const uint16_t* residual,
-                             uint16_t* out, int32_t* ids_out, float* scores_out, void* workspace,
-                             size_t workspace_bytes, void* stream) {
-    vmi::clear_error();
+namespace {
+
+// Argument checks of vmi_moe_layer (and its no-allocation variant); VMI_OK when
+// the layer can run.
+int check_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, const uint16_t* out) {
     if (!desc) return vmi::fail(VMI_ERR_INVALID, "null desc");
     const vmi_moe_layer_desc& D = *desc;
     int rc = check_shape(T, D.top_k, D.hidden, D.inter, D.group, D.bits);
@@ -1454,10 +1457,14 @@ extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, 
         return vmi::fail(VMI_ERR_INVALID, "shared expert arrays must be non-null and 16-byte aligned");
     if (has_sgate && !qmat_ok(D.shared_expert_gate)) return vmi::fail(VMI_ERR_INVALID, "shared_expert_gate arrays");
     if (D.cap <= 0) return vmi::fail(VMI_ERR_INVALID, "cap=%d", D.cap);
-    const vmi::MoeWorkspace ws = vmi::carve_workspace(workspace, T, D.top_k, D.hidden, D.inter, D.num_experts);
-    if (!workspace || workspace_bytes < ws.bytes)
-        return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", ws.bytes, workspace_bytes);
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    return VMI_OK;
+}
+
+// The three kernels of one MoE layer call on a carved workspace.
+int launch_moe_layer(const vmi_moe_layer_desc& D, const uint16_t* x, int T, const uint16_t* residual, uint16_t* out,
+                     int32_t* ids_out, float* scores_out, const vmi::MoeWorkspace& ws, hipStream_t s) {
+    const int has_shared = D.shared_gate.w != nullptr;
+    const int has_sgate = has_shared && D.shared_expert_gate.w != nullptr;
     const OperandOut ops{ws.xop, ws.xsum, ws.fscale};
 
     RouterArgs ra{};
@@ -1504,6 +1511,71 @@ extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, 
     e = launch_down(da, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "k_down_rows launch");
     return VMI_OK;
+}
+
+// Static scratch of vmi_moe_layer_noalloc: one copy per device, held until the
+// process ends.  Host code never passes the array's name to a kernel (on the
+// host it is a stand-in, not a device address): every use goes through the
+// per-device address from hipGetSymbolAddress.
+constexpr size_t kNoAllocScratchBytes = (size_t)3 << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// Device address of the current device's scratch, looked up once per device.
+int scratch_for_current_device(void** ptr) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return vmi::hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return vmi::fail(VMI_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return vmi::hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return vmi::fail(VMI_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return VMI_OK;
+}
+
+}  // namespace
+
+extern "C" int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, const uint16_t* residual,
+                             uint16_t* out, int32_t* ids_out, float* scores_out, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+    vmi::clear_error();
+    int rc = check_moe_layer(desc, x, T, out);
+    if (rc) return rc;
+    const vmi_moe_layer_desc& D = *desc;
+    const vmi::MoeWorkspace ws = vmi::carve_workspace(workspace, T, D.top_k, D.hidden, D.inter, D.num_experts);
+    if (!workspace || workspace_bytes < ws.bytes)
+        return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", ws.bytes, workspace_bytes);
+    return launch_moe_layer(D, x, T, residual, out, ids_out, scores_out, ws, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int vmi_moe_layer_noalloc(const vmi_moe_layer_desc* desc, const uint16_t* x, int T,
+                                     const uint16_t* residual, uint16_t* out, int32_t* ids_out, float* scores_out,
+                                     uint32_t* status, void* stream) {
+    vmi::clear_error();
+    int rc = check_moe_layer(desc, x, T, out);
+    if (rc) return rc;
+    const vmi_moe_layer_desc& D = *desc;
+    const size_t need = vmi::carve_workspace(nullptr, T, D.top_k, D.hidden, D.inter, D.num_experts).bytes;
+    if (need > kNoAllocScratchBytes)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d top_k=%d hidden=%d inter=%d num_experts=%d needs %zu bytes of "
+                         "scratch, beyond the static %zu", T, D.top_k, D.hidden, D.inter, D.num_experts, need,
+                         kNoAllocScratchBytes);
+    void* base = nullptr;
+    rc = scratch_for_current_device(&base);
+    if (rc) return rc;
+    vmi::MoeWorkspace ws = vmi::carve_workspace(base, T, D.top_k, D.hidden, D.inter, D.num_experts);
+    // the device status bits go to the caller's word (left as they are when
+    // the caller gives none: the scratch's own word is never read)
+    if (status) ws.status = status;
+    return launch_moe_layer(D, x, T, residual, out, ids_out, scores_out, ws, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int vmi_workspace_status(void* workspace, void* stream, uint32_t* flags) {
