@@ -41,6 +41,8 @@ enum vmi_dtype { VMI_F32 = 0, VMI_BF16 = 1 };
 /* Device-side status bits (vmi_workspace_status). */
 #define VMI_STATUS_BAD_SLOT 0x1u   /* a routed slot was outside [0, cap) */
 #define VMI_STATUS_BAD_ROUTE 0x2u  /* router produced a non-finite logit */
+#define VMI_STATUS_BAD_POS 0x4u    /* a device-side position outside [0, max_len - T] */
+#define VMI_STATUS_BAD_RECORD 0x8u /* an acceptance record outside what vmi_spec_commit allows */
 
 /* Last error message of the calling thread ("" when none). */
 const char* vmi_last_error(void);
@@ -188,16 +190,20 @@ int vmi_dequant_affine(vmi_qmat m, int rows, int cols, int group, int bits, floa
  * weight bf16 [vocab, hidden] (a tied embedding or the head).  Outputs, each
  * optional: logits f32 [T, vocab]; argmax int32 [T] and max_logit f32 [T],
  * the first maximum of each row (ties to the lower vocabulary row, NaN
- * never wins - mx.argmax's rule).  Accumulation is fp32 (bf16 MFMA).
+ * never wins - mx.argmax's rule); top_prob f32 [T], the softmax probability
+ * of the argmax, 1 / sum_j exp(l_j - max l) (fp32 running maxima and sums
+ * merged in a fixed order), the per-draft confidence of
+ * mlx_streaming/mtp/drafter.py:42-62 (conf *= softmax(lg)[d]).
+ * Accumulation is fp32 (bf16 MFMA).
  * Supported: T <= 16, hidden a multiple of 512 up to 2048, pointers 16-byte
- * aligned.  workspace (required when argmax or max_logit is requested):
+ * aligned.  workspace (required when argmax, max_logit or top_prob is requested):
  * vmi_lm_head_workspace_bytes(T, vocab) bytes, all zero before the first
  * call and left zero by every call; one call in flight per workspace.
  * ------------------------------------------------------------------------ */
 size_t vmi_lm_head_workspace_bytes(int T, int vocab);
 int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weight, float norm_eps,
                 const uint16_t* weight, int vocab, float* logits, int32_t* argmax, float* max_logit,
-                void* workspace, size_t workspace_bytes, void* stream);
+                float* top_prob, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * vmi_qgemv -- y = W x for a small batch of tokens with an affine-quantised W
@@ -237,10 +243,12 @@ int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int 
  * result does not depend on the batch it is verified in (bit for bit).
  * pos_device (int32 on the device, or NULL): when set, the batch position is
  * read from it when the kernels run instead of pos0 (a captured graph replays
- * with positions that advance on the device); it is clamped to
- * [0, max_len - T], and the chunk grid covers the whole capacity.
- * workspace: vmi_attention_layer_workspace_bytes(T, hidden, n_heads,
- * n_kv_heads, max_len) bytes.
+ * with positions that advance on the device); a value outside
+ * [0, max_len - T] is clamped into it and sets VMI_STATUS_BAD_POS in the
+ * workspace's status word (vmi_workspace_status), and the chunk grid covers
+ * the whole capacity.  workspace: vmi_attention_layer_workspace_bytes(T,
+ * hidden, n_heads, n_kv_heads, max_len) bytes whose first 4 bytes (the
+ * status word) are zero before its first use.
  * ------------------------------------------------------------------------ */
 typedef struct vmi_attn_layer_desc {
     int hidden, n_heads, n_kv_heads, head_dim, rope_dim;
@@ -350,18 +358,27 @@ int vmi_accept_greedy(const int32_t* drafts, const int32_t* preds, int P, int K,
 
 /* ------------------------------------------------------------------------
  * vmi_spec_commit -- the commit of one speculative step on the device, after
- * vmi_accept_greedy (mode 1), so that a captured step needs no host round
- * trip: H = hid[matched] (bf16 [hidden]; hid holds the pre-norm hidden of
- * the K + 1 verify rows), x = the last emitted token, pos += accepted_len,
- * mtp_len += matched + 1, and mtp_pos[i] = mtp_len + i for i < K (the next
- * step's draft positions).  Replaces the state update of the reference's
- * decode loop: mlx_streaming/mtp/generate.py:850-856 (the next input token
- * is the last emitted one), :819 (accepted_len), and kv_cache.py:222-251
- * (committing the accepted prefix by setting lengths).  result is
- * vmi_accept_greedy's record; H must not overlap hid.  K <= 15.
+ * vmi_accept_greedy, so that a captured step needs no host round trip.  With
+ * acc = accepted_len and w = the winning path of the record:
+ *   H = hid[w][acc - 1] (bf16 [hidden]; hid [paths][rows][hidden] holds the
+ *   pre-norm hidden of the verify rows), x = the last emitted token,
+ *   pos += acc, mtp_len += acc, mtp_pos[i] = mtp_len + i for i < K (the next
+ *   step's draft positions).
+ * Both verify layouts: rows = K + 1 after a mode-1 record (T = K + 1, acc =
+ * matched + 1, a bonus token when every draft matches), rows = the step's
+ * verify length after a mode-0 record (the reference's T = K layout: acc =
+ * min(matched + 1, rows), x = the last draft when all match), paths > 1 for
+ * a tree.  Replaces the state update of the reference's decode loop:
+ * mlx_streaming/mtp/generate.py:819 (accepted_len), :850-856 (new tokens and
+ * the next input x), :895 (H_last = rH[:, -1]) and kv_cache.py:222-251
+ * (committing the accepted prefix by setting lengths); tree_verify_step's
+ * winner row, generate.py:386 and :416-420.  A record with no emitted token, acc
+ * outside [1, rows], more than rows + 1 tokens or a path outside [0, paths)
+ * changes nothing and ORs VMI_STATUS_BAD_RECORD into *status (may be NULL).
+ * H must not overlap hid.  K <= 15, rows <= 16.
  * ------------------------------------------------------------------------ */
-int vmi_spec_commit(const int32_t* result, const uint16_t* hid, int hidden, int K, uint16_t* H, int32_t* x,
-                    int32_t* pos, int32_t* mtp_len, int32_t* mtp_pos, void* stream);
+int vmi_spec_commit(const int32_t* result, const uint16_t* hid, int rows, int paths, int hidden, int K, uint16_t* H,
+                    int32_t* x, int32_t* pos, int32_t* mtp_len, int32_t* mtp_pos, uint32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------
  * vmi_accept_stochastic -- speculative sampling (Leviathan et al. 2023,

@@ -56,9 +56,11 @@ def test_invalid_arguments_rejected_before_any_device_call(lib):
     assert rc == L.VMI_ERR_UNSUPPORTED
     rc = lib.vmi_moe_layer(None, None, 4, None, None, None, None, None, 0, None)
     assert rc == L.VMI_ERR_INVALID
-    rc = lib.vmi_spec_commit(None, None, 2048, 0, None, None, None, None, None, None)
+    rc = lib.vmi_spec_commit(None, None, 4, 1, 2048, 0, None, None, None, None, None, None, None)
     assert rc == L.VMI_ERR_INVALID and b"K=0" in lib.vmi_last_error()
-    rc = lib.vmi_spec_commit(None, None, 2048, 3, None, None, None, None, None, None)
+    rc = lib.vmi_spec_commit(None, None, 0, 1, 2048, 3, None, None, None, None, None, None, None)
+    assert rc == L.VMI_ERR_INVALID and b"rows=0" in lib.vmi_last_error()
+    rc = lib.vmi_spec_commit(None, None, 4, 1, 2048, 3, None, None, None, None, None, None, None)
     assert rc == L.VMI_ERR_INVALID
 
 

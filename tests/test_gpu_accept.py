@@ -155,34 +155,64 @@ def test_sample_top_p_bit_exact(gpu, orc, V):
         assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("m", [0, 1, 3])
-def test_spec_commit_state_update(gpu, orc, m):
-    """vmi_spec_commit after a mode-1 acceptance record: H = hid[m], x = the last
-    emitted token, pos += accepted_len, mtp_len += m + 1, mtp_pos = mtp_len + i;
-    expectations from the record's definition, on random state."""
-    log(f"case: spec_commit K=3 matched={m}")
+@pytest.mark.parametrize("mode,T,m", [(1, 4, 0), (1, 4, 1), (1, 4, 3), (0, 3, 0), (0, 3, 2), (0, 3, 3), (0, 1, 1),
+                                      (0, 2, 0)])
+def test_spec_commit_state_update(gpu, orc, mode, T, m):
+    """vmi_spec_commit after an acceptance record of either layout (mode 1:
+    T = K + 1 rows; mode 0: the reference's T = K rows, accepted_len =
+    min(m + 1, T), x = the last draft when all match): H = hid[acc - 1],
+    x = the last emitted token, pos += acc, mtp_len += acc,
+    mtp_pos = mtp_len + i; expectations from the record's definition."""
+    log(f"case: spec_commit mode={mode} T={T} matched={m}")
     import torch
     from vates_amd.accept import accept_greedy, spec_commit
-    K, hidden = 3, 2048
-    g = torch.Generator().manual_seed(11 + m)
+    K = T - mode          # drafts checked
+    hidden = 2048
+    g = torch.Generator().manual_seed(11 + 7 * m + T + mode)
     drafts = torch.randint(0, 151936, (K,), generator=g, dtype=torch.int32)
-    preds = torch.randint(0, 151936, (K + 1,), generator=g, dtype=torch.int32)
+    preds = torch.randint(0, 151936, (T,), generator=g, dtype=torch.int32)
     preds[:m] = drafts[:m]
     if m < K:
         preds[m] = (drafts[m] + 1) % 151936
-    rec = accept_greedy(drafts.to(gpu), preds.to(gpu), mode=1)
-    hid = torch.randn((K + 1, hidden), generator=g).to(torch.bfloat16).to(gpu)
+    rec = accept_greedy(drafts.to(gpu), preds.to(gpu), mode=mode)
+    hid = torch.randn((T, hidden), generator=g).to(torch.bfloat16).to(gpu)
     H = torch.zeros((1, hidden), dtype=torch.bfloat16, device=gpu)
     x = torch.zeros(1, dtype=torch.int32, device=gpu)
     state = torch.tensor([1000, 400], dtype=torch.int32, device=gpu)
-    mtp_pos = torch.zeros(K, dtype=torch.int32, device=gpu)
-    spec_commit(rec, hid, H, x, state[0:1], state[1:2], mtp_pos)
+    mtp_pos = torch.zeros(3, dtype=torch.int32, device=gpu)
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
+    spec_commit(rec, hid, H, x, state[0:1], state[1:2], mtp_pos, rows=T, status=status)
     torch.cuda.synchronize()
     r = rec.cpu().tolist()
-    assert r[1] == m and r[2] == m + 1
-    emitted = drafts[:m].tolist() + [int(preds[m])]
+    acc = m + 1 if mode == 1 else min(m + 1, T)
+    assert r[1] == m and r[2] == acc
+    emitted = drafts[:m].tolist() + [int(preds[m])] if m < K or mode == 1 else drafts[:K].tolist()
     assert r[4:4 + r[0]] == emitted
-    assert torch.equal(H[0].view(torch.int16), hid[m].view(torch.int16))
+    assert torch.equal(H[0].view(torch.int16), hid[acc - 1].view(torch.int16))
     assert int(x) == emitted[-1]
-    assert state.cpu().tolist() == [1000 + m + 1, 400 + m + 1]
-    assert mtp_pos.cpu().tolist() == [400 + m + 1 + i for i in range(K)]
+    assert state.cpu().tolist() == [1000 + acc, 400 + acc]
+    assert mtp_pos.cpu().tolist() == [400 + acc + i for i in range(3)]
+    assert int(status) == 0
+
+
+def test_spec_commit_rejects_bad_record(gpu):
+    """A record whose accepted length exceeds the verify rows (here a mode-1
+    record of 4 rows committed as 2) changes nothing and sets
+    VMI_STATUS_BAD_RECORD."""
+    log("case: spec_commit with an out-of-range record")
+    import torch
+    from vates_amd._lib import VMI_STATUS_BAD_RECORD
+    from vates_amd.accept import accept_greedy, spec_commit
+    drafts = torch.tensor([5, 6, 7], dtype=torch.int32, device=gpu)
+    preds = torch.tensor([5, 6, 7, 8], dtype=torch.int32, device=gpu)
+    rec = accept_greedy(drafts, preds, mode=1)          # accepted_len 4
+    hid = torch.ones((4, 512), dtype=torch.bfloat16, device=gpu)
+    H = torch.zeros((1, 512), dtype=torch.bfloat16, device=gpu)
+    x = torch.full((1,), 99, dtype=torch.int32, device=gpu)
+    state = torch.tensor([10, 20], dtype=torch.int32, device=gpu)
+    mtp_pos = torch.zeros(3, dtype=torch.int32, device=gpu)
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
+    spec_commit(rec, hid[:2], H, x, state[0:1], state[1:2], mtp_pos, rows=2, status=status)
+    torch.cuda.synchronize()
+    assert int(status) == VMI_STATUS_BAD_RECORD
+    assert state.cpu().tolist() == [10, 20] and int(x) == 99 and not H.float().any()

@@ -7,8 +7,15 @@
   top-two logit margin exceeds 1e-2 of the logit scale.
 * Speculative decoding with K=3 emits exactly the tokens of non-speculative
   greedy decoding (the reference's lossless invariant,
-  tests/test_mtp_generate.py:421-489), with scripted drafts that make every
-  acceptance length 0..K occur, and with the MTP layer's own drafts.
+  tests/test_mtp_generate.py:421-489), in both verify layouts ([x, d1..dK],
+  and the reference's [x, d1..d_{K-1}], generate.py:604), eagerly and as
+  captured graphs, with scripted drafts that make every acceptance length
+  0..K occur, and with the MTP layer's own drafts; the graph decoder drafts
+  exactly what the eager drafter drafts from the same committed state.
+* Adaptive depth (draft_adaptive, drafter.py:42-62): the depth of every step
+  equals the tau rule replayed in float64 on the MTP logits of that step
+  (away from the threshold), the stream equals greedy decoding, and the
+  graph decoder reproduces the eager one step for step.
 * draft_paths takes its first tokens from the top-P of the MTP logits.
 """
 import sys
@@ -43,60 +50,9 @@ def _prompt(gpu, n=8, seed=5):
 
 
 def test_mtp_step_matches_oracle(gpu, orc, model):
-    log("case: one MTP step vs the oracle composition")
-    import torch
-    from vates_amd.mtp import MTPDrafter
-    mtp = model.mtp
-    w = mtp.w
-    H, V = SMALL["hidden"], SMALL["vocab"]
-    drafter = MTPDrafter(mtp, 64)
-    from vates_amd.synth import synth_bf16
-    h = synth_bf16(91, 77, (1, H), device=gpu)
-    tok = torch.tensor([123], dtype=torch.int32, device=gpu)
-    am, Hn, logits = mtp.step(h, tok, drafter.cache, want_logits=True)
-    torch.cuda.synchronize()
-    # oracle: emb/hid norms -> fc -> attention -> MoE (post-attention norm inside) -> norm -> head
-    emb = orc.rmsnorm_bf16(u16(w.embed)[123:124], u16(w.norm_emb), 1e-6)[0]
-    hid = orc.rmsnorm_bf16(u16(h), u16(w.norm_hid), 1e-6)[0]
-    cat = np.concatenate([emb, hid], axis=1)
-    fc = w.fc
-    x = orc.qgemv_f64(u32(fc.weight).reshape(H, -1), u16(fc.scales).reshape(H, -1), u16(fc.biases).reshape(H, -1),
-                      H, 2 * H, orc.bf16_to_f32(cat))
-    xb = orc.f32_to_bf16(x.astype(np.float32))
-    at = w.attn
-    A = {"H": H, "n_heads": SMALL["n_heads"], "n_kv": SMALL["n_kv_heads"], "rope_dim": 64, "theta": 1e7,
-         "eps": 1e-6, "bits": 4}
-    q, k, v, o, inn, qn, kn = at._keep
-    for name, p in (("q", q), ("k", k), ("v", v), ("o", o)):
-        A[name + "_w"], A[name + "_s"], A[name + "_b"] = u32(p.weight), u16(p.scales), u16(p.biases)
-    A["in_norm"], A["q_norm"], A["k_norm"] = u16(inn), u16(qn), u16(kn)
-    zero = np.zeros((SMALL["n_kv_heads"], 64, 256), np.uint16)
-    ya, _, _ = orc.attention_layer(xb, A, 0, zero, zero)
-    yab = orc.f32_to_bf16(ya.astype(np.float32))
-    moe = w.moe
-    mw = moe._keep
-    L = {"H": H, "I": SMALL["inter"], "E": SMALL["num_experts"], "k": SMALL["top_k"], "group": 64, "norm": 1,
-         "router_bits": moe.desc.router_bits, "bits": 4, "cap": moe.cap, "sg_bits": 8}
-    L["router_w"], L["router_s"], L["router_b"] = u32(mw[0].weight), u16(mw[0].scales), u16(mw[0].biases)
-    for key, p in (("gate", mw[1]), ("up", mw[2]), ("down", mw[3]), ("sh_gate", mw[4]), ("sh_up", mw[5]),
-                   ("sh_down", mw[6])):
-        L[key + "_w"], L[key + "_s"], L[key + "_b"] = u32(p.weight), u16(p.scales), u16(p.biases)
-    L["sg_w"], L["sg_s"], L["sg_b"] = u32(mw[7].weight), u16(mw[7].scales), u16(mw[7].biases)
-    L["table"] = None if mw[8] is None else mw[8].cpu().numpy()
-    L["bias"] = None if mw[9] is None else mw[9].cpu().numpy()
-    L["norm_w"] = u16(mw[10])
-    L["norm_eps"] = 1e-6
-    ym, ymb, _, _, _ = orc.moe_layer(yab, L, residual=True)
-    Hr = orc.rmsnorm_bf16(ymb, u16(w.norm), 1e-6)[0]
-    got = orc.bf16_to_f32(u16(Hn)).astype(np.float64).ravel()
-    ref = orc.bf16_to_f32(Hr).astype(np.float64).ravel()
-    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
-    cos = got @ ref / (np.linalg.norm(got) * np.linalg.norm(ref))
-    assert rel <= 2e-2 and cos >= 0.999, (rel, cos)
-    lg, _ = orc.lm_head(Hr, None, 1e-6, u16(w.lm_head))
-    srt = np.sort(lg[0])
-    if srt[-1] - srt[-2] > 1e-2 * np.abs(lg).max():
-        assert am.item() == int(np.argmax(lg[0]))
+    log("case: two chained MTP steps vs the oracle composition (reduced shape)")
+    from model_oracle import check_mtp_steps
+    check_mtp_steps(gpu, model, SMALL["hidden"], log)
 
 
 class ScriptedDrafter:
@@ -108,41 +64,141 @@ class ScriptedDrafter:
         self.inner, self.truth, self.P, self.n = inner, truth, prompt_len, 0
         self.cache, self.mtp = inner.cache, inner.mtp
 
-    def draft(self, H_last, x, K):
+    def _plant(self, d, start):
         import torch
-        d = self.inner.draft(H_last, x, K)
-        base = self.cache.length - K + 1 - self.P  # index of the next token in the greedy stream
+        K = d.numel()
+        base = start + 1 - self.P  # index of the next token in the greedy stream
         m = self.n % (K + 1)
         self.n += 1
         planted = [self.truth[base + i] if i < m else (self.truth[base + i] + 1) % SMALL["vocab"] for i in range(K)]
         d.copy_(torch.tensor(planted, dtype=torch.int32, device=d.device))
         return d
 
+    def draft(self, H_last, x, K):
+        start = self.cache.length
+        return self._plant(self.inner.draft(H_last, x, K), start)
+
+    def draft_adaptive(self, H_last, x, depth_max, tau):
+        start = self.cache.length
+        return self._plant(self.inner.draft_adaptive(H_last, x, depth_max, tau), start)
+
     def sync(self, start, h_seq, tokens):
         self.inner.sync(start, h_seq, tokens)
 
 
-def test_speculative_equals_greedy(gpu, model):
-    import torch
-    from vates_amd.decode import greedy_decode, prefill, speculative_decode
-    from vates_amd.mtp import MTPDrafter
-    n_tok, K = 40, 3
-    prompt = _prompt(gpu)
+def _greedy_truth(gpu, model, prompt, n):
+    from vates_amd.decode import greedy_decode, prefill
     caches = model.new_caches(256)
     x, h = prefill(model, prompt, caches)
-    ref = greedy_decode(model, caches, x, prompt.numel(), n_tok + K + 1)
-    log(f"case: greedy stream {ref.tokens[:12]}...")
+    return greedy_decode(model, caches, x, prompt.numel(), n).tokens
+
+
+def _fresh(gpu, model, prompt):
+    from vates_amd.decode import prefill
+    from vates_amd.mtp import MTPDrafter
+    caches = model.new_caches(256)
+    drafter = MTPDrafter(model.mtp, 256)
+    x, h = prefill(model, prompt, caches, drafter)
+    return caches, drafter, x, h
+
+
+@pytest.mark.parametrize("layout", ["k+1", "k"])
+def test_speculative_equals_greedy(gpu, model, layout):
+    from vates_amd.decode import speculative_decode
+    n_tok, K = 40, 3
+    prompt = _prompt(gpu)
+    truth = _greedy_truth(gpu, model, prompt, n_tok + K + 1)
+    log(f"case: greedy stream {truth[:12]}...")
     for scripted in (True, False):
-        log(f"case: speculative K=3 scripted={scripted}")
-        caches = model.new_caches(256)
-        drafter = MTPDrafter(model.mtp, 256)
-        x, h = prefill(model, prompt, caches, drafter)
-        d = ScriptedDrafter(drafter, ref.tokens, prompt.numel()) if scripted else drafter
-        st = speculative_decode(model, d, caches, x, h, prompt.numel(), n_tok, K=K)
-        assert st.tokens == ref.tokens[:n_tok], (st.tokens, ref.tokens[:n_tok])
+        log(f"case: speculative K=3 layout={layout} scripted={scripted}")
+        caches, drafter, x, h = _fresh(gpu, model, prompt)
+        d = ScriptedDrafter(drafter, truth, prompt.numel()) if scripted else drafter
+        st = speculative_decode(model, d, caches, x, h, prompt.numel(), n_tok, K=K, layout=layout)
+        assert st.tokens == truth[:n_tok], (st.tokens, truth[:n_tok])
         if scripted:
             assert set(st.accept_hist) == set(range(K + 1)), st.accept_hist
         log(f"accept_hist {st.accept_hist} steps {st.steps}")
+
+
+def _adaptive_oracle_depth(probs, depth_max, tau):
+    """draft_adaptive's rule (drafter.py:42-62) on float64 probabilities:
+    (depth, whether some decision lay within 1e-4 of tau)."""
+    conf, near = 1.0, False
+    for i, p in enumerate(probs):
+        if i + 1 >= depth_max:
+            return depth_max, near
+        conf *= p
+        near |= abs(conf - tau) <= 1e-4 * max(tau, 1e-30)
+        if conf < tau:
+            return i + 1, near
+    return len(probs), near
+
+
+def _sample_probs(gpu, model, prompt, steps=12, K=3):
+    """Draft probabilities of the first `steps` steps of a depth-K decode."""
+    import torch
+    from vates_amd.decode import speculative_decode
+    caches, drafter, x, h = _fresh(gpu, model, prompt)
+    seen = []
+    orig = drafter.draft_adaptive
+
+    def rec(H_last, x_tok, depth_max, tau):
+        lg = []
+        d = orig(H_last, x_tok, depth_max, tau, logits_out=lg)
+        for l in lg:
+            v = l[0].double().cpu().numpy()
+            seen.append(1.0 / np.exp(v - v.max()).sum())
+        return d
+    drafter.draft_adaptive = rec
+    speculative_decode(model, drafter, caches, x, h, prompt.numel(), steps, K=K, layout="k", tau=0.0)
+    torch.cuda.synchronize()
+    return np.array(seen).reshape(-1, K)
+
+
+def test_adaptive_depth_matches_tau_rule(gpu, model):
+    """Eager adaptive decoding: depth per step from the fp32 probabilities the
+    head fuses equals the tau rule on float64 softmax of the step's logits;
+    tau = 0 always drafts K, tau > 1 always 1, a middle tau mixes depths;
+    the stream equals greedy decoding in every case."""
+    import torch
+    from vates_amd.decode import speculative_decode
+    n_tok, K = 40, 3
+    prompt = _prompt(gpu, seed=12)
+    truth = _greedy_truth(gpu, model, prompt, n_tok + K + 1)
+    P = _sample_probs(gpu, model, prompt)
+    # thresholds inside the spread of the first and of the two-draft confidence
+    mids = (float(np.median(P[:, 0])), float(np.median(P[:, 0] * P[:, 1])))
+    log(f"draft probabilities (first steps) {np.round(P[:4], 6).tolist()}, middle taus {mids}")
+    seen = set()
+    for tau in (0.0, 1.1) + mids:
+        log(f"case: adaptive depth tau={tau:.3g}")
+        caches, drafter, x, h = _fresh(gpu, model, prompt)
+        orig = drafter.draft_adaptive
+        oracle = []
+
+        def rec(H_last, x_tok, depth_max, tau_):
+            lg = []
+            d = orig(H_last, x_tok, depth_max, tau_, logits_out=lg)
+            probs = []
+            for l in lg:
+                v = l[0].double().cpu().numpy()
+                probs.append(1.0 / np.exp(v - v.max()).sum())
+            oracle.append(_adaptive_oracle_depth(probs, depth_max, tau_) + (d.numel(),))
+            return d
+        drafter.draft_adaptive = rec
+        st = speculative_decode(model, drafter, caches, x, h, prompt.numel(), n_tok, K=K, layout="k", tau=tau)
+        torch.cuda.synchronize()
+        assert st.tokens == truth[:n_tok], (st.tokens, truth[:n_tok])
+        for want, near, got in oracle:
+            assert near or want == got, oracle
+        assert st.depths == [o[2] for o in oracle]
+        if tau == 0.0:
+            assert set(st.depths) == {K}
+        elif tau > 1.0:
+            assert set(st.depths) == {1}
+        seen |= set(st.depths)
+        log(f"depths {st.depths}")
+    assert seen == {1, 2, 3}
 
 
 def test_draft_paths_top_p(gpu, model):
@@ -164,39 +220,62 @@ def test_draft_paths_top_p(gpu, model):
     assert paths[:, 0].cpu().tolist() == order.tolist()
 
 
-def test_graph_decode_equals_greedy(gpu, model):
+@pytest.mark.parametrize("layout", ["k+1", "k"])
+def test_graph_decode_equals_greedy(gpu, model, layout):
     """The captured-graph step (positions on the device) emits the greedy stream,
-    with the MTP layer's drafts and with planted drafts that make every
-    acceptance length 0..K occur."""
-    import torch
-    from vates_amd.decode import GraphSpecDecoder, greedy_decode, prefill
-    from vates_amd.mtp import MTPDrafter
+    with the MTP layer's drafts (identical to the eager drafter's from the same
+    state, step for step) and with planted drafts that make every acceptance
+    length 0..K occur."""
+    from vates_amd.decode import GraphSpecDecoder, speculative_decode
     n_tok, K = 40, 3
     prompt = _prompt(gpu, seed=8)
-    caches = model.new_caches(256)
-    x, h = prefill(model, prompt, caches)
-    ref = greedy_decode(model, caches, x, prompt.numel(), n_tok + 2 * (K + 1))
+    truth = _greedy_truth(gpu, model, prompt, n_tok + 2 * (K + 1))
     P = prompt.numel()
+    caches, drafter, x, h = _fresh(gpu, model, prompt)
+    eager = speculative_decode(model, drafter, caches, x, h, P, n_tok, K=K, layout=layout, trace=True)
     for planted in (False, True):
-        log(f"case: graph speculative K=3 planted={planted}")
-        caches = model.new_caches(256)
-        drafter = MTPDrafter(model.mtp, 256)
-        x, h = prefill(model, prompt, caches, drafter)
-        dec = GraphSpecDecoder(model, drafter, caches, K=K, planted=planted)
+        log(f"case: graph speculative K=3 layout={layout} planted={planted}")
+        caches, drafter, x, h = _fresh(gpu, model, prompt)
+        dec = GraphSpecDecoder(model, drafter, caches, K=K, planted=planted, layout=layout)
         dec.start(x, h, P)
 
         def plant(step, pos):
             m = step % (K + 1)
             base = pos - P  # greedy stream index of the token at position pos + 1
-            return [ref.tokens[base + i] if i < m else (ref.tokens[base + i] + 1) % SMALL["vocab"] for i in range(K)]
+            return [truth[base + i] if i < m else (truth[base + i] + 1) % SMALL["vocab"] for i in range(K)]
 
-        st = dec.run(n_tok, plant=plant if planted else None)
-        assert st.tokens == ref.tokens[:n_tok], (st.tokens, ref.tokens[:n_tok])
+        st = dec.run(n_tok, plant=plant if planted else None, trace=not planted)
+        assert st.tokens == truth[:n_tok], (st.tokens, truth[:n_tok])
         if planted:
             assert set(st.accept_hist) == set(range(K + 1)), st.accept_hist
+        else:  # the device-side handoff (H, x, MTP positions) drafts what the eager drafter does
+            assert st.drafts == eager.drafts and st.accept_hist == eager.accept_hist
         log(f"accept_hist {st.accept_hist} steps {st.steps}")
         # the host view of the caches follows the device positions
-        assert all(c.length == P + sum(m + 1 for m in st.accept_hist) for c in caches if c is not None)
+        acc = [m + 1 if layout == "k+1" else min(m + 1, K) for m in st.accept_hist]
+        assert all(c.length == P + sum(acc) for c in caches if c is not None)
+
+
+def test_graph_adaptive_equals_eager(gpu, model):
+    """Adaptive depth as graphs (one per draft step, one verify per depth)
+    reproduces the eager adaptive decoder: tokens, depths, drafts."""
+    from vates_amd.decode import GraphSpecDecoder, speculative_decode
+    n_tok, K = 40, 3
+    prompt = _prompt(gpu, seed=12)
+    Pr = _sample_probs(gpu, model, prompt)
+    tau = float(np.median(Pr[:, 0]))
+    truth = _greedy_truth(gpu, model, prompt, n_tok + 2 * (K + 1))
+    P = prompt.numel()
+    caches, drafter, x, h = _fresh(gpu, model, prompt)
+    eager = speculative_decode(model, drafter, caches, x, h, P, n_tok, K=K, layout="k", tau=tau, trace=True)
+    log(f"case: graph adaptive tau={tau:.3g}, eager depths {eager.depths}")
+    caches, drafter, x, h = _fresh(gpu, model, prompt)
+    dec = GraphSpecDecoder(model, drafter, caches, K=K, layout="k", tau=tau)
+    dec.start(x, h, P)
+    st = dec.run(n_tok, trace=True)
+    assert st.tokens == truth[:n_tok]
+    assert st.depths == eager.depths and st.drafts == eager.drafts and st.accept_hist == eager.accept_hist
+    assert len(set(st.depths)) >= 2, st.depths
 
 
 def test_tree_decode_equals_greedy(gpu, model):

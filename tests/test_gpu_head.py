@@ -7,7 +7,10 @@ Bars (written here):
   oracle (fp32 accumulation of bf16 products), relative L2 <= 1e-6;
   argmax / max logit: bit-exact against the oracle's first-maximum rule applied
   to the GPU's own logits, and equal to the oracle's argmax wherever the
-  oracle's top-two margin exceeds the error bound.
+  oracle's top-two margin exceeds the error bound;
+  top_prob (softmax probability of the argmax): relative error <= 1e-5
+  against 1 / sum exp(l - max l) in float64 over the GPU's own logits (fp32
+  exponentials and sums over up to 151,936 terms).
 """
 import sys
 
@@ -112,3 +115,29 @@ def test_lm_head_vocab_151936(gpu, orc):
     _, am1, _ = lm_head(x[1:2].contiguous(), W, nw, want_logits=False)
     torch.cuda.synchronize()
     assert am1.item() == am[1].item()
+
+
+@pytest.mark.parametrize("T,V,scale", [(1, 151936, 0.02), (4, 151936, 1.0), (3, 4099, 3.0), (16, 1601, 0.5)])
+def test_lm_head_top_prob(gpu, orc, T, V, scale):
+    """The fused top-1 probability (draft_adaptive's confidence,
+    mlx_streaming/mtp/drafter.py:42-62) against float64 softmax of the GPU's
+    logits; the argmax and logits are unchanged by asking for it."""
+    log(f"case: lm_head top_prob T={T} V={V} weight std {scale}")
+    import torch
+    from vates_amd.head import lm_head
+    from vates_amd.synth import synth_bf16
+    H = 2048
+    W = synth_bf16(61, 1, (V, H), std=scale, device=gpu)
+    x = synth_bf16(61, 2, (T, H), device=gpu)
+    nw = synth_bf16(61, 3, (H,), std=0.1, device=gpu) + 1.0
+    p = torch.empty(T, dtype=torch.float32, device=gpu)
+    logits, am, mx = lm_head(x, W, nw, top_prob=p)
+    logits2, am2, _ = lm_head(x, W, nw)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, logits2) and torch.equal(am, am2)
+    lg = logits.cpu().numpy().astype(np.float64)
+    ref = 1.0 / np.exp(lg - lg.max(axis=1, keepdims=True)).sum(axis=1)
+    got = p.cpu().numpy().astype(np.float64)
+    log(f"  top_prob {got} ref {ref}")
+    assert np.all(np.abs(got - ref) <= 1e-5 * ref), (got, ref)
+

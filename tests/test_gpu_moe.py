@@ -86,6 +86,7 @@ def test_fused_moe_slots_parity(gpu, orc, torch_mod, H, I, xdt):
     for T in (1, 2, 4):
         log(f"case: fused_moe_slots H={H} I={I} x={xdt} T={T}")
         slots = np.stack([rng.choice(cap, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+        slots[0, k - 1] = slots[0, 0]  # one slot twice within a token (legal in the reference)
         if T > 1:
             slots[1, :3] = slots[0, :3]  # experts shared across tokens
         scores = rng.random((T, k)).astype(np.float32)
@@ -105,6 +106,44 @@ def test_fused_moe_slots_parity(gpu, orc, torch_mod, H, I, xdt):
         ref = orc.fused_moe_slots(x_ref, slots, scores, P, T, k, H, I, cap)
         assert out.dtype == torch.float32 and tuple(out.shape) == (T, H)
         assert_moe_close(out.cpu().numpy(), ref, f"slots H={H} I={I} {xdt} T={T}")
+
+
+def test_fused_moe_slots_slot_pool_fixture(gpu, orc, torch_mod):
+    """The reference's slot-pool known answer (test_native_moe_ext.py:50-72):
+    a 4-slot pool acquiring experts [1, 2, 1] gives local slots [0, 1, 0], then
+    [2, 1] gives [1, 0].  With those pool slots holding experts 1 and 2, the
+    operator on the local slots equals the oracle on the expert ids of the full
+    stack (the call repeats expert 1 within one token)."""
+    import json
+    from pathlib import Path
+    torch = torch_mod
+    from vates_amd import fused_moe_slots
+    from vates_amd.synth import synth_proj
+    fx = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())["slot_pool"]
+    H, I, E = 512, 128, 8
+    gate = synth_proj(33, 1, E, I, H, device=gpu)
+    up = synth_proj(33, 2, E, I, H, device=gpu)
+    down = synth_proj(33, 3, E, H, I, device=gpu)
+    full = pool_np(gate, up, down)
+    cap = fx["cap"]
+    held = {}  # slot -> expert, as the fixture's acquisitions fill the pool
+    for ids, local in zip(fx["calls"], fx["local"]):
+        for e, s in zip(ids, local):
+            assert held.setdefault(s, e) == e
+    order = [held.get(s, 0) for s in range(cap)]
+    pool = [t[order].contiguous() for t in (gate.weight, gate.scales, gate.biases, up.weight, up.scales,
+                                            up.biases, down.weight, down.scales, down.biases)]
+    rng = np.random.default_rng(9)
+    for ids, local in zip(fx["calls"], fx["local"]):
+        log(f"case: slot pool fixture experts {ids} -> slots {local}")
+        k = len(ids)
+        x = rng.normal(size=(1, H)).astype(np.float32)
+        scores = rng.random((1, k)).astype(np.float32)
+        out = fused_moe_slots(torch.from_numpy(x).to(gpu), torch.tensor([local], dtype=torch.int32, device=gpu),
+                              torch.from_numpy(scores).to(gpu), *pool, H, I, 64, 4)
+        torch.cuda.synchronize()
+        ref = orc.fused_moe_slots(x, np.array([ids], np.int32), scores, full, 1, k, H, I, E)
+        assert_moe_close(out.cpu().numpy(), ref, f"slot pool {ids}")
 
 
 def test_fused_moe_slots_bad_slot_flags_and_skips(gpu, orc, torch_mod):

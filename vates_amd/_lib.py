@@ -20,6 +20,8 @@ VMI_F32 = 0
 VMI_BF16 = 1
 VMI_STATUS_BAD_SLOT = 0x1
 VMI_STATUS_BAD_ROUTE = 0x2
+VMI_STATUS_BAD_POS = 0x4
+VMI_STATUS_BAD_RECORD = 0x8
 
 
 class VmiError(RuntimeError):
@@ -68,8 +70,8 @@ _SIGNATURES = {
                                     c_void_p, c_void_p]),
     "vmi_synth_bf16": (c_int, [c_uint64, c_uint32, c_int64, c_float, c_void_p, c_void_p]),
     "vmi_accept_greedy": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
-    "vmi_spec_commit": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                c_void_p]),
+    "vmi_spec_commit": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_void_p, c_void_p, c_void_p]),
     "vmi_accept_stochastic_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "vmi_accept_stochastic": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_float, c_uint64,
                                       c_uint64, c_void_p, c_void_p, c_size_t, c_void_p]),
@@ -89,7 +91,7 @@ _SIGNATURES = {
     "vmi_topk_rows": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "vmi_lm_head_workspace_bytes": (c_size_t, [c_int, c_int]),
     "vmi_lm_head": (c_int, [c_void_p, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p, c_void_p,
-                            c_void_p, c_void_p, c_size_t, c_void_p]),
+                            c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
 }
 
 _lib = None

@@ -55,22 +55,43 @@ def accept_greedy(drafts: torch.Tensor, preds: torch.Tensor, *, mode: int = 1, o
 
 
 def spec_commit(rec: torch.Tensor, hid: torch.Tensor, H: torch.Tensor, x: torch.Tensor, pos: torch.Tensor,
-                mtp_len: torch.Tensor, mtp_pos: torch.Tensor, *, stream=None) -> None:
+                mtp_len: torch.Tensor, mtp_pos: torch.Tensor, *, rows: Optional[int] = None, paths: int = 1,
+                status: Optional[torch.Tensor] = None, stream=None) -> None:
     """Commits one speculative step on the device from accept_greedy's record
-    (mode 1): H = hid[matched], x = the last emitted token, pos +=
-    accepted_len, mtp_len += matched + 1, mtp_pos = mtp_len + arange(K)."""
+    (vmi_spec_commit), with acc = accepted_len and w = the winning path:
+    H = hid[w * rows + acc - 1], x = the last emitted token, pos += acc,
+    mtp_len += acc, mtp_pos = mtp_len + arange(K).  hid bf16 [paths * rows, H]
+    holds the verify rows (rows = K + 1 after a mode-1 record, the step's
+    verify length after a mode-0 one; default: all of hid's rows).  A record
+    outside [1, rows] changes nothing and sets VMI_STATUS_BAD_RECORD in status
+    (int32 [1] on the device, or None)."""
     dev = rec.device
     K = mtp_pos.numel()
-    if hid.dim() != 2 or hid.shape[0] < K + 1:
-        raise VmiError(f"hid must hold at least {K + 1} rows")
+    if hid.dim() != 2 or hid.dtype != torch.bfloat16 or H.dtype != torch.bfloat16:
+        raise VmiError("hid must be bf16 [rows, hidden] and H bf16")
+    if hid.shape[0] % paths:
+        raise VmiError(f"hid's {hid.shape[0]} rows do not split into {paths} paths")
+    rows = hid.shape[0] // paths if rows is None else rows
+    if rows <= 0 or rows * paths > hid.shape[0]:
+        raise VmiError(f"hid holds {hid.shape[0]} rows, fewer than {paths} x {rows}")
     hidden = hid.shape[1]
     if H.numel() != hidden:
         raise VmiError(f"H must hold {hidden} values")
+    if rec.dtype != torch.int32 or rec.numel() < 4 + rows:
+        raise VmiError(f"the record must be int32 with at least {4 + rows} entries")
+    for t, name in ((x, "x"), (pos, "pos"), (mtp_len, "mtp_len")):
+        if t.dtype != torch.int32 or t.numel() != 1:
+            raise VmiError(f"{name} must be int32 [1]")
+    if mtp_pos.dtype != torch.int32:
+        raise VmiError("mtp_pos must be int32")
     for t, name, elem in ((rec, "result", 4), (hid, "hid", 2), (H, "H", 2), (x, "x", 4), (pos, "pos", 4),
                           (mtp_len, "mtp_len", 4), (mtp_pos, "mtp_pos", 4)):
         _require(t, name, elem, dev)
-    rc = load().vmi_spec_commit(rec.data_ptr(), hid.data_ptr(), hidden, K, H.data_ptr(), x.data_ptr(),
-                                pos.data_ptr(), mtp_len.data_ptr(), mtp_pos.data_ptr(), _stream_handle(stream))
+    if status is not None:
+        _require(status, "status", 4, dev)
+    rc = load().vmi_spec_commit(rec.data_ptr(), hid.data_ptr(), rows, paths, hidden, K, H.data_ptr(), x.data_ptr(),
+                                pos.data_ptr(), mtp_len.data_ptr(), mtp_pos.data_ptr(),
+                                None if status is None else status.data_ptr(), _stream_handle(stream))
     check(rc, "vmi_spec_commit")
 
 

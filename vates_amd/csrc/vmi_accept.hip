@@ -720,29 +720,38 @@ void sd_bind(SdArgs& a, uint8_t* ws, const SdLayout& L) {
     a.W = reinterpret_cast<uint32_t*>(ws + L.W);
 }
 
-// The commit of one speculative step from k_accept_greedy's record (mode 1):
-// H = hid[matched], x = the last emitted token, pos += accepted_len,
-// mtp_len += matched + 1 and the next step's draft positions mtp_len + i.
-// One workgroup: the threads copy the hidden row, thread 0 the scalars.
+// The commit of one speculative step from k_accept_greedy's record, in either
+// verify layout: with acc = accepted_len and w = the winning path,
+// H = hid[w][acc - 1], x = the last emitted token, pos += acc,
+// mtp_len += acc and the next step's draft positions mtp_len + i.  A record
+// outside what the call allows (no emitted token, acc outside [1, rows], more
+// than rows + 1 tokens, a path outside [0, paths)) changes nothing and sets
+// VMI_STATUS_BAD_RECORD.  One workgroup: the threads copy the hidden row,
+// thread 0 the scalars.
 struct CommitArgs {
     const int32_t* rec;
     const uint16_t* hid;
-    int hidden, K;
+    int rows, paths, hidden, K;
     uint16_t* H;
     int32_t* x;
     int32_t* pos;
     int32_t* mtp_len;
     int32_t* mtp_pos;
+    uint32_t* status;
 };
 
 __global__ __launch_bounds__(256) void k_spec_commit(CommitArgs a) {
-    const int m = a.rec[1];  // 0 <= m <= K: row m of the K + 1 verify rows
-    const uint16_t* src = a.hid + (size_t)m * a.hidden;
+    const int n = a.rec[0], acc = a.rec[2], w = a.rec[3];
+    if (n < 1 || n > a.rows + 1 || acc < 1 || acc > a.rows || w < 0 || w >= a.paths) {
+        if (threadIdx.x == 0 && a.status) atomicOr(a.status, VMI_STATUS_BAD_RECORD);
+        return;
+    }
+    const uint16_t* src = a.hid + ((size_t)w * a.rows + acc - 1) * a.hidden;
     for (int i = threadIdx.x; i < a.hidden; i += 256) a.H[i] = src[i];
     if (threadIdx.x == 0) {
-        a.x[0] = a.rec[a.rec[0] + 3];  // record entry 4 + n - 1: the last of the n emitted tokens
-        a.pos[0] += a.rec[2];
-        const int ml = a.mtp_len[0] + m + 1;
+        a.x[0] = a.rec[4 + n - 1];
+        a.pos[0] += acc;
+        const int ml = a.mtp_len[0] + acc;
         a.mtp_len[0] = ml;
         for (int i = 0; i < a.K; ++i) a.mtp_pos[i] = ml + i;
     }
@@ -763,16 +772,19 @@ extern "C" int vmi_accept_greedy(const int32_t* drafts, const int32_t* preds, in
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "k_accept_greedy launch");
 }
 
-extern "C" int vmi_spec_commit(const int32_t* result, const uint16_t* hid, int hidden, int K, uint16_t* H, int32_t* x,
-                               int32_t* pos, int32_t* mtp_len, int32_t* mtp_pos, void* stream) {
+extern "C" int vmi_spec_commit(const int32_t* result, const uint16_t* hid, int rows, int paths, int hidden, int K,
+                               uint16_t* H, int32_t* x, int32_t* pos, int32_t* mtp_len, int32_t* mtp_pos,
+                               uint32_t* status, void* stream) {
     vmi::clear_error();
     if (K <= 0 || K > kMaxK || hidden <= 0) return vmi::fail(VMI_ERR_INVALID, "K=%d hidden=%d", K, hidden);
+    if (rows <= 0 || rows > kMaxK + 1 || paths <= 0 || paths > 0xffff)
+        return vmi::fail(VMI_ERR_INVALID, "rows=%d paths=%d", rows, paths);
     if (!result || !hid || !H || !x || !pos || !mtp_len || !mtp_pos)
         return vmi::fail(VMI_ERR_INVALID, "null result/hid/H/x/pos/mtp_len/mtp_pos");
-    const uintptr_t hb = reinterpret_cast<uintptr_t>(hid), he = hb + (size_t)(K + 1) * hidden * 2;
+    const uintptr_t hb = reinterpret_cast<uintptr_t>(hid), he = hb + (size_t)paths * rows * hidden * 2;
     const uintptr_t Hb = reinterpret_cast<uintptr_t>(H), Hend = Hb + (size_t)hidden * 2;
     if (Hb < he && hb < Hend) return vmi::fail(VMI_ERR_INVALID, "H overlaps hid");
-    CommitArgs c{result, hid, hidden, K, H, x, pos, mtp_len, mtp_pos};
+    CommitArgs c{result, hid, rows, paths, hidden, K, H, x, pos, mtp_len, mtp_pos, status};
     hipLaunchKernelGGL(k_spec_commit, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), c);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "k_spec_commit launch");

@@ -224,6 +224,7 @@ struct AttnArgs {
     uint16_t* v_cache;
     int T, n_heads, n_kv, pos0, max_len;
     const int32_t* pos_dev;   // if set: pos0 is read here
+    uint32_t* status;         // workspace status word (VMI_STATUS_BAD_POS)
     int nstride;              // chunk capacity of the partial buffers
     float* part_o;            // [n_kv, nstride, RP, 256]
     float* part_ml;           // [n_kv, nstride, RP, 2]
@@ -302,6 +303,8 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     const int lane = tid & 63, w = at_wave(), nl = lane & 15, q4 = lane >> 4;
     const int T = a.T, G = a.n_heads / a.n_kv, R = T * G;
     const int pos0 = batch_pos0(a.pos0, a.pos_dev, T, a.max_len);
+    if (a.pos_dev && blockIdx.x == 0 && g == 0 && tid == 0 && *a.pos_dev != pos0)
+        atomicOr(a.status, VMI_STATUS_BAD_POS);    // clamped: the caller's position overran the cache
     const int L = pos0 + T;                            // positions present
     if (c * kChunkKeys >= L) return;                   // chunk beyond the cache (whole workgroup)
     const int b0 = c * kChunkWaves;
@@ -874,7 +877,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
 int attn_chunks(int L) { return (L + kChunkKeys - 1) / kChunkKeys; }
 
 struct AttnLayout {
-    size_t xn, qkv, part_o, part_ml, o, bytes;
+    size_t status, xn, qkv, part_o, part_ml, o, bytes;
 };
 
 AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len) {
@@ -887,6 +890,7 @@ AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len) {
     };
     const int RP = 16 * ((T * (n_heads / n_kv) + 15) / 16);
     const int stride = n_heads * 2 * kHeadDim + 2 * n_kv * kHeadDim;
+    L.status = take(4);
     L.xn = take((size_t)T * H * 2);
     L.qkv = take((size_t)T * stride * 4);
     const int nc = attn_chunks(max_len);
@@ -1025,6 +1029,7 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     at.rope_dim = D.rope_dim; at.theta = D.rope_theta; at.eps = D.norm_eps;
     at.k_cache = k_cache; at.v_cache = v_cache;
     at.T = T; at.n_heads = D.n_heads; at.n_kv = D.n_kv_heads; at.pos0 = pos0; at.pos_dev = pos_device;
+    at.status = reinterpret_cast<uint32_t*>(ws + L.status);
     at.max_len = max_len;
     at.nstride = attn_chunks(max_len);
     // with the position on the device every chunk of the capacity is launched; those past the cache exit

@@ -20,6 +20,13 @@
 // NaN ranks below every number - mx.argmax's first-maximum rule
 // (mlx_streaming/mtp/generate.py:756, drafter.py:31).
 //
+// Top-1 probability: every lane keeps, per token, a running (maximum m,
+// sum s of exp(l - m)) over its logits; the pairs merge across the 16 lanes
+// of a row, the waves of the workgroup and (in the last workgroup, in a fixed
+// order) the workgroups, and p = 1 / S where S = sum_j exp(l_j - max_j l):
+// softmax(l)[argmax], the draft confidence of draft_adaptive
+// (mlx_streaming/mtp/drafter.py:42-62, conf *= mx.softmax(lg)[d]).
+//
 // Semantics: generate.py:208-217 (logits = lm_head(norm(h))),
 // drafter.py:20-40 (draft token = argmax of the MTP head's logits).
 
@@ -54,8 +61,38 @@ struct HeadArgs {
     uint32_t* counter;        // arrival counter, 0 between calls
     int32_t* argmax;          // [T] or null
     float* maxval;            // [T] or null
+    float* top_prob;          // [T] or null: softmax probability of the argmax
+    float2* ms_partial;       // [gridDim.x, kHeadMaxT] workgroup (max, sum of exp) pairs
     int want_keys;
 };
+
+// (m, s) pairs: s = sum of exp(l - m) over a set of logits with maximum m.
+// The merge is symmetric in its operands (bit for bit), so both lanes of a
+// DPP or shuffle exchange hold the same result.
+__device__ __forceinline__ float2 ms_merge(float2 a, float2 b) {
+    const float m = fmaxf(a.x, b.x);
+    return make_float2(m, a.y * __expf(a.x - m) + b.y * __expf(b.x - m));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float2 ms_dpp(float2 v) {
+    return make_float2(vmi_dpp_f32<CTRL>(v.x), vmi_dpp_f32<CTRL>(v.y));
+}
+
+__device__ __forceinline__ float2 row_ms(float2 v) {
+    v = ms_merge(v, ms_dpp<VMI_DPP_XOR1>(v));
+    v = ms_merge(v, ms_dpp<VMI_DPP_XOR2>(v));
+    v = ms_merge(v, ms_dpp<VMI_DPP_HALF_MIRROR>(v));
+    v = ms_merge(v, ms_dpp<VMI_DPP_MIRROR>(v));
+    return v;  // every lane of a 16-lane row holds its row's pair
+}
+
+__device__ __forceinline__ float2 wave_ms(float2 v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+        v = ms_merge(v, make_float2(__shfl_xor(v.x, off), __shfl_xor(v.y, off)));
+    return v;
+}
 
 __device__ __forceinline__ uint64_t row_max_u64(uint64_t v) {
     v = vmi_u64_max(v, vmi_dpp_u64<VMI_DPP_XOR1>(v));
@@ -132,6 +169,7 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t s_w6[NBUF > 6 ? NW : 1][NBUF > 6 ? kChunk : 16];
     __shared__ __attribute__((aligned(16))) uint8_t s_w7[NBUF > 7 ? NW : 1][NBUF > 7 ? kChunk : 16];
     __shared__ uint64_t s_best[NW][MAXT];
+    __shared__ float2 s_ms[NW][MAXT];
     __shared__ int s_last;
 
     const int lane = threadIdx.x & 63, w = head_wave_id();
@@ -169,6 +207,10 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
     };
 
     uint64_t best[4] = {0ull, 0ull, 0ull, 0ull};
+    float2 ms[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ms[r] = make_float2(-__FLT_MAX__, 0.0f);
+    const bool want_prob = a.top_prob != nullptr;
     vmi_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     const bool a_live = n < T;  // A row n is token n; rows past T stay zero
 
@@ -215,6 +257,7 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
             if (t < T && row < V) {
                 if (a.logits) a.logits[(size_t)t * V + row] = acc[r];
                 best[r] = vmi_u64_max(best[r], vmi_rank_key(acc[r], row));
+                if (want_prob) ms[r] = ms_merge(ms[r], make_float2(acc[r], 1.0f));
             }
         }
         acc = vmi_f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -228,6 +271,10 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
         const uint64_t k = row_max_u64(best[r]);
         const int t = 4 * g + r;
         if (n == 0 && t < MAXT) s_best[w][t] = k;
+        if (want_prob) {
+            const float2 v = row_ms(ms[r]);
+            if (n == 0 && t < MAXT) s_ms[w][t] = v;
+        }
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -235,6 +282,13 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
             uint64_t k = 0ull;
             for (int v = 0; v < NW; ++v) k = vmi_u64_max(k, s_best[v][t]);
             __hip_atomic_store(&a.partial[(size_t)b * kHeadMaxT + t], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (want_prob) {
+                float2 m = s_ms[0][t];
+                for (int v = 1; v < NW; ++v) m = ms_merge(m, s_ms[v][t]);
+                float* dst = reinterpret_cast<float*>(&a.ms_partial[(size_t)b * kHeadMaxT + t]);
+                __hip_atomic_store(dst, m.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(dst + 1, m.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         const uint32_t prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         s_last = (prev == (uint32_t)(G - 1));
@@ -250,6 +304,17 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
         if (lane == 0) {
             if (a.argmax) a.argmax[t] = (int32_t)(0xffffffffu - (uint32_t)k);
             if (a.maxval) a.maxval[t] = vmi_order_key_value((uint32_t)(k >> 32));
+        }
+        if (want_prob) {
+            // lane l merges workgroups l, l + 64, ... in order, then a fixed tree
+            float2 m = make_float2(-__FLT_MAX__, 0.0f);
+            for (int i = lane; i < G; i += 64) {
+                const float* src = reinterpret_cast<const float*>(&a.ms_partial[(size_t)i * kHeadMaxT + t]);
+                m = ms_merge(m, make_float2(__hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                            __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+            }
+            m = wave_ms(m);
+            if (lane == 0) a.top_prob[t] = 1.0f / m.y;
         }
     }
     if (threadIdx.x == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -307,14 +372,19 @@ __global__ __launch_bounds__(256) void k_topk_rows(TopkArgs a) {
 
 }  // namespace
 
+namespace {
+constexpr size_t kKeysBytes = (size_t)kHeadMaxGrid * kHeadMaxT * sizeof(uint64_t);
+constexpr size_t kMsBytes = (size_t)kHeadMaxGrid * kHeadMaxT * sizeof(float2);
+}  // namespace
+
 extern "C" size_t vmi_lm_head_workspace_bytes(int T, int vocab) {
     if (T <= 0 || vocab <= 0) return 0;
-    return vmi::align256((size_t)kHeadMaxGrid * kHeadMaxT * sizeof(uint64_t)) + 256;
+    return vmi::align256(kKeysBytes) + vmi::align256(kMsBytes) + 256;
 }
 
 extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weight, float norm_eps,
                            const uint16_t* weight, int vocab, float* logits, int32_t* argmax, float* max_logit,
-                           void* workspace, size_t workspace_bytes, void* stream) {
+                           float* top_prob, void* workspace, size_t workspace_bytes, void* stream) {
     vmi::clear_error();
     if (T <= 0 || T > kHeadMaxT) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, %d]", T, kHeadMaxT);
     if (hidden <= 0 || hidden % 512 || hidden > kHeadMaxH)
@@ -325,8 +395,9 @@ extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t*
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
          reinterpret_cast<uintptr_t>(norm_weight)) & 15)
         return vmi::fail(VMI_ERR_INVALID, "x, weight and norm_weight must be 16-byte aligned");
-    const bool want_keys = argmax || max_logit;
-    if (!logits && !want_keys) return vmi::fail(VMI_ERR_INVALID, "nothing to compute (logits, argmax and max all null)");
+    const bool want_keys = argmax || max_logit || top_prob;
+    if (!logits && !want_keys)
+        return vmi::fail(VMI_ERR_INVALID, "nothing to compute (logits, argmax, max and top_prob all null)");
     const size_t need = vmi_lm_head_workspace_bytes(T, vocab);
     if (want_keys && (!workspace || workspace_bytes < need))
         return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", need, workspace_bytes);
@@ -334,11 +405,13 @@ extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t*
     HeadArgs a{};
     a.x = x; a.norm_w = norm_weight; a.eps = norm_eps; a.W = weight;
     a.T = T; a.H = hidden; a.V = vocab; a.ntiles = (vocab + 15) / 16;
-    a.logits = logits; a.argmax = argmax; a.maxval = max_logit; a.want_keys = want_keys ? 1 : 0;
+    a.logits = logits; a.argmax = argmax; a.maxval = max_logit; a.top_prob = top_prob;
+    a.want_keys = want_keys ? 1 : 0;
     if (want_keys) {
         uint8_t* ws = static_cast<uint8_t*>(workspace);
         a.partial = reinterpret_cast<uint64_t*>(ws);
-        a.counter = reinterpret_cast<uint32_t*>(ws + vmi::align256((size_t)kHeadMaxGrid * kHeadMaxT * sizeof(uint64_t)));
+        a.ms_partial = reinterpret_cast<float2*>(ws + vmi::align256(kKeysBytes));
+        a.counter = reinterpret_cast<uint32_t*>(ws + vmi::align256(kKeysBytes) + vmi::align256(kMsBytes));
     }
     int G = vmi::device_cus();
     if (G > kHeadMaxGrid) G = kHeadMaxGrid;

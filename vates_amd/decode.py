@@ -24,6 +24,7 @@ import time
 from dataclasses import dataclass, field
 from typing import List, Optional
 
+import numpy as np
 import torch
 
 from ._lib import VmiError
@@ -47,6 +48,8 @@ class DecodeStats:
     tokens: List[int] = field(default_factory=list)
     steps: int = 0
     accept_hist: List[int] = field(default_factory=list)   # matched drafts per step
+    depths: List[int] = field(default_factory=list)        # drafts verified per step (adaptive depth)
+    drafts: List[List[int]] = field(default_factory=list)  # the drafts of each step (with trace=True)
     seconds: float = 0.0
 
     @property
@@ -90,6 +93,23 @@ class SpecModel:
                 c.length = length
 
 
+def commit_verified_prefix(caches: list, verified_len: int, accepted_len: int) -> bool:
+    """Commits the accepted prefix of a verify batch of verified_len positions
+    (kv_cache.py:222-251): every cache drops the rejected verified_len -
+    accepted_len positions.  Attention caches keep their keys below the new
+    length; linear-attention caches continue from the state captured after the
+    last accepted token (the reference's checkpoint[accepted_len - 1]), which
+    the position-indexed rings already hold.  Returns True (the rings always
+    hold every token's state, so the commit cannot fall back to a replay)."""
+    rejected = verified_len - accepted_len
+    if rejected < 0 or accepted_len < 0:
+        raise VmiError("accepted_len cannot exceed verified_len")
+    for c in caches:
+        if c is not None:
+            c.trim(rejected)
+    return True
+
+
 def prefill(model: SpecModel, prompt: torch.Tensor, caches, drafter: Optional[MTPDrafter] = None, chunk: int = 8):
     """Runs the prompt (int32 [P] on the device) through the model in chunks of
     at most `chunk` tokens and, with a drafter, advances its cache over the
@@ -124,40 +144,73 @@ def greedy_decode(model: SpecModel, caches, x: torch.Tensor, pos: int, n_tokens:
     return st
 
 
+LAYOUTS = ("k+1", "k")
+
+
+def _check_layout(layout: str, tau: Optional[float]) -> None:
+    if layout not in LAYOUTS:
+        raise VmiError(f"layout {layout!r} is not one of {LAYOUTS}")
+    if tau is not None and layout != "k":
+        raise VmiError("adaptive depth verifies in the T = K layout (layout='k')")
+
+
 def speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: torch.Tensor, H_last: torch.Tensor,
-                       pos: int, n_tokens: int, K: int = 3) -> DecodeStats:
-    """K-draft MTP decoding with greedy acceptance in the [x, d1..dK] layout.
+                       pos: int, n_tokens: int, K: int = 3, *, layout: str = "k+1",
+                       tau: Optional[float] = None, trace: bool = False) -> DecodeStats:
+    """K-draft MTP decoding with greedy acceptance.
+
+    layout "k+1": the verify batch is [x, d1..dK] (T = K + 1): every draft is
+    checked and the model's token after the last accepted one is emitted, so
+    a step emits up to K + 1 tokens (accept mode 1).
+    layout "k": the reference's batch [x, d1..d_{K-1}] (T = K,
+    generate.py:604): dK is checked against the model's last prediction,
+    accepted_len = min(matched + 1, K) and a step emits up to K tokens; when
+    every draft matches, the next input is dK itself (generate.py:819,
+    850-856; accept mode 0).
+    tau: adaptive depth (draft_adaptive, drafter.py:42-62, layout "k"): each
+    step drafts 1..K tokens while the product of their softmax probabilities
+    stays at or above tau and verifies [x, d1..d_{depth-1}].
 
     x: the last emitted token [1] (not yet run through the model) at position
     `pos`; H_last: the model's pre-norm hidden at pos - 1 [1, H]; the MTP cache
-    holds every committed position before pos.
+    holds every committed position before pos.  trace: record each step's
+    drafts (one more host read per step).
     """
     if model.mtp is None:
         raise VmiError("the model has no MTP layer")
+    _check_layout(layout, tau)
     st = DecodeStats()
     dev = x.device
     verify = torch.empty(K + 1, dtype=torch.int32, device=dev)
     t0 = time.perf_counter()
     while len(st.tokens) < n_tokens:
         mtp_start = drafter.cache.length
-        drafts = drafter.draft(H_last, x, K)
+        if tau is not None:
+            drafts = drafter.draft_adaptive(H_last, x, K, tau)
+        else:
+            drafts = drafter.draft(H_last, x, K)
+        d = drafts.numel()
+        T = d + 1 if layout == "k+1" else d
         verify[0:1].copy_(x)
-        verify[1:].copy_(drafts)
-        preds, hid, _ = model.forward(verify, caches, pos)
-        rec = accept_greedy(drafts, preds, mode=1)
+        verify[1:T].copy_(drafts[:T - 1])
+        preds, hid, _ = model.forward(verify[:T], caches, pos)
+        rec = accept_greedy(drafts, preds, mode=1 if layout == "k+1" else 0)
         r = rec.cpu().tolist()  # the step's one host synchronisation
         n, m, acc = r[0], r[1], r[2]
         emitted = r[4:4 + n]
-        model.commit(caches, pos + acc)
-        # MTP cache: (main hidden at pos-1 .. pos+m-1, tokens x, d1..dm)
-        h_seq = torch.cat([H_last, hid[:m]]) if m else H_last
-        drafter.sync(mtp_start, h_seq.contiguous(), verify[:m + 1].contiguous())
+        commit_verified_prefix(caches, T, acc)
+        # MTP cache: (main hidden at pos-1 .. pos+acc-2, tokens of the acc accepted positions)
+        h_seq = torch.cat([H_last, hid[:acc - 1]]) if acc > 1 else H_last
+        drafter.sync(mtp_start, h_seq.contiguous(), verify[:acc].contiguous())
         st.tokens.extend(emitted)
         st.accept_hist.append(m)
+        st.depths.append(d)
+        if trace:
+            st.drafts.append(drafts.cpu().tolist())
         st.steps += 1
         pos += acc
         x = torch.tensor([emitted[-1]], dtype=torch.int32, device=dev)
-        H_last = hid[m:m + 1].clone()
+        H_last = hid[acc - 1:acc].clone()
     st.seconds = time.perf_counter() - t0
     st.tokens = st.tokens[:n_tokens]
     return st
@@ -217,64 +270,86 @@ def tree_speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: to
 
 
 class GraphSpecDecoder:
-    """The speculative decode step of ``speculative_decode`` captured once as a
-    HIP graph and replayed per step, with every position on the device.
+    """The speculative decode step of ``speculative_decode`` captured as HIP
+    graphs and replayed per step, with every position on the device.
 
-    One replay runs: the K draft steps of the MTP layer at MTP positions
-    mtp_len + i; the verify forward of [x, d1..dK] at pos; greedy acceptance
-    (``vmi_accept_greedy``, mode 1); the MTP cache update over all K + 1 rows
-    (main hidden at pos-1..pos+K-1, tokens x, d1..dK) at mtp_len, whose rows
-    past the accepted ones lie beyond the committed length and are written
-    over by the next step; and the commit: pos += accepted, mtp_len += m + 1,
-    x = the last emitted token, H_last = hidden of position pos + m.  The host
-    reads the acceptance record once per step.  Results equal
+    A step runs: the draft steps of the MTP layer at MTP positions
+    mtp_len + i; the verify forward at pos; greedy acceptance
+    (``vmi_accept_greedy``); the MTP cache update over all verify rows (main
+    hidden at pos-1.., tokens x, d1..) at mtp_len, whose rows past the
+    accepted ones lie beyond the committed length and are written over by the
+    next step; and the commit (``vmi_spec_commit``): pos += accepted_len,
+    mtp_len += accepted_len, x = the last emitted token, H_last = the hidden of
+    the last accepted position.  Layouts as ``speculative_decode``:
+    "k+1" verifies [x, d1..dK], "k" verifies [x, d1..d_{K-1}].  With a fixed
+    depth the whole step is one graph and the host reads the acceptance
+    record once per step.  With tau (adaptive depth, layout "k") each draft
+    step is its own graph and the verify of each depth 1..K another; the host
+    reads each draft's probability to choose the depth, as the reference's
+    draft_adaptive does (drafter.py:42-62).  Results equal
     ``speculative_decode`` token for token (the kernels' results do not depend
     on batch composition).
     """
 
-    def __init__(self, model: SpecModel, drafter: MTPDrafter, caches: list, K: int = 3, planted: bool = False):
+    def __init__(self, model: SpecModel, drafter: MTPDrafter, caches: list, K: int = 3, planted: bool = False,
+                 layout: str = "k+1", tau: Optional[float] = None):
         """planted: the verify batch takes its drafts from ``self.planted``
         (int32 [K], written by the host before each replay) instead of the MTP
         layer's, which still runs and keeps its cache; for drafts from another
         source and for tests that force acceptance lengths."""
         if model.mtp is None:
             raise VmiError("the model has no MTP layer")
+        _check_layout(layout, tau)
         self.model, self.drafter, self.caches, self.K = model, drafter, caches, K
+        self.layout, self.tau = layout, tau
         dev = model.embed.device
         self.dev = dev
         self.state = torch.zeros(2, dtype=torch.int32, device=dev)     # [pos, mtp_len]
         self.pos, self.mtp_len = self.state[0:1], self.state[1:2]
         self.mtp_pos = torch.zeros(K, dtype=torch.int32, device=dev)
         self.steps_ar = torch.arange(K, dtype=torch.int32, device=dev)
-        # the verify batch [x, d1..dK] holds the step's input token and the
-        # drafts the MTP layer writes; row 0 of the MTP update holds H_last
+        # verify rows [x, d1..dK] hold the step's input token and the drafts the
+        # MTP layer writes; row 0 of the MTP update holds H_last
         self.verify = torch.zeros(K + 1, dtype=torch.int32, device=dev)
         self.x, self.drafts = self.verify[0:1], self.verify[1:]
+        self.probs = torch.zeros(K, dtype=torch.float32, device=dev)
         self.hseq = torch.zeros((K + 1, model.hidden), dtype=torch.bfloat16, device=dev)
         self.H = self.hseq[0:1]
         self.rec_buf = torch.zeros(4 + K + 1, dtype=torch.int32, device=dev)
+        self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         self.use_planted = planted
         self.planted = torch.zeros(K, dtype=torch.int32, device=dev)
         self.stream = torch.cuda.Stream(device=dev)
-        self.graph = None
-        self.rec = None
+        self.graph = None        # fixed depth: the whole step
+        self.draft_graphs = []   # adaptive: one per draft step
+        self.verify_graphs = {}  # adaptive: depth -> verify + accept + commit
+        self._keep = []
+
+    def _draft(self, i: int, h: torch.Tensor) -> torch.Tensor:
+        tok = self.x if i == 0 else self.drafts[i - 1:i]
+        _, hn, _ = self.model.mtp.step(h, tok, self.drafter.cache, pos_device=self.mtp_pos[i:i + 1],
+                                       argmax_out=self.drafts[i:i + 1], prob_out=self.probs[i:i + 1])
+        return hn
+
+    def _verify(self, d: int) -> torch.Tensor:
+        """Verify, accept and commit after d drafts."""
+        T = d + 1 if self.layout == "k+1" else d
+        mtp = self.model.mtp
+        if self.use_planted:
+            self.drafts[:d].copy_(self.planted[:d])
+        preds, hid, _ = self.model.forward(self.verify[:T], self.caches, 0, pos_device=self.pos)
+        rec = accept_greedy(self.drafts[:d], preds, mode=1 if self.layout == "k+1" else 0, out=self.rec_buf)
+        if T > 1:
+            self.hseq[1:T].copy_(hid[:T - 1])
+        mtp.advance(self.hseq[:T], self.verify[:T], self.drafter.cache, pos_device=self.mtp_len)
+        spec_commit(rec, hid, self.H, self.x, self.pos, self.mtp_len, self.mtp_pos, rows=T, status=self.status)
+        return rec
 
     def _step(self) -> torch.Tensor:
-        K, mtp = self.K, self.model.mtp
-        h, tok = self.H, self.x
-        for i in range(K):
-            d = self.drafts[i:i + 1]
-            _, h, _ = mtp.step(h, tok, self.drafter.cache, pos_device=self.mtp_pos[i:i + 1], argmax_out=d)
-            tok = d
-        if self.use_planted:
-            self.drafts.copy_(self.planted)
-        preds, hid, _ = self.model.forward(self.verify, self.caches, 0, pos_device=self.pos)
-        rec = accept_greedy(self.drafts, preds, mode=1, out=self.rec_buf)
-        self.hseq[1:].copy_(hid[:K])
-        mtp.advance(self.hseq, self.verify, self.drafter.cache, pos_device=self.mtp_len)
-        # commit on the device (also the next step's draft positions)
-        spec_commit(rec, hid, self.H, self.x, self.pos, self.mtp_len, self.mtp_pos)
-        return rec
+        h = self.H
+        for i in range(self.K):
+            h = self._draft(i, h)
+        return self._verify(self.K)
 
     def start(self, x: torch.Tensor, H_last: torch.Tensor, pos: int) -> None:
         """Sets the state: x (int32 [1]) at position pos, H_last [1, H] the
@@ -285,26 +360,62 @@ class GraphSpecDecoder:
         torch.add(self.steps_ar, self.mtp_len, out=self.mtp_pos)
         self.pos_host = pos
 
+    def _capture(self, fn):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
+            out = fn()
+        self._keep.append(out)
+        return g, out
+
     def capture(self) -> None:
-        """Warms the workspaces up on the capture stream, restores the state,
-        and captures one step."""
-        saved = [t.clone() for t in (self.state, self.x, self.H, self.mtp_pos)]
+        """Warms the workspaces up on the capture stream (every shape the
+        graphs use), restores the state, and captures."""
+        live = (self.state, self.x, self.H, self.mtp_pos)
+        saved = [t.clone() for t in live]
         self.stream.wait_stream(torch.cuda.current_stream(self.dev))
-        with torch.cuda.stream(self.stream):
-            self._step()
-        self.stream.synchronize()
-        for t, v in zip((self.state, self.x, self.H, self.mtp_pos), saved):
-            t.copy_(v)
+        # each warm-up starts from the saved state, so none writes a ring slot
+        # the real steps read (linear-attention rings hold K + 2 or more states)
+        warmups = [self._step] + ([lambda d=d: self._verify(d) for d in range(1, self.K)] if self.tau is not None else [])
+        for fn in warmups:
+            with torch.cuda.stream(self.stream):
+                fn()
+                for t, v in zip(live, saved):
+                    t.copy_(v)
+            self.stream.synchronize()
         torch.cuda.synchronize(self.dev)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=self.stream):
-            self.rec = self._step()
+        if self.tau is None:
+            self.graph, self.rec = self._capture(self._step)
+        else:
+            h = self.H
+            for i in range(self.K):
+                g, h = self._capture(lambda i=i, h=h: self._draft(i, h))
+                self.draft_graphs.append(g)
+            for d in range(1, self.K + 1):
+                self.verify_graphs[d], self.rec = self._capture(lambda d=d: self._verify(d))
         torch.cuda.synchronize(self.dev)
 
-    def run(self, n_tokens: int, plant=None) -> DecodeStats:
+    def _replay_step(self) -> None:
+        if self.tau is None:
+            self.graph.replay()
+            self._depth = self.K
+            return
+        conf = np.float32(1.0)
+        d = 0
+        for i in range(self.K):
+            self.draft_graphs[i].replay()
+            d = i + 1
+            if i + 1 < self.K:
+                conf = np.float32(conf * np.float32(self.probs[i].item()))
+                if conf < self.tau:
+                    break
+        self.verify_graphs[d].replay()
+        self._depth = d
+
+    def run(self, n_tokens: int, plant=None, trace: bool = False) -> DecodeStats:
         """Decodes n_tokens tokens by graph replays.  plant(step, pos) -> K
-        draft tokens for a decoder made with planted=True."""
-        if self.graph is None:
+        draft tokens for a decoder made with planted=True; trace records each
+        step's drafts (one more host read per step)."""
+        if self.graph is None and not self.draft_graphs:
             self.capture()
         K = self.K
         need = self.pos_host + n_tokens + 2 * K + 2  # the last step overshoots by < K + 1 and writes K + 1 rows
@@ -317,16 +428,21 @@ class GraphSpecDecoder:
         while len(st.tokens) < n_tokens:
             if plant is not None:
                 self.planted.copy_(torch.tensor(plant(st.steps, pos), dtype=torch.int32), non_blocking=False)
-            self.graph.replay()
-            r = self.rec.cpu().tolist()  # the step's one host synchronisation
+            self._replay_step()
+            r = self.rec_buf.cpu().tolist()  # the step's one host synchronisation
             n, m = r[0], r[1]
             pos += r[2]
             st.tokens.extend(r[4:4 + n])
             st.accept_hist.append(m)
+            st.depths.append(self._depth)
+            if trace:
+                st.drafts.append(self.drafts[:self._depth].cpu().tolist())
             st.steps += 1
         st.seconds = time.perf_counter() - t0
         st.tokens = st.tokens[:n_tokens]
         pos, mtp_len = self.state.cpu().tolist()
+        if int(self.status.item()):
+            raise VmiError(f"device status {int(self.status.item()):#x}: an acceptance record was out of range")
         self.pos_host = pos
         for c in self.caches:
             if c is not None:

@@ -17,10 +17,13 @@ from .moe import _require, _stream_handle, workspace
 
 def lm_head(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor] = None, *,
             eps: float = 1e-6, want_logits: bool = True, logits: Optional[torch.Tensor] = None,
-            argmax: Optional[torch.Tensor] = None, max_logit: Optional[torch.Tensor] = None, stream=None):
+            argmax: Optional[torch.Tensor] = None, max_logit: Optional[torch.Tensor] = None,
+            top_prob: Optional[torch.Tensor] = None, stream=None):
     """Returns (logits f32 [T, V] or None, argmax int32 [T], max logit f32 [T]).
 
     x bf16 [T, H] (T <= 16), weight bf16 [V, H], norm_weight bf16 [H] or None.
+    top_prob (f32 [T], optional) receives the softmax probability of each
+    row's argmax (the draft confidence of drafter.py:42-62).
     """
     dev = x.device
     if x.dim() != 2:
@@ -41,7 +44,8 @@ def lm_head(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.T
         argmax = torch.empty(T, dtype=torch.int32, device=dev)
     if max_logit is None:
         max_logit = torch.empty(T, dtype=torch.float32, device=dev)
-    for t, name, n in ((logits, "logits", T * V), (argmax, "argmax", T), (max_logit, "max_logit", T)):
+    for t, name, n in ((logits, "logits", T * V), (argmax, "argmax", T), (max_logit, "max_logit", T),
+                       (top_prob, "top_prob", T)):
         if t is not None:
             _require(t, name, 4, dev)
             if t.numel() != n:
@@ -52,6 +56,7 @@ def lm_head(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.T
     ws = workspace(nbytes, dev, sh, tag="lm_head")
     rc = lib.vmi_lm_head(x.data_ptr(), T, H, None if norm_weight is None else norm_weight.data_ptr(), float(eps),
                          weight.data_ptr(), V, None if logits is None else logits.data_ptr(), argmax.data_ptr(),
-                         max_logit.data_ptr(), ws.data_ptr(), ws.numel(), sh)
+                         max_logit.data_ptr(), None if top_prob is None else top_prob.data_ptr(), ws.data_ptr(),
+                         ws.numel(), sh)
     check(rc, "vmi_lm_head")
     return logits, argmax, max_logit

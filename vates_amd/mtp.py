@@ -6,8 +6,8 @@
   the routed MoE with its shared expert), H = norm(x), logits = lm_head(H).
 * ``MTPLayer.advance`` is ``mtp_advance`` (:66-73): the same without lm_head,
   used to commit accepted positions to the MTP cache.
-* ``MTPDrafter`` mirrors ``MTPDrafter.draft`` / ``draft_paths`` / ``sync``
-  (mlx_streaming/mtp/drafter.py:20-40, 150-188).  Draft tokens stay on the
+* ``MTPDrafter`` mirrors ``MTPDrafter.draft`` / ``draft_adaptive`` /
+  ``draft_paths`` / ``sync`` (mlx_streaming/mtp/drafter.py:20-62, 150-188).  Draft tokens stay on the
   device: each step's argmax feeds the next step's embedding gather directly,
   so drafting needs no host synchronisation (the reference synchronises once
   per draft token, drafter.py:21-23).
@@ -17,6 +17,7 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import List, Optional
 
+import numpy as np
 import torch
 
 from ._lib import VmiError, check, load
@@ -73,12 +74,15 @@ class MTPLayer:
         return rmsnorm(x, self.w.norm, eps=self.w.eps, stream=stream)
 
     def step(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, *, want_logits: bool = False,
-             stream=None, pos_device: Optional[torch.Tensor] = None, argmax_out: Optional[torch.Tensor] = None):
+             stream=None, pos_device: Optional[torch.Tensor] = None, argmax_out: Optional[torch.Tensor] = None,
+             prob_out: Optional[torch.Tensor] = None):
         """(argmax int32 [T], MTP hidden H bf16 [T, H], logits f32 [T, V] or None).
         With pos_device the cache position is read on the device; with
-        argmax_out (int32 [T]) the argmax is written there."""
+        argmax_out (int32 [T]) the argmax is written there; with prob_out
+        (f32 [T]) the softmax probability of the argmax."""
         Hn = self._trunk(hidden, tokens, cache, stream, pos_device)
-        logits, am, _ = lm_head(Hn, self.w.lm_head, None, want_logits=want_logits, argmax=argmax_out, stream=stream)
+        logits, am, _ = lm_head(Hn, self.w.lm_head, None, want_logits=want_logits, argmax=argmax_out,
+                                top_prob=prob_out, stream=stream)
         return am, Hn, logits
 
     def advance(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None,
@@ -100,6 +104,32 @@ class MTPDrafter:
             am, h, _ = self.mtp.step(h, tok, self.cache)
             drafts[i:i + 1].copy_(am)
             tok = drafts[i:i + 1]
+        return drafts
+
+    def draft_adaptive(self, H_last: torch.Tensor, x_tok: torch.Tensor, depth_max: int, tau: float,
+                       logits_out: Optional[list] = None) -> torch.Tensor:
+        """Confidence-gated drafts (draft_adaptive, drafter.py:42-62): greedy
+        drafts while the running product of their softmax probabilities stays
+        at or above tau, at least one and at most depth_max; the last position
+        is not gated.  The product is taken in fp32 on the host, which reads
+        each step's probability (the reference reads it the same way).
+        Returns int32 [depth] on the device.  logits_out (a list) receives each
+        step's f32 logits [1, V] (tests)."""
+        dev = H_last.device
+        drafts = torch.empty(depth_max, dtype=torch.int32, device=dev)
+        probs = torch.empty(depth_max, dtype=torch.float32, device=dev)
+        h, tok = H_last, x_tok
+        conf = np.float32(1.0)
+        for i in range(depth_max):
+            _, h, lg = self.mtp.step(h, tok, self.cache, want_logits=logits_out is not None,
+                                     argmax_out=drafts[i:i + 1], prob_out=probs[i:i + 1])
+            if logits_out is not None:
+                logits_out.append(lg)
+            tok = drafts[i:i + 1]
+            if i + 1 < depth_max:
+                conf = np.float32(conf * np.float32(probs[i].item()))
+                if conf < tau:
+                    return drafts[:i + 1]
         return drafts
 
     def draft_paths(self, H_last: torch.Tensor, x_tok: torch.Tensor, K: int, P: int) -> torch.Tensor:
