@@ -211,7 +211,8 @@ int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weigh
  * by the MTP fc and attention projections, qwen3_next_mtp.py:28-30, 40-53).
  * x bf16 [T, K]; W [N, K] packed (bits 4 or 8, group 64); out f32 [T, N]
  * and/or out_bf16 = bf16(y + residual) [T, N] (residual bf16 or NULL).
- * T <= 8, T*K <= 32768, K a multiple of 64.
+ * T <= 16 (launched in pieces of 8 tokens), min(T, 8)*K <= 32768, K a
+ * multiple of 64.
  * ------------------------------------------------------------------------ */
 int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int group, float* out,
               const uint16_t* residual, uint16_t* out_bf16, void* stream);
@@ -311,6 +312,68 @@ size_t vmi_gdn_layer_workspace_bytes(int T, int hidden, int n_k_heads, int n_v_h
 int vmi_gdn_layer(const vmi_gdn_layer_desc* desc, const uint16_t* x, int T, int pos0, const int32_t* pos_device,
                   uint16_t* conv_ring, float* state_ring, int n_slots, uint16_t* out, void* workspace,
                   size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Tree verification: the P paths of a draft tree, each [x, d1 .. d_{span-1}]
+ * at positions pos0 .. pos0 + span - 1 over the shared caches, verified in one
+ * forward and the winning path committed afterwards.  Replaces
+ * tree_verify_step's batched forward over tiled caches and commit_tree_row
+ * (mlx_streaming/mtp/generate.py:355-420, kv_cache.py:283-316).
+ *
+ * vmi_attention_tree -- vmi_attention_layer over x bf16 [paths * span,
+ * hidden] (path p's rows p*span ..): every path's token j attends to the cache
+ * below pos0 and to its own path's tokens 0..j; the caches are only read, and
+ * each path's new keys and values go to tree_kv bf16
+ * [paths][n_kv_heads][2][span][256] (keys, then values; plain dims).  A
+ * path's rows equal what vmi_attention_layer gives its tokens as a chain, bit
+ * for bit.  paths * span <= 16, span <= 8.  workspace:
+ * vmi_attention_tree_workspace_bytes(paths, span, ...) bytes.
+ *
+ * vmi_gdn_tree -- vmi_gdn_layer over the same layout: each path starts from
+ * the state before pos0 and the conv rows below pos0; the rings are only
+ * read; the conv inputs go to tree_conv bf16 [paths * span][conv_dim] and
+ * each token's recurrence inputs to tree_side f32 [paths * span][n_k * 128 +
+ * n_v * 128 + 2 n_v] (normalised k of every key head, v of every value head,
+ * (g, beta) of every value head).  Rows equal vmi_gdn_layer's per path, bit
+ * for bit.  workspace: vmi_gdn_layer_workspace_bytes(paths * span, ...).
+ *
+ * vmi_tree_commit -- after vmi_accept_greedy (mode 0, P paths): for the
+ * record's winning path w and accepted length acc, writes into every layer of
+ * the table (device memory, n_layers entries) the entries of positions pos0
+ * .. pos0 + acc - 1: attention keys/values from tree_kv into the caches;
+ * Gated DeltaNet conv inputs into the conv ring and the state before
+ * pos0 + acc (the state before pos0 with path w's first acc tokens applied,
+ * the same arithmetic as vmi_gdn_layer) into ring slot (pos0 + acc) %
+ * n_slots.  pos0 from pos_device when set (read before vmi_spec_commit moves
+ * it).  max_heads: the largest n_kv_heads / n_v_heads of the table (<= 64);
+ * paths, span: the tree's shape (the table's buffers hold paths * span
+ * tokens); a record whose path or length lies outside it commits nothing.
+ * ------------------------------------------------------------------------ */
+#define VMI_TREE_ATTENTION 1
+#define VMI_TREE_GDN 2
+typedef struct vmi_tree_layer {
+    int kind;                          /* VMI_TREE_ATTENTION or VMI_TREE_GDN */
+    int n_kv_heads, max_len;           /* attention */
+    int n_k_heads, n_v_heads, n_slots; /* Gated DeltaNet */
+    uint16_t* k_cache;                 /* attention: the layer's caches and tree_kv */
+    uint16_t* v_cache;
+    const uint16_t* tree_kv;
+    uint16_t* conv_ring;               /* Gated DeltaNet: the rings, tree_conv and tree_side */
+    float* state_ring;
+    const uint16_t* tree_conv;
+    const float* tree_side;
+} vmi_tree_layer;
+
+size_t vmi_attention_tree_workspace_bytes(int paths, int span, int hidden, int n_heads, int n_kv_heads, int max_len);
+int vmi_attention_tree(const vmi_attn_layer_desc* desc, const uint16_t* x, int paths, int span, int pos0,
+                       const int32_t* pos_device, const uint16_t* k_cache, const uint16_t* v_cache, int max_len,
+                       uint16_t* tree_kv, uint16_t* out, void* workspace, size_t workspace_bytes, void* stream);
+int vmi_gdn_tree(const vmi_gdn_layer_desc* desc, const uint16_t* x, int paths, int span, int pos0,
+                 const int32_t* pos_device, const uint16_t* conv_ring, const float* state_ring, int n_slots,
+                 uint16_t* tree_conv, float* tree_side, uint16_t* out, void* workspace, size_t workspace_bytes,
+                 void* stream);
+int vmi_tree_commit(const int32_t* result, const vmi_tree_layer* layers, int n_layers, int max_heads, int paths,
+                    int span, int pos0, const int32_t* pos_device, void* stream);
 
 /* ------------------------------------------------------------------------
  * vmi_rmsnorm -- out = bf16(x * 1/sqrt(mean(x^2) + eps) * weight) per token

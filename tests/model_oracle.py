@@ -201,3 +201,70 @@ def check_mtp_steps(gpu, model, H, log):
         # chain both on the GPU's draft so the two compositions see the same tokens
         h, tok = Hn, am[:1].clone()
         h_np, tok_np = u16(Hn), int(am.item())
+
+
+def check_tree_forward(gpu, model, prompt, P, K, log, seed=0):
+    """forward_tree over P paths of K tokens against chain forwards of each
+    path (bit for bit: argmax and hidden rows), then TreeCommit of a winner
+    against a chain forward of the winner's accepted prefix: attention keys
+    and values, Gated DeltaNet conv rows and the state before the next
+    position, bit for bit.  Two cache sets filled by the same prefill."""
+    import torch
+    from vates_amd.accept import accept_greedy
+    from vates_amd.attention import KVCache
+    from vates_amd.decode import TreeCommit, prefill
+    V = model.embed.shape[0]
+    n = prompt.numel()
+    A = model.new_caches(128)
+    B = model.new_caches(128)
+    x, _ = prefill(model, prompt, A)
+    prefill(model, prompt, B)
+    rng = np.random.default_rng(seed)
+    paths = torch.tensor(rng.integers(0, V, (P, K)), dtype=torch.int32, device=gpu)
+    verify = torch.cat([x.view(1, 1).expand(P, 1), paths[:, :K - 1]], dim=1).contiguous()
+    am_t, hid_t, _ = model.forward_tree(verify.view(-1), A, n, P)
+    torch.cuda.synchronize()
+    assert all(c.length == n for c in A if c is not None), "a tree forward must not move the caches"
+    for p in range(P):
+        am_c, hid_c, _ = model.forward(verify[p], B, n)
+        torch.cuda.synchronize()
+        assert torch.equal(am_t[p * K:(p + 1) * K], am_c), f"path {p}: argmax differs from its chain forward"
+        assert torch.equal(hid_t[p * K:(p + 1) * K].view(torch.int16), hid_c.view(torch.int16)), f"path {p}: hidden"
+    log(f"  tree rows equal chain rows for {P} paths of {K}")
+    # a winner: plant the model's own predictions into one path so that it matches m drafts
+    for w, m in ((P - 1, K), (0, 0), (P // 2, 1)):
+        drafts = paths.clone()
+        preds = am_t.view(P, K).clone()
+        drafts[w, :m] = preds[w, :m]
+        if m < K:
+            drafts[w, m] = (preds[w, m] + 1) % V
+        for q in range(P):
+            if q != w:
+                drafts[q, 0] = (preds[q, 0] + 1) % V  # other paths match nothing
+        rec = accept_greedy(drafts, preds.view(-1), mode=0)
+        r = rec.cpu().tolist()
+        acc = min(m + 1, K)
+        assert r[1] == m and r[2] == acc and r[3] == (w if m > 0 else 0), r
+        w = r[3]
+        A2 = model.new_caches(128)
+        B2 = model.new_caches(128)
+        prefill(model, prompt, A2)
+        prefill(model, prompt, B2)
+        model.forward_tree(verify.view(-1), A2, n, P)
+        TreeCommit(A2, P, K)(rec, pos0=n)
+        model.forward(verify[w, :acc].contiguous(), B2, n)
+        torch.cuda.synchronize()
+        for li, (ca, cb) in enumerate(zip(A2, B2)):
+            if ca is None:
+                continue
+            if isinstance(ca, KVCache):
+                for name in ("keys", "values"):
+                    ga = getattr(ca, name)(n, n + acc)
+                    gb = getattr(cb, name)(n, n + acc)
+                    assert torch.equal(ga.view(torch.int16), gb.view(torch.int16)), (li, name, w, acc)
+            else:
+                assert torch.equal(ca.conv_rows(n + acc).view(torch.int16), cb.conv_rows(n + acc).view(torch.int16)), \
+                    (li, "conv", w, acc)
+                assert torch.equal(ca.state_before(n + acc).view(torch.int32),
+                                   cb.state_before(n + acc).view(torch.int32)), (li, "state", w, acc)
+        log(f"  commit of path {w} with {acc} accepted equals the chain forward of its prefix")

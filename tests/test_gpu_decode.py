@@ -17,6 +17,10 @@
   (away from the threshold), the stream equals greedy decoding, and the
   graph decoder reproduces the eager one step for step.
 * draft_paths takes its first tokens from the top-P of the MTP logits.
+* Tree verification: one forward over the P x K tokens of the paths equals
+  each path's chain forward bit for bit; committing the winner leaves every
+  cache as a chain forward of its accepted prefix would; tree decoding emits
+  the greedy stream.
 """
 import sys
 
@@ -276,6 +280,17 @@ def test_graph_adaptive_equals_eager(gpu, model):
     assert st.tokens == truth[:n_tok]
     assert st.depths == eager.depths and st.drafts == eager.drafts and st.accept_hist == eager.accept_hist
     assert len(set(st.depths)) >= 2, st.depths
+
+
+def test_tree_forward_equals_chains_and_commit(gpu, model):
+    """forward_tree (one forward over P x K tokens) equals each path's chain
+    forward bit for bit; TreeCommit leaves the caches exactly as a chain
+    forward of the winner's accepted prefix would."""
+    from model_oracle import check_tree_forward
+    log("case: tree forward P=3 K=3 vs chains, commit vs the winner's chain")
+    check_tree_forward(gpu, model, _prompt(gpu, seed=13), 3, 3, log)
+    log("case: tree forward P=4 K=4 (16 tokens) vs chains")
+    check_tree_forward(gpu, model, _prompt(gpu, seed=14), 4, 4, log, seed=1)
 
 
 def test_tree_decode_equals_greedy(gpu, model):

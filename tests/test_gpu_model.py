@@ -162,6 +162,16 @@ def test_forward_block_by_block(gpu, orc, full, full_oracle):
         assert torch.equal(am_f, am)
 
 
+def test_tree_forward_full_width(gpu, full):
+    """The batched tree forward at the full shape (9 tokens: the projection
+    GEMVs in two launches, 16/2 attention heads, 16/32 linear-attention heads,
+    T=9 MoE) equals chain forwards, and its commit equals the winner's chain."""
+    from model_oracle import check_tree_forward
+    log("case: tree forward P=3 K=3 at full width")
+    prompt = _ids(gpu, np.random.default_rng(21).integers(0, V, 8))
+    check_tree_forward(gpu, full, prompt, 3, 3, log)
+
+
 def test_mtp_steps_full_width(gpu, orc, full):
     log("case: two chained MTP steps vs the oracle composition (full width)")
     from model_oracle import check_mtp_steps

@@ -36,6 +36,18 @@ class QMat(ctypes.Structure):
     _fields_ = [("w", c_void_p), ("s", c_void_p), ("b", c_void_p)]
 
 
+VMI_TREE_ATTENTION = 1
+VMI_TREE_GDN = 2
+
+
+class TreeLayer(ctypes.Structure):
+    """vmi_tree_layer: one layer's entry of vmi_tree_commit's table."""
+    _fields_ = [("kind", c_int), ("n_kv_heads", c_int), ("max_len", c_int), ("n_k_heads", c_int),
+                ("n_v_heads", c_int), ("n_slots", c_int), ("k_cache", c_void_p), ("v_cache", c_void_p),
+                ("tree_kv", c_void_p), ("conv_ring", c_void_p), ("state_ring", c_void_p), ("tree_conv", c_void_p),
+                ("tree_side", c_void_p)]
+
+
 class MoeLayerDesc(ctypes.Structure):
     _fields_ = [
         ("hidden", c_int), ("inter", c_int), ("num_experts", c_int), ("top_k", c_int),
@@ -83,6 +95,12 @@ _SIGNATURES = {
     "vmi_attention_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "vmi_attention_layer": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
                                     c_void_p, c_size_t, c_void_p]),
+    "vmi_attention_tree_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
+    "vmi_attention_tree": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int,
+                                   c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "vmi_gdn_tree": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
+                             c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "vmi_tree_commit": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
     "vmi_gdn_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "vmi_gdn_layer": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
                               c_void_p, c_size_t, c_void_p]),

@@ -80,6 +80,14 @@ class KVCache:
         self.k = torch.zeros((n_kv_heads, nb, KV_BLOCK * head_dim), dtype=torch.bfloat16, device=device)
         self.v = torch.zeros_like(self.k)
         self.length = 0  # committed positions
+        self.n_kv = n_kv_heads
+        self.tree_kv = None  # [paths, n_kv, 2, span, 256] bf16: a draft tree's new keys and values
+
+    def tree_buffer(self, paths: int, span: int) -> torch.Tensor:
+        shape = (paths, self.n_kv, 2, span, 256)
+        if self.tree_kv is None or tuple(self.tree_kv.shape) != shape:
+            self.tree_kv = torch.zeros(shape, dtype=torch.bfloat16, device=self.k.device)
+        return self.tree_kv
 
     def trim(self, n: int) -> None:
         """Drops the last n positions (kv_cache.py:222-251: rejected drafts)."""
@@ -162,3 +170,30 @@ class AttentionLayer:
         if pos_device is None:
             cache.length = pos0 + T
         return out
+
+    def tree(self, x: torch.Tensor, cache: KVCache, paths: int, *, pos0: Optional[int] = None,
+             out: Optional[torch.Tensor] = None, stream=None, pos_device: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The block over a draft tree: x bf16 [paths * span, hidden], path p's
+        tokens at rows p*span.. and positions pos0.. (default: cache.length).
+        The cache is only read; every path's new keys and values go to
+        cache.tree_kv until vmi_tree_commit writes the winner's."""
+        T = x.shape[0]
+        if T % paths:
+            raise VmiError(f"{T} rows do not split into {paths} paths")
+        span = T // paths
+        pos0 = cache.length if pos0 is None else pos0
+        _require(x, "x", 2, self.device)
+        if out is None:
+            out = torch.empty_like(x)
+        tkv = cache.tree_buffer(paths, span)
+        sh = _stream_handle(stream)
+        lib = load()
+        ws = workspace(lib.vmi_attention_tree_workspace_bytes(paths, span, self.hidden, self.n_heads, self.n_kv,
+                                                              cache.max_len), self.device, sh, tag="attention")
+        rc = lib.vmi_attention_tree(ctypes.byref(self.desc), x.data_ptr(), paths, span, pos0,
+                                    None if pos_device is None else pos_device.data_ptr(), cache.k.data_ptr(),
+                                    cache.v.data_ptr(), cache.max_len, tkv.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                    ws.numel(), sh)
+        check(rc, "vmi_attention_tree")
+        return out
+

@@ -45,7 +45,8 @@
 namespace {
 
 constexpr int kAThreads = 256;
-constexpr int kQgMaxT = 8;
+constexpr int kQgMaxT = 8;       // tokens of one GEMV launch (and of one attention path)
+constexpr int kQgMaxBatch = 16;  // tokens of a GEMV call (launched in pieces of kQgMaxT)
 constexpr int kHeadDim = 256;
 
 // The batch's first position: the argument, or read on the device (graph
@@ -201,16 +202,10 @@ __global__ __launch_bounds__(kAThreads) void k_qgemv(QgArgs a) {
 constexpr int kKvBlock = 32;                      // positions per cache block
 constexpr int kKvBlockElems = kKvBlock * kHeadDim;
 
-__device__ __forceinline__ size_t kv_block(int g, int max_len, int pos) {
-    return ((size_t)g * (max_len / kKvBlock) + pos / kKvBlock) * kKvBlockElems;
-}
-__device__ __forceinline__ int k_elem(int kt, int d) {
-    const int nl = 4 * (kt >> 3) + (kt & 3), a = (kt >> 2) & 1;
-    return (((a * 8 + (d >> 5)) * 64 + ((d >> 3) & 3) * 16 + nl) << 3) + (d & 7);
-}
-__device__ __forceinline__ int v_elem(int kt, int d) {
-    return ((((d >> 4) * 64 + (kt >> 3) * 16 + (d & 15)) << 3) + (kt & 7));
-}
+static_assert(kKvBlock == VMI_KV_BLOCK, "cache block");
+__device__ __forceinline__ size_t kv_block(int g, int max_len, int pos) { return vmi_kv_block(g, max_len, pos); }
+__device__ __forceinline__ int k_elem(int kt, int d) { return vmi_k_elem(kt, d); }
+__device__ __forceinline__ int v_elem(int kt, int d) { return vmi_v_elem(kt, d); }
 
 // -------------------------------------------------------------- attention
 struct AttnArgs {
@@ -223,6 +218,9 @@ struct AttnArgs {
     uint16_t* k_cache;        // blocks of 32 positions, see the layout above
     uint16_t* v_cache;
     int T, n_heads, n_kv, pos0, max_len;
+    int paths, span;          // T = paths * span: path p's tokens p*span .. at positions pos0 ..
+    int chunks;               // chunks of the cache capacity the grid covers
+    uint16_t* tree_kv;        // or null: [paths][n_kv][2][span][256] new keys/values instead of the cache
     const int32_t* pos_dev;   // if set: pos0 is read here
     uint32_t* status;         // workspace status word (VMI_STATUS_BAD_POS)
     int nstride;              // chunk capacity of the partial buffers
@@ -299,9 +297,23 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     __shared__ float s_row[kChunkWaves][kHeadDim];                  // a wave's normalised row
     __shared__ float2 s_cs[kQgMaxT][kHeadDim / 2];                  // (cos, sin) per (token, frequency)
     __shared__ __attribute__((aligned(16))) uint16_t s_new[2][kQgMaxT][kHeadDim];  // new keys, values (bf16)
-    const int c = gridDim.x - 1 - blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    // one path: chunk gridDim.x - 1 - blockIdx.x.  Several (a tree): groups of
+    // 8 chunks x paths, a chunk's paths 8 apart in launch order (the same XCD,
+    // hence one L2 fetch of its cache blocks for all paths).
+    const int P = a.paths, T = a.span;                // T: this workgroup's tokens (one path)
+    int c, p = 0;
+    if (P == 1) {
+        c = gridDim.x - 1 - blockIdx.x;
+    } else {
+        const int grp = blockIdx.x / (8 * P), rem = blockIdx.x - grp * 8 * P;
+        p = rem >> 3;
+        c = a.chunks - 1 - (grp * 8 + (rem & 7));
+        if (c < 0) return;
+    }
+    const int g = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, w = at_wave(), nl = lane & 15, q4 = lane >> 4;
-    const int T = a.T, G = a.n_heads / a.n_kv, R = T * G;
+    const int G = a.n_heads / a.n_kv, R = T * G;
+    const int tok0 = p * T;                            // the path's first row of qkv
     const int pos0 = batch_pos0(a.pos0, a.pos_dev, T, a.max_len);
     if (a.pos_dev && blockIdx.x == 0 && g == 0 && tid == 0 && *a.pos_dev != pos0)
         atomicOr(a.status, VMI_STATUS_BAD_POS);    // clamped: the caller's position overran the cache
@@ -315,7 +327,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
 
     // projections (lanes and rows past the batch read zeros), then the cache
     constexpr int QR = 2 * MS;                         // query rows per wave
-    const __amdgpu_buffer_rsrc_t rq = vmi_rsrc(a.qkv, (uint32_t)(T * a.stride) * 4u);
+    const __amdgpu_buffer_rsrc_t rq = vmi_rsrc(a.qkv + (size_t)tok0 * a.stride, (uint32_t)(T * a.stride) * 4u);
     float qv[QR][4], kv[4], vv[4];
     uint32_t qnr[4], knr[4];
 #pragma unroll
@@ -395,19 +407,26 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
             for (int j = 0; j < 4; ++j) s_q[row][lane + 64 * j] = o[j];
         }
     }
-    // the new key and value of position pos0 + tn: to the cache and to LDS
+    // the new key and value of position pos0 + tn: to the cache (a tree: to
+    // the path's rows of tree_kv, committed for the winning path only) and to LDS
     if (has_new) {
         const int pos = pos0 + tn;
         uint16_t o[4];
         norm_rope_row(kv, kn, a.eps, s_cs[tn], a.rope_dim, s_row[w], o);
         const size_t blk = kv_block(g, a.max_len, pos);
         const int kt = pos % kKvBlock;
+        uint16_t* side = a.tree_kv ? a.tree_kv + ((size_t)(p * a.n_kv + g) * 2 * T + tn) * kHeadDim : nullptr;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int d = lane + 64 * j;
             const uint16_t vb16 = vmi_f32_to_bf16(vv[j]);
-            a.k_cache[blk + k_elem(kt, d)] = o[j];
-            a.v_cache[blk + v_elem(kt, d)] = vb16;
+            if (side) {
+                side[d] = o[j];
+                side[(size_t)T * kHeadDim + d] = vb16;
+            } else {
+                a.k_cache[blk + k_elem(kt, d)] = o[j];
+                a.v_cache[blk + v_elem(kt, d)] = vb16;
+            }
             s_new[0][tn][d] = o[j];
             s_new[1][tn][d] = vb16;
         }
@@ -514,7 +533,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         }
     }
     // O = P V for dims 32 w + 16 dt + nl; A = P of block sb (written by wave sb)
-    const size_t pbase = ((size_t)g * a.nstride + c) * RP;
+    const size_t pbase = (((size_t)g * a.nstride + c) * P + p) * RP;  // a chunk holds the rows of every path
 #pragma unroll
     for (int m = 0; m < MS; ++m) {
 #pragma unroll
@@ -541,7 +560,8 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
 // grid (T * n_heads, 4): one quarter of a head's dims per workgroup.  Chunk c
 // is added by slot c % 16 in increasing c and the 16 slots are combined in a
 // fixed tree, so the result does not depend on how many chunks a launch has:
-// chunks past a query's last position carry weight exactly zero.
+// chunks past a query's last position carry weight exactly zero.  Token t
+// belongs to path t / span; RP is a path's rows per chunk.
 constexpr int kMergeMaxChunks = 2048;
 __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
     __shared__ float s_f[kMergeMaxChunks];
@@ -549,8 +569,10 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
     __shared__ float4 s_num[kAThreads / 64][16];
     const int t = blockIdx.x / a.n_heads, h = blockIdx.x % a.n_heads, tid = threadIdx.x;
     const int lane = tid & 63, w = at_wave();
-    const int G = a.n_heads / a.n_kv, g = h / G, row = t * G + (h % G);
-    const int NC = (batch_pos0(a.pos0, a.pos_dev, a.T, a.max_len) + a.T + kChunkKeys - 1) / kChunkKeys;
+    const int pth = t / a.span, tt = t - pth * a.span;
+    const int G = a.n_heads / a.n_kv, g = h / G, row = pth * RP + tt * G + (h % G);
+    const int NC = (batch_pos0(a.pos0, a.pos_dev, a.span, a.max_len) + a.span + kChunkKeys - 1) / kChunkKeys;
+    RP *= a.paths;  // rows per chunk
     // loads in issue order: every chunk's (max, sum) of this row (branch-free,
     // chunks past the cache read nothing), then this lane's first 8 partial
     // outputs, which arrive while the maximum and the denominator form
@@ -880,7 +902,7 @@ struct AttnLayout {
     size_t status, xn, qkv, part_o, part_ml, o, bytes;
 };
 
-AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len) {
+AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len, int paths = 1) {
     AttnLayout L{};
     size_t off = 0;
     auto take = [&](size_t b) {
@@ -888,7 +910,7 @@ AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len) {
         off += vmi::align256(b);
         return o;
     };
-    const int RP = 16 * ((T * (n_heads / n_kv) + 15) / 16);
+    const int RP = paths * 16 * ((T / paths * (n_heads / n_kv) + 15) / 16);
     const int stride = n_heads * 2 * kHeadDim + 2 * n_kv * kHeadDim;
     L.status = take(4);
     L.xn = take((size_t)T * H * 2);
@@ -905,7 +927,22 @@ bool qm_ok(const vmi_qmat& m) { return vmi::qmat_ok(m); }
 
 }  // namespace
 
-hipError_t vmi::launch_qgemv(const QgemvCall& q, hipStream_t s) {
+hipError_t vmi::launch_qgemv(const QgemvCall& q0, hipStream_t s) {
+    if (q0.T > kQgMaxT) {
+        // pieces of up to kQgMaxT tokens: a token's result does not depend on its batch
+        for (int t0 = 0; t0 < q0.T; t0 += kQgMaxT) {
+            QgemvCall c = q0;
+            c.T = q0.T - t0 < kQgMaxT ? q0.T - t0 : kQgMaxT;
+            c.x = q0.x + (size_t)t0 * q0.K;
+            if (c.out) c.out = q0.out + (size_t)t0 * q0.out_stride;
+            if (c.out_bf16) c.out_bf16 = q0.out_bf16 + (size_t)t0 * q0.out_stride;
+            if (c.residual) c.residual = q0.residual + (size_t)t0 * q0.out_stride;
+            const hipError_t e = launch_qgemv(c, s);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    const QgemvCall& q = q0;
     const int ks = q.K / kQ4Kw;
     uintptr_t sb_align = 0;  // the MFMA kernel reads 8 scales / biases as one 16-byte load
     for (int i = 0; i < 3; ++i)
@@ -938,7 +975,7 @@ bool vmi::qgemv_fuses_norm(const QgemvCall& q) {
     for (int i = 0; i < 3; ++i)
         if (q.rows[i] > 0 || i == 0)
             sb_align |= reinterpret_cast<uintptr_t>(q.m[i].s) | reinterpret_cast<uintptr_t>(q.m[i].b);
-    return q.bits == 4 && (q.K == 512 || q.K == 1024 || q.K == kQ4MaxK) && q.T <= kQgMaxT && !(sb_align & 15) &&
+    return q.bits == 4 && (q.K == 512 || q.K == 1024 || q.K == kQ4MaxK) && !(sb_align & 15) &&
            !(reinterpret_cast<uintptr_t>(q.norm_w) & 15);
 }
 
@@ -949,9 +986,10 @@ bool vmi::qmat_ok(const vmi_qmat& m) {
 extern "C" int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int group, float* out,
                          const uint16_t* residual, uint16_t* out_bf16, void* stream) {
     vmi::clear_error();
-    if (T <= 0 || T > kQgMaxT) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, %d]", T, kQgMaxT);
+    if (T <= 0 || T > kQgMaxBatch) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, %d]", T, kQgMaxBatch);
     if (K <= 0 || K % 64 || N <= 0) return vmi::fail(VMI_ERR_INVALID, "K=%d (multiple of 64) N=%d", K, N);
-    if ((size_t)T * K * 2 > 65536) return vmi::fail(VMI_ERR_UNSUPPORTED, "T*K=%d exceeds 32768", T * K);
+    if ((size_t)(T < kQgMaxT ? T : kQgMaxT) * K * 2 > 65536)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "K=%d too wide for %d tokens", K, T);
     if ((bits != 4 && bits != 8) || group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", bits, group);
     if (!x || !qm_ok(w) || (!out && !out_bf16)) return vmi::fail(VMI_ERR_INVALID, "null x/weights/out");
     if ((reinterpret_cast<uintptr_t>(x) & 15)) return vmi::fail(VMI_ERR_INVALID, "x must be 16-byte aligned");
@@ -969,25 +1007,41 @@ extern "C" size_t vmi_attention_layer_workspace_bytes(int T, int hidden, int n_h
     return attn_layout(T, hidden, n_heads, n_kv_heads, max_len).bytes;
 }
 
-extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int T, int pos0,
-                                   const int32_t* pos_device, uint16_t* k_cache, uint16_t* v_cache, int max_len, uint16_t* out,
-                                   void* workspace, size_t workspace_bytes, void* stream) {
-    vmi::clear_error();
+extern "C" size_t vmi_attention_tree_workspace_bytes(int paths, int span, int hidden, int n_heads, int n_kv_heads,
+                                                     int max_len) {
+    if (paths <= 0 || span <= 0 || hidden <= 0 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads ||
+        max_len <= 0)
+        return 0;
+    return attn_layout(paths * span, hidden, n_heads, n_kv_heads, max_len, paths).bytes;
+}
+
+namespace {
+
+// The attention block over `paths` sequences of `span` tokens that share the
+// cache up to pos0 (one path: the verify batch; several: a draft tree, new
+// keys/values to tree_kv instead of the cache).
+int attention_impl(const vmi_attn_layer_desc* desc, const uint16_t* x, int paths, int span, int pos0,
+                   const int32_t* pos_device, uint16_t* k_cache, uint16_t* v_cache, int max_len, uint16_t* tree_kv,
+                   uint16_t* out, void* workspace, size_t workspace_bytes, void* stream) {
     if (!desc) return vmi::fail(VMI_ERR_INVALID, "null desc");
     const vmi_attn_layer_desc& D = *desc;
-    if (T <= 0 || T > kQgMaxT) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, %d]", T, kQgMaxT);
+    const int T = paths * span;
+    if (span <= 0 || span > kQgMaxT) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, %d]", span, kQgMaxT);
+    if (paths <= 0 || T > kQgMaxBatch)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "paths=%d x span=%d exceeds %d tokens", paths, span, kQgMaxBatch);
     if (D.head_dim != kHeadDim) return vmi::fail(VMI_ERR_UNSUPPORTED, "head_dim=%d (256 only)", D.head_dim);
     if (D.n_heads <= 0 || D.n_kv_heads <= 0 || D.n_heads % D.n_kv_heads)
         return vmi::fail(VMI_ERR_INVALID, "n_heads=%d n_kv_heads=%d", D.n_heads, D.n_kv_heads);
     const int G = D.n_heads / D.n_kv_heads;
-    if (T * G > 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "T * heads per kv head = %d exceeds 64", T * G);
+    if (span * G > 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "T * heads per kv head = %d exceeds 64", span * G);
     if (D.hidden % 512 || D.hidden > 4096) return vmi::fail(VMI_ERR_UNSUPPORTED, "hidden=%d", D.hidden);
-    if (D.n_heads * kHeadDim * T * 2 > 65536 || D.hidden * T * 2 > 65536)
+    const int Tp = T < kQgMaxT ? T : kQgMaxT;  // tokens of one GEMV launch
+    if (D.n_heads * kHeadDim * Tp * 2 > 65536 || D.hidden * Tp * 2 > 65536)
         return vmi::fail(VMI_ERR_UNSUPPORTED, "T too large for the projection GEMV");
     if (D.rope_dim < 0 || D.rope_dim > kHeadDim || D.rope_dim % 2) return vmi::fail(VMI_ERR_INVALID, "rope_dim=%d", D.rope_dim);
     if ((D.bits != 4 && D.bits != 8) || D.group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", D.bits, D.group);
-    if (T > max_len || (!pos_device && (pos0 < 0 || pos0 + T > max_len)))
-        return vmi::fail(VMI_ERR_INVALID, "pos0=%d T=%d max_len=%d", pos0, T, max_len);
+    if (span > max_len || (!pos_device && (pos0 < 0 || pos0 + span > max_len)))
+        return vmi::fail(VMI_ERR_INVALID, "pos0=%d T=%d max_len=%d", pos0, span, max_len);
     if (max_len % kKvBlock) return vmi::fail(VMI_ERR_INVALID, "max_len=%d must be a multiple of %d", max_len, kKvBlock);
     if (attn_chunks(max_len) > kMergeMaxChunks)
         return vmi::fail(VMI_ERR_UNSUPPORTED, "max_len=%d exceeds %d", max_len, kMergeMaxChunks * kChunkKeys);
@@ -998,7 +1052,7 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(k_cache) |
          reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(D.input_norm)) & 15)
         return vmi::fail(VMI_ERR_INVALID, "x, out, caches and norm weight must be 16-byte aligned");
-    const AttnLayout L = attn_layout(T, D.hidden, D.n_heads, D.n_kv_heads, max_len);
+    const AttnLayout L = attn_layout(T, D.hidden, D.n_heads, D.n_kv_heads, max_len, paths);
     if (!workspace || workspace_bytes < L.bytes)
         return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -1029,16 +1083,18 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     at.rope_dim = D.rope_dim; at.theta = D.rope_theta; at.eps = D.norm_eps;
     at.k_cache = k_cache; at.v_cache = v_cache;
     at.T = T; at.n_heads = D.n_heads; at.n_kv = D.n_kv_heads; at.pos0 = pos0; at.pos_dev = pos_device;
+    at.paths = paths; at.span = span; at.tree_kv = tree_kv;
     at.status = reinterpret_cast<uint32_t*>(ws + L.status);
     at.max_len = max_len;
     at.nstride = attn_chunks(max_len);
     // with the position on the device every chunk of the capacity is launched; those past the cache exit
-    const int grid_chunks = pos_device ? at.nstride : attn_chunks(pos0 + T);
+    const int grid_chunks = pos_device ? at.nstride : attn_chunks(pos0 + span);
+    at.chunks = grid_chunks;
     at.part_o = reinterpret_cast<float*>(ws + L.part_o);
     at.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
     at.o = ob;
-    const int MS = (T * G + 15) / 16;
-    const dim3 ag(grid_chunks, D.n_kv_heads);
+    const int MS = (span * G + 15) / 16;
+    const dim3 ag(paths == 1 ? grid_chunks : (grid_chunks + 7) / 8 * 8 * paths, D.n_kv_heads);
     switch (MS) {
         case 1: hipLaunchKernelGGL(k_attn_chunk<1>, ag, dim3(kChunkThreads), 0, s, at); break;
         case 2: hipLaunchKernelGGL(k_attn_chunk<2>, ag, dim3(kChunkThreads), 0, s, at); break;
@@ -1055,6 +1111,27 @@ extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16
     e = vmi::launch_qgemv(o, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "o_proj launch");
     return VMI_OK;
+}
+
+}  // namespace
+
+extern "C" int vmi_attention_layer(const vmi_attn_layer_desc* desc, const uint16_t* x, int T, int pos0,
+                                   const int32_t* pos_device, uint16_t* k_cache, uint16_t* v_cache, int max_len, uint16_t* out,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    vmi::clear_error();
+    return attention_impl(desc, x, 1, T, pos0, pos_device, k_cache, v_cache, max_len, nullptr, out, workspace,
+                          workspace_bytes, stream);
+}
+
+extern "C" int vmi_attention_tree(const vmi_attn_layer_desc* desc, const uint16_t* x, int paths, int span, int pos0,
+                                  const int32_t* pos_device, const uint16_t* k_cache, const uint16_t* v_cache,
+                                  int max_len, uint16_t* tree_kv, uint16_t* out, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+    vmi::clear_error();
+    if (paths < 1 || !tree_kv) return vmi::fail(VMI_ERR_INVALID, "paths=%d tree_kv=%p", paths, (void*)tree_kv);
+    // the caches are only read: every path's new keys and values go to tree_kv
+    return attention_impl(desc, x, paths, span, pos0, pos_device, const_cast<uint16_t*>(k_cache),
+                          const_cast<uint16_t*>(v_cache), max_len, tree_kv, out, workspace, workspace_bytes, stream);
 }
 
 extern "C" int vmi_rmsnorm(const uint16_t* x, const int32_t* ids, int rows, int T, int hidden, const uint16_t* weight,

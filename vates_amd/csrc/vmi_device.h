@@ -361,3 +361,18 @@ __device__ __forceinline__ uint32_t vmi_bload_b32(__amdgpu_buffer_rsrc_t r, uint
 __device__ __forceinline__ uint32_t vmi_bload_b16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
 }
+
+// KV cache of the attention layers: per kv head, blocks of 32 positions x 256
+// dims (8192 bf16), each in the operand order of the attention kernel's MFMAs
+// (vmi.h, vmi_attention_layer, states the element formulas).
+constexpr int VMI_KV_BLOCK = 32;
+__device__ __forceinline__ size_t vmi_kv_block(int g, int max_len, int pos) {
+    return ((size_t)g * (max_len / VMI_KV_BLOCK) + pos / VMI_KV_BLOCK) * (size_t)(VMI_KV_BLOCK * 256);
+}
+__device__ __forceinline__ int vmi_k_elem(int kt, int d) {
+    const int nl = 4 * (kt >> 3) + (kt & 3), a = (kt >> 2) & 1;
+    return (((a * 8 + (d >> 5)) * 64 + ((d >> 3) & 3) * 16 + nl) << 3) + (d & 7);
+}
+__device__ __forceinline__ int vmi_v_elem(int kt, int d) {
+    return ((((d >> 4) * 64 + (kt >> 3) * 16 + (d & 15)) << 3) + (kt & 7));
+}

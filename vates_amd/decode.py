@@ -27,7 +27,7 @@ from typing import List, Optional
 import numpy as np
 import torch
 
-from ._lib import VmiError
+from ._lib import VmiError, check, load
 from .accept import accept_greedy, spec_commit
 from .attention import AttentionLayer, KVCache
 from .gdn import GatedDeltaNetLayer, GdnCache
@@ -84,6 +84,25 @@ class SpecModel:
         logits, am, _ = lm_head(x, self.head, self.final_norm, eps=self.eps, want_logits=want_logits)
         return am, x, logits
 
+    def forward_tree(self, ids: torch.Tensor, caches: list, pos0: int, paths: int, *, want_logits: bool = False,
+                     pos_device: Optional[torch.Tensor] = None):
+        """One forward over a draft tree (tree_verify_step's batched forward,
+        generate.py:355-376): ids int32 [paths * span], path p's tokens at rows
+        p*span.. and positions pos0..; every path sees the committed caches and
+        its own earlier tokens, and the caches are left untouched (the new
+        entries wait in the caches' tree buffers for ``TreeCommit``).  Returns
+        (argmax int32 [paths * span], pre-norm hidden bf16 [paths * span, H],
+        logits or None); a path's rows equal ``forward`` of its tokens alone."""
+        x = rmsnorm(self.embed, None, ids=ids)
+        for layer, cache in zip(self.layers, caches):
+            if layer.attn is not None:
+                x = layer.attn.tree(x, cache, paths, pos0=pos0, pos_device=pos_device)
+            elif layer.gdn is not None:
+                x = layer.gdn.tree(x, cache, paths, pos0=pos0, pos_device=pos_device)
+            x = layer.moe(x, residual=x)
+        logits, am, _ = lm_head(x, self.head, self.final_norm, eps=self.eps, want_logits=want_logits)
+        return am, x, logits
+
     def commit(self, caches: list, length: int) -> None:
         """Keeps positions < length in every cache (commit_verified_prefix,
         kv_cache.py:222-251): attention caches drop the rejected keys, linear
@@ -91,6 +110,48 @@ class SpecModel:
         for c in caches:
             if c is not None:
                 c.length = length
+
+
+class TreeCommit:
+    """Commits the winning path of a tree forward into every cache in one
+    launch (vmi_tree_commit; commit_tree_row, kv_cache.py:283-316): for the
+    acceptance record's path w and accepted length acc, the attention layers'
+    keys and values of positions pos0 .. pos0 + acc - 1, the linear-attention
+    layers' conv inputs of those positions and their state before pos0 + acc.
+    The layer table lives in device memory."""
+
+    def __init__(self, caches: list, paths: int, span: int):
+        from ._lib import VMI_TREE_ATTENTION, VMI_TREE_GDN, TreeLayer
+        rows = []
+        heads = 1
+        for c in caches:
+            if c is None:
+                continue
+            e = TreeLayer()
+            if isinstance(c, KVCache):
+                tkv = c.tree_buffer(paths, span)
+                e.kind, e.n_kv_heads, e.max_len = VMI_TREE_ATTENTION, c.n_kv, c.max_len
+                e.k_cache, e.v_cache, e.tree_kv = c.k.data_ptr(), c.v.data_ptr(), tkv.data_ptr()
+                heads = max(heads, c.n_kv)
+            elif isinstance(c, GdnCache):
+                e.kind, e.n_k_heads, e.n_v_heads, e.n_slots = VMI_TREE_GDN, c.n_k, c.n_v, c.n_slots
+                e.conv_ring, e.state_ring = c.conv.data_ptr(), c.state.data_ptr()
+                e.tree_conv, e.tree_side = c.tree_conv.data_ptr(), c.tree_side.data_ptr()
+                heads = max(heads, c.n_v)
+            else:
+                raise VmiError(f"cannot commit a tree into {type(c).__name__}")
+            rows.append(bytes(e))
+        self.n, self.heads, self.paths, self.span = len(rows), heads, paths, span
+        self.caches = caches
+        dev = next(c.k.device if isinstance(c, KVCache) else c.conv.device for c in caches if c is not None)
+        self.table = torch.frombuffer(bytearray(b"".join(rows)), dtype=torch.uint8).to(dev)
+
+    def __call__(self, rec: torch.Tensor, *, pos0: int = 0, pos_device: Optional[torch.Tensor] = None,
+                 stream=None) -> None:
+        from .moe import _stream_handle
+        rc = load().vmi_tree_commit(rec.data_ptr(), self.table.data_ptr(), self.n, self.heads, self.paths, self.span, pos0,
+                                    None if pos_device is None else pos_device.data_ptr(), _stream_handle(stream))
+        check(rc, "vmi_tree_commit")
 
 
 def commit_verified_prefix(caches: list, verified_len: int, accepted_len: int) -> bool:
@@ -220,22 +281,21 @@ def tree_speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: to
                             pos: int, n_tokens: int, K: int = 3, P: int = 3, plant=None) -> DecodeStats:
     """Tree verification (tree_verify_step, generate.py:355-420): the MTP
     drafter's P paths (draft_paths: top-P first tokens, greedy continuations,
-    drafter.py:150-177), each verified as [x, d1..d_{K-1}] (the T = K layout);
-    the winner is the longest matched prefix, ties to the lower path
-    (vmi_accept_greedy, generate.py:383); emission and accepted length as
-    accept_prefix's T = K rules (generate.py:338-351, 819).
-
-    The paths are verified one after another over the same caches (each
-    writes the same positions; the linear-attention rings keep the state of
-    pos untouched), then the winner's accepted prefix is run once more so the
-    caches hold exactly its entries; the kernels' results do not depend on
-    batch size, so this equals the reference's batched forward and commit of
-    the winner's row (commit_tree_row, kv_cache.py:283-316).  plant(step, pos)
-    -> P x K draft tokens replaces the drafts (tests)."""
+    drafter.py:150-177), each [x, d1..d_{K-1}] (the T = K layout), verified in
+    one forward over the P x K tokens (``SpecModel.forward_tree``); the winner
+    is the longest matched prefix, ties to the lower path (vmi_accept_greedy,
+    generate.py:383); emission and accepted length as accept_prefix's T = K
+    rules (generate.py:338-351, 819); the winner's entries are committed into
+    every cache in one launch (``TreeCommit``, commit_tree_row,
+    kv_cache.py:283-316).  plant(step, pos) -> P x K draft tokens replaces the
+    drafts (tests)."""
     if model.mtp is None:
         raise VmiError("the model has no MTP layer")
+    if P * K > 16:
+        raise VmiError(f"a tree of {P} x {K} tokens exceeds 16")
     st = DecodeStats()
     dev = x.device
+    commit = TreeCommit(caches, P, K)
     t0 = time.perf_counter()
     while len(st.tokens) < n_tokens:
         mtp_start = drafter.cache.length
@@ -243,27 +303,23 @@ def tree_speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: to
         if plant is not None:
             paths.copy_(torch.tensor(plant(st.steps, pos), dtype=torch.int32))
         verify = torch.cat([x.view(1, 1).expand(P, 1), paths[:, :K - 1]], dim=1).contiguous()  # [P, K]
-        preds = torch.empty((P, K), dtype=torch.int32, device=dev)
-        hids = []
-        for p in range(P):
-            am, hid, _ = model.forward(verify[p], caches, pos)
-            preds[p].copy_(am)
-            hids.append(hid)
+        preds, hid, _ = model.forward_tree(verify.view(-1), caches, pos, P)
         rec = accept_greedy(paths, preds, mode=0)
+        commit(rec, pos0=pos)
         r = rec.cpu().tolist()  # the step's one host synchronisation
         n, m, acc, best = r[0], r[1], r[2], r[3]
         emitted = r[4:4 + n]
-        # the caches now hold the last path's entries: write the winner's accepted prefix again
-        _, hid_w, _ = model.forward(verify[best, :acc].contiguous(), caches, pos)
         model.commit(caches, pos + acc)
-        h_seq = torch.cat([H_last, hid_w[:acc - 1]]) if acc > 1 else H_last
+        w0 = best * K
+        h_seq = torch.cat([H_last, hid[w0:w0 + acc - 1]]) if acc > 1 else H_last
         drafter.sync(mtp_start, h_seq.contiguous(), verify[best, :acc].contiguous())
         st.tokens.extend(emitted)
         st.accept_hist.append(m)
+        st.depths.append(K)
         st.steps += 1
         pos += acc
         x = torch.tensor([emitted[-1]], dtype=torch.int32, device=dev)
-        H_last = hid_w[acc - 1:acc].clone()
+        H_last = hid[w0 + acc - 1:w0 + acc].clone()
     st.seconds = time.perf_counter() - t0
     st.tokens = st.tokens[:n_tokens]
     return st

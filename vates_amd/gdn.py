@@ -43,6 +43,11 @@ class GdnCache:
         self.state = torch.zeros((n_slots, n_v_heads, HEAD_DIM, HEAD_DIM), dtype=torch.float32, device=device)
         self.n_slots = n_slots
         self.length = 0
+        self.n_k, self.n_v = n_k_heads, n_v_heads
+        # a draft tree's conv inputs and recurrence inputs, per token (16 tokens at most)
+        self.tree_conv = torch.zeros((16, self.conv_dim), dtype=torch.bfloat16, device=device)
+        self.tree_side = torch.zeros((16, (n_k_heads + n_v_heads) * HEAD_DIM + 2 * n_v_heads), dtype=torch.float32,
+                                     device=device)
 
     def trim(self, n: int) -> None:
         """Drops the last n positions (the rejected drafts of a verify batch)."""
@@ -123,3 +128,29 @@ class GatedDeltaNetLayer:
         if pos_device is None:
             cache.length = pos0 + T
         return out
+
+    def tree(self, x: torch.Tensor, cache: GdnCache, paths: int, *, pos0: Optional[int] = None,
+             out: Optional[torch.Tensor] = None, stream=None, pos_device: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The block over a draft tree: x bf16 [paths * span, hidden], every
+        path from the state before pos0 (default: cache.length).  The rings are
+        only read; conv and recurrence inputs go to cache.tree_conv /
+        cache.tree_side until vmi_tree_commit applies the winner's."""
+        T = x.shape[0]
+        if T % paths or T > cache.tree_conv.shape[0]:
+            raise VmiError(f"{T} rows do not split into {paths} paths of a tree of at most 16 tokens")
+        span = T // paths
+        pos0 = cache.length if pos0 is None else pos0
+        _require(x, "x", 2, self.device)
+        if out is None:
+            out = torch.empty_like(x)
+        sh = _stream_handle(stream)
+        lib = load()
+        ws = workspace(lib.vmi_gdn_layer_workspace_bytes(T, self.hidden, self.n_k, self.n_v), self.device, sh,
+                       tag="gdn")
+        rc = lib.vmi_gdn_tree(ctypes.byref(self.desc), x.data_ptr(), paths, span, pos0,
+                              None if pos_device is None else pos_device.data_ptr(), cache.conv.data_ptr(),
+                              cache.state.data_ptr(), cache.n_slots, cache.tree_conv.data_ptr(),
+                              cache.tree_side.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), sh)
+        check(rc, "vmi_gdn_tree")
+        return out
+
