@@ -37,16 +37,15 @@ ROUTER8_BYTES = 512 * 2048 + 2 * 512 * 32 * 2  # 1,114,112
 SGATE8_BYTES = 2048 + 2 * 32 * 2  # 2,176
 SEED = 1234
 ZIPF_S, ZIPF_ALPHA = 1.1, 0.5
-# HBM bytes a layer call of the MoE stack moves, per algorithmic byte, from
-# rocprofv3 counter passes over `--layers 8 --steps 3 --warmup 1 --no-graph`
-# (32 layer calls, 31.42 distinct experts on average, 58,525,824 algorithmic
-# bytes a call): FETCH_SIZE summed over k_router, k_gateup and k_down_rows
-# 29,703.7 KiB a call x 2.000 (a plain copy of 512 MiB reads 262,157 KiB on
-# that counter) plus WRITE_SIZE 227.8 KiB x 1.000 (the copy's 524,288 KiB) =
-# 61,066,445 bytes, i.e. 1.0434 of the algorithmic bytes.
-MOE_TRAFFIC_PER_ALGO_BYTE = 1.0434
-MOE_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over 32 layer calls, scaled by a 512 MiB copy "
-                      "(x2.000 / x1.000): 61,066,445 B against 58,525,824 algorithmic B")
+# HBM bytes a layer call of the MoE stack moves, measured by rocprofv3 counter
+# passes (profiles/moe_layer_48x_T4_traffic.md) over `--layers 8 --steps 3
+# --warmup 1 --no-graph --no-decode` (32 layer calls): FETCH_SIZE summed over
+# the layer's kernels, scaled by what the counter reads for a plain copy of
+# known size (bench.py --path copy), plus WRITE_SIZE likewise.  A committed
+# measurement of the kernels as they are, not a figure of this run.
+MOE_TRAFFIC_BYTES = 61066445
+MOE_TRAFFIC_SOURCE = ("profiles/moe_layer_48x_T4_traffic.md: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over 32 layer "
+                      "calls, scaled by a 512 MiB copy (x2.000 / x1.000): 61,066,445 B against 58,525,824 algorithmic B")
 
 
 def eprint(*a):
@@ -57,33 +56,70 @@ def layer_bytes(U: np.ndarray, T: int, H: int) -> np.ndarray:
     return U.astype(np.float64) * EXPERT_BYTES + EXPERT_BYTES + ROUTER8_BYTES + SGATE8_BYTES + 3 * T * H * 2
 
 
-def cpu_baseline(layers_w, x_bank, args, budget_s: float):
+def _threads_label(threads: int) -> int:
+    avail = len(os.sched_getaffinity(0))
+    return min(threads, avail) if threads > 0 else min(int(os.environ.get("OMP_NUM_THREADS", "0")) or avail, avail)
+
+
+def cpu_baseline(layers_w, x_bank, args, budget_s: float, threads: int = 0):
     """Times the CPU oracle (OpenMP, float64 accumulation) on a bounded sample of
     the same workload: the first layers' weights copied to host, fed with the
-    first steps' activations, until `budget_s` seconds of CPU work."""
+    first steps' activations, until `budget_s` seconds of CPU work.  threads:
+    OpenMP threads (0: all the process may use)."""
     from oracle import oracle as orc
     from oracle.torch_bridge import layer_np
 
     n_layers = min(2, len(layers_w))
     Ls = [layer_np(layers_w[i], args.top_k) for i in range(n_layers)]
+    prev = orc.set_threads(threads if threads > 0 else len(os.sched_getaffinity(0)))
     done_bytes, done = 0.0, 0
     t0 = time.perf_counter()
     s = 0
-    while time.perf_counter() - t0 < budget_s:
-        x = x_bank[s % x_bank.shape[0]].view(np.uint16)
-        for L in Ls:
-            out_f32, out_bf16, ids, sc, sl = orc.moe_layer(x, L, residual=True)
-            U = len(np.unique(ids))
-            done_bytes += float(layer_bytes(np.array([U]), args.T, args.hidden)[0])
-            done += 1
-            x = out_bf16
-        s += 1
+    try:
+        while time.perf_counter() - t0 < budget_s:
+            x = x_bank[s % x_bank.shape[0]].view(np.uint16)
+            for L in Ls:
+                out_f32, out_bf16, ids, sc, sl = orc.moe_layer(x, L, residual=True)
+                U = len(np.unique(ids))
+                done_bytes += float(layer_bytes(np.array([U]), args.T, args.hidden)[0])
+                done += 1
+                x = out_bf16
+            s += 1
+    finally:
+        orc.set_threads(prev)
     el = time.perf_counter() - t0
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
-    threads = min(threads, len(os.sched_getaffinity(0)))
-    return {"value": round(done_bytes / el / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(done_bytes / el / 1e9, 4), "unit": "GB/s", "cores": _threads_label(threads),
+            "kind": "port",
             "sample": f"{done} layer calls ({n_layers} layers x {s} steps, T={args.T}) of the same stack, "
                       f"{el:.1f} s, float64 oracle with OpenMP"}
+
+
+def moe_parity(layers, layers_w, x, args) -> dict:
+    """The first two layers of the stack on one verify batch against the oracle:
+    routed ids, and each layer's output from the GPU's own input (relative L2,
+    cosine, worst token)."""
+    import torch
+    from oracle import oracle as orc
+    from oracle.torch_bridge import layer_np, u16
+
+    T, k = x.shape[0], args.top_k
+    cur = x
+    worst_rel, worst_cos, ids_equal = 0.0, 1.0, True
+    for l in range(2):
+        ids = torch.empty((T, k), dtype=torch.int32, device=x.device)
+        out = layers[l](cur, residual=cur, ids_out=ids)
+        torch.cuda.synchronize()
+        ref32, _, rid, _, _ = orc.moe_layer(u16(cur), layer_np(layers_w[l], k), residual=True)
+        ids_equal &= bool(np.array_equal(ids.cpu().numpy(), rid))
+        got = orc.bf16_to_f32(u16(out).reshape(T, -1)).astype(np.float64)
+        for t in range(T):
+            g, r = got[t], ref32[t]
+            worst_rel = max(worst_rel, float(np.linalg.norm(g - r) / np.linalg.norm(r)))
+            worst_cos = min(worst_cos, float(g @ r / (np.linalg.norm(g) * np.linalg.norm(r))))
+        cur = out
+    ok = ids_equal and worst_rel <= 1e-2 and worst_cos >= 0.9999
+    return {"layers": 2, "tokens": T, "routed_ids_equal": ids_equal, "max_rel_l2": round(worst_rel, 6),
+            "min_cosine": round(worst_cos, 8), "bar": "ids exact, rel L2 <= 1e-2, cos >= 0.9999", "ok": ok}
 
 
 def bench_copy(args) -> int:
@@ -177,20 +213,139 @@ def bench_lm_head(args) -> int:
     return 0
 
 
-def bench_decode(args) -> int:
+def _proj_bytes(p) -> int:
+    return p.weight.numel() * 4 + p.scales.numel() * 2 + p.biases.numel() * 2
+
+
+def _moe_fixed_bytes(moe) -> int:
+    """Router, shared expert and its gate of one MoE layer (bytes read per call)."""
+    k = moe._keep
+    return sum(_proj_bytes(q) for q in (k[0], k[4], k[5], k[6], k[7]) if q is not None)
+
+
+def _trace_moe_calls(fn):
+    """Runs fn() with every MoE layer call recording its routed ids; returns
+    {layer object id: [distinct experts per call]}."""
+    import torch
+    from vates_amd.moe import MoELayer
+    seen = {}
+    orig = MoELayer.__call__
+
+    def traced(self, x, residual=None, *, out=None, ids_out=None, scores_out=None, stream=None, ws=None):
+        T = x.numel() // self.hidden
+        ids = ids_out if ids_out is not None else torch.empty((T, self.top_k), dtype=torch.int32, device=x.device)
+        y = orig(self, x, residual, out=out, ids_out=ids, scores_out=scores_out, stream=stream, ws=ws)
+        seen.setdefault(id(self), []).append(ids)
+        return y
+
+    MoELayer.__call__ = traced
+    try:
+        fn()
+    finally:
+        MoELayer.__call__ = orig
+    torch.cuda.synchronize()
+    return {k: [int(np.unique(i.cpu().numpy()).size) for i in v] for k, v in seen.items()}
+
+
+def decode_step_bytes(model, K: int, L: int, U: dict) -> dict:
+    """Algorithmic HBM bytes of one speculative step in the [x, d1..dK] layout
+    at context L: the verify forward (T = K + 1), K MTP draft steps (T = 1)
+    and the MTP update (T = K + 1).  Weights are read once per call, caches
+    as the kernels read them; U: distinct experts per MoE call, traced."""
+    T = K + 1
+    H = model.hidden
+    V = model.head.shape[0]
+    head = V * H * 2
+    items = {"verify_attention": 0, "verify_gdn": 0, "verify_moe": 0, "verify_head": head, "mtp_drafts": 0,
+             "mtp_update": 0}
+    for layer in model.layers:
+        if layer.attn is not None:
+            a = layer.attn
+            kv_read = 2 * a.n_kv * L * 256 * 2
+            items["verify_attention"] += sum(_proj_bytes(q) for q in a._keep[:4]) + kv_read + 2 * a.n_kv * T * 512
+        elif layer.gdn is not None:
+            g = layer.gdn
+            state = g.n_v * 128 * 128 * 4
+            conv = g._keep[4].numel() * 2
+            items["verify_gdn"] += sum(_proj_bytes(q) for q in g._keep[:3]) + conv + state + T * state
+        u = U[id(layer.moe)][0]
+        items["verify_moe"] += u * EXPERT_BYTES + _moe_fixed_bytes(layer.moe)
+    w = model.mtp.w
+    att = sum(_proj_bytes(q) for q in w.attn._keep[:4])
+    kv = 2 * w.attn.n_kv * L * 256 * 2
+    mtp_u = U[id(w.moe)]  # K draft calls (T = 1), then the update (T = K + 1)
+    for i in range(K):
+        items["mtp_drafts"] += _proj_bytes(w.fc) + att + kv + mtp_u[i] * EXPERT_BYTES + _moe_fixed_bytes(w.moe) + head
+    items["mtp_update"] = _proj_bytes(w.fc) + att + kv + mtp_u[K] * EXPERT_BYTES + _moe_fixed_bytes(w.moe)
+    items["total"] = sum(items.values())
+    return items
+
+
+def decode_cpu_baseline(model, ctx: int, budget_s: float, threads: int) -> dict:
+    """Greedy decoding cost per token of the oracle (float64, OpenMP) on the
+    host: one full-attention block at a ctx-token context, one Gated DeltaNet
+    block, one MoE layer and the head, each at T = 1, timed and weighted by the
+    model's layer counts.  Weights of those blocks copied to the host; the
+    context's keys and values are synthetic (their values do not change the
+    cost)."""
+    import torch
+    from oracle import oracle as orc
+    from oracle.torch_bridge import u16
+    sys.path.insert(0, str(ROOT / "tests"))
+    from model_oracle import attn_dict, gdn_dict, moe_dict
+
+    la = next(l for l in model.layers if l.attn is not None)
+    lg = next(l for l in model.layers if l.gdn is not None)
+    A, G, L = attn_dict(la.attn), gdn_dict(lg.gdn), moe_dict(la.moe)
+    W, nw = u16(model.head), u16(model.final_norm)
+    rng = np.random.default_rng(0)
+    x = orc.f32_to_bf16(rng.standard_normal((1, model.hidden)).astype(np.float32))
+    kc = orc.f32_to_bf16(rng.standard_normal((la.attn.n_kv, ctx + 32, 256)).astype(np.float32))
+    cd = 2 * G["n_k"] * 128 + G["n_v"] * 128
+    conv_in = rng.standard_normal((3, cd)) * 0.1
+    state_in = rng.standard_normal((G["n_v"], 128, 128)) * 0.01
+    calls = {"attention": lambda: orc.attention_layer(x, A, ctx, kc, kc),
+             "gdn": lambda: orc.gdn_layer(x, G, conv_in=conv_in, state_in=state_in),
+             "moe": lambda: orc.moe_layer(x, L, residual=True),
+             "head": lambda: orc.lm_head(x, nw, 1e-6, W)}
+    prev = orc.set_threads(threads if threads > 0 else len(os.sched_getaffinity(0)))
+    per = {}
+    t_all = time.perf_counter()
+    try:
+        for name, fn in calls.items():
+            n, t0 = 0, time.perf_counter()
+            while n == 0 or time.perf_counter() - t0 < budget_s / len(calls):
+                fn()
+                n += 1
+            per[name] = (time.perf_counter() - t0) / n
+    finally:
+        orc.set_threads(prev)
+    n_att = sum(l.attn is not None for l in model.layers)
+    n_gdn = sum(l.gdn is not None for l in model.layers)
+    sec = n_att * per["attention"] + n_gdn * per["gdn"] + len(model.layers) * per["moe"] + per["head"]
+    return {"value": round(1.0 / sec, 4), "unit": "tokens/s", "cores": _threads_label(threads), "kind": "port",
+            "sample": f"oracle greedy decode cost per token at T=1, context {ctx}: attention "
+                      f"{per['attention'] * 1e3:.1f} ms x {n_att}, Gated DeltaNet {per['gdn'] * 1e3:.1f} ms x {n_gdn}, "
+                      f"MoE {per['moe'] * 1e3:.1f} ms x {len(model.layers)}, head {per['head'] * 1e3:.1f} ms "
+                      f"({time.perf_counter() - t_all:.1f} s timed), float64 with OpenMP"}
+
+
+def decode_record(args) -> dict:
     """K-draft MTP speculative decoding of a random-init Qwen3-Next-shaped model:
     `layers` decoder layers (full attention on every attn_every-th, Gated
     DeltaNet linear attention on the others, the 512-expert top-10 4-bit MoE
-    with the shared expert on all), the MTP layer, bf16
-    embedding and head over 151,936 tokens.  The attention and MTP caches hold a
-    `context`-token synthetic prompt (random bf16 keys and values: decode speed
-    does not depend on their content).  Timed: `new_tokens` decoded tokens, wall
-    clock, including drafting, verification, acceptance, commit and the MTP
-    cache update.  Then the same start state is decoded greedily without
-    speculation and the two token streams are compared."""
+    with the shared expert on all), the MTP layer, bf16 embedding and head over
+    151,936 tokens.  The attention and MTP caches hold a `context`-token
+    synthetic context (random bf16 keys and values: decode speed does not
+    depend on their content).  Timed: `new_tokens` decoded tokens by graph
+    replays, wall clock, including drafting, verification, acceptance, commit
+    and the MTP cache update.  The same start state is then decoded greedily
+    (one token per graph replay, the like-for-like baseline) and the two token
+    streams are compared; drafts planted at a fixed agreement rate show the
+    acceptance-dependent speed."""
     import torch
     from vates_amd.attention import KVCache
-    from vates_amd.decode import GraphSpecDecoder, greedy_decode, speculative_decode
+    from vates_amd.decode import GraphGreedyDecoder, GraphSpecDecoder, speculative_decode
     from vates_amd.mtp import MTPDrafter
     from vates_amd.synth import synth_bf16
     from vates_amd.workload import synth_spec_model
@@ -202,14 +357,13 @@ def bench_decode(args) -> int:
                              inter=args.inter, num_experts=args.experts, top_k=args.top_k, vocab=args.vocab,
                              device=dev)
     ctx, N, K = args.context, args.new_tokens, args.K
-    max_len = ctx + N + 2 * K + 8
+    max_len = ctx + 2 * N + 4 * (K + 1) + 8
     caches = model.new_caches(max_len)
     drafter = MTPDrafter(model.mtp, max_len)
     for i, c in enumerate(caches + [drafter.cache]):
-        if not isinstance(c, KVCache):
-            continue  # linear-attention states start from zero: their cost does not depend on content
-        c.write(0, synth_bf16(SEED, 0xCA000 + 2 * i, (c.k.shape[0], ctx, 256), device=dev),
-                synth_bf16(SEED, 0xCA001 + 2 * i, (c.v.shape[0], ctx, 256), device=dev))
+        if isinstance(c, KVCache):
+            c.write(0, synth_bf16(SEED, 0xCA000 + 2 * i, (c.k.shape[0], ctx, 256), device=dev),
+                    synth_bf16(SEED, 0xCA001 + 2 * i, (c.v.shape[0], ctx, 256), device=dev))
     x0 = torch.tensor([4242], dtype=torch.int32, device=dev)
     h0 = synth_bf16(SEED, 0xCA0FF, (1, args.hidden), device=dev)
     torch.cuda.synchronize()
@@ -225,38 +379,42 @@ def bench_decode(args) -> int:
                 c.length = ctx
         drafter.cache.length = ctx - 1
 
-    def graph_run(planted=None):
+    # distinct experts of every MoE call of one step, traced on an eager step
+    reset()
+    U = _trace_moe_calls(lambda: speculative_decode(model, drafter, caches, x0, h0, ctx, 1, K=K))
+    step_bytes = decode_step_bytes(model, K, ctx + K + 1, U)
+
+    def graph_spec(planted=None, **kw):
         reset()
-        dec = GraphSpecDecoder(model, drafter, caches, K=K, planted=planted is not None)
+        dec = GraphSpecDecoder(model, drafter, caches, K=K, planted=planted is not None, **kw)
         dec.start(x0, h0, ctx)
         dec.capture()
         if args.warmup:
-            dec.run(args.warmup * (K + 1), plant=planted)  # warm-up replays
+            dec.run(args.warmup * (K + 1), plant=planted)
             reset()
             dec.start(x0, h0, ctx)
         torch.cuda.synchronize()
         return dec.run(N, plant=planted)
 
-    if args.eager:
-        reset()
-        speculative_decode(model, drafter, caches, x0, h0, ctx, max(args.warmup, 1) * (K + 1), K=K)  # warm-up
-        reset()
-        torch.cuda.synchronize()
-        st = speculative_decode(model, drafter, caches, x0, h0, ctx, N, K=K)
-    else:
-        st = graph_run()
-    torch.cuda.synchronize()
+    st = graph_spec()
     tps = N / st.seconds
-    eprint(f"[bench] decode ({'eager' if args.eager else 'graph'}): {N} tokens in {st.seconds:.3f} s = "
-           f"{tps:.1f} tokens/s, {st.steps} steps, avg accept len {st.avg_accept_len:.2f}")
+    ms_step = st.seconds * 1e3 / st.steps
+    eprint(f"[bench] decode (graph, MTP drafts): {N} tokens in {st.seconds:.3f} s = {tps:.1f} tokens/s, "
+           f"{st.steps} steps, {ms_step:.3f} ms per step, avg accept len {st.avg_accept_len:.2f}")
     reset()
-    gr = greedy_decode(model, caches, x0, ctx, N + 2 * (K + 1))
+    gd = GraphGreedyDecoder(model, caches, N + 4 * (K + 1))
+    gd.start(x0, ctx)
+    gd.capture()
+    if args.warmup:
+        gd.run(args.warmup)
+        reset()
+        gd.start(x0, ctx)
+    gr = gd.run(N + 2 * (K + 1))
     truth = gr.tokens
     gr_tps = len(truth) / gr.seconds
     same = truth[:N] == st.tokens
     first_diff = next((i for i, (a, b) in enumerate(zip(truth, st.tokens)) if a != b), None)
-    eprint(f"[bench] greedy (non-speculative, eager): {gr_tps:.1f} tokens/s; speculative == greedy: {same}")
-    # drafts that agree with the greedy stream with probability plant_rate per position
+    eprint(f"[bench] greedy (graph, one token per replay): {gr_tps:.1f} tokens/s; speculative == greedy: {same}")
     rng = np.random.default_rng(SEED)
 
     def plant(step, pos):
@@ -264,32 +422,57 @@ def bench_decode(args) -> int:
         return [truth[base + i] if rng.random() < args.plant_rate else (truth[base + i] + 1) % args.vocab
                 for i in range(K)]
 
-    sp = graph_run(plant)
+    sp = graph_spec(plant)
     sp_tps = N / sp.seconds
     sp_same = sp.tokens == truth[:N]
     eprint(f"[bench] decode (graph, drafts planted at agreement {args.plant_rate}): {sp_tps:.1f} tokens/s, "
            f"avg accept len {sp.avg_accept_len:.2f}, equals greedy: {sp_same}")
+    ad = graph_spec(layout="k", tau=args.tau)
+    ad_tps = N / ad.seconds
+    ad_same = ad.tokens == truth[:N]
+    eprint(f"[bench] decode (graph, adaptive depth tau={args.tau}, T=K layout): {ad_tps:.1f} tokens/s, "
+           f"depths {[ad.depths.count(d) for d in range(1, K + 1)]}, equals greedy: {ad_same}")
     hist = [st.accept_hist.count(m) for m in range(K + 1)]
-    line = {
+    achieved = step_bytes["total"] / (ms_step * 1e-3) / 1e9
+    cpu = cpu1 = None
+    if args.cpu_baseline_s > 0:
+        cpu = decode_cpu_baseline(model, ctx, args.cpu_baseline_s * 0.6, 0)
+        cpu1 = decode_cpu_baseline(model, ctx, 1.0, 1)
+        eprint(f"[bench] decode oracle on the host: {cpu['value']} tokens/s ({cpu['cores']} cores), "
+               f"{cpu1['value']} tokens/s (1 core)")
+    del model, caches, drafter
+    torch.cuda.empty_cache()
+    return {
         "metric": "K=3 MTP decode tokens/s", "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,
-        "steps": st.steps, "warmup": args.warmup, "ms_per_step": round(st.seconds * 1e3 / st.steps, 4),
+        "steps": st.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "u4 experts/projections, bf16 head and KV, f32 accumulate", "data": "synthetic",
         "config": {"workload": f"{args.layers}-layer random-init Qwen3-Next-shaped model ({args.layers // args.attn_every}"
                                f" full-attention and {args.layers - args.layers // args.attn_every} Gated DeltaNet "
                                f"layers, every layer MoE 512x top-{args.top_k} + shared expert), MTP K={K}, "
-                               f"{N} new tokens after a {ctx}-token "
-                               f"synthetic context, vocab {args.vocab}",
-                   "step": "eager launches" if args.eager else "one HIP graph replay per step",
+                               f"{N} new tokens after a {ctx}-token synthetic context, vocab {args.vocab}",
+                   "step": "one HIP graph replay per step, verify [x, d1..dK]",
                    "accept_hist": hist, "avg_accept_len": round(st.avg_accept_len, 3),
                    "speculative_equals_greedy": same, "first_divergence": first_diff,
-                   "greedy_tokens_per_s": round(gr_tps, 2),
+                   "greedy_graph_tokens_per_s": round(gr_tps, 2),
                    "planted_agreement": args.plant_rate, "planted_tokens_per_s": round(sp_tps, 2),
-                   "planted_avg_accept_len": round(sp.avg_accept_len, 3), "planted_equals_greedy": sp_same},
-        "roofline": None, "cpu_baseline": None,
+                   "planted_avg_accept_len": round(sp.avg_accept_len, 3), "planted_equals_greedy": sp_same,
+                   "adaptive_tau": args.tau, "adaptive_tokens_per_s": round(ad_tps, 2),
+                   "adaptive_depths": [ad.depths.count(d) for d in range(1, K + 1)],
+                   "adaptive_equals_greedy": ad_same},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit_of_work": "one speculative step (K MTP drafts, verify of K+1 tokens, MTP update)",
+                     "bytes_per_step": {k: int(v) for k, v in step_bytes.items()},
+                     "us_per_step": round(ms_step * 1e3, 2)},
+        "cpu_baseline": cpu, "cpu_baseline_1core": cpu1,
     }
+
+
+def bench_decode(args) -> int:
+    line = decode_record(args)
     print(json.dumps(line), flush=True)
-    return 0
+    return 0 if line["config"]["speculative_equals_greedy"] else 3
 
 
 PEAK_MFMA_TFLOPS = 2500.0  # dense fp16/bf16
@@ -401,6 +584,8 @@ def main() -> int:
     ap.add_argument("--new-tokens", type=int, default=512)
     ap.add_argument("--K", type=int, default=3)
     ap.add_argument("--attn-every", type=int, default=4)
+    ap.add_argument("--tau", type=float, default=0.3, help="decode: adaptive-depth confidence threshold")
+    ap.add_argument("--no-decode", action="store_true", help="default path: skip the decode record")
     ap.add_argument("--vocab", type=int, default=151936)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -499,10 +684,20 @@ def main() -> int:
         eprint(f"[bench] device status flags {status:#x}")
         return 3
 
-    cpu = None
+    parity = moe_parity(layers, ws_list, x_bank[0], args)
+    eprint(f"[bench] first two layers against the oracle: {parity}")
+    cpu = cpu1 = None
     if args.cpu_baseline_s > 0:
-        cpu = cpu_baseline(ws_list, x_bank[: args.steps].view(torch.int16).cpu().numpy().view(np.uint16), args,
-                           args.cpu_baseline_s)
+        xs_host = x_bank[: args.steps].view(torch.int16).cpu().numpy().view(np.uint16)
+        cpu = cpu_baseline(ws_list, xs_host, args, args.cpu_baseline_s)
+        cpu1 = cpu_baseline(ws_list, xs_host, args, max(2.0, args.cpu_baseline_s / 3), threads=1)
+        eprint(f"[bench] oracle on the host: {cpu['value']} GB/s ({cpu['cores']} cores), {cpu1['value']} GB/s (1 core)")
+    hip_graph = graph is not None
+    decode = None
+    if not args.no_decode and args.layers == 48 and args.hidden == 2048:
+        del layers, ws_list, graph, run
+        torch.cuda.empty_cache()
+        decode = decode_record(args)
 
     line = {
         "metric": METRIC,
@@ -523,7 +718,7 @@ def main() -> int:
                         f"Zipf(1.1) routing bias, {args.steps} steps",
             "layers": args.layers, "T": T, "top_k": k, "experts": args.experts, "hidden": H, "inter": args.inter,
             "distinct_experts_per_layer": round(float(U.mean()), 2),
-            "hip_graph": graph is not None,
+            "hip_graph": hip_graph,
         },
         "roofline": {
             "bound": "hbm",
@@ -531,16 +726,19 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(per_layer_bytes / (per_layer_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": round(MOE_TRAFFIC_PER_ALGO_BYTE * per_layer_bytes) if args.hidden == 2048 and T == 4 else None,
+            "traffic": MOE_TRAFFIC_BYTES if args.hidden == 2048 and T == 4 else None,
             "traffic_source": MOE_TRAFFIC_SOURCE if args.hidden == 2048 and T == 4 else None,
             "unit_of_work": "one MoE layer call (router+topk, gate/up, down+combine kernels)",
             "bytes_per_launch": round(per_layer_bytes),
             "us_per_launch": round(per_layer_us, 3),
         },
         "cpu_baseline": cpu,
+        "cpu_baseline_1core": cpu1,
+        "parity": parity,
+        "decode": decode,
     }
     print(json.dumps(line), flush=True)
-    return 0
+    return 0 if parity["ok"] and (decode is None or decode["config"]["speculative_equals_greedy"]) else 3
 
 
 if __name__ == "__main__":

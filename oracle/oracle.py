@@ -389,3 +389,11 @@ def attention_layer(x, A: dict, pos0: int, k_cache, v_cache):
          "attention_layer")
     return out, kn, vn
 
+
+def set_threads(n: int) -> int:
+    """Threads of the oracle's OpenMP loops; returns the previous setting."""
+    fn = lib().orc_set_threads
+    fn.argtypes = [c_int]
+    fn.restype = c_int
+    return fn(int(n))
+

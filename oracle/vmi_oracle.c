@@ -28,6 +28,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <math.h>
+#include <omp.h>
 
 #define ORC_OK 0
 #define ORC_EINVAL -1
@@ -1136,3 +1137,12 @@ int orc_accept_stochastic(const float* target, const float* draft, const int32_t
 }
 
 int orc_version(void) { return 1; }
+
+/* Threads of the oracle's parallel loops (the CPU baseline is timed on all
+ * cores and on one); returns the previous setting. */
+int orc_set_threads(int n) {
+    const int prev = omp_get_max_threads();
+    if (n > 0) omp_set_num_threads(n);
+    return prev;
+}
+

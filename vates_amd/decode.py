@@ -505,3 +505,76 @@ class GraphSpecDecoder:
                 c.length = pos
         self.drafter.cache.length = mtp_len
         return st
+
+
+class GraphGreedyDecoder:
+    """Non-speculative greedy decoding (one token per forward) captured as a
+    HIP graph: one replay runs the forward of the last token at the position
+    held on the device, writes its argmax as the next input and into the
+    token log at the step index, and advances the position and the index.
+    Replays need no host synchronisation; the host reads the log at the end.
+    The like-for-like baseline of ``GraphSpecDecoder``."""
+
+    def __init__(self, model: SpecModel, caches: list, max_tokens: int):
+        self.model, self.caches = model, caches
+        dev = model.embed.device
+        self.dev = dev
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.x = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.idx = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.log = torch.zeros(max_tokens, dtype=torch.int32, device=dev)
+        self.one_i32 = torch.ones(1, dtype=torch.int32, device=dev)
+        self.one_i64 = torch.ones(1, dtype=torch.int64, device=dev)
+        self.stream = torch.cuda.Stream(device=dev)
+        self.graph = None
+
+    def _step(self) -> None:
+        am, _, _ = self.model.forward(self.x, self.caches, 0, pos_device=self.pos)
+        self.x.copy_(am)
+        self.log.index_copy_(0, self.idx, am)
+        self.pos.add_(self.one_i32)
+        self.idx.add_(self.one_i64)
+
+    def start(self, x: torch.Tensor, pos: int) -> None:
+        self.x.copy_(x)
+        self.pos.fill_(pos)
+        self.idx.zero_()
+        self.pos_host = pos
+
+    def capture(self) -> None:
+        live = (self.x, self.pos, self.idx)
+        saved = [t.clone() for t in live]
+        self.stream.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(self.stream):
+            self._step()
+            for t, v in zip(live, saved):
+                t.copy_(v)
+        self.stream.synchronize()
+        torch.cuda.synchronize(self.dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            self._step()
+        torch.cuda.synchronize(self.dev)
+
+    def run(self, n_tokens: int) -> DecodeStats:
+        if self.graph is None:
+            self.capture()
+        if n_tokens > self.log.numel():
+            raise VmiError(f"the token log holds {self.log.numel()} tokens")
+        for c in self.caches:
+            if isinstance(c, KVCache) and self.pos_host + n_tokens > c.max_len:
+                raise VmiError(f"cache capacity {c.max_len} < {self.pos_host + n_tokens} positions needed")
+        st = DecodeStats()
+        torch.cuda.synchronize(self.dev)
+        t0 = time.perf_counter()
+        for _ in range(n_tokens):
+            self.graph.replay()
+        torch.cuda.synchronize(self.dev)
+        st.seconds = time.perf_counter() - t0
+        st.tokens = self.log[:n_tokens].cpu().tolist()
+        st.steps = n_tokens
+        self.pos_host += n_tokens
+        for c in self.caches:
+            if c is not None:
+                c.length = self.pos_host
+        return st
