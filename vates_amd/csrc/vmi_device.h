@@ -11,6 +11,25 @@ typedef uint32_t vmi_u4 __attribute__((ext_vector_type(4)));
 
 #define VMI_WAVE 64
 
+// Timeline stamps for tuning builds only (compiled with -DVMI_TIMELINE): the
+// first thread of a workgroup records the 100 MHz real-time counter at point
+// `slot` of kernel `kid` into the buffer set by vmi_timeline_set() (one per
+// translation unit), laid out [kid][workgroup < 4096][slot < 16].  The product
+// build compiles these to nothing.
+#ifdef VMI_TIMELINE
+#define VMI_TL_DECL static __device__ unsigned long long* vmi_tl_buf = nullptr;
+#define VMI_STAMP(kid, slot)                                                                       \
+    do {                                                                                           \
+        if (threadIdx.x == 0 && vmi_tl_buf && blockIdx.x < 4096)                                   \
+            vmi_tl_buf[((size_t)(kid) * 4096 + blockIdx.x) * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define VMI_TL_DECL
+#define VMI_STAMP(kid, slot) \
+    do {                     \
+    } while (0)
+#endif
+
 __device__ __forceinline__ float vmi_bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
 // Round-to-nearest-even fp32 -> bf16 bit pattern (quiet NaN kept).

@@ -36,6 +36,8 @@
 #include "vmi_device.h"
 #include "vmi_internal.h"
 
+VMI_TL_DECL
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -314,6 +316,7 @@ __device__ __forceinline__ void operands_from_wave(const uint4 (&xr)[NCH], int H
 template <int CPL>
 __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     constexpr int NCH = CPL / 8;  // packed 8-column chunks per lane
+    VMI_STAMP(0, 0);
     const int lane = threadIdx.x & 63, w = vmi_wave_id();
     const int T = a.T, H = a.H;
     const int G = H / 64;
@@ -418,6 +421,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
             a.logits[(size_t)t * a.E + row] = lv;
         }
     }
+    VMI_STAMP(0, 1);
 }
 
 // ----------------------------------------------------------- routing
@@ -653,6 +657,7 @@ __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, 
     if (!a.from_slots) {
         route_topk_dispatch(a.logits, T, a.E, k, a.norm, a.table, s_table, R);
         __syncthreads();
+        VMI_STAMP(1, 1);
         if (tid < npairs) {
             const int id = R.ids[tid];
             int sl = (id >= 0 && id < a.E) ? (a.table ? s_table[id] : id) : -1;
@@ -674,6 +679,7 @@ __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, 
     }
     __syncthreads();
     dedup_lds(npairs, k, a.cap, R, s_first);
+    VMI_STAMP(1, 2);
 }
 
 // The route table for k_down_rows, the caller's ids/scores and the status
@@ -732,6 +738,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     const int item = blockIdx.x;
     const bool is_shared = item < nsh;
     const vmi_u4 zero4 = {0u, 0u, 0u, 0u};
+    VMI_STAMP(1, 0);
 
     // the MoE input operands do not depend on the routing: issued before it,
     // so their latency overlaps the router logits'
@@ -908,6 +915,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
             }
         }
     }
+    VMI_STAMP(1, 3);
     // affine-bias term: lane block q carries groups 2*NB*q + 2b, +1
     vmi_f4 bgd = zf, bud = zf;
 #pragma unroll
@@ -965,6 +973,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
             if (kk == 0) a.axs[((size_t)aidx * T + t) * NGd + c] = xs;
         }
     }
+    VMI_STAMP(1, 4);
 }
 
 // --------------------------------------------------------- down + combine
@@ -1053,6 +1062,7 @@ __global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
     const int npass = (T + 7) / 8;
     const int NEmax = hs + a.npairs;
     const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
+    VMI_STAMP(2, 0);
 
     // activation operands of the wave's expert i (list position e), tokens
     // tb..tb+tpass-1: lane l holds word l (+64c) of each token row
@@ -1101,6 +1111,7 @@ __global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
     for (int i = tid; i < 1024 / 4; i += kDnThreads) reinterpret_cast<uint32_t*>(s_zero)[i] = 0u;
     const int NE = hs + U;
     __syncthreads();
+    VMI_STAMP(2, 1);
 
     for (int c0 = 0; c0 < NE; c0 += CAP) {
         const int nc = min(CAP, NE - c0);
@@ -1259,6 +1270,7 @@ __global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
         else
             reinterpret_cast<float*>(a.out)[o] = acc;
     }
+    VMI_STAMP(2, 2);
 }
 
 // --------------------------------------------------------------- prep (slots API)
@@ -1577,6 +1589,13 @@ extern "C" int vmi_moe_layer_noalloc(const vmi_moe_layer_desc* desc, const uint1
     if (status) ws.status = status;
     return launch_moe_layer(D, x, T, residual, out, ids_out, scores_out, ws, static_cast<hipStream_t>(stream));
 }
+
+#ifdef VMI_TIMELINE
+// Tuning builds only: where the kernels of this file record their stamps.
+extern "C" int vmi_timeline_set(void* buf) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(vmi_tl_buf), &buf, sizeof(buf)) == hipSuccess ? VMI_OK : VMI_ERR_HIP;
+}
+#endif
 
 extern "C" int vmi_workspace_status(void* workspace, void* stream, uint32_t* flags) {
     vmi::clear_error();
