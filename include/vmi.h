@@ -84,6 +84,21 @@ int vmi_fused_moe_slots(const void* x, int x_dtype, const int32_t* local_slots, 
                         void* stream);
 
 /* ------------------------------------------------------------------------
+ * vmi_fused_moe_staged -- replaces fused_moe_staged, the slot-less sibling
+ *   native/ext/compute/fused_moe.h:11-16 (declaration),
+ *   native/ext/compute/fused_moe.cpp:443-504, 605-633 (primitive + factory),
+ *   native/ext/bindings.cpp:31-50 (Python binding).
+ * The weight stacks hold one pre-sliced matrix per (token, rank) pair: pair
+ * p = t*k + j reads matrix p (gate/up [T*k, inter, hidden], down
+ * [T*k, hidden, inter]); otherwise as vmi_fused_moe_slots with
+ * local_slots[p] = p, including the workspace
+ * (vmi_fused_moe_slots_workspace_bytes).
+ * ------------------------------------------------------------------------ */
+int vmi_fused_moe_staged(const void* x, int x_dtype, const float* scores, vmi_qmat gate, vmi_qmat up,
+                         vmi_qmat down, int T, int k, int hidden, int inter, int group, int bits, void* out,
+                         int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * vmi_moe_layer -- one full routed-MoE layer on a verify batch; replaces the
  * production branch of FileStreamingMoeBlock.__call__
  *   mlx_streaming/core/moe/block.py:245-1013 (router :251-253, softmax/top-k/

@@ -108,6 +108,38 @@ def test_fused_moe_slots_parity(gpu, orc, torch_mod, H, I, xdt):
         assert_moe_close(out.cpu().numpy(), ref, f"slots H={H} I={I} {xdt} T={T}")
 
 
+@pytest.mark.parametrize("H,I,T", [(2048, 512, 4), (512, 128, 3)])
+def test_fused_moe_staged_equals_identity_slots(gpu, orc, torch_mod, H, I, T):
+    """fused_moe_staged (fused_moe.cpp:443-504, 605-633): pair t*k + j reads
+    matrix t*k + j of the pre-sliced stacks.  Bit-identical to
+    fused_moe_slots with local_slots = 0..T*k-1 on the same stacks, and within
+    the MoE bar of the oracle."""
+    torch = torch_mod
+    from vates_amd import fused_moe_slots, fused_moe_staged
+    from vates_amd.synth import synth_proj
+    k = 10
+    n = T * k
+    log(f"case: fused_moe_staged H={H} I={I} T={T}")
+    gate = synth_proj(41, 1, n, I, H, device=gpu)
+    up = synth_proj(41, 2, n, I, H, device=gpu)
+    down = synth_proj(41, 3, n, H, I, device=gpu)
+    rng = np.random.default_rng(H + T)
+    scores = rng.random((T, k)).astype(np.float32)
+    scores /= scores.sum(1, keepdims=True)
+    x = rng.normal(size=(T, H)).astype(np.float32)
+    xt, st = torch.from_numpy(x).to(gpu), torch.from_numpy(scores).to(gpu)
+    w = (gate.weight, gate.scales, gate.biases, up.weight, up.scales, up.biases, down.weight, down.scales,
+         down.biases)
+    staged = fused_moe_staged(xt, st, *w, H, I, 64, 4)
+    ident = torch.arange(n, dtype=torch.int32, device=gpu).view(T, k)
+    slots = fused_moe_slots(xt, ident, st, *w, H, I, 64, 4)
+    torch.cuda.synchronize()
+    assert torch.equal(staged.view(torch.int32), slots.view(torch.int32))
+    ref = orc.fused_moe_slots(x, np.arange(n, dtype=np.int32).reshape(T, k), scores, pool_np(gate, up, down), T, k,
+                              H, I, n)
+    assert_moe_close(staged.cpu().numpy(), ref, f"staged H={H} I={I} T={T}")
+
+
 def test_fused_moe_slots_slot_pool_fixture(gpu, orc, torch_mod):
     """The reference's slot-pool known answer (test_native_moe_ext.py:50-72):
     a 4-slot pool acquiring experts [1, 2, 1] gives local slots [0, 1, 0], then

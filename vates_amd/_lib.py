@@ -68,6 +68,8 @@ _SIGNATURES = {
     "vmi_fused_moe_slots_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "vmi_fused_moe_slots": (c_int, [c_void_p, c_int, c_void_p, c_void_p, QMat, QMat, QMat, c_int, c_int, c_int,
                                     c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    "vmi_fused_moe_staged": (c_int, [c_void_p, c_int, c_void_p, QMat, QMat, QMat, c_int, c_int, c_int, c_int, c_int,
+                                     c_int, c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
     "vmi_moe_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "vmi_moe_layer": (c_int, [POINTER(MoeLayerDesc), c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_size_t, c_void_p]),

@@ -635,7 +635,7 @@ struct GateUpArgs {
     int norm, cap;
     const float* logits;          // [T, E]
     const int32_t* table;         // [E] or nullptr
-    const int32_t* slots;         // [T*k] (from_slots)
+    const int32_t* slots;         // [T*k] (from_slots), or nullptr: pair p uses matrix p
     const float* in_scores;       // [T*k] (from_slots)
     vmi_qmat gate, up, sh_gate, sh_up;
     const vmi_u4* xop;            // [T, H/8]
@@ -670,7 +670,7 @@ __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, 
     } else {
         __syncthreads();
         if (tid < npairs) {
-            const int s = a.slots[tid];
+            const int s = a.slots ? a.slots[tid] : tid;  // no slot list: pair p uses matrix p
             const bool ok = s >= 0 && s < a.cap;
             R.slot[tid] = ok ? s : -1;
             R.scores[tid] = a.in_scores[tid];
@@ -1393,14 +1393,19 @@ extern "C" size_t vmi_moe_layer_workspace_bytes(int T, int top_k, int hidden, in
     return vmi::carve_workspace(nullptr, T, top_k, hidden, inter, num_experts).bytes;
 }
 
-extern "C" int vmi_fused_moe_slots(const void* x, int x_dtype, const int32_t* local_slots, const float* scores,
-                                   vmi_qmat gate, vmi_qmat up, vmi_qmat down, int T, int k, int hidden, int inter,
-                                   int group, int bits, int cap, void* out, int out_dtype, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
+namespace {
+
+// vmi_fused_moe_slots with a slot list, or vmi_fused_moe_staged without one
+// (pair p reads matrix p of stacks holding T*k matrices).
+int fused_moe_pairs(const void* x, int x_dtype, bool staged, const int32_t* local_slots, const float* scores,
+                    vmi_qmat gate, vmi_qmat up, vmi_qmat down, int T, int k, int hidden, int inter, int group,
+                    int bits, int cap, void* out, int out_dtype, void* workspace, size_t workspace_bytes,
+                    void* stream) {
     vmi::clear_error();
     int rc = check_shape(T, k, hidden, inter, group, bits);
     if (rc) return rc;
-    if (!x || !local_slots || !scores || !out) return vmi::fail(VMI_ERR_INVALID, "null x/local_slots/scores/out");
+    if (!x || !scores || !out) return vmi::fail(VMI_ERR_INVALID, "null x/scores/out");
+    if (!staged && !local_slots) return vmi::fail(VMI_ERR_INVALID, "null local_slots");
     if (x_dtype != VMI_F32 && x_dtype != VMI_BF16) return vmi::fail(VMI_ERR_INVALID, "x_dtype=%d", x_dtype);
     if (out_dtype != VMI_F32 && out_dtype != VMI_BF16) return vmi::fail(VMI_ERR_INVALID, "out_dtype=%d", out_dtype);
     if (!aligned(x, 16)) return vmi::fail(VMI_ERR_INVALID, "x must be 16-byte aligned");
@@ -1440,6 +1445,23 @@ extern "C" int vmi_fused_moe_slots(const void* x, int x_dtype, const int32_t* lo
     e = launch_down(da, s);
     if (e != hipSuccess) return vmi::hip_fail(e, "k_down_rows launch");
     return VMI_OK;
+}
+
+}  // namespace
+
+extern "C" int vmi_fused_moe_slots(const void* x, int x_dtype, const int32_t* local_slots, const float* scores,
+                                   vmi_qmat gate, vmi_qmat up, vmi_qmat down, int T, int k, int hidden, int inter,
+                                   int group, int bits, int cap, void* out, int out_dtype, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    return fused_moe_pairs(x, x_dtype, false, local_slots, scores, gate, up, down, T, k, hidden, inter, group, bits, cap, out,
+                           out_dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int vmi_fused_moe_staged(const void* x, int x_dtype, const float* scores, vmi_qmat gate, vmi_qmat up,
+                                    vmi_qmat down, int T, int k, int hidden, int inter, int group, int bits,
+                                    void* out, int out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    return fused_moe_pairs(x, x_dtype, true, nullptr, scores, gate, up, down, T, k, hidden, inter, group, bits, T * k, out,
+                           out_dtype, workspace, workspace_bytes, stream);
 }
 
 namespace {

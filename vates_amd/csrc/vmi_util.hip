@@ -3,6 +3,8 @@
 #include <stdio.h>
 
 #include "vmi_device.h"
+#include <atomic>
+
 #include "vmi_internal.h"
 
 namespace {
@@ -26,15 +28,18 @@ int hip_fail(hipError_t e, const char* what) {
 
 void clear_error() { g_err[0] = 0; }
 
-// Compute units of the current device (queried once per device).
+// Compute units of the current device, queried once per device.  The cache
+// entries are atomics: threads calling at once may each query, and all store
+// the same value, so the function is re-entrant without a lock.
 int device_cus() {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (cached[dev] > 0) return cached[dev];
+    const int known = cached[dev].load(std::memory_order_relaxed);
+    if (known > 0) return known;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
+    cached[dev].store(cus, std::memory_order_relaxed);
     return cus;
 }
 

@@ -79,6 +79,52 @@ class QuantizedProj:
         _require(self.biases, f"{name}.biases", 2, device)
 
 
+def _fused_moe_pairs(x: torch.Tensor, local_slots: Optional[torch.Tensor], scores: torch.Tensor, k: int,
+                     projs: list, hidden: int, inter: int, group: int, bits: int, stream,
+                     out_dtype: torch.dtype) -> torch.Tensor:
+    lib = load()
+    device = x.device
+    if x.shape[-1] != hidden:
+        raise VmiError(f"x last dim {x.shape[-1]} != hidden {hidden}")
+    T = x.numel() // hidden
+    if scores.numel() != T * k or (local_slots is not None and local_slots.numel() != T * k):
+        raise VmiError("shape mismatch: local_slots/scores must hold T*k entries")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise VmiError(f"x dtype {x.dtype} not supported (f32 or bf16)")
+    _require(x, "x", x.element_size(), device)
+    if local_slots is not None:
+        _require(local_slots, "local_slots", 4, device)
+    if scores.dtype != torch.float32:
+        raise VmiError("scores must be float32")
+    _require(scores, "scores", 4, device)
+    for name, p in zip(("gate", "up", "down"), projs):
+        p.check(name, device)
+    cap = projs[0].weight.shape[0]
+    if local_slots is None and cap < T * k:
+        raise VmiError(f"staged stacks hold {cap} matrices, the batch needs T*k = {T * k}")
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise VmiError("out_dtype must be float32 or bfloat16")
+    out = torch.empty(tuple(x.shape[:-1]) + (hidden,), dtype=out_dtype, device=device)
+    sh = _stream_handle(stream)
+    nbytes = lib.vmi_fused_moe_slots_workspace_bytes(T, k, hidden, inter)
+    ws = workspace(nbytes, device, sh)
+    xdt = _lib.VMI_BF16 if x.dtype == torch.bfloat16 else _lib.VMI_F32
+    odt = _lib.VMI_BF16 if out_dtype == torch.bfloat16 else _lib.VMI_F32
+    if local_slots is not None:
+        rc = lib.vmi_fused_moe_slots(x.data_ptr(), xdt, local_slots.data_ptr(), scores.data_ptr(),
+                                     projs[0].qmat(), projs[1].qmat(), projs[2].qmat(),
+                                     T, k, hidden, inter, group, bits, cap, out.data_ptr(), odt,
+                                     ws.data_ptr(), ws.numel(), sh)
+        check(rc, "vmi_fused_moe_slots")
+    else:
+        rc = lib.vmi_fused_moe_staged(x.data_ptr(), xdt, scores.data_ptr(),
+                                      projs[0].qmat(), projs[1].qmat(), projs[2].qmat(),
+                                      T, k, hidden, inter, group, bits, out.data_ptr(), odt,
+                                      ws.data_ptr(), ws.numel(), sh)
+        check(rc, "vmi_fused_moe_staged")
+    return out
+
+
 def fused_moe_slots(x: torch.Tensor, local_slots: torch.Tensor, scores: torch.Tensor,
                     gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b,
                     hidden: int, inter: int, group: int, bits: int, *, stream=None,
@@ -90,41 +136,23 @@ def fused_moe_slots(x: torch.Tensor, local_slots: torch.Tensor, scores: torch.Te
     pool arrays [cap, out, in*bits/32] / [cap, out, in/group].  Returns
     sum_j scores[..., j] * SwiGLU_expert_{slot}(x) as ``out_dtype``.
     """
-    lib = load()
-    device = x.device
-    if x.shape[-1] != hidden:
-        raise VmiError(f"x last dim {x.shape[-1]} != hidden {hidden}")
     k = local_slots.shape[-1] if local_slots.dim() > 0 else 1
-    T = x.numel() // hidden
-    if local_slots.numel() != T * k or scores.numel() != T * k:
-        raise VmiError("shape mismatch: local_slots/scores must hold T*k entries")
-    if x.dtype not in (torch.float32, torch.bfloat16):
-        raise VmiError(f"x dtype {x.dtype} not supported (f32 or bf16)")
-    _require(x, "x", x.element_size(), device)
-    _require(local_slots, "local_slots", 4, device)
-    if scores.dtype != torch.float32:
-        raise VmiError("scores must be float32")
-    _require(scores, "scores", 4, device)
     projs = [QuantizedProj(gate_w, gate_s, gate_b), QuantizedProj(up_w, up_s, up_b),
              QuantizedProj(down_w, down_s, down_b)]
-    for name, p in zip(("gate", "up", "down"), projs):
-        p.check(name, device)
-    cap = gate_w.shape[0]
-    if out_dtype not in (torch.float32, torch.bfloat16):
-        raise VmiError("out_dtype must be float32 or bfloat16")
-    out = torch.empty(tuple(x.shape[:-1]) + (hidden,), dtype=out_dtype, device=device)
-    sh = _stream_handle(stream)
-    nbytes = lib.vmi_fused_moe_slots_workspace_bytes(T, k, hidden, inter)
-    ws = workspace(nbytes, device, sh)
-    rc = lib.vmi_fused_moe_slots(
-        x.data_ptr(), _lib.VMI_BF16 if x.dtype == torch.bfloat16 else _lib.VMI_F32,
-        local_slots.data_ptr(), scores.data_ptr(),
-        projs[0].qmat(), projs[1].qmat(), projs[2].qmat(),
-        T, k, hidden, inter, group, bits, cap,
-        out.data_ptr(), _lib.VMI_BF16 if out_dtype == torch.bfloat16 else _lib.VMI_F32,
-        ws.data_ptr(), ws.numel(), sh)
-    check(rc, "vmi_fused_moe_slots")
-    return out
+    return _fused_moe_pairs(x, local_slots, scores, k, projs, hidden, inter, group, bits, stream, out_dtype)
+
+
+def fused_moe_staged(x: torch.Tensor, scores: torch.Tensor,
+                     gate_w, gate_s, gate_b, up_w, up_s, up_b, down_w, down_s, down_b,
+                     hidden: int, inter: int, group: int, bits: int, *, stream=None,
+                     out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Fused 4-bit MoE over pre-sliced weights (reference: fused_moe_staged,
+    fused_moe.cpp:443-504, 605-633): scores [..., k] f32; the stacks hold one
+    matrix per (token, rank) pair, pair t*k + j reading matrix t*k + j."""
+    k = scores.shape[-1] if scores.dim() > 0 else 1
+    projs = [QuantizedProj(gate_w, gate_s, gate_b), QuantizedProj(up_w, up_s, up_b),
+             QuantizedProj(down_w, down_s, down_b)]
+    return _fused_moe_pairs(x, None, scores, k, projs, hidden, inter, group, bits, stream, out_dtype)
 
 
 def workspace_status(ws: torch.Tensor, stream=None) -> int:
