@@ -478,7 +478,11 @@ int vmi_spec_commit(const int32_t* result, const uint16_t* hid, int rows, int pa
  * seed and counter (offset lo, offset hi, i, 0x5A3D1E57).  Bit-identical to
  * the CPU oracle.  temperature > 0 (use vmi_accept_greedy for 0), 0 < top_p <= 1.
  * workspace: vmi_accept_stochastic_workspace_bytes(K, vocab, draft_logits != NULL)
- * bytes, zero before the first call and left so by every call.
+ * bytes, zero before the first call and left so by every call; one call in
+ * flight per workspace.  The kernel's workgroups wait for each other between
+ * its phases, so all of them must be resident at once (the grid is at most
+ * two workgroups per CU); a wait that outlasts its bound (the CUs held by
+ * other work) gives up, and the call then writes record [0, 0, 0, -1].
  * ------------------------------------------------------------------------ */
 size_t vmi_accept_stochastic_workspace_bytes(int K, int vocab, int has_draft_logits);
 int vmi_accept_stochastic(const float* target_logits, const float* draft_logits, const int32_t* drafts, int K,
@@ -490,7 +494,9 @@ int vmi_accept_stochastic(const float* target_logits, const float* draft_logits,
  * same temperature / top-p distribution (row r uses V_r of counter
  * (offset, r)); the drafter's sampler when drafting stochastically.  The
  * reference drafts by argmax only (drafter.py:20-40).  out int32 [rows]
- * (-1 for a row without a finite logit).
+ * (-1 for a row without a finite logit, and for a row drawn after one of the
+ * kernel's waits outlasted its bound).  Workspace and residency as for
+ * vmi_accept_stochastic.
  * ------------------------------------------------------------------------ */
 size_t vmi_sample_top_p_workspace_bytes(int rows, int vocab);
 int vmi_sample_top_p(const float* logits, int rows, int vocab, float temperature, float top_p, uint64_t seed,

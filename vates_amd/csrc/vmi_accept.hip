@@ -8,19 +8,12 @@
 // when u_i q(d_i) <= p(d_i), else draw from norm(max(0, p - q)); a bonus token
 // from p_K when every draft is kept.  p and q are temperature / top-p
 // transforms of the target and draft logits.  The same machinery samples one
-// token per row (the drafter's sampler).  Each distribution's vocabulary is
-// split over NB workgroups so that the whole chip streams it:
-//   k_sd_max     row maxima per slice; clears the row's histograms
-//   k_sd_mass    integer masses W (kept in the workspace), level-1 histogram
-//   k_sd_level2  crossing bin of level 1, level-2 histogram inside it
-//   k_sd_level3  level-3 histogram; the last slice of a row to finish fixes
-//                the nucleus threshold and mass
-//   k_sd_draw    acceptance decisions (recomputed identically by every
-//                slice), masses of the distribution to draw from per slice;
-//                the last slice of a draw finds the token.
-// "Last to finish" is a release/acquire arrival counter per row in the
-// workspace, reset by that workgroup.  Histograms are integer sums (global
-// atomics), so their value does not depend on arrival order.
+// token per row (the drafter's sampler).  One launch (k_sd_fused): each
+// distribution's vocabulary is split over NB resident workgroups, which meet
+// at per-distribution arrival counters between the phases (maxima, masses and
+// level-1 histogram, level-2 and level-3 histograms of a three-level radix
+// select of the top-p threshold, the draw).  Histograms are integer sums
+// (global atomics), so their value does not depend on arrival order.
 //
 // Every probability is an integer mass (W_j = floor(2^31 2^z), z =
 // (l_j - max l) / temperature * log2 e, 2^z from a fixed fp32 polynomial), so
@@ -30,6 +23,8 @@
 
 #include "vmi_device.h"
 #include "vmi_internal.h"
+
+VMI_TL_DECL
 
 namespace {
 
@@ -101,8 +96,7 @@ struct SdArgs {
     uint64_t seed, offset;
     int accept, K, has_q;    // accept mode: K drafts, draft rows present
     const int32_t* drafts;
-    uint32_t* ctr_d;         // [kMaxRows] arrival counters of k_sd_level3
-    uint32_t* ctr_r;         // [kMaxRows] arrival counters of k_sd_draw
+    uint32_t* ctr_r;         // [kMaxRows] arrival counters of the draws
     SdStats* stats;          // [nd]
     float* pmax;             // [nd, NB]
     unsigned long long* hist;  // [nd, kHistAll]: level 1 | level 2 | level 3
@@ -148,32 +142,45 @@ __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int o) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// Reverse inclusive scan over the lanes of a wave: lane l gets
+// sum_{l' >= l} v(l').
+__device__ __forceinline__ uint64_t suffix_scan64(uint64_t v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, (lane + o) & 63);
+        const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), (lane + o) & 63);
+        if (lane + o < 64) v += ((uint64_t)hi << 32) | lo;
+    }
+    return v;
+}
+
 // One wave: the largest bin b of h[0..nbins) with above + sum_{i >= b} h[i] >= C,
-// and above + sum_{i > b} h[i].  Uniform results.
-__device__ void find_crossing(const unsigned long long* h, int nbins, uint64_t C, uint64_t above, uint32_t& b_out,
-                              uint64_t& above_out) {
+// and above + sum_{i > b} h[i].  Uniform results.  Lane l owns bins
+// [l*per, (l+1)*per); the crossing lane comes from a suffix scan of the lane
+// sums (the lanes meeting the target form a prefix, counted by a ballot),
+// the crossing bin from a suffix scan of that lane's bins.
+__device__ __forceinline__ void find_crossing(const unsigned long long* h, int nbins, uint64_t C, uint64_t above,
+                                              uint32_t& b_out, uint64_t& above_out) {
     const int lane = threadIdx.x & 63;
     const int per = nbins / 64;
     uint64_t own = 0;
-    for (int i = 0; i < per; ++i) own += h[lane * per + i];
-    uint64_t acc = above;
-    int L = 0;
-    for (int l = 63; l >= 0; --l) {
-        const uint64_t v = readlane64(own, l);
-        if (acc + v >= C) { L = l; break; }
-        acc += v;
-    }
-    int b = L * per;
-    for (int i = per - 1; i >= 0; --i) {
-        const uint64_t v = h[L * per + i];
-        if (acc + v >= C) { b = L * per + i; break; }
-        acc += v;
-    }
-    b_out = (uint32_t)b;
-    above_out = acc;
+    for (int i = 0; i < per; ++i) own += h[lane * per + ((i + lane) & (per - 1))];  // rotated: no bank conflicts
+    const uint64_t S = suffix_scan64(own);  // mass of lanes >= lane
+    const int nl = __popcll(__ballot(above + S >= C));
+    const int L = nl > 0 ? nl - 1 : 0;
+    const uint64_t SL1 = L + 1 < 64 ? readlane64(S, L + 1) : 0ull;
+    const uint64_t acc = above + (nl > 0 ? SL1 : readlane64(S, 0));
+    // the bins of lane L, one per lane
+    const uint64_t hv = lane < per ? h[L * per + lane] : 0ull;
+    const uint64_t Tb = suffix_scan64(hv);  // mass of bins >= L*per + lane within lane L
+    const int nb = __popcll(__ballot(lane < per && acc + Tb >= C));
+    const int i = nb > 0 ? nb - 1 : 0;
+    b_out = (uint32_t)(L * per + i);
+    above_out = acc + (i + 1 < 64 ? readlane64(Tb, i + 1) : 0ull);
 }
 
-__device__ uint64_t block_sum_u64(unsigned long long* red, uint64_t v) {
+__device__ __forceinline__ uint64_t block_sum_u64(unsigned long long* red, uint64_t v) {
     const int lane = threadIdx.x & 63, w = acc_wave_id();
     for (int o = 32; o >= 1; o >>= 1) v += shfl_xor64(v, o);
     __syncthreads();
@@ -186,7 +193,7 @@ __device__ uint64_t block_sum_u64(unsigned long long* red, uint64_t v) {
 }
 
 // Adds the non-zero bins of an LDS histogram into a global one.
-__device__ void flush_hist(const unsigned long long* lds, unsigned long long* g, int nbins) {
+__device__ __forceinline__ void flush_hist(const unsigned long long* lds, unsigned long long* g, int nbins) {
     for (int i = threadIdx.x; i < nbins; i += kSdThreads)
         if (lds[i]) atomicAdd(&g[i], lds[i]);
 }
@@ -216,172 +223,114 @@ __device__ __forceinline__ void for_slice(int j0, int j1, const T* __restrict__ 
     }
 }
 
-__global__ __launch_bounds__(kSdThreads) void k_sd_max(SdArgs a) {
-    __shared__ float s_red[kSdWaves];
-    const int d = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
-    int j0, j1;
-    slice_of(a, b, j0, j1);
-    const float* __restrict__ row = sd_row(a, d);
-    float m0 = -INFINITY;
-    for_slice(j0, j1, row, [&](int, float l) { m0 = fmaxf(m0, l); });
-    float m = vmi_wave_max(m0);
-    if ((tid & 63) == 0) s_red[acc_wave_id()] = m;
-    unsigned long long* h = a.hist + (size_t)d * kHistAll;
-    for (int i = b * kSdThreads + tid; i < kHistAll; i += a.NB * kSdThreads) h[i] = 0ull;
-    __syncthreads();
-    if (tid == 0) {
-        for (int i = 1; i < kSdWaves; ++i) m = fmaxf(m, s_red[i]);
-        a.pmax[d * a.NB + b] = m;
-    }
-}
+// One launch for the whole acceptance (or sampling) call: workgroup (b, d)
+// owns slice b of distribution d through five phases, and all NB * nd
+// workgroups are resident at once (the host sizes NB for that), so the
+// phases meet at per-distribution arrival counters with bounded waits:
+//   1. slice maxima; the distribution's histograms cleared
+//   2. integer masses W of the slice (from the distribution's maximum),
+//      level-1 histogram
+//   3. the level-1 crossing bin (every workgroup of the distribution finds the
+//      same one), level-2 histogram inside it
+//   4. the level-2 crossing, level-3 histogram
+//   5. workgroup 0 of the distribution fixes the nucleus threshold and mass
+//      from the level-3 histogram and publishes them; the draw workgroups
+//      wait until every distribution has, then run the draw (acceptance
+//      decisions recomputed identically by every slice, masses of the
+//      distribution to draw from per slice; the last slice of a draw to
+//      finish finds the token).
+// Every value that crosses workgroups (maxima, histograms, masses, the
+// nucleus statistics, draw partial sums) is written and read with
+// agent-scope (coherent) accesses, and a workgroup's stores have completed
+// before it counts itself, so no fence writes back or invalidates the L2.
+// Histograms are integer sums, so their value does not depend on arrival
+// order, and the results equal those of the phases run as separate launches.
+constexpr int kSdSpinLimit = 1 << 16;  // polls (each a coherent load) before a wait gives up
 
-__global__ __launch_bounds__(kSdThreads) void k_sd_mass(SdArgs a) {
-    __shared__ unsigned long long s_h[kBins];
-    __shared__ float s_red[kSdWaves];
-    const int d = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
-    float m = -INFINITY;
-    for (int i = tid; i < a.NB; i += kSdThreads) m = fmaxf(m, a.pmax[d * a.NB + i]);
-    m = vmi_wave_max(m);
-    if ((tid & 63) == 0) s_red[acc_wave_id()] = m;
-    for (int i = tid; i < kBins; i += kSdThreads) s_h[i] = 0ull;
-    __syncthreads();
-    float M = s_red[0];
-    for (int i = 1; i < kSdWaves; ++i) M = fmaxf(M, s_red[i]);
-    int j0, j1;
-    slice_of(a, b, j0, j1);
-    const float* __restrict__ row = sd_row(a, d);
-    uint32_t* __restrict__ W = a.W + (size_t)d * a.V;
-    BinRun run;
-    const float s2 = a.s2;
-    for_slice(j0, j1, row, [&](int j, float l) {
-        const uint32_t x = sd_weight(l, M, s2);
-        W[j] = x;
-        run.add(s_h, (int)(x >> 21), x);
-    });
-    run.flush(s_h);
-    __syncthreads();
-    flush_hist(s_h, a.hist + (size_t)d * kHistAll, kBins);
-}
+struct SdSync {
+    uint32_t* row;     // [kMaxRows] arrivals per distribution, 64 bytes apart (16 words)
+    uint32_t* ready;   // distributions whose nucleus statistics are published
+    uint32_t* done;    // distributions whose workgroups have all finished (the last resets every counter)
+    uint32_t* rdone;   // [kMaxRows] workgroups of each distribution finished, 64 bytes apart
+    uint32_t* flag;    // a wait gave up
+    uint32_t* go;      // [nd * NB] per-workgroup release words, 64 bytes apart: the phase the workgroup may enter
+};
 
-__global__ __launch_bounds__(kSdThreads) void k_sd_level2(SdArgs a) {
-    __shared__ unsigned long long s_h[kBins];
-    __shared__ unsigned long long s_red[kSdWaves];
-    __shared__ uint32_t s_b1;
-    __shared__ unsigned long long s_above1;
-    const int d = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
-    const unsigned long long* g1 = a.hist + (size_t)d * kHistAll;
-    uint64_t part = 0;
-    for (int i = tid; i < kBins; i += kSdThreads) {
-        s_h[i] = g1[i];
-        part += s_h[i];
-    }
-    const uint64_t Z = block_sum_u64(s_red, part);
-    SdStats* st = &a.stats[d];
-    if (Z == 0) {
-        if (b == 0 && tid == 0) st->valid = 0;
-        return;
-    }
-    uint64_t C = (a.top_p >= 1.0f) ? Z : (uint64_t)ceil((double)a.top_p * (double)Z);
-    if (C == 0) C = 1;
-    if (acc_wave_id() == 0) {
-        uint32_t b1;
-        uint64_t above1;
-        find_crossing(s_h, kBins, C, 0, b1, above1);
-        if (tid == 0) {
-            s_b1 = b1;
-            s_above1 = above1;
-            if (b == 0) {
-                st->valid = 1;
-                st->z = Z;
-                st->C = C;
-                st->b1 = b1;
-                st->above1 = above1;
+__device__ __forceinline__ void sd_wait(uint32_t* c, uint32_t target, uint32_t* flag) {
+    if (threadIdx.x == 0) {
+        int spins = 0;
+        while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins >= kSdSpinLimit) {
+                __hip_atomic_fetch_or(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
             }
         }
     }
     __syncthreads();
-    const uint32_t b1 = s_b1;
-    for (int i = tid; i < kBins; i += kSdThreads) s_h[i] = 0ull;
-    __syncthreads();
-    int j0, j1;
-    slice_of(a, b, j0, j1);
-    const uint32_t* __restrict__ W = a.W + (size_t)d * a.V;
-    BinRun run;
-    for_slice(j0, j1, W, [&](int, uint32_t x) {
-        if ((x >> 21) == b1) run.add(s_h, (int)((x >> 10) & 0x7ffu), x);
-    });
-    run.flush(s_h);
-    __syncthreads();
-    flush_hist(s_h, a.hist + (size_t)d * kHistAll + kBins, kBins);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-__global__ __launch_bounds__(kSdThreads) void k_sd_level3(SdArgs a) {
-    __shared__ unsigned long long s_h[kBins];
-    __shared__ uint32_t s_pre;
-    __shared__ unsigned long long s_above2;
-    __shared__ int s_last;
-    const int d = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
-    SdStats* st = &a.stats[d];
-    if (!st->valid) return;  // uniform: written by the previous kernel
-    const uint64_t C = st->C;
-    const unsigned long long* g2 = a.hist + (size_t)d * kHistAll + kBins;
-    for (int i = tid; i < kBins; i += kSdThreads) s_h[i] = g2[i];
+// Phase barrier of the n workgroups sharing counter c: this workgroup's
+// stores are complete, then it counts itself; the last to arrive (the counter
+// at target - 1) raises the release word of each of the n workgroups to
+// `phase`, and every workgroup waits on its own word (its own 64-byte line, so
+// the waits do not all poll one address).
+__device__ __forceinline__ void sd_barrier(uint32_t* c, uint32_t target, uint32_t* go, int n, int self,
+                                           uint32_t phase, uint32_t* flag) {
+    __shared__ int s_rel;
+    vmi_vm_wait_c<0>();
     __syncthreads();
-    if (acc_wave_id() == 0) {
-        uint32_t b2;
-        uint64_t above2;
-        find_crossing(s_h, kBins, C, st->above1, b2, above2);
-        if (tid == 0) {
-            s_pre = (st->b1 << 11) | b2;
-            s_above2 = above2;
-            if (b == 0) {
-                st->b2 = b2;
-                st->above2 = above2;
-            }
-        }
+    if (threadIdx.x == 0)
+        s_rel = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == target - 1u;
+    __syncthreads();
+    if (s_rel)
+        for (int i = threadIdx.x; i < n; i += kSdThreads)
+            __hip_atomic_store(go + 16 * i, phase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sd_wait(go + 16 * self, phase, flag);
+}
+
+__device__ __forceinline__ uint64_t ld64c(const unsigned long long* p) {
+    return __hip_atomic_load(const_cast<unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st64c(unsigned long long* p, uint64_t v) {
+    __hip_atomic_store(p, (unsigned long long)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld32c(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Histogram bins [0, n) of g (written by other workgroups' atomics) into LDS,
+// every load issued before any is used; returns the sum of this thread's bins.
+template <int N>
+__device__ __forceinline__ uint64_t hist_to_lds(const unsigned long long* g, unsigned long long* lds) {
+    constexpr int PER = N / kSdThreads;
+    const __amdgpu_buffer_rsrc_t rg = vmi_rsrc(g, (uint32_t)N * 8u);
+    uint2 v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) v[u] = vmi_bload_b64_coh(rg, (uint32_t)(threadIdx.x + kSdThreads * u) * 8u, 0);
+    uint64_t sum = 0;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const uint64_t x = ((uint64_t)v[u].y << 32) | v[u].x;
+        lds[threadIdx.x + kSdThreads * u] = x;
+        sum += x;
     }
-    __syncthreads();
-    const uint32_t pre = s_pre;
-    for (int i = tid; i < 1024; i += kSdThreads) s_h[i] = 0ull;
-    __syncthreads();
-    int j0, j1;
-    slice_of(a, b, j0, j1);
-    const uint32_t* __restrict__ W = a.W + (size_t)d * a.V;
-    BinRun run;
-    for_slice(j0, j1, W, [&](int, uint32_t x) {
-        if ((x >> 10) == pre) run.add(s_h, (int)(x & 0x3ffu), x);
-    });
-    run.flush(s_h);
-    __syncthreads();
-    unsigned long long* g3 = a.hist + (size_t)d * kHistAll + 2 * kBins;
-    flush_hist(s_h, g3, 1024);
-    // the last slice of row d to finish fixes the nucleus
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&a.ctr_d[d], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == (uint32_t)(a.NB - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    for (int i = tid; i < 1024; i += kSdThreads)
-        s_h[i] = __hip_atomic_load(&g3[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (acc_wave_id() == 0) {
-        uint32_t b3;
-        uint64_t above3;
-        find_crossing(s_h, 1024, C, s_above2, b3, above3);
-        if (tid == 0) {
-            st->theta = (pre << 10) | b3;
-            st->zs = above3 + s_h[b3];
-            __hip_atomic_store(&a.ctr_d[d], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
+    return sum;
+}
+
+// The nucleus statistics of distribution d as the draw reads them.
+__device__ __forceinline__ SdStats sd_stats(const SdArgs& a, int d) {
+    const SdStats* sp = &a.stats[d];
+    SdStats s{};
+    s.theta = ld32c(&sp->theta);
+    s.valid = ld32c(&sp->valid);
+    s.zs = ld64c(&sp->zs);
+    return s;
 }
 
 __device__ __forceinline__ uint32_t nucleus_mass(const uint32_t* __restrict__ W, uint32_t theta, int j) {
-    const uint32_t x = W[j];
+    const uint32_t x = ld32c(W + j);
     return x >= theta ? x : 0u;
 }
 
@@ -397,10 +346,10 @@ struct DrawPlan {
     double zp, zq;
 };
 
-__device__ DrawPlan plan_draw(const SdArgs& a, int r) {
+__device__ __forceinline__ DrawPlan plan_draw(const SdArgs& a, int r) {
     DrawPlan P{};
     if (!a.accept) {
-        const SdStats& s = a.stats[r];
+        const SdStats s = sd_stats(a, r);
         P.bad = !s.valid;
         P.dp = r;
         P.th_p = s.theta;
@@ -409,7 +358,7 @@ __device__ DrawPlan plan_draw(const SdArgs& a, int r) {
         sd_uniforms(a.seed, a.offset, r, U, P.Vr);
         return P;
     }
-    for (int d = 0; d < a.nd; ++d) P.bad |= !a.stats[d].valid;
+    for (int d = 0; d < a.nd; ++d) P.bad |= !ld32c(&a.stats[d].valid);
     if (P.bad) return P;
     const int K = a.K, V = a.V;
     int m = 0;
@@ -419,10 +368,10 @@ __device__ DrawPlan plan_draw(const SdArgs& a, int r) {
         sd_uniforms(a.seed, a.offset, m, U, Vr);
         double pp = 0.0, qq = 1.0;
         if (dj >= 0 && dj < V) {
-            const SdStats& sp = a.stats[m];
+            const SdStats sp = sd_stats(a, m);
             pp = (double)nucleus_mass(a.W + (size_t)m * V, sp.theta, dj) / (double)sp.zs;
             if (a.has_q) {
-                const SdStats& sq = a.stats[K + 1 + m];
+                const SdStats sq = sd_stats(a, K + 1 + m);
                 qq = (double)nucleus_mass(a.W + (size_t)(K + 1 + m) * V, sq.theta, dj) / (double)sq.zs;
             }
         }
@@ -433,15 +382,17 @@ __device__ DrawPlan plan_draw(const SdArgs& a, int r) {
     uint32_t U;
     sd_uniforms(a.seed, a.offset, m, U, P.Vr);
     P.dp = m;
-    P.th_p = a.stats[m].theta;
-    P.zp = (double)a.stats[m].zs;
+    const SdStats sm = sd_stats(a, m);
+    P.th_p = sm.theta;
+    P.zp = (double)sm.zs;
     P.resid = m < K;
     if (P.resid) {
         P.dm = a.drafts[m];
         if (a.has_q) {
             P.dq = K + 1 + m;
-            P.th_q = a.stats[P.dq].theta;
-            P.zq = (double)a.stats[P.dq].zs;
+            const SdStats sq = sd_stats(a, P.dq);
+            P.th_q = sq.theta;
+            P.zq = (double)sq.zs;
         }
     }
     return P;
@@ -456,33 +407,29 @@ __device__ __forceinline__ uint32_t resid_value(const SdArgs& a, const DrawPlan&
     return rr > 0.0 ? (uint32_t)(rr * 0x1p31) : 0u;
 }
 
-__device__ __forceinline__ uint32_t resid_mass(const SdArgs& a, const DrawPlan& P, int j) {
-    const uint32_t pm = nucleus_mass(a.W + (size_t)P.dp * a.V, P.th_p, j);
-    const uint32_t wq = a.has_q ? a.W[(size_t)P.dq * a.V + j] : 0u;
-    return resid_value(a, P, j, pm, wq);
-}
-
-__global__ __launch_bounds__(kSdThreads) void k_sd_draw(SdArgs a) {
-    __shared__ unsigned long long s_red[kSdWaves];
-    __shared__ unsigned long long s_scan[kSdThreads];
+// The draw of row r by slice b; the last slice of the row to finish finds the
+// token and writes the result.
+__device__ __forceinline__ void sd_draw(const SdArgs& a, const SdSync& y, int r, int b, unsigned long long* s_scan,
+                        unsigned long long* s_red) {
     __shared__ int s_last, s_bstar, s_tok;
     __shared__ unsigned long long s_base, s_t;
     __shared__ int s_use_p;
-    const int r = blockIdx.y, b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
     const DrawPlan P = plan_draw(a, r);
     int j0, j1;
     slice_of(a, b, j0, j1);
     uint64_t sr = 0, sp = 0;
     if (!P.bad) {
-        const uint32_t* __restrict__ Wp = a.W + (size_t)P.dp * a.V;
-        const uint32_t* __restrict__ Wq = a.has_q && P.resid ? a.W + (size_t)P.dq * a.V : Wp;
+        const __amdgpu_buffer_rsrc_t rp = vmi_rsrc(a.W + (size_t)P.dp * a.V, (uint32_t)a.V * 4u);
+        const __amdgpu_buffer_rsrc_t rq =
+            vmi_rsrc(a.W + (size_t)(a.has_q && P.resid ? P.dq : P.dp) * a.V, (uint32_t)a.V * 4u);
         for (int base = j0 + tid; base < j1; base += kBatch * kSdThreads) {
             uint32_t vp[kBatch], vq[kBatch];
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
                 const int j = base + u * kSdThreads;
-                vp[u] = j < j1 ? Wp[j] : 0u;
-                vq[u] = j < j1 ? Wq[j] : 0u;
+                vp[u] = vmi_bload_b32_coh(rp, j < j1 ? (uint32_t)j * 4u : VMI_OOB, 0);
+                vq[u] = vmi_bload_b32_coh(rq, j < j1 ? (uint32_t)j * 4u : VMI_OOB, 0);
             }
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
@@ -498,43 +445,39 @@ __global__ __launch_bounds__(kSdThreads) void k_sd_draw(SdArgs a) {
     sr = block_sum_u64(s_red, sr);
     sp = block_sum_u64(s_red, sp);
     if (tid == 0) {
-        a.partR[r * a.NB + b] = sr;
-        a.partP[r * a.NB + b] = sp;
+        st64c(&a.partR[r * a.NB + b], sr);
+        st64c(&a.partP[r * a.NB + b], sp);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    vmi_vm_wait_c<0>();
     __syncthreads();
     if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&a.ctr_r[r], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t prev = __hip_atomic_fetch_add(&a.ctr_r[r], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev == (uint32_t)(a.NB - 1);
+        if (s_last) __hip_atomic_store(&a.ctr_r[r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (P.bad) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (P.bad || ld32c(y.flag)) {
         if (tid == 0) {
             if (a.accept) {
                 a.out[0] = 0; a.out[1] = 0; a.out[2] = 0; a.out[3] = -1;
             } else {
                 a.out[r] = -1;
             }
-            __hip_atomic_store(&a.ctr_r[r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
     }
     // totals, the slice holding the draw point, and the mass before it (wave 0;
     // lane i holds slices i and i + 64, NB <= 128)
     if (acc_wave_id() == 0) {
-        const unsigned long long* pr = a.partR + r * a.NB;
-        const unsigned long long* pp = a.partP + r * a.NB;
-        uint64_t r0 = 0, r1 = 0, p0 = 0, p1 = 0;
-        if (lane < a.NB) {
-            r0 = __hip_atomic_load(&pr[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            p0 = __hip_atomic_load(&pp[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if (lane + 64 < a.NB) {
-            r1 = __hip_atomic_load(&pr[lane + 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            p1 = __hip_atomic_load(&pp[lane + 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        const __amdgpu_buffer_rsrc_t rr = vmi_rsrc(a.partR + r * a.NB, (uint32_t)a.NB * 8u);
+        const __amdgpu_buffer_rsrc_t rpp = vmi_rsrc(a.partP + r * a.NB, (uint32_t)a.NB * 8u);
+        const uint2 r0v = vmi_bload_b64_coh(rr, (uint32_t)lane * 8u, 0), p0v = vmi_bload_b64_coh(rpp, (uint32_t)lane * 8u, 0);
+        const uint2 r1v = vmi_bload_b64_coh(rr, (uint32_t)(lane + 64) * 8u, 0);
+        const uint2 p1v = vmi_bload_b64_coh(rpp, (uint32_t)(lane + 64) * 8u, 0);
+        const uint64_t r0 = ((uint64_t)r0v.y << 32) | r0v.x, p0 = ((uint64_t)p0v.y << 32) | p0v.x;
+        const uint64_t r1 = ((uint64_t)r1v.y << 32) | r1v.x, p1 = ((uint64_t)p1v.y << 32) | p1v.x;
         uint64_t totR = r0 + r1, totP = p0 + p1;
         for (int o = 32; o >= 1; o >>= 1) {
             totR += shfl_xor64(totR, o);
@@ -571,14 +514,23 @@ __global__ __launch_bounds__(kSdThreads) void k_sd_draw(SdArgs a) {
     const uint64_t t = s_t;
     int k0, k1;
     slice_of(a, bs, k0, k1);
+    const __amdgpu_buffer_rsrc_t sp_ = vmi_rsrc(a.W + (size_t)P.dp * a.V, (uint32_t)a.V * 4u);
+    const __amdgpu_buffer_rsrc_t sq_ = vmi_rsrc(a.W + (size_t)(a.has_q && P.resid ? P.dq : P.dp) * a.V, (uint32_t)a.V * 4u);
     for (int g0 = k0; g0 < k1; g0 += kBatch * kSdThreads) {
         const int gj = g0 + kBatch * tid;
-        uint32_t v[kBatch];
+        uint32_t v[kBatch], wq[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const uint32_t off = gj + u < k1 ? (uint32_t)(gj + u) * 4u : VMI_OOB;
+            v[u] = vmi_bload_b32_coh(sp_, off, 0);
+            wq[u] = vmi_bload_b32_coh(sq_, off, 0);
+        }
         uint64_t gs = 0;
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const int j = gj + u;
-            v[u] = j < k1 ? (use_p ? nucleus_mass(a.W + (size_t)P.dp * a.V, P.th_p, j) : resid_mass(a, P, j)) : 0u;
+            const uint32_t pm = v[u] >= P.th_p ? v[u] : 0u;
+            v[u] = j < k1 ? (use_p ? pm : resid_value(a, P, j, pm, wq[u])) : 0u;
             gs += v[u];
         }
         s_scan[tid] = gs;
@@ -618,7 +570,195 @@ __global__ __launch_bounds__(kSdThreads) void k_sd_draw(SdArgs a) {
         } else {
             a.out[r] = tok;
         }
-        __hip_atomic_store(&a.ctr_r[r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+__global__ __launch_bounds__(kSdThreads) void k_sd_fused(SdArgs a, SdSync y, int rows) {
+    __shared__ unsigned long long s_h[kBins];
+    __shared__ unsigned long long s_red[kSdWaves];
+    __shared__ float s_redf[kSdWaves];
+    __shared__ uint32_t s_b1, s_pre;
+    __shared__ unsigned long long s_above1, s_above2, s_C;
+    __shared__ int s_valid;
+    const int d = blockIdx.y, b = blockIdx.x, tid = threadIdx.x;
+    const int NB = a.NB;
+    uint32_t* rc = y.row + 16 * d;
+    unsigned long long* h = a.hist + (size_t)d * kHistAll;
+    int j0, j1;
+    slice_of(a, b, j0, j1);
+    const float* __restrict__ row = sd_row(a, d);
+    uint32_t* W = a.W + (size_t)d * a.V;
+    VMI_STAMP(d, 0);
+
+    // 1. slice maximum; this workgroup's share of the histograms cleared
+    float m0 = -INFINITY;
+    for_slice(j0, j1, row, [&](int, float l) { m0 = fmaxf(m0, l); });
+    {
+        float m = vmi_wave_max(m0);
+        if ((tid & 63) == 0) s_redf[acc_wave_id()] = m;
+        for (int i = b * kSdThreads + tid; i < kHistAll; i += NB * kSdThreads) st64c(&h[i], 0ull);
+        __syncthreads();
+        if (tid == 0) {
+            for (int i = 1; i < kSdWaves; ++i) m = fmaxf(m, s_redf[i]);
+            __hip_atomic_store(&a.pmax[d * NB + b], m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    VMI_STAMP(d, 1);
+    sd_barrier(rc, (uint32_t)NB, y.go + 16 * NB * d, NB, b, 1u, y.flag);
+    VMI_STAMP(d, 2);
+
+    // 2. masses and the level-1 histogram
+    {
+        float m = -INFINITY;
+        for (int i = tid; i < NB; i += kSdThreads)
+            m = fmaxf(m, __hip_atomic_load(&a.pmax[d * NB + i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        m = vmi_wave_max(m);
+        if ((tid & 63) == 0) s_redf[acc_wave_id()] = m;
+        for (int i = tid; i < kBins; i += kSdThreads) s_h[i] = 0ull;
+        __syncthreads();
+        float M = s_redf[0];
+        for (int i = 1; i < kSdWaves; ++i) M = fmaxf(M, s_redf[i]);
+        BinRun run;
+        const float s2 = a.s2;
+        for_slice(j0, j1, row, [&](int j, float l) {
+            const uint32_t x = sd_weight(l, M, s2);
+            __hip_atomic_store(W + j, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            run.add(s_h, (int)(x >> 21), x);
+        });
+        run.flush(s_h);
+        __syncthreads();
+        flush_hist(s_h, h, kBins);
+    }
+    VMI_STAMP(d, 3);
+    sd_barrier(rc, 2u * NB, y.go + 16 * NB * d, NB, b, 2u, y.flag);
+    VMI_STAMP(d, 4);
+
+    // 3. total mass, nucleus target, level-1 crossing; level-2 histogram
+    {
+        const uint64_t part = hist_to_lds<kBins>(h, s_h);
+        const uint64_t Z = block_sum_u64(s_red, part);
+        if (Z > 0 && acc_wave_id() == 0) {
+            uint64_t C = (a.top_p >= 1.0f) ? Z : (uint64_t)ceil((double)a.top_p * (double)Z);
+            if (C == 0) C = 1;
+            uint32_t b1;
+            uint64_t above1;
+            find_crossing(s_h, kBins, C, 0, b1, above1);
+            if (tid == 0) {
+                s_b1 = b1;
+                s_above1 = above1;
+                s_C = C;
+            }
+        }
+        if (tid == 0) s_valid = Z > 0;
+        __syncthreads();
+        for (int i = tid; i < kBins; i += kSdThreads) s_h[i] = 0ull;
+        __syncthreads();
+        if (s_valid) {
+            const uint32_t b1 = s_b1;
+            BinRun run;
+            for_slice(j0, j1, W, [&](int, uint32_t x) {
+                if ((x >> 21) == b1) run.add(s_h, (int)((x >> 10) & 0x7ffu), x);
+            });
+            run.flush(s_h);
+            __syncthreads();
+            flush_hist(s_h, h + kBins, kBins);
+        }
+    }
+    VMI_STAMP(d, 5);
+    sd_barrier(rc, 3u * NB, y.go + 16 * NB * d, NB, b, 3u, y.flag);
+    VMI_STAMP(d, 6);
+
+    // 4. level-2 crossing; level-3 histogram
+    if (s_valid) {
+        hist_to_lds<kBins>(h + kBins, s_h);
+        __syncthreads();
+        if (acc_wave_id() == 0) {
+            uint32_t b2;
+            uint64_t above2;
+            find_crossing(s_h, kBins, s_C, s_above1, b2, above2);
+            if (tid == 0) {
+                s_pre = (s_b1 << 11) | b2;
+                s_above2 = above2;
+            }
+        }
+        __syncthreads();
+        const uint32_t pre = s_pre;
+        for (int i = tid; i < 1024; i += kSdThreads) s_h[i] = 0ull;
+        __syncthreads();
+        BinRun run;
+        for_slice(j0, j1, W, [&](int, uint32_t x) {
+            if ((x >> 10) == pre) run.add(s_h, (int)(x & 0x3ffu), x);
+        });
+        run.flush(s_h);
+        __syncthreads();
+        flush_hist(s_h, h + 2 * kBins, 1024);
+    }
+    VMI_STAMP(d, 7);
+    sd_barrier(rc, 4u * NB, y.go + 16 * NB * d, NB, b, 4u, y.flag);
+    VMI_STAMP(d, 8);
+
+    // 5. the nucleus of distribution d (its workgroup 0), then the draws
+    if (b == 0) {
+        SdStats* st = &a.stats[d];
+        if (s_valid) {
+            hist_to_lds<1024>(h + 2 * kBins, s_h);
+            __syncthreads();
+            if (acc_wave_id() == 0) {
+                uint32_t b3;
+                uint64_t above3;
+                find_crossing(s_h, 1024, s_C, s_above2, b3, above3);
+                if (tid == 0) {
+                    __hip_atomic_store(&st->theta, (s_pre << 10) | b3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    st64c(&st->zs, above3 + s_h[b3]);
+                }
+            }
+        }
+        if (tid == 0) __hip_atomic_store(&st->valid, (uint32_t)s_valid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        vmi_vm_wait_c<0>();
+        __syncthreads();
+        __shared__ int s_rel5;
+        if (tid == 0)
+            s_rel5 = __hip_atomic_fetch_add(y.ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     (uint32_t)a.nd - 1u;
+        __syncthreads();
+        if (s_rel5)
+            for (int i = tid; i < rows * NB; i += kSdThreads)
+                __hip_atomic_store(y.go + 16 * i, 5u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    VMI_STAMP(d, 9);
+    if (d < rows) {
+        sd_wait(y.go + 16 * (NB * d + b), 5u, y.flag);
+        VMI_STAMP(d, 10);
+        sd_draw(a, y, d, b, s_h, s_red);
+        VMI_STAMP(d, 11);
+    }
+    // the last workgroup of the last distribution to finish clears the
+    // counters for the next call (two levels, so no counter sees more than NB
+    // arrivals)
+    __shared__ int s_fin;
+    vmi_vm_wait_c<0>();
+    __syncthreads();
+    if (tid == 0) {
+        int fin = 0;
+        if (__hip_atomic_fetch_add(y.rdone + 16 * d, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            (uint32_t)NB - 1u)
+            fin = __hip_atomic_fetch_add(y.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  (uint32_t)a.nd - 1u;
+        s_fin = fin;
+    }
+    __syncthreads();
+    if (s_fin) {
+        for (int i = tid; i < a.nd * NB; i += kSdThreads)
+            __hip_atomic_store(y.go + 16 * i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int i = tid; i < a.nd; i += kSdThreads) {
+            __hip_atomic_store(y.row + 16 * i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(y.rdone + 16 * i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (tid == 0) {
+            __hip_atomic_store(y.ready, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(y.flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(y.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -669,17 +809,18 @@ __global__ __launch_bounds__(64) void k_accept_greedy(GreedyArgs a) {
 }
 
 // Workspace: counters first (fixed offsets whatever the shape, zero between
-// calls), then per-row state.
+// calls): the per-distribution phase counters one 64-byte line each, the
+// ready / done / gave-up words and the draws' counters; then per-row state.
+constexpr int kSdMaxWgs = 2048;  // release words (one 64-byte line per workgroup of a launch)
+constexpr size_t kSdSyncBytes = 64 * kMaxRows + 256 + kMaxRows * sizeof(uint32_t) + 64 * kSdMaxWgs + 64 * kMaxRows;
+
 struct SdLayout {
-    size_t ctr_d, ctr_r, stats, pmax, hist, partR, partP, W, bytes;
+    size_t stats, pmax, hist, partR, partP, W, bytes;
 };
 
 SdLayout sd_layout(int nd, int rows, int V, int NB) {
     SdLayout L{};
-    size_t off = 0;
-    L.ctr_d = off; off += kMaxRows * sizeof(uint32_t);
-    L.ctr_r = off; off += kMaxRows * sizeof(uint32_t);
-    off = vmi::align256(off);
+    size_t off = vmi::align256(kSdSyncBytes);
     L.stats = off; off += vmi::align256((size_t)nd * sizeof(SdStats));
     L.pmax = off; off += vmi::align256((size_t)nd * NB * sizeof(float));
     L.hist = off; off += vmi::align256((size_t)nd * kHistAll * sizeof(unsigned long long));
@@ -697,21 +838,32 @@ int sd_slices(int V) {
     return nb < 1 ? 1 : (nb > 128 ? 128 : nb);
 }
 
+// Slices per row for a launch of nd distributions: every workgroup of the
+// launch must be resident at once (two per compute unit is well within the
+// kernel's registers and LDS), so NB * nd <= 2 * CUs.
+int sd_slices_resident(int V, int nd) {
+    int cap = 2 * vmi::device_cus() / nd;
+    if (cap * nd > kSdMaxWgs) cap = kSdMaxWgs / nd;
+    const int nb = sd_slices(V);
+    return nb < cap ? nb : (cap < 1 ? 1 : cap);
+}
+
 float sd_scale(float temperature) { return (float)((1.0 / (double)temperature) * 1.4426950408889634); }
 
-hipError_t sd_launch(SdArgs& a, int rows, hipStream_t s) {
-    const dim3 blk(kSdThreads), gd(a.NB, a.nd);
-    hipLaunchKernelGGL(k_sd_max, gd, blk, 0, s, a);
-    hipLaunchKernelGGL(k_sd_mass, gd, blk, 0, s, a);
-    hipLaunchKernelGGL(k_sd_level2, gd, blk, 0, s, a);
-    hipLaunchKernelGGL(k_sd_level3, gd, blk, 0, s, a);
-    hipLaunchKernelGGL(k_sd_draw, dim3(a.NB, rows), blk, 0, s, a);
+hipError_t sd_launch(SdArgs& a, uint8_t* ws, int rows, hipStream_t s) {
+    SdSync y{};
+    y.row = reinterpret_cast<uint32_t*>(ws);
+    y.ready = reinterpret_cast<uint32_t*>(ws + 64 * kMaxRows);
+    y.done = reinterpret_cast<uint32_t*>(ws + 64 * kMaxRows + 64);
+    y.flag = reinterpret_cast<uint32_t*>(ws + 64 * kMaxRows + 128);
+    a.ctr_r = reinterpret_cast<uint32_t*>(ws + 64 * kMaxRows + 256);
+    y.go = reinterpret_cast<uint32_t*>(ws + 64 * kMaxRows + 256 + kMaxRows * sizeof(uint32_t));
+    y.rdone = reinterpret_cast<uint32_t*>(ws + 64 * kMaxRows + 256 + kMaxRows * sizeof(uint32_t) + 64 * kSdMaxWgs);
+    hipLaunchKernelGGL(k_sd_fused, dim3(a.NB, a.nd), dim3(kSdThreads), 0, s, a, y, rows);
     return hipGetLastError();
 }
 
 void sd_bind(SdArgs& a, uint8_t* ws, const SdLayout& L) {
-    a.ctr_d = reinterpret_cast<uint32_t*>(ws + L.ctr_d);
-    a.ctr_r = reinterpret_cast<uint32_t*>(ws + L.ctr_r);
     a.stats = reinterpret_cast<SdStats*>(ws + L.stats);
     a.pmax = reinterpret_cast<float*>(ws + L.pmax);
     a.hist = reinterpret_cast<unsigned long long*>(ws + L.hist);
@@ -807,8 +959,8 @@ extern "C" int vmi_accept_stochastic(const float* target_logits, const float* dr
     if (!(top_p > 0.0f) || top_p > 1.0f) return vmi::fail(VMI_ERR_INVALID, "top_p must be in (0, 1]");
     if (!target_logits || !drafts || !result) return vmi::fail(VMI_ERR_INVALID, "null target/drafts/result");
     const int nd = (K + 1) + (draft_logits ? K : 0);
-    const int NB = sd_slices(vocab);
-    const SdLayout L = sd_layout(nd, 1, vocab, NB);
+    const SdLayout L = sd_layout(nd, 1, vocab, sd_slices(vocab));
+    const int NB = sd_slices_resident(vocab, nd);
     if (!workspace || workspace_bytes < L.bytes)
         return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
     SdArgs a{};
@@ -818,7 +970,7 @@ extern "C" int vmi_accept_stochastic(const float* target_logits, const float* dr
     a.accept = 1; a.K = K; a.has_q = draft_logits != nullptr; a.drafts = drafts;
     a.out = result;
     sd_bind(a, static_cast<uint8_t*>(workspace), L);
-    const hipError_t e = sd_launch(a, 1, static_cast<hipStream_t>(stream));
+    const hipError_t e = sd_launch(a, static_cast<uint8_t*>(workspace), 1, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "stochastic acceptance launch");
 }
 
@@ -836,8 +988,8 @@ extern "C" int vmi_sample_top_p(const float* logits, int rows, int vocab, float 
     if (!(temperature > 0.0f) || !(temperature < 1e30f)) return vmi::fail(VMI_ERR_INVALID, "temperature must be positive");
     if (!(top_p > 0.0f) || top_p > 1.0f) return vmi::fail(VMI_ERR_INVALID, "top_p must be in (0, 1]");
     if (!logits || !out) return vmi::fail(VMI_ERR_INVALID, "null logits/out");
-    const int NB = sd_slices(vocab);
-    const SdLayout L = sd_layout(rows, rows, vocab, NB);
+    const SdLayout L = sd_layout(rows, rows, vocab, sd_slices(vocab));
+    const int NB = sd_slices_resident(vocab, rows);
     if (!workspace || workspace_bytes < L.bytes)
         return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
     SdArgs a{};
@@ -847,6 +999,13 @@ extern "C" int vmi_sample_top_p(const float* logits, int rows, int vocab, float 
     a.accept = 0; a.K = 0; a.has_q = 0; a.drafts = nullptr;
     a.out = out;
     sd_bind(a, static_cast<uint8_t*>(workspace), L);
-    const hipError_t e = sd_launch(a, rows, static_cast<hipStream_t>(stream));
+    const hipError_t e = sd_launch(a, static_cast<uint8_t*>(workspace), rows, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "top-p sampling launch");
 }
+
+#ifdef VMI_TIMELINE
+// Tuning builds only: where the kernels of this file record their stamps.
+extern "C" int vmi_timeline_set_accept(void* buf) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(vmi_tl_buf), &buf, sizeof(buf)) == hipSuccess ? VMI_OK : VMI_ERR_HIP;
+}
+#endif

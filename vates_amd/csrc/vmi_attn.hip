@@ -42,6 +42,8 @@
 #include "vmi_device.h"
 #include "vmi_internal.h"
 
+VMI_TL_DECL
+
 namespace {
 
 constexpr int kAThreads = 256;
@@ -699,6 +701,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     const int T = a.T, K = a.K, G = K / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = at_wave();
     const int nl = lane & 15, q4 = lane >> 4;
+    VMI_STAMP(3, 0);
     const int ks = K / kQ4Kw, tiles = kQ4Waves / ks;
     const int tile = w / ks, kw = w % ks;
     const int n = (blockIdx.x * tiles + tile) * 16 + nl;
@@ -855,6 +858,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = fmaf(sc, d[e], acc[e]);
     }
+    VMI_STAMP(3, 1);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -876,6 +880,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
         for (int e = 0; e < 4; ++e) s_part[w][nl][4 * q4 + e] = acc[e];
     }
     __syncthreads();
+    VMI_STAMP(3, 2);
     for (int i = tid; i < tiles * 16 * T; i += kQ4Threads) {
         const int tl = i / (16 * T), rr = (i / T) % 16, t = i % T;
         float y = s_part[tl * ks][rr][t];
@@ -891,6 +896,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
             }
         }
     }
+    VMI_STAMP(3, 3);
 }
 
 // ------------------------------------------------------------------ host
@@ -1149,3 +1155,9 @@ extern "C" int vmi_rmsnorm(const uint16_t* x, const int32_t* ids, int rows, int 
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "k_rms_rows launch");
 }
 
+#ifdef VMI_TIMELINE
+// Tuning builds only: where the kernels of this file record their stamps.
+extern "C" int vmi_timeline_set_attn(void* buf) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(vmi_tl_buf), &buf, sizeof(buf)) == hipSuccess ? VMI_OK : VMI_ERR_HIP;
+}
+#endif

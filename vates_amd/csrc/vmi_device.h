@@ -377,6 +377,28 @@ __device__ __forceinline__ uint2 vmi_bload_b64(__amdgpu_buffer_rsrc_t r, uint32_
 __device__ __forceinline__ uint32_t vmi_bload_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
 }
+// Coherent forms (cache policy sc1: device-scope coherence, the bit the
+// compiler sets on agent-scope atomic loads) for data that other workgroups
+// of the same kernel wrote with agent-scope stores.  Unlike atomic loads they
+// are ordinary loads to the compiler, so a batch of them is issued back to
+// back instead of one wait per load.
+#define VMI_CP_SC1 0x10
+__device__ __forceinline__ uint32_t vmi_bload_b32_coh(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, VMI_CP_SC1);
+}
+__device__ __forceinline__ uint2 vmi_bload_b64_coh(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, VMI_CP_SC1);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ vmi_u4 vmi_bload_b128_coh(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, VMI_CP_SC1);
+    vmi_u4 o;
+    o[0] = v[0];
+    o[1] = v[1];
+    o[2] = v[2];
+    o[3] = v[3];
+    return o;
+}
 __device__ __forceinline__ uint32_t vmi_bload_b16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
 }
