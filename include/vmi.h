@@ -67,8 +67,13 @@ typedef struct vmi_qmat {
  * gate/up stacks [cap, inter, hidden], down stack [cap, hidden, inter],
  * out [T, hidden] in out_dtype = sum_j scores[t*k+j] * expert_{slot}(x_t)
  * (SwiGLU expert: g*sigmoid(g)*u then down; fixed j order as reduce_pairs).
+ * Arithmetic: with f32 x, the reference operator's fp32 throughout (fp32 x,
+ * weights q*s + b, activations and pair outputs; relative error about 1e-6
+ * against a float64 evaluation); with bf16 x, the decode path's MFMA operands
+ * (fp16 x scaled by a power of two, bf16 activations, fp32 accumulation;
+ * relative error about 2e-3).
  * Supported: bits == 4, group == 64, T*k <= 160, T <= 16,
- * hidden in {256, 512, 1024, 2048}, inter in {128, 256, 512}.
+ * hidden in {512, 1024, 2048}, inter a multiple of 64 up to 512.
  * The reference raises on shape mismatch (fused_moe.cpp:522-524); this
  * returns VMI_ERR_INVALID.  A slot outside [0, cap) contributes zero and sets
  * VMI_STATUS_BAD_SLOT.

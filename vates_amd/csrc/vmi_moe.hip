@@ -682,6 +682,23 @@ __device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, 
     VMI_STAMP(1, 2);
 }
 
+// Routing of a caller's slot list (or pair p on matrix p without one): the
+// from-slots half of route_batch, without the top-k code.
+__device__ void route_slots(const GateUpArgs& a, RouteLds& R, int32_t* s_first) {
+    const int tid = threadIdx.x;
+    if (tid == 0) R.bad = 0u;
+    __syncthreads();
+    if (tid < a.npairs) {
+        const int s = a.slots ? a.slots[tid] : tid;
+        const bool ok = s >= 0 && s < a.cap;
+        R.slot[tid] = ok ? s : -1;
+        R.scores[tid] = a.in_scores[tid];
+        if (!ok) atomicOr(&R.bad, VMI_STATUS_BAD_SLOT);
+    }
+    __syncthreads();
+    dedup_lds(a.npairs, a.k, a.cap, R, s_first);
+}
+
 // The route table for k_down_rows, the caller's ids/scores and the status
 // bits, written by one routed workgroup once its own work is issued (nothing
 // in this kernel reads them).
@@ -1286,6 +1303,316 @@ __global__ __launch_bounds__(kThreads) void k_prep(PrepArgs a) {
     write_operands<XT, CPL>(reinterpret_cast<const XT*>(a.x) + (size_t)t * a.H, nullptr, 0.0f, a.H, t, a.ops);
 }
 
+// ------------------------------------------------- fp32 operator path
+// vmi_fused_moe_slots / vmi_fused_moe_staged with f32 x keep the reference
+// operator's fp32 arithmetic (fused_moe.cpp:221-298: fp32 x, fp32 dequantised
+// weights, fp32 activations, reduce_pairs over j in order).  Each 16-byte
+// chunk of a weight row holds 32 columns of one quantisation group, so the
+// affine dequantisation q*s + b is factored out of the chunk's sum:
+//   sum_c (q_c s + b) x_c = s * sum_c q_c x_c + b * sum_c x_c,
+// with both sums in fp32 (the 4-bit values are exact, the products rounded
+// once each), then the chunks of a row are added across the lanes that hold
+// them.  Three launches: gate/up + SwiGLU per (distinct slot, 32 rows of I)
+// into fp32 activation rows, down per (distinct slot, rows of H) into one
+// fp32 output row per (token, distinct slot), and the combine per (t, h).
+
+constexpr int kFTok = 4;  // token rows per LDS chunk
+// Staged rows keep each 32-column chunk 36 floats apart, so the eight lanes
+// reading eight consecutive chunks of one row start on different LDS banks.
+constexpr int kFChunk = 36;
+
+// Lane geometry of a weight row of LEN columns (LEN a multiple of 64): LPR
+// lanes share a row, each taking NI 16-byte chunks; a wave covers RPW rows
+// and a 256-thread workgroup RPB.
+template <int LEN>
+struct FRow {
+    static constexpr int NHG = LEN / 32;  // 32-column chunks (half groups)
+    static constexpr int LPR = NHG % 8 == 0 ? 8 : (NHG % 4 == 0 ? 4 : 2);
+    static constexpr int NI = NHG / LPR;
+    static constexpr int RPW = VMI_WAVE / LPR;
+    static constexpr int RPB = (kThreads / VMI_WAVE) * RPW;
+};
+
+// sum_c q_c x_c over the 32 columns of one 16-byte chunk; xs points at the
+// chunk's first column in LDS.
+__device__ __forceinline__ float dot32_u4_f32(const vmi_u4& wv, const float* xs) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        uint32_t word = wv[m];
+        asm volatile("" : "+v"(word));
+        const float4 x0 = *reinterpret_cast<const float4*>(xs + 8 * m);
+        const float4 x1 = *reinterpret_cast<const float4*>(xs + 8 * m + 4);
+        acc = fmaf((float)(word & 15u), x0.x, acc);
+        acc = fmaf((float)((word >> 4) & 15u), x0.y, acc);
+        acc = fmaf((float)((word >> 8) & 15u), x0.z, acc);
+        acc = fmaf((float)((word >> 12) & 15u), x0.w, acc);
+        acc = fmaf((float)((word >> 16) & 15u), x1.x, acc);
+        acc = fmaf((float)((word >> 20) & 15u), x1.y, acc);
+        acc = fmaf((float)((word >> 24) & 15u), x1.z, acc);
+        acc = fmaf((float)(word >> 28), x1.w, acc);
+    }
+    return acc;
+}
+
+// Rows src + ridx[j] * LEN (j < kFTok, ridx < 0: zeros) into s[j] (chunk hg
+// at kFChunk * hg), then the fp32 sum of every 32-column chunk into sh[j].
+// All threads; ends synced.
+template <int LEN>
+__device__ __forceinline__ void stage_rows_f32(const float* __restrict__ src, const int (&ridx)[kFTok],
+                                               float (*s)[LEN / 32 * kFChunk], float (*sh)[LEN / 32]) {
+    const int tid = threadIdx.x;
+    __syncthreads();  // the previous chunk's readers are done
+    for (int i = tid; i < kFTok * (LEN / 4); i += kThreads) {
+        const int j = i / (LEN / 4), c4 = i - j * (LEN / 4);
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (ridx[j] >= 0) v = *reinterpret_cast<const float4*>(src + (size_t)ridx[j] * LEN + 4 * c4);
+        *reinterpret_cast<float4*>(&s[j][kFChunk * (c4 >> 3) + 4 * (c4 & 7)]) = v;
+    }
+    __syncthreads();
+    for (int i = tid; i < kFTok * (LEN / 32); i += kThreads) {
+        const int j = i / (LEN / 32), hg = i - j * (LEN / 32);
+        const float* xs = &s[j][kFChunk * hg];
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 32; c += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(xs + c);
+            acc += v.x;
+            acc += v.y;
+            acc += v.z;
+            acc += v.w;
+        }
+        sh[j][hg] = acc;
+    }
+    __syncthreads();
+}
+
+// One lane's share of a row times staged row j: its NI chunks, each
+// s * (q . x) + b * (x sum), then the row total over the LPR lanes.
+template <int LEN>
+__device__ __forceinline__ float row_dot_f32(const vmi_u4 (&wv)[FRow<LEN>::NI], const float (&sc)[FRow<LEN>::NI],
+                                             const float (&bi)[FRow<LEN>::NI], const float* s_row,
+                                             const float* sh_row, int part) {
+    using G = FRow<LEN>;
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < G::NI; ++i) {
+        const int hg = G::LPR * i + part;
+        const float d = dot32_u4_f32(wv[i], s_row + kFChunk * hg);
+        acc = fmaf(sc[i], d, acc);
+        acc = fmaf(bi[i], sh_row[hg], acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int o = 1; o < G::LPR; o <<= 1) acc += __shfl_xor(acc, o, VMI_WAVE);
+    return acc;
+}
+
+// row_dot_f32 of two matrices' rows (gate and up) over the same staged row,
+// chunk by chunk, so that each chunk of x is read from LDS once.
+template <int LEN>
+__device__ __forceinline__ void row_dot2_f32(const vmi_u4 (&w0)[FRow<LEN>::NI], const float (&s0)[FRow<LEN>::NI],
+                                             const float (&b0)[FRow<LEN>::NI], const vmi_u4 (&w1)[FRow<LEN>::NI],
+                                             const float (&s1)[FRow<LEN>::NI], const float (&b1)[FRow<LEN>::NI],
+                                             const float* s_row, const float* sh_row, int part, float& r0,
+                                             float& r1) {
+    using G = FRow<LEN>;
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < G::NI; ++i) {
+        const int hg = G::LPR * i + part;
+        const float* xs = s_row + kFChunk * hg;
+        float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            uint32_t u0 = w0[i][m], u1 = w1[i][m];
+            // opaque per call: keeps the compiler from converting every
+            // weight once, ahead of the token loop, into 64 * NI registers
+            asm volatile("" : "+v"(u0), "+v"(u1));
+            const float4 x0 = *reinterpret_cast<const float4*>(xs + 8 * m);
+            const float4 x1 = *reinterpret_cast<const float4*>(xs + 8 * m + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                d0 = fmaf((float)((u0 >> (4 * n)) & 15u), xv[n], d0);
+                d1 = fmaf((float)((u1 >> (4 * n)) & 15u), xv[n], d1);
+            }
+        }
+        const float xh = sh_row[hg];
+        a0 = fmaf(s0[i], d0, a0);
+        a0 = fmaf(b0[i], xh, a0);
+        a1 = fmaf(s1[i], d1, a1);
+        a1 = fmaf(b1[i], xh, a1);
+        // one chunk of x in registers at a time (hoisting every chunk's LDS
+        // reads ahead of the arithmetic would need 8 * NI registers a lane)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int o = 1; o < G::LPR; o <<= 1) {
+        a0 += __shfl_xor(a0, o, VMI_WAVE);
+        a1 += __shfl_xor(a1, o, VMI_WAVE);
+    }
+    r0 = a0;
+    r1 = a1;
+}
+
+// Weights, scales and biases of row `row` of matrix `mat` (uniform) of a
+// stack of rows x LEN matrices, the lane's NI chunks (chunk i at column
+// 32 * (LPR * i + part)).  The buffer resources span the whole matrix, so
+// they stay uniform; the row is in the per-lane offset.
+template <int LEN>
+__device__ __forceinline__ void load_row_f32(const vmi_qmat& m, int mat, int rows, int row, int part,
+                                             vmi_u4 (&wv)[FRow<LEN>::NI], float (&sc)[FRow<LEN>::NI],
+                                             float (&bi)[FRow<LEN>::NI]) {
+    using G = FRow<LEN>;
+    constexpr int NG = LEN / 64;
+    const size_t m0 = (size_t)mat * rows;
+    const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(m.w + m0 * (LEN / 8), (uint32_t)rows * (LEN / 2));
+    const __amdgpu_buffer_rsrc_t rs = vmi_rsrc(m.s + m0 * NG, (uint32_t)rows * NG * 2);
+    const __amdgpu_buffer_rsrc_t rb = vmi_rsrc(m.b + m0 * NG, (uint32_t)rows * NG * 2);
+    const uint32_t wrow = (uint32_t)row * (LEN / 2), srow = (uint32_t)row * NG * 2;
+#pragma unroll
+    for (int i = 0; i < G::NI; ++i) {
+        const int hg = G::LPR * i + part;
+        wv[i] = vmi_bload_b128_nt(rw, wrow + 16u * hg, 0);
+        sc[i] = __uint_as_float(vmi_bload_b16(rs, srow + 2u * (hg >> 1), 0) << 16);
+        bi[i] = __uint_as_float(vmi_bload_b16(rb, srow + 2u * (hg >> 1), 0) << 16);
+    }
+}
+
+// Gate/up + SwiGLU.  Item blockIdx.x = u * (I / RPB) + c: rows c*RPB.. of
+// distinct slot u's gate and up matrices for the tokens routed to it, in
+// chunks of kFTok tokens.  act row t*k + j (j the token's first rank on the
+// slot) receives the token's activations.  The first workgroup publishes the
+// route and prow[p] = the activation/output row of pair p (-1: bad slot).
+template <int H>
+__global__ __launch_bounds__(kThreads) void k_gateup_f32(GateUpArgs a, const float* __restrict__ x,
+                                                         float* __restrict__ act, int32_t* __restrict__ prow) {
+    using G = FRow<H>;
+    __shared__ float s_x[kFTok][H / 32 * kFChunk];
+    __shared__ float s_h[kFTok][H / 32];
+    __shared__ RouteLds R;
+    __shared__ int32_t s_first[kFirstTable];
+    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
+    const int part = lane % G::LPR, rr = lane / G::LPR;
+    const int I = a.I, NC = I / G::RPB, k = a.k;
+    route_slots(a, R, s_first);
+    const int item = blockIdx.x, u = item / NC, c = item - u * NC;
+    if (item == 0) {
+        publish_route(a, R);
+        if (tid < a.npairs) {
+            const int sl = R.slot[tid], t = tid / k;
+            int pr = -1;
+            if (sl >= 0)
+                for (int j = 0; j < k; ++j)
+                    if (R.slot[t * k + j] == sl) {
+                        pr = t * k + j;
+                        break;
+                    }
+            prow[tid] = pr;
+        }
+    }
+    if (u >= vmi_uniform(R.U)) return;
+    const int slot = vmi_uniform(R.uslot[u]);
+    uint32_t tmask = (uint32_t)vmi_uniform((int)R.umask[u]);
+    const int row = c * G::RPB + G::RPW * w + rr;
+
+    vmi_u4 gw[G::NI], uw[G::NI];
+    float gs[G::NI], gb[G::NI], us[G::NI], ub[G::NI];
+    load_row_f32<H>(a.gate, slot, I, row, part, gw, gs, gb);
+    load_row_f32<H>(a.up, slot, I, row, part, uw, us, ub);
+
+    while (tmask) {  // uniform: chunks of up to kFTok of the slot's tokens
+        int ridx[kFTok];
+#pragma unroll
+        for (int j = 0; j < kFTok; ++j) {
+            ridx[j] = tmask ? __builtin_ctz(tmask) : -1;
+            tmask &= tmask ? tmask - 1u : 0u;
+        }
+        stage_rows_f32<H>(x, ridx, s_x, s_h);
+#pragma unroll 1
+        for (int j = 0; j < kFTok; ++j) {
+            if (ridx[j] < 0) break;
+            float g, v;
+            row_dot2_f32<H>(gw, gs, gb, uw, us, ub, s_x[j], s_h[j], part, g, v);
+            if (part == 0) {
+                const int t = ridx[j];
+                int pr = t * k;
+                for (int jj = 0; jj < k; ++jj)
+                    if (R.slot[t * k + jj] == slot) {
+                        pr = t * k + jj;
+                        break;
+                    }
+                act[(size_t)pr * I + row] = g * (1.0f / (1.0f + expf(-g))) * v;
+            }
+        }
+    }
+}
+
+// Down projection.  Item blockIdx.x = u * (H / RPB) + c: rows c*RPB.. of
+// distinct slot u's down matrix times the activation row of every token
+// routed to it, into output row t*k + jr[u][t].
+template <int I>
+__global__ __launch_bounds__(kThreads) void k_down_f32(const RouteInfo* __restrict__ route, vmi_qmat down, int T,
+                                                       int k, int H, const float* __restrict__ act,
+                                                       float* __restrict__ y) {
+    using G = FRow<I>;
+    __shared__ float s_a[kFTok][I / 32 * kFChunk];
+    __shared__ float s_h[kFTok][I / 32];
+    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
+    const int part = lane % G::LPR, rr = lane / G::LPR;
+    const int NC = H / G::RPB;
+    const int item = blockIdx.x, u = item / NC, c = item - u * NC;
+    if (u >= vmi_uniform(route->U)) return;
+    const int slot = vmi_uniform(route->uslot[u]);
+    const int row = c * G::RPB + G::RPW * w + rr;
+    vmi_u4 dw[G::NI];
+    float ds[G::NI], db[G::NI];
+    load_row_f32<I>(down, slot, H, row, part, dw, ds, db);
+    int t0 = 0;
+    while (true) {  // uniform: the next kFTok tokens with a pair on u
+        int ridx[kFTok], orow[kFTok];
+        int n = 0;
+        for (; t0 < T && n < kFTok; ++t0) {
+            const int jr = route->jr[u][t0];
+            if (jr >= 0) {
+                ridx[n] = t0 * k + jr;
+                orow[n] = ridx[n];
+                ++n;
+            }
+        }
+        if (n == 0) break;
+        for (int j = n; j < kFTok; ++j) ridx[j] = orow[j] = -1;
+        stage_rows_f32<I>(act, ridx, s_a, s_h);
+#pragma unroll 1
+        for (int j = 0; j < kFTok; ++j) {
+            if (orow[j] < 0) break;
+            const float v = row_dot_f32<I>(dw, ds, db, s_a[j], s_h[j], part);
+            if (part == 0) y[(size_t)orow[j] * H + row] = v;
+        }
+    }
+}
+
+// out[t][h] = sum over j in order of y[prow[t*k+j]][h] * scores[t*k+j]
+// (reduce_pairs, fused_moe.cpp:286-298); a pair with a bad slot adds nothing.
+__global__ __launch_bounds__(kThreads) void k_combine_f32(const int32_t* __restrict__ prow,
+                                                          const float* __restrict__ scores,
+                                                          const float* __restrict__ y, int T, int k, int H,
+                                                          void* out, int out_dtype) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= T * H) return;
+    const int t = i / H, h = i - t * H;
+    float acc = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        const int pr = prow[t * k + j];
+        if (pr >= 0) acc += y[(size_t)pr * H + h] * scores[t * k + j];
+    }
+    if (out_dtype == VMI_F32)
+        reinterpret_cast<float*>(out)[i] = acc;
+    else
+        reinterpret_cast<uint16_t*>(out)[i] = vmi_f32_to_bf16(acc);
+}
+
 // ---------------------------------------------------------------- host
 bool aligned(const void* p, size_t n) { return ((uintptr_t)p % n) == 0; }
 
@@ -1344,6 +1671,70 @@ hipError_t launch_down(const DownArgs& da, hipStream_t s) {
     return launch_down_t<8, 2, 2>(da, s);
 }
 
+// Workspace of the fp32 operator path: the status word and route table at the
+// offsets carve_workspace gives them, then the pair rows.
+struct F32Workspace {
+    uint32_t* status;
+    RouteInfo* route;
+    int32_t* prow;  // [T*k]
+    float* act;     // [T*k, I]
+    float* y;       // [T*k, H]
+    size_t bytes;
+};
+
+F32Workspace carve_f32(void* base, int T, int k, int H, int I) {
+    F32Workspace w{};
+    char* p = static_cast<char*>(base);
+    size_t off = 0;
+    auto take = [&](size_t n) -> char* {
+        char* r = p ? p + off : nullptr;
+        off += vmi::align256(n);
+        return r;
+    };
+    const size_t np = (size_t)T * k;
+    w.status = reinterpret_cast<uint32_t*>(take(256));
+    w.route = reinterpret_cast<RouteInfo*>(take(sizeof(RouteInfo)));
+    w.prow = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * np));
+    w.act = reinterpret_cast<float*>(take(sizeof(float) * np * I));
+    w.y = reinterpret_cast<float*>(take(sizeof(float) * np * H));
+    w.bytes = off;
+    return w;
+}
+
+template <int I>
+void launch_down_f32_t(const F32Workspace& ws, vmi_qmat down, int T, int k, int H, hipStream_t s) {
+    const dim3 grid(T * k * (H / FRow<I>::RPB));
+    hipLaunchKernelGGL((k_down_f32<I>), grid, dim3(kThreads), 0, s, ws.route, down, T, k, H, ws.act, ws.y);
+}
+
+hipError_t launch_moe_f32(const GateUpArgs& ga, const float* x, vmi_qmat down, int H, const F32Workspace& ws,
+                          void* out, int out_dtype, hipStream_t s) {
+    const int T = ga.T, k = ga.k, I = ga.I;
+    const dim3 ggrid(T * k * (I / FRow<512>::RPB));
+    switch (H) {
+        case 512: hipLaunchKernelGGL((k_gateup_f32<512>), ggrid, dim3(kThreads), 0, s, ga, x, ws.act, ws.prow); break;
+        case 1024: hipLaunchKernelGGL((k_gateup_f32<1024>), ggrid, dim3(kThreads), 0, s, ga, x, ws.act, ws.prow); break;
+        default: hipLaunchKernelGGL((k_gateup_f32<2048>), ggrid, dim3(kThreads), 0, s, ga, x, ws.act, ws.prow); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    switch (I / 64) {
+        case 1: launch_down_f32_t<64>(ws, down, T, k, H, s); break;
+        case 2: launch_down_f32_t<128>(ws, down, T, k, H, s); break;
+        case 3: launch_down_f32_t<192>(ws, down, T, k, H, s); break;
+        case 4: launch_down_f32_t<256>(ws, down, T, k, H, s); break;
+        case 5: launch_down_f32_t<320>(ws, down, T, k, H, s); break;
+        case 6: launch_down_f32_t<384>(ws, down, T, k, H, s); break;
+        case 7: launch_down_f32_t<448>(ws, down, T, k, H, s); break;
+        default: launch_down_f32_t<512>(ws, down, T, k, H, s); break;
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_combine_f32, dim3((T * H + kThreads - 1) / kThreads), dim3(kThreads), 0, s, ws.prow,
+                       ga.in_scores, ws.y, T, k, H, out, out_dtype);
+    return hipGetLastError();
+}
+
 template <typename XT>
 void launch_prep(const PrepArgs& pa, hipStream_t s) {
     const dim3 grid(pa.T);
@@ -1385,7 +1776,9 @@ MoeWorkspace carve_workspace(void* base, int T, int k, int hidden, int inter, in
 
 extern "C" size_t vmi_fused_moe_slots_workspace_bytes(int T, int k, int hidden, int inter) {
     if (T <= 0 || k <= 0 || hidden <= 0 || inter <= 0) return 0;
-    return vmi::carve_workspace(nullptr, T, k, hidden, inter, 0).bytes;
+    const size_t b16 = vmi::carve_workspace(nullptr, T, k, hidden, inter, 0).bytes;
+    const size_t f32 = carve_f32(nullptr, T, k, hidden, inter).bytes;
+    return b16 > f32 ? b16 : f32;
 }
 
 extern "C" size_t vmi_moe_layer_workspace_bytes(int T, int top_k, int hidden, int inter, int num_experts) {
@@ -1412,10 +1805,24 @@ int fused_moe_pairs(const void* x, int x_dtype, bool staged, const int32_t* loca
     if (!qmat_ok(gate) || !qmat_ok(up) || !qmat_ok(down))
         return vmi::fail(VMI_ERR_INVALID, "weight arrays must be non-null and 16-byte aligned");
     if (cap <= 0) return vmi::fail(VMI_ERR_INVALID, "cap=%d", cap);
-    const vmi::MoeWorkspace ws = vmi::carve_workspace(workspace, T, k, hidden, inter, 0);
-    if (!workspace || workspace_bytes < ws.bytes)
-        return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", ws.bytes, workspace_bytes);
+    const size_t need = vmi_fused_moe_slots_workspace_bytes(T, k, hidden, inter);
+    if (!workspace || workspace_bytes < need)
+        return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", need, workspace_bytes);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (x_dtype == VMI_F32) {
+        // the reference operator's fp32 arithmetic throughout
+        const F32Workspace fw = carve_f32(workspace, T, k, hidden, inter);
+        GateUpArgs ga{};
+        ga.T = T; ga.I = inter; ga.k = k; ga.E = 0; ga.npairs = T * k; ga.has_shared = 0;
+        ga.from_slots = 1; ga.norm = 1; ga.cap = cap;
+        ga.slots = local_slots; ga.in_scores = scores;
+        ga.gate = gate; ga.up = up; ga.sh_gate = gate; ga.sh_up = up;
+        ga.route = fw.route; ga.status = fw.status;
+        const hipError_t e = launch_moe_f32(ga, static_cast<const float*>(x), down, hidden, fw, out, out_dtype, s);
+        if (e != hipSuccess) return vmi::hip_fail(e, "fp32 MoE launch");
+        return VMI_OK;
+    }
+    const vmi::MoeWorkspace ws = vmi::carve_workspace(workspace, T, k, hidden, inter, 0);
     const OperandOut ops{ws.xop, ws.xsum, ws.fscale};
 
     const PrepArgs pa{x, T, hidden, ops};
