@@ -37,10 +37,12 @@ def test_python_binding_covers_header():
 
 def test_version_and_workspace_queries(lib):
     assert lib.vmi_version() == 1
-    # at least the per-(distinct slot, token) fp16 activation operands of the down projection
+    # at least the per-(distinct slot, token) bf16 activation operands of the down projection,
+    # and the fp32 path's activation and output rows per pair
     assert lib.vmi_fused_moe_slots_workspace_bytes(4, 10, 2048, 512) >= (4 * 10 + 1) * 4 * 512 * 2
-    assert lib.vmi_moe_layer_workspace_bytes(4, 10, 2048, 512, 512) > lib.vmi_fused_moe_slots_workspace_bytes(
-        4, 10, 2048, 512)
+    assert lib.vmi_fused_moe_slots_workspace_bytes(4, 10, 2048, 512) >= 4 * 10 * (512 + 2048) * 4
+    # the whole layer also holds the router logits [T, E]
+    assert lib.vmi_moe_layer_workspace_bytes(4, 10, 2048, 512, 512) >= (4 * 10 + 1) * 4 * 512 * 2 + 4 * 512 * 4
     assert lib.vmi_fused_moe_slots_workspace_bytes(0, 10, 2048, 512) == 0
 
 
