@@ -20,6 +20,12 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
+# Per-source additions.  The prefill GEMMs scale every MFMA result by FMA:
+# MFMA results in VGPRs (not accumulation registers) save a copy per value.
+SOURCE_FLAGS = {
+    "vmi_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -37,7 +43,7 @@ def build_library(verbose: bool = False) -> Path:
     procs = []
     for src in SOURCES:
         obj = objdir / (Path(src).stem + ".o")
-        cmd = [cc, *HIP_FLAGS, f"-I{ROOT / 'include'}", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), f"-I{ROOT / 'include'}", "-c", str(CSRC / src), "-o", str(obj)]
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
         objs.append(obj)
     for cmd, p in procs:

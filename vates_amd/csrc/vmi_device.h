@@ -240,6 +240,37 @@ __device__ __forceinline__ bool vmi_better(float a, int ia, float b, int ib) {
     return ia < ib;
 }
 
+// Affine-bias term sum_g b[row][g] * X[t][g] as one bf16 MFMA: X is split into
+// bf16 hi + mid + lo (24 significant bits); lane block q carries two groups:
+//   A = [hi(X0), mid(X0), lo(X0), 0, hi(X1), mid(X1), lo(X1), 0]
+//   B = [b0, b0, b0, 0, b1, b1, b1, 0]   (b0/b1 = low/high bf16 of one word)
+__device__ __forceinline__ void vmi_split3_bf16(float x, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+    hi = vmi_f32_to_bf16(x);
+    const float r1 = x - vmi_bf16_to_f32(hi);
+    mid = vmi_f32_to_bf16(r1);
+    lo = vmi_f32_to_bf16(r1 - vmi_bf16_to_f32(mid));
+}
+__device__ __forceinline__ vmi_u4 vmi_bias_a_operand(float x0, float x1) {
+    uint32_t h0, m0, l0, h1, m1, l1;
+    vmi_split3_bf16(x0, h0, m0, l0);
+    vmi_split3_bf16(x1, h1, m1, l1);
+    vmi_u4 r;
+    r[0] = h0 | (m0 << 16);
+    r[1] = l0;
+    r[2] = h1 | (m1 << 16);
+    r[3] = l1;
+    return r;
+}
+__device__ __forceinline__ vmi_u4 vmi_bias_b_operand(uint32_t bb) {
+    const uint32_t b0 = bb & 0xffffu, b1 = bb >> 16;
+    vmi_u4 r;
+    r[0] = b0 | (b0 << 16);
+    r[1] = b0;
+    r[2] = b1 | (b1 << 16);
+    r[3] = b1;
+    return r;
+}
+
 // ------------------------------------------------------- direct-to-LDS loads
 // global_load_lds: lane l's `size` bytes from its own global address land at
 // lds + size*l (lds is wave-uniform); vmcnt counts the copy until the bytes are

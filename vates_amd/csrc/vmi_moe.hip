@@ -90,37 +90,6 @@ __device__ __forceinline__ vmi_u4 make_act_operand(const float (&xv)[8], float f
     return r;
 }
 
-// Affine-bias term sum_g b[row][g] * X[t][g] as one bf16 MFMA: X is split into
-// bf16 hi + mid + lo (24 significant bits); lane block q carries two groups:
-//   A = [hi(X0), mid(X0), lo(X0), 0, hi(X1), mid(X1), lo(X1), 0]
-//   B = [b0, b0, b0, 0, b1, b1, b1, 0]   (b0/b1 = low/high bf16 of one word)
-__device__ __forceinline__ void split3_bf16(float x, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
-    hi = vmi_f32_to_bf16(x);
-    const float r1 = x - vmi_bf16_to_f32(hi);
-    mid = vmi_f32_to_bf16(r1);
-    lo = vmi_f32_to_bf16(r1 - vmi_bf16_to_f32(mid));
-}
-__device__ __forceinline__ vmi_u4 bias_a_operand(float x0, float x1) {
-    uint32_t h0, m0, l0, h1, m1, l1;
-    split3_bf16(x0, h0, m0, l0);
-    split3_bf16(x1, h1, m1, l1);
-    vmi_u4 r;
-    r[0] = h0 | (m0 << 16);
-    r[1] = l0;
-    r[2] = h1 | (m1 << 16);
-    r[3] = l1;
-    return r;
-}
-__device__ __forceinline__ vmi_u4 bias_b_operand(uint32_t bb) {
-    const uint32_t b0 = bb & 0xffffu, b1 = bb >> 16;
-    vmi_u4 r;
-    r[0] = b0 | (b0 << 16);
-    r[1] = b0;
-    r[2] = b1 | (b1 << 16);
-    r[3] = b1;
-    return r;
-}
-
 template <typename XT>
 __device__ __forceinline__ void load_x8(const XT* __restrict__ row, int c, float (&v)[8]);
 
@@ -938,9 +907,9 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int g0 = 2 * NB * q + 2 * b;
-        const vmi_u4 ab = (r < T) ? bias_a_operand(s_xs[r][g0], s_xs[r][g0 + 1]) : zero4;
-        bgd = vmi_mfma_bf16(ab, bias_b_operand(bgw[b]), bgd);
-        bud = vmi_mfma_bf16(ab, bias_b_operand(buw[b]), bud);
+        const vmi_u4 ab = (r < T) ? vmi_bias_a_operand(s_xs[r][g0], s_xs[r][g0 + 1]) : zero4;
+        bgd = vmi_mfma_bf16(ab, vmi_bias_b_operand(bgw[b]), bgd);
+        bud = vmi_mfma_bf16(ab, vmi_bias_b_operand(buw[b]), bud);
     }
     // SwiGLU of token t = 4*(lane/16) + e, row 16w + r of the slice
     const int tq = lane >> 4;

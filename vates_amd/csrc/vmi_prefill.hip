@@ -14,12 +14,12 @@
 //   k_pf_sgate    shared-expert gate logit per token (one wave per token)
 //   k_pf_topk     one wave per token: top-k, softmax, renorm, slot table
 //   k_pf_count    routes per slot and each route's rank in its slot
-//   k_pf_scan     exclusive scan of the counts, the list of 64-row M tiles
+//   k_pf_scan     exclusive scan of the counts, the list of 128-row M tiles
 //   k_pf_place    every routed (token, rank) into its slot's list
-//   k_pf_gateup   per (M tile, 64 intermediate rows): gate and up MFMA GEMMs
+//   k_pf_gateup3  per (M tile, 128 intermediate rows): gate and up MFMA GEMMs
 //                 over the tile's gathered tokens, SwiGLU, bf16 operands of
 //                 the activations and their per-group sums
-//   k_pf_down     per (M tile, 64 hidden rows): down MFMA GEMM, times the
+//   k_pf_down3    per (M tile, 128 hidden rows): down MFMA GEMM, times the
 //                 route's combine weight, one bf16 row per (token, rank)
 //   k_pf_combine  out[t] = sum over ranks 0..k (rank k: the gated shared
 //                 expert) in rank order, fp32, + residual
@@ -39,7 +39,8 @@
 namespace {
 
 constexpr int kPfThreads = 256;
-constexpr int kTileM = 64;
+constexpr int kTileM = 64;   // tokens per router tile
+constexpr int kTM3 = 128;    // routes per tile of the expert GEMMs
 constexpr int kPfMaxE = 1024;
 constexpr int kPfMaxK = 16;
 
@@ -200,9 +201,9 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
 }
 
 // ------------------------------------------------------- grouped GEMM core
-// One wave accumulates a 16 (rows) x 16 (output features) tile over the
+// One wave accumulates 16 (rows) x 16 (output features) tiles over the
 // quantisation groups of K: per group two MFMAs with the group's weights as
-// exact subnormals, then acc += D * scale * 2^24 + bias * operand_sum.
+// exact subnormals, then acc += D * scale * 2^24 (+ the affine-bias term).
 // Lane l: A row m = l%16 (rows of the tile), K block q = l/16; B column
 // n = l%16; D rows 4q + r, column n.
 
@@ -393,7 +394,7 @@ __global__ __launch_bounds__(1024) void k_pf_scan(PfArgs a) {
     const int tid = threadIdx.x;
     const int c = tid < a.cap ? a.counts[tid] : 0;
     s_cnt[tid] = c;
-    s_tl[tid] = (c + kTileM - 1) / kTileM;
+    s_tl[tid] = (c + kTM3 - 1) / kTM3;
     __syncthreads();
     // inclusive Hillis-Steele scans of counts and tile counts
     for (int o = 1; o < 1024; o <<= 1) {
@@ -405,17 +406,17 @@ __global__ __launch_bounds__(1024) void k_pf_scan(PfArgs a) {
         __syncthreads();
     }
     const int off = s_cnt[tid] - c;
-    const int ntl = (c + kTileM - 1) / kTileM;
+    const int ntl = (c + kTM3 - 1) / kTM3;
     const int toff = s_tl[tid] - ntl;
     if (tid < a.cap) {
         a.offsets[tid] = off;
         for (int i = 0; i < ntl; ++i)
-            a.tiles[toff + i] = make_int4(tid, off + i * kTileM, min(kTileM, c - i * kTileM), 0);
+            a.tiles[toff + i] = make_int4(tid, off + i * kTM3, min(kTM3, c - i * kTM3), 0);
     }
     const int routed_tiles = s_tl[1023];
-    const int sh_tiles = a.has_shared ? (a.T + kTileM - 1) / kTileM : 0;
+    const int sh_tiles = a.has_shared ? (a.T + kTM3 - 1) / kTM3 : 0;
     for (int i = tid; i < sh_tiles; i += 1024)
-        a.tiles[routed_tiles + i] = make_int4(-1, i * kTileM, min(kTileM, a.T - i * kTileM), 0);
+        a.tiles[routed_tiles + i] = make_int4(-1, i * kTM3, min(kTM3, a.T - i * kTM3), 0);
     if (tid == 0) a.ntiles[0] = routed_tiles + sh_tiles;
 }
 
@@ -469,304 +470,240 @@ __device__ __forceinline__ int tile_route(const PfArgs& a, const int4& tl, int i
     return tl.x >= 0 ? a.list[tl.y + i] : (tl.y + i) * (a.k + 1) + a.k;
 }
 
-// ---------------------------------------------------------------- gate/up
-// Grid (max_tiles, I/64), 4 waves; wave w: tile rows 16w..16w+15, the 64
-// intermediate rows of the N tile (4 subtiles) in gate and in up.
-__global__ __launch_bounds__(kPfThreads) void k_pf_gateup(PfArgs a) {
-    __shared__ float s_act[kTileM][64 + 1];
-    __shared__ int s_route[kTileM];
-    const int ti = blockIdx.x;
-    if (ti >= a.ntiles[0]) return;
-    const int4 tl = a.tiles[ti];
-    const int lane = threadIdx.x & 63, w = pf_wave(), tid = threadIdx.x;
-    const int m = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.y * 64;
-    if (tid < kTileM) s_route[tid] = tile_route(a, tl, tid);
-    __syncthreads();
-    const vmi_qmat G = tl.x >= 0 ? a.gate : a.sh_gate;
-    const vmi_qmat U = tl.x >= 0 ? a.up : a.sh_up;
-    const size_t mat = tl.x >= 0 ? (size_t)tl.x : 0;
-    const int H = a.H, HW = H / 8, NG = H / 64;
-    const int my_route = s_route[16 * w + m];
-    const int my_tok = my_route >= 0 ? my_route / (a.k + 1) : 0;
-    const vmi_u4* arow = a.xop4 + (size_t)my_tok * HW;
-    int rtok[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int rr = s_route[16 * w + 4 * q + r];
-        rtok[r] = rr >= 0 ? rr / (a.k + 1) : -1;
-    }
-    vmi_f4 ag[4], au[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) ag[s] = au[s] = vmi_f4{0.f, 0.f, 0.f, 0.f};
-    const size_t wrow0 = mat * (size_t)a.I + n0;  // first weight row of the N tile
-    for (int g = 0; g < NG; ++g) {
-        vmi_u4 a0 = arow[8 * g + 2 * q], a1 = arow[8 * g + 2 * q + 1];
-        if (my_route < 0) a0 = a1 = vmi_u4{0u, 0u, 0u, 0u};
-        float xsr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xsr[r] = rtok[r] >= 0 ? a.xsum4[(size_t)rtok[r] * NG + g] : 0.0f;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const size_t row = wrow0 + 16 * s + m;
-            const uint2 wg = *reinterpret_cast<const uint2*>(G.w + row * HW + 8 * g + 2 * q);
-            const uint2 wu = *reinterpret_cast<const uint2*>(U.w + row * HW + 8 * g + 2 * q);
-            vmi_f4 dg = vmi_mfma_f16(a0, vmi_unpack_u4_f16(wg.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
-            dg = vmi_mfma_f16(a1, vmi_unpack_u4_f16(wg.y), dg);
-            vmi_f4 du = vmi_mfma_f16(a0, vmi_unpack_u4_f16(wu.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
-            du = vmi_mfma_f16(a1, vmi_unpack_u4_f16(wu.y), du);
-            const float sg = vmi_bf16_to_f32(G.s[row * NG + g]) * 16777216.0f;
-            const float bg = vmi_bf16_to_f32(G.b[row * NG + g]);
-            const float su = vmi_bf16_to_f32(U.s[row * NG + g]) * 16777216.0f;
-            const float bu = vmi_bf16_to_f32(U.b[row * NG + g]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ag[s][r] = fmaf(dg[r], sg, fmaf(bg, xsr[r], ag[s][r]));
-                au[s][r] = fmaf(du[r], su, fmaf(bu, xsr[r], au[s][r]));
-            }
-        }
-    }
-    // SwiGLU into LDS: act[row][col], rows 16w + 4q + r, cols 16 s + m
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float inv = rtok[r] >= 0 ? 1.0f / a.fscale[rtok[r]] : 0.0f;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const float gv = ag[s][r] * inv, uv = au[s][r] * inv;
-            const float act = gv / (1.0f + expf(-gv)) * uv;
-            s_act[16 * w + 4 * q + r][16 * s + m] = act;
-        }
-    }
-    __syncthreads();
-    // bf16 operands: thread -> (row, word of 8 columns): 64 rows x 8 words
-    const int IW = a.I / 8, IG = a.I / 64;
-    for (int i = tid; i < kTileM * 8; i += kPfThreads) {
-        const int row = i >> 3, wd = i & 7;
-        const int route = s_route[row];
-        if (route < 0) continue;
-        float v[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) v[c] = vmi_bf16_to_f32(vmi_f32_to_bf16(s_act[row][8 * wd + c]));
-        // slot order of vmi_unpack_u4_bf16_128: {0,4,1,5,2,6,3,7}
-        vmi_u4 o;
-        o[0] = (uint32_t)vmi_f32_to_bf16(v[0]) | ((uint32_t)vmi_f32_to_bf16(v[4]) << 16);
-        o[1] = (uint32_t)vmi_f32_to_bf16(v[1]) | ((uint32_t)vmi_f32_to_bf16(v[5]) << 16);
-        o[2] = (uint32_t)vmi_f32_to_bf16(v[2]) | ((uint32_t)vmi_f32_to_bf16(v[6]) << 16);
-        o[3] = (uint32_t)vmi_f32_to_bf16(v[3]) | ((uint32_t)vmi_f32_to_bf16(v[7]) << 16);
-        a.actop[(size_t)route * IW + (n0 >> 3) + wd] = o;
-    }
-    // per-group sums of the bf16 activations: one group = this N tile
-    if (tid < kTileM) {
-        const int route = s_route[tid];
-        if (route >= 0) {
-            float sum = 0.0f;
-            for (int c = 0; c < 64; ++c) sum += vmi_bf16_to_f32(vmi_f32_to_bf16(s_act[tid][c]));
-            a.axs[(size_t)route * IG + (n0 >> 6)] = sum;
-        }
-    }
-}
-
-// ------------------------------------------------------------------ down
-// Grid (max_tiles, H/64), 4 waves: wave w tile rows 16w..16w+15, 64 hidden
-// rows (4 subtiles).  bf16 MFMA with weights 128 + q (exact) and the
-// correction y = sum_g s (D_g - 128 A_g) + b A_g, A_g the group's act sum.
-__global__ __launch_bounds__(kPfThreads) void k_pf_down(PfArgs a) {
-    __shared__ int s_route[kTileM];
-    const int ti = blockIdx.x;
-    if (ti >= a.ntiles[0]) return;
-    const int4 tl = a.tiles[ti];
-    const int lane = threadIdx.x & 63, w = pf_wave(), tid = threadIdx.x;
-    const int m = lane & 15, q = lane >> 4;
-    const int h0 = blockIdx.y * 64;
-    if (tid < kTileM) s_route[tid] = tile_route(a, tl, tid);
-    __syncthreads();
-    const vmi_qmat D = tl.x >= 0 ? a.down : a.sh_down;
-    const size_t mat = tl.x >= 0 ? (size_t)tl.x : 0;
-    const int IW = a.I / 8, IG = a.I / 64;
-    const int my_route = s_route[16 * w + m];
-    const vmi_u4* arow = a.actop + (size_t)(my_route >= 0 ? my_route : 0) * IW;
-    int rr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) rr[r] = s_route[16 * w + 4 * q + r];
-    vmi_f4 acc[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) acc[s] = vmi_f4{0.f, 0.f, 0.f, 0.f};
-    const size_t drow0 = mat * (size_t)a.H + h0;
-    for (int g = 0; g < IG; ++g) {
-        vmi_u4 a0 = arow[8 * g + 2 * q], a1 = arow[8 * g + 2 * q + 1];
-        if (my_route < 0) a0 = a1 = vmi_u4{0u, 0u, 0u, 0u};
-        float asr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) asr[r] = rr[r] >= 0 ? a.axs[(size_t)rr[r] * IG + g] : 0.0f;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const size_t row = drow0 + 16 * s + m;
-            const uint2 wd = *reinterpret_cast<const uint2*>(D.w + row * IW + 8 * g + 2 * q);
-            vmi_f4 d = vmi_mfma_bf16(a0, vmi_unpack_u4_bf16_128(wd.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
-            d = vmi_mfma_bf16(a1, vmi_unpack_u4_bf16_128(wd.y), d);
-            const float sc = vmi_bf16_to_f32(D.s[row * IG + g]);
-            const float bi = vmi_bf16_to_f32(D.b[row * IG + g]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[s][r] = fmaf(sc, fmaf(-128.0f, asr[r], d[r]), fmaf(bi, asr[r], acc[s][r]));
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int route = rr[r];
-        if (route < 0) continue;
-        const int t = route / (a.k + 1), j = route - t * (a.k + 1);
-        float wgt;
-        if (j < a.k) {
-            wgt = a.scores[t * a.k + j];
-        } else {
-            wgt = a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f;
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) a.ybuf[(size_t)route * a.H + h0 + 16 * s + m] = vmi_f32_to_bf16(acc[s][r] * wgt);
-    }
-}
-
-// ------------------------------------------- pipelined grouped GEMMs
-// Both GEMMs stream their weights one quantisation group (64 K values, 32 B
-// per row) at a time through a ring of 4 LDS slots of 4 KB: every thread moves
-// one 16-byte piece per group with global_load_lds (opaque to the compiler's
-// wait-count pass; ordered by explicit vmcnt waits), prefetch distance 3
-// groups.  Row r's 16-byte halves are swapped when bit 3 of r is set, so the
-// 8-byte operand reads of 16 consecutive rows hit distinct banks.  Per-group
-// scales (times 2^24 for the subnormal operands) and biases, and the operand
-// sums of the tile's rows, are loaded into LDS once per tile.
-
-constexpr int kRing = 4;
 constexpr int kMaxG = 32;  // quantisation groups along K (K <= 2048)
+
+// s_waitcnt vmcnt(N): the GEMMs' LDS copies are inline assembly the
+// compiler does not count, so the ring orders them itself.
 
 template <int N>
 __device__ __forceinline__ void pf_wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Byte offset of 8-byte unit `unit8` (0..3) of packed weight row `row` inside
+// a slot: the row's 16-byte halves are swapped when bit 3 of the row is set,
+// so the 8-byte operand reads of 16 consecutive rows hit distinct banks.
 __device__ __forceinline__ uint32_t ring_off(int row, int unit8) {
-    // byte offset of 8-byte unit `unit8` (0..3) of row `row` inside a slot
     return 32u * row + 16u * (((unsigned)unit8 >> 1) ^ (((unsigned)row >> 3) & 1u)) + 8u * (unit8 & 1);
 }
 
-struct Ring {
-    uint8_t* s0;
-    uint8_t* s1;
-    uint8_t* s2;
-    uint8_t* s3;
-    __device__ __forceinline__ uint8_t* at(int u) const { return u == 0 ? s0 : u == 1 ? s1 : u == 2 ? s2 : s3; }
-};
+// ----------------------------------------------- 128 x 128 tile GEMMs
+// Both GEMMs run one workgroup per (tile of 128 routes, 128 output rows)
+// with four waves in a 2 x 2 grid: wave (mh, nh) owns routes 64mh..64mh+63
+// (four 16-row MFMA blocks) and output rows 64nh..64nh+63 (four 16-column
+// blocks), so every unpacked weight operand feeds four MFMAs.  K streams one
+// quantisation group (64 values) per stage through a ring of kPfStages LDS
+// slots filled by global_load_lds: the A operands (128 routes x 128 bytes)
+// and the packed weights (rows x 32 bytes), each thread moving whole 16-byte
+// pieces.  A slot's A row r keeps its 16-byte piece c at position c ^ (r & 7),
+// so the 16 rows one MFMA operand read touches start on distinct banks; the
+// weight rows keep the half-swap on bit 3 of the row.  Per stage and output
+// element the only VALU work is one FMA with the group's scale; the affine
+// bias term sum_g b_g X_g goes through bf16 MFMAs once at the end (X split
+// into hi + mid + lo bf16, 24 significant bits).  Workgroup L runs tile
+// 8*(L/8/NB) + L%8 and column block (L/8)%NB: the column blocks of one tile
+// share an XCD, so its A rows reach that L2 once.
+constexpr int kPfStages = 2;   // LDS ring depth: kPfStages - 1 groups in flight
+constexpr int kPfA = kTM3 * 128;
 
-// Gate/up: tile M 64 routes x N 64 intermediate rows, gate and up.
-__global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup2(PfArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t r0[4096], r1[4096], r2[4096], r3[4096];
-    __shared__ __attribute__((aligned(16))) float2 s_sb[kMaxG][2][64];
-    __shared__ __attribute__((aligned(16))) float s_xs[kMaxG][kTileM];
-    __shared__ float s_act[kTileM][64 + 1];
-    __shared__ int s_route[kTileM];
-    __shared__ int s_tok[kTileM];
-    const int ti = blockIdx.x;
+__device__ __forceinline__ void pf_tile_of(int L, int nb_count, int& ti, int& nb) {
+    const int xcd = L & 7, idx = L >> 3;
+    ti = 8 * (idx / nb_count) + xcd;
+    nb = idx % nb_count;
+}
+
+// byte offset of A row r, logical 16-byte piece c, inside a slot
+__device__ __forceinline__ uint32_t pf_a_off(int r, int c) { return 16u * (8u * r + (unsigned)(c ^ (r & 7))); }
+
+// Gate/up: tile 128 routes x 128 intermediate rows of gate and of up (256
+// weight rows per stage), K = H.  Then SwiGLU, the bf16 down-projection
+// operands of the activations and their per-group sums.
+__global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
+    constexpr int kB = 256 * 32;
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[kPfStages * (kPfA + kB)];
+    __shared__ uint16_t s_scale[kMaxG][256];  // bf16 bits
+    __shared__ int s_route[kTM3];
+    __shared__ int s_tok[kTM3];
+    const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
+    const int n = lane & 15, q = lane >> 4;
+    const int mh = w & 1, nh = w >> 1;
+    const int NB = (a.I + 127) / 128;
+    int ti, nb;
+    pf_tile_of(blockIdx.x, NB, ti, nb);
     if (ti >= a.ntiles[0]) return;
     const int4 tl = a.tiles[ti];
-    const int lane = threadIdx.x & 63, w = pf_wave(), tid = threadIdx.x;
-    const int n = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.y * 64;
-    const int H = a.H, HW = H / 8, G = H / 64;
+    const int H = a.H, HW = H / 8, G = H / 64, I = a.I;
+    const int n0 = nb * 128, nvalid = min(128, I - n0);
     const vmi_qmat Gm = tl.x >= 0 ? a.gate : a.sh_gate;
     const vmi_qmat Um = tl.x >= 0 ? a.up : a.sh_up;
-    const size_t row0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)a.I + n0;
-    if (tid < kTileM) {
+    const size_t mrow0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)I;
+    if (tid < kTM3) {
         const int rt = tile_route(a, tl, tid);
         s_route[tid] = rt;
         s_tok[tid] = rt >= 0 ? rt / (a.k + 1) : 0;
     }
-    // scales / biases: 2 matrices x {s, b} x 64 rows x G groups, 16-byte loads of 8 groups
-    for (int i = tid; i < 2 * 2 * 64 * (G / 8); i += kPfThreads) {
-        const int chunk = i % (G / 8), row = (i / (G / 8)) % 64, sb = (i / (G / 8 * 64)) % 2, mt = i / (G / 8 * 128);
-        const vmi_qmat& M = mt == 0 ? Gm : Um;
-        const uint16_t* src = (sb == 0 ? M.s : M.b) + (row0 + row) * G + 8 * chunk;
-        const uint4 v = *reinterpret_cast<const uint4*>(src);
+    // scales as bf16 bits: [group][matrix * 128 + row]
+    for (int i = tid; i < 2 * 128 * (G / 8); i += kPfThreads) {
+        const int chunk = i % (G / 8), row = (i / (G / 8)) % 128, mt = i / (G / 8 * 128);
+        const int rr = min(n0 + row, I - 1);
+        const uint4 v = *reinterpret_cast<const uint4*>((mt ? Um.s : Gm.s) + (mrow0 + rr) * G + 8 * chunk);
         const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float f = vmi_bf16_to_f32((wv[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-            float* dst = reinterpret_cast<float*>(&s_sb[8 * chunk + j][mt][row]);
-            dst[sb] = sb == 0 ? f * 16777216.0f : f;
-        }
+        for (int j = 0; j < 8; ++j)
+            s_scale[8 * chunk + j][128 * mt + row] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xffffu);
     }
     __syncthreads();
-    for (int i = tid; i < kTileM * G; i += kPfThreads) {
-        const int row = i / G, g = i - row * G;
-        s_xs[g][row] = a.xsum4[(size_t)s_tok[row] * G + g];
+    // this thread's DMA sources: A pieces p = tid + 256 j (row p/8, slot piece
+    // p%8 = logical piece (p%8) ^ (row & 7)); weight pieces p = tid + 256 j
+    // (row p/2: matrix row/128, row n0 + row%128; half (p%2) ^ bit 3 of row)
+    const vmi_u4* asrc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int p = tid + kPfThreads * j, row = p >> 3, c = (p & 7) ^ (row & 7);
+        asrc[j] = a.xop4 + (size_t)s_tok[row] * HW + c;
     }
-    const Ring R{r0, r1, r2, r3};
-    // this thread's DMA piece: matrix mt, row r, half h (16i bytes into a slot)
-    const int dmt = tid >> 7, dr = (tid >> 1) & 63, dh = tid & 1;
-    const uint32_t* dsrc = (dmt == 0 ? Gm.w : Um.w) + (row0 + dr) * HW + 4 * (dh ^ ((dr >> 3) & 1));
-    const vmi_u4* arow = a.xop4 + (size_t)s_tok[16 * w + n] * HW;
-    auto issue = [&](int g, int u, vmi_u4& x0, vmi_u4& x1) {
-        vmi_lds_dma16_opaque(dsrc + 8 * g, R.at(u) + 1024 * w);
-        x0 = arow[8 * g + 2 * q];
-        x1 = arow[8 * g + 2 * q + 1];
+    const uint32_t* bsrc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int p = tid + kPfThreads * j, row = p >> 1, h = (p & 1) ^ ((row >> 3) & 1);
+        const int mt = row >> 7, rr = min(n0 + (row & 127), I - 1);
+        bsrc[j] = (mt ? Um.w : Gm.w) + (mrow0 + rr) * HW + 4 * h;
+    }
+    auto issue = [&](int g, int u) {
+        uint8_t* A = s_ring + u * (kPfA + kB);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPfThreads * j + 64 * w));
+#pragma unroll
+        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(bsrc[j] + 8 * g, A + kPfA + 16 * (kPfThreads * j + 64 * w));
     };
-    vmi_u4 ap[kRing][2];
-    vmi_f4 acc[2][4];
+    vmi_f4 acc[4][4][2];
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) acc[m][s4] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+        for (int sb = 0; sb < 4; ++sb)
 #pragma unroll
-    for (int u = 0; u < kRing - 1; ++u) issue(u < G ? u : G - 1, u, ap[u][0], ap[u][1]);
+            for (int mt = 0; mt < 2; ++mt) acc[m][sb][mt] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kPfStages - 1; ++u) issue(u < G ? u : G - 1, u);
 #pragma unroll 1
-    for (int g0 = 0; g0 < G; g0 += kRing) {
+    for (int g = 0; g < G; ++g) {
+        const int u = g % kPfStages;
+        pf_wait_vmcnt<6 * (kPfStages - 2)>();  // group g's pieces (this thread's) have landed
+        __syncthreads();                        // everyone's; and the slot of group g-1 is free
+        {
+            const int gn = g + kPfStages - 1;
+            issue(gn < G ? gn : G - 1, gn % kPfStages);
+        }
+        const uint8_t* A = s_ring + u * (kPfA + kB);
+        const uint8_t* B = A + kPfA;
+        vmi_u4 av[4][2];
 #pragma unroll
-        for (int u = 0; u < kRing; ++u) {
-            const int g = g0 + u;
-            pf_wait_vmcnt<3 * (kRing - 2)>();  // group g's DMA and operand loads have landed
-            __syncthreads();                    // every wave's piece of group g; slot of g-1 free
-            const int gn = g + kRing - 1;
-            issue(gn < G ? gn : G - 1, (u + kRing - 1) % kRing, ap[(u + kRing - 1) % kRing][0],
-                  ap[(u + kRing - 1) % kRing][1]);
-            const uint8_t* slot = R.at(u);
-            const float4 xs = *reinterpret_cast<const float4*>(&s_xs[g][16 * w + 4 * q]);
-            const float xsr[4] = {xs.x, xs.y, xs.z, xs.w};
+        for (int m = 0; m < 4; ++m) {
+            const int row = 64 * mh + 16 * m + n;
+            av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
+            av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+        }
+        // eight (column block, matrix) blocks of four MFMA pairs each, software
+        // pipelined: block i's MFMAs are issued with block i-1's scale FMAs, so
+        // only two blocks' results are live and they stay in VGPRs
+        vmi_f4 dp[4];
+        float scp = 0.0f;
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
+        for (int blk = 0; blk <= 8; ++blk) {
+            vmi_f4 dc[4];
+            float scc = 0.0f;
+            if (blk < 8) {
+                const int sb = blk >> 1, mt = blk & 1;
+                const int brow = 128 * mt + 64 * nh + 16 * sb + n;
+                const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
+                // the scale times 2^24: the 4-bit operands are n * 2^-24
+                scc = vmi_bf16_to_f32(s_scale[g][brow]) * 16777216.0f;
+                const vmi_u4 b0 = vmi_unpack_u4_f16(wq.x), b1 = vmi_unpack_u4_f16(wq.y);
 #pragma unroll
-                for (int s4 = 0; s4 < 4; ++s4) {
-                    const int row = 16 * s4 + n;
-                    const uint2 wq = *reinterpret_cast<const uint2*>(slot + 2048 * mt + ring_off(row, q));
-                    vmi_f4 d = vmi_mfma_f16(ap[u][0], vmi_unpack_u4_f16(wq.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
-                    d = vmi_mfma_f16(ap[u][1], vmi_unpack_u4_f16(wq.y), d);
-                    const float2 sb = s_sb[g][mt][row];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[mt][s4][r] = fmaf(d[r], sb.x, fmaf(sb.y, xsr[r], acc[mt][s4][r]));
+                for (int m = 0; m < 4; ++m) {
+                    dc[m] = vmi_mfma_f16(av[m][0], b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
+                    dc[m] = vmi_mfma_f16(av[m][1], b1, dc[m]);
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);  // keep groups apart: bounded live registers
+            if (blk > 0) {
+                const int sb = (blk - 1) >> 1, mt = (blk - 1) & 1;
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[m][sb][mt][r] = fmaf(dp[m][r], scp, acc[m][sb][mt][r]);
+            }
+            if (blk < 8) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) dp[m] = dc[m];
+                scp = scc;
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     pf_wait_vmcnt<0>();
-    // SwiGLU into LDS: rows 16w + 4q + r, columns 16 s4 + n
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = 16 * w + 4 * q + r;
-        const float inv = s_route[row] >= 0 ? 1.0f / a.fscale[s_tok[row]] : 0.0f;
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-            const float gv = acc[0][s4][r] * inv, uv = acc[1][s4][r] * inv;
-            s_act[row][16 * s4 + n] = gv / (1.0f + expf(-gv)) * uv;
-        }
+    __syncthreads();
+    // affine-bias term: operand sums X [128 routes][G] and the biases as bf16
+    // pairs [256 rows][G/2] in the ring's space
+    constexpr int XS = kMaxG + 1, BS = kMaxG / 2 + 1;
+    static_assert(kTM3 * XS * 4 + 256 * BS * 4 <= sizeof(s_ring), "bias operands exceed the ring");
+    float* s_xs = reinterpret_cast<float*>(s_ring);                       // [128][XS]
+    uint32_t* s_b = reinterpret_cast<uint32_t*>(s_ring + kTM3 * XS * 4);  // [256][BS]
+    for (int i = tid; i < kTM3 * G; i += kPfThreads) {
+        const int row = i / G, g = i - row * G;
+        s_xs[row * XS + g] = a.xsum4[(size_t)s_tok[row] * G + g];
+    }
+    for (int i = tid; i < 256 * (G / 2); i += kPfThreads) {
+        const int row = i / (G / 2), c = i - row * (G / 2);
+        const int mt = row >> 7, rr = min(n0 + (row & 127), I - 1);
+        s_b[row * BS + c] = reinterpret_cast<const uint32_t*>((mt ? Um.b : Gm.b) + (mrow0 + rr) * G)[c];
     }
     __syncthreads();
-    const int IW = a.I / 8, IG = a.I / 64;
-    for (int i = tid; i < kTileM * 8; i += kPfThreads) {
-        const int row = i >> 3, wd = i & 7;
+#pragma unroll 1
+    for (int c8 = 0; c8 < G / 8; ++c8) {
+        const int g0 = 8 * c8 + 2 * q;
+        vmi_u4 ab[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int row = 64 * mh + 16 * m + n;
+            ab[m] = vmi_bias_a_operand(s_xs[row * XS + g0], s_xs[row * XS + g0 + 1]);
+        }
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const int brow = 128 * mt + 64 * nh + 16 * sb + n;
+                const vmi_u4 bb = vmi_bias_b_operand(s_b[brow * BS + (g0 >> 1)]);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) acc[m][sb][mt] = vmi_mfma_bf16(ab[m], bb, acc[m][sb][mt]);
+            }
+    }
+    __syncthreads();
+    // SwiGLU into LDS as bf16 (the rounding of the down-projection operands):
+    // route row 64mh + 16m + 4q + r, column 64nh + 16sb + n
+    constexpr int AS = 136;
+    static_assert(kTM3 * AS * 2 <= sizeof(s_ring), "activation staging exceeds the ring");
+    uint16_t* s_act = reinterpret_cast<uint16_t*>(s_ring);  // [128][AS]
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 64 * mh + 16 * m + 4 * q + r;
+            const float inv = s_route[row] >= 0 ? 1.0f / a.fscale[s_tok[row]] : 0.0f;
+#pragma unroll
+            for (int sb = 0; sb < 4; ++sb) {
+                const float gv = acc[m][sb][0][r] * inv, uv = acc[m][sb][1][r] * inv;
+                s_act[row * AS + 64 * nh + 16 * sb + n] = vmi_f32_to_bf16(gv / (1.0f + expf(-gv)) * uv);
+            }
+        }
+    __syncthreads();
+    const int IW = I / 8, IG = I / 64, nw8 = nvalid / 8, ng = nvalid / 64;
+    for (int i = tid; i < kTM3 * nw8; i += kPfThreads) {
+        const int row = i / nw8, wd = i - row * nw8;
         const int route = s_route[row];
         if (route < 0) continue;
         uint16_t b[8];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) b[c] = vmi_f32_to_bf16(s_act[row][8 * wd + c]);
+        for (int c = 0; c < 8; ++c) b[c] = s_act[row * AS + 8 * wd + c];
         vmi_u4 o;  // slot order of vmi_unpack_u4_bf16_128: {0,4,1,5,2,6,3,7}
         o[0] = (uint32_t)b[0] | ((uint32_t)b[4] << 16);
         o[1] = (uint32_t)b[1] | ((uint32_t)b[5] << 16);
@@ -774,101 +711,169 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup2(PfArgs a) {
         o[3] = (uint32_t)b[3] | ((uint32_t)b[7] << 16);
         a.actop[(size_t)route * IW + (n0 >> 3) + wd] = o;
     }
-    if (tid < kTileM) {
-        const int route = s_route[tid];
-        if (route >= 0) {
-            float sum = 0.0f;
-            for (int c = 0; c < 64; ++c) sum += vmi_bf16_to_f32(vmi_f32_to_bf16(s_act[tid][c]));
-            a.axs[(size_t)route * IG + (n0 >> 6)] = sum;
-        }
+    for (int i = tid; i < kTM3 * ng; i += kPfThreads) {
+        const int row = i / ng, gg = i - row * ng;
+        const int route = s_route[row];
+        if (route < 0) continue;
+        float sum = 0.0f;
+        for (int c = 0; c < 64; ++c) sum += vmi_bf16_to_f32(s_act[row * AS + 64 * gg + c]);
+        a.axs[(size_t)route * IG + (n0 >> 6) + gg] = sum;
     }
 }
 
-// Down: tile M 64 routes x N 128 hidden rows; K = inter.
-__global__ __launch_bounds__(kPfThreads, 2) void k_pf_down2(PfArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t r0[4096], r1[4096], r2[4096], r3[4096];
-    __shared__ __attribute__((aligned(16))) float2 s_sb[kMaxG][128];
-    __shared__ __attribute__((aligned(16))) float s_as[kMaxG][kTileM];
-    __shared__ int s_route[kTileM];
-    const int ti = blockIdx.x;
+// Down: tile 128 routes x 128 hidden rows, K = I.  4-bit values enter as exact
+// bf16 (128 + q); per group y += s * D, and at the end
+// y += sum_g (b_g - 128 s_g) X_g with X the activations' group sums (as the
+// bf16 MFMAs sum_g b_g X_g + sum_g s_g (-128 X_g)); then times the route's
+// combine weight into one bf16 row per (token, rank).
+__global__ __launch_bounds__(kPfThreads, 2) void k_pf_down3(PfArgs a) {
+    constexpr int kB = 128 * 32;
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[kPfStages * (kPfA + kB)];
+    // scales and biases as bf16 bits, and the activation sums, each zero past
+    // group G up to the next multiple of 8 (the affine MFMAs take 8 groups)
+    __shared__ uint16_t s_s16[128][kMaxG + 2];
+    __shared__ uint16_t s_b16[128][kMaxG + 2];
+    __shared__ float s_as[kTM3][kMaxG + 1];
+    __shared__ int s_route[kTM3];
+    const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
+    const int n = lane & 15, q = lane >> 4;
+    const int mh = w & 1, nh = w >> 1;
+    const int NB = a.H / 128;
+    int ti, nb;
+    pf_tile_of(blockIdx.x, NB, ti, nb);
     if (ti >= a.ntiles[0]) return;
     const int4 tl = a.tiles[ti];
-    const int lane = threadIdx.x & 63, w = pf_wave(), tid = threadIdx.x;
-    const int n = lane & 15, q = lane >> 4;
-    const int h0 = blockIdx.y * 128;
-    const int IW = a.I / 8, G = a.I / 64;
+    const int I = a.I, IW = I / 8, G = I / 64;
+    const int h0 = nb * 128;
     const vmi_qmat Dm = tl.x >= 0 ? a.down : a.sh_down;
-    const size_t row0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)a.H + h0;
-    if (tid < kTileM) s_route[tid] = tile_route(a, tl, tid);
-    // scales / biases: {s, b} x 128 rows x G groups (G a multiple of 1; 8-group chunks when possible)
-    for (int i = tid; i < 2 * 128 * G; i += kPfThreads) {
-        const int g = i % G, row = (i / G) % 128, sb = i / (G * 128);
-        const float f = vmi_bf16_to_f32((sb == 0 ? Dm.s : Dm.b)[(row0 + row) * G + g]);
-        reinterpret_cast<float*>(&s_sb[g][row])[sb] = f;
+    const size_t mrow0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)a.H + h0;
+    if (tid < kTM3) s_route[tid] = tile_route(a, tl, tid);
+    const int G8 = (G + 7) & ~7;
+    for (int i = tid; i < 128 * G8; i += kPfThreads) {
+        const int g = i % G8, row = i / G8;
+        s_s16[row][g] = g < G ? Dm.s[(mrow0 + row) * G + g] : (uint16_t)0;
+        s_b16[row][g] = g < G ? Dm.b[(mrow0 + row) * G + g] : (uint16_t)0;
     }
     __syncthreads();
-    for (int i = tid; i < kTileM * G; i += kPfThreads) {
-        const int row = i / G, g = i - row * G;
+    for (int i = tid; i < kTM3 * G8; i += kPfThreads) {
+        const int row = i / G8, g = i - row * G8;
         const int rt = s_route[row];
-        s_as[g][row] = rt >= 0 ? a.axs[(size_t)rt * G + g] : 0.0f;
+        s_as[row][g] = rt >= 0 && g < G ? a.axs[(size_t)rt * G + g] : 0.0f;
     }
-    const Ring R{r0, r1, r2, r3};
-    const int dr = tid >> 1, dh = tid & 1;
-    const uint32_t* dsrc = Dm.w + (row0 + dr) * IW + 4 * (dh ^ ((dr >> 3) & 1));
-    const int my_route = s_route[16 * w + n];
-    const vmi_u4* arow = a.actop + (size_t)(my_route >= 0 ? my_route : 0) * IW;
-    auto issue = [&](int g, int u, vmi_u4& x0, vmi_u4& x1) {
-        vmi_lds_dma16_opaque(dsrc + 8 * g, R.at(u) + 1024 * w);
-        x0 = arow[8 * g + 2 * q];
-        x1 = arow[8 * g + 2 * q + 1];
+    const vmi_u4* asrc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int p = tid + kPfThreads * j, row = p >> 3, c = (p & 7) ^ (row & 7);
+        const int rt = s_route[row];
+        asrc[j] = a.actop + (size_t)(rt >= 0 ? rt : 0) * IW + c;
+    }
+    const uint32_t* bsrc;
+    {
+        const int row = tid >> 1, h = (tid & 1) ^ ((row >> 3) & 1);
+        bsrc = Dm.w + (mrow0 + row) * IW + 4 * h;
+    }
+    auto issue = [&](int g, int u) {
+        uint8_t* A = s_ring + u * (kPfA + kB);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPfThreads * j + 64 * w));
+        vmi_lds_dma16_opaque(bsrc + 8 * g, A + kPfA + 16 * (64 * w));
     };
-    vmi_u4 ap[kRing][2];
-    vmi_f4 acc[8];
+    vmi_f4 acc[4][4];
 #pragma unroll
-    for (int s8 = 0; s8 < 8; ++s8) acc[s8] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int u = 0; u < kRing - 1; ++u) issue(u < G ? u : G - 1, u, ap[u][0], ap[u][1]);
+        for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kPfStages - 1; ++u) issue(u < G ? u : G - 1, u);
 #pragma unroll 1
-    for (int g0 = 0; g0 < G; g0 += kRing) {
+    for (int g = 0; g < G; ++g) {
+        const int u = g % kPfStages;
+        pf_wait_vmcnt<5 * (kPfStages - 2)>();
+        __syncthreads();
+        {
+            const int gn = g + kPfStages - 1;
+            issue(gn < G ? gn : G - 1, gn % kPfStages);
+        }
+        const uint8_t* A = s_ring + u * (kPfA + kB);
+        const uint8_t* B = A + kPfA;
+        vmi_u4 av[4][2];
 #pragma unroll
-        for (int u = 0; u < kRing; ++u) {
-            const int g = g0 + u;
-            if (g < G) {  // uniform
-                pf_wait_vmcnt<3 * (kRing - 2)>();
-                __syncthreads();
-                const int gn = g + kRing - 1;
-                issue(gn < G ? gn : G - 1, (u + kRing - 1) % kRing, ap[(u + kRing - 1) % kRing][0],
-                      ap[(u + kRing - 1) % kRing][1]);
-                const uint8_t* slot = R.at(u);
-                const float4 as = *reinterpret_cast<const float4*>(&s_as[g][16 * w + 4 * q]);
-                const float asr[4] = {as.x, as.y, as.z, as.w};
+        for (int m = 0; m < 4; ++m) {
+            const int row = 64 * mh + 16 * m + n;
+            av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
+            av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+        }
+        // four column blocks, software pipelined as in k_pf_gateup3
+        vmi_f4 dp[4];
+        float scp = 0.0f;
 #pragma unroll
-                for (int s8 = 0; s8 < 8; ++s8) {
-                    const int row = 16 * s8 + n;
-                    const uint2 wq = *reinterpret_cast<const uint2*>(slot + ring_off(row, q));
-                    vmi_f4 d = vmi_mfma_bf16(ap[u][0], vmi_unpack_u4_bf16_128(wq.x), vmi_f4{0.f, 0.f, 0.f, 0.f});
-                    d = vmi_mfma_bf16(ap[u][1], vmi_unpack_u4_bf16_128(wq.y), d);
-                    const float2 sb = s_sb[g][row];
+        for (int sb = 0; sb <= 4; ++sb) {
+            vmi_f4 dc[4];
+            float scc = 0.0f;
+            if (sb < 4) {
+                const int brow = 64 * nh + 16 * sb + n;
+                const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
+                scc = vmi_bf16_to_f32(s_s16[brow][g]);
+                const vmi_u4 b0 = vmi_unpack_u4_bf16_128(wq.x), b1 = vmi_unpack_u4_bf16_128(wq.y);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[s8][r] = fmaf(sb.x, fmaf(-128.0f, asr[r], d[r]), fmaf(sb.y, asr[r], acc[s8][r]));
+                for (int m = 0; m < 4; ++m) {
+                    dc[m] = vmi_mfma_bf16(av[m][0], b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
+                    dc[m] = vmi_mfma_bf16(av[m][1], b1, dc[m]);
                 }
+            }
+            if (sb > 0) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[m][sb - 1][r] = fmaf(dp[m][r], scp, acc[m][sb - 1][r]);
+            }
+            if (sb < 4) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) dp[m] = dc[m];
+                scp = scc;
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
     pf_wait_vmcnt<0>();
+    // the affine terms, eight groups per MFMA
+#pragma unroll 1
+    for (int c8 = 0; c8 < G8 / 8; ++c8) {
+        const int g0 = 8 * c8 + 2 * q;
+        vmi_u4 ab[4], am[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int route = s_route[16 * w + 4 * q + r];
-        if (route < 0) continue;
-        const int t = route / (a.k + 1), j = route - t * (a.k + 1);
-        const float wgt = j < a.k ? a.scores[t * a.k + j]
-                                  : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
+        for (int m = 0; m < 4; ++m) {
+            const int row = 64 * mh + 16 * m + n;
+            const float x0 = s_as[row][g0], x1 = s_as[row][g0 + 1];
+            ab[m] = vmi_bias_a_operand(x0, x1);
+            am[m] = vmi_bias_a_operand(-128.0f * x0, -128.0f * x1);
+        }
 #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8)
-            a.ybuf[(size_t)route * a.H + h0 + 16 * s8 + n] = vmi_f32_to_bf16(acc[s8][r] * wgt);
+        for (int sb = 0; sb < 4; ++sb) {
+            const int brow = 64 * nh + 16 * sb + n;
+            const vmi_u4 bb = vmi_bias_b_operand((uint32_t)s_b16[brow][g0] | ((uint32_t)s_b16[brow][g0 + 1] << 16));
+            const vmi_u4 bs = vmi_bias_b_operand((uint32_t)s_s16[brow][g0] | ((uint32_t)s_s16[brow][g0 + 1] << 16));
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                acc[m][sb] = vmi_mfma_bf16(ab[m], bb, acc[m][sb]);
+                acc[m][sb] = vmi_mfma_bf16(am[m], bs, acc[m][sb]);
+            }
+        }
     }
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 64 * mh + 16 * m + 4 * q + r;
+            const int route = s_route[row];
+            if (route < 0) continue;
+            const int t = route / (a.k + 1), j = route - t * (a.k + 1);
+            const float wgt = j < a.k ? a.scores[t * a.k + j]
+                                      : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
+#pragma unroll
+            for (int sb = 0; sb < 4; ++sb)
+                a.ybuf[(size_t)route * a.H + h0 + 64 * nh + 16 * sb + n] = vmi_f32_to_bf16(acc[m][sb][r] * wgt);
+        }
 }
 
 // --------------------------------------------------------------- combine
@@ -917,7 +922,7 @@ PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) 
         return o;
     };
     const size_t R = (size_t)T * (k + 1);
-    L.max_tiles = (T * k + kTileM - 1) / kTileM + cap + (T + kTileM - 1) / kTileM;
+    L.max_tiles = (T * k + kTM3 - 1) / kTM3 + cap + (T + kTM3 - 1) / kTM3;
     L.status = take(256);
     L.xop4 = take((size_t)T * (H / 8) * 16);
     L.xsum4 = take((size_t)T * (H / 64) * 4);
@@ -1042,8 +1047,9 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     hipLaunchKernelGGL(k_pf_count, dim3((T * D.top_k + kCountRoutes - 1) / kCountRoutes), dim3(kPfThreads), 0, s, a);
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
-    hipLaunchKernelGGL(k_pf_gateup2, dim3(L.max_tiles, D.inter / 64), dim3(kPfThreads), 0, s, a);
-    hipLaunchKernelGGL(k_pf_down2, dim3(L.max_tiles, D.hidden / 128), dim3(kPfThreads), 0, s, a);
+    const int tile_slots = 8 * ((L.max_tiles + 7) / 8);
+    hipLaunchKernelGGL(k_pf_gateup3, dim3(tile_slots * ((D.inter + 127) / 128)), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_down3, dim3(tile_slots * (D.hidden / 128)), dim3(kPfThreads), 0, s, a);
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(kPfThreads), 0, s, a);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill launch");
