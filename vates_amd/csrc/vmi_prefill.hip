@@ -9,7 +9,7 @@
 //
 //   k_pf_prep     per token: optional RMSNorm, MFMA operands of x (fp16, range
 //                 factor per token), per-group operand sums; clears counters
-//   k_pf_router   router logits [T, E] as a grouped MFMA GEMM on the 4/8-bit
+//   k_pf_router3  router logits [T, E] as a tiled MFMA GEMM on the 4/8-bit
 //                 router (weights enter the MFMA as exact fp16 subnormals)
 //   k_pf_sgate    shared-expert gate logit per token (one wave per token)
 //   k_pf_topk     one wave per token: top-k, softmax, renorm, slot table
@@ -39,7 +39,6 @@
 namespace {
 
 constexpr int kPfThreads = 256;
-constexpr int kTileM = 64;   // tokens per router tile
 constexpr int kTM3 = 128;    // routes per tile of the expert GEMMs
 constexpr int kPfMaxE = 1024;
 constexpr int kPfMaxK = 16;
@@ -206,72 +205,6 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
 // exact subnormals, then acc += D * scale * 2^24 (+ the affine-bias term).
 // Lane l: A row m = l%16 (rows of the tile), K block q = l/16; B column
 // n = l%16; D rows 4q + r, column n.
-
-// ----------------------------------------------------------------- router
-// Grid (ceil(T/64), E/64), 4 waves: wave w owns rows 16w..16w+15 of the 64
-// tokens and all 64 experts of the N tile (4 subtiles).
-template <int BITS>
-__global__ __launch_bounds__(kPfThreads) void k_pf_router(PfArgs a) {
-    const int lane = threadIdx.x & 63, w = pf_wave();
-    const int m = lane & 15, q = lane >> 4;
-    const int t0 = blockIdx.x * kTileM + 16 * w;
-    const int e0 = blockIdx.y * 64;
-    const int tm = t0 + m;
-    const bool row_ok = tm < a.T;
-    const int HW = a.H / 8, G = a.H / 64;
-    const vmi_u4* xop = BITS == 4 ? a.xop4 : a.xop8;
-    const float* xs = BITS == 4 ? a.xsum4 : a.xsum8;
-    const vmi_u4* arow = xop + (size_t)(row_ok ? tm : 0) * HW;
-    const int wpr = a.H * BITS / 32;  // packed words per router row
-    vmi_f4 acc[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) acc[s] = vmi_f4{0.f, 0.f, 0.f, 0.f};
-    for (int g = 0; g < G; ++g) {
-        vmi_u4 a0 = arow[8 * g + 2 * q], a1 = arow[8 * g + 2 * q + 1];
-        if (!row_ok) a0 = a1 = vmi_u4{0u, 0u, 0u, 0u};
-        float xsr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tr = t0 + 4 * q + r;
-            xsr[r] = tr < a.T ? xs[(size_t)tr * G + g] : 0.0f;
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int e = e0 + 16 * s + m;  // B column of this lane
-            const uint32_t* wr = a.router.w + (size_t)e * wpr;
-            vmi_u4 b0, b1;
-            if (BITS == 4) {
-                const uint2 ww = *reinterpret_cast<const uint2*>(wr + 8 * g + 2 * q);
-                b0 = vmi_unpack_u4_f16(ww.x);
-                b1 = vmi_unpack_u4_f16(ww.y);
-            } else {
-                // group g = 16 words; MFMA 0 takes words 8g'.. for K block q: columns 16q..16q+7
-                const uint4 ww = *reinterpret_cast<const uint4*>(wr + 16 * g + 4 * q);
-                b0 = unpack_u8_f16(ww.x, ww.y);
-                b1 = unpack_u8_f16(ww.z, ww.w);
-            }
-            vmi_f4 d = vmi_mfma_f16(a0, b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
-            d = vmi_mfma_f16(a1, b1, d);
-            const float sc = vmi_bf16_to_f32(a.router.s[(size_t)e * G + g]) * 16777216.0f;
-            const float bi = vmi_bf16_to_f32(a.router.b[(size_t)e * G + g]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[s][r] = fmaf(d[r], sc, fmaf(bi, xsr[r], acc[s][r]));
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int tr = t0 + 4 * q + r;
-        if (tr >= a.T) continue;
-        const float inv = 1.0f / a.fscale[tr];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int e = e0 + 16 * s + m;
-            float v = acc[s][r] * inv;
-            if (a.logit_bias) v += a.logit_bias[e];
-            a.logits[(size_t)tr * a.E + e] = v;
-        }
-    }
-}
 
 // Shared-expert gate logit: one wave per token, lane-contiguous columns in a
 // fixed order, on the effective fp16 operands (x * f) and the dequantised
@@ -876,6 +809,183 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_down3(PfArgs a) {
         }
 }
 
+// Router logits [T, E] as the same 128 x 128 tile GEMM (tokens x experts, K =
+// H), dense: tile L/8-major as above with NB = ceil(E/128) expert blocks.
+// 4-bit rows are 32 bytes a group (as gate/up); 8-bit rows 64 bytes, 16-byte
+// piece c of row r kept at c ^ ((r >> 2) & 3).  logits = acc / f (+ bias).
+__device__ __forceinline__ uint32_t pf_b8_off(int r, int c) { return 16u * (4u * r + (unsigned)(c ^ ((r >> 2) & 3))); }
+
+template <int BITS>
+__global__ __launch_bounds__(kPfThreads, 2) void k_pf_router3(PfArgs a) {
+    constexpr int kB = 128 * 8 * BITS;  // one group of 128 rows
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[kPfStages * (kPfA + kB)];
+    __shared__ uint16_t s_scale[kMaxG][128];
+    const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
+    const int n = lane & 15, q = lane >> 4;
+    const int mh = w & 1, nh = w >> 1;
+    const int NB = (a.E + 127) / 128;
+    int ti, nb;
+    pf_tile_of(blockIdx.x, NB, ti, nb);
+    const int t0 = ti * kTM3;
+    if (t0 >= a.T) return;
+    const int H = a.H, HW = H / 8, G = H / 64, E = a.E;
+    const int e0 = nb * 128;
+    const int wpr = H * BITS / 32;
+    const vmi_u4* xop = BITS == 4 ? a.xop4 : a.xop8;
+    const float* xsum = BITS == 4 ? a.xsum4 : a.xsum8;
+    for (int i = tid; i < 128 * (G / 8); i += kPfThreads) {
+        const int chunk = i % (G / 8), row = i / (G / 8);
+        const int e = min(e0 + row, E - 1);
+        const uint4 v = *reinterpret_cast<const uint4*>(a.router.s + (size_t)e * G + 8 * chunk);
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s_scale[8 * chunk + j][row] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+    }
+    __syncthreads();
+    const vmi_u4* asrc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int p = tid + kPfThreads * j, row = p >> 3, c = (p & 7) ^ (row & 7);
+        asrc[j] = xop + (size_t)min(t0 + row, a.T - 1) * HW + c;
+    }
+    constexpr int NBD = BITS == 8 ? 2 : 1;  // weight pieces per thread and group
+    const uint32_t* bsrc[NBD];
+#pragma unroll
+    for (int j = 0; j < NBD; ++j) {
+        const int p = tid + kPfThreads * j;
+        int row, off;
+        if constexpr (BITS == 8) {
+            row = p >> 2;
+            off = 4 * ((p & 3) ^ ((row >> 2) & 3));
+        } else {
+            row = p >> 1;
+            off = 4 * ((p & 1) ^ ((row >> 3) & 1));
+        }
+        bsrc[j] = a.router.w + (size_t)min(e0 + row, E - 1) * wpr + off;
+    }
+    auto issue = [&](int g, int u) {
+        uint8_t* A = s_ring + u * (kPfA + kB);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPfThreads * j + 64 * w));
+#pragma unroll
+        for (int j = 0; j < NBD; ++j)
+            vmi_lds_dma16_opaque(bsrc[j] + 2 * BITS * g, A + kPfA + 16 * (kPfThreads * j + 64 * w));
+    };
+    vmi_f4 acc[4][4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kPfStages - 1; ++u) issue(u < G ? u : G - 1, u);
+#pragma unroll 1
+    for (int g = 0; g < G; ++g) {
+        const int u = g % kPfStages;
+        pf_wait_vmcnt<(4 + NBD) * (kPfStages - 2)>();
+        __syncthreads();
+        {
+            const int gn = g + kPfStages - 1;
+            issue(gn < G ? gn : G - 1, gn % kPfStages);
+        }
+        const uint8_t* A = s_ring + u * (kPfA + kB);
+        const uint8_t* B = A + kPfA;
+        vmi_u4 av[4][2];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int row = 64 * mh + 16 * m + n;
+            av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
+            av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+        }
+        vmi_f4 dp[4];
+        float scp = 0.0f;
+#pragma unroll
+        for (int sb = 0; sb <= 4; ++sb) {
+            vmi_f4 dc[4];
+            float scc = 0.0f;
+            if (sb < 4) {
+                const int brow = 64 * nh + 16 * sb + n;
+                vmi_u4 b0, b1;
+                if constexpr (BITS == 8) {
+                    const uint4 ww = *reinterpret_cast<const uint4*>(B + pf_b8_off(brow, q));
+                    b0 = unpack_u8_f16(ww.x, ww.y);
+                    b1 = unpack_u8_f16(ww.z, ww.w);
+                } else {
+                    const uint2 ww = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
+                    b0 = vmi_unpack_u4_f16(ww.x);
+                    b1 = vmi_unpack_u4_f16(ww.y);
+                }
+                scc = vmi_bf16_to_f32(s_scale[g][brow]) * 16777216.0f;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    dc[m] = vmi_mfma_f16(av[m][0], b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
+                    dc[m] = vmi_mfma_f16(av[m][1], b1, dc[m]);
+                }
+            }
+            if (sb > 0) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[m][sb - 1][r] = fmaf(dp[m][r], scp, acc[m][sb - 1][r]);
+            }
+            if (sb < 4) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) dp[m] = dc[m];
+                scp = scc;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    pf_wait_vmcnt<0>();
+    __syncthreads();
+    // affine-bias term through bf16 MFMAs, as in k_pf_gateup3
+    constexpr int XS = kMaxG + 1, BS = kMaxG / 2 + 1;
+    static_assert(kTM3 * XS * 4 + 128 * BS * 4 <= sizeof(s_ring), "bias operands exceed the ring");
+    float* s_xs = reinterpret_cast<float*>(s_ring);
+    uint32_t* s_b = reinterpret_cast<uint32_t*>(s_ring + kTM3 * XS * 4);
+    for (int i = tid; i < kTM3 * G; i += kPfThreads) {
+        const int row = i / G, g = i - row * G;
+        s_xs[row * XS + g] = xsum[(size_t)min(t0 + row, a.T - 1) * G + g];
+    }
+    for (int i = tid; i < 128 * (G / 2); i += kPfThreads) {
+        const int row = i / (G / 2), c = i - row * (G / 2);
+        s_b[row * BS + c] = reinterpret_cast<const uint32_t*>(a.router.b + (size_t)min(e0 + row, E - 1) * G)[c];
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int c8 = 0; c8 < G / 8; ++c8) {
+        const int g0 = 8 * c8 + 2 * q;
+        vmi_u4 ab[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int row = 64 * mh + 16 * m + n;
+            ab[m] = vmi_bias_a_operand(s_xs[row * XS + g0], s_xs[row * XS + g0 + 1]);
+        }
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+            const int brow = 64 * nh + 16 * sb + n;
+            const vmi_u4 bb = vmi_bias_b_operand(s_b[brow * BS + (g0 >> 1)]);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) acc[m][sb] = vmi_mfma_bf16(ab[m], bb, acc[m][sb]);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = t0 + 64 * mh + 16 * m + 4 * q + r;
+            if (t >= a.T) continue;
+            const float inv = 1.0f / a.fscale[t];
+#pragma unroll
+            for (int sb = 0; sb < 4; ++sb) {
+                const int e = e0 + 64 * nh + 16 * sb + n;
+                if (e >= E) continue;
+                float v = acc[m][sb][r] * inv;
+                if (a.logit_bias) v += a.logit_bias[e];
+                a.logits[(size_t)t * E + e] = v;
+            }
+        }
+}
+
 // --------------------------------------------------------------- combine
 // out[t][h] = bf16(sum_{j <= k} y[t(k+1)+j][h] (valid routes, rank order) + residual)
 __global__ __launch_bounds__(kPfThreads) void k_pf_combine(PfArgs a) {
@@ -1031,11 +1141,11 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
         case 4: hipLaunchKernelGGL(k_pf_prep<4>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
         default: return vmi::fail(VMI_ERR_UNSUPPORTED, "hidden=%d must be 512, 1024 or 2048", D.hidden);
     }
-    const dim3 rgrid((T + kTileM - 1) / kTileM, D.num_experts / 64);
+    const dim3 rgrid(8 * (((T + kTM3 - 1) / kTM3 + 7) / 8) * ((D.num_experts + 127) / 128));
     if (D.router_bits == 4)
-        hipLaunchKernelGGL(k_pf_router<4>, rgrid, dim3(kPfThreads), 0, s, a);
+        hipLaunchKernelGGL(k_pf_router3<4>, rgrid, dim3(kPfThreads), 0, s, a);
     else
-        hipLaunchKernelGGL(k_pf_router<8>, rgrid, dim3(kPfThreads), 0, s, a);
+        hipLaunchKernelGGL(k_pf_router3<8>, rgrid, dim3(kPfThreads), 0, s, a);
     if (has_sgate) {
         switch (D.hidden / 512) {
             case 1: hipLaunchKernelGGL(k_pf_sgate<1>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
