@@ -16,10 +16,10 @@
 //   k_pf_count    routes per slot and each route's rank in its slot
 //   k_pf_scan     exclusive scan of the counts, the list of 128-row M tiles
 //   k_pf_place    every routed (token, rank) into its slot's list
-//   k_pf_gateup3  per (M tile, 128 intermediate rows): gate and up MFMA GEMMs
+//   k_pf_gateup3  per (M tile, 256 intermediate rows): gate and up MFMA GEMMs
 //                 over the tile's gathered tokens, SwiGLU, bf16 operands of
 //                 the activations and their per-group sums
-//   k_pf_down3    per (M tile, 128 hidden rows): down MFMA GEMM, times the
+//   k_pf_down3    per (M tile, 512 hidden rows): down MFMA GEMM, times the
 //                 route's combine weight, one bf16 row per (token, rank)
 //   k_pf_combine  out[t] = sum over ranks 0..k (rank k: the gated shared
 //                 expert) in rank order, fp32, + residual
@@ -448,25 +448,29 @@ __device__ __forceinline__ void pf_tile_of(int L, int nb_count, int& ti, int& nb
 // byte offset of A row r, logical 16-byte piece c, inside a slot
 __device__ __forceinline__ uint32_t pf_a_off(int r, int c) { return 16u * (8u * r + (unsigned)(c ^ (r & 7))); }
 
-// Gate/up: tile 128 routes x 128 intermediate rows of gate and of up (256
-// weight rows per stage), K = H.  Then SwiGLU, the bf16 down-projection
-// operands of the activations and their per-group sums.
-__global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
-    constexpr int kB = 256 * 32;
-    __shared__ __attribute__((aligned(16))) uint8_t s_ring[kPfStages * (kPfA + kB)];
-    __shared__ uint16_t s_scale[kMaxG][256];  // bf16 bits
+// Gate/up: tile 128 routes x 256 intermediate rows of gate and of up (512
+// weight rows per stage), K = H, eight waves in a 2 x 4 grid (wave (mh, nq):
+// routes 64mh.., intermediate rows 64nq.. of both matrices).  Then SwiGLU,
+// the bf16 down-projection operands of the activations and their per-group
+// sums.
+constexpr int kPf8Threads = 512;
+template <int STAGES>
+__global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
+    constexpr int kB = 512 * 32;
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[STAGES * (kPfA + kB)];
+    __shared__ uint16_t s_scale[kMaxG][512];  // bf16 bits: [group][matrix * 256 + row]
     __shared__ int s_route[kTM3];
     __shared__ int s_tok[kTM3];
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
-    const int mh = w & 1, nh = w >> 1;
-    const int NB = (a.I + 127) / 128;
+    const int mh = w & 1, nq = w >> 1;
+    const int NB = (a.I + 255) / 256;
     int ti, nb;
     pf_tile_of(blockIdx.x, NB, ti, nb);
     if (ti >= a.ntiles[0]) return;
     const int4 tl = a.tiles[ti];
     const int H = a.H, HW = H / 8, G = H / 64, I = a.I;
-    const int n0 = nb * 128, nvalid = min(128, I - n0);
+    const int n0 = nb * 256, nvalid = min(256, I - n0);
     const vmi_qmat Gm = tl.x >= 0 ? a.gate : a.sh_gate;
     const vmi_qmat Um = tl.x >= 0 ? a.up : a.sh_up;
     const size_t mrow0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)I;
@@ -475,39 +479,36 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
         s_route[tid] = rt;
         s_tok[tid] = rt >= 0 ? rt / (a.k + 1) : 0;
     }
-    // scales as bf16 bits: [group][matrix * 128 + row]
-    for (int i = tid; i < 2 * 128 * (G / 8); i += kPfThreads) {
-        const int chunk = i % (G / 8), row = (i / (G / 8)) % 128, mt = i / (G / 8 * 128);
+    for (int i = tid; i < 2 * 256 * (G / 8); i += kPf8Threads) {
+        const int chunk = i % (G / 8), row = (i / (G / 8)) % 256, mt = i / (G / 8 * 256);
         const int rr = min(n0 + row, I - 1);
         const uint4 v = *reinterpret_cast<const uint4*>((mt ? Um.s : Gm.s) + (mrow0 + rr) * G + 8 * chunk);
         const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            s_scale[8 * chunk + j][128 * mt + row] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+            s_scale[8 * chunk + j][256 * mt + row] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xffffu);
     }
     __syncthreads();
-    // this thread's DMA sources: A pieces p = tid + 256 j (row p/8, slot piece
-    // p%8 = logical piece (p%8) ^ (row & 7)); weight pieces p = tid + 256 j
-    // (row p/2: matrix row/128, row n0 + row%128; half (p%2) ^ bit 3 of row)
-    const vmi_u4* asrc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int p = tid + kPfThreads * j, row = p >> 3, c = (p & 7) ^ (row & 7);
-        asrc[j] = a.xop4 + (size_t)s_tok[row] * HW + c;
-    }
+    // DMA sources: A pieces p = tid + 512 j (row p/8, slot piece p%8 = logical
+    // piece (p%8) ^ (row & 7)); weight pieces p = tid + 512 j (row p/2: matrix
+    // row/256, intermediate row n0 + row%256; half (p%2) ^ bit 3 of row)
+    const vmi_u4* asrc[2];
     const uint32_t* bsrc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int p = tid + kPfThreads * j, row = p >> 1, h = (p & 1) ^ ((row >> 3) & 1);
-        const int mt = row >> 7, rr = min(n0 + (row & 127), I - 1);
+        const int p = tid + kPf8Threads * j;
+        const int arow = p >> 3, c = (p & 7) ^ (arow & 7);
+        asrc[j] = a.xop4 + (size_t)s_tok[arow] * HW + c;
+        const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
+        const int mt = brow >> 8, rr = min(n0 + (brow & 255), I - 1);
         bsrc[j] = (mt ? Um.w : Gm.w) + (mrow0 + rr) * HW + 4 * h;
     }
     auto issue = [&](int g, int u) {
         uint8_t* A = s_ring + u * (kPfA + kB);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPfThreads * j + 64 * w));
+        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
 #pragma unroll
-        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(bsrc[j] + 8 * g, A + kPfA + 16 * (kPfThreads * j + 64 * w));
+        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(bsrc[j] + 8 * g, A + kPfA + 16 * (kPf8Threads * j + 64 * w));
     };
     vmi_f4 acc[4][4][2];
 #pragma unroll
@@ -517,15 +518,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) acc[m][sb][mt] = vmi_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kPfStages - 1; ++u) issue(u < G ? u : G - 1, u);
+    for (int u = 0; u < STAGES - 1; ++u) issue(u < G ? u : G - 1, u);
 #pragma unroll 1
     for (int g = 0; g < G; ++g) {
-        const int u = g % kPfStages;
-        pf_wait_vmcnt<6 * (kPfStages - 2)>();  // group g's pieces (this thread's) have landed
-        __syncthreads();                        // everyone's; and the slot of group g-1 is free
+        const int u = g % STAGES;
+        pf_wait_vmcnt<4 * (STAGES - 2)>();  // group g's pieces (this thread's) have landed
+        __syncthreads();                    // everyone's; and the slot of group g-1 is free
         {
-            const int gn = g + kPfStages - 1;
-            issue(gn < G ? gn : G - 1, gn % kPfStages);
+            const int gn = g + STAGES - 1;
+            issue(gn < G ? gn : G - 1, gn % STAGES);
         }
         const uint8_t* A = s_ring + u * (kPfA + kB);
         const uint8_t* B = A + kPfA;
@@ -547,7 +548,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
             float scc = 0.0f;
             if (blk < 8) {
                 const int sb = blk >> 1, mt = blk & 1;
-                const int brow = 128 * mt + 64 * nh + 16 * sb + n;
+                const int brow = 256 * mt + 64 * nq + 16 * sb + n;
                 const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
                 // the scale times 2^24: the 4-bit operands are n * 2^-24
                 scc = vmi_bf16_to_f32(s_scale[g][brow]) * 16777216.0f;
@@ -576,18 +577,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
     pf_wait_vmcnt<0>();
     __syncthreads();
     // affine-bias term: operand sums X [128 routes][G] and the biases as bf16
-    // pairs [256 rows][G/2] in the ring's space
+    // pairs [512 rows][G/2] in the ring's space
     constexpr int XS = kMaxG + 1, BS = kMaxG / 2 + 1;
-    static_assert(kTM3 * XS * 4 + 256 * BS * 4 <= sizeof(s_ring), "bias operands exceed the ring");
+    static_assert(kTM3 * XS * 4 + 512 * BS * 4 <= sizeof(s_ring), "bias operands exceed the ring");
     float* s_xs = reinterpret_cast<float*>(s_ring);                       // [128][XS]
-    uint32_t* s_b = reinterpret_cast<uint32_t*>(s_ring + kTM3 * XS * 4);  // [256][BS]
-    for (int i = tid; i < kTM3 * G; i += kPfThreads) {
+    uint32_t* s_b = reinterpret_cast<uint32_t*>(s_ring + kTM3 * XS * 4);  // [512][BS]
+    for (int i = tid; i < kTM3 * G; i += kPf8Threads) {
         const int row = i / G, g = i - row * G;
         s_xs[row * XS + g] = a.xsum4[(size_t)s_tok[row] * G + g];
     }
-    for (int i = tid; i < 256 * (G / 2); i += kPfThreads) {
+    for (int i = tid; i < 512 * (G / 2); i += kPf8Threads) {
         const int row = i / (G / 2), c = i - row * (G / 2);
-        const int mt = row >> 7, rr = min(n0 + (row & 127), I - 1);
+        const int mt = row >> 8, rr = min(n0 + (row & 255), I - 1);
         s_b[row * BS + c] = reinterpret_cast<const uint32_t*>((mt ? Um.b : Gm.b) + (mrow0 + rr) * G)[c];
     }
     __syncthreads();
@@ -604,7 +605,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
         for (int sb = 0; sb < 4; ++sb)
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
-                const int brow = 128 * mt + 64 * nh + 16 * sb + n;
+                const int brow = 256 * mt + 64 * nq + 16 * sb + n;
                 const vmi_u4 bb = vmi_bias_b_operand(s_b[brow * BS + (g0 >> 1)]);
 #pragma unroll
                 for (int m = 0; m < 4; ++m) acc[m][sb][mt] = vmi_mfma_bf16(ab[m], bb, acc[m][sb][mt]);
@@ -612,8 +613,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
     }
     __syncthreads();
     // SwiGLU into LDS as bf16 (the rounding of the down-projection operands):
-    // route row 64mh + 16m + 4q + r, column 64nh + 16sb + n
-    constexpr int AS = 136;
+    // route row 64mh + 16m + 4q + r, column 64nq + 16sb + n
+    constexpr int AS = 264;
     static_assert(kTM3 * AS * 2 <= sizeof(s_ring), "activation staging exceeds the ring");
     uint16_t* s_act = reinterpret_cast<uint16_t*>(s_ring);  // [128][AS]
 #pragma unroll
@@ -625,12 +626,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
 #pragma unroll
             for (int sb = 0; sb < 4; ++sb) {
                 const float gv = acc[m][sb][0][r] * inv, uv = acc[m][sb][1][r] * inv;
-                s_act[row * AS + 64 * nh + 16 * sb + n] = vmi_f32_to_bf16(gv / (1.0f + expf(-gv)) * uv);
+                s_act[row * AS + 64 * nq + 16 * sb + n] = vmi_f32_to_bf16(gv / (1.0f + expf(-gv)) * uv);
             }
         }
     __syncthreads();
     const int IW = I / 8, IG = I / 64, nw8 = nvalid / 8, ng = nvalid / 64;
-    for (int i = tid; i < kTM3 * nw8; i += kPfThreads) {
+    for (int i = tid; i < kTM3 * nw8; i += kPf8Threads) {
         const int row = i / nw8, wd = i - row * nw8;
         const int route = s_route[row];
         if (route < 0) continue;
@@ -644,7 +645,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
         o[3] = (uint32_t)b[3] | ((uint32_t)b[7] << 16);
         a.actop[(size_t)route * IW + (n0 >> 3) + wd] = o;
     }
-    for (int i = tid; i < kTM3 * ng; i += kPfThreads) {
+    for (int i = tid; i < kTM3 * ng; i += kPf8Threads) {
         const int row = i / ng, gg = i - row * ng;
         const int route = s_route[row];
         if (route < 0) continue;
@@ -654,78 +655,96 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_gateup3(PfArgs a) {
     }
 }
 
-// Down: tile 128 routes x 128 hidden rows, K = I.  4-bit values enter as exact
-// bf16 (128 + q); per group y += s * D, and at the end
+// Down: tile 128 routes x 512 hidden rows, K = I, eight waves in a 2 x 4 grid
+// (wave (mh, nq): routes 64mh.., hidden rows 128nq..).  4-bit values enter as
+// exact bf16 (128 + q); per group y += s * D, and at the end
 // y += sum_g (b_g - 128 s_g) X_g with X the activations' group sums (as the
 // bf16 MFMAs sum_g b_g X_g + sum_g s_g (-128 X_g)); then times the route's
-// combine weight into one bf16 row per (token, rank).
-__global__ __launch_bounds__(kPfThreads, 2) void k_pf_down3(PfArgs a) {
-    constexpr int kB = 128 * 32;
-    __shared__ __attribute__((aligned(16))) uint8_t s_ring[kPfStages * (kPfA + kB)];
+// combine weight into one bf16 row per (token, rank).  MAXG bounds the
+// quantisation groups of K the LDS tables hold.
+template <int STAGES, int MAXG>
+__global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
+    constexpr int kB = 512 * 32;
+    constexpr int GS = MAXG + 2, XS = MAXG + 1;
+    __shared__ __attribute__((aligned(16))) uint8_t s_ring[STAGES * (kPfA + kB)];
     // scales and biases as bf16 bits, and the activation sums, each zero past
     // group G up to the next multiple of 8 (the affine MFMAs take 8 groups)
-    __shared__ uint16_t s_s16[128][kMaxG + 2];
-    __shared__ uint16_t s_b16[128][kMaxG + 2];
-    __shared__ float s_as[kTM3][kMaxG + 1];
+    __shared__ uint16_t s_s16[512][GS];
+    __shared__ uint16_t s_b16[512][GS];
+    __shared__ float s_as[kTM3][XS];
     __shared__ int s_route[kTM3];
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
-    const int mh = w & 1, nh = w >> 1;
-    const int NB = a.H / 128;
+    const int mh = w & 1, nq = w >> 1;
+    const int NB = a.H / 512;
     int ti, nb;
     pf_tile_of(blockIdx.x, NB, ti, nb);
     if (ti >= a.ntiles[0]) return;
     const int4 tl = a.tiles[ti];
     const int I = a.I, IW = I / 8, G = I / 64;
-    const int h0 = nb * 128;
+    const int h0 = nb * 512;
     const vmi_qmat Dm = tl.x >= 0 ? a.down : a.sh_down;
     const size_t mrow0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)a.H + h0;
     if (tid < kTM3) s_route[tid] = tile_route(a, tl, tid);
     const int G8 = (G + 7) & ~7;
-    for (int i = tid; i < 128 * G8; i += kPfThreads) {
-        const int g = i % G8, row = i / G8;
-        s_s16[row][g] = g < G ? Dm.s[(mrow0 + row) * G + g] : (uint16_t)0;
-        s_b16[row][g] = g < G ? Dm.b[(mrow0 + row) * G + g] : (uint16_t)0;
+    if ((G & 7) == 0) {
+        for (int i = tid; i < 2 * 512 * (G / 8); i += kPf8Threads) {
+            const int c = i % (G / 8), row = (i / (G / 8)) % 512, sb = i / (G / 8 * 512);
+            const uint4 v = *reinterpret_cast<const uint4*>((sb ? Dm.b : Dm.s) + (mrow0 + row) * G + 8 * c);
+            uint16_t* dst = sb ? &s_b16[row][8 * c] : &s_s16[row][8 * c];
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                dst[2 * j] = (uint16_t)(wv[j] & 0xffffu);
+                dst[2 * j + 1] = (uint16_t)(wv[j] >> 16);
+            }
+        }
+    } else {
+        for (int i = tid; i < 512 * G8; i += kPf8Threads) {
+            const int g = i % G8, row = i / G8;
+            s_s16[row][g] = g < G ? Dm.s[(mrow0 + row) * G + g] : (uint16_t)0;
+            s_b16[row][g] = g < G ? Dm.b[(mrow0 + row) * G + g] : (uint16_t)0;
+        }
     }
     __syncthreads();
-    for (int i = tid; i < kTM3 * G8; i += kPfThreads) {
+    for (int i = tid; i < kTM3 * G8; i += kPf8Threads) {
         const int row = i / G8, g = i - row * G8;
         const int rt = s_route[row];
         s_as[row][g] = rt >= 0 && g < G ? a.axs[(size_t)rt * G + g] : 0.0f;
     }
-    const vmi_u4* asrc[4];
+    const vmi_u4* asrc[2];
+    const uint32_t* bsrc[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int p = tid + kPfThreads * j, row = p >> 3, c = (p & 7) ^ (row & 7);
-        const int rt = s_route[row];
+    for (int j = 0; j < 2; ++j) {
+        const int p = tid + kPf8Threads * j;
+        const int arow = p >> 3, c = (p & 7) ^ (arow & 7);
+        const int rt = s_route[arow];
         asrc[j] = a.actop + (size_t)(rt >= 0 ? rt : 0) * IW + c;
-    }
-    const uint32_t* bsrc;
-    {
-        const int row = tid >> 1, h = (tid & 1) ^ ((row >> 3) & 1);
-        bsrc = Dm.w + (mrow0 + row) * IW + 4 * h;
+        const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
+        bsrc[j] = Dm.w + (mrow0 + brow) * IW + 4 * h;
     }
     auto issue = [&](int g, int u) {
         uint8_t* A = s_ring + u * (kPfA + kB);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPfThreads * j + 64 * w));
-        vmi_lds_dma16_opaque(bsrc + 8 * g, A + kPfA + 16 * (64 * w));
+        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
+#pragma unroll
+        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(bsrc[j] + 8 * g, A + kPfA + 16 * (kPf8Threads * j + 64 * w));
     };
-    vmi_f4 acc[4][4];
+    vmi_f4 acc[4][8];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+        for (int sb = 0; sb < 8; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kPfStages - 1; ++u) issue(u < G ? u : G - 1, u);
+    for (int u = 0; u < STAGES - 1; ++u) issue(u < G ? u : G - 1, u);
 #pragma unroll 1
     for (int g = 0; g < G; ++g) {
-        const int u = g % kPfStages;
-        pf_wait_vmcnt<5 * (kPfStages - 2)>();
+        const int u = g % STAGES;
+        pf_wait_vmcnt<4 * (STAGES - 2)>();
         __syncthreads();
         {
-            const int gn = g + kPfStages - 1;
-            issue(gn < G ? gn : G - 1, gn % kPfStages);
+            const int gn = g + STAGES - 1;
+            issue(gn < G ? gn : G - 1, gn % STAGES);
         }
         const uint8_t* A = s_ring + u * (kPfA + kB);
         const uint8_t* B = A + kPfA;
@@ -736,15 +755,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_down3(PfArgs a) {
             av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
             av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
         }
-        // four column blocks, software pipelined as in k_pf_gateup3
+        // eight column blocks, software pipelined as in k_pf_gateup3
         vmi_f4 dp[4];
         float scp = 0.0f;
 #pragma unroll
-        for (int sb = 0; sb <= 4; ++sb) {
+        for (int sb = 0; sb <= 8; ++sb) {
             vmi_f4 dc[4];
             float scc = 0.0f;
-            if (sb < 4) {
-                const int brow = 64 * nh + 16 * sb + n;
+            if (sb < 8) {
+                const int brow = 128 * nq + 16 * sb + n;
                 const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
                 scc = vmi_bf16_to_f32(s_s16[brow][g]);
                 const vmi_u4 b0 = vmi_unpack_u4_bf16_128(wq.x), b1 = vmi_unpack_u4_bf16_128(wq.y);
@@ -760,7 +779,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_down3(PfArgs a) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[m][sb - 1][r] = fmaf(dp[m][r], scp, acc[m][sb - 1][r]);
             }
-            if (sb < 4) {
+            if (sb < 8) {
 #pragma unroll
                 for (int m = 0; m < 4; ++m) dp[m] = dc[m];
                 scp = scc;
@@ -782,8 +801,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_down3(PfArgs a) {
             am[m] = vmi_bias_a_operand(-128.0f * x0, -128.0f * x1);
         }
 #pragma unroll
-        for (int sb = 0; sb < 4; ++sb) {
-            const int brow = 64 * nh + 16 * sb + n;
+        for (int sb = 0; sb < 8; ++sb) {
+            const int brow = 128 * nq + 16 * sb + n;
             const vmi_u4 bb = vmi_bias_b_operand((uint32_t)s_b16[brow][g0] | ((uint32_t)s_b16[brow][g0 + 1] << 16));
             const vmi_u4 bs = vmi_bias_b_operand((uint32_t)s_s16[brow][g0] | ((uint32_t)s_s16[brow][g0 + 1] << 16));
 #pragma unroll
@@ -804,8 +823,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_down3(PfArgs a) {
             const float wgt = j < a.k ? a.scores[t * a.k + j]
                                       : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
 #pragma unroll
-            for (int sb = 0; sb < 4; ++sb)
-                a.ybuf[(size_t)route * a.H + h0 + 64 * nh + 16 * sb + n] = vmi_f32_to_bf16(acc[m][sb][r] * wgt);
+            for (int sb = 0; sb < 8; ++sb)
+                a.ybuf[(size_t)route * a.H + h0 + 128 * nq + 16 * sb + n] = vmi_f32_to_bf16(acc[m][sb][r] * wgt);
         }
 }
 
@@ -1095,6 +1114,18 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
          reinterpret_cast<uintptr_t>(D.up.w) | reinterpret_cast<uintptr_t>(D.down.w) |
          reinterpret_cast<uintptr_t>(D.norm_weight)) & 15)
         return vmi::fail(VMI_ERR_INVALID, "x, out, residual, norm weight and packed weights must be 16-byte aligned");
+    {
+        // the GEMMs read scales and biases as 16-byte vectors
+        uintptr_t sb = reinterpret_cast<uintptr_t>(D.router.s) | reinterpret_cast<uintptr_t>(D.router.b) |
+                       reinterpret_cast<uintptr_t>(D.gate.s) | reinterpret_cast<uintptr_t>(D.gate.b) |
+                       reinterpret_cast<uintptr_t>(D.up.s) | reinterpret_cast<uintptr_t>(D.up.b) |
+                       reinterpret_cast<uintptr_t>(D.down.s) | reinterpret_cast<uintptr_t>(D.down.b);
+        if (has_shared)
+            sb |= reinterpret_cast<uintptr_t>(D.shared_gate.s) | reinterpret_cast<uintptr_t>(D.shared_gate.b) |
+                  reinterpret_cast<uintptr_t>(D.shared_up.s) | reinterpret_cast<uintptr_t>(D.shared_up.b) |
+                  reinterpret_cast<uintptr_t>(D.shared_down.s) | reinterpret_cast<uintptr_t>(D.shared_down.b);
+        if (sb & 15) return vmi::fail(VMI_ERR_INVALID, "scales and biases must be 16-byte aligned");
+    }
     const PfLayout L = pf_layout(T, D.top_k, D.hidden, D.inter, D.num_experts, D.cap, D.router_bits);
     if (!workspace || workspace_bytes < L.bytes)
         return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
@@ -1158,8 +1189,11 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
     const int tile_slots = 8 * ((L.max_tiles + 7) / 8);
-    hipLaunchKernelGGL(k_pf_gateup3, dim3(tile_slots * ((D.inter + 127) / 128)), dim3(kPfThreads), 0, s, a);
-    hipLaunchKernelGGL(k_pf_down3, dim3(tile_slots * (D.hidden / 128)), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_gateup3<3>, dim3(tile_slots * ((D.inter + 255) / 256)), dim3(kPf8Threads), 0, s, a);
+    if (D.inter <= 512)
+        hipLaunchKernelGGL((k_pf_down3<3, 8>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_pf_down3<2, kMaxG>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(kPfThreads), 0, s, a);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill launch");
