@@ -36,6 +36,8 @@
 #include "vmi_device.h"
 #include "vmi_internal.h"
 
+VMI_TL_DECL
+
 namespace {
 
 constexpr int kPfThreads = 256;
@@ -447,6 +449,8 @@ __device__ __forceinline__ void pf_tile_of(int L, int nb_count, int& ti, int& nb
 
 // byte offset of A row r, logical 16-byte piece c, inside a slot
 __device__ __forceinline__ uint32_t pf_a_off(int r, int c) { return 16u * (8u * r + (unsigned)(c ^ (r & 7))); }
+// the logical piece a slot position holds (the inverse of pf_a_off's swizzle)
+__device__ __forceinline__ int pf_a_piece(int r, int pos) { return pos ^ (r & 7); }
 
 // Gate/up: tile 128 routes x 256 intermediate rows of gate and of up (512
 // weight rows per stage), K = H, eight waves in a 2 x 4 grid (wave (mh, nq):
@@ -461,6 +465,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     __shared__ uint16_t s_scale[kMaxG][512];  // bf16 bits: [group][matrix * 256 + row]
     __shared__ int s_route[kTM3];
     __shared__ int s_tok[kTM3];
+    __shared__ float s_inv[kTM3];  // 1 / f of the route's token (0 past the tile)
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
     const int mh = w & 1, nq = w >> 1;
@@ -471,22 +476,43 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     const int4 tl = a.tiles[ti];
     const int H = a.H, HW = H / 8, G = H / 64, I = a.I;
     const int n0 = nb * 256, nvalid = min(256, I - n0);
+    VMI_STAMP(4, 0);
     const vmi_qmat Gm = tl.x >= 0 ? a.gate : a.sh_gate;
     const vmi_qmat Um = tl.x >= 0 ? a.up : a.sh_up;
     const size_t mrow0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)I;
-    if (tid < kTM3) {
-        const int rt = tile_route(a, tl, tid);
-        s_route[tid] = rt;
-        s_tok[tid] = rt >= 0 ? rt / (a.k + 1) : 0;
-    }
-    for (int i = tid; i < 2 * 256 * (G / 8); i += kPf8Threads) {
-        const int chunk = i % (G / 8), row = (i / (G / 8)) % 256, mt = i / (G / 8 * 256);
-        const int rr = min(n0 + row, I - 1);
-        const uint4 v = *reinterpret_cast<const uint4*>((mt ? Um.s : Gm.s) + (mrow0 + rr) * G + 8 * chunk);
-        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+    // staging loads are all issued before their values are stored, so the
+    // workgroup waits for one memory latency, not one per loop iteration
+    {
+        constexpr int kIt = (2 * 256 * (kMaxG / 8) + kPf8Threads - 1) / kPf8Threads;
+        const int n16 = 2 * 256 * (G / 8);
+        uint4 v[kIt];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            s_scale[8 * chunk + j][256 * mt + row] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+        for (int it = 0; it < kIt; ++it) {
+            const int i = tid + kPf8Threads * it;
+            if (i < n16) {
+                const int chunk = i % (G / 8), row = (i / (G / 8)) % 256, mt = i / (G / 8 * 256);
+                const int rr = min(n0 + row, I - 1);
+                v[it] = *reinterpret_cast<const uint4*>((mt ? Um.s : Gm.s) + (mrow0 + rr) * G + 8 * chunk);
+            }
+        }
+        if (tid < kTM3) {
+            const int rt = tile_route(a, tl, tid);
+            const int tok = rt >= 0 ? rt / (a.k + 1) : 0;
+            s_route[tid] = rt;
+            s_tok[tid] = tok;
+            s_inv[tid] = rt >= 0 ? 1.0f / a.fscale[tok] : 0.0f;
+        }
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int i = tid + kPf8Threads * it;
+            if (i < n16) {
+                const int chunk = i % (G / 8), row = (i / (G / 8)) % 256, mt = i / (G / 8 * 256);
+                const uint32_t wv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    s_scale[8 * chunk + j][256 * mt + row] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+            }
+        }
     }
     __syncthreads();
     // DMA sources: A pieces p = tid + 512 j (row p/8, slot piece p%8 = logical
@@ -497,7 +523,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int p = tid + kPf8Threads * j;
-        const int arow = p >> 3, c = (p & 7) ^ (arow & 7);
+        const int arow = p >> 3, c = pf_a_piece(arow, p & 7);
         asrc[j] = a.xop4 + (size_t)s_tok[arow] * HW + c;
         const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
         const int mt = brow >> 8, rr = min(n0 + (brow & 255), I - 1);
@@ -517,6 +543,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         for (int sb = 0; sb < 4; ++sb)
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) acc[m][sb][mt] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+    VMI_STAMP(4, 1);
 #pragma unroll
     for (int u = 0; u < STAGES - 1; ++u) issue(u < G ? u : G - 1, u);
 #pragma unroll 1
@@ -524,6 +551,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         const int u = g % STAGES;
         pf_wait_vmcnt<4 * (STAGES - 2)>();  // group g's pieces (this thread's) have landed
         __syncthreads();                    // everyone's; and the slot of group g-1 is free
+        if ((g & 3) == 0 && g < 32) VMI_STAMP(4, 2 + (g >> 2));
         {
             const int gn = g + STAGES - 1;
             issue(gn < G ? gn : G - 1, gn % STAGES);
@@ -576,20 +604,50 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     }
     pf_wait_vmcnt<0>();
     __syncthreads();
+    VMI_STAMP(4, 10);
     // affine-bias term: operand sums X [128 routes][G] and the biases as bf16
     // pairs [512 rows][G/2] in the ring's space
     constexpr int XS = kMaxG + 1, BS = kMaxG / 2 + 1;
     static_assert(kTM3 * XS * 4 + 512 * BS * 4 <= sizeof(s_ring), "bias operands exceed the ring");
     float* s_xs = reinterpret_cast<float*>(s_ring);                       // [128][XS]
     uint32_t* s_b = reinterpret_cast<uint32_t*>(s_ring + kTM3 * XS * 4);  // [512][BS]
-    for (int i = tid; i < kTM3 * G; i += kPf8Threads) {
-        const int row = i / G, g = i - row * G;
-        s_xs[row * XS + g] = a.xsum4[(size_t)s_tok[row] * G + g];
-    }
-    for (int i = tid; i < 512 * (G / 2); i += kPf8Threads) {
-        const int row = i / (G / 2), c = i - row * (G / 2);
-        const int mt = row >> 8, rr = min(n0 + (row & 255), I - 1);
-        s_b[row * BS + c] = reinterpret_cast<const uint32_t*>((mt ? Um.b : Gm.b) + (mrow0 + rr) * G)[c];
+    {
+        constexpr int kXi = (kTM3 * kMaxG + kPf8Threads - 1) / kPf8Threads;
+        constexpr int kBi = (512 * (kMaxG / 8) + kPf8Threads - 1) / kPf8Threads;
+        const int nx = kTM3 * G, nb16 = 512 * (G / 8);
+        float xv[kXi];
+        uint4 bv[kBi];
+#pragma unroll
+        for (int it = 0; it < kXi; ++it) {
+            const int i = tid + kPf8Threads * it;
+            if (i < nx) xv[it] = a.xsum4[(size_t)s_tok[i / G] * G + (i % G)];
+        }
+#pragma unroll
+        for (int it = 0; it < kBi; ++it) {
+            const int i = tid + kPf8Threads * it;
+            if (i < nb16) {
+                const int row = i / (G / 8), c = i % (G / 8);
+                const int mt = row >> 8, rr = min(n0 + (row & 255), I - 1);
+                bv[it] = *reinterpret_cast<const uint4*>((mt ? Um.b : Gm.b) + (mrow0 + rr) * G + 8 * c);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kXi; ++it) {
+            const int i = tid + kPf8Threads * it;
+            if (i < nx) s_xs[(i / G) * XS + (i % G)] = xv[it];
+        }
+#pragma unroll
+        for (int it = 0; it < kBi; ++it) {
+            const int i = tid + kPf8Threads * it;
+            if (i < nb16) {
+                const int row = i / (G / 8), c = i % (G / 8);
+                uint32_t* d = s_b + row * BS + 4 * c;
+                d[0] = bv[it].x;
+                d[1] = bv[it].y;
+                d[2] = bv[it].z;
+                d[3] = bv[it].w;
+            }
+        }
     }
     __syncthreads();
 #pragma unroll 1
@@ -612,6 +670,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
             }
     }
     __syncthreads();
+    VMI_STAMP(4, 11);
     // SwiGLU into LDS as bf16 (the rounding of the down-projection operands):
     // route row 64mh + 16m + 4q + r, column 64nq + 16sb + n
     constexpr int AS = 264;
@@ -622,11 +681,14 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = 64 * mh + 16 * m + 4 * q + r;
-            const float inv = s_route[row] >= 0 ? 1.0f / a.fscale[s_tok[row]] : 0.0f;
+            const float inv = s_inv[row];
 #pragma unroll
             for (int sb = 0; sb < 4; ++sb) {
                 const float gv = acc[m][sb][0][r] * inv, uv = acc[m][sb][1][r] * inv;
-                s_act[row * AS + 64 * nq + 16 * sb + n] = vmi_f32_to_bf16(gv / (1.0f + expf(-gv)) * uv);
+                // hardware exp2 and reciprocal (about 1 ulp each): the value is
+                // rounded to bf16 right after
+                const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv * 1.44269504f));
+                s_act[row * AS + 64 * nq + 16 * sb + n] = vmi_f32_to_bf16(gv * sg * uv);
             }
         }
     __syncthreads();
@@ -645,14 +707,24 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         o[3] = (uint32_t)b[3] | ((uint32_t)b[7] << 16);
         a.actop[(size_t)route * IW + (n0 >> 3) + wd] = o;
     }
-    for (int i = tid; i < kTM3 * ng; i += kPf8Threads) {
-        const int row = i / ng, gg = i - row * ng;
-        const int route = s_route[row];
-        if (route < 0) continue;
+    // group sums of the bf16 activations: eight lanes per (row, group), each
+    // adding 8 values in column order, then a fixed xor tree over the eight
+    for (int i0 = 0; i0 < kTM3 * ng * 8; i0 += kPf8Threads) {
+        const int i = i0 + tid;
+        const int e = i >> 3, part = i & 7;
+        const int row = e / max(ng, 1), gg = e - row * max(ng, 1);
         float sum = 0.0f;
-        for (int c = 0; c < 64; ++c) sum += vmi_bf16_to_f32(s_act[row * AS + 64 * gg + c]);
-        a.axs[(size_t)route * IG + (n0 >> 6) + gg] = sum;
+        if (i < kTM3 * ng * 8) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) sum += vmi_bf16_to_f32(s_act[row * AS + 64 * gg + 8 * part + c]);
+        }
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 4);
+        if (i < kTM3 * ng * 8 && part == 0 && s_route[row] >= 0)
+            a.axs[(size_t)s_route[row] * IG + (n0 >> 6) + gg] = sum;
     }
+    VMI_STAMP(4, 12);
 }
 
 // Down: tile 128 routes x 512 hidden rows, K = I, eight waves in a 2 x 4 grid
@@ -688,15 +760,30 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     if (tid < kTM3) s_route[tid] = tile_route(a, tl, tid);
     const int G8 = (G + 7) & ~7;
     if ((G & 7) == 0) {
-        for (int i = tid; i < 2 * 512 * (G / 8); i += kPf8Threads) {
-            const int c = i % (G / 8), row = (i / (G / 8)) % 512, sb = i / (G / 8 * 512);
-            const uint4 v = *reinterpret_cast<const uint4*>((sb ? Dm.b : Dm.s) + (mrow0 + row) * G + 8 * c);
-            uint16_t* dst = sb ? &s_b16[row][8 * c] : &s_s16[row][8 * c];
-            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+        // all loads first, then the stores (one memory latency, not one per iteration)
+        constexpr int kIt = (2 * 512 * (MAXG / 8) + kPf8Threads - 1) / kPf8Threads;
+        const int n16 = 2 * 512 * (G / 8);
+        uint4 v[kIt];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                dst[2 * j] = (uint16_t)(wv[j] & 0xffffu);
-                dst[2 * j + 1] = (uint16_t)(wv[j] >> 16);
+        for (int it = 0; it < kIt; ++it) {
+            const int i = tid + kPf8Threads * it;
+            if (i < n16) {
+                const int c = i % (G / 8), row = (i / (G / 8)) % 512, sb = i / (G / 8 * 512);
+                v[it] = *reinterpret_cast<const uint4*>((sb ? Dm.b : Dm.s) + (mrow0 + row) * G + 8 * c);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int i = tid + kPf8Threads * it;
+            if (i < n16) {
+                const int c = i % (G / 8), row = (i / (G / 8)) % 512, sb = i / (G / 8 * 512);
+                uint16_t* dst = sb ? &s_b16[row][8 * c] : &s_s16[row][8 * c];
+                const uint32_t wv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    dst[2 * j] = (uint16_t)(wv[j] & 0xffffu);
+                    dst[2 * j + 1] = (uint16_t)(wv[j] >> 16);
+                }
             }
         }
     } else {
@@ -707,17 +794,31 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         }
     }
     __syncthreads();
-    for (int i = tid; i < kTM3 * G8; i += kPf8Threads) {
-        const int row = i / G8, g = i - row * G8;
-        const int rt = s_route[row];
-        s_as[row][g] = rt >= 0 && g < G ? a.axs[(size_t)rt * G + g] : 0.0f;
+    {
+        constexpr int kIt = (kTM3 * MAXG + kPf8Threads - 1) / kPf8Threads;
+        float v[kIt];
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int i = tid + kPf8Threads * it;
+            const int row = i / G8, g = i - row * G8;
+            v[it] = 0.0f;
+            if (i < kTM3 * G8) {
+                const int rt = s_route[row];
+                if (rt >= 0 && g < G) v[it] = a.axs[(size_t)rt * G + g];
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int i = tid + kPf8Threads * it;
+            if (i < kTM3 * G8) s_as[i / G8][i % G8] = v[it];
+        }
     }
     const vmi_u4* asrc[2];
     const uint32_t* bsrc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int p = tid + kPf8Threads * j;
-        const int arow = p >> 3, c = (p & 7) ^ (arow & 7);
+        const int arow = p >> 3, c = pf_a_piece(arow, p & 7);
         const int rt = s_route[arow];
         asrc[j] = a.actop + (size_t)(rt >= 0 ? rt : 0) * IW + c;
         const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
@@ -864,7 +965,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_router3(PfArgs a) {
     const vmi_u4* asrc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int p = tid + kPfThreads * j, row = p >> 3, c = (p & 7) ^ (row & 7);
+        const int p = tid + kPfThreads * j, row = p >> 3, c = pf_a_piece(row, p & 7);
         asrc[j] = xop + (size_t)min(t0 + row, a.T - 1) * HW + c;
     }
     constexpr int NBD = BITS == 8 ? 2 : 1;  // weight pieces per thread and group
@@ -1198,3 +1299,9 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill launch");
 }
+
+#ifdef VMI_TIMELINE
+extern "C" int vmi_timeline_set_prefill(unsigned long long* buf) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(vmi_tl_buf), &buf, sizeof(buf)) == hipSuccess ? 0 : -1;
+}
+#endif
