@@ -21,6 +21,12 @@
   each path's chain forward bit for bit; committing the winner leaves every
   cache as a chain forward of its accepted prefix would; tree decoding emits
   the greedy stream.
+* The minimal tree (draft_tree, drafter.py:102-148) and the adaptive tree
+  (draft_adaptive_tree, drafter.py:64-100): the branches fork from the MTP
+  state where the reference forks them (checked against draft, draft_paths,
+  draft_adaptive and the MTP logits from the same state); decoding with them
+  emits the greedy stream, and planted trees make the position-0 and
+  position-1 rescues win (generate.py:764-801).
 """
 import sys
 
@@ -330,3 +336,129 @@ def test_tree_decode_equals_greedy(gpu, model):
         if planted:
             assert set(st.accept_hist) == set(range(K + 1)), st.accept_hist
         log(f"accept_hist {st.accept_hist}")
+
+
+def _same_state(drafter, base):
+    drafter.cache.length = base
+
+
+def test_draft_tree_branches(gpu, model):
+    """draft_tree's rows: A = the greedy chain (draft), B = the second-best
+    first token continued greedily (draft_paths' second path), C = A's first
+    token, then the second-best second token continued greedily."""
+    log("case: draft_tree K=3 pos1")
+    import torch
+    from vates_amd.decode import prefill
+    from vates_amd.mtp import MTPDrafter
+    K = 3
+    prompt = _prompt(gpu, seed=15)
+    caches = model.new_caches(128)
+    drafter = MTPDrafter(model.mtp, 128)
+    x, h = prefill(model, prompt, caches, drafter)
+    base = drafter.cache.length
+    tree = drafter.draft_tree(h, x, K, pos1=True).cpu().numpy()
+    _same_state(drafter, base)
+    chain = drafter.draft(h, x, K).cpu().numpy()
+    _same_state(drafter, base)
+    two = drafter.draft_paths(h, x, K, 2).cpu().numpy()
+    _same_state(drafter, base)
+    _, h1, _ = model.mtp.step(h, x, drafter.cache)
+    a0 = torch.tensor([int(tree[0, 0])], dtype=torch.int32, device=gpu)
+    _, h2, lg2 = model.mtp.step(h1, a0, drafter.cache, want_logits=True)
+    lg = lg2[0].cpu().numpy()
+    second = int(np.lexsort((np.arange(lg.size), -lg))[1])
+    cont = [int(tree[0, 0]), second]
+    hh, tok = h2, torch.tensor([second], dtype=torch.int32, device=gpu)
+    for _ in range(K - 2):
+        am, hh, _ = model.mtp.step(hh, tok, drafter.cache)
+        cont.append(int(am.cpu()[0]))
+        tok = am
+    torch.cuda.synchronize()
+    assert tree.shape == (3, K)
+    assert tree[0].tolist() == chain.tolist()
+    assert tree[1].tolist() == two[1].tolist()
+    assert tree[2].tolist() == cont
+    log(f"tree {tree.tolist()}")
+    _same_state(drafter, base)
+    t2 = drafter.draft_tree(h, x, K, pos1=False).cpu().numpy()
+    assert t2.shape == (2, K) and t2[0].tolist() == chain.tolist() and t2[1].tolist() == two[1].tolist()
+
+
+def test_draft_adaptive_tree_branches(gpu, model):
+    """draft_adaptive_tree: chain A equals draft_adaptive from the same state
+    (tau at each end of the range and in between); chain B (when A is at least
+    two long) is the second-best first token continued greedily to A's
+    length."""
+    from vates_amd.decode import prefill
+    from vates_amd.mtp import MTPDrafter
+    K = 3
+    prompt = _prompt(gpu, seed=16)
+    Pr = _sample_probs(gpu, model, prompt)
+    caches = model.new_caches(128)
+    drafter = MTPDrafter(model.mtp, 128)
+    x, h = prefill(model, prompt, caches, drafter)
+    base = drafter.cache.length
+    seen = set()
+    for tau in (0.0, float(np.median(Pr[:, 0])), float(Pr[:, 0].max()) * 0.999, 1.5):
+        log(f"case: draft_adaptive_tree K=3 tau={tau:.3g}")
+        _same_state(drafter, base)
+        a, b = drafter.draft_adaptive_tree(h, x, K, tau)
+        _same_state(drafter, base)
+        ref = drafter.draft_adaptive(h, x, K, tau)
+        n = a.numel()
+        assert a.cpu().tolist() == ref.cpu().tolist()
+        if n >= 2:
+            _same_state(drafter, base)
+            two = drafter.draft_paths(h, x, n, 2)
+            assert b is not None and b.cpu().tolist() == two[1].cpu().tolist()
+        else:
+            assert b is None
+        seen.add(n)
+    assert 1 in seen and K in seen, seen
+
+
+def test_tree_modes_equal_greedy(gpu, model):
+    """Decoding with the minimal tree (with and without the position-1 branch)
+    and with the adaptive tree emits the greedy stream; planted minimal trees
+    make A, B (position-0 rescue) and C (position-1 rescue) win in turn."""
+    from vates_amd.decode import greedy_decode, prefill, tree_speculative_decode
+    from vates_amd.mtp import MTPDrafter
+    n_tok, K = 30, 3
+    prompt = _prompt(gpu, seed=17)
+    Pn = prompt.numel()
+    V = SMALL["vocab"]
+    Pr = _sample_probs(gpu, model, prompt)
+    caches = model.new_caches(256)
+    x, h = prefill(model, prompt, caches)
+    ref = greedy_decode(model, caches, x, Pn, n_tok + 2 * (K + 1))
+
+    def plant(step, pos):
+        base = pos - Pn
+        t = [ref.tokens[base + i] for i in range(K)]
+        bad = lambda v, d: (v + d) % V
+        case = step % 4
+        if case == 0:    # A matches two, B and C do not reach past it
+            return [[t[0], t[1], bad(t[2], 1)], [bad(t[0], 2), t[1], t[2]], [t[0], bad(t[1], 3), t[2]]]
+        if case == 1:    # A rejects at position 0, B's first token is the model's
+            return [[bad(t[0], 1), t[1], t[2]], [t[0], t[1], bad(t[2], 2)], [bad(t[0], 1), t[1], t[2]]]
+        if case == 2:    # A rejects at position 1, C's second token is the model's
+            return [[t[0], bad(t[1], 1), t[2]], [bad(t[0], 2), t[1], t[2]], [t[0], t[1], t[2]]]
+        # every path rejects at position 0: the lowest index, A, stands
+        return [[bad(t[0], 1), t[1], t[2]], [bad(t[0], 2), t[1], t[2]], [bad(t[0], 1), bad(t[1], 3), t[2]]]
+
+    runs = [("tree", dict(pos1=True), None), ("tree", dict(pos1=False), None), ("tree", dict(pos1=True), plant),
+            ("adaptive_tree", dict(tau=float(np.median(Pr[:, 0]))), None)]
+    for mode, kw, pl in runs:
+        log(f"case: tree decode mode={mode} {kw} planted={pl is not None}")
+        caches = model.new_caches(256)
+        drafter = MTPDrafter(model.mtp, 256)
+        x, h = prefill(model, prompt, caches, drafter)
+        st = tree_speculative_decode(model, drafter, caches, x, h, Pn, n_tok, K=K, mode=mode, plant=pl, **kw)
+        assert st.tokens == ref.tokens[:n_tok], (st.tokens, ref.tokens[:n_tok])
+        log(f"accept_hist {st.accept_hist} winners {st.rescues} depths {st.depths}")
+        if pl is not None:
+            assert set(st.rescues) == {0, 1, 2}, st.rescues
+            for i, w in enumerate(st.rescues):
+                assert w == (0, 1, 2, 0)[i % 4], (i, w)
+        if mode == "adaptive_tree":
+            assert all(1 <= d <= K for d in st.depths)

@@ -82,11 +82,17 @@ class KVCache:
         self.length = 0  # committed positions
         self.n_kv = n_kv_heads
         self.tree_kv = None  # [paths, n_kv, 2, span, 256] bf16: a draft tree's new keys and values
+        self._tree_flat = None
 
     def tree_buffer(self, paths: int, span: int) -> torch.Tensor:
-        shape = (paths, self.n_kv, 2, span, 256)
-        if self.tree_kv is None or tuple(self.tree_kv.shape) != shape:
-            self.tree_kv = torch.zeros(shape, dtype=torch.bfloat16, device=self.k.device)
+        """The tree forward's keys and values [paths, n_kv, 2, span, 256]: one
+        allocation for every tree of at most 16 tokens, so commit tables built
+        for different (paths, span) see the same address."""
+        if paths * span > 16:
+            raise VmiError(f"a tree of {paths} x {span} tokens exceeds 16")
+        if self._tree_flat is None:
+            self._tree_flat = torch.zeros(16 * self.n_kv * 2 * 256, dtype=torch.bfloat16, device=self.k.device)
+        self.tree_kv = self._tree_flat[:paths * self.n_kv * 2 * span * 256].view(paths, self.n_kv, 2, span, 256)
         return self.tree_kv
 
     def trim(self, n: int) -> None:

@@ -49,6 +49,7 @@ class DecodeStats:
     steps: int = 0
     accept_hist: List[int] = field(default_factory=list)   # matched drafts per step
     depths: List[int] = field(default_factory=list)        # drafts verified per step (adaptive depth)
+    rescues: List[int] = field(default_factory=list)       # tree decoding: the winning path per step
     drafts: List[List[int]] = field(default_factory=list)  # the drafts of each step (with trace=True)
     seconds: float = 0.0
 
@@ -278,44 +279,75 @@ def speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: torch.T
 
 
 def tree_speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: torch.Tensor, H_last: torch.Tensor,
-                            pos: int, n_tokens: int, K: int = 3, P: int = 3, plant=None) -> DecodeStats:
+                            pos: int, n_tokens: int, K: int = 3, P: int = 3, plant=None, *, mode: str = "paths",
+                            pos1: bool = True, tau: Optional[float] = None) -> DecodeStats:
     """Tree verification (tree_verify_step, generate.py:355-420): the MTP
-    drafter's P paths (draft_paths: top-P first tokens, greedy continuations,
-    drafter.py:150-177), each [x, d1..d_{K-1}] (the T = K layout), verified in
-    one forward over the P x K tokens (``SpecModel.forward_tree``); the winner
+    drafter's paths, each [x, d1..d_{K-1}] (the T = K layout), verified in
+    one forward over the paths' tokens (``SpecModel.forward_tree``); the winner
     is the longest matched prefix, ties to the lower path (vmi_accept_greedy,
     generate.py:383); emission and accepted length as accept_prefix's T = K
     rules (generate.py:338-351, 819); the winner's entries are committed into
     every cache in one launch (``TreeCommit``, commit_tree_row,
-    kv_cache.py:283-316).  plant(step, pos) -> P x K draft tokens replaces the
-    drafts (tests)."""
+    kv_cache.py:283-316).  Drafting (mode):
+      "paths"          P paths: top-P first tokens, greedy continuations
+                       (draft_paths, drafter.py:150-177);
+      "tree"           the minimal tree A, B (position-0 rescue) and, with
+                       pos1, C (position-1 rescue) (draft_tree,
+                       drafter.py:102-148; generate.py:587-588, 764-801);
+      "adaptive_tree"  a confidence-gated chain of depth n <= K with tau and,
+                       when n >= 2, its position-0 branch (draft_adaptive_tree,
+                       drafter.py:64-100; generate.py:592-599, 764-784): the
+                       step verifies depth n.
+    Verified together, the lowest-index longest match picks the same path as
+    the reference's sequential rescue: a branch wins only where the chain
+    before it rejected exactly at its fork and the branch's token there is the
+    model's.  plant(step, pos) -> rows x K draft tokens replaces the drafts of
+    "paths" and "tree" (tests)."""
     if model.mtp is None:
         raise VmiError("the model has no MTP layer")
-    if P * K > 16:
-        raise VmiError(f"a tree of {P} x {K} tokens exceeds 16")
+    if mode not in ("paths", "tree", "adaptive_tree"):
+        raise VmiError(f"unknown tree mode {mode!r}")
+    if mode == "adaptive_tree" and tau is None:
+        raise VmiError("adaptive_tree needs tau")
+    width = P if mode == "paths" else (3 if mode == "tree" and pos1 and K >= 2 else 2)
+    if width * K > 16:
+        raise VmiError(f"a tree of {width} x {K} tokens exceeds 16")
     st = DecodeStats()
     dev = x.device
-    commit = TreeCommit(caches, P, K)
+    commits = {}
     t0 = time.perf_counter()
     while len(st.tokens) < n_tokens:
         mtp_start = drafter.cache.length
-        paths = drafter.draft_paths(H_last, x, K, P)           # [P, K]
-        if plant is not None:
-            paths.copy_(torch.tensor(plant(st.steps, pos), dtype=torch.int32))
-        verify = torch.cat([x.view(1, 1).expand(P, 1), paths[:, :K - 1]], dim=1).contiguous()  # [P, K]
-        preds, hid, _ = model.forward_tree(verify.view(-1), caches, pos, P)
+        if mode == "paths":
+            paths = drafter.draft_paths(H_last, x, K, P)       # [P, K]
+            if plant is not None:
+                paths.copy_(torch.tensor(plant(st.steps, pos), dtype=torch.int32))
+        elif mode == "tree":
+            paths = drafter.draft_tree(H_last, x, K, pos1)      # [2 or 3, K]
+            if plant is not None:
+                paths.copy_(torch.tensor(plant(st.steps, pos), dtype=torch.int32))
+        else:
+            chain_a, chain_b = drafter.draft_adaptive_tree(H_last, x, K, tau)
+            paths = (chain_a.view(1, -1) if chain_b is None else torch.stack([chain_a, chain_b])).contiguous()
+        pw, span = paths.shape
+        commit = commits.get((pw, span))
+        if commit is None:
+            commit = commits[(pw, span)] = TreeCommit(caches, pw, span)
+        verify = torch.cat([x.view(1, 1).expand(pw, 1), paths[:, :span - 1]], dim=1).contiguous()  # [pw, span]
+        preds, hid, _ = model.forward_tree(verify.view(-1), caches, pos, pw)
         rec = accept_greedy(paths, preds, mode=0)
         commit(rec, pos0=pos)
         r = rec.cpu().tolist()  # the step's one host synchronisation
         n, m, acc, best = r[0], r[1], r[2], r[3]
         emitted = r[4:4 + n]
         model.commit(caches, pos + acc)
-        w0 = best * K
+        w0 = best * span
         h_seq = torch.cat([H_last, hid[w0:w0 + acc - 1]]) if acc > 1 else H_last
         drafter.sync(mtp_start, h_seq.contiguous(), verify[best, :acc].contiguous())
         st.tokens.extend(emitted)
         st.accept_hist.append(m)
-        st.depths.append(K)
+        st.depths.append(span)
+        st.rescues.append(best)
         st.steps += 1
         pos += acc
         x = torch.tensor([emitted[-1]], dtype=torch.int32, device=dev)

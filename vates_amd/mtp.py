@@ -151,6 +151,87 @@ class MTPDrafter:
                 tok = paths[p, i:i + 1]
         return paths
 
+    def _top2(self, logits: torch.Tensor) -> torch.Tensor:
+        """The two largest logits' token ids of a [1, V] row, int32 [2]
+        (descending, ties to the lower id)."""
+        out = torch.empty((1, 2), dtype=torch.int32, device=logits.device)
+        check(load().vmi_topk_rows(logits.data_ptr(), 1, logits.shape[1], 2, out.data_ptr(), None,
+                                   _stream_handle(None)), "vmi_topk_rows")
+        return out[0]
+
+    def _continue(self, h: torch.Tensor, first: torch.Tensor, n: int, out: torch.Tensor) -> None:
+        """out[0] = first; then n greedy drafts from MTP hidden h (drafter.py's
+        _continue helpers)."""
+        out[0:1].copy_(first)
+        tok = out[0:1]
+        for i in range(1, n + 1):
+            am, h, _ = self.mtp.step(h, tok, self.cache)
+            out[i:i + 1].copy_(am)
+            tok = out[i:i + 1]
+
+    def draft_tree(self, H_last: torch.Tensor, x_tok: torch.Tensor, K: int, pos1: bool = True) -> torch.Tensor:
+        """The minimal tree (draft_tree, drafter.py:102-148): rows [A, B, C] of
+        K drafts each.  A is all top-1; B takes the second-best first token
+        (the position-0 rescue); C (pos1, K >= 2) keeps A's first token and
+        takes the second-best second token (the position-1 rescue).  Every
+        branch continues greedily from the MTP state at its fork: the cache
+        length is set back to the fork (drafter.py's _restore).  Verified
+        together (``tree_speculative_decode``), the longest matched prefix with
+        ties to the lower row picks the path the reference's sequential rescue
+        (generate.py:764-801) ends on."""
+        if K < 1:
+            raise VmiError("K must be at least 1")
+        dev = H_last.device
+        P = 3 if pos1 and K >= 2 else 2
+        paths = torch.empty((P, K), dtype=torch.int32, device=dev)
+        _, h1, lg1 = self.mtp.step(H_last, x_tok, self.cache, want_logits=True)
+        t1 = self._top2(lg1)                       # [d1a, d1b]
+        base = self.cache.length                   # the state after x
+        if P == 3:
+            _, h2, lg2 = self.mtp.step(h1, t1[0:1], self.cache, want_logits=True)
+            t2 = self._top2(lg2)                   # [d2a, d2c]
+            base2 = self.cache.length              # the state after d1a
+            paths[0, 0:1].copy_(t1[0:1])
+            paths[2, 0:1].copy_(t1[0:1])
+            self._continue(h2, t2[0:1], K - 2, paths[0, 1:])
+            self.cache.length = base2
+            self._continue(h2, t2[1:2], K - 2, paths[2, 1:])
+        else:
+            self._continue(h1, t1[0:1], K - 1, paths[0])
+        self.cache.length = base
+        self._continue(h1, t1[1:2], K - 1, paths[1])
+        return paths
+
+    def draft_adaptive_tree(self, H_last: torch.Tensor, x_tok: torch.Tensor, depth_max: int, tau: float):
+        """Confidence-gated depth with the position-0 branch
+        (draft_adaptive_tree, drafter.py:64-100): (chainA int32 [n], chainB
+        int32 [n] or None).  chainA is greedy while the running product of its
+        drafts' softmax probabilities stays at or above tau (1 <= n <=
+        depth_max, the product in fp32 on the host as ``draft_adaptive``);
+        chainB, only when n >= 2, takes the second-best first token and
+        continues greedily to the same length from the state after x."""
+        if depth_max < 1:
+            raise VmiError("depth_max must be at least 1")
+        dev = H_last.device
+        a = torch.empty(depth_max, dtype=torch.int32, device=dev)
+        probs = torch.empty(depth_max, dtype=torch.float32, device=dev)
+        _, h1, lg1 = self.mtp.step(H_last, x_tok, self.cache, want_logits=True, argmax_out=a[0:1],
+                                   prob_out=probs[0:1])
+        t1 = self._top2(lg1)
+        base = self.cache.length
+        conf = np.float32(probs[0].item())
+        n, h = 1, h1
+        while n < depth_max and conf >= tau:
+            _, h, _ = self.mtp.step(h, a[n - 1:n], self.cache, argmax_out=a[n:n + 1], prob_out=probs[n:n + 1])
+            conf = np.float32(conf * np.float32(probs[n].item()))
+            n += 1
+        chain_b = None
+        if n >= 2:
+            self.cache.length = base
+            chain_b = torch.empty(n, dtype=torch.int32, device=dev)
+            self._continue(h1, t1[1:2], n - 1, chain_b)
+        return a[:n], chain_b
+
     def sync(self, start: int, h_seq: torch.Tensor, tokens: torch.Tensor) -> None:
         """Replaces the draft-time cache entries from `start` by the accepted
         positions' (main hidden, token) pairs (drafter.py:178-188)."""
