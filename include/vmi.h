@@ -456,7 +456,7 @@ int vmi_accept_greedy(const int32_t* drafts, const int32_t* preds, int P, int K,
  * the next input x), :895 (H_last = rH[:, -1]) and kv_cache.py:222-251
  * (committing the accepted prefix by setting lengths); tree_verify_step's
  * winner row, generate.py:386 and :416-420.  A record with no emitted token, acc
- * outside [1, rows], more than rows + 1 tokens or a path outside [0, paths)
+ * outside [1, rows], more than rows tokens or a path outside [0, paths)
  * changes nothing and ORs VMI_STATUS_BAD_RECORD into *status (may be NULL).
  * H must not overlap hid.  K <= 15, rows <= 16.
  * ------------------------------------------------------------------------ */

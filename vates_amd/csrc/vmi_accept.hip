@@ -894,7 +894,8 @@ struct CommitArgs {
 
 __global__ __launch_bounds__(256) void k_spec_commit(CommitArgs a) {
     const int n = a.rec[0], acc = a.rec[2], w = a.rec[3];
-    if (n < 1 || n > a.rows + 1 || acc < 1 || acc > a.rows || w < 0 || w >= a.paths) {
+    // a valid record emits at most one token per verify row
+    if (n < 1 || n > a.rows || acc < 1 || acc > a.rows || w < 0 || w >= a.paths) {
         if (threadIdx.x == 0 && a.status) atomicOr(a.status, VMI_STATUS_BAD_RECORD);
         return;
     }
