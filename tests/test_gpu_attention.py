@@ -95,8 +95,13 @@ def make_attention(gpu, seed, H=2048, n_heads=16, n_kv=2):
     return layer, A
 
 
+# Capacities up to 32,768 positions split the keys into 256-key chunks; 33,376 into 288-key chunks
+# (9 blocks: 2 x 116 chunks fit 256 CUs) and 40,960 into 320-key chunks (10 blocks), where the
+# batch's keys land in a chunk's extra blocks (positions 288c + 256.., 320c + 256..) or straddle a
+# chunk boundary (33,120 = 115 x 288).
 @pytest.mark.parametrize("T,pos0,max_len", [(1, 0, 256), (4, 0, 256), (1, 63, 256), (4, 200, 512), (4, 1000, 2048),
-                                            (1, 4095, 4096), (4, 30000, 32768)])
+                                            (1, 4095, 4096), (4, 30000, 32768), (4, 33090, 33376),
+                                            (4, 33118, 33376), (1, 39000, 40960), (4, 39006, 40960)])
 def test_attention_layer_parity(gpu, orc, T, pos0, max_len):
     log(f"case: attention layer H=2048 16/2 heads T={T} pos0={pos0} max_len={max_len}")
     import torch
@@ -128,13 +133,13 @@ def test_attention_layer_parity(gpu, orc, T, pos0, max_len):
     assert not changed[~touched].any()
 
 
-def test_attention_batch_equals_steps(gpu, orc):
-    log("case: attention T=4 batch vs four single-token steps")
+@pytest.mark.parametrize("pos0,max_len", [(500, 1024), (33117, 33376), (39005, 40960)])
+def test_attention_batch_equals_steps(gpu, orc, pos0, max_len):
+    log(f"case: attention T=4 batch vs four single-token steps pos0={pos0} max_len={max_len}")
     import torch
     from vates_amd.synth import synth_bf16
     layer, A = make_attention(gpu, 82)
-    pos0 = 500
-    c1, c2 = layer.new_cache(1024), layer.new_cache(1024)
+    c1, c2 = layer.new_cache(max_len), layer.new_cache(max_len)
     pre_k = synth_bf16(82, 20, (2, pos0, 256), device=gpu)
     pre_v = synth_bf16(82, 21, (2, pos0, 256), device=gpu)
     for c in (c1, c2):
@@ -167,3 +172,33 @@ def test_attention_position_on_device(gpu):
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     assert torch.equal(c1.k.view(torch.int16), c2.k.view(torch.int16))
     assert torch.equal(c1.v.view(torch.int16), c2.v.view(torch.int16))
+
+
+@pytest.mark.parametrize("pos0,max_len", [(1000, 2048), (33090, 33376), (39005, 40960)])
+def test_attention_tree_equals_paths(gpu, pos0, max_len):
+    """The block over a tree of 3 paths x 3 tokens equals each path run alone
+    on a copy of the cache, bit for bit: outputs, and the path's new keys and
+    values against the entries the single-path call wrote (256-, 288- and
+    320-key chunks)."""
+    log(f"case: attention tree 3 x 3 vs paths pos0={pos0} max_len={max_len}")
+    import torch
+    from vates_amd.synth import synth_bf16
+    layer, _ = make_attention(gpu, 84)
+    P, S = 3, 3
+    base = layer.new_cache(max_len)
+    base.write(0, synth_bf16(84, 20, (2, pos0, 256), device=gpu), synth_bf16(84, 21, (2, pos0, 256), device=gpu))
+    base.length = pos0
+    x = synth_bf16(84, 30, (P * S, 2048), device=gpu)
+    out_t = layer.tree(x, base, P, pos0=pos0)
+    tkv = base.tree_kv.clone()
+    torch.cuda.synchronize()
+    for p in range(P):
+        c = layer.new_cache(max_len)
+        c.k.copy_(base.k)
+        c.v.copy_(base.v)
+        c.length = pos0
+        o = layer(x[p * S:(p + 1) * S].contiguous(), c, pos0=pos0)
+        torch.cuda.synchronize()
+        assert torch.equal(out_t[p * S:(p + 1) * S].view(torch.int16), o.view(torch.int16)), f"path {p}: output"
+        assert torch.equal(tkv[p, :, 0].view(torch.int16), c.keys(pos0, pos0 + S).view(torch.int16)), f"path {p}: keys"
+        assert torch.equal(tkv[p, :, 1].view(torch.int16), c.values(pos0, pos0 + S).view(torch.int16)), f"path {p}: values"

@@ -16,15 +16,18 @@
 //   k_qgemv        y[t][n] = sum_k x[t][k] W[n][k], 4/8-bit affine W, T <= 8:
 //                  one wave per output row, 16 bytes of packed weights per
 //                  lane per step, tokens staged in LDS, fp32 accumulation
-//   k_attn_chunk   per (kv head, chunk of 256 keys), 8 waves: while the
+//   k_attn_chunk   per (kv head, chunk of 256, 288 or 320 keys: 8 + NX
+//                  blocks of 32, NX set by the cache capacity so that one
+//                  workgroup per CU covers the cache), 8 waves: while the
 //                  chunk's keys and values stream in, the workgroup forms the
 //                  head group's queries (q RMSNorm, rotary, bf16) and, in the
 //                  chunk holding a batch position, that position's key and
 //                  value (k RMSNorm, rotary), appended to the cache and put
 //                  into the loaded operands; wave w scores the 32-key block w
-//                  against the query rows (S^T = K Q^T), the chunk max and the
-//                  bf16 probabilities go through LDS, then wave w forms P V
-//                  for dims 32w..32w+31 over all 256 keys; writes (max, sum, O)
+//                  (waves x < NX also block 8 + x, staged in LDS) against the
+//                  query rows (S^T = K Q^T), the chunk max and the bf16
+//                  probabilities go through LDS, then wave w forms P V for
+//                  dims 32w..32w+31 over all the chunk's keys; writes (max, sum, O)
 //   k_attn_merge   per (token, head, quarter of the dims): merges the chunks
 //                  in a fixed order, times sigmoid(gate), bf16 input of o_proj
 //
@@ -38,6 +41,8 @@
 //          keys, already the A operand of P V);
 //   values element ((dt*64 + q4*16 + nl)*8 + e) holds position 8*q4 + e,
 //          dim 16*dt + nl (the B operand of P V).
+
+#include <type_traits>
 
 #include "vmi_device.h"
 #include "vmi_internal.h"
@@ -216,7 +221,8 @@ struct AttnArgs {
     const uint16_t* q_norm;   // [256]
     const uint16_t* k_norm;   // [256]
     int rope_dim;
-    float theta, eps;
+    float eps;
+    double rope_base;         // theta^(-2/rope_dim), in double
     uint16_t* k_cache;        // blocks of 32 positions, see the layout above
     uint16_t* v_cache;
     int T, n_heads, n_kv, pos0, max_len;
@@ -229,11 +235,13 @@ struct AttnArgs {
     float* part_o;            // [n_kv, nstride, RP, 256]
     float* part_ml;           // [n_kv, nstride, RP, 2]
     uint16_t* o;              // [T, n_heads * 256] bf16 gated attention output
+    int chunk_keys;           // keys per chunk: 32 (8 + extra blocks)
 };
 
 constexpr int kChunkWaves = 8;                         // one cache block per wave
 constexpr int kChunkThreads = 64 * kChunkWaves;
-constexpr int kChunkKeys = kChunkWaves * kKvBlock;     // 256
+constexpr int kChunkKeys = kChunkWaves * kKvBlock;     // 256: the shortest chunk
+constexpr int kMaxExtraBlocks = 2;                     // blocks per chunk beyond one per wave
 
 __device__ __forceinline__ vmi_u4 keep_first(vmi_u4 v, int n) {  // zero bf16 elements e >= n
 #pragma unroll
@@ -277,25 +285,30 @@ __device__ __forceinline__ void norm_rope_row(float (&v)[4], const float (&nw)[4
 }
 
 // Rows of a head group: row = t * G + hl (G = n_heads / n_kv query heads per
-// kv head), RP = 16 MS >= T * G.  Loads in issue order: the projections of
-// the wave's query rows (rows w, w + 8, ...), in the chunk holding batch
-// positions the key and value projections of one of them per wave, then the
-// keys of the wave's block (16 x 1 KB) and values of all 8 blocks for the
-// wave's 32 dims (16 x 1 KB); the queries and new keys are formed while the
-// cache streams.  Positions >= pos0 + T are not read past their block; inside
+// kv head), RP = 16 MS >= T * G.  A chunk is NB = 8 + NX blocks of 32 keys:
+// wave w scores block w from registers, and waves x < NX also score block
+// 8 + x, whose keys every wave helps stage in LDS (2 KB each).  Loads in issue
+// order: the projections of the wave's query rows (rows w, w + 8, ...), in the
+// chunk holding batch positions the key and value projections of one of them
+// per wave, then the keys of the wave's block (16 x 1 KB), its share of the
+// extra blocks' keys, and values of all NB blocks for the wave's 32 dims
+// (2 NB x 1 KB); the queries and new keys are formed while the cache streams.  Positions >= pos0 + T are not read past their block; inside
 // the last block they are masked (scores -inf, values zeroed), so stale cache
 // contents never reach the result.  The batch's own positions are read from
 // the cache too, before this workgroup writes them: their operands are then
 // replaced by the new keys and values.
-template <int MS>
+template <int MS, int NX>
 __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     constexpr int RP = 16 * MS;
+    constexpr int NB = kChunkWaves + NX;  // blocks per chunk
+    constexpr int CK = NB * kKvBlock;     // keys per chunk
+    static_assert(NX >= 0 && NX <= kMaxExtraBlocks, "extra blocks");
     __shared__ __attribute__((aligned(16))) uint16_t s_q[RP][kHeadDim + 8];
-    __shared__ vmi_u4 s_pa[MS][kChunkWaves][64];
+    __shared__ vmi_u4 s_pa[MS][NB][64];
+    __shared__ vmi_u4 s_kx[NX > 0 ? NX : 1][16][64];  // keys of block 8 + x, operand order
     __shared__ float s_wm[kChunkWaves][RP], s_wl[kChunkWaves][RP];
     // chunks in reverse launch order: the last (partly filled) chunk and those
-    // past the cache take the first CUs and free them early, so the full
-    // chunks beyond one per CU start while the first ones still stream
+    // past the cache take the first CUs and free them early
     __shared__ float s_row[kChunkWaves][kHeadDim];                  // a wave's normalised row
     __shared__ float2 s_cs[kQgMaxT][kHeadDim / 2];                  // (cos, sin) per (token, frequency)
     __shared__ __attribute__((aligned(16))) uint16_t s_new[2][kQgMaxT][kHeadDim];  // new keys, values (bf16)
@@ -313,6 +326,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         if (c < 0) return;
     }
     const int g = blockIdx.y, tid = threadIdx.x;
+    VMI_STAMP(4 + g, 0);
     const int lane = tid & 63, w = at_wave(), nl = lane & 15, q4 = lane >> 4;
     const int G = a.n_heads / a.n_kv, R = T * G;
     const int tok0 = p * T;                            // the path's first row of qkv
@@ -320,10 +334,10 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     if (a.pos_dev && blockIdx.x == 0 && g == 0 && tid == 0 && *a.pos_dev != pos0)
         atomicOr(a.status, VMI_STATUS_BAD_POS);    // clamped: the caller's position overran the cache
     const int L = pos0 + T;                            // positions present
-    if (c * kChunkKeys >= L) return;                   // chunk beyond the cache (whole workgroup)
-    const int b0 = c * kChunkWaves;
+    if (c * CK >= L) return;                           // chunk beyond the cache (whole workgroup)
+    const int b0 = c * NB;
     // batch tokens whose positions lie in this chunk: t_lo .. t_hi - 1
-    const int t_lo = max(0, c * kChunkKeys - pos0), t_hi = min(T, (c + 1) * kChunkKeys - pos0);
+    const int t_lo = max(0, c * CK - pos0), t_hi = min(T, (c + 1) * CK - pos0);
     const int tn = t_lo + w;                           // this wave's new position (if tn < t_hi)
     const bool has_new = w < t_hi - t_lo;
 
@@ -358,22 +372,36 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         }
     }
     asm volatile("" ::: "memory");
-    // rotary table while the projections arrive (before the cache loads: its
-    // double-precision temporaries and the cache operands are never live
-    // together); angle pos * theta^(-2i/rd) in double (fp32 rounding of
-    // angles up to ~3e4 rad would move the rotation by ~1e-3)
-    for (int i = tid; i < T * (a.rope_dim / 2); i += kChunkThreads) {
-        const int t = i / (a.rope_dim / 2), fi = i - t * (a.rope_dim / 2);
-        const double ang = (double)(pos0 + t) * pow((double)a.theta, -(double)(2 * fi) / (double)a.rope_dim);
-        s_cs[t][fi] = make_float2((float)cos(ang), (float)sin(ang));
+    // rotary table while the projections arrive: the angle pos * theta^(-2i/rd)
+    // in turns and in double (theta^(-2i/rd) as rope_base^i by repeated
+    // squaring), reduced to [-1/2, 1/2] turn, then (cos, sin) of the reduced
+    // angle in fp32: within 2e-7 of the exact values at positions up to 2^20,
+    // where fp32 rounding of the unreduced angle would move the rotation by
+    // up to 1e-3
+    {
+        const int half = a.rope_dim / 2;
+        for (int i = tid; i < T * half; i += kChunkThreads) {
+            const int t = i / half, fi = i - t * half;
+            double f = 1.0, b = a.rope_base;
+            for (int e = fi; e; e >>= 1) {
+                if (e & 1) f *= b;
+                b *= b;
+            }
+            const double turns = (double)(pos0 + t) * (f * 0.15915494309189535);  // 1 / (2 pi)
+            const float r = (float)((turns - rint(turns)) * 6.283185307179586);
+            float sn, cs;
+            sincosf(r, &sn, &cs);
+            s_cs[t][fi] = make_float2(cs, sn);
+        }
     }
+    VMI_STAMP(4 + g, 1);
     // the cache blocks: branch-free buffer loads, blocks past the cache
     // reading zeros (a load under a branch would leave every later wait
     // counting as if none of them had been issued)
     const uint32_t head_bytes = (uint32_t)(a.max_len / kKvBlock) * kKvBlockElems * 2u;
     const __amdgpu_buffer_rsrc_t rk = vmi_rsrc(a.k_cache + kv_block(g, a.max_len, 0), head_bytes);
     const __amdgpu_buffer_rsrc_t rv = vmi_rsrc(a.v_cache + kv_block(g, a.max_len, 0), head_bytes);
-    vmi_u4 kr[2][8], vr[2][kChunkWaves];
+    vmi_u4 kr[2][8], vr[2][NB];
     const int bw = b0 + w;
     {
         const uint32_t kbase = kKvBlock * bw < L ? (uint32_t)bw * kKvBlockElems * 2u + lane * 16u : VMI_OOB;
@@ -382,8 +410,18 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) kr[h][kk] = vmi_bload_b128_nt(rk, kbase + (uint32_t)(h * 8 + kk) * 1024u, 0);
     }
+    // pieces 2w, 2w + 1 (of 16 x 1 KB) of each extra block's keys
+    vmi_u4 kxr[NX > 0 ? NX : 1][2];
 #pragma unroll
-    for (int sb = 0; sb < kChunkWaves; ++sb) {
+    for (int x = 0; x < NX; ++x) {
+        const int bx = b0 + kChunkWaves + x;
+        const uint32_t xbase =
+            kKvBlock * bx < L ? (uint32_t)bx * kKvBlockElems * 2u + (uint32_t)(2 * w) * 1024u + lane * 16u : VMI_OOB;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) kxr[x][j] = vmi_bload_b128_nt(rk, xbase + (uint32_t)j * 1024u, 0);
+    }
+#pragma unroll
+    for (int sb = 0; sb < NB; ++sb) {
         const int bs = b0 + sb;
         const uint32_t vbase =
             kKvBlock * bs < L ? (uint32_t)bs * kKvBlockElems * 2u + (uint32_t)(2 * w) * 1024u + lane * 16u : VMI_OOB;
@@ -392,6 +430,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     }
 
     __syncthreads();
+    VMI_STAMP(4 + g, 2);
     float qn[4], kn[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -433,9 +472,15 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
             s_new[1][tn][d] = vb16;
         }
     }
+    // the extra blocks' keys into LDS (waiting only for those loads: the
+    // values, issued after them, keep streaming)
+#pragma unroll
+    for (int x = 0; x < NX; ++x)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) s_kx[x][2 * w + j][lane] = kxr[x][j];
     // the last block: values of positions >= L are zeroed (0 * stale could be NaN)
 #pragma unroll
-    for (int sb = 0; sb < kChunkWaves; ++sb) {
+    for (int sb = 0; sb < NB; ++sb) {
         const int p0 = kKvBlock * (b0 + sb);
         if (p0 < L && p0 + kKvBlock > L) {
 #pragma unroll
@@ -461,34 +506,77 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         }
     }
 
-    // scores: lane (nl, q4) of tile h holds keys 8 q4 + 4 h + r of block bw for query row 16 m + nl
-    float sc[MS][8];
+    // the extra block of wave w < NX: the batch's new keys into its LDS copy
+    // (only this wave reads that copy), as for the registers above
+    const bool xw = NX > 0 && w < NX;
+    const int bx = b0 + kChunkWaves + w;
+    if (xw) {
+        for (int t = t_lo; t < t_hi; ++t) {
+            const int p = pos0 + t;
+            if ((p >> 5) != bx) continue;
+            const int kt = p & (kKvBlock - 1);
+            if (nl == 4 * (kt >> 3) + (kt & 3)) {
+                const uint16_t* src = &s_new[0][t][8 * q4];
+                const int hh = (kt >> 2) & 1;
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) s_kx[w][8 * hh + kk][lane] = *reinterpret_cast<const vmi_u4*>(src + 32 * kk);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    VMI_STAMP(4 + g, 3);
+    // scores: lane (nl, q4) of tile h holds keys 8 q4 + 4 h + r of block bw
+    // (sc) and of block bx (scx, waves w < NX) for query row 16 m + nl
+    float sc[MS][8], scx[MS][8];
+    auto mask_scale = [&](const vmi_f4& acc0, const vmi_f4& acc1, int p, int last, float (&o)[8]) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            o[r] = p + r <= last ? acc0[r] * 0.0625f : -INFINITY;  // 1 / sqrt(256)
+            o[4 + r] = p + 4 + r <= last ? acc1[r] * 0.0625f : -INFINITY;
+        }
+    };
 #pragma unroll
     for (int m = 0; m < MS; ++m) {
         vmi_f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+        vmi_f4 ax0 = {0.f, 0.f, 0.f, 0.f}, ax1 = {0.f, 0.f, 0.f, 0.f};
+        if (xw) {
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            const uint4 qv = *reinterpret_cast<const uint4*>(&s_q[16 * m + nl][32 * kk + 8 * q4]);
-            const vmi_u4 qb = {qv.x, qv.y, qv.z, qv.w};
-            acc0 = vmi_mfma_bf16(kr[0][kk], qb, acc0);
-            acc1 = vmi_mfma_bf16(kr[1][kk], qb, acc1);
+            for (int kk = 0; kk < 8; ++kk) {
+                const uint4 qv = *reinterpret_cast<const uint4*>(&s_q[16 * m + nl][32 * kk + 8 * q4]);
+                const vmi_u4 qb = {qv.x, qv.y, qv.z, qv.w};
+                acc0 = vmi_mfma_bf16(kr[0][kk], qb, acc0);
+                acc1 = vmi_mfma_bf16(kr[1][kk], qb, acc1);
+                ax0 = vmi_mfma_bf16(s_kx[NX > 0 ? w : 0][kk][lane], qb, ax0);
+                ax1 = vmi_mfma_bf16(s_kx[NX > 0 ? w : 0][8 + kk][lane], qb, ax1);
+            }
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const uint4 qv = *reinterpret_cast<const uint4*>(&s_q[16 * m + nl][32 * kk + 8 * q4]);
+                const vmi_u4 qb = {qv.x, qv.y, qv.z, qv.w};
+                acc0 = vmi_mfma_bf16(kr[0][kk], qb, acc0);
+                acc1 = vmi_mfma_bf16(kr[1][kk], qb, acc1);
+            }
         }
         const int row = 16 * m + nl;
         const int last = row < R ? min(L - 1, pos0 + row / G) : -1;  // last visible position
-        const int p = kKvBlock * bw + 8 * q4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sc[m][r] = p + r <= last ? acc0[r] * 0.0625f : -INFINITY;  // 1 / sqrt(256)
-            sc[m][4 + r] = p + 4 + r <= last ? acc1[r] * 0.0625f : -INFINITY;
-        }
+        mask_scale(acc0, acc1, kKvBlock * bw + 8 * q4, last, sc[m]);
+        // a wave without an extra block masks it whole (last = -1)
+        mask_scale(ax0, ax1, kKvBlock * bx + 8 * q4, xw ? last : -1, scx[m]);
         float mx = sc[m][0];
 #pragma unroll
         for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[m][e]);
+        if (NX > 0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) mx = fmaxf(mx, scx[m][e]);
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         if (q4 == 0) s_wm[w][row] = mx;
     }
     __syncthreads();
+    VMI_STAMP(4 + g, 4);
     // probabilities against the chunk max, rounded to bf16 (the P.V operand);
     // the row sum adds the rounded values
 #pragma unroll
@@ -498,20 +586,24 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
 #pragma unroll
         for (int v = 1; v < kChunkWaves; ++v) M = fmaxf(M, s_wm[v][row]);
         float ls = 0.0f;
-        vmi_u4 pk;
+        auto probs = [&](const float (&sv)[8]) {
+            vmi_u4 pk;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float x0 = sc[m][2 * i], x1 = sc[m][2 * i + 1];
-            const uint32_t u0 = x0 == -INFINITY ? 0u : vmi_f32_to_bf16(expf(x0 - M));
-            const uint32_t u1 = x1 == -INFINITY ? 0u : vmi_f32_to_bf16(expf(x1 - M));
-            ls += vmi_bf16_to_f32(u0);
-            ls += vmi_bf16_to_f32(u1);
-            pk[i] = u0 | (u1 << 16);
-        }
+            for (int i = 0; i < 4; ++i) {
+                const float x0 = sv[2 * i], x1 = sv[2 * i + 1];
+                const uint32_t u0 = x0 == -INFINITY ? 0u : vmi_f32_to_bf16(expf(x0 - M));
+                const uint32_t u1 = x1 == -INFINITY ? 0u : vmi_f32_to_bf16(expf(x1 - M));
+                ls += vmi_bf16_to_f32(u0);
+                ls += vmi_bf16_to_f32(u1);
+                pk[i] = u0 | (u1 << 16);
+            }
+            return pk;
+        };
+        s_pa[m][w][lane] = probs(sc[m]);
+        if (xw) s_pa[m][NX > 0 ? kChunkWaves + w : 0][lane] = probs(scx[m]);
         ls += __shfl_xor(ls, 16);
         ls += __shfl_xor(ls, 32);
         if (q4 == 0) s_wl[w][row] = ls;
-        s_pa[m][w][lane] = pk;
     }
     __syncthreads();
     // new values into the value operands: position 8 q4 + e of block sb is
@@ -521,7 +613,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         if (q4 != (kt >> 3)) continue;
         const int e = kt & 7;
 #pragma unroll
-        for (int sb = 0; sb < kChunkWaves; ++sb) {
+        for (int sb = 0; sb < NB; ++sb) {
             if ((p >> 5) != b0 + sb) continue;
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
@@ -534,6 +626,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
             }
         }
     }
+    VMI_STAMP(4 + g, 5);
     // O = P V for dims 32 w + 16 dt + nl; A = P of block sb (written by wave sb)
     const size_t pbase = (((size_t)g * a.nstride + c) * P + p) * RP;  // a chunk holds the rows of every path
 #pragma unroll
@@ -542,7 +635,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         for (int dt = 0; dt < 2; ++dt) {
             vmi_f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int sb = 0; sb < kChunkWaves; ++sb) acc = vmi_mfma_bf16(s_pa[m][sb][lane], vr[dt][sb], acc);
+            for (int sb = 0; sb < NB; ++sb) acc = vmi_mfma_bf16(s_pa[m][sb][lane], vr[dt][sb], acc);
             float* po = a.part_o + (pbase + 16 * m + 4 * q4) * kHeadDim + 32 * w + 16 * dt + nl;
 #pragma unroll
             for (int r = 0; r < 4; ++r) po[r * kHeadDim] = acc[r];
@@ -557,6 +650,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         }
         *reinterpret_cast<float2*>(a.part_ml + (pbase + tid) * 2) = make_float2(M, l);
     }
+    VMI_STAMP(4 + g, 6);
 }
 
 // grid (T * n_heads, 4): one quarter of a head's dims per workgroup.  Chunk c
@@ -573,7 +667,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
     const int lane = tid & 63, w = at_wave();
     const int pth = t / a.span, tt = t - pth * a.span;
     const int G = a.n_heads / a.n_kv, g = h / G, row = pth * RP + tt * G + (h % G);
-    const int NC = (batch_pos0(a.pos0, a.pos_dev, a.span, a.max_len) + a.span + kChunkKeys - 1) / kChunkKeys;
+    const int NC = (batch_pos0(a.pos0, a.pos_dev, a.span, a.max_len) + a.span + a.chunk_keys - 1) / a.chunk_keys;
     RP *= a.paths;  // rows per chunk
     // loads in issue order: every chunk's (max, sum) of this row (branch-free,
     // chunks past the cache read nothing), then this lane's first 8 partial
@@ -900,9 +994,30 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
 }
 
 // ------------------------------------------------------------------ host
-// Keys are split into chunks of kChunkKeys at fixed absolute positions, so a
-// query's result does not depend on how many tokens share its batch.
+// Keys are split into chunks at fixed absolute positions, so a query's result
+// does not depend on how many tokens share its batch.  Upper bound of the
+// chunk count (256-key chunks), for buffer sizes:
 int attn_chunks(int L) { return (L + kChunkKeys - 1) / kChunkKeys; }
+
+// Blocks per chunk beyond 8 for a cache of max_len positions: the fewest that
+// give every chunk of every kv head a CU of its own (one chunk workgroup per
+// CU), at most kMaxExtraBlocks.  A function of the cache capacity and the
+// device alone, so every call on one cache (any batch size, a tree or a
+// single path) splits the keys alike.
+int attn_extra_blocks(int max_len, int n_kv) {
+    static int ncu[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (!ncu[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        ncu[dev] = n;
+    }
+    const int blocks = max_len / kKvBlock;  // per kv head
+    for (int nx = 0; nx < kMaxExtraBlocks; ++nx)
+        if ((long)n_kv * ((blocks + kChunkWaves + nx - 1) / (kChunkWaves + nx)) <= ncu[dev]) return nx;
+    return kMaxExtraBlocks;
+}
 
 struct AttnLayout {
     size_t status, xn, qkv, part_o, part_ml, o, bytes;
@@ -1086,26 +1201,39 @@ int attention_impl(const vmi_attn_layer_desc* desc, const uint16_t* x, int paths
 
     AttnArgs at{};
     at.qkv = qkv; at.stride = stride; at.q_norm = D.q_norm; at.k_norm = D.k_norm;
-    at.rope_dim = D.rope_dim; at.theta = D.rope_theta; at.eps = D.norm_eps;
+    at.rope_dim = D.rope_dim; at.eps = D.norm_eps;
+    at.rope_base = D.rope_dim ? pow((double)D.rope_theta, -2.0 / (double)D.rope_dim) : 1.0;
     at.k_cache = k_cache; at.v_cache = v_cache;
     at.T = T; at.n_heads = D.n_heads; at.n_kv = D.n_kv_heads; at.pos0 = pos0; at.pos_dev = pos_device;
     at.paths = paths; at.span = span; at.tree_kv = tree_kv;
     at.status = reinterpret_cast<uint32_t*>(ws + L.status);
     at.max_len = max_len;
-    at.nstride = attn_chunks(max_len);
+    const int NX = attn_extra_blocks(max_len, D.n_kv_heads);
+    at.chunk_keys = (kChunkWaves + NX) * kKvBlock;
+    at.nstride = (max_len + at.chunk_keys - 1) / at.chunk_keys;  // <= attn_chunks(max_len): the layout's bound
     // with the position on the device every chunk of the capacity is launched; those past the cache exit
-    const int grid_chunks = pos_device ? at.nstride : attn_chunks(pos0 + span);
+    const int grid_chunks = pos_device ? at.nstride : (pos0 + span + at.chunk_keys - 1) / at.chunk_keys;
     at.chunks = grid_chunks;
     at.part_o = reinterpret_cast<float*>(ws + L.part_o);
     at.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
     at.o = ob;
     const int MS = (span * G + 15) / 16;
     const dim3 ag(paths == 1 ? grid_chunks : (grid_chunks + 7) / 8 * 8 * paths, D.n_kv_heads);
+    static_assert(kMaxExtraBlocks == 2, "the launch below covers NX = 0..2");
+    auto chunk_kernel = [&](auto ms) {
+        constexpr int M = decltype(ms)::value;
+        if (NX == 0)
+            hipLaunchKernelGGL((k_attn_chunk<M, 0>), ag, dim3(kChunkThreads), 0, s, at);
+        else if (NX == 1)
+            hipLaunchKernelGGL((k_attn_chunk<M, 1>), ag, dim3(kChunkThreads), 0, s, at);
+        else
+            hipLaunchKernelGGL((k_attn_chunk<M, 2>), ag, dim3(kChunkThreads), 0, s, at);
+    };
     switch (MS) {
-        case 1: hipLaunchKernelGGL(k_attn_chunk<1>, ag, dim3(kChunkThreads), 0, s, at); break;
-        case 2: hipLaunchKernelGGL(k_attn_chunk<2>, ag, dim3(kChunkThreads), 0, s, at); break;
-        case 3: hipLaunchKernelGGL(k_attn_chunk<3>, ag, dim3(kChunkThreads), 0, s, at); break;
-        default: hipLaunchKernelGGL(k_attn_chunk<4>, ag, dim3(kChunkThreads), 0, s, at); break;
+        case 1: chunk_kernel(std::integral_constant<int, 1>{}); break;
+        case 2: chunk_kernel(std::integral_constant<int, 2>{}); break;
+        case 3: chunk_kernel(std::integral_constant<int, 3>{}); break;
+        default: chunk_kernel(std::integral_constant<int, 4>{}); break;
     }
     hipLaunchKernelGGL(k_attn_merge, dim3(T * D.n_heads, 4), dim3(kAThreads), 0, s, at, 16 * MS);
 

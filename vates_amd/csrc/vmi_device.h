@@ -17,16 +17,36 @@ typedef uint32_t vmi_u4 __attribute__((ext_vector_type(4)));
 // translation unit), laid out [kid][workgroup < 4096][slot < 16].  The product
 // build compiles these to nothing.
 #ifdef VMI_TIMELINE
-#define VMI_TL_DECL static __device__ unsigned long long* vmi_tl_buf = nullptr;
+// The pointer sits in constant memory (a scalar load) and the stamp is a
+// global store: neither makes the wave wait for its outstanding vector loads.
+#define VMI_TL_DECL static __constant__ unsigned long long* vmi_tl_buf = nullptr;
 #define VMI_STAMP(kid, slot)                                                                       \
     do {                                                                                           \
-        if (threadIdx.x == 0 && vmi_tl_buf && blockIdx.x < 4096)                                   \
-            vmi_tl_buf[((size_t)(kid) * 4096 + blockIdx.x) * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+        if (threadIdx.x == 0 && vmi_tl_buf && blockIdx.x < 4096) {                                 \
+            __attribute__((address_space(1))) unsigned long long* tl_p_ =                         \
+                (__attribute__((address_space(1))) unsigned long long*)vmi_tl_buf;                \
+            tl_p_[((size_t)(kid) * 4096 + blockIdx.x) * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+        }                                                                                          \
+    } while (0)
+// The wave's hardware placement (HW_ID: CU, shader array and engine in bits
+// 8..14; XCC_ID in the upper word) at point `slot`.
+#define VMI_STAMP_HWID(kid, slot)                                                                  \
+    do {                                                                                           \
+        if (threadIdx.x == 0 && vmi_tl_buf && blockIdx.x < 4096) {                                 \
+            __attribute__((address_space(1))) unsigned long long* tl_p_ =                         \
+                (__attribute__((address_space(1))) unsigned long long*)vmi_tl_buf;                \
+            const unsigned long long hw_ = (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);    \
+            const unsigned long long xcc_ = (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 20);  \
+            tl_p_[((size_t)(kid) * 4096 + blockIdx.x) * 16 + (slot)] = hw_ | (xcc_ << 32);         \
+        }                                                                                          \
     } while (0)
 #else
 #define VMI_TL_DECL
 #define VMI_STAMP(kid, slot) \
     do {                     \
+    } while (0)
+#define VMI_STAMP_HWID(kid, slot) \
+    do {                          \
     } while (0)
 #endif
 

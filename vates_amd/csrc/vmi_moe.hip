@@ -725,6 +725,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     const bool is_shared = item < nsh;
     const vmi_u4 zero4 = {0u, 0u, 0u, 0u};
     VMI_STAMP(1, 0);
+    VMI_STAMP_HWID(1, 5);
 
     // the MoE input operands do not depend on the routing: issued before it,
     // so their latency overlaps the router logits'
@@ -1049,6 +1050,7 @@ __global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
     const int NEmax = hs + a.npairs;
     const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
     VMI_STAMP(2, 0);
+    VMI_STAMP_HWID(2, 3);
 
     // activation operands of the wave's expert i (list position e), tokens
     // tb..tb+tpass-1: lane l holds word l (+64c) of each token row
