@@ -250,38 +250,102 @@ __device__ __forceinline__ vmi_u4 keep_first(vmi_u4 v, int n) {  // zero bf16 el
     return v;
 }
 
-// One head row (dims lane + 64 j in v) in place: RMSNorm in the canonical
-// order, times the norm weight, rounded to bf16 (the model dtype), then the
-// rotary pairs (i, i + rd/2) in fp32 with (cos, sin) of pos * theta^(-2i/rd)
-// from cs, rounded to bf16.  srow is the wave's own LDS row (the rotary
-// partner of a dim lives in another lane).
-__device__ __forceinline__ void norm_rope_row(float (&v)[4], const float (&nw)[4], float eps, const float2* cs, int rd,
-                                              float* srow, uint16_t (&o)[4]) {
+// NR head rows of one wave (dims lane + 64 j of row i in v[i]) in place:
+// RMSNorm (x^2 of the lane's four dims in order, then the canonical wave
+// sum), times the norm weight, rounded to bf16 (the model dtype), then the
+// rotary pairs (d, d + rd/2) in fp32 with (cos, sin) of pos * theta^(-2i/rd)
+// from cs[i], rounded to bf16.  The rows go through together and nothing
+// branches on the lane, so their reductions and LDS reads overlap.  The
+// rotary partner of dim d: for rd = 64 the lane 32 apart, for rd = 128 and
+// 256 another register of the same lane; other widths go through srow, the
+// wave's own LDS row, one row at a time.
+template <int NR>
+__device__ __forceinline__ void norm_rope_rows(float (&v)[NR][4], const float (&nw)[4], float eps,
+                                               const float2* const (&cs)[NR], int rd, float* srow,
+                                               uint16_t (&o)[NR][4]) {
     const int lane = threadIdx.x & 63;
-    float ss = 0.0f;
+    float ss[NR];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ss = fmaf(v[j], v[j], ss);
-    ss = vmi_wave_sum_canon(ss);
-    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * (1.0f / (float)kHeadDim) + eps));
+    for (int i = 0; i < NR; ++i) {
+        ss[i] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        v[j] = vmi_bf16_to_f32(vmi_f32_to_bf16((v[j] * inv) * nw[j]));
-        srow[lane + 64 * j] = v[j];
+        for (int j = 0; j < 4; ++j) ss[i] = fmaf(v[i][j], v[i][j], ss[i]);
     }
-    __builtin_amdgcn_wave_barrier();  // srow is this wave's own row: LDS order within a wave suffices
+#pragma unroll
+    for (int i = 0; i < NR; ++i) ss[i] = vmi_wave_sum_canon(ss[i]);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss[i] * (1.0f / (float)kHeadDim) + eps));
+        const uint32_t u01 = vmi_pack_bf16x2((v[i][0] * inv) * nw[0], (v[i][1] * inv) * nw[1]);
+        const uint32_t u23 = vmi_pack_bf16x2((v[i][2] * inv) * nw[2], (v[i][3] * inv) * nw[3]);
+        v[i][0] = __uint_as_float(u01 << 16);
+        v[i][1] = __uint_as_float(u01 & 0xffff0000u);
+        v[i][2] = __uint_as_float(u23 << 16);
+        v[i][3] = __uint_as_float(u23 & 0xffff0000u);
+    }
     const int half = rd / 2;
+    auto store = [&](int i, const float (&r)[4]) {
+        const uint32_t a = vmi_pack_bf16x2(r[0], r[1]), b = vmi_pack_bf16x2(r[2], r[3]);
+        o[i][0] = (uint16_t)a;
+        o[i][1] = (uint16_t)(a >> 16);
+        o[i][2] = (uint16_t)b;
+        o[i][3] = (uint16_t)(b >> 16);
+    };
+    if (rd == 64 || rd == 128 || rd == 256) {
+        // register j of every lane is rotated or not as a whole (rd is a
+        // multiple of 64): the table reads need no lane mask
+        float2 c[NR][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int d = lane + 64 * j;
-        float r = v[j];
-        if (d < rd) {
-            const float2 c = cs[d < half ? d : d - half];
-            const float partner = d < half ? -srow[d + half] : srow[d - half];
-            r = v[j] * c.x + partner * c.y;
+        for (int i = 0; i < NR; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = lane + 64 * j;
+                c[i][j] = 64 * j < rd ? cs[i][d < half ? d : d - half] : make_float2(1.0f, 0.0f);
+            }
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            float pr[4];
+            if (rd == 64) {
+                pr[0] = __shfl_xor(v[i][0], 32, 64);
+                pr[1] = pr[2] = pr[3] = 0.0f;
+            } else if (rd == 128) {
+                pr[0] = v[i][1];
+                pr[1] = v[i][0];
+                pr[2] = pr[3] = 0.0f;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) pr[j] = v[i][j ^ 2];
+            }
+            float r[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = lane + 64 * j;
+                const float partner = d < half ? -pr[j] : pr[j];
+                r[j] = 64 * j < rd ? v[i][j] * c[i][j].x + partner * c[i][j].y : v[i][j];
+            }
+            store(i, r);
         }
-        o[j] = vmi_f32_to_bf16(r);
+        return;
     }
-    __builtin_amdgcn_wave_barrier();  // every lane has read its partner before srow is rewritten
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) srow[lane + 64 * j] = v[i][j];
+        __builtin_amdgcn_wave_barrier();  // srow is this wave's own row: LDS order within a wave suffices
+        float r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = lane + 64 * j;
+            r[j] = v[i][j];
+            if (d < rd) {
+                const float2 c = cs[i][d < half ? d : d - half];
+                const float partner = d < half ? -srow[d + half] : srow[d - half];
+                r[j] = v[i][j] * c.x + partner * c.y;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // every lane has read its partner before srow is rewritten
+        store(i, r);
+    }
 }
 
 // Rows of a head group: row = t * G + hl (G = n_heads / n_kv query heads per
@@ -437,23 +501,33 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
         qn[j] = __uint_as_float(qnr[j] << 16);
         kn[j] = __uint_as_float(knr[j] << 16);
     }
-    // the wave's query rows into s_q (rows past the batch: zeros)
+    // the wave's query rows into s_q (rows past the batch: zeros; their
+    // projections read as zeros and their table row is a valid one)
+    {
+        const float2* csr[QR];
+        uint16_t o[QR][4];
 #pragma unroll
-    for (int i = 0; i < QR; ++i) {
-        const int row = w + kChunkWaves * i;
-        if (row < RP) {
-            uint16_t o[4] = {0, 0, 0, 0};
-            if (row < R) norm_rope_row(qv[i], qn, a.eps, s_cs[row / G], a.rope_dim, s_row[w], o);
+        for (int i = 0; i < QR; ++i) csr[i] = s_cs[min((w + kChunkWaves * i) / G, T - 1)];
+        norm_rope_rows<QR>(qv, qn, a.eps, csr, a.rope_dim, s_row[w], o);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) s_q[row][lane + 64 * j] = o[j];
+        for (int i = 0; i < QR; ++i) {
+            const int row = w + kChunkWaves * i;
+            if (row < RP) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s_q[row][lane + 64 * j] = row < R ? o[i][j] : (uint16_t)0;
+            }
         }
     }
+    VMI_STAMP(4 + g, 7);
     // the new key and value of position pos0 + tn: to the cache (a tree: to
     // the path's rows of tree_kv, committed for the winning path only) and to LDS
     if (has_new) {
         const int pos = pos0 + tn;
-        uint16_t o[4];
-        norm_rope_row(kv, kn, a.eps, s_cs[tn], a.rope_dim, s_row[w], o);
+        float kv1[1][4] = {{kv[0], kv[1], kv[2], kv[3]}};
+        const float2* csk[1] = {s_cs[tn]};
+        uint16_t ok[1][4];
+        norm_rope_rows<1>(kv1, kn, a.eps, csk, a.rope_dim, s_row[w], ok);
+        const uint16_t (&o)[4] = ok[0];
         const size_t blk = kv_block(g, a.max_len, pos);
         const int kt = pos % kKvBlock;
         uint16_t* side = a.tree_kv ? a.tree_kv + ((size_t)(p * a.n_kv + g) * 2 * T + tn) * kHeadDim : nullptr;
@@ -472,6 +546,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
             s_new[1][tn][d] = vb16;
         }
     }
+    VMI_STAMP(4 + g, 8);
     // the extra blocks' keys into LDS (waiting only for those loads: the
     // values, issued after them, keep streaming)
 #pragma unroll
@@ -487,6 +562,7 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
             for (int dt = 0; dt < 2; ++dt) vr[dt][sb] = keep_first(vr[dt][sb], L - p0 - 8 * q4);
         }
     }
+    VMI_STAMP(4 + g, 9);
     __syncthreads();
     // new keys into the wave's key operands: position kt of the block sits in
     // lanes nl = 4 (kt >> 3) + (kt & 3), tile (kt >> 2) & 1, dims 32 kk + 8 q4 ..
@@ -586,16 +662,20 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
 #pragma unroll
         for (int v = 1; v < kChunkWaves; ++v) M = fmaxf(M, s_wm[v][row]);
         float ls = 0.0f;
+        // exp(x - M) as 2^(x log2 e - M log2 e) on the hardware exp2; masked
+        // scores (-inf, also in a row with nothing visible) give 0
+        const float Ml = M * 1.44269504088896341f;
         auto probs = [&](const float (&sv)[8]) {
             vmi_u4 pk;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float x0 = sv[2 * i], x1 = sv[2 * i + 1];
-                const uint32_t u0 = x0 == -INFINITY ? 0u : vmi_f32_to_bf16(expf(x0 - M));
-                const uint32_t u1 = x1 == -INFINITY ? 0u : vmi_f32_to_bf16(expf(x1 - M));
-                ls += vmi_bf16_to_f32(u0);
-                ls += vmi_bf16_to_f32(u1);
-                pk[i] = u0 | (u1 << 16);
+                const float e0 = x0 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(x0, 1.44269504088896341f, -Ml));
+                const float e1 = x1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(x1, 1.44269504088896341f, -Ml));
+                const uint32_t u = vmi_pack_bf16x2(e0, e1);
+                ls += __uint_as_float(u << 16);
+                ls += __uint_as_float(u & 0xffff0000u);
+                pk[i] = u;
             }
             return pk;
         };

@@ -52,6 +52,15 @@ typedef uint32_t vmi_u4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float vmi_bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
+// bf16(a) | bf16(b) << 16, both rounded to nearest even by one
+// v_cvt_pk_bf16_f32 (the bits vmi_f32_to_bf16 gives for every non-NaN input).
+__device__ __forceinline__ uint32_t vmi_pack_bf16x2(float a, float b) {
+    typedef __bf16 vmi_bf2 __attribute__((ext_vector_type(2)));
+    typedef float vmi_f2 __attribute__((ext_vector_type(2)));
+    const vmi_f2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, vmi_bf2));
+}
+
 // Round-to-nearest-even fp32 -> bf16 bit pattern (quiet NaN kept).
 __device__ __forceinline__ uint16_t vmi_f32_to_bf16(float f) {
     uint32_t u = __float_as_uint(f);
