@@ -868,17 +868,22 @@ constexpr int kQ4Kw = 512;  // columns per wave
 // its operands from there.
 constexpr int kQ4MaxK = 2048;  // widest K the NORM form stages
 
-template <bool NORM>
+// RT: weight rows per wave tile, 16, or 8 where 16-row tiles would leave
+// half the CUs idle (lanes 8..15 then repeat rows 0..7: the same addresses in
+// the same load, and MFMA columns 8..15 that are not stored).
+template <bool NORM, int RT>
 __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
+    static_assert(RT == 8 || RT == 16, "row tile");
     __shared__ float s_X[kQ4Waves][kQgMaxT][8];       // group sums of x per wave: [token][group of the wave]
     __shared__ float s_part[kQ4Waves][16][kQgMaxT];
     const int T = a.T, K = a.K, G = K / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = at_wave();
     const int nl = lane & 15, q4 = lane >> 4;
     VMI_STAMP(3, 0);
+    VMI_STAMP_HWID(3, 4);
     const int ks = K / kQ4Kw, tiles = kQ4Waves / ks;
     const int tile = w / ks, kw = w % ks;
-    const int n = (blockIdx.x * tiles + tile) * 16 + nl;
+    const int n = (blockIdx.x * tiles + tile) * RT + (nl & (RT - 1));
     const int nn = n < a.nrows ? n : a.nrows - 1;
     // matrix of row nn, selected from the kernel arguments by value (an
     // indexed argument would be a dependent vector load before the weights)
@@ -925,12 +930,12 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     // raw bf16 bits, issued now so that its latency overlaps the weights'; a
     // branch-free buffer load whose value is first used at the end, so no
     // wait on it (and on everything issued before it) lands here
-    const int nout = tiles * 16 * T;
+    const int nout = tiles * RT * T;
     // (unconditional: without a residual the range is empty and every lane
     // reads zero without touching memory)
     const __amdgpu_buffer_rsrc_t rres =
         vmi_rsrc(a.residual, a.out_bf16 && a.residual ? (uint32_t)((size_t)T * a.out_stride * 2) : 0u);
-    const int row0 = (blockIdx.x * tiles + tid / (16 * T)) * 16 + (tid / T) % 16;
+    const int row0 = (blockIdx.x * tiles + tid / (RT * T)) * RT + (tid / T) % RT;
     const uint32_t res0 = vmi_bload_b16(
         rres, tid < nout && row0 < a.nrows ? (uint32_t)(((size_t)(tid % T) * a.out_stride + row0) * 2) : VMI_OOB, 0);
     if constexpr (NORM) {
@@ -1055,11 +1060,11 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     }
     __syncthreads();
     VMI_STAMP(3, 2);
-    for (int i = tid; i < tiles * 16 * T; i += kQ4Threads) {
-        const int tl = i / (16 * T), rr = (i / T) % 16, t = i % T;
+    for (int i = tid; i < tiles * RT * T; i += kQ4Threads) {
+        const int tl = i / (RT * T), rr = (i / T) % RT, t = i % T;
         float y = s_part[tl * ks][rr][t];
         for (int k2 = 1; k2 < ks; ++k2) y += s_part[tl * ks + k2][rr][t];
-        const int row = (blockIdx.x * tiles + tl) * 16 + rr;
+        const int row = (blockIdx.x * tiles + tl) * RT + rr;
         if (row < a.nrows) {
             if (a.out) a.out[(size_t)t * a.out_stride + row] = y;
             if (a.out_bf16) {
@@ -1085,17 +1090,10 @@ int attn_chunks(int L) { return (L + kChunkKeys - 1) / kChunkKeys; }
 // device alone, so every call on one cache (any batch size, a tree or a
 // single path) splits the keys alike.
 int attn_extra_blocks(int max_len, int n_kv) {
-    static int ncu[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    if (!ncu[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        ncu[dev] = n;
-    }
+    const int ncu = vmi::device_cus();
     const int blocks = max_len / kKvBlock;  // per kv head
     for (int nx = 0; nx < kMaxExtraBlocks; ++nx)
-        if ((long)n_kv * ((blocks + kChunkWaves + nx - 1) / (kChunkWaves + nx)) <= ncu[dev]) return nx;
+        if ((long)n_kv * ((blocks + kChunkWaves + nx - 1) / (kChunkWaves + nx)) <= ncu) return nx;
     return kMaxExtraBlocks;
 }
 
@@ -1151,12 +1149,24 @@ hipError_t vmi::launch_qgemv(const QgemvCall& q0, hipStream_t s) {
             sb_align |= reinterpret_cast<uintptr_t>(q.m[i].s) | reinterpret_cast<uintptr_t>(q.m[i].b);
     if (q.norm_w && !qgemv_fuses_norm(q)) return hipErrorInvalidValue;
     if (q.bits == 4 && q.K % kQ4Kw == 0 && ks <= kQ4Waves && kQ4Waves % ks == 0 && !(sb_align & 15)) {
-        const int rows_per_wg = 16 * (kQ4Waves / ks);
-        const dim3 grid((q.nrows + rows_per_wg - 1) / rows_per_wg);
-        if (q.norm_w)
-            hipLaunchKernelGGL(k_qgemv4<true>, grid, dim3(kQ4Threads), 0, s, q);
-        else
-            hipLaunchKernelGGL(k_qgemv4<false>, grid, dim3(kQ4Threads), 0, s, q);
+        // 8-row tiles when 16-row tiles fill at most half the CUs and 8-row
+        // ones still give each workgroup a CU of its own
+        const int tiles = kQ4Waves / ks;
+        const int wg16 = (q.nrows + 16 * tiles - 1) / (16 * tiles), wg8 = (q.nrows + 8 * tiles - 1) / (8 * tiles);
+        const int ncu = vmi::device_cus();
+        const bool rt8 = 2 * wg16 <= ncu && wg8 <= ncu;
+        const dim3 grid(rt8 ? wg8 : wg16);
+        if (q.norm_w) {
+            if (rt8)
+                hipLaunchKernelGGL((k_qgemv4<true, 8>), grid, dim3(kQ4Threads), 0, s, q);
+            else
+                hipLaunchKernelGGL((k_qgemv4<true, 16>), grid, dim3(kQ4Threads), 0, s, q);
+        } else {
+            if (rt8)
+                hipLaunchKernelGGL((k_qgemv4<false, 8>), grid, dim3(kQ4Threads), 0, s, q);
+            else
+                hipLaunchKernelGGL((k_qgemv4<false, 16>), grid, dim3(kQ4Threads), 0, s, q);
+        }
     } else {
         const size_t lds = (size_t)q.T * q.K * 2;
         hipLaunchKernelGGL(k_qgemv, dim3((q.nrows + 3) / 4), dim3(kAThreads), lds, s, q);
