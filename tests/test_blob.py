@@ -21,13 +21,16 @@ from vates_amd._lib import VmiError
 def test_layout_qwen3_next_known_answer():
     segs, stride = blob_layout(2048, 512, 4, 64)
     assert stride == 1_769_472
-    assert [(p, t) for p, t, _, _, _ in segs] == [(p, t) for p in ("gate_proj", "up_proj", "down_proj")
-                                                   for t in ("weight", "scales", "biases")]
-    sizes = {(p, t): nb for p, t, _, _, nb in segs}
+    assert [(sg.proj, sg.tensor) for sg in segs] == [(p, t) for p in ("gate_proj", "up_proj", "down_proj")
+                                                      for t in ("weight", "scales", "biases")]
+    sizes = {(sg.proj, sg.tensor): sg.nbytes for sg in segs}
     assert sizes[("gate_proj", "weight")] == 524_288 and sizes[("up_proj", "weight")] == 524_288
     assert sizes[("down_proj", "weight")] == 524_288
     assert all(sizes[(p, t)] == 32_768 for p in ("gate_proj", "up_proj", "down_proj") for t in ("scales", "biases"))
-    shapes = {(p, t): sh for p, t, _, sh, _ in segs}
+    shapes = {(sg.proj, sg.tensor): sg.shape for sg in segs}
+    # each segment starts where the one before it ends
+    assert segs[0].offset == 0 and all(a.offset + a.nbytes == b.offset for a, b in zip(segs, segs[1:]))
+    assert segs[-1].offset + segs[-1].nbytes == stride
     assert shapes[("gate_proj", "weight")] == (512, 256) and shapes[("down_proj", "weight")] == (2048, 64)
     assert shapes[("down_proj", "scales")] == (2048, 8)
     # 8-bit: twice the words
@@ -54,12 +57,11 @@ def test_writer_byte_order(tmp_path):
     raw = np.fromfile(path, dtype=np.uint8)
     assert raw.size == E * stride
     for e in range(E):
-        off = e * stride
-        for (p, t, _, _, nb), val in zip(segs, [((e + 1) & 0xFF), ((e + 100) & 0xFF), ((e + 7) & 0xFF),
-                                                ((e + 1) & 0xFF), ((e + 100) & 0xFF), ((e + 14) & 0xFF),
-                                                ((e + 1) & 0xFF), ((e + 100) & 0xFF), ((e + 21) & 0xFF)]):
-            assert np.all(raw[off:off + nb] == val), (e, p, t)
-            off += nb
+        for sg, val in zip(segs, [((e + 1) & 0xFF), ((e + 100) & 0xFF), ((e + 7) & 0xFF),
+                                  ((e + 1) & 0xFF), ((e + 100) & 0xFF), ((e + 14) & 0xFF),
+                                  ((e + 1) & 0xFF), ((e + 100) & 0xFF), ((e + 21) & 0xFF)]):
+            off = e * stride + sg.offset
+            assert np.all(raw[off:off + sg.nbytes] == val), (e, sg.proj, sg.tensor)
 
 
 def test_blob_index(tmp_path):

@@ -44,10 +44,8 @@ def test_blob_byte_pattern_per_slot(gpu, tmp_path):
     segs, stride = blob_layout(H, I)
     raw = np.empty((E, stride), dtype=np.uint8)
     for e in range(E):
-        off = 0
-        for j, (_, _, _, _, nb) in enumerate(segs):
-            raw[e, off:off + nb] = (e + 1 + 17 * j) & 0xFF
-            off += nb
+        for j, sg in enumerate(segs):
+            raw[e, sg.offset:sg.offset + sg.nbytes] = (e + 1 + 17 * j) & 0xFF
     path = tmp_path / "layer07.blob"
     raw.tofile(path)
     got = load_layer_blob(path, H, I, device=gpu, chunk_bytes=stride * 4)

@@ -17,6 +17,7 @@ from __future__ import annotations
 import json
 import os
 from pathlib import Path
+from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
 
 import torch
@@ -25,30 +26,47 @@ from ._lib import VmiError
 from .moe import QuantizedProj
 
 BLOB_V1_AFFINE = "expert_blob_v1"
-Segment = Tuple[str, str, str, Tuple[int, int], int]  # proj, tensor, dtype, shape, nbytes
 
 
-def blob_layout(hidden: int, inter: int, bits: int = 4, group: int = 64) -> Tuple[List[Segment], int]:
-    """Segments of one expert in file order and the expert stride in bytes
-    (the v1 affine layout of blob_layout.py:18-32)."""
+@dataclass(frozen=True)
+class BlobSegment:
+    """One tensor of an expert's record in a v1 blob."""
+    proj: str               # gate_proj, up_proj or down_proj
+    tensor: str             # weight, scales or biases
+    dtype: str              # uint32: packed quantised words; uint16: bf16 bits
+    shape: Tuple[int, int]  # per expert
+    offset: int             # bytes from the start of the expert's record
+    nbytes: int
+
+
+def blob_layout(hidden: int, inter: int, bits: int = 4, group: int = 64) -> Tuple[List[BlobSegment], int]:
+    """The tensors of one expert's record, in file order, and the record size
+    (the expert stride) in bytes.  File order (blob_layout.py:18-32): the
+    gate, up and down projections, each as its packed words, then one bf16
+    scale and one bf16 bias per quantisation group of each output row."""
     if hidden % group or inter % group or 32 % bits:
         raise VmiError(f"hidden={hidden} inter={inter} must be multiples of group={group}; bits={bits}")
-    segs: List[Segment] = []
-    for proj, out_d, in_d in (("gate_proj", inter, hidden), ("up_proj", inter, hidden), ("down_proj", hidden, inter)):
-        words = in_d * bits // 32
-        groups = in_d // group
-        segs.append((proj, "weight", "uint32", (out_d, words), out_d * words * 4))
-        segs.append((proj, "scales", "uint16", (out_d, groups), out_d * groups * 2))
-        segs.append((proj, "biases", "uint16", (out_d, groups), out_d * groups * 2))
-    return segs, sum(s[-1] for s in segs)
+    # (projection, output rows, input columns)
+    shapes = (("gate_proj", inter, hidden), ("up_proj", inter, hidden), ("down_proj", hidden, inter))
+    segs: List[BlobSegment] = []
+    offset = 0
+    for proj, rows, cols in shapes:
+        per_row = (("weight", "uint32", cols * bits // 32, 4),
+                   ("scales", "uint16", cols // group, 2),
+                   ("biases", "uint16", cols // group, 2))
+        for tensor, dtype, width, itemsize in per_row:
+            nbytes = rows * width * itemsize
+            segs.append(BlobSegment(proj, tensor, dtype, (rows, width), offset, nbytes))
+            offset += nbytes
+    return segs, offset
 
 
 _TORCH = {"uint32": torch.int32, "uint16": torch.int16}
 
 
-def _pools(segs: List[Segment], num_experts: int, device) -> Dict[str, torch.Tensor]:
-    return {f"{p}.{t}": torch.empty((num_experts, *shape), dtype=_TORCH[dt], device=device)
-            for p, t, dt, shape, _ in segs}
+def _pools(segs: List[BlobSegment], num_experts: int, device) -> Dict[str, torch.Tensor]:
+    return {f"{sg.proj}.{sg.tensor}": torch.empty((num_experts, *sg.shape), dtype=_TORCH[sg.dtype], device=device)
+            for sg in segs}
 
 
 def load_layer_blob(path, hidden: int, inter: int, *, bits: int = 4, group: int = 64,
@@ -85,11 +103,9 @@ def load_layer_blob(path, hidden: int, inter: int, *, bits: int = 4, group: int 
                 got += r
             dev[b][:cnt * stride].copy_(host[b][:cnt * stride], non_blocking=True)
             raw = dev[b][:cnt * stride].view(cnt, stride)
-            off = 0
-            for p, t, dt, shape, nb in segs:
-                dst = pools[f"{p}.{t}"][e0:e0 + cnt].view(torch.uint8).view(cnt, nb)
-                dst.copy_(raw[:, off:off + nb])
-                off += nb
+            for sg in segs:
+                dst = pools[f"{sg.proj}.{sg.tensor}"][e0:e0 + cnt].view(torch.uint8).view(cnt, sg.nbytes)
+                dst.copy_(raw[:, sg.offset:sg.offset + sg.nbytes])
             ev = torch.cuda.Event()
             ev.record(stream)
             done[b] = ev
