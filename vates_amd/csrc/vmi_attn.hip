@@ -503,15 +503,25 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
     }
     // the wave's query rows into s_q (rows past the batch: zeros; their
     // projections read as zeros and their table row is a valid one)
-    {
-        const float2* csr[QR];
-        uint16_t o[QR][4];
+    // (up to four rows at once; beyond that two at a time: all of a wave's
+    // rows at once would not fit the registers beside the cache operands)
+    constexpr int NRB = QR <= 4 ? QR : 2;
+    static_assert(QR % NRB == 0, "rows in groups");
 #pragma unroll
-        for (int i = 0; i < QR; ++i) csr[i] = s_cs[min((w + kChunkWaves * i) / G, T - 1)];
-        norm_rope_rows<QR>(qv, qn, a.eps, csr, a.rope_dim, s_row[w], o);
+    for (int i0 = 0; i0 < QR; i0 += NRB) {
+        float v2[NRB][4];
+        const float2* csr[NRB];
+        uint16_t o[NRB][4];
 #pragma unroll
-        for (int i = 0; i < QR; ++i) {
-            const int row = w + kChunkWaves * i;
+        for (int i = 0; i < NRB; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v2[i][j] = qv[i0 + i][j];
+            csr[i] = s_cs[min((w + kChunkWaves * (i0 + i)) / G, T - 1)];
+        }
+        norm_rope_rows<NRB>(v2, qn, a.eps, csr, a.rope_dim, s_row[w], o);
+#pragma unroll
+        for (int i = 0; i < NRB; ++i) {
+            const int row = w + kChunkWaves * (i0 + i);
             if (row < RP) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) s_q[row][lane + 64 * j] = row < R ? o[i][j] : (uint16_t)0;
