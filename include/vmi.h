@@ -260,8 +260,10 @@ int vmi_qgemv(const uint16_t* x, int T, int K, vmi_qmat w, int N, int bits, int 
  * contiguous 1 KB).  Positions >= pos0 + T are never used.  head_dim 256;
  * T * n_heads / n_kv_heads <= 64; norm weights are the multipliers applied
  * (a checkpoint's zero-centred weights plus one).  Keys are processed in
- * chunks of 256 at fixed positions and merged in a fixed order, so a token's
- * result does not depend on the batch it is verified in (bit for bit).
+ * chunks of 256, 288 or 320 at fixed positions (the length set by max_len,
+ * n_kv_heads and the device's CU count: the shortest that gives every chunk a
+ * CU) and merged in a fixed order, so a token's result does not depend on
+ * the batch it is verified in (bit for bit) for a given cache capacity.
  * pos_device (int32 on the device, or NULL): when set, the batch position is
  * read from it when the kernels run instead of pos0 (a captured graph replays
  * with positions that advance on the device); a value outside
