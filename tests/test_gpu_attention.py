@@ -155,13 +155,15 @@ def test_attention_batch_equals_steps(gpu, orc, pos0, max_len):
     assert torch.equal(batch.view(torch.int16), steps.view(torch.int16)), "batch result differs from single steps"
 
 
-def test_attention_position_on_device(gpu):
-    """pos_device gives the result and cache of the host position, bit for bit."""
+@pytest.mark.parametrize("pos0,max_len", [(700, 1024), (33100, 33376)])
+def test_attention_position_on_device(gpu, pos0, max_len):
+    """pos_device gives the result and cache of the host position, bit for bit
+    (every chunk of the capacity launched, those past the cache exiting)."""
+    log(f"case: attention position on the device pos0={pos0} max_len={max_len}")
     import torch
     from vates_amd.synth import synth_bf16
     layer, _ = make_attention(gpu, 83)
-    pos0 = 700
-    c1, c2 = layer.new_cache(1024), layer.new_cache(1024)
+    c1, c2 = layer.new_cache(max_len), layer.new_cache(max_len)
     pk, pv = synth_bf16(83, 20, (2, pos0, 256), device=gpu), synth_bf16(83, 21, (2, pos0, 256), device=gpu)
     c1.write(0, pk, pv)
     c2.write(0, pk, pv)

@@ -513,19 +513,49 @@ class GraphSpecDecoder:
         st = DecodeStats()
         t0 = time.perf_counter()
         pos = self.pos_host
-        while len(st.tokens) < n_tokens:
-            if plant is not None:
-                self.planted.copy_(torch.tensor(plant(st.steps, pos), dtype=torch.int32), non_blocking=False)
-            self._replay_step()
-            r = self.rec_buf.cpu().tolist()  # the step's one host synchronisation
+
+        def take(r):
+            nonlocal pos
             n, m = r[0], r[1]
             pos += r[2]
             st.tokens.extend(r[4:4 + n])
             st.accept_hist.append(m)
             st.depths.append(self._depth)
-            if trace:
-                st.drafts.append(self.drafts[:self._depth].cpu().tolist())
             st.steps += 1
+
+        if plant is None and self.tau is None and not trace:
+            # one step ahead: each step's record goes to pinned memory in stream
+            # order and is read while the next step runs; a step is enqueued
+            # ahead only while the pending ones cannot finish the run even if
+            # they accept everything, so the run stops where the synchronous
+            # loop would
+            bufs = [torch.empty(self.rec_buf.shape, dtype=self.rec_buf.dtype).pin_memory() for _ in range(2)]
+            evs = [torch.cuda.Event() for _ in range(2)]
+            pending = []
+
+            def enqueue():
+                i = (pending[-1] + 1) % 2 if pending else 0
+                self._replay_step()
+                bufs[i].copy_(self.rec_buf, non_blocking=True)
+                evs[i].record()
+                pending.append(i)
+
+            while len(st.tokens) < n_tokens:
+                if not pending:
+                    enqueue()
+                if len(pending) == 1 and len(st.tokens) + (K + 1) < n_tokens:
+                    enqueue()
+                i = pending.pop(0)
+                evs[i].synchronize()  # the step's one host synchronisation, under the next step
+                take(bufs[i].tolist())
+        else:
+            while len(st.tokens) < n_tokens:
+                if plant is not None:
+                    self.planted.copy_(torch.tensor(plant(st.steps, pos), dtype=torch.int32), non_blocking=False)
+                self._replay_step()
+                take(self.rec_buf.cpu().tolist())  # the step's one host synchronisation
+                if trace:
+                    st.drafts.append(self.drafts[:self._depth].cpu().tolist())
         st.seconds = time.perf_counter() - t0
         st.tokens = st.tokens[:n_tokens]
         pos, mtp_len = self.state.cpu().tolist()
