@@ -1109,30 +1109,47 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_router3(PfArgs a) {
 // --------------------------------------------------------------- combine
 // out[t][h] = bf16(sum_{j <= k} y[t(k+1)+j][h] (valid routes, rank order) + residual)
 __global__ __launch_bounds__(kPfThreads) void k_pf_combine(PfArgs a) {
+    // one token per workgroup, 8 columns per thread and pass; every rank's
+    // 16-byte piece is requested before the sums, which add the ranks in
+    // order and then the residual, per column
     const int t = blockIdx.x;
     const int K1 = a.k + 1;
-    for (int h = threadIdx.x * 4; h < a.H; h += kPfThreads * 4) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < K1; ++j) {
-            const bool ok = j < a.k ? a.slots[t * a.k + j] >= 0 : a.has_shared;
-            if (!ok) continue;
-            const uint2 y = *reinterpret_cast<const uint2*>(a.ybuf + ((size_t)t * K1 + j) * a.H + h);
-            acc[0] += __uint_as_float(y.x << 16);
-            acc[1] += __uint_as_float(y.x & 0xffff0000u);
-            acc[2] += __uint_as_float(y.y << 16);
-            acc[3] += __uint_as_float(y.y & 0xffff0000u);
+    uint32_t okm = 0u;  // ranks that contribute (uniform)
+    for (int j = 0; j < K1; ++j) {
+        const bool ok = j < a.k ? a.slots[t * a.k + j] >= 0 : a.has_shared != 0;
+        okm |= (ok ? 1u : 0u) << j;
+    }
+    const vmi_u4 z4 = {0u, 0u, 0u, 0u};
+    for (int h = threadIdx.x * 8; h < a.H; h += kPfThreads * 8) {
+        vmi_u4 y[kPfMaxK + 1];
+#pragma unroll
+        for (int j = 0; j <= kPfMaxK; ++j)
+            y[j] = (j < K1 && ((okm >> j) & 1u))
+                       ? *reinterpret_cast<const vmi_u4*>(a.ybuf + ((size_t)t * K1 + j) * a.H + h)
+                       : z4;
+        const vmi_u4 rv = a.residual ? *reinterpret_cast<const vmi_u4*>(a.residual + (size_t)t * a.H + h) : z4;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j <= kPfMaxK; ++j) {
+            if (j < K1 && ((okm >> j) & 1u)) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[2 * e] += __uint_as_float(y[j][e] << 16);
+                    acc[2 * e + 1] += __uint_as_float(y[j][e] & 0xffff0000u);
+                }
+            }
         }
         if (a.residual) {
-            const uint2 rv = *reinterpret_cast<const uint2*>(a.residual + (size_t)t * a.H + h);
-            acc[0] += __uint_as_float(rv.x << 16);
-            acc[1] += __uint_as_float(rv.x & 0xffff0000u);
-            acc[2] += __uint_as_float(rv.y << 16);
-            acc[3] += __uint_as_float(rv.y & 0xffff0000u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[2 * e] += __uint_as_float(rv[e] << 16);
+                acc[2 * e + 1] += __uint_as_float(rv[e] & 0xffff0000u);
+            }
         }
-        uint2 o;
-        o.x = (uint32_t)vmi_f32_to_bf16(acc[0]) | ((uint32_t)vmi_f32_to_bf16(acc[1]) << 16);
-        o.y = (uint32_t)vmi_f32_to_bf16(acc[2]) | ((uint32_t)vmi_f32_to_bf16(acc[3]) << 16);
-        *reinterpret_cast<uint2*>(a.out + (size_t)t * a.H + h) = o;
+        vmi_u4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = vmi_pack_bf16x2(acc[2 * e], acc[2 * e + 1]);
+        *reinterpret_cast<vmi_u4*>(a.out + (size_t)t * a.H + h) = o;
     }
 }
 
