@@ -215,6 +215,14 @@ __device__ __forceinline__ uint32_t vmi_wave_max_u32(uint32_t v) {
 
 __device__ __forceinline__ uint64_t vmi_u64_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+// Compare-exchange of 64-bit keys: a keeps the larger when desc.
+__device__ __forceinline__ void vmi_cx64(uint64_t& a, uint64_t& b, bool desc) {
+    const bool sw = desc ? (a < b) : (a > b);
+    const uint64_t lo = sw ? b : a, hi = sw ? a : b;
+    a = lo;
+    b = hi;
+}
+
 template <int CTRL>
 __device__ __forceinline__ uint64_t vmi_dpp_u64(uint64_t v) {
     const uint32_t lo = vmi_dpp_u32<CTRL>((uint32_t)v), hi = vmi_dpp_u32<CTRL>((uint32_t)(v >> 32));

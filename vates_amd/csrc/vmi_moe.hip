@@ -419,13 +419,6 @@ __device__ __forceinline__ uint64_t topk_rank_key(float f, int e) {
     return ((uint64_t)hi << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
 }
 
-// Compare-exchange of 64-bit keys: a keeps the larger when desc.
-__device__ __forceinline__ void cx64(uint64_t& a, uint64_t& b, bool desc) {
-    const bool sw = desc ? (a < b) : (a > b);
-    const uint64_t lo = sw ? b : a, hi = sw ? a : b;
-    a = lo;
-    b = hi;
-}
 
 // Softmax + top-k + renorm of token t's logits by one wave (block.py:321-329).
 // Lane l holds experts l + 64i (i < NI) as rank keys, sorted descending once
@@ -451,7 +444,7 @@ __device__ void topk_token(const float (&v)[NI], int E, int k, int norm, int t, 
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 const int j = i ^ stride;
-                if (j > i) cx64(key[i], key[j], (i & size) == 0);
+                if (j > i) vmi_cx64(key[i], key[j], (i & size) == 0);
             }
     // each round: the wave maximum of the 32-bit value keys of the lane heads;
     // the lane holding it (a ballot names it; equal values fall back to the

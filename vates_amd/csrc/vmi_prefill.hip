@@ -270,33 +270,56 @@ __device__ __forceinline__ uint64_t pf_rank_key(float f, int e) {
 }
 
 // One wave per token (block.py:321-329): lane l holds experts l + 64 i
-// (i < E/64 <= 16) in registers; k rounds of a wave-wide maximum over each
-// lane's best remaining rank key.
+// (i < E/64 <= 16) as rank keys, sorted descending once (bitonic network);
+// each of the k rounds takes the wave-wide maximum of the lanes' head values
+// (the full (value, index) key only when values tie) and the winning lane
+// records the expert and pops its head.
+template <int NI>
 __global__ __launch_bounds__(kPfThreads) void k_pf_topk(PfArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * (kPfThreads / 64) + pf_wave();
-    if (t >= a.T) return;
+    __shared__ int s_sel[kPfThreads / 64][kPfMaxK];  // a wave's winners in round order
+    const int lane = threadIdx.x & 63, w = pf_wave();
+    const int t = blockIdx.x * (kPfThreads / 64) + w;
+    if (t >= a.T) return;  // whole waves; nothing below synchronises the workgroup
     const float* lt = a.logits + (size_t)t * a.E;
-    const int NI = a.E / 64;  // E is a multiple of 64, at most 1024
-    uint64_t key[16];
+    const int nreal = a.E >> 6;  // key slots i < E/64 are real (uniform)
+    uint64_t key[NI];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) key[i] = i < NI ? pf_rank_key(lt[lane + 64 * i], lane + 64 * i) : 0ull;
-    uint64_t my_key = 0ull;
-    float mx = 0.0f;
+    for (int i = 0; i < NI; ++i) key[i] = i < nreal ? pf_rank_key(lt[lane + 64 * i], lane + 64 * i) : 0ull;
+#pragma unroll
+    for (int size = 2; size <= NI; size *= 2)
+#pragma unroll
+        for (int stride = size / 2; stride > 0; stride /= 2)
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int j = i ^ stride;
+                if (j > i) vmi_cx64(key[i], key[j], (i & size) == 0);
+            }
+#pragma unroll 1
     for (int j = 0; j < a.k; ++j) {
-        uint64_t best = 0ull;
+        const uint32_t hv = (uint32_t)(key[0] >> 32);
+        const uint32_t Mv = vmi_wave_max_u32(hv);
+        const uint64_t cand = __ballot(hv == Mv);
+        bool win;
+        if (__popcll(cand) == 1) {
+            win = hv == Mv;
+        } else {
+            const uint64_t M = vmi_wave_max_u64(hv == Mv ? key[0] : 0ull);
+            win = key[0] == M;
+        }
+        if (win) {
+            s_sel[w][j] = (int)(0xffffffffu - (uint32_t)key[0]);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) best = key[i] > best ? key[i] : best;
-        const uint64_t M = vmi_wave_max_u64(best);
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            if (key[i] == M) key[i] = 0ull;  // the one lane holding the winner drops it
-        if (lane == j) my_key = M;
+            for (int i = 0; i + 1 < NI; ++i) key[i] = key[i + 1];
+            key[NI - 1] = 0ull;
+        }
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const bool sel = lane < a.k;
-    const int my_idx = (int)(0xffffffffu - (uint32_t)my_key);
+    const int my_idx = sel ? s_sel[w][lane] : 0;
     const float my_val = sel ? lt[my_idx] : 0.0f;
-    mx = vmi_readlane_f32(my_val, 0);
+    const float mx = vmi_readlane_f32(my_val, 0);
     const bool bad = __ballot(sel && !(fabsf(my_val) < 3.0e38f)) != 0;
     const float e = sel ? expf(my_val - mx) : 0.0f;
     float den = 0.0f;
@@ -304,7 +327,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_topk(PfArgs a) {
         for (int j = 0; j < a.k; ++j) den = den + vmi_readlane_f32(e, j);
     } else {
         float part = 0.0f;
-        for (int i = 0; i < NI; ++i) part = part + expf(lt[lane + 64 * i] - mx);
+        for (int i = 0; i < nreal; ++i) part = part + expf(lt[lane + 64 * i] - mx);
         den = vmi_wave_sum_canon(part);
     }
     if (sel) {
@@ -1302,7 +1325,19 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
             default: hipLaunchKernelGGL(k_pf_sgate<4>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
         }
     }
-    hipLaunchKernelGGL(k_pf_topk, dim3(tok_blocks), dim3(kPfThreads), 0, s, a);
+    {
+        const int ni = D.num_experts / 64;  // key slots per lane, padded to a power of two
+        if (ni <= 1)
+            hipLaunchKernelGGL(k_pf_topk<1>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a);
+        else if (ni <= 2)
+            hipLaunchKernelGGL(k_pf_topk<2>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a);
+        else if (ni <= 4)
+            hipLaunchKernelGGL(k_pf_topk<4>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a);
+        else if (ni <= 8)
+            hipLaunchKernelGGL(k_pf_topk<8>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL(k_pf_topk<16>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a);
+    }
     hipLaunchKernelGGL(k_pf_count, dim3((T * D.top_k + kCountRoutes - 1) / kCountRoutes), dim3(kPfThreads), 0, s, a);
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
