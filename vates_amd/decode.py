@@ -71,17 +71,19 @@ class SpecModel:
                 l.gdn.new_cache(max_batch) if l.gdn is not None else None for l in self.layers]
 
     def forward(self, ids: torch.Tensor, caches: list, pos0: int, *, want_logits: bool = False,
-                pos_device: Optional[torch.Tensor] = None):
+                pos_device: Optional[torch.Tensor] = None, hidden_out: Optional[torch.Tensor] = None):
         """ids int32 [T] on the device at positions pos0.. (or at the position
         held by pos_device, int32 [1] on the device); returns (argmax int32 [T],
-        pre-norm hidden bf16 [T, H], logits f32 [T, V] or None)."""
+        pre-norm hidden bf16 [T, H], logits f32 [T, V] or None).  hidden_out
+        (bf16 [T, H], optional): where the last layer writes the hidden."""
         x = rmsnorm(self.embed, None, ids=ids)
-        for layer, cache in zip(self.layers, caches):
+        last = len(self.layers) - 1
+        for i, (layer, cache) in enumerate(zip(self.layers, caches)):
             if layer.attn is not None:
                 x = layer.attn(x, cache, pos0=pos0, pos_device=pos_device)
             elif layer.gdn is not None:
                 x = layer.gdn(x, cache, pos0=pos0, pos_device=pos_device)
-            x = layer.moe(x, residual=x)
+            x = layer.moe(x, residual=x, out=hidden_out if i == last else None)
         logits, am, _ = lm_head(x, self.head, self.final_norm, eps=self.eps, want_logits=want_logits)
         return am, x, logits
 
@@ -401,7 +403,11 @@ class GraphSpecDecoder:
         self.verify = torch.zeros(K + 1, dtype=torch.int32, device=dev)
         self.x, self.drafts = self.verify[0:1], self.verify[1:]
         self.probs = torch.zeros(K, dtype=torch.float32, device=dev)
-        self.hseq = torch.zeros((K + 1, model.hidden), dtype=torch.bfloat16, device=dev)
+        # hidden rows of the MTP update: row 0 H_last, rows 1.. the verify
+        # forward's hidden, which it writes there itself (one row beyond the
+        # update's K + 1 takes the last verify row)
+        hext = torch.zeros((K + 2, model.hidden), dtype=torch.bfloat16, device=dev)
+        self.hseq, self.hrows = hext[0:K + 1], hext[1:K + 2]
         self.H = self.hseq[0:1]
         self.rec_buf = torch.zeros(4 + K + 1, dtype=torch.int32, device=dev)
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -425,10 +431,9 @@ class GraphSpecDecoder:
         mtp = self.model.mtp
         if self.use_planted:
             self.drafts[:d].copy_(self.planted[:d])
-        preds, hid, _ = self.model.forward(self.verify[:T], self.caches, 0, pos_device=self.pos)
+        preds, hid, _ = self.model.forward(self.verify[:T], self.caches, 0, pos_device=self.pos,
+                                           hidden_out=self.hrows[:T])
         rec = accept_greedy(self.drafts[:d], preds, mode=1 if self.layout == "k+1" else 0, out=self.rec_buf)
-        if T > 1:
-            self.hseq[1:T].copy_(hid[:T - 1])
         mtp.advance(self.hseq[:T], self.verify[:T], self.drafter.cache, pos_device=self.mtp_len)
         spec_commit(rec, hid, self.H, self.x, self.pos, self.mtp_len, self.mtp_pos, rows=T, status=self.status)
         return rec
