@@ -891,8 +891,16 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     const int nl = lane & 15, q4 = lane >> 4;
     VMI_STAMP(3, 0);
     VMI_STAMP_HWID(3, 4);
-    const int ks = K / kQ4Kw, tiles = kQ4Waves / ks;
-    const int tile = w / ks, kw = w % ks;
+    // every argument read below in SGPRs at once: one wait for the argument
+    // block (fields read lazily, under the matrix branches, cost a round trip
+    // each before the first load could issue)
+    asm volatile("" ::"s"(a.x), "s"(a.m[0].w), "s"(a.m[0].s), "s"(a.m[0].b), "s"(a.m[1].w), "s"(a.m[1].s),
+                 "s"(a.m[1].b), "s"(a.m[2].w), "s"(a.m[2].s), "s"(a.m[2].b));
+    asm volatile("" ::"s"(a.rows[0]), "s"(a.rows[1]), "s"(a.nrows), "s"(a.residual), "s"(a.out_bf16), "s"(a.out),
+                 "s"(a.out_stride), "s"(T), "s"(K));
+    const int lks = __builtin_ctz((unsigned)K) - 9;  // K / kQ4Kw = 1 << lks (K is 512, 1024, 2048 or 4096)
+    const int ks = 1 << lks, tiles = kQ4Waves >> lks;
+    const int tile = w >> lks, kw = w & (ks - 1);
     const int n = (blockIdx.x * tiles + tile) * RT + (nl & (RT - 1));
     const int nn = n < a.nrows ? n : a.nrows - 1;
     // matrix of row nn, selected from the kernel arguments by value (an
@@ -913,7 +921,21 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     // A operands: token tk, columns kw*512 + 128 m + 32 q4 + 8 j .. + 7
     const int tk = nl & 7;
     const bool xreal = ((q4 < 2) == (nl < 8)) && tk < T;
-    uint4 xu[4][4];
+    const uint4* xr;  // the lane's operand words in LDS (set below)
+    // Without the norm, each wave reads its 512-column slice of the T input
+    // rows first, whole 1 KB rows per load (lane L: 16 bytes at 16 L), and
+    // puts it in operand order through LDS below.  The operand order itself
+    // (16 bytes at 64-byte steps across the lanes, 16 loads a lane) touched
+    // eight times as many cache lines and was what the CU's load pipeline
+    // spent its time on.
+    vmi_u4 xv[kQgMaxT];
+    if constexpr (!NORM) {
+        const __amdgpu_buffer_rsrc_t rx = vmi_rsrc(a.x, (uint32_t)(T * K) * 2u);
+#pragma unroll
+        for (int i = 0; i < kQgMaxT; ++i)
+            if (i < T) xv[i] = vmi_bload_b128(rx, (uint32_t)((i * K + kw * kQ4Kw) * 2 + lane * 16), 0);
+        asm volatile("" ::: "memory");
+    }
     constexpr int NXW = NORM ? kQgMaxT * kQ4MaxK / 8 / kQ4Threads : 1;
     vmi_u4 xw[NXW], nw;
     if constexpr (NORM) {
@@ -926,6 +948,13 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
         nw = vmi_bload_b128(rn, (uint32_t)tid * 16u, 0);
         asm volatile("" ::: "memory");
     }
+    // Every wave's input loads are issued before any wave's weight loads: a
+    // CU returns vector loads in issue order, so a wave that issued its
+    // input behind another wave's weights would wait for those weights
+    // (waves 4..7 had their x 1.6 us after waves 0..3).  The barrier does
+    // not wait for the loads themselves.
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
     const uint4* wrow = reinterpret_cast<const uint4*>(M.w + (size_t)r * (K / 8));
     uint4 wv[4];
 #pragma unroll
@@ -948,6 +977,20 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     const int row0 = (blockIdx.x * tiles + tid / (RT * T)) * RT + (tid / T) % RT;
     const uint32_t res0 = vmi_bload_b16(
         rres, tid < nout && row0 < a.nrows ? (uint32_t)(((size_t)(tid % T) * a.out_stride + row0) * 2) : VMI_OOB, 0);
+    asm volatile("" ::: "memory");
+    if constexpr (!NORM) {
+        // the wave's slice into its own LDS rows (padded by 16 bytes against
+        // bank conflicts between tokens); the same wave reads it back in
+        // operand order below
+        __shared__ uint4 s_xw[kQ4Waves][kQgMaxT][kQ4Kw / 8 + 1];
+#pragma unroll
+        for (int i = 0; i < kQgMaxT; ++i)
+            if (i < T) s_xw[w][i][lane] = make_uint4(xv[i][0], xv[i][1], xv[i][2], xv[i][3]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        xr = &s_xw[w][xreal ? tk : 0][4 * q4];
+    }
     if constexpr (NORM) {
         // the rows into LDS, wave t normalises token t there, every wave then
         // reads its operands (the weights keep streaming meanwhile)
@@ -994,25 +1037,24 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
             }
         }
         __syncthreads();
-        const uint4* xr = s_xn + (size_t)(xreal ? tk : 0) * (K / 8) + kw * (kQ4Kw / 8) + 4 * q4;
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) xu[m][j] = xr[16 * m + j];
+        xr = s_xn + (size_t)(xreal ? tk : 0) * (K / 8) + kw * (kQ4Kw / 8) + 4 * q4;
     }
+    // the lane's operand words from LDS (uint4 16 m + 4 q4 + j of its
+    // token's slice; lanes outside the batch read token 0 and use zeros) and
+    // their group sums
+    uint4 xu[4][4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xu[m][j] = xr[16 * m + j];
     vmi_u4 ax[4][4];
     float xs[4] = {0.f, 0.f, 0.f, 0.f};
     if (xreal) {
-        const uint4* xg = reinterpret_cast<const uint4*>(a.x + (size_t)tk * K + kw * kQ4Kw) + 4 * q4;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                uint4 u;
-                if constexpr (NORM)
-                    u = xu[m][j];
-                else
-                    u = xg[16 * m + j];
+                const uint4 u = xu[m][j];
                 ax[m][j][0] = (u.x & 0xffffu) | (u.z << 16);
                 ax[m][j][1] = (u.x >> 16) | (u.z & 0xffff0000u);
                 ax[m][j][2] = (u.y & 0xffffu) | (u.w << 16);
