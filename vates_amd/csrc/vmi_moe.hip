@@ -1044,6 +1044,11 @@ __global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
     const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
     VMI_STAMP(2, 0);
     VMI_STAMP_HWID(2, 3);
+    // the arguments in SGPRs at once: one wait for the argument block rather
+    // than one per field read lazily under a branch
+    asm volatile("" ::"s"(a.route), "s"(a.down.w), "s"(a.down.s), "s"(a.down.b), "s"(a.sh_down.w), "s"(a.sh_down.s),
+                 "s"(a.sh_down.b), "s"(a.actop), "s"(a.axs), "s"(a.sg_logit), "s"(a.residual), "s"(a.out));
+    asm volatile("" ::"s"(a.I), "s"(a.has_sgate), "s"(a.out_dtype));
 
     // activation operands of the wave's expert i (list position e), tokens
     // tb..tb+tpass-1: lane l holds word l (+64c) of each token row
@@ -1081,12 +1086,19 @@ __global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
                       fin ? (uint32_t)((tid >> 3) * H + h0 + (tid & 7)) * 2u : VMI_OOB, 0);
     // the route through the scalar cache (written by the previous kernel; the
     // scalar cache starts empty in every kernel)
+    // (every address is inside the route record, so the loads are issued
+    // together and waited for once; the unused ones are discarded)
     const int U = vmi_sload_i32(&a.route->U);
     int slots0[PW];
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
         const int e = w + kDnWaves * i;
-        slots0[i] = (e >= hs && e < NEmax) ? vmi_sload_i32(&a.route->uslot[e - hs]) : 0;
+        slots0[i] = vmi_sload_i32(&a.route->uslot[min(max(e - hs, 0), vmi::kRouteMaxPairs - 1)]);
+    }
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+        const int e = w + kDnWaves * i;
+        if (!(e >= hs && e < NEmax)) slots0[i] = 0;
     }
     for (int i = tid; i < TMAX * kDnRanks * 2 * kDnRows; i += kDnThreads) (&s_pair[0][0][0][0])[i] = 0.0f;
     for (int i = tid; i < 1024 / 4; i += kDnThreads) reinterpret_cast<uint32_t*>(s_zero)[i] = 0u;
