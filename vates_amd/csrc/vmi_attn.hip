@@ -952,8 +952,10 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     // CU returns vector loads in issue order, so a wave that issued its
     // input behind another wave's weights would wait for those weights
     // (waves 4..7 had their x 1.6 us after waves 0..3).  The barrier does
-    // not wait for the loads themselves.
-    __builtin_amdgcn_s_barrier();
+    // not wait for the loads themselves.  The normalising form goes without:
+    // its input words are two whole-row loads a thread, and it measured
+    // slightly faster without the barrier.
+    if constexpr (!NORM) __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const uint4* wrow = reinterpret_cast<const uint4*>(M.w + (size_t)r * (K / 8));
     uint4 wv[4];
