@@ -67,11 +67,10 @@ typedef struct vmi_qmat {
  * gate/up stacks [cap, inter, hidden], down stack [cap, hidden, inter],
  * out [T, hidden] in out_dtype = sum_j scores[t*k+j] * expert_{slot}(x_t)
  * (SwiGLU expert: g*sigmoid(g)*u then down; fixed j order as reduce_pairs).
- * Arithmetic: with f32 x, the reference operator's fp32 throughout (fp32 x,
- * weights q*s + b, activations and pair outputs; relative error about 1e-6
- * against a float64 evaluation); with bf16 x, the decode path's MFMA operands
- * (fp16 x scaled by a power of two, bf16 activations, fp32 accumulation;
- * relative error about 2e-3).
+ * Arithmetic: the reference operator's fp32 throughout (x widened to fp32 -
+ * exactly, for bf16 x - weights q*s + b, activations and pair outputs;
+ * relative error about 1e-6 against a float64 evaluation).  The pool stacks
+ * keep the reference's layout.
  * Supported: bits == 4, group == 64, T*k <= 160, T <= 16,
  * hidden in {512, 1024, 2048}, inter a multiple of 64 up to 512.
  * The reference raises on shape mismatch (fused_moe.cpp:522-524); this
@@ -131,13 +130,22 @@ typedef struct vmi_moe_layer_desc {
     vmi_qmat router;              /* [1, num_experts, hidden] */
     const float* router_logit_bias; /* [num_experts] added to raw logits, or NULL */
     const int32_t* slot_table;    /* [num_experts] expert -> pool slot, or NULL */
-    vmi_qmat gate, up, down;      /* pool stacks [cap, ...] */
-    vmi_qmat shared_gate, shared_up, shared_down; /* [1, ...]; shared_gate.w == NULL: no shared expert */
+    vmi_qmat gate, up, down;      /* pool stacks [cap, ...] in the kernels' layouts (below) */
+    vmi_qmat shared_gate, shared_up, shared_down; /* [1, ...], same layouts; shared_gate.w == NULL: none */
     vmi_qmat shared_expert_gate;  /* [1, 1, hidden]; .w == NULL: gate fixed to 1 */
     int shared_expert_gate_bits;  /* 4 or 8 */
     const uint16_t* norm_weight;  /* [hidden] bf16 RMSNorm weight, or NULL: no norm */
     float norm_eps;
 } vmi_moe_layer_desc;
+/* Pool layouts of vmi_moe_layer / vmi_moe_prefill (the packed values, scales
+ * and biases are the reference's; only their order in memory differs, and
+ * vates_amd/moe.py re-lays the reference's stacks at load time):
+ *   gate, up (MFMA-major): words [cap, inter/64, 4, hidden/128, 64, 4] - block
+ *     (c, w, m), entry l = 16 q + r holds the 16 bytes at byte 64 m + 16 q of
+ *     row 64 c + 16 w + r of the reference's [cap, inter, hidden/8] words;
+ *     scales and biases [cap, inter, hidden/64] as in the reference;
+ *   down (group-major): words [cap, inter/64, hidden, 8] - quantisation group
+ *     g of row h; scales and biases [cap, inter/64, hidden]. */
 
 size_t vmi_moe_layer_workspace_bytes(int T, int top_k, int hidden, int inter, int num_experts);
 int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, const uint16_t* residual,
@@ -149,7 +157,7 @@ int vmi_moe_layer(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, cons
  * without any allocation: no counterpart in the reference.  It is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The same kernels run on a
- * static device array of 3 MiB per GPU (held until the process ends, looked
+ * static device array of 16 MiB per GPU (held until the process ends, looked
  * up once per device); shapes whose workspace
  * (vmi_moe_layer_workspace_bytes) exceeds it are rejected with
  * VMI_ERR_UNSUPPORTED.  Every call on one GPU shares that array and leaves

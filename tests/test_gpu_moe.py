@@ -266,7 +266,7 @@ def _layer_case(gpu, orc, torch, T, *, zipf_alpha=1.0, router_bits=8, norm=True,
     return moe, x, out, ids, sc, ref_f32, rid, rsc
 
 
-@pytest.mark.parametrize("T", [1, 4, 9, 16])
+@pytest.mark.parametrize("T", [1, 4, 6, 9, 16])
 def test_moe_layer_parity(gpu, orc, torch_mod, T):
     torch = torch_mod
     for residual in (False, True):
@@ -302,7 +302,7 @@ def test_moe_layer_repeatable_bitwise(gpu, orc, torch_mod):
         assert torch.equal(o.view(torch.int16), out.view(torch.int16))
 
 
-@pytest.mark.parametrize("T", [4, 9, 16])
+@pytest.mark.parametrize("T", [4, 6, 9, 16])
 def test_moe_layer_batch_invariant(gpu, orc, torch_mod, T):
     """Every token's output equals its output in a batch of one, bit for bit:
     each token adds its experts in its own rank order (speculative decoding

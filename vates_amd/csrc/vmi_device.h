@@ -141,6 +141,14 @@ __device__ __forceinline__ float vmi_readlane_f32(float v, int lane) {
     return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), lane));
 }
 
+// `from` shifted by a DPP row control into the lane banks (4-lane groups of
+// each 16-lane row) selected by BANKS; the other lanes keep `keep`.
+template <int CTRL, int BANKS>
+__device__ __forceinline__ float vmi_dpp_into(float keep, float from) {
+    return __uint_as_float(
+        (uint32_t)__builtin_amdgcn_update_dpp((int)__float_as_uint(keep), (int)__float_as_uint(from), CTRL, 0xF, BANKS, false));
+}
+
 // Row rotate by 8 inside each 16-lane row (lane r reads lane r ^ 8), written
 // only to lanes 8..15 (banks 2, 3) or 0..7 (banks 0, 1) of each row; the other
 // lanes keep `keep`.
@@ -287,15 +295,19 @@ __device__ __forceinline__ void vmi_split3_bf16(float x, uint32_t& hi, uint32_t&
     mid = vmi_f32_to_bf16(r1);
     lo = vmi_f32_to_bf16(r1 - vmi_bf16_to_f32(mid));
 }
+// The two values' splits are formed together, each level by one
+// v_cvt_pk_bf16_f32 (the bits of vmi_split3_bf16 for every non-NaN input).
 __device__ __forceinline__ vmi_u4 vmi_bias_a_operand(float x0, float x1) {
-    uint32_t h0, m0, l0, h1, m1, l1;
-    vmi_split3_bf16(x0, h0, m0, l0);
-    vmi_split3_bf16(x1, h1, m1, l1);
+    const uint32_t hi = vmi_pack_bf16x2(x0, x1);
+    const float r0 = x0 - __uint_as_float(hi << 16), r1 = x1 - __uint_as_float(hi & 0xffff0000u);
+    const uint32_t mid = vmi_pack_bf16x2(r0, r1);
+    const float s0 = r0 - __uint_as_float(mid << 16), s1 = r1 - __uint_as_float(mid & 0xffff0000u);
+    const uint32_t lo = vmi_pack_bf16x2(s0, s1);
     vmi_u4 r;
-    r[0] = h0 | (m0 << 16);
-    r[1] = l0;
-    r[2] = h1 | (m1 << 16);
-    r[3] = l1;
+    r[0] = (hi & 0xffffu) | (mid << 16);
+    r[1] = lo & 0xffffu;
+    r[2] = (hi >> 16) | (mid & 0xffff0000u);
+    r[3] = lo >> 16;
     return r;
 }
 __device__ __forceinline__ vmi_u4 vmi_bias_b_operand(uint32_t bb) {
@@ -466,6 +478,11 @@ __device__ __forceinline__ vmi_u4 vmi_bload_b128_coh(__amdgpu_buffer_rsrc_t r, u
     o[2] = v[2];
     o[3] = v[3];
     return o;
+}
+// Buffer store of 16 bytes; a lane whose offset is VMI_OOB (past the
+// resource's range) stores nothing, so a predicated store needs no branch.
+__device__ __forceinline__ void vmi_bstore_b128(const vmi_u4& v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)voff, (int)soff, 0);
 }
 __device__ __forceinline__ uint32_t vmi_bload_b16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);

@@ -28,11 +28,10 @@ struct RouteInfo {
     float wt[kRouteMaxPairs][kRouteMaxT];    // combine weight of (u, token): sum of its pairs' scores
     int32_t jr[kRouteMaxPairs][kRouteMaxT];  // rank j of the token's first pair on u, -1 if none: the
                                              // token's experts are added in rank order
+    int32_t pv[kRouteMaxPairs];              // 1: pair p is its token's first pair on a valid slot
 };
 
-// Workspace carve-up shared by vmi_fused_moe_slots and vmi_moe_layer.  Expert
-// activations are indexed by distinct slot u < T*k; index T*k is the shared
-// expert.
+// Workspace carve-up of vmi_moe_layer (and its no-allocation variant).
 struct MoeWorkspace {
     uint32_t* status;     // device status word (VMI_STATUS_*)
     RouteInfo* route;
@@ -41,8 +40,8 @@ struct MoeWorkspace {
     uint32_t __attribute__((ext_vector_type(4)))* xop;    // [T, H/8] MFMA operands of the MoE input
     float* xsum;          // [T, H/64] per-group sums of those operands
     float* fscale;        // [T] power-of-two range factor of the operands
-    uint32_t __attribute__((ext_vector_type(4)))* actop;  // [T*k+1, T, I/8] bf16 down-projection operands
-    float* axs;           // [T*k+1, T, I/64] per-group activation sums
+    float* part;          // [T*k + T, I/64, H] weighted fp32 partial rows: pair p's (or the shared
+                          // expert's for token t, row T*k + t) down projection of each slice
     size_t bytes;
 };
 

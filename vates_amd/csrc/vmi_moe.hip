@@ -90,22 +90,6 @@ __device__ __forceinline__ vmi_u4 make_act_operand(const float (&xv)[8], float f
     return r;
 }
 
-template <typename XT>
-__device__ __forceinline__ void load_x8(const XT* __restrict__ row, int c, float (&v)[8]);
-
-template <>
-__device__ __forceinline__ void load_x8<uint16_t>(const uint16_t* __restrict__ row, int c, float (&v)[8]) {
-    unpack_bf16x8(*reinterpret_cast<const uint4*>(row + c), v);
-}
-
-template <>
-__device__ __forceinline__ void load_x8<float>(const float* __restrict__ row, int c, float (&v)[8]) {
-    const float4 p = *reinterpret_cast<const float4*>(row + c);
-    const float4 q = *reinterpret_cast<const float4*>(row + c + 4);
-    v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w;
-    v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
-}
-
 // Canonical inverse rms shared with the CPU oracle: lane l of a wave holds
 // columns [l*cpl, (l+1)*cpl) (cpl/8 packed chunks); x^2 summed with fmaf in
 // column order, the canonical wave-sum tree, then 1/sqrt(ss/H + eps) with
@@ -129,83 +113,6 @@ struct OperandOut {
     float* xsum;    // [T, H/64]
     float* fscale;  // [T]
 };
-
-// One 256-thread workgroup writes the MFMA operands of token t: the MoE input
-// (x, or the RMSNorm output rounded to bf16) scaled by a power of two f with
-// max|x f| in (2^13, 2^14], in fp16, per-group sums, and f.
-template <typename XT, int CPL>
-__device__ void write_operands(const XT* __restrict__ xrow, const uint16_t* __restrict__ norm_w, float eps, int H,
-                               int t, const OperandOut& o) {
-    __shared__ float s_red[kThreads / VMI_WAVE];
-    __shared__ float s_inv;
-    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
-    constexpr int kChunksPerThread = (64 * CPL) / (8 * kThreads) > 0 ? (64 * CPL) / (8 * kThreads) : 1;
-    const bool active = 8 * tid < H;
-    float v[kChunksPerThread][8];
-#pragma unroll
-    for (int ch = 0; ch < kChunksPerThread; ++ch) {
-        const int c0 = 8 * tid + ch * 8 * kThreads;
-        if (active) {
-            load_x8<XT>(xrow, c0, v[ch]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[ch][i] = 0.0f;
-        }
-    }
-    float inv = 1.0f;
-    if (norm_w) {
-        if constexpr (sizeof(XT) == 2) {
-            if (w == 0) {
-                uint4 xr[CPL / 8];
-#pragma unroll
-                for (int ch = 0; ch < CPL / 8; ++ch)
-                    xr[ch] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(xrow) + lane * CPL +
-                                                             8 * ch);
-                const float iv = canonical_inv_rms<CPL / 8>(xr, H, eps);
-                if (lane == 0) s_inv = iv;
-            }
-        }
-        __syncthreads();
-        inv = s_inv;
-#pragma unroll
-        for (int ch = 0; ch < kChunksPerThread; ++ch) {
-            if (active) {
-                float nw[8];
-                load_x8<uint16_t>(norm_w, 8 * tid + ch * 8 * kThreads, nw);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) v[ch][i] = vmi_bf16r((v[ch][i] * inv) * nw[i]);
-            }
-        }
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int ch = 0; ch < kChunksPerThread; ++ch)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[ch][i]));
-    amax = vmi_wave_max(amax);
-    if (lane == 0) s_red[w] = amax;
-    __syncthreads();
-    float am = s_red[0];
-#pragma unroll
-    for (int i = 1; i < kThreads / VMI_WAVE; ++i) am = fmaxf(am, s_red[i]);
-    const float f = vmi_fp16_range_scale(am);
-    const int G = H / 64;
-#pragma unroll
-    for (int ch = 0; ch < kChunksPerThread; ++ch) {
-        const int c0 = 8 * tid + ch * 8 * kThreads;
-        float xs = 0.0f;
-        const vmi_u4 op = make_act_operand(v[ch], f, xs);
-        // group sum over the 8 threads holding one 64-column group
-        xs += __shfl_xor(xs, 1, VMI_WAVE);
-        xs += __shfl_xor(xs, 2, VMI_WAVE);
-        xs += __shfl_xor(xs, 4, VMI_WAVE);
-        if (active) {
-            o.xop[(size_t)t * (H / 8) + c0 / 8] = op;
-            if ((tid & 7) == 0) o.xsum[(size_t)t * G + c0 / 64] = xs;
-        }
-    }
-    if (tid == 0) o.fscale[t] = f;
-}
 
 // ---------------------------------------------------------------- router
 struct RouterArgs {
@@ -590,63 +497,48 @@ __device__ void dedup_lds(int npairs, int k, int cap, RouteLds& R, int32_t* s_fi
     __syncthreads();
 }
 
-// ---------------------------------------------------------------- gate/up
-struct GateUpArgs {
-    int T, I, k, E, npairs, has_shared;
+// ------------------------------------------------------------- experts
+// Routing inputs and outputs shared by the two routed kernels (k_experts on
+// the router's logits, k_gateup_f32 on a caller's slot list).
+struct RouteArgs {
+    int T, I, k, E, npairs;
     int from_slots;               // 1: caller slots + scores, 0: route from logits
     int norm, cap;
     const float* logits;          // [T, E]
     const int32_t* table;         // [E] or nullptr
     const int32_t* slots;         // [T*k] (from_slots), or nullptr: pair p uses matrix p
     const float* in_scores;       // [T*k] (from_slots)
-    vmi_qmat gate, up, sh_gate, sh_up;
-    const vmi_u4* xop;            // [T, H/8]
-    const float* xsum;            // [T, H/64]
-    const float* fscale;          // [T]
     RouteInfo* route;             // written by the first routed workgroup
     uint32_t* status;
     int32_t* ids_out;             // [T*k] or nullptr
     float* scores_out;            // [T*k] or nullptr
-    vmi_u4* actop;                // [npairs+1, T, I/8] bf16 down-projection operands
-    float* axs;                   // [npairs+1, T, I/64] their per-group sums
 };
 
-// Routing of the batch inside one k_gateup workgroup (all threads).
-__device__ void route_batch(const GateUpArgs& a, RouteLds& R, int32_t* s_table, int32_t* s_first) {
-    const int tid = threadIdx.x, w = vmi_wave_id();
+// Routing of the batch from the router logits inside one workgroup (all
+// threads): top-k per token, slot table, first-appearance distinct slots.
+__device__ void route_batch(const RouteArgs& a, RouteLds& R, int32_t* s_table, int32_t* s_first) {
+    const int tid = threadIdx.x;
     const int T = a.T, k = a.k, npairs = a.npairs;
     if (tid == 0) R.bad = 0u;
-    if (!a.from_slots) {
-        route_topk_dispatch(a.logits, T, a.E, k, a.norm, a.table, s_table, R);
-        __syncthreads();
-        VMI_STAMP(1, 1);
-        if (tid < npairs) {
-            const int id = R.ids[tid];
-            int sl = (id >= 0 && id < a.E) ? (a.table ? s_table[id] : id) : -1;
-            if (sl < 0 || sl >= a.cap) {
-                sl = -1;
-                atomicOr(&R.bad, VMI_STATUS_BAD_SLOT);
-            }
-            R.slot[tid] = sl;
+    route_topk_dispatch(a.logits, T, a.E, k, a.norm, a.table, s_table, R);
+    __syncthreads();
+    VMI_STAMP(1, 1);
+    if (tid < npairs) {
+        const int id = R.ids[tid];
+        int sl = (id >= 0 && id < a.E) ? (a.table ? s_table[id] : id) : -1;
+        if (sl < 0 || sl >= a.cap) {
+            sl = -1;
+            atomicOr(&R.bad, VMI_STATUS_BAD_SLOT);
         }
-    } else {
-        __syncthreads();
-        if (tid < npairs) {
-            const int s = a.slots ? a.slots[tid] : tid;  // no slot list: pair p uses matrix p
-            const bool ok = s >= 0 && s < a.cap;
-            R.slot[tid] = ok ? s : -1;
-            R.scores[tid] = a.in_scores[tid];
-            if (!ok) atomicOr(&R.bad, VMI_STATUS_BAD_SLOT);
-        }
+        R.slot[tid] = sl;
     }
     __syncthreads();
     dedup_lds(npairs, k, a.cap, R, s_first);
     VMI_STAMP(1, 2);
 }
 
-// Routing of a caller's slot list (or pair p on matrix p without one): the
-// from-slots half of route_batch, without the top-k code.
-__device__ void route_slots(const GateUpArgs& a, RouteLds& R, int32_t* s_first) {
+// Routing of a caller's slot list (or pair p on matrix p without one).
+__device__ void route_slots(const RouteArgs& a, RouteLds& R, int32_t* s_first) {
     const int tid = threadIdx.x;
     if (tid == 0) R.bad = 0u;
     __syncthreads();
@@ -661,15 +553,23 @@ __device__ void route_slots(const GateUpArgs& a, RouteLds& R, int32_t* s_first) 
     dedup_lds(a.npairs, a.k, a.cap, R, s_first);
 }
 
-// The route table for k_down_rows, the caller's ids/scores and the status
-// bits, written by one routed workgroup once its own work is issued (nothing
-// in this kernel reads them).
-__device__ void publish_route(const GateUpArgs& a, const RouteLds& R) {
+// The route table for the later kernels, the caller's ids/scores and the
+// status bits, written by one routed workgroup once its own work is issued
+// (nothing in the same kernel reads them).  pv[p] = 1 marks pair p as the
+// first pair of its token on a valid slot: the pair whose rows carry that
+// slot's contribution to the token.
+__device__ void publish_route(const RouteArgs& a, const RouteLds& R) {
     const int tid = threadIdx.x;
     const int T = a.T, k = a.k, npairs = a.npairs;
     const int U = R.U;
     if (tid == 0) a.route->U = U;
-    if (tid < npairs) a.route->uslot[tid] = tid < U ? R.uslot[tid] : -1;
+    if (tid < npairs) {
+        a.route->uslot[tid] = tid < U ? R.uslot[tid] : -1;
+        const int s = R.slot[tid], t0 = (tid / k) * k;
+        bool first = s >= 0;
+        for (int p = t0; p < tid; ++p) first = first && R.slot[p] != s;
+        a.route->pv[tid] = first ? 1 : 0;
+    }
     // combine weight of (u, t): its pairs' scores in j order; rank of its first pair
     for (int i = tid; i < U * T; i += kThreads) {
         const int u = i / T, t = i - u * T;
@@ -691,28 +591,70 @@ __device__ void publish_route(const GateUpArgs& a, const RouteLds& R) {
     if (tid == 0 && R.bad) atomicOr(a.status, R.bad);
 }
 
+struct ExpertArgs {
+    RouteArgs ra;
+    int has_shared, has_sgate;
+    vmi_qmat gate, up, sh_gate, sh_up;
+    vmi_qmat down, sh_down;       // group-major [n, I/64, H, 8 words], scales/biases [n, I/64, H]
+    const vmi_u4* xop;            // [T, H/8]
+    const float* xsum;            // [T, H/64]
+    const float* fscale;          // [T]
+    const float* sg_logit;        // [T] (has_sgate)
+    float* part;                  // [npairs + T, I/64, H] weighted partial rows
+};
+
 // One workgroup (4 waves) per item = blockIdx.x: items [0, NC) are the shared
 // expert's slices (when present), then distinct slot u's slices c at
 // nsh + u*NC + c.  Workgroups past the batch's item count exit after routing.
-// Wave w: rows c*64 + 16w + (lane % 16) of gate and up; lane block q = lane/16
-// loads 16 bytes at 64m + 16q of its row for m = 0..NM-1 (two groups per m).
-template <int NM, bool PACK>
-__global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
+//
+// Gate/up: wave w owns rows c*64 + 16w + (lane % 16) of gate and up; lane
+// block q = lane/16 loads 16 bytes at 64m + 16q of its row for m = 0..NM-1
+// (two quantisation groups per m).  SwiGLU of the slice's 64 rows into LDS.
+//
+// Down (split over the intermediate dimension): the slice's 64 activations
+// are exactly quantisation group c of the down projection's input, so the
+// workgroup projects them through that group's column strip of every down
+// row - H rows x 32 bytes, contiguous in the group-major pool - and writes
+// one weighted fp32 partial row per (token, slice).  Wave w takes rows
+// w*H/4 + 16b + r (b < H/64); lane (q, r) reads bytes 8q..8q+7 of row r of
+// block b, so a wave's load covers 512 contiguous bytes.  The strip's loads
+// are issued two blocks per gate/up step, into the registers the step frees.
+// MFMA (v_mfma_f32_16x16x32_bf16, A = weights as exact bf16 128 + n, B =
+// activations, D[4q + e][r] = row 4q + e of the block, token r): MFMA 0 takes
+// dword 2q of each row (columns 16q..16q+7), MFMA 1 dword 2q + 1
+// (16q+8..16q+15), and the activation operands follow that column order.
+// Per row and token y = s (D - 128 X) + b X with X the token's activation
+// sum over the group; the partial is y times the token's combine weight (the
+// shared expert: its sigmoid gate).  Only token columns r < TB of D are
+// real, so PF = 16 / TB blocks are packed into one register set by DPP row
+// shifts first (block i's columns move to lanes r + i TB): the arithmetic and
+// the stores then use every lane.
+template <int NM, int TB>
+__global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArgs a) {
+    constexpr bool PACK = TB <= 8;  // tokens of the even and odd groups share one gate/up MFMA
     constexpr int kT = PACK ? 8 : 16;
+    constexpr int PF = 16 / TB;     // down blocks whose token columns share one register set
     constexpr int H = NM * 128, H8 = H / 8, NG = H / 64;
     constexpr int NB = NM / 4;      // bias MFMAs of 8 groups each
-    constexpr int NSV = NG / 8;     // 16-byte loads of one row's scales
     constexpr int XPT = (kT * H8 + kThreads - 1) / kThreads;
+    constexpr int RPW = H / 4;      // down rows per wave
+    constexpr int NBW = RPW / 16;   // 16-row down blocks per wave (2 per gate/up step)
+    constexpr int NDMA = H / 256;   // LDS copies of the strip's scales and biases (64 x 16 bytes each)
+    static_assert(NBW == 2 * NM, "two down blocks per gate/up step");
     __shared__ vmi_u4 s_x[kT][H8 + 1];
     __shared__ float s_xs[kT][NG];
     __shared__ float s_inv[kT];
     __shared__ float s_act[kT][kSlice + 1];
+    __shared__ __align__(16) uint32_t s_gus[2][kSlice][NG / 2];  // gate, up scales of the slice's rows (bf16 pairs)
+    __shared__ __align__(16) uint16_t s_dsb[2][H];  // the strip's scales, then biases (bf16)
+    __shared__ int32_t s_prow[kMaxT];
+    __shared__ float s_wt[kMaxT];
     __shared__ RouteLds R;
     __shared__ int32_t s_table[kMaxE];
     __shared__ int32_t s_first[kFirstTable];
     const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     const int q = lane >> 4, r = lane & 15;
-    const int T = a.T, I = a.I, NC = I / kSlice;
+    const int T = a.ra.T, I = a.ra.I, k = a.ra.k, NC = I / kSlice;
     const int nsh = a.has_shared ? NC : 0;
     const int item = blockIdx.x;
     const bool is_shared = item < nsh;
@@ -732,23 +674,23 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
 #pragma unroll
     for (int i = 0; i < XSPT; ++i) xsr[i] = vmi_bload_b32(rxs, (uint32_t)(tid + kThreads * i) * 4u, 0);
     const uint32_t fsr = vmi_bload_b32(vmi_rsrc(a.fscale, (uint32_t)T * 4u), (uint32_t)tid * 4u, 0);
+    const uint32_t sgr = vmi_bload_b32(vmi_rsrc(a.sg_logit, a.has_sgate ? (uint32_t)T * 4u : 0u), (uint32_t)tid * 4u, 0);
 
-    int slot = 0, c = item, aidx = a.npairs;
+    int slot = 0, c = item;
     uint32_t tmask = (1u << T) - 1u;
     if (!is_shared) {
-        route_batch(a, R, s_table, s_first);
+        route_batch(a.ra, R, s_table, s_first);
         const int ii = item - nsh, u = ii / NC;
         if (u >= vmi_uniform(R.U)) {
-            if (item == nsh) publish_route(a, R);  // no routed item at all
+            if (item == nsh) publish_route(a.ra, R);  // no routed item at all
             return;
         }
         c = ii - u * NC;
         slot = vmi_uniform(R.uslot[u]);
         tmask = (uint32_t)vmi_uniform((int)R.umask[u]);
-        aidx = u;
     }
 
-    // every weight load of the item (scales, biases, gate/up words by m):
+    // every gate/up weight load of the item (scales, biases, words by m):
     // loads retire in issue order, so everything the arithmetic needs first is
     // issued first
     const vmi_qmat mg = is_shared ? a.sh_gate : a.gate;
@@ -756,17 +698,21 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     const uint32_t wbytes = (uint32_t)I * (H / 2), sbytes = (uint32_t)I * NG * 2u;
     const __amdgpu_buffer_rsrc_t rgw = vmi_rsrc(mg.w + (size_t)slot * I * H8, wbytes);
     const __amdgpu_buffer_rsrc_t ruw = vmi_rsrc(mu.w + (size_t)slot * I * H8, wbytes);
-    const __amdgpu_buffer_rsrc_t rgs = vmi_rsrc(mg.s + (size_t)slot * I * NG, sbytes);
-    const __amdgpu_buffer_rsrc_t rus = vmi_rsrc(mu.s + (size_t)slot * I * NG, sbytes);
     const __amdgpu_buffer_rsrc_t rgb = vmi_rsrc(mg.b + (size_t)slot * I * NG, sbytes);
     const __amdgpu_buffer_rsrc_t rub = vmi_rsrc(mu.b + (size_t)slot * I * NG, sbytes);
     const uint32_t row = (uint32_t)(c * kSlice + 16 * w + r);
     const uint32_t sboff = row * NG * 2u;
-    vmi_u4 sg4[NSV], su4[NSV];
+    // the slice's gate and up scales straight into LDS (64 rows x NG bf16
+    // each, contiguous): copy i (wave i % 4) moves 16-byte units 64i..64i+63
+    {
+        constexpr int NSC = 2 * kSlice * NG * 2 / 1024;  // 1 KB copies
+        constexpr int UPM = kSlice * NG * 2 / 16;          // units per matrix
 #pragma unroll
-    for (int i = 0; i < NSV; ++i) {
-        sg4[i] = vmi_bload_b128_nt(rgs, sboff, 16u * i);
-        su4[i] = vmi_bload_b128_nt(rus, sboff, 16u * i);
+        for (int i = w; i < NSC; i += 4) {
+            const int u = 64 * i + lane, x = u / UPM, o = u - x * UPM;
+            vmi_lds_dma16_opaque_nt(reinterpret_cast<const uint8_t*>((x ? mu.s : mg.s) + ((size_t)slot * I + c * kSlice) * NG) + 16 * o,
+                                    &s_gus[0][0][0] + 256 * i);
+        }
     }
     uint32_t bgw[NB], buw[NB];
     {
@@ -787,43 +733,46 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
             buw[0] = vmi_bload_b32_nt(rub, boff, 0);
         }
     }
-    // Weights in whole 128-byte lines, nontemporal: load pair p covers rows
-    // 16w..16w+7 (then +8) x bytes 128p..128p+127, lanes r < 8 taking the even
-    // 64-byte chunk of row r and lanes r >= 8 the odd chunk of row r - 8.  A
-    // row rotate by 8 inside each 16-lane row then gives lane r row r's even
-    // chunk (m = 2p) and odd chunk (m = 2p + 1), the MFMA operand layout; the
-    // rotates happen at the MFMA that uses them, so the waits for the stream
-    // stay spread over the MFMA loop.  wl[x][2p], wl[x][2p + 1] hold pair p's
-    // two loads of matrix x (0 gate, 1 up).
-    // (The 16-token form keeps 64-byte row pieces, wl[x][m] in operand layout:
-    // it has no registers to spare for the rotates.)
-    const uint32_t rowa = (uint32_t)(c * kSlice + 16 * w + (r & 7));
-    const uint32_t woffa = rowa * (uint32_t)(H / 2) + 64u * (uint32_t)(r >> 3) + 16u * q;
-    const uint32_t woffb = woffa + 8u * (uint32_t)(H / 2);
+    // Gate/up words in MFMA operand order (the pool is MFMA-major): block
+    // (c, w, m) of a slot's matrix holds lane l's 16 bytes at 16 l, so each
+    // wave load is 1 KB of contiguous memory and a slice 64 KB.
     vmi_u4 wl[2][NM];
-    if constexpr (!PACK) {
-        const uint32_t woff = row * (uint32_t)(H / 2) + 16u * q;
+    {
+        const uint32_t woff = (uint32_t)((c * 4 + w) * NM) * 1024u + 16u * (uint32_t)lane;
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-            wl[0][m] = vmi_bload_b128_nt(rgw, woff, 64u * m);
-            wl[1][m] = vmi_bload_b128_nt(ruw, woff, 64u * m);
-        }
-    } else {
-#pragma unroll
-        for (int pp = 0; pp < NM / 2; ++pp) {
-            wl[0][2 * pp] = vmi_bload_b128_nt(rgw, woffa, 128u * pp);
-            wl[0][2 * pp + 1] = vmi_bload_b128_nt(rgw, woffb, 128u * pp);
-            wl[1][2 * pp] = vmi_bload_b128_nt(ruw, woffa, 128u * pp);
-            wl[1][2 * pp + 1] = vmi_bload_b128_nt(ruw, woffb, 128u * pp);
+            wl[0][m] = vmi_bload_b128_nt(rgw, woff, 1024u * m);
+            wl[1][m] = vmi_bload_b128_nt(ruw, woff, 1024u * m);
         }
     }
-    auto woperand = [&](int x, int m) -> vmi_u4 {
-        if constexpr (!PACK) return wl[x][m];
-        return (m & 1) ? vmi_row_swap8_lo(wl[x][m], wl[x][m - 1]) : vmi_row_swap8_hi(wl[x][m], wl[x][m + 1]);
-    };
+    // the down strip of this slice: rows of 32 bytes, group-major
+    const vmi_qmat md = is_shared ? a.sh_down : a.down;
+    const size_t drow0 = ((size_t)slot * NC + c) * H;
+    const __amdgpu_buffer_rsrc_t rdw = vmi_rsrc(md.w + drow0 * 8, (uint32_t)H * 32u);
+    const uint32_t doff = (uint32_t)(RPW * w + r) * 32u + 8u * (uint32_t)q;
+    uint2 dw[NBW];
 
     // the first routed workgroup publishes the route while its weights stream
-    if (item == nsh && !is_shared) publish_route(a, R);
+    if (item == nsh && !is_shared) publish_route(a.ra, R);
+    // partial row and combine weight of each token: a routed token's first
+    // pair on this slot and the sum of its pairs' scores there; the shared
+    // expert's rows follow the pairs, weighted by its sigmoid gate
+    if (tid < T) {
+        int pr = -1;
+        float wt = 0.0f;
+        if (is_shared) {
+            pr = a.ra.npairs + tid;
+            wt = a.has_sgate ? 1.0f / (1.0f + expf(-__uint_as_float(sgr))) : 1.0f;
+        } else {
+            for (int j = 0; j < k; ++j)
+                if (R.slot[tid * k + j] == slot) {
+                    wt += R.scores[tid * k + j];
+                    if (pr < 0) pr = tid * k + j;
+                }
+        }
+        s_prow[tid] = pr;
+        s_wt[tid] = wt;
+    }
 
     // operands into LDS
 #pragma unroll
@@ -837,6 +786,10 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
         if (idx < T * NG) s_xs[idx / NG][idx % NG] = __uint_as_float(xsr[i]);
     }
     if (tid < T) s_inv[tid] = 1.0f / __uint_as_float(fsr);
+    // the scale copies precede the two bias loads and the 2 NM weight loads
+    // (and, in one workgroup, the route's stores): with at most 2 + 2 NM
+    // operations outstanding they have landed
+    vmi_vm_wait_c<2 + 2 * NM>();
     __syncthreads();
 
     // main MFMAs: m-th load pair covers groups 2m (K blocks 0-1) and 2m+1 (2-3)
@@ -851,14 +804,14 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
     const int tkc = tk < T ? tk : 0;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-        const vmi_u4 wgm = woperand(0, m), wum = woperand(1, m);
+        const vmi_u4 wgm = wl[0][m], wum = wl[1][m];
         vmi_u4 ax[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const vmi_u4 v = s_x[tkc][16 * m + 4 * q + j];
             ax[j] = xreal ? v : zero4;
         }
-        const uint32_t swg = sg4[m / 4][m % 4], swu = su4[m / 4][m % 4];
+        const uint32_t swg = s_gus[0][16 * w + r][m], swu = s_gus[1][16 * w + r][m];
         if constexpr (PACK) {
             vmi_f4 dg = zf, du = zf;
 #pragma unroll
@@ -894,7 +847,32 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
                 accu1[e] = fmaf(su1, du1[e], accu1[e]);
             }
         }
+        // the step's accumulators are settled here, so its MFMA results die
+        // here (the scale FMAs are not sunk past the loop, which would hold
+        // those results across it)
+        asm volatile("" : "+v"(accg[0]), "+v"(accg[1]), "+v"(accg[2]), "+v"(accg[3]));
+        asm volatile("" : "+v"(accu[0]), "+v"(accu[1]), "+v"(accu[2]), "+v"(accu[3]));
+        if constexpr (!PACK) {
+            asm volatile("" : "+v"(accg1[0]), "+v"(accg1[1]), "+v"(accg1[2]), "+v"(accg1[3]));
+            asm volatile("" : "+v"(accu1[0]), "+v"(accu1[1]), "+v"(accu1[2]), "+v"(accu1[3]));
+        }
+        // two blocks of the down strip into the registers this step freed
+        dw[2 * m] = vmi_bload_b64_nt(rdw, doff + 1024u * (uint32_t)m, 0);
+        dw[2 * m + 1] = vmi_bload_b64_nt(rdw, doff + 1024u * (uint32_t)m + 512u, 0);
+        // the strip's scales and biases straight into LDS (no registers held):
+        // copy i (wave i % 4) moves 16-byte units 64i..64i+63 of [scales, biases]
+        if (m == 0) {
+#pragma unroll
+            for (int i = w; i < NDMA; i += 4) {
+                const int u = 64 * i + lane, arr = u / H8, o = u - arr * H8;
+                vmi_lds_dma16_opaque_nt((arr ? md.b : md.s) + drow0 + 8 * o, &s_dsb[0][0] + 8 * 64 * i);
+            }
+        }
     }
+    // the copies were issued after the first two strip loads: with at most
+    // NBW - 2 operations outstanding they have landed (the barrier below then
+    // publishes them to every wave)
+    vmi_vm_wait_c<NBW - 2>();
     VMI_STAMP(1, 3);
     // affine-bias term: lane block q carries groups 2*NB*q + 2b, +1
     vmi_f4 bgd = zf, bud = zf;
@@ -926,363 +904,185 @@ __global__ __launch_bounds__(kThreads, 2) void k_gateup(GateUpArgs a) {
         }
     }
     __syncthreads();
-    // down-projection operands of this slice: bf16 activations, thread (t, kk)
-    // packs columns 8kk..8kk+7 in slot order {0,4,1,5,2,6,3,7}
-    // (vmi_unpack_u4_bf16_128); the slice's fp32 sum of those bf16 values
-    // feeds the affine-bias term
-    const int NGd = NC;
-    if (w < (T + 7) / 8) {
-        const int t = 8 * w + (lane >> 3), kk = lane & 7;
-        uint32_t hb[8];
-        float xs = 0.0f;
+    VMI_STAMP(1, 4);
+
+    // down: token r's 64 activations as bf16 B operands, and their sum X in
+    // column order (each lane its 16 columns, then across the lane blocks)
+    const bool tcol = r < T;
+    vmi_u4 b0, b1;
+    float X = 0.0f;
+    {
+        float av[16];
+        const float* ar = &s_act[tcol ? r : 0][16 * q];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            hb[i] = (t < T) ? vmi_f32_to_bf16(s_act[t][8 * kk + i]) : 0u;
-            xs += vmi_bf16_to_f32(hb[i]);
+        for (int i = 0; i < 16; ++i) av[i] = tcol ? ar[i] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            b0[i] = vmi_pack_bf16x2(av[i], av[i + 4]);
+            b1[i] = vmi_pack_bf16x2(av[8 + i], av[12 + i]);
         }
-        vmi_u4 op;
-        op[0] = hb[0] | (hb[4] << 16);
-        op[1] = hb[1] | (hb[5] << 16);
-        op[2] = hb[2] | (hb[6] << 16);
-        op[3] = hb[3] | (hb[7] << 16);
-        xs += __shfl_xor(xs, 1, VMI_WAVE);
-        xs += __shfl_xor(xs, 2, VMI_WAVE);
-        xs += __shfl_xor(xs, 4, VMI_WAVE);
-        if (t < T) {
-            a.actop[((size_t)aidx * T + t) * (I / 8) + 8 * c + kk] = op;
-            if (kk == 0) a.axs[((size_t)aidx * T + t) * NGd + c] = xs;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X += __uint_as_float(b0[i] << 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X += __uint_as_float(b0[i] & 0xffff0000u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X += __uint_as_float(b1[i] << 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) X += __uint_as_float(b1[i] & 0xffff0000u);
+    }
+    X += __shfl_xor(X, 16, VMI_WAVE);
+    X += __shfl_xor(X, 32, VMI_WAVE);
+    // the wave's rows' scale s and c = b - 128 s in fp32, into the x operand
+    // buffer (every wave is past the gate/up MFMAs): y = s D + c X, as
+    // s (D - 128 X) + b X for D = sum (128 + n) a
+    float* scw = reinterpret_cast<float*>(&s_x[0][0]);  // s [H], then c [H]
+    static_assert(sizeof(s_x) >= 2 * H * sizeof(float), "scales fit the operand buffer");
+#pragma unroll
+    for (int i = lane; i < RPW / 8; i += VMI_WAVE) {
+        const int h8 = RPW * w + 8 * i;
+        const vmi_u4 sv = *reinterpret_cast<const vmi_u4*>(&s_dsb[0][h8]);
+        const vmi_u4 bv = *reinterpret_cast<const vmi_u4*>(&s_dsb[1][h8]);
+        float sf[8], cf[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sf[2 * j] = __uint_as_float(sv[j] << 16);
+            sf[2 * j + 1] = __uint_as_float(sv[j] & 0xffff0000u);
+            cf[2 * j] = fmaf(-128.0f, sf[2 * j], __uint_as_float(bv[j] << 16));
+            cf[2 * j + 1] = fmaf(-128.0f, sf[2 * j + 1], __uint_as_float(bv[j] & 0xffff0000u));
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            *reinterpret_cast<float4*>(&scw[h8 + 4 * j]) = make_float4(sf[4 * j], sf[4 * j + 1], sf[4 * j + 2], sf[4 * j + 3]);
+            *reinterpret_cast<float4*>(&scw[H + h8 + 4 * j]) = make_float4(cf[4 * j], cf[4 * j + 1], cf[4 * j + 2], cf[4 * j + 3]);
         }
     }
-    VMI_STAMP(1, 4);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // after packing, lane (q, r) holds token rt = r % TB of block r / TB: its
+    // activation sum comes from lane (q, rt)
+    const int rt = r % TB, pi = r / TB;
+    const float Xp = __shfl(X, (lane & ~15) | rt, VMI_WAVE);
+    const bool store = rt < T && ((tmask >> rt) & 1u);
+    const float wt = store ? s_wt[rt] : 0.0f;
+    const int prow = store ? s_prow[rt] : 0;
+    // partial rows through a buffer resource: lanes without a row of theirs
+    // store past its range, so the loop has no branch and the blocks' MFMAs
+    // and arithmetic interleave
+    const __amdgpu_buffer_rsrc_t rpart =
+        vmi_rsrc(a.part, (uint32_t)((size_t)(a.ra.npairs + T) * NC * H * sizeof(float)));
+    const uint32_t pbase =
+        store ? (uint32_t)((((size_t)prow * NC + c) * H + RPW * w + 16 * pi + 4 * q) * sizeof(float)) : VMI_OOB;
+    // every block of the strip has landed before the first store (stores share
+    // the wave's vector-memory counter, so a wait for a later block inside the
+    // loop could also wait for stores)
+    vmi_vm_wait_c<0>();
+    VMI_STAMP(1, 7);
+    static_assert(NBW % PF == 0, "whole block packs");
+#pragma unroll
+    for (int bb = 0; bb < NBW; bb += PF) {
+        if (bb == NBW / 2) VMI_STAMP(1, 8);
+        vmi_f4 D[PF];
+#pragma unroll
+        for (int i = 0; i < PF; ++i) D[i] = vmi_mfma_bf16(vmi_unpack_u4_bf16_128(dw[bb + i].x), b0, zf);
+#pragma unroll
+        for (int i = 0; i < PF; ++i) D[i] = vmi_mfma_bf16(vmi_unpack_u4_bf16_128(dw[bb + i].y), b1, D[i]);
+        vmi_f4 E = D[0];
+        if constexpr (PF == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                E[e] = vmi_dpp_into<0x114, 0x2>(E[e], D[1][e]);  // row_shr:4 into lanes 4..7
+                E[e] = vmi_dpp_into<0x118, 0x4>(E[e], D[2][e]);  // row_shr:8 into lanes 8..11
+                E[e] = vmi_dpp_into<0x11C, 0x8>(E[e], D[3][e]);  // row_shr:12 into lanes 12..15
+            }
+        } else if constexpr (PF == 2) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) E[e] = vmi_dpp_into<0x118, 0xC>(E[e], D[1][e]);  // row_shr:8 into lanes 8..15
+        }
+        const int h = RPW * w + 16 * (bb + pi) + 4 * q;
+        const float4 sv = *reinterpret_cast<const float4*>(&scw[h]);
+        const float4 cv = *reinterpret_cast<const float4*>(&scw[H + h]);
+        vmi_u4 o;
+        o[0] = __float_as_uint(wt * fmaf(sv.x, E[0], cv.x * Xp));
+        o[1] = __float_as_uint(wt * fmaf(sv.y, E[1], cv.y * Xp));
+        o[2] = __float_as_uint(wt * fmaf(sv.z, E[2], cv.z * Xp));
+        o[3] = __float_as_uint(wt * fmaf(sv.w, E[3], cv.w * Xp));
+        vmi_bstore_b128(o, rpart, pbase, 64u * (uint32_t)bb);
+    }
+    VMI_STAMP(1, 6);
 }
 
-// --------------------------------------------------------- down + combine
-struct DownArgs {
-    int T, H, I, npairs, has_shared, has_sgate;
+// ------------------------------------------------------------- combine
+struct CombineArgs {
+    int T, H, NC, k, npairs, has_shared;
     const RouteInfo* route;
-    vmi_qmat down, sh_down;
-    const vmi_u4* actop;       // [npairs+1, T, I/8] bf16 operands
-    const float* axs;          // [npairs+1, T, I/64]
-    const float* sg_logit;     // [T] (has_sgate)
+    const float* part;         // [npairs + T, NC, H]
     const uint16_t* residual;  // [T, H] or nullptr
-    void* out;
-    int out_dtype;
+    uint16_t* out;             // [T, H] bf16
 };
 
-constexpr int kDnRows = 8;  // output rows per workgroup
-constexpr int kDnWaves = 8;
-constexpr int kDnThreads = kDnWaves * VMI_WAVE;
-constexpr int kDnRanks = kMaxK + 1;  // a token's routed ranks, then the shared expert
+constexpr int kCbRows = 8;  // output rows per combine workgroup
 
-// bf16 in the low (hi == false) or high half of a word as fp32, by one v_perm:
-// selector bytes 4..7 pick the word's bytes, 0x0C gives zero.
-__device__ __forceinline__ float bf16_half(uint32_t w, uint32_t sel) {
-    return __uint_as_float(__builtin_amdgcn_perm(w, 0u, sel));
-}
-
-// One workgroup (8 waves) per 8 output rows h0..h0+7 of the down projection,
-// over every expert of the batch: [shared (when present), distinct slots in
-// first-appearance order].  Wave w takes experts w, w+8, ... of a chunk of
-// 8 PW experts.  Loads, all into registers and in this order:
-//   1. the bf16 activation operands of its experts' tokens (one 16-byte load
-//      per lane and token row); the first chunk's are issued before the route
-//      is read, since an expert's activation block is found from its position
-//      in the list alone;
-//   2. once the slots are known, expert by expert: the 8 weight rows (8 rows x
-//      64 bytes per load), one dword per lane of the rows' scales and biases
-//      and of the activation group sums, combine weights and ranks.
-// The activations then go to the wave's NSLOT LDS slots (an expert past NSLOT
-// keeps its registers until a slot frees), which reorders them into MFMA
-// operand order; the weights stream meanwhile.  Loads complete in issue order, so the
-// compiler's counted waits then release the experts one after another while
-// the rest of the weights stream.
-//
-// MFMA mapping (v_mfma_f32_16x16x32_bf16, lane l = 16q + r, h = r >> 3):
-//   A (weights, exact bf16 128 + n): row r = weight row r & 7 in quantisation
-//     group 2m + h, lane block q holding words 2q + j of that group;
-//   B (activations): column r = token tb + (r & 7) at the same group and words.
-// Rows and columns 0..7 meet on the even group of pair step m and 8..15 on
-// the odd one; D[4q + e][r] is useful when (q >> 1) == h: weight row
-// 4(q & 1) + e, token tb + (r & 7), group 2m + h.  Per group
-//   y += s * (D - 128 X) + b * X,   X = sum of the token's activations in it,
-// accumulated over the even and the odd groups separately (lanes h = 0, 1),
-// each weighted by the combine weight into LDS by (token, rank, half); a
-// token's output adds its ranks in order, the shared expert last, so it does
-// not depend on the other tokens of the batch.
-//
-// TS: token rows per pass (4: T <= 4; 8: T <= 16 in passes of eight tokens).
-template <int NG, int TS, int PW, int NSLOT>
-__global__ __launch_bounds__(kDnThreads, 1) void k_down_rows(DownArgs a) {
-    constexpr int CAP = PW * kDnWaves;    // experts per chunk
-    constexpr int NM2 = (NG + 1) / 2;     // group pairs
-    constexpr int RB = NG * 32;           // bytes of one weight row (I / 2)
-    constexpr int RBA = NG * 128 + 16;    // LDS bytes of one token's activation operands (+ pad)
-    constexpr int TMAX = TS == 4 ? 4 : 16;
-    constexpr int SMW = TMAX * NG + 2 * TMAX;  // dwords of X [T][NG], weights [T], ranks [T]
-    constexpr int NSM = (SMW + 63) / 64;
-    constexpr int NA = (NG * 8 + 63) / 64;     // 16-byte loads per lane of one token row
-    static_assert(8 * NG <= 64, "scales + biases of 8 rows fit one dword per lane");
-    static_assert(PW >= NSLOT && PW <= 2 * NSLOT, "experts past the slots reuse the first slots once");
-    __shared__ __align__(16) uint8_t s_act[kDnWaves][NSLOT][TS * RBA];
-    __shared__ __align__(16) uint8_t s_zero[1024];
-    __shared__ __align__(16) uint32_t s_sb[kDnWaves][64];      // scales [8][NG] then biases [8][NG] (bf16)
-    __shared__ __align__(16) uint32_t s_sm[kDnWaves][NSM * 64];
-    __shared__ __align__(16) float s_pair[TMAX][kDnRanks][2][kDnRows];
-
-    const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
-    const int q = lane >> 4, r = lane & 15, h = r >> 3, rho = r & 7;
-    const int p = q >> 1;  // group parity of this lane's D rows
-    const bool useful = p == h;
-    const uint32_t sel = p ? 0x07060C0Cu : 0x05040C0Cu;
-    const int T = a.T, H = a.H, I8 = NG * 8;
-    const int h0 = blockIdx.x * kDnRows;
-    const int hs = a.has_shared;
-    const int k = a.npairs / T;
-    const int smw = T * NG + 2 * T;
-    const int npass = (T + 7) / 8;
-    const int NEmax = hs + a.npairs;
-    const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
+// One workgroup per 8 output rows h0..h0+7, the tiles of one XCD adjacent
+// (workgroup i sits on XCD i % 8 and takes tile (i % 8) * (tiles / 8) + i / 8),
+// so the 32-byte pieces of a partial row that neighbouring tiles read share
+// that XCD's L2 lines.  Per token, in a fixed order: every pair's slices
+// 0..NC-1, then the pairs in rank order (a pair without rows of its own - a
+// repeated or invalid slot - adds nothing), the shared expert last, then the
+// residual.  Nothing depends on the other tokens of the batch.
+__global__ __launch_bounds__(kThreads) void k_moe_combine(CombineArgs a) {
+    __shared__ float s_y[kMaxT][kMaxK + 1][kCbRows];
+    const int tid = threadIdx.x;
+    const int T = a.T, k = a.k, H = a.H, NC = a.NC;
+    const int per = H / kCbRows / 8;
+    const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    const int h0 = tile * kCbRows;
     VMI_STAMP(2, 0);
-    VMI_STAMP_HWID(2, 3);
-    // the arguments in SGPRs at once: one wait for the argument block rather
-    // than one per field read lazily under a branch
-    asm volatile("" ::"s"(a.route), "s"(a.down.w), "s"(a.down.s), "s"(a.down.b), "s"(a.sh_down.w), "s"(a.sh_down.s),
-                 "s"(a.sh_down.b), "s"(a.actop), "s"(a.axs), "s"(a.sg_logit), "s"(a.residual), "s"(a.out));
-    asm volatile("" ::"s"(a.I), "s"(a.has_sgate), "s"(a.out_dtype));
-
-    // activation operands of the wave's expert i (list position e), tokens
-    // tb..tb+tpass-1: lane l holds word l (+64c) of each token row
-    vmi_u4 av[PW][TS][NA];
-    auto load_act = [&](int i, int e, int tb, int tpass) {
-        const bool real = e < NEmax;
-        const int aidx = e < hs ? a.npairs : e - hs;
-        const __amdgpu_buffer_rsrc_t ra = vmi_rsrc(a.actop + (real ? ((size_t)aidx * T + tb) * I8 : 0),
-                                                   real ? (uint32_t)tpass * I8 * 16u : 0u);
-#pragma unroll
-        for (int t = 0; t < TS; ++t)
-#pragma unroll
-            for (int c = 0; c < NA; ++c)
-                av[i][t][c] = vmi_bload_b128(ra, (64 * c + lane < I8) ? (uint32_t)(t * I8 + 64 * c + lane) * 16u : VMI_OOB, 0);
-    };
-    auto store_act = [&](int i, int slot) {
-        uint8_t* al = &s_act[w][slot][0];
-#pragma unroll
-        for (int t = 0; t < TS; ++t)
-#pragma unroll
-            for (int c = 0; c < NA; ++c)
-                if (64 * c + lane < I8) *reinterpret_cast<vmi_u4*>(al + t * RBA + (64 * c + lane) * 16) = av[i][t][c];
-    };
-    // loads are kept in program order (compiler barriers between experts):
-    // they complete in issue order, which the expert loop relies on
-#pragma unroll
-    for (int i = 0; i < PW; ++i) {
-        load_act(i, w + kDnWaves * i, 0, min(T, TS));
-        asm volatile("" ::: "memory");
-    }
-    // residual bits (converted at the end)
-    const bool fin = tid < T * kDnRows;
+    const bool fin = tid < T * kCbRows;
     const uint32_t resid_bits =
         vmi_bload_b16(vmi_rsrc(a.residual, a.residual ? (uint32_t)T * H * 2u : 0u),
                       fin ? (uint32_t)((tid >> 3) * H + h0 + (tid & 7)) * 2u : VMI_OOB, 0);
-    // the route through the scalar cache (written by the previous kernel; the
-    // scalar cache starts empty in every kernel)
-    // (every address is inside the route record, so the loads are issued
-    // together and waited for once; the unused ones are discarded)
-    const int U = vmi_sload_i32(&a.route->U);
-    int slots0[PW];
+    const int nitem = T * (k + 1) * 2;
+    for (int i = tid; i < nitem; i += kThreads) {
+        const int half = i & 1, tj = i >> 1;
+        const int t = tj / (k + 1), j = tj - t * (k + 1);
+        const int p = j < k ? t * k + j : a.npairs + t;
+        // the flag and the partials load together (rows without a flag hold
+        // stale data, dropped below)
+        const int flag = j < k ? a.route->pv[p] : a.has_shared;
+        const float* src = a.part + (size_t)p * NC * H + h0 + 4 * half;
+        float4 v[kMaxInter / kSlice];
 #pragma unroll
-    for (int i = 0; i < PW; ++i) {
-        const int e = w + kDnWaves * i;
-        slots0[i] = vmi_sload_i32(&a.route->uslot[min(max(e - hs, 0), vmi::kRouteMaxPairs - 1)]);
-    }
+        for (int cc = 0; cc < kMaxInter / kSlice; ++cc)
+            if (cc < NC) v[cc] = *reinterpret_cast<const float4*>(src + (size_t)cc * H);
+        float4 y = v[0];
 #pragma unroll
-    for (int i = 0; i < PW; ++i) {
-        const int e = w + kDnWaves * i;
-        if (!(e >= hs && e < NEmax)) slots0[i] = 0;
-    }
-    for (int i = tid; i < TMAX * kDnRanks * 2 * kDnRows; i += kDnThreads) (&s_pair[0][0][0][0])[i] = 0.0f;
-    for (int i = tid; i < 1024 / 4; i += kDnThreads) reinterpret_cast<uint32_t*>(s_zero)[i] = 0u;
-    const int NE = hs + U;
-    __syncthreads();
-    VMI_STAMP(2, 1);
-
-    for (int c0 = 0; c0 < NE; c0 += CAP) {
-        const int nc = min(CAP, NE - c0);
-        const int n = nc > w ? (nc - w + kDnWaves - 1) / kDnWaves : 0;  // this wave's experts (uniform)
-        int slots[PW];
-#pragma unroll
-        for (int i = 0; i < PW; ++i) {
-            const int e = c0 + w + kDnWaves * i;
-            slots[i] = c0 == 0 ? slots0[i] : ((e >= hs && e < NE) ? vmi_sload_i32(&a.route->uslot[e - hs]) : 0);
-        }
-        auto expert = [&](int i) { return c0 + w + kDnWaves * i; };
-
-        for (int pass = 0; pass < npass; ++pass) {
-            const int tb = 8 * pass;
-            const int tpass = min(T - tb, TS);  // token rows of this pass
-            if (c0 > 0 || pass > 0) {
-#pragma unroll
-                for (int i = 0; i < PW; ++i) {
-                    load_act(i, expert(i), tb, tpass);
-                    asm volatile("" ::: "memory");
-                }
+        for (int cc = 1; cc < kMaxInter / kSlice; ++cc)
+            if (cc < NC) {
+                y.x += v[cc].x;
+                y.y += v[cc].y;
+                y.z += v[cc].z;
+                y.w += v[cc].w;
             }
-            // weights, scales/biases and small operands of every expert of the
-            // chunk, issued before the activations are waited for (loads
-            // complete in issue order, so that wait does not cover them); past
-            // the wave's experts the buffer ranges are empty and the dword loads
-            // read a valid dummy address, so every path issues the same loads and
-            // the compiler's counted waits stay exact
-            uint2 wts[PW][NM2];
-            uint32_t sbv[PW], smv[PW][NSM];
-#pragma unroll
-            for (int i = 0; i < PW; ++i) {
-                const bool real = i < n;
-                const int e = expert(i);
-                const bool sh = e < hs;
-                const int aidx = sh ? a.npairs : e - hs;
-                const vmi_qmat md = sh ? a.sh_down : a.down;
-                const int sj = slots[i];
-                const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(
-                    reinterpret_cast<const uint8_t*>(md.w) + (real ? ((size_t)sj * H + h0) * RB : 0), real ? 8u * RB : 0u);
-#pragma unroll
-                for (int m = 0; m < NM2; ++m) {
-                    const int g = 2 * m + h;
-                    wts[i][m] = vmi_bload_b64_nt(rw, g < NG ? (uint32_t)(rho * RB + g * 32 + 8 * q) : VMI_OOB, 0);
-                }
-                // one dword per lane: lane l < 4NG the scales' dword l, 4NG <= l <
-                // 8NG the biases' dword l - 4NG
-                const uint32_t* sbp = reinterpret_cast<const uint32_t*>(a.axs);
-                if (real && lane < 8 * NG)
-                    sbp = lane < 4 * NG ? reinterpret_cast<const uint32_t*>(md.s + ((size_t)sj * H + h0) * NG) + lane
-                                        : reinterpret_cast<const uint32_t*>(md.b + ((size_t)sj * H + h0) * NG) + (lane - 4 * NG);
-                sbv[i] = __builtin_nontemporal_load(sbp);
-                // X [T][NG], then the combine weights [T] and ranks [T] (the shared
-                // expert: gate logits, no ranks)
-#pragma unroll
-                for (int d = 0; d < NSM; ++d) {
-                    const int idx = 64 * d + lane;
-                    const uint32_t* sp = reinterpret_cast<const uint32_t*>(a.axs);
-                    if (real && idx < smw) {
-                        if (idx < T * NG) {
-                            sp = reinterpret_cast<const uint32_t*>(a.axs + (size_t)aidx * T * NG + idx);
-                        } else if (idx < T * NG + T) {
-                            if (!sh) sp = reinterpret_cast<const uint32_t*>(&a.route->wt[e - hs][idx - T * NG]);
-                            else if (a.has_sgate) sp = reinterpret_cast<const uint32_t*>(a.sg_logit + (idx - T * NG));
-                        } else if (!sh) {
-                            sp = reinterpret_cast<const uint32_t*>(&a.route->jr[e - hs][idx - T * NG - T]);
-                        }
-                    }
-                    smv[i][d] = *sp;
-                }
-                asm volatile("" ::: "memory");
-            }
-            // the activations landed first: into the LDS slots
-#pragma unroll
-            for (int i = 0; i < NSLOT; ++i) store_act(i, i);
-#pragma unroll
-            for (int i = 0; i < PW; ++i) {
-                if (i >= n) break;
-                const int slot = i % NSLOT;
-                if (i >= NSLOT) store_act(i, slot);  // expert i - NSLOT is done with this slot
-                const int e = expert(i);
-                const bool sh = e < hs;
-                // small operands through the wave's staging area, read back through
-                // the arrays' own type (uint32_t) so that no read can be moved
-                // ahead of these writes
-                s_sb[w][lane] = sbv[i];
-#pragma unroll
-                for (int d = 0; d < NSM; ++d) s_sm[w][64 * d + lane] = smv[i][d];
-                const uint32_t* sbl = &s_sb[w][0];
-                const uint32_t* sml = &s_sm[w][0];
-                const int tok = tb + rho;
-                const int tk = tok < T ? tok : 0;
-                const uint8_t* arow = (rho < tpass) ? &s_act[w][slot][rho * RBA] : s_zero;
-                float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int m = 0; m < NM2; ++m) {
-                    const int g = 2 * m + h;
-                    const uint8_t* ap = (g < NG) ? arow + (8 * g + 2 * q) * 16 : s_zero;
-                    const vmi_u4 a0 = *reinterpret_cast<const vmi_u4*>(ap);
-                    const vmi_u4 a1 = *reinterpret_cast<const vmi_u4*>(ap + 16);
-                    vmi_f4 D = vmi_mfma_bf16(vmi_unpack_u4_bf16_128(wts[i][m].x), a0, zf);
-                    D = vmi_mfma_bf16(vmi_unpack_u4_bf16_128(wts[i][m].y), a1, D);
-                    const int gp = 2 * m + p;
-                    if (gp < NG) {
-                        const float X = __uint_as_float(sml[tk * NG + gp]);
-#pragma unroll
-                        for (int ee = 0; ee < 4; ++ee) {
-                            const int row = 4 * (q & 1) + ee;
-                            float sv, bv;
-                            if constexpr (NG % 2 == 0) {
-                                sv = bf16_half(sbl[row * (NG / 2) + m], sel);
-                                bv = bf16_half(sbl[4 * NG + row * (NG / 2) + m], sel);
-                            } else {
-                                // bf16 element j of the scales (j < 8NG) or biases: word j / 2, half j & 1
-                                const int js = row * NG + gp, jb = 8 * NG + row * NG + gp;
-                                sv = bf16_half(sbl[js >> 1], (js & 1) ? 0x07060C0Cu : 0x05040C0Cu);
-                                bv = bf16_half(sbl[jb >> 1], (jb & 1) ? 0x07060C0Cu : 0x05040C0Cu);
-                            }
-                            y[ee] = fmaf(sv, fmaf(-128.0f, X, D[ee]), fmaf(bv, X, y[ee]));
-                        }
-                    }
-                }
-                if (useful && tok < T) {
-                    float wt;
-                    int rank;
-                    if (sh) {
-                        wt = a.has_sgate ? 1.0f / (1.0f + expf(-__uint_as_float(sml[T * NG + tok]))) : 1.0f;
-                        rank = k;
-                    } else {
-                        wt = __uint_as_float(sml[T * NG + tok]);
-                        rank = (int)sml[T * NG + T + tok];
-                    }
-                    if (rank >= 0) {
-                        float4 v;
-                        v.x = wt * y[0];
-                        v.y = wt * y[1];
-                        v.z = wt * y[2];
-                        v.w = wt * y[3];
-                        *reinterpret_cast<float4*>(&s_pair[tok][rank][h][4 * (q & 1)]) = v;
-                    }
-                }
-            }
-        }
+        if (!flag) y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        *reinterpret_cast<float4*>(&s_y[t][j][4 * half]) = y;
     }
     __syncthreads();
-    // each token's ranks in order (even + odd groups), the shared expert last,
-    // then the residual
     if (fin) {
         const int t = tid >> 3, rr = tid & 7;
         float acc = 0.0f;
-        for (int j = 0; j <= k; ++j) acc += s_pair[t][j][0][rr] + s_pair[t][j][1][rr];
+        for (int j = 0; j <= k; ++j) acc += s_y[t][j][rr];
         acc += vmi_bf16_to_f32(resid_bits);
-        const size_t o = (size_t)t * H + h0 + rr;
-        if (a.out_dtype == VMI_BF16)
-            reinterpret_cast<uint16_t*>(a.out)[o] = vmi_f32_to_bf16(acc);
-        else
-            reinterpret_cast<float*>(a.out)[o] = acc;
+        a.out[(size_t)t * H + h0 + rr] = vmi_f32_to_bf16(acc);
     }
-    VMI_STAMP(2, 2);
-}
-
-// --------------------------------------------------------------- prep (slots API)
-struct PrepArgs {
-    const void* x;
-    int T, H;
-    OperandOut ops;
-};
-
-template <typename XT, int CPL>
-__global__ __launch_bounds__(kThreads) void k_prep(PrepArgs a) {
-    const int t = blockIdx.x;
-    write_operands<XT, CPL>(reinterpret_cast<const XT*>(a.x) + (size_t)t * a.H, nullptr, 0.0f, a.H, t, a.ops);
+    VMI_STAMP(2, 1);
 }
 
 // ------------------------------------------------- fp32 operator path
-// vmi_fused_moe_slots / vmi_fused_moe_staged with f32 x keep the reference
-// operator's fp32 arithmetic (fused_moe.cpp:221-298: fp32 x, fp32 dequantised
-// weights, fp32 activations, reduce_pairs over j in order).  Each 16-byte
+// vmi_fused_moe_slots / vmi_fused_moe_staged keep the reference operator's
+// fp32 arithmetic (fused_moe.cpp:221-298: fp32 x - bf16 x is widened exactly
+// when staged, as the reference's caller casts it, native_moe.py:481 - fp32
+// dequantised weights, fp32 activations, reduce_pairs over j in order).  Each 16-byte
 // chunk of a weight row holds 32 columns of one quantisation group, so the
 // affine dequantisation q*s + b is factored out of the chunk's sum:
 //   sum_c (q_c s + b) x_c = s * sum_c q_c x_c + b * sum_c x_c,
@@ -1334,15 +1134,22 @@ __device__ __forceinline__ float dot32_u4_f32(const vmi_u4& wv, const float* xs)
 // Rows src + ridx[j] * LEN (j < kFTok, ridx < 0: zeros) into s[j] (chunk hg
 // at kFChunk * hg), then the fp32 sum of every 32-column chunk into sh[j].
 // All threads; ends synced.
-template <int LEN>
-__device__ __forceinline__ void stage_rows_f32(const float* __restrict__ src, const int (&ridx)[kFTok],
+__device__ __forceinline__ float4 load_f4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load_f4(const uint16_t* p) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                       __uint_as_float(v.y & 0xffff0000u));
+}
+
+template <int LEN, typename XT>
+__device__ __forceinline__ void stage_rows_f32(const XT* __restrict__ src, const int (&ridx)[kFTok],
                                                float (*s)[LEN / 32 * kFChunk], float (*sh)[LEN / 32]) {
     const int tid = threadIdx.x;
     __syncthreads();  // the previous chunk's readers are done
     for (int i = tid; i < kFTok * (LEN / 4); i += kThreads) {
         const int j = i / (LEN / 4), c4 = i - j * (LEN / 4);
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (ridx[j] >= 0) v = *reinterpret_cast<const float4*>(src + (size_t)ridx[j] * LEN + 4 * c4);
+        if (ridx[j] >= 0) v = load_f4(src + (size_t)ridx[j] * LEN + 4 * c4);
         *reinterpret_cast<float4*>(&s[j][kFChunk * (c4 >> 3) + 4 * (c4 & 7)]) = v;
     }
     __syncthreads();
@@ -1461,9 +1268,15 @@ __device__ __forceinline__ void load_row_f32(const vmi_qmat& m, int mat, int row
 // chunks of kFTok tokens.  act row t*k + j (j the token's first rank on the
 // slot) receives the token's activations.  The first workgroup publishes the
 // route and prow[p] = the activation/output row of pair p (-1: bad slot).
-template <int H>
-__global__ __launch_bounds__(kThreads) void k_gateup_f32(GateUpArgs a, const float* __restrict__ x,
+struct F32Args {
+    RouteArgs ra;
+    vmi_qmat gate, up;
+};
+
+template <int H, typename XT>
+__global__ __launch_bounds__(kThreads) void k_gateup_f32(F32Args fa, const XT* __restrict__ x,
                                                          float* __restrict__ act, int32_t* __restrict__ prow) {
+    const RouteArgs& a = fa.ra;
     using G = FRow<H>;
     __shared__ float s_x[kFTok][H / 32 * kFChunk];
     __shared__ float s_h[kFTok][H / 32];
@@ -1495,8 +1308,8 @@ __global__ __launch_bounds__(kThreads) void k_gateup_f32(GateUpArgs a, const flo
 
     vmi_u4 gw[G::NI], uw[G::NI];
     float gs[G::NI], gb[G::NI], us[G::NI], ub[G::NI];
-    load_row_f32<H>(a.gate, slot, I, row, part, gw, gs, gb);
-    load_row_f32<H>(a.up, slot, I, row, part, uw, us, ub);
+    load_row_f32<H>(fa.gate, slot, I, row, part, gw, gs, gb);
+    load_row_f32<H>(fa.up, slot, I, row, part, uw, us, ub);
 
     while (tmask) {  // uniform: chunks of up to kFTok of the slot's tokens
         int ridx[kFTok];
@@ -1505,7 +1318,7 @@ __global__ __launch_bounds__(kThreads) void k_gateup_f32(GateUpArgs a, const flo
             ridx[j] = tmask ? __builtin_ctz(tmask) : -1;
             tmask &= tmask ? tmask - 1u : 0u;
         }
-        stage_rows_f32<H>(x, ridx, s_x, s_h);
+        stage_rows_f32<H, XT>(x, ridx, s_x, s_h);
 #pragma unroll 1
         for (int j = 0; j < kFTok; ++j) {
             if (ridx[j] < 0) break;
@@ -1559,7 +1372,7 @@ __global__ __launch_bounds__(kThreads) void k_down_f32(const RouteInfo* __restri
         }
         if (n == 0) break;
         for (int j = n; j < kFTok; ++j) ridx[j] = orow[j] = -1;
-        stage_rows_f32<I>(act, ridx, s_a, s_h);
+        stage_rows_f32<I, float>(act, ridx, s_a, s_h);
 #pragma unroll 1
         for (int j = 0; j < kFTok; ++j) {
             if (orow[j] < 0) break;
@@ -1608,43 +1421,23 @@ int check_shape(int T, int k, int hidden, int inter, int group, int bits) {
     return VMI_OK;
 }
 
-template <bool PACK>
-hipError_t launch_gateup_t(const GateUpArgs& ga, int H, hipStream_t s) {
-    const int NC = ga.I / kSlice;
-    const dim3 grid((ga.has_shared ? NC : 0) + ga.npairs * NC);
+template <int TB>
+hipError_t launch_experts_t(const ExpertArgs& ea, int H, hipStream_t s) {
+    const int NC = ea.ra.I / kSlice;
+    const dim3 grid((ea.has_shared ? NC : 0) + ea.ra.npairs * NC);
     switch (H) {
-        case 512: hipLaunchKernelGGL((k_gateup<4, PACK>), grid, dim3(kThreads), 0, s, ga); break;
-        case 1024: hipLaunchKernelGGL((k_gateup<8, PACK>), grid, dim3(kThreads), 0, s, ga); break;
-        default: hipLaunchKernelGGL((k_gateup<16, PACK>), grid, dim3(kThreads), 0, s, ga); break;
+        case 512: hipLaunchKernelGGL((k_experts<4, TB>), grid, dim3(kThreads), 0, s, ea); break;
+        case 1024: hipLaunchKernelGGL((k_experts<8, TB>), grid, dim3(kThreads), 0, s, ea); break;
+        default: hipLaunchKernelGGL((k_experts<16, TB>), grid, dim3(kThreads), 0, s, ea); break;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_gateup(const GateUpArgs& ga, int H, hipStream_t s) {
-    return ga.T <= 8 ? launch_gateup_t<true>(ga, H, s) : launch_gateup_t<false>(ga, H, s);
-}
-
-template <int TS, int PW, int NSLOT>
-hipError_t launch_down_t(const DownArgs& da, hipStream_t s) {
-    const dim3 grid(da.H / kDnRows), block(kDnThreads);
-    switch (da.I / 64) {
-        case 1: hipLaunchKernelGGL((k_down_rows<1, TS, PW, NSLOT>), grid, block, 0, s, da); break;
-        case 2: hipLaunchKernelGGL((k_down_rows<2, TS, PW, NSLOT>), grid, block, 0, s, da); break;
-        case 3: hipLaunchKernelGGL((k_down_rows<3, TS, PW, NSLOT>), grid, block, 0, s, da); break;
-        case 4: hipLaunchKernelGGL((k_down_rows<4, TS, PW, NSLOT>), grid, block, 0, s, da); break;
-        case 5: hipLaunchKernelGGL((k_down_rows<5, TS, PW, NSLOT>), grid, block, 0, s, da); break;
-        case 6: hipLaunchKernelGGL((k_down_rows<6, TS, PW, NSLOT>), grid, block, 0, s, da); break;
-        case 7: hipLaunchKernelGGL((k_down_rows<7, TS, PW, NSLOT>), grid, block, 0, s, da); break;
-        default: hipLaunchKernelGGL((k_down_rows<8, TS, PW, NSLOT>), grid, block, 0, s, da); break;
-    }
-    return hipGetLastError();
-}
-
-// T <= 4: token rows of four, 5 experts a wave (40 per chunk) over 4 LDS
-// slots; larger batches: passes of eight tokens, 2 experts a wave.
-hipError_t launch_down(const DownArgs& da, hipStream_t s) {
-    if (da.T <= 4) return launch_down_t<4, 5, 4>(da, s);
-    return launch_down_t<8, 2, 2>(da, s);
+// token blocks of 4, 8 or 16: the batch's tokens fill that many MFMA columns
+hipError_t launch_experts(const ExpertArgs& ea, int H, hipStream_t s) {
+    if (ea.ra.T <= 4) return launch_experts_t<4>(ea, H, s);
+    if (ea.ra.T <= 8) return launch_experts_t<8>(ea, H, s);
+    return launch_experts_t<16>(ea, H, s);
 }
 
 // Workspace of the fp32 operator path: the status word and route table at the
@@ -1683,14 +1476,15 @@ void launch_down_f32_t(const F32Workspace& ws, vmi_qmat down, int T, int k, int 
     hipLaunchKernelGGL((k_down_f32<I>), grid, dim3(kThreads), 0, s, ws.route, down, T, k, H, ws.act, ws.y);
 }
 
-hipError_t launch_moe_f32(const GateUpArgs& ga, const float* x, vmi_qmat down, int H, const F32Workspace& ws,
+template <typename XT>
+hipError_t launch_moe_f32(const F32Args& fa, const XT* x, vmi_qmat down, int H, const F32Workspace& ws,
                           void* out, int out_dtype, hipStream_t s) {
-    const int T = ga.T, k = ga.k, I = ga.I;
+    const int T = fa.ra.T, k = fa.ra.k, I = fa.ra.I;
     const dim3 ggrid(T * k * (I / FRow<512>::RPB));
     switch (H) {
-        case 512: hipLaunchKernelGGL((k_gateup_f32<512>), ggrid, dim3(kThreads), 0, s, ga, x, ws.act, ws.prow); break;
-        case 1024: hipLaunchKernelGGL((k_gateup_f32<1024>), ggrid, dim3(kThreads), 0, s, ga, x, ws.act, ws.prow); break;
-        default: hipLaunchKernelGGL((k_gateup_f32<2048>), ggrid, dim3(kThreads), 0, s, ga, x, ws.act, ws.prow); break;
+        case 512: hipLaunchKernelGGL((k_gateup_f32<512, XT>), ggrid, dim3(kThreads), 0, s, fa, x, ws.act, ws.prow); break;
+        case 1024: hipLaunchKernelGGL((k_gateup_f32<1024, XT>), ggrid, dim3(kThreads), 0, s, fa, x, ws.act, ws.prow); break;
+        default: hipLaunchKernelGGL((k_gateup_f32<2048, XT>), ggrid, dim3(kThreads), 0, s, fa, x, ws.act, ws.prow); break;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1707,18 +1501,8 @@ hipError_t launch_moe_f32(const GateUpArgs& ga, const float* x, vmi_qmat down, i
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_combine_f32, dim3((T * H + kThreads - 1) / kThreads), dim3(kThreads), 0, s, ws.prow,
-                       ga.in_scores, ws.y, T, k, H, out, out_dtype);
+                       fa.ra.in_scores, ws.y, T, k, H, out, out_dtype);
     return hipGetLastError();
-}
-
-template <typename XT>
-void launch_prep(const PrepArgs& pa, hipStream_t s) {
-    const dim3 grid(pa.T);
-    switch (pa.H) {
-        case 512: hipLaunchKernelGGL((k_prep<XT, 8>), grid, dim3(kThreads), 0, s, pa); break;
-        case 1024: hipLaunchKernelGGL((k_prep<XT, 16>), grid, dim3(kThreads), 0, s, pa); break;
-        default: hipLaunchKernelGGL((k_prep<XT, 32>), grid, dim3(kThreads), 0, s, pa); break;
-    }
 }
 
 }  // namespace
@@ -1734,7 +1518,7 @@ MoeWorkspace carve_workspace(void* base, int T, int k, int hidden, int inter, in
         off += align256(n);
         return r;
     };
-    const size_t nact = (size_t)T * k + 1;  // distinct slots + the shared expert
+    const size_t nrows = (size_t)T * k + T;  // one partial row set per pair, then the shared expert's per token
     w.status = reinterpret_cast<uint32_t*>(take(256));
     w.route = reinterpret_cast<RouteInfo*>(take(sizeof(RouteInfo)));
     w.logits = reinterpret_cast<float*>(take(sizeof(float) * (size_t)T * (num_experts > 0 ? num_experts : 1)));
@@ -1742,8 +1526,7 @@ MoeWorkspace carve_workspace(void* base, int T, int k, int hidden, int inter, in
     w.xop = reinterpret_cast<vmi_u4*>(take(sizeof(uint16_t) * (size_t)T * hidden));
     w.xsum = reinterpret_cast<float*>(take(sizeof(float) * (size_t)T * (hidden / 64)));
     w.fscale = reinterpret_cast<float*>(take(sizeof(float) * (size_t)T));
-    w.actop = reinterpret_cast<vmi_u4*>(take(sizeof(uint16_t) * nact * T * inter));
-    w.axs = reinterpret_cast<float*>(take(sizeof(float) * nact * T * (inter / 64)));
+    w.part = reinterpret_cast<float*>(take(sizeof(float) * nrows * (inter / 64) * hidden));
     w.bytes = off;
     return w;
 }
@@ -1752,9 +1535,7 @@ MoeWorkspace carve_workspace(void* base, int T, int k, int hidden, int inter, in
 
 extern "C" size_t vmi_fused_moe_slots_workspace_bytes(int T, int k, int hidden, int inter) {
     if (T <= 0 || k <= 0 || hidden <= 0 || inter <= 0) return 0;
-    const size_t b16 = vmi::carve_workspace(nullptr, T, k, hidden, inter, 0).bytes;
-    const size_t f32 = carve_f32(nullptr, T, k, hidden, inter).bytes;
-    return b16 > f32 ? b16 : f32;
+    return carve_f32(nullptr, T, k, hidden, inter).bytes;
 }
 
 extern "C" size_t vmi_moe_layer_workspace_bytes(int T, int top_k, int hidden, int inter, int num_experts) {
@@ -1785,48 +1566,19 @@ int fused_moe_pairs(const void* x, int x_dtype, bool staged, const int32_t* loca
     if (!workspace || workspace_bytes < need)
         return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", need, workspace_bytes);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (x_dtype == VMI_F32) {
-        // the reference operator's fp32 arithmetic throughout
-        const F32Workspace fw = carve_f32(workspace, T, k, hidden, inter);
-        GateUpArgs ga{};
-        ga.T = T; ga.I = inter; ga.k = k; ga.E = 0; ga.npairs = T * k; ga.has_shared = 0;
-        ga.from_slots = 1; ga.norm = 1; ga.cap = cap;
-        ga.slots = local_slots; ga.in_scores = scores;
-        ga.gate = gate; ga.up = up; ga.sh_gate = gate; ga.sh_up = up;
-        ga.route = fw.route; ga.status = fw.status;
-        const hipError_t e = launch_moe_f32(ga, static_cast<const float*>(x), down, hidden, fw, out, out_dtype, s);
-        if (e != hipSuccess) return vmi::hip_fail(e, "fp32 MoE launch");
-        return VMI_OK;
-    }
-    const vmi::MoeWorkspace ws = vmi::carve_workspace(workspace, T, k, hidden, inter, 0);
-    const OperandOut ops{ws.xop, ws.xsum, ws.fscale};
-
-    const PrepArgs pa{x, T, hidden, ops};
-    if (x_dtype == VMI_BF16)
-        launch_prep<uint16_t>(pa, s);
-    else
-        launch_prep<float>(pa, s);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return vmi::hip_fail(e, "k_prep launch");
-
-    GateUpArgs ga{};
-    ga.T = T; ga.I = inter; ga.k = k; ga.E = 0; ga.npairs = T * k; ga.has_shared = 0;
-    ga.from_slots = 1; ga.norm = 1; ga.cap = cap;
-    ga.slots = local_slots; ga.in_scores = scores;
-    ga.gate = gate; ga.up = up; ga.sh_gate = gate; ga.sh_up = up;
-    ga.xop = ws.xop; ga.xsum = ws.xsum; ga.fscale = ws.fscale;
-    ga.route = ws.route; ga.status = ws.status;
-    ga.actop = ws.actop; ga.axs = ws.axs;
-    e = launch_gateup(ga, hidden, s);
-    if (e != hipSuccess) return vmi::hip_fail(e, "k_gateup launch");
-
-    DownArgs da{};
-    da.T = T; da.H = hidden; da.I = inter; da.npairs = T * k; da.has_shared = 0; da.has_sgate = 0;
-    da.route = ws.route; da.down = down; da.sh_down = down;
-    da.actop = ws.actop; da.axs = ws.axs;
-    da.residual = nullptr; da.out = out; da.out_dtype = out_dtype;
-    e = launch_down(da, s);
-    if (e != hipSuccess) return vmi::hip_fail(e, "k_down_rows launch");
+    // the reference operator's fp32 arithmetic for either x dtype
+    const F32Workspace fw = carve_f32(workspace, T, k, hidden, inter);
+    F32Args fa{};
+    fa.ra.T = T; fa.ra.I = inter; fa.ra.k = k; fa.ra.E = 0; fa.ra.npairs = T * k;
+    fa.ra.from_slots = 1; fa.ra.norm = 1; fa.ra.cap = cap;
+    fa.ra.slots = local_slots; fa.ra.in_scores = scores;
+    fa.ra.route = fw.route; fa.ra.status = fw.status;
+    fa.gate = gate; fa.up = up;
+    const hipError_t e =
+        x_dtype == VMI_F32
+            ? launch_moe_f32(fa, static_cast<const float*>(x), down, hidden, fw, out, out_dtype, s)
+            : launch_moe_f32(fa, static_cast<const uint16_t*>(x), down, hidden, fw, out, out_dtype, s);
+    if (e != hipSuccess) return vmi::hip_fail(e, "fp32 MoE launch");
     return VMI_OK;
 }
 
@@ -1906,27 +1658,28 @@ int launch_moe_layer(const vmi_moe_layer_desc& D, const uint16_t* x, int T, cons
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return vmi::hip_fail(e, "k_router launch");
 
-    GateUpArgs ga{};
-    ga.T = T; ga.I = D.inter; ga.k = D.top_k; ga.E = D.num_experts; ga.npairs = T * D.top_k;
-    ga.has_shared = has_shared; ga.from_slots = 0; ga.norm = D.norm_topk_prob; ga.cap = D.cap;
-    ga.logits = ws.logits; ga.table = D.slot_table;
-    ga.gate = D.gate; ga.up = D.up;
-    ga.sh_gate = has_shared ? D.shared_gate : D.gate;
-    ga.sh_up = has_shared ? D.shared_up : D.up;
-    ga.xop = ws.xop; ga.xsum = ws.xsum; ga.fscale = ws.fscale;
-    ga.route = ws.route; ga.status = ws.status; ga.ids_out = ids_out; ga.scores_out = scores_out;
-    ga.actop = ws.actop; ga.axs = ws.axs;
-    e = launch_gateup(ga, D.hidden, s);
-    if (e != hipSuccess) return vmi::hip_fail(e, "k_gateup launch");
+    ExpertArgs ea{};
+    ea.ra.T = T; ea.ra.I = D.inter; ea.ra.k = D.top_k; ea.ra.E = D.num_experts; ea.ra.npairs = T * D.top_k;
+    ea.ra.from_slots = 0; ea.ra.norm = D.norm_topk_prob; ea.ra.cap = D.cap;
+    ea.ra.logits = ws.logits; ea.ra.table = D.slot_table;
+    ea.ra.route = ws.route; ea.ra.status = ws.status; ea.ra.ids_out = ids_out; ea.ra.scores_out = scores_out;
+    ea.has_shared = has_shared; ea.has_sgate = has_sgate;
+    ea.gate = D.gate; ea.up = D.up; ea.down = D.down;
+    ea.sh_gate = has_shared ? D.shared_gate : D.gate;
+    ea.sh_up = has_shared ? D.shared_up : D.up;
+    ea.sh_down = has_shared ? D.shared_down : D.down;
+    ea.xop = ws.xop; ea.xsum = ws.xsum; ea.fscale = ws.fscale; ea.sg_logit = ws.sg_logit;
+    ea.part = ws.part;
+    e = launch_experts(ea, D.hidden, s);
+    if (e != hipSuccess) return vmi::hip_fail(e, "k_experts launch");
 
-    DownArgs da{};
-    da.T = T; da.H = D.hidden; da.I = D.inter; da.npairs = T * D.top_k;
-    da.has_shared = has_shared; da.has_sgate = has_sgate;
-    da.route = ws.route; da.down = D.down; da.sh_down = has_shared ? D.shared_down : D.down;
-    da.actop = ws.actop; da.axs = ws.axs; da.sg_logit = ws.sg_logit;
-    da.residual = residual; da.out = out; da.out_dtype = VMI_BF16;
-    e = launch_down(da, s);
-    if (e != hipSuccess) return vmi::hip_fail(e, "k_down_rows launch");
+    CombineArgs ca{};
+    ca.T = T; ca.H = D.hidden; ca.NC = D.inter / kSlice; ca.k = D.top_k; ca.npairs = T * D.top_k;
+    ca.has_shared = has_shared;
+    ca.route = ws.route; ca.part = ws.part; ca.residual = residual; ca.out = out;
+    hipLaunchKernelGGL(k_moe_combine, dim3(D.hidden / kCbRows), dim3(kThreads), 0, s, ca);
+    e = hipGetLastError();
+    if (e != hipSuccess) return vmi::hip_fail(e, "k_moe_combine launch");
     return VMI_OK;
 }
 
@@ -1934,7 +1687,7 @@ int launch_moe_layer(const vmi_moe_layer_desc& D, const uint16_t* x, int T, cons
 // process ends.  Host code never passes the array's name to a kernel (on the
 // host it is a stand-in, not a device address): every use goes through the
 // per-device address from hipGetSymbolAddress.
-constexpr size_t kNoAllocScratchBytes = (size_t)3 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
 constexpr int kMaxDevices = 64;
 __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 std::mutex g_scratch_mu;

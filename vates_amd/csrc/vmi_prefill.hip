@@ -56,7 +56,7 @@ struct PfArgs {
     vmi_qmat router;            // [E, H]
     const float* logit_bias;    // [E] or null
     const int32_t* table;       // [E] or null
-    vmi_qmat gate, up, down;    // [cap, ...]
+    vmi_qmat gate, up, down;    // [cap, ...]: gate/up words MFMA-major, down group-major [cap, I/64, H, 8 words]
     vmi_qmat sh_gate, sh_up, sh_down, sgate;
     // workspace
     vmi_u4* xop4;               // [T, H/8] fp16 operands, 4-bit slot order
@@ -550,14 +550,17 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         asrc[j] = a.xop4 + (size_t)s_tok[arow] * HW + c;
         const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
         const int mt = brow >> 8, rr = min(n0 + (brow & 255), I - 1);
-        bsrc[j] = (mt ? Um.w : Gm.w) + (mrow0 + rr) * HW + 4 * h;
+        // MFMA-major pool: the 16 bytes of group g, half h of row rr sit in
+        // block (rr / 16, g / 2) at lane 16 (2 (g % 2) + h) + rr % 16
+        bsrc[j] = (mt ? Um.w : Gm.w) + mrow0 * HW + (size_t)(rr >> 4) * (H / 128) * 256 + 64 * h + 4 * (rr & 15);
     }
     auto issue = [&](int g, int u) {
         uint8_t* A = s_ring + u * (kPfA + kB);
 #pragma unroll
         for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
 #pragma unroll
-        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(bsrc[j] + 8 * g, A + kPfA + 16 * (kPf8Threads * j + 64 * w));
+        for (int j = 0; j < 2; ++j)
+            vmi_lds_dma16_opaque(bsrc[j] + 256 * (g >> 1) + 128 * (g & 1), A + kPfA + 16 * (kPf8Threads * j + 64 * w));
     };
     vmi_f4 acc[4][4][2];
 #pragma unroll
@@ -779,41 +782,39 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     const int I = a.I, IW = I / 8, G = I / 64;
     const int h0 = nb * 512;
     const vmi_qmat Dm = tl.x >= 0 ? a.down : a.sh_down;
-    const size_t mrow0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)a.H + h0;
+    // the down projection is group-major: row h of group g of slot m at
+    // (m * G + g) * H + h (32 bytes of words; one bf16 scale and bias)
+    const size_t mbase = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)G * a.H + h0;
     if (tid < kTM3) s_route[tid] = tile_route(a, tl, tid);
     const int G8 = (G + 7) & ~7;
-    if ((G & 7) == 0) {
-        // all loads first, then the stores (one memory latency, not one per iteration)
-        constexpr int kIt = (2 * 512 * (MAXG / 8) + kPf8Threads - 1) / kPf8Threads;
-        const int n16 = 2 * 512 * (G / 8);
+    {
+        // 16-byte pieces = 8 consecutive rows of one group; groups G..G8-1 are
+        // zero.  All loads first, then the stores (one memory latency).
+        constexpr int kIt = (2 * 64 * MAXG + kPf8Threads - 1) / kPf8Threads;
+        const int n16 = 2 * 64 * G8;
         uint4 v[kIt];
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
             const int i = tid + kPf8Threads * it;
-            if (i < n16) {
-                const int c = i % (G / 8), row = (i / (G / 8)) % 512, sb = i / (G / 8 * 512);
-                v[it] = *reinterpret_cast<const uint4*>((sb ? Dm.b : Dm.s) + (mrow0 + row) * G + 8 * c);
-            }
+            const int r8 = i % 64, g = (i / 64) % G8, sb = i / (64 * G8);
+            v[it] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < n16 && g < G)
+                v[it] = *reinterpret_cast<const uint4*>((sb ? Dm.b : Dm.s) + mbase + (size_t)g * a.H + 8 * r8);
         }
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
             const int i = tid + kPf8Threads * it;
             if (i < n16) {
-                const int c = i % (G / 8), row = (i / (G / 8)) % 512, sb = i / (G / 8 * 512);
-                uint16_t* dst = sb ? &s_b16[row][8 * c] : &s_s16[row][8 * c];
+                const int r8 = i % 64, g = (i / 64) % G8, sb = i / (64 * G8);
                 const uint32_t wv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    dst[2 * j] = (uint16_t)(wv[j] & 0xffffu);
-                    dst[2 * j + 1] = (uint16_t)(wv[j] >> 16);
+                    uint16_t* d0 = sb ? &s_b16[8 * r8 + 2 * j][g] : &s_s16[8 * r8 + 2 * j][g];
+                    uint16_t* d1 = sb ? &s_b16[8 * r8 + 2 * j + 1][g] : &s_s16[8 * r8 + 2 * j + 1][g];
+                    *d0 = (uint16_t)(wv[j] & 0xffffu);
+                    *d1 = (uint16_t)(wv[j] >> 16);
                 }
             }
-        }
-    } else {
-        for (int i = tid; i < 512 * G8; i += kPf8Threads) {
-            const int g = i % G8, row = i / G8;
-            s_s16[row][g] = g < G ? Dm.s[(mrow0 + row) * G + g] : (uint16_t)0;
-            s_b16[row][g] = g < G ? Dm.b[(mrow0 + row) * G + g] : (uint16_t)0;
         }
     }
     __syncthreads();
@@ -845,14 +846,15 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         const int rt = s_route[arow];
         asrc[j] = a.actop + (size_t)(rt >= 0 ? rt : 0) * IW + c;
         const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
-        bsrc[j] = Dm.w + (mrow0 + brow) * IW + 4 * h;
+        bsrc[j] = Dm.w + (mbase + brow) * 8 + 4 * h;
     }
     auto issue = [&](int g, int u) {
         uint8_t* A = s_ring + u * (kPfA + kB);
 #pragma unroll
         for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
 #pragma unroll
-        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(bsrc[j] + 8 * g, A + kPfA + 16 * (kPf8Threads * j + 64 * w));
+        for (int j = 0; j < 2; ++j)
+            vmi_lds_dma16_opaque(bsrc[j] + (size_t)g * a.H * 8, A + kPfA + 16 * (kPf8Threads * j + 64 * w));
     };
     vmi_f4 acc[4][8];
 #pragma unroll

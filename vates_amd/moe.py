@@ -7,7 +7,7 @@
 * ``MoELayer`` is the analogue of ``FileStreamingMoeBlock.__call__``
   (mlx_streaming/core/moe/block.py:245-1013, production branch): router,
   softmax/top-k/renorm, expert->slot table, SwiGLU experts, weighted combine
-  and the sigmoid-gated shared expert, in four HIP kernels.
+  and the sigmoid-gated shared expert, in three HIP kernels.
 
 Tensors live on the current HIP device (torch "cuda" device on ROCm).  Every
 call is asynchronous on ``torch.cuda.current_stream()`` unless a stream is
@@ -77,6 +77,40 @@ class QuantizedProj:
         _require(self.weight, f"{name}.weight", 4, device)
         _require(self.scales, f"{name}.scales", 2, device)
         _require(self.biases, f"{name}.biases", 2, device)
+
+
+def down_group_major(p: QuantizedProj, group: int = 64, bits: int = 4) -> QuantizedProj:
+    """A down-projection stack [n, hidden, inter*bits/32] (the reference's pool
+    layout) re-laid group-major for ``MoELayer``: words [n, inter/group, hidden,
+    group*bits/32], scales and biases [n, inter/group, hidden].  Quantisation
+    group g of row h is then contiguous with group g of rows h+1, h+2, ...:
+    the verify kernel projects one group's activations through that strip,
+    and the prefill kernel streams the strip of each group in turn."""
+    n, rows, words = p.weight.shape
+    wpg = group * bits // 32
+    G = words // wpg
+    if G * wpg != words or tuple(p.scales.shape) != (n, rows, G) or tuple(p.biases.shape) != (n, rows, G):
+        raise VmiError(f"down stack shapes {tuple(p.weight.shape)}/{tuple(p.scales.shape)} do not match group={group}")
+    w = p.weight.view(n, rows, G, wpg).permute(0, 2, 1, 3).contiguous()
+    s = p.scales.permute(0, 2, 1).contiguous()
+    b = p.biases.permute(0, 2, 1).contiguous()
+    return QuantizedProj(w, s, b)
+
+
+def gateup_mfma_major(p: QuantizedProj, group: int = 64, bits: int = 4) -> QuantizedProj:
+    """A gate or up stack [n, inter, hidden*bits/32] re-laid in the operand
+    order of the verify kernel's MFMAs: words [n, inter/64, 4, hidden/128, 64,
+    4], where block (c, w, m) holds, for lane l = 16 q + r, the 16 bytes at
+    byte 64 m + 16 q of row 64 c + 16 w + r.  One wave's load of a block is
+    then 1 KB of contiguous memory, and a 64-row slice of the intermediate
+    dimension is one contiguous run.  Scales and biases keep their layout."""
+    if bits != 4 or group != 64:
+        raise VmiError(f"the MFMA-major layout is built for bits=4 group=64 (got {bits}, {group})")
+    n, rows, words = p.weight.shape
+    if rows % 64 or words % 16:
+        raise VmiError(f"gate/up stack shape {tuple(p.weight.shape)} needs inter % 64 == 0 and hidden % 128 == 0")
+    w = p.weight.view(n, rows // 64, 4, 16, words // 16, 4, 4).permute(0, 1, 2, 4, 5, 3, 6).contiguous()
+    return QuantizedProj(w.view(n, rows, words), p.scales, p.biases)
 
 
 def _fused_moe_pairs(x: torch.Tensor, local_slots: Optional[torch.Tensor], scores: torch.Tensor, k: int,
@@ -172,6 +206,10 @@ class MoELayer:
     maps each of ``num_experts`` router outputs to its slot.  With
     ``norm_weight`` the layer applies the decoder's pre-MoE RMSNorm to its
     input first (the residual passed to ``__call__`` is added unnormalised).
+
+    The stacks are given in the reference's pool layout; the layer keeps its
+    own copies in the layouts its kernels read: gate and up in MFMA operand
+    order (``gateup_mfma_major``), down group-major (``down_group_major``).
     """
 
     def __init__(self, router: QuantizedProj, gate: QuantizedProj, up: QuantizedProj, down: QuantizedProj, *,
@@ -209,6 +247,12 @@ class MoELayer:
             if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != self.hidden:
                 raise VmiError("norm_weight must be bf16 [hidden]")
             _require(norm_weight, "norm_weight", 2, device)
+        gate, up = gateup_mfma_major(gate, group, bits), gateup_mfma_major(up, group, bits)
+        down = down_group_major(down, group, bits)
+        if has_shared:
+            shared_gate = gateup_mfma_major(shared_gate, group, bits)
+            shared_up = gateup_mfma_major(shared_up, group, bits)
+            shared_down = down_group_major(shared_down, group, bits)
         # keep every tensor alive: the descriptor stores raw pointers
         self._keep = (router, gate, up, down, shared_gate, shared_up, shared_down, shared_expert_gate, slot_table,
                       router_logit_bias, norm_weight)
