@@ -42,19 +42,23 @@ def gdn_dict(layer, eps: float = 1e-6) -> dict:
 
 
 def moe_dict(moe) -> dict:
-    """vates_amd.moe.MoELayer -> oracle.moe_layer's dict."""
-    mw = moe._keep
+    """vates_amd.moe.MoELayer -> oracle.moe_layer's dict (expert stacks taken
+    back to the reference's pool layout: the layer stores them re-laid)."""
+    mw = moe.reference_weights()
     d = moe.desc
     L = {"H": d.hidden, "I": d.inter, "E": d.num_experts, "k": d.top_k, "group": 64, "norm": int(d.norm_topk_prob),
          "router_bits": d.router_bits, "bits": 4, "cap": moe.cap, "sg_bits": d.shared_expert_gate_bits}
-    L["router_w"], L["router_s"], L["router_b"] = u32(mw[0].weight), u16(mw[0].scales), u16(mw[0].biases)
-    for key, p in (("gate", mw[1]), ("up", mw[2]), ("down", mw[3]), ("sh_gate", mw[4]), ("sh_up", mw[5]),
-                   ("sh_down", mw[6])):
+    r = mw["router"]
+    L["router_w"], L["router_s"], L["router_b"] = u32(r.weight), u16(r.scales), u16(r.biases)
+    for key, name in (("gate", "gate"), ("up", "up"), ("down", "down"), ("sh_gate", "shared_gate"),
+                      ("sh_up", "shared_up"), ("sh_down", "shared_down")):
+        p = mw[name]
         L[key + "_w"], L[key + "_s"], L[key + "_b"] = u32(p.weight), u16(p.scales), u16(p.biases)
-    L["sg_w"], L["sg_s"], L["sg_b"] = u32(mw[7].weight), u16(mw[7].scales), u16(mw[7].biases)
-    L["table"] = None if mw[8] is None else mw[8].cpu().numpy()
-    L["bias"] = None if mw[9] is None else mw[9].cpu().numpy()
-    L["norm_w"] = None if mw[10] is None else u16(mw[10])
+    sg = mw["shared_expert_gate"]
+    L["sg_w"], L["sg_s"], L["sg_b"] = u32(sg.weight), u16(sg.scales), u16(sg.biases)
+    L["table"] = None if mw["slot_table"] is None else mw["slot_table"].cpu().numpy()
+    L["bias"] = None if mw["router_logit_bias"] is None else mw["router_logit_bias"].cpu().numpy()
+    L["norm_w"] = None if mw["norm_weight"] is None else u16(mw["norm_weight"])
     L["norm_eps"] = float(d.norm_eps)
     return L
 

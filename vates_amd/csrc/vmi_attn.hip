@@ -124,8 +124,7 @@ __global__ __launch_bounds__(kAThreads) void k_rms_rows(RmsArgs a) {
         uint32_t o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            o[i] = (uint32_t)vmi_f32_to_bf16((f[2 * i] * inv) * g[2 * i]) |
-                   ((uint32_t)vmi_f32_to_bf16((f[2 * i + 1] * inv) * g[2 * i + 1]) << 16);
+            o[i] = vmi_pack_bf16x2((f[2 * i] * inv) * g[2 * i], (f[2 * i + 1] * inv) * g[2 * i + 1]);
         *reinterpret_cast<uint4*>(orow + 8 * v) = make_uint4(o[0], o[1], o[2], o[3]);
     }
 }
@@ -849,7 +848,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
         for (int i = 0; i < 2; ++i) {
             const float y0 = (den > 0.0f ? n[2 * i] / den : 0.0f) / (1.0f + expf(-gp[2 * i]));
             const float y1 = (den > 0.0f ? n[2 * i + 1] / den : 0.0f) / (1.0f + expf(-gp[2 * i + 1]));
-            out[i] = (uint32_t)vmi_f32_to_bf16(y0) | ((uint32_t)vmi_f32_to_bf16(y1) << 16);
+            out[i] = vmi_pack_bf16x2(y0, y1);
         }
         *reinterpret_cast<uint2*>(a.o + ((size_t)t * a.n_heads + h) * kHeadDim + d0) = make_uint2(out[0], out[1]);
     }
@@ -1033,8 +1032,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
                 uint32_t o[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    o[e] = (uint32_t)vmi_f32_to_bf16((f[2 * e] * inv) * g[2 * e]) |
-                           ((uint32_t)vmi_f32_to_bf16((f[2 * e + 1] * inv) * g[2 * e + 1]) << 16);
+                    o[e] = vmi_pack_bf16x2((f[2 * e] * inv) * g[2 * e], (f[2 * e + 1] * inv) * g[2 * e + 1]);
                 s_xn[i] = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }

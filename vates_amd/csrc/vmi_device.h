@@ -61,12 +61,13 @@ __device__ __forceinline__ uint32_t vmi_pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, vmi_bf2));
 }
 
-// Round-to-nearest-even fp32 -> bf16 bit pattern (quiet NaN kept).
+// Round-to-nearest-even fp32 -> bf16 bit pattern (quiet NaN kept), branch
+// free: the NaN case is a select, so a wave never splits on it.
 __device__ __forceinline__ uint16_t vmi_f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t qnan = (u >> 16) | 0x40u;
+    return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? qnan : rne);
 }
 
 __device__ __forceinline__ uint32_t vmi_h2_bits(_Float16 lo, _Float16 hi) {
@@ -483,6 +484,11 @@ __device__ __forceinline__ vmi_u4 vmi_bload_b128_coh(__amdgpu_buffer_rsrc_t r, u
 // resource's range) stores nothing, so a predicated store needs no branch.
 __device__ __forceinline__ void vmi_bstore_b128(const vmi_u4& v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)voff, (int)soff, 0);
+}
+// Nontemporal form, for data the next kernel reads once.
+__device__ __forceinline__ void vmi_bstore_b128_nt(const vmi_u4& v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                   uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)voff, (int)soff, 2);
 }
 __device__ __forceinline__ uint32_t vmi_bload_b16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);

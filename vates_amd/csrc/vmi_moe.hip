@@ -125,7 +125,7 @@ struct RouterArgs {
     const float* bias;
     vmi_qmat sgate;
     int sgbits, has_sgate;
-    int row_wgs;      // row groups (four rows each) per token
+    int row_wgs;      // row groups (four waves of kRouterRows rows each) per token
     float* logits;    // [T, E]
     float* sg_logit;  // [T]
     OperandOut ops;
@@ -178,21 +178,31 @@ __device__ __forceinline__ void operands_from_wave(const uint4 (&xr)[NCH], int H
 }
 
 // Router rows for one token per workgroup: workgroup i covers row group b
-// (wave w takes row 4b + w) for token t, where the T workgroups of a row group
-// sit on one XCD (workgroups are dealt to the 8 XCDs round-robin by index), so
-// the rows' weights reach that XCD's L2 once.  Row E is the shared-expert
-// gate; row E + has_sgate (the row groups always cover it) writes token t's
-// MFMA operands instead of a logit.
+// (wave w takes rows RW (4b + w) .. + RW - 1) for token t, where the T
+// workgroups of a row group sit on one XCD (workgroups are dealt to the 8
+// XCDs round-robin by index), so the rows' weights reach that XCD's L2 once.
+// Row E is the shared-expert gate; the wave whose first row is the first
+// multiple of RW at or past E + has_sgate (the row groups always cover it)
+// writes token t's MFMA operands instead of logits.
 // Each wave loads token t's input with lane l owning columns
 // [l*CPL, (l+1)*CPL): the canonical inverse rms, the bf16-rounded normalised
-// input, then fmaf(w, x, acc) in column order; the 64 partials meet in the
-// canonical wave-sum tree.  No LDS and no barrier: a wave depends on nothing
-// but its own loads.  The CPU oracle reproduces this order bit for bit
-// (orc_router_logits_f32).
+// input (once for its RW rows), then per row fmaf(w, x, acc) in column
+// order; the 64 partials meet in the canonical wave-sum tree.  No LDS and no
+// barrier: a wave depends on nothing but its own loads.  The CPU oracle
+// reproduces this order bit for bit (orc_router_logits_f32).
+constexpr int kRouterRows = 2;  // router rows per wave
+
 template <int CPL>
 __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     constexpr int NCH = CPL / 8;  // packed 8-column chunks per lane
+    constexpr int RW = kRouterRows;
     VMI_STAMP(0, 0);
+    // every argument in SGPRs at once: one scalar round trip for the argument
+    // block, not one per field as the code first needs it
+    asm volatile("" ::"s"(a.x), "s"(a.norm_w), "s"(a.eps), "s"(a.T), "s"(a.H), "s"(a.E), "s"(a.router.w),
+                 "s"(a.router.s), "s"(a.router.b), "s"(a.rbits), "s"(a.bias));
+    asm volatile("" ::"s"(a.sgate.w), "s"(a.sgate.s), "s"(a.sgate.b), "s"(a.sgbits), "s"(a.has_sgate),
+                 "s"(a.row_wgs), "s"(a.logits), "s"(a.sg_logit), "s"(a.ops.xop), "s"(a.ops.xsum), "s"(a.ops.fscale));
     const int lane = threadIdx.x & 63, w = vmi_wave_id();
     const int T = a.T, H = a.H;
     const int G = H / 64;
@@ -200,17 +210,13 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     const int t = jb % T, b = (jb / T) * 8 + xcd;
     if (b >= a.row_wgs) return;
     const int c0 = lane * CPL;
-    const int row = b * (kThreads / VMI_WAVE) + w;
+    const int row0 = RW * (b * (kThreads / VMI_WAVE) + w);
     const int nrows = a.E + a.has_sgate;
-    const bool row_ok = row < nrows;
-    const bool is_ops = row == nrows;
-    const bool is_sg = row_ok && row >= a.E;  // wave-uniform
-    if (!row_ok && !is_ops) return;
-    const vmi_qmat m = is_sg ? a.sgate : a.router;
-    const int bits = is_sg ? a.sgbits : a.rbits;
-    const int r = is_sg ? 0 : (row_ok ? row : 0);
+    const int ops_row = RW * ((nrows + RW - 1) / RW);
+    const bool is_ops = row0 == ops_row;
+    if (row0 >= nrows && !is_ops) return;
     // the input and the norm weights first (the normalisation needs them),
-    // then the router row; loads retire in issue order
+    // then the router rows; loads retire in issue order
     const __amdgpu_buffer_rsrc_t rx = vmi_rsrc(a.x + (size_t)t * H, (uint32_t)H * 2u);
     const __amdgpu_buffer_rsrc_t rn = vmi_rsrc(a.norm_w ? a.norm_w : a.x, a.norm_w ? (uint32_t)H * 2u : 0u);
     uint4 xr[NCH], nwv[NCH];
@@ -222,39 +228,50 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
         nwv[ch] = make_uint4(nv[0], nv[1], nv[2], nv[3]);
     }
     asm volatile("" ::: "memory");
-    // weights: 8-bit -> CPL/4 words, 4-bit -> CPL/8 words of this lane's columns
-    const uint32_t row_words = (uint32_t)(H * bits / 32);
-    const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(m.w + (size_t)r * row_words, row_ok ? row_words * 4u : 0u);
-    const __amdgpu_buffer_rsrc_t rs = vmi_rsrc(m.s + (size_t)r * G, row_ok ? (uint32_t)G * 2u : 0u);
-    const __amdgpu_buffer_rsrc_t rb = vmi_rsrc(m.b + (size_t)r * G, row_ok ? (uint32_t)G * 2u : 0u);
-    const uint32_t wbase = (uint32_t)(c0 * bits / 32) * 4u;
-    const int nwords = CPL * bits / 32;  // words of this lane's columns: 1, 2, 4 or 8 (wave-uniform)
-    uint32_t wword[CPL / 4];
+    // each row's words (8-bit: CPL/4 words of this lane's columns, 4-bit:
+    // CPL/8), its scale and bias, and its logit bias, by the same loads for
+    // either width (an 8-bit share is CPL/16 16-byte pieces; a 4-bit share
+    // uses the first CPL/32 of them, the rest reads past it unused; single
+    // words where 16-byte pieces would not stay aligned): no branch, so no
+    // wait for loads in flight ahead of them
+    uint32_t wword[RW][CPL / 4], sv[RW], bv[RW];
+    float rbias[RW];
+    bool row_ok[RW], is_sg[RW];
+    int bitsr[RW];
 #pragma unroll
-    for (int i = 0; i < CPL / 4; ++i) wword[i] = 0u;
-    if (nwords >= 4) {
+    for (int j = 0; j < RW; ++j) {
+        const int row = row0 + j;
+        row_ok[j] = row < nrows;
+        is_sg[j] = row_ok[j] && row >= a.E;  // wave-uniform
+        const vmi_qmat m = is_sg[j] ? a.sgate : a.router;
+        const int bits = is_sg[j] ? a.sgbits : a.rbits;
+        bitsr[j] = bits;
+        const int r = is_sg[j] ? 0 : (row_ok[j] ? row : 0);
+        const uint32_t row_words = (uint32_t)(H * bits / 32);
+        const __amdgpu_buffer_rsrc_t rw = vmi_rsrc(m.w + (size_t)r * row_words, row_ok[j] ? row_words * 4u : 0u);
+        const __amdgpu_buffer_rsrc_t rs = vmi_rsrc(m.s + (size_t)r * G, row_ok[j] ? (uint32_t)G * 2u : 0u);
+        const __amdgpu_buffer_rsrc_t rb = vmi_rsrc(m.b + (size_t)r * G, row_ok[j] ? (uint32_t)G * 2u : 0u);
+        const uint32_t wbase = (uint32_t)(c0 * bits / 32) * 4u;
+        if constexpr (CPL >= 32) {
+            vmi_u4 wq[CPL / 16];
 #pragma unroll
-        for (int i = 0; i < (CPL / 16 > 0 ? CPL / 16 : 1); ++i) {
-            const vmi_u4 q = vmi_bload_b128_nt(rw, (4 * i < nwords) ? wbase + 16u * i : VMI_OOB, 0);
+            for (int i = 0; i < CPL / 16; ++i) wq[i] = vmi_bload_b128_nt(rw, wbase + 16u * i, 0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (4 * i + j < CPL / 4) wword[4 * i + j] = q[j];
+            for (int i = 0; i < CPL / 4; ++i) wword[j][i] = wq[i / 4][i % 4];
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPL / 4; ++i) wword[j][i] = vmi_bload_b32_nt(rw, wbase + 4u * i, 0);
         }
-    } else if (nwords == 2) {
-        const uint2 q = vmi_bload_b64_nt(rw, wbase, 0);
-        wword[0] = q.x;
-        wword[1] = q.y;
-    } else {
-        wword[0] = vmi_bload_b32_nt(rw, wbase, 0);
+        sv[j] = vmi_bload_b16(rs, (uint32_t)(c0 / 64) * 2u, 0);
+        bv[j] = vmi_bload_b16(rb, (uint32_t)(c0 / 64) * 2u, 0);
+        const bool has_bias = a.bias != nullptr && row_ok[j] && !is_sg[j];
+        rbias[j] = __uint_as_float(vmi_bload_b32(
+            vmi_rsrc(has_bias ? a.bias : a.logits, has_bias ? 4u * (uint32_t)a.E : 0u), 4u * (uint32_t)r, 0));
     }
-    const uint32_t sv = vmi_bload_b16(rs, (uint32_t)(c0 / 64) * 2u, 0);
-    const uint32_t bv = vmi_bload_b16(rb, (uint32_t)(c0 / 64) * 2u, 0);
-    // the logit bias of this row, needed last, issued last
-    const bool has_bias = a.bias != nullptr && row_ok && !is_sg;
-    const float rbias = __uint_as_float(
-        vmi_bload_b32(vmi_rsrc(has_bias ? a.bias : a.logits, has_bias ? 4u * (uint32_t)a.E : 0u), 4u * (uint32_t)r, 0));
+    VMI_STAMP(0, 2);
     if (a.norm_w) {
         const float inv = canonical_inv_rms<NCH>(xr, H, a.eps);
+        VMI_STAMP(0, 3);
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) {
             float xf[8], nw[8];
@@ -263,8 +280,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
             uint32_t pk[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                pk[i] = (uint32_t)vmi_f32_to_bf16((xf[2 * i] * inv) * nw[2 * i]) |
-                        ((uint32_t)vmi_f32_to_bf16((xf[2 * i + 1] * inv) * nw[2 * i + 1]) << 16);
+                pk[i] = vmi_pack_bf16x2((xf[2 * i] * inv) * nw[2 * i], (xf[2 * i + 1] * inv) * nw[2 * i + 1]);
             xr[ch] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         }
     }
@@ -272,29 +288,35 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
         operands_from_wave<NCH>(xr, H, t, a.ops);
         return;
     }
-    // dequantised weights (w = q*s + b is exact in fp32), one fmaf chain in column order
-    const float sc = vmi_bf16_to_f32(sv), bi = vmi_bf16_to_f32(bv);
-    float acc = 0.0f;
+    VMI_STAMP(0, 4);
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        float xf[8];
-        unpack_bf16x8(xr[ch], xf);
+    for (int j = 0; j < RW; ++j) {
+        if (!row_ok[j]) continue;  // wave-uniform
+        // dequantised weights (w = q*s + b is exact in fp32), one fmaf chain in column order
+        const float sc = vmi_bf16_to_f32(sv[j]), bi = vmi_bf16_to_f32(bv[j]);
+        const int bits = bitsr[j];
+        float acc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = 8 * ch + i;
-            const uint32_t qv = (bits == 4) ? (wword[c / 8] >> (4 * (c % 8))) & 15u
-                                            : (wword[c / 4] >> (8 * (c % 4))) & 255u;
-            acc = fmaf(fmaf((float)qv, sc, bi), xf[i], acc);
+        for (int ch = 0; ch < NCH; ++ch) {
+            float xf[8];
+            unpack_bf16x8(xr[ch], xf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = 8 * ch + i;
+                const uint32_t qv = (bits == 4) ? (wword[j][c / 8] >> (4 * (c % 8))) & 15u
+                                                : (wword[j][c / 4] >> (8 * (c % 4))) & 255u;
+                acc = fmaf(fmaf((float)qv, sc, bi), xf[i], acc);
+            }
         }
-    }
-    const float v = vmi_wave_sum_canon(acc);
-    if (lane == 0) {
-        if (is_sg) {
-            a.sg_logit[t] = v;
-        } else {
-            float lv = v;
-            if (has_bias) lv = lv + rbias;
-            a.logits[(size_t)t * a.E + row] = lv;
+        const float v = vmi_wave_sum_canon(acc);
+        if (lane == 0) {
+            if (is_sg[j]) {
+                a.sg_logit[t] = v;
+            } else {
+                float lv = v;
+                if (a.bias != nullptr) lv = lv + rbias[j];
+                a.logits[(size_t)t * a.E + row0 + j] = lv;
+            }
         }
     }
     VMI_STAMP(0, 1);
@@ -344,6 +366,8 @@ __device__ void topk_token(const float (&v)[NI], int E, int k, int norm, int t, 
         const uint64_t kk = topk_rank_key(v[i], lane + 64 * i);
         key[i] = (i < nreal) ? kk : 0ull;
     }
+    asm volatile("" ::"v"(key[NI - 1]));
+    VMI_STAMP(1, 9);
 #pragma unroll
     for (int size = 2; size <= NI; size *= 2)
 #pragma unroll
@@ -357,31 +381,32 @@ __device__ void topk_token(const float (&v)[NI], int E, int k, int norm, int t, 
     // the lane holding it (a ballot names it; equal values fall back to the
     // full (value, index) key) writes its expert and value into the round's
     // entry itself, so no key is broadcast
+    // round j's winner goes to lane j's registers (its index word and value
+    // key read from the winning lane), so the loop has no LDS traffic
+    uint32_t my_lo = 0u, my_hv = 0u;
 #pragma unroll 1
     for (int j = 0; j < k; ++j) {
         const uint32_t hv = (uint32_t)(key[0] >> 32);
         const uint32_t Mv = vmi_wave_max_u32(hv);
         const uint64_t cand = __ballot(hv == Mv);
-        bool win;
-        if (__popcll(cand) == 1) {
-            win = hv == Mv;
-        } else {
+        uint64_t winm = cand;
+        if (__popcll(cand) != 1) {
             const uint64_t M = vmi_wave_max_u64(hv == Mv ? key[0] : 0ull);
-            win = key[0] == M;
+            winm = __ballot(key[0] == M);
         }
-        if (win) {
-            R.ids[t * k + j] = (int)(0xffffffffu - (uint32_t)key[0]);
-            R.scores[t * k + j] = vmi_order_key_value(hv);
+        const int wl = __builtin_ctzll(winm);  // uniform
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key[0], wl);
+        my_lo = lane == j ? lo : my_lo;
+        my_hv = lane == j ? Mv : my_hv;
+        if (lane == wl) {
 #pragma unroll
             for (int i = 0; i + 1 < NI; ++i) key[i] = key[i + 1];
             key[NI - 1] = 0ull;
         }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int my_idx = lane < k ? R.ids[t * k + lane] : 0;
-    const float my_val = lane < k ? R.scores[t * k + lane] : 0.0f;
+    VMI_STAMP(1, 10);
+    const int my_idx = lane < k ? (int)(0xffffffffu - my_lo) : 0;
+    const float my_val = lane < k ? vmi_order_key_value(my_hv) : 0.0f;
     const float mx = vmi_readlane_f32(my_val, 0);
     const bool sel = lane < k;
     const bool bad = __ballot(sel && !(fabsf(my_val) < 3.0e38f)) != 0;
@@ -514,6 +539,44 @@ struct RouteArgs {
     float* scores_out;            // [T*k] or nullptr
 };
 
+// Slot table and first-appearance distinct slots of a batch of at most 64
+// pairs by one wave (lane p: pair p), after the top-k: the same result as the
+// workgroup-wide path below (a slot's distinct index is the number of
+// distinct slots whose first pair comes earlier), with wave-level ordering of
+// the LDS table instead of workgroup barriers.
+__device__ void slots_dedup_wave(const RouteArgs& a, RouteLds& R, const int32_t* s_table, int32_t* s_first) {
+    const int lane = threadIdx.x & 63;
+    const int npairs = a.npairs, k = a.k;
+    const bool pair = lane < npairs;
+    int sl = -1;
+    if (pair) {
+        const int id = R.ids[lane];
+        sl = (id >= 0 && id < a.E) ? (a.table ? s_table[id] : id) : -1;
+        if (sl < 0 || sl >= a.cap) {
+            sl = -1;
+            atomicOr(&R.bad, VMI_STATUS_BAD_SLOT);
+        }
+        R.slot[lane] = sl;
+        R.umask[lane] = 0u;
+        if (sl >= 0) s_first[sl] = 0x7fffffff;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (sl >= 0) atomicMin(&s_first[sl], lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int fidx = sl >= 0 ? s_first[sl] : -1;
+    const uint64_t bal = __ballot(sl >= 0 && fidx == lane);
+    if (sl >= 0) {
+        const int u = __popcll(bal & ((1ull << fidx) - 1ull));  // distinct index of the pair's slot
+        if (fidx == lane) R.uslot[u] = sl;
+        atomicOr(&R.umask[u], 1u << (lane / k));
+    }
+    if (lane == 0) R.U = __popcll(bal);
+}
+
 // Routing of the batch from the router logits inside one workgroup (all
 // threads): top-k per token, slot table, first-appearance distinct slots.
 __device__ void route_batch(const RouteArgs& a, RouteLds& R, int32_t* s_table, int32_t* s_first) {
@@ -523,6 +586,12 @@ __device__ void route_batch(const RouteArgs& a, RouteLds& R, int32_t* s_table, i
     route_topk_dispatch(a.logits, T, a.E, k, a.norm, a.table, s_table, R);
     __syncthreads();
     VMI_STAMP(1, 1);
+    if (npairs <= VMI_WAVE && a.cap <= kFirstTable) {
+        if (tid < VMI_WAVE) slots_dedup_wave(a, R, s_table, s_first);
+        __syncthreads();
+        VMI_STAMP(1, 2);
+        return;
+    }
     if (tid < npairs) {
         const int id = R.ids[tid];
         int sl = (id >= 0 && id < a.E) ? (a.table ? s_table[id] : id) : -1;
@@ -603,9 +672,12 @@ struct ExpertArgs {
     float* part;                  // [npairs + T, I/64, H] weighted partial rows
 };
 
-// One workgroup (4 waves) per item = blockIdx.x: items [0, NC) are the shared
-// expert's slices (when present), then distinct slot u's slices c at
-// nsh + u*NC + c.  Workgroups past the batch's item count exit after routing.
+// One workgroup (4 waves) per item = blockIdx.x = u*NC + c: distinct slot u's
+// slice c for u < U, the shared expert's slices at u = U (when present);
+// workgroups past those exit after routing.  Every workgroup routes first:
+// a CU then never holds one workgroup streaming weights while another waits
+// for its router logits behind them (a CU returns loads in issue order, and
+// workgroup 256 + j shares the CU of workgroup j).
 //
 // Gate/up: wave w owns rows c*64 + 16w + (lane % 16) of gate and up; lane
 // block q = lane/16 loads 16 bytes at 64m + 16q of its row for m = 0..NM-1
@@ -655,12 +727,19 @@ __global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArg
     const int tid = threadIdx.x, lane = tid & 63, w = vmi_wave_id();
     const int q = lane >> 4, r = lane & 15;
     const int T = a.ra.T, I = a.ra.I, k = a.ra.k, NC = I / kSlice;
-    const int nsh = a.has_shared ? NC : 0;
     const int item = blockIdx.x;
-    const bool is_shared = item < nsh;
     const vmi_u4 zero4 = {0u, 0u, 0u, 0u};
     VMI_STAMP(1, 0);
     VMI_STAMP_HWID(1, 5);
+    // every argument in SGPRs at once (one scalar round trip)
+    asm volatile("" ::"s"(a.ra.T), "s"(a.ra.I), "s"(a.ra.k), "s"(a.ra.E), "s"(a.ra.npairs), "s"(a.ra.norm),
+                 "s"(a.ra.cap), "s"(a.ra.logits), "s"(a.ra.table), "s"(a.ra.route), "s"(a.ra.status));
+    asm volatile("" ::"s"(a.ra.ids_out), "s"(a.ra.scores_out), "s"(a.has_shared), "s"(a.has_sgate), "s"(a.gate.w),
+                 "s"(a.gate.s), "s"(a.gate.b), "s"(a.up.w), "s"(a.up.s), "s"(a.up.b));
+    asm volatile("" ::"s"(a.sh_gate.w), "s"(a.sh_gate.s), "s"(a.sh_gate.b), "s"(a.sh_up.w), "s"(a.sh_up.s),
+                 "s"(a.sh_up.b), "s"(a.down.w), "s"(a.down.s), "s"(a.down.b), "s"(a.sh_down.w));
+    asm volatile("" ::"s"(a.sh_down.s), "s"(a.sh_down.b), "s"(a.xop), "s"(a.xsum), "s"(a.fscale), "s"(a.sg_logit),
+                 "s"(a.part));
 
     // the MoE input operands do not depend on the routing: issued before it,
     // so their latency overlaps the router logits'
@@ -676,19 +755,16 @@ __global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArg
     const uint32_t fsr = vmi_bload_b32(vmi_rsrc(a.fscale, (uint32_t)T * 4u), (uint32_t)tid * 4u, 0);
     const uint32_t sgr = vmi_bload_b32(vmi_rsrc(a.sg_logit, a.has_sgate ? (uint32_t)T * 4u : 0u), (uint32_t)tid * 4u, 0);
 
-    int slot = 0, c = item;
-    uint32_t tmask = (1u << T) - 1u;
-    if (!is_shared) {
-        route_batch(a.ra, R, s_table, s_first);
-        const int ii = item - nsh, u = ii / NC;
-        if (u >= vmi_uniform(R.U)) {
-            if (item == nsh) publish_route(a.ra, R);  // no routed item at all
-            return;
-        }
-        c = ii - u * NC;
-        slot = vmi_uniform(R.uslot[u]);
-        tmask = (uint32_t)vmi_uniform((int)R.umask[u]);
+    route_batch(a.ra, R, s_table, s_first);
+    const int u = item / NC, c = item - u * NC;
+    const int U = vmi_uniform(R.U);
+    const bool is_shared = u == U;
+    if (u > U || (is_shared && !a.has_shared)) {
+        if (item == 0) publish_route(a.ra, R);  // no item to compute at all
+        return;
     }
+    const int slot = is_shared ? 0 : vmi_uniform(R.uslot[u]);
+    const uint32_t tmask = is_shared ? (1u << T) - 1u : (uint32_t)vmi_uniform((int)R.umask[u]);
 
     // every gate/up weight load of the item (scales, biases, words by m):
     // loads retire in issue order, so everything the arithmetic needs first is
@@ -752,8 +828,8 @@ __global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArg
     const uint32_t doff = (uint32_t)(RPW * w + r) * 32u + 8u * (uint32_t)q;
     uint2 dw[NBW];
 
-    // the first routed workgroup publishes the route while its weights stream
-    if (item == nsh && !is_shared) publish_route(a.ra, R);
+    // the first workgroup publishes the route while its weights stream
+    if (item == 0) publish_route(a.ra, R);
     // partial row and combine weight of each token: a routed token's first
     // pair on this slot and the sum of its pairs' scores there; the shared
     // expert's rows follow the pairs, weighted by its sigmoid gate
@@ -792,13 +868,26 @@ __global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArg
     vmi_vm_wait_c<2 + 2 * NM>();
     __syncthreads();
 
+    // affine-bias term first: its inputs (the x group sums and the bias words,
+    // loaded ahead of every weight word) are already here, so it runs while
+    // the weights stream rather than after them.  Lane block q carries groups
+    // 2*NB*q + 2b, +1.
+    const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
+    vmi_f4 bgd = zf, bud = zf;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int g0 = 2 * NB * q + 2 * b;
+        const vmi_u4 ab = (r < T) ? vmi_bias_a_operand(s_xs[r][g0], s_xs[r][g0 + 1]) : zero4;
+        bgd = vmi_mfma_bf16(ab, vmi_bias_b_operand(bgw[b]), bgd);
+        bud = vmi_mfma_bf16(ab, vmi_bias_b_operand(buw[b]), bud);
+    }
+
     // main MFMAs: m-th load pair covers groups 2m (K blocks 0-1) and 2m+1 (2-3)
     const int par = lane >> 5;  // PACK: D rows 8..15 (lanes 32..63) hold the odd group
     float accg[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     // without PACK the odd groups accumulate apart and meet the even ones at the
     // end, as the two lane halves do with PACK: the same rounding for every T
     float accg1[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accu1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const vmi_f4 zf = {0.0f, 0.0f, 0.0f, 0.0f};
     const int tk = PACK ? (r & 7) : r;
     const bool xreal = PACK ? (((q < 2) == (r < 8)) && tk < T) : (r < T);
     const int tkc = tk < T ? tk : 0;
@@ -874,15 +963,6 @@ __global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArg
     // publishes them to every wave)
     vmi_vm_wait_c<NBW - 2>();
     VMI_STAMP(1, 3);
-    // affine-bias term: lane block q carries groups 2*NB*q + 2b, +1
-    vmi_f4 bgd = zf, bud = zf;
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        const int g0 = 2 * NB * q + 2 * b;
-        const vmi_u4 ab = (r < T) ? vmi_bias_a_operand(s_xs[r][g0], s_xs[r][g0 + 1]) : zero4;
-        bgd = vmi_mfma_bf16(ab, vmi_bias_b_operand(bgw[b]), bgd);
-        bud = vmi_mfma_bf16(ab, vmi_bias_b_operand(buw[b]), bud);
-    }
     // SwiGLU of token t = 4*(lane/16) + e, row 16w + r of the slice
     const int tq = lane >> 4;
 #pragma unroll
@@ -973,10 +1053,8 @@ __global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArg
         vmi_rsrc(a.part, (uint32_t)((size_t)(a.ra.npairs + T) * NC * H * sizeof(float)));
     const uint32_t pbase =
         store ? (uint32_t)((((size_t)prow * NC + c) * H + RPW * w + 16 * pi + 4 * q) * sizeof(float)) : VMI_OOB;
-    // every block of the strip has landed before the first store (stores share
-    // the wave's vector-memory counter, so a wait for a later block inside the
-    // loop could also wait for stores)
-    vmi_vm_wait_c<0>();
+    // (the strip's loads were all issued before the first store, so the counted
+    // wait for a block never waits for a store)
     VMI_STAMP(1, 7);
     static_assert(NBW % PF == 0, "whole block packs");
 #pragma unroll
@@ -1038,34 +1116,53 @@ __global__ __launch_bounds__(kThreads) void k_moe_combine(CombineArgs a) {
     const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
     const int h0 = tile * kCbRows;
     VMI_STAMP(2, 0);
+    asm volatile("" ::"s"(a.T), "s"(a.H), "s"(a.NC), "s"(a.k), "s"(a.npairs), "s"(a.has_shared), "s"(a.route),
+                 "s"(a.part), "s"(a.residual), "s"(a.out));
     const bool fin = tid < T * kCbRows;
     const uint32_t resid_bits =
         vmi_bload_b16(vmi_rsrc(a.residual, a.residual ? (uint32_t)T * H * 2u : 0u),
                       fin ? (uint32_t)((tid >> 3) * H + h0 + (tid & 7)) * 2u : VMI_OOB, 0);
+    // every item's flag and slices through buffer resources (slices past NC
+    // and items past the batch read nothing), all requested before any wait;
+    // T * (k + 1) * 2 <= 2 (160 + 16) items fit two passes of the workgroup
     const int nitem = T * (k + 1) * 2;
-    for (int i = tid; i < nitem; i += kThreads) {
-        const int half = i & 1, tj = i >> 1;
-        const int t = tj / (k + 1), j = tj - t * (k + 1);
+    const __amdgpu_buffer_rsrc_t rp = vmi_rsrc(a.part, (uint32_t)((size_t)(a.npairs + T) * NC * H * sizeof(float)));
+    const __amdgpu_buffer_rsrc_t rf = vmi_rsrc(a.route->pv, (uint32_t)a.npairs * 4u);
+    constexpr int MC = kMaxInter / kSlice;
+    vmi_u4 v[2][MC];
+    uint32_t flag[2];
+    int tj[2];
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int i = tid + kThreads * it;
+        const bool ok = i < nitem;
+        const int half = i & 1;
+        tj[it] = ok ? i >> 1 : 0;
+        const int t = tj[it] / (k + 1), j = tj[it] - t * (k + 1);
         const int p = j < k ? t * k + j : a.npairs + t;
-        // the flag and the partials load together (rows without a flag hold
-        // stale data, dropped below)
-        const int flag = j < k ? a.route->pv[p] : a.has_shared;
-        const float* src = a.part + (size_t)p * NC * H + h0 + 4 * half;
-        float4 v[kMaxInter / kSlice];
+        const uint32_t fl = vmi_bload_b32(rf, (ok && j < k) ? 4u * (uint32_t)p : VMI_OOB, 0);
+        flag[it] = j < k ? fl : (uint32_t)(ok && a.has_shared);
+        const uint32_t off = (uint32_t)(((size_t)p * NC * H + h0 + 4 * half) * sizeof(float));
 #pragma unroll
-        for (int cc = 0; cc < kMaxInter / kSlice; ++cc)
-            if (cc < NC) v[cc] = *reinterpret_cast<const float4*>(src + (size_t)cc * H);
-        float4 y = v[0];
+        for (int cc = 0; cc < MC; ++cc)
+            v[it][cc] = vmi_bload_b128(rp, (ok && cc < NC) ? off + (uint32_t)(cc * H * sizeof(float)) : VMI_OOB, 0);
+    }
 #pragma unroll
-        for (int cc = 1; cc < kMaxInter / kSlice; ++cc)
-            if (cc < NC) {
-                y.x += v[cc].x;
-                y.y += v[cc].y;
-                y.z += v[cc].z;
-                y.w += v[cc].w;
-            }
-        if (!flag) y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        *reinterpret_cast<float4*>(&s_y[t][j][4 * half]) = y;
+    for (int it = 0; it < 2; ++it) {
+        const int i = tid + kThreads * it;
+        if (i < nitem) {
+            const int half = i & 1, t = tj[it] / (k + 1), j = tj[it] - t * (k + 1);
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = __uint_as_float(v[it][0][e]);
+#pragma unroll
+            for (int cc = 1; cc < MC; ++cc)
+                if (cc < NC)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) y[e] += __uint_as_float(v[it][cc][e]);
+            *reinterpret_cast<float4*>(&s_y[t][j][4 * half]) =
+                flag[it] ? make_float4(y[0], y[1], y[2], y[3]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
     }
     __syncthreads();
     if (fin) {
@@ -1643,11 +1740,12 @@ int launch_moe_layer(const vmi_moe_layer_desc& D, const uint16_t* x, int T, cons
     ra.sgate = has_sgate ? D.shared_expert_gate : D.router;
     ra.sgbits = has_sgate ? D.shared_expert_gate_bits : D.router_bits;
     ra.has_sgate = has_sgate;
-    // row groups of four rows covering the router rows, the shared-expert gate
-    // and one spare row (the wave that writes the MFMA operands), times T
-    // tokens, in whole blocks of 8 groups (one per XCD)
-    constexpr int rows_per_wg = kThreads / VMI_WAVE;
-    ra.row_wgs = (D.num_experts + has_sgate + 1 + rows_per_wg - 1) / rows_per_wg;
+    // row groups of 4 waves x kRouterRows rows covering the router rows, the
+    // shared-expert gate and one more wave (the one that writes the MFMA
+    // operands), times T tokens, in whole blocks of 8 groups (one per XCD)
+    constexpr int waves_per_wg = kThreads / VMI_WAVE;
+    const int row_waves = (D.num_experts + has_sgate + kRouterRows - 1) / kRouterRows + 1;
+    ra.row_wgs = (row_waves + waves_per_wg - 1) / waves_per_wg;
     ra.logits = ws.logits; ra.sg_logit = ws.sg_logit; ra.ops = ops;
     const dim3 rgrid((unsigned)(((ra.row_wgs + 7) / 8) * 8 * T));
     switch (D.hidden) {

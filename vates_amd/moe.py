@@ -113,6 +113,24 @@ def gateup_mfma_major(p: QuantizedProj, group: int = 64, bits: int = 4) -> Quant
     return QuantizedProj(w.view(n, rows, words), p.scales, p.biases)
 
 
+def gateup_reference_layout(p: QuantizedProj) -> QuantizedProj:
+    """Inverse of ``gateup_mfma_major``: the stack back in the reference's
+    [n, inter, hidden*bits/32] row-major pool layout (a new tensor)."""
+    n, rows, words = p.weight.shape
+    w = p.weight.view(n, rows // 64, 4, words // 16, 4, 16, 4).permute(0, 1, 2, 5, 3, 4, 6).contiguous()
+    return QuantizedProj(w.view(n, rows, words), p.scales, p.biases)
+
+
+def down_reference_layout(p: QuantizedProj, group: int = 64, bits: int = 4) -> QuantizedProj:
+    """Inverse of ``down_group_major``: words [n, hidden, inter*bits/32],
+    scales and biases [n, hidden, inter/group] (new tensors)."""
+    n, G, rows, wpg = p.weight.shape
+    if wpg != group * bits // 32:
+        raise VmiError(f"group-major down words {tuple(p.weight.shape)} do not match group={group}")
+    w = p.weight.permute(0, 2, 1, 3).contiguous().view(n, rows, G * wpg)
+    return QuantizedProj(w, p.scales.permute(0, 2, 1).contiguous(), p.biases.permute(0, 2, 1).contiguous())
+
+
 def _fused_moe_pairs(x: torch.Tensor, local_slots: Optional[torch.Tensor], scores: torch.Tensor, k: int,
                      projs: list, hidden: int, inter: int, group: int, bits: int, stream,
                      out_dtype: torch.dtype) -> torch.Tensor:
@@ -273,6 +291,23 @@ class MoELayer:
         d.norm_weight = _ptr(norm_weight)
         d.norm_eps = norm_eps
         self.desc = d
+        self.group, self.bits = group, bits
+
+    def reference_weights(self) -> dict:
+        """The layer's weights in the reference's layouts (new tensors for the
+        six expert stacks, the stored tensors for the rest): keys router, gate,
+        up, down, shared_gate, shared_up, shared_down, shared_expert_gate,
+        slot_table, router_logit_bias, norm_weight."""
+        names = ("router", "gate", "up", "down", "shared_gate", "shared_up", "shared_down", "shared_expert_gate",
+                 "slot_table", "router_logit_bias", "norm_weight")
+        out = dict(zip(names, self._keep))
+        for key in ("gate", "up", "shared_gate", "shared_up"):
+            if out[key] is not None:
+                out[key] = gateup_reference_layout(out[key])
+        for key in ("down", "shared_down"):
+            if out[key] is not None:
+                out[key] = down_reference_layout(out[key], self.group, self.bits)
+        return out
 
     def workspace_bytes(self, T: int) -> int:
         return load().vmi_moe_layer_workspace_bytes(T, self.top_k, self.hidden, self.inter, self.num_experts)
