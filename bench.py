@@ -37,15 +37,17 @@ ROUTER8_BYTES = 512 * 2048 + 2 * 512 * 32 * 2  # 1,114,112
 SGATE8_BYTES = 2048 + 2 * 32 * 2  # 2,176
 SEED = 1234
 ZIPF_S, ZIPF_ALPHA = 1.1, 0.5
-# HBM bytes a layer call of the MoE stack moves, measured by rocprofv3 counter
-# passes (profiles/moe_layer_48x_T4_traffic.md) over `--layers 8 --steps 3
-# --warmup 1 --no-graph --no-decode` (32 layer calls): FETCH_SIZE summed over
-# the layer's kernels, scaled by what the counter reads for a plain copy of
-# known size (bench.py --path copy), plus WRITE_SIZE likewise.  A committed
-# measurement of the kernels as they are, not a figure of this run.
-MOE_TRAFFIC_BYTES = 61066445
-MOE_TRAFFIC_SOURCE = ("profiles/moe_layer_48x_T4_traffic.md: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over 32 layer "
-                      "calls, scaled by a 512 MiB copy (x2.000 / x1.000): 61,066,445 B against 58,525,824 algorithmic B")
+# HBM bytes a layer call of the MoE stack moves per algorithmic byte, measured
+# by rocprofv3 counter passes (profiles/moe_layer_48x_T4_traffic.md) over
+# `--layers 8 --steps 3 --warmup 1 --no-graph --no-decode --no-ceiling`:
+# FETCH_SIZE summed over the layer's kernels, scaled by what the counter reads
+# for a plain copy of known size (bench.py --path copy), plus WRITE_SIZE
+# likewise, divided by those calls' algorithmic bytes.  The line reports
+# roofline.traffic = this ratio x this run's algorithmic bytes per call.
+MOE_TRAFFIC_RATIO = 1.1071
+MOE_TRAFFIC_SOURCE = ("profiles/moe_layer_48x_T4_traffic.md: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over 34 layer "
+                      "calls, scaled by a 512 MiB copy (x2.000 / x1.000): 64,877,214 B against 58,602,501 "
+                      "algorithmic B (expert weights x1.003; 5.8 MB of split-K partial rows written and re-read)")
 
 
 def eprint(*a):
@@ -146,6 +148,145 @@ def bench_copy(args) -> int:
                       "us_per_launch": round(ms * 1e3 / args.steps, 3),
                       "GBps": round(nbytes * args.steps / (ms / 1e3) / 1e9, 1)}), flush=True)
     return 0
+
+
+def measure_stream_peak(mib: int = 4096, reps: int = 10) -> dict:
+    """Read ceiling of this GPU's HBM, measured with libvmi's read-only stream
+    kernel (vmi_stream_read) over a `mib` MiB buffer: best GB/s over a sweep
+    of workgroup counts, nontemporal and cached loads, each the mean of `reps`
+    launches timed with HIP events.  The XOR of the buffer is checked against
+    torch's, so a launch that skipped bytes would not count."""
+    import torch
+    from vates_amd._lib import check, load
+    lib = load()
+    dev = torch.device("cuda:0")
+    n = mib * (1 << 20) // 4
+    if n & (n - 1):
+        raise ValueError(f"stream buffer of {mib} MiB: a power of two is needed")
+    buf = torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device=dev)
+    fold = buf  # XOR of all words by halving on the device (n is a power of two)
+    while fold.numel() > 1:
+        h = fold.numel() // 2
+        fold = torch.bitwise_xor(fold[:h], fold[h:])
+    want = int(fold.cpu().numpy().view(np.uint32)[0])
+    del fold
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    results = {}
+    for nt in (1, 0):
+        for per_cu in (1, 2, 4, 8, 16):
+            wgs = cus * per_cu
+            sink.zero_()
+            check(lib.vmi_stream_read(buf.data_ptr(), buf.numel() * 4, nt, wgs, sink.data_ptr(), stream),
+                  "vmi_stream_read")
+            torch.cuda.synchronize()
+            if int(sink.cpu().numpy().view(np.uint32)[0]) != want:
+                raise RuntimeError(f"vmi_stream_read checksum mismatch (nt={nt}, workgroups={wgs})")
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(reps):
+                lib.vmi_stream_read(buf.data_ptr(), buf.numel() * 4, nt, wgs, sink.data_ptr(), stream)
+            end.record()
+            torch.cuda.synchronize()
+            gbs = buf.numel() * 4 * reps / (start.elapsed_time(end) / 1e3) / 1e9
+            results[(nt, wgs)] = gbs
+    del buf
+    torch.cuda.empty_cache()
+    best_nt = max((v, k) for k, v in results.items() if k[0] == 1)
+    best_c = max((v, k) for k, v in results.items() if k[0] == 0)
+    return {"gbs": round(max(best_nt[0], best_c[0]), 1), "nontemporal_gbs": round(best_nt[0], 1),
+            "nontemporal_workgroups": best_nt[1][1], "cached_gbs": round(best_c[0], 1),
+            "cached_workgroups": best_c[1][1], "buffer_mib": mib, "launches_each": reps,
+            "kernel": "vmi_stream_read (libvmi): 16-byte buffer loads, 8 in flight per lane, XOR-checked"}
+
+
+def measure_mfma_peak(iters: int = 20000) -> dict:
+    """Dense fp16 MFMA ceiling of this GPU, measured with libvmi's
+    vmi_mfma_peak (four independent v_mfma_f32_16x16x32_f16 chains per wave,
+    the instruction of the prefill GEMMs): best TFLOP/s over a sweep of
+    workgroup counts, each the mean of 3 launches timed with HIP events."""
+    import torch
+    from vates_amd._lib import check, load
+    lib = load()
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = torch.cuda.current_stream().cuda_stream
+    best = (0.0, 0)
+    for per_cu in (2, 4, 8, 16):
+        wgs = cus * per_cu
+        sink = torch.zeros(wgs, dtype=torch.float32, device=dev)
+        check(lib.vmi_mfma_peak(wgs, 64, sink.data_ptr(), stream), "vmi_mfma_peak")
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(3):
+            lib.vmi_mfma_peak(wgs, iters, sink.data_ptr(), stream)
+        end.record()
+        torch.cuda.synchronize()
+        tfs = 3 * wgs * 16.0 * iters * 16384 / (start.elapsed_time(end) / 1e3) / 1e12
+        if not bool(torch.isfinite(sink).all()):
+            raise RuntimeError("vmi_mfma_peak produced a non-finite checksum")
+        best = max(best, (tfs, wgs))
+    return {"tflops": round(best[0], 1), "workgroups": best[1], "iters": iters,
+            "kernel": "vmi_mfma_peak (libvmi): v_mfma_f32_16x16x32_f16, 4 independent chains per wave"}
+
+
+def bench_stream(args) -> int:
+    """The device's measured ceilings on their own: HBM read (vmi_stream_read)
+    and dense fp16 MFMA (vmi_mfma_peak)."""
+    import torch
+    torch.cuda.set_device(0)
+    st = measure_stream_peak(args.stream_mib)
+    mf = measure_mfma_peak()
+    eprint(f"[bench] stream read {st['gbs']} GB/s (nt {st['nontemporal_gbs']}, cached {st['cached_gbs']}); "
+           f"MFMA {mf['tflops']} TFLOP/s")
+    print(json.dumps({"path": "stream", "metric": "measured HBM read ceiling", "value": st["gbs"], "unit": "GB/s",
+                      "frac_of_published": round(st["gbs"] / PEAK_HBM_GBS, 4), "stream": st,
+                      "mfma": mf, "mfma_frac_of_published": round(mf["tflops"] / PEAK_MFMA_TFLOPS, 4)}),
+          flush=True)
+    return 0
+
+
+def layer_latency(one_step, layers_n: int, xa, x_bank, steps: int) -> dict:
+    """Per-layer-call latency distribution of the MoE stack.  Each step's
+    layer calls are launched eagerly with a HIP event between consecutive
+    calls; a bounded device-side sleep (torch.cuda._sleep) ahead of every step
+    lets the host queue the whole step before the GPU reaches it, so the event
+    gaps hold device time, not host latency.  Event markers add to each call,
+    so the same steps are also run without them (one event pair per step) and
+    the difference is reported as the markers' cost.  (ROCm does not record
+    events inside a captured graph.)"""
+    import torch
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    torch.cuda._sleep(2_000_000)
+    e1.record()
+    torch.cuda.synchronize()
+    cyc_per_us = 2_000_000 / max(e0.elapsed_time(e1) * 1e3, 1.0)
+    head_start = int(cyc_per_us * layers_n * 80)  # 80 us of host time per layer call
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(layers_n + 1)]
+    samples, plain = [], []
+    for st in range(steps):
+        xa.copy_(x_bank[st])
+        torch.cuda._sleep(head_start)
+        one_step(ev)
+        torch.cuda.synchronize()
+        samples += [ev[l].elapsed_time(ev[l + 1]) * 1e3 for l in range(layers_n)]
+        xa.copy_(x_bank[st])
+        torch.cuda._sleep(head_start)
+        e0.record()
+        one_step(None)
+        e1.record()
+        torch.cuda.synchronize()
+        plain.append(e0.elapsed_time(e1) * 1e3 / layers_n)
+    a = np.array(samples)
+    return {"p50_us": round(float(np.percentile(a, 50)), 3), "p99_us": round(float(np.percentile(a, 99)), 3),
+            "mean_us": round(float(a.mean()), 3), "max_us": round(float(a.max()), 3), "samples": int(a.size),
+            "mean_us_without_markers": round(float(np.mean(plain)), 3),
+            "marker_cost_us": round(float(a.mean() - np.mean(plain)), 3),
+            "method": f"{steps} steps x {layers_n} layer calls launched eagerly behind a device-side sleep, "
+                      "HIP events between calls"}
 
 
 def bench_lm_head(args) -> int:
@@ -515,6 +656,8 @@ def bench_prefill(args) -> int:
     gbs = nbytes / (us * 1e-6) / 1e9
     hbm_bound = flops / nbytes < PEAK_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
     eprint(f"[bench] prefill T={T}: {us:.1f} us per layer, {tfs:.1f} TFLOP/s, {gbs:.1f} GB/s, {U} experts touched")
+    mf = measure_mfma_peak()
+    eprint(f"[bench] measured MFMA ceiling {mf['tflops']} TFLOP/s")
     from vates_amd.moe import workspace, workspace_status
     ws = workspace(moe.prefill_workspace_bytes(T), dev, torch.cuda.current_stream().cuda_stream, tag="prefill")
     if workspace_status(ws):
@@ -551,6 +694,9 @@ def bench_prefill(args) -> int:
                      "peak": PEAK_HBM_GBS if hbm_bound else PEAK_MFMA_TFLOPS,
                      "unit": "GB/s" if hbm_bound else "TFLOP/s",
                      "frac": round((gbs / PEAK_HBM_GBS) if hbm_bound else (tfs / PEAK_MFMA_TFLOPS), 4),
+                     "peak_measured": None if hbm_bound else mf["tflops"],
+                     "frac_measured": None if hbm_bound else round(tfs / mf["tflops"], 4),
+                     "peak_measured_source": None if hbm_bound else mf,
                      "traffic": None, "unit_of_work": "one vmi_moe_prefill call",
                      "flops_per_launch": flops, "bytes_per_launch": nbytes, "us_per_launch": round(us, 3)},
         "cpu_baseline": cpu,
@@ -574,18 +720,21 @@ def main() -> int:
     ap.add_argument("--experts", type=int, default=512)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-baseline-s", type=float, default=15.0)
-    ap.add_argument("--path", choices=["moe", "lm_head", "prefill", "decode", "copy"], default="moe",
+    ap.add_argument("--path", choices=["moe", "lm_head", "prefill", "decode", "copy", "stream"], default="moe",
                     help="moe: the 48-layer verify stack (default); lm_head: the vocabulary GEMV + argmax; "
                          "prefill: one expert-major MoE layer on a T-token prompt; decode: K=3 MTP speculative "
                          "decoding end to end; copy: a plain elementwise copy of known size (calibrates the "
-                         "HBM byte counters)")
+                         "HBM byte counters); stream: the measured HBM read and dense MFMA ceilings")
     ap.add_argument("--copy-mib", type=int, default=512)
+    ap.add_argument("--stream-mib", type=int, default=4096, help="stream: buffer size (a power of two)")
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--new-tokens", type=int, default=512)
     ap.add_argument("--K", type=int, default=3)
     ap.add_argument("--attn-every", type=int, default=4)
     ap.add_argument("--tau", type=float, default=0.3, help="decode: adaptive-depth confidence threshold")
     ap.add_argument("--no-decode", action="store_true", help="default path: skip the decode record")
+    ap.add_argument("--no-ceiling", action="store_true",
+                    help="default path: skip the latency pass and the measured read ceiling (counter passes)")
     ap.add_argument("--vocab", type=int, default=151936)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -601,6 +750,8 @@ def main() -> int:
         return bench_decode(args)
     if args.path == "copy":
         return bench_copy(args)
+    if args.path == "stream":
+        return bench_stream(args)
 
     import torch
     from vates_amd.synth import synth_bf16
@@ -627,11 +778,15 @@ def main() -> int:
     ids = torch.zeros((args.layers, T, k), dtype=torch.int32, device=dev)
     ws = torch.zeros(layers[0].workspace_bytes(T), dtype=torch.uint8, device=dev)
 
-    def one_step():
+    def one_step(events=None):
         cur, nxt = xa, xb
         for l, layer in enumerate(layers):
+            if events is not None:
+                events[l].record()
             layer(cur, residual=cur, out=nxt, ids_out=ids[l], ws=ws)
             cur, nxt = nxt, cur
+        if events is not None:
+            events[len(layers)].record()
         return cur
 
     graph = None
@@ -685,6 +840,15 @@ def main() -> int:
         eprint(f"[bench] device status flags {status:#x}")
         return 3
 
+    lat = peak = None
+    if not args.no_ceiling:
+        lat = layer_latency(one_step, len(layers), xa, x_bank, min(args.steps, 40))
+        eprint(f"[bench] layer call latency: p50 {lat['p50_us']} us, p99 {lat['p99_us']} us, "
+               f"mean {lat['mean_us']} us over {lat['samples']} calls ({lat['marker_cost_us']} us of event markers)")
+        peak = measure_stream_peak()
+        eprint(f"[bench] measured read ceiling {peak['gbs']} GB/s (nt {peak['nontemporal_gbs']}, "
+               f"cached {peak['cached_gbs']})")
+
     parity = moe_parity(layers, ws_list, x_bank[0], args)
     eprint(f"[bench] first two layers against the oracle: {parity}")
     cpu = cpu1 = None
@@ -700,6 +864,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         decode = decode_record(args)
 
+    achieved = per_layer_bytes / (per_layer_us * 1e-6) / 1e9
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -723,12 +888,19 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(per_layer_bytes / (per_layer_us * 1e-6) / 1e9, 2),
+            "achieved": round(achieved, 2),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
-            "frac": round(per_layer_bytes / (per_layer_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-            "traffic": MOE_TRAFFIC_BYTES if args.hidden == 2048 and T == 4 else None,
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "peak_measured": peak["gbs"] if peak else None,
+            "frac_measured": round(achieved / peak["gbs"], 4) if peak else None,
+            "peak_measured_source": peak,
+            "traffic": round(MOE_TRAFFIC_RATIO * per_layer_bytes) if args.hidden == 2048 and T == 4 else None,
+            "traffic_ratio": MOE_TRAFFIC_RATIO if args.hidden == 2048 and T == 4 else None,
             "traffic_source": MOE_TRAFFIC_SOURCE if args.hidden == 2048 and T == 4 else None,
+            "p50_us": lat["p50_us"] if lat else None,
+            "p99_us": lat["p99_us"] if lat else None,
+            "latency": lat,
             "unit_of_work": "one MoE layer call (router+topk, gate/up, down+combine kernels)",
             "bytes_per_launch": round(per_layer_bytes),
             "us_per_launch": round(per_layer_us, 3),

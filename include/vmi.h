@@ -529,6 +529,24 @@ int vmi_synth_quantized(uint64_t seed, uint32_t stream_id, int64_t rows, int col
                         uint32_t* w, uint16_t* s, uint16_t* b, void* stream);
 int vmi_synth_bf16(uint64_t seed, uint32_t stream_id, int64_t n, float scale, uint16_t* out, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Device ceilings (no reference counterpart: the reference publishes no
+ * kernel figures).  Measurement kernels whose rates are the denominators a
+ * benchmark reports beside the published peaks.
+ * vmi_stream_read reads bytes at src once with 16-byte loads (nontemporal
+ * loads when nontemporal != 0), `workgroups` workgroups of 256 lanes each
+ * striding over 32 KB chunks, and XORs every 32-bit word of the buffer into
+ * *sink (the caller zeroes it first; the result is the XOR of all words).
+ * src 16-byte aligned, bytes a non-zero multiple of 16.
+ * vmi_mfma_peak runs `workgroups` workgroups of four waves; each wave issues
+ * iters rounds of four independent v_mfma_f32_16x16x32_f16 of 16,384 flops
+ * each (16 * iters * 16,384 dense flops per workgroup), and workgroup g
+ * writes to sink[g] (float [workgroups]) the sum of element 0..3 of its first
+ * lane's four accumulators (chain j's element j).
+ * ------------------------------------------------------------------------ */
+int vmi_stream_read(const void* src, size_t bytes, int nontemporal, int workgroups, uint32_t* sink, void* stream);
+int vmi_mfma_peak(int workgroups, int iters, float* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -109,6 +109,8 @@ _SIGNATURES = {
     "vmi_rmsnorm": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p,
                             c_void_p]),
     "vmi_topk_rows": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "vmi_stream_read": (c_int, [c_void_p, c_size_t, c_int, c_int, c_void_p, c_void_p]),
+    "vmi_mfma_peak": (c_int, [c_int, c_int, c_void_p, c_void_p]),
     "vmi_lm_head_workspace_bytes": (c_size_t, [c_int, c_int]),
     "vmi_lm_head": (c_int, [c_void_p, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p, c_void_p,
                             c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -10,7 +10,11 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libvmi.so"
-SOURCES = ["vmi_moe.hip", "vmi_util.hip", "vmi_head.hip", "vmi_accept.hip", "vmi_prefill.hip", "vmi_attn.hip", "vmi_gdn.hip"]
+# A tuning variant: the same sources with the kernels' real-time stamps on
+# (-DVMI_TIMELINE), read by vates_amd.timeline.  Never loaded by the product.
+TIMELINE_LIB = PKG / "libvmi_timeline.so"
+SOURCES = ["vmi_moe.hip", "vmi_util.hip", "vmi_head.hip", "vmi_accept.hip", "vmi_prefill.hip", "vmi_attn.hip", "vmi_gdn.hip",
+           "vmi_peak.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
@@ -34,16 +38,20 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libvmi.so)")
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compiles every source to an object, then links libvmi.so atomically."""
-    objdir = ROOT / "_build"
-    objdir.mkdir(exist_ok=True)
+def build_library(verbose: bool = False, timeline: bool = False) -> Path:
+    """Compiles every source to an object, then links libvmi.so atomically
+    (timeline: libvmi_timeline.so, the stamped tuning variant)."""
+    objdir = ROOT / "_build" / ("timeline" if timeline else "")
+    objdir.mkdir(parents=True, exist_ok=True)
+    target = TIMELINE_LIB if timeline else LIB
+    extra = ["-DVMI_TIMELINE"] if timeline else []
     cc = hipcc()
     objs = []
     procs = []
     for src in SOURCES:
         obj = objdir / (Path(src).stem + ".o")
-        cmd = [cc, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), f"-I{ROOT / 'include'}", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *HIP_FLAGS, *extra, *SOURCE_FLAGS.get(src, []), f"-I{ROOT / 'include'}", "-c", str(CSRC / src),
+               "-o", str(obj)]
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
         objs.append(obj)
     for cmd, p in procs:
@@ -53,14 +61,15 @@ def build_library(verbose: bool = False) -> Path:
             raise RuntimeError(f"hipcc failed: {' '.join(cmd)}\n{text}")
         if verbose and text.strip():
             print(text)
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = target.with_suffix(".so.tmp")
     cmd = [cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}{res.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, target)
+    return target
 
 
 if __name__ == "__main__":
-    print(build_library(verbose=True))
+    import sys
+    print(build_library(verbose=True, timeline="--timeline" in sys.argv[1:]))
