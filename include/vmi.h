@@ -43,6 +43,8 @@ enum vmi_dtype { VMI_F32 = 0, VMI_BF16 = 1 };
 #define VMI_STATUS_BAD_ROUTE 0x2u  /* router produced a non-finite logit */
 #define VMI_STATUS_BAD_POS 0x4u    /* a device-side position outside [0, max_len - T] */
 #define VMI_STATUS_BAD_RECORD 0x8u /* an acceptance record outside what vmi_spec_commit allows */
+#define VMI_STATUS_WAIT_GAVE_UP 0x10u /* a wait of vmi_accept_stochastic / vmi_sample_top_p outlasted its bound */
+#define VMI_STATUS_BAD_LOGITS 0x20u   /* a logit row of those calls had no finite value */
 
 /* Last error message of the calling thread ("" when none). */
 const char* vmi_last_error(void);
@@ -492,17 +494,25 @@ int vmi_spec_commit(const int32_t* result, const uint16_t* hid, int rows, int pa
  * running mass exceeds t.  (U_i, V_i) = words 0, 1 of Philox4x32-10 with key
  * seed and counter (offset lo, offset hi, i, 0x5A3D1E57).  Bit-identical to
  * the CPU oracle.  temperature > 0 (use vmi_accept_greedy for 0), 0 < top_p <= 1.
+ * offset_device (uint64 on the device, or NULL): when set, the counter
+ * offset is offset + *offset_device, read when the kernel runs (a captured
+ * graph replays with offsets that advance on the device).
  * workspace: vmi_accept_stochastic_workspace_bytes(K, vocab, draft_logits != NULL)
  * bytes, zero before the first call and left so by every call; one call in
  * flight per workspace.  The kernel's workgroups wait for each other between
- * its phases, so all of them must be resident at once (the grid is at most
- * two workgroups per CU); a wait that outlasts its bound (the CUs held by
- * other work) gives up, and the call then writes record [0, 0, 0, -1].
+ * its phases, so all of them must be resident at once (the grid holds at
+ * most min(2, the occupancy calculator's figure) workgroups per CU); a wait
+ * that outlasts its bound (the CUs held by other work; vmi_set_wait_limit)
+ * gives up, and the call then writes record [0, 0, 0, -1] and ORs
+ * VMI_STATUS_WAIT_GAVE_UP into *status; a logit row with no finite value
+ * writes the same record and ORs VMI_STATUS_BAD_LOGITS.  status (uint32 on
+ * the device, or NULL) is the caller's: the kernel never clears it.
  * ------------------------------------------------------------------------ */
 size_t vmi_accept_stochastic_workspace_bytes(int K, int vocab, int has_draft_logits);
 int vmi_accept_stochastic(const float* target_logits, const float* draft_logits, const int32_t* drafts, int K,
-                          int vocab, float temperature, float top_p, uint64_t seed, uint64_t offset, int32_t* result,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          int vocab, float temperature, float top_p, uint64_t seed, uint64_t offset,
+                          const uint64_t* offset_device, int32_t* result, void* workspace, size_t workspace_bytes,
+                          uint32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------
  * vmi_sample_top_p -- one token per row of logits f32 [rows, vocab] from the
@@ -510,12 +520,24 @@ int vmi_accept_stochastic(const float* target_logits, const float* draft_logits,
  * (offset, r)); the drafter's sampler when drafting stochastically.  The
  * reference drafts by argmax only (drafter.py:20-40).  out int32 [rows]
  * (-1 for a row without a finite logit, and for a row drawn after one of the
- * kernel's waits outlasted its bound).  Workspace and residency as for
- * vmi_accept_stochastic.
+ * kernel's waits outlasted its bound; the status bits as for
+ * vmi_accept_stochastic).  offset_device, workspace, residency and status as
+ * for vmi_accept_stochastic.
  * ------------------------------------------------------------------------ */
 size_t vmi_sample_top_p_workspace_bytes(int rows, int vocab);
 int vmi_sample_top_p(const float* logits, int rows, int vocab, float temperature, float top_p, uint64_t seed,
-                     uint64_t offset, int32_t* out, void* workspace, size_t workspace_bytes, void* stream);
+                     uint64_t offset, const uint64_t* offset_device, int32_t* out, void* workspace,
+                     size_t workspace_bytes, uint32_t* status, void* stream);
+
+/* ------------------------------------------------------------------------
+ * vmi_set_wait_limit -- the bound (in polls: a coherent load and a short sleep) of the
+ * co-residency waits of vmi_accept_stochastic and vmi_sample_top_p, for
+ * calls launched afterwards from any thread; polls <= 0 restores the
+ * default (65,536).  Returns the previous bound.  No reference counterpart:
+ * tests force the give-up path with a bound of 1, so the kernels still exit
+ * normally.
+ * ------------------------------------------------------------------------ */
+int vmi_set_wait_limit(int polls);
 
 /* ------------------------------------------------------------------------
  * Synthetic data (no reference counterpart: the reference loads real

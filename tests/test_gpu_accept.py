@@ -6,7 +6,11 @@ Greedy: the reference's literal accept_prefix answers
 both verify layouts and P-path trees.  Stochastic: random small vocabularies
 with and without draft logits, the full 151,936 vocabulary with target logits
 N(0, 3) and a planted argmax agreement of 0.7 at temperature 0.7 / top-p 0.9,
-and the edge cases (identical draft, a row without finite logits).
+and the edge cases (identical draft, a row without finite logits: the failure
+record, VMI_STATUS_BAD_LOGITS in the caller's status word, VmiError without
+one); a device-side counter offset adds to the host one; a wait bound of one
+poll makes the co-residency waits give up, which every workgroup survives: the
+failure record, VMI_STATUS_WAIT_GAVE_UP, the workspace counters back at zero.
 """
 import json
 import sys
@@ -14,6 +18,8 @@ from pathlib import Path
 
 import numpy as np
 import pytest
+
+from vates_amd._lib import VMI_STATUS_BAD_LOGITS, VMI_STATUS_WAIT_GAVE_UP, VmiError
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_known_answers.json"
@@ -136,9 +142,91 @@ def test_stochastic_edges(gpu, orc):
         assert r["matched"] == K and r["emitted"][:K] == drafts.cpu().tolist()
     bad = target.copy()
     bad[2] = np.nan
+    status = torch.zeros(1, dtype=torch.int32, device=gpu)
     r = decode_result(accept_stochastic(_t(bad, gpu), None, _t(np.zeros(K, np.int32), gpu), temperature=0.7,
-                                        top_p=0.9, seed=1, offset=0).cpu())
+                                        top_p=0.9, seed=1, offset=0, status=status).cpu())
     assert r["path"] == -1 and r["emitted"] == []
+    assert int(status.item()) == VMI_STATUS_BAD_LOGITS
+    with pytest.raises(VmiError, match="finite"):
+        accept_stochastic(_t(bad, gpu), None, _t(np.zeros(K, np.int32), gpu), temperature=0.7, top_p=0.9, seed=1,
+                          offset=0)
+    # the status word is the caller's: a later good call leaves it as it was
+    accept_stochastic(tt, None, _t(np.zeros(K, np.int32), gpu), temperature=0.7, top_p=0.9, seed=1, offset=0,
+                      status=status)
+    assert int(status.item()) == VMI_STATUS_BAD_LOGITS
+
+
+def test_offset_device_adds_to_offset(gpu, orc):
+    """offset_device (a device word read when the kernel runs) adds to offset:
+    the draws equal the oracle's at the sum."""
+    log("case: sampling and stochastic accept with a device-side counter offset")
+    import torch
+    from vates_amd.accept import accept_stochastic, sample_top_p
+    rng = np.random.default_rng(62)
+    K, V = 3, 3000
+    target = rng.normal(0, 3, (K + 1, V)).astype(np.float32)
+    draft = rng.normal(0, 3, (K, V)).astype(np.float32)
+    dev_off = torch.tensor([1 << 40], dtype=torch.int64, device=gpu)
+    for off in (0, 5, 63):
+        got = sample_top_p(_t(draft, gpu), temperature=0.7, top_p=0.9, seed=8, offset=off,
+                           offset_device=dev_off).cpu().numpy()
+        assert np.array_equal(got, orc.sample_top_p(draft, 0.7, 0.9, 8, (1 << 40) + off))
+        drafts = got.astype(np.int32)
+        want = _record(orc, target, draft, drafts, 0.7, 0.9, 9, (1 << 40) + off)
+        rec = accept_stochastic(_t(target, gpu), _t(draft, gpu), _t(drafts, gpu), temperature=0.7, top_p=0.9,
+                                seed=9, offset=off, offset_device=dev_off).cpu().numpy()
+        assert np.array_equal(rec[:4 + want[0]], want[:4 + want[0]])
+
+
+def test_wait_give_up_is_reported_and_leaves_workspace_clean(gpu, orc):
+    """A wait bound of one poll (vmi_set_wait_limit) makes the co-residency
+    waits give up while their peers are still on the way: every workgroup
+    still exits, the call writes the failure record and sets
+    VMI_STATUS_WAIT_GAVE_UP in the caller's status word (and raises without
+    one), and the workspace's counters are back at zero for the next call,
+    which, with the default bound restored, equals the oracle."""
+    log("case: stochastic accept / top-p sampling with a one-poll wait bound")
+    import torch
+    from vates_amd.accept import accept_stochastic, sample_top_p, set_wait_limit
+    from vates_amd.moe import workspace
+    rng = np.random.default_rng(63)
+    K, V = 3, 151936
+    target = rng.normal(0, 3, (K + 1, V)).astype(np.float32)
+    draft = rng.normal(0, 3, (K, V)).astype(np.float32)
+    drafts = orc.sample_top_p(draft, 0.7, 0.9, 4, 0)
+    tt, dd, dr = _t(target, gpu), _t(draft, gpu), _t(drafts, gpu)
+    want = _record(orc, target, draft, drafts, 0.7, 0.9, 5, 1)
+    sync_bytes = 64 * 64 + 256 + 64 * 4 + 64 * 2048 + 64 * 64  # the counters at the workspace's start
+    gave_up = 0
+    prev = set_wait_limit(1)
+    try:
+        for attempt in range(4):
+            status = torch.zeros(1, dtype=torch.int32, device=gpu)
+            rec = accept_stochastic(tt, dd, dr, temperature=0.7, top_p=0.9, seed=5, offset=1,
+                                    status=status).cpu().numpy()
+            bits = int(status.item())
+            if bits:
+                assert bits == VMI_STATUS_WAIT_GAVE_UP and list(rec[:4]) == [0, 0, 0, -1], (bits, rec)
+                gave_up += 1
+            else:
+                assert np.array_equal(rec[:4 + want[0]], want[:4 + want[0]])
+            ws = workspace(1, gpu, torch.cuda.current_stream().cuda_stream, tag="accept")
+            assert int(ws[:sync_bytes].count_nonzero().item()) == 0
+            st2 = torch.zeros(1, dtype=torch.int32, device=gpu)
+            toks = sample_top_p(dd, temperature=0.7, top_p=0.9, seed=4, offset=0, status=st2).cpu().numpy()
+            if int(st2.item()):
+                assert int(st2.item()) == VMI_STATUS_WAIT_GAVE_UP and (toks == -1).any()
+                gave_up += 1
+        log(f"{gave_up} of 8 calls gave up")
+        assert gave_up > 0, "a one-poll bound never gave up"
+        with pytest.raises(VmiError):
+            for _ in range(8):  # raises at the first call that gives up
+                accept_stochastic(tt, dd, dr, temperature=0.7, top_p=0.9, seed=5, offset=1)
+    finally:
+        set_wait_limit(prev)
+    rec = accept_stochastic(tt, dd, dr, temperature=0.7, top_p=0.9, seed=5, offset=1).cpu().numpy()
+    assert np.array_equal(rec[:4 + want[0]], want[:4 + want[0]])
+    assert np.array_equal(sample_top_p(dd, temperature=0.7, top_p=0.9, seed=4, offset=0).cpu().numpy(), drafts)
 
 
 @pytest.mark.parametrize("V", [3, 1000, 151936])

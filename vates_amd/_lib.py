@@ -22,6 +22,8 @@ VMI_STATUS_BAD_SLOT = 0x1
 VMI_STATUS_BAD_ROUTE = 0x2
 VMI_STATUS_BAD_POS = 0x4
 VMI_STATUS_BAD_RECORD = 0x8
+VMI_STATUS_WAIT_GAVE_UP = 0x10
+VMI_STATUS_BAD_LOGITS = 0x20
 
 
 class VmiError(RuntimeError):
@@ -88,10 +90,11 @@ _SIGNATURES = {
                                 c_void_p, c_void_p, c_void_p, c_void_p]),
     "vmi_accept_stochastic_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "vmi_accept_stochastic": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_float, c_uint64,
-                                      c_uint64, c_void_p, c_void_p, c_size_t, c_void_p]),
+                                      c_uint64, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "vmi_sample_top_p_workspace_bytes": (c_size_t, [c_int, c_int]),
     "vmi_sample_top_p": (c_int, [c_void_p, c_int, c_int, c_float, c_float, c_uint64, c_uint64, c_void_p, c_void_p,
-                                 c_size_t, c_void_p]),
+                                 c_void_p, c_size_t, c_void_p, c_void_p]),
+    "vmi_set_wait_limit": (c_int, [c_int]),
     "vmi_qgemv": (c_int, [c_void_p, c_int, c_int, QMat, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
                           c_void_p]),
     "vmi_attention_layer_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),

@@ -18,7 +18,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import VmiError, check, load
+from ._lib import VMI_ERR_HIP, VMI_STATUS_BAD_LOGITS, VMI_STATUS_WAIT_GAVE_UP, VmiError, check, load
 from .moe import _require, _stream_handle, workspace
 
 
@@ -95,10 +95,43 @@ def spec_commit(rec: torch.Tensor, hid: torch.Tensor, H: torch.Tensor, x: torch.
     check(rc, "vmi_spec_commit")
 
 
+def _status_word(status: Optional[torch.Tensor], dev) -> torch.Tensor:
+    if status is None:
+        return torch.zeros(1, dtype=torch.int32, device=dev)
+    _require(status, "status", 4, dev)
+    return status
+
+
+def _offset_device(offset_device: Optional[torch.Tensor], dev):
+    if offset_device is None:
+        return None
+    if offset_device.dtype != torch.int64 or offset_device.numel() != 1:
+        raise VmiError("offset_device must be int64 [1] on the device")
+    _require(offset_device, "offset_device", 8, dev)
+    return offset_device.data_ptr()
+
+
+def raise_sampling_status(bits: int, what: str) -> None:
+    """Raises VmiError for the status bits a sampling or stochastic
+    acceptance call sets (a wait that gave up, a row without a finite logit)."""
+    if bits & VMI_STATUS_WAIT_GAVE_UP:
+        raise VmiError(f"{what}: a co-residency wait gave up (the device was busy with other work); "
+                       "the result is the failure record", VMI_ERR_HIP)
+    if bits & VMI_STATUS_BAD_LOGITS:
+        raise VmiError(f"{what}: a logit row had no finite value")
+
+
 def accept_stochastic(target_logits: torch.Tensor, draft_logits: Optional[torch.Tensor], drafts: torch.Tensor, *,
                       temperature: float, top_p: float, seed: int, offset: int, out: Optional[torch.Tensor] = None,
+                      offset_device: Optional[torch.Tensor] = None, status: Optional[torch.Tensor] = None,
                       stream=None) -> torch.Tensor:
-    """target_logits f32 [K+1, V]; draft_logits f32 [K, V] or None; drafts int32 [K]."""
+    """target_logits f32 [K+1, V]; draft_logits f32 [K, V] or None; drafts int32 [K].
+
+    offset_device (int64 [1] on the device): added to offset when the kernel
+    runs.  status (int32 [1] on the device): the caller's status word, which
+    receives VMI_STATUS_WAIT_GAVE_UP / VMI_STATUS_BAD_LOGITS and is read by
+    the caller (graph-safe).  Without it the call waits for its result and
+    raises VmiError when either bit is set (the record is then [0, 0, 0, -1])."""
     dev = target_logits.device
     K1, V = target_logits.shape
     K = K1 - 1
@@ -111,30 +144,48 @@ def accept_stochastic(target_logits: torch.Tensor, draft_logits: Optional[torch.
         if tuple(draft_logits.shape) != (K, V):
             raise VmiError(f"draft_logits must be [{K}, {V}]")
     out = _result(K, dev, out)
+    st = _status_word(status, dev)
+    od = _offset_device(offset_device, dev)
     sh = _stream_handle(stream)
     lib = load()
     nbytes = lib.vmi_accept_stochastic_workspace_bytes(K, V, int(draft_logits is not None))
     ws = workspace(nbytes, dev, sh, tag="accept")
     rc = lib.vmi_accept_stochastic(target_logits.data_ptr(), None if draft_logits is None else draft_logits.data_ptr(),
                                    drafts.data_ptr(), K, V, float(temperature), float(top_p), int(seed) & (2**64 - 1),
-                                   int(offset) & (2**64 - 1), out.data_ptr(), ws.data_ptr(), ws.numel(), sh)
+                                   int(offset) & (2**64 - 1), od, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                   st.data_ptr(), sh)
     check(rc, "vmi_accept_stochastic")
+    if status is None:
+        raise_sampling_status(int(st.item()), "vmi_accept_stochastic")
     return out
 
 
 def sample_top_p(logits: torch.Tensor, *, temperature: float, top_p: float, seed: int, offset: int,
-                 out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
-    """logits f32 [rows, V] -> int32 [rows]."""
+                 out: Optional[torch.Tensor] = None, offset_device: Optional[torch.Tensor] = None,
+                 status: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """logits f32 [rows, V] -> int32 [rows].  offset_device and status as for
+    ``accept_stochastic`` (without status the call raises on a failed row)."""
     dev = logits.device
     rows, V = logits.shape
     _require(logits, "logits", 4, dev)
     if out is None:
         out = torch.empty(rows, dtype=torch.int32, device=dev)
     _require(out, "out", 4, dev)
+    st = _status_word(status, dev)
+    od = _offset_device(offset_device, dev)
     sh = _stream_handle(stream)
     lib = load()
     ws = workspace(lib.vmi_sample_top_p_workspace_bytes(rows, V), dev, sh, tag="sample")
     rc = lib.vmi_sample_top_p(logits.data_ptr(), rows, V, float(temperature), float(top_p), int(seed) & (2**64 - 1),
-                              int(offset) & (2**64 - 1), out.data_ptr(), ws.data_ptr(), ws.numel(), sh)
+                              int(offset) & (2**64 - 1), od, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                              st.data_ptr(), sh)
     check(rc, "vmi_sample_top_p")
+    if status is None:
+        raise_sampling_status(int(st.item()), "vmi_sample_top_p")
     return out
+
+
+def set_wait_limit(polls: int) -> int:
+    """Bound of the sampling kernels' co-residency waits (vmi_set_wait_limit);
+    polls <= 0 restores the default.  Returns the previous bound."""
+    return int(load().vmi_set_wait_limit(int(polls)))

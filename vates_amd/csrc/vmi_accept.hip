@@ -21,6 +21,8 @@
 // oracle; decisions use IEEE double operations only.  Uniforms come from
 // Philox4x32-10 (key = seed, counter = (offset, position, 0x5A3D1E57)).
 
+#include <atomic>
+
 #include "vmi_device.h"
 #include "vmi_internal.h"
 
@@ -93,7 +95,9 @@ struct SdArgs {
     const float* base1;      // rows [n0, nd)
     int nd, V, NB, chunk;
     float s2, top_p;
-    uint64_t seed, offset;
+    uint64_t seed, offset;   // the effective offset adds *offset_dev when that is set
+    const uint64_t* offset_dev;
+    uint32_t* status;        // caller's status word (VMI_STATUS_WAIT_GAVE_UP / BAD_LOGITS), or null
     int accept, K, has_q;    // accept mode: K drafts, draft rows present
     const int32_t* drafts;
     uint32_t* ctr_r;         // [kMaxRows] arrival counters of the draws
@@ -245,7 +249,7 @@ __device__ __forceinline__ void for_slice(int j0, int j1, const T* __restrict__ 
 // before it counts itself, so no fence writes back or invalidates the L2.
 // Histograms are integer sums, so their value does not depend on arrival
 // order, and the results equal those of the phases run as separate launches.
-constexpr int kSdSpinLimit = 1 << 16;  // polls (each a coherent load) before a wait gives up
+constexpr int kSdSpinLimit = 1 << 16;  // polls (each a coherent load) before a wait gives up, by default
 
 struct SdSync {
     uint32_t* row;     // [kMaxRows] arrivals per distribution, 64 bytes apart (16 words)
@@ -254,14 +258,15 @@ struct SdSync {
     uint32_t* rdone;   // [kMaxRows] workgroups of each distribution finished, 64 bytes apart
     uint32_t* flag;    // a wait gave up
     uint32_t* go;      // [nd * NB] per-workgroup release words, 64 bytes apart: the phase the workgroup may enter
+    int spin_limit;    // polls before a wait gives up (>= 1)
 };
 
-__device__ __forceinline__ void sd_wait(uint32_t* c, uint32_t target, uint32_t* flag) {
+__device__ __forceinline__ void sd_wait(uint32_t* c, uint32_t target, uint32_t* flag, int limit) {
     if (threadIdx.x == 0) {
         int spins = 0;
         while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
             __builtin_amdgcn_s_sleep(1);
-            if (++spins >= kSdSpinLimit) {
+            if (++spins >= limit) {
                 __hip_atomic_fetch_or(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
@@ -277,7 +282,7 @@ __device__ __forceinline__ void sd_wait(uint32_t* c, uint32_t target, uint32_t* 
 // `phase`, and every workgroup waits on its own word (its own 64-byte line, so
 // the waits do not all poll one address).
 __device__ __forceinline__ void sd_barrier(uint32_t* c, uint32_t target, uint32_t* go, int n, int self,
-                                           uint32_t phase, uint32_t* flag) {
+                                           uint32_t phase, uint32_t* flag, int limit) {
     __shared__ int s_rel;
     vmi_vm_wait_c<0>();
     __syncthreads();
@@ -287,7 +292,7 @@ __device__ __forceinline__ void sd_barrier(uint32_t* c, uint32_t target, uint32_
     if (s_rel)
         for (int i = threadIdx.x; i < n; i += kSdThreads)
             __hip_atomic_store(go + 16 * i, phase, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sd_wait(go + 16 * self, phase, flag);
+    sd_wait(go + 16 * self, phase, flag, limit);
 }
 
 __device__ __forceinline__ uint64_t ld64c(const unsigned long long* p) {
@@ -460,6 +465,8 @@ __device__ __forceinline__ void sd_draw(const SdArgs& a, const SdSync& y, int r,
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (P.bad || ld32c(y.flag)) {
         if (tid == 0) {
+            if (a.status)
+                atomicOr(a.status, (P.bad ? VMI_STATUS_BAD_LOGITS : 0u) | (ld32c(y.flag) ? VMI_STATUS_WAIT_GAVE_UP : 0u));
             if (a.accept) {
                 a.out[0] = 0; a.out[1] = 0; a.out[2] = 0; a.out[3] = -1;
             } else {
@@ -574,6 +581,7 @@ __device__ __forceinline__ void sd_draw(const SdArgs& a, const SdSync& y, int r,
 }
 
 __global__ __launch_bounds__(kSdThreads) void k_sd_fused(SdArgs a, SdSync y, int rows) {
+    if (a.offset_dev) a.offset += *a.offset_dev;
     __shared__ unsigned long long s_h[kBins];
     __shared__ unsigned long long s_red[kSdWaves];
     __shared__ float s_redf[kSdWaves];
@@ -604,7 +612,7 @@ __global__ __launch_bounds__(kSdThreads) void k_sd_fused(SdArgs a, SdSync y, int
         }
     }
     VMI_STAMP(d, 1);
-    sd_barrier(rc, (uint32_t)NB, y.go + 16 * NB * d, NB, b, 1u, y.flag);
+    sd_barrier(rc, (uint32_t)NB, y.go + 16 * NB * d, NB, b, 1u, y.flag, y.spin_limit);
     VMI_STAMP(d, 2);
 
     // 2. masses and the level-1 histogram
@@ -630,7 +638,7 @@ __global__ __launch_bounds__(kSdThreads) void k_sd_fused(SdArgs a, SdSync y, int
         flush_hist(s_h, h, kBins);
     }
     VMI_STAMP(d, 3);
-    sd_barrier(rc, 2u * NB, y.go + 16 * NB * d, NB, b, 2u, y.flag);
+    sd_barrier(rc, 2u * NB, y.go + 16 * NB * d, NB, b, 2u, y.flag, y.spin_limit);
     VMI_STAMP(d, 4);
 
     // 3. total mass, nucleus target, level-1 crossing; level-2 histogram
@@ -665,7 +673,7 @@ __global__ __launch_bounds__(kSdThreads) void k_sd_fused(SdArgs a, SdSync y, int
         }
     }
     VMI_STAMP(d, 5);
-    sd_barrier(rc, 3u * NB, y.go + 16 * NB * d, NB, b, 3u, y.flag);
+    sd_barrier(rc, 3u * NB, y.go + 16 * NB * d, NB, b, 3u, y.flag, y.spin_limit);
     VMI_STAMP(d, 6);
 
     // 4. level-2 crossing; level-3 histogram
@@ -694,7 +702,7 @@ __global__ __launch_bounds__(kSdThreads) void k_sd_fused(SdArgs a, SdSync y, int
         flush_hist(s_h, h + 2 * kBins, 1024);
     }
     VMI_STAMP(d, 7);
-    sd_barrier(rc, 4u * NB, y.go + 16 * NB * d, NB, b, 4u, y.flag);
+    sd_barrier(rc, 4u * NB, y.go + 16 * NB * d, NB, b, 4u, y.flag, y.spin_limit);
     VMI_STAMP(d, 8);
 
     // 5. the nucleus of distribution d (its workgroup 0), then the draws
@@ -727,7 +735,7 @@ __global__ __launch_bounds__(kSdThreads) void k_sd_fused(SdArgs a, SdSync y, int
     }
     VMI_STAMP(d, 9);
     if (d < rows) {
-        sd_wait(y.go + 16 * (NB * d + b), 5u, y.flag);
+        sd_wait(y.go + 16 * (NB * d + b), 5u, y.flag, y.spin_limit);
         VMI_STAMP(d, 10);
         sd_draw(a, y, d, b, s_h, s_red);
         VMI_STAMP(d, 11);
@@ -838,11 +846,31 @@ int sd_slices(int V) {
     return nb < 1 ? 1 : (nb > 128 ? 128 : nb);
 }
 
+// Workgroups of k_sd_fused one compute unit holds at once, from the
+// occupancy calculator (registers, LDS), at most two: the waits need every
+// workgroup of a launch resident, and a second one per CU leaves room for
+// other work on the device.  Queried once per device (re-entrant as
+// vmi::device_cus).
+int sd_resident_per_cu() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    const int known = cached[dev].load(std::memory_order_relaxed);
+    if (known > 0) return known;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_sd_fused, kSdThreads, 0) != hipSuccess || n < 1) n = 1;
+    if (n > 2) n = 2;
+    cached[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+// Bound of the kernel's co-residency waits (polls); vmi_set_wait_limit.
+std::atomic<int> g_sd_spin_limit{kSdSpinLimit};
+
 // Slices per row for a launch of nd distributions: every workgroup of the
-// launch must be resident at once (two per compute unit is well within the
-// kernel's registers and LDS), so NB * nd <= 2 * CUs.
+// launch must be resident at once, so NB * nd <= sd_resident_per_cu() * CUs.
 int sd_slices_resident(int V, int nd) {
-    int cap = 2 * vmi::device_cus() / nd;
+    int cap = sd_resident_per_cu() * vmi::device_cus() / nd;
     if (cap * nd > kSdMaxWgs) cap = kSdMaxWgs / nd;
     const int nb = sd_slices(V);
     return nb < cap ? nb : (cap < 1 ? 1 : cap);
@@ -859,6 +887,7 @@ hipError_t sd_launch(SdArgs& a, uint8_t* ws, int rows, hipStream_t s) {
     a.ctr_r = reinterpret_cast<uint32_t*>(ws + 64 * kMaxRows + 256);
     y.go = reinterpret_cast<uint32_t*>(ws + 64 * kMaxRows + 256 + kMaxRows * sizeof(uint32_t));
     y.rdone = reinterpret_cast<uint32_t*>(ws + 64 * kMaxRows + 256 + kMaxRows * sizeof(uint32_t) + 64 * kSdMaxWgs);
+    y.spin_limit = g_sd_spin_limit.load(std::memory_order_relaxed);
     hipLaunchKernelGGL(k_sd_fused, dim3(a.NB, a.nd), dim3(kSdThreads), 0, s, a, y, rows);
     return hipGetLastError();
 }
@@ -951,7 +980,8 @@ extern "C" size_t vmi_accept_stochastic_workspace_bytes(int K, int vocab, int ha
 
 extern "C" int vmi_accept_stochastic(const float* target_logits, const float* draft_logits, const int32_t* drafts,
                                      int K, int vocab, float temperature, float top_p, uint64_t seed, uint64_t offset,
-                                     int32_t* result, void* workspace, size_t workspace_bytes, void* stream) {
+                                     const uint64_t* offset_device, int32_t* result, void* workspace,
+                                     size_t workspace_bytes, uint32_t* status, void* stream) {
     vmi::clear_error();
     if (K <= 0 || K > kMaxK) return vmi::fail(VMI_ERR_UNSUPPORTED, "K=%d must be in [1, %d]", K, kMaxK);
     if (vocab <= 0 || vocab > (1 << 24)) return vmi::fail(VMI_ERR_INVALID, "vocab=%d", vocab);
@@ -968,6 +998,7 @@ extern "C" int vmi_accept_stochastic(const float* target_logits, const float* dr
     a.base0 = target_logits; a.n0 = K + 1; a.base1 = draft_logits;
     a.nd = nd; a.V = vocab; a.NB = NB; a.chunk = (vocab + NB - 1) / NB;
     a.s2 = sd_scale(temperature); a.top_p = top_p; a.seed = seed; a.offset = offset;
+    a.offset_dev = offset_device; a.status = status;
     a.accept = 1; a.K = K; a.has_q = draft_logits != nullptr; a.drafts = drafts;
     a.out = result;
     sd_bind(a, static_cast<uint8_t*>(workspace), L);
@@ -981,8 +1012,8 @@ extern "C" size_t vmi_sample_top_p_workspace_bytes(int rows, int vocab) {
 }
 
 extern "C" int vmi_sample_top_p(const float* logits, int rows, int vocab, float temperature, float top_p,
-                                uint64_t seed, uint64_t offset, int32_t* out, void* workspace, size_t workspace_bytes,
-                                void* stream) {
+                                uint64_t seed, uint64_t offset, const uint64_t* offset_device, int32_t* out,
+                                void* workspace, size_t workspace_bytes, uint32_t* status, void* stream) {
     vmi::clear_error();
     if (rows <= 0 || rows > kMaxRows) return vmi::fail(VMI_ERR_UNSUPPORTED, "rows=%d must be in [1, %d]", rows, kMaxRows);
     if (vocab <= 0 || vocab > (1 << 24)) return vmi::fail(VMI_ERR_INVALID, "vocab=%d", vocab);
@@ -997,6 +1028,7 @@ extern "C" int vmi_sample_top_p(const float* logits, int rows, int vocab, float 
     a.base0 = logits; a.n0 = rows; a.base1 = nullptr;
     a.nd = rows; a.V = vocab; a.NB = NB; a.chunk = (vocab + NB - 1) / NB;
     a.s2 = sd_scale(temperature); a.top_p = top_p; a.seed = seed; a.offset = offset;
+    a.offset_dev = offset_device; a.status = status;
     a.accept = 0; a.K = 0; a.has_q = 0; a.drafts = nullptr;
     a.out = out;
     sd_bind(a, static_cast<uint8_t*>(workspace), L);
@@ -1010,3 +1042,9 @@ extern "C" int vmi_timeline_set_accept(void* buf) {
     return hipMemcpyToSymbol(HIP_SYMBOL(vmi_tl_buf), &buf, sizeof(buf)) == hipSuccess ? VMI_OK : VMI_ERR_HIP;
 }
 #endif
+
+extern "C" int vmi_set_wait_limit(int polls) {
+    const int prev = g_sd_spin_limit.load(std::memory_order_relaxed);
+    g_sd_spin_limit.store(polls > 0 ? polls : kSdSpinLimit, std::memory_order_relaxed);
+    return prev;
+}

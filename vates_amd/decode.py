@@ -13,6 +13,10 @@
   the MTP cache with the accepted positions (drafter.py:178-188).
 * ``greedy_decode`` is the non-speculative reference the speculative loop must
   reproduce token for token (test_mtp_generate.py:421-489).
+* With a ``Sampling`` the same loop decodes stochastically (speculative
+  sampling; the reference has only the greedy loop): drafts sampled from the
+  MTP layer's temperature / top-p distributions, accepted or replaced by
+  ``vmi_accept_stochastic`` against the verify rows' distributions.
 
 Each decoder layer runs full attention or the Gated DeltaNet block (or
 neither), then the MoE block.
@@ -28,7 +32,7 @@ import numpy as np
 import torch
 
 from ._lib import VmiError, check, load
-from .accept import accept_greedy, spec_commit
+from .accept import accept_greedy, accept_stochastic, raise_sampling_status, sample_top_p, spec_commit
 from .attention import AttentionLayer, KVCache
 from .gdn import GatedDeltaNetLayer, GdnCache
 from .head import lm_head
@@ -51,11 +55,33 @@ class DecodeStats:
     depths: List[int] = field(default_factory=list)        # drafts verified per step (adaptive depth)
     rescues: List[int] = field(default_factory=list)       # tree decoding: the winning path per step
     drafts: List[List[int]] = field(default_factory=list)  # the drafts of each step (with trace=True)
+    samples: List[dict] = field(default_factory=list)      # stochastic steps with trace=True: logits, drafts, record
     seconds: float = 0.0
 
     @property
     def avg_accept_len(self) -> float:
         return (sum(self.accept_hist) / len(self.accept_hist) + 1.0) if self.accept_hist else 0.0
+
+
+@dataclass(frozen=True)
+class Sampling:
+    """Stochastic speculative decoding (speculative sampling, Leviathan et al.
+    2023; no counterpart in the reference, whose loop is greedy): the K drafts
+    are sampled from the MTP layer's temperature / top-p distributions
+    (vmi_sample_top_p), the verify rows' distributions accept or replace them
+    (vmi_accept_stochastic), and vmi_spec_commit commits the record as in the
+    greedy loop.  Step s of a run draws with Philox key `seed` and counter
+    offsets 64 (first_step + s) + i for draft i and 64 (first_step + s) + 63
+    for the acceptance, so every draw of a run has its own counter."""
+    temperature: float
+    top_p: float = 1.0
+    seed: int = 0
+    first_step: int = 0
+
+    ACCEPT_OFFSET = 63
+
+    def step_base(self, step: int) -> int:
+        return 64 * (self.first_step + step)
 
 
 class SpecModel:
@@ -71,11 +97,13 @@ class SpecModel:
                 l.gdn.new_cache(max_batch) if l.gdn is not None else None for l in self.layers]
 
     def forward(self, ids: torch.Tensor, caches: list, pos0: int, *, want_logits: bool = False,
-                pos_device: Optional[torch.Tensor] = None, hidden_out: Optional[torch.Tensor] = None):
+                pos_device: Optional[torch.Tensor] = None, hidden_out: Optional[torch.Tensor] = None,
+                logits_out: Optional[torch.Tensor] = None):
         """ids int32 [T] on the device at positions pos0.. (or at the position
         held by pos_device, int32 [1] on the device); returns (argmax int32 [T],
         pre-norm hidden bf16 [T, H], logits f32 [T, V] or None).  hidden_out
-        (bf16 [T, H], optional): where the last layer writes the hidden."""
+        (bf16 [T, H], optional): where the last layer writes the hidden;
+        logits_out (f32 [T, V], optional): where the head writes the logits."""
         x = rmsnorm(self.embed, None, ids=ids)
         last = len(self.layers) - 1
         for i, (layer, cache) in enumerate(zip(self.layers, caches)):
@@ -84,7 +112,8 @@ class SpecModel:
             elif layer.gdn is not None:
                 x = layer.gdn(x, cache, pos0=pos0, pos_device=pos_device)
             x = layer.moe(x, residual=x, out=hidden_out if i == last else None)
-        logits, am, _ = lm_head(x, self.head, self.final_norm, eps=self.eps, want_logits=want_logits)
+        logits, am, _ = lm_head(x, self.head, self.final_norm, eps=self.eps,
+                                want_logits=want_logits or logits_out is not None, logits=logits_out)
         return am, x, logits
 
     def forward_tree(self, ids: torch.Tensor, caches: list, pos0: int, paths: int, *, want_logits: bool = False,
@@ -220,8 +249,10 @@ def _check_layout(layout: str, tau: Optional[float]) -> None:
 
 def speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: torch.Tensor, H_last: torch.Tensor,
                        pos: int, n_tokens: int, K: int = 3, *, layout: str = "k+1",
-                       tau: Optional[float] = None, trace: bool = False) -> DecodeStats:
-    """K-draft MTP decoding with greedy acceptance.
+                       tau: Optional[float] = None, trace: bool = False,
+                       sampling: Optional[Sampling] = None) -> DecodeStats:
+    """K-draft MTP decoding with greedy acceptance (or, with `sampling`,
+    stochastic: see ``Sampling``; layout "k+1" at a fixed depth).
 
     layout "k+1": the verify batch is [x, d1..dK] (T = K + 1): every draft is
     checked and the model's token after the last accepted one is emitted, so
@@ -238,18 +269,32 @@ def speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: torch.T
     x: the last emitted token [1] (not yet run through the model) at position
     `pos`; H_last: the model's pre-norm hidden at pos - 1 [1, H]; the MTP cache
     holds every committed position before pos.  trace: record each step's
-    drafts (one more host read per step).
+    drafts (one more host read per step; stochastic steps also keep their
+    target and draft logits and record in ``samples``).  A stochastic step
+    whose acceptance fails (record [0, 0, 0, -1]: a wait of the sampling
+    kernels gave up, or a logit row had no finite value) raises VmiError.
     """
     if model.mtp is None:
         raise VmiError("the model has no MTP layer")
     _check_layout(layout, tau)
+    if sampling is not None and (layout != "k+1" or tau is not None):
+        raise VmiError("stochastic decoding verifies [x, d1..dK] (layout 'k+1') at a fixed depth")
     st = DecodeStats()
     dev = x.device
     verify = torch.empty(K + 1, dtype=torch.int32, device=dev)
+    if sampling is not None:
+        V = model.head.shape[0]
+        dlog = torch.empty((K, V), dtype=torch.float32, device=dev)
+        tlog = torch.empty((K + 1, V), dtype=torch.float32, device=dev)
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
     t0 = time.perf_counter()
     while len(st.tokens) < n_tokens:
         mtp_start = drafter.cache.length
-        if tau is not None:
+        if sampling is not None:
+            base = sampling.step_base(st.steps)
+            drafts = drafter.draft_sampled(H_last, x, K, temperature=sampling.temperature, top_p=sampling.top_p,
+                                           seed=sampling.seed, offset=base, logits_out=dlog, status=status)
+        elif tau is not None:
             drafts = drafter.draft_adaptive(H_last, x, K, tau)
         else:
             drafts = drafter.draft(H_last, x, K)
@@ -257,9 +302,21 @@ def speculative_decode(model: SpecModel, drafter: MTPDrafter, caches, x: torch.T
         T = d + 1 if layout == "k+1" else d
         verify[0:1].copy_(x)
         verify[1:T].copy_(drafts[:T - 1])
-        preds, hid, _ = model.forward(verify[:T], caches, pos)
-        rec = accept_greedy(drafts, preds, mode=1 if layout == "k+1" else 0)
+        preds, hid, _ = model.forward(verify[:T], caches, pos, logits_out=tlog if sampling is not None else None)
+        if sampling is not None:
+            rec = accept_stochastic(tlog, dlog, drafts, temperature=sampling.temperature, top_p=sampling.top_p,
+                                    seed=sampling.seed, offset=base + Sampling.ACCEPT_OFFSET, status=status)
+        else:
+            rec = accept_greedy(drafts, preds, mode=1 if layout == "k+1" else 0)
         r = rec.cpu().tolist()  # the step's one host synchronisation
+        if sampling is not None:
+            bits = int(status.item())
+            raise_sampling_status(bits, f"stochastic decode step {st.steps}")
+            if r[3] < 0:
+                raise VmiError(f"stochastic decode step {st.steps}: acceptance failed (record {r[:4]})")
+            if trace:
+                st.samples.append({"offset": base, "target": tlog.cpu().numpy(), "draft": dlog.cpu().numpy(),
+                                   "drafts": drafts.cpu().tolist(), "record": r})
         n, m, acc = r[0], r[1], r[2]
         emitted = r[4:4 + n]
         commit_verified_prefix(caches, T, acc)
@@ -378,11 +435,18 @@ class GraphSpecDecoder:
     reads each draft's probability to choose the depth, as the reference's
     draft_adaptive does (drafter.py:42-62).  Results equal
     ``speculative_decode`` token for token (the kernels' results do not depend
-    on batch composition).
+    on batch composition).  With `sampling` (``Sampling``; layout "k+1", fixed
+    depth) each draft step samples its token (vmi_sample_top_p into the verify
+    row, the step's logits kept as the draft distribution), the verify
+    computes the target logits and vmi_accept_stochastic the record; the
+    counter offsets come from a device word that the step advances by 64, so
+    replays draw what ``speculative_decode`` with the same Sampling draws.  A
+    failed acceptance (record [0, 0, 0, -1]) raises VmiError when the host
+    reads that step's record.
     """
 
     def __init__(self, model: SpecModel, drafter: MTPDrafter, caches: list, K: int = 3, planted: bool = False,
-                 layout: str = "k+1", tau: Optional[float] = None):
+                 layout: str = "k+1", tau: Optional[float] = None, sampling: Optional[Sampling] = None):
         """planted: the verify batch takes its drafts from ``self.planted``
         (int32 [K], written by the host before each replay) instead of the MTP
         layer's, which still runs and keeps its cache; for drafts from another
@@ -390,6 +454,9 @@ class GraphSpecDecoder:
         if model.mtp is None:
             raise VmiError("the model has no MTP layer")
         _check_layout(layout, tau)
+        if sampling is not None and (layout != "k+1" or tau is not None or planted):
+            raise VmiError("stochastic decoding verifies [x, d1..dK] (layout 'k+1') at a fixed depth, unplanted")
+        self.sampling = sampling
         self.model, self.drafter, self.caches, self.K = model, drafter, caches, K
         self.layout, self.tau = layout, tau
         dev = model.embed.device
@@ -413,6 +480,11 @@ class GraphSpecDecoder:
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         self.use_planted = planted
         self.planted = torch.zeros(K, dtype=torch.int32, device=dev)
+        if sampling is not None:
+            V = model.head.shape[0]
+            self.dlog = torch.zeros((K, V), dtype=torch.float32, device=dev)      # draft distributions
+            self.tlog = torch.zeros((K + 1, V), dtype=torch.float32, device=dev)  # verify distributions
+            self.rng = torch.full((1,), sampling.step_base(0), dtype=torch.int64, device=dev)
         self.stream = torch.cuda.Stream(device=dev)
         self.graph = None        # fixed depth: the whole step
         self.draft_graphs = []   # adaptive: one per draft step
@@ -421,6 +493,13 @@ class GraphSpecDecoder:
 
     def _draft(self, i: int, h: torch.Tensor) -> torch.Tensor:
         tok = self.x if i == 0 else self.drafts[i - 1:i]
+        sp = self.sampling
+        if sp is not None:
+            _, hn, _ = self.model.mtp.step(h, tok, self.drafter.cache, pos_device=self.mtp_pos[i:i + 1],
+                                           logits_out=self.dlog[i:i + 1])
+            sample_top_p(self.dlog[i:i + 1], temperature=sp.temperature, top_p=sp.top_p, seed=sp.seed, offset=i,
+                         offset_device=self.rng, out=self.drafts[i:i + 1], status=self.status)
+            return hn
         _, hn, _ = self.model.mtp.step(h, tok, self.drafter.cache, pos_device=self.mtp_pos[i:i + 1],
                                        argmax_out=self.drafts[i:i + 1], prob_out=self.probs[i:i + 1])
         return hn
@@ -431,11 +510,19 @@ class GraphSpecDecoder:
         mtp = self.model.mtp
         if self.use_planted:
             self.drafts[:d].copy_(self.planted[:d])
+        sp = self.sampling
         preds, hid, _ = self.model.forward(self.verify[:T], self.caches, 0, pos_device=self.pos,
-                                           hidden_out=self.hrows[:T])
-        rec = accept_greedy(self.drafts[:d], preds, mode=1 if self.layout == "k+1" else 0, out=self.rec_buf)
+                                           hidden_out=self.hrows[:T], logits_out=self.tlog[:T] if sp else None)
+        if sp is not None:
+            rec = accept_stochastic(self.tlog[:T], self.dlog[:d], self.drafts[:d], temperature=sp.temperature,
+                                    top_p=sp.top_p, seed=sp.seed, offset=Sampling.ACCEPT_OFFSET,
+                                    offset_device=self.rng, out=self.rec_buf, status=self.status)
+        else:
+            rec = accept_greedy(self.drafts[:d], preds, mode=1 if self.layout == "k+1" else 0, out=self.rec_buf)
         mtp.advance(self.hseq[:T], self.verify[:T], self.drafter.cache, pos_device=self.mtp_len)
         spec_commit(rec, hid, self.H, self.x, self.pos, self.mtp_len, self.mtp_pos, rows=T, status=self.status)
+        if sp is not None:
+            self.rng.add_(64)
         return rec
 
     def _step(self) -> torch.Tensor:
@@ -463,7 +550,8 @@ class GraphSpecDecoder:
     def capture(self) -> None:
         """Warms the workspaces up on the capture stream (every shape the
         graphs use), restores the state, and captures."""
-        live = (self.state, self.x, self.H, self.mtp_pos)
+        live = (self.state, self.x, self.H, self.mtp_pos, self.status) + \
+            ((self.rng,) if self.sampling is not None else ())
         saved = [t.clone() for t in live]
         self.stream.wait_stream(torch.cuda.current_stream(self.dev))
         # each warm-up starts from the saved state, so none writes a ring slot
@@ -521,6 +609,10 @@ class GraphSpecDecoder:
 
         def take(r):
             nonlocal pos
+            if r[3] < 0:
+                bits = int(self.status.item())
+                raise_sampling_status(bits, f"graph decode step {st.steps}")
+                raise VmiError(f"graph decode step {st.steps}: acceptance failed (record {r[:4]}, status {bits:#x})")
             n, m = r[0], r[1]
             pos += r[2]
             st.tokens.extend(r[4:4 + n])
@@ -564,8 +656,10 @@ class GraphSpecDecoder:
         st.seconds = time.perf_counter() - t0
         st.tokens = st.tokens[:n_tokens]
         pos, mtp_len = self.state.cpu().tolist()
-        if int(self.status.item()):
-            raise VmiError(f"device status {int(self.status.item()):#x}: an acceptance record was out of range")
+        bits = int(self.status.item())
+        if bits:
+            raise_sampling_status(bits, "graph decode")
+            raise VmiError(f"device status {bits:#x}: an acceptance record was out of range")
         self.pos_host = pos
         for c in self.caches:
             if c is not None:

@@ -75,14 +75,15 @@ class MTPLayer:
 
     def step(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, *, want_logits: bool = False,
              stream=None, pos_device: Optional[torch.Tensor] = None, argmax_out: Optional[torch.Tensor] = None,
-             prob_out: Optional[torch.Tensor] = None):
+             prob_out: Optional[torch.Tensor] = None, logits_out: Optional[torch.Tensor] = None):
         """(argmax int32 [T], MTP hidden H bf16 [T, H], logits f32 [T, V] or None).
         With pos_device the cache position is read on the device; with
         argmax_out (int32 [T]) the argmax is written there; with prob_out
-        (f32 [T]) the softmax probability of the argmax."""
+        (f32 [T]) the softmax probability of the argmax; with logits_out
+        (f32 [T, V]) the logits are written there (want_logits implied)."""
         Hn = self._trunk(hidden, tokens, cache, stream, pos_device)
-        logits, am, _ = lm_head(Hn, self.w.lm_head, None, want_logits=want_logits, argmax=argmax_out,
-                                top_prob=prob_out, stream=stream)
+        logits, am, _ = lm_head(Hn, self.w.lm_head, None, want_logits=want_logits or logits_out is not None,
+                                logits=logits_out, argmax=argmax_out, top_prob=prob_out, stream=stream)
         return am, Hn, logits
 
     def advance(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None,
@@ -105,6 +106,31 @@ class MTPDrafter:
             drafts[i:i + 1].copy_(am)
             tok = drafts[i:i + 1]
         return drafts
+
+    def draft_sampled(self, H_last: torch.Tensor, x_tok: torch.Tensor, K: int, *, temperature: float,
+                      top_p: float, seed: int, offset: int, offset_device: Optional[torch.Tensor] = None,
+                      logits_out: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                      status: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """K drafts sampled from the MTP layer's own temperature / top-p
+        distributions (the stochastic counterpart of ``draft``, whose argmax is
+        the reference's drafter.py:20-40): draft i is vmi_sample_top_p of the
+        step's logits with counter offset `offset + i` (plus *offset_device).
+        logits_out (f32 [K, V]) keeps every step's logits, the draft
+        distributions q that stochastic acceptance needs; out (int32 [K])
+        receives the drafts; status as for ``sample_top_p``."""
+        from .accept import sample_top_p
+        dev = H_last.device
+        if logits_out is None:
+            logits_out = torch.empty((K, self.mtp.vocab), dtype=torch.float32, device=dev)
+        if out is None:
+            out = torch.empty(K, dtype=torch.int32, device=dev)
+        h, tok = H_last, x_tok
+        for i in range(K):
+            _, h, _ = self.mtp.step(h, tok, self.cache, logits_out=logits_out[i:i + 1])
+            sample_top_p(logits_out[i:i + 1], temperature=temperature, top_p=top_p, seed=seed, offset=offset + i,
+                         offset_device=offset_device, out=out[i:i + 1], status=status)
+            tok = out[i:i + 1]
+        return out
 
     def draft_adaptive(self, H_last: torch.Tensor, x_tok: torch.Tensor, depth_max: int, tau: float,
                        logits_out: Optional[list] = None) -> torch.Tensor:
