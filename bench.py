@@ -476,19 +476,22 @@ def decode_record(args) -> dict:
     `layers` decoder layers (full attention on every attn_every-th, Gated
     DeltaNet linear attention on the others, the 512-expert top-10 4-bit MoE
     with the shared expert on all), the MTP layer, bf16 embedding and head over
-    151,936 tokens.  The attention and MTP caches hold a `context`-token
-    synthetic context (random bf16 keys and values: decode speed does not
-    depend on their content).  Timed: `new_tokens` decoded tokens by graph
-    replays, wall clock, including drafting, verification, acceptance, commit
-    and the MTP cache update.  The same start state is then decoded greedily
-    (one token per graph replay, the like-for-like baseline) and the two token
-    streams are compared; drafts planted at a fixed agreement rate show the
-    acceptance-dependent speed."""
+    151,936 tokens.  A `context`-token synthetic prompt (random token ids) is
+    run through the model first, 8 tokens per forward, filling the attention
+    caches, the linear-attention states and the MTP cache.  Timed: `new_tokens`
+    decoded tokens by graph replays, wall clock, including drafting,
+    verification, acceptance, commit and the MTP cache update.  The same start
+    state is then decoded greedily (one token per graph replay, the
+    like-for-like baseline) and the two token streams are compared.  A
+    random-init MTP layer's argmax drafts almost never match the main model's,
+    so the greedy speculative run measures the cost of speculation with no
+    gain; drafts planted at a fixed agreement rate show the
+    acceptance-dependent speed, and a sampled run (temperature 0.7, top-p 0.9,
+    speculative sampling) the stochastic loop."""
     import torch
-    from vates_amd.attention import KVCache
-    from vates_amd.decode import GraphGreedyDecoder, GraphSpecDecoder, speculative_decode
+    from vates_amd.decode import GraphGreedyDecoder, GraphSpecDecoder, Sampling, speculative_decode
+    from vates_amd.gdn import GdnCache
     from vates_amd.mtp import MTPDrafter
-    from vates_amd.synth import synth_bf16
     from vates_amd.workload import synth_spec_model
 
     dev = torch.device("cuda:0")
@@ -501,23 +504,41 @@ def decode_record(args) -> dict:
     max_len = ctx + 2 * N + 4 * (K + 1) + 8
     caches = model.new_caches(max_len)
     drafter = MTPDrafter(model.mtp, max_len)
-    for i, c in enumerate(caches + [drafter.cache]):
-        if isinstance(c, KVCache):
-            c.write(0, synth_bf16(SEED, 0xCA000 + 2 * i, (c.k.shape[0], ctx, 256), device=dev),
-                    synth_bf16(SEED, 0xCA001 + 2 * i, (c.v.shape[0], ctx, 256), device=dev))
-    x0 = torch.tensor([4242], dtype=torch.int32, device=dev)
-    h0 = synth_bf16(SEED, 0xCA0FF, (1, args.hidden), device=dev)
     torch.cuda.synchronize()
     eprint(f"[bench] decode model resident: {torch.cuda.memory_allocated() / 2**30:.1f} GiB in {time.time() - t0:.1f} s")
+    prompt = torch.from_numpy(np.random.default_rng(SEED).integers(0, args.vocab, ctx).astype(np.int32)).to(dev)
+    t1 = time.time()
+    # the prompt through the model 8 tokens per forward (as decode.prefill),
+    # then the MTP cache over its (hidden, next token) pairs; a line every
+    # 4,096 tokens
+    hs, am = [], None
+    for s0 in range(0, ctx, 8):
+        am, h, _ = model.forward(prompt[s0:s0 + 8], caches, s0)
+        hs.append(h)
+        if (s0 + 8) % 4096 == 0 or s0 + 8 >= ctx:
+            torch.cuda.synchronize()
+            eprint(f"[bench] prompt prefill: {min(ctx, s0 + 8)} of {ctx} tokens, {time.time() - t1:.1f} s")
+    hid = torch.cat(hs)
+    drafter.cache.length = 0
+    for s0 in range(0, ctx - 1, 8):
+        e = min(ctx - 1, s0 + 8)
+        drafter.mtp.advance(hid[s0:e].contiguous(), prompt[s0 + 1:e + 1].contiguous(), drafter.cache)
+        if (s0 + 8) % 8192 == 0:
+            torch.cuda.synchronize()
+            eprint(f"[bench] MTP cache: {e} of {ctx - 1} positions, {time.time() - t1:.1f} s")
+    x0, h0 = am[-1:].clone(), hid[-1:].clone()
+    del hs, hid
+    torch.cuda.synchronize()
+    eprint(f"[bench] prompt of {ctx} tokens run through the model and the MTP layer in {time.time() - t1:.1f} s")
+    saved = [(c.conv.clone(), c.state.clone()) if isinstance(c, GdnCache) else None for c in caches]
 
     def reset():
-        for c in caches:
-            if isinstance(c, KVCache):
+        for c, sv in zip(caches, saved):
+            if c is not None:
                 c.length = ctx
-            elif c is not None:  # linear-attention rings hold only recent positions: restart from zero state
-                c.conv.zero_()
-                c.state.zero_()
-                c.length = ctx
+            if sv is not None:  # the linear-attention rings as the prompt left them
+                c.conv.copy_(sv[0])
+                c.state.copy_(sv[1])
         drafter.cache.length = ctx - 1
 
     # distinct experts of every MoE call of one step, traced on an eager step
@@ -573,6 +594,12 @@ def decode_record(args) -> dict:
     ad_same = ad.tokens == truth[:N]
     eprint(f"[bench] decode (graph, adaptive depth tau={args.tau}, T=K layout): {ad_tps:.1f} tokens/s, "
            f"depths {[ad.depths.count(d) for d in range(1, K + 1)]}, equals greedy: {ad_same}")
+    smp = graph_spec(sampling=Sampling(0.7, 0.9, SEED))
+    smp_tps = N / smp.seconds
+    smp_hist = [smp.accept_hist.count(m) for m in range(K + 1)]
+    eprint(f"[bench] decode (graph, sampled: temperature 0.7, top-p 0.9): {smp_tps:.1f} tokens/s, "
+           f"{smp.steps} steps, {smp.seconds * 1e3 / smp.steps:.3f} ms per step, avg accept len "
+           f"{smp.avg_accept_len:.2f}, matched histogram {smp_hist}")
     hist = [st.accept_hist.count(m) for m in range(K + 1)]
     achieved = step_bytes["total"] / (ms_step * 1e-3) / 1e9
     cpu = cpu1 = None
@@ -584,23 +611,33 @@ def decode_record(args) -> dict:
     del model, caches, drafter
     torch.cuda.empty_cache()
     return {
-        "metric": "K=3 MTP decode tokens/s", "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,
+        "metric": f"K=3 MTP decode tokens/s (greedy, random-init MTP drafts: avg accept len "
+                  f"{st.avg_accept_len:.2f}, {tps / gr_tps:.3f}x greedy decoding)",
+        "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1,
         "steps": st.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "u4 experts/projections, bf16 head and KV, f32 accumulate", "data": "synthetic",
         "config": {"workload": f"{args.layers}-layer random-init Qwen3-Next-shaped model ({args.layers // args.attn_every}"
                                f" full-attention and {args.layers - args.layers // args.attn_every} Gated DeltaNet "
                                f"layers, every layer MoE 512x top-{args.top_k} + shared expert), MTP K={K}, "
-                               f"{N} new tokens after a {ctx}-token synthetic context, vocab {args.vocab}",
+                               f"{N} new tokens after a {ctx}-token synthetic prompt, vocab {args.vocab}",
                    "step": "one HIP graph replay per step, verify [x, d1..dK]",
                    "accept_hist": hist, "avg_accept_len": round(st.avg_accept_len, 3),
                    "speculative_equals_greedy": same, "first_divergence": first_diff,
                    "greedy_graph_tokens_per_s": round(gr_tps, 2),
+                   "spec_over_greedy": round(tps / gr_tps, 4),
                    "planted_agreement": args.plant_rate, "planted_tokens_per_s": round(sp_tps, 2),
+                   "planted_over_greedy": round(sp_tps / gr_tps, 4),
                    "planted_avg_accept_len": round(sp.avg_accept_len, 3), "planted_equals_greedy": sp_same,
                    "adaptive_tau": args.tau, "adaptive_tokens_per_s": round(ad_tps, 2),
                    "adaptive_depths": [ad.depths.count(d) for d in range(1, K + 1)],
-                   "adaptive_equals_greedy": ad_same},
+                   "adaptive_equals_greedy": ad_same,
+                   "sampled": {"temperature": 0.7, "top_p": 0.9, "seed": SEED, "tokens_per_s": round(smp_tps, 2),
+                               "ms_per_step": round(smp.seconds * 1e3 / smp.steps, 4),
+                               "avg_accept_len": round(smp.avg_accept_len, 3), "accept_hist": smp_hist,
+                               "over_greedy": round(smp_tps / gr_tps, 4),
+                               "step": "sampled MTP drafts (vmi_sample_top_p), verify, vmi_accept_stochastic, "
+                                       "vmi_spec_commit: one HIP graph replay"}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                      "unit_of_work": "one speculative step (K MTP drafts, verify of K+1 tokens, MTP update)",
