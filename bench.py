@@ -170,18 +170,17 @@ def measure_stream_peak(mib: int = 4096, reps: int = 10) -> dict:
         fold = torch.bitwise_xor(fold[:h], fold[h:])
     want = int(fold.cpu().numpy().view(np.uint32)[0])
     del fold
-    sink = torch.zeros(1, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.zeros(cus * 16, dtype=torch.int32, device=dev)
     results = {}
     for nt in (1, 0):
         for per_cu in (1, 2, 4, 8, 16):
             wgs = cus * per_cu
-            sink.zero_()
             check(lib.vmi_stream_read(buf.data_ptr(), buf.numel() * 4, nt, wgs, sink.data_ptr(), stream),
                   "vmi_stream_read")
             torch.cuda.synchronize()
-            if int(sink.cpu().numpy().view(np.uint32)[0]) != want:
+            if int(np.bitwise_xor.reduce(sink[:wgs].cpu().numpy().view(np.uint32))) != want:
                 raise RuntimeError(f"vmi_stream_read checksum mismatch (nt={nt}, workgroups={wgs})")
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record()

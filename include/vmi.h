@@ -557,9 +557,9 @@ int vmi_synth_bf16(uint64_t seed, uint32_t stream_id, int64_t n, float scale, ui
  * benchmark reports beside the published peaks.
  * vmi_stream_read reads bytes at src once with 16-byte loads (nontemporal
  * loads when nontemporal != 0), `workgroups` workgroups of 256 lanes each
- * striding over 32 KB chunks, and XORs every 32-bit word of the buffer into
- * *sink (the caller zeroes it first; the result is the XOR of all words).
- * src 16-byte aligned, bytes a non-zero multiple of 16.
+ * striding over 32 KB chunks; workgroup g stores the XOR of the 32-bit words
+ * it read to sink[g] (uint32 [workgroups]), so the XOR of sink is the XOR of
+ * the whole buffer.  src 16-byte aligned, bytes a non-zero multiple of 16.
  * vmi_mfma_peak runs `workgroups` workgroups of four waves; each wave issues
  * iters rounds of four independent v_mfma_f32_16x16x32_f16 of 16,384 flops
  * each (16 * iters * 16,384 dense flops per workgroup), and workgroup g

@@ -1,9 +1,9 @@
 """The measurement kernels behind the benchmark's measured ceilings.
 
-vmi_stream_read must read every byte it is given: its XOR of all 32-bit words
-equals numpy's, for nontemporal and cached loads, with a tail that is not a
-whole 32 KB chunk.  vmi_mfma_peak's checksum equals the product the MFMA lane
-layout defines (lane l supplies A[l % 16][8 (l / 16) + s] and
+vmi_stream_read must read every byte it is given: the XOR of its per-workgroup
+words equals numpy's XOR of the buffer, for nontemporal and cached loads, with
+a tail that is not a whole 32 KB chunk.  vmi_mfma_peak's checksum equals the
+product the MFMA lane layout defines (lane l supplies A[l % 16][8 (l / 16) + s] and
 B[8 (l / 16) + s][l % 16], and holds D[4 (l / 16) + e][l % 16]), built here
 from that layout with numpy: a wrong operand order or layout fails it.
 """
@@ -31,11 +31,12 @@ def test_stream_read_reads_every_word(gpu):
         for nt in (1, 0):
             for wgs in (1, 7, 512):
                 log(f"case: stream_read bytes={nbytes} nt={nt} workgroups={wgs}")
-                sink = torch.zeros(1, dtype=torch.int32, device=gpu)
+                sink = torch.full((wgs,), -1, dtype=torch.int32, device=gpu)
                 check(lib.vmi_stream_read(buf.data_ptr(), nbytes, nt, wgs, sink.data_ptr(),
                                           torch.cuda.current_stream().cuda_stream), "vmi_stream_read")
                 torch.cuda.synchronize()
-                assert int(sink.cpu().numpy().view(np.uint32)[0]) == int(np.bitwise_xor.reduce(host))
+                got = int(np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)))
+                assert got == int(np.bitwise_xor.reduce(host))
 
 
 def test_stream_read_rejects_bad_arguments(gpu):

@@ -15,7 +15,8 @@ constexpr size_t kChunk = (size_t)kThreads * kUnroll;  // 16-byte units per work
 // chunk, load u of lane t reads unit u * 256 + t, so every wave load is 1 KB
 // of contiguous memory.  Nontemporal loads mark the lines for early eviction,
 // as the MoE kernels' weight streams do.  Every 32-bit word is XORed into one
-// value per wave, which one atomic folds into *sink.
+// value per workgroup, stored to sink[blockIdx.x] (a plain store: atomics on
+// one shared word would serialise at the L2 and cost microseconds per launch).
 template <bool NT>
 __global__ __launch_bounds__(kThreads) void k_stream_read(const vmi_u4* __restrict__ src, size_t n16,
                                                           uint32_t* __restrict__ sink) {
@@ -35,10 +36,18 @@ __global__ __launch_bounds__(kThreads) void k_stream_read(const vmi_u4* __restri
     // the tail (n16 not a multiple of the chunk): workgroup 0 alone
     if (blockIdx.x == 0)
         for (size_t i = full * kChunk + threadIdx.x; i < n16; i += kThreads) acc ^= src[i];
+    __shared__ uint32_t s_x[kThreads / VMI_WAVE];
     uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
-    if ((threadIdx.x & (VMI_WAVE - 1)) == 0) atomicXor(sink, x);
+    if ((threadIdx.x & (VMI_WAVE - 1)) == 0) s_x[threadIdx.x / VMI_WAVE] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < kThreads / VMI_WAVE; ++i) w ^= s_x[i];
+        sink[blockIdx.x] = w;
+    }
 }
 
 // Four independent accumulation chains per wave keep the matrix core busy
