@@ -32,6 +32,17 @@ def test_commit_kv_trim_known_answer():
 
 
 def test_commit_checkpoint_known_answer():
+    """The reference's checkpoint commit (kv_cache.py:222-251) on its own
+    fixture, translated to the rings: the reference keeps, per verified token
+    j, a (conv window, state) checkpoint and restores token acc-1's; here
+    token j's conv input is ring row (pos0 + j) % 32 and the state after it is
+    state slot (pos0 + j + 1) % n_slots, so committing is setting the length to
+    pos0 + acc.  The state before that length must be the fixture's state sum
+    (80 over its 4 elements), and the whole 3-row conv window before it must be
+    the rows of positions pos0 + acc - 3 .. pos0 + acc - 1: the row before the
+    batch (never written, zero), then tokens 0 and 1, the newest carrying the
+    fixture's conv sum (24 over its 12 elements).  (The fixture fills each
+    checkpoint uniformly, so only its newest row has a counterpart here.)"""
     import torch
     from vates_amd.decode import commit_verified_prefix
     from vates_amd.gdn import GdnCache
@@ -50,8 +61,10 @@ def test_commit_checkpoint_known_answer():
     st = c.state_before(c.length)
     assert torch.all(st == fx["sums_after"][1] / 4.0)          # 80 over the fixture's 4 elements
     rows = c.conv_rows(c.length)
+    assert tuple(rows.shape) == (3, c.conv_dim)
     assert torch.all(rows[-1] == fx["sums_after"][0] / 12.0)   # 24 over the fixture's 12 elements
     assert torch.all(rows[-2] == conv_vals[acc - 2])
+    assert acc == 2 and torch.all(rows[-3] == 0)               # position pos0 - 1: before the batch
 
 
 def test_commit_rejects_bad_lengths():
