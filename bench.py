@@ -507,28 +507,44 @@ def decode_record(args) -> dict:
     eprint(f"[bench] decode model resident: {torch.cuda.memory_allocated() / 2**30:.1f} GiB in {time.time() - t0:.1f} s")
     prompt = torch.from_numpy(np.random.default_rng(SEED).integers(0, args.vocab, ctx).astype(np.int32)).to(dev)
     t1 = time.time()
-    # the prompt through the model 8 tokens per forward (as decode.prefill),
-    # then the MTP cache over its (hidden, next token) pairs; a line every
-    # 4,096 tokens
-    hs, am = [], None
-    for s0 in range(0, ctx, 8):
-        am, h, _ = model.forward(prompt[s0:s0 + 8], caches, s0)
-        hs.append(h)
-        if (s0 + 8) % 4096 == 0 or s0 + 8 >= ctx:
-            torch.cuda.synchronize()
-            eprint(f"[bench] prompt prefill: {min(ctx, s0 + 8)} of {ctx} tokens, {time.time() - t1:.1f} s")
-    hid = torch.cat(hs)
-    drafter.cache.length = 0
-    for s0 in range(0, ctx - 1, 8):
-        e = min(ctx - 1, s0 + 8)
-        drafter.mtp.advance(hid[s0:e].contiguous(), prompt[s0 + 1:e + 1].contiguous(), drafter.cache)
-        if (s0 + 8) % 8192 == 0:
-            torch.cuda.synchronize()
-            eprint(f"[bench] MTP cache: {e} of {ctx - 1} positions, {time.time() - t1:.1f} s")
-    x0, h0 = am[-1:].clone(), hid[-1:].clone()
-    del hs, hid
-    torch.cuda.synchronize()
-    eprint(f"[bench] prompt of {ctx} tokens run through the model and the MTP layer in {time.time() - t1:.1f} s")
+    if args.synthetic_cache:
+        # profiling runs: random keys and values in the caches instead of the
+        # prompt's (a decode step's cost does not depend on the contents)
+        from vates_amd.attention import KVCache
+        from vates_amd.synth import synth_bf16
+        for i, c in enumerate(caches + [drafter.cache]):
+            if isinstance(c, KVCache):
+                c.write(0, synth_bf16(SEED, 0xCA000 + 2 * i, (c.k.shape[0], ctx, 256), device=dev),
+                        synth_bf16(SEED, 0xCA001 + 2 * i, (c.v.shape[0], ctx, 256), device=dev))
+            elif c is not None:
+                c.length = ctx
+        drafter.cache.length = ctx - 1
+        x0 = prompt[-1:].clone()
+        h0 = synth_bf16(SEED, 0xCA0FF, (1, args.hidden), device=dev)
+        eprint("[bench] synthetic cache contents (profiling run): the prompt was not run")
+    else:
+        # the prompt through the model 8 tokens per forward (as decode.prefill),
+        # then the MTP cache over its (hidden, next token) pairs; a line every
+        # 4,096 tokens
+        hs, am = [], None
+        for s0 in range(0, ctx, 8):
+            am, h, _ = model.forward(prompt[s0:s0 + 8], caches, s0)
+            hs.append(h)
+            if (s0 + 8) % 4096 == 0 or s0 + 8 >= ctx:
+                torch.cuda.synchronize()
+                eprint(f"[bench] prompt prefill: {min(ctx, s0 + 8)} of {ctx} tokens, {time.time() - t1:.1f} s")
+        hid = torch.cat(hs)
+        drafter.cache.length = 0
+        for s0 in range(0, ctx - 1, 8):
+            e = min(ctx - 1, s0 + 8)
+            drafter.mtp.advance(hid[s0:e].contiguous(), prompt[s0 + 1:e + 1].contiguous(), drafter.cache)
+            if (s0 + 8) % 8192 == 0:
+                torch.cuda.synchronize()
+                eprint(f"[bench] MTP cache: {e} of {ctx - 1} positions, {time.time() - t1:.1f} s")
+        x0, h0 = am[-1:].clone(), hid[-1:].clone()
+        del hs, hid
+        torch.cuda.synchronize()
+        eprint(f"[bench] prompt of {ctx} tokens run through the model and the MTP layer in {time.time() - t1:.1f} s")
     saved = [(c.conv.clone(), c.state.clone()) if isinstance(c, GdnCache) else None for c in caches]
 
     def reset():
@@ -619,7 +635,9 @@ def decode_record(args) -> dict:
         "config": {"workload": f"{args.layers}-layer random-init Qwen3-Next-shaped model ({args.layers // args.attn_every}"
                                f" full-attention and {args.layers - args.layers // args.attn_every} Gated DeltaNet "
                                f"layers, every layer MoE 512x top-{args.top_k} + shared expert), MTP K={K}, "
-                               f"{N} new tokens after a {ctx}-token synthetic prompt, vocab {args.vocab}",
+                               f"{N} new tokens after a {ctx}-token synthetic prompt"
+                               f"{' (cache contents synthetic, prompt not run)' if args.synthetic_cache else ''}, "
+                               f"vocab {args.vocab}",
                    "step": "one HIP graph replay per step, verify [x, d1..dK]",
                    "accept_hist": hist, "avg_accept_len": round(st.avg_accept_len, 3),
                    "speculative_equals_greedy": same, "first_divergence": first_diff,
@@ -769,6 +787,8 @@ def main() -> int:
     ap.add_argument("--attn-every", type=int, default=4)
     ap.add_argument("--tau", type=float, default=0.3, help="decode: adaptive-depth confidence threshold")
     ap.add_argument("--no-decode", action="store_true", help="default path: skip the decode record")
+    ap.add_argument("--synthetic-cache", action="store_true",
+                    help="decode: random cache contents instead of running the prompt (profiling runs)")
     ap.add_argument("--no-ceiling", action="store_true",
                     help="default path: skip the latency pass and the measured read ceiling (counter passes)")
     ap.add_argument("--vocab", type=int, default=151936)

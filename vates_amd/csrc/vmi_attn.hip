@@ -864,6 +864,13 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
 // 8..15 against the odd one, so one MFMA covers both groups and each D lane
 // applies its own group's scale:  y = sum_g s_g D_g + (b_g - 128 s_g) X_g with
 // X_g the group sum of x.  A token's result does not depend on the batch.
+// 8 bf16 values in MFMA operand order: pairs (e, e + 4), the order in which
+// vmi_unpack_u4_bf16_128 yields a word's nibbles.
+__device__ __forceinline__ uint4 qg_operand_order(const vmi_u4& u) {
+    return make_uint4(__builtin_amdgcn_perm(u[2], u[0], 0x05040100u), __builtin_amdgcn_perm(u[2], u[0], 0x07060302u),
+                      __builtin_amdgcn_perm(u[3], u[1], 0x05040100u), __builtin_amdgcn_perm(u[3], u[1], 0x07060302u));
+}
+
 constexpr int kQ4Waves = 8;
 constexpr int kQ4Threads = 64 * kQ4Waves;
 constexpr int kQ4Kw = 512;  // columns per wave
@@ -883,13 +890,13 @@ constexpr int kQ4MaxK = 2048;  // widest K the NORM form stages
 template <bool NORM, int RT>
 __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     static_assert(RT == 8 || RT == 16, "row tile");
-    __shared__ float s_X[kQ4Waves][kQgMaxT][8];       // group sums of x per wave: [token][group of the wave]
     __shared__ float s_part[kQ4Waves][16][kQgMaxT];
     const int T = a.T, K = a.K, G = K / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = at_wave();
     const int nl = lane & 15, q4 = lane >> 4;
-    VMI_STAMP(3, 0);
-    VMI_STAMP_HWID(3, 4);
+    constexpr int kid = NORM ? 3 : 2;  // timeline kernel id of the form
+    VMI_STAMP(kid, 0);
+    VMI_STAMP_HWID(kid, 4);
     // every argument read below in SGPRs at once: one wait for the argument
     // block (fields read lazily, under the matrix branches, cost a round trip
     // each before the first load could issue)
@@ -979,25 +986,30 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     const uint32_t res0 = vmi_bload_b16(
         rres, tid < nout && row0 < a.nrows ? (uint32_t)(((size_t)(tid % T) * a.out_stride + row0) * 2) : VMI_OOB, 0);
     asm volatile("" ::: "memory");
+    VMI_STAMP(kid, 5);
     if constexpr (!NORM) {
         // the wave's slice into its own LDS rows (padded by 16 bytes against
         // bank conflicts between tokens); the same wave reads it back in
         // operand order below
-        __shared__ uint4 s_xw[kQ4Waves][kQgMaxT][kQ4Kw / 8 + 1];
+        // (row kQgMaxT stays zero: the operand row of lanes outside the batch)
+        __shared__ uint4 s_xw[kQ4Waves][kQgMaxT + 1][kQ4Kw / 8 + 1];
+        s_xw[w][kQgMaxT][lane] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
         for (int i = 0; i < kQgMaxT; ++i)
-            if (i < T) s_xw[w][i][lane] = make_uint4(xv[i][0], xv[i][1], xv[i][2], xv[i][3]);
+            if (i < T) s_xw[w][i][lane] = qg_operand_order(xv[i]);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        xr = &s_xw[w][xreal ? tk : 0][4 * q4];
+        xr = &s_xw[w][xreal ? tk : kQgMaxT][4 * q4];
     }
     if constexpr (NORM) {
         // the rows into LDS, wave t normalises token t there, every wave then
         // reads its operands (the weights keep streaming meanwhile)
-        __shared__ uint4 s_xn[kQgMaxT * kQ4MaxK / 8];
+        // (row kQgMaxT: zeros, the operand row of lanes outside the batch)
+        __shared__ uint4 s_xn[(kQgMaxT + 1) * kQ4MaxK / 8];
         __shared__ uint4 s_nw[kQ4MaxK / 8];
         const int nxw = T * K / 8, nnw = K / 8;
+        if (tid < nnw) s_xn[kQgMaxT * (K / 8) + tid] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
         for (int d = 0; d < NXW; ++d) {
             const int i = tid + kQ4Threads * d;
@@ -1029,80 +1041,63 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
                 float f[8], g[8];
                 bf16x8f(s_xn[i], f);
                 bf16x8f(s_nw[i % (K / 8)], g);
+                // in MFMA operand order: pairs (e, e + 4), the weight unpack's order
                 uint32_t o[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    o[e] = vmi_pack_bf16x2((f[2 * e] * inv) * g[2 * e], (f[2 * e + 1] * inv) * g[2 * e + 1]);
+                    o[e] = vmi_pack_bf16x2((f[e] * inv) * g[e], (f[e + 4] * inv) * g[e + 4]);
                 s_xn[i] = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }
         __syncthreads();
-        xr = s_xn + (size_t)(xreal ? tk : 0) * (K / 8) + kw * (kQ4Kw / 8) + 4 * q4;
+        xr = s_xn + (size_t)(xreal ? tk : kQgMaxT) * (K / 8) + kw * (kQ4Kw / 8) + 4 * q4;
     }
-    // the lane's operand words from LDS (uint4 16 m + 4 q4 + j of its
-    // token's slice; lanes outside the batch read token 0 and use zeros) and
-    // their group sums
-    uint4 xu[4][4];
+    VMI_STAMP(kid, 6);
+    // the lane's operand words from LDS, already in operand order (uint4
+    // 16 m + 4 q4 + j of its token's slice; lanes outside the batch read the
+    // zero row)
+    vmi_u4 ax[4][4];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xu[m][j] = xr[16 * m + j];
-    vmi_u4 ax[4][4];
-    float xs[4] = {0.f, 0.f, 0.f, 0.f};
-    if (xreal) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint4 u = xu[m][j];
-                ax[m][j][0] = (u.x & 0xffffu) | (u.z << 16);
-                ax[m][j][1] = (u.x >> 16) | (u.z & 0xffff0000u);
-                ax[m][j][2] = (u.y & 0xffffu) | (u.w << 16);
-                ax[m][j][3] = (u.y >> 16) | (u.w & 0xffff0000u);
-                const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) xs[m] += __uint_as_float(uu[i] << 16) + __uint_as_float(uu[i] & 0xffff0000u);
-            }
-    } else {
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) ax[m][j] = vmi_u4{0u, 0u, 0u, 0u};
-    }
-    // group 2m + (q4 >> 1) of the wave = 64 columns = lanes q4 and q4 ^ 1
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const float g = xs[m] + __shfl_xor(xs[m], 16);
-        if (xreal && (q4 & 1) == 0) s_X[w][tk][2 * m + (q4 >> 1)] = g;
-    }
+        for (int j = 0; j < 4; ++j) {
+            const uint4 u = xr[16 * m + j];
+            ax[m][j] = vmi_u4{u.x, u.y, u.z, u.w};
+        }
     const int par = q4 >> 1;
+    VMI_STAMP(kid, 7);
     const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
     const vmi_f4 zf = {0.f, 0.f, 0.f, 0.f};
+    // X_g, the group sums of x, by the matrix core: against an all-ones B,
+    // D row 4 q4 + e (token 4 (q4 & 1) + e, group 2m + par) is the sum of the
+    // 64 values of that token's group in every column, so each lane gets the
+    // sums its own outputs need (zero for rows outside the batch)
+    const vmi_u4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    vmi_f4 xg[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         const uint32_t ww[4] = {wv[m].x, wv[m].y, wv[m].z, wv[m].w};
-        vmi_f4 d = zf;
+        vmi_f4 d = zf, xd = zf;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) d = vmi_mfma_bf16(ax[m][j], vmi_unpack_u4_bf16_128(ww[j]), d);
+        for (int j = 0; j < 4; ++j) {
+            d = vmi_mfma_bf16(ax[m][j], vmi_unpack_u4_bf16_128(ww[j]), d);
+            xd = vmi_mfma_bf16(ax[m][j], ones, xd);
+        }
+        xg[m] = xd;
         const float sc = __uint_as_float(par ? (sw[m] & 0xffff0000u) : (sw[m] << 16));
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = fmaf(sc, d[e], acc[e]);
     }
-    VMI_STAMP(3, 1);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    // (b_g - 128 s_g) X_g for tokens 4 (q4 & 1) + e over the groups of this lane's parity
-    const int tb = 4 * (q4 & 1);
+    VMI_STAMP(kid, 1);
+    // (b_g - 128 s_g) X_g over the groups of this lane's parity
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
         const float sc = __uint_as_float(par ? (sw[m] & 0xffff0000u) : (sw[m] << 16));
         const float bi = __uint_as_float(par ? (bw[m] & 0xffff0000u) : (bw[m] << 16));
         const float c = fmaf(-128.0f, sc, bi);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (tb + e < T) acc[e] = fmaf(c, s_X[w][tb + e][2 * m + par], acc[e]);
+        for (int e = 0; e < 4; ++e) acc[e] = fmaf(c, xg[m][e], acc[e]);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], 32);
@@ -1111,7 +1106,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
         for (int e = 0; e < 4; ++e) s_part[w][nl][4 * q4 + e] = acc[e];
     }
     __syncthreads();
-    VMI_STAMP(3, 2);
+    VMI_STAMP(kid, 2);
     for (int i = tid; i < tiles * RT * T; i += kQ4Threads) {
         const int tl = i / (RT * T), rr = (i / T) % RT, t = i % T;
         float y = s_part[tl * ks][rr][t];
@@ -1127,7 +1122,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
             }
         }
     }
-    VMI_STAMP(3, 3);
+    VMI_STAMP(kid, 3);
 }
 
 // ------------------------------------------------------------------ host
