@@ -28,6 +28,16 @@ typedef uint32_t vmi_u4 __attribute__((ext_vector_type(4)));
             tl_p_[((size_t)(kid) * 4096 + blockIdx.x) * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
         }                                                                                          \
     } while (0)
+// The same by the first lane of every wave (slot + wave index).
+#define VMI_STAMP_WAVE(kid, slot)                                                                  \
+    do {                                                                                           \
+        if ((threadIdx.x & 63) == 0 && vmi_tl_buf && blockIdx.x < 4096) {                          \
+            __attribute__((address_space(1))) unsigned long long* tl_p_ =                         \
+                (__attribute__((address_space(1))) unsigned long long*)vmi_tl_buf;                \
+            tl_p_[((size_t)(kid) * 4096 + blockIdx.x) * 16 + (slot) + (threadIdx.x >> 6)] =       \
+                __builtin_amdgcn_s_memrealtime();                                                  \
+        }                                                                                          \
+    } while (0)
 // The wave's hardware placement (HW_ID: CU, shader array and engine in bits
 // 8..14; XCC_ID in the upper word) at point `slot`.
 #define VMI_STAMP_HWID(kid, slot)                                                                  \
@@ -46,6 +56,9 @@ typedef uint32_t vmi_u4 __attribute__((ext_vector_type(4)));
     do {                     \
     } while (0)
 #define VMI_STAMP_HWID(kid, slot) \
+    do {                          \
+    } while (0)
+#define VMI_STAMP_WAVE(kid, slot) \
     do {                          \
     } while (0)
 #endif

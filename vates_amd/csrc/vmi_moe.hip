@@ -286,6 +286,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
     }
     if (is_ops) {
         operands_from_wave<NCH>(xr, H, t, a.ops);
+        VMI_STAMP_WAVE(0, 8);
         return;
     }
     VMI_STAMP(0, 4);
@@ -320,6 +321,7 @@ __global__ __launch_bounds__(kThreads) void k_router(RouterArgs a) {
         }
     }
     VMI_STAMP(0, 1);
+    VMI_STAMP_WAVE(0, 8);
 }
 
 // ----------------------------------------------------------- routing

@@ -33,6 +33,8 @@
 // and exact bf16 (128 + q) in down; per-group scale and bias are applied to
 // each group's MFMA result (FMA), with the bias through per-group operand sums.
 
+#include <type_traits>
+
 #include "vmi_device.h"
 #include "vmi_internal.h"
 
@@ -491,7 +493,9 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     __shared__ float s_inv[kTM3];  // 1 / f of the route's token (0 past the tile)
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
-    const int mh = w & 1, nq = w >> 1;
+    // waves w and w + 4 share a SIMD: one of each route half there, so a tile
+    // with fewer routes leaves every SIMD half its MFMAs, not two SIMDs all
+    const int mh = w >> 2, nq = w & 3;
     const int NB = (a.I + 255) / 256;
     int ti, nb;
     pf_tile_of(blockIdx.x, NB, ti, nb);
@@ -499,6 +503,9 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     const int4 tl = a.tiles[ti];
     const int H = a.H, HW = H / 8, G = H / 64, I = a.I;
     const int n0 = nb * 256, nvalid = min(256, I - n0);
+    // 16-route blocks of this wave's half holding routes (wave-uniform): the
+    // blocks past the tile's count issue no MFMA and no scale FMA
+    const int mcnt = __builtin_amdgcn_readfirstlane(max(0, min(4, (tl.z - 64 * mh + 15) / 16)));
     VMI_STAMP(4, 0);
     const vmi_qmat Gm = tl.x >= 0 ? a.gate : a.sh_gate;
     const vmi_qmat Um = tl.x >= 0 ? a.up : a.sh_up;
@@ -572,61 +579,77 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     VMI_STAMP(4, 1);
 #pragma unroll
     for (int u = 0; u < STAGES - 1; ++u) issue(u < G ? u : G - 1, u);
+    // the stage loop for MC of the wave's 16-route blocks holding routes (a
+    // loop per MC, so each keeps its own register allocation; MC = 0 only
+    // moves the ring and keeps the barriers)
+    auto stage_loop = [&](auto mc_tag) {
+        constexpr int MC = decltype(mc_tag)::value;
 #pragma unroll 1
-    for (int g = 0; g < G; ++g) {
-        const int u = g % STAGES;
-        pf_wait_vmcnt<4 * (STAGES - 2)>();  // group g's pieces (this thread's) have landed
-        __syncthreads();                    // everyone's; and the slot of group g-1 is free
-        if ((g & 3) == 0 && g < 32) VMI_STAMP(4, 2 + (g >> 2));
-        {
-            const int gn = g + STAGES - 1;
-            issue(gn < G ? gn : G - 1, gn % STAGES);
-        }
-        const uint8_t* A = s_ring + u * (kPfA + kB);
-        const uint8_t* B = A + kPfA;
-        vmi_u4 av[4][2];
+        for (int g = 0; g < G; ++g) {
+            const int u = g % STAGES;
+            pf_wait_vmcnt<4 * (STAGES - 2)>();  // group g's pieces (this thread's) have landed
+            __syncthreads();                    // everyone's; and the slot of group g-1 is free
+            if ((g & 3) == 0 && g < 32) VMI_STAMP(4, 2 + (g >> 2));
+            {
+                const int gn = g + STAGES - 1;
+                issue(gn < G ? gn : G - 1, gn % STAGES);
+            }
+            if constexpr (MC > 0) {
+                const uint8_t* A = s_ring + u * (kPfA + kB);
+                const uint8_t* B = A + kPfA;
+                vmi_u4 av[MC][2];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int row = 64 * mh + 16 * m + n;
-            av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
-            av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
-        }
-        // eight (column block, matrix) blocks of four MFMA pairs each, software
-        // pipelined: block i's MFMAs are issued with block i-1's scale FMAs, so
-        // only two blocks' results are live and they stay in VGPRs
-        vmi_f4 dp[4];
-        float scp = 0.0f;
+                for (int m = 0; m < MC; ++m) {
+                    const int row = 64 * mh + 16 * m + n;
+                    av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
+                    av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+                }
+                // eight (column block, matrix) blocks of MC MFMA pairs each,
+                // software pipelined: block i's MFMAs are issued with block
+                // i-1's scale FMAs, so only two blocks' results are live and
+                // they stay in VGPRs
+                vmi_f4 dp[MC];
+                float scp = 0.0f;
 #pragma unroll
-        for (int blk = 0; blk <= 8; ++blk) {
-            vmi_f4 dc[4];
-            float scc = 0.0f;
-            if (blk < 8) {
-                const int sb = blk >> 1, mt = blk & 1;
-                const int brow = 256 * mt + 64 * nq + 16 * sb + n;
-                const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
-                // the scale times 2^24: the 4-bit operands are n * 2^-24
-                scc = vmi_bf16_to_f32(s_scale[g][brow]) * 16777216.0f;
-                const vmi_u4 b0 = vmi_unpack_u4_f16(wq.x), b1 = vmi_unpack_u4_f16(wq.y);
+                for (int blk = 0; blk <= 8; ++blk) {
+                    vmi_f4 dc[MC];
+                    float scc = 0.0f;
+                    if (blk < 8) {
+                        const int sb = blk >> 1, mt = blk & 1;
+                        const int brow = 256 * mt + 64 * nq + 16 * sb + n;
+                        const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
+                        // the scale times 2^24: the 4-bit operands are n * 2^-24
+                        scc = vmi_bf16_to_f32(s_scale[g][brow]) * 16777216.0f;
+                        const vmi_u4 b0 = vmi_unpack_u4_f16(wq.x), b1 = vmi_unpack_u4_f16(wq.y);
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    dc[m] = vmi_mfma_f16(av[m][0], b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
-                    dc[m] = vmi_mfma_f16(av[m][1], b1, dc[m]);
+                        for (int m = 0; m < MC; ++m) {
+                            dc[m] = vmi_mfma_f16(av[m][0], b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
+                            dc[m] = vmi_mfma_f16(av[m][1], b1, dc[m]);
+                        }
+                    }
+                    if (blk > 0) {
+                        const int sb = (blk - 1) >> 1, mt = (blk - 1) & 1;
+#pragma unroll
+                        for (int m = 0; m < MC; ++m)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) acc[m][sb][mt][r] = fmaf(dp[m][r], scp, acc[m][sb][mt][r]);
+                    }
+                    if (blk < 8) {
+#pragma unroll
+                        for (int m = 0; m < MC; ++m) dp[m] = dc[m];
+                        scp = scc;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            if (blk > 0) {
-                const int sb = (blk - 1) >> 1, mt = (blk - 1) & 1;
-#pragma unroll
-                for (int m = 0; m < 4; ++m)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[m][sb][mt][r] = fmaf(dp[m][r], scp, acc[m][sb][mt][r]);
-            }
-            if (blk < 8) {
-#pragma unroll
-                for (int m = 0; m < 4; ++m) dp[m] = dc[m];
-                scp = scc;
-            }
-            __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    switch (mcnt) {
+        case 4: stage_loop(std::integral_constant<int, 4>{}); break;
+        case 3: stage_loop(std::integral_constant<int, 3>{}); break;
+        case 2: stage_loop(std::integral_constant<int, 2>{}); break;
+        case 1: stage_loop(std::integral_constant<int, 1>{}); break;
+        default: stage_loop(std::integral_constant<int, 0>{}); break;
     }
     pf_wait_vmcnt<0>();
     __syncthreads();
@@ -773,12 +796,13 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     __shared__ int s_route[kTM3];
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
-    const int mh = w & 1, nq = w >> 1;
+    const int mh = w >> 2, nq = w & 3;  // one wave of each route half per SIMD (as k_pf_gateup3)
     const int NB = a.H / 512;
     int ti, nb;
     pf_tile_of(blockIdx.x, NB, ti, nb);
     if (ti >= a.ntiles[0]) return;
     const int4 tl = a.tiles[ti];
+    const int mcnt = __builtin_amdgcn_readfirstlane(max(0, min(4, (tl.z - 64 * mh + 15) / 16)));
     const int I = a.I, IW = I / 8, G = I / 64;
     const int h0 = nb * 512;
     const vmi_qmat Dm = tl.x >= 0 ? a.down : a.sh_down;
@@ -863,55 +887,68 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         for (int sb = 0; sb < 8; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < STAGES - 1; ++u) issue(u < G ? u : G - 1, u);
+    // the stage loop for MC active 16-route blocks, as in k_pf_gateup3
+    auto stage_loop = [&](auto mc_tag) {
+        constexpr int MC = decltype(mc_tag)::value;
 #pragma unroll 1
-    for (int g = 0; g < G; ++g) {
-        const int u = g % STAGES;
-        pf_wait_vmcnt<4 * (STAGES - 2)>();
-        __syncthreads();
-        {
-            const int gn = g + STAGES - 1;
-            issue(gn < G ? gn : G - 1, gn % STAGES);
-        }
-        const uint8_t* A = s_ring + u * (kPfA + kB);
-        const uint8_t* B = A + kPfA;
-        vmi_u4 av[4][2];
+        for (int g = 0; g < G; ++g) {
+            const int u = g % STAGES;
+            pf_wait_vmcnt<4 * (STAGES - 2)>();
+            __syncthreads();
+            {
+                const int gn = g + STAGES - 1;
+                issue(gn < G ? gn : G - 1, gn % STAGES);
+            }
+            if constexpr (MC > 0) {
+                const uint8_t* A = s_ring + u * (kPfA + kB);
+                const uint8_t* B = A + kPfA;
+                vmi_u4 av[MC][2];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int row = 64 * mh + 16 * m + n;
-            av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
-            av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
-        }
-        // eight column blocks, software pipelined as in k_pf_gateup3
-        vmi_f4 dp[4];
-        float scp = 0.0f;
+                for (int m = 0; m < MC; ++m) {
+                    const int row = 64 * mh + 16 * m + n;
+                    av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
+                    av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+                }
+                // eight column blocks, software pipelined as in k_pf_gateup3
+                vmi_f4 dp[MC];
+                float scp = 0.0f;
 #pragma unroll
-        for (int sb = 0; sb <= 8; ++sb) {
-            vmi_f4 dc[4];
-            float scc = 0.0f;
-            if (sb < 8) {
-                const int brow = 128 * nq + 16 * sb + n;
-                const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
-                scc = vmi_bf16_to_f32(s_s16[brow][g]);
-                const vmi_u4 b0 = vmi_unpack_u4_bf16_128(wq.x), b1 = vmi_unpack_u4_bf16_128(wq.y);
+                for (int sb = 0; sb <= 8; ++sb) {
+                    vmi_f4 dc[MC];
+                    float scc = 0.0f;
+                    if (sb < 8) {
+                        const int brow = 128 * nq + 16 * sb + n;
+                        const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
+                        scc = vmi_bf16_to_f32(s_s16[brow][g]);
+                        const vmi_u4 b0 = vmi_unpack_u4_bf16_128(wq.x), b1 = vmi_unpack_u4_bf16_128(wq.y);
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    dc[m] = vmi_mfma_bf16(av[m][0], b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
-                    dc[m] = vmi_mfma_bf16(av[m][1], b1, dc[m]);
+                        for (int m = 0; m < MC; ++m) {
+                            dc[m] = vmi_mfma_bf16(av[m][0], b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
+                            dc[m] = vmi_mfma_bf16(av[m][1], b1, dc[m]);
+                        }
+                    }
+                    if (sb > 0) {
+#pragma unroll
+                        for (int m = 0; m < MC; ++m)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) acc[m][sb - 1][r] = fmaf(dp[m][r], scp, acc[m][sb - 1][r]);
+                    }
+                    if (sb < 8) {
+#pragma unroll
+                        for (int m = 0; m < MC; ++m) dp[m] = dc[m];
+                        scp = scc;
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            if (sb > 0) {
-#pragma unroll
-                for (int m = 0; m < 4; ++m)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[m][sb - 1][r] = fmaf(dp[m][r], scp, acc[m][sb - 1][r]);
-            }
-            if (sb < 8) {
-#pragma unroll
-                for (int m = 0; m < 4; ++m) dp[m] = dc[m];
-                scp = scc;
-            }
-            __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    switch (mcnt) {
+        case 4: stage_loop(std::integral_constant<int, 4>{}); break;
+        case 3: stage_loop(std::integral_constant<int, 3>{}); break;
+        case 2: stage_loop(std::integral_constant<int, 2>{}); break;
+        case 1: stage_loop(std::integral_constant<int, 1>{}); break;
+        default: stage_loop(std::integral_constant<int, 0>{}); break;
     }
     pf_wait_vmcnt<0>();
     // the affine terms, eight groups per MFMA

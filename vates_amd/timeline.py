@@ -5,7 +5,7 @@ The stamped tuning build (``python -m vates_amd.build --timeline`` writes
 vates_amd/libvmi_timeline.so) makes the first lane of every workgroup record
 the 100 MHz real-time counter at fixed points of the layer's three kernels:
 
-  k_router       0 start, 1 end
+  k_router       0 start, 1 end (first wave), 8.. every wave's end
   k_experts      0 start, 9 top-k keys loaded, 10 top-k rounds done,
                  1 routing done, 2 slot dedup done, 3 gate/up weights landed,
                  4 SwiGLU barrier passed, 7 down loop start, 6 end
@@ -75,7 +75,8 @@ def run(T: int = 4, reps: int = 20) -> list:
     with torch.cuda.graph(g):
         step()
 
-    stages = [("router", 0, 0, "start (first)"), ("router", 0, 1, "end"),
+    stages = [("router", 0, 0, "start (first)"), ("router", 0, 1, "end (first wave)"),
+              ("router", 0, -8, "end (last wave)"),
               ("experts", 1, 0, "start"), ("experts", 1, 9, "top-k keys loaded"),
               ("experts", 1, 10, "top-k rounds done"), ("experts", 1, 1, "routing done"),
               ("experts", 1, 2, "slot dedup done"), ("experts", 1, 3, "gate/up weights landed"),
@@ -94,7 +95,7 @@ def run(T: int = 4, reps: int = 20) -> list:
         t0 = b[0, :, 0][b[0, :, 0] > 0].min()
         real = b[1, :, 6] > 0  # expert workgroups that ran an item (the rest exit after routing)
         for i, (_, kid, slot, _) in enumerate(stages):
-            v = b[kid, :, slot]
+            v = b[kid, :, slot] if slot >= 0 else b[kid, :, -slot:-slot + 4].max(axis=1)
             sel = (v > 0) & (real if kid == 1 and slot in (3, 4, 7, 6) else True)
             us = (v[sel] - t0) * 0.01
             med[i].append(float(np.median(us)) if us.size else float("nan"))
