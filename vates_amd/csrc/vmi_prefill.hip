@@ -457,10 +457,12 @@ __device__ __forceinline__ uint32_t ring_off(int row, int unit8) {
 // and the packed weights (rows x 32 bytes), each thread moving whole 16-byte
 // pieces.  A slot's A row r keeps its 16-byte piece c at position c ^ (r & 7),
 // so the 16 rows one MFMA operand read touches start on distinct banks; the
-// weight rows keep the half-swap on bit 3 of the row.  Per stage and output
-// element the only VALU work is one FMA with the group's scale; the affine
-// bias term sum_g b_g X_g goes through bf16 MFMAs once at the end (X split
-// into hi + mid + lo bf16, 24 significant bits).  Workgroup L runs tile
+// weight rows keep the half-swap on bit 3 of the row.  Gate/up folds each
+// group's scale into its fp16 weight operand (one packed multiply per two
+// values; the MFMAs then accumulate over all of K), down applies it by one
+// FMA per output element and group; the affine bias term sum_g b_g X_g goes
+// through bf16 MFMAs once at the end (X split into hi + mid + lo bf16, 24
+// significant bits).  Workgroup L runs tile
 // 8*(L/8/NB) + L%8 and column block (L/8)%NB: the column blocks of one tile
 // share an XCD, so its A rows reach that L2 once.
 constexpr int kPfStages = 2;   // LDS ring depth: kPfStages - 1 groups in flight
@@ -477,6 +479,22 @@ __device__ __forceinline__ uint32_t pf_a_off(int r, int c) { return 16u * (8u * 
 // the logical piece a slot position holds (the inverse of pf_a_off's swizzle)
 __device__ __forceinline__ int pf_a_piece(int r, int pos) { return pos ^ (r & 7); }
 
+// Four fp16 pairs times one fp16 pair (packed multiplies, rounded to nearest).
+// The elements are taken into named scalars first: a bit cast of a vector
+// element indexed by a loop counter compiled to one element's product
+// replicated four times.
+typedef _Float16 pf_h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ vmi_u4 pf_scale_f16(const vmi_u4& v, uint32_t s2) {
+    const pf_h2 s = __builtin_bit_cast(pf_h2, s2);
+    const uint32_t v0 = v.x, v1 = v.y, v2 = v.z, v3 = v.w;
+    vmi_u4 r;
+    r.x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2, v0) * s);
+    r.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2, v1) * s);
+    r.z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2, v2) * s);
+    r.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2, v3) * s);
+    return r;
+}
+
 // Gate/up: tile 128 routes x 256 intermediate rows of gate and of up (512
 // weight rows per stage), K = H, eight waves in a 2 x 4 grid (wave (mh, nq):
 // routes 64mh.., intermediate rows 64nq.. of both matrices).  Then SwiGLU,
@@ -487,7 +505,10 @@ template <int STAGES>
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     constexpr int kB = 512 * 32;
     __shared__ __attribute__((aligned(16))) uint8_t s_ring[STAGES * (kPfA + kB)];
-    __shared__ uint16_t s_scale[kMaxG][512];  // bf16 bits: [group][matrix * 256 + row]
+    // the groups' scales, staged as bf16 bits and then rewritten as the fp16
+    // factor s * 2^P of the row's operands: [group][matrix * 256 + row]
+    __shared__ uint16_t s_scale[kMaxG][512];
+    __shared__ float s_post[512];  // 2^(24 - P): what the row's sums are multiplied by at the end
     __shared__ int s_route[kTM3];
     __shared__ int s_tok[kTM3];
     __shared__ float s_inv[kTM3];  // 1 / f of the route's token (0 past the tile)
@@ -532,15 +553,33 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
             s_tok[tid] = tok;
             s_inv[tid] = rt >= 0 ? 1.0f / a.fscale[tok] : 0.0f;
         }
+        // a row's G/8 chunks of eight scales sit in G/8 consecutive lanes
+        // (G/8 is 1, 2 or 4, and the branch is uniform: it < G/8).  Each
+        // row's power of two 2^P puts its largest |scale| in [2^14, 2^15):
+        // s 2^P is then exact in fp16 (a bf16 value times a power of two),
+        // and the operand (q 2^-24) (s 2^P) a normal fp16 for every q > 0 of
+        // a group whose scale is at least 1/32 of the row's largest
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
             const int i = tid + kPf8Threads * it;
             if (i < n16) {
                 const int chunk = i % (G / 8), row = (i / (G / 8)) % 256, mt = i / (G / 8 * 256);
                 const uint32_t wv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+                uint32_t mx = 0u;  // |scale| as float bits: ordered as integers
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    s_scale[8 * chunk + j][256 * mt + row] = (uint16_t)((wv[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                for (int j = 0; j < 8; ++j) mx = max(mx, (wv[j >> 1] << (16 - 16 * (j & 1))) & 0x7fff0000u);
+                for (int o = 1; o < G / 8; o <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
+                int e = 0;
+                (void)frexpf(__uint_as_float(mx), &e);  // mx = f 2^e, f in [0.5, 1)
+                const int P = mx ? min(15 - e, 127) : 0;
+                const float pw = ldexpf(1.0f, P);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t sb = (wv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                    s_scale[8 * chunk + j][256 * mt + row] =
+                        __builtin_bit_cast(uint16_t, (_Float16)(vmi_bf16_to_f32((uint16_t)sb) * pw));
+                }
+                if (chunk == 0) s_post[256 * mt + row] = ldexpf(1.0f, 24 - P);
             }
         }
     }
@@ -604,42 +643,22 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
                     av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
                     av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
                 }
-                // eight (column block, matrix) blocks of MC MFMA pairs each,
-                // software pipelined: block i's MFMAs are issued with block
-                // i-1's scale FMAs, so only two blocks' results are live and
-                // they stay in VGPRs
-                vmi_f4 dp[MC];
-                float scp = 0.0f;
+                // eight (column block, matrix) blocks of MC MFMA pairs each:
+                // the 4-bit operands (n 2^-24, fp16 subnormals) times the
+                // group's fp16 factor, accumulated over all of K
 #pragma unroll
-                for (int blk = 0; blk <= 8; ++blk) {
-                    vmi_f4 dc[MC];
-                    float scc = 0.0f;
-                    if (blk < 8) {
-                        const int sb = blk >> 1, mt = blk & 1;
-                        const int brow = 256 * mt + 64 * nq + 16 * sb + n;
-                        const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
-                        // the scale times 2^24: the 4-bit operands are n * 2^-24
-                        scc = vmi_bf16_to_f32(s_scale[g][brow]) * 16777216.0f;
-                        const vmi_u4 b0 = vmi_unpack_u4_f16(wq.x), b1 = vmi_unpack_u4_f16(wq.y);
+                for (int blk = 0; blk < 8; ++blk) {
+                    const int sb = blk >> 1, mt = blk & 1;
+                    const int brow = 256 * mt + 64 * nq + 16 * sb + n;
+                    const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
+                    const uint32_t sh = s_scale[g][brow];
+                    const vmi_u4 b0 = pf_scale_f16(vmi_unpack_u4_f16(wq.x), sh | (sh << 16));
+                    const vmi_u4 b1 = pf_scale_f16(vmi_unpack_u4_f16(wq.y), sh | (sh << 16));
 #pragma unroll
-                        for (int m = 0; m < MC; ++m) {
-                            dc[m] = vmi_mfma_f16(av[m][0], b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
-                            dc[m] = vmi_mfma_f16(av[m][1], b1, dc[m]);
-                        }
+                    for (int m = 0; m < MC; ++m) {
+                        acc[m][sb][mt] = vmi_mfma_f16(av[m][0], b0, acc[m][sb][mt]);
+                        acc[m][sb][mt] = vmi_mfma_f16(av[m][1], b1, acc[m][sb][mt]);
                     }
-                    if (blk > 0) {
-                        const int sb = (blk - 1) >> 1, mt = (blk - 1) & 1;
-#pragma unroll
-                        for (int m = 0; m < MC; ++m)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) acc[m][sb][mt][r] = fmaf(dp[m][r], scp, acc[m][sb][mt][r]);
-                    }
-                    if (blk < 8) {
-#pragma unroll
-                        for (int m = 0; m < MC; ++m) dp[m] = dc[m];
-                        scp = scc;
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
         }
@@ -654,6 +673,17 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     pf_wait_vmcnt<0>();
     __syncthreads();
     VMI_STAMP(4, 10);
+    // the rows' power-of-two factors out of the sums (exact)
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            const float post = s_post[256 * mt + 64 * nq + 16 * sb + n];
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[m][sb][mt][r] *= post;
+        }
     // affine-bias term: operand sums X [128 routes][G] and the biases as bf16
     // pairs [512 rows][G/2] in the ring's space
     constexpr int XS = kMaxG + 1, BS = kMaxG / 2 + 1;
