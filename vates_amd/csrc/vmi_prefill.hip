@@ -496,8 +496,9 @@ __device__ __forceinline__ vmi_u4 pf_scale_f16(const vmi_u4& v, uint32_t s2) {
 }
 
 // Gate/up: tile 128 routes x 256 intermediate rows of gate and of up (512
-// weight rows per stage), K = H, eight waves in a 2 x 4 grid (wave (mh, nq):
-// routes 64mh.., intermediate rows 64nq.. of both matrices).  Then SwiGLU,
+// weight rows per stage), K = H, eight waves side by side (wave w: all 128
+// routes, intermediate rows 32w.. of both matrices, so each unpacked weight
+// operand feeds up to eight 16-route blocks).  Then SwiGLU,
 // the bf16 down-projection operands of the activations and their per-group
 // sums.
 constexpr int kPf8Threads = 512;
@@ -514,9 +515,6 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     __shared__ float s_inv[kTM3];  // 1 / f of the route's token (0 past the tile)
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
-    // waves w and w + 4 share a SIMD: one of each route half there, so a tile
-    // with fewer routes leaves every SIMD half its MFMAs, not two SIMDs all
-    const int mh = w >> 2, nq = w & 3;
     const int NB = (a.I + 255) / 256;
     int ti, nb;
     pf_tile_of(blockIdx.x, NB, ti, nb);
@@ -524,9 +522,9 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     const int4 tl = a.tiles[ti];
     const int H = a.H, HW = H / 8, G = H / 64, I = a.I;
     const int n0 = nb * 256, nvalid = min(256, I - n0);
-    // 16-route blocks of this wave's half holding routes (wave-uniform): the
-    // blocks past the tile's count issue no MFMA and no scale FMA
-    const int mcnt = __builtin_amdgcn_readfirstlane(max(0, min(4, (tl.z - 64 * mh + 15) / 16)));
+    // 16-route blocks holding routes (uniform): the blocks past the tile's
+    // count issue no MFMA
+    const int mcnt = __builtin_amdgcn_readfirstlane(max(0, min(8, (tl.z + 15) / 16)));
     VMI_STAMP(4, 0);
     const vmi_qmat Gm = tl.x >= 0 ? a.gate : a.sh_gate;
     const vmi_qmat Um = tl.x >= 0 ? a.up : a.sh_up;
@@ -608,11 +606,11 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         for (int j = 0; j < 2; ++j)
             vmi_lds_dma16_opaque(bsrc[j] + 256 * (g >> 1) + 128 * (g & 1), A + kPfA + 16 * (kPf8Threads * j + 64 * w));
     };
-    vmi_f4 acc[4][4][2];
+    vmi_f4 acc[8][2][2];
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < 8; ++m)
 #pragma unroll
-        for (int sb = 0; sb < 4; ++sb)
+        for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) acc[m][sb][mt] = vmi_f4{0.f, 0.f, 0.f, 0.f};
     VMI_STAMP(4, 1);
@@ -636,34 +634,41 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
             if constexpr (MC > 0) {
                 const uint8_t* A = s_ring + u * (kPfA + kB);
                 const uint8_t* B = A + kPfA;
-                vmi_u4 av[MC][2];
+                // four (column block, matrix) weight operands: the 4-bit
+                // values (n 2^-24, fp16 subnormals) times the group's fp16
+                // factor
+                vmi_u4 bo[4][2];
 #pragma unroll
-                for (int m = 0; m < MC; ++m) {
-                    const int row = 64 * mh + 16 * m + n;
-                    av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
-                    av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
-                }
-                // eight (column block, matrix) blocks of MC MFMA pairs each:
-                // the 4-bit operands (n 2^-24, fp16 subnormals) times the
-                // group's fp16 factor, accumulated over all of K
-#pragma unroll
-                for (int blk = 0; blk < 8; ++blk) {
+                for (int blk = 0; blk < 4; ++blk) {
                     const int sb = blk >> 1, mt = blk & 1;
-                    const int brow = 256 * mt + 64 * nq + 16 * sb + n;
+                    const int brow = 256 * mt + 32 * w + 16 * sb + n;
                     const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
                     const uint32_t sh = s_scale[g][brow];
-                    const vmi_u4 b0 = pf_scale_f16(vmi_unpack_u4_f16(wq.x), sh | (sh << 16));
-                    const vmi_u4 b1 = pf_scale_f16(vmi_unpack_u4_f16(wq.y), sh | (sh << 16));
+                    bo[blk][0] = pf_scale_f16(vmi_unpack_u4_f16(wq.x), sh | (sh << 16));
+                    bo[blk][1] = pf_scale_f16(vmi_unpack_u4_f16(wq.y), sh | (sh << 16));
+                }
+                // each 16-route block's operands against the four, accumulated
+                // over all of K
 #pragma unroll
-                    for (int m = 0; m < MC; ++m) {
-                        acc[m][sb][mt] = vmi_mfma_f16(av[m][0], b0, acc[m][sb][mt]);
-                        acc[m][sb][mt] = vmi_mfma_f16(av[m][1], b1, acc[m][sb][mt]);
-                    }
+                for (int m = 0; m < MC; ++m) {
+                    const int row = 16 * m + n;
+                    const vmi_u4 a0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
+                    const vmi_u4 a1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+#pragma unroll
+                    for (int blk = 0; blk < 4; ++blk)
+                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(a0, bo[blk][0], acc[m][blk >> 1][blk & 1]);
+#pragma unroll
+                    for (int blk = 0; blk < 4; ++blk)
+                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(a1, bo[blk][1], acc[m][blk >> 1][blk & 1]);
                 }
             }
         }
     };
     switch (mcnt) {
+        case 8: stage_loop(std::integral_constant<int, 8>{}); break;
+        case 7: stage_loop(std::integral_constant<int, 7>{}); break;
+        case 6: stage_loop(std::integral_constant<int, 6>{}); break;
+        case 5: stage_loop(std::integral_constant<int, 5>{}); break;
         case 4: stage_loop(std::integral_constant<int, 4>{}); break;
         case 3: stage_loop(std::integral_constant<int, 3>{}); break;
         case 2: stage_loop(std::integral_constant<int, 2>{}); break;
@@ -675,12 +680,12 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     VMI_STAMP(4, 10);
     // the rows' power-of-two factors out of the sums (exact)
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb)
+    for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-            const float post = s_post[256 * mt + 64 * nq + 16 * sb + n];
+            const float post = s_post[256 * mt + 32 * w + 16 * sb + n];
 #pragma unroll
-            for (int m = 0; m < 4; ++m)
+            for (int m = 0; m < 8; ++m)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[m][sb][mt][r] *= post;
         }
@@ -732,45 +737,48 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 #pragma unroll 1
     for (int c8 = 0; c8 < G / 8; ++c8) {
         const int g0 = 8 * c8 + 2 * q;
-        vmi_u4 ab[4];
+        vmi_u4 bb[2][2];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int row = 64 * mh + 16 * m + n;
-            ab[m] = vmi_bias_a_operand(s_xs[row * XS + g0], s_xs[row * XS + g0 + 1]);
-        }
-#pragma unroll
-        for (int sb = 0; sb < 4; ++sb)
+        for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
-                const int brow = 256 * mt + 64 * nq + 16 * sb + n;
-                const vmi_u4 bb = vmi_bias_b_operand(s_b[brow * BS + (g0 >> 1)]);
-#pragma unroll
-                for (int m = 0; m < 4; ++m) acc[m][sb][mt] = vmi_mfma_bf16(ab[m], bb, acc[m][sb][mt]);
+                const int brow = 256 * mt + 32 * w + 16 * sb + n;
+                bb[sb][mt] = vmi_bias_b_operand(s_b[brow * BS + (g0 >> 1)]);
             }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const int row = 16 * m + n;
+            const vmi_u4 ab = vmi_bias_a_operand(s_xs[row * XS + g0], s_xs[row * XS + g0 + 1]);
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) acc[m][sb][mt] = vmi_mfma_bf16(ab, bb[sb][mt], acc[m][sb][mt]);
+        }
     }
     __syncthreads();
     VMI_STAMP(4, 11);
     // SwiGLU into LDS as bf16 (the rounding of the down-projection operands):
-    // route row 64mh + 16m + 4q + r, column 64nq + 16sb + n
+    // route row 16m + 4q + r, column 32w + 16sb + n
     constexpr int AS = 264;
     static_assert(kTM3 * AS * 2 <= sizeof(s_ring), "activation staging exceeds the ring");
     uint16_t* s_act = reinterpret_cast<uint16_t*>(s_ring);  // [128][AS]
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < 8; ++m)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int row = 64 * mh + 16 * m + 4 * q + r;
+            const int row = 16 * m + 4 * q + r;
             const float inv = s_inv[row];
 #pragma unroll
-            for (int sb = 0; sb < 4; ++sb) {
+            for (int sb = 0; sb < 2; ++sb) {
                 const float gv = acc[m][sb][0][r] * inv, uv = acc[m][sb][1][r] * inv;
                 // hardware exp2 and reciprocal (about 1 ulp each): the value is
                 // rounded to bf16 right after
                 const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv * 1.44269504f));
-                s_act[row * AS + 64 * nq + 16 * sb + n] = vmi_f32_to_bf16(gv * sg * uv);
+                s_act[row * AS + 32 * w + 16 * sb + n] = vmi_f32_to_bf16(gv * sg * uv);
             }
         }
     __syncthreads();
+    VMI_STAMP(4, 13);
     const int IW = I / 8, IG = I / 64, nw8 = nvalid / 8, ng = nvalid / 64;
     for (int i = tid; i < kTM3 * nw8; i += kPf8Threads) {
         const int row = i / nw8, wd = i - row * nw8;
@@ -811,17 +819,21 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 // exact bf16 (128 + q); per group y += s * D, and at the end
 // y += sum_g (b_g - 128 s_g) X_g with X the activations' group sums (as the
 // bf16 MFMAs sum_g b_g X_g + sum_g s_g (-128 X_g)); then times the route's
-// combine weight into one bf16 row per (token, rank).  MAXG bounds the
-// quantisation groups of K the LDS tables hold.
+// combine weight into one bf16 row per (token, rank).  The MFMAs take the
+// weights as their first operand, so a lane holds four consecutive hidden
+// rows of one route (y transposed): its four scales are one 8-byte read and
+// its four outputs one 8-byte store.  MAXG bounds the quantisation groups of
+// K the LDS tables hold.
 template <int STAGES, int MAXG>
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     constexpr int kB = 512 * 32;
-    constexpr int GS = MAXG + 2, XS = MAXG + 1;
+    constexpr int G8MAX = (MAXG + 7) & ~7, XS = MAXG + 1;
     __shared__ __attribute__((aligned(16))) uint8_t s_ring[STAGES * (kPfA + kB)];
-    // scales and biases as bf16 bits, and the activation sums, each zero past
-    // group G up to the next multiple of 8 (the affine MFMAs take 8 groups)
-    __shared__ uint16_t s_s16[512][GS];
-    __shared__ uint16_t s_b16[512][GS];
+    // scales and biases as bf16 bits [group][hidden row], and the activation
+    // sums, each zero past group G up to the next multiple of 8 (the affine
+    // MFMAs take 8 groups)
+    __shared__ __attribute__((aligned(16))) uint16_t s_st[G8MAX][512];
+    __shared__ __attribute__((aligned(16))) uint16_t s_bt[G8MAX][512];
     __shared__ float s_as[kTM3][XS];
     __shared__ int s_route[kTM3];
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
@@ -833,6 +845,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     if (ti >= a.ntiles[0]) return;
     const int4 tl = a.tiles[ti];
     const int mcnt = __builtin_amdgcn_readfirstlane(max(0, min(4, (tl.z - 64 * mh + 15) / 16)));
+    VMI_STAMP(3, 0);
     const int I = a.I, IW = I / 8, G = I / 64;
     const int h0 = nb * 512;
     const vmi_qmat Dm = tl.x >= 0 ? a.down : a.sh_down;
@@ -860,14 +873,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
             const int i = tid + kPf8Threads * it;
             if (i < n16) {
                 const int r8 = i % 64, g = (i / 64) % G8, sb = i / (64 * G8);
-                const uint32_t wv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint16_t* d0 = sb ? &s_b16[8 * r8 + 2 * j][g] : &s_s16[8 * r8 + 2 * j][g];
-                    uint16_t* d1 = sb ? &s_b16[8 * r8 + 2 * j + 1][g] : &s_s16[8 * r8 + 2 * j + 1][g];
-                    *d0 = (uint16_t)(wv[j] & 0xffffu);
-                    *d1 = (uint16_t)(wv[j] >> 16);
-                }
+                *reinterpret_cast<uint4*>(sb ? &s_bt[g][8 * r8] : &s_st[g][8 * r8]) = v[it];
             }
         }
     }
@@ -915,6 +921,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     for (int m = 0; m < 4; ++m)
 #pragma unroll
         for (int sb = 0; sb < 8; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+    VMI_STAMP(3, 1);
 #pragma unroll
     for (int u = 0; u < STAGES - 1; ++u) issue(u < G ? u : G - 1, u);
     // the stage loop for MC active 16-route blocks, as in k_pf_gateup3
@@ -939,34 +946,43 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
                     av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
                     av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
                 }
-                // eight column blocks, software pipelined as in k_pf_gateup3
+                // eight column blocks, software pipelined: block i's MFMAs are
+                // issued with block i-1's scale FMAs, so only two blocks'
+                // results are live and they stay in VGPRs
                 vmi_f4 dp[MC];
-                float scp = 0.0f;
+                float scp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int sb = 0; sb <= 8; ++sb) {
                     vmi_f4 dc[MC];
-                    float scc = 0.0f;
+                    float scc[4] = {0.f, 0.f, 0.f, 0.f};
                     if (sb < 8) {
                         const int brow = 128 * nq + 16 * sb + n;
                         const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
-                        scc = vmi_bf16_to_f32(s_s16[brow][g]);
+                        // the scales of this lane's hidden rows 4q .. 4q + 3
+                        const uint2 s4 = *reinterpret_cast<const uint2*>(&s_st[g][128 * nq + 16 * sb + 4 * q]);
+                        scc[0] = vmi_bf16_to_f32(s4.x & 0xffffu);
+                        scc[1] = vmi_bf16_to_f32(s4.x >> 16);
+                        scc[2] = vmi_bf16_to_f32(s4.y & 0xffffu);
+                        scc[3] = vmi_bf16_to_f32(s4.y >> 16);
                         const vmi_u4 b0 = vmi_unpack_u4_bf16_128(wq.x), b1 = vmi_unpack_u4_bf16_128(wq.y);
 #pragma unroll
                         for (int m = 0; m < MC; ++m) {
-                            dc[m] = vmi_mfma_bf16(av[m][0], b0, vmi_f4{0.f, 0.f, 0.f, 0.f});
-                            dc[m] = vmi_mfma_bf16(av[m][1], b1, dc[m]);
+                            dc[m] = vmi_mfma_bf16(b0, av[m][0], vmi_f4{0.f, 0.f, 0.f, 0.f});
+                            dc[m] = vmi_mfma_bf16(b1, av[m][1], dc[m]);
                         }
                     }
                     if (sb > 0) {
 #pragma unroll
                         for (int m = 0; m < MC; ++m)
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) acc[m][sb - 1][r] = fmaf(dp[m][r], scp, acc[m][sb - 1][r]);
+                            for (int r = 0; r < 4; ++r)
+                                acc[m][sb - 1][r] = fmaf(dp[m][r], scp[r], acc[m][sb - 1][r]);
                     }
                     if (sb < 8) {
 #pragma unroll
                         for (int m = 0; m < MC; ++m) dp[m] = dc[m];
-                        scp = scc;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) scp[r] = scc[r];
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -981,6 +997,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         default: stage_loop(std::integral_constant<int, 0>{}); break;
     }
     pf_wait_vmcnt<0>();
+    VMI_STAMP(3, 2);
     // the affine terms, eight groups per MFMA
 #pragma unroll 1
     for (int c8 = 0; c8 < G8 / 8; ++c8) {
@@ -996,29 +1013,35 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
 #pragma unroll
         for (int sb = 0; sb < 8; ++sb) {
             const int brow = 128 * nq + 16 * sb + n;
-            const vmi_u4 bb = vmi_bias_b_operand((uint32_t)s_b16[brow][g0] | ((uint32_t)s_b16[brow][g0 + 1] << 16));
-            const vmi_u4 bs = vmi_bias_b_operand((uint32_t)s_s16[brow][g0] | ((uint32_t)s_s16[brow][g0 + 1] << 16));
+            const vmi_u4 bb = vmi_bias_b_operand((uint32_t)s_bt[g0][brow] | ((uint32_t)s_bt[g0 + 1][brow] << 16));
+            const vmi_u4 bs = vmi_bias_b_operand((uint32_t)s_st[g0][brow] | ((uint32_t)s_st[g0 + 1][brow] << 16));
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                acc[m][sb] = vmi_mfma_bf16(ab[m], bb, acc[m][sb]);
-                acc[m][sb] = vmi_mfma_bf16(am[m], bs, acc[m][sb]);
+                acc[m][sb] = vmi_mfma_bf16(bb, ab[m], acc[m][sb]);
+                acc[m][sb] = vmi_mfma_bf16(bs, am[m], acc[m][sb]);
             }
         }
     }
+    VMI_STAMP(3, 3);
+    // lane (n, q): route 64mh + 16m + n, hidden rows h0 + 128nq + 16sb + 4q ..
+    // + 3: four bf16 in one 8-byte store
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < 4; ++m) {
+        const int route = s_route[64 * mh + 16 * m + n];
+        if (route < 0) continue;
+        const int t = route / (a.k + 1), j = route - t * (a.k + 1);
+        const float wgt = j < a.k ? a.scores[t * a.k + j]
+                                  : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
+        uint16_t* yrow = a.ybuf + (size_t)route * a.H + h0 + 128 * nq + 4 * q;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 64 * mh + 16 * m + 4 * q + r;
-            const int route = s_route[row];
-            if (route < 0) continue;
-            const int t = route / (a.k + 1), j = route - t * (a.k + 1);
-            const float wgt = j < a.k ? a.scores[t * a.k + j]
-                                      : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
-#pragma unroll
-            for (int sb = 0; sb < 8; ++sb)
-                a.ybuf[(size_t)route * a.H + h0 + 128 * nq + 16 * sb + n] = vmi_f32_to_bf16(acc[m][sb][r] * wgt);
+        for (int sb = 0; sb < 8; ++sb) {
+            uint2 o;
+            o.x = vmi_pack_bf16x2(acc[m][sb][0] * wgt, acc[m][sb][1] * wgt);
+            o.y = vmi_pack_bf16x2(acc[m][sb][2] * wgt, acc[m][sb][3] * wgt);
+            *reinterpret_cast<uint2*>(yrow + 16 * sb) = o;
         }
+    }
+    VMI_STAMP(3, 4);
 }
 
 // Router logits [T, E] as the same 128 x 128 tile GEMM (tokens x experts, K =
