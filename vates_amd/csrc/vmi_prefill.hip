@@ -77,8 +77,8 @@ struct PfArgs {
     int4* tiles;                // [max_tiles]: slot (-1 shared), list start (or token start), rows, 0
     int32_t* ntiles;            // [1]
     int32_t* list;              // [T*k] route rows t*(k+1)+j grouped by slot
-    vmi_u4* actop;              // [T*(k+1), I/8] bf16 operands
-    float* axs;                 // [T*(k+1), I/64]
+    vmi_u4* actop;              // [T*(k+1), I/8] fp16 operands (times 2^-E), 4-bit slot order
+    int32_t* aexp;              // [T*(k+1), ceil(I/256)]: E of each route and 256-column block
     uint16_t* ybuf;             // [T*(k+1), H] bf16 weighted expert outputs
     uint16_t* out;              // [T, H]
     uint32_t* status;
@@ -498,9 +498,9 @@ __device__ __forceinline__ vmi_u4 pf_scale_f16(const vmi_u4& v, uint32_t s2) {
 // Gate/up: tile 128 routes x 256 intermediate rows of gate and of up (512
 // weight rows per stage), K = H, eight waves side by side (wave w: all 128
 // routes, intermediate rows 32w.. of both matrices, so each unpacked weight
-// operand feeds up to eight 16-route blocks).  Then SwiGLU,
-// the bf16 down-projection operands of the activations and their per-group
-// sums.
+// operand feeds up to eight 16-route blocks).  Then SwiGLU rounded to bf16,
+// and the down projection's fp16 operands of the activations: each route's
+// 256 columns times 2^-E, E the route's exponent for this block.
 constexpr int kPf8Threads = 512;
 template <int STAGES>
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
@@ -513,6 +513,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     __shared__ int s_route[kTM3];
     __shared__ int s_tok[kTM3];
     __shared__ float s_inv[kTM3];  // 1 / f of the route's token (0 past the tile)
+    __shared__ int s_rexp[kTM3];   // E of each route row's activations
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
     const int NB = (a.I + 255) / 256;
@@ -757,7 +758,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     }
     __syncthreads();
     VMI_STAMP(4, 11);
-    // SwiGLU into LDS as bf16 (the rounding of the down-projection operands):
+    // SwiGLU into LDS as bf16 (the rounding of the activations):
     // route row 16m + 4q + r, column 32w + 16sb + n
     constexpr int AS = 264;
     static_assert(kTM3 * AS * 2 <= sizeof(s_ring), "activation staging exceeds the ring");
@@ -779,124 +780,147 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         }
     __syncthreads();
     VMI_STAMP(4, 13);
-    const int IW = I / 8, IG = I / 64, nw8 = nvalid / 8, ng = nvalid / 64;
+    // each route row's largest |activation| over the block's columns (four
+    // lanes per row, 64 columns each; float bits ordered as integers) gives
+    // its exponent E: the largest value times 2^-E lies in [2^14, 2^15)
+    {
+        const int row = tid >> 2, part = tid & 3;
+        uint32_t mx = 0u;
+        if (64 * part < nvalid) {
+#pragma unroll
+            for (int c = 0; c < 64; c += 8) {
+                const vmi_u4 v = *reinterpret_cast<const vmi_u4*>(s_act + row * AS + 64 * part + c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mx = max(mx, max((v[e] << 16) & 0x7fff0000u, v[e] & 0x7fff0000u));
+            }
+        }
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1));
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2));
+        int e = 0;
+        (void)frexpf(__uint_as_float(mx), &e);  // mx = f 2^e, f in [0.5, 1)
+        if (part == 0) s_rexp[row] = mx ? e - 15 : 0;
+    }
+    __syncthreads();
+    const int IW = I / 8, IB = (I + 255) / 256, nw8 = nvalid / 8;
     for (int i = tid; i < kTM3 * nw8; i += kPf8Threads) {
         const int row = i / nw8, wd = i - row * nw8;
         const int route = s_route[row];
         if (route < 0) continue;
-        uint16_t b[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) b[c] = s_act[row * AS + 8 * wd + c];
-        vmi_u4 o;  // slot order of vmi_unpack_u4_bf16_128: {0,4,1,5,2,6,3,7}
-        o[0] = (uint32_t)b[0] | ((uint32_t)b[4] << 16);
-        o[1] = (uint32_t)b[1] | ((uint32_t)b[5] << 16);
-        o[2] = (uint32_t)b[2] | ((uint32_t)b[6] << 16);
-        o[3] = (uint32_t)b[3] | ((uint32_t)b[7] << 16);
+        const vmi_u4 v = *reinterpret_cast<const vmi_u4*>(s_act + row * AS + 8 * wd);
+        const float fe = ldexpf(1.0f, -s_rexp[row]), fo = 0.0625f * fe;  // odd slots also divided by 16
+        const uint32_t b0 = v[0] << 16, b1 = v[0] & 0xffff0000u, b2 = v[1] << 16, b3 = v[1] & 0xffff0000u;
+        const uint32_t b4 = v[2] << 16, b5 = v[2] & 0xffff0000u, b6 = v[3] << 16, b7 = v[3] & 0xffff0000u;
+        vmi_u4 o;  // slot order of vmi_unpack_u4_f16: {0,4,1,5,2,6,3,7}, exact (bf16 times a power of two)
+        o[0] = vmi_h2_bits((_Float16)(__uint_as_float(b0) * fe), (_Float16)(__uint_as_float(b4) * fe));
+        o[1] = vmi_h2_bits((_Float16)(__uint_as_float(b1) * fo), (_Float16)(__uint_as_float(b5) * fo));
+        o[2] = vmi_h2_bits((_Float16)(__uint_as_float(b2) * fe), (_Float16)(__uint_as_float(b6) * fe));
+        o[3] = vmi_h2_bits((_Float16)(__uint_as_float(b3) * fo), (_Float16)(__uint_as_float(b7) * fo));
         a.actop[(size_t)route * IW + (n0 >> 3) + wd] = o;
     }
-    // group sums of the bf16 activations: eight lanes per (row, group), each
-    // adding 8 values in column order, then a fixed xor tree over the eight
-    for (int i0 = 0; i0 < kTM3 * ng * 8; i0 += kPf8Threads) {
-        const int i = i0 + tid;
-        const int e = i >> 3, part = i & 7;
-        const int row = e / max(ng, 1), gg = e - row * max(ng, 1);
-        float sum = 0.0f;
-        if (i < kTM3 * ng * 8) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) sum += vmi_bf16_to_f32(s_act[row * AS + 64 * gg + 8 * part + c]);
-        }
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
-        sum += __shfl_xor(sum, 4);
-        if (i < kTM3 * ng * 8 && part == 0 && s_route[row] >= 0)
-            a.axs[(size_t)s_route[row] * IG + (n0 >> 6) + gg] = sum;
-    }
+    if (tid < kTM3 && s_route[tid] >= 0) a.aexp[(size_t)s_route[tid] * IB + nb] = s_rexp[tid];
     VMI_STAMP(4, 12);
 }
 
-// Down: tile 128 routes x 512 hidden rows, K = I, eight waves in a 2 x 4 grid
-// (wave (mh, nq): routes 64mh.., hidden rows 128nq..).  4-bit values enter as
-// exact bf16 (128 + q); per group y += s * D, and at the end
-// y += sum_g (b_g - 128 s_g) X_g with X the activations' group sums (as the
-// bf16 MFMAs sum_g b_g X_g + sum_g s_g (-128 X_g)); then times the route's
-// combine weight into one bf16 row per (token, rank).  The MFMAs take the
-// weights as their first operand, so a lane holds four consecutive hidden
-// rows of one route (y transposed): its four scales are one 8-byte read and
-// its four outputs one 8-byte store.  MAXG bounds the quantisation groups of
-// K the LDS tables hold.
+// Down: tile 128 routes x 512 hidden rows, K = I, eight waves side by side
+// (wave w: all 128 routes, hidden rows 64w..).  The MFMAs take the weights
+// first, so a lane holds four consecutive hidden rows of one route (y
+// transposed): its four outputs are one 8-byte store.  The weight operand is
+// the dequantised value in fp16, (q 2^-24) s' + b' by one packed FMA per two
+// values, with s' = s 2^P and b' = b 2^(P-24) for the hidden row's power of
+// two P (its largest |scale| into [2^14, 2^15)); the activations are fp16
+// times 2^-E, E per route and 256-column block.  The sums are scaled by
+// 2^(E_prev - E) at each block boundary and by 2^(24-P) 2^E_last at the end,
+// then times the route's combine weight into one bf16 row per (token, rank).
+// MAXG bounds the quantisation groups of K the LDS table holds.
+constexpr int kPfMaxIB = 8;  // 256-column blocks of the intermediate size (I <= 2048)
+typedef _Float16 pf_h2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pf_fma_h2(uint32_t x, uint32_t y, uint32_t z) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(pf_h2v, x),
+                                                                  __builtin_bit_cast(pf_h2v, y),
+                                                                  __builtin_bit_cast(pf_h2v, z)));
+}
+// the eight values of one packed word, dequantised: s2 = (s', s'), b2 = (b', b'),
+// b16 = 16 b2 (the odd words of vmi_unpack_u4_f16 carry 16 q)
+__device__ __forceinline__ vmi_u4 pf_dequant_f16(uint32_t wq, uint32_t s2, uint32_t b2, uint32_t b16) {
+    const vmi_u4 u = vmi_unpack_u4_f16(wq);
+    const uint32_t u0 = u.x, u1 = u.y, u2 = u.z, u3 = u.w;
+    vmi_u4 r;
+    r.x = pf_fma_h2(u0, s2, b2);
+    r.y = pf_fma_h2(u1, s2, b16);
+    r.z = pf_fma_h2(u2, s2, b2);
+    r.w = pf_fma_h2(u3, s2, b16);
+    return r;
+}
+
 template <int STAGES, int MAXG>
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     constexpr int kB = 512 * 32;
-    constexpr int G8MAX = (MAXG + 7) & ~7, XS = MAXG + 1;
     __shared__ __attribute__((aligned(16))) uint8_t s_ring[STAGES * (kPfA + kB)];
-    // scales and biases as bf16 bits [group][hidden row], and the activation
-    // sums, each zero past group G up to the next multiple of 8 (the affine
-    // MFMAs take 8 groups)
-    __shared__ __attribute__((aligned(16))) uint16_t s_st[G8MAX][512];
-    __shared__ __attribute__((aligned(16))) uint16_t s_bt[G8MAX][512];
-    __shared__ float s_as[kTM3][XS];
+    __shared__ uint32_t s_sb[MAXG][512];                        // fp16 s' | b' << 16: [group][hidden row]
+    __shared__ __attribute__((aligned(16))) float s_post[512];  // 2^(24 - P)
     __shared__ int s_route[kTM3];
+    __shared__ int s_exp[kTM3][kPfMaxIB];
+    __shared__ float s_rf[kTM3];  // the route's combine weight times 2^E of its last block
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
-    const int mh = w >> 2, nq = w & 3;  // one wave of each route half per SIMD (as k_pf_gateup3)
     const int NB = a.H / 512;
     int ti, nb;
     pf_tile_of(blockIdx.x, NB, ti, nb);
     if (ti >= a.ntiles[0]) return;
     const int4 tl = a.tiles[ti];
-    const int mcnt = __builtin_amdgcn_readfirstlane(max(0, min(4, (tl.z - 64 * mh + 15) / 16)));
+    // 16-route blocks holding routes (uniform): the blocks past the tile's
+    // count issue no MFMA
+    const int mcnt = __builtin_amdgcn_readfirstlane(max(0, min(8, (tl.z + 15) / 16)));
     VMI_STAMP(3, 0);
-    const int I = a.I, IW = I / 8, G = I / 64;
+    const int I = a.I, IW = I / 8, G = I / 64, IB = (I + 255) / 256;
     const int h0 = nb * 512;
     const vmi_qmat Dm = tl.x >= 0 ? a.down : a.sh_down;
     // the down projection is group-major: row h of group g of slot m at
     // (m * G + g) * H + h (32 bytes of words; one bf16 scale and bias)
     const size_t mbase = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)G * a.H + h0;
-    if (tid < kTM3) s_route[tid] = tile_route(a, tl, tid);
-    const int G8 = (G + 7) & ~7;
     {
-        // 16-byte pieces = 8 consecutive rows of one group; groups G..G8-1 are
-        // zero.  All loads first, then the stores (one memory latency).
-        constexpr int kIt = (2 * 64 * MAXG + kPf8Threads - 1) / kPf8Threads;
-        const int n16 = 2 * 64 * G8;
-        uint4 v[kIt];
+        // thread t: hidden row h0 + t, every group (a wave reads 128
+        // contiguous bytes per group); these loads are issued first, the
+        // routes' dependent loads wait behind them
+        uint32_t sv[MAXG], bv[MAXG];
 #pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-            const int i = tid + kPf8Threads * it;
-            const int r8 = i % 64, g = (i / 64) % G8, sb = i / (64 * G8);
-            v[it] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < n16 && g < G)
-                v[it] = *reinterpret_cast<const uint4*>((sb ? Dm.b : Dm.s) + mbase + (size_t)g * a.H + 8 * r8);
-        }
-#pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-            const int i = tid + kPf8Threads * it;
-            if (i < n16) {
-                const int r8 = i % 64, g = (i / 64) % G8, sb = i / (64 * G8);
-                *reinterpret_cast<uint4*>(sb ? &s_bt[g][8 * r8] : &s_st[g][8 * r8]) = v[it];
+        for (int g = 0; g < MAXG; ++g) {
+            sv[g] = 0u;
+            bv[g] = 0u;
+            if (g < G) {
+                sv[g] = Dm.s[mbase + (size_t)g * a.H + tid];
+                bv[g] = Dm.b[mbase + (size_t)g * a.H + tid];
             }
         }
+        if (tid < kTM3) {
+            const int rt = tile_route(a, tl, tid);
+            s_route[tid] = rt;
+            int el = 0;
+            for (int b = 0; b < IB; ++b) {
+                el = rt >= 0 ? a.aexp[(size_t)rt * IB + b] : 0;
+                s_exp[tid][b] = el;
+            }
+            float wgt = 0.0f;
+            if (rt >= 0) {
+                const int t = rt / (a.k + 1), j = rt - t * (a.k + 1);
+                wgt = j < a.k ? a.scores[t * a.k + j] : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
+            }
+            s_rf[tid] = wgt * ldexpf(1.0f, el);
+        }
+        uint32_t mx = 0u;  // |scale| as float bits: ordered as integers
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g) mx = max(mx, (sv[g] << 16) & 0x7fff0000u);
+        int e = 0;
+        (void)frexpf(__uint_as_float(mx), &e);  // mx = f 2^e, f in [0.5, 1)
+        const int P = mx ? min(15 - e, 127) : 0;
+        const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g)
+            if (g < G)
+                s_sb[g][tid] = vmi_h2_bits((_Float16)(vmi_bf16_to_f32(sv[g]) * ps), (_Float16)(vmi_bf16_to_f32(bv[g]) * pb));
+        s_post[tid] = ldexpf(1.0f, 24 - P);
     }
     __syncthreads();
-    {
-        constexpr int kIt = (kTM3 * MAXG + kPf8Threads - 1) / kPf8Threads;
-        float v[kIt];
-#pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-            const int i = tid + kPf8Threads * it;
-            const int row = i / G8, g = i - row * G8;
-            v[it] = 0.0f;
-            if (i < kTM3 * G8) {
-                const int rt = s_route[row];
-                if (rt >= 0 && g < G) v[it] = a.axs[(size_t)rt * G + g];
-            }
-        }
-#pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-            const int i = tid + kPf8Threads * it;
-            if (i < kTM3 * G8) s_as[i / G8][i % G8] = v[it];
-        }
-    }
     const vmi_u4* asrc[2];
     const uint32_t* bsrc[2];
 #pragma unroll
@@ -916,15 +940,17 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         for (int j = 0; j < 2; ++j)
             vmi_lds_dma16_opaque(bsrc[j] + (size_t)g * a.H * 8, A + kPfA + 16 * (kPf8Threads * j + 64 * w));
     };
-    vmi_f4 acc[4][8];
+    vmi_f4 acc[8][4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < 8; ++m)
 #pragma unroll
-        for (int sb = 0; sb < 8; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+        for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
     VMI_STAMP(3, 1);
 #pragma unroll
     for (int u = 0; u < STAGES - 1; ++u) issue(u < G ? u : G - 1, u);
-    // the stage loop for MC active 16-route blocks, as in k_pf_gateup3
+    // the stage loop for MC active 16-route blocks (a loop per MC, so each
+    // keeps its own register allocation; MC = 0 only moves the ring and keeps
+    // the barriers)
     auto stage_loop = [&](auto mc_tag) {
         constexpr int MC = decltype(mc_tag)::value;
 #pragma unroll 1
@@ -937,59 +963,52 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
                 issue(gn < G ? gn : G - 1, gn % STAGES);
             }
             if constexpr (MC > 0) {
+                if (g > 0 && (g & 3) == 0) {
+                    // a new 256-column block: the sums so far times 2^(E_prev - E)
+                    const int b = g >> 2;
+#pragma unroll
+                    for (int m = 0; m < MC; ++m) {
+                        const int row = 16 * m + n;
+                        const float f = ldexpf(1.0f, s_exp[row][b - 1] - s_exp[row][b]);
+#pragma unroll
+                        for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) acc[m][sb][r] *= f;
+                    }
+                }
                 const uint8_t* A = s_ring + u * (kPfA + kB);
                 const uint8_t* B = A + kPfA;
-                vmi_u4 av[MC][2];
+                // the four column blocks' weights, dequantised
+                vmi_u4 wo[4][2];
+#pragma unroll
+                for (int sb = 0; sb < 4; ++sb) {
+                    const int brow = 64 * w + 16 * sb + n;
+                    const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
+                    const uint32_t sbw = s_sb[g][brow];
+                    const uint32_t s2 = __builtin_amdgcn_perm(sbw, sbw, 0x01000100u);
+                    const uint32_t b2 = __builtin_amdgcn_perm(sbw, sbw, 0x03020302u);
+                    const uint32_t b16 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2v, b2) * (pf_h2v){16.0f16, 16.0f16});
+                    wo[sb][0] = pf_dequant_f16(wq.x, s2, b2, b16);
+                    wo[sb][1] = pf_dequant_f16(wq.y, s2, b2, b16);
+                }
 #pragma unroll
                 for (int m = 0; m < MC; ++m) {
-                    const int row = 64 * mh + 16 * m + n;
-                    av[m][0] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
-                    av[m][1] = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
-                }
-                // eight column blocks, software pipelined: block i's MFMAs are
-                // issued with block i-1's scale FMAs, so only two blocks'
-                // results are live and they stay in VGPRs
-                vmi_f4 dp[MC];
-                float scp[4] = {0.f, 0.f, 0.f, 0.f};
+                    const int row = 16 * m + n;
+                    const vmi_u4 a0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
+                    const vmi_u4 a1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
 #pragma unroll
-                for (int sb = 0; sb <= 8; ++sb) {
-                    vmi_f4 dc[MC];
-                    float scc[4] = {0.f, 0.f, 0.f, 0.f};
-                    if (sb < 8) {
-                        const int brow = 128 * nq + 16 * sb + n;
-                        const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
-                        // the scales of this lane's hidden rows 4q .. 4q + 3
-                        const uint2 s4 = *reinterpret_cast<const uint2*>(&s_st[g][128 * nq + 16 * sb + 4 * q]);
-                        scc[0] = vmi_bf16_to_f32(s4.x & 0xffffu);
-                        scc[1] = vmi_bf16_to_f32(s4.x >> 16);
-                        scc[2] = vmi_bf16_to_f32(s4.y & 0xffffu);
-                        scc[3] = vmi_bf16_to_f32(s4.y >> 16);
-                        const vmi_u4 b0 = vmi_unpack_u4_bf16_128(wq.x), b1 = vmi_unpack_u4_bf16_128(wq.y);
+                    for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wo[sb][0], a0, acc[m][sb]);
 #pragma unroll
-                        for (int m = 0; m < MC; ++m) {
-                            dc[m] = vmi_mfma_bf16(b0, av[m][0], vmi_f4{0.f, 0.f, 0.f, 0.f});
-                            dc[m] = vmi_mfma_bf16(b1, av[m][1], dc[m]);
-                        }
-                    }
-                    if (sb > 0) {
-#pragma unroll
-                        for (int m = 0; m < MC; ++m)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                acc[m][sb - 1][r] = fmaf(dp[m][r], scp[r], acc[m][sb - 1][r]);
-                    }
-                    if (sb < 8) {
-#pragma unroll
-                        for (int m = 0; m < MC; ++m) dp[m] = dc[m];
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) scp[r] = scc[r];
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
+                    for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wo[sb][1], a1, acc[m][sb]);
                 }
             }
         }
     };
     switch (mcnt) {
+        case 8: stage_loop(std::integral_constant<int, 8>{}); break;
+        case 7: stage_loop(std::integral_constant<int, 7>{}); break;
+        case 6: stage_loop(std::integral_constant<int, 6>{}); break;
+        case 5: stage_loop(std::integral_constant<int, 5>{}); break;
         case 4: stage_loop(std::integral_constant<int, 4>{}); break;
         case 3: stage_loop(std::integral_constant<int, 3>{}); break;
         case 2: stage_loop(std::integral_constant<int, 2>{}); break;
@@ -998,46 +1017,22 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     }
     pf_wait_vmcnt<0>();
     VMI_STAMP(3, 2);
-    // the affine terms, eight groups per MFMA
-#pragma unroll 1
-    for (int c8 = 0; c8 < G8 / 8; ++c8) {
-        const int g0 = 8 * c8 + 2 * q;
-        vmi_u4 ab[4], am[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int row = 64 * mh + 16 * m + n;
-            const float x0 = s_as[row][g0], x1 = s_as[row][g0 + 1];
-            ab[m] = vmi_bias_a_operand(x0, x1);
-            am[m] = vmi_bias_a_operand(-128.0f * x0, -128.0f * x1);
-        }
-#pragma unroll
-        for (int sb = 0; sb < 8; ++sb) {
-            const int brow = 128 * nq + 16 * sb + n;
-            const vmi_u4 bb = vmi_bias_b_operand((uint32_t)s_bt[g0][brow] | ((uint32_t)s_bt[g0 + 1][brow] << 16));
-            const vmi_u4 bs = vmi_bias_b_operand((uint32_t)s_st[g0][brow] | ((uint32_t)s_st[g0 + 1][brow] << 16));
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                acc[m][sb] = vmi_mfma_bf16(bb, ab[m], acc[m][sb]);
-                acc[m][sb] = vmi_mfma_bf16(bs, am[m], acc[m][sb]);
-            }
-        }
-    }
     VMI_STAMP(3, 3);
-    // lane (n, q): route 64mh + 16m + n, hidden rows h0 + 128nq + 16sb + 4q ..
-    // + 3: four bf16 in one 8-byte store
+    // lane (n, q): route row 16m + n, hidden rows h0 + 64w + 16sb + 4q .. + 3
+    float4 post[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const int route = s_route[64 * mh + 16 * m + n];
+    for (int sb = 0; sb < 4; ++sb) post[sb] = *reinterpret_cast<const float4*>(&s_post[64 * w + 16 * sb + 4 * q]);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int route = s_route[16 * m + n];
         if (route < 0) continue;
-        const int t = route / (a.k + 1), j = route - t * (a.k + 1);
-        const float wgt = j < a.k ? a.scores[t * a.k + j]
-                                  : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
-        uint16_t* yrow = a.ybuf + (size_t)route * a.H + h0 + 128 * nq + 4 * q;
+        const float f = s_rf[16 * m + n];
+        uint16_t* yrow = a.ybuf + (size_t)route * a.H + h0 + 64 * w + 4 * q;
 #pragma unroll
-        for (int sb = 0; sb < 8; ++sb) {
+        for (int sb = 0; sb < 4; ++sb) {
             uint2 o;
-            o.x = vmi_pack_bf16x2(acc[m][sb][0] * wgt, acc[m][sb][1] * wgt);
-            o.y = vmi_pack_bf16x2(acc[m][sb][2] * wgt, acc[m][sb][3] * wgt);
+            o.x = vmi_pack_bf16x2(acc[m][sb][0] * post[sb].x * f, acc[m][sb][1] * post[sb].y * f);
+            o.y = vmi_pack_bf16x2(acc[m][sb][2] * post[sb].z * f, acc[m][sb][3] * post[sb].w * f);
             *reinterpret_cast<uint2*>(yrow + 16 * sb) = o;
         }
     }
@@ -1271,7 +1266,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_combine(PfArgs a) {
 // -------------------------------------------------------------- workspace
 struct PfLayout {
     size_t status, xop4, xsum4, xop8, xsum8, fscale, logits, sglogit, ids, scores, slots, counts, offsets, fill,
-        tiles, ntiles, list, actop, axs, ybuf, bytes;
+        tiles, ntiles, list, actop, aexp, ybuf, bytes;
     int max_tiles;
 };
 
@@ -1303,7 +1298,7 @@ PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) 
     L.ntiles = take(4);
     L.list = take((size_t)T * k * 4);
     L.actop = take(R * (I / 8) * 16);
-    L.axs = take(R * (I / 64) * 4);
+    L.aexp = take(R * ((I + 255) / 256) * 4);
     L.ybuf = take(R * H * 2);
     L.bytes = off;
     return L;
@@ -1392,7 +1387,7 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     a.ntiles = reinterpret_cast<int32_t*>(ws + L.ntiles);
     a.list = reinterpret_cast<int32_t*>(ws + L.list);
     a.actop = reinterpret_cast<vmi_u4*>(ws + L.actop);
-    a.axs = reinterpret_cast<float*>(ws + L.axs);
+    a.aexp = reinterpret_cast<int32_t*>(ws + L.aexp);
     a.ybuf = reinterpret_cast<uint16_t*>(ws + L.ybuf);
     a.out = out; a.ids_out = ids_out; a.scores_out = scores_out;
     a.max_tiles = L.max_tiles;
