@@ -479,36 +479,56 @@ __device__ __forceinline__ uint32_t pf_a_off(int r, int c) { return 16u * (8u * 
 // the logical piece a slot position holds (the inverse of pf_a_off's swizzle)
 __device__ __forceinline__ int pf_a_piece(int r, int pos) { return pos ^ (r & 7); }
 
-// Four fp16 pairs times one fp16 pair (packed multiplies, rounded to nearest).
-// The elements are taken into named scalars first: a bit cast of a vector
-// element indexed by a loop counter compiled to one element's product
+// The eight 4-bit values of one packed word, dequantised in fp16 by one
+// packed FMA per two values: (q 2^-24) s' + b' with s2 = (s', s'),
+// b2 = (b', b') and b16 = 16 b2 (the odd words of vmi_unpack_u4_f16 carry
+// 16 q).  The elements are taken into named scalars first: a bit cast of a
+// vector element indexed by a loop counter compiled to one element's result
 // replicated four times.
-typedef _Float16 pf_h2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ vmi_u4 pf_scale_f16(const vmi_u4& v, uint32_t s2) {
-    const pf_h2 s = __builtin_bit_cast(pf_h2, s2);
-    const uint32_t v0 = v.x, v1 = v.y, v2 = v.z, v3 = v.w;
+typedef _Float16 pf_h2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pf_fma_h2(uint32_t x, uint32_t y, uint32_t z) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(pf_h2v, x),
+                                                                  __builtin_bit_cast(pf_h2v, y),
+                                                                  __builtin_bit_cast(pf_h2v, z)));
+}
+__device__ __forceinline__ vmi_u4 pf_dequant_f16(uint32_t wq, uint32_t s2, uint32_t b2, uint32_t b16) {
+    const vmi_u4 u = vmi_unpack_u4_f16(wq);
+    const uint32_t u0 = u.x, u1 = u.y, u2 = u.z, u3 = u.w;
     vmi_u4 r;
-    r.x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2, v0) * s);
-    r.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2, v1) * s);
-    r.z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2, v2) * s);
-    r.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2, v3) * s);
+    r.x = pf_fma_h2(u0, s2, b2);
+    r.y = pf_fma_h2(u1, s2, b16);
+    r.z = pf_fma_h2(u2, s2, b2);
+    r.w = pf_fma_h2(u3, s2, b16);
     return r;
+}
+
+// (s', b') of a table word -> s2, b2, b16
+__device__ __forceinline__ void pf_affine_pairs(uint32_t sbw, uint32_t& s2, uint32_t& b2, uint32_t& b16) {
+    s2 = __builtin_amdgcn_perm(sbw, sbw, 0x01000100u);
+    b2 = __builtin_amdgcn_perm(sbw, sbw, 0x03020302u);
+    b16 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2v, b2) * (pf_h2v){16.0f16, 16.0f16});
 }
 
 // Gate/up: tile 128 routes x 256 intermediate rows of gate and of up (512
 // weight rows per stage), K = H, eight waves side by side (wave w: all 128
 // routes, intermediate rows 32w.. of both matrices, so each unpacked weight
-// operand feeds up to eight 16-route blocks).  Then SwiGLU rounded to bf16,
+// operand feeds up to eight 16-route blocks).  The weight operand is the
+// dequantised value in fp16, (q 2^-24) s' + b' (s' = s 2^P, b' = b 2^(P-24),
+// P the weight row's power of two), so the MFMAs accumulate the whole
+// affine product over all of K and the row's sums are times 2^(24-P) at the
+// end.  Then SwiGLU rounded to bf16,
 // and the down projection's fp16 operands of the activations: each route's
 // 256 columns times 2^-E, E the route's exponent for this block.
 constexpr int kPf8Threads = 512;
 template <int STAGES>
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     constexpr int kB = 512 * 32;
-    __shared__ __attribute__((aligned(16))) uint8_t s_ring[STAGES * (kPfA + kB)];
-    // the groups' scales, staged as bf16 bits and then rewritten as the fp16
-    // factor s * 2^P of the row's operands: [group][matrix * 256 + row]
-    __shared__ uint16_t s_scale[kMaxG][512];
+    constexpr int kRing = STAGES * (kPfA + kB);
+    // the ring, then the groups' fp16 (s', b') pairs [group][matrix * 256 +
+    // row]; after the loop both hold the activation staging
+    __shared__ __attribute__((aligned(16))) uint8_t s_mem[kRing + kMaxG * 512 * 4];
+    uint8_t* const s_ring = s_mem;
+    uint32_t(*const s_sb)[512] = reinterpret_cast<uint32_t(*)[512]>(s_mem + kRing);
     __shared__ float s_post[512];  // 2^(24 - P): what the row's sums are multiplied by at the end
     __shared__ int s_route[kTM3];
     __shared__ int s_tok[kTM3];
@@ -535,7 +555,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     {
         constexpr int kIt = (2 * 256 * (kMaxG / 8) + kPf8Threads - 1) / kPf8Threads;
         const int n16 = 2 * 256 * (G / 8);
-        uint4 v[kIt];
+        uint4 v[kIt], vb[kIt];
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
             const int i = tid + kPf8Threads * it;
@@ -543,6 +563,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
                 const int chunk = i % (G / 8), row = (i / (G / 8)) % 256, mt = i / (G / 8 * 256);
                 const int rr = min(n0 + row, I - 1);
                 v[it] = *reinterpret_cast<const uint4*>((mt ? Um.s : Gm.s) + (mrow0 + rr) * G + 8 * chunk);
+                vb[it] = *reinterpret_cast<const uint4*>((mt ? Um.b : Gm.b) + (mrow0 + rr) * G + 8 * chunk);
             }
         }
         if (tid < kTM3) {
@@ -555,9 +576,8 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         // a row's G/8 chunks of eight scales sit in G/8 consecutive lanes
         // (G/8 is 1, 2 or 4, and the branch is uniform: it < G/8).  Each
         // row's power of two 2^P puts its largest |scale| in [2^14, 2^15):
-        // s 2^P is then exact in fp16 (a bf16 value times a power of two),
-        // and the operand (q 2^-24) (s 2^P) a normal fp16 for every q > 0 of
-        // a group whose scale is at least 1/32 of the row's largest
+        // s 2^P and b 2^(P-24) are then exact in fp16 (bf16 values times
+        // powers of two), and the dequantised values about 2^-6 at most
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
             const int i = tid + kPf8Threads * it;
@@ -571,12 +591,14 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
                 int e = 0;
                 (void)frexpf(__uint_as_float(mx), &e);  // mx = f 2^e, f in [0.5, 1)
                 const int P = mx ? min(15 - e, 127) : 0;
-                const float pw = ldexpf(1.0f, P);
+                const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
+                const uint32_t bw[4] = {vb[it].x, vb[it].y, vb[it].z, vb[it].w};
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const uint32_t sb = (wv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-                    s_scale[8 * chunk + j][256 * mt + row] =
-                        __builtin_bit_cast(uint16_t, (_Float16)(vmi_bf16_to_f32((uint16_t)sb) * pw));
+                    const uint32_t sv = (wv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                    const uint32_t bv = (bw[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+                    s_sb[8 * chunk + j][256 * mt + row] =
+                        vmi_h2_bits((_Float16)(vmi_bf16_to_f32(sv) * ps), (_Float16)(vmi_bf16_to_f32(bv) * pb));
                 }
                 if (chunk == 0) s_post[256 * mt + row] = ldexpf(1.0f, 24 - P);
             }
@@ -635,18 +657,17 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
             if constexpr (MC > 0) {
                 const uint8_t* A = s_ring + u * (kPfA + kB);
                 const uint8_t* B = A + kPfA;
-                // four (column block, matrix) weight operands: the 4-bit
-                // values (n 2^-24, fp16 subnormals) times the group's fp16
-                // factor
+                // four (column block, matrix) weight operands, dequantised
                 vmi_u4 bo[4][2];
 #pragma unroll
                 for (int blk = 0; blk < 4; ++blk) {
                     const int sb = blk >> 1, mt = blk & 1;
                     const int brow = 256 * mt + 32 * w + 16 * sb + n;
                     const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
-                    const uint32_t sh = s_scale[g][brow];
-                    bo[blk][0] = pf_scale_f16(vmi_unpack_u4_f16(wq.x), sh | (sh << 16));
-                    bo[blk][1] = pf_scale_f16(vmi_unpack_u4_f16(wq.y), sh | (sh << 16));
+                    uint32_t s2, b2, b16;
+                    pf_affine_pairs(s_sb[g][brow], s2, b2, b16);
+                    bo[blk][0] = pf_dequant_f16(wq.x, s2, b2, b16);
+                    bo[blk][1] = pf_dequant_f16(wq.y, s2, b2, b16);
                 }
                 // each 16-route block's operands against the four, accumulated
                 // over all of K
@@ -690,79 +711,13 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[m][sb][mt][r] *= post;
         }
-    // affine-bias term: operand sums X [128 routes][G] and the biases as bf16
-    // pairs [512 rows][G/2] in the ring's space
-    constexpr int XS = kMaxG + 1, BS = kMaxG / 2 + 1;
-    static_assert(kTM3 * XS * 4 + 512 * BS * 4 <= sizeof(s_ring), "bias operands exceed the ring");
-    float* s_xs = reinterpret_cast<float*>(s_ring);                       // [128][XS]
-    uint32_t* s_b = reinterpret_cast<uint32_t*>(s_ring + kTM3 * XS * 4);  // [512][BS]
-    {
-        constexpr int kXi = (kTM3 * kMaxG + kPf8Threads - 1) / kPf8Threads;
-        constexpr int kBi = (512 * (kMaxG / 8) + kPf8Threads - 1) / kPf8Threads;
-        const int nx = kTM3 * G, nb16 = 512 * (G / 8);
-        float xv[kXi];
-        uint4 bv[kBi];
-#pragma unroll
-        for (int it = 0; it < kXi; ++it) {
-            const int i = tid + kPf8Threads * it;
-            if (i < nx) xv[it] = a.xsum4[(size_t)s_tok[i / G] * G + (i % G)];
-        }
-#pragma unroll
-        for (int it = 0; it < kBi; ++it) {
-            const int i = tid + kPf8Threads * it;
-            if (i < nb16) {
-                const int row = i / (G / 8), c = i % (G / 8);
-                const int mt = row >> 8, rr = min(n0 + (row & 255), I - 1);
-                bv[it] = *reinterpret_cast<const uint4*>((mt ? Um.b : Gm.b) + (mrow0 + rr) * G + 8 * c);
-            }
-        }
-#pragma unroll
-        for (int it = 0; it < kXi; ++it) {
-            const int i = tid + kPf8Threads * it;
-            if (i < nx) s_xs[(i / G) * XS + (i % G)] = xv[it];
-        }
-#pragma unroll
-        for (int it = 0; it < kBi; ++it) {
-            const int i = tid + kPf8Threads * it;
-            if (i < nb16) {
-                const int row = i / (G / 8), c = i % (G / 8);
-                uint32_t* d = s_b + row * BS + 4 * c;
-                d[0] = bv[it].x;
-                d[1] = bv[it].y;
-                d[2] = bv[it].z;
-                d[3] = bv[it].w;
-            }
-        }
-    }
-    __syncthreads();
-#pragma unroll 1
-    for (int c8 = 0; c8 < G / 8; ++c8) {
-        const int g0 = 8 * c8 + 2 * q;
-        vmi_u4 bb[2][2];
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-                const int brow = 256 * mt + 32 * w + 16 * sb + n;
-                bb[sb][mt] = vmi_bias_b_operand(s_b[brow * BS + (g0 >> 1)]);
-            }
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const int row = 16 * m + n;
-            const vmi_u4 ab = vmi_bias_a_operand(s_xs[row * XS + g0], s_xs[row * XS + g0 + 1]);
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt) acc[m][sb][mt] = vmi_mfma_bf16(ab, bb[sb][mt], acc[m][sb][mt]);
-        }
-    }
     __syncthreads();
     VMI_STAMP(4, 11);
     // SwiGLU into LDS as bf16 (the rounding of the activations):
     // route row 16m + 4q + r, column 32w + 16sb + n
     constexpr int AS = 264;
-    static_assert(kTM3 * AS * 2 <= sizeof(s_ring), "activation staging exceeds the ring");
-    uint16_t* s_act = reinterpret_cast<uint16_t*>(s_ring);  // [128][AS]
+    static_assert(kTM3 * AS * 2 <= sizeof(s_mem), "activation staging exceeds the ring and table");
+    uint16_t* s_act = reinterpret_cast<uint16_t*>(s_mem);  // [128][AS]
 #pragma unroll
     for (int m = 0; m < 8; ++m)
 #pragma unroll
@@ -833,25 +788,6 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 // then times the route's combine weight into one bf16 row per (token, rank).
 // MAXG bounds the quantisation groups of K the LDS table holds.
 constexpr int kPfMaxIB = 8;  // 256-column blocks of the intermediate size (I <= 2048)
-typedef _Float16 pf_h2v __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pf_fma_h2(uint32_t x, uint32_t y, uint32_t z) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(pf_h2v, x),
-                                                                  __builtin_bit_cast(pf_h2v, y),
-                                                                  __builtin_bit_cast(pf_h2v, z)));
-}
-// the eight values of one packed word, dequantised: s2 = (s', s'), b2 = (b', b'),
-// b16 = 16 b2 (the odd words of vmi_unpack_u4_f16 carry 16 q)
-__device__ __forceinline__ vmi_u4 pf_dequant_f16(uint32_t wq, uint32_t s2, uint32_t b2, uint32_t b16) {
-    const vmi_u4 u = vmi_unpack_u4_f16(wq);
-    const uint32_t u0 = u.x, u1 = u.y, u2 = u.z, u3 = u.w;
-    vmi_u4 r;
-    r.x = pf_fma_h2(u0, s2, b2);
-    r.y = pf_fma_h2(u1, s2, b16);
-    r.z = pf_fma_h2(u2, s2, b2);
-    r.w = pf_fma_h2(u3, s2, b16);
-    return r;
-}
-
 template <int STAGES, int MAXG>
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     constexpr int kB = 512 * 32;
@@ -984,10 +920,8 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
                 for (int sb = 0; sb < 4; ++sb) {
                     const int brow = 64 * w + 16 * sb + n;
                     const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
-                    const uint32_t sbw = s_sb[g][brow];
-                    const uint32_t s2 = __builtin_amdgcn_perm(sbw, sbw, 0x01000100u);
-                    const uint32_t b2 = __builtin_amdgcn_perm(sbw, sbw, 0x03020302u);
-                    const uint32_t b16 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2v, b2) * (pf_h2v){16.0f16, 16.0f16});
+                    uint32_t s2, b2, b16;
+                    pf_affine_pairs(s_sb[g][brow], s2, b2, b16);
                     wo[sb][0] = pf_dequant_f16(wq.x, s2, b2, b16);
                     wo[sb][1] = pf_dequant_f16(wq.y, s2, b2, b16);
                 }
@@ -1429,7 +1363,7 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
     const int tile_slots = 8 * ((L.max_tiles + 7) / 8);
-    hipLaunchKernelGGL(k_pf_gateup3<3>, dim3(tile_slots * ((D.inter + 255) / 256)), dim3(kPf8Threads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_gateup3<2>, dim3(tile_slots * ((D.inter + 255) / 256)), dim3(kPf8Threads), 0, s, a);
     if (D.inter <= 512)
         hipLaunchKernelGGL((k_pf_down3<3, 8>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
     else
