@@ -550,6 +550,27 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     const vmi_qmat Gm = tl.x >= 0 ? a.gate : a.sh_gate;
     const vmi_qmat Um = tl.x >= 0 ? a.up : a.sh_up;
     const size_t mrow0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)I;
+    // DMA sources of the weights: pieces p = tid + 512 j (row p/2: matrix
+    // row/256, intermediate row n0 + row%256; half (p%2) ^ bit 3 of row)
+    const uint32_t* bsrc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int p = tid + kPf8Threads * j;
+        const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
+        const int mt = brow >> 8, rr = min(n0 + (brow & 255), I - 1);
+        // MFMA-major pool: the 16 bytes of group g, half h of row rr sit in
+        // block (rr / 16, g / 2) at lane 16 (2 (g % 2) + h) + rr % 16
+        bsrc[j] = (mt ? Um.w : Gm.w) + mrow0 * HW + (size_t)(rr >> 4) * (H / 128) * 256 + 64 * h + 4 * (rr & 15);
+    }
+    auto issue_b = [&](int g, int u) {
+        uint8_t* A = s_ring + u * (kPfA + kB);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            vmi_lds_dma16_opaque(bsrc[j] + 256 * (g >> 1) + 128 * (g & 1), A + kPfA + 16 * (kPf8Threads * j + 64 * w));
+    };
+    // the first groups' weights are in flight while the prologue runs
+#pragma unroll
+    for (int u = 0; u < STAGES - 1; ++u) issue_b(u < G ? u : G - 1, u);
     // staging loads are all issued before their values are stored, so the
     // workgroup waits for one memory latency, not one per loop iteration
     {
@@ -605,29 +626,23 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         }
     }
     __syncthreads();
-    // DMA sources: A pieces p = tid + 512 j (row p/8, slot piece p%8 = logical
-    // piece (p%8) ^ (row & 7)); weight pieces p = tid + 512 j (row p/2: matrix
-    // row/256, intermediate row n0 + row%256; half (p%2) ^ bit 3 of row)
+    // DMA sources of the operands: pieces p = tid + 512 j (row p/8, slot
+    // piece p%8 = logical piece (p%8) ^ (row & 7))
     const vmi_u4* asrc[2];
-    const uint32_t* bsrc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int p = tid + kPf8Threads * j;
         const int arow = p >> 3, c = pf_a_piece(arow, p & 7);
         asrc[j] = a.xop4 + (size_t)s_tok[arow] * HW + c;
-        const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
-        const int mt = brow >> 8, rr = min(n0 + (brow & 255), I - 1);
-        // MFMA-major pool: the 16 bytes of group g, half h of row rr sit in
-        // block (rr / 16, g / 2) at lane 16 (2 (g % 2) + h) + rr % 16
-        bsrc[j] = (mt ? Um.w : Gm.w) + mrow0 * HW + (size_t)(rr >> 4) * (H / 128) * 256 + 64 * h + 4 * (rr & 15);
     }
-    auto issue = [&](int g, int u) {
+    auto issue_a = [&](int g, int u) {
         uint8_t* A = s_ring + u * (kPfA + kB);
 #pragma unroll
         for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            vmi_lds_dma16_opaque(bsrc[j] + 256 * (g >> 1) + 128 * (g & 1), A + kPfA + 16 * (kPf8Threads * j + 64 * w));
+    };
+    auto issue = [&](int g, int u) {
+        issue_a(g, u);
+        issue_b(g, u);
     };
     vmi_f4 acc[8][2][2];
 #pragma unroll
@@ -638,7 +653,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
             for (int mt = 0; mt < 2; ++mt) acc[m][sb][mt] = vmi_f4{0.f, 0.f, 0.f, 0.f};
     VMI_STAMP(4, 1);
 #pragma unroll
-    for (int u = 0; u < STAGES - 1; ++u) issue(u < G ? u : G - 1, u);
+    for (int u = 0; u < STAGES - 1; ++u) issue_a(u < G ? u : G - 1, u);
     // the stage loop for MC of the wave's 16-route blocks holding routes (a
     // loop per MC, so each keeps its own register allocation; MC = 0 only
     // moves the ring and keeps the barriers)
@@ -647,7 +662,12 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 #pragma unroll 1
         for (int g = 0; g < G; ++g) {
             const int u = g % STAGES;
-            pf_wait_vmcnt<4 * (STAGES - 2)>();  // group g's pieces (this thread's) have landed
+            // group g's pieces (this thread's) have landed: the weights of
+            // the first STAGES - 1 groups went out before their operands
+            if (g == 0)
+                pf_wait_vmcnt<2 * (STAGES - 2)>();
+            else
+                pf_wait_vmcnt<4 * (STAGES - 2)>();
             __syncthreads();                    // everyone's; and the slot of group g-1 is free
             if ((g & 3) == 0 && g < 32) VMI_STAMP(4, 2 + (g >> 2));
             {
@@ -670,7 +690,8 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
                     bo[blk][1] = pf_dequant_f16(wq.y, s2, b2, b16);
                 }
                 // each 16-route block's operands against the four, accumulated
-                // over all of K
+                // over all of K; the weights go first, so a lane holds four
+                // consecutive weight rows of one route
 #pragma unroll
                 for (int m = 0; m < MC; ++m) {
                     const int row = 16 * m + n;
@@ -678,10 +699,10 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
                     const vmi_u4 a1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
 #pragma unroll
                     for (int blk = 0; blk < 4; ++blk)
-                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(a0, bo[blk][0], acc[m][blk >> 1][blk & 1]);
+                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bo[blk][0], a0, acc[m][blk >> 1][blk & 1]);
 #pragma unroll
                     for (int blk = 0; blk < 4; ++blk)
-                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(a1, bo[blk][1], acc[m][blk >> 1][blk & 1]);
+                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bo[blk][1], a1, acc[m][blk >> 1][blk & 1]);
                 }
             }
         }
@@ -700,39 +721,51 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     pf_wait_vmcnt<0>();
     __syncthreads();
     VMI_STAMP(4, 10);
-    // the rows' power-of-two factors out of the sums (exact)
+    // the rows' power-of-two factors out of the sums (exact): lane (n, q)
+    // holds route row 16m + n, weight rows 256mt + 32w + 16sb + 4q .. + 3
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-            const float post = s_post[256 * mt + 32 * w + 16 * sb + n];
+            const float4 p4 = *reinterpret_cast<const float4*>(&s_post[256 * mt + 32 * w + 16 * sb + 4 * q]);
 #pragma unroll
-            for (int m = 0; m < 8; ++m)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[m][sb][mt][r] *= post;
+            for (int m = 0; m < 8; ++m) {
+                acc[m][sb][mt][0] *= p4.x;
+                acc[m][sb][mt][1] *= p4.y;
+                acc[m][sb][mt][2] *= p4.z;
+                acc[m][sb][mt][3] *= p4.w;
+            }
         }
     __syncthreads();
     VMI_STAMP(4, 11);
     // SwiGLU into LDS as bf16 (the rounding of the activations):
-    // route row 16m + 4q + r, column 32w + 16sb + n
+    // route row 16m + n, columns 32w + 16sb + 4q .. + 3 (one 8-byte store);
+    // the 16-route blocks past the tile's count hold no route
     constexpr int AS = 264;
     static_assert(kTM3 * AS * 2 <= sizeof(s_mem), "activation staging exceeds the ring and table");
     uint16_t* s_act = reinterpret_cast<uint16_t*>(s_mem);  // [128][AS]
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
+    for (int m = 0; m < 8; ++m) {
+        if (m >= mcnt) break;
+        const int row = 16 * m + n;
+        const float inv = s_inv[row];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = 16 * m + 4 * q + r;
-            const float inv = s_inv[row];
+        for (int sb = 0; sb < 2; ++sb) {
+            float v[4];
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb) {
+            for (int r = 0; r < 4; ++r) {
                 const float gv = acc[m][sb][0][r] * inv, uv = acc[m][sb][1][r] * inv;
                 // hardware exp2 and reciprocal (about 1 ulp each): the value is
                 // rounded to bf16 right after
                 const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gv * 1.44269504f));
-                s_act[row * AS + 32 * w + 16 * sb + n] = vmi_f32_to_bf16(gv * sg * uv);
+                v[r] = gv * sg * uv;
             }
+            uint2 o;
+            o.x = vmi_pack_bf16x2(v[0], v[1]);
+            o.y = vmi_pack_bf16x2(v[2], v[3]);
+            *reinterpret_cast<uint2*>(s_act + row * AS + 32 * w + 16 * sb + 4 * q) = o;
         }
+    }
     __syncthreads();
     VMI_STAMP(4, 13);
     // each route row's largest |activation| over the block's columns (four
@@ -814,6 +847,24 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     // the down projection is group-major: row h of group g of slot m at
     // (m * G + g) * H + h (32 bytes of words; one bf16 scale and bias)
     const size_t mbase = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)G * a.H + h0;
+    // DMA sources of the weights: pieces p = tid + 512 j (row p/2, half
+    // (p%2) ^ bit 3 of the row)
+    const uint32_t* bsrc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int p = tid + kPf8Threads * j;
+        const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
+        bsrc[j] = Dm.w + (mbase + brow) * 8 + 4 * h;
+    }
+    auto issue_b = [&](int g, int u) {
+        uint8_t* A = s_ring + u * (kPfA + kB);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            vmi_lds_dma16_opaque(bsrc[j] + (size_t)g * a.H * 8, A + kPfA + 16 * (kPf8Threads * j + 64 * w));
+    };
+    // the first groups' weights are in flight while the prologue runs
+#pragma unroll
+    for (int u = 0; u < STAGES - 1; ++u) issue_b(u < G ? u : G - 1, u);
     {
         // thread t: hidden row h0 + t, every group (a wave reads 128
         // contiguous bytes per group); these loads are issued first, the
@@ -858,23 +909,21 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     }
     __syncthreads();
     const vmi_u4* asrc[2];
-    const uint32_t* bsrc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int p = tid + kPf8Threads * j;
         const int arow = p >> 3, c = pf_a_piece(arow, p & 7);
         const int rt = s_route[arow];
         asrc[j] = a.actop + (size_t)(rt >= 0 ? rt : 0) * IW + c;
-        const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
-        bsrc[j] = Dm.w + (mbase + brow) * 8 + 4 * h;
     }
-    auto issue = [&](int g, int u) {
+    auto issue_a = [&](int g, int u) {
         uint8_t* A = s_ring + u * (kPfA + kB);
 #pragma unroll
         for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            vmi_lds_dma16_opaque(bsrc[j] + (size_t)g * a.H * 8, A + kPfA + 16 * (kPf8Threads * j + 64 * w));
+    };
+    auto issue = [&](int g, int u) {
+        issue_a(g, u);
+        issue_b(g, u);
     };
     vmi_f4 acc[8][4];
 #pragma unroll
@@ -883,7 +932,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
     VMI_STAMP(3, 1);
 #pragma unroll
-    for (int u = 0; u < STAGES - 1; ++u) issue(u < G ? u : G - 1, u);
+    for (int u = 0; u < STAGES - 1; ++u) issue_a(u < G ? u : G - 1, u);
     // the stage loop for MC active 16-route blocks (a loop per MC, so each
     // keeps its own register allocation; MC = 0 only moves the ring and keeps
     // the barriers)
@@ -892,7 +941,12 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
 #pragma unroll 1
         for (int g = 0; g < G; ++g) {
             const int u = g % STAGES;
-            pf_wait_vmcnt<4 * (STAGES - 2)>();
+            // group g's pieces (this thread's) have landed: the weights of
+            // the first STAGES - 1 groups went out before their operands
+            if (g == 0)
+                pf_wait_vmcnt<2 * (STAGES - 2)>();
+            else
+                pf_wait_vmcnt<4 * (STAGES - 2)>();
             __syncthreads();
             {
                 const int gn = g + STAGES - 1;
