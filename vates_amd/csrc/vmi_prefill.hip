@@ -10,7 +10,8 @@
 //   k_pf_prep     per token: optional RMSNorm, MFMA operands of x (fp16, range
 //                 factor per token), per-group operand sums; clears counters
 //   k_pf_router3  router logits [T, E] as a tiled MFMA GEMM on the 4/8-bit
-//                 router (weights enter the MFMA as exact fp16 subnormals)
+//                 router (weights enter the MFMA as exact fp16 subnormals),
+//                 in two halves of K that the top-k adds
 //   k_pf_sgate    shared-expert gate logit per token (one wave per token)
 //   k_pf_topk     one wave per token: top-k, softmax, renorm, slot table
 //   k_pf_count    routes per slot and each route's rank in its slot
@@ -66,7 +67,7 @@ struct PfArgs {
     vmi_u4* xop8;               // [T, H/8] fp16 operands, 8-bit slot order (8-bit router)
     float* xsum8;               // [T, H/64]
     float* fscale;              // [T]
-    float* logits;              // [T, E]
+    float* logits;              // [2, T, E]: the router's two halves of K
     float* sglogit;             // [T]
     int32_t* ids;               // [T, k]
     float* scores;              // [T, k]
@@ -282,11 +283,17 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_topk(PfArgs a) {
     const int lane = threadIdx.x & 63, w = pf_wave();
     const int t = blockIdx.x * (kPfThreads / 64) + w;
     if (t >= a.T) return;  // whole waves; nothing below synchronises the workgroup
+    // the logit is the sum of the router's two halves of K, in that order
     const float* lt = a.logits + (size_t)t * a.E;
+    const float* lt2 = lt + (size_t)a.T * a.E;
     const int nreal = a.E >> 6;  // key slots i < E/64 are real (uniform)
+    float lv[NI];
     uint64_t key[NI];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) key[i] = i < nreal ? pf_rank_key(lt[lane + 64 * i], lane + 64 * i) : 0ull;
+    for (int i = 0; i < NI; ++i) {
+        lv[i] = i < nreal ? lt[lane + 64 * i] + lt2[lane + 64 * i] : 0.0f;
+        key[i] = i < nreal ? pf_rank_key(lv[i], lane + 64 * i) : 0ull;
+    }
 #pragma unroll
     for (int size = 2; size <= NI; size *= 2)
 #pragma unroll
@@ -320,7 +327,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_topk(PfArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const bool sel = lane < a.k;
     const int my_idx = sel ? s_sel[w][lane] : 0;
-    const float my_val = sel ? lt[my_idx] : 0.0f;
+    const float my_val = sel ? lt[my_idx] + lt2[my_idx] : 0.0f;
     const float mx = vmi_readlane_f32(my_val, 0);
     const bool bad = __ballot(sel && !(fabsf(my_val) < 3.0e38f)) != 0;
     const float e = sel ? expf(my_val - mx) : 0.0f;
@@ -329,7 +336,9 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_topk(PfArgs a) {
         for (int j = 0; j < a.k; ++j) den = den + vmi_readlane_f32(e, j);
     } else {
         float part = 0.0f;
-        for (int i = 0; i < nreal; ++i) part = part + expf(lt[lane + 64 * i] - mx);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            if (i < nreal) part = part + expf(lv[i] - mx);
         den = vmi_wave_sum_canon(part);
     }
     if (sel) {
@@ -1028,9 +1037,10 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
 }
 
 // Router logits [T, E] as the same 128 x 128 tile GEMM (tokens x experts, K =
-// H), dense: tile L/8-major as above with NB = ceil(E/128) expert blocks.
-// 4-bit rows are 32 bytes a group (as gate/up); 8-bit rows 64 bytes, 16-byte
-// piece c of row r kept at c ^ ((r >> 2) & 3).  logits = acc / f (+ bias).
+// H), dense: tile L/8-major as above with NB = 2 ceil(E/128) (expert block,
+// half of K) pairs.  4-bit rows are 32 bytes a group (as gate/up); 8-bit rows
+// 64 bytes, 16-byte piece c of row r kept at c ^ ((r >> 2) & 3).  Half kh of
+// the logits = acc / f (+ bias in half 0); the top-k adds half 0 and half 1.
 __device__ __forceinline__ uint32_t pf_b8_off(int r, int c) { return 16u * (4u * r + (unsigned)(c ^ ((r >> 2) & 3))); }
 
 template <int BITS>
@@ -1041,12 +1051,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_router3(PfArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
     const int mh = w & 1, nh = w >> 1;
-    const int NB = (a.E + 127) / 128;
-    int ti, nb;
-    pf_tile_of(blockIdx.x, NB, ti, nb);
+    // two workgroups per tile, one per half of K (kh), so a CU holds two
+    const int NB = 2 * ((a.E + 127) / 128);
+    int ti, nbk;
+    pf_tile_of(blockIdx.x, NB, ti, nbk);
     const int t0 = ti * kTM3;
     if (t0 >= a.T) return;
+    const int nb = nbk >> 1, kh = nbk & 1;
     const int H = a.H, HW = H / 8, G = H / 64, E = a.E;
+    const int g0 = kh * (G / 2), g1 = g0 + G / 2;  // this half's groups
     const int e0 = nb * 128;
     const int wpr = H * BITS / 32;
     const vmi_u4* xop = BITS == 4 ? a.xop4 : a.xop8;
@@ -1095,15 +1108,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_router3(PfArgs a) {
 #pragma unroll
         for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kPfStages - 1; ++u) issue(u < G ? u : G - 1, u);
+    for (int u = 0; u < kPfStages - 1; ++u) issue(g0 + u < g1 ? g0 + u : g1 - 1, u);
 #pragma unroll 1
-    for (int g = 0; g < G; ++g) {
-        const int u = g % kPfStages;
+    for (int g = g0; g < g1; ++g) {
+        const int u = (g - g0) % kPfStages;
         pf_wait_vmcnt<(4 + NBD) * (kPfStages - 2)>();
         __syncthreads();
         {
             const int gn = g + kPfStages - 1;
-            issue(gn < G ? gn : G - 1, gn % kPfStages);
+            issue(gn < g1 ? gn : g1 - 1, (gn - g0) % kPfStages);
         }
         const uint8_t* A = s_ring + u * (kPfA + kB);
         const uint8_t* B = A + kPfA;
@@ -1169,23 +1182,27 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_router3(PfArgs a) {
         s_b[row * BS + c] = reinterpret_cast<const uint32_t*>(a.router.b + (size_t)min(e0 + row, E - 1) * G)[c];
     }
     __syncthreads();
+    // the affine terms of eight groups per MFMA: chunks [0, C/2) in the first
+    // half's workgroup (rounded up), the rest in the second's
+    const int C = G / 8, ch = (C + 1) / 2;
 #pragma unroll 1
-    for (int c8 = 0; c8 < G / 8; ++c8) {
-        const int g0 = 8 * c8 + 2 * q;
+    for (int c8 = kh ? ch : 0; c8 < (kh ? C : ch); ++c8) {
+        const int gq = 8 * c8 + 2 * q;
         vmi_u4 ab[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             const int row = 64 * mh + 16 * m + n;
-            ab[m] = vmi_bias_a_operand(s_xs[row * XS + g0], s_xs[row * XS + g0 + 1]);
+            ab[m] = vmi_bias_a_operand(s_xs[row * XS + gq], s_xs[row * XS + gq + 1]);
         }
 #pragma unroll
         for (int sb = 0; sb < 4; ++sb) {
             const int brow = 64 * nh + 16 * sb + n;
-            const vmi_u4 bb = vmi_bias_b_operand(s_b[brow * BS + (g0 >> 1)]);
+            const vmi_u4 bb = vmi_bias_b_operand(s_b[brow * BS + (gq >> 1)]);
 #pragma unroll
             for (int m = 0; m < 4; ++m) acc[m][sb] = vmi_mfma_bf16(ab[m], bb, acc[m][sb]);
         }
     }
+    float* const lo = a.logits + (size_t)kh * a.T * E;
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -1198,8 +1215,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_router3(PfArgs a) {
                 const int e = e0 + 64 * nh + 16 * sb + n;
                 if (e >= E) continue;
                 float v = acc[m][sb][r] * inv;
-                if (a.logit_bias) v += a.logit_bias[e];
-                a.logits[(size_t)t * E + e] = v;
+                if (a.logit_bias && kh == 0) v += a.logit_bias[e];
+                lo[(size_t)t * E + e] = v;
             }
         }
 }
@@ -1274,7 +1291,7 @@ PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) 
     L.xop8 = router_bits == 8 ? take((size_t)T * (H / 8) * 16) : 0;
     L.xsum8 = router_bits == 8 ? take((size_t)T * (H / 64) * 4) : 0;
     L.fscale = take((size_t)T * 4);
-    L.logits = take((size_t)T * E * 4);
+    L.logits = take((size_t)2 * T * E * 4);
     L.sglogit = take((size_t)T * 4);
     L.ids = take((size_t)T * k * 4);
     L.scores = take((size_t)T * k * 4);
@@ -1388,7 +1405,7 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
         case 4: hipLaunchKernelGGL(k_pf_prep<4>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
         default: return vmi::fail(VMI_ERR_UNSUPPORTED, "hidden=%d must be 512, 1024 or 2048", D.hidden);
     }
-    const dim3 rgrid(8 * (((T + kTM3 - 1) / kTM3 + 7) / 8) * ((D.num_experts + 127) / 128));
+    const dim3 rgrid(8 * (((T + kTM3 - 1) / kTM3 + 7) / 8) * 2 * ((D.num_experts + 127) / 128));
     if (D.router_bits == 4)
         hipLaunchKernelGGL(k_pf_router3<4>, rgrid, dim3(kPfThreads), 0, s, a);
     else
