@@ -63,7 +63,7 @@ struct PfArgs {
     vmi_qmat sh_gate, sh_up, sh_down, sgate;
     // workspace
     vmi_u4* xop4;               // [T, H/8] fp16 operands, 4-bit slot order
-    float* xsum4;               // [T, H/64]
+    float* xsum4;               // [T, H/64] (4-bit router only, else null)
     vmi_u4* xop8;               // [T, H/8] fp16 operands, 8-bit slot order (8-bit router)
     float* xsum8;               // [T, H/64]
     float* fscale;              // [T]
@@ -90,13 +90,16 @@ struct PfArgs {
 
 // ------------------------------------------------------------------ prep
 // fp16 operand of 8 columns for 4-bit words: slots {0,4,1,5,2,6,3,7}, odd
-// nibble slots divided by 16; s accumulates what the MFMA multiplies.
+// nibble slots divided by 16; with SUM, s accumulates what the MFMA
+// multiplies (the 4-bit router's affine term needs it).
+template <bool SUM>
 __device__ __forceinline__ vmi_u4 op4(const float (&v)[8], float f, float& s) {
     const _Float16 h0 = (_Float16)(v[0] * f), h1 = (_Float16)(v[4] * f);
     const _Float16 h2 = (_Float16)(v[1] * f * 0.0625f), h3 = (_Float16)(v[5] * f * 0.0625f);
     const _Float16 h4 = (_Float16)(v[2] * f), h5 = (_Float16)(v[6] * f);
     const _Float16 h6 = (_Float16)(v[3] * f * 0.0625f), h7 = (_Float16)(v[7] * f * 0.0625f);
-    s += (float)h0 + (float)h1 + (float)h4 + (float)h5 + 16.0f * ((float)h2 + (float)h3 + (float)h6 + (float)h7);
+    if constexpr (SUM)
+        s += (float)h0 + (float)h1 + (float)h4 + (float)h5 + 16.0f * ((float)h2 + (float)h3 + (float)h6 + (float)h7);
     vmi_u4 r;
     r[0] = vmi_h2_bits(h0, h1);
     r[1] = vmi_h2_bits(h2, h3);
@@ -170,8 +173,14 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
         for (int c = 0; c < NCH; ++c) {
             float g[8];
             bf16x8(*reinterpret_cast<const uint4*>(nw + 8 * c), g);
+            // rounded to bf16 in pairs (v_cvt_pk_bf16_f32: the bits of
+            // vmi_f32_to_bf16 for every non-NaN value)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[c][i] = vmi_bf16_to_f32(vmi_f32_to_bf16((v[c][i] * inv) * g[i]));
+            for (int i = 0; i < 8; i += 2) {
+                const uint32_t pk = vmi_pack_bf16x2((v[c][i] * inv) * g[i], (v[c][i + 1] * inv) * g[i + 1]);
+                v[c][i] = __uint_as_float(pk << 16);
+                v[c][i + 1] = __uint_as_float(pk & 0xffff0000u);
+            }
         }
     }
     float amax = 0.0f;
@@ -185,10 +194,16 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
     constexpr int LPG = 8 / NCH;
     float s4 = 0.0f, s8 = 0.0f;
     const size_t orow = (size_t)t * (a.H / 8) + lane * NCH;
+    if (a.xsum4) {
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        a.xop4[orow + c] = op4(v[c], f, s4);
-        if (a.xop8) a.xop8[orow + c] = op8(v[c], f, s8);
+        for (int c = 0; c < NCH; ++c) a.xop4[orow + c] = op4<true>(v[c], f, s4);
+    } else {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) a.xop4[orow + c] = op4<false>(v[c], f, s4);
+    }
+    if (a.xop8) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) a.xop8[orow + c] = op8(v[c], f, s8);
     }
     // lanes of one group sum their partials in lane order
 #pragma unroll
@@ -198,7 +213,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
     }
     if ((lane % LPG) == 0) {
         const size_t g = (size_t)t * (a.H / 64) + lane / LPG;
-        a.xsum4[g] = s4;
+        if (a.xsum4) a.xsum4[g] = s4;
         if (a.xsum8) a.xsum8[g] = s8;
     }
     if (lane == 0) a.fscale[t] = f;
@@ -1287,7 +1302,7 @@ PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) 
     L.max_tiles = (T * k + kTM3 - 1) / kTM3 + cap + (T + kTM3 - 1) / kTM3;
     L.status = take(256);
     L.xop4 = take((size_t)T * (H / 8) * 16);
-    L.xsum4 = take((size_t)T * (H / 64) * 4);
+    L.xsum4 = router_bits == 4 ? take((size_t)T * (H / 64) * 4) : 0;  // the 4-bit router's affine term
     L.xop8 = router_bits == 8 ? take((size_t)T * (H / 8) * 16) : 0;
     L.xsum8 = router_bits == 8 ? take((size_t)T * (H / 64) * 4) : 0;
     L.fscale = take((size_t)T * 4);
@@ -1376,7 +1391,7 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     a.sgate = D.shared_expert_gate;
     a.status = reinterpret_cast<uint32_t*>(ws + L.status);
     a.xop4 = reinterpret_cast<vmi_u4*>(ws + L.xop4);
-    a.xsum4 = reinterpret_cast<float*>(ws + L.xsum4);
+    a.xsum4 = L.xsum4 ? reinterpret_cast<float*>(ws + L.xsum4) : nullptr;
     a.xop8 = D.router_bits == 8 ? reinterpret_cast<vmi_u4*>(ws + L.xop8) : nullptr;
     a.xsum8 = D.router_bits == 8 ? reinterpret_cast<float*>(ws + L.xsum8) : nullptr;
     a.fscale = reinterpret_cast<float*>(ws + L.fscale);
