@@ -498,10 +498,16 @@ __device__ __forceinline__ void pf_tile_of(int L, int nb_count, int& ti, int& nb
     nb = idx % nb_count;
 }
 
-// byte offset of A row r, logical 16-byte piece c, inside a slot
-__device__ __forceinline__ uint32_t pf_a_off(int r, int c) { return 16u * (8u * r + (unsigned)(c ^ (r & 7))); }
+// byte offset of A row r, logical 16-byte piece c, inside a slot.  Rows are
+// 128 bytes (half of the 64 four-byte banks), so rows r and r + 1 take the
+// two bank halves and the piece is swizzled by bits 1..3 of the row: the 16
+// rows a ds_read_b128 of one piece touches (16 lanes) then cover all 64 banks
+// once.
+__device__ __forceinline__ uint32_t pf_a_off(int r, int c) {
+    return 16u * (8u * r + (unsigned)(c ^ ((r >> 1) & 7)));
+}
 // the logical piece a slot position holds (the inverse of pf_a_off's swizzle)
-__device__ __forceinline__ int pf_a_piece(int r, int pos) { return pos ^ (r & 7); }
+__device__ __forceinline__ int pf_a_piece(int r, int pos) { return pos ^ ((r >> 1) & 7); }
 
 // The eight 4-bit values of one packed word, dequantised in fp16 by one
 // packed FMA per two values: (q 2^-24) s' + b' with s2 = (s', s'),
@@ -544,14 +550,17 @@ __device__ __forceinline__ void pf_affine_pairs(uint32_t sbw, uint32_t& s2, uint
 // and the down projection's fp16 operands of the activations: each route's
 // 256 columns times 2^-E, E the route's exponent for this block.
 constexpr int kPf8Threads = 512;
-template <int STAGES>
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     constexpr int kB = 512 * 32;
-    constexpr int kRing = STAGES * (kPfA + kB);
-    // the ring, then the groups' fp16 (s', b') pairs [group][matrix * 256 +
-    // row]; after the loop both hold the activation staging
+    // two slots of operand rows (shared by the waves) and three of weight
+    // rows (a wave DMAs exactly the weight rows it reads, so their slots need
+    // no barrier, and group g + 1's weights are dequantised under group g's
+    // MFMAs), then the groups' fp16 (s', b') pairs [group][matrix * 256 +
+    // row]; after the loop all of it holds the activation staging
+    constexpr int kAS = 2, kBS = 3, kRing = kAS * kPfA + kBS * kB;
     __shared__ __attribute__((aligned(16))) uint8_t s_mem[kRing + kMaxG * 512 * 4];
-    uint8_t* const s_ring = s_mem;
+    uint8_t* const s_ra = s_mem;
+    uint8_t* const s_rb = s_mem + kAS * kPfA;
     uint32_t(*const s_sb)[512] = reinterpret_cast<uint32_t(*)[512]>(s_mem + kRing);
     __shared__ float s_post[512];  // 2^(24 - P): what the row's sums are multiplied by at the end
     __shared__ int s_route[kTM3];
@@ -587,14 +596,14 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         bsrc[j] = (mt ? Um.w : Gm.w) + mrow0 * HW + (size_t)(rr >> 4) * (H / 128) * 256 + 64 * h + 4 * (rr & 15);
     }
     auto issue_b = [&](int g, int u) {
-        uint8_t* A = s_ring + u * (kPfA + kB);
+        uint8_t* B = s_rb + u * kB;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            vmi_lds_dma16_opaque(bsrc[j] + 256 * (g >> 1) + 128 * (g & 1), A + kPfA + 16 * (kPf8Threads * j + 64 * w));
+            vmi_lds_dma16_opaque(bsrc[j] + 256 * (g >> 1) + 128 * (g & 1), B + 16 * (kPf8Threads * j + 64 * w));
     };
-    // the first groups' weights are in flight while the prologue runs
-#pragma unroll
-    for (int u = 0; u < STAGES - 1; ++u) issue_b(u < G ? u : G - 1, u);
+    // the first two groups' weights are in flight while the prologue runs
+    issue_b(0, 0);
+    issue_b(G > 1 ? 1 : 0, 1);
     // staging loads are all issued before their values are stored, so the
     // workgroup waits for one memory latency, not one per loop iteration
     {
@@ -660,13 +669,24 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         asrc[j] = a.xop4 + (size_t)s_tok[arow] * HW + c;
     }
     auto issue_a = [&](int g, int u) {
-        uint8_t* A = s_ring + u * (kPfA + kB);
+        uint8_t* A = s_ra + u * kPfA;
 #pragma unroll
         for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
     };
-    auto issue = [&](int g, int u) {
-        issue_a(g, u);
-        issue_b(g, u);
+    // this wave's four (column block, matrix) weight operands of group g from
+    // weight slot u, dequantised
+    auto dequant = [&](vmi_u4 (&bo)[4][2], int u, int g) {
+        const uint8_t* B = s_rb + u * kB;
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            const int sb = blk >> 1, mt = blk & 1;
+            const int brow = 256 * mt + 32 * w + 16 * sb + n;
+            const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
+            uint32_t s2, b2, b16;
+            pf_affine_pairs(s_sb[g][brow], s2, b2, b16);
+            bo[blk][0] = pf_dequant_f16(wq.x, s2, b2, b16);
+            bo[blk][1] = pf_dequant_f16(wq.y, s2, b2, b16);
+        }
     };
     vmi_f4 acc[8][2][2];
 #pragma unroll
@@ -676,59 +696,62 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) acc[m][sb][mt] = vmi_f4{0.f, 0.f, 0.f, 0.f};
     VMI_STAMP(4, 1);
-#pragma unroll
-    for (int u = 0; u < STAGES - 1; ++u) issue_a(u < G ? u : G - 1, u);
-    // the stage loop for MC of the wave's 16-route blocks holding routes (a
-    // loop per MC, so each keeps its own register allocation; MC = 0 only
-    // moves the ring and keeps the barriers)
+    issue_a(0, 0);
+    // the stage loop for MC of the 16-route blocks holding routes (a loop per
+    // MC, so each keeps its own register allocation; MC = 0 only moves the
+    // ring and keeps the barriers).  Stage g: group g's operands (everyone's
+    // DMA, hence the barrier) against its weights dequantised during stage
+    // g - 1, while group g + 1's weights (this wave's own DMA, landed) are
+    // dequantised; the DMA of operands g + 1 and weights g + 2 goes out.
     auto stage_loop = [&](auto mc_tag) {
         constexpr int MC = decltype(mc_tag)::value;
-#pragma unroll 1
-        for (int g = 0; g < G; ++g) {
-            const int u = g % STAGES;
-            // group g's pieces (this thread's) have landed: the weights of
-            // the first STAGES - 1 groups went out before their operands
-            if (g == 0)
-                pf_wait_vmcnt<2 * (STAGES - 2)>();
-            else
-                pf_wait_vmcnt<4 * (STAGES - 2)>();
-            __syncthreads();                    // everyone's; and the slot of group g-1 is free
+        // stage g with this group's dequantised weights bcur, filling bnext
+        auto stage = [&](int g, const vmi_u4 (&bcur)[4][2], vmi_u4 (&bnext)[4][2]) {
+            pf_wait_vmcnt<0>();  // operands g and weights g + 1 (this thread's) have landed
+            __syncthreads();     // everyone's operands g; operand slot (g + 1) % 2 is free
             if ((g & 3) == 0 && g < 32) VMI_STAMP(4, 2 + (g >> 2));
-            {
-                const int gn = g + STAGES - 1;
-                issue(gn < G ? gn : G - 1, gn % STAGES);
-            }
+            if (g + 1 < G) issue_a(g + 1, (g + 1) & 1);
+            if (g + 2 < G) issue_b(g + 2, (g + 2) % kBS);
             if constexpr (MC > 0) {
-                const uint8_t* A = s_ring + u * (kPfA + kB);
-                const uint8_t* B = A + kPfA;
-                // four (column block, matrix) weight operands, dequantised
-                vmi_u4 bo[4][2];
-#pragma unroll
-                for (int blk = 0; blk < 4; ++blk) {
-                    const int sb = blk >> 1, mt = blk & 1;
-                    const int brow = 256 * mt + 32 * w + 16 * sb + n;
-                    const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
-                    uint32_t s2, b2, b16;
-                    pf_affine_pairs(s_sb[g][brow], s2, b2, b16);
-                    bo[blk][0] = pf_dequant_f16(wq.x, s2, b2, b16);
-                    bo[blk][1] = pf_dequant_f16(wq.y, s2, b2, b16);
-                }
-                // each 16-route block's operands against the four, accumulated
-                // over all of K; the weights go first, so a lane holds four
-                // consecutive weight rows of one route
+                const uint8_t* A = s_ra + (g & 1) * kPfA;
+                // the next group's weights (past the last group: a valid slot
+                // and table row whose values go unused, so this stays one
+                // block with the MFMAs)
+                dequant(bnext, (g + 1) % kBS, min(g + 1, G - 1));
+                // each 16-route block's operands (read one block ahead)
+                // against the four, accumulated over all of K; the weights go
+                // first, so a lane holds four consecutive weight rows of one
+                // route
+                vmi_u4 an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(n, 2 * q));
+                vmi_u4 an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(n, 2 * q + 1));
 #pragma unroll
                 for (int m = 0; m < MC; ++m) {
-                    const int row = 16 * m + n;
-                    const vmi_u4 a0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
-                    const vmi_u4 a1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+                    const vmi_u4 a0 = an0, a1 = an1;
+                    if (m + 1 < MC) {
+                        const int row = 16 * (m + 1) + n;
+                        an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
+                        an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+                    }
 #pragma unroll
                     for (int blk = 0; blk < 4; ++blk)
-                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bo[blk][0], a0, acc[m][blk >> 1][blk & 1]);
+                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bcur[blk][0], a0, acc[m][blk >> 1][blk & 1]);
 #pragma unroll
                     for (int blk = 0; blk < 4; ++blk)
-                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bo[blk][1], a1, acc[m][blk >> 1][blk & 1]);
+                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bcur[blk][1], a1, acc[m][blk >> 1][blk & 1]);
                 }
             }
+        };
+        vmi_u4 b0[4][2], b1[4][2];
+        if constexpr (MC > 0) {
+            pf_wait_vmcnt<2>();  // this wave's weights of group 0 (operands 0 may be in flight)
+            dequant(b0, 0, 0);
+        }
+        // two stages per iteration, so the two weight buffers trade roles
+        // without copies (G is even: H is 512, 1024 or 2048)
+#pragma unroll 1
+        for (int g = 0; g < G; g += 2) {
+            stage(g, b0, b1);
+            stage(g + 1, b1, b0);
         }
     };
     switch (mcnt) {
@@ -1449,7 +1472,7 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
     const int tile_slots = 8 * ((L.max_tiles + 7) / 8);
-    hipLaunchKernelGGL(k_pf_gateup3<2>, dim3(tile_slots * ((D.inter + 255) / 256)), dim3(kPf8Threads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_gateup3, dim3(tile_slots * ((D.inter + 255) / 256)), dim3(kPf8Threads), 0, s, a);
     if (D.inter <= 512)
         hipLaunchKernelGGL((k_pf_down3<3, 8>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
     else
