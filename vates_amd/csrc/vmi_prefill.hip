@@ -858,20 +858,36 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 
 // Down: tile 128 routes x 512 hidden rows, K = I, eight waves side by side
 // (wave w: all 128 routes, hidden rows 64w..).  The MFMAs take the weights
-// first, so a lane holds four consecutive hidden rows of one route (y
-// transposed): its four outputs are one 8-byte store.  The weight operand is
-// the dequantised value in fp16, (q 2^-24) s' + b' by one packed FMA per two
-// values, with s' = s 2^P and b' = b 2^(P-24) for the hidden row's power of
-// two P (its largest |scale| into [2^14, 2^15)); the activations are fp16
-// times 2^-E, E per route and 256-column block.  The sums are scaled by
-// 2^(E_prev - E) at each block boundary and by 2^(24-P) 2^E_last at the end,
-// then times the route's combine weight into one bf16 row per (token, rank).
-// MAXG bounds the quantisation groups of K the LDS table holds.
+// first, so a lane holds consecutive hidden rows of one route (y
+// transposed); the weight rows of column blocks 2t and 2t + 1 interleave in
+// fours (row 8i + r of the pair feeds MFMA row 4i + r of block 2t, row
+// 8i + 4 + r that of block 2t + 1), so a lane's eight outputs of a pair are
+// consecutive and one 16-byte store.  The weight operand is the dequantised
+// value in fp16, (q 2^-24) s' + b' by one packed FMA per two values, with
+// s' = s 2^P and b' = b 2^(P-24) for the hidden row's power of two P (its
+// largest |scale| into [2^14, 2^15)); the activations are fp16 times 2^-E,
+// E per route and 256-column block.  The sums are scaled by 2^(E_prev - E) at
+// each block boundary and by 2^(24-P) 2^E_last at the end, then times the
+// route's combine weight into one bf16 row per (token, rank).  As in
+// k_pf_gateup3, a wave DMAs exactly the weight rows it reads (three slots,
+// two groups ahead, dequantised one group ahead under the MFMAs) and the
+// operand rows go through two shared slots.  MAXG bounds the quantisation
+// groups of K the LDS table holds.
 constexpr int kPfMaxIB = 8;  // 256-column blocks of the intermediate size (I <= 2048)
-template <int STAGES, int MAXG>
+// Hidden row (inside a wave's 64) of weight position p: positions 16sb..16sb+15
+// are MFMA block sb's rows, and row n of block sb (= 2t + s) is hidden row
+// 32t + 8(n/4) + 4s + n%4, so a lane's outputs of blocks 2t and 2t + 1 are
+// eight consecutive hidden rows.
+__device__ __forceinline__ int pf_down_row(int p) {
+    return (p & 32) | (((p >> 2) & 3) << 3) | (((p >> 4) & 1) << 2) | (p & 3);
+}
+
+template <int MAXG>
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     constexpr int kB = 512 * 32;
-    __shared__ __attribute__((aligned(16))) uint8_t s_ring[STAGES * (kPfA + kB)];
+    constexpr int kAS = 2, kBS = 3;
+    __shared__ __attribute__((aligned(16))) uint8_t s_ra[kAS * kPfA];
+    __shared__ __attribute__((aligned(16))) uint8_t s_rb[kBS * kB];
     __shared__ uint32_t s_sb[MAXG][512];                        // fp16 s' | b' << 16: [group][hidden row]
     __shared__ __attribute__((aligned(16))) float s_post[512];  // 2^(24 - P)
     __shared__ int s_route[kTM3];
@@ -894,24 +910,26 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     // the down projection is group-major: row h of group g of slot m at
     // (m * G + g) * H + h (32 bytes of words; one bf16 scale and bias)
     const size_t mbase = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)G * a.H + h0;
-    // DMA sources of the weights: pieces p = tid + 512 j (row p/2, half
-    // (p%2) ^ bit 3 of the row)
+    // weight DMA into the wave's own 2 KB of the slot: 32-byte position
+    // p = 32j + lane/2 of wave w holds hidden row 64w + pf_down_row(p), half
+    // (lane%2) ^ bit 3 of p (pf_down_row puts the 16 rows an MFMA block reads
+    // in 16 consecutive positions, which ds_read_b64 reads without bank
+    // conflicts)
     const uint32_t* bsrc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int p = tid + kPf8Threads * j;
-        const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
-        bsrc[j] = Dm.w + (mbase + brow) * 8 + 4 * h;
+        const int p = 32 * j + (lane >> 1), h = (lane & 1) ^ ((p >> 3) & 1);
+        bsrc[j] = Dm.w + (mbase + 64 * w + pf_down_row(p)) * 8 + 4 * h;
     }
     auto issue_b = [&](int g, int u) {
-        uint8_t* A = s_ring + u * (kPfA + kB);
+        uint8_t* B = s_rb + u * kB;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            vmi_lds_dma16_opaque(bsrc[j] + (size_t)g * a.H * 8, A + kPfA + 16 * (kPf8Threads * j + 64 * w));
+            vmi_lds_dma16_opaque(bsrc[j] + (size_t)g * a.H * 8, B + 16 * (128 * w + 64 * j));
     };
-    // the first groups' weights are in flight while the prologue runs
-#pragma unroll
-    for (int u = 0; u < STAGES - 1; ++u) issue_b(u < G ? u : G - 1, u);
+    // the first two groups' weights are in flight while the prologue runs
+    issue_b(0, 0);
+    issue_b(G > 1 ? 1 : 0, 1);
     {
         // thread t: hidden row h0 + t, every group (a wave reads 128
         // contiguous bytes per group); these loads are issued first, the
@@ -964,13 +982,24 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         asrc[j] = a.actop + (size_t)(rt >= 0 ? rt : 0) * IW + c;
     }
     auto issue_a = [&](int g, int u) {
-        uint8_t* A = s_ring + u * (kPfA + kB);
+        uint8_t* A = s_ra + u * kPfA;
 #pragma unroll
         for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
     };
-    auto issue = [&](int g, int u) {
-        issue_a(g, u);
-        issue_b(g, u);
+    // this wave's four column blocks of group g from weight slot u,
+    // dequantised; block sb row n is hidden row 64w + pf_down_row(16sb + n)
+    auto dequant = [&](vmi_u4 (&wo)[4][2], int u, int g) {
+        const uint8_t* B = s_rb + u * kB;
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) {
+            const int pos = 64 * w + 16 * sb + n;
+            const int brow = 64 * w + pf_down_row(16 * sb + n);
+            const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(pos, q));
+            uint32_t s2, b2, b16;
+            pf_affine_pairs(s_sb[g][brow], s2, b2, b16);
+            wo[sb][0] = pf_dequant_f16(wq.x, s2, b2, b16);
+            wo[sb][1] = pf_dequant_f16(wq.y, s2, b2, b16);
+        }
     };
     vmi_f4 acc[8][4];
 #pragma unroll
@@ -978,27 +1007,17 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
 #pragma unroll
         for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
     VMI_STAMP(3, 1);
-#pragma unroll
-    for (int u = 0; u < STAGES - 1; ++u) issue_a(u < G ? u : G - 1, u);
+    issue_a(0, 0);
     // the stage loop for MC active 16-route blocks (a loop per MC, so each
-    // keeps its own register allocation; MC = 0 only moves the ring and keeps
-    // the barriers)
+    // keeps its own register allocation; MC = 0 only moves the rings and
+    // keeps the barriers)
     auto stage_loop = [&](auto mc_tag) {
         constexpr int MC = decltype(mc_tag)::value;
-#pragma unroll 1
-        for (int g = 0; g < G; ++g) {
-            const int u = g % STAGES;
-            // group g's pieces (this thread's) have landed: the weights of
-            // the first STAGES - 1 groups went out before their operands
-            if (g == 0)
-                pf_wait_vmcnt<2 * (STAGES - 2)>();
-            else
-                pf_wait_vmcnt<4 * (STAGES - 2)>();
-            __syncthreads();
-            {
-                const int gn = g + STAGES - 1;
-                issue(gn < G ? gn : G - 1, gn % STAGES);
-            }
+        auto stage = [&](int g, const vmi_u4 (&wcur)[4][2], vmi_u4 (&wnext)[4][2]) {
+            pf_wait_vmcnt<0>();  // operands g and weights g + 1 (this thread's) have landed
+            __syncthreads();     // everyone's operands g; operand slot (g + 1) % 2 is free
+            if (g + 1 < G) issue_a(g + 1, (g + 1) & 1);
+            if (g + 2 < G) issue_b(g + 2, (g + 2) % kBS);
             if constexpr (MC > 0) {
                 if (g > 0 && (g & 3) == 0) {
                     // a new 256-column block: the sums so far times 2^(E_prev - E)
@@ -1013,31 +1032,38 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
                             for (int r = 0; r < 4; ++r) acc[m][sb][r] *= f;
                     }
                 }
-                const uint8_t* A = s_ring + u * (kPfA + kB);
-                const uint8_t* B = A + kPfA;
-                // the four column blocks' weights, dequantised
-                vmi_u4 wo[4][2];
-#pragma unroll
-                for (int sb = 0; sb < 4; ++sb) {
-                    const int brow = 64 * w + 16 * sb + n;
-                    const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
-                    uint32_t s2, b2, b16;
-                    pf_affine_pairs(s_sb[g][brow], s2, b2, b16);
-                    wo[sb][0] = pf_dequant_f16(wq.x, s2, b2, b16);
-                    wo[sb][1] = pf_dequant_f16(wq.y, s2, b2, b16);
-                }
+                const uint8_t* A = s_ra + (g & 1) * kPfA;
+                // the next group's weights (past the last group: a valid slot
+                // and table row whose values go unused)
+                dequant(wnext, (g + 1) % kBS, min(g + 1, G - 1));
+                vmi_u4 an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(n, 2 * q));
+                vmi_u4 an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(n, 2 * q + 1));
 #pragma unroll
                 for (int m = 0; m < MC; ++m) {
-                    const int row = 16 * m + n;
-                    const vmi_u4 a0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
-                    const vmi_u4 a1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+                    const vmi_u4 a0 = an0, a1 = an1;
+                    if (m + 1 < MC) {
+                        const int row = 16 * (m + 1) + n;
+                        an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
+                        an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
+                    }
 #pragma unroll
-                    for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wo[sb][0], a0, acc[m][sb]);
+                    for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wcur[sb][0], a0, acc[m][sb]);
 #pragma unroll
-                    for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wo[sb][1], a1, acc[m][sb]);
+                    for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wcur[sb][1], a1, acc[m][sb]);
                 }
             }
+        };
+        vmi_u4 w0[4][2], w1[4][2];
+        if constexpr (MC > 0) {
+            pf_wait_vmcnt<2>();  // this wave's weights of group 0 (operands 0 may be in flight)
+            dequant(w0, 0, 0);
         }
+#pragma unroll 1
+        for (int g = 0; g + 1 < G; g += 2) {
+            stage(g, w0, w1);
+            stage(g + 1, w1, w0);
+        }
+        if (G & 1) stage(G - 1, w0, w1);
     };
     switch (mcnt) {
         case 8: stage_loop(std::integral_constant<int, 8>{}); break;
@@ -1053,22 +1079,30 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     pf_wait_vmcnt<0>();
     VMI_STAMP(3, 2);
     VMI_STAMP(3, 3);
-    // lane (n, q): route row 16m + n, hidden rows h0 + 64w + 16sb + 4q .. + 3
-    float4 post[4];
+    // lane (n, q): route row 16m + n, hidden rows h0 + 64w + 32t + 8q .. + 7
+    // (column blocks 2t and 2t + 1)
+    float4 post[2][2];
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) post[sb] = *reinterpret_cast<const float4*>(&s_post[64 * w + 16 * sb + 4 * q]);
+    for (int t = 0; t < 2; ++t) {
+        post[t][0] = *reinterpret_cast<const float4*>(&s_post[64 * w + 32 * t + 8 * q]);
+        post[t][1] = *reinterpret_cast<const float4*>(&s_post[64 * w + 32 * t + 8 * q + 4]);
+    }
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
         const int route = s_route[16 * m + n];
         if (route < 0) continue;
         const float f = s_rf[16 * m + n];
-        uint16_t* yrow = a.ybuf + (size_t)route * a.H + h0 + 64 * w + 4 * q;
+        uint16_t* yrow = a.ybuf + (size_t)route * a.H + h0 + 64 * w + 8 * q;
 #pragma unroll
-        for (int sb = 0; sb < 4; ++sb) {
-            uint2 o;
-            o.x = vmi_pack_bf16x2(acc[m][sb][0] * post[sb].x * f, acc[m][sb][1] * post[sb].y * f);
-            o.y = vmi_pack_bf16x2(acc[m][sb][2] * post[sb].z * f, acc[m][sb][3] * post[sb].w * f);
-            *reinterpret_cast<uint2*>(yrow + 16 * sb) = o;
+        for (int t = 0; t < 2; ++t) {
+            const vmi_f4& lo = acc[m][2 * t];
+            const vmi_f4& hi = acc[m][2 * t + 1];
+            uint4 o;
+            o.x = vmi_pack_bf16x2(lo[0] * post[t][0].x * f, lo[1] * post[t][0].y * f);
+            o.y = vmi_pack_bf16x2(lo[2] * post[t][0].z * f, lo[3] * post[t][0].w * f);
+            o.z = vmi_pack_bf16x2(hi[0] * post[t][1].x * f, hi[1] * post[t][1].y * f);
+            o.w = vmi_pack_bf16x2(hi[2] * post[t][1].z * f, hi[3] * post[t][1].w * f);
+            *reinterpret_cast<uint4*>(yrow + 32 * t) = o;
         }
     }
     VMI_STAMP(3, 4);
@@ -1474,9 +1508,9 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     const int tile_slots = 8 * ((L.max_tiles + 7) / 8);
     hipLaunchKernelGGL(k_pf_gateup3, dim3(tile_slots * ((D.inter + 255) / 256)), dim3(kPf8Threads), 0, s, a);
     if (D.inter <= 512)
-        hipLaunchKernelGGL((k_pf_down3<3, 8>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
+        hipLaunchKernelGGL((k_pf_down3<8>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
     else
-        hipLaunchKernelGGL((k_pf_down3<2, kMaxG>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
+        hipLaunchKernelGGL((k_pf_down3<kMaxG>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(kPfThreads), 0, s, a);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill launch");
