@@ -159,6 +159,18 @@ __device__ __forceinline__ uint64_t suffix_scan64(uint64_t v) {
     return v;
 }
 
+// Inclusive scan over the lanes of a wave: lane l gets sum_{l' <= l} v(l').
+__device__ __forceinline__ uint64_t prefix_scan64(uint64_t v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, (lane - o) & 63);
+        const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), (lane - o) & 63);
+        if (lane >= o) v += ((uint64_t)hi << 32) | lo;
+    }
+    return v;
+}
+
 // One wave: the largest bin b of h[0..nbins) with above + sum_{i >= b} h[i] >= C,
 // and above + sum_{i > b} h[i].  Uniform results.  Lane l owns bins
 // [l*per, (l+1)*per); the crossing lane comes from a suffix scan of the lane
@@ -363,41 +375,61 @@ __device__ __forceinline__ DrawPlan plan_draw(const SdArgs& a, int r) {
         sd_uniforms(a.seed, a.offset, r, U, P.Vr);
         return P;
     }
-    for (int d = 0; d < a.nd; ++d) P.bad |= !ld32c(&a.stats[d].valid);
-    if (P.bad) return P;
+    // lane i loads what decision i needs (the statistics of p row i and q row
+    // K + 1 + i and draft i's masses in both) and lane d the validity of
+    // distribution d, all in one round of loads; the decisions are the
+    // sequential rule's (the first rejected draft ends the run)
+    const int lane = threadIdx.x & 63;
     const int K = a.K, V = a.V;
-    int m = 0;
-    for (; m < K; ++m) {
-        const int dj = a.drafts[m];
-        uint32_t U, Vr;
-        sd_uniforms(a.seed, a.offset, m, U, Vr);
-        double pp = 0.0, qq = 1.0;
-        if (dj >= 0 && dj < V) {
-            const SdStats sp = sd_stats(a, m);
-            pp = (double)nucleus_mass(a.W + (size_t)m * V, sp.theta, dj) / (double)sp.zs;
+    P.bad = __ballot(lane < a.nd && !ld32c(&a.stats[lane < a.nd ? lane : 0].valid)) != 0ull;
+    if (P.bad) return P;
+    uint32_t thp = 0u, thq = 0u, wp = 0u, wq = 0u;
+    uint64_t zp = 1ull, zq = 1ull;
+    int dj = -1;
+    if (lane <= K) {
+        const SdStats sp = sd_stats(a, lane);
+        thp = sp.theta;
+        zp = sp.zs;
+        if (lane < K) {
+            dj = a.drafts[lane];
             if (a.has_q) {
-                const SdStats sq = sd_stats(a, K + 1 + m);
-                qq = (double)nucleus_mass(a.W + (size_t)(K + 1 + m) * V, sq.theta, dj) / (double)sq.zs;
+                const SdStats sq = sd_stats(a, K + 1 + lane);
+                thq = sq.theta;
+                zq = sq.zs;
+            }
+            if (dj >= 0 && dj < V) {
+                wp = ld32c(a.W + (size_t)lane * V + dj);
+                if (a.has_q) wq = ld32c(a.W + (size_t)(K + 1 + lane) * V + dj);
             }
         }
-        const double u = (double)U * 0x1p-32;
-        if (!(pp > 0.0 && u * qq <= pp)) break;
     }
+    bool keep = false;
+    if (lane < K) {
+        uint32_t U, Vr;
+        sd_uniforms(a.seed, a.offset, lane, U, Vr);
+        double pp = 0.0, qq = 1.0;
+        if (dj >= 0 && dj < V) {
+            pp = (double)(wp >= thp ? wp : 0u) / (double)zp;
+            if (a.has_q) qq = (double)(wq >= thq ? wq : 0u) / (double)zq;
+        }
+        const double u = (double)U * 0x1p-32;
+        keep = pp > 0.0 && u * qq <= pp;
+    }
+    const uint64_t rejected = __ballot(lane < K && !keep);
+    const int m = rejected ? (int)__builtin_ctzll(rejected) : K;
     P.m = m;
     uint32_t U;
     sd_uniforms(a.seed, a.offset, m, U, P.Vr);
     P.dp = m;
-    const SdStats sm = sd_stats(a, m);
-    P.th_p = sm.theta;
-    P.zp = (double)sm.zs;
+    P.th_p = (uint32_t)__builtin_amdgcn_readlane((int)thp, m);
+    P.zp = (double)readlane64(zp, m);
     P.resid = m < K;
     if (P.resid) {
-        P.dm = a.drafts[m];
+        P.dm = __builtin_amdgcn_readlane(dj, m);
         if (a.has_q) {
             P.dq = K + 1 + m;
-            const SdStats sq = sd_stats(a, P.dq);
-            P.th_q = sq.theta;
-            P.zq = (double)sq.zs;
+            P.th_q = (uint32_t)__builtin_amdgcn_readlane((int)thq, m);
+            P.zq = (double)readlane64(zq, m);
         }
     }
     return P;
@@ -462,6 +494,7 @@ __device__ __forceinline__ void sd_draw(const SdArgs& a, const SdSync& y, int r,
     }
     __syncthreads();
     if (!s_last) return;
+    VMI_STAMP(r, 12);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (P.bad || ld32c(y.flag)) {
         if (tid == 0) {
@@ -494,16 +527,20 @@ __device__ __forceinline__ void sd_draw(const SdArgs& a, const SdSync& y, int r,
         const uint64_t tot = use_p ? totP : totR;
         const uint64_t v0 = use_p ? p0 : r0, v1 = use_p ? p1 : r1;
         const uint64_t t = __umul64hi(tot, (uint64_t)P.Vr << 32);
+        // the first slice whose inclusive prefix passes t, and the mass before
+        // it (slices past NB load as zero)
+        const uint64_t c0 = prefix_scan64(v0);
+        const uint64_t c1 = readlane64(c0, 63) + prefix_scan64(v1);
+        const uint64_t h0 = __ballot(c0 > t), h1 = __ballot(c1 > t);
+        int bstar = a.NB - 1;  // unreachable fallback: t < total
         uint64_t acc = 0;
-        int bstar = a.NB - 1;
-        bool found = false;
-        for (int i = 0; i < 64 && i < a.NB && !found; ++i) {
-            const uint64_t v = readlane64(v0, i);
-            if (acc + v > t) { bstar = i; found = true; } else { acc += v; }
-        }
-        for (int i = 0; i < 64 && i + 64 < a.NB && !found; ++i) {
-            const uint64_t v = readlane64(v1, i);
-            if (acc + v > t) { bstar = i + 64; found = true; } else { acc += v; }
+        if (h0) {
+            bstar = (int)__builtin_ctzll(h0);
+            acc = readlane64(c0, bstar) - readlane64(v0, bstar);
+        } else if (h1) {
+            const int i = (int)__builtin_ctzll(h1);
+            bstar = i + 64;
+            acc = readlane64(c1, i) - readlane64(v1, i);
         }
         if (lane == 0) {
             s_bstar = bstar;
@@ -514,6 +551,7 @@ __device__ __forceinline__ void sd_draw(const SdArgs& a, const SdSync& y, int r,
         }
     }
     __syncthreads();
+    VMI_STAMP(r, 13);
     // inside slice b*: thread i owns the contiguous group of kBatch indices
     // k0 + kBatch i ..; an exclusive scan of the group sums finds the group
     // holding the draw point, whose owner walks it.
@@ -540,16 +578,17 @@ __device__ __forceinline__ void sd_draw(const SdArgs& a, const SdSync& y, int r,
             v[u] = j < k1 ? (use_p ? pm : resid_value(a, P, j, pm, wq[u])) : 0u;
             gs += v[u];
         }
-        s_scan[tid] = gs;
+        // inclusive scan of the group sums over the workgroup: per wave, then
+        // the preceding waves' totals
+        const uint64_t ws = prefix_scan64(gs);
+        if ((tid & 63) == 63) s_scan[acc_wave_id()] = ws;
         __syncthreads();
-        for (int o = 1; o < kSdThreads; o <<= 1) {
-            const uint64_t add = tid >= o ? s_scan[tid - o] : 0ull;
-            __syncthreads();
-            s_scan[tid] += add;
-            __syncthreads();
-        }
+        uint64_t before = 0;
+        for (int i = 0; i < acc_wave_id(); ++i) before += s_scan[i];
+        uint64_t wtot = 0;
+        for (int i = 0; i < kSdWaves; ++i) wtot += s_scan[i];
         const uint64_t base = s_base;
-        const uint64_t incl = base + s_scan[tid];
+        const uint64_t incl = base + before + ws;
         uint64_t run = incl - gs;
         if (gs > 0 && run <= t && incl > t) {
 #pragma unroll
@@ -559,10 +598,11 @@ __device__ __forceinline__ void sd_draw(const SdArgs& a, const SdSync& y, int r,
             }
         }
         __syncthreads();
-        if (tid == 0) s_base = base + s_scan[kSdThreads - 1];
+        if (tid == 0) s_base = base + wtot;
         __syncthreads();
         if (s_tok >= 0) break;
     }
+    VMI_STAMP(r, 14);
     if (tid == 0) {
         int tok = s_tok;
         if (tok < 0) tok = k1 - 1;  // unreachable: t < total
