@@ -1307,13 +1307,14 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_combine(PfArgs a) {
         okm |= (ok ? 1u : 0u) << j;
     }
     const vmi_u4 z4 = {0u, 0u, 0u, 0u};
+    // the token's K1 rows are one contiguous run of ybuf, read once:
+    // nontemporal, branch-free buffer loads (an absent rank reads as zero)
+    const __amdgpu_buffer_rsrc_t ry = vmi_rsrc(a.ybuf + (size_t)t * K1 * a.H, (uint32_t)(K1 * a.H * 2));
     for (int h = threadIdx.x * 8; h < a.H; h += kPfThreads * 8) {
         vmi_u4 y[kPfMaxK + 1];
 #pragma unroll
         for (int j = 0; j <= kPfMaxK; ++j)
-            y[j] = (j < K1 && ((okm >> j) & 1u))
-                       ? *reinterpret_cast<const vmi_u4*>(a.ybuf + ((size_t)t * K1 + j) * a.H + h)
-                       : z4;
+            y[j] = j < K1 ? vmi_bload_b128_nt(ry, ((okm >> j) & 1u) ? (uint32_t)((j * a.H + h) * 2) : VMI_OOB, 0) : z4;
         const vmi_u4 rv = a.residual ? *reinterpret_cast<const vmi_u4*>(a.residual + (size_t)t * a.H + h) : z4;
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
