@@ -86,6 +86,18 @@ def test_prefill_parity_small(gpu, orc, T, router_bits):
         _check_against_oracle(orc, w, x, out, ids, sc, 4, residual, f"small T={T}")
 
 
+@pytest.mark.parametrize("H,I,E,k,T", [(1024, 320, 64, 4, 150), (512, 768, 64, 6, 90)])
+def test_prefill_parity_odd_shapes(gpu, orc, H, I, E, k, T):
+    """Intermediate sizes that are not a multiple of 256 and above 512: I=320
+    has an odd count of down quantisation groups (5) and a last column block
+    of 64 rows; I=768 takes the down kernel's large-table form (12 groups,
+    three 256-column blocks, so two exponent rescales); H=1024 runs the
+    16-group prep, gate/up and router forms."""
+    log(f"case: prefill H={H} I={I} E={E} k={k} T={T}")
+    w, moe, x, out, ids, sc = _case(gpu, orc, T, H=H, I=I, E=E, k=k)
+    _check_against_oracle(orc, w, x, out, ids, sc, k, True, f"H={H} I={I} T={T}")
+
+
 def test_prefill_parity_full_shape(gpu, orc):
     log("case: prefill H=2048 I=512 E=512 k=10 T=192")
     w, moe, x, out, ids, sc = _case(gpu, orc, 192, H=2048, I=512, E=512, k=10)
