@@ -8,7 +8,8 @@
 // there is no group-size bound to respect, so one pass covers the layer:
 //
 //   k_pf_prep     per token: optional RMSNorm, MFMA operands of x (fp16, range
-//                 factor per token), per-group operand sums; clears counters
+//                 factor per token), per-group operand sums for the router's
+//                 affine term; clears counters
 //   k_pf_router3  router logits [T, E] as a tiled MFMA GEMM on the 4/8-bit
 //                 router (weights enter the MFMA as exact fp16 subnormals),
 //                 in two halves of K that the top-k adds
@@ -18,8 +19,9 @@
 //   k_pf_scan     exclusive scan of the counts, the list of 128-row M tiles
 //   k_pf_place    every routed (token, rank) into its slot's list
 //   k_pf_gateup3  per (M tile, 256 intermediate rows): gate and up MFMA GEMMs
-//                 over the tile's gathered tokens, SwiGLU, bf16 operands of
-//                 the activations and their per-group sums
+//                 over the tile's gathered tokens, SwiGLU rounded to bf16,
+//                 the activations as fp16 operands times 2^-E (E per route
+//                 and 256-column block)
 //   k_pf_down3    per (M tile, 512 hidden rows): down MFMA GEMM, times the
 //                 route's combine weight, one bf16 row per (token, rank)
 //   k_pf_combine  out[t] = sum over ranks 0..k (rank k: the gated shared
@@ -29,10 +31,14 @@
 // buffers, so no result depends on the order in which assignments are placed:
 // the layer is bit-deterministic run to run.
 //
-// 4-bit weights are exact fp16 subnormals in gate/up (nibble masks, slot order
-// {0,4,1,5,2,6,3,7}, /16 on odd nibbles folded into the activation operand)
-// and exact bf16 (128 + q) in down; per-group scale and bias are applied to
-// each group's MFMA result (FMA), with the bias through per-group operand sums.
+// 4-bit weights unpack as exact fp16 subnormals q 2^-24 (nibble masks, slot
+// order {0,4,1,5,2,6,3,7}, the odd nibbles carrying 16 q and the other operand
+// divided by 16 there).  The expert GEMMs dequantise them in fp16 with the
+// group's scale and bias folded in (one packed FMA per two values), so their
+// MFMAs accumulate the whole affine product over K; the router keeps the
+// exact operand, applies each group's scale to the group's MFMA result (FMA)
+// and adds the bias through per-group operand sums, so its logits stay exact
+// enough for the top-k.
 
 #include <type_traits>
 
@@ -471,24 +477,18 @@ __device__ __forceinline__ uint32_t ring_off(int row, int unit8) {
     return 32u * row + 16u * (((unsigned)unit8 >> 1) ^ (((unsigned)row >> 3) & 1u)) + 8u * (unit8 & 1);
 }
 
-// ----------------------------------------------- 128 x 128 tile GEMMs
-// Both GEMMs run one workgroup per (tile of 128 routes, 128 output rows)
-// with four waves in a 2 x 2 grid: wave (mh, nh) owns routes 64mh..64mh+63
-// (four 16-row MFMA blocks) and output rows 64nh..64nh+63 (four 16-column
-// blocks), so every unpacked weight operand feeds four MFMAs.  K streams one
-// quantisation group (64 values) per stage through a ring of kPfStages LDS
-// slots filled by global_load_lds: the A operands (128 routes x 128 bytes)
-// and the packed weights (rows x 32 bytes), each thread moving whole 16-byte
-// pieces.  A slot's A row r keeps its 16-byte piece c at position c ^ (r & 7),
-// so the 16 rows one MFMA operand read touches start on distinct banks; the
-// weight rows keep the half-swap on bit 3 of the row.  Gate/up folds each
-// group's scale into its fp16 weight operand (one packed multiply per two
-// values; the MFMAs then accumulate over all of K), down applies it by one
-// FMA per output element and group; the affine bias term sum_g b_g X_g goes
-// through bf16 MFMAs once at the end (X split into hi + mid + lo bf16, 24
-// significant bits).  Workgroup L runs tile
-// 8*(L/8/NB) + L%8 and column block (L/8)%NB: the column blocks of one tile
-// share an XCD, so its A rows reach that L2 once.
+// ----------------------------------------------- tiled MFMA GEMMs
+// The tile GEMMs stream K one quantisation group (64 values) per stage
+// through LDS slots filled by global_load_lds, each thread moving whole
+// 16-byte pieces: the A operands (128 rows x 128 bytes, fp16) and the packed
+// weight rows (32 bytes each).  An A row r keeps its 16-byte piece c at
+// position c ^ ((r >> 1) & 7) (pf_a_off), so the 16 rows of one ds_read_b128
+// phase cover the 64 banks once; a weight row keeps the half-swap on bit 3 of
+// the row (ring_off).  The router (k_pf_router3) runs four waves in a 2 x 2
+// grid over a ring of kPfStages slots; the expert GEMMs (k_pf_gateup3,
+// k_pf_down3) run eight waves side by side with their own slot layout.
+// Workgroup L runs tile 8*(L/8/NB) + L%8 and column block (L/8)%NB: the
+// column blocks of one tile share an XCD, so its A rows reach that L2 once.
 constexpr int kPfStages = 2;   // LDS ring depth: kPfStages - 1 groups in flight
 constexpr int kPfA = kTM3 * 128;
 
