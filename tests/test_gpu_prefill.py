@@ -98,6 +98,39 @@ def test_prefill_parity_odd_shapes(gpu, orc, H, I, E, k, T):
     _check_against_oracle(orc, w, x, out, ids, sc, k, True, f"H={H} I={I} T={T}")
 
 
+def test_prefill_degenerate_rows(gpu, orc):
+    """Weight rows whose biases dwarf their scales (scales 2^-30, biases 0.5:
+    a nearly constant row) and rows whose scales are all zero, in gate, up,
+    down and the shared expert: the power of two of the fp16 dequantisation
+    table must keep b 2^(P-24) finite (it is bound by the largest bias as
+    well as by the largest scale)."""
+    import torch
+    from vates_amd.synth import synth_bf16
+    from vates_amd.workload import make_layer, synth_layer
+    H, I, E, k, T = 512, 128, 64, 4, 96
+    w = synth_layer(57, 0, hidden=H, inter=I, num_experts=E, zipf_alpha=1.0, device=gpu)
+
+    def bits(v):
+        return int(torch.tensor([v], dtype=torch.bfloat16).view(torch.int16).item())
+
+    for proj, rows in ((w.gate, slice(0, 8)), (w.up, slice(8, 16)), (w.down, slice(0, 8)),
+                       (w.sh_gate, slice(0, 4)), (w.sh_down, slice(16, 24))):
+        proj.scales[:, rows, :] = bits(2.0 ** -30)
+        proj.biases[:, rows, :] = bits(0.5)
+    for proj, rows, bias in ((w.up, slice(16, 24), -0.25), (w.down, slice(8, 16), 0.125)):
+        proj.scales[:, rows, :] = 0
+        proj.biases[:, rows, :] = bits(bias)
+    moe = make_layer(w, top_k=k)
+    x = synth_bf16(57, 2000 + T, (T, H), device=gpu)
+    ids = torch.empty((T, k), dtype=torch.int32, device=gpu)
+    sc = torch.empty((T, k), dtype=torch.float32, device=gpu)
+    log(f"case: prefill with degenerate weight rows H={H} I={I} T={T}")
+    out = moe.prefill(x, residual=x, ids_out=ids, scores_out=sc)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    _check_against_oracle(orc, w, x, out, ids, sc, k, True, "degenerate rows")
+
+
 def test_prefill_parity_full_shape(gpu, orc):
     log("case: prefill H=2048 I=512 E=512 k=10 T=192")
     w, moe, x, out, ids, sc = _case(gpu, orc, 192, H=2048, I=512, E=512, k=10)

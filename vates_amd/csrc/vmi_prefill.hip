@@ -532,6 +532,27 @@ __device__ __forceinline__ vmi_u4 pf_dequant_f16(uint32_t wq, uint32_t s2, uint3
     return r;
 }
 
+// The weight row's power of two P for the fp16 table: its largest |scale|
+// times 2^P below 2^15 (in [2^14, 2^15) unless the biases bind) and its
+// largest |bias| times 2^(P-24) below 2^11, so s 2^P and b 2^(P-24) are
+// finite and exact in fp16 (bf16 values times powers of two, down to fp16's
+// subnormals), 16 b 2^(P-24) (the odd words' bias) is finite too, and a
+// dequantised value stays below 2^16.  mxs, mxb: the largest |scale| and
+// |bias| as float bits (zero: all zero).  P is kept in [-100, 127], so
+// 2^(24-P) is a finite float.
+__device__ __forceinline__ int pf_row_pow2(uint32_t mxs, uint32_t mxb) {
+    int P = 127, e = 0;
+    if (mxs) {
+        (void)frexpf(__uint_as_float(mxs), &e);  // mxs = f 2^e, f in [0.5, 1)
+        P = min(P, 15 - e);
+    }
+    if (mxb) {
+        (void)frexpf(__uint_as_float(mxb), &e);
+        P = min(P, 35 - e);
+    }
+    return (mxs | mxb) ? max(P, -100) : 0;
+}
+
 // (s', b') of a table word -> s2, b2, b16
 __device__ __forceinline__ void pf_affine_pairs(uint32_t sbw, uint32_t& s2, uint32_t& b2, uint32_t& b16) {
     s2 = __builtin_amdgcn_perm(sbw, sbw, 0x01000100u);
@@ -544,7 +565,7 @@ __device__ __forceinline__ void pf_affine_pairs(uint32_t sbw, uint32_t& s2, uint
 // routes, intermediate rows 32w.. of both matrices, so each unpacked weight
 // operand feeds up to eight 16-route blocks).  The weight operand is the
 // dequantised value in fp16, (q 2^-24) s' + b' (s' = s 2^P, b' = b 2^(P-24),
-// P the weight row's power of two), so the MFMAs accumulate the whole
+// P the weight row's power of two from pf_row_pow2), so the MFMAs accumulate the whole
 // affine product over all of K and the row's sums are times 2^(24-P) at the
 // end.  Then SwiGLU rounded to bf16,
 // and the down projection's fp16 operands of the activations: each route's
@@ -627,26 +648,28 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
             s_tok[tid] = tok;
             s_inv[tid] = rt >= 0 ? 1.0f / a.fscale[tok] : 0.0f;
         }
-        // a row's G/8 chunks of eight scales sit in G/8 consecutive lanes
-        // (G/8 is 1, 2 or 4, and the branch is uniform: it < G/8).  Each
-        // row's power of two 2^P puts its largest |scale| in [2^14, 2^15):
-        // s 2^P and b 2^(P-24) are then exact in fp16 (bf16 values times
-        // powers of two), and the dequantised values about 2^-6 at most
+        // a row's G/8 chunks of eight scales (and biases) sit in G/8
+        // consecutive lanes (G/8 is 1, 2 or 4, and the branch is uniform:
+        // it < G/8); each row's power of two comes from pf_row_pow2
 #pragma unroll
         for (int it = 0; it < kIt; ++it) {
             const int i = tid + kPf8Threads * it;
             if (i < n16) {
                 const int chunk = i % (G / 8), row = (i / (G / 8)) % 256, mt = i / (G / 8 * 256);
                 const uint32_t wv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-                uint32_t mx = 0u;  // |scale| as float bits: ordered as integers
-#pragma unroll
-                for (int j = 0; j < 8; ++j) mx = max(mx, (wv[j >> 1] << (16 - 16 * (j & 1))) & 0x7fff0000u);
-                for (int o = 1; o < G / 8; o <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
-                int e = 0;
-                (void)frexpf(__uint_as_float(mx), &e);  // mx = f 2^e, f in [0.5, 1)
-                const int P = mx ? min(15 - e, 127) : 0;
-                const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
                 const uint32_t bw[4] = {vb[it].x, vb[it].y, vb[it].z, vb[it].w};
+                uint32_t mx = 0u, mxb = 0u;  // |scale|, |bias| as float bits: ordered as integers
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    mx = max(mx, (wv[j >> 1] << (16 - 16 * (j & 1))) & 0x7fff0000u);
+                    mxb = max(mxb, (bw[j >> 1] << (16 - 16 * (j & 1))) & 0x7fff0000u);
+                }
+                for (int o = 1; o < G / 8; o <<= 1) {
+                    mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
+                    mxb = max(mxb, (uint32_t)__shfl_xor((int)mxb, o));
+                }
+                const int P = pf_row_pow2(mx, mxb);
+                const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const uint32_t sv = (wv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
@@ -864,8 +887,8 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 // 8i + 4 + r that of block 2t + 1), so a lane's eight outputs of a pair are
 // consecutive and one 16-byte store.  The weight operand is the dequantised
 // value in fp16, (q 2^-24) s' + b' by one packed FMA per two values, with
-// s' = s 2^P and b' = b 2^(P-24) for the hidden row's power of two P (its
-// largest |scale| into [2^14, 2^15)); the activations are fp16 times 2^-E,
+// s' = s 2^P and b' = b 2^(P-24) for the hidden row's power of two P
+// (pf_row_pow2); the activations are fp16 times 2^-E,
 // E per route and 256-column block.  The sums are scaled by 2^(E_prev - E) at
 // each block boundary and by 2^(24-P) 2^E_last at the end, then times the
 // route's combine weight into one bf16 row per (token, rank).  As in
@@ -959,12 +982,13 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
             }
             s_rf[tid] = wgt * ldexpf(1.0f, el);
         }
-        uint32_t mx = 0u;  // |scale| as float bits: ordered as integers
+        uint32_t mx = 0u, mxb = 0u;  // |scale|, |bias| as float bits: ordered as integers
 #pragma unroll
-        for (int g = 0; g < MAXG; ++g) mx = max(mx, (sv[g] << 16) & 0x7fff0000u);
-        int e = 0;
-        (void)frexpf(__uint_as_float(mx), &e);  // mx = f 2^e, f in [0.5, 1)
-        const int P = mx ? min(15 - e, 127) : 0;
+        for (int g = 0; g < MAXG; ++g) {
+            mx = max(mx, (sv[g] << 16) & 0x7fff0000u);
+            mxb = max(mxb, (bv[g] << 16) & 0x7fff0000u);
+        }
+        const int P = pf_row_pow2(mx, mxb);
         const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
 #pragma unroll
         for (int g = 0; g < MAXG; ++g)
