@@ -840,7 +840,10 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     VMI_STAMP(4, 13);
     // each route row's largest |activation| over the block's columns (four
     // lanes per row, 64 columns each; float bits ordered as integers) gives
-    // its exponent E: the largest value times 2^-E lies in [2^14, 2^15)
+    // its exponent E: the largest value times 2^-E lies in [2^14, 2^15).  E
+    // is at least -40, so the down kernel's rescale 2^(E_prev - E) between
+    // blocks stays finite (a block whose values are all below 2^-25 loses
+    // what falls under fp16's subnormals)
     {
         const int row = tid >> 2, part = tid & 3;
         uint32_t mx = 0u;
@@ -856,7 +859,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
         mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2));
         int e = 0;
         (void)frexpf(__uint_as_float(mx), &e);  // mx = f 2^e, f in [0.5, 1)
-        if (part == 0) s_rexp[row] = mx ? e - 15 : 0;
+        if (part == 0) s_rexp[row] = mx ? max(e - 15, -40) : 0;
     }
     __syncthreads();
     const int IW = I / 8, IB = (I + 255) / 256, nw8 = nvalid / 8;
