@@ -178,7 +178,7 @@ int vmi_moe_layer_noalloc(const vmi_moe_layer_desc* desc, const uint16_t* x, int
  *   experts, per-expert gathers, SwitchGLU per group, weighted scatter) and
  *   its deterministic reduce core/moe/custom_kernel.py:20-118.
  * With every expert resident there is no group bound: one pass sorts the T*k
- * routes by pool slot and runs grouped MFMA GEMMs over 64-route tiles of each
+ * routes by pool slot and runs grouped MFMA GEMMs over 128-route tiles of each
  * slot (gate/up + SwiGLU, then down); the shared expert is a dense GEMM over
  * all tokens.  Every (token, rank) result has its own row and the combine adds
  * ranks 0..k-1, then the gated shared expert, in fp32 in that order: the output

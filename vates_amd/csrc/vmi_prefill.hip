@@ -18,6 +18,8 @@
 //   k_pf_count    routes per slot and each route's rank in its slot
 //   k_pf_scan     exclusive scan of the counts, the list of 128-row M tiles
 //   k_pf_place    every routed (token, rank) into its slot's list
+//   k_pf_table    per touched expert (and the shared one): the fp16
+//                 dequantisation table of its gate, up and down rows
 //   k_pf_gateup3  per (M tile, 256 intermediate rows): gate and up MFMA GEMMs
 //                 over the tile's gathered tokens, SwiGLU rounded to bf16,
 //                 the activations as fp16 operands times 2^-E (E per route
@@ -84,6 +86,10 @@ struct PfArgs {
     int4* tiles;                // [max_tiles]: slot (-1 shared), list start (or token start), rows, 0
     int32_t* ntiles;            // [1]
     int32_t* list;              // [T*k] route rows t*(k+1)+j grouped by slot
+    uint32_t* tgu;              // [cap+1, H/128, 2, I, 2] fp16 (s', b') of gate/up rows per group pair (slot cap: shared)
+    float* pgu;                 // [cap+1, 2, I] 2^(24-P) per gate/up row
+    uint32_t* tdn;              // [cap+1, ceil(I/128), H, 2] the same for down rows
+    float* pdn;                 // [cap+1, H]
     vmi_u4* actop;              // [T*(k+1), I/8] fp16 operands (times 2^-E), 4-bit slot order
     int32_t* aexp;              // [T*(k+1), ceil(I/256)]: E of each route and 256-column block
     uint16_t* ybuf;             // [T*(k+1), H] bf16 weighted expert outputs
@@ -560,30 +566,110 @@ __device__ __forceinline__ void pf_affine_pairs(uint32_t sbw, uint32_t& s2, uint
     b16 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2v, b2) * (pf_h2v){16.0f16, 16.0f16});
 }
 
+// The fp16 dequantisation tables of every expert the routing touched (and of
+// the shared expert, slot cap): per weight row, its power of two P
+// (pf_row_pow2) and per group the pair (s 2^P, b 2^(P-24)) as fp16 bits, laid
+// out per group pair so a wave's rows of one pair are one contiguous run;
+// 2^(24-P) per row.  One thread per row: gate and up rows first, then down.
+__global__ __launch_bounds__(kPfThreads) void k_pf_table(PfArgs a) {
+    const int I = a.I, H = a.H, G = H / 64, GP = G / 2, Gd = I / 64, GPd = (Gd + 1) / 2;
+    const int bps = (2 * I + H + kPfThreads - 1) / kPfThreads;
+    const int slot = blockIdx.x / bps, r = (blockIdx.x - slot * bps) * kPfThreads + threadIdx.x;
+    const bool shared = slot == a.cap;
+    if (shared ? !a.has_shared : a.counts[slot] == 0) return;
+    // |scale|, |bias| as float bits (ordered as integers) over the row, then
+    // the row's pairs; the second pass reads the row again from the cache
+    if (r < 2 * I) {
+        const int mt = r >= I, row = r - mt * I;
+        const vmi_qmat M = mt ? (shared ? a.sh_up : a.up) : (shared ? a.sh_gate : a.gate);
+        const uint16_t* sp = M.s + ((shared ? 0 : (size_t)slot) * I + row) * G;
+        const uint16_t* bp = M.b + ((shared ? 0 : (size_t)slot) * I + row) * G;
+        uint32_t mx = 0u, mxb = 0u;
+        for (int c = 0; c < G / 8; ++c) {
+            const uint4 sv = *reinterpret_cast<const uint4*>(sp + 8 * c), bv = *reinterpret_cast<const uint4*>(bp + 8 * c);
+            const uint32_t ws[4] = {sv.x, sv.y, sv.z, sv.w}, wb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                mx = max(mx, max((ws[e] << 16) & 0x7fff0000u, ws[e] & 0x7fff0000u));
+                mxb = max(mxb, max((wb[e] << 16) & 0x7fff0000u, wb[e] & 0x7fff0000u));
+            }
+        }
+        const int P = pf_row_pow2(mx, mxb);
+        const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
+        uint32_t* tp = a.tgu + (((size_t)slot * GP * 2 + mt) * I + row) * 2;
+        for (int c = 0; c < G / 8; ++c) {
+            const uint4 sv = *reinterpret_cast<const uint4*>(sp + 8 * c), bv = *reinterpret_cast<const uint4*>(bp + 8 * c);
+            const uint32_t ws[4] = {sv.x, sv.y, sv.z, sv.w}, wb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {  // groups 8c + 2e, 8c + 2e + 1: pair 4c + e
+                uint2 o;
+                o.x = vmi_h2_bits((_Float16)(vmi_bf16_to_f32(ws[e] & 0xffffu) * ps), (_Float16)(vmi_bf16_to_f32(wb[e] & 0xffffu) * pb));
+                o.y = vmi_h2_bits((_Float16)(vmi_bf16_to_f32(ws[e] >> 16) * ps), (_Float16)(vmi_bf16_to_f32(wb[e] >> 16) * pb));
+                *reinterpret_cast<uint2*>(tp + (size_t)(4 * c + e) * 4 * I) = o;
+            }
+        }
+        a.pgu[((size_t)slot * 2 + mt) * I + row] = ldexpf(1.0f, 24 - P);
+    } else if (r < 2 * I + H) {
+        const int h = r - 2 * I;
+        const vmi_qmat Dm = shared ? a.sh_down : a.down;
+        const size_t mb = (shared ? 0 : (size_t)slot) * Gd * H + h;
+        uint32_t mx = 0u, mxb = 0u;
+        for (int g = 0; g < Gd; ++g) {
+            mx = max(mx, ((uint32_t)Dm.s[mb + (size_t)g * H] << 16) & 0x7fff0000u);
+            mxb = max(mxb, ((uint32_t)Dm.b[mb + (size_t)g * H] << 16) & 0x7fff0000u);
+        }
+        const int P = pf_row_pow2(mx, mxb);
+        const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
+        for (int gp = 0; gp < GPd; ++gp) {
+            uint32_t o[2] = {0u, 0u};  // a missing second group (Gd odd) is zero: its values contribute nothing
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int g = 2 * gp + j;
+                if (g < Gd)
+                    o[j] = vmi_h2_bits((_Float16)(vmi_bf16_to_f32(Dm.s[mb + (size_t)g * H]) * ps),
+                                       (_Float16)(vmi_bf16_to_f32(Dm.b[mb + (size_t)g * H]) * pb));
+            }
+            *reinterpret_cast<uint2*>(a.tdn + (((size_t)slot * GPd + gp) * H + h) * 2) = make_uint2(o[0], o[1]);
+        }
+        a.pdn[(size_t)slot * H + h] = ldexpf(1.0f, 24 - P);
+    }
+}
+
 // Gate/up: tile 128 routes x 256 intermediate rows of gate and of up (512
-// weight rows per stage), K = H, eight waves side by side (wave w: all 128
-// routes, intermediate rows 32w.. of both matrices, so each unpacked weight
+// weight rows), K = H, eight waves side by side (wave w: all 128 routes,
+// intermediate rows 32w.. of both matrices, so each dequantised weight
 // operand feeds up to eight 16-route blocks).  The weight operand is the
-// dequantised value in fp16, (q 2^-24) s' + b' (s' = s 2^P, b' = b 2^(P-24),
-// P the weight row's power of two from pf_row_pow2), so the MFMAs accumulate the whole
-// affine product over all of K and the row's sums are times 2^(24-P) at the
-// end.  Then SwiGLU rounded to bf16,
-// and the down projection's fp16 operands of the activations: each route's
-// 256 columns times 2^-E, E the route's exponent for this block.
+// dequantised value in fp16, (q 2^-24) s' + b', with (s', b') from the table
+// k_pf_table built (s' = s 2^P, b' = b 2^(P-24), P the row's power of two), so
+// the MFMAs accumulate the whole affine product over all of K and the row's
+// sums are times 2^(24-P) at the end.  K streams two quantisation groups per
+// stage: the operand rows (gathered by token, shared by the waves: two slots
+// and a barrier per stage) and each wave's own weight blocks and table pairs
+// (two slots, no barrier: a wave DMAs exactly what it reads); the next
+// group's weights are dequantised under the current group's MFMAs.  Then
+// SwiGLU rounded to bf16, and the down projection's fp16 operands of the
+// activations: each route's 256 columns times 2^-E, E the route's exponent for
+// this block.
 constexpr int kPf8Threads = 512;
+constexpr int kPfA2 = kTM3 * 256;    // operand slot: 128 rows x two groups of 64 fp16
+constexpr int kPfB2 = 8 * 4 * 1024;  // weight slot: per wave 4 pool blocks (16 rows x one group pair)
+constexpr int kPfT2 = 8 * 512;       // table slot: per wave 64 rows x two groups x (s', b')
+// byte offset of operand row r, logical 16-byte piece c (of 16), in a
+// two-group slot: rows are 256 bytes (one pass over the 64 banks), so piece c
+// sits at position c ^ (r & 15) and the 16 rows of a ds_read_b128 phase cover
+// the banks once
+__device__ __forceinline__ uint32_t pf_a2_off(int r, int c) { return 16u * (16u * r + (unsigned)(c ^ (r & 15))); }
+// the logical piece a position holds (the inverse of pf_a2_off's swizzle)
+__device__ __forceinline__ int pf_a2_piece(int r, int pos) { return pos ^ (r & 15); }
+
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
-    constexpr int kB = 512 * 32;
-    // two slots of operand rows (shared by the waves) and three of weight
-    // rows (a wave DMAs exactly the weight rows it reads, so their slots need
-    // no barrier, and group g + 1's weights are dequantised under group g's
-    // MFMAs), then the groups' fp16 (s', b') pairs [group][matrix * 256 +
-    // row]; after the loop all of it holds the activation staging
-    constexpr int kAS = 2, kBS = 3, kRing = kAS * kPfA + kBS * kB;
-    __shared__ __attribute__((aligned(16))) uint8_t s_mem[kRing + kMaxG * 512 * 4];
+    // [operand slots 0, 1][weight slots 0, 1][table slots 0, 1]; after the
+    // loop all of it holds the activation staging
+    __shared__ __attribute__((aligned(16))) uint8_t s_mem[2 * (kPfA2 + kPfB2 + kPfT2)];
     uint8_t* const s_ra = s_mem;
-    uint8_t* const s_rb = s_mem + kAS * kPfA;
-    uint32_t(*const s_sb)[512] = reinterpret_cast<uint32_t(*)[512]>(s_mem + kRing);
-    __shared__ float s_post[512];  // 2^(24 - P): what the row's sums are multiplied by at the end
+    uint8_t* const s_rb = s_mem + 2 * kPfA2;
+    uint8_t* const s_rt = s_rb + 2 * kPfB2;
+    __shared__ __attribute__((aligned(16))) float s_post[512];  // 2^(24 - P): the row's sums are times this at the end
     __shared__ int s_route[kTM3];
     __shared__ int s_tok[kTM3];
     __shared__ float s_inv[kTM3];  // 1 / f of the route's token (0 past the tile)
@@ -595,7 +681,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     pf_tile_of(blockIdx.x, NB, ti, nb);
     if (ti >= a.ntiles[0]) return;
     const int4 tl = a.tiles[ti];
-    const int H = a.H, HW = H / 8, G = H / 64, I = a.I;
+    const int H = a.H, HW = H / 8, G = H / 64, GP = G / 2, I = a.I;
     const int n0 = nb * 256, nvalid = min(256, I - n0);
     // 16-route blocks holding routes (uniform): the blocks past the tile's
     // count issue no MFMA
@@ -604,109 +690,72 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
     const vmi_qmat Gm = tl.x >= 0 ? a.gate : a.sh_gate;
     const vmi_qmat Um = tl.x >= 0 ? a.up : a.sh_up;
     const size_t mrow0 = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)I;
-    // DMA sources of the weights: pieces p = tid + 512 j (row p/2: matrix
-    // row/256, intermediate row n0 + row%256; half (p%2) ^ bit 3 of row)
-    const uint32_t* bsrc[2];
+    const int slot = tl.x >= 0 ? tl.x : a.cap;  // table slot (cap: the shared expert)
+    // weight DMA of wave w: block b = 2mt + sb is pool block (rows n0 + 32w +
+    // 16sb .. + 15 of matrix mt, group pair gp), 1 KB contiguous: 16 bytes of
+    // group 2gp + g2, half h of row i at 16 (16 (2 g2 + h) + i).  Blocks past
+    // I (a partial last column block) fetch the last block again.
+    const uint32_t* bsrc[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int p = tid + kPf8Threads * j;
-        const int brow = p >> 1, h = (p & 1) ^ ((brow >> 3) & 1);
-        const int mt = brow >> 8, rr = min(n0 + (brow & 255), I - 1);
-        // MFMA-major pool: the 16 bytes of group g, half h of row rr sit in
-        // block (rr / 16, g / 2) at lane 16 (2 (g % 2) + h) + rr % 16
-        bsrc[j] = (mt ? Um.w : Gm.w) + mrow0 * HW + (size_t)(rr >> 4) * (H / 128) * 256 + 64 * h + 4 * (rr & 15);
+    for (int b = 0; b < 4; ++b) {
+        const int mt = b >> 1, sb = b & 1, rr = min(n0 + 32 * w + 16 * sb, I - 16);
+        bsrc[b] = (mt ? Um.w : Gm.w) + mrow0 * HW + (size_t)(rr >> 4) * (H / 128) * 256 + 4 * lane;
     }
-    auto issue_b = [&](int g, int u) {
-        uint8_t* B = s_rb + u * kB;
+    // table DMA of wave w, per matrix: rows n0 + 32w + lane/2, group lane%2 of
+    // the pair, one dword each
+    const uint32_t* tsrc[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            vmi_lds_dma16_opaque(bsrc[j] + 256 * (g >> 1) + 128 * (g & 1), B + 16 * (kPf8Threads * j + 64 * w));
+    for (int mt = 0; mt < 2; ++mt) {
+        const int row = min(n0 + 32 * w + (lane >> 1), I - 1);
+        tsrc[mt] = a.tgu + (((size_t)slot * GP * 2 + mt) * I + row) * 2 + (lane & 1);
+    }
+    auto issue_b = [&](int gp, int u) {
+        uint8_t* B = s_rb + u * kPfB2 + 4096 * w;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) vmi_lds_dma16_opaque(bsrc[b] + 256 * gp, B + 1024 * b);
+        uint8_t* Tt = s_rt + u * kPfT2 + 512 * w;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) vmi_lds_dma4_opaque(tsrc[mt] + (size_t)gp * 4 * I, Tt + 256 * mt);
     };
-    // the first two groups' weights are in flight while the prologue runs
+    // the first two group pairs' weights are in flight while the prologue runs
     issue_b(0, 0);
-    issue_b(G > 1 ? 1 : 0, 1);
-    // staging loads are all issued before their values are stored, so the
-    // workgroup waits for one memory latency, not one per loop iteration
-    {
-        constexpr int kIt = (2 * 256 * (kMaxG / 8) + kPf8Threads - 1) / kPf8Threads;
-        const int n16 = 2 * 256 * (G / 8);
-        uint4 v[kIt], vb[kIt];
-#pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-            const int i = tid + kPf8Threads * it;
-            if (i < n16) {
-                const int chunk = i % (G / 8), row = (i / (G / 8)) % 256, mt = i / (G / 8 * 256);
-                const int rr = min(n0 + row, I - 1);
-                v[it] = *reinterpret_cast<const uint4*>((mt ? Um.s : Gm.s) + (mrow0 + rr) * G + 8 * chunk);
-                vb[it] = *reinterpret_cast<const uint4*>((mt ? Um.b : Gm.b) + (mrow0 + rr) * G + 8 * chunk);
-            }
-        }
-        if (tid < kTM3) {
-            const int rt = tile_route(a, tl, tid);
-            const int tok = rt >= 0 ? rt / (a.k + 1) : 0;
-            s_route[tid] = rt;
-            s_tok[tid] = tok;
-            s_inv[tid] = rt >= 0 ? 1.0f / a.fscale[tok] : 0.0f;
-        }
-        // a row's G/8 chunks of eight scales (and biases) sit in G/8
-        // consecutive lanes (G/8 is 1, 2 or 4, and the branch is uniform:
-        // it < G/8); each row's power of two comes from pf_row_pow2
-#pragma unroll
-        for (int it = 0; it < kIt; ++it) {
-            const int i = tid + kPf8Threads * it;
-            if (i < n16) {
-                const int chunk = i % (G / 8), row = (i / (G / 8)) % 256, mt = i / (G / 8 * 256);
-                const uint32_t wv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
-                const uint32_t bw[4] = {vb[it].x, vb[it].y, vb[it].z, vb[it].w};
-                uint32_t mx = 0u, mxb = 0u;  // |scale|, |bias| as float bits: ordered as integers
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    mx = max(mx, (wv[j >> 1] << (16 - 16 * (j & 1))) & 0x7fff0000u);
-                    mxb = max(mxb, (bw[j >> 1] << (16 - 16 * (j & 1))) & 0x7fff0000u);
-                }
-                for (int o = 1; o < G / 8; o <<= 1) {
-                    mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
-                    mxb = max(mxb, (uint32_t)__shfl_xor((int)mxb, o));
-                }
-                const int P = pf_row_pow2(mx, mxb);
-                const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t sv = (wv[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-                    const uint32_t bv = (bw[j >> 1] >> (16 * (j & 1))) & 0xffffu;
-                    s_sb[8 * chunk + j][256 * mt + row] =
-                        vmi_h2_bits((_Float16)(vmi_bf16_to_f32(sv) * ps), (_Float16)(vmi_bf16_to_f32(bv) * pb));
-                }
-                if (chunk == 0) s_post[256 * mt + row] = ldexpf(1.0f, 24 - P);
-            }
-        }
+    issue_b(GP > 1 ? 1 : 0, 1);
+    if (tid < kTM3) {
+        const int rt = tile_route(a, tl, tid);
+        const int tok = rt >= 0 ? rt / (a.k + 1) : 0;
+        s_route[tid] = rt;
+        s_tok[tid] = tok;
+        s_inv[tid] = rt >= 0 ? 1.0f / a.fscale[tok] : 0.0f;
     }
+    s_post[tid] = a.pgu[((size_t)slot * 2 + (tid >> 8)) * I + min(n0 + (tid & 255), I - 1)];
     __syncthreads();
-    // DMA sources of the operands: pieces p = tid + 512 j (row p/8, slot
-    // piece p%8 = logical piece (p%8) ^ (row & 7))
-    const vmi_u4* asrc[2];
+    // operand DMA: pieces p = tid + 512 j (row p/16, position p%16 holding
+    // logical piece pf_a2_piece(row, p%16) of the pair)
+    const vmi_u4* asrc[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < 4; ++j) {
         const int p = tid + kPf8Threads * j;
-        const int arow = p >> 3, c = pf_a_piece(arow, p & 7);
+        const int arow = p >> 4, c = pf_a2_piece(arow, p & 15);
         asrc[j] = a.xop4 + (size_t)s_tok[arow] * HW + c;
     }
-    auto issue_a = [&](int g, int u) {
-        uint8_t* A = s_ra + u * kPfA;
+    auto issue_a = [&](int gp, int u) {
+        uint8_t* A = s_ra + u * kPfA2;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
+        for (int j = 0; j < 4; ++j) vmi_lds_dma16_opaque(asrc[j] + 16 * gp, A + 16 * (kPf8Threads * j + 64 * w));
     };
-    // this wave's four (column block, matrix) weight operands of group g from
-    // weight slot u, dequantised
-    auto dequant = [&](vmi_u4 (&bo)[4][2], int u, int g) {
-        const uint8_t* B = s_rb + u * kB;
+    issue_a(0, 0);
+    // this wave's four (column block, matrix) weight operands of group g2 of
+    // the pair in slot u, dequantised
+    auto dequant = [&](vmi_u4 (&bo)[4][2], int u, int g2) {
+        const uint8_t* B = s_rb + u * kPfB2 + 4096 * w;
+        const uint8_t* Tt = s_rt + u * kPfT2 + 512 * w;
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {
             const int sb = blk >> 1, mt = blk & 1;
-            const int brow = 256 * mt + 32 * w + 16 * sb + n;
-            const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(brow, q));
+            const uint2 wq = *reinterpret_cast<const uint2*>(B + 1024 * (2 * mt + sb) + 256 * (2 * g2 + (q >> 1)) +
+                                                             16 * n + 8 * (q & 1));
             uint32_t s2, b2, b16;
-            pf_affine_pairs(s_sb[g][brow], s2, b2, b16);
+            pf_affine_pairs(*reinterpret_cast<const uint32_t*>(Tt + 256 * mt + 4 * (2 * (16 * sb + n) + g2)), s2, b2, b16);
             bo[blk][0] = pf_dequant_f16(wq.x, s2, b2, b16);
             bo[blk][1] = pf_dequant_f16(wq.y, s2, b2, b16);
         }
@@ -719,62 +768,65 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) acc[m][sb][mt] = vmi_f4{0.f, 0.f, 0.f, 0.f};
     VMI_STAMP(4, 1);
-    issue_a(0, 0);
     // the stage loop for MC of the 16-route blocks holding routes (a loop per
     // MC, so each keeps its own register allocation; MC = 0 only moves the
-    // ring and keeps the barriers).  Stage g: group g's operands (everyone's
-    // DMA, hence the barrier) against its weights dequantised during stage
-    // g - 1, while group g + 1's weights (this wave's own DMA, landed) are
-    // dequantised; the DMA of operands g + 1 and weights g + 2 goes out.
+    // rings and keeps the barriers).  Per thread and stage the DMA is 4
+    // operand pieces and 6 weight and table copies, issued in the order the
+    // waits below count.
     auto stage_loop = [&](auto mc_tag) {
         constexpr int MC = decltype(mc_tag)::value;
-        // stage g with this group's dequantised weights bcur, filling bnext
-        auto stage = [&](int g, const vmi_u4 (&bcur)[4][2], vmi_u4 (&bnext)[4][2]) {
-            pf_wait_vmcnt<0>();  // operands g and weights g + 1 (this thread's) have landed
-            __syncthreads();     // everyone's operands g; operand slot (g + 1) % 2 is free
-            if ((g & 3) == 0 && g < 32) VMI_STAMP(4, 2 + (g >> 2));
-            if (g + 1 < G) issue_a(g + 1, (g + 1) & 1);
-            if (g + 2 < G) issue_b(g + 2, (g + 2) % kBS);
-            if constexpr (MC > 0) {
-                const uint8_t* A = s_ra + (g & 1) * kPfA;
-                // the next group's weights (past the last group: a valid slot
-                // and table row whose values go unused, so this stays one
-                // block with the MFMAs)
-                dequant(bnext, (g + 1) % kBS, min(g + 1, G - 1));
-                // each 16-route block's operands (read one block ahead)
-                // against the four, accumulated over all of K; the weights go
-                // first, so a lane holds four consecutive weight rows of one
-                // route
-                vmi_u4 an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(n, 2 * q));
-                vmi_u4 an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(n, 2 * q + 1));
+        // one group of the stage's pair: each 16-route block's operands (read
+        // one block ahead) against the four weight operands; the weights go
+        // first, so a lane holds four consecutive weight rows of one route
+        auto mfma_group = [&](const uint8_t* A, int g2, const vmi_u4 (&bo)[4][2]) {
+            vmi_u4 an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a2_off(n, 8 * g2 + 2 * q));
+            vmi_u4 an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a2_off(n, 8 * g2 + 2 * q + 1));
 #pragma unroll
-                for (int m = 0; m < MC; ++m) {
-                    const vmi_u4 a0 = an0, a1 = an1;
-                    if (m + 1 < MC) {
-                        const int row = 16 * (m + 1) + n;
-                        an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
-                        an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
-                    }
-#pragma unroll
-                    for (int blk = 0; blk < 4; ++blk)
-                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bcur[blk][0], a0, acc[m][blk >> 1][blk & 1]);
-#pragma unroll
-                    for (int blk = 0; blk < 4; ++blk)
-                        acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bcur[blk][1], a1, acc[m][blk >> 1][blk & 1]);
+            for (int m = 0; m < MC; ++m) {
+                const vmi_u4 a0 = an0, a1 = an1;
+                if (m + 1 < MC) {
+                    const int row = 16 * (m + 1) + n;
+                    an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a2_off(row, 8 * g2 + 2 * q));
+                    an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a2_off(row, 8 * g2 + 2 * q + 1));
                 }
+#pragma unroll
+                for (int blk = 0; blk < 4; ++blk)
+                    acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bo[blk][0], a0, acc[m][blk >> 1][blk & 1]);
+#pragma unroll
+                for (int blk = 0; blk < 4; ++blk)
+                    acc[m][blk >> 1][blk & 1] = vmi_mfma_f16(bo[blk][1], a1, acc[m][blk >> 1][blk & 1]);
             }
         };
-        vmi_u4 b0[4][2], b1[4][2];
+        vmi_u4 b0[4][2], b1[4][2];  // group 0 and group 1 of a pair
         if constexpr (MC > 0) {
-            pf_wait_vmcnt<2>();  // this wave's weights of group 0 (operands 0 may be in flight)
+            pf_wait_vmcnt<4>();  // this wave's weights of pair 0 (operands 0 may be in flight)
             dequant(b0, 0, 0);
         }
-        // two stages per iteration, so the two weight buffers trade roles
-        // without copies (G is even: H is 512, 1024 or 2048)
 #pragma unroll 1
-        for (int g = 0; g < G; g += 2) {
-            stage(g, b0, b1);
-            stage(g + 1, b1, b0);
+        for (int gp = 0; gp < GP; ++gp) {
+            const int u = gp & 1;
+            // operands gp (this thread's pieces) have landed; weights gp + 1
+            // may still be in flight
+            if (gp == 0)
+                pf_wait_vmcnt<0>();
+            else
+                pf_wait_vmcnt<6>();
+            __syncthreads();  // everyone's operands gp; operand slot u ^ 1 is free
+            if ((gp & 1) == 0 && gp < 16) VMI_STAMP(4, 2 + (gp >> 1));
+            issue_a(min(gp + 1, GP - 1), u ^ 1);
+            if constexpr (MC > 0) {
+                dequant(b1, u, 1);
+                mfma_group(s_ra + u * kPfA2, 0, b0);
+            }
+            // weight slot u is read: pair gp + 2 refills it (past the last
+            // pair, the last again: never read)
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            issue_b(min(gp + 2, GP - 1), u);
+            if constexpr (MC > 0) {
+                pf_wait_vmcnt<10>();  // this wave's weights of pair gp + 1
+                dequant(b0, u ^ 1, 0);  // past the last pair: stale values, unused
+                mfma_group(s_ra + u * kPfA2, 1, b1);
+            }
         }
     };
     switch (mcnt) {
@@ -895,10 +947,9 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_gateup3(PfArgs a) {
 // E per route and 256-column block.  The sums are scaled by 2^(E_prev - E) at
 // each block boundary and by 2^(24-P) 2^E_last at the end, then times the
 // route's combine weight into one bf16 row per (token, rank).  As in
-// k_pf_gateup3, a wave DMAs exactly the weight rows it reads (three slots,
-// two groups ahead, dequantised one group ahead under the MFMAs) and the
-// operand rows go through two shared slots.  MAXG bounds the quantisation
-// groups of K the LDS table holds.
+// k_pf_gateup3, K streams two groups per stage: the operand rows through two
+// shared slots, each wave's own weight rows and table pairs through two slots
+// of its own, dequantised one group ahead under the MFMAs.
 constexpr int kPfMaxIB = 8;  // 256-column blocks of the intermediate size (I <= 2048)
 // Hidden row (inside a wave's 64) of weight position p: positions 16sb..16sb+15
 // are MFMA block sb's rows, and row n of block sb (= 2t + s) is hidden row
@@ -908,13 +959,13 @@ __device__ __forceinline__ int pf_down_row(int p) {
     return (p & 32) | (((p >> 2) & 3) << 3) | (((p >> 4) & 1) << 2) | (p & 3);
 }
 
-template <int MAXG>
 __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
-    constexpr int kB = 512 * 32;
-    constexpr int kAS = 2, kBS = 3;
-    __shared__ __attribute__((aligned(16))) uint8_t s_ra[kAS * kPfA];
-    __shared__ __attribute__((aligned(16))) uint8_t s_rb[kBS * kB];
-    __shared__ uint32_t s_sb[MAXG][512];                        // fp16 s' | b' << 16: [group][hidden row]
+    // [operand slots 0, 1][weight slots 0, 1][table slots 0, 1], one group
+    // pair each
+    __shared__ __attribute__((aligned(16))) uint8_t s_mem[2 * (kPfA2 + kPfB2 + kPfT2)];
+    uint8_t* const s_ra = s_mem;
+    uint8_t* const s_rb = s_mem + 2 * kPfA2;
+    uint8_t* const s_rt = s_rb + 2 * kPfB2;
     __shared__ __attribute__((aligned(16))) float s_post[512];  // 2^(24 - P)
     __shared__ int s_route[kTM3];
     __shared__ int s_exp[kTM3][kPfMaxIB];
@@ -930,14 +981,15 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     // count issue no MFMA
     const int mcnt = __builtin_amdgcn_readfirstlane(max(0, min(8, (tl.z + 15) / 16)));
     VMI_STAMP(3, 0);
-    const int I = a.I, IW = I / 8, G = I / 64, IB = (I + 255) / 256;
+    const int H = a.H, I = a.I, IW = I / 8, G = I / 64, GP = (G + 1) / 2, IB = (I + 255) / 256;
     const int h0 = nb * 512;
     const vmi_qmat Dm = tl.x >= 0 ? a.down : a.sh_down;
+    const int slot = tl.x >= 0 ? tl.x : a.cap;  // table slot (cap: the shared expert)
     // the down projection is group-major: row h of group g of slot m at
-    // (m * G + g) * H + h (32 bytes of words; one bf16 scale and bias)
-    const size_t mbase = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)G * a.H + h0;
-    // weight DMA into the wave's own 2 KB of the slot: 32-byte position
-    // p = 32j + lane/2 of wave w holds hidden row 64w + pf_down_row(p), half
+    // (m * G + g) * H + h (32 bytes of words)
+    const size_t mbase = (tl.x >= 0 ? (size_t)tl.x : 0) * (size_t)G * H + h0 + 64 * w;
+    // weight DMA into the wave's own 2 KB per group: 32-byte position
+    // p = 32j + lane/2 holds hidden row 64w + pf_down_row(p), half
     // (lane%2) ^ bit 3 of p (pf_down_row puts the 16 rows an MFMA block reads
     // in 16 consecutive positions, which ds_read_b64 reads without bank
     // conflicts)
@@ -945,85 +997,77 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int p = 32 * j + (lane >> 1), h = (lane & 1) ^ ((p >> 3) & 1);
-        bsrc[j] = Dm.w + (mbase + 64 * w + pf_down_row(p)) * 8 + 4 * h;
+        bsrc[j] = Dm.w + (mbase + pf_down_row(p)) * 8 + 4 * h;
     }
-    auto issue_b = [&](int g, int u) {
-        uint8_t* B = s_rb + u * kB;
+    // table DMA: the wave's 64 hidden rows in order, two words (the pair's
+    // groups) each
+    const uint32_t* tsrc = a.tdn + ((size_t)slot * GP * H + h0 + 64 * w) * 2 + lane;
+    auto issue_b = [&](int gp, int u) {
+        uint8_t* B = s_rb + u * kPfB2 + 4096 * w;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            vmi_lds_dma16_opaque(bsrc[j] + (size_t)g * a.H * 8, B + 16 * (128 * w + 64 * j));
+        for (int g2 = 0; g2 < 2; ++g2) {
+            // a missing second group (G odd) fetches the last again: its table pair is zero
+            const int g = min(2 * gp + g2, G - 1);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(bsrc[j] + (size_t)g * H * 8, B + 2048 * g2 + 1024 * j);
+        }
+        uint8_t* Tt = s_rt + u * kPfT2 + 512 * w;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) vmi_lds_dma4_opaque(tsrc + (size_t)gp * 2 * H + 64 * j, Tt + 256 * j);
     };
-    // the first two groups' weights are in flight while the prologue runs
+    // the first two group pairs' weights are in flight while the prologue runs
     issue_b(0, 0);
-    issue_b(G > 1 ? 1 : 0, 1);
-    {
-        // thread t: hidden row h0 + t, every group (a wave reads 128
-        // contiguous bytes per group); these loads are issued first, the
-        // routes' dependent loads wait behind them
-        uint32_t sv[MAXG], bv[MAXG];
-#pragma unroll
-        for (int g = 0; g < MAXG; ++g) {
-            sv[g] = 0u;
-            bv[g] = 0u;
-            if (g < G) {
-                sv[g] = Dm.s[mbase + (size_t)g * a.H + tid];
-                bv[g] = Dm.b[mbase + (size_t)g * a.H + tid];
-            }
+    issue_b(GP > 1 ? 1 : 0, 1);
+    if (tid < kTM3) {
+        const int rt = tile_route(a, tl, tid);
+        s_route[tid] = rt;
+        int el = 0;
+        for (int b = 0; b < IB; ++b) {
+            el = rt >= 0 ? a.aexp[(size_t)rt * IB + b] : 0;
+            s_exp[tid][b] = el;
         }
-        if (tid < kTM3) {
-            const int rt = tile_route(a, tl, tid);
-            s_route[tid] = rt;
-            int el = 0;
-            for (int b = 0; b < IB; ++b) {
-                el = rt >= 0 ? a.aexp[(size_t)rt * IB + b] : 0;
-                s_exp[tid][b] = el;
-            }
-            float wgt = 0.0f;
-            if (rt >= 0) {
-                const int t = rt / (a.k + 1), j = rt - t * (a.k + 1);
-                wgt = j < a.k ? a.scores[t * a.k + j] : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
-            }
-            s_rf[tid] = wgt * ldexpf(1.0f, el);
+        float wgt = 0.0f;
+        if (rt >= 0) {
+            const int t = rt / (a.k + 1), j = rt - t * (a.k + 1);
+            wgt = j < a.k ? a.scores[t * a.k + j] : (a.has_sgate ? 1.0f / (1.0f + expf(-a.sglogit[t])) : 1.0f);
         }
-        uint32_t mx = 0u, mxb = 0u;  // |scale|, |bias| as float bits: ordered as integers
-#pragma unroll
-        for (int g = 0; g < MAXG; ++g) {
-            mx = max(mx, (sv[g] << 16) & 0x7fff0000u);
-            mxb = max(mxb, (bv[g] << 16) & 0x7fff0000u);
-        }
-        const int P = pf_row_pow2(mx, mxb);
-        const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
-#pragma unroll
-        for (int g = 0; g < MAXG; ++g)
-            if (g < G)
-                s_sb[g][tid] = vmi_h2_bits((_Float16)(vmi_bf16_to_f32(sv[g]) * ps), (_Float16)(vmi_bf16_to_f32(bv[g]) * pb));
-        s_post[tid] = ldexpf(1.0f, 24 - P);
+        s_rf[tid] = wgt * ldexpf(1.0f, el);
     }
+    s_post[tid] = a.pdn[(size_t)slot * H + h0 + tid];
     __syncthreads();
-    const vmi_u4* asrc[2];
+    // operand DMA: pieces p = tid + 512 j (row p/16, position p%16 holding
+    // logical piece pf_a2_piece(row, p%16) of the pair); a missing second
+    // group reads the first again (its weights are zero)
+    const vmi_u4* asrc[4];
+    int apc[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < 4; ++j) {
         const int p = tid + kPf8Threads * j;
-        const int arow = p >> 3, c = pf_a_piece(arow, p & 7);
+        const int arow = p >> 4;
         const int rt = s_route[arow];
-        asrc[j] = a.actop + (size_t)(rt >= 0 ? rt : 0) * IW + c;
+        apc[j] = pf_a2_piece(arow, p & 15);
+        asrc[j] = a.actop + (size_t)(rt >= 0 ? rt : 0) * IW;
     }
-    auto issue_a = [&](int g, int u) {
-        uint8_t* A = s_ra + u * kPfA;
+    auto issue_a = [&](int gp, int u) {
+        uint8_t* A = s_ra + u * kPfA2;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(asrc[j] + 8 * g, A + 16 * (kPf8Threads * j + 64 * w));
+        for (int j = 0; j < 4; ++j) {
+            const int pc = 16 * gp + apc[j];
+            vmi_lds_dma16_opaque(asrc[j] + (pc < IW ? pc : pc - 8), A + 16 * (kPf8Threads * j + 64 * w));
+        }
     };
-    // this wave's four column blocks of group g from weight slot u,
+    issue_a(0, 0);
+    // this wave's four column blocks of group g2 of the pair in slot u,
     // dequantised; block sb row n is hidden row 64w + pf_down_row(16sb + n)
-    auto dequant = [&](vmi_u4 (&wo)[4][2], int u, int g) {
-        const uint8_t* B = s_rb + u * kB;
+    auto dequant = [&](vmi_u4 (&wo)[4][2], int u, int g2) {
+        const uint8_t* B = s_rb + u * kPfB2 + 4096 * w + 2048 * g2;
+        const uint8_t* Tt = s_rt + u * kPfT2 + 512 * w;
 #pragma unroll
         for (int sb = 0; sb < 4; ++sb) {
-            const int pos = 64 * w + 16 * sb + n;
-            const int brow = 64 * w + pf_down_row(16 * sb + n);
+            const int pos = 16 * sb + n;
             const uint2 wq = *reinterpret_cast<const uint2*>(B + ring_off(pos, q));
             uint32_t s2, b2, b16;
-            pf_affine_pairs(s_sb[g][brow], s2, b2, b16);
+            pf_affine_pairs(*reinterpret_cast<const uint32_t*>(Tt + 4 * (2 * pf_down_row(pos) + g2)), s2, b2, b16);
             wo[sb][0] = pf_dequant_f16(wq.x, s2, b2, b16);
             wo[sb][1] = pf_dequant_f16(wq.y, s2, b2, b16);
         }
@@ -1034,21 +1078,48 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
 #pragma unroll
         for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
     VMI_STAMP(3, 1);
-    issue_a(0, 0);
     // the stage loop for MC active 16-route blocks (a loop per MC, so each
     // keeps its own register allocation; MC = 0 only moves the rings and
-    // keeps the barriers)
+    // keeps the barriers).  Per thread and stage the DMA is 4 operand pieces
+    // and 6 weight and table copies, issued in the order the waits count.
     auto stage_loop = [&](auto mc_tag) {
         constexpr int MC = decltype(mc_tag)::value;
-        auto stage = [&](int g, const vmi_u4 (&wcur)[4][2], vmi_u4 (&wnext)[4][2]) {
-            pf_wait_vmcnt<0>();  // operands g and weights g + 1 (this thread's) have landed
-            __syncthreads();     // everyone's operands g; operand slot (g + 1) % 2 is free
-            if (g + 1 < G) issue_a(g + 1, (g + 1) & 1);
-            if (g + 2 < G) issue_b(g + 2, (g + 2) % kBS);
+        auto mfma_group = [&](const uint8_t* A, int g2, const vmi_u4 (&wo)[4][2]) {
+            vmi_u4 an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a2_off(n, 8 * g2 + 2 * q));
+            vmi_u4 an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a2_off(n, 8 * g2 + 2 * q + 1));
+#pragma unroll
+            for (int m = 0; m < MC; ++m) {
+                const vmi_u4 a0 = an0, a1 = an1;
+                if (m + 1 < MC) {
+                    const int row = 16 * (m + 1) + n;
+                    an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a2_off(row, 8 * g2 + 2 * q));
+                    an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a2_off(row, 8 * g2 + 2 * q + 1));
+                }
+#pragma unroll
+                for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wo[sb][0], a0, acc[m][sb]);
+#pragma unroll
+                for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wo[sb][1], a1, acc[m][sb]);
+            }
+        };
+        vmi_u4 b0[4][2], b1[4][2];  // group 0 and group 1 of a pair
+        if constexpr (MC > 0) {
+            pf_wait_vmcnt<4>();  // this wave's weights of pair 0 (operands 0 may be in flight)
+            dequant(b0, 0, 0);
+        }
+#pragma unroll 1
+        for (int gp = 0; gp < GP; ++gp) {
+            const int u = gp & 1;
+            if (gp == 0)
+                pf_wait_vmcnt<0>();
+            else
+                pf_wait_vmcnt<6>();
+            __syncthreads();  // everyone's operands gp; operand slot u ^ 1 is free
+            issue_a(min(gp + 1, GP - 1), u ^ 1);
             if constexpr (MC > 0) {
-                if (g > 0 && (g & 3) == 0) {
-                    // a new 256-column block: the sums so far times 2^(E_prev - E)
-                    const int b = g >> 2;
+                if (gp > 0 && (gp & 1) == 0) {
+                    // a new 256-column block (two pairs): the sums so far
+                    // times 2^(E_prev - E)
+                    const int b = gp >> 1;
 #pragma unroll
                     for (int m = 0; m < MC; ++m) {
                         const int row = 16 * m + n;
@@ -1059,38 +1130,17 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
                             for (int r = 0; r < 4; ++r) acc[m][sb][r] *= f;
                     }
                 }
-                const uint8_t* A = s_ra + (g & 1) * kPfA;
-                // the next group's weights (past the last group: a valid slot
-                // and table row whose values go unused)
-                dequant(wnext, (g + 1) % kBS, min(g + 1, G - 1));
-                vmi_u4 an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(n, 2 * q));
-                vmi_u4 an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(n, 2 * q + 1));
-#pragma unroll
-                for (int m = 0; m < MC; ++m) {
-                    const vmi_u4 a0 = an0, a1 = an1;
-                    if (m + 1 < MC) {
-                        const int row = 16 * (m + 1) + n;
-                        an0 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q));
-                        an1 = *reinterpret_cast<const vmi_u4*>(A + pf_a_off(row, 2 * q + 1));
-                    }
-#pragma unroll
-                    for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wcur[sb][0], a0, acc[m][sb]);
-#pragma unroll
-                    for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wcur[sb][1], a1, acc[m][sb]);
-                }
+                dequant(b1, u, 1);
+                mfma_group(s_ra + u * kPfA2, 0, b0);
             }
-        };
-        vmi_u4 w0[4][2], w1[4][2];
-        if constexpr (MC > 0) {
-            pf_wait_vmcnt<2>();  // this wave's weights of group 0 (operands 0 may be in flight)
-            dequant(w0, 0, 0);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): weight slot u is read
+            issue_b(min(gp + 2, GP - 1), u);
+            if constexpr (MC > 0) {
+                pf_wait_vmcnt<10>();  // this wave's weights of pair gp + 1
+                dequant(b0, u ^ 1, 0);  // past the last pair: stale values, unused
+                mfma_group(s_ra + u * kPfA2, 1, b1);
+            }
         }
-#pragma unroll 1
-        for (int g = 0; g + 1 < G; g += 2) {
-            stage(g, w0, w1);
-            stage(g + 1, w1, w0);
-        }
-        if (G & 1) stage(G - 1, w0, w1);
     };
     switch (mcnt) {
         case 8: stage_loop(std::integral_constant<int, 8>{}); break;
@@ -1371,7 +1421,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_combine(PfArgs a) {
 // -------------------------------------------------------------- workspace
 struct PfLayout {
     size_t status, xop4, xsum4, xop8, xsum8, fscale, logits, sglogit, ids, scores, slots, counts, offsets, fill,
-        tiles, ntiles, list, actop, aexp, ybuf, bytes;
+        tiles, ntiles, list, tgu, pgu, tdn, pdn, actop, aexp, ybuf, bytes;
     int max_tiles;
 };
 
@@ -1402,6 +1452,10 @@ PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) 
     L.tiles = take((size_t)L.max_tiles * 16);
     L.ntiles = take(4);
     L.list = take((size_t)T * k * 4);
+    L.tgu = take((size_t)(cap + 1) * (H / 128) * 2 * I * 2 * 4);
+    L.pgu = take((size_t)(cap + 1) * 2 * I * 4);
+    L.tdn = take((size_t)(cap + 1) * ((I / 64 + 1) / 2) * H * 2 * 4);
+    L.pdn = take((size_t)(cap + 1) * H * 4);
     L.actop = take(R * (I / 8) * 16);
     L.aexp = take(R * ((I + 255) / 256) * 4);
     L.ybuf = take(R * H * 2);
@@ -1491,6 +1545,10 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     a.tiles = reinterpret_cast<int4*>(ws + L.tiles);
     a.ntiles = reinterpret_cast<int32_t*>(ws + L.ntiles);
     a.list = reinterpret_cast<int32_t*>(ws + L.list);
+    a.tgu = reinterpret_cast<uint32_t*>(ws + L.tgu);
+    a.pgu = reinterpret_cast<float*>(ws + L.pgu);
+    a.tdn = reinterpret_cast<uint32_t*>(ws + L.tdn);
+    a.pdn = reinterpret_cast<float*>(ws + L.pdn);
     a.actop = reinterpret_cast<vmi_u4*>(ws + L.actop);
     a.aexp = reinterpret_cast<int32_t*>(ws + L.aexp);
     a.ybuf = reinterpret_cast<uint16_t*>(ws + L.ybuf);
@@ -1533,12 +1591,11 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     hipLaunchKernelGGL(k_pf_count, dim3((T * D.top_k + kCountRoutes - 1) / kCountRoutes), dim3(kPfThreads), 0, s, a);
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_table, dim3((D.cap + 1) * ((2 * D.inter + D.hidden + kPfThreads - 1) / kPfThreads)),
+                       dim3(kPfThreads), 0, s, a);
     const int tile_slots = 8 * ((L.max_tiles + 7) / 8);
     hipLaunchKernelGGL(k_pf_gateup3, dim3(tile_slots * ((D.inter + 255) / 256)), dim3(kPf8Threads), 0, s, a);
-    if (D.inter <= 512)
-        hipLaunchKernelGGL((k_pf_down3<8>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
-    else
-        hipLaunchKernelGGL((k_pf_down3<kMaxG>), dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_down3, dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(kPfThreads), 0, s, a);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill launch");
