@@ -570,24 +570,35 @@ __device__ __forceinline__ void pf_affine_pairs(uint32_t sbw, uint32_t& s2, uint
 // the shared expert, slot cap): per weight row, its power of two P
 // (pf_row_pow2) and per group the pair (s 2^P, b 2^(P-24)) as fp16 bits, laid
 // out per group pair so a wave's rows of one pair are one contiguous run;
-// 2^(24-P) per row.  One thread per row: gate and up rows first, then down.
+// 2^(24-P) per row.  A thread takes one gate or up row (its scales and biases
+// in registers, one pass) or four consecutive down rows (8-byte loads of the
+// group-major scales; a second pass reads them again from the cache).
+// Column blocks of 512 hidden rows one down workgroup runs in sequence (two
+// when the count is even), so the prologue is paid once per pair of blocks.
+__host__ __device__ __forceinline__ int pf_down_blocks(int H) { return (H / 512) % 2 == 0 ? 2 : 1; }
+__host__ __device__ __forceinline__ int pf_table_blocks(int H, int I) { return (2 * I + H / 4 + kPfThreads - 1) / kPfThreads; }
+
 __global__ __launch_bounds__(kPfThreads) void k_pf_table(PfArgs a) {
     const int I = a.I, H = a.H, G = H / 64, GP = G / 2, Gd = I / 64, GPd = (Gd + 1) / 2;
-    const int bps = (2 * I + H + kPfThreads - 1) / kPfThreads;
+    const int bps = pf_table_blocks(H, I);
     const int slot = blockIdx.x / bps, r = (blockIdx.x - slot * bps) * kPfThreads + threadIdx.x;
     const bool shared = slot == a.cap;
     if (shared ? !a.has_shared : a.counts[slot] == 0) return;
-    // |scale|, |bias| as float bits (ordered as integers) over the row, then
-    // the row's pairs; the second pass reads the row again from the cache
     if (r < 2 * I) {
         const int mt = r >= I, row = r - mt * I;
         const vmi_qmat M = mt ? (shared ? a.sh_up : a.up) : (shared ? a.sh_gate : a.gate);
         const uint16_t* sp = M.s + ((shared ? 0 : (size_t)slot) * I + row) * G;
         const uint16_t* bp = M.b + ((shared ? 0 : (size_t)slot) * I + row) * G;
-        uint32_t mx = 0u, mxb = 0u;
-        for (int c = 0; c < G / 8; ++c) {
-            const uint4 sv = *reinterpret_cast<const uint4*>(sp + 8 * c), bv = *reinterpret_cast<const uint4*>(bp + 8 * c);
-            const uint32_t ws[4] = {sv.x, sv.y, sv.z, sv.w}, wb[4] = {bv.x, bv.y, bv.z, bv.w};
+        uint4 sv[kMaxG / 8], bv[kMaxG / 8];
+#pragma unroll
+        for (int c = 0; c < kMaxG / 8; ++c) {
+            sv[c] = c < G / 8 ? *reinterpret_cast<const uint4*>(sp + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+            bv[c] = c < G / 8 ? *reinterpret_cast<const uint4*>(bp + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        uint32_t mx = 0u, mxb = 0u;  // |scale|, |bias| as float bits: ordered as integers
+#pragma unroll
+        for (int c = 0; c < kMaxG / 8; ++c) {
+            const uint32_t ws[4] = {sv[c].x, sv[c].y, sv[c].z, sv[c].w}, wb[4] = {bv[c].x, bv[c].y, bv[c].z, bv[c].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 mx = max(mx, max((ws[e] << 16) & 0x7fff0000u, ws[e] & 0x7fff0000u));
@@ -597,9 +608,10 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_table(PfArgs a) {
         const int P = pf_row_pow2(mx, mxb);
         const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
         uint32_t* tp = a.tgu + (((size_t)slot * GP * 2 + mt) * I + row) * 2;
-        for (int c = 0; c < G / 8; ++c) {
-            const uint4 sv = *reinterpret_cast<const uint4*>(sp + 8 * c), bv = *reinterpret_cast<const uint4*>(bp + 8 * c);
-            const uint32_t ws[4] = {sv.x, sv.y, sv.z, sv.w}, wb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+        for (int c = 0; c < kMaxG / 8; ++c) {
+            if (c >= G / 8) break;
+            const uint32_t ws[4] = {sv[c].x, sv[c].y, sv[c].z, sv[c].w}, wb[4] = {bv[c].x, bv[c].y, bv[c].z, bv[c].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {  // groups 8c + 2e, 8c + 2e + 1: pair 4c + e
                 uint2 o;
@@ -609,29 +621,50 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_table(PfArgs a) {
             }
         }
         a.pgu[((size_t)slot * 2 + mt) * I + row] = ldexpf(1.0f, 24 - P);
-    } else if (r < 2 * I + H) {
-        const int h = r - 2 * I;
+    } else if (r < 2 * I + H / 4) {
+        const int h = 4 * (r - 2 * I);  // rows h .. h + 3
         const vmi_qmat Dm = shared ? a.sh_down : a.down;
         const size_t mb = (shared ? 0 : (size_t)slot) * Gd * H + h;
-        uint32_t mx = 0u, mxb = 0u;
+        uint32_t mx[4] = {0u, 0u, 0u, 0u}, mxb[4] = {0u, 0u, 0u, 0u};
         for (int g = 0; g < Gd; ++g) {
-            mx = max(mx, ((uint32_t)Dm.s[mb + (size_t)g * H] << 16) & 0x7fff0000u);
-            mxb = max(mxb, ((uint32_t)Dm.b[mb + (size_t)g * H] << 16) & 0x7fff0000u);
-        }
-        const int P = pf_row_pow2(mx, mxb);
-        const float ps = ldexpf(1.0f, P), pb = ldexpf(1.0f, P - 24);
-        for (int gp = 0; gp < GPd; ++gp) {
-            uint32_t o[2] = {0u, 0u};  // a missing second group (Gd odd) is zero: its values contribute nothing
+            const uint2 sv = *reinterpret_cast<const uint2*>(Dm.s + mb + (size_t)g * H);
+            const uint2 bv = *reinterpret_cast<const uint2*>(Dm.b + mb + (size_t)g * H);
+            const uint32_t ws[4] = {sv.x << 16, sv.x & 0xffff0000u, sv.y << 16, sv.y & 0xffff0000u};
+            const uint32_t wb[4] = {bv.x << 16, bv.x & 0xffff0000u, bv.y << 16, bv.y & 0xffff0000u};
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int g = 2 * gp + j;
-                if (g < Gd)
-                    o[j] = vmi_h2_bits((_Float16)(vmi_bf16_to_f32(Dm.s[mb + (size_t)g * H]) * ps),
-                                       (_Float16)(vmi_bf16_to_f32(Dm.b[mb + (size_t)g * H]) * pb));
+            for (int j = 0; j < 4; ++j) {
+                mx[j] = max(mx[j], ws[j] & 0x7fff0000u);
+                mxb[j] = max(mxb[j], wb[j] & 0x7fff0000u);
             }
-            *reinterpret_cast<uint2*>(a.tdn + (((size_t)slot * GPd + gp) * H + h) * 2) = make_uint2(o[0], o[1]);
         }
-        a.pdn[(size_t)slot * H + h] = ldexpf(1.0f, 24 - P);
+        float ps[4], pb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int P = pf_row_pow2(mx[j], mxb[j]);
+            ps[j] = ldexpf(1.0f, P);
+            pb[j] = ldexpf(1.0f, P - 24);
+            a.pdn[(size_t)slot * H + h + j] = ldexpf(1.0f, 24 - P);
+        }
+        for (int gp = 0; gp < GPd; ++gp) {
+            uint32_t o[2][4];  // [group of the pair][row]; a missing second group (Gd odd) is zero
+#pragma unroll
+            for (int g2 = 0; g2 < 2; ++g2) {
+                const int g = 2 * gp + g2;
+                uint2 sv = make_uint2(0u, 0u), bv = make_uint2(0u, 0u);
+                if (g < Gd) {
+                    sv = *reinterpret_cast<const uint2*>(Dm.s + mb + (size_t)g * H);
+                    bv = *reinterpret_cast<const uint2*>(Dm.b + mb + (size_t)g * H);
+                }
+                const uint32_t ws[4] = {sv.x << 16, sv.x & 0xffff0000u, sv.y << 16, sv.y & 0xffff0000u};
+                const uint32_t wb[4] = {bv.x << 16, bv.x & 0xffff0000u, bv.y << 16, bv.y & 0xffff0000u};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    o[g2][j] = vmi_h2_bits((_Float16)(__uint_as_float(ws[j]) * ps[j]), (_Float16)(__uint_as_float(wb[j]) * pb[j]));
+            }
+            uint4* tp = reinterpret_cast<uint4*>(a.tdn + (((size_t)slot * GPd + gp) * H + h) * 2);
+            tp[0] = make_uint4(o[0][0], o[1][0], o[0][1], o[1][1]);
+            tp[1] = make_uint4(o[0][2], o[1][2], o[0][3], o[1][3]);
+        }
     }
 }
 
@@ -966,13 +999,13 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     uint8_t* const s_ra = s_mem;
     uint8_t* const s_rb = s_mem + 2 * kPfA2;
     uint8_t* const s_rt = s_rb + 2 * kPfB2;
-    __shared__ __attribute__((aligned(16))) float s_post[512];  // 2^(24 - P)
+    __shared__ __attribute__((aligned(16))) float s_post[2 * 512];  // 2^(24 - P) of the column blocks' rows
     __shared__ int s_route[kTM3];
     __shared__ int s_exp[kTM3][kPfMaxIB];
     __shared__ float s_rf[kTM3];  // the route's combine weight times 2^E of its last block
     const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
     const int n = lane & 15, q = lane >> 4;
-    const int NB = a.H / 512;
+    const int NBL = pf_down_blocks(a.H), NB = a.H / (512 * NBL);
     int ti, nb;
     pf_tile_of(blockIdx.x, NB, ti, nb);
     if (ti >= a.ntiles[0]) return;
@@ -982,7 +1015,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     const int mcnt = __builtin_amdgcn_readfirstlane(max(0, min(8, (tl.z + 15) / 16)));
     VMI_STAMP(3, 0);
     const int H = a.H, I = a.I, IW = I / 8, G = I / 64, GP = (G + 1) / 2, IB = (I + 255) / 256;
-    const int h0 = nb * 512;
+    const int h0 = nb * 512 * NBL;
     const vmi_qmat Dm = tl.x >= 0 ? a.down : a.sh_down;
     const int slot = tl.x >= 0 ? tl.x : a.cap;  // table slot (cap: the shared expert)
     // the down projection is group-major: row h of group g of slot m at
@@ -1002,22 +1035,26 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
     // table DMA: the wave's 64 hidden rows in order, two words (the pair's
     // groups) each
     const uint32_t* tsrc = a.tdn + ((size_t)slot * GP * H + h0 + 64 * w) * 2 + lane;
-    auto issue_b = [&](int gp, int u) {
+    // pair v of the workgroup's sequence: column block v / GP, group pair v % GP
+    auto issue_b = [&](int v, int u) {
+        const int blk = v >= GP ? 1 : 0, gp = v - blk * GP;
         uint8_t* B = s_rb + u * kPfB2 + 4096 * w;
 #pragma unroll
         for (int g2 = 0; g2 < 2; ++g2) {
             // a missing second group (G odd) fetches the last again: its table pair is zero
             const int g = min(2 * gp + g2, G - 1);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) vmi_lds_dma16_opaque(bsrc[j] + (size_t)g * H * 8, B + 2048 * g2 + 1024 * j);
+            for (int j = 0; j < 2; ++j)
+                vmi_lds_dma16_opaque(bsrc[j] + ((size_t)g * H + 512 * blk) * 8, B + 2048 * g2 + 1024 * j);
         }
         uint8_t* Tt = s_rt + u * kPfT2 + 512 * w;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) vmi_lds_dma4_opaque(tsrc + (size_t)gp * 2 * H + 64 * j, Tt + 256 * j);
+        for (int j = 0; j < 2; ++j) vmi_lds_dma4_opaque(tsrc + ((size_t)gp * H + 512 * blk) * 2 + 64 * j, Tt + 256 * j);
     };
-    // the first two group pairs' weights are in flight while the prologue runs
+    // the first two pairs' weights are in flight while the prologue runs
+    const int NV = NBL * GP;
     issue_b(0, 0);
-    issue_b(GP > 1 ? 1 : 0, 1);
+    issue_b(NV > 1 ? 1 : 0, 1);
     if (tid < kTM3) {
         const int rt = tile_route(a, tl, tid);
         s_route[tid] = rt;
@@ -1034,6 +1071,7 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         s_rf[tid] = wgt * ldexpf(1.0f, el);
     }
     s_post[tid] = a.pdn[(size_t)slot * H + h0 + tid];
+    if (NBL == 2) s_post[512 + tid] = a.pdn[(size_t)slot * H + h0 + 512 + tid];
     __syncthreads();
     // operand DMA: pieces p = tid + 512 j (row p/16, position p%16 holding
     // logical piece pf_a2_piece(row, p%16) of the pair); a missing second
@@ -1048,7 +1086,8 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         apc[j] = pf_a2_piece(arow, p & 15);
         asrc[j] = a.actop + (size_t)(rt >= 0 ? rt : 0) * IW;
     }
-    auto issue_a = [&](int gp, int u) {
+    auto issue_a = [&](int v, int u) {
+        const int gp = v >= GP ? v - GP : v;
         uint8_t* A = s_ra + u * kPfA2;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -1101,24 +1140,62 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
                 for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_mfma_f16(wo[sb][1], a1, acc[m][sb]);
             }
         };
+        // column block blk's results: times 2^(24-P) of the row and the
+        // route's weight, one bf16 row piece per lane (lane (n, q): route row
+        // 16m + n, hidden rows 64w + 32t + 8q .. + 7 of the block), then the
+        // sums start again
+        auto store_block = [&](int blk) {
+            float4 post[2][2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                post[t][0] = *reinterpret_cast<const float4*>(&s_post[512 * blk + 64 * w + 32 * t + 8 * q]);
+                post[t][1] = *reinterpret_cast<const float4*>(&s_post[512 * blk + 64 * w + 32 * t + 8 * q + 4]);
+            }
+#pragma unroll
+            for (int m = 0; m < MC; ++m) {
+                const int route = s_route[16 * m + n];
+                if (route >= 0) {
+                    const float f = s_rf[16 * m + n];
+                    uint16_t* yrow = a.ybuf + (size_t)route * H + h0 + 512 * blk + 64 * w + 8 * q;
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const vmi_f4& lo = acc[m][2 * t];
+                        const vmi_f4& hi = acc[m][2 * t + 1];
+                        uint4 o;
+                        o.x = vmi_pack_bf16x2(lo[0] * post[t][0].x * f, lo[1] * post[t][0].y * f);
+                        o.y = vmi_pack_bf16x2(lo[2] * post[t][0].z * f, lo[3] * post[t][0].w * f);
+                        o.z = vmi_pack_bf16x2(hi[0] * post[t][1].x * f, hi[1] * post[t][1].y * f);
+                        o.w = vmi_pack_bf16x2(hi[2] * post[t][1].z * f, hi[3] * post[t][1].w * f);
+                        *reinterpret_cast<uint4*>(yrow + 32 * t) = o;
+                    }
+                }
+#pragma unroll
+                for (int sb = 0; sb < 4; ++sb) acc[m][sb] = vmi_f4{0.f, 0.f, 0.f, 0.f};
+            }
+        };
         vmi_u4 b0[4][2], b1[4][2];  // group 0 and group 1 of a pair
         if constexpr (MC > 0) {
             pf_wait_vmcnt<4>();  // this wave's weights of pair 0 (operands 0 may be in flight)
             dequant(b0, 0, 0);
         }
+        // a block's results are stored once every DMA issued so far has
+        // landed (vmcnt 0), so the next pair needs no wait: the stores then
+        // drain under its MFMAs instead of counting against its waits
+        bool landed = false;
 #pragma unroll 1
-        for (int gp = 0; gp < GP; ++gp) {
-            const int u = gp & 1;
-            if (gp == 0)
+        for (int v = 0; v < NV; ++v) {
+            const int u = v & 1;
+            const int blk = v >= GP ? 1 : 0, gp = v - blk * GP;
+            if (v == 0)
                 pf_wait_vmcnt<0>();
-            else
+            else if (!landed)
                 pf_wait_vmcnt<6>();
-            __syncthreads();  // everyone's operands gp; operand slot u ^ 1 is free
-            issue_a(min(gp + 1, GP - 1), u ^ 1);
+            __syncthreads();  // everyone's operands v; operand slot u ^ 1 is free
+            issue_a(min(v + 1, NV - 1), u ^ 1);
             if constexpr (MC > 0) {
                 if (gp > 0 && (gp & 1) == 0) {
-                    // a new 256-column block (two pairs): the sums so far
-                    // times 2^(E_prev - E)
+                    // a new 256-column block of K (two pairs): the sums so
+                    // far times 2^(E_prev - E)
                     const int b = gp >> 1;
 #pragma unroll
                     for (int m = 0; m < MC; ++m) {
@@ -1134,11 +1211,17 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
                 mfma_group(s_ra + u * kPfA2, 0, b0);
             }
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): weight slot u is read
-            issue_b(min(gp + 2, GP - 1), u);
+            issue_b(min(v + 2, NV - 1), u);
             if constexpr (MC > 0) {
-                pf_wait_vmcnt<10>();  // this wave's weights of pair gp + 1
+                if (!landed) pf_wait_vmcnt<10>();  // this wave's weights of pair v + 1
                 dequant(b0, u ^ 1, 0);  // past the last pair: stale values, unused
                 mfma_group(s_ra + u * kPfA2, 1, b1);
+            }
+            landed = false;
+            if (gp == GP - 1) {
+                pf_wait_vmcnt<0>();
+                if constexpr (MC > 0) store_block(blk);
+                landed = true;
             }
         }
     };
@@ -1153,35 +1236,8 @@ __global__ __launch_bounds__(kPf8Threads, 1) void k_pf_down3(PfArgs a) {
         case 1: stage_loop(std::integral_constant<int, 1>{}); break;
         default: stage_loop(std::integral_constant<int, 0>{}); break;
     }
-    pf_wait_vmcnt<0>();
     VMI_STAMP(3, 2);
     VMI_STAMP(3, 3);
-    // lane (n, q): route row 16m + n, hidden rows h0 + 64w + 32t + 8q .. + 7
-    // (column blocks 2t and 2t + 1)
-    float4 post[2][2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        post[t][0] = *reinterpret_cast<const float4*>(&s_post[64 * w + 32 * t + 8 * q]);
-        post[t][1] = *reinterpret_cast<const float4*>(&s_post[64 * w + 32 * t + 8 * q + 4]);
-    }
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const int route = s_route[16 * m + n];
-        if (route < 0) continue;
-        const float f = s_rf[16 * m + n];
-        uint16_t* yrow = a.ybuf + (size_t)route * a.H + h0 + 64 * w + 8 * q;
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const vmi_f4& lo = acc[m][2 * t];
-            const vmi_f4& hi = acc[m][2 * t + 1];
-            uint4 o;
-            o.x = vmi_pack_bf16x2(lo[0] * post[t][0].x * f, lo[1] * post[t][0].y * f);
-            o.y = vmi_pack_bf16x2(lo[2] * post[t][0].z * f, lo[3] * post[t][0].w * f);
-            o.z = vmi_pack_bf16x2(hi[0] * post[t][1].x * f, hi[1] * post[t][1].y * f);
-            o.w = vmi_pack_bf16x2(hi[2] * post[t][1].z * f, hi[3] * post[t][1].w * f);
-            *reinterpret_cast<uint4*>(yrow + 32 * t) = o;
-        }
-    }
     VMI_STAMP(3, 4);
 }
 
@@ -1591,11 +1647,12 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     hipLaunchKernelGGL(k_pf_count, dim3((T * D.top_k + kCountRoutes - 1) / kCountRoutes), dim3(kPfThreads), 0, s, a);
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
-    hipLaunchKernelGGL(k_pf_table, dim3((D.cap + 1) * ((2 * D.inter + D.hidden + kPfThreads - 1) / kPfThreads)),
+    hipLaunchKernelGGL(k_pf_table, dim3((D.cap + 1) * pf_table_blocks(D.hidden, D.inter)),
                        dim3(kPfThreads), 0, s, a);
     const int tile_slots = 8 * ((L.max_tiles + 7) / 8);
     hipLaunchKernelGGL(k_pf_gateup3, dim3(tile_slots * ((D.inter + 255) / 256)), dim3(kPf8Threads), 0, s, a);
-    hipLaunchKernelGGL(k_pf_down3, dim3(tile_slots * (D.hidden / 512)), dim3(kPf8Threads), 0, s, a);
+    hipLaunchKernelGGL(k_pf_down3, dim3(tile_slots * (D.hidden / (512 * pf_down_blocks(D.hidden)))), dim3(kPf8Threads),
+                       0, s, a);
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(kPfThreads), 0, s, a);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill launch");
