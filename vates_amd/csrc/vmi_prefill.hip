@@ -9,11 +9,10 @@
 //
 //   k_pf_prep     per token: optional RMSNorm, MFMA operands of x (fp16, range
 //                 factor per token), per-group operand sums for the router's
-//                 affine term; clears counters
+//                 affine term, the shared-expert gate logit; clears counters
 //   k_pf_router3  router logits [T, E] as a tiled MFMA GEMM on the 4/8-bit
 //                 router (weights enter the MFMA as exact fp16 subnormals),
 //                 in two halves of K that the top-k adds
-//   k_pf_sgate    shared-expert gate logit per token (one wave per token)
 //   k_pf_topk     one wave per token: top-k, softmax, renorm, slot table
 //   k_pf_count    routes per slot and each route's rank in its slot
 //   k_pf_scan     exclusive scan of the counts, the list of 128-row M tiles
@@ -158,8 +157,57 @@ __device__ __forceinline__ void bf16x8(const uint4& q, float (&v)[8]) {
     }
 }
 
+// Shared-expert gate logit of one token by its wave (lane l: the same
+// columns as its operand words u), on the effective fp16 operands (x * f) and
+// the dequantised gate row, in a fixed order, canonical wave sum; the caller
+// divides by f.
+template <int NCH>
+__device__ __forceinline__ float pf_sgate_dot(const vmi_u4 (&u)[NCH], const PfArgs& a) {
+    const int lane = threadIdx.x & 63;
+    const int bits = a.sg_bits;
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        // op4 slot s holds column {0,4,1,5,2,6,3,7}[s]; odd columns carry /16
+        float xv[8];
+        const _Float16 h[8] = {
+            __builtin_bit_cast(_Float16, (uint16_t)(u[c][0] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[c][0] >> 16)),
+            __builtin_bit_cast(_Float16, (uint16_t)(u[c][1] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[c][1] >> 16)),
+            __builtin_bit_cast(_Float16, (uint16_t)(u[c][2] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[c][2] >> 16)),
+            __builtin_bit_cast(_Float16, (uint16_t)(u[c][3] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[c][3] >> 16))};
+        xv[0] = (float)h[0];
+        xv[4] = (float)h[1];
+        xv[1] = 16.0f * (float)h[2];
+        xv[5] = 16.0f * (float)h[3];
+        xv[2] = (float)h[4];
+        xv[6] = (float)h[5];
+        xv[3] = 16.0f * (float)h[6];
+        xv[7] = 16.0f * (float)h[7];
+        const int c0 = 8 * (lane * NCH + c);  // first column of this word
+        const int gi = c0 >> 6;
+        const float sc = vmi_bf16_to_f32(a.sgate.s[gi]), bi = vmi_bf16_to_f32(a.sgate.b[gi]);
+        uint32_t qv[8];
+        if (bits == 4) {
+            const uint32_t wd = a.sgate.w[c0 >> 3];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qv[i] = (wd >> (4 * i)) & 0xFu;
+        } else {
+            const uint32_t w0 = a.sgate.w[c0 >> 2], w1 = a.sgate.w[(c0 >> 2) + 1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                qv[i] = (w0 >> (8 * i)) & 0xFFu;
+                qv[4 + i] = (w1 >> (8 * i)) & 0xFFu;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = fmaf(xv[i], fmaf((float)qv[i], sc, bi), acc);
+    }
+    return vmi_wave_sum_canon(acc);
+}
+
 // One wave per token; lane l owns columns [l*H/64, (l+1)*H/64) (H/512 chunks
-// of 8).  RMSNorm (canonical order) when norm_w, range factor, operands.
+// of 8).  RMSNorm (canonical order) when norm_w, range factor, operands, and
+// the shared-expert gate logit from those operands.
 template <int NCH>
 __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
     const int lane = threadIdx.x & 63;
@@ -206,13 +254,16 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
     constexpr int LPG = 8 / NCH;
     float s4 = 0.0f, s8 = 0.0f;
     const size_t orow = (size_t)t * (a.H / 8) + lane * NCH;
+    vmi_u4 u[NCH];
     if (a.xsum4) {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) a.xop4[orow + c] = op4<true>(v[c], f, s4);
+        for (int c = 0; c < NCH; ++c) u[c] = op4<true>(v[c], f, s4);
     } else {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) a.xop4[orow + c] = op4<false>(v[c], f, s4);
+        for (int c = 0; c < NCH; ++c) u[c] = op4<false>(v[c], f, s4);
     }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) a.xop4[orow + c] = u[c];
     if (a.xop8) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) a.xop8[orow + c] = op8(v[c], f, s8);
@@ -229,6 +280,10 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
         if (a.xsum8) a.xsum8[g] = s8;
     }
     if (lane == 0) a.fscale[t] = f;
+    if (a.has_sgate) {
+        const float sg = pf_sgate_dot<NCH>(u, a);
+        if (lane == 0) a.sglogit[t] = sg / f;
+    }
 }
 
 // ------------------------------------------------------- grouped GEMM core
@@ -237,58 +292,6 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
 // exact subnormals, then acc += D * scale * 2^24 (+ the affine-bias term).
 // Lane l: A row m = l%16 (rows of the tile), K block q = l/16; B column
 // n = l%16; D rows 4q + r, column n.
-
-// Shared-expert gate logit: one wave per token, lane-contiguous columns in a
-// fixed order, on the effective fp16 operands (x * f) and the dequantised
-// gate row, canonical wave sum, divided by f.
-template <int NCH>
-__global__ __launch_bounds__(kPfThreads) void k_pf_sgate(PfArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * (kPfThreads / 64) + pf_wave();
-    if (t >= a.T) return;
-    const int bits = a.sg_bits;
-    const vmi_u4* xo = a.xop4 + (size_t)t * (a.H / 8) + lane * NCH;
-    float acc = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const vmi_u4 u = xo[c];
-        // op4 slot s holds column {0,4,1,5,2,6,3,7}[s]; odd columns carry /16
-        float xv[8];
-        const _Float16 h[8] = {
-            __builtin_bit_cast(_Float16, (uint16_t)(u[0] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[0] >> 16)),
-            __builtin_bit_cast(_Float16, (uint16_t)(u[1] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[1] >> 16)),
-            __builtin_bit_cast(_Float16, (uint16_t)(u[2] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[2] >> 16)),
-            __builtin_bit_cast(_Float16, (uint16_t)(u[3] & 0xffffu)), __builtin_bit_cast(_Float16, (uint16_t)(u[3] >> 16))};
-        xv[0] = (float)h[0];
-        xv[4] = (float)h[1];
-        xv[1] = 16.0f * (float)h[2];
-        xv[5] = 16.0f * (float)h[3];
-        xv[2] = (float)h[4];
-        xv[6] = (float)h[5];
-        xv[3] = 16.0f * (float)h[6];
-        xv[7] = 16.0f * (float)h[7];
-        const int c0 = 8 * (lane * NCH + c);  // first column of this word
-        const int gi = c0 >> 6;
-        const float sc = vmi_bf16_to_f32(a.sgate.s[gi]), bi = vmi_bf16_to_f32(a.sgate.b[gi]);
-        uint32_t qv[8];
-        if (bits == 4) {
-            const uint32_t wd = a.sgate.w[c0 >> 3];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qv[i] = (wd >> (4 * i)) & 0xFu;
-        } else {
-            const uint32_t w0 = a.sgate.w[c0 >> 2], w1 = a.sgate.w[(c0 >> 2) + 1];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                qv[i] = (w0 >> (8 * i)) & 0xFFu;
-                qv[4 + i] = (w1 >> (8 * i)) & 0xFFu;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(xv[i], fmaf((float)qv[i], sc, bi), acc);
-    }
-    acc = vmi_wave_sum_canon(acc);
-    if (lane == 0) a.sglogit[t] = acc / a.fscale[t];
-}
 
 // ------------------------------------------------------------------ top-k
 __device__ __forceinline__ uint64_t pf_rank_key(float f, int e) {
@@ -1624,13 +1627,6 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
         hipLaunchKernelGGL(k_pf_router3<4>, rgrid, dim3(kPfThreads), 0, s, a);
     else
         hipLaunchKernelGGL(k_pf_router3<8>, rgrid, dim3(kPfThreads), 0, s, a);
-    if (has_sgate) {
-        switch (D.hidden / 512) {
-            case 1: hipLaunchKernelGGL(k_pf_sgate<1>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
-            case 2: hipLaunchKernelGGL(k_pf_sgate<2>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
-            default: hipLaunchKernelGGL(k_pf_sgate<4>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a); break;
-        }
-    }
     {
         const int ni = D.num_experts / 64;  // key slots per lane, padded to a power of two
         if (ni <= 1)
