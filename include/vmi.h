@@ -138,6 +138,7 @@ typedef struct vmi_moe_layer_desc {
     int shared_expert_gate_bits;  /* 4 or 8 */
     const uint16_t* norm_weight;  /* [hidden] bf16 RMSNorm weight, or NULL: no norm */
     float norm_eps;
+    const void* prefill_tables;   /* vmi_moe_prefill_tables() of these pools, or NULL (vmi_moe_prefill only) */
 } vmi_moe_layer_desc;
 /* Pool layouts of vmi_moe_layer / vmi_moe_prefill (the packed values, scales
  * and biases are the reference's; only their order in memory differs, and
@@ -196,6 +197,22 @@ size_t vmi_moe_prefill_workspace_bytes(int T, int top_k, int hidden, int inter, 
 int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x, int T, const uint16_t* residual,
                     uint16_t* out, int32_t* ids_out, float* scores_out, void* workspace, size_t workspace_bytes,
                     void* stream);
+
+/* ------------------------------------------------------------------------
+ * vmi_moe_prefill_tables -- the fp16 dequantisation tables vmi_moe_prefill's
+ * expert GEMMs read, for every pool slot and the shared expert, built once
+ * from the pools' scales and biases.  No counterpart in the reference: a
+ * derived form of the pools, as their MFMA-major order is.  With
+ * desc->prefill_tables pointing at them, vmi_moe_prefill no longer builds the
+ * touched experts' tables in its workspace on every call.  They follow the
+ * pools' contents: a caller that rewrites pool slots builds them again.
+ * Per weight row: P, the row's power of two (bounded by its largest scale and
+ * bias), 2^(24-P) as f32, and per quantisation group the fp16 pair
+ * (scale 2^P, bias 2^(P-24)).  tables: vmi_moe_prefill_tables_bytes(hidden,
+ * inter, cap) bytes, 16-byte aligned; desc as vmi_moe_prefill.
+ * ------------------------------------------------------------------------ */
+size_t vmi_moe_prefill_tables_bytes(int hidden, int inter, int cap);
+int vmi_moe_prefill_tables(const vmi_moe_layer_desc* desc, void* tables, size_t bytes, void* stream);
 
 /* Reads and clears the device status word of a workspace (synchronises the
  * stream).  *flags receives VMI_STATUS_* bits. */

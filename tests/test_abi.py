@@ -58,6 +58,15 @@ def test_invalid_arguments_rejected_before_any_device_call(lib):
     assert rc == L.VMI_ERR_UNSUPPORTED
     rc = lib.vmi_moe_layer(None, None, 4, None, None, None, None, None, 0, None)
     assert rc == L.VMI_ERR_INVALID
+    # the prefill tables: two fp16 halves per (row, group) of gate, up and down
+    # for every slot and the shared expert, plus a factor per row
+    assert lib.vmi_moe_prefill_tables_bytes(2048, 512, 512) >= 513 * (2 * 512 * 32 + 2048 * 8) * 4
+    assert lib.vmi_moe_prefill_tables_bytes(2048, 100, 512) == 0
+    assert lib.vmi_moe_prefill_tables(None, None, 0, None) == L.VMI_ERR_INVALID
+    d = L.MoeLayerDesc()
+    d.hidden, d.inter, d.cap, d.bits, d.group = 2048, 512, 512, 4, 64
+    rc = lib.vmi_moe_prefill_tables(ctypes.byref(d), None, 0, None)
+    assert rc == L.VMI_ERR_INVALID and b"scales" in lib.vmi_last_error()
     rc = lib.vmi_spec_commit(None, None, 4, 1, 2048, 0, None, None, None, None, None, None, None)
     assert rc == L.VMI_ERR_INVALID and b"K=0" in lib.vmi_last_error()
     rc = lib.vmi_spec_commit(None, None, 0, 1, 2048, 3, None, None, None, None, None, None, None)

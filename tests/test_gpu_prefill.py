@@ -89,10 +89,11 @@ def test_prefill_parity_small(gpu, orc, T, router_bits):
 @pytest.mark.parametrize("H,I,E,k,T", [(1024, 320, 64, 4, 150), (512, 768, 64, 6, 90)])
 def test_prefill_parity_odd_shapes(gpu, orc, H, I, E, k, T):
     """Intermediate sizes that are not a multiple of 256 and above 512: I=320
-    has an odd count of down quantisation groups (5) and a last column block
-    of 64 rows; I=768 takes the down kernel's large-table form (12 groups,
-    three 256-column blocks, so two exponent rescales); H=1024 runs the
-    16-group prep, gate/up and router forms."""
+    has an odd count of down quantisation groups (5: the last group pair is
+    half empty) and a last column block of 64 rows; I=768 has 12 groups in
+    three 256-column blocks, so two exponent rescales; H=1024 runs the
+    16-group prep, gate/up and router forms and two down column blocks per
+    workgroup, H=512 one."""
     log(f"case: prefill H={H} I={I} E={E} k={k} T={T}")
     w, moe, x, out, ids, sc = _case(gpu, orc, T, H=H, I=I, E=E, k=k)
     _check_against_oracle(orc, w, x, out, ids, sc, k, True, f"H={H} I={I} T={T}")
@@ -129,6 +130,21 @@ def test_prefill_degenerate_rows(gpu, orc):
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
     _check_against_oracle(orc, w, x, out, ids, sc, k, True, "degenerate rows")
+
+
+@pytest.mark.parametrize("H,I,E,k,T", [(1024, 320, 64, 4, 150), (2048, 512, 512, 10, 192)])
+def test_prefill_layer_tables_match_per_call_tables(gpu, orc, H, I, E, k, T):
+    """The layer's dequantisation tables, built once for every pool slot and
+    the shared expert (vmi_moe_prefill_tables), give the same bits as the
+    tables a call builds in its workspace for the experts it touches."""
+    import torch
+    log(f"case: prefill layer tables vs per-call tables H={H} I={I} E={E} k={k} T={T}")
+    w, moe, x, out, ids, sc = _case(gpu, orc, T, H=H, I=I, E=E, k=k)
+    assert moe.desc.prefill_tables, "the first prefill call builds the layer's tables"
+    out2 = moe.prefill(x, residual=x, use_tables=False)
+    torch.cuda.synchronize()
+    assert moe.desc.prefill_tables
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
 def test_prefill_parity_full_shape(gpu, orc):

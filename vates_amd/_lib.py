@@ -59,7 +59,7 @@ class MoeLayerDesc(ctypes.Structure):
         ("gate", QMat), ("up", QMat), ("down", QMat),
         ("shared_gate", QMat), ("shared_up", QMat), ("shared_down", QMat),
         ("shared_expert_gate", QMat), ("shared_expert_gate_bits", c_int),
-        ("norm_weight", c_void_p), ("norm_eps", c_float),
+        ("norm_weight", c_void_p), ("norm_eps", c_float), ("prefill_tables", c_void_p),
     ]
 
 
@@ -80,6 +80,8 @@ _SIGNATURES = {
     "vmi_moe_prefill_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "vmi_moe_prefill": (c_int, [POINTER(MoeLayerDesc), c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_void_p, c_size_t, c_void_p]),
+    "vmi_moe_prefill_tables_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "vmi_moe_prefill_tables": (c_int, [POINTER(MoeLayerDesc), c_void_p, c_size_t, c_void_p]),
     "vmi_workspace_status": (c_int, [c_void_p, c_void_p, POINTER(c_uint32)]),
     "vmi_dequant_affine": (c_int, [QMat, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
     "vmi_synth_quantized": (c_int, [c_uint64, c_uint32, c_int64, c_int, c_int, c_int, c_float, c_void_p, c_void_p,

@@ -586,7 +586,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_table(PfArgs a) {
     const int bps = pf_table_blocks(H, I);
     const int slot = blockIdx.x / bps, r = (blockIdx.x - slot * bps) * kPfThreads + threadIdx.x;
     const bool shared = slot == a.cap;
-    if (shared ? !a.has_shared : a.counts[slot] == 0) return;
+    if (shared ? !a.has_shared : (a.counts && a.counts[slot] == 0)) return;  // counts null: every slot
     if (r < 2 * I) {
         const int mt = r >= I, row = r - mt * I;
         const vmi_qmat M = mt ? (shared ? a.sh_up : a.up) : (shared ? a.sh_gate : a.gate);
@@ -1484,6 +1484,29 @@ struct PfLayout {
     int max_tiles;
 };
 
+// The dequantisation tables (k_pf_table), in the workspace or in a caller's
+// buffer (vmi_moe_prefill_tables): gate/up pairs, gate/up factors, down pairs,
+// down factors, each 256-byte aligned.
+struct PfTables {
+    size_t tgu, pgu, tdn, pdn, bytes;
+};
+
+PfTables pf_tables_layout(int H, int I, int cap) {
+    PfTables L{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += vmi::align256(bytes);
+        return o;
+    };
+    L.tgu = take((size_t)(cap + 1) * (H / 128) * 2 * I * 2 * 4);
+    L.pgu = take((size_t)(cap + 1) * 2 * I * 4);
+    L.tdn = take((size_t)(cap + 1) * ((I / 64 + 1) / 2) * H * 2 * 4);
+    L.pdn = take((size_t)(cap + 1) * H * 4);
+    L.bytes = off;
+    return L;
+}
+
 PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) {
     PfLayout L{};
     size_t off = 0;
@@ -1511,10 +1534,12 @@ PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) 
     L.tiles = take((size_t)L.max_tiles * 16);
     L.ntiles = take(4);
     L.list = take((size_t)T * k * 4);
-    L.tgu = take((size_t)(cap + 1) * (H / 128) * 2 * I * 2 * 4);
-    L.pgu = take((size_t)(cap + 1) * 2 * I * 4);
-    L.tdn = take((size_t)(cap + 1) * ((I / 64 + 1) / 2) * H * 2 * 4);
-    L.pdn = take((size_t)(cap + 1) * H * 4);
+    const PfTables TB = pf_tables_layout(H, I, cap);
+    const size_t tb = take(TB.bytes);
+    L.tgu = tb + TB.tgu;
+    L.pgu = tb + TB.pgu;
+    L.tdn = tb + TB.tdn;
+    L.pdn = tb + TB.pdn;
     L.actop = take(R * (I / 8) * 16);
     L.aexp = take(R * ((I + 255) / 256) * 4);
     L.ybuf = take(R * H * 2);
@@ -1572,6 +1597,8 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
                   reinterpret_cast<uintptr_t>(D.shared_down.s) | reinterpret_cast<uintptr_t>(D.shared_down.b);
         if (sb & 15) return vmi::fail(VMI_ERR_INVALID, "scales and biases must be 16-byte aligned");
     }
+    if (reinterpret_cast<uintptr_t>(D.prefill_tables) & 15)
+        return vmi::fail(VMI_ERR_INVALID, "prefill tables must be 16-byte aligned");
     const PfLayout L = pf_layout(T, D.top_k, D.hidden, D.inter, D.num_experts, D.cap, D.router_bits);
     if (!workspace || workspace_bytes < L.bytes)
         return vmi::fail(VMI_ERR_WORKSPACE, "workspace needs %zu bytes (got %zu)", L.bytes, workspace_bytes);
@@ -1604,10 +1631,19 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     a.tiles = reinterpret_cast<int4*>(ws + L.tiles);
     a.ntiles = reinterpret_cast<int32_t*>(ws + L.ntiles);
     a.list = reinterpret_cast<int32_t*>(ws + L.list);
-    a.tgu = reinterpret_cast<uint32_t*>(ws + L.tgu);
-    a.pgu = reinterpret_cast<float*>(ws + L.pgu);
-    a.tdn = reinterpret_cast<uint32_t*>(ws + L.tdn);
-    a.pdn = reinterpret_cast<float*>(ws + L.pdn);
+    if (D.prefill_tables) {
+        const PfTables TB = pf_tables_layout(D.hidden, D.inter, D.cap);
+        uint8_t* tb = static_cast<uint8_t*>(const_cast<void*>(D.prefill_tables));
+        a.tgu = reinterpret_cast<uint32_t*>(tb + TB.tgu);
+        a.pgu = reinterpret_cast<float*>(tb + TB.pgu);
+        a.tdn = reinterpret_cast<uint32_t*>(tb + TB.tdn);
+        a.pdn = reinterpret_cast<float*>(tb + TB.pdn);
+    } else {
+        a.tgu = reinterpret_cast<uint32_t*>(ws + L.tgu);
+        a.pgu = reinterpret_cast<float*>(ws + L.pgu);
+        a.tdn = reinterpret_cast<uint32_t*>(ws + L.tdn);
+        a.pdn = reinterpret_cast<float*>(ws + L.pdn);
+    }
     a.actop = reinterpret_cast<vmi_u4*>(ws + L.actop);
     a.aexp = reinterpret_cast<int32_t*>(ws + L.aexp);
     a.ybuf = reinterpret_cast<uint16_t*>(ws + L.ybuf);
@@ -1643,8 +1679,9 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     hipLaunchKernelGGL(k_pf_count, dim3((T * D.top_k + kCountRoutes - 1) / kCountRoutes), dim3(kPfThreads), 0, s, a);
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
-    hipLaunchKernelGGL(k_pf_table, dim3((D.cap + 1) * pf_table_blocks(D.hidden, D.inter)),
-                       dim3(kPfThreads), 0, s, a);
+    if (!D.prefill_tables)
+        hipLaunchKernelGGL(k_pf_table, dim3((D.cap + 1) * pf_table_blocks(D.hidden, D.inter)), dim3(kPfThreads), 0, s,
+                           a);
     const int tile_slots = 8 * ((L.max_tiles + 7) / 8);
     hipLaunchKernelGGL(k_pf_gateup3, dim3(tile_slots * ((D.inter + 255) / 256)), dim3(kPf8Threads), 0, s, a);
     hipLaunchKernelGGL(k_pf_down3, dim3(tile_slots * (D.hidden / (512 * pf_down_blocks(D.hidden)))), dim3(kPf8Threads),
@@ -1652,6 +1689,57 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(kPfThreads), 0, s, a);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill launch");
+}
+
+extern "C" size_t vmi_moe_prefill_tables_bytes(int hidden, int inter, int cap) {
+    if (hidden <= 0 || hidden % 512 || inter <= 0 || inter % 64 || cap <= 0) return 0;
+    return pf_tables_layout(hidden, inter, cap).bytes;
+}
+
+extern "C" int vmi_moe_prefill_tables(const vmi_moe_layer_desc* desc, void* tables, size_t bytes, void* stream) {
+    vmi::clear_error();
+    if (!desc) return vmi::fail(VMI_ERR_INVALID, "null desc");
+    const vmi_moe_layer_desc& D = *desc;
+    if (D.bits != 4 || D.group != 64) return vmi::fail(VMI_ERR_UNSUPPORTED, "bits=%d group=%d", D.bits, D.group);
+    if (D.hidden != 512 && D.hidden != 1024 && D.hidden != 2048)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "hidden=%d must be 512, 1024 or 2048", D.hidden);
+    if (D.inter % 64 || D.inter <= 0 || D.inter > 2048)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "inter=%d must be a multiple of 64 up to 2048", D.inter);
+    if (D.cap <= 0 || D.cap > 1024) return vmi::fail(VMI_ERR_UNSUPPORTED, "cap=%d must be in [1, 1024]", D.cap);
+    const bool has_shared = D.shared_gate.w != nullptr;
+    if (!D.gate.s || !D.gate.b || !D.up.s || !D.up.b || !D.down.s || !D.down.b)
+        return vmi::fail(VMI_ERR_INVALID, "null scales or biases");
+    if (has_shared && (!D.shared_gate.s || !D.shared_gate.b || !D.shared_up.s || !D.shared_up.b ||
+                       !D.shared_down.s || !D.shared_down.b))
+        return vmi::fail(VMI_ERR_INVALID, "null shared-expert scales or biases");
+    uintptr_t sb = reinterpret_cast<uintptr_t>(D.gate.s) | reinterpret_cast<uintptr_t>(D.gate.b) |
+                   reinterpret_cast<uintptr_t>(D.up.s) | reinterpret_cast<uintptr_t>(D.up.b) |
+                   reinterpret_cast<uintptr_t>(D.down.s) | reinterpret_cast<uintptr_t>(D.down.b);
+    if (has_shared)
+        sb |= reinterpret_cast<uintptr_t>(D.shared_gate.s) | reinterpret_cast<uintptr_t>(D.shared_gate.b) |
+              reinterpret_cast<uintptr_t>(D.shared_up.s) | reinterpret_cast<uintptr_t>(D.shared_up.b) |
+              reinterpret_cast<uintptr_t>(D.shared_down.s) | reinterpret_cast<uintptr_t>(D.shared_down.b);
+    if (sb & 15) return vmi::fail(VMI_ERR_INVALID, "scales and biases must be 16-byte aligned");
+    const PfTables TB = pf_tables_layout(D.hidden, D.inter, D.cap);
+    if (!tables || bytes < TB.bytes)
+        return vmi::fail(VMI_ERR_WORKSPACE, "tables need %zu bytes (got %zu)", TB.bytes, bytes);
+    if (reinterpret_cast<uintptr_t>(tables) & 15) return vmi::fail(VMI_ERR_INVALID, "tables must be 16-byte aligned");
+    uint8_t* tb = static_cast<uint8_t*>(tables);
+    PfArgs a{};
+    a.H = D.hidden; a.I = D.inter; a.cap = D.cap; a.has_shared = has_shared;
+    a.gate = D.gate; a.up = D.up; a.down = D.down;
+    a.sh_gate = has_shared ? D.shared_gate : D.gate;
+    a.sh_up = has_shared ? D.shared_up : D.up;
+    a.sh_down = has_shared ? D.shared_down : D.down;
+    a.counts = nullptr;  // every slot
+    a.tgu = reinterpret_cast<uint32_t*>(tb + TB.tgu);
+    a.pgu = reinterpret_cast<float*>(tb + TB.pgu);
+    a.tdn = reinterpret_cast<uint32_t*>(tb + TB.tdn);
+    a.pdn = reinterpret_cast<float*>(tb + TB.pdn);
+    hipLaunchKernelGGL(k_pf_table, dim3((D.cap + 1) * pf_table_blocks(D.hidden, D.inter)), dim3(kPfThreads), 0,
+                       static_cast<hipStream_t>(stream), a);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? VMI_OK : vmi::hip_fail(e, "prefill tables launch");
 }
 
 #ifdef VMI_TIMELINE

@@ -292,6 +292,27 @@ class MoELayer:
         d.norm_eps = norm_eps
         self.desc = d
         self.group, self.bits = group, bits
+        self._pf_tables: Optional[torch.Tensor] = None
+
+    def prefill_tables(self, stream=None) -> torch.Tensor:
+        """The fp16 dequantisation tables of the prefill's expert GEMMs for
+        every pool slot (vmi_moe_prefill_tables), built on first use and kept
+        with the layer: prefill() then reads them instead of building the
+        touched experts' tables on every call.  The first call synchronises
+        its stream, so it must not run under graph capture (call this method
+        before capturing a prefill)."""
+        if self._pf_tables is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise VmiError("the prefill tables are built outside graph capture: call prefill_tables() first")
+            lib = load()
+            n = lib.vmi_moe_prefill_tables_bytes(self.hidden, self.inter, self.cap)
+            t = torch.empty(n, dtype=torch.uint8, device=self.device)
+            sh = _stream_handle(stream)
+            check(lib.vmi_moe_prefill_tables(ctypes.byref(self.desc), t.data_ptr(), n, sh), "vmi_moe_prefill_tables")
+            (stream if stream is not None else torch.cuda.current_stream()).synchronize()
+            self._pf_tables = t
+            self.desc.prefill_tables = t.data_ptr()
+        return self._pf_tables
 
     def reference_weights(self) -> dict:
         """The layer's weights in the reference's layouts (new tensors for the
@@ -319,8 +340,10 @@ class MoELayer:
     def prefill(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None, *,
                 out: Optional[torch.Tensor] = None, ids_out: Optional[torch.Tensor] = None,
                 scores_out: Optional[torch.Tensor] = None, stream=None,
-                ws: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """The layer on a long prompt, expert-major (block.py:111-243): x bf16 [T, hidden]."""
+                ws: Optional[torch.Tensor] = None, use_tables: bool = True) -> torch.Tensor:
+        """The layer on a long prompt, expert-major (block.py:111-243): x bf16 [T, hidden].
+        use_tables=False builds the touched experts' dequantisation tables in
+        the workspace for this call instead of reading the layer's own."""
         lib = load()
         if x.dtype != torch.bfloat16 or x.shape[-1] != self.hidden:
             raise VmiError("x must be bf16 [..., hidden]")
@@ -342,10 +365,18 @@ class MoELayer:
                     raise VmiError(f"{name} must be {dt} [T, top_k]")
                 _require(t, name, 4, self.device)
         sh = _stream_handle(stream)
+        if use_tables:
+            self.prefill_tables(stream)
         if ws is None:
             ws = workspace(self.prefill_workspace_bytes(T), self.device, sh, tag="prefill")
-        rc = lib.vmi_moe_prefill(ctypes.byref(self.desc), x.data_ptr(), T, _ptr(residual), out.data_ptr(),
-                                 _ptr(ids_out), _ptr(scores_out), ws.data_ptr(), ws.numel(), sh)
+        saved = self.desc.prefill_tables
+        if not use_tables:
+            self.desc.prefill_tables = None
+        try:
+            rc = lib.vmi_moe_prefill(ctypes.byref(self.desc), x.data_ptr(), T, _ptr(residual), out.data_ptr(),
+                                     _ptr(ids_out), _ptr(scores_out), ws.data_ptr(), ws.numel(), sh)
+        finally:
+            self.desc.prefill_tables = saved
         check(rc, "vmi_moe_prefill")
         return out
 
