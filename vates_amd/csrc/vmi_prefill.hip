@@ -70,9 +70,7 @@ struct PfArgs {
     vmi_qmat sh_gate, sh_up, sh_down, sgate;
     // workspace
     vmi_u4* xop4;               // [T, H/8] fp16 operands, 4-bit slot order
-    float* xsum4;               // [T, H/64] (4-bit router only, else null)
-    vmi_u4* xop8;               // [T, H/8] fp16 operands, 8-bit slot order (8-bit router)
-    float* xsum8;               // [T, H/64]
+    float* xsum4;               // [T, H/64] per group, the sum of what the router MFMAs multiply
     float* fscale;              // [T]
     float* logits;              // [2, T, E]: the router's two halves of K
     float* sglogit;             // [T]
@@ -119,32 +117,19 @@ __device__ __forceinline__ vmi_u4 op4(const float (&v)[8], float f, float& s) {
     return r;
 }
 
-// fp16 operand of 8 columns for 8-bit words (two words of 4 columns):
-// slots {0,2,1,3,4,6,5,7}.
-__device__ __forceinline__ vmi_u4 op8(const float (&v)[8], float f, float& s) {
-    _Float16 h[8];
-    const int perm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        h[i] = (_Float16)(v[perm[i]] * f);
-        s += (float)h[i];
-    }
-    vmi_u4 r;
-    r[0] = vmi_h2_bits(h[0], h[1]);
-    r[1] = vmi_h2_bits(h[2], h[3]);
-    r[2] = vmi_h2_bits(h[4], h[5]);
-    r[3] = vmi_h2_bits(h[6], h[7]);
-    return r;
-}
+typedef _Float16 pf_h2v __attribute__((ext_vector_type(2)));
 
-// Eight 8-bit values of two packed words as exact fp16 subnormals n * 2^-24,
-// slot order {0,2,1,3,4,6,5,7}.
+// Eight 8-bit values of two packed words (columns 0..3, 4..7) as exact fp16
+// subnormals n * 2^-24 in the operand's slot order {0,4,1,5,2,6,3,7}, the
+// odd slots times 16 (exact) to match the operand's odd slots divided by 16.
 __device__ __forceinline__ vmi_u4 unpack_u8_f16(uint32_t w0, uint32_t w1) {
     vmi_u4 r;
-    r[0] = w0 & 0x00FF00FFu;
-    r[1] = (w0 >> 8) & 0x00FF00FFu;
-    r[2] = w1 & 0x00FF00FFu;
-    r[3] = (w1 >> 8) & 0x00FF00FFu;
+    r[0] = __builtin_amdgcn_perm(w1, w0, 0x0C040C00u);
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2v, __builtin_amdgcn_perm(w1, w0, 0x0C050C01u)) *
+                                            (pf_h2v){16.0f16, 16.0f16});
+    r[2] = __builtin_amdgcn_perm(w1, w0, 0x0C060C02u);
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(pf_h2v, __builtin_amdgcn_perm(w1, w0, 0x0C070C03u)) *
+                                            (pf_h2v){16.0f16, 16.0f16});
     return r;
 }
 
@@ -252,33 +237,17 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_prep(PfArgs a) {
     const float f = vmi_fp16_range_scale(amax);
     // group of 64 columns = 8 chunks: lanes (8 / NCH) per group
     constexpr int LPG = 8 / NCH;
-    float s4 = 0.0f, s8 = 0.0f;
+    float s4 = 0.0f;
     const size_t orow = (size_t)t * (a.H / 8) + lane * NCH;
     vmi_u4 u[NCH];
-    if (a.xsum4) {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) u[c] = op4<true>(v[c], f, s4);
-    } else {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) u[c] = op4<false>(v[c], f, s4);
-    }
+    for (int c = 0; c < NCH; ++c) u[c] = op4<true>(v[c], f, s4);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) a.xop4[orow + c] = u[c];
-    if (a.xop8) {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) a.xop8[orow + c] = op8(v[c], f, s8);
-    }
     // lanes of one group sum their partials in lane order
 #pragma unroll
-    for (int o = 1; o < LPG; o <<= 1) {
-        s4 += __shfl_xor(s4, o);
-        s8 += __shfl_xor(s8, o);
-    }
-    if ((lane % LPG) == 0) {
-        const size_t g = (size_t)t * (a.H / 64) + lane / LPG;
-        if (a.xsum4) a.xsum4[g] = s4;
-        if (a.xsum8) a.xsum8[g] = s8;
-    }
+    for (int o = 1; o < LPG; o <<= 1) s4 += __shfl_xor(s4, o);
+    if ((lane % LPG) == 0) a.xsum4[(size_t)t * (a.H / 64) + lane / LPG] = s4;
     if (lane == 0) a.fscale[t] = f;
     if (a.has_sgate) {
         const float sg = pf_sgate_dot<NCH>(u, a);
@@ -524,7 +493,6 @@ __device__ __forceinline__ int pf_a_piece(int r, int pos) { return pos ^ ((r >> 
 // 16 q).  The elements are taken into named scalars first: a bit cast of a
 // vector element indexed by a loop counter compiled to one element's result
 // replicated four times.
-typedef _Float16 pf_h2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pf_fma_h2(uint32_t x, uint32_t y, uint32_t z) {
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(pf_h2v, x),
                                                                   __builtin_bit_cast(pf_h2v, y),
@@ -1270,8 +1238,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void k_pf_router3(PfArgs a) {
     const int g0 = kh * (G / 2), g1 = g0 + G / 2;  // this half's groups
     const int e0 = nb * 128;
     const int wpr = H * BITS / 32;
-    const vmi_u4* xop = BITS == 4 ? a.xop4 : a.xop8;
-    const float* xsum = BITS == 4 ? a.xsum4 : a.xsum8;
+    const vmi_u4* xop = a.xop4;  // the 8-bit words unpack into the same slot order
+    const float* xsum = a.xsum4;
     for (int i = tid; i < 128 * (G / 8); i += kPfThreads) {
         const int chunk = i % (G / 8), row = i / (G / 8);
         const int e = min(e0 + row, E - 1);
@@ -1479,7 +1447,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_combine(PfArgs a) {
 
 // -------------------------------------------------------------- workspace
 struct PfLayout {
-    size_t status, xop4, xsum4, xop8, xsum8, fscale, logits, sglogit, ids, scores, slots, counts, offsets, fill,
+    size_t status, xop4, xsum4, fscale, logits, sglogit, ids, scores, slots, counts, offsets, fill,
         tiles, ntiles, list, tgu, pgu, tdn, pdn, actop, aexp, ybuf, bytes;
     int max_tiles;
 };
@@ -1519,9 +1487,7 @@ PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) 
     L.max_tiles = (T * k + kTM3 - 1) / kTM3 + cap + (T + kTM3 - 1) / kTM3;
     L.status = take(256);
     L.xop4 = take((size_t)T * (H / 8) * 16);
-    L.xsum4 = router_bits == 4 ? take((size_t)T * (H / 64) * 4) : 0;  // the 4-bit router's affine term
-    L.xop8 = router_bits == 8 ? take((size_t)T * (H / 8) * 16) : 0;
-    L.xsum8 = router_bits == 8 ? take((size_t)T * (H / 64) * 4) : 0;
+    L.xsum4 = take((size_t)T * (H / 64) * 4);  // the router's affine term
     L.fscale = take((size_t)T * 4);
     L.logits = take((size_t)2 * T * E * 4);
     L.sglogit = take((size_t)T * 4);
@@ -1616,9 +1582,7 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     a.sgate = D.shared_expert_gate;
     a.status = reinterpret_cast<uint32_t*>(ws + L.status);
     a.xop4 = reinterpret_cast<vmi_u4*>(ws + L.xop4);
-    a.xsum4 = L.xsum4 ? reinterpret_cast<float*>(ws + L.xsum4) : nullptr;
-    a.xop8 = D.router_bits == 8 ? reinterpret_cast<vmi_u4*>(ws + L.xop8) : nullptr;
-    a.xsum8 = D.router_bits == 8 ? reinterpret_cast<float*>(ws + L.xsum8) : nullptr;
+    a.xsum4 = reinterpret_cast<float*>(ws + L.xsum4);
     a.fscale = reinterpret_cast<float*>(ws + L.fscale);
     a.logits = reinterpret_cast<float*>(ws + L.logits);
     a.sglogit = reinterpret_cast<float*>(ws + L.sglogit);
