@@ -3,7 +3,9 @@
 Bars (written here):
   routed ids: equal to the oracle's for every token whose top-(k+1) router
   logits are separated by more than 1e-4 (1 + |logit|) (the prefill router is
-  an MFMA GEMM; near-ties of fp32 rounding may order differently);
+  an MFMA GEMM; near-ties of fp32 rounding may order differently), and for
+  every token a top-k of the oracle's logits within that margin, with scores
+  the softmax of the oracle's logits at the chosen ids within 1e-3;
   MoE outputs: with the GPU's own routing given to the oracle, relative L2
   <= 1e-2, cosine >= 0.9999, max |err| <= 1e-2 max |ref| per token;
   the layer is bit-deterministic run to run, and at T=2048 and T=8192 agrees with the
@@ -35,6 +37,32 @@ def assert_close(got, ref, what):
         cos = float(g @ r / max(np.linalg.norm(g) * np.linalg.norm(r), 1e-30))
         mx = np.abs(g - r).max() / max(np.abs(r).max(), 1e-30)
         assert rel <= REL and cos >= COS and mx <= REL, f"{what} token {t}: rel={rel:.3g} cos={cos:.7f} max={mx:.3g}"
+
+
+def oracle_logits(orc, L, x_np):
+    xn = orc.rmsnorm_bf16(x_np, L["norm_w"], L["norm_eps"])[0] if L["norm_w"] is not None else x_np
+    return orc.router_logits(L["router_w"], L["router_s"], L["router_b"], xn, L["E"], L["H"], bits=L["router_bits"],
+                             bias=L["bias"])
+
+
+def assert_topk_within(orc, L, x_np, gid, gsc, k, norm_topk, what):
+    """Every token (not only the clearly separated ones): the GPU's k ids are
+    distinct, in descending order and a top-k of the oracle's router logits up
+    to d = 1e-4 (1 + max |logit|) (no expert left out beats a chosen one by
+    more than d), and its scores are the softmax of the oracle's logits at
+    those ids (renormalised over the k when norm_topk) within 1e-3."""
+    lg = np.asarray(oracle_logits(orc, L, x_np), np.float64)
+    for t in range(lg.shape[0]):
+        row, ids = lg[t], gid[t]
+        d = 1e-4 * (1.0 + np.abs(row).max())
+        assert len(set(ids.tolist())) == k and ids.min() >= 0 and ids.max() < row.size, f"{what} token {t}: ids {ids}"
+        chosen = row[ids]
+        rest = np.delete(row, ids)
+        assert rest.max() <= chosen.min() + d, f"{what} token {t}: expert left out beats a chosen one by > {d:.3g}"
+        assert np.all(np.diff(chosen) <= d), f"{what} token {t}: ids not in descending logit order"
+        e = np.exp(chosen - row.max())
+        ref = e / (e.sum() if norm_topk else np.exp(row - row.max()).sum())
+        assert np.allclose(gsc[t], ref, rtol=1e-3, atol=1e-6), f"{what} token {t}: scores {gsc[t]} vs {ref}"
 
 
 def clear_tokens(orc, L, x_np, k):
@@ -71,6 +99,7 @@ def _check_against_oracle(orc, w, x, out, ids, sc, k, residual, what):
     gid = ids.cpu().numpy()
     assert np.array_equal(gid[clear], rid[clear]), f"{what}: routed ids differ on clearly separated tokens"
     assert clear.mean() > 0.8
+    assert_topk_within(orc, L, x_np, gid, sc.cpu().numpy(), k, True, what)
     ref32, _ = orc.moe_layer_routed(x_np, L, gid, sc.cpu().numpy(), residual=residual)
     got = orc.bf16_to_f32(u16(out).reshape(T, -1))
     assert_close(got, ref32, what)
@@ -197,6 +226,7 @@ def test_prefill_T8192_sampled_oracle_parity(gpu, orc):
     clear = clear_tokens(orc, L, xs, k)
     assert clear.mean() > 0.8
     assert np.array_equal(gid[clear], rid[clear]), "T=8192: routed ids differ on clearly separated tokens"
+    assert_topk_within(orc, L, xs, gid, gsc, k, True, "T=8192 sample")
     ref32, _ = orc.moe_layer_routed(xs, L, gid, gsc, residual=True)
     got = orc.bf16_to_f32(u16(out).reshape(T, -1))[sample]
     assert_close(got, ref32, "T=8192 sample")
