@@ -13,9 +13,10 @@ Qwen3-Next shape.
       router near-tie that the drifted activations resolve the other way
       changes one expert of one token, and the linear-attention state carries
       that change to every later position (measured: 0.7% at positions 0-1,
-      1.2-2.0% from position 2 on).  The GPU's argmax is the oracle's best up
-      to twice the measured logit error, and equal to the oracle's argmax
-      wherever the oracle's top-two margin exceeds that;
+      1.2-2.0% from position 2 on).  Every logit within 0.15 of the
+      oracle's (largest seen: 0.092); the GPU's argmax is the oracle's best up
+      to twice that bar, and equal to the oracle's argmax wherever the
+      oracle's top-two margin exceeds twice the measured logit error;
     - block by block, each block fed the GPU's own input and caches: relative
       L2 <= 1e-2 and cosine >= 0.9999 per token (the single-block bars);
       logits within 1e-4 * sum |x w| per element of the float64 head;
@@ -34,6 +35,7 @@ import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
+LOGIT_ABS = 0.15  # |GPU logit - oracle logit| bar of the end-to-end forward
 V = 151936
 FULL = dict(n_layers=4, attn_every=4, hidden=2048, inter=512, num_experts=512, top_k=10, vocab=V, n_heads=16,
             n_kv_heads=2, n_k_heads=16, n_v_heads=32)
@@ -92,8 +94,11 @@ def test_forward_matches_oracle_composition(gpu, orc, full, full_oracle):
             log(f"  position {pos0 + t}: hidden rel={rel:.3g} cos={cos:.6f} argmax={g} oracle={r} "
                 f"max|dlogit|={err:.3g} margin={np.sort(ref_lg[t])[-1] - np.sort(ref_lg[t])[-2]:.3g}")
             assert rel <= 3e-2 and cos >= 0.999, (what, t, rel, cos)
-            # the GPU's choice is the oracle's best up to the measured logit error
-            assert ref_lg[t][g] >= ref_lg[t][r] - 2 * err, (what, t)
+            # the logits within a fixed bar of the oracle's (the largest error
+            # seen at these positions is 0.092), and the GPU's choice the
+            # oracle's best up to twice that bar
+            assert err <= LOGIT_ABS, (what, t, err)
+            assert ref_lg[t][g] >= ref_lg[t][r] - 2 * LOGIT_ABS, (what, t)
             if clear_margin(ref_lg[t], 0.0) and np.sort(ref_lg[t])[-1] - np.sort(ref_lg[t])[-2] > 2 * err:
                 assert g == r, (what, t)
         log(f"  hidden rel per position {np.round(rels, 4).tolist()}")
