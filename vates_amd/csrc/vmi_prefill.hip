@@ -15,8 +15,9 @@
 //                 in two halves of K that the top-k adds
 //   k_pf_topk     one wave per token: top-k, softmax, renorm, slot table
 //   k_pf_count    routes per slot and each route's rank in its slot
-//   k_pf_scan     exclusive scan of the counts, the list of 128-row M tiles
-//   k_pf_place    every routed (token, rank) into its slot's list
+//   k_pf_place    exclusive scans of the counts (each workgroup), every
+//                 routed (token, rank) into its slot's list, the list of
+//                 128-route tiles
 //   k_pf_table    per touched expert (and the shared one): the fp16
 //                 dequantisation table of its gate, up and down rows
 //   k_pf_gateup3  per (M tile, 256 intermediate rows): gate and up MFMA GEMMs
@@ -78,7 +79,6 @@ struct PfArgs {
     float* scores;              // [T, k]
     int32_t* slots;             // [T, k] (-1: invalid)
     int32_t* counts;            // [cap]
-    int32_t* offsets;           // [cap]
     int32_t* fill;              // [T*k] rank of each route inside its slot
     int4* tiles;                // [max_tiles]: slot (-1 shared), list start (or token start), rows, 0
     int32_t* ntiles;            // [1]
@@ -355,37 +355,55 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_topk(PfArgs a) {
 }
 
 // ------------------------------------------------------------ scan, place
-// One workgroup of 1024 threads, cap <= 1024: slot offsets and the tile list.
-__global__ __launch_bounds__(1024) void k_pf_scan(PfArgs a) {
-    __shared__ int s_cnt[1024];
-    __shared__ int s_tl[1024];
-    const int tid = threadIdx.x;
-    const int c = tid < a.cap ? a.counts[tid] : 0;
-    s_cnt[tid] = c;
-    s_tl[tid] = (c + kTM3 - 1) / kTM3;
+// Exclusive prefix sums over the slots (cap <= 1024) of the route counts and
+// of their 128-route tile counts, by one workgroup of kPfThreads threads into
+// LDS: thread i takes slots 4i..4i+3, the waves scan their lanes' sums, then
+// the wave totals.  Returns the routed tiles in all.
+__device__ int pf_slot_scan(const PfArgs& a, int* s_off, int* s_toff) {
+    __shared__ int s_wsum[kPfThreads / 64][2];
+    const int tid = threadIdx.x, lane = tid & 63, w = pf_wave();
+    int c[4], cs = 0, ts = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int slot = 4 * tid + i;
+        c[i] = slot < a.cap ? a.counts[slot] : 0;
+        cs += c[i];
+        ts += (c[i] + kTM3 - 1) / kTM3;
+    }
+    // inclusive wave scans of the thread sums
+    int ic = cs, it = ts;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int vc = __shfl_up(ic, o), vt = __shfl_up(it, o);
+        if (lane >= o) {
+            ic += vc;
+            it += vt;
+        }
+    }
+    if (lane == 63) {
+        s_wsum[w][0] = ic;
+        s_wsum[w][1] = it;
+    }
     __syncthreads();
-    // inclusive Hillis-Steele scans of counts and tile counts
-    for (int o = 1; o < 1024; o <<= 1) {
-        const int ac = tid >= o ? s_cnt[tid - o] : 0;
-        const int at = tid >= o ? s_tl[tid - o] : 0;
-        __syncthreads();
-        s_cnt[tid] += ac;
-        s_tl[tid] += at;
-        __syncthreads();
+    int bc = 0, bt = 0, total_t = 0;
+#pragma unroll
+    for (int v = 0; v < kPfThreads / 64; ++v) {
+        if (v < w) {
+            bc += s_wsum[v][0];
+            bt += s_wsum[v][1];
+        }
+        total_t += s_wsum[v][1];
     }
-    const int off = s_cnt[tid] - c;
-    const int ntl = (c + kTM3 - 1) / kTM3;
-    const int toff = s_tl[tid] - ntl;
-    if (tid < a.cap) {
-        a.offsets[tid] = off;
-        for (int i = 0; i < ntl; ++i)
-            a.tiles[toff + i] = make_int4(tid, off + i * kTM3, min(kTM3, c - i * kTM3), 0);
+    int oc = bc + ic - cs, ot = bt + it - ts;  // exclusive
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s_off[4 * tid + i] = oc;
+        s_toff[4 * tid + i] = ot;
+        oc += c[i];
+        ot += (c[i] + kTM3 - 1) / kTM3;
     }
-    const int routed_tiles = s_tl[1023];
-    const int sh_tiles = a.has_shared ? (a.T + kTM3 - 1) / kTM3 : 0;
-    for (int i = tid; i < sh_tiles; i += 1024)
-        a.tiles[routed_tiles + i] = make_int4(-1, i * kTM3, min(kTM3, a.T - i * kTM3), 0);
-    if (tid == 0) a.ntiles[0] = routed_tiles + sh_tiles;
+    __syncthreads();
+    return total_t;
 }
 
 // Routes per slot and each route's rank inside its slot: a block counts its
@@ -422,14 +440,33 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_count(PfArgs a) {
     }
 }
 
-// Every valid route into its slot's list at offsets[slot] + rank.
+// Every valid route into its slot's list at offset[slot] + rank, every
+// workgroup scanning the slot counts itself (no separate scan launch);
+// workgroup 0 also writes the list of 128-route tiles (the shared expert's
+// last).
 __global__ __launch_bounds__(kPfThreads) void k_pf_place(PfArgs a) {
-    const int p = blockIdx.x * kPfThreads + threadIdx.x;
+    static_assert(4 * kPfThreads >= 1024, "four slots per thread cover cap <= 1024");
+    __shared__ int s_off[4 * kPfThreads];
+    __shared__ int s_toff[4 * kPfThreads];
+    const int routed_tiles = pf_slot_scan(a, s_off, s_toff);
+    const int tid = threadIdx.x;
+    if (blockIdx.x == 0) {
+        for (int slot = tid; slot < a.cap; slot += kPfThreads) {
+            const int c = a.counts[slot], off = s_off[slot], toff = s_toff[slot];
+            for (int i = 0; i * kTM3 < c; ++i)
+                a.tiles[toff + i] = make_int4(slot, off + i * kTM3, min(kTM3, c - i * kTM3), 0);
+        }
+        const int sh_tiles = a.has_shared ? (a.T + kTM3 - 1) / kTM3 : 0;
+        for (int i = tid; i < sh_tiles; i += kPfThreads)
+            a.tiles[routed_tiles + i] = make_int4(-1, i * kTM3, min(kTM3, a.T - i * kTM3), 0);
+        if (tid == 0) a.ntiles[0] = routed_tiles + sh_tiles;
+    }
+    const int p = blockIdx.x * kPfThreads + tid;
     if (p >= a.T * a.k) return;
     const int slot = a.slots[p];
     if (slot < 0) return;
     const int t = p / a.k, j = p - t * a.k;
-    a.list[a.offsets[slot] + a.fill[p]] = t * (a.k + 1) + j;
+    a.list[s_off[slot] + a.fill[p]] = t * (a.k + 1) + j;
 }
 
 // Route row of tile row i (or -1 past the tile).
@@ -1447,7 +1484,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_combine(PfArgs a) {
 
 // -------------------------------------------------------------- workspace
 struct PfLayout {
-    size_t status, xop4, xsum4, fscale, logits, sglogit, ids, scores, slots, counts, offsets, fill,
+    size_t status, xop4, xsum4, fscale, logits, sglogit, ids, scores, slots, counts, fill,
         tiles, ntiles, list, tgu, pgu, tdn, pdn, actop, aexp, ybuf, bytes;
     int max_tiles;
 };
@@ -1495,7 +1532,6 @@ PfLayout pf_layout(int T, int k, int H, int I, int E, int cap, int router_bits) 
     L.scores = take((size_t)T * k * 4);
     L.slots = take((size_t)T * k * 4);
     L.counts = take((size_t)cap * 4);
-    L.offsets = take((size_t)cap * 4);
     L.fill = take((size_t)T * k * 4);
     L.tiles = take((size_t)L.max_tiles * 16);
     L.ntiles = take(4);
@@ -1590,7 +1626,6 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
     a.scores = reinterpret_cast<float*>(ws + L.scores);
     a.slots = reinterpret_cast<int32_t*>(ws + L.slots);
     a.counts = reinterpret_cast<int32_t*>(ws + L.counts);
-    a.offsets = reinterpret_cast<int32_t*>(ws + L.offsets);
     a.fill = reinterpret_cast<int32_t*>(ws + L.fill);
     a.tiles = reinterpret_cast<int4*>(ws + L.tiles);
     a.ntiles = reinterpret_cast<int32_t*>(ws + L.ntiles);
@@ -1641,7 +1676,6 @@ extern "C" int vmi_moe_prefill(const vmi_moe_layer_desc* desc, const uint16_t* x
             hipLaunchKernelGGL(k_pf_topk<16>, dim3(tok_blocks), dim3(kPfThreads), 0, s, a);
     }
     hipLaunchKernelGGL(k_pf_count, dim3((T * D.top_k + kCountRoutes - 1) / kCountRoutes), dim3(kPfThreads), 0, s, a);
-    hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, a);
     hipLaunchKernelGGL(k_pf_place, dim3((T * D.top_k + kPfThreads - 1) / kPfThreads), dim3(kPfThreads), 0, s, a);
     if (!D.prefill_tables)
         hipLaunchKernelGGL(k_pf_table, dim3((D.cap + 1) * pf_table_blocks(D.hidden, D.inter)), dim3(kPfThreads), 0, s,
