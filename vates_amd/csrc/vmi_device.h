@@ -498,6 +498,11 @@ __device__ __forceinline__ vmi_u4 vmi_bload_b128_coh(__amdgpu_buffer_rsrc_t r, u
 __device__ __forceinline__ void vmi_bstore_b128(const vmi_u4& v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)voff, (int)soff, 0);
 }
+// The same for 8 bytes.
+__device__ __forceinline__ void vmi_bstore_b64(uint2 v, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b64((uint32_t __attribute__((ext_vector_type(2)))){v.x, v.y}, r, (int)voff,
+                                          (int)soff, 0);
+}
 // Nontemporal form, for data the next kernel reads once.
 __device__ __forceinline__ void vmi_bstore_b128_nt(const vmi_u4& v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
                                                    uint32_t soff) {

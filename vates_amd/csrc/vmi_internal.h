@@ -40,7 +40,7 @@ struct MoeWorkspace {
     uint32_t __attribute__((ext_vector_type(4)))* xop;    // [T, H/8] MFMA operands of the MoE input
     float* xsum;          // [T, H/64] per-group sums of those operands
     float* fscale;        // [T] power-of-two range factor of the operands
-    float* part;          // [T*k + T, I/64, H] weighted fp32 partial rows: pair p's (or the shared
+    uint16_t* part;       // [T*k + T, I/64, H] weighted bf16 partial rows: pair p's (or the shared
                           // expert's for token t, row T*k + t) down projection of each slice
     size_t bytes;
 };

@@ -671,7 +671,7 @@ struct ExpertArgs {
     const float* xsum;            // [T, H/64]
     const float* fscale;          // [T]
     const float* sg_logit;        // [T] (has_sgate)
-    float* part;                  // [npairs + T, I/64, H] weighted partial rows
+    uint16_t* part;               // [npairs + T, I/64, H] weighted partial rows, bf16
 };
 
 // One workgroup (4 waves) per item = blockIdx.x = u*NC + c: distinct slot u's
@@ -1052,9 +1052,9 @@ __global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArg
     // store past its range, so the loop has no branch and the blocks' MFMAs
     // and arithmetic interleave
     const __amdgpu_buffer_rsrc_t rpart =
-        vmi_rsrc(a.part, (uint32_t)((size_t)(a.ra.npairs + T) * NC * H * sizeof(float)));
+        vmi_rsrc(a.part, (uint32_t)((size_t)(a.ra.npairs + T) * NC * H * sizeof(uint16_t)));
     const uint32_t pbase =
-        store ? (uint32_t)((((size_t)prow * NC + c) * H + RPW * w + 16 * pi + 4 * q) * sizeof(float)) : VMI_OOB;
+        store ? (uint32_t)((((size_t)prow * NC + c) * H + RPW * w + 16 * pi + 4 * q) * sizeof(uint16_t)) : VMI_OOB;
     // (the strip's loads were all issued before the first store, so the counted
     // wait for a block never waits for a store)
     VMI_STAMP(1, 7);
@@ -1082,12 +1082,10 @@ __global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArg
         const int h = RPW * w + 16 * (bb + pi) + 4 * q;
         const float4 sv = *reinterpret_cast<const float4*>(&scw[h]);
         const float4 cv = *reinterpret_cast<const float4*>(&scw[H + h]);
-        vmi_u4 o;
-        o[0] = __float_as_uint(wt * fmaf(sv.x, E[0], cv.x * Xp));
-        o[1] = __float_as_uint(wt * fmaf(sv.y, E[1], cv.y * Xp));
-        o[2] = __float_as_uint(wt * fmaf(sv.z, E[2], cv.z * Xp));
-        o[3] = __float_as_uint(wt * fmaf(sv.w, E[3], cv.w * Xp));
-        vmi_bstore_b128(o, rpart, pbase, 64u * (uint32_t)bb);
+        // the partial row rounded to bf16 (the reference's expert outputs are bf16)
+        const uint2 o = make_uint2(vmi_pack_bf16x2(wt * fmaf(sv.x, E[0], cv.x * Xp), wt * fmaf(sv.y, E[1], cv.y * Xp)),
+                                   vmi_pack_bf16x2(wt * fmaf(sv.z, E[2], cv.z * Xp), wt * fmaf(sv.w, E[3], cv.w * Xp)));
+        vmi_bstore_b64(o, rpart, pbase, 32u * (uint32_t)bb);
     }
     VMI_STAMP(1, 6);
 }
@@ -1096,7 +1094,7 @@ __global__ __launch_bounds__(kThreads, TB <= 8 ? 2 : 1) void k_experts(ExpertArg
 struct CombineArgs {
     int T, H, NC, k, npairs, has_shared;
     const RouteInfo* route;
-    const float* part;         // [npairs + T, NC, H]
+    const uint16_t* part;      // [npairs + T, NC, H] bf16
     const uint16_t* residual;  // [T, H] or nullptr
     uint16_t* out;             // [T, H] bf16
 };
@@ -1128,10 +1126,10 @@ __global__ __launch_bounds__(kThreads) void k_moe_combine(CombineArgs a) {
     // and items past the batch read nothing), all requested before any wait;
     // T * (k + 1) * 2 <= 2 (160 + 16) items fit two passes of the workgroup
     const int nitem = T * (k + 1) * 2;
-    const __amdgpu_buffer_rsrc_t rp = vmi_rsrc(a.part, (uint32_t)((size_t)(a.npairs + T) * NC * H * sizeof(float)));
+    const __amdgpu_buffer_rsrc_t rp = vmi_rsrc(a.part, (uint32_t)((size_t)(a.npairs + T) * NC * H * sizeof(uint16_t)));
     const __amdgpu_buffer_rsrc_t rf = vmi_rsrc(a.route->pv, (uint32_t)a.npairs * 4u);
     constexpr int MC = kMaxInter / kSlice;
-    vmi_u4 v[2][MC];
+    uint2 v[2][MC];
     uint32_t flag[2];
     int tj[2];
 #pragma unroll
@@ -1144,24 +1142,26 @@ __global__ __launch_bounds__(kThreads) void k_moe_combine(CombineArgs a) {
         const int p = j < k ? t * k + j : a.npairs + t;
         const uint32_t fl = vmi_bload_b32(rf, (ok && j < k) ? 4u * (uint32_t)p : VMI_OOB, 0);
         flag[it] = j < k ? fl : (uint32_t)(ok && a.has_shared);
-        const uint32_t off = (uint32_t)(((size_t)p * NC * H + h0 + 4 * half) * sizeof(float));
+        const uint32_t off = (uint32_t)(((size_t)p * NC * H + h0 + 4 * half) * sizeof(uint16_t));
 #pragma unroll
         for (int cc = 0; cc < MC; ++cc)
-            v[it][cc] = vmi_bload_b128(rp, (ok && cc < NC) ? off + (uint32_t)(cc * H * sizeof(float)) : VMI_OOB, 0);
+            v[it][cc] = vmi_bload_b64(rp, (ok && cc < NC) ? off + (uint32_t)(cc * H * sizeof(uint16_t)) : VMI_OOB, 0);
     }
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int i = tid + kThreads * it;
         if (i < nitem) {
             const int half = i & 1, t = tj[it] / (k + 1), j = tj[it] - t * (k + 1);
-            float y[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = __uint_as_float(v[it][0][e]);
+            float y[4] = {__uint_as_float(v[it][0].x << 16), __uint_as_float(v[it][0].x & 0xffff0000u),
+                          __uint_as_float(v[it][0].y << 16), __uint_as_float(v[it][0].y & 0xffff0000u)};
 #pragma unroll
             for (int cc = 1; cc < MC; ++cc)
-                if (cc < NC)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) y[e] += __uint_as_float(v[it][cc][e]);
+                if (cc < NC) {
+                    y[0] += __uint_as_float(v[it][cc].x << 16);
+                    y[1] += __uint_as_float(v[it][cc].x & 0xffff0000u);
+                    y[2] += __uint_as_float(v[it][cc].y << 16);
+                    y[3] += __uint_as_float(v[it][cc].y & 0xffff0000u);
+                }
             *reinterpret_cast<float4*>(&s_y[t][j][4 * half]) =
                 flag[it] ? make_float4(y[0], y[1], y[2], y[3]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
@@ -1625,7 +1625,7 @@ MoeWorkspace carve_workspace(void* base, int T, int k, int hidden, int inter, in
     w.xop = reinterpret_cast<vmi_u4*>(take(sizeof(uint16_t) * (size_t)T * hidden));
     w.xsum = reinterpret_cast<float*>(take(sizeof(float) * (size_t)T * (hidden / 64)));
     w.fscale = reinterpret_cast<float*>(take(sizeof(float) * (size_t)T));
-    w.part = reinterpret_cast<float*>(take(sizeof(float) * nrows * (inter / 64) * hidden));
+    w.part = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * nrows * (inter / 64) * hidden));
     w.bytes = off;
     return w;
 }
