@@ -44,10 +44,10 @@ ZIPF_S, ZIPF_ALPHA = 1.1, 0.5
 # for a plain copy of known size (bench.py --path copy), plus WRITE_SIZE
 # likewise, divided by those calls' algorithmic bytes.  The line reports
 # roofline.traffic = this ratio x this run's algorithmic bytes per call.
-MOE_TRAFFIC_RATIO = 1.1071
+MOE_TRAFFIC_RATIO = 1.0585
 MOE_TRAFFIC_SOURCE = ("profiles/moe_layer_48x_T4_traffic.md: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over 34 layer "
-                      "calls, scaled by a 512 MiB copy (x2.000 / x1.000): 64,877,214 B against 58,602,501 "
-                      "algorithmic B (expert weights x1.003; 5.8 MB of split-K partial rows written and re-read)")
+                      "calls, scaled by a 512 MiB copy (x2.000 / x1.000): 61,948,825 B against 58,525,824 "
+                      "algorithmic B (expert weights x1.003; 2.9 MB of bf16 split-K partial rows written and re-read)")
 
 
 def eprint(*a):
