@@ -231,7 +231,7 @@ struct AttnArgs {
     const int32_t* pos_dev;   // if set: pos0 is read here
     uint32_t* status;         // workspace status word (VMI_STATUS_BAD_POS)
     int nstride;              // chunk capacity of the partial buffers
-    float* part_o;            // [n_kv, nstride, RP, 256]
+    uint16_t* part_o;         // [n_kv, nstride, RP, 256] bf16 (unnormalised P V of each chunk)
     float* part_ml;           // [n_kv, nstride, RP, 2]
     uint16_t* o;              // [T, n_heads * 256] bf16 gated attention output
     int chunk_keys;           // keys per chunk: 32 (8 + extra blocks)
@@ -725,9 +725,9 @@ __global__ __launch_bounds__(kChunkThreads) void k_attn_chunk(AttnArgs a) {
             vmi_f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int sb = 0; sb < NB; ++sb) acc = vmi_mfma_bf16(s_pa[m][sb][lane], vr[dt][sb], acc);
-            float* po = a.part_o + (pbase + 16 * m + 4 * q4) * kHeadDim + 32 * w + 16 * dt + nl;
+            uint16_t* po = a.part_o + (pbase + 16 * m + 4 * q4) * kHeadDim + 32 * w + 16 * dt + nl;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) po[r * kHeadDim] = acc[r];
+            for (int r = 0; r < 4; ++r) po[r * kHeadDim] = (uint16_t)vmi_f32_to_bf16(acc[r]);
         }
     }
     if (tid < RP) {
@@ -765,7 +765,7 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
     const size_t rbase = (size_t)g * a.nstride * RP + row;
     const __amdgpu_buffer_rsrc_t rml = vmi_rsrc(a.part_ml + rbase * 2, (uint32_t)(a.nstride * RP * 2) * 4u);
     const __amdgpu_buffer_rsrc_t rpo =
-        vmi_rsrc(a.part_o + rbase * kHeadDim, (uint32_t)(a.nstride * RP) * kHeadDim * 4u);
+        vmi_rsrc(a.part_o + rbase * kHeadDim, (uint32_t)(a.nstride * RP) * kHeadDim * 2u);
     uint2 mlr[kMlPer];
 #pragma unroll
     for (int i = 0; i < kMlPer; ++i) {
@@ -773,11 +773,11 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
         mlr[i] = vmi_bload_b64(rml, c < NC ? (uint32_t)(c * RP * 2) * 4u : VMI_OOB, 0);
     }
     const int slot = 4 * w + (lane >> 4), d0 = 64 * blockIdx.y + 4 * (lane & 15);
-    vmi_u4 pv[8];
+    uint2 pv[8];  // four bf16 each
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int c = slot + 16 * i;
-        pv[i] = vmi_bload_b128(rpo, c < NC ? ((uint32_t)(c * RP) * kHeadDim + d0) * 4u : VMI_OOB, 0);
+        pv[i] = vmi_bload_b64(rpo, c < NC ? ((uint32_t)(c * RP) * kHeadDim + d0) * 2u : VMI_OOB, 0);
     }
     float M = -INFINITY;
 #pragma unroll
@@ -815,21 +815,23 @@ __global__ __launch_bounds__(kAThreads) void k_attn_merge(AttnArgs a, int RP) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int c = slot + 16 * i;
-        if (c < NC) add(c, __uint_as_float(pv[i][0]), __uint_as_float(pv[i][1]), __uint_as_float(pv[i][2]),
-                        __uint_as_float(pv[i][3]));
+        if (c < NC) add(c, __uint_as_float(pv[i].x << 16), __uint_as_float(pv[i].x & 0xffff0000u),
+                        __uint_as_float(pv[i].y << 16), __uint_as_float(pv[i].y & 0xffff0000u));
     }
-    const float* po = a.part_o + rbase * kHeadDim + d0;  // chunk c at + c * RP * 256
+    const uint16_t* po = a.part_o + rbase * kHeadDim + d0;  // chunk c at + c * RP * 256
     for (int c0 = slot + 16 * 8; c0 < NC; c0 += 16 * 8) {
-        float4 v[8];
+        uint2 v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int c = c0 + 16 * i;
-            v[i] = c < NC ? *reinterpret_cast<const float4*>(po + (size_t)c * RP * kHeadDim) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[i] = c < NC ? *reinterpret_cast<const uint2*>(po + (size_t)c * RP * kHeadDim) : make_uint2(0u, 0u);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int c = c0 + 16 * i;
-            if (c < NC) add(c, v[i].x, v[i].y, v[i].z, v[i].w);
+            if (c < NC)
+                add(c, __uint_as_float(v[i].x << 16), __uint_as_float(v[i].x & 0xffff0000u), __uint_as_float(v[i].y << 16),
+                    __uint_as_float(v[i].y & 0xffff0000u));
         }
     }
     acc.x += __shfl_xor(acc.x, 16); acc.y += __shfl_xor(acc.y, 16);
@@ -1162,7 +1164,7 @@ AttnLayout attn_layout(int T, int H, int n_heads, int n_kv, int max_len, int pat
     L.xn = take((size_t)T * H * 2);
     L.qkv = take((size_t)T * stride * 4);
     const int nc = attn_chunks(max_len);
-    L.part_o = take((size_t)n_kv * nc * RP * kHeadDim * 4);
+    L.part_o = take((size_t)n_kv * nc * RP * kHeadDim * 2);
     L.part_ml = take((size_t)n_kv * nc * RP * 2 * 4);
     L.o = take((size_t)T * n_heads * kHeadDim * 2);
     L.bytes = off;
@@ -1351,7 +1353,7 @@ int attention_impl(const vmi_attn_layer_desc* desc, const uint16_t* x, int paths
     // with the position on the device every chunk of the capacity is launched; those past the cache exit
     const int grid_chunks = pos_device ? at.nstride : (pos0 + span + at.chunk_keys - 1) / at.chunk_keys;
     at.chunks = grid_chunks;
-    at.part_o = reinterpret_cast<float*>(ws + L.part_o);
+    at.part_o = reinterpret_cast<uint16_t*>(ws + L.part_o);
     at.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
     at.o = ob;
     const int MS = (span * G + 15) / 16;
