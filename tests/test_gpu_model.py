@@ -23,7 +23,7 @@ Qwen3-Next shape.
     - the block-by-block run ends in the same hidden states as
       ``SpecModel.forward``, bit for bit.
 * The MTP step at that shape: two chained steps against the oracle.
-* BASELINE config 4's decode: a 48-layer model (12 full-attention and 36
+* The end-to-end decode shape: a 48-layer model (12 full-attention and 36
   Gated DeltaNet layers, every layer MoE) with a 32,768-position context in
   its caches; the captured-graph speculative decoder (K=3) emits exactly the
   greedy stream over 64 tokens, with planted drafts that make every
@@ -194,7 +194,7 @@ def test_config4_graph_decode_equals_greedy(gpu):
     from vates_amd.synth import synth_bf16
     from vates_amd.workload import synth_spec_model
     seed, ctx, N, K = 29, 32768, 64, 3
-    log("case: config 4 model, 48 layers, 32768-position context")
+    log("case: 48-layer model, 32768-position context")
     model = synth_spec_model(seed, n_layers=48, attn_every=4, device=gpu)
     assert sum(l.attn is not None for l in model.layers) == 12
     assert sum(l.gdn is not None for l in model.layers) == 36
@@ -229,7 +229,7 @@ def test_config4_graph_decode_equals_greedy(gpu):
         return [truth[base + i] if i < m else (truth[base + i] + 1) % V for i in range(K)]
 
     for planted in (True, False):
-        log(f"case: config 4 graph speculative K=3 planted={planted}")
+        log(f"case: 48-layer graph speculative K=3 planted={planted}")
         reset()
         dec = GraphSpecDecoder(model, drafter, caches, K=K, planted=planted)
         dec.start(x0, h0, ctx)

@@ -206,10 +206,12 @@ def test_prefill_deterministic_and_matches_verify_path(gpu, orc):
 
 
 def test_prefill_T8192_sampled_oracle_parity(gpu, orc):
-    """BASELINE config 2 at T=8192 (81,920 routed assignments): bit-deterministic
-    run to run; on 64 sampled tokens, routed ids equal the oracle's wherever the
-    router has no near-tie, and the outputs meet the oracle bars given the GPU's
-    routing; two 16-token windows agree with the verify-batch kernels."""
+    """The full prefill shape at T=8192 (81,920 routed assignments):
+    bit-deterministic run to run; on 64 sampled tokens, routed ids equal the
+    oracle's wherever the router has no near-tie, every token's ids and scores
+    are a top-k of the oracle's logits within the near-tie bar, and the outputs
+    meet the oracle bars given the GPU's routing; two 16-token windows agree
+    with the verify-batch kernels."""
     log("case: prefill T=8192 full shape, 64 sampled tokens vs the oracle")
     import torch
     T, k = 8192, 10
