@@ -889,10 +889,12 @@ constexpr int kQ4MaxK = 2048;  // widest K the NORM form stages
 // RT: weight rows per wave tile, 16, or 8 where 16-row tiles would leave
 // half the CUs idle (lanes 8..15 then repeat rows 0..7: the same addresses in
 // the same load, and MFMA columns 8..15 that are not stored).
-template <bool NORM, int RT>
-__global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
+template <bool NORM, int RT, int NW>
+__global__ __launch_bounds__(NW * 64) void k_qgemv4(QgArgs a) {
     static_assert(RT == 8 || RT == 16, "row tile");
-    __shared__ float s_part[kQ4Waves][16][kQgMaxT];
+    static_assert(NW == kQ4Waves || (NW == 12 && NORM), "8 waves, or 12 for the normalising form");
+    constexpr int NT = NW * 64;
+    __shared__ float s_part[NW][16][kQgMaxT];
     const int T = a.T, K = a.K, G = K / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = at_wave();
     const int nl = lane & 15, q4 = lane >> 4;
@@ -907,7 +909,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     asm volatile("" ::"s"(a.rows[0]), "s"(a.rows[1]), "s"(a.nrows), "s"(a.residual), "s"(a.out_bf16), "s"(a.out),
                  "s"(a.out_stride), "s"(T), "s"(K));
     const int lks = __builtin_ctz((unsigned)K) - 9;  // K / kQ4Kw = 1 << lks (K is 512, 1024, 2048 or 4096)
-    const int ks = 1 << lks, tiles = kQ4Waves >> lks;
+    const int ks = 1 << lks, tiles = NW >> lks;
     const int tile = w >> lks, kw = w & (ks - 1);
     const int n = (blockIdx.x * tiles + tile) * RT + (nl & (RT - 1));
     const int nn = n < a.nrows ? n : a.nrows - 1;
@@ -944,7 +946,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
             if (i < T) xv[i] = vmi_bload_b128(rx, (uint32_t)((i * K + kw * kQ4Kw) * 2 + lane * 16), 0);
         asm volatile("" ::: "memory");
     }
-    constexpr int NXW = NORM ? kQgMaxT * kQ4MaxK / 8 / kQ4Threads : 1;
+    constexpr int NXW = NORM ? (kQgMaxT * kQ4MaxK / 8 + NT - 1) / NT : 1;
     vmi_u4 xw[NXW], nw;
     if constexpr (NORM) {
         // the T input rows and the norm weights as 16-byte words, first: the
@@ -952,7 +954,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
         const __amdgpu_buffer_rsrc_t rx = vmi_rsrc(a.x, (uint32_t)(T * K / 8) * 16u);
         const __amdgpu_buffer_rsrc_t rn = vmi_rsrc(a.norm_w, (uint32_t)(K / 8) * 16u);
 #pragma unroll
-        for (int d = 0; d < NXW; ++d) xw[d] = vmi_bload_b128(rx, (uint32_t)(tid + kQ4Threads * d) * 16u, 0);
+        for (int d = 0; d < NXW; ++d) xw[d] = vmi_bload_b128(rx, (uint32_t)(tid + NT * d) * 16u, 0);
         nw = vmi_bload_b128(rn, (uint32_t)tid * 16u, 0);
         asm volatile("" ::: "memory");
     }
@@ -979,14 +981,18 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     // raw bf16 bits, issued now so that its latency overlaps the weights'; a
     // branch-free buffer load whose value is first used at the end, so no
     // wait on it (and on everything issued before it) lands here
-    const int nout = tiles * RT * T;
+    // outputs i = (tile, row, token) with the token in the low three bits
+    // (kQgMaxT = 8 slots, those past T idle): shifts, not divisions by T
+    static_assert(kQgMaxT == 8, "three token bits");
+    constexpr int LRT = RT == 16 ? 4 : 3;
+    const int nout = tiles * RT * kQgMaxT;
     // (unconditional: without a residual the range is empty and every lane
     // reads zero without touching memory)
     const __amdgpu_buffer_rsrc_t rres =
         vmi_rsrc(a.residual, a.out_bf16 && a.residual ? (uint32_t)((size_t)T * a.out_stride * 2) : 0u);
-    const int row0 = (blockIdx.x * tiles + tid / (RT * T)) * RT + (tid / T) % RT;
+    const int row0 = (blockIdx.x * tiles + (tid >> (3 + LRT))) * RT + ((tid >> 3) & (RT - 1)), t0 = tid & 7;
     const uint32_t res0 = vmi_bload_b16(
-        rres, tid < nout && row0 < a.nrows ? (uint32_t)(((size_t)(tid % T) * a.out_stride + row0) * 2) : VMI_OOB, 0);
+        rres, tid < nout && t0 < T && row0 < a.nrows ? (uint32_t)(((size_t)t0 * a.out_stride + row0) * 2) : VMI_OOB, 0);
     asm volatile("" ::: "memory");
     VMI_STAMP(kid, 5);
     if constexpr (!NORM) {
@@ -994,7 +1000,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
         // bank conflicts between tokens); the same wave reads it back in
         // operand order below
         // (row kQgMaxT stays zero: the operand row of lanes outside the batch)
-        __shared__ uint4 s_xw[kQ4Waves][kQgMaxT + 1][kQ4Kw / 8 + 1];
+        __shared__ uint4 s_xw[NW][kQgMaxT + 1][kQ4Kw / 8 + 1];
         s_xw[w][kQgMaxT][lane] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
         for (int i = 0; i < kQgMaxT; ++i)
@@ -1014,7 +1020,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
         if (tid < nnw) s_xn[kQgMaxT * (K / 8) + tid] = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
         for (int d = 0; d < NXW; ++d) {
-            const int i = tid + kQ4Threads * d;
+            const int i = tid + NT * d;
             if (i < nxw) s_xn[i] = make_uint4(xw[d][0], xw[d][1], xw[d][2], xw[d][3]);
         }
         if (tid < nnw) s_nw[tid] = make_uint4(nw[0], nw[1], nw[2], nw[3]);
@@ -1037,7 +1043,7 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
         // every thread rewrites its words of the rows in place
 #pragma unroll
         for (int d = 0; d < NXW; ++d) {
-            const int i = tid + kQ4Threads * d;
+            const int i = tid + NT * d;
             if (i < nxw) {
                 const float inv = s_inv[i / (K / 8)];
                 float f[8], g[8];
@@ -1109,8 +1115,9 @@ __global__ __launch_bounds__(kQ4Threads) void k_qgemv4(QgArgs a) {
     }
     __syncthreads();
     VMI_STAMP(kid, 2);
-    for (int i = tid; i < tiles * RT * T; i += kQ4Threads) {
-        const int tl = i / (RT * T), rr = (i / T) % RT, t = i % T;
+    for (int i = tid; i < nout; i += NT) {
+        const int tl = i >> (3 + LRT), rr = (i >> 3) & (RT - 1), t = i & 7;
+        if (t >= T) continue;
         float y = s_part[tl * ks][rr][t];
         for (int k2 = 1; k2 < ks; ++k2) y += s_part[tl * ks + k2][rr][t];
         const int row = (blockIdx.x * tiles + tl) * RT + rr;
@@ -1204,17 +1211,25 @@ hipError_t vmi::launch_qgemv(const QgemvCall& q0, hipStream_t s) {
         const int wg16 = (q.nrows + 16 * tiles - 1) / (16 * tiles), wg8 = (q.nrows + 8 * tiles - 1) / (8 * tiles);
         const int ncu = vmi::device_cus();
         const bool rt8 = 2 * wg16 <= ncu && wg8 <= ncu;
-        const dim3 grid(rt8 ? wg8 : wg16);
+        // 12-wave workgroups of three 16-row tiles (normalising form) when the
+        // 8-wave ones would put two workgroups on some CU and three tiles per
+        // workgroup give every workgroup a CU of its own (9,216 and 12,288
+        // rows at K = 2048: 192 and 256 workgroups instead of 288 and 384)
+        const int tiles12 = 12 / ks, wg12 = (q.nrows + 16 * tiles12 - 1) / (16 * tiles12);
+        const bool w12 = q.norm_w && !rt8 && 12 % ks == 0 && wg16 > ncu && wg12 <= ncu;
+        const dim3 grid(rt8 ? wg8 : w12 ? wg12 : wg16);
         if (q.norm_w) {
             if (rt8)
-                hipLaunchKernelGGL((k_qgemv4<true, 8>), grid, dim3(kQ4Threads), 0, s, q);
+                hipLaunchKernelGGL((k_qgemv4<true, 8, kQ4Waves>), grid, dim3(kQ4Threads), 0, s, q);
+            else if (w12)
+                hipLaunchKernelGGL((k_qgemv4<true, 16, 12>), grid, dim3(12 * 64), 0, s, q);
             else
-                hipLaunchKernelGGL((k_qgemv4<true, 16>), grid, dim3(kQ4Threads), 0, s, q);
+                hipLaunchKernelGGL((k_qgemv4<true, 16, kQ4Waves>), grid, dim3(kQ4Threads), 0, s, q);
         } else {
             if (rt8)
-                hipLaunchKernelGGL((k_qgemv4<false, 8>), grid, dim3(kQ4Threads), 0, s, q);
+                hipLaunchKernelGGL((k_qgemv4<false, 8, kQ4Waves>), grid, dim3(kQ4Threads), 0, s, q);
             else
-                hipLaunchKernelGGL((k_qgemv4<false, 16>), grid, dim3(kQ4Threads), 0, s, q);
+                hipLaunchKernelGGL((k_qgemv4<false, 16, kQ4Waves>), grid, dim3(kQ4Threads), 0, s, q);
         }
     } else {
         const size_t lds = (size_t)q.T * q.K * 2;
