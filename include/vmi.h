@@ -253,6 +253,23 @@ int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weigh
                 float* top_prob, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * vmi_head_tiles / vmi_lm_head_tiled -- no counterpart in the reference: the
+ * head re-laid once (at load) for callers that run it every decode step.
+ * vmi_head_tiles copies a row-major bf16 [vocab, hidden] head into
+ * vmi_head_tiles_bytes(vocab, hidden) bytes of tile-major order: element
+ * (v, h) at ((v / 16) * (hidden / 128) + h / 128) * 2048 + (v % 16) * 128 +
+ * h % 128, rows past vocab (up to a multiple of 16) zero; out must not alias
+ * weight.  vmi_lm_head_tiled is vmi_lm_head on that copy (same arguments,
+ * results bit for bit): each of its 4 KB weight chunks is contiguous, which
+ * the kernel's LDS DMA streams faster than four rows' 256-byte runs.
+ * ------------------------------------------------------------------------ */
+size_t vmi_head_tiles_bytes(int vocab, int hidden);
+int vmi_head_tiles(const uint16_t* weight, int vocab, int hidden, uint16_t* out, void* stream);
+int vmi_lm_head_tiled(const uint16_t* x, int T, int hidden, const uint16_t* norm_weight, float norm_eps,
+                      const uint16_t* tiles, int vocab, float* logits, int32_t* argmax, float* max_logit,
+                      float* top_prob, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * vmi_qgemv -- y = W x for a small batch of tokens with an affine-quantised W
  * (the reference's quantized Linear layers: QuantizedLinear of mlx, as used
  * by the MTP fc and attention projections, qwen3_next_mtp.py:28-30, 40-53).

@@ -141,3 +141,39 @@ def test_lm_head_top_prob(gpu, orc, T, V, scale):
     log(f"  top_prob {got} ref {ref}")
     assert np.all(np.abs(got - ref) <= 1e-5 * ref), (got, ref)
 
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,V,norm", [(4, 151936, True), (1, 151936, False), (5, 1000, True), (16, 1003, False)])
+def test_lm_head_tiled_equals_row_major(gpu, T, V, norm):
+    """vmi_lm_head_tiled on the vmi_head_tiles copy gives vmi_lm_head's logits,
+    argmax, maximum and top-1 probability bit for bit, including vocabularies
+    that are not a multiple of 16 (the copy's zero padding rows)."""
+    import torch
+    from vates_amd.head import TiledHead, lm_head
+    from vates_amd.synth import synth_bf16
+    H = 2048
+    log(f"case: tiled head T={T} V={V} norm={norm}")
+    W = synth_bf16(31, 0x7100 + V, (V, H), std=0.02, device=gpu)
+    x = synth_bf16(31, 0x7200 + T, (T, H), device=gpu)
+    nw = synth_bf16(31, 0x7300, (H,), std=0.1, device=gpu) + 1.0 if norm else None
+    Wt = TiledHead(W)
+    assert Wt.tiles.numel() == ((V + 15) // 16) * 16 * H
+    outs = []
+    for head in (W, Wt):
+        prob = torch.empty(T, dtype=torch.float32, device=gpu)
+        lg, am, mx = lm_head(x, head, nw, top_prob=prob)
+        torch.cuda.synchronize()
+        outs.append((lg.cpu(), am.cpu(), mx.cpu(), prob.cpu()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    # the copy itself: element (v, h) at ((v/16)(H/128) + h/128) 2048 + (v%16) 128 + h%128
+    v = torch.arange(V, device=gpu)[:, None]
+    h = torch.arange(H, device=gpu)[None, :]
+    idx = ((v // 16) * (H // 128) + h // 128) * 2048 + (v % 16) * 128 + h % 128
+    assert torch.equal(Wt.tiles[idx.reshape(-1)].reshape(V, H), W)
+    Vp = ((V + 15) // 16) * 16
+    if Vp > V:  # the padding rows are zeros
+        vp = torch.arange(V, Vp, device=gpu)[:, None]
+        pidx = ((vp // 16) * (H // 128) + h // 128) * 2048 + (vp % 16) * 128 + h % 128
+        assert not Wt.tiles[pidx.reshape(-1)].float().any()

@@ -119,6 +119,10 @@ _SIGNATURES = {
     "vmi_lm_head_workspace_bytes": (c_size_t, [c_int, c_int]),
     "vmi_lm_head": (c_int, [c_void_p, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p, c_void_p,
                             c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "vmi_head_tiles_bytes": (c_size_t, [c_int, c_int]),
+    "vmi_head_tiles": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "vmi_lm_head_tiled": (c_int, [c_void_p, c_int, c_int, c_void_p, c_float, c_void_p, c_int, c_void_p, c_void_p,
+                                  c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
 }
 
 _lib = None

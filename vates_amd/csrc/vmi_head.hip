@@ -154,7 +154,10 @@ __device__ void stage_token(const HeadArgs& a, int t, uint8_t* s_row) {
         if (v < nv) *reinterpret_cast<uint4*>(s_row + 2 * (lane * cpl + 8 * v)) = xv[v];
 }
 
-template <int MAXT, int NW, int NBUF>
+// TILED: W is tile-major (vmi_head_tiles): chunk (tile, c), the 16 rows x 256
+// bytes that one ring slot holds, is 4 KB of contiguous memory, so each DMA
+// instruction reads 1 KB at once instead of four 256-byte runs of four rows.
+template <int MAXT, int NW, int NBUF, bool TILED>
 __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
     constexpr int kRow = 2 * kHeadMaxH + 16;  // LDS bytes per token row (16-byte pad: conflict-free A reads)
     __shared__ __attribute__((aligned(16))) uint8_t s_x[MAXT * kRow];
@@ -200,8 +203,13 @@ __global__ __launch_bounds__(NW * 64) void k_head(HeadArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 4 * i + g;
-            const int row = min(tile * 16 + r, V - 1);
-            const uint8_t* src = wbase + (size_t)row * row_bytes + 256 * c + 16 * ((lane & 15) ^ r);
+            const uint8_t* src;
+            if constexpr (TILED) {  // rows past the vocabulary are the layout's zero padding
+                src = wbase + ((size_t)(tile * nch + c) * 16 + r) * 256 + 16 * ((lane & 15) ^ r);
+            } else {
+                const int row = min(tile * 16 + r, V - 1);
+                src = wbase + (size_t)row * row_bytes + 256 * c + 16 * ((lane & 15) ^ r);
+            }
             vmi_lds_dma16_opaque_nt(src, buf + 1024 * i);
         }
     };
@@ -375,16 +383,55 @@ __global__ __launch_bounds__(256) void k_topk_rows(TopkArgs a) {
 namespace {
 constexpr size_t kKeysBytes = (size_t)kHeadMaxGrid * kHeadMaxT * sizeof(uint64_t);
 constexpr size_t kMsBytes = (size_t)kHeadMaxGrid * kHeadMaxT * sizeof(float2);
+// Tile-major copy of a row-major bf16 [V, H] head: 16-byte unit u of row r
+// of chunk (tile, c) - vocabulary row 16 tile + r, hidden values
+// 128 c + 8 u .. + 7 - goes to unit ((tile (H / 128) + c) 16 + r) 16 + u;
+// rows past V are zeros.  One thread per destination unit.
+__global__ __launch_bounds__(256) void k_head_tiles(const uint4* __restrict__ W, int V, int H, size_t units,
+                                                    uint4* __restrict__ out) {
+    const size_t d = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (d >= units) return;
+    const int nch = H >> 7;
+    const int u = (int)(d & 15), r = (int)((d >> 4) & 15);
+    const size_t tc = d >> 8;
+    const int c = (int)(tc % (size_t)nch);
+    const size_t row = (tc / (size_t)nch) * 16 + r;
+    out[d] = row < (size_t)V ? W[row * (size_t)(H >> 3) + (size_t)c * 16 + u] : make_uint4(0u, 0u, 0u, 0u);
+}
+
 }  // namespace
+
+extern "C" size_t vmi_head_tiles_bytes(int vocab, int hidden) {
+    if (vocab <= 0 || hidden <= 0 || hidden % 128) return 0;
+    return (size_t)((vocab + 15) / 16) * 16 * (size_t)hidden * 2;
+}
+
+extern "C" int vmi_head_tiles(const uint16_t* weight, int vocab, int hidden, uint16_t* out, void* stream) {
+    vmi::clear_error();
+    if (vocab <= 0 || hidden <= 0 || hidden % 512 || hidden > kHeadMaxH)
+        return vmi::fail(VMI_ERR_UNSUPPORTED, "vocab=%d hidden=%d (hidden a multiple of 512 up to %d)", vocab, hidden,
+                         kHeadMaxH);
+    if (!weight || !out) return vmi::fail(VMI_ERR_INVALID, "null weight/out");
+    if ((reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(out)) & 15)
+        return vmi::fail(VMI_ERR_INVALID, "weight and out must be 16-byte aligned");
+    if (weight == out) return vmi::fail(VMI_ERR_INVALID, "weight and out must not alias");
+    const size_t units = vmi_head_tiles_bytes(vocab, hidden) / 16;
+    hipLaunchKernelGGL(k_head_tiles, dim3((unsigned)((units + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), reinterpret_cast<const uint4*>(weight), vocab, hidden, units,
+                       reinterpret_cast<uint4*>(out));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return vmi::hip_fail(e, "k_head_tiles launch");
+    return VMI_OK;
+}
 
 extern "C" size_t vmi_lm_head_workspace_bytes(int T, int vocab) {
     if (T <= 0 || vocab <= 0) return 0;
     return vmi::align256(kKeysBytes) + vmi::align256(kMsBytes) + 256;
 }
 
-extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weight, float norm_eps,
-                           const uint16_t* weight, int vocab, float* logits, int32_t* argmax, float* max_logit,
-                           float* top_prob, void* workspace, size_t workspace_bytes, void* stream) {
+static int lm_head_call(const uint16_t* x, int T, int hidden, const uint16_t* norm_weight, float norm_eps,
+                        const uint16_t* weight, int vocab, float* logits, int32_t* argmax, float* max_logit,
+                        float* top_prob, void* workspace, size_t workspace_bytes, void* stream, bool tiled) {
     vmi::clear_error();
     if (T <= 0 || T > kHeadMaxT) return vmi::fail(VMI_ERR_UNSUPPORTED, "T=%d must be in [1, %d]", T, kHeadMaxT);
     if (hidden <= 0 || hidden % 512 || hidden > kHeadMaxH)
@@ -417,15 +464,38 @@ extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t*
     if (G > kHeadMaxGrid) G = kHeadMaxGrid;
     if (G > a.ntiles) G = a.ntiles;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (T <= 4 && hidden % 1024 == 0)
-        hipLaunchKernelGGL((k_head<4, 4, 8>), dim3(G), dim3(4 * 64), 0, s, a);
-    else if (T <= 4)
-        hipLaunchKernelGGL((k_head<4, 8, 4>), dim3(G), dim3(8 * 64), 0, s, a);
-    else
-        hipLaunchKernelGGL((k_head<16, 8, 2>), dim3(G), dim3(8 * 64), 0, s, a);
+    if (tiled) {
+        if (T <= 4 && hidden % 1024 == 0)
+            hipLaunchKernelGGL((k_head<4, 4, 8, true>), dim3(G), dim3(4 * 64), 0, s, a);
+        else if (T <= 4)
+            hipLaunchKernelGGL((k_head<4, 8, 4, true>), dim3(G), dim3(8 * 64), 0, s, a);
+        else
+            hipLaunchKernelGGL((k_head<16, 8, 2, true>), dim3(G), dim3(8 * 64), 0, s, a);
+    } else {
+        if (T <= 4 && hidden % 1024 == 0)
+            hipLaunchKernelGGL((k_head<4, 4, 8, false>), dim3(G), dim3(4 * 64), 0, s, a);
+        else if (T <= 4)
+            hipLaunchKernelGGL((k_head<4, 8, 4, false>), dim3(G), dim3(8 * 64), 0, s, a);
+        else
+            hipLaunchKernelGGL((k_head<16, 8, 2, false>), dim3(G), dim3(8 * 64), 0, s, a);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return vmi::hip_fail(e, "k_head launch");
     return VMI_OK;
+}
+
+extern "C" int vmi_lm_head(const uint16_t* x, int T, int hidden, const uint16_t* norm_weight, float norm_eps,
+                           const uint16_t* weight, int vocab, float* logits, int32_t* argmax, float* max_logit,
+                           float* top_prob, void* workspace, size_t workspace_bytes, void* stream) {
+    return lm_head_call(x, T, hidden, norm_weight, norm_eps, weight, vocab, logits, argmax, max_logit, top_prob,
+                        workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int vmi_lm_head_tiled(const uint16_t* x, int T, int hidden, const uint16_t* norm_weight, float norm_eps,
+                                 const uint16_t* tiles, int vocab, float* logits, int32_t* argmax, float* max_logit,
+                                 float* top_prob, void* workspace, size_t workspace_bytes, void* stream) {
+    return lm_head_call(x, T, hidden, norm_weight, norm_eps, tiles, vocab, logits, argmax, max_logit, top_prob,
+                        workspace, workspace_bytes, stream, true);
 }
 
 extern "C" int vmi_topk_rows(const float* logits, int rows, int vocab, int k, int32_t* ids, float* vals, void* stream) {

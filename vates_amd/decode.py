@@ -35,7 +35,7 @@ from ._lib import VmiError, check, load
 from .accept import accept_greedy, accept_stochastic, raise_sampling_status, sample_top_p, spec_commit
 from .attention import AttentionLayer, KVCache
 from .gdn import GatedDeltaNetLayer, GdnCache
-from .head import lm_head
+from .head import TiledHead, lm_head
 from .moe import MoELayer
 from .mtp import MTPDrafter, MTPLayer, rmsnorm
 
@@ -89,6 +89,11 @@ class SpecModel:
                  head: torch.Tensor, mtp: Optional[MTPLayer] = None, eps: float = 1e-6):
         self.embed, self.layers, self.final_norm, self.head, self.mtp, self.eps = embed, layers, final_norm, head, mtp, eps
         self.hidden = embed.shape[1]
+        # the head as the decode loop reads it every step (tile-major copy,
+        # shared with an MTP layer whose head is this one)
+        self.head_tiles = TiledHead(head)
+        if mtp is not None and mtp.w.lm_head is head:
+            mtp.head_tiles = self.head_tiles
 
     def new_caches(self, max_len: int, max_batch: int = 8) -> list:
         """Per layer: a KVCache (full attention), a GdnCache (linear attention,
@@ -112,7 +117,7 @@ class SpecModel:
             elif layer.gdn is not None:
                 x = layer.gdn(x, cache, pos0=pos0, pos_device=pos_device)
             x = layer.moe(x, residual=x, out=hidden_out if i == last else None)
-        logits, am, _ = lm_head(x, self.head, self.final_norm, eps=self.eps,
+        logits, am, _ = lm_head(x, self.head_tiles, self.final_norm, eps=self.eps,
                                 want_logits=want_logits or logits_out is not None, logits=logits_out)
         return am, x, logits
 
@@ -132,7 +137,7 @@ class SpecModel:
             elif layer.gdn is not None:
                 x = layer.gdn.tree(x, cache, paths, pos0=pos0, pos_device=pos_device)
             x = layer.moe(x, residual=x)
-        logits, am, _ = lm_head(x, self.head, self.final_norm, eps=self.eps, want_logits=want_logits)
+        logits, am, _ = lm_head(x, self.head_tiles, self.final_norm, eps=self.eps, want_logits=want_logits)
         return am, x, logits
 
     def commit(self, caches: list, length: int) -> None:

@@ -15,13 +15,38 @@ from ._lib import VmiError, check, load
 from .moe import _require, _stream_handle, workspace
 
 
-def lm_head(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor] = None, *,
+class TiledHead:
+    """A bf16 [vocab, hidden] head re-laid once in tile-major order
+    (``vmi_head_tiles``: each 16-row x 128-value chunk is 4 KB of contiguous
+    memory), for callers that run the head every decode step; ``lm_head`` on it
+    gives the row-major head's results bit for bit, faster."""
+
+    def __init__(self, weight: torch.Tensor, stream=None):
+        if weight.dim() != 2 or weight.dtype != torch.bfloat16 or not weight.is_cuda:
+            raise VmiError("weight must be a bf16 [vocab, hidden] device tensor")
+        weight = weight.contiguous()
+        self.vocab, self.hidden = int(weight.shape[0]), int(weight.shape[1])
+        lib = load()
+        nbytes = int(lib.vmi_head_tiles_bytes(self.vocab, self.hidden))
+        if nbytes == 0:
+            raise VmiError(f"unsupported head shape {tuple(weight.shape)}")
+        self.tiles = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=weight.device)
+        check(lib.vmi_head_tiles(weight.data_ptr(), self.vocab, self.hidden, self.tiles.data_ptr(),
+                                 _stream_handle(stream)), "vmi_head_tiles")
+
+    @property
+    def device(self):
+        return self.tiles.device
+
+
+def lm_head(x: torch.Tensor, weight, norm_weight: Optional[torch.Tensor] = None, *,
             eps: float = 1e-6, want_logits: bool = True, logits: Optional[torch.Tensor] = None,
             argmax: Optional[torch.Tensor] = None, max_logit: Optional[torch.Tensor] = None,
             top_prob: Optional[torch.Tensor] = None, stream=None):
     """Returns (logits f32 [T, V] or None, argmax int32 [T], max logit f32 [T]).
 
-    x bf16 [T, H] (T <= 16), weight bf16 [V, H], norm_weight bf16 [H] or None.
+    x bf16 [T, H] (T <= 16), weight bf16 [V, H] or a TiledHead of one,
+    norm_weight bf16 [H] or None.
     top_prob (f32 [T], optional) receives the softmax probability of each
     row's argmax (the draft confidence of drafter.py:42-62).
     """
@@ -29,11 +54,17 @@ def lm_head(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.T
     if x.dim() != 2:
         raise VmiError(f"x must be [T, hidden], got {tuple(x.shape)}")
     T, H = x.shape
-    if weight.dim() != 2 or weight.shape[1] != H:
-        raise VmiError(f"weight must be [vocab, {H}], got {tuple(weight.shape)}")
-    V = weight.shape[0]
+    tiled = isinstance(weight, TiledHead)
+    if tiled:
+        if weight.hidden != H:
+            raise VmiError(f"tiled head has hidden {weight.hidden}, x has {H}")
+        V, wt = weight.vocab, weight.tiles
+    else:
+        if weight.dim() != 2 or weight.shape[1] != H:
+            raise VmiError(f"weight must be [vocab, {H}], got {tuple(weight.shape)}")
+        V, wt = weight.shape[0], weight
     _require(x, "x", 2, dev)
-    _require(weight, "weight", 2, dev)
+    _require(wt, "weight", 2, dev)
     if norm_weight is not None:
         _require(norm_weight, "norm_weight", 2, dev)
         if norm_weight.numel() != H:
@@ -54,9 +85,10 @@ def lm_head(x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.T
     lib = load()
     nbytes = lib.vmi_lm_head_workspace_bytes(T, V)
     ws = workspace(nbytes, dev, sh, tag="lm_head")
-    rc = lib.vmi_lm_head(x.data_ptr(), T, H, None if norm_weight is None else norm_weight.data_ptr(), float(eps),
-                         weight.data_ptr(), V, None if logits is None else logits.data_ptr(), argmax.data_ptr(),
+    fn = lib.vmi_lm_head_tiled if tiled else lib.vmi_lm_head
+    rc = fn(x.data_ptr(), T, H, None if norm_weight is None else norm_weight.data_ptr(), float(eps),
+                         wt.data_ptr(), V, None if logits is None else logits.data_ptr(), argmax.data_ptr(),
                          max_logit.data_ptr(), None if top_prob is None else top_prob.data_ptr(), ws.data_ptr(),
                          ws.numel(), sh)
-    check(rc, "vmi_lm_head")
+    check(rc, "vmi_lm_head_tiled" if tiled else "vmi_lm_head")
     return logits, argmax, max_logit

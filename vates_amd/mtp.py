@@ -22,7 +22,7 @@ import torch
 
 from ._lib import VmiError, check, load
 from .attention import AttentionLayer, KVCache, qgemv
-from .head import lm_head
+from .head import TiledHead, lm_head
 from .moe import MoELayer, QuantizedProj, _require, _stream_handle
 
 
@@ -60,6 +60,19 @@ class MTPLayer:
         self.w = w
         self.hidden = w.embed.shape[1]
         self.vocab = w.embed.shape[0]
+        self._head_tiles: Optional[TiledHead] = None
+
+    @property
+    def head_tiles(self) -> TiledHead:
+        """The head in tile-major order (made on first use unless the model
+        that shares this head has set its own)."""
+        if self._head_tiles is None:
+            self._head_tiles = TiledHead(self.w.lm_head)
+        return self._head_tiles
+
+    @head_tiles.setter
+    def head_tiles(self, t: TiledHead) -> None:
+        self._head_tiles = t
 
     def _trunk(self, hidden: torch.Tensor, tokens: torch.Tensor, cache: KVCache, stream=None,
                pos_device: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -82,7 +95,7 @@ class MTPLayer:
         (f32 [T]) the softmax probability of the argmax; with logits_out
         (f32 [T, V]) the logits are written there (want_logits implied)."""
         Hn = self._trunk(hidden, tokens, cache, stream, pos_device)
-        logits, am, _ = lm_head(Hn, self.w.lm_head, None, want_logits=want_logits or logits_out is not None,
+        logits, am, _ = lm_head(Hn, self.head_tiles, None, want_logits=want_logits or logits_out is not None,
                                 logits=logits_out, argmax=argmax_out, top_prob=prob_out, stream=stream)
         return am, Hn, logits
 
